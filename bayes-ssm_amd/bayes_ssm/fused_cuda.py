@@ -1,0 +1,428 @@
+"""Exact fused Bayesian core on MI355X: the drop-in for the reference ``fused_cuda``.
+
+Mirrors bayes_ssm/fused_cuda.py of the reference: ``_load_extension(key_dim)``
+returns an object exposing the same per-key-dim method names and signatures as
+the reference pybind modules (``forward_chunked``, ``backward_chunked``, ...;
+export sets at persistent_bayes_chunked_d1m8.cu:673, _d2m8.cu:602,
+_d4m8.cu:577, _d8.cu:653), ``_ChunkedBayesianFunction`` keeps the reference
+autograd slot conventions (fused_cuda.py:58-322), and
+``fused_diagonal_bayesian`` keeps the contract gate (fused_cuda.py:325-388).
+
+Every method is a thin shim over the C ABI of ``libbssm_hip.so``: it checks the
+tensors like the reference ``TORCH_CHECK``s, allocates the outputs with
+``torch.empty`` on the inputs' device (the C ABI never allocates) and launches
+on ``torch.cuda.current_stream()``.
+
+Deliberate differences from the reference, all result-preserving:
+
+* No JIT build: the library is prebuilt for gfx950.  A missing or stale
+  library raises ``RuntimeError`` instead of silently returning ``None``, so a
+  GPU run can never fall back to a slower path unnoticed.
+  ``BAYES_SSM_DISABLE_FUSED_CUDA=1`` still disables the extension.
+* Checkpoint interval: the autograd function checkpoints the belief every
+  ``bssm_preferred_checkpoint(D)`` tokens (the on-chip replay length of the
+  reverse kernel) rather than every ``chunk_length`` tokens.  The recurrence
+  ignores chunking, so outputs and gradients are identical for every interval;
+  ``BAYES_SSM_HIP_CHECKPOINT=chunk`` restores the caller's chunk length and an
+  integer value forces a specific interval.
+* D1 keeps its boundaries through the replay kernel by default; the reference
+  saved-history ABI (forward_chunked_saved / backward_chunked_saved*) is still
+  exported and is used when ``BAYES_SSM_D1_SAVED_HISTORY=1``.
+"""
+from __future__ import annotations
+
+import os
+from typing import Optional
+
+import torch
+from torch import Tensor
+
+from . import _hip
+
+_SUPPORTED = ((1, 8), (2, 8), (4, 8), (8, 8))
+_EXTENSIONS: dict[int, "_Extension"] = {}
+
+# Method names of the reference extension module for each key_dim.
+_EXPORTS = {
+    1: ("forward_chunked", "forward_chunked_saved", "backward_chunked_saved_d1", "backward_chunked",
+        "backward_chunked_lean", "backward_chunked_saved", "backward_chunked_saved_lean",
+        "forward_chunked_fixed", "backward_chunked_lean_fixed", "backward_chunked_fixed"),
+    2: ("forward_chunked", "backward_chunked", "backward_chunked_noinitial", "backward_chunked_lean",
+        "forward_chunked_fixed", "backward_chunked_lean_fixed", "backward_chunked_fixed",
+        "backward_chunked_noinitial_fixed"),
+    4: ("forward_chunked", "backward_chunked", "backward_chunked_lean", "forward_chunked_fixed",
+        "backward_chunked_lean_fixed", "backward_chunked_fixed"),
+    8: ("forward_chunked", "backward_chunked", "backward_chunked_lean", "forward_chunked_fixed",
+        "backward_chunked_lean_fixed", "backward_chunked_fixed"),
+}
+
+
+_ALL_METHODS = frozenset(name for names in _EXPORTS.values() for name in names)
+
+
+def _check(cond: bool, message: str) -> None:
+    if not cond:
+        raise RuntimeError(message)
+
+
+def _check_inputs(key_dim: int, tensors: tuple[Tensor, ...], names: tuple[str, ...]) -> None:
+    for x, name in zip(tensors, names):
+        _check(isinstance(x, Tensor), f"fused Bayesian {name} must be a tensor")
+        _check(x.is_cuda, "fused Bayesian inputs must be CUDA tensors")
+        _check(x.dtype == torch.float32, "fused Bayesian inputs must be float32")
+        _check(x.is_contiguous(), "fused Bayesian inputs must be contiguous")
+    k, v, q = tensors[:3]
+    _check(k.dim() == 3 and v.dim() == 3 and q.dim() == 3 and k.size(2) == key_dim and q.size(2) == key_dim
+           and v.size(2) == 8, f"fused Bayesian kernel expects [N,T,{key_dim}] keys/queries and [N,T,8] values")
+    n, t = k.shape[:2]
+    _check(tuple(v.shape[:2]) == (n, t) and tuple(q.shape[:2]) == (n, t), "keys/values/queries batch-time mismatch")
+    _check(all(x.device == k.device for x in tensors), "fused Bayesian inputs must share one device")
+
+
+class _Extension:
+    """Per-key-dim method table over the C ABI (replaces the pybind module)."""
+
+    def __init__(self, key_dim: int) -> None:
+        self.key_dim = key_dim
+        self.value_dim = 8
+        self._exports = frozenset(_EXPORTS[key_dim])
+
+    def __getattribute__(self, name: str):
+        # Methods outside this key_dim's reference export set behave as absent,
+        # so ``hasattr`` probes see the same module surface as the reference.
+        if name in _ALL_METHODS and name not in object.__getattribute__(self, "_exports"):
+            raise AttributeError(f"key_dim={object.__getattribute__(self, 'key_dim')} extension has no {name}")
+        return object.__getattribute__(self, name)
+
+    def __dir__(self):
+        return sorted(self._exports)
+
+    # -- helpers ---------------------------------------------------------
+    def _sizes(self, keys: Tensor) -> tuple[int, int]:
+        return int(keys.size(0)), int(keys.size(1))
+
+    def _forward(self, name: str, fixed: bool, keys, values, queries, decay, process, observation, mean0, cov0,
+                 chunks: int, floor: float, saved: bool = False):
+        tensors = (keys, values, queries) + (() if fixed else (decay, process, observation)) + (mean0, cov0)
+        names = ("keys", "values", "queries") + (() if fixed else ("decay", "process", "observation")) + (
+            "mean0", "cov0")
+        _check_inputs(self.key_dim, tensors, names)
+        _check(int(chunks) > 0, "fused Bayesian chunk length must be positive")
+        n, t = self._sizes(keys)
+        d, m = self.key_dim, self.value_dim
+        nb = -(-t // int(chunks))
+        opt = dict(device=keys.device, dtype=torch.float32)
+        out = torch.empty((n, t, m), **opt)
+        mf = torch.empty_like(mean0)
+        cf = torch.empty_like(cov0)
+        bm = torch.empty((n, nb + 1, d, m), **opt)
+        bc = torch.empty((n, nb + 1, d, d), **opt)
+        hist = ()
+        if saved:
+            hist = (torch.empty((n, t, d, m), **opt), torch.empty((n, t, d, d), **opt),
+                    torch.empty((n, t, d), **opt), torch.empty((n, t), **opt), torch.empty((n, t, m), **opt))
+        P = _hip.ptr
+        with torch.cuda.device(keys.device):
+            _hip.call(name, d, m, P(keys), P(values), P(queries),
+                      None if fixed else P(decay), None if fixed else P(process), None if fixed else P(observation),
+                      P(mean0), P(cov0), P(out), P(mf), P(cf), P(bm), P(bc), *[P(h) for h in hist],
+                      n, t, int(chunks), float(floor), _hip.stream_of(keys.device))
+        return [out, mf, cf, bm, bc, *hist]
+
+    def _backward(self, name: str, fixed: bool, outputs: int, keys, values, queries, decay, process, observation,
+                  mean0, cov0, bm, bc, history, gy, gmf, gcf, chunks: int, floor: float):
+        tensors = (keys, values, queries) + (() if fixed else (decay, process, observation)) + (bm, bc, gy)
+        names = ("keys", "values", "queries") + (() if fixed else ("decay", "process", "observation")) + (
+            "boundary_mean", "boundary_covariance", "grad_output")
+        _check_inputs(self.key_dim, tensors, names)
+        for extra in (gmf, gcf, *history):
+            if extra is not None:
+                _check(extra.is_cuda and extra.dtype == torch.float32 and extra.is_contiguous(),
+                       "fused Bayesian backward inputs must be contiguous CUDA float32 tensors")
+        _check(int(chunks) > 0, "fused Bayesian chunk length must be positive")
+        n, t = self._sizes(keys)
+        nb = -(-t // int(chunks))
+        d, m = self.key_dim, self.value_dim
+        _check(tuple(bm.shape) == (n, nb + 1, d, m) and tuple(bc.shape) == (n, nb + 1, d, d),
+               "boundary tensors do not match the chunk length")
+        _check(tuple(gy.shape) == (n, t, m), "grad_output must be [N,T,M]")
+        opt = dict(device=keys.device, dtype=torch.float32)
+        gk = torch.empty((n, t, d), **opt)
+        gv = torch.empty((n, t, m), **opt)
+        gq = torch.empty((n, t, d), **opt)
+        grads = [gk, gv, gq]
+        if outputs >= 6:
+            grads += [torch.empty((n, t, d), **opt), torch.empty((n, t), **opt), torch.empty((n, t), **opt)]
+        if outputs == 8:
+            grads += [torch.empty((n, d, m), **opt), torch.empty((n, d, d), **opt)]
+        P = _hip.ptr
+        with torch.cuda.device(keys.device):
+            _hip.call(name, d, m, P(keys), P(values), P(queries),
+                      None if fixed else P(decay), None if fixed else P(process), None if fixed else P(observation),
+                      P(mean0), P(cov0), P(bm), P(bc), *[P(h) for h in history], P(gy), P(gmf), P(gcf),
+                      *[P(g) for g in grads], n, t, int(chunks), float(floor), _hip.stream_of(keys.device))
+        return grads
+
+    # -- reference method names ------------------------------------------
+    def forward_chunked(self, keys, values, queries, decay, process, observation, mean0, cov0, chunks, floor):
+        return self._forward("bssm_forward_chunked", False, keys, values, queries, decay, process, observation,
+                             mean0, cov0, chunks, floor)
+
+    def forward_chunked_fixed(self, keys, values, queries, decay, process, observation, mean0, cov0, chunks, floor):
+        return self._forward("bssm_forward_chunked_fixed", True, keys, values, queries, decay, process, observation,
+                             mean0, cov0, chunks, floor)
+
+    def forward_chunked_saved(self, keys, values, queries, decay, process, observation, mean0, cov0, chunks, floor):
+        self._require("forward_chunked_saved")
+        _check(int(chunks) == int(keys.size(1)), "saved D1 history requires one full-sequence chunk")
+        return self._forward("bssm_forward_chunked_saved", False, keys, values, queries, decay, process,
+                             observation, mean0, cov0, chunks, floor, saved=True)
+
+    def backward_chunked(self, keys, values, queries, decay, process, observation, mean0, cov0, bm, bc, gy, gmf,
+                         gcf, chunks, floor):
+        return self._backward("bssm_backward_chunked", False, 8, keys, values, queries, decay, process,
+                              observation, mean0, cov0, bm, bc, (), gy, gmf, gcf, chunks, floor)
+
+    def backward_chunked_lean(self, keys, values, queries, decay, process, observation, mean0, cov0, bm, bc, gy,
+                              gmf, gcf, chunks, floor):
+        return self._backward("bssm_backward_chunked_lean", False, 3, keys, values, queries, decay, process,
+                              observation, mean0, cov0, bm, bc, (), gy, gmf, gcf, chunks, floor)
+
+    def backward_chunked_noinitial(self, keys, values, queries, decay, process, observation, mean0, cov0, bm, bc,
+                                   gy, gmf, gcf, chunks, floor):
+        self._require("backward_chunked_noinitial")
+        return self._backward("bssm_backward_chunked_noinitial", False, 6, keys, values, queries, decay, process,
+                              observation, mean0, cov0, bm, bc, (), gy, gmf, gcf, chunks, floor)
+
+    def backward_chunked_fixed(self, keys, values, queries, decay, process, observation, mean0, cov0, bm, bc, gy,
+                               gmf, gcf, chunks, floor):
+        return self._backward("bssm_backward_chunked_fixed", True, 8, keys, values, queries, decay, process,
+                              observation, mean0, cov0, bm, bc, (), gy, gmf, gcf, chunks, floor)
+
+    def backward_chunked_lean_fixed(self, keys, values, queries, decay, process, observation, mean0, cov0, bm, bc,
+                                    gy, gmf, gcf, chunks, floor):
+        return self._backward("bssm_backward_chunked_lean_fixed", True, 3, keys, values, queries, decay, process,
+                              observation, mean0, cov0, bm, bc, (), gy, gmf, gcf, chunks, floor)
+
+    def backward_chunked_noinitial_fixed(self, keys, values, queries, decay, process, observation, mean0, cov0, bm,
+                                         bc, gy, gmf, gcf, chunks, floor):
+        self._require("backward_chunked_noinitial_fixed")
+        return self._backward("bssm_backward_chunked_noinitial_fixed", True, 6, keys, values, queries, decay,
+                              process, observation, mean0, cov0, bm, bc, (), gy, gmf, gcf, chunks, floor)
+
+    def backward_chunked_saved(self, keys, values, queries, decay, process, observation, mean0, cov0, bm, bc, mp, pp,
+                               uh, bh, eh, gy, gmf, gcf, chunks, floor):
+        self._require("backward_chunked_saved")
+        return self._backward("bssm_backward_chunked_saved", False, 8, keys, values, queries, decay, process,
+                              observation, mean0, cov0, bm, bc, (mp, pp, uh, bh, eh), gy, gmf, gcf, chunks, floor)
+
+    def backward_chunked_saved_lean(self, keys, values, queries, decay, process, observation, mean0, cov0, bm, bc,
+                                    mp, pp, uh, bh, eh, gy, gmf, gcf, chunks, floor):
+        self._require("backward_chunked_saved_lean")
+        return self._backward("bssm_backward_chunked_saved_lean", False, 3, keys, values, queries, decay, process,
+                              observation, mean0, cov0, bm, bc, (mp, pp, uh, bh, eh), gy, gmf, gcf, chunks, floor)
+
+    def backward_chunked_saved_d1(self, keys, values, queries, decay, process, observation, mean0, cov0, bm, bc, mp,
+                                  pp, uh, bh, eh, gy, gmf, gcf, chunks, floor):
+        # The reference's register-only D1 reverse returns the same eight
+        # gradients as backward_chunked_saved (d1m8.cu:600-630).
+        self._require("backward_chunked_saved_d1")
+        return self._backward("bssm_backward_chunked_saved", False, 8, keys, values, queries, decay, process,
+                              observation, mean0, cov0, bm, bc, (mp, pp, uh, bh, eh), gy, gmf, gcf, chunks, floor)
+
+    def _require(self, name: str) -> None:
+        # Reached only through an explicit unbound call; mirror the missing attribute.
+        if name not in self._exports:
+            raise AttributeError(f"key_dim={self.key_dim} extension has no {name}")
+
+
+def _has(extension: Optional[_Extension], name: str) -> bool:
+    return extension is not None and name in extension._exports
+
+
+def _load_extension(key_dim: int) -> Optional[_Extension]:
+    """Extension object for ``key_dim`` or ``None`` when unsupported/disabled.
+
+    Raises ``RuntimeError`` when the prebuilt HIP library is missing or stale:
+    on a GPU the fused path must never degrade silently.
+    """
+    if os.environ.get("BAYES_SSM_DISABLE_FUSED_CUDA", "0") == "1":
+        return None
+    if key_dim not in _EXPORTS:
+        return None
+    ext = _EXTENSIONS.get(key_dim)
+    if ext is None:
+        _hip.load()
+        ext = _EXTENSIONS.setdefault(key_dim, _Extension(key_dim))
+    return ext
+
+
+def _checkpoint_interval(key_dim: int, t: int, chunk_length: int) -> int:
+    mode = os.environ.get("BAYES_SSM_HIP_CHECKPOINT", "auto").strip().lower()
+    if mode == "chunk":
+        return max(1, int(chunk_length))
+    if mode not in ("", "auto"):
+        value = int(mode)
+        if value <= 0:
+            raise ValueError("BAYES_SSM_HIP_CHECKPOINT must be 'auto', 'chunk' or a positive integer")
+        return value
+    preferred = _hip.preferred_checkpoint(key_dim)
+    return max(1, preferred if preferred > 0 else int(chunk_length))
+
+
+class _ChunkedBayesianFunction(torch.autograd.Function):
+    """Autograd boundary of the fused recurrence (slot conventions of fused_cuda.py:58-322)."""
+
+    @staticmethod
+    def forward(ctx, keys, values, queries, decay, process, observation, initial_mean, initial_covariance,
+                chunk_length, denominator_floor, fixed_dynamics):
+        extension = _load_extension(keys.shape[-1])
+        if extension is None:
+            raise RuntimeError("the fused Bayesian HIP extension is unavailable")
+        n, t, d = keys.shape
+        use_saved_history = (
+            d == 1 and not fixed_dynamics and os.environ.get("BAYES_SSM_D1_SAVED_HISTORY", "0") == "1"
+            and os.environ.get("BAYES_SSM_DISABLE_SAVED_HISTORY", "0") != "1"
+        )
+        if use_saved_history:
+            interval = max(int(t), 1)
+            (output, final_mean, final_covariance, boundary_mean, boundary_covariance, mp_history, pp_history,
+             u_history, beta_history, e_history) = extension.forward_chunked_saved(
+                keys, values, queries, decay, process, observation, initial_mean, initial_covariance, interval,
+                float(denominator_floor))
+            ctx.save_for_backward(keys, values, queries, decay, process, observation, initial_mean,
+                                  initial_covariance, boundary_mean, boundary_covariance, mp_history, pp_history,
+                                  u_history, beta_history, e_history)
+        else:
+            interval = _checkpoint_interval(d, t, chunk_length)
+            forward_impl = extension.forward_chunked_fixed if fixed_dynamics else extension.forward_chunked
+            output, final_mean, final_covariance, boundary_mean, boundary_covariance = forward_impl(
+                keys, values, queries, decay, process, observation, initial_mean, initial_covariance, interval,
+                float(denominator_floor))
+            ctx.save_for_backward(keys, values, queries, decay, process, observation, initial_mean,
+                                  initial_covariance, boundary_mean, boundary_covariance)
+        ctx.use_saved_history = use_saved_history
+        ctx.chunk_length = interval
+        ctx.denominator_floor = float(denominator_floor)
+        ctx.fixed_dynamics = bool(fixed_dynamics)
+        ctx.need_dynamics_grad = any(
+            x.requires_grad for x in (decay, process, observation, initial_mean, initial_covariance))
+        ctx.need_initial_grad = initial_mean.requires_grad or initial_covariance.requires_grad
+        ctx.noinitial_backward = False
+        ctx.mean_shape = tuple(final_mean.shape)
+        ctx.covariance_shape = tuple(final_covariance.shape)
+        ctx.output_shape = tuple(output.shape)
+        ctx.set_materialize_grads(False)
+        return output, final_mean, final_covariance
+
+    @staticmethod
+    def backward(ctx, grad_output, grad_mean, grad_covariance):
+        saved = ctx.saved_tensors
+        (keys, values, queries, decay, process, observation, initial_mean, initial_covariance, boundary_mean,
+         boundary_covariance) = saved[:10]
+        history = saved[10:]
+        extension = _load_extension(keys.shape[-1])
+        if extension is None:  # pragma: no cover - loaded in forward
+            raise RuntimeError("the fused Bayesian HIP extension is unavailable")
+        lean = not ctx.need_dynamics_grad and grad_mean is None and grad_covariance is None
+        if grad_output is None:
+            grad_output = torch.zeros(ctx.output_shape, device=keys.device, dtype=keys.dtype)
+        else:
+            grad_output = grad_output.contiguous()
+        # Null final-state gradients mean zero in the C ABI; no zero tensors needed.
+        gm = None if grad_mean is None else grad_mean.contiguous()
+        gc = None if grad_covariance is None else grad_covariance.contiguous()
+        args_head = (keys, values, queries, decay, process, observation, initial_mean, initial_covariance,
+                     boundary_mean, boundary_covariance)
+        ctx.noinitial_backward = False
+        if ctx.use_saved_history:
+            if lean:
+                backward = extension.backward_chunked_saved_lean
+            elif _has(extension, "backward_chunked_saved_d1") and \
+                    os.environ.get("BAYES_SSM_DISABLE_D1_SPECIALIZED", "0") != "1":
+                backward = extension.backward_chunked_saved_d1
+            else:
+                backward = extension.backward_chunked_saved
+            gradients = backward(*args_head, *history, grad_output, gm, gc, ctx.chunk_length, ctx.denominator_floor)
+        else:
+            if ctx.fixed_dynamics:
+                if not lean and not ctx.need_initial_grad and _has(extension, "backward_chunked_noinitial_fixed"):
+                    backward = extension.backward_chunked_noinitial_fixed
+                    ctx.noinitial_backward = True
+                else:
+                    backward = extension.backward_chunked_lean_fixed if lean else extension.backward_chunked_fixed
+            else:
+                if not lean and not ctx.need_initial_grad and _has(extension, "backward_chunked_noinitial"):
+                    backward = extension.backward_chunked_noinitial
+                    ctx.noinitial_backward = True
+                else:
+                    backward = extension.backward_chunked_lean if lean else extension.backward_chunked
+            gradients = backward(*args_head, grad_output, gm, gc, ctx.chunk_length, ctx.denominator_floor)
+        if lean:
+            # 3 tensor gradients + 5 tensor and 3 scalar non-differentiable slots.
+            return (*gradients, None, None, None, None, None, None, None, None)
+        if ctx.noinitial_backward:
+            # 6 tensor gradients + initial mean/covariance + 3 scalar slots.
+            return (*gradients, None, None, None, None, None)
+        # 8 tensor gradients + 3 scalar slots.
+        return (*gradients, None, None, None)
+
+
+def fused_diagonal_bayesian(
+    keys: Tensor,
+    values: Tensor,
+    queries: Tensor,
+    decay: Tensor,
+    process: Tensor,
+    observation: Tensor,
+    initial_mean: Tensor,
+    initial_covariance: Tensor,
+    *,
+    chunk_length: int,
+    denominator_floor: float,
+    fixed_dynamics: bool = False,
+) -> tuple[Tensor, Tensor, Tensor] | None:
+    """Run the exact HIP core when its contract holds; ``None`` means "use the torch path".
+
+    Contract (fused_cuda.py:346-371): CUDA device, 3-D fp32 tensors,
+    (D, M) in {(1,8), (2,8), (4,8), (8,8)}, decay [N,T,D], process and
+    observation [N,T], initial mean [N,D,M] and covariance [N,D,D].
+    """
+    if (
+        keys.device.type != "cuda"
+        or keys.ndim != 3
+        or values.ndim != 3
+        or queries.ndim != 3
+        or (keys.shape[-1], values.shape[-1]) not in _SUPPORTED
+        or queries.shape[-1] != keys.shape[-1]
+        or keys.shape != queries.shape
+        or values.shape[:2] != keys.shape[:2]
+        or not all(x.dtype == torch.float32 for x in (keys, values, queries, decay, process, observation,
+                                                      initial_mean, initial_covariance))
+    ):
+        return None
+    key_dim = keys.shape[-1]
+    extension = _load_extension(key_dim)
+    if extension is None:
+        return None
+    n, t, _ = keys.shape
+    if decay.shape != (n, t, key_dim) or process.shape != (n, t) or observation.shape != (n, t):
+        return None
+    value_dim = values.shape[-1]
+    if initial_mean.shape != (n, key_dim, value_dim) or initial_covariance.shape != (n, key_dim, key_dim):
+        return None
+    keys = keys.contiguous()
+    values = values.contiguous()
+    queries = queries.contiguous()
+    decay = decay.contiguous()
+    process = process.contiguous()
+    observation = observation.contiguous()
+    initial_mean = initial_mean.contiguous()
+    initial_covariance = initial_covariance.contiguous()
+    return _ChunkedBayesianFunction.apply(
+        keys, values, queries, decay, process, observation, initial_mean, initial_covariance,
+        int(chunk_length), float(denominator_floor), bool(fixed_dynamics),
+    )
+
+
+__all__ = ["fused_diagonal_bayesian"]

@@ -1,0 +1,376 @@
+// C ABI of the gfx950 Bayesian-recurrence library (declared in include/bssm.h).
+//
+// The wrappers validate arguments, derive the checkpoint count and the
+// 16-byte staging flags, and enqueue exactly one kernel per call on the
+// caller's stream.  They never allocate, synchronise or keep state, which
+// keeps every entry point usable under HIP graph capture.  Failures return a
+// BSSM_ERR_* code and leave the message for bssm_last_error() on the calling
+// thread (the reference raises through TORCH_CHECK,
+// persistent_bayes_chunked_d4m8.cu:463-466, and checks launches with
+// C10_CUDA_KERNEL_LAUNCH_CHECK, :467).
+
+#include <cstdarg>
+#include <cstdio>
+
+#include "../../include/bssm.h"
+#include "bssm_recurrence.h"
+
+namespace {
+
+thread_local char g_error[512] = "";
+
+int fail(int code, const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_error, sizeof(g_error), fmt, ap);
+  va_end(ap);
+  return code;
+}
+
+int ok() {
+  g_error[0] = '\0';
+  return BSSM_OK;
+}
+
+bool supported(int d, int m) { return m == 8 && (d == 1 || d == 2 || d == 4 || d == 8); }
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+// 16-byte staging is valid when every sequence row of the stream starts on a
+// 16-byte boundary: base aligned and (T * width) a multiple of 4 floats.
+int vec_flag(const float* p, int64_t t, int64_t width) {
+  return (p == nullptr || aligned16(p)) && ((t * width) % 4 == 0);
+}
+
+int check_common(const char* fn, int d, int m, int64_t n, int64_t t, int64_t chunk, float floor) {
+  if (!supported(d, m))
+    return fail(BSSM_ERR_UNSUPPORTED, "%s: unsupported (key_dim, value_dim) = (%d, %d)", fn, d, m);
+  if (n < 0 || t < 0) return fail(BSSM_ERR_ARGUMENT, "%s: negative size n=%lld t=%lld", fn, (long long)n, (long long)t);
+  if (chunk <= 0) return fail(BSSM_ERR_ARGUMENT, "%s: chunk must be positive, got %lld", fn, (long long)chunk);
+  if (!(floor > 0.f)) return fail(BSSM_ERR_ARGUMENT, "%s: denominator_floor must be positive", fn);
+  if (n > (int64_t)0x7fffffff * 4) return fail(BSSM_ERR_ARGUMENT, "%s: n too large", fn);
+  return BSSM_OK;
+}
+
+#define BSSM_REQUIRE(ptr)                                                          \
+  do {                                                                             \
+    if ((ptr) == nullptr && n > 0) return fail(BSSM_ERR_ARGUMENT, "%s: %s is null", fn, #ptr); \
+  } while (0)
+
+#define BSSM_REQUIRE_T(ptr)                                                                   \
+  do {                                                                                        \
+    if ((ptr) == nullptr && n > 0 && t > 0) return fail(BSSM_ERR_ARGUMENT, "%s: %s is null", fn, #ptr); \
+  } while (0)
+
+int launched(const char* fn, hipError_t err) {
+  if (err != hipSuccess) return fail(BSSM_ERR_LAUNCH, "%s: kernel launch failed: %s", fn, hipGetErrorString(err));
+  return ok();
+}
+
+int forward_impl(const char* fn, bool fixed, int d, int m, const float* keys, const float* values,
+                 const float* queries, const float* decay, const float* process, const float* observation,
+                 const float* mean0, const float* cov0, float* out, float* mean_final, float* cov_final,
+                 float* bmean, float* bcov, int64_t n, int64_t t, int64_t chunk, float floor, void* stream) {
+  if (int rc = check_common(fn, d, m, n, t, chunk, floor)) return rc;
+  BSSM_REQUIRE_T(keys);
+  BSSM_REQUIRE_T(values);
+  BSSM_REQUIRE_T(queries);
+  BSSM_REQUIRE_T(out);
+  if (!fixed) {
+    BSSM_REQUIRE_T(decay);
+    BSSM_REQUIRE_T(process);
+    BSSM_REQUIRE_T(observation);
+  }
+  BSSM_REQUIRE(mean0);
+  BSSM_REQUIRE(cov0);
+  BSSM_REQUIRE(mean_final);
+  BSSM_REQUIRE(cov_final);
+  BSSM_REQUIRE(bmean);
+  BSSM_REQUIRE(bcov);
+  bssm::FwdArgs a{};
+  a.k = keys; a.v = values; a.q = queries; a.d = decay; a.p = process; a.r = observation;
+  a.m0 = mean0; a.c0 = cov0; a.y = out; a.mT = mean_final; a.cT = cov_final; a.bm = bmean; a.bc = bcov;
+  a.n = n; a.t = t; a.chunk = chunk; a.nb = (t + chunk - 1) / chunk; a.floor = floor;
+  a.vec_kqd = vec_flag(keys, t, d) && vec_flag(queries, t, d) && (fixed || vec_flag(decay, t, d));
+  a.vec_v = vec_flag(values, t, m) && vec_flag(out, t, m);
+  a.vec_pr = fixed || (vec_flag(process, t, 1) && vec_flag(observation, t, 1));
+  if (n == 0) return ok();
+  return launched(fn, bssm::launch_forward(d, fixed, a, static_cast<hipStream_t>(stream)));
+}
+
+struct BwdOut {
+  float *gk, *gv, *gq, *gd, *gp, *gr, *gm0, *gc0;
+};
+
+int backward_impl(const char* fn, bool fixed, bool dyn, int d, int m, const float* keys, const float* values,
+                  const float* queries, const float* decay, const float* process, const float* observation,
+                  const float* mean0, const float* cov0, const float* bmean, const float* bcov, const float* gy,
+                  const float* gmf, const float* gcf, BwdOut o, int64_t n, int64_t t, int64_t chunk, float floor,
+                  void* stream) {
+  if (int rc = check_common(fn, d, m, n, t, chunk, floor)) return rc;
+  BSSM_REQUIRE_T(keys);
+  BSSM_REQUIRE_T(values);
+  BSSM_REQUIRE_T(queries);
+  BSSM_REQUIRE_T(gy);
+  if (!fixed) {
+    BSSM_REQUIRE_T(decay);
+    BSSM_REQUIRE_T(process);
+    BSSM_REQUIRE_T(observation);
+  }
+  BSSM_REQUIRE(bmean);
+  BSSM_REQUIRE(bcov);
+  BSSM_REQUIRE_T(o.gk);
+  BSSM_REQUIRE_T(o.gv);
+  BSSM_REQUIRE_T(o.gq);
+  bssm::BwdArgs a{};
+  a.k = keys; a.v = values; a.q = queries; a.d = decay; a.p = process; a.r = observation;
+  a.m0 = mean0; a.c0 = cov0; a.bm = bmean; a.bc = bcov; a.gy = gy; a.gmf = gmf; a.gcf = gcf;
+  a.gk = o.gk; a.gv = o.gv; a.gq = o.gq; a.gd = o.gd; a.gp = o.gp; a.gr = o.gr; a.gm0 = o.gm0; a.gc0 = o.gc0;
+  a.n = n; a.t = t; a.chunk = chunk; a.nb = (t + chunk - 1) / chunk; a.floor = floor;
+  a.vec_kqd = vec_flag(keys, t, d) && vec_flag(queries, t, d) && (fixed || vec_flag(decay, t, d)) &&
+              vec_flag(o.gk, t, d) && vec_flag(o.gq, t, d) && vec_flag(o.gd, t, d);
+  a.vec_v = vec_flag(values, t, m) && vec_flag(gy, t, m) && vec_flag(o.gv, t, m);
+  a.vec_pr = (fixed || (vec_flag(process, t, 1) && vec_flag(observation, t, 1))) && vec_flag(o.gp, t, 1) &&
+             vec_flag(o.gr, t, 1);
+  if (n == 0) return ok();
+  return launched(fn, bssm::launch_backward(d, fixed, dyn, a, static_cast<hipStream_t>(stream)));
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* bssm_last_error(void) { return g_error; }
+
+int bssm_abi_version(void) { return 1; }
+
+int bssm_supported(int key_dim, int value_dim) { return supported(key_dim, value_dim) ? 1 : 0; }
+
+int bssm_preferred_checkpoint(int key_dim) { return bssm::preferred_checkpoint(key_dim); }
+
+int bssm_forward_chunked(int key_dim, int value_dim, const float* keys, const float* values, const float* queries,
+                         const float* decay, const float* process, const float* observation, const float* mean0,
+                         const float* cov0, float* out, float* mean_final, float* cov_final, float* bmean,
+                         float* bcov, int64_t n, int64_t t, int64_t chunk, float denominator_floor, void* stream) {
+  return forward_impl("bssm_forward_chunked", false, key_dim, value_dim, keys, values, queries, decay, process,
+                      observation, mean0, cov0, out, mean_final, cov_final, bmean, bcov, n, t, chunk,
+                      denominator_floor, stream);
+}
+
+int bssm_forward_chunked_fixed(int key_dim, int value_dim, const float* keys, const float* values,
+                               const float* queries, const float* decay, const float* process,
+                               const float* observation, const float* mean0, const float* cov0, float* out,
+                               float* mean_final, float* cov_final, float* bmean, float* bcov, int64_t n, int64_t t,
+                               int64_t chunk, float denominator_floor, void* stream) {
+  return forward_impl("bssm_forward_chunked_fixed", true, key_dim, value_dim, keys, values, queries, decay, process,
+                      observation, mean0, cov0, out, mean_final, cov_final, bmean, bcov, n, t, chunk,
+                      denominator_floor, stream);
+}
+
+int bssm_backward_chunked(int key_dim, int value_dim, const float* keys, const float* values, const float* queries,
+                          const float* decay, const float* process, const float* observation, const float* mean0,
+                          const float* cov0, const float* bmean, const float* bcov, const float* gy,
+                          const float* gmf, const float* gcf, float* gk, float* gv, float* gq, float* gd, float* gp,
+                          float* gr, float* gm0, float* gc0, int64_t n, int64_t t, int64_t chunk,
+                          float denominator_floor, void* stream) {
+  const char* fn = "bssm_backward_chunked";
+  if (n > 0 && (gm0 == nullptr || gc0 == nullptr || (t > 0 && (gd == nullptr || gp == nullptr || gr == nullptr))))
+    return fail(BSSM_ERR_ARGUMENT, "%s: all eight gradient outputs are required", fn);
+  return backward_impl(fn, false, true, key_dim, value_dim, keys, values, queries, decay, process, observation,
+                       mean0, cov0, bmean, bcov, gy, gmf, gcf, BwdOut{gk, gv, gq, gd, gp, gr, gm0, gc0}, n, t,
+                       chunk, denominator_floor, stream);
+}
+
+int bssm_backward_chunked_lean(int key_dim, int value_dim, const float* keys, const float* values,
+                               const float* queries, const float* decay, const float* process,
+                               const float* observation, const float* mean0, const float* cov0, const float* bmean,
+                               const float* bcov, const float* gy, const float* gmf, const float* gcf, float* gk,
+                               float* gv, float* gq, int64_t n, int64_t t, int64_t chunk, float denominator_floor,
+                               void* stream) {
+  return backward_impl("bssm_backward_chunked_lean", false, false, key_dim, value_dim, keys, values, queries, decay,
+                       process, observation, mean0, cov0, bmean, bcov, gy, gmf, gcf,
+                       BwdOut{gk, gv, gq, nullptr, nullptr, nullptr, nullptr, nullptr}, n, t, chunk,
+                       denominator_floor, stream);
+}
+
+int bssm_backward_chunked_noinitial(int key_dim, int value_dim, const float* keys, const float* values,
+                                    const float* queries, const float* decay, const float* process,
+                                    const float* observation, const float* mean0, const float* cov0,
+                                    const float* bmean, const float* bcov, const float* gy, const float* gmf,
+                                    const float* gcf, float* gk, float* gv, float* gq, float* gd, float* gp,
+                                    float* gr, int64_t n, int64_t t, int64_t chunk, float denominator_floor,
+                                    void* stream) {
+  const char* fn = "bssm_backward_chunked_noinitial";
+  if (n > 0 && t > 0 && (gd == nullptr || gp == nullptr || gr == nullptr))
+    return fail(BSSM_ERR_ARGUMENT, "%s: gd, gp and gr are required", fn);
+  return backward_impl(fn, false, true, key_dim, value_dim, keys, values, queries, decay, process, observation,
+                       mean0, cov0, bmean, bcov, gy, gmf, gcf, BwdOut{gk, gv, gq, gd, gp, gr, nullptr, nullptr}, n,
+                       t, chunk, denominator_floor, stream);
+}
+
+int bssm_backward_chunked_fixed(int key_dim, int value_dim, const float* keys, const float* values,
+                                const float* queries, const float* decay, const float* process,
+                                const float* observation, const float* mean0, const float* cov0, const float* bmean,
+                                const float* bcov, const float* gy, const float* gmf, const float* gcf, float* gk,
+                                float* gv, float* gq, float* gd, float* gp, float* gr, float* gm0, float* gc0,
+                                int64_t n, int64_t t, int64_t chunk, float denominator_floor, void* stream) {
+  const char* fn = "bssm_backward_chunked_fixed";
+  if (n > 0 && (gm0 == nullptr || gc0 == nullptr || (t > 0 && (gd == nullptr || gp == nullptr || gr == nullptr))))
+    return fail(BSSM_ERR_ARGUMENT, "%s: all eight gradient outputs are required", fn);
+  return backward_impl(fn, true, false, key_dim, value_dim, keys, values, queries, decay, process, observation,
+                       mean0, cov0, bmean, bcov, gy, gmf, gcf, BwdOut{gk, gv, gq, gd, gp, gr, gm0, gc0}, n, t,
+                       chunk, denominator_floor, stream);
+}
+
+int bssm_backward_chunked_lean_fixed(int key_dim, int value_dim, const float* keys, const float* values,
+                                     const float* queries, const float* decay, const float* process,
+                                     const float* observation, const float* mean0, const float* cov0,
+                                     const float* bmean, const float* bcov, const float* gy, const float* gmf,
+                                     const float* gcf, float* gk, float* gv, float* gq, int64_t n, int64_t t,
+                                     int64_t chunk, float denominator_floor, void* stream) {
+  return backward_impl("bssm_backward_chunked_lean_fixed", true, false, key_dim, value_dim, keys, values, queries,
+                       decay, process, observation, mean0, cov0, bmean, bcov, gy, gmf, gcf,
+                       BwdOut{gk, gv, gq, nullptr, nullptr, nullptr, nullptr, nullptr}, n, t, chunk,
+                       denominator_floor, stream);
+}
+
+int bssm_backward_chunked_noinitial_fixed(int key_dim, int value_dim, const float* keys, const float* values,
+                                          const float* queries, const float* decay, const float* process,
+                                          const float* observation, const float* mean0, const float* cov0,
+                                          const float* bmean, const float* bcov, const float* gy, const float* gmf,
+                                          const float* gcf, float* gk, float* gv, float* gq, float* gd, float* gp,
+                                          float* gr, int64_t n, int64_t t, int64_t chunk, float denominator_floor,
+                                          void* stream) {
+  const char* fn = "bssm_backward_chunked_noinitial_fixed";
+  if (n > 0 && t > 0 && (gd == nullptr || gp == nullptr || gr == nullptr))
+    return fail(BSSM_ERR_ARGUMENT, "%s: gd, gp and gr are required", fn);
+  return backward_impl(fn, true, false, key_dim, value_dim, keys, values, queries, decay, process, observation,
+                       mean0, cov0, bmean, bcov, gy, gmf, gcf, BwdOut{gk, gv, gq, gd, gp, gr, nullptr, nullptr}, n,
+                       t, chunk, denominator_floor, stream);
+}
+
+int bssm_forward_chunked_saved(int key_dim, int value_dim, const float* keys, const float* values,
+                               const float* queries, const float* decay, const float* process,
+                               const float* observation, const float* mean0, const float* cov0, float* out,
+                               float* mean_final, float* cov_final, float* bmean, float* bcov, float* mp, float* pp,
+                               float* uh, float* bh, float* eh, int64_t n, int64_t t, int64_t chunk,
+                               float denominator_floor, void* stream) {
+  const char* fn = "bssm_forward_chunked_saved";
+  if (int rc = check_common(fn, key_dim, value_dim, n, t, chunk, denominator_floor)) return rc;
+  if (chunk != t) return fail(BSSM_ERR_ARGUMENT, "%s: saved history requires one full-sequence chunk", fn);
+  BSSM_REQUIRE_T(mp);
+  BSSM_REQUIRE_T(pp);
+  BSSM_REQUIRE_T(uh);
+  BSSM_REQUIRE_T(bh);
+  BSSM_REQUIRE_T(eh);
+  BSSM_REQUIRE_T(keys);
+  BSSM_REQUIRE_T(values);
+  BSSM_REQUIRE_T(queries);
+  BSSM_REQUIRE_T(decay);
+  BSSM_REQUIRE_T(process);
+  BSSM_REQUIRE_T(observation);
+  BSSM_REQUIRE_T(out);
+  BSSM_REQUIRE(mean0);
+  BSSM_REQUIRE(cov0);
+  BSSM_REQUIRE(mean_final);
+  BSSM_REQUIRE(cov_final);
+  BSSM_REQUIRE(bmean);
+  BSSM_REQUIRE(bcov);
+  bssm::FwdArgs a{};
+  a.k = keys; a.v = values; a.q = queries; a.d = decay; a.p = process; a.r = observation;
+  a.m0 = mean0; a.c0 = cov0; a.y = out; a.mT = mean_final; a.cT = cov_final; a.bm = bmean; a.bc = bcov;
+  a.n = n; a.t = t; a.chunk = chunk; a.nb = (t + chunk - 1) / chunk; a.floor = denominator_floor;
+  bssm::HistArgs h{mp, pp, uh, bh, eh};
+  if (n == 0) return ok();
+  return launched(fn, bssm::launch_forward_saved(key_dim, a, h, static_cast<hipStream_t>(stream)));
+}
+
+static int backward_saved_impl(const char* fn, bool dyn, int key_dim, int value_dim, const float* keys,
+                               const float* values, const float* queries, const float* decay, const float* process,
+                               const float* observation, const float* mean0, const float* cov0, const float* bmean,
+                               const float* bcov, const float* mp, const float* pp, const float* uh, const float* bh,
+                               const float* eh, const float* gy, const float* gmf, const float* gcf, BwdOut o,
+                               int64_t n, int64_t t, int64_t chunk, float floor, void* stream) {
+  if (int rc = check_common(fn, key_dim, value_dim, n, t, chunk, floor)) return rc;
+  if (chunk != t) return fail(BSSM_ERR_ARGUMENT, "%s: saved history requires one full-sequence chunk", fn);
+  BSSM_REQUIRE_T(mp);
+  BSSM_REQUIRE_T(pp);
+  BSSM_REQUIRE_T(uh);
+  BSSM_REQUIRE_T(bh);
+  BSSM_REQUIRE_T(eh);
+  BSSM_REQUIRE_T(keys);
+  BSSM_REQUIRE_T(queries);
+  BSSM_REQUIRE_T(decay);
+  BSSM_REQUIRE_T(process);
+  BSSM_REQUIRE_T(observation);
+  BSSM_REQUIRE_T(gy);
+  BSSM_REQUIRE(bmean);
+  BSSM_REQUIRE(bcov);
+  BSSM_REQUIRE_T(o.gk);
+  BSSM_REQUIRE_T(o.gv);
+  BSSM_REQUIRE_T(o.gq);
+  bssm::BwdArgs a{};
+  a.k = keys; a.v = values; a.q = queries; a.d = decay; a.p = process; a.r = observation;
+  a.m0 = mean0; a.c0 = cov0; a.bm = bmean; a.bc = bcov; a.gy = gy; a.gmf = gmf; a.gcf = gcf;
+  a.gk = o.gk; a.gv = o.gv; a.gq = o.gq; a.gd = o.gd; a.gp = o.gp; a.gr = o.gr; a.gm0 = o.gm0; a.gc0 = o.gc0;
+  a.n = n; a.t = t; a.chunk = chunk; a.nb = (t + chunk - 1) / chunk; a.floor = floor;
+  bssm::HistArgs h{const_cast<float*>(mp), const_cast<float*>(pp), const_cast<float*>(uh), const_cast<float*>(bh),
+                   const_cast<float*>(eh)};
+  if (n == 0) return ok();
+  return launched(fn, bssm::launch_backward_saved(key_dim, dyn, a, h, static_cast<hipStream_t>(stream)));
+}
+
+int bssm_backward_chunked_saved(int key_dim, int value_dim, const float* keys, const float* values,
+                                const float* queries, const float* decay, const float* process,
+                                const float* observation, const float* mean0, const float* cov0, const float* bmean,
+                                const float* bcov, const float* mp, const float* pp, const float* uh, const float* bh,
+                                const float* eh, const float* gy, const float* gmf, const float* gcf, float* gk,
+                                float* gv, float* gq, float* gd, float* gp, float* gr, float* gm0, float* gc0,
+                                int64_t n, int64_t t, int64_t chunk, float denominator_floor, void* stream) {
+  const char* fn = "bssm_backward_chunked_saved";
+  if (n > 0 && (gm0 == nullptr || gc0 == nullptr || (t > 0 && (gd == nullptr || gp == nullptr || gr == nullptr))))
+    return fail(BSSM_ERR_ARGUMENT, "%s: all eight gradient outputs are required", fn);
+  return backward_saved_impl(fn, true, key_dim, value_dim, keys, values, queries, decay, process, observation, mean0,
+                             cov0, bmean, bcov, mp, pp, uh, bh, eh, gy, gmf, gcf,
+                             BwdOut{gk, gv, gq, gd, gp, gr, gm0, gc0}, n, t, chunk, denominator_floor, stream);
+}
+
+int bssm_backward_chunked_saved_lean(int key_dim, int value_dim, const float* keys, const float* values,
+                                     const float* queries, const float* decay, const float* process,
+                                     const float* observation, const float* mean0, const float* cov0,
+                                     const float* bmean, const float* bcov, const float* mp, const float* pp,
+                                     const float* uh, const float* bh, const float* eh, const float* gy,
+                                     const float* gmf, const float* gcf, float* gk, float* gv, float* gq, int64_t n,
+                                     int64_t t, int64_t chunk, float denominator_floor, void* stream) {
+  return backward_saved_impl("bssm_backward_chunked_saved_lean", false, key_dim, value_dim, keys, values, queries,
+                             decay, process, observation, mean0, cov0, bmean, bcov, mp, pp, uh, bh, eh, gy, gmf, gcf,
+                             BwdOut{gk, gv, gq, nullptr, nullptr, nullptr, nullptr, nullptr}, n, t, chunk,
+                             denominator_floor, stream);
+}
+
+int bssm_associative_static_scan(const float* keys, const float* values, const float* queries,
+                                 const float* observation, const float* mean0, const float* cov0, float* out,
+                                 float* mean_final, float* cov_final, int64_t b, int64_t t, int key_dim,
+                                 int value_dim, void* stream) {
+  const char* fn = "bssm_associative_static_scan";
+  if (key_dim <= 0 || key_dim > 32 || value_dim <= 0 || value_dim > 64)
+    return fail(BSSM_ERR_UNSUPPORTED, "%s: needs 0 < key_dim <= 32 and 0 < value_dim <= 64, got (%d, %d)", fn,
+                key_dim, value_dim);
+  if (b < 0 || t < 0) return fail(BSSM_ERR_ARGUMENT, "%s: negative size", fn);
+  if (b > 65535 || t > 0x7fffffff) return fail(BSSM_ERR_ARGUMENT, "%s: b or t too large", fn);
+  const int64_t n = b;
+  BSSM_REQUIRE(mean0);
+  BSSM_REQUIRE(cov0);
+  BSSM_REQUIRE(mean_final);
+  BSSM_REQUIRE(cov_final);
+  BSSM_REQUIRE_T(keys);
+  BSSM_REQUIRE_T(values);
+  BSSM_REQUIRE_T(queries);
+  BSSM_REQUIRE_T(observation);
+  BSSM_REQUIRE_T(out);
+  return launched(fn, bssm::launch_associative_scan(keys, values, queries, observation, mean0, cov0, out, mean_final,
+                                                    cov_final, b, t, key_dim, value_dim,
+                                                    static_cast<hipStream_t>(stream)));
+}
+
+}  // extern "C"

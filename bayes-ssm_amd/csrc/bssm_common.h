@@ -1,0 +1,210 @@
+// Device primitives shared by the gfx950 Bayesian-recurrence kernels.
+//
+// Work decomposition used by every recurrence kernel: one wave64 per
+// workgroup; a *group* of G adjacent lanes owns one sequence.  Inside a group
+// the value columns of the mean are split into contiguous blocks of M/G
+// columns per lane, and the covariance rows are split round-robin
+// (row r lives in lane r % G when D >= G; with D < G the rows are replicated
+// and lane g owns row g % D).  All cross-lane traffic inside a group uses DPP
+// (quad permutes / half-row mirror) so it stays on the VALU and never touches
+// LDS or memory.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace bssm {
+
+constexpr int kWave = 64;
+
+// ---------------------------------------------------------------- DPP moves
+// dpp_ctrl encodings (gfx9 family): quad_perm = 8-bit lane selector,
+// row_shl/shr/ror = 0x100 + n, row_mirror = 0x140, row_half_mirror = 0x141.
+template <int CTRL>
+__device__ __forceinline__ float dpp(float x) {
+  return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), CTRL, 0xF, 0xF, false));
+}
+
+constexpr int quad_perm(int a, int b, int c, int d) { return a | (b << 2) | (c << 4) | (d << 6); }
+constexpr int kXor1 = quad_perm(1, 0, 3, 2);
+constexpr int kXor2 = quad_perm(2, 3, 0, 1);
+constexpr int kHalfMirror = 0x141;  // lane l <- lane 7-l inside each 8-lane half-row
+
+// Value of lane (l ^ (1 << B)).  B = 0, 1 are single DPP quad permutes; B = 2
+// (8-lane groups) goes through the cross-lane permute unit.
+template <int B>
+__device__ __forceinline__ float xor_lane(float x) {
+  if constexpr (B == 0) return dpp<kXor1>(x);
+  else if constexpr (B == 1) return dpp<kXor2>(x);
+  else return __shfl_xor(x, 1 << B, kWave);
+}
+
+// Sum over the G lanes of the caller's group; every lane of the group gets
+// the bitwise-identical result (each step adds two commuted operands).
+template <int G>
+__device__ __forceinline__ float group_sum(float x) {
+  static_assert(G == 1 || G == 2 || G == 4 || G == 8, "group size");
+  if constexpr (G >= 2) x += dpp<kXor1>(x);
+  if constexpr (G >= 4) x += dpp<kXor2>(x);
+  if constexpr (G >= 8) x += dpp<kHalfMirror>(x);
+  return x;
+}
+
+// Value held by lane SRC of the caller's group.
+template <int G, int SRC>
+__device__ __forceinline__ float group_bcast(float x, int lane) {
+  static_assert(SRC >= 0 && SRC < G, "source lane");
+  if constexpr (G == 1) {
+    return x;
+  } else if constexpr (G == 2) {
+    return dpp<quad_perm(SRC, SRC, 2 + SRC, 2 + SRC)>(x);
+  } else if constexpr (G == 4) {
+    return dpp<quad_perm(SRC, SRC, SRC, SRC)>(x);
+  } else {
+    // Broadcast inside each quad, then take the mirrored half for the quad
+    // that does not contain SRC.
+    constexpr int q = SRC & 3;
+    const float y = dpp<quad_perm(q, q, q, q)>(x);
+    const float z = dpp<kHalfMirror>(y);
+    return (((lane >> 2) & 1) == (SRC >> 2)) ? y : z;
+  }
+}
+
+// ------------------------------------------------------ row/column ownership
+template <int D, int M, int G>
+struct Layout {
+  static_assert(M % G == 0, "value columns must split evenly over the group");
+  static constexpr int SPW = kWave / G;             // sequences per wave
+  static constexpr int CPL = M / G;                 // value columns per lane
+  static constexpr int RPL = (D >= G) ? D / G : 1;  // covariance rows per lane
+  static constexpr int OWNERS = (D >= G) ? G : D;   // lanes that own distinct rows
+  // Row of slot jj for lane g.
+  static __device__ __forceinline__ int row(int g, int jj) { return (D >= G) ? g + G * jj : g % D; }
+  // Lane (within the group) and slot holding row r.
+  static constexpr int owner(int r) { return (D >= G) ? r % G : r; }
+  static constexpr int slot(int r) { return (D >= G) ? r / G : 0; }
+  // Lanes that write per-row outputs (one writer per row).
+  static __device__ __forceinline__ bool row_writer(int g) { return (D >= G) || g < D; }
+};
+
+// Per-lane register arrays: own covariance rows, and all rows x own columns.
+template <int D, int M, int G>
+using RowsArr = float[Layout<D, M, G>::RPL][D];
+template <int D, int M, int G>
+using ColsArr = float[D][Layout<D, M, G>::CPL];
+template <int D, int M, int G>
+using OwnRowVec = float[Layout<D, M, G>::RPL];
+
+// Every lane contributes a partial x[r] for each row r; returns the group
+// total of the lane's own rows (own[jj] = sum over lanes of x[row(g, jj)]).
+// Recursive halving: log2(min(G, D)) exchange stages, then plain all-reduce
+// stages when rows are replicated (G > D).
+template <int D, int G>
+__device__ __forceinline__ void group_reduce_rows(const float (&x)[D], float (&own)[(D >= G) ? D / G : 1],
+                                                  int g) {
+  constexpr int RS = (D >= G) ? G : D;  // lanes taking part in the scatter
+  float cur[D];
+#pragma unroll
+  for (int r = 0; r < D; ++r) cur[r] = x[r];
+  int width = D;
+#pragma unroll
+  for (int b = 0; (1 << b) < RS; ++b) {
+    const bool hi = (g >> b) & 1;
+#pragma unroll
+    for (int m = 0; m < D / 2; ++m) {
+      if (2 * m + 1 < width) {
+        const float lo_v = cur[2 * m], hi_v = cur[2 * m + 1];
+        const float send = hi ? lo_v : hi_v;
+        const float keep = hi ? hi_v : lo_v;
+        float recv;
+        if (b == 0) recv = xor_lane<0>(send);
+        else if (b == 1) recv = xor_lane<1>(send);
+        else recv = xor_lane<2>(send);
+        cur[m] = keep + recv;
+      }
+    }
+    width >>= 1;
+  }
+  if constexpr (G > D) {
+    // Replicated rows: finish with an all-reduce over the copies.
+#pragma unroll
+    for (int b = 0; (1 << b) < G; ++b) {
+      if ((1 << b) >= D) {
+        if (b == 0) cur[0] += xor_lane<0>(cur[0]);
+        else if (b == 1) cur[0] += xor_lane<1>(cur[0]);
+        else cur[0] += xor_lane<2>(cur[0]);
+      }
+    }
+  }
+#pragma unroll
+  for (int jj = 0; jj < ((D >= G) ? D / G : 1); ++jj) own[jj] = cur[jj];
+}
+
+__device__ __forceinline__ float fast_rcp(float x) { return __builtin_amdgcn_rcpf(x); }
+
+// ---------------------------------------------------------- tile staging
+// A tile holds TT tokens of SPW sequences for one stream of W floats per
+// token.  In LDS, sequence s occupies [s * stride, s * stride + TT * W) with
+// stride = TT * W + 4, so per-token reads of 16 different sequences do not
+// land in the same LDS banks.
+template <int W, int TT>
+struct Tile {
+  static constexpr int PER = TT * W;
+  static constexpr int STRIDE = PER + 4;
+};
+
+// Global -> LDS copy of one tile (tokens [t0, t0 + len) of sequences
+// [n0, n0 + SPW)).  Rows past N and tokens past len are zero-filled so idle
+// lanes compute on finite data.  `vec` selects 16-byte accesses; it must only
+// be set when every accessed 4-float group is 16-byte aligned.
+template <int W, int TT, int SPW>
+__device__ __forceinline__ void stage_in(float* __restrict__ lds, const float* __restrict__ g, int64_t n0,
+                                         int64_t n, int64_t t, int64_t t0, int len, bool vec, int lane) {
+  using T_ = Tile<W, TT>;
+  constexpr int TOTAL = SPW * T_::PER;
+  const int valid = len * W;
+  if (vec) {
+#pragma unroll
+    for (int e = lane * 4; e < TOTAL; e += kWave * 4) {
+      const int s = e / T_::PER, o = e - s * T_::PER;
+      float4 val = make_float4(0.f, 0.f, 0.f, 0.f);
+      if (n0 + s < n && o < valid)
+        val = *reinterpret_cast<const float4*>(g + ((n0 + s) * t + t0) * W + o);
+      *reinterpret_cast<float4*>(lds + s * T_::STRIDE + o) = val;
+    }
+  } else {
+#pragma unroll
+    for (int e = lane; e < TOTAL; e += kWave) {
+      const int s = e / T_::PER, o = e - s * T_::PER;
+      float val = 0.f;
+      if (n0 + s < n && o < valid) val = g[((n0 + s) * t + t0) * W + o];
+      lds[s * T_::STRIDE + o] = val;
+    }
+  }
+}
+
+// LDS -> global copy of the first len tokens of a tile.
+template <int W, int TT, int SPW>
+__device__ __forceinline__ void stage_out(const float* __restrict__ lds, float* __restrict__ g, int64_t n0,
+                                          int64_t n, int64_t t, int64_t t0, int len, bool vec, int lane) {
+  using T_ = Tile<W, TT>;
+  constexpr int TOTAL = SPW * T_::PER;
+  const int valid = len * W;
+  if (vec) {
+#pragma unroll
+    for (int e = lane * 4; e < TOTAL; e += kWave * 4) {
+      const int s = e / T_::PER, o = e - s * T_::PER;
+      if (n0 + s < n && o < valid)
+        *reinterpret_cast<float4*>(g + ((n0 + s) * t + t0) * W + o) =
+            *reinterpret_cast<const float4*>(lds + s * T_::STRIDE + o);
+    }
+  } else {
+#pragma unroll
+    for (int e = lane; e < TOTAL; e += kWave) {
+      const int s = e / T_::PER, o = e - s * T_::PER;
+      if (n0 + s < n && o < valid) g[((n0 + s) * t + t0) * W + o] = lds[s * T_::STRIDE + o];
+    }
+  }
+}
+
+}  // namespace bssm

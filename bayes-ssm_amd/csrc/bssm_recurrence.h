@@ -1,0 +1,83 @@
+// Internal launch interface between the C ABI (bssm_capi.hip) and the
+// recurrence kernels (bssm_recurrence.hip).
+#pragma once
+
+#include "bssm_common.h"
+
+namespace bssm {
+
+struct FwdArgs {
+  const float* k;
+  const float* v;
+  const float* q;
+  const float* d;
+  const float* p;
+  const float* r;
+  const float* m0;
+  const float* c0;
+  float* y;
+  float* mT;
+  float* cT;
+  float* bm;
+  float* bc;
+  int64_t n;
+  int64_t t;
+  int64_t chunk;
+  int64_t nb;
+  float floor;
+  int vec_kqd, vec_v, vec_pr;  // 16-byte staging allowed per stream class
+};
+
+struct BwdArgs {
+  const float* k;
+  const float* v;
+  const float* q;
+  const float* d;
+  const float* p;
+  const float* r;
+  const float* m0;
+  const float* c0;
+  const float* bm;
+  const float* bc;
+  const float* gy;
+  const float* gmf;  // may be null (zero)
+  const float* gcf;  // may be null (zero)
+  float* gk;
+  float* gv;
+  float* gq;
+  float* gd;   // null: not requested
+  float* gp;   // null: not requested
+  float* gr;   // null: not requested
+  float* gm0;  // null: not requested
+  float* gc0;  // null: not requested
+  int64_t n;
+  int64_t t;
+  int64_t chunk;
+  int64_t nb;
+  float floor;
+  int vec_kqd, vec_v, vec_pr;
+};
+
+// Replay-history tensors of the saved-history ABI.
+struct HistArgs {
+  float* mp;  // [N,T,D,M] decay * mean before the token
+  float* pp;  // [N,T,D,D] predicted covariance
+  float* uh;  // [N,T,D]
+  float* bh;  // [N,T]    1 / max(s, floor)
+  float* eh;  // [N,T,M]
+};
+
+hipError_t launch_forward(int key_dim, bool fixed, const FwdArgs& a, hipStream_t stream);
+hipError_t launch_backward(int key_dim, bool fixed, bool dynamics_grads, const BwdArgs& a, hipStream_t stream);
+hipError_t launch_forward_saved(int key_dim, const FwdArgs& a, const HistArgs& h, hipStream_t stream);
+hipError_t launch_backward_saved(int key_dim, bool dynamics_grads, const BwdArgs& a, const HistArgs& h,
+                                 hipStream_t stream);
+hipError_t launch_associative_scan(const float* k, const float* v, const float* q, const float* r,
+                                   const float* m0, const float* c0, float* y, float* mT, float* cT,
+                                   int64_t b, int64_t t, int d, int m, hipStream_t stream);
+
+// Checkpoint interval at which the replay backward needs no in-chunk replay
+// restarts (the register-history length for this key dimension).
+int preferred_checkpoint(int key_dim);
+
+}  // namespace bssm

@@ -1,0 +1,213 @@
+#!/usr/bin/env python3
+"""Bayes-layer fwd+bwd throughput on one MI355X (BASELINE.json metric).
+
+Workload (config 3): B=256, T=512, H=64 heads -> N = B*H = 16384 sequences,
+D=4 key dims, M=8 value columns, chunk length 64, fp32 state.  Inputs are
+synthetic (seeded): k, v, q ~ N(0,1) rounded through bf16, decay =
+sigmoid(N(2,1)), process = softplus(N(-3,1)), observation = 1e-4 +
+softplus(N(0,1)); all six require grad (full 8-gradient ABI), gy ~ N(0,1).
+
+One step = the fused forward plus the full backward of
+``bayes_ssm.fused_cuda.fused_diagonal_bayesian`` (inputs resident in HBM).
+Prints one JSON line.  ``--gpus`` above 1 is rejected: this build measures
+one GPU (sequences shard with no exchange).
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT / "bayes-ssm_amd"))
+sys.path.insert(0, str(ROOT))
+
+import torch  # noqa: E402
+
+METRIC = "Bayes-layer fwd+bwd tokens/s at B256×T512×H64 D4M8; % HBM roofline"
+HBM_PEAK = 8.0e12  # MI355X spec peak, bytes/s
+
+
+def algorithmic_bytes(d: int, m: int) -> tuple[int, int]:
+    """(forward, backward) bytes per (sequence, token) at the fp32 ABI.
+
+    forward reads k, q, d (D each), v (M), p, r and writes y (M);
+    backward reads the same inputs plus gy (M) and writes their 3D+M+2 gradients.
+    """
+    inputs = 3 * d + m + 2
+    return (inputs + m) * 4, (2 * inputs + m) * 4
+
+
+def make_workload(b, t, h, d, m, device, seed=0):
+    n = b * h
+    g = torch.Generator(device=device).manual_seed(seed)
+    k = torch.randn(n, t, d, device=device, generator=g).bfloat16().float()
+    v = torch.randn(n, t, m, device=device, generator=g).bfloat16().float()
+    q = torch.randn(n, t, d, device=device, generator=g).bfloat16().float()
+    dec = torch.sigmoid(torch.randn(n, t, d, device=device, generator=g) + 2.0)
+    p = torch.nn.functional.softplus(torch.randn(n, t, device=device, generator=g) - 3.0)
+    r = 1e-4 + torch.nn.functional.softplus(torch.randn(n, t, device=device, generator=g))
+    gy = torch.randn(n, t, m, device=device, generator=g)
+    leaves = [x.requires_grad_(True) for x in (k, v, q, dec, p, r)]
+    m0 = torch.zeros(n, d, m, device=device)
+    c0 = torch.eye(d, device=device).expand(n, d, d).contiguous()
+    return leaves, m0, c0, gy
+
+
+def cpu_baseline(t: int, d: int, m: int, heads: int, budget_s: float) -> dict:
+    """Time the CPU restatement of the reference CPU path on a bounded sample.
+
+    ``bayesian_layer(..., optimized=False, chunk_length=64)`` is the
+    transported-history chunk algorithm (oracle ``reference_layer``) with
+    autograd backward, fp32, on all host cores.
+    """
+    from oracle import bssm_oracle as O
+
+    threads = os.cpu_count() or 1
+    torch.set_num_threads(threads)
+    n = 256
+    while True:
+        k, v, q, dec, p, r, gy = O.make_inputs(n, t, d, m, seed=1, requires_grad=True)
+        start = time.perf_counter()
+        y, _, _ = O.reference_layer(k, v, q, dec, p, r, chunk=64)
+        torch.autograd.grad(y, (k, v, q, dec, p, r), gy)
+        elapsed = time.perf_counter() - start
+        if elapsed * 2 > budget_s or n >= 16384:
+            break
+        n *= 2
+    model_tokens = n * t / heads
+    return {
+        "value": model_tokens / elapsed,
+        "unit": "tokens/s",
+        "cores": threads,
+        "kind": "port",
+        "sample": (f"{n} of 16384 head-sequences x T={t} (D{d}M{m}), fwd+bwd of the oracle's restatement of "
+                   f"bayesian_layer(optimized=False, chunk_length=64) with autograd, fp32, {threads} threads, "
+                   f"{elapsed:.1f} s; sequences are independent, so tokens/s scales linearly to the full batch"),
+    }
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--batch", type=int, default=256)
+    ap.add_argument("--seq", type=int, default=512)
+    ap.add_argument("--heads", type=int, default=64)
+    ap.add_argument("--key-dim", type=int, default=4)
+    ap.add_argument("--chunk", type=int, default=64)
+    ap.add_argument("--kernel-iters", type=int, default=20, help="iterations of the per-kernel event timing")
+    ap.add_argument("--cpu-budget", type=float, default=20.0, help="seconds of CPU-baseline work (0 = skip)")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU only: the layer shards over sequences with no exchange, "
+              "so multi-GPU runs are not part of this build", file=sys.stderr)
+        return 2
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU", file=sys.stderr)
+        return 2
+
+    from bayes_ssm import _hip, fused_cuda
+
+    device = torch.device("cuda:0")
+    torch.cuda.set_device(device)
+    b, t, h, d, m = args.batch, args.seq, args.heads, args.key_dim, 8
+    n = b * h
+    leaves, m0, c0, gy = make_workload(b, t, h, d, m, device)
+
+    def step():
+        y, _, _ = fused_cuda.fused_diagonal_bayesian(*leaves, m0, c0, chunk_length=args.chunk,
+                                                     denominator_floor=1e-6)
+        return torch.autograd.grad(y, leaves, gy)
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    start = torch.cuda.Event(enable_timing=True)
+    stop = torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(args.steps):
+        step()
+    stop.record()
+    torch.cuda.synchronize()
+    ms_per_step = start.elapsed_time(stop) / args.steps
+    tokens_per_s = b * t / (ms_per_step * 1e-3)
+
+    # Per-kernel timing with events on the launch stream (torch's current stream).
+    ext = fused_cuda._load_extension(d)
+    interval = fused_cuda._checkpoint_interval(d, t, args.chunk)
+    raw = [x.detach() for x in leaves]
+    fwd_out = ext.forward_chunked(*raw, m0, c0, interval, 1e-6)
+    bm, bc = fwd_out[3], fwd_out[4]
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(4)]
+    torch.cuda.synchronize()
+    ev[0].record()
+    for _ in range(args.kernel_iters):
+        ext.forward_chunked(*raw, m0, c0, interval, 1e-6)
+    ev[1].record()
+    for _ in range(args.kernel_iters):
+        ext.backward_chunked(*raw, m0, c0, bm, bc, gy, None, None, interval, 1e-6)
+    ev[2].record()
+    torch.cuda.synchronize()
+    fwd_ms = ev[0].elapsed_time(ev[1]) / args.kernel_iters
+    bwd_ms = ev[1].elapsed_time(ev[2]) / args.kernel_iters
+    fwd_b, bwd_b = algorithmic_bytes(d, m)
+    units = n * t
+    bwd_gbs = bwd_b * units / (bwd_ms * 1e-3) / 1e9
+    fwd_gbs = fwd_b * units / (fwd_ms * 1e-3) / 1e9
+    step_frac = (fwd_b + bwd_b) * units / (ms_per_step * 1e-3) / HBM_PEAK
+
+    traffic = None
+    traffic_file = ROOT / "profiles" / f"traffic_d{d}m{m}_b{b}t{t}h{h}.json"
+    if traffic_file.exists():
+        traffic = json.loads(traffic_file.read_text()).get("backward_bytes_per_launch")
+
+    result = {
+        "metric": METRIC,
+        "value": tokens_per_s,
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": ms_per_step,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp32",
+        "data": "synthetic",
+        "config": {
+            "workload": "bayes_layer_fwd_bwd_config3",
+            "B": b, "T": t, "H": h, "D": d, "M": m, "sequences": n,
+            "chunk_length": args.chunk, "checkpoint_interval": interval,
+            "gradients": "k,v,q,decay,process,observation (full ABI)",
+            "parallelism": "single GPU",
+        },
+        "roofline": {
+            "bound": "hbm",
+            "kernel": "backward_kernel<4,8,4,8,false,true> (chunk replay + reverse)",
+            "achieved": bwd_gbs,
+            "peak": HBM_PEAK / 1e9,
+            "unit": "GB/s",
+            "frac": bwd_gbs * 1e9 / HBM_PEAK,
+            "traffic": traffic,
+            "bytes_per_launch": bwd_b * units,
+            "avg_launch_ms": bwd_ms,
+        },
+        "roofline_forward": {"achieved": fwd_gbs, "frac": fwd_gbs * 1e9 / HBM_PEAK, "avg_launch_ms": fwd_ms,
+                             "bytes_per_launch": fwd_b * units},
+        "roofline_step_frac": step_frac,
+        "device": torch.cuda.get_device_name(device),
+        "hip_library": str(_hip.LIB_PATH.relative_to(ROOT)),
+    }
+    if args.cpu_budget > 0:
+        result["cpu_baseline"] = cpu_baseline(t, d, m, h, args.cpu_budget)
+    print(json.dumps(result), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,234 @@
+/*
+ * bssm.h — C ABI of the MI355X (gfx950) Bayesian-recurrence library.
+ *
+ * Every entry point takes raw device pointers (row-major, contiguous fp32),
+ * sizes, scalar options and a HIP stream handle passed as `void*`
+ * (a `hipStream_t`; NULL = the legacy default stream).  Nothing here
+ * allocates device memory, synchronises the stream or keeps state between
+ * calls, so every entry point is safe to call under HIP graph capture and
+ * from several host threads (each call only enqueues kernels).
+ *
+ * Return value: BSSM_OK (0) or a BSSM_ERR_* code; bssm_last_error() returns
+ * the message of the most recent failure on the calling host thread.
+ *
+ * Shapes follow the reference extension ABI (N sequences, T tokens, key dim
+ * D, value dim M, nb = ceil(T / chunk)):
+ *   keys, queries, decay  [N, T, D]      values, out, gy          [N, T, M]
+ *   process, observation  [N, T]         mean0, mean_final, gm*   [N, D, M]
+ *   cov0, cov_final, gc*  [N, D, D]      bmean [N, nb+1, D, M]   bcov [N, nb+1, D, D]
+ * bmean[:, c] / bcov[:, c] hold the belief before token c*chunk; index nb
+ * holds the final belief.
+ *
+ * Supported (D, M): (1, 8), (2, 8), (4, 8), (8, 8).
+ */
+#ifndef BSSM_H_
+#define BSSM_H_
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum {
+  BSSM_OK = 0,
+  BSSM_ERR_ARGUMENT = 1,     /* null pointer, bad size, chunk <= 0, ...      */
+  BSSM_ERR_UNSUPPORTED = 2,  /* (D, M) outside the supported set             */
+  BSSM_ERR_LAUNCH = 3,       /* the HIP runtime rejected a kernel launch     */
+};
+
+/* Message of the last failure on this host thread ("" if none). */
+const char* bssm_last_error(void);
+
+/* ABI revision of this library (bumped on any signature change). */
+int bssm_abi_version(void);
+
+/* 1 if (key_dim, value_dim) has a kernel, else 0. */
+int bssm_supported(int key_dim, int value_dim);
+
+/* Checkpoint interval (tokens) at which bssm_backward_chunked* replays each
+ * chunk exactly once from its checkpoint (the kernel's on-chip history
+ * length for this key dimension); 0 if unsupported.  Larger chunks are
+ * valid but re-replay each chunk prefix once per history-length piece.
+ * No reference counterpart: the reference backward always replays whole
+ * chunks through HBM history tensors (persistent_bayes_chunked_d4m8.cu:524-548). */
+int bssm_preferred_checkpoint(int key_dim);
+
+/* ------------------------------------------------------------------------
+ * Dynamic-diagonal forward with chunk-boundary checkpoints.
+ * Replaces the pybind function `forward_chunked`
+ * (bayes_ssm/persistent_bayes_chunked_d4m8.cu:461-468; same contract in
+ * _d1m8.cu:387-393, _d2m8.cu forward_chunked, _d8.cu forward_chunked).
+ * Per token: P' = diag(d) P diag(d) + p I, u = P' k, s = max(r + k.u, floor),
+ * e = v - (d*M)^T k, M <- d*M + u e^T / s, P <- P' - u u^T / s, y = M^T q.
+ */
+int bssm_forward_chunked(int key_dim, int value_dim,
+                         const float* keys, const float* values, const float* queries,
+                         const float* decay, const float* process, const float* observation,
+                         const float* mean0, const float* cov0,
+                         float* out, float* mean_final, float* cov_final,
+                         float* bmean, float* bcov,
+                         int64_t n, int64_t t, int64_t chunk, float denominator_floor,
+                         void* stream);
+
+/* Fixed dynamics A = 0.97 I, Q = 0.1 I, R = 1: decay/process/observation are
+ * not read (they may be NULL).  Replaces `forward_chunked_fixed`
+ * (persistent_bayes_chunked_d4m8.cu:470-474). */
+int bssm_forward_chunked_fixed(int key_dim, int value_dim,
+                               const float* keys, const float* values, const float* queries,
+                               const float* decay, const float* process, const float* observation,
+                               const float* mean0, const float* cov0,
+                               float* out, float* mean_final, float* cov_final,
+                               float* bmean, float* bcov,
+                               int64_t n, int64_t t, int64_t chunk, float denominator_floor,
+                               void* stream);
+
+/* Forward that also writes the per-token replay history used by the D1
+ * saved-history reverse: mp = d*M_prev [N,T,D,M], pp = P' [N,T,D,D],
+ * uh = u [N,T,D], bh = 1/s [N,T], eh = e [N,T,M].  Requires chunk == t
+ * (one full-sequence chunk, so nb = 1).  Replaces `forward_chunked_saved`
+ * (persistent_bayes_chunked_d1m8.cu:387-414). */
+int bssm_forward_chunked_saved(int key_dim, int value_dim,
+                               const float* keys, const float* values, const float* queries,
+                               const float* decay, const float* process, const float* observation,
+                               const float* mean0, const float* cov0,
+                               float* out, float* mean_final, float* cov_final,
+                               float* bmean, float* bcov,
+                               float* mp, float* pp, float* uh, float* bh, float* eh,
+                               int64_t n, int64_t t, int64_t chunk, float denominator_floor,
+                               void* stream);
+
+/* ------------------------------------------------------------------------
+ * Chunk-replay reverse.  Each checkpoint chunk is replayed on chip from
+ * bmean/bcov and then reversed; the adjoint of the belief is carried across
+ * chunks inside the kernel (one launch per call).
+ *
+ * gmf / gcf are the gradients of mean_final / cov_final; NULL means zero.
+ * Output gradients: gk, gq, gd [N,T,D]; gv [N,T,M]; gp, gr [N,T];
+ * gm0 [N,D,M]; gc0 [N,D,D].  gc0 keeps the full (asymmetric) derivative with
+ * respect to the unconstrained initial covariance: (sym(G) + gu k^T) * d d^T.
+ *
+ * Replaces `backward_chunked` (persistent_bayes_chunked_d4m8.cu:556-559):
+ * all eight gradients. */
+int bssm_backward_chunked(int key_dim, int value_dim,
+                          const float* keys, const float* values, const float* queries,
+                          const float* decay, const float* process, const float* observation,
+                          const float* mean0, const float* cov0,
+                          const float* bmean, const float* bcov,
+                          const float* gy, const float* gmf, const float* gcf,
+                          float* gk, float* gv, float* gq, float* gd, float* gp, float* gr,
+                          float* gm0, float* gc0,
+                          int64_t n, int64_t t, int64_t chunk, float denominator_floor,
+                          void* stream);
+
+/* Keys/values/queries gradients only.  Replaces `backward_chunked_lean`
+ * (persistent_bayes_chunked_d4m8.cu:561-564). */
+int bssm_backward_chunked_lean(int key_dim, int value_dim,
+                               const float* keys, const float* values, const float* queries,
+                               const float* decay, const float* process, const float* observation,
+                               const float* mean0, const float* cov0,
+                               const float* bmean, const float* bcov,
+                               const float* gy, const float* gmf, const float* gcf,
+                               float* gk, float* gv, float* gq,
+                               int64_t n, int64_t t, int64_t chunk, float denominator_floor,
+                               void* stream);
+
+/* Six gradients (no initial-state outputs).  Replaces
+ * `backward_chunked_noinitial` (persistent_bayes_chunked_d2m8.cu:576-580). */
+int bssm_backward_chunked_noinitial(int key_dim, int value_dim,
+                                    const float* keys, const float* values, const float* queries,
+                                    const float* decay, const float* process, const float* observation,
+                                    const float* mean0, const float* cov0,
+                                    const float* bmean, const float* bcov,
+                                    const float* gy, const float* gmf, const float* gcf,
+                                    float* gk, float* gv, float* gq, float* gd, float* gp, float* gr,
+                                    int64_t n, int64_t t, int64_t chunk, float denominator_floor,
+                                    void* stream);
+
+/* Fixed-dynamics reverse (A = 0.97 I, Q = 0.1 I, R = 1).  gd, gp, gr are
+ * written as zeros, as the reference fixed ABI returns them.  Replaces
+ * `backward_chunked_fixed` (persistent_bayes_chunked_d4m8.cu:572-575). */
+int bssm_backward_chunked_fixed(int key_dim, int value_dim,
+                                const float* keys, const float* values, const float* queries,
+                                const float* decay, const float* process, const float* observation,
+                                const float* mean0, const float* cov0,
+                                const float* bmean, const float* bcov,
+                                const float* gy, const float* gmf, const float* gcf,
+                                float* gk, float* gv, float* gq, float* gd, float* gp, float* gr,
+                                float* gm0, float* gc0,
+                                int64_t n, int64_t t, int64_t chunk, float denominator_floor,
+                                void* stream);
+
+/* Replaces `backward_chunked_lean_fixed` (persistent_bayes_chunked_d4m8.cu:566-569). */
+int bssm_backward_chunked_lean_fixed(int key_dim, int value_dim,
+                                     const float* keys, const float* values, const float* queries,
+                                     const float* decay, const float* process, const float* observation,
+                                     const float* mean0, const float* cov0,
+                                     const float* bmean, const float* bcov,
+                                     const float* gy, const float* gmf, const float* gcf,
+                                     float* gk, float* gv, float* gq,
+                                     int64_t n, int64_t t, int64_t chunk, float denominator_floor,
+                                     void* stream);
+
+/* Replaces `backward_chunked_noinitial_fixed` (persistent_bayes_chunked_d2m8.cu:597-600). */
+int bssm_backward_chunked_noinitial_fixed(int key_dim, int value_dim,
+                                          const float* keys, const float* values, const float* queries,
+                                          const float* decay, const float* process, const float* observation,
+                                          const float* mean0, const float* cov0,
+                                          const float* bmean, const float* bcov,
+                                          const float* gy, const float* gmf, const float* gcf,
+                                          float* gk, float* gv, float* gq, float* gd, float* gp, float* gr,
+                                          int64_t n, int64_t t, int64_t chunk, float denominator_floor,
+                                          void* stream);
+
+/* Saved-history reverse: consumes mp/pp/uh/bh/eh written by
+ * bssm_forward_chunked_saved instead of replaying.  Requires chunk == t.
+ * Replaces `backward_chunked_saved` (persistent_bayes_chunked_d1m8.cu:632-640)
+ * and `backward_chunked_saved_d1` (:600-630), which return the same eight
+ * gradients. */
+int bssm_backward_chunked_saved(int key_dim, int value_dim,
+                                const float* keys, const float* values, const float* queries,
+                                const float* decay, const float* process, const float* observation,
+                                const float* mean0, const float* cov0,
+                                const float* bmean, const float* bcov,
+                                const float* mp, const float* pp, const float* uh,
+                                const float* bh, const float* eh,
+                                const float* gy, const float* gmf, const float* gcf,
+                                float* gk, float* gv, float* gq, float* gd, float* gp, float* gr,
+                                float* gm0, float* gc0,
+                                int64_t n, int64_t t, int64_t chunk, float denominator_floor,
+                                void* stream);
+
+/* Replaces `backward_chunked_saved_lean` (persistent_bayes_chunked_d1m8.cu:642-650). */
+int bssm_backward_chunked_saved_lean(int key_dim, int value_dim,
+                                     const float* keys, const float* values, const float* queries,
+                                     const float* decay, const float* process, const float* observation,
+                                     const float* mean0, const float* cov0,
+                                     const float* bmean, const float* bcov,
+                                     const float* mp, const float* pp, const float* uh,
+                                     const float* bh, const float* eh,
+                                     const float* gy, const float* gmf, const float* gcf,
+                                     float* gk, float* gv, float* gq,
+                                     int64_t n, int64_t t, int64_t chunk, float denominator_floor,
+                                     void* stream);
+
+/* ------------------------------------------------------------------------
+ * Static (A = I, Q = 0) associative scan in information form.
+ * Replaces the torch-op chain of `associative_static_bayesian`
+ * (bayes_ssm/replay_ssm.py:251-270):
+ *   L_t = inv(P0) + sum_{s<=t} k_s k_s^T / r_s,  N_t = inv(P0) M0 + sum k_s v_s^T / r_s,
+ *   M_t = L_t^{-1} N_t (Cholesky), y_t = M_t^T q_t, P_T = L_T^{-1}.
+ * keys/queries [B,T,D], values [B,T,M], observation [B,T] (>= floor, checked
+ * by the caller), mean0 [B,D,M], cov0 [B,D,D] (SPD).  Outputs out [B,T,M],
+ * mean_final [B,D,M], cov_final [B,D,D].  Supports D <= 32, M <= 64. */
+int bssm_associative_static_scan(const float* keys, const float* values, const float* queries,
+                                 const float* observation, const float* mean0, const float* cov0,
+                                 float* out, float* mean_final, float* cov_final,
+                                 int64_t b, int64_t t, int key_dim, int value_dim,
+                                 void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* BSSM_H_ */

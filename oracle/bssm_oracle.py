@@ -1,0 +1,282 @@
+"""CPU oracle for the bayes-ssm Bayesian recurrence — TEST INFRASTRUCTURE ONLY.
+
+Only ``tests/``, ``__graft_entry__.smoke()`` and ``bench.py``'s CPU-baseline
+leg may import this module, and only as the checker / the timed CPU
+baseline.  The product path (``bayes_ssm``) never imports it.
+
+Each function restates one reference routine in plain PyTorch (float64 or
+float32, autograd-friendly), written from the equations:
+
+* ``dense_step`` / ``run_dense``     — bayes_ssm/bayesian_layer.py:153-204 (_step, _core_loop)
+* ``run_diagonal``                   — bayesian_layer.py:207-251 (_core_loop_diagonal_transition)
+* ``run_fixed``                      — bayesian_layer.py:343-397 (_core_loop_fixed_diagonal)
+* ``run_chunked``                    — bayesian_layer.py:670-732 (_run_chunked, paper §C.2
+                                       transported-history chunk algorithm; the reference
+                                       CPU path of ``bayesian_layer(optimized=False)``)
+* ``reference_layer``                — bayesian_layer.py:1169-1182 (the optimized=False dispatch:
+                                       diag_embed + _run_chunked)
+* ``checkpoints``                    — boundary layout of persistent_bayes_chunked_d4m8.cu:208-211, :244
+* ``associative_static``             — bayes_ssm/replay_ssm.py:155-270 (information-form scan)
+* ``closed_form_static``             — Bayesian linear regression, the A=I, Q=0 closed form
+
+Pinning (tests/test_oracle.py): closed forms (scalar Kalman filter, one-step
+u = (d^2+p)k, no-update limits, Bayesian linear regression), invariants
+(symmetric PSD covariance, P_post <= P_pred, chunk-length invariance),
+cross-formulation agreement (dense == diagonal == transported-history ==
+information-form, as the reference's own tests assert at 1e-12/1e-10), and
+fp64 gradcheck of the gradients that the reference obtains by autograd.
+No function here is left "parity unpinned".
+"""
+from __future__ import annotations
+
+from typing import Optional
+
+import torch
+from torch import Tensor
+
+FIXED_DECAY = 0.97
+FIXED_PROCESS = 0.1
+FIXED_OBSERVATION = 1.0
+
+
+def _sym(x: Tensor) -> Tensor:
+    return 0.5 * (x + x.transpose(-1, -2))
+
+
+def dense_step(mean, cov, k, v, q, A, Q, r, floor):
+    """One predict/condition/read step (bayesian_layer.py:153-181).
+
+    mean [..., D, M], cov [..., D, D], k/q [..., D], v [..., M], A/Q [..., D, D], r [...].
+    """
+    cov_pred = A @ cov @ A.transpose(-1, -2) + Q
+    mean_pred = A @ mean
+    u = (cov_pred @ k.unsqueeze(-1)).squeeze(-1)
+    s = (r + (k * u).sum(-1)).clamp_min(floor)
+    beta = 1.0 / s
+    e = v - (mean_pred.transpose(-1, -2) @ k.unsqueeze(-1)).squeeze(-1)
+    bu = beta[..., None] * u
+    mean_new = mean_pred + bu[..., :, None] * e[..., None, :]
+    cov_new = _sym(cov_pred - bu[..., :, None] * u[..., None, :])
+    y = (mean_new.transpose(-1, -2) @ q.unsqueeze(-1)).squeeze(-1)
+    return mean_new, cov_new, y
+
+
+def run_dense(k, v, q, A, Q, r, mean0, cov0, floor):
+    """Token loop over dense dynamics (bayesian_layer.py:184-204).  A, Q: [..., T, D, D]."""
+    mean, cov = mean0, cov0
+    ys = []
+    for t in range(k.shape[-2]):
+        mean, cov, y = dense_step(mean, cov, k[..., t, :], v[..., t, :], q[..., t, :], A[..., t, :, :],
+                                  Q[..., t, :, :], r[..., t], floor)
+        ys.append(y)
+    return torch.stack(ys, dim=-2), mean, cov
+
+
+def run_diagonal(k, v, q, d, p, r, mean0, cov0, floor):
+    """Diagonal-transition token loop (bayesian_layer.py:207-251).
+
+    The predicted covariance is d_i P_ij d_j + p delta_ij; the initial
+    covariance is used as given (not symmetrised), so autograd yields the
+    full asymmetric initial-covariance gradient the fused kernels return.
+    """
+    mean, cov = mean0, cov0
+    eye = torch.eye(k.shape[-1], dtype=k.dtype, device=k.device)
+    ys = []
+    for t in range(k.shape[-2]):
+        dt = d[..., t, :]
+        mean_pred = dt[..., :, None] * mean
+        cov_pred = dt[..., :, None] * cov * dt[..., None, :] + p[..., t, None, None] * eye
+        kt = k[..., t, :]
+        u = (cov_pred @ kt.unsqueeze(-1)).squeeze(-1)
+        s = (r[..., t] + (kt * u).sum(-1)).clamp_min(floor)
+        beta = 1.0 / s
+        e = v[..., t, :] - (mean_pred * kt[..., :, None]).sum(-2)
+        bu = beta[..., None] * u
+        mean = mean_pred + bu[..., :, None] * e[..., None, :]
+        cov = _sym(cov_pred - bu[..., :, None] * u[..., None, :])
+        ys.append((mean * q[..., t, :, None]).sum(-2))
+    return torch.stack(ys, dim=-2), mean, cov
+
+
+def run_fixed(k, v, q, mean0, cov0, floor):
+    """Constant dynamics A = 0.97 I, Q = 0.1 I, R = 1 (bayesian_layer.py:343-397)."""
+    mean, cov = mean0, cov0
+    eye = torch.eye(k.shape[-1], dtype=k.dtype, device=k.device)
+    rho, rho2 = FIXED_DECAY, FIXED_DECAY * FIXED_DECAY
+    ys = []
+    for t in range(k.shape[-2]):
+        kt = k[..., t, :]
+        mean_pred = rho * mean
+        u = rho2 * (cov * kt[..., None, :]).sum(-1) + FIXED_PROCESS * kt
+        s = (FIXED_OBSERVATION + (kt * u).sum(-1)).clamp_min(floor)
+        beta = 1.0 / s
+        e = v[..., t, :] - (mean_pred * kt[..., :, None]).sum(-2)
+        bu = beta[..., None] * u
+        mean = mean_pred + bu[..., :, None] * e[..., None, :]
+        cov = _sym(rho2 * cov + FIXED_PROCESS * eye - bu[..., :, None] * u[..., None, :])
+        ys.append((mean * q[..., t, :, None]).sum(-2))
+    return torch.stack(ys, dim=-2), mean, cov
+
+
+def run_chunked(k, v, q, A, Q, r, mean0, cov0, chunk, floor):
+    """Transported-history chunk algorithm (bayesian_layer.py:670-732).
+
+    Inside a chunk the covariance is kept as Pi_t (the prediction with the
+    chunk's own observations removed) plus the transported rank-one update
+    directions w_s; the dense posterior is only formed at chunk exit.
+    """
+    T = k.shape[-2]
+    mean, cov = mean0, cov0
+    ys = []
+    for start in range(0, T, chunk):
+        stop = min(T, start + chunk)
+        pi = cov
+        m = mean
+        dirs: list[Tensor] = []
+        betas: list[Tensor] = []
+        for t in range(start, stop):
+            At = A[..., t, :, :]
+            pi = _sym(At @ pi @ At.transpose(-1, -2) + Q[..., t, :, :])
+            m = At @ m
+            dirs = [(At @ w.unsqueeze(-1)).squeeze(-1) for w in dirs]
+            kt = k[..., t, :]
+            u = (pi @ kt.unsqueeze(-1)).squeeze(-1)
+            for w, b in zip(dirs, betas):
+                u = u - b[..., None] * w * (w * kt).sum(-1)[..., None]
+            s = (r[..., t] + (kt * u).sum(-1)).clamp_min(floor)
+            beta = 1.0 / s
+            e = v[..., t, :] - (m.transpose(-1, -2) @ kt.unsqueeze(-1)).squeeze(-1)
+            m = m + beta[..., None, None] * u[..., :, None] * e[..., None, :]
+            ys.append((m.transpose(-1, -2) @ q[..., t, :].unsqueeze(-1)).squeeze(-1))
+            dirs.append(u)
+            betas.append(beta)
+        cov = pi
+        for w, b in zip(dirs, betas):
+            cov = cov - b[..., None, None] * w[..., :, None] * w[..., None, :]
+        cov = _sym(cov)
+        mean = m
+    return torch.stack(ys, dim=-2), mean, cov
+
+
+def diagonal_as_dense(d, p):
+    """diag_embed(d) and p I as dense [..., T, D, D] dynamics (bayesian_layer.py:1175-1179)."""
+    eye = torch.eye(d.shape[-1], dtype=d.dtype, device=d.device)
+    return torch.diag_embed(d), p[..., None, None] * eye
+
+
+def reference_layer(k, v, q, d, p, r, mean0=None, cov0=None, chunk=64, floor=1e-6):
+    """The reference CPU path ``bayesian_layer(..., transition_diagonals=d, optimized=False)``."""
+    D, M = k.shape[-1], v.shape[-1]
+    batch = k.shape[:-2]
+    if mean0 is None:
+        mean0 = torch.zeros(*batch, D, M, dtype=k.dtype)
+    if cov0 is None:
+        cov0 = torch.eye(D, dtype=k.dtype).expand(*batch, D, D).clone()
+    A, Q = diagonal_as_dense(d, p)
+    return run_chunked(k, v, q, A, Q, r, mean0, cov0, chunk, floor)
+
+
+def checkpoints(k, v, q, d, p, r, mean0, cov0, chunk, floor):
+    """Boundary beliefs: index c holds the belief before token c*chunk, index nb the final one."""
+    T = k.shape[-2]
+    nb = -(-T // chunk)
+    means, covs = [mean0], [cov0]
+    mean, cov = mean0, cov0
+    for c in range(1, nb + 1):
+        stop = min(T, c * chunk)
+        start = (c - 1) * chunk
+        _, mean, cov = run_diagonal(k[..., start:stop, :], v[..., start:stop, :], q[..., start:stop, :],
+                                    d[..., start:stop, :], p[..., start:stop], r[..., start:stop], mean, cov, floor)
+        means.append(mean)
+        covs.append(cov)
+    return torch.stack(means, dim=-3), torch.stack(covs, dim=-3)
+
+
+def associative_static(k, v, q, r, mean0: Optional[Tensor] = None, cov0: Optional[Tensor] = None):
+    """Information-form static scan (replay_ssm.py:251-270): prefix precision/natural, Cholesky solve."""
+    D, M = k.shape[-1], v.shape[-1]
+    batch = k.shape[:-2]
+    if cov0 is None:
+        cov0 = torch.eye(D, dtype=k.dtype).expand(*batch, D, D)
+    if mean0 is None:
+        mean0 = torch.zeros(*batch, D, M, dtype=k.dtype)
+    lam0 = torch.linalg.inv(cov0)
+    nat0 = lam0 @ mean0
+    wk = k / r[..., :, None]
+    lam = lam0.unsqueeze(-3) + (k[..., :, :, None] * wk[..., :, None, :]).cumsum(-3)
+    nat = nat0.unsqueeze(-3) + (wk[..., :, :, None] * v[..., :, None, :]).cumsum(-3)
+    lam = _sym(lam)
+    chol = torch.linalg.cholesky(lam)
+    mean = torch.cholesky_solve(nat, chol)
+    y = (mean.transpose(-1, -2) @ q.unsqueeze(-1)).squeeze(-1)
+    cov_last = torch.cholesky_inverse(chol[..., -1, :, :])
+    return y, mean[..., -1, :, :], cov_last
+
+
+def closed_form_static(k, v, r, mean0, cov0):
+    """A = I, Q = 0 posterior after all tokens: M = (P0^-1 + sum k k^T/r)^-1 (P0^-1 M0 + sum k v^T/r)."""
+    lam0 = torch.linalg.inv(cov0)
+    lam = lam0 + torch.einsum("...ti,...tj->...ij", k / r[..., :, None], k)
+    nat = lam0 @ mean0 + torch.einsum("...ti,...tc->...ic", k / r[..., :, None], v)
+    mean = torch.linalg.solve(lam, nat)
+    return mean, torch.linalg.inv(lam)
+
+
+# --------------------------------------------------------------- inputs
+def make_inputs(n: int, t: int, d: int, m: int = 8, *, seed: int = 0, dtype=torch.float32,
+                bf16_round: bool = True, requires_grad: bool = False):
+    """Seeded synthetic inputs of the measurement configs (CPU tensors).
+
+    Draw order k, v, q, decay-logit, process-logit, observation-logit, gy:
+    k, v, q ~ N(0,1) (rounded through bf16), decay = sigmoid(N(2,1)),
+    p = softplus(N(-3,1)), r = 1e-4 + softplus(N(0,1)), gy ~ N(0,1).
+    """
+    gen = torch.Generator().manual_seed(seed)
+    k = torch.randn(n, t, d, generator=gen)
+    v = torch.randn(n, t, m, generator=gen)
+    q = torch.randn(n, t, d, generator=gen)
+    if bf16_round:
+        k, v, q = (x.to(torch.bfloat16).float() for x in (k, v, q))
+    dec = torch.sigmoid(torch.randn(n, t, d, generator=gen) + 2.0)
+    p = torch.nn.functional.softplus(torch.randn(n, t, generator=gen) - 3.0)
+    r = 1e-4 + torch.nn.functional.softplus(torch.randn(n, t, generator=gen))
+    gy = torch.randn(n, t, m, generator=gen)
+    out = [x.to(dtype) for x in (k, v, q, dec, p, r, gy)]
+    if requires_grad:
+        for x in out[:6]:
+            x.requires_grad_(True)
+    return out
+
+
+def make_scan_inputs(b: int, t: int, d: int, m: int, *, seed: int = 0, dtype=torch.float32):
+    """Associative-scan configs: k ~ N(0, 1/D), v, q ~ N(0,1), r = 1e-4 + softplus(N(0,1))."""
+    gen = torch.Generator().manual_seed(seed)
+    k = torch.randn(b, t, d, generator=gen) / (d ** 0.5)
+    v = torch.randn(b, t, m, generator=gen)
+    q = torch.randn(b, t, d, generator=gen)
+    r = 1e-4 + torch.nn.functional.softplus(torch.randn(b, t, generator=gen))
+    return [x.to(dtype) for x in (k, v, q, r)]
+
+
+def diagonal_grads(k, v, q, d, p, r, mean0, cov0, gy, gmf=None, gcf=None, floor=1e-6, chunk=None):
+    """Outputs and all eight gradients by autograd through the oracle.
+
+    ``chunk=None`` differentiates ``run_diagonal``; an integer differentiates
+    the transported-history ``run_chunked`` (the reference CPU path).
+    Returns (y, mean_T, cov_T, [gk, gv, gq, gd, gp, gr, gm0, gc0]).
+    """
+    leaves = [x.detach().clone().requires_grad_(True) for x in (k, v, q, d, p, r, mean0, cov0)]
+    k_, v_, q_, d_, p_, r_, m0_, c0_ = leaves
+    if chunk is None:
+        y, mT, cT = run_diagonal(k_, v_, q_, d_, p_, r_, m0_, c0_, floor)
+    else:
+        A, Q = diagonal_as_dense(d_, p_)
+        y, mT, cT = run_chunked(k_, v_, q_, A, Q, r_, m0_, c0_, chunk, floor)
+    loss = (y * gy).sum()
+    if gmf is not None:
+        loss = loss + (mT * gmf).sum()
+    if gcf is not None:
+        loss = loss + (cT * gcf).sum()
+    grads = torch.autograd.grad(loss, leaves, allow_unused=True)
+    grads = [torch.zeros_like(x) if g is None else g for g, x in zip(grads, leaves)]
+    return y.detach(), mT.detach(), cT.detach(), grads

@@ -1,0 +1,123 @@
+"""C ABI of libbssm_hip.so — CPU only (loads the library, never launches a kernel)."""
+from __future__ import annotations
+
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+ROOT = Path(__file__).resolve().parents[1]
+HEADER = ROOT / "include" / "bssm.h"
+
+
+def declared_symbols() -> list[str]:
+    text = HEADER.read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(bssm_[a-z0-9_]+)\s*\(", text)))
+
+
+@pytest.fixture(scope="module")
+def lib():
+    from bayes_ssm import _hip
+
+    return _hip.load()
+
+
+def test_library_exports_every_declared_symbol(lib):
+    names = declared_symbols()
+    assert len(names) >= 16
+    for name in names:
+        assert hasattr(lib, name), f"{name} declared in include/bssm.h but not exported"
+
+
+def test_binding_signatures_cover_header():
+    from bayes_ssm import _hip
+
+    missing = [n for n in declared_symbols() if n not in _hip._SIGNATURES and n != "bssm_last_error"]
+    assert not missing, missing
+
+
+def test_abi_version_and_support(lib):
+    from bayes_ssm import _hip
+
+    assert lib.bssm_abi_version() == _hip.ABI_VERSION
+    for d in (1, 2, 4, 8):
+        assert lib.bssm_supported(d, 8) == 1
+        assert lib.bssm_preferred_checkpoint(d) > 0
+    for d, m in ((3, 8), (4, 4), (64, 64), (16, 8)):
+        assert lib.bssm_supported(d, m) == 0
+    assert lib.bssm_preferred_checkpoint(3) == 0
+
+
+def _fwd(lib, d=4, m=8, n=1, t=1, chunk=1, floor=1e-6, null=True):
+    return lib.bssm_forward_chunked(d, m, *([None] * 13), n, t, chunk, ctypes.c_float(floor), None)
+
+
+def test_argument_errors_are_reported(lib):
+    assert _fwd(lib, d=3) == 2
+    assert b"unsupported" in lib.bssm_last_error()
+    assert _fwd(lib, chunk=0) == 1
+    assert b"chunk" in lib.bssm_last_error()
+    assert _fwd(lib, floor=0.0) == 1
+    assert b"floor" in lib.bssm_last_error()
+    assert _fwd(lib, n=-1) == 1
+    assert _fwd(lib) == 1 and b"null" in lib.bssm_last_error()
+    # Nothing to do: success without touching a device.
+    assert _fwd(lib, n=0, t=5) == 0
+    assert lib.bssm_last_error() == b""
+
+
+def test_backward_requires_outputs(lib):
+    rc = lib.bssm_backward_chunked(4, 8, *([None] * 21), 2, 3, 1, ctypes.c_float(1e-6), None)
+    assert rc == 1 and b"required" in lib.bssm_last_error()
+    rc = lib.bssm_forward_chunked_saved(1, 8, *([None] * 18), 2, 3, 2, ctypes.c_float(1e-6), None)
+    assert rc == 1 and b"full-sequence" in lib.bssm_last_error()
+    rc = lib.bssm_associative_static_scan(*([None] * 9), 1, 4, 40, 4, None)
+    assert rc == 2
+
+
+def test_python_wrapper_raises_runtime_error():
+    from bayes_ssm import _hip
+
+    with pytest.raises(RuntimeError, match="chunk must be positive"):
+        _hip.call("bssm_forward_chunked", 4, 8, *([None] * 13), 1, 1, 0, 1e-6, None)
+
+
+def test_extension_method_sets_match_reference():
+    """Per-key-dim method names of the reference pybind modules."""
+    from bayes_ssm import fused_cuda
+
+    ext1 = fused_cuda._load_extension(1)
+    ext2 = fused_cuda._load_extension(2)
+    ext4 = fused_cuda._load_extension(4)
+    for name in ("forward_chunked_saved", "backward_chunked_saved", "backward_chunked_saved_lean",
+                 "backward_chunked_saved_d1"):
+        assert hasattr(ext1, name) and not hasattr(ext4, name)
+    for name in ("backward_chunked_noinitial", "backward_chunked_noinitial_fixed"):
+        assert hasattr(ext2, name) and not hasattr(ext4, name) and not hasattr(ext1, name)
+    for ext in (ext1, ext2, ext4, fused_cuda._load_extension(8)):
+        for name in ("forward_chunked", "forward_chunked_fixed", "backward_chunked", "backward_chunked_lean",
+                     "backward_chunked_fixed", "backward_chunked_lean_fixed"):
+            assert hasattr(ext, name)
+    assert fused_cuda._load_extension(3) is None
+    assert fused_cuda._load_extension(64) is None
+
+
+def test_disable_env(monkeypatch):
+    from bayes_ssm import fused_cuda
+
+    monkeypatch.setenv("BAYES_SSM_DISABLE_FUSED_CUDA", "1")
+    assert fused_cuda._load_extension(4) is None
+
+
+def test_contract_gate_returns_none_on_cpu():
+    import torch
+
+    from bayes_ssm.fused_cuda import fused_diagonal_bayesian
+
+    k = torch.randn(2, 3, 4)
+    out = fused_diagonal_bayesian(k, torch.randn(2, 3, 8), k, torch.ones(2, 3, 4), torch.zeros(2, 3),
+                                  torch.ones(2, 3), torch.zeros(2, 4, 8), torch.eye(4).expand(2, 4, 4),
+                                  chunk_length=2, denominator_floor=1e-6)
+    assert out is None

@@ -1,0 +1,223 @@
+"""Pins of the CPU oracle (oracle/bssm_oracle.py) — CPU only.
+
+The reference ships no golden vectors; its tests assert self-consistency
+(diagonal == dense at 1e-12, replay/dense gradients at 1e-10,
+tests/test_bayesian_layer_diagonal.py:54-123).  Here the oracle is pinned by
+those cross-formulation checks plus closed forms that a plausible mistake
+(dropped process noise, wrong decay placement, transposed operand, missing
+symmetrisation, wrong floor gate) would fail, plus fp64 gradcheck.
+"""
+from __future__ import annotations
+
+import math
+
+import pytest
+import torch
+
+from oracle import bssm_oracle as O
+
+torch.set_default_dtype(torch.float64)
+
+
+def _rand(n, t, d, m, seed, dtype=torch.float64):
+    g = torch.Generator().manual_seed(seed)
+    k = torch.randn(n, t, d, generator=g, dtype=dtype)
+    v = torch.randn(n, t, m, generator=g, dtype=dtype)
+    q = torch.randn(n, t, d, generator=g, dtype=dtype)
+    dec = 0.6 + 0.39 * torch.rand(n, t, d, generator=g, dtype=dtype)
+    p = 0.05 + 0.2 * torch.rand(n, t, generator=g, dtype=dtype)
+    r = 0.2 + torch.rand(n, t, generator=g, dtype=dtype)
+    m0 = 0.3 * torch.randn(n, d, m, generator=g, dtype=dtype)
+    a = torch.randn(n, d, d, generator=g, dtype=dtype)
+    c0 = a @ a.transpose(-1, -2) / d + 0.5 * torch.eye(d, dtype=dtype)
+    return k, v, q, dec, p, r, m0, c0
+
+
+def test_scalar_kalman_textbook():
+    """D = M = 1 is the scalar Kalman filter; compare with its textbook gain form."""
+    k, v, q, dec, p, r, m0, c0 = _rand(1, 12, 1, 1, seed=3)
+    y, mT, cT = O.run_diagonal(k, v, q, dec, p, r, m0, c0, 1e-6)
+    x, P = float(m0[0, 0, 0]), float(c0[0, 0, 0])
+    for t in range(12):
+        a, h, z = float(dec[0, t, 0]), float(k[0, t, 0]), float(v[0, t, 0])
+        x_pred, P_pred = a * x, a * a * P + float(p[0, t])
+        S = h * h * P_pred + float(r[0, t])
+        K = P_pred * h / S
+        x = x_pred + K * (z - h * x_pred)
+        P = (1.0 - K * h) * P_pred
+        assert math.isclose(float(y[0, t, 0]), x * float(q[0, t, 0]), rel_tol=1e-12, abs_tol=1e-12)
+    assert math.isclose(float(mT[0, 0, 0]), x, rel_tol=1e-12)
+    assert math.isclose(float(cT[0, 0, 0]), P, rel_tol=1e-12)
+
+
+def test_first_step_closed_form():
+    """From M0 = 0, P0 = I one step gives u = (d^2 + p) k, M1 = u v^T / (r + k.u)."""
+    k, v, q, dec, p, r, _, _ = _rand(3, 1, 4, 5, seed=4)
+    m0 = torch.zeros(3, 4, 5)
+    c0 = torch.eye(4).expand(3, 4, 4).clone()
+    y, mT, cT = O.run_diagonal(k, v, q, dec, p, r, m0, c0, 1e-6)
+    u = (dec[:, 0] ** 2 + p[:, 0, None]) * k[:, 0]
+    s = r[:, 0] + (k[:, 0] * u).sum(-1)
+    M1 = u[:, :, None] * v[:, 0, None, :] / s[:, None, None]
+    P1 = torch.diag_embed(dec[:, 0] ** 2 + p[:, 0, None]) - u[:, :, None] * u[:, None, :] / s[:, None, None]
+    torch.testing.assert_close(mT, M1, rtol=1e-13, atol=1e-13)
+    torch.testing.assert_close(cT, P1, rtol=1e-13, atol=1e-13)
+    torch.testing.assert_close(y[:, 0], (M1 * q[:, 0, :, None]).sum(-2), rtol=1e-13, atol=1e-13)
+
+
+def test_no_observation_limit():
+    """k = 0 (or r -> inf) leaves only the prediction: M <- d M, P <- d P d + p I."""
+    k, v, q, dec, p, r, m0, c0 = _rand(2, 5, 3, 2, seed=5)
+    for variant in ("zero_key", "huge_r"):
+        kk = torch.zeros_like(k) if variant == "zero_key" else k
+        rr = r if variant == "zero_key" else torch.full_like(r, 1e30)
+        _, mT, cT = O.run_diagonal(kk, v, q, dec, p, rr, m0, c0, 1e-6)
+        M, P = m0.clone(), c0.clone()
+        for t in range(5):
+            M = dec[:, t, :, None] * M
+            P = dec[:, t, :, None] * P * dec[:, t, None, :] + p[:, t, None, None] * torch.eye(3)
+        torch.testing.assert_close(mT, M, rtol=1e-12, atol=1e-12)
+        torch.testing.assert_close(cT, P, rtol=1e-12, atol=1e-12)
+
+
+def test_static_closed_form_and_associative_scan():
+    """A = I, Q = 0 is Bayesian linear regression; recurrence and information-form scan agree."""
+    k, v, q, _, _, r, m0, c0 = _rand(3, 9, 4, 3, seed=6)
+    ones = torch.ones_like(k)
+    zeros = torch.zeros(k.shape[:-1])
+    y, mT, cT = O.run_diagonal(k, v, q, ones, zeros, r, m0, c0, 1e-6)
+    M_cf, P_cf = O.closed_form_static(k, v, r, m0, c0)
+    torch.testing.assert_close(mT, M_cf, rtol=1e-10, atol=1e-11)
+    torch.testing.assert_close(cT, P_cf, rtol=1e-10, atol=1e-11)
+    ys, ms, cs = O.associative_static(k, v, q, r, m0, c0)
+    torch.testing.assert_close(ys, y, rtol=1e-10, atol=1e-11)
+    torch.testing.assert_close(ms, mT, rtol=1e-10, atol=1e-11)
+    torch.testing.assert_close(cs, cT, rtol=1e-10, atol=1e-11)
+    # Every prefix matches the closed form of that prefix.
+    for t in (0, 4, 8):
+        M_t, _ = O.closed_form_static(k[:, : t + 1], v[:, : t + 1], r[:, : t + 1], m0, c0)
+        torch.testing.assert_close(y[:, t], (M_t * q[:, t, :, None]).sum(-2), rtol=1e-10, atol=1e-11)
+
+
+@pytest.mark.parametrize("chunk", [1, 2, 3, 7, 64])
+def test_dense_diagonal_chunked_agree(chunk):
+    """The three recurrence formulations agree (reference tests use 1e-12 / 1e-10)."""
+    k, v, q, dec, p, r, m0, c0 = _rand(2, 11, 4, 3, seed=7)
+    yd, md, cd = O.run_diagonal(k, v, q, dec, p, r, m0, c0, 1e-6)
+    A, Q = O.diagonal_as_dense(dec, p)
+    ye, me, ce = O.run_dense(k, v, q, A, Q, r, m0, c0, 1e-6)
+    yc, mc, cc = O.run_chunked(k, v, q, A, Q, r, m0, c0, chunk, 1e-6)
+    for a, b in ((yd, ye), (md, me), (cd, ce)):
+        torch.testing.assert_close(a, b, rtol=1e-12, atol=1e-12)
+    for a, b in ((yd, yc), (md, mc), (cd, cc)):
+        torch.testing.assert_close(a, b, rtol=1e-10, atol=1e-11)
+
+
+def test_covariance_invariants():
+    """Posterior covariance stays symmetric PSD and below the prediction (P_post <= P_pred)."""
+    k, v, q, dec, p, r, m0, c0 = _rand(4, 20, 4, 2, seed=8)
+    mean, cov = m0, c0
+    for t in range(20):
+        P_pred = dec[:, t, :, None] * cov * dec[:, t, None, :] + p[:, t, None, None] * torch.eye(4)
+        _, mean, cov = O.run_diagonal(k[:, t:t + 1], v[:, t:t + 1], q[:, t:t + 1], dec[:, t:t + 1],
+                                      p[:, t:t + 1], r[:, t:t + 1], mean, cov, 1e-6)
+        assert torch.equal(cov, cov.transpose(-1, -2))
+        assert torch.linalg.eigvalsh(cov).min() > 0
+        assert torch.linalg.eigvalsh(P_pred - cov).min() > -1e-12
+
+
+def test_fixed_dynamics_is_constant_diagonal():
+    k, v, q, _, _, _, m0, c0 = _rand(2, 8, 4, 3, seed=9)
+    yf, mf, cf = O.run_fixed(k, v, q, m0, c0, 1e-6)
+    dec = torch.full_like(k, O.FIXED_DECAY)
+    p = torch.full(k.shape[:-1], O.FIXED_PROCESS)
+    r = torch.full(k.shape[:-1], O.FIXED_OBSERVATION)
+    yd, md, cd = O.run_diagonal(k, v, q, dec, p, r, m0, c0, 1e-6)
+    for a, b in ((yf, yd), (mf, md), (cf, cd)):
+        torch.testing.assert_close(a, b, rtol=1e-12, atol=1e-12)
+
+
+def test_floor_clamps_innovation():
+    """With r + k.u below the floor the gain uses 1/floor (bayesian_layer.py:243)."""
+    k = torch.full((1, 1, 1), 1e-4)
+    v = torch.ones(1, 1, 1)
+    q = torch.ones(1, 1, 1)
+    dec = torch.ones(1, 1, 1)
+    p = torch.zeros(1, 1)
+    r = torch.full((1, 1), 1e-9)
+    m0 = torch.zeros(1, 1, 1)
+    c0 = torch.ones(1, 1, 1)
+    floor = 1e-3
+    y, _, cT = O.run_diagonal(k, v, q, dec, p, r, m0, c0, floor)
+    u = 1e-4
+    assert math.isclose(float(y), u / floor, rel_tol=1e-12)
+    assert math.isclose(float(cT), 1.0 - u * u / floor, rel_tol=1e-12)
+
+
+def test_checkpoint_layout():
+    """bm[:, c] is the belief before token c*chunk, bm[:, nb] the final belief."""
+    k, v, q, dec, p, r, m0, c0 = _rand(2, 10, 2, 3, seed=10)
+    bm, bc = O.checkpoints(k, v, q, dec, p, r, m0, c0, 4, 1e-6)
+    assert bm.shape == (2, 4, 2, 3) and bc.shape == (2, 4, 2, 2)
+    torch.testing.assert_close(bm[:, 0], m0, rtol=0, atol=0)
+    for c, stop in ((1, 4), (2, 8), (3, 10)):
+        _, mt, ct = O.run_diagonal(k[:, :stop], v[:, :stop], q[:, :stop], dec[:, :stop], p[:, :stop],
+                                   r[:, :stop], m0, c0, 1e-6)
+        torch.testing.assert_close(bm[:, c], mt, rtol=1e-13, atol=1e-13)
+        torch.testing.assert_close(bc[:, c], ct, rtol=1e-13, atol=1e-13)
+
+
+def test_gradcheck_diagonal():
+    k, v, q, dec, p, r, m0, c0 = _rand(1, 3, 2, 2, seed=11)
+    leaves = [x.clone().requires_grad_(True) for x in (k, v, q, dec, p, r, m0, c0)]
+
+    def f(*xs):
+        return O.run_diagonal(*xs, 1e-6)
+
+    assert torch.autograd.gradcheck(f, leaves, eps=1e-6, atol=1e-7, rtol=1e-5)
+
+
+def test_gradients_agree_across_formulations():
+    """Autograd of diagonal vs transported-history oracle (reference: 1e-10 / 1e-11)."""
+    k, v, q, dec, p, r, m0, c0 = _rand(2, 9, 3, 2, seed=12)
+    g = torch.Generator().manual_seed(1)
+    gy = torch.randn(2, 9, 2, generator=g)
+    gmf = torch.randn(2, 3, 2, generator=g)
+    gcf = torch.randn(2, 3, 3, generator=g)
+    _, _, _, ga = O.diagonal_grads(k, v, q, dec, p, r, m0, c0, gy, gmf, gcf)
+    _, _, _, gb = O.diagonal_grads(k, v, q, dec, p, r, m0, c0, gy, gmf, gcf, chunk=4)
+    # The transported-history path symmetrises the prediction before u = P' k,
+    # so only the symmetric part of the initial-covariance gradient is shared.
+    for i, (a, b) in enumerate(zip(ga, gb)):
+        if i == 7:
+            a, b = 0.5 * (a + a.transpose(-1, -2)), 0.5 * (b + b.transpose(-1, -2))
+        torch.testing.assert_close(a, b, rtol=1e-9, atol=1e-10)
+
+
+def test_asymmetric_initial_covariance_gradient():
+    """dL/dP0 keeps the row-wise (asymmetric) term from u = P' k: (S + gu k^T) * d d^T."""
+    k, v, q, dec, p, r, m0, c0 = _rand(1, 1, 3, 2, seed=13)
+    g = torch.Generator().manual_seed(2)
+    gy = torch.randn(1, 1, 2, generator=g)
+    _, _, _, grads = O.diagonal_grads(k, v, q, dec, p, r, m0, c0, gy)
+    gc0 = grads[7]
+    assert (gc0 - gc0.transpose(-1, -2)).abs().max() > 1e-6
+    # Finite difference along an antisymmetric direction matches.
+    direction = torch.zeros(1, 3, 3)
+    direction[0, 0, 1], direction[0, 1, 0] = 1.0, -1.0
+    eps = 1e-6
+
+    def loss(c):
+        y, _, _ = O.run_diagonal(k, v, q, dec, p, r, m0, c, 1e-6)
+        return float((y * gy).sum())
+
+    fd = (loss(c0 + eps * direction) - loss(c0 - eps * direction)) / (2 * eps)
+    assert math.isclose(fd, float((gc0 * direction).sum()), rel_tol=1e-6, abs_tol=1e-9)
+
+
+def test_mutation_is_detected():
+    """A planted oracle mistake (process noise dropped) fails the textbook pin."""
+    k, v, q, dec, p, r, m0, c0 = _rand(1, 6, 1, 1, seed=3)
+    _, good, _ = O.run_diagonal(k, v, q, dec, p, r, m0, c0, 1e-6)
+    _, bad, _ = O.run_diagonal(k, v, q, dec, torch.zeros_like(p), r, m0, c0, 1e-6)
+    assert (good - bad).abs().max() > 1e-3
