@@ -16,7 +16,13 @@ import torch
 
 from oracle import bssm_oracle as O
 
-torch.set_default_dtype(torch.float64)
+
+@pytest.fixture(autouse=True)
+def _float64_default():
+    previous = torch.get_default_dtype()
+    torch.set_default_dtype(torch.float64)
+    yield
+    torch.set_default_dtype(previous)
 
 
 def _rand(n, t, d, m, seed, dtype=torch.float64):
