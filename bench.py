@@ -102,6 +102,8 @@ def main() -> int:
     ap.add_argument("--chunk", type=int, default=64)
     ap.add_argument("--kernel-iters", type=int, default=20, help="iterations of the per-kernel event timing")
     ap.add_argument("--cpu-budget", type=float, default=20.0, help="seconds of CPU-baseline work (0 = skip)")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="also run one 256 MiB device copy (reference kernel for PMC byte counters)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: the layer shards over sequences with no exchange, "
@@ -118,6 +120,13 @@ def main() -> int:
     b, t, h, d, m = args.batch, args.seq, args.heads, args.key_dim, 8
     n = b * h
     leaves, m0, c0, gy = make_workload(b, t, h, d, m, device)
+    if args.copy_calibration:
+        # 64 Mi floats read + 64 Mi floats written (256 MiB each way).
+        src = torch.randn(64 << 20, device=device)
+        dst = torch.empty_like(src)
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
 
     def step():
         y, _, _ = fused_cuda.fused_diagonal_bayesian(*leaves, m0, c0, chunk_length=args.chunk,
