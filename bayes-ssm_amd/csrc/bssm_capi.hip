@@ -49,6 +49,9 @@ int check_common(const char* fn, int d, int m, int64_t n, int64_t t, int64_t chu
   if (chunk <= 0) return fail(BSSM_ERR_ARGUMENT, "%s: chunk must be positive, got %lld", fn, (long long)chunk);
   if (!(floor > 0.f)) return fail(BSSM_ERR_ARGUMENT, "%s: denominator_floor must be positive", fn);
   if (n > (int64_t)0x7fffffff * 4) return fail(BSSM_ERR_ARGUMENT, "%s: n too large", fn);
+  // Tile loads address up to 64 sequence rows with 32-bit lane offsets.
+  if (t * (d > m ? d : m) > (int64_t)1 << 25)
+    return fail(BSSM_ERR_ARGUMENT, "%s: t * max(key_dim, value_dim) must be <= 2^25, got t=%lld", fn, (long long)t);
   return BSSM_OK;
 }
 

@@ -153,33 +153,81 @@ struct Tile {
   static constexpr int STRIDE = PER + 4;
 };
 
-// Global -> LDS copy of one tile (tokens [t0, t0 + len) of sequences
-// [n0, n0 + SPW)).  Rows past N and tokens past len are zero-filled so idle
-// lanes compute on finite data.  `vec` selects 16-byte accesses; it must only
-// be set when every accessed 4-float group is 16-byte aligned.
+// This lane's share of one tile of one stream, held in registers between
+// the global loads and the LDS commit.  Every load of a tile is issued before
+// any of them is consumed, so a tile costs one memory latency, and a tile can
+// be loaded while the previous one is being computed.  Element e (a multiple
+// of 4) of the tile belongs to lane (e / 4) % 64; rows past N and tokens past
+// len read as zero so idle lanes compute on finite data.  Requires every
+// 4-float group to be 16-byte aligned (checked by the caller).
 template <int W, int TT, int SPW>
-__device__ __forceinline__ void stage_in(float* __restrict__ lds, const float* __restrict__ g, int64_t n0,
-                                         int64_t n, int64_t t, int64_t t0, int len, bool vec, int lane) {
+struct TileRegs {
+  using T_ = Tile<W, TT>;
+  static constexpr int TOTAL = SPW * T_::PER;
+  static constexpr int NV = (TOTAL + 4 * kWave - 1) / (4 * kWave);
+  // One wave instruction covers 4 * 64 floats = SEQ_STEP whole sequence rows,
+  // so lane l always holds column o0 of rows s0 + it * SEQ_STEP: one lane
+  // offset, and a wave-uniform base that advances per instruction.
+  static constexpr int SEQ_STEP = 4 * kWave / T_::PER;
+  static_assert(T_::PER % 4 == 0 && (4 * kWave) % T_::PER == 0, "tile rows must divide a wave instruction");
+  float4 r[NV];
+
+  // Rows of one tile are `row` floats apart in global memory (row = T * W).
+  __device__ __forceinline__ void load(const float* __restrict__ g, int64_t n0, int64_t n, int64_t t, int64_t t0,
+                                       int len, int lane) {
+    const int s0 = (lane * 4) / T_::PER, o0 = (lane * 4) % T_::PER;
+    const int64_t row = t * W;
+    const float* base = g + n0 * row + t0 * W;
+    const uint32_t off = static_cast<uint32_t>(s0) * static_cast<uint32_t>(row) + static_cast<uint32_t>(o0);
+    const bool col_ok = o0 < len * W;
+#pragma unroll
+    for (int it = 0; it < NV; ++it) {
+      const int s = s0 + it * SEQ_STEP;
+      float4 val = make_float4(0.f, 0.f, 0.f, 0.f);
+      if (s < SPW && col_ok && n0 + s < n)
+        val = *reinterpret_cast<const float4*>(base + static_cast<int64_t>(it * SEQ_STEP) * row + off);
+      r[it] = val;
+    }
+  }
+
+  __device__ __forceinline__ void commit(float* __restrict__ lds, int lane) const {
+    const int s0 = (lane * 4) / T_::PER, o0 = (lane * 4) % T_::PER;
+    float* dst = lds + s0 * T_::STRIDE + o0;
+#pragma unroll
+    for (int it = 0; it < NV; ++it) {
+      if (s0 + it * SEQ_STEP < SPW)
+        *reinterpret_cast<float4*>(dst + it * SEQ_STEP * T_::STRIDE) = r[it];
+    }
+  }
+};
+
+// Scalar global -> LDS copy of one tile, for streams whose rows are not
+// 16-byte aligned (T * W not a multiple of 4, or an unaligned base pointer).
+// A compact rolled loop: this is the rarely used fallback, kept small so it
+// does not inflate the register budget of the fast path.
+template <int W, int TT, int SPW>
+__device__ __forceinline__ void stage_in_scalar(float* __restrict__ lds, const float* __restrict__ g, int64_t n0,
+                                                int64_t n, int64_t t, int64_t t0, int len, int lane) {
   using T_ = Tile<W, TT>;
   constexpr int TOTAL = SPW * T_::PER;
   const int valid = len * W;
+#pragma unroll 1
+  for (int e = lane; e < TOTAL; e += kWave) {
+    const int s = e / T_::PER, o = e - s * T_::PER;
+    lds[s * T_::STRIDE + o] = (n0 + s < n && o < valid) ? g[((n0 + s) * t + t0) * W + o] : 0.f;
+  }
+}
+
+// Register-staged copy of one tile (loads, then LDS commit).
+template <int W, int TT, int SPW>
+__device__ __forceinline__ void stage_in(float* __restrict__ lds, const float* __restrict__ g, int64_t n0,
+                                         int64_t n, int64_t t, int64_t t0, int len, bool vec, int lane) {
   if (vec) {
-#pragma unroll
-    for (int e = lane * 4; e < TOTAL; e += kWave * 4) {
-      const int s = e / T_::PER, o = e - s * T_::PER;
-      float4 val = make_float4(0.f, 0.f, 0.f, 0.f);
-      if (n0 + s < n && o < valid)
-        val = *reinterpret_cast<const float4*>(g + ((n0 + s) * t + t0) * W + o);
-      *reinterpret_cast<float4*>(lds + s * T_::STRIDE + o) = val;
-    }
+    TileRegs<W, TT, SPW> regs;
+    regs.load(g, n0, n, t, t0, len, lane);
+    regs.commit(lds, lane);
   } else {
-#pragma unroll
-    for (int e = lane; e < TOTAL; e += kWave) {
-      const int s = e / T_::PER, o = e - s * T_::PER;
-      float val = 0.f;
-      if (n0 + s < n && o < valid) val = g[((n0 + s) * t + t0) * W + o];
-      lds[s * T_::STRIDE + o] = val;
-    }
+    stage_in_scalar<W, TT, SPW>(lds, g, n0, n, t, t0, len, lane);
   }
 }
 
@@ -191,15 +239,21 @@ __device__ __forceinline__ void stage_out(const float* __restrict__ lds, float* 
   constexpr int TOTAL = SPW * T_::PER;
   const int valid = len * W;
   if (vec) {
+    using R = TileRegs<W, TT, SPW>;
+    const int s0 = (lane * 4) / T_::PER, o0 = (lane * 4) % T_::PER;
+    const int64_t row = t * W;
+    float* base = g + n0 * row + t0 * W;
+    const uint32_t off = static_cast<uint32_t>(s0) * static_cast<uint32_t>(row) + static_cast<uint32_t>(o0);
+    const float* src = lds + s0 * T_::STRIDE + o0;
 #pragma unroll
-    for (int e = lane * 4; e < TOTAL; e += kWave * 4) {
-      const int s = e / T_::PER, o = e - s * T_::PER;
-      if (n0 + s < n && o < valid)
-        *reinterpret_cast<float4*>(g + ((n0 + s) * t + t0) * W + o) =
-            *reinterpret_cast<const float4*>(lds + s * T_::STRIDE + o);
+    for (int it = 0; it < R::NV; ++it) {
+      const int s = s0 + it * R::SEQ_STEP;
+      if (s < SPW && o0 < valid && n0 + s < n)
+        *reinterpret_cast<float4*>(base + static_cast<int64_t>(it * R::SEQ_STEP) * row + off) =
+            *reinterpret_cast<const float4*>(src + it * R::SEQ_STEP * T_::STRIDE);
     }
   } else {
-#pragma unroll
+#pragma unroll 1
     for (int e = lane; e < TOTAL; e += kWave) {
       const int s = e / T_::PER, o = e - s * T_::PER;
       if (n0 + s < n && o < valid) g[((n0 + s) * t + t0) * W + o] = lds[s * T_::STRIDE + o];

@@ -67,22 +67,51 @@ __global__ __launch_bounds__(kWave) void forward_kernel(FwdArgs a) {
   const float* qs = sq + s * SD;
   float* ys = sv + s * SM;
 
+  // All streams 16-byte aligned for every tile: register-staged loads with
+  // the next tile in flight while this one is computed.  Otherwise scalar
+  // staging per tile.
+  const bool vec = a.vec_kqd && a.vec_v && a.vec_pr;
+  TileRegs<D, TT, SPW> rk, rq, rd;
+  TileRegs<M, TT, SPW> rv;
+  TileRegs<1, TT, SPW> rp, rr;
+  auto issue = [&](int64_t t0) {
+    const int len = tile_len(T, t0, TT);
+    rk.load(a.k, n0, a.n, T, t0, len, lane);
+    rq.load(a.q, n0, a.n, T, t0, len, lane);
+    rv.load(a.v, n0, a.n, T, t0, len, lane);
+    if constexpr (!FIXED) {
+      rd.load(a.d, n0, a.n, T, t0, len, lane);
+      rp.load(a.p, n0, a.n, T, t0, len, lane);
+      rr.load(a.r, n0, a.n, T, t0, len, lane);
+    }
+  };
+  if (vec && T > 0) issue(0);
+
   int64_t next_ckpt = a.chunk;
   int64_t ckpt = 1;
   for (int64_t t0 = 0; t0 < T; t0 += TT) {
     const int len = tile_len(T, t0, TT);
-    const bool vq = a.vec_kqd && ((t0 * D) % 4 == 0);
-    const bool vv = a.vec_v && ((t0 * M) % 4 == 0);
-    const bool vp = a.vec_pr && (t0 % 4 == 0);
-    stage_in<D, TT, SPW>(sk, a.k, n0, a.n, T, t0, len, vq, lane);
-    stage_in<D, TT, SPW>(sq, a.q, n0, a.n, T, t0, len, vq, lane);
-    stage_in<M, TT, SPW>(sv, a.v, n0, a.n, T, t0, len, vv, lane);
-    if constexpr (!FIXED) {
-      stage_in<D, TT, SPW>(sd, a.d, n0, a.n, T, t0, len, vq, lane);
-      stage_in<1, TT, SPW>(sp, a.p, n0, a.n, T, t0, len, vp, lane);
-      stage_in<1, TT, SPW>(sr, a.r, n0, a.n, T, t0, len, vp, lane);
+    if (vec) {
+      rk.commit(sk, lane);
+      rq.commit(sq, lane);
+      rv.commit(sv, lane);
+      if constexpr (!FIXED) {
+        rd.commit(sd, lane);
+        rp.commit(sp, lane);
+        rr.commit(sr, lane);
+      }
+    } else {
+      stage_in_scalar<D, TT, SPW>(sk, a.k, n0, a.n, T, t0, len, lane);
+      stage_in_scalar<D, TT, SPW>(sq, a.q, n0, a.n, T, t0, len, lane);
+      stage_in_scalar<M, TT, SPW>(sv, a.v, n0, a.n, T, t0, len, lane);
+      if constexpr (!FIXED) {
+        stage_in_scalar<D, TT, SPW>(sd, a.d, n0, a.n, T, t0, len, lane);
+        stage_in_scalar<1, TT, SPW>(sp, a.p, n0, a.n, T, t0, len, lane);
+        stage_in_scalar<1, TT, SPW>(sr, a.r, n0, a.n, T, t0, len, lane);
+      }
     }
     __syncthreads();
+    if (vec && t0 + TT < T) issue(t0 + TT);
     for (int tt = 0; tt < len; ++tt) {
       if (t0 + tt == next_ckpt) {
         if (active)
@@ -106,7 +135,7 @@ __global__ __launch_bounds__(kWave) void forward_kernel(FwdArgs a) {
       }
     }
     __syncthreads();
-    stage_out<M, TT, SPW>(sv, a.y, n0, a.n, T, t0, len, vv, lane);
+    stage_out<M, TT, SPW>(sv, a.y, n0, a.n, T, t0, len, vec, lane);
     __syncthreads();
   }
   if (active) {
@@ -190,6 +219,7 @@ __global__ __launch_bounds__(kWave) void backward_kernel(BwdArgs a) {
   float* grs = sr + s * S1;
 
   const int64_t bm_seq = (a.nb + 1) * D * M, bc_seq = (a.nb + 1) * D * D;
+  const bool vec_all = a.vec_kqd && a.vec_v && a.vec_pr;
   for (int64_t c = a.nb - 1; c >= 0; --c) {
     const int64_t tc0 = c * a.chunk;
     const int64_t lc = (T - tc0) < a.chunk ? (T - tc0) : a.chunk;
@@ -200,15 +230,13 @@ __global__ __launch_bounds__(kWave) void backward_kernel(BwdArgs a) {
       // Advance from the chunk checkpoint to the start of piece sc.
       for (int j = 0; j < sc; ++j) {
         const int64_t ts = tc0 + static_cast<int64_t>(j) * SUB;
-        const bool vq = a.vec_kqd && ((ts * D) % 4 == 0);
-        const bool vv = a.vec_v && ((ts * M) % 4 == 0);
-        const bool vp = a.vec_pr && (ts % 4 == 0);
-        stage_in<D, SUB, SPW>(sk, a.k, n0, a.n, T, ts, SUB, vq, lane);
-        stage_in<M, SUB, SPW>(sv, a.v, n0, a.n, T, ts, SUB, vv, lane);
+        const bool vec = vec_all && (ts % 4 == 0);
+        stage_in<D, SUB, SPW>(sk, a.k, n0, a.n, T, ts, SUB, vec, lane);
+        stage_in<M, SUB, SPW>(sv, a.v, n0, a.n, T, ts, SUB, vec, lane);
         if constexpr (!FIXED) {
-          stage_in<D, SUB, SPW>(sd, a.d, n0, a.n, T, ts, SUB, vq, lane);
-          stage_in<1, SUB, SPW>(sp, a.p, n0, a.n, T, ts, SUB, vp, lane);
-          stage_in<1, SUB, SPW>(sr, a.r, n0, a.n, T, ts, SUB, vp, lane);
+          stage_in<D, SUB, SPW>(sd, a.d, n0, a.n, T, ts, SUB, vec, lane);
+          stage_in<1, SUB, SPW>(sp, a.p, n0, a.n, T, ts, SUB, vec, lane);
+          stage_in<1, SUB, SPW>(sr, a.r, n0, a.n, T, ts, SUB, vec, lane);
         }
         __syncthreads();
         for (int tt = 0; tt < SUB; ++tt) {
@@ -221,17 +249,40 @@ __global__ __launch_bounds__(kWave) void backward_kernel(BwdArgs a) {
       }
       const int64_t ts = tc0 + static_cast<int64_t>(sc) * SUB;
       const int len = static_cast<int>((lc - sc * SUB) < SUB ? (lc - sc * SUB) : SUB);
-      const bool vq = a.vec_kqd && ((ts * D) % 4 == 0);
-      const bool vv = a.vec_v && ((ts * M) % 4 == 0);
-      const bool vp = a.vec_pr && (ts % 4 == 0);
-      stage_in<D, SUB, SPW>(sk, a.k, n0, a.n, T, ts, len, vq, lane);
-      stage_in<D, SUB, SPW>(sq, a.q, n0, a.n, T, ts, len, vq, lane);
-      stage_in<M, SUB, SPW>(sv, a.v, n0, a.n, T, ts, len, vv, lane);
-      stage_in<M, SUB, SPW>(sg, a.gy, n0, a.n, T, ts, len, vv, lane);
-      if constexpr (!FIXED) {
-        stage_in<D, SUB, SPW>(sd, a.d, n0, a.n, T, ts, len, vq, lane);
-        stage_in<1, SUB, SPW>(sp, a.p, n0, a.n, T, ts, len, vp, lane);
-        stage_in<1, SUB, SPW>(sr, a.r, n0, a.n, T, ts, len, vp, lane);
+      const bool vec = vec_all && (ts % 4 == 0);
+      const bool vq = vec, vv = vec, vp = vec;
+      if (vec) {
+        TileRegs<D, SUB, SPW> rk, rq, rd;
+        TileRegs<M, SUB, SPW> rv, rg;
+        TileRegs<1, SUB, SPW> rp, rr;
+        rk.load(a.k, n0, a.n, T, ts, len, lane);
+        rq.load(a.q, n0, a.n, T, ts, len, lane);
+        rv.load(a.v, n0, a.n, T, ts, len, lane);
+        rg.load(a.gy, n0, a.n, T, ts, len, lane);
+        if constexpr (!FIXED) {
+          rd.load(a.d, n0, a.n, T, ts, len, lane);
+          rp.load(a.p, n0, a.n, T, ts, len, lane);
+          rr.load(a.r, n0, a.n, T, ts, len, lane);
+        }
+        rk.commit(sk, lane);
+        rq.commit(sq, lane);
+        rv.commit(sv, lane);
+        rg.commit(sg, lane);
+        if constexpr (!FIXED) {
+          rd.commit(sd, lane);
+          rp.commit(sp, lane);
+          rr.commit(sr, lane);
+        }
+      } else {
+        stage_in_scalar<D, SUB, SPW>(sk, a.k, n0, a.n, T, ts, len, lane);
+        stage_in_scalar<D, SUB, SPW>(sq, a.q, n0, a.n, T, ts, len, lane);
+        stage_in_scalar<M, SUB, SPW>(sv, a.v, n0, a.n, T, ts, len, lane);
+        stage_in_scalar<M, SUB, SPW>(sg, a.gy, n0, a.n, T, ts, len, lane);
+        if constexpr (!FIXED) {
+          stage_in_scalar<D, SUB, SPW>(sd, a.d, n0, a.n, T, ts, len, lane);
+          stage_in_scalar<1, SUB, SPW>(sp, a.p, n0, a.n, T, ts, len, lane);
+          stage_in_scalar<1, SUB, SPW>(sr, a.r, n0, a.n, T, ts, len, lane);
+        }
       }
       __syncthreads();
 
