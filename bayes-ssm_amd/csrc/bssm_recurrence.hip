@@ -220,160 +220,190 @@ __global__ __launch_bounds__(kWave) void backward_kernel(BwdArgs a) {
 
   const int64_t bm_seq = (a.nb + 1) * D * M, bc_seq = (a.nb + 1) * D * D;
   const bool vec_all = a.vec_kqd && a.vec_v && a.vec_pr;
-  for (int64_t c = a.nb - 1; c >= 0; --c) {
-    const int64_t tc0 = c * a.chunk;
-    const int64_t lc = (T - tc0) < a.chunk ? (T - tc0) : a.chunk;
-    const int nsub = static_cast<int>((lc + SUB - 1) / SUB);
-    for (int sc = nsub - 1; sc >= 0; --sc) {
-      Belief<D, M, G> b;
-      load_belief<D, M, G>(b, a.bm + na * bm_seq + c * D * M, a.bc + na * bc_seq + c * D * D, g, active);
-      // Advance from the chunk checkpoint to the start of piece sc.
-      for (int j = 0; j < sc; ++j) {
-        const int64_t ts = tc0 + static_cast<int64_t>(j) * SUB;
+
+  // Replay tokens [ts, ts + len) of the staged piece from belief b, keeping
+  // the replay history in registers, then run the reverse over them; the
+  // gradients overwrite the input tiles in LDS.
+  auto run_piece = [&](Belief<D, M, G>& b, int64_t ts, int len) {
+    Hist<D, M, G> h[SUB];
+#pragma unroll
+    for (int tt = 0; tt < SUB; ++tt) {
+      if (tt < len) {
+        TokenIn<D, M, G> in;
+        read_token<D, M, G, FIXED>(in, st, tt, g, true);
+#pragma unroll
+        for (int jj = 0; jj < RPL; ++jj)
+#pragma unroll
+          for (int j = 0; j < D; ++j) h[tt].Pp[jj][j] = b.P[jj][j];
+#pragma unroll
+        for (int i = 0; i < D; ++i)
+#pragma unroll
+          for (int cc = 0; cc < CPL; ++cc) h[tt].Mp[i][cc] = b.Mv[i][cc];
+        StepOut<D, M, G> o;
+        forward_step<D, M, G>(b, in, eye, a.floor, lane, o);
+#pragma unroll
+        for (int j = 0; j < D; ++j) h[tt].u[j] = o.u[j];
+#pragma unroll
+        for (int jj = 0; jj < RPL; ++jj) h[tt].u_own[jj] = o.u_own[jj];
+        h[tt].s = o.s;
+#pragma unroll
+        for (int cc = 0; cc < CPL; ++cc) h[tt].e[cc] = o.e[cc];
+      }
+    }
+#pragma unroll
+    for (int tt = SUB - 1; tt >= 0; --tt) {
+      if (tt < len) {
+        TokenIn<D, M, G> in;
+        read_token<D, M, G, FIXED>(in, st, tt, g, false);
+        const Hist<D, M, G>& hh = h[tt];
+        RevIn<D, M, G> x;
+#pragma unroll
+        for (int j = 0; j < D; ++j) x.q[j] = gqs[tt * D + j];
+#pragma unroll
+        for (int cc = 0; cc < CPL; ++cc) x.gy[cc] = gys[tt * M + g * CPL + cc];
+        x.beta = fast_rcp(fmaxf(hh.s, a.floor));
+        x.s = hh.s;
+#pragma unroll
+        for (int j = 0; j < D; ++j) x.u[j] = hh.u[j];
+#pragma unroll
+        for (int jj = 0; jj < RPL; ++jj) x.u_own[jj] = hh.u_own[jj];
+#pragma unroll
+        for (int cc = 0; cc < CPL; ++cc) x.e[cc] = hh.e[cc];
+#pragma unroll
+        for (int i = 0; i < D; ++i)
+#pragma unroll
+          for (int cc = 0; cc < CPL; ++cc) {
+            x.Mprev[i][cc] = hh.Mp[i][cc];
+            x.mp[i][cc] = in.d[i] * hh.Mp[i][cc];
+          }
+#pragma unroll
+        for (int jj = 0; jj < RPL; ++jj)
+#pragma unroll
+          for (int j = 0; j < D; ++j) {
+            x.Pprev[jj][j] = hh.Pp[jj][j];
+            x.Pb[jj][j] = fmaf(in.p, eye[jj][j], (in.d_own[jj] * in.d[j]) * hh.Pp[jj][j]);
+          }
+        RevOut<D, M, G> o;
+        reverse_step<D, M, G, DYN>(in, x, gM, Gs, eye, a.floor, g, lane, ts + tt == 0, gc0r, o);
+        if (writer) {
+#pragma unroll
+          for (int jj = 0; jj < RPL; ++jj) {
+            const int rr = L::row(g, jj);
+            gks[tt * D + rr] = o.gk_own[jj];
+            gqs[tt * D + rr] = o.gq_own[jj];
+            gds[tt * D + rr] = o.gd_own[jj];
+          }
+        }
+#pragma unroll
+        for (int cc = 0; cc < CPL; ++cc) gvs[tt * M + g * CPL + cc] = o.gv[cc];
+        if (g == 0) {
+          gps[tt] = o.gp;
+          grs[tt] = o.gr;
+        }
+      }
+    }
+  };
+
+  auto store_grads = [&](int64_t ts, int len, bool vec) {
+    stage_out<D, SUB, SPW>(sk, a.gk, n0, a.n, T, ts, len, vec, lane);
+    stage_out<D, SUB, SPW>(sq, a.gq, n0, a.n, T, ts, len, vec, lane);
+    stage_out<M, SUB, SPW>(sv, a.gv, n0, a.n, T, ts, len, vec, lane);
+    if (a.gd) stage_out<D, SUB, SPW>(sd, a.gd, n0, a.n, T, ts, len, vec, lane);
+    if (a.gp) stage_out<1, SUB, SPW>(sp, a.gp, n0, a.n, T, ts, len, vec, lane);
+    if (a.gr) stage_out<1, SUB, SPW>(sr, a.gr, n0, a.n, T, ts, len, vec, lane);
+  };
+
+  if (vec_all && a.chunk <= SUB && a.chunk % 4 == 0) {
+    // Hot path: one replay piece per checkpoint chunk.  The inputs and the
+    // checkpoint belief of chunk c-1 are loaded into registers while chunk c
+    // is replayed and reversed.
+    TileRegs<D, SUB, SPW> rk, rq, rd;
+    TileRegs<M, SUB, SPW> rv, rg;
+    TileRegs<1, SUB, SPW> rp, rr;
+    Belief<D, M, G> nb_belief;
+    auto issue = [&](int64_t c) {
+      const int64_t ts = c * a.chunk;
+      const int len = tile_len(T, ts, static_cast<int>(a.chunk));
+      rk.load(a.k, n0, a.n, T, ts, len, lane);
+      rq.load(a.q, n0, a.n, T, ts, len, lane);
+      rv.load(a.v, n0, a.n, T, ts, len, lane);
+      rg.load(a.gy, n0, a.n, T, ts, len, lane);
+      if constexpr (!FIXED) {
+        rd.load(a.d, n0, a.n, T, ts, len, lane);
+        rp.load(a.p, n0, a.n, T, ts, len, lane);
+        rr.load(a.r, n0, a.n, T, ts, len, lane);
+      }
+      load_belief<D, M, G>(nb_belief, a.bm + na * bm_seq + c * D * M, a.bc + na * bc_seq + c * D * D, g, active);
+    };
+    if (a.nb > 0) issue(a.nb - 1);
+    for (int64_t c = a.nb - 1; c >= 0; --c) {
+      const int64_t ts = c * a.chunk;
+      const int len = tile_len(T, ts, static_cast<int>(a.chunk));
+      rk.commit(sk, lane);
+      rq.commit(sq, lane);
+      rv.commit(sv, lane);
+      rg.commit(sg, lane);
+      if constexpr (!FIXED) {
+        rd.commit(sd, lane);
+        rp.commit(sp, lane);
+        rr.commit(sr, lane);
+      }
+      Belief<D, M, G> b = nb_belief;
+      __syncthreads();
+      if (c > 0) issue(c - 1);
+      run_piece(b, ts, len);
+      __syncthreads();
+      store_grads(ts, len, true);
+      __syncthreads();
+    }
+  } else {
+    // General path: chunks longer than SUB are replayed piece by piece from
+    // their checkpoint; tiles are staged synchronously.
+    for (int64_t c = a.nb - 1; c >= 0; --c) {
+      const int64_t tc0 = c * a.chunk;
+      const int64_t lc = (T - tc0) < a.chunk ? (T - tc0) : a.chunk;
+      const int nsub = static_cast<int>((lc + SUB - 1) / SUB);
+      for (int sc = nsub - 1; sc >= 0; --sc) {
+        Belief<D, M, G> b;
+        load_belief<D, M, G>(b, a.bm + na * bm_seq + c * D * M, a.bc + na * bc_seq + c * D * D, g, active);
+        for (int j = 0; j < sc; ++j) {
+          const int64_t ts = tc0 + static_cast<int64_t>(j) * SUB;
+          const bool vec = vec_all && (ts % 4 == 0);
+          stage_in<D, SUB, SPW>(sk, a.k, n0, a.n, T, ts, SUB, vec, lane);
+          stage_in<M, SUB, SPW>(sv, a.v, n0, a.n, T, ts, SUB, vec, lane);
+          if constexpr (!FIXED) {
+            stage_in<D, SUB, SPW>(sd, a.d, n0, a.n, T, ts, SUB, vec, lane);
+            stage_in<1, SUB, SPW>(sp, a.p, n0, a.n, T, ts, SUB, vec, lane);
+            stage_in<1, SUB, SPW>(sr, a.r, n0, a.n, T, ts, SUB, vec, lane);
+          }
+          __syncthreads();
+#pragma unroll 1
+          for (int tt = 0; tt < SUB; ++tt) {
+            TokenIn<D, M, G> in;
+            read_token<D, M, G, FIXED>(in, st, tt, g, true);
+            StepOut<D, M, G> o;
+            forward_step<D, M, G>(b, in, eye, a.floor, lane, o);
+          }
+          __syncthreads();
+        }
+        const int64_t ts = tc0 + static_cast<int64_t>(sc) * SUB;
+        const int len = static_cast<int>((lc - sc * SUB) < SUB ? (lc - sc * SUB) : SUB);
         const bool vec = vec_all && (ts % 4 == 0);
-        stage_in<D, SUB, SPW>(sk, a.k, n0, a.n, T, ts, SUB, vec, lane);
-        stage_in<M, SUB, SPW>(sv, a.v, n0, a.n, T, ts, SUB, vec, lane);
+        stage_in<D, SUB, SPW>(sk, a.k, n0, a.n, T, ts, len, vec, lane);
+        stage_in<D, SUB, SPW>(sq, a.q, n0, a.n, T, ts, len, vec, lane);
+        stage_in<M, SUB, SPW>(sv, a.v, n0, a.n, T, ts, len, vec, lane);
+        stage_in<M, SUB, SPW>(sg, a.gy, n0, a.n, T, ts, len, vec, lane);
         if constexpr (!FIXED) {
-          stage_in<D, SUB, SPW>(sd, a.d, n0, a.n, T, ts, SUB, vec, lane);
-          stage_in<1, SUB, SPW>(sp, a.p, n0, a.n, T, ts, SUB, vec, lane);
-          stage_in<1, SUB, SPW>(sr, a.r, n0, a.n, T, ts, SUB, vec, lane);
+          stage_in<D, SUB, SPW>(sd, a.d, n0, a.n, T, ts, len, vec, lane);
+          stage_in<1, SUB, SPW>(sp, a.p, n0, a.n, T, ts, len, vec, lane);
+          stage_in<1, SUB, SPW>(sr, a.r, n0, a.n, T, ts, len, vec, lane);
         }
         __syncthreads();
-        for (int tt = 0; tt < SUB; ++tt) {
-          TokenIn<D, M, G> in;
-          read_token<D, M, G, FIXED>(in, st, tt, g, true);
-          StepOut<D, M, G> o;
-          forward_step<D, M, G>(b, in, eye, a.floor, lane, o);
-        }
+        run_piece(b, ts, len);
+        __syncthreads();
+        store_grads(ts, len, vec);
         __syncthreads();
       }
-      const int64_t ts = tc0 + static_cast<int64_t>(sc) * SUB;
-      const int len = static_cast<int>((lc - sc * SUB) < SUB ? (lc - sc * SUB) : SUB);
-      const bool vec = vec_all && (ts % 4 == 0);
-      const bool vq = vec, vv = vec, vp = vec;
-      if (vec) {
-        TileRegs<D, SUB, SPW> rk, rq, rd;
-        TileRegs<M, SUB, SPW> rv, rg;
-        TileRegs<1, SUB, SPW> rp, rr;
-        rk.load(a.k, n0, a.n, T, ts, len, lane);
-        rq.load(a.q, n0, a.n, T, ts, len, lane);
-        rv.load(a.v, n0, a.n, T, ts, len, lane);
-        rg.load(a.gy, n0, a.n, T, ts, len, lane);
-        if constexpr (!FIXED) {
-          rd.load(a.d, n0, a.n, T, ts, len, lane);
-          rp.load(a.p, n0, a.n, T, ts, len, lane);
-          rr.load(a.r, n0, a.n, T, ts, len, lane);
-        }
-        rk.commit(sk, lane);
-        rq.commit(sq, lane);
-        rv.commit(sv, lane);
-        rg.commit(sg, lane);
-        if constexpr (!FIXED) {
-          rd.commit(sd, lane);
-          rp.commit(sp, lane);
-          rr.commit(sr, lane);
-        }
-      } else {
-        stage_in_scalar<D, SUB, SPW>(sk, a.k, n0, a.n, T, ts, len, lane);
-        stage_in_scalar<D, SUB, SPW>(sq, a.q, n0, a.n, T, ts, len, lane);
-        stage_in_scalar<M, SUB, SPW>(sv, a.v, n0, a.n, T, ts, len, lane);
-        stage_in_scalar<M, SUB, SPW>(sg, a.gy, n0, a.n, T, ts, len, lane);
-        if constexpr (!FIXED) {
-          stage_in_scalar<D, SUB, SPW>(sd, a.d, n0, a.n, T, ts, len, lane);
-          stage_in_scalar<1, SUB, SPW>(sp, a.p, n0, a.n, T, ts, len, lane);
-          stage_in_scalar<1, SUB, SPW>(sr, a.r, n0, a.n, T, ts, len, lane);
-        }
-      }
-      __syncthreads();
-
-      // Replay the piece and keep what the reverse needs.
-      Hist<D, M, G> h[SUB];
-#pragma unroll
-      for (int tt = 0; tt < SUB; ++tt) {
-        if (tt < len) {
-          TokenIn<D, M, G> in;
-          read_token<D, M, G, FIXED>(in, st, tt, g, true);
-#pragma unroll
-          for (int jj = 0; jj < RPL; ++jj)
-#pragma unroll
-            for (int j = 0; j < D; ++j) h[tt].Pp[jj][j] = b.P[jj][j];
-#pragma unroll
-          for (int i = 0; i < D; ++i)
-#pragma unroll
-            for (int cc = 0; cc < CPL; ++cc) h[tt].Mp[i][cc] = b.Mv[i][cc];
-          StepOut<D, M, G> o;
-          forward_step<D, M, G>(b, in, eye, a.floor, lane, o);
-#pragma unroll
-          for (int j = 0; j < D; ++j) h[tt].u[j] = o.u[j];
-#pragma unroll
-          for (int jj = 0; jj < RPL; ++jj) h[tt].u_own[jj] = o.u_own[jj];
-          h[tt].s = o.s;
-#pragma unroll
-          for (int cc = 0; cc < CPL; ++cc) h[tt].e[cc] = o.e[cc];
-        }
-      }
-
-      // Reverse over the piece.
-#pragma unroll
-      for (int tt = SUB - 1; tt >= 0; --tt) {
-        if (tt < len) {
-          TokenIn<D, M, G> in;
-          read_token<D, M, G, FIXED>(in, st, tt, g, false);
-          const Hist<D, M, G>& hh = h[tt];
-          RevIn<D, M, G> x;
-#pragma unroll
-          for (int j = 0; j < D; ++j) x.q[j] = gqs[tt * D + j];
-#pragma unroll
-          for (int cc = 0; cc < CPL; ++cc) x.gy[cc] = gys[tt * M + g * CPL + cc];
-          x.beta = fast_rcp(fmaxf(hh.s, a.floor));
-          x.s = hh.s;
-#pragma unroll
-          for (int j = 0; j < D; ++j) x.u[j] = hh.u[j];
-#pragma unroll
-          for (int jj = 0; jj < RPL; ++jj) x.u_own[jj] = hh.u_own[jj];
-#pragma unroll
-          for (int cc = 0; cc < CPL; ++cc) x.e[cc] = hh.e[cc];
-#pragma unroll
-          for (int i = 0; i < D; ++i)
-#pragma unroll
-            for (int cc = 0; cc < CPL; ++cc) {
-              x.Mprev[i][cc] = hh.Mp[i][cc];
-              x.mp[i][cc] = in.d[i] * hh.Mp[i][cc];
-            }
-#pragma unroll
-          for (int jj = 0; jj < RPL; ++jj)
-#pragma unroll
-            for (int j = 0; j < D; ++j) {
-              x.Pprev[jj][j] = hh.Pp[jj][j];
-              x.Pb[jj][j] = fmaf(in.p, eye[jj][j], (in.d_own[jj] * in.d[j]) * hh.Pp[jj][j]);
-            }
-          RevOut<D, M, G> o;
-          reverse_step<D, M, G, DYN>(in, x, gM, Gs, eye, a.floor, g, lane, ts + tt == 0, gc0r, o);
-          if (writer) {
-#pragma unroll
-            for (int jj = 0; jj < RPL; ++jj) {
-              const int rr = L::row(g, jj);
-              gks[tt * D + rr] = o.gk_own[jj];
-              gqs[tt * D + rr] = o.gq_own[jj];
-              gds[tt * D + rr] = o.gd_own[jj];
-            }
-          }
-#pragma unroll
-          for (int cc = 0; cc < CPL; ++cc) gvs[tt * M + g * CPL + cc] = o.gv[cc];
-          if (g == 0) {
-            gps[tt] = o.gp;
-            grs[tt] = o.gr;
-          }
-        }
-      }
-      __syncthreads();
-      stage_out<D, SUB, SPW>(sk, a.gk, n0, a.n, T, ts, len, vq, lane);
-      stage_out<D, SUB, SPW>(sq, a.gq, n0, a.n, T, ts, len, vq, lane);
-      stage_out<M, SUB, SPW>(sv, a.gv, n0, a.n, T, ts, len, vv, lane);
-      if (a.gd) stage_out<D, SUB, SPW>(sd, a.gd, n0, a.n, T, ts, len, vq, lane);
-      if (a.gp) stage_out<1, SUB, SPW>(sp, a.gp, n0, a.n, T, ts, len, vp, lane);
-      if (a.gr) stage_out<1, SUB, SPW>(sr, a.gr, n0, a.n, T, ts, len, vp, lane);
-      __syncthreads();
     }
   }
 
