@@ -16,8 +16,10 @@ from pathlib import Path
 
 ROOT = Path(__file__).resolve().parent
 CSRC = ROOT / "csrc"
-OUT = ROOT / "bayes_ssm" / "libbssm_hip.so"
-BUILD = ROOT / "_build"
+OUT = Path(os.environ.get("BSSM_BUILD_OUT", ROOT / "bayes_ssm" / "libbssm_hip.so"))
+BUILD = Path(os.environ.get("BSSM_BUILD_DIR", ROOT / "_build"))
+# Extra compiler flags (e.g. -D tuning macros) for experiments.
+EXTRA = os.environ.get("BSSM_EXTRA_FLAGS", "").split()
 ARCH = os.environ.get("BSSM_OFFLOAD_ARCH", "gfx950")
 
 COMMON_FLAGS = [
@@ -30,6 +32,7 @@ COMMON_FLAGS = [
     "-Wall",
     "-Wno-unused-function",
     "-Wno-unused-variable",
+    *EXTRA,
 ]
 
 
@@ -53,7 +56,8 @@ def _compile(src: Path) -> Path:
 
 
 def build(verbose: bool = True) -> Path:
-    BUILD.mkdir(exist_ok=True)
+    BUILD.mkdir(parents=True, exist_ok=True)
+    OUT.parent.mkdir(parents=True, exist_ok=True)
     sources = sorted(CSRC.glob("*.hip"))
     with concurrent.futures.ThreadPoolExecutor(max_workers=min(8, len(sources))) as pool:
         objects = list(pool.map(_compile, sources))
@@ -64,7 +68,7 @@ def build(verbose: bool = True) -> Path:
         raise RuntimeError(f"link failed:\n{proc.stderr}")
     os.replace(tmp, OUT)
     if verbose:
-        print(f"built {OUT.relative_to(ROOT.parent)}")
+        print(f"built {OUT}")
     return OUT
 
 

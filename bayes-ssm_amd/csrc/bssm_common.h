@@ -17,6 +17,31 @@ namespace bssm {
 
 constexpr int kWave = 64;
 
+// Native 4-float vector (the builtins below need a plain vector type).
+typedef float v4f __attribute__((ext_vector_type(4)));
+
+// Streamed data is touched once per pass.  Tile rows that cover whole
+// 128-byte lines use nontemporal accesses (no L2 retention); shorter row
+// segments (e.g. 8 tokens of a per-token scalar = 32 bytes) use ordinary
+// accesses so the rest of the line stays in L2 for the neighbouring tiles.
+// The byte thresholds are measured tuning choices.
+#ifndef BSSM_NT_LOAD_MIN
+#define BSSM_NT_LOAD_MIN 128
+#endif
+#ifndef BSSM_NT_STORE_MIN
+#define BSSM_NT_STORE_MIN 128
+#endif
+template <bool NT>
+__device__ __forceinline__ v4f load_stream(const float* p) {
+  if constexpr (NT) return __builtin_nontemporal_load(reinterpret_cast<const v4f*>(p));
+  else return *reinterpret_cast<const v4f*>(p);
+}
+template <bool NT>
+__device__ __forceinline__ void store_stream(float* p, v4f v) {
+  if constexpr (NT) __builtin_nontemporal_store(v, reinterpret_cast<v4f*>(p));
+  else *reinterpret_cast<v4f*>(p) = v;
+}
+
 // ---------------------------------------------------------------- DPP moves
 // dpp_ctrl encodings (gfx9 family): quad_perm = 8-bit lane selector,
 // row_shl/shr/ror = 0x100 + n, row_mirror = 0x140, row_half_mirror = 0x141.
@@ -170,7 +195,7 @@ struct TileRegs {
   // offset, and a wave-uniform base that advances per instruction.
   static constexpr int SEQ_STEP = 4 * kWave / T_::PER;
   static_assert(T_::PER % 4 == 0 && (4 * kWave) % T_::PER == 0, "tile rows must divide a wave instruction");
-  float4 r[NV];
+  v4f r[NV];
 
   // Rows of one tile are `row` floats apart in global memory (row = T * W).
   __device__ __forceinline__ void load(const float* __restrict__ g, int64_t n0, int64_t n, int64_t t, int64_t t0,
@@ -183,9 +208,9 @@ struct TileRegs {
 #pragma unroll
     for (int it = 0; it < NV; ++it) {
       const int s = s0 + it * SEQ_STEP;
-      float4 val = make_float4(0.f, 0.f, 0.f, 0.f);
+      v4f val = {0.f, 0.f, 0.f, 0.f};
       if (s < SPW && col_ok && n0 + s < n)
-        val = *reinterpret_cast<const float4*>(base + static_cast<int64_t>(it * SEQ_STEP) * row + off);
+        val = load_stream<(T_::PER * 4 >= BSSM_NT_LOAD_MIN)>(base + static_cast<int64_t>(it * SEQ_STEP) * row + off);
       r[it] = val;
     }
   }
@@ -196,7 +221,7 @@ struct TileRegs {
 #pragma unroll
     for (int it = 0; it < NV; ++it) {
       if (s0 + it * SEQ_STEP < SPW)
-        *reinterpret_cast<float4*>(dst + it * SEQ_STEP * T_::STRIDE) = r[it];
+        *reinterpret_cast<v4f*>(dst + it * SEQ_STEP * T_::STRIDE) = r[it];
     }
   }
 };
@@ -249,8 +274,8 @@ __device__ __forceinline__ void stage_out(const float* __restrict__ lds, float* 
     for (int it = 0; it < R::NV; ++it) {
       const int s = s0 + it * R::SEQ_STEP;
       if (s < SPW && o0 < valid && n0 + s < n)
-        *reinterpret_cast<float4*>(base + static_cast<int64_t>(it * R::SEQ_STEP) * row + off) =
-            *reinterpret_cast<const float4*>(src + it * R::SEQ_STEP * T_::STRIDE);
+        store_stream<(T_::PER * 4 >= BSSM_NT_STORE_MIN)>(base + static_cast<int64_t>(it * R::SEQ_STEP) * row + off,
+                                                          *reinterpret_cast<const v4f*>(src + it * R::SEQ_STEP * T_::STRIDE));
     }
   } else {
 #pragma unroll 1

@@ -112,27 +112,38 @@ __global__ __launch_bounds__(kWave) void forward_kernel(FwdArgs a) {
     }
     __syncthreads();
     if (vec && t0 + TT < T) issue(t0 + TT);
+    // Software pipeline: the LDS reads of token tt+1 are issued before the
+    // update of token tt, so their latency hides behind the arithmetic.
+    TokenIn<D, M, G> cur;
+    float qc[D];
+    read_token<D, M, G, FIXED>(cur, st, 0, g, true);
+#pragma unroll
+    for (int j = 0; j < D; ++j) qc[j] = qs[j];
     for (int tt = 0; tt < len; ++tt) {
+      const int nx = (tt + 1 < len) ? tt + 1 : tt;
+      TokenIn<D, M, G> nxt;
+      float qn[D];
+      read_token<D, M, G, FIXED>(nxt, st, nx, g, true);
+#pragma unroll
+      for (int j = 0; j < D; ++j) qn[j] = qs[nx * D + j];
       if (t0 + tt == next_ckpt) {
         if (active)
           store_belief<D, M, G>(b, a.bm + na * bm_seq + ckpt * D * M, a.bc + na * bc_seq + ckpt * D * D, g);
         ++ckpt;
         next_ckpt += a.chunk;
       }
-      TokenIn<D, M, G> in;
-      read_token<D, M, G, FIXED>(in, st, tt, g, true);
       StepOut<D, M, G> o;
-      forward_step<D, M, G>(b, in, eye, a.floor, lane, o);
-      float q[D];
-#pragma unroll
-      for (int j = 0; j < D; ++j) q[j] = qs[tt * D + j];
+      forward_step<D, M, G>(b, cur, eye, a.floor, lane, o);
 #pragma unroll
       for (int c = 0; c < L::CPL; ++c) {
         float y = 0.f;
 #pragma unroll
-        for (int i = 0; i < D; ++i) y = fmaf(b.Mv[i][c], q[i], y);
+        for (int i = 0; i < D; ++i) y = fmaf(b.Mv[i][c], qc[i], y);
         ys[tt * M + g * L::CPL + c] = y;
       }
+      cur = nxt;
+#pragma unroll
+      for (int j = 0; j < D; ++j) qc[j] = qn[j];
     }
     __syncthreads();
     stage_out<M, TT, SPW>(sv, a.y, n0, a.n, T, t0, len, vec, lane);
