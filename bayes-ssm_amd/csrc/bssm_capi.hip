@@ -11,6 +11,7 @@
 
 #include <cstdarg>
 #include <cstdio>
+#include <initializer_list>
 
 #include "../../include/bssm.h"
 #include "bssm_recurrence.h"
@@ -35,6 +36,18 @@ int ok() {
 bool supported(int d, int m) { return m == 8 && (d == 1 || d == 2 || d == 4 || d == 8); }
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+bool aligned8(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 7u) == 0; }
+
+// The D = 4 rotated-layout kernels address each 16-sequence block through
+// 32-bit buffer offsets, move every stream in 16-byte chunks and store the
+// belief in 8-byte pieces.
+bool rot4_ok(int d, int m, int64_t t, int64_t nb, bool streams16, std::initializer_list<const void*> belief) {
+  if (d != 4 || m != 8 || t <= 0 || t % 4 != 0 || !streams16) return false;
+  if ((nb + 1) * 128 * 16 >= ((int64_t)1 << 31)) return false;
+  for (const void* p : belief)
+    if (p != nullptr && !aligned8(p)) return false;
+  return true;
+}
 
 // 16-byte staging is valid when every sequence row of the stream starts on a
 // 16-byte boundary: base aligned and (T * width) a multiple of 4 floats.
@@ -97,6 +110,7 @@ int forward_impl(const char* fn, bool fixed, int d, int m, const float* keys, co
   a.vec_kqd = vec_flag(keys, t, d) && vec_flag(queries, t, d) && (fixed || vec_flag(decay, t, d));
   a.vec_v = vec_flag(values, t, m) && vec_flag(out, t, m);
   a.vec_pr = fixed || (vec_flag(process, t, 1) && vec_flag(observation, t, 1));
+  a.rot4 = rot4_ok(d, m, t, a.nb, a.vec_kqd && a.vec_v && a.vec_pr, {mean0, cov0, mean_final, cov_final, bmean, bcov});
   if (n == 0) return ok();
   return launched(fn, bssm::launch_forward(d, fixed, a, static_cast<hipStream_t>(stream)));
 }
@@ -135,6 +149,8 @@ int backward_impl(const char* fn, bool fixed, bool dyn, int d, int m, const floa
   a.vec_v = vec_flag(values, t, m) && vec_flag(gy, t, m) && vec_flag(o.gv, t, m);
   a.vec_pr = (fixed || (vec_flag(process, t, 1) && vec_flag(observation, t, 1))) && vec_flag(o.gp, t, 1) &&
              vec_flag(o.gr, t, 1);
+  a.rot4 = chunk == bssm::kRot4Chunk &&
+           rot4_ok(d, m, t, a.nb, a.vec_kqd && a.vec_v && a.vec_pr, {bmean, bcov, gmf, gcf, o.gm0, o.gc0});
   if (n == 0) return ok();
   return launched(fn, bssm::launch_backward(d, fixed, dyn, a, static_cast<hipStream_t>(stream)));
 }

@@ -45,9 +45,13 @@ __device__ __forceinline__ void store_stream(float* p, v4f v) {
 // ---------------------------------------------------------------- DPP moves
 // dpp_ctrl encodings (gfx9 family): quad_perm = 8-bit lane selector,
 // row_shl/shr/ror = 0x100 + n, row_mirror = 0x140, row_half_mirror = 0x141.
+// Every pattern used here (quad permutes, half-row mirror) reads a valid
+// lane for every lane, so bound_ctrl never takes effect; setting it (with a
+// zero `old`) lets the compiler fold the move into the consuming VALU op
+// (v_add_f32_dpp and the like).
 template <int CTRL>
 __device__ __forceinline__ float dpp(float x) {
-  return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), CTRL, 0xF, 0xF, false));
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, 0xF, 0xF, true));
 }
 
 constexpr int quad_perm(int a, int b, int c, int d) { return a | (b << 2) | (c << 4) | (d << 6); }
@@ -273,9 +277,17 @@ __device__ __forceinline__ void stage_out(const float* __restrict__ lds, float* 
 #pragma unroll
     for (int it = 0; it < R::NV; ++it) {
       const int s = s0 + it * R::SEQ_STEP;
-      if (s < SPW && o0 < valid && n0 + s < n)
-        store_stream<(T_::PER * 4 >= BSSM_NT_STORE_MIN)>(base + static_cast<int64_t>(it * R::SEQ_STEP) * row + off,
-                                                          *reinterpret_cast<const v4f*>(src + it * R::SEQ_STEP * T_::STRIDE));
+      if (s < SPW && o0 < valid && n0 + s < n) {
+        float* dst = base + static_cast<int64_t>(it * R::SEQ_STEP) * row + off;
+        const float* lsrc = src + it * R::SEQ_STEP * T_::STRIDE;
+        if (o0 + 4 <= valid) {
+          store_stream<(T_::PER * 4 >= BSSM_NT_STORE_MIN)>(dst, *reinterpret_cast<const v4f*>(lsrc));
+        } else {
+          // The group straddles the end of the tile: the floats past `valid`
+          // belong to the next tile's tokens and must not be overwritten.
+          for (int e = 0; e < valid - o0; ++e) dst[e] = lsrc[e];
+        }
+      }
     }
   } else {
 #pragma unroll 1

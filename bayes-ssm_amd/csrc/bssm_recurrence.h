@@ -26,6 +26,7 @@ struct FwdArgs {
   int64_t nb;
   float floor;
   int vec_kqd, vec_v, vec_pr;  // 16-byte staging allowed per stream class
+  int rot4;                    // D = 4 rotated-layout kernels allowed (see bssm_rot4.hip)
 };
 
 struct BwdArgs {
@@ -56,6 +57,7 @@ struct BwdArgs {
   int64_t nb;
   float floor;
   int vec_kqd, vec_v, vec_pr;
+  int rot4;  // D = 4 rotated-layout kernels allowed (see bssm_rot4.hip)
 };
 
 // Replay-history tensors of the saved-history ABI.
@@ -72,6 +74,14 @@ hipError_t launch_backward(int key_dim, bool fixed, bool dynamics_grads, const B
 hipError_t launch_forward_saved(int key_dim, const FwdArgs& a, const HistArgs& h, hipStream_t stream);
 hipError_t launch_backward_saved(int key_dim, bool dynamics_grads, const BwdArgs& a, const HistArgs& h,
                                  hipStream_t stream);
+// D = 4, M = 8 kernels with the rotated per-lane layout (bssm_rot4.hip).
+// Preconditions (checked by the C ABI, recorded in rot4): 16-byte aligned
+// streams, T a positive multiple of 4, 8-byte aligned belief tensors, and for
+// the backward a checkpoint chunk of exactly kRot4Chunk tokens.
+constexpr int kRot4Chunk = 8;
+hipError_t launch_forward_r4(bool fixed, const FwdArgs& a, hipStream_t stream);
+hipError_t launch_backward_r4(bool fixed, bool dyn, const BwdArgs& a, hipStream_t stream);
+
 hipError_t launch_associative_scan(const float* k, const float* v, const float* q, const float* r,
                                    const float* m0, const float* c0, float* y, float* mT, float* cT,
                                    int64_t b, int64_t t, int d, int m, hipStream_t stream);

@@ -487,6 +487,7 @@ int preferred_checkpoint(int key_dim) {
 }
 
 hipError_t launch_forward(int key_dim, bool fixed, const FwdArgs& a, hipStream_t stream) {
+  if (key_dim == 4 && a.rot4) return launch_forward_r4(fixed, a, stream);
   switch (key_dim) {
     case 1: return fixed ? launch_forward_d<1, true>(a, stream) : launch_forward_d<1, false>(a, stream);
     case 2: return fixed ? launch_forward_d<2, true>(a, stream) : launch_forward_d<2, false>(a, stream);
@@ -503,6 +504,7 @@ hipError_t launch_backward_dd(bool fixed, bool dyn, const BwdArgs& a, hipStream_
 }
 
 hipError_t launch_backward(int key_dim, bool fixed, bool dyn, const BwdArgs& a, hipStream_t stream) {
+  if (key_dim == 4 && a.rot4) return launch_backward_r4(fixed, dyn, a, stream);
   switch (key_dim) {
     case 1: return launch_backward_dd<1>(fixed, dyn, a, stream);
     case 2: return launch_backward_dd<2>(fixed, dyn, a, stream);

@@ -1,0 +1,846 @@
+// gfx950 kernels for the model shape of the Bayes layer: D = 4 key dims,
+// M = 8 value columns (bayes_ssm/persistent_bayes_chunked_d4m8.cu is the
+// reference extension for this shape; bayes_ssm/bayesian_layer.py:207-251
+// is the equation reference).
+//
+// Work decomposition: one wave64 per workgroup, 16 sequences per wave, a
+// quad of 4 lanes per sequence.  Lane g of a quad owns covariance row g and
+// value columns 2g, 2g+1 of the mean.  Everything a lane holds per row is
+// stored *rotated*: slot m holds row (g + m) % 4, so
+//   P[m]     = P[g][(g+m)%4]          Mv[m][c] = M[(g+m)%4][2g+c]
+// and token vectors are read rotated from LDS (kr[m] = k[(g+m)%4]).  With
+// that layout every cross-lane step is a single quad DPP rotation:
+//   gather  (row values from their owners):  x_rot[m] = rot_m(x_g)
+//   reduce-scatter (per-row partial sums):   x_g = x[0] + rot_3(x[1]) + rot_2(x[2]) + rot_1(x[3])
+//   all-reduce (per-sequence scalars):       two xor DPP adds (bitwise identical in the quad)
+// and the covariance stays bitwise symmetric, because entry (g, h) and its
+// mirror (h, g) are computed by two lanes from commutative products only.
+//
+// Memory: all streamed tensors move through LDS tiles written by LDS-DMA
+// (buffer_load ... lds), addressed by per-workgroup buffer descriptors whose
+// range ends at the last valid sequence, so rows past N read as zero and
+// their stores are dropped without branches.  Tiles are token-major inside
+// LDS (16-byte chunk (token, sequence) at chunk index token * 16 + sequence),
+// which makes the per-token reads of 16 sequences bank-conflict free.  A
+// workgroup is a single wave, so LDS needs no barriers; the compiler tracks
+// the LDS-DMA of each tile slot (separate __shared__ objects) and waits only
+// for the slot it reads next.
+//
+// Forward: ring of 3 tiles of 8 tokens (two in flight).  Backward: the
+// belief is checkpointed every 8 tokens; each chunk is replayed on chip
+// (history in registers) and reversed, with the next chunk's inputs and
+// checkpoint loading meanwhile (ring of 2).  Checkpoints move as whole
+// 16-byte pieces of each belief record (staged through LDS).
+
+#include <type_traits>
+
+#include "bssm_step.h"
+
+namespace bssm {
+namespace r4 {
+
+constexpr int SPW = 16;   // sequences per wave
+constexpr int TT = 8;     // forward tile, tokens
+constexpr int SUB = 8;    // backward checkpoint chunk, tokens
+constexpr int kDword3 = 0x00020000;  // raw fp32 buffer, gfx9 family
+constexpr uint32_t kOob = 0x80000000u;  // offset past every descriptor range: load 0, drop store
+
+typedef float v2f __attribute__((ext_vector_type(2)));
+using Rsrc = __amdgpu_buffer_rsrc_t;
+
+__device__ __forceinline__ Rsrc make_rsrc(const float* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(base), 0, static_cast<int>(bytes), kDword3);
+}
+
+// 64 lanes x 16 bytes from global (voff + soff) into LDS at lds + 16 * lane.
+// Issued as inline assembly on purpose: the compiler's own LDS-DMA tracking
+// records a 16-byte footprint at `lds` and would let reads of the rest of
+// the block run ahead of the data.  These loads are invisible to the
+// compiler; their completion is awaited explicitly with vm_wait().
+// The whole offset goes in the VGPR operand so that the descriptor's range
+// check covers it (the scalar offset is outside the check on gfx9).
+__device__ __forceinline__ void dma16(Rsrc r, const float* lds, uint32_t voff) {
+  const uint32_t base = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(lds));
+  asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
+               :
+               : "s"(base), "v"(voff), "s"(r)
+               : "memory");
+}
+
+// Wait until at most N vector-memory operations are outstanding.  Loads
+// complete in issue order among themselves (stores may overtake them), so
+// N = the number of loads issued after the one awaited is always safe.
+// The builtin keeps the compiler's own wait bookkeeping informed; the empty
+// asm statements stop LDS reads from moving across the wait.
+template <int N>
+__device__ __forceinline__ void vm_wait() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  // gfx9 s_waitcnt: vmcnt in bits 3:0 and 15:14, expcnt 6:4, lgkmcnt 11:8.
+  constexpr int kImm = (N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8);
+  asm volatile("" : : : "memory");
+  __builtin_amdgcn_s_waitcnt(kImm);
+  asm volatile("" : : : "memory");
+}
+
+// The raw buffer builtins move untyped 32-bit words; floats are bit-cast.
+typedef uint32_t v2u __attribute__((ext_vector_type(2)));
+typedef uint32_t v4u __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ void st128(Rsrc r, v4f x, uint32_t voff, uint32_t soff) {
+  __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(v4u, x), r, static_cast<int>(voff),
+                                         static_cast<int>(soff), 0);
+}
+__device__ __forceinline__ void st64(Rsrc r, v2f x, uint32_t voff, uint32_t soff) {
+  __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(v2u, x), r, static_cast<int>(voff),
+                                        static_cast<int>(soff), 0);
+}
+__device__ __forceinline__ void st32(Rsrc r, float x, uint32_t voff, uint32_t soff) {
+  __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, x), r, static_cast<int>(voff),
+                                        static_cast<int>(soff), 0);
+}
+__device__ __forceinline__ v2f ld64(Rsrc r, uint32_t voff, uint32_t soff) {
+  return __builtin_bit_cast(v2f, __builtin_amdgcn_raw_buffer_load_b64(r, static_cast<int>(voff),
+                                                                      static_cast<int>(soff), 0));
+}
+__device__ __forceinline__ float ld32(Rsrc r, uint32_t voff, uint32_t soff) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, static_cast<int>(voff),
+                                                                        static_cast<int>(soff), 0));
+}
+
+// Value held by lane (g + R) % 4 of the caller's quad.
+template <int R>
+__device__ __forceinline__ float rot(float x) {
+  constexpr int a = R & 3, b = (R + 1) & 3, c = (R + 2) & 3, d = (R + 3) & 3;
+  return dpp<quad_perm(a, b, c, d)>(x);
+}
+
+// Sum over the quad; identical bits in all four lanes.
+__device__ __forceinline__ float quad_sum(float x) {
+  x += dpp<kXor1>(x);
+  return x + dpp<kXor2>(x);
+}
+
+// Row-g total of a rotated per-row partial vector (slot m = row (g+m)%4).
+__device__ __forceinline__ float reduce_scatter(const float (&x)[4]) {
+  return ((x[0] + rot<3>(x[1])) + rot<2>(x[2])) + rot<1>(x[3]);
+}
+
+struct Bel {
+  float P[4];      // P[g][(g+m)%4]
+  float Mv[4][2];  // M[(g+m)%4][2g+c]
+};
+
+// Byte offsets of this lane's rotated belief entries inside one belief
+// record of a sequence ([D, M] mean, [D, D] covariance, row-major).
+struct BelOff {
+  uint32_t m[4], c[4];
+  __device__ __forceinline__ BelOff(int s, int g, uint32_t mean_stride, uint32_t cov_stride) {
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const int row = (g + k) & 3;
+      m[k] = static_cast<uint32_t>(s) * mean_stride + row * 32 + g * 8;
+      c[k] = static_cast<uint32_t>(s) * cov_stride + g * 16 + row * 4;
+    }
+  }
+};
+
+__device__ __forceinline__ void load_bel(Bel& b, Rsrc rm, Rsrc rc, const BelOff& o, uint32_t soff_m,
+                                         uint32_t soff_c) {
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    b.P[k] = ld32(rc, o.c[k], soff_c);
+    const v2f x = ld64(rm, o.m[k], soff_m);
+    b.Mv[k][0] = x[0];
+    b.Mv[k][1] = x[1];
+  }
+}
+
+__device__ __forceinline__ void store_bel(const Bel& b, Rsrc rm, Rsrc rc, const BelOff& o, uint32_t soff_m,
+                                          uint32_t soff_c) {
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    st32(rc, b.P[k], o.c[k], soff_c);
+    v2f x;
+    x[0] = b.Mv[k][0];
+    x[1] = b.Mv[k][1];
+    st64(rm, x, o.m[k], soff_m);
+  }
+}
+
+// A block of 16 belief records in LDS, natural layout: means [16][4][8] at
+// float 0, covariances [16][4][4] at float 512.  Used to move checkpoints
+// between registers (rotated) and memory (whole 16-byte pieces of each
+// record, so every store or load covers its record contiguously).
+constexpr int kRecFloats = 768;
+__device__ __forceinline__ void bel_to_lds(const Bel& b, float* rec, int s, int g) {
+#pragma unroll
+  for (int m = 0; m < 4; ++m) {
+    const int row = (g + m) & 3;
+    v2f x;
+    x[0] = b.Mv[m][0];
+    x[1] = b.Mv[m][1];
+    *reinterpret_cast<v2f*>(&rec[s * 32 + row * 8 + 2 * g]) = x;
+    rec[512 + s * 16 + g * 4 + row] = b.P[m];
+  }
+}
+__device__ __forceinline__ void bel_from_lds(Bel& b, const float* rec, int s, int g) {
+#pragma unroll
+  for (int m = 0; m < 4; ++m) {
+    const int row = (g + m) & 3;
+    const v2f x = *reinterpret_cast<const v2f*>(&rec[s * 32 + row * 8 + 2 * g]);
+    b.Mv[m][0] = x[0];
+    b.Mv[m][1] = x[1];
+    b.P[m] = rec[512 + s * 16 + g * 4 + row];
+  }
+}
+// Lane offsets of the 16-byte pieces of a record block: piece 64 j + lane of
+// the means (j = 0, 1) and piece lane of the covariances, for records
+// `mean_stride` / `cov_stride` bytes apart in memory.
+struct RecOff {
+  uint32_t m0, m1, c;
+  __device__ __forceinline__ RecOff(int lane, uint32_t mean_stride, uint32_t cov_stride) {
+    m0 = static_cast<uint32_t>(lane >> 3) * mean_stride + (lane & 7) * 16;
+    m1 = static_cast<uint32_t>((64 + lane) >> 3) * mean_stride + (lane & 7) * 16;
+    c = static_cast<uint32_t>(lane >> 2) * cov_stride + (lane & 3) * 16;
+  }
+};
+
+// Token inputs of one lane (rotated vectors).
+struct Tok {
+  float kr[4], dr[4];
+  float v[2];
+  float p, r;
+};
+
+struct StepOut {
+  float ug;    // u_g = (P' k)_g
+  float s;     // unclamped innovation variance r + k.u
+  float e[2];  // innovations of the own columns
+};
+
+// One token of the recurrence on the rotated belief.  u = P' k is computed
+// as d * (P (d * k)) + p k; s = r + k.u is an all-reduce over the quad.
+__device__ __forceinline__ void forward_step(Bel& b, const Tok& in, float floor, StepOut& o) {
+  float wk[4];
+#pragma unroll
+  for (int m = 0; m < 4; ++m) wk[m] = in.dr[m] * in.kr[m];
+  float z = b.P[0] * wk[0];
+#pragma unroll
+  for (int m = 1; m < 4; ++m) z = fmaf(b.P[m], wk[m], z);
+  const float ug = fmaf(in.dr[0], z, in.p * in.kr[0]);
+  const float s = quad_sum(in.kr[0] * ug) + in.r;
+  const float beta = fast_rcp(fmaxf(s, floor));
+  float ur[4];
+  ur[0] = ug;
+  ur[1] = rot<1>(ug);
+  ur[2] = rot<2>(ug);
+  ur[3] = rot<3>(ug);
+#pragma unroll
+  for (int c = 0; c < 2; ++c) {
+    float e = in.v[c];
+#pragma unroll
+    for (int m = 0; m < 4; ++m) e = fmaf(-b.Mv[m][c], wk[m], e);
+    o.e[c] = e;
+  }
+#pragma unroll
+  for (int m = 0; m < 4; ++m) {
+    const float bu = beta * ur[m];
+#pragma unroll
+    for (int c = 0; c < 2; ++c) b.Mv[m][c] = fmaf(bu, o.e[c], in.dr[m] * b.Mv[m][c]);
+  }
+#pragma unroll
+  for (int m = 0; m < 4; ++m) {
+    float dp = (in.dr[0] * in.dr[m]) * b.P[m];
+    if (m == 0) dp += in.p;
+    b.P[m] = fmaf(-beta, ug * ur[m], dp);
+  }
+  o.ug = ug;
+  o.s = s;
+}
+
+// Replay history of one token (everything the reverse needs that is not a
+// token input): the belief before the token and the step intermediates.
+struct Hist {
+  float Pp[4];
+  float Mp[4][2];
+  float ug, s, e[2];
+};
+
+struct RevTok {
+  float kr[4], dr[4], qr[4];
+  float gy[2];
+  float p;
+};
+
+struct RevOut {
+  float gk, gq, gd, gp, gr;
+  float gv[2];
+};
+
+// Reverse of one token.  Carried adjoints (rotated like the belief):
+// gM = dL/dM (own columns) and S = sym(dL/dP) (own row), updated in place to
+// their values before the token.  With dL/dM_new including q gy^T:
+//   ge = beta gM^T u (= dL/dv),  a = gM e,  w = S u,  z = u.(a - w)
+//   gs = (s > floor) ? -z beta^2 : 0 (= dL/dr)
+//   gu = beta (a - 2 w) + gs k
+//   dL/dk = -d*(M_prev ge) + gs u + P' gu,   dL/dq = d*(M_prev gy) + beta u (e.gy)
+//   H = S + sym(gu k^T),  dL/dd_i = 2 sum_j H_ij d_j P_ij + sum_c (gM - k ge^T)_ic M_prev_ic
+//   dL/dp = trace(H),  S_prev = H * d d^T,  gM_prev = (gM - k ge^T) * d
+// gc0 receives (S + gu k^T) * d d^T (the full asymmetric adjoint of the
+// covariance entering the token, persistent_bayes_chunked_d4m8.cu:320-326);
+// the caller keeps the value of the sequence's first token.
+template <bool DYN>
+__device__ __forceinline__ void reverse_step(const RevTok& in, const Hist& h, float (&gM)[4][2], float (&S)[4],
+                                             float floor, float (&gc0)[4], RevOut& o) {
+  const float beta = fast_rcp(fmaxf(h.s, floor));
+  float ur[4];
+  ur[0] = h.ug;
+  ur[1] = rot<1>(h.ug);
+  ur[2] = rot<2>(h.ug);
+  ur[3] = rot<3>(h.ug);
+#pragma unroll
+  for (int m = 0; m < 4; ++m)
+#pragma unroll
+    for (int c = 0; c < 2; ++c) gM[m][c] = fmaf(in.qr[m], in.gy[c], gM[m][c]);
+  float ge[2];
+#pragma unroll
+  for (int c = 0; c < 2; ++c) {
+    float z = gM[0][c] * ur[0];
+#pragma unroll
+    for (int m = 1; m < 4; ++m) z = fmaf(gM[m][c], ur[m], z);
+    ge[c] = beta * z;
+    o.gv[c] = ge[c];
+  }
+  float av[4], Av[4], Cv[4], Bv[4];
+#pragma unroll
+  for (int m = 0; m < 4; ++m) {
+    av[m] = fmaf(gM[m][1], h.e[1], gM[m][0] * h.e[0]);
+    Av[m] = fmaf(h.Mp[m][1], ge[1], h.Mp[m][0] * ge[0]);
+    Cv[m] = fmaf(h.Mp[m][1], in.gy[1], h.Mp[m][0] * in.gy[0]);
+    float gb[2];
+#pragma unroll
+    for (int c = 0; c < 2; ++c) {
+      gb[c] = fmaf(-in.kr[m], ge[c], gM[m][c]);
+      gM[m][c] = gb[c] * in.dr[m];
+    }
+    Bv[m] = DYN ? fmaf(gb[1], h.Mp[m][1], gb[0] * h.Mp[m][0]) : 0.f;
+  }
+  const float eg = quad_sum(fmaf(h.e[1], in.gy[1], h.e[0] * in.gy[0]));
+  const float a_g = reduce_scatter(av);
+  const float A_g = reduce_scatter(Av);
+  const float C_g = reduce_scatter(Cv);
+  o.gq = fmaf(in.dr[0], C_g, (beta * h.ug) * eg);
+
+  float w = S[0] * ur[0];
+#pragma unroll
+  for (int m = 1; m < 4; ++m) w = fmaf(S[m], ur[m], w);
+  const float z = quad_sum(h.ug * (a_g - w));
+  const float gs = (h.s > floor) ? -z * beta * beta : 0.f;
+  const float gu = fmaf(beta, fmaf(-2.f, w, a_g), gs * in.kr[0]);
+  float gur[4];
+  gur[0] = gu;
+  gur[1] = rot<1>(gu);
+  gur[2] = rot<2>(gu);
+  gur[3] = rot<3>(gu);
+  float dd[4], gk = fmaf(-in.dr[0], A_g, gs * h.ug);
+#pragma unroll
+  for (int m = 0; m < 4; ++m) {
+    dd[m] = in.dr[0] * in.dr[m];
+    float pb = dd[m] * h.Pp[m];
+    if (m == 0) pb += in.p;
+    gk = fmaf(pb, gur[m], gk);
+  }
+  o.gk = gk;
+  const float hg = 0.5f * gu, hk = 0.5f * in.kr[0];
+  float gd = 0.f;
+#pragma unroll
+  for (int m = 0; m < 4; ++m) {
+    const float hs = fmaf(hg, in.kr[m], fmaf(gur[m], hk, S[m]));
+    if (DYN) gd = fmaf(hs * in.dr[m], h.Pp[m], gd);
+    if (m == 0) o.gp = DYN ? quad_sum(hs) : 0.f;
+    gc0[m] = fmaf(gu, in.kr[m], S[m]) * dd[m];
+    S[m] = hs * dd[m];
+  }
+  o.gd = DYN ? fmaf(2.f, gd, reduce_scatter(Bv)) : 0.f;
+  o.gr = DYN ? gs : 0.f;
+}
+
+// ------------------------------------------------------------------ forward
+// One forward tile slot (floats): k, d, q [8 tokens x 16 sequences x 4],
+// v [8 x 16 x 8] (values in, readouts out, in place), p and r [16 x 8 used;
+// the rest catches the idle half of their DMA].  Each slot is one __shared__
+// object so the compiler can wait for the LDS-DMA of one slot at a time.
+struct FwdTile {
+  static constexpr int K = 0, D = 512, Q = 1024, V = 1536, P = 2560, R = 2816, SIZE = 3072;
+};
+
+template <bool FIXED>
+__global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(1, 1))) void forward_kernel(FwdArgs a) {
+  __shared__ float ta[FwdTile::SIZE], tb[FwdTile::SIZE], tc[FwdTile::SIZE];
+  __shared__ float ckst[kRecFloats];  // checkpoint staging
+  const int lane = threadIdx.x;
+  const int g = lane & 3, s = lane >> 2;
+  const int64_t n0 = static_cast<int64_t>(blockIdx.x) * SPW;
+  const int64_t T = a.t;
+  const uint32_t valid = static_cast<uint32_t>((a.n - n0) < SPW ? (a.n - n0) : SPW);
+  const uint32_t row4 = static_cast<uint32_t>(T) * 16u, row8 = static_cast<uint32_t>(T) * 32u,
+                 row1 = static_cast<uint32_t>(T) * 4u;
+  const Rsrc rk = make_rsrc(a.k + n0 * T * 4, valid * row4);
+  const Rsrc rq = make_rsrc(a.q + n0 * T * 4, valid * row4);
+  const Rsrc rv = make_rsrc(a.v + n0 * T * 8, valid * row8);
+  const Rsrc ry = make_rsrc(a.y + n0 * T * 8, valid * row8);
+  const Rsrc rd = make_rsrc(FIXED ? a.k : a.d + n0 * T * 4, valid * row4);
+  const Rsrc rp = make_rsrc(FIXED ? a.k : a.p + n0 * T, valid * row1);
+  const Rsrc rr = make_rsrc(FIXED ? a.k : a.r + n0 * T, valid * row1);
+  const uint32_t nbp = static_cast<uint32_t>(a.nb + 1);
+  const Rsrc rbm = make_rsrc(a.bm + n0 * nbp * 32, valid * nbp * 128u);
+  const Rsrc rbc = make_rsrc(a.bc + n0 * nbp * 16, valid * nbp * 64u);
+  const Rsrc rm0 = make_rsrc(a.m0 + n0 * 32, valid * 128u);
+  const Rsrc rc0 = make_rsrc(a.c0 + n0 * 16, valid * 64u);
+  const Rsrc rmT = make_rsrc(a.mT + n0 * 32, valid * 128u);
+  const Rsrc rcT = make_rsrc(a.cT + n0 * 16, valid * 64u);
+
+  // DMA lane offsets: chunk column lane >> 4 of sequence row lane & 15.
+  const uint32_t dk = (lane & 15) * row4 + (lane >> 4) * 16;
+  const uint32_t dv = (lane & 15) * row8 + (lane >> 4) * 16;
+  const uint32_t dp = lane < 32 ? (lane & 15) * row1 + (lane >> 4) * 16 : kOob;
+  // LDS read offsets (floats) of this lane inside a tile.
+  int ok4[4];
+#pragma unroll
+  for (int m = 0; m < 4; ++m) ok4[m] = s * 4 + ((g + m) & 3);
+  const int ov = (g >> 1) * 64 + s * 4 + (g & 1) * 2;
+  const int o1 = s * 4;
+
+  const BelOff unit(s, g, 128u, 64u);
+  const RecOff ckoff(lane, nbp * 128u, nbp * 64u);
+  Bel b;
+  load_bel(b, rm0, rc0, unit, 0, 0);
+  // Checkpoint c of the 16 sequences: through LDS, then whole 16-byte pieces.
+  auto store_ckpt = [&](uint32_t c) __attribute__((always_inline)) {
+    bel_to_lds(b, ckst, s, g);
+    const v4f x0 = *reinterpret_cast<const v4f*>(&ckst[lane * 4]);
+    const v4f x1 = *reinterpret_cast<const v4f*>(&ckst[256 + lane * 4]);
+    const v4f x2 = *reinterpret_cast<const v4f*>(&ckst[512 + lane * 4]);
+    st128(rbm, x0, ckoff.m0, c * 128u);
+    st128(rbm, x1, ckoff.m1, c * 128u);
+    st128(rbc, x2, ckoff.c, c * 64u);
+  };
+  store_ckpt(0);
+
+  auto issue = [&](float* tl, int64_t t0) __attribute__((always_inline)) {
+    const uint32_t s4 = static_cast<uint32_t>(t0) * 16u, s8 = static_cast<uint32_t>(t0) * 32u,
+                   s1 = static_cast<uint32_t>(t0) * 4u;
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      dma16(rk, (tl + FwdTile::K) + 256 * j, dk + s4 + 64 * j);
+      dma16(rq, (tl + FwdTile::Q) + 256 * j, dk + s4 + 64 * j);
+      if constexpr (!FIXED) dma16(rd, (tl + FwdTile::D) + 256 * j, dk + s4 + 64 * j);
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) dma16(rv, (tl + FwdTile::V) + 256 * j, dv + s8 + 64 * j);
+    if constexpr (!FIXED) {
+      dma16(rp, (tl + FwdTile::P), dp + s1);
+      dma16(rr, (tl + FwdTile::R), dp + s1);
+    }
+  };
+
+  int64_t next_ckpt = a.chunk;
+  uint32_t ckpt = 1;
+
+  // Token inputs of one lane, read from LDS ahead of their use.
+  struct FwdIn {
+    Tok t;
+    float qr[4];
+  };
+  auto read_in = [&](const float* tl, int tt, FwdIn& x) __attribute__((always_inline)) {
+#pragma unroll
+    for (int m = 0; m < 4; ++m) {
+      x.t.kr[m] = (tl + FwdTile::K)[tt * 64 + ok4[m]];
+      x.t.dr[m] = FIXED ? kFixedDecay : (tl + FwdTile::D)[tt * 64 + ok4[m]];
+      x.qr[m] = (tl + FwdTile::Q)[tt * 64 + ok4[m]];
+    }
+    const v2f vv = *reinterpret_cast<const v2f*>(&(tl + FwdTile::V)[tt * 128 + ov]);
+    x.t.v[0] = vv[0];
+    x.t.v[1] = vv[1];
+    x.t.p = FIXED ? kFixedProcess : (tl + FwdTile::P)[(tt >> 2) * 64 + o1 + (tt & 3)];
+    x.t.r = FIXED ? kFixedObservation : (tl + FwdTile::R)[(tt >> 2) * 64 + o1 + (tt & 3)];
+  };
+  auto step = [&](const FwdIn& x, v2f& y) __attribute__((always_inline)) {
+    StepOut o;
+    forward_step(b, x.t, a.floor, o);
+#pragma unroll
+    for (int c = 0; c < 2; ++c) {
+      float acc = b.Mv[0][c] * x.qr[0];
+#pragma unroll
+      for (int m = 1; m < 4; ++m) acc = fmaf(b.Mv[m][c], x.qr[m], acc);
+      y[c] = acc;
+    }
+  };
+  auto put_y = [&](float* tl, int tt, v2f y) __attribute__((always_inline)) {
+    *reinterpret_cast<v2f*>(&(tl + FwdTile::V)[tt * 128 + ov]) = y;
+  };
+  // A full tile: the LDS reads of tokens 2j+2 and 2j+3 are issued before
+  // tokens 2j and 2j+1 are computed (the scheduling barrier keeps them
+  // there), and the readouts stay in registers until the last token, so no
+  // LDS write sits between reads.
+  auto full_tile = [&](float* tl) __attribute__((always_inline)) {
+    FwdIn x[TT];
+    v2f y[TT];
+    read_in(tl, 0, x[0]);
+    read_in(tl, 1, x[1]);
+#pragma unroll
+    for (int j = 0; j < TT / 2; ++j) {
+      if (j + 1 < TT / 2) {
+        read_in(tl, 2 * j + 2, x[2 * j + 2]);
+        read_in(tl, 2 * j + 3, x[2 * j + 3]);
+      }
+      step(x[2 * j], y[2 * j]);
+      step(x[2 * j + 1], y[2 * j + 1]);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+#pragma unroll
+    for (int tt = 0; tt < TT; ++tt) put_y(tl, tt, y[tt]);
+  };
+
+  const int64_t ntiles = (T + TT - 1) / TT;
+  constexpr int kTileLoads = FIXED ? 8 : 12;  // DMA instructions per tile (see issue)
+  auto tile_len = [&](int64_t i) __attribute__((always_inline)) {
+    return static_cast<int>((T - i * TT) < TT ? (T - i * TT) : TT);
+  };
+  // Readouts of tile i (slot `tl`): chunk 64 j + lane holds token (4 j + lane / 16) / 2.
+  auto store_y = [&](const float* tl, int64_t i) __attribute__((always_inline)) {
+    const int len = tile_len(i);
+    const uint32_t s8 = static_cast<uint32_t>(i * TT) * 32u;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int tok = (4 * j + (lane >> 4)) >> 1;
+      const v4f x = *reinterpret_cast<const v4f*>(&(tl + FwdTile::V)[(64 * j + lane) * 4]);
+      st128(ry, x, tok < len ? dv : kOob, s8 + 64 * j);
+    }
+  };
+  // Tile i lives in slot i % 3.  At its start: wait for its DMA (issued two
+  // tiles earlier; only the kTileLoads DMA loads of tile i + 1 may still be
+  // in flight), store the readouts of tile i - 1 from the slot that tile i + 2
+  // then loads into, and compute.
+  auto run_tile = [&](float* cur, float* prev, int64_t i) __attribute__((always_inline)) {
+    if (i + 1 < ntiles) vm_wait<kTileLoads>();
+    else vm_wait<0>();
+    if (i > 0) store_y(prev, i - 1);
+    if (i + 2 < ntiles) issue(prev, (i + 2) * TT);
+    const int64_t t0 = i * TT;
+    const int len = tile_len(i);
+    if (t0 == next_ckpt && t0 > 0) {
+      store_ckpt(ckpt);
+      ++ckpt;
+      next_ckpt += a.chunk;
+    }
+    if (len == TT && next_ckpt >= t0 + TT) {
+      full_tile(cur);
+    } else {
+#pragma unroll 1
+      for (int tt = 0; tt < len; ++tt) {
+        if (t0 + tt == next_ckpt) {
+          store_ckpt(ckpt);
+          ++ckpt;
+          next_ckpt += a.chunk;
+        }
+        FwdIn x;
+        v2f y;
+        read_in(cur, tt, x);
+        step(x, y);
+        put_y(cur, tt, y);
+      }
+    }
+  };
+
+  if (ntiles > 0) issue(ta, 0);
+  if (ntiles > 1) issue(tb, TT);
+  for (int64_t i = 0; i < ntiles; i += 3) {
+    run_tile(ta, tc, i);
+    if (i + 1 < ntiles) run_tile(tb, ta, i + 1);
+    if (i + 2 < ntiles) run_tile(tc, tb, i + 2);
+  }
+  if (ntiles > 0) {
+    const int64_t last = ntiles - 1;
+    store_y(last % 3 == 0 ? ta : (last % 3 == 1 ? tb : tc), last);
+  }
+  store_bel(b, rmT, rcT, unit, 0, 0);
+  const uint32_t nbc = static_cast<uint32_t>(a.nb);
+  store_ckpt(nbc);
+}
+
+// ----------------------------------------------------------------- backward
+// One backward chunk slot (floats): k, d, q [8 x 16 x 4] (inputs, then their
+// gradients in place), v [8 x 16 x 8] (values, then value gradients), gy
+// [8 x 16 x 8], p and r [16 x 8 used] (inputs, then gradients), and the
+// chunk's checkpoint (belief records, natural layout).
+struct BwdTile {
+  static constexpr int K = 0, D = 512, Q = 1024, V = 1536, GY = 2560, P = 3584, R = 3840, CK = 4096,
+                       SIZE = 4096 + kRecFloats;
+};
+
+template <bool FIXED, bool DYN>
+__global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(1, 1))) void backward_kernel(BwdArgs a) {
+  __shared__ float ta[BwdTile::SIZE], tb[BwdTile::SIZE];
+  const int lane = threadIdx.x;
+  const int g = lane & 3, s = lane >> 2;
+  const int64_t n0 = static_cast<int64_t>(blockIdx.x) * SPW;
+  const int64_t T = a.t;
+  const uint32_t valid = static_cast<uint32_t>((a.n - n0) < SPW ? (a.n - n0) : SPW);
+  const uint32_t row4 = static_cast<uint32_t>(T) * 16u, row8 = static_cast<uint32_t>(T) * 32u,
+                 row1 = static_cast<uint32_t>(T) * 4u;
+  const Rsrc rk = make_rsrc(a.k + n0 * T * 4, valid * row4);
+  const Rsrc rq = make_rsrc(a.q + n0 * T * 4, valid * row4);
+  const Rsrc rv = make_rsrc(a.v + n0 * T * 8, valid * row8);
+  const Rsrc rgy = make_rsrc(a.gy + n0 * T * 8, valid * row8);
+  const Rsrc rd = make_rsrc(FIXED ? a.k : a.d + n0 * T * 4, valid * row4);
+  const Rsrc rp = make_rsrc(FIXED ? a.k : a.p + n0 * T, valid * row1);
+  const Rsrc rr = make_rsrc(FIXED ? a.k : a.r + n0 * T, valid * row1);
+  const Rsrc rgk = make_rsrc(a.gk + n0 * T * 4, valid * row4);
+  const Rsrc rgq = make_rsrc(a.gq + n0 * T * 4, valid * row4);
+  const Rsrc rgv = make_rsrc(a.gv + n0 * T * 8, valid * row8);
+  const Rsrc rgd = make_rsrc(a.gd ? a.gd + n0 * T * 4 : a.gk, a.gd ? valid * row4 : 0u);
+  const Rsrc rgp = make_rsrc(a.gp ? a.gp + n0 * T : a.gk, a.gp ? valid * row1 : 0u);
+  const Rsrc rgr = make_rsrc(a.gr ? a.gr + n0 * T : a.gk, a.gr ? valid * row1 : 0u);
+  const uint32_t nbp = static_cast<uint32_t>(a.nb + 1);
+  const Rsrc rbm = make_rsrc(a.bm + n0 * nbp * 32, valid * nbp * 128u);
+  const Rsrc rbc = make_rsrc(a.bc + n0 * nbp * 16, valid * nbp * 64u);
+
+  const uint32_t dk = (lane & 15) * row4 + (lane >> 4) * 16;
+  const uint32_t dv = (lane & 15) * row8 + (lane >> 4) * 16;
+  const uint32_t dp = lane < 32 ? (lane & 15) * row1 + (lane >> 4) * 16 : kOob;
+  int ok4[4];
+#pragma unroll
+  for (int m = 0; m < 4; ++m) ok4[m] = s * 4 + ((g + m) & 3);
+  const int ov = (g >> 1) * 64 + s * 4 + (g & 1) * 2;
+  const int o1 = s * 4;
+  const int ow = s * 4 + g;  // own-row word of a W=4 token chunk
+
+  // Carried adjoints from the final-state gradients (null = zero).
+  const BelOff unit(s, g, 128u, 64u);
+  float gM[4][2], S[4], gc0[4];
+  {
+    const bool has_m = a.gmf != nullptr, has_c = a.gcf != nullptr;
+    const Rsrc rgm = make_rsrc(has_m ? a.gmf + n0 * 32 : a.gk, has_m ? valid * 128u : 0u);
+    const Rsrc rgc = make_rsrc(has_c ? a.gcf + n0 * 16 : a.gk, has_c ? valid * 64u : 0u);
+#pragma unroll
+    for (int m = 0; m < 4; ++m) {
+      const v2f x = ld64(rgm, unit.m[m], 0);
+      gM[m][0] = x[0];
+      gM[m][1] = x[1];
+      // Mirror entry (row (g+m)%4, column g) sits at the transposed offset.
+      const int h = (g + m) & 3;
+      const uint32_t tr = static_cast<uint32_t>(s) * 64u + h * 16 + g * 4;
+      S[m] = 0.5f * (ld32(rgc, unit.c[m], 0) + ld32(rgc, tr, 0));
+      gc0[m] = 0.f;
+    }
+  }
+
+  const RecOff ckoff(lane, nbp * 128u, nbp * 64u);
+  const int64_t nb = a.nb;
+
+  auto issue = [&](float* tl, int64_t c) __attribute__((always_inline)) {
+    const int64_t t0 = c * SUB;
+    const uint32_t s4 = static_cast<uint32_t>(t0) * 16u, s8 = static_cast<uint32_t>(t0) * 32u,
+                   s1 = static_cast<uint32_t>(t0) * 4u;
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      dma16(rk, (tl + BwdTile::K) + 256 * j, dk + s4 + 64 * j);
+      dma16(rq, (tl + BwdTile::Q) + 256 * j, dk + s4 + 64 * j);
+      if constexpr (!FIXED) dma16(rd, (tl + BwdTile::D) + 256 * j, dk + s4 + 64 * j);
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      dma16(rv, (tl + BwdTile::V) + 256 * j, dv + s8 + 64 * j);
+      dma16(rgy, (tl + BwdTile::GY) + 256 * j, dv + s8 + 64 * j);
+    }
+    if constexpr (!FIXED) {
+      dma16(rp, (tl + BwdTile::P), dp + s1);
+      dma16(rr, (tl + BwdTile::R), dp + s1);
+    }
+    const uint32_t cm = static_cast<uint32_t>(c) * 128u, cc = static_cast<uint32_t>(c) * 64u;
+    dma16(rbm, (tl + BwdTile::CK), ckoff.m0 + cm);
+    dma16(rbm, (tl + BwdTile::CK) + 256, ckoff.m1 + cm);
+    dma16(rbc, (tl + BwdTile::CK) + 512, ckoff.c + cc);
+  };
+
+  auto read_tok = [&](const float* tl, int tt, Tok& in) __attribute__((always_inline)) {
+#pragma unroll
+    for (int m = 0; m < 4; ++m) {
+      in.kr[m] = (tl + BwdTile::K)[tt * 64 + ok4[m]];
+      in.dr[m] = FIXED ? kFixedDecay : (tl + BwdTile::D)[tt * 64 + ok4[m]];
+    }
+    const v2f vv = *reinterpret_cast<const v2f*>(&(tl + BwdTile::V)[tt * 128 + ov]);
+    in.v[0] = vv[0];
+    in.v[1] = vv[1];
+    in.p = FIXED ? kFixedProcess : (tl + BwdTile::P)[(tt >> 2) * 64 + o1 + (tt & 3)];
+    in.r = FIXED ? kFixedObservation : (tl + BwdTile::R)[(tt >> 2) * 64 + o1 + (tt & 3)];
+  };
+
+  auto read_rev = [&](const float* tl, int tt, RevTok& in) __attribute__((always_inline)) {
+#pragma unroll
+    for (int m = 0; m < 4; ++m) {
+      in.kr[m] = (tl + BwdTile::K)[tt * 64 + ok4[m]];
+      in.dr[m] = FIXED ? kFixedDecay : (tl + BwdTile::D)[tt * 64 + ok4[m]];
+      in.qr[m] = (tl + BwdTile::Q)[tt * 64 + ok4[m]];
+    }
+    const v2f gyv = *reinterpret_cast<const v2f*>(&(tl + BwdTile::GY)[tt * 128 + ov]);
+    in.gy[0] = gyv[0];
+    in.gy[1] = gyv[1];
+    in.p = FIXED ? kFixedProcess : (tl + BwdTile::P)[(tt >> 2) * 64 + o1 + (tt & 3)];
+  };
+  auto replay = [&](Bel& b, const Tok& in, Hist& h) __attribute__((always_inline)) {
+#pragma unroll
+    for (int m = 0; m < 4; ++m) {
+      h.Pp[m] = b.P[m];
+      h.Mp[m][0] = b.Mv[m][0];
+      h.Mp[m][1] = b.Mv[m][1];
+    }
+    StepOut o;
+    forward_step(b, in, a.floor, o);
+    h.ug = o.ug;
+    h.s = o.s;
+    h.e[0] = o.e[0];
+    h.e[1] = o.e[1];
+  };
+  auto reverse = [&](float* tl, int tt, const RevTok& in, const Hist& h) __attribute__((always_inline)) {
+    RevOut o;
+    reverse_step<DYN>(in, h, gM, S, a.floor, gc0, o);
+    (tl + BwdTile::K)[tt * 64 + ow] = o.gk;
+    (tl + BwdTile::Q)[tt * 64 + ow] = o.gq;
+    (tl + BwdTile::D)[tt * 64 + ow] = o.gd;
+    v2f gv;
+    gv[0] = o.gv[0];
+    gv[1] = o.gv[1];
+    *reinterpret_cast<v2f*>(&(tl + BwdTile::V)[tt * 128 + ov]) = gv;
+    (tl + BwdTile::P)[(tt >> 2) * 64 + o1 + (tt & 3)] = o.gp;
+    (tl + BwdTile::R)[(tt >> 2) * 64 + o1 + (tt & 3)] = o.gr;
+  };
+
+  // Replay the chunk from its checkpoint, then reverse it; gradients
+  // overwrite the chunk's input tiles.  Token pairs are separated by
+  // scheduling barriers, and each pair's LDS reads are issued one pair ahead
+  // (the reads of the first reverse pair during the last replay pair), in
+  // program order before the gradient writes that follow them.
+  auto process = [&](float* tl, Bel& b, auto len_tag) __attribute__((always_inline)) {
+    constexpr int LEN = decltype(len_tag)::value;
+    static_assert(LEN % 2 == 0, "token pairs");
+    Hist h[LEN];
+    Tok x[LEN];
+    RevTok rx[LEN];
+    read_tok(tl, 0, x[0]);
+    read_tok(tl, 1, x[1]);
+#pragma unroll
+    for (int j = 0; j < LEN / 2; ++j) {
+      if (j + 1 < LEN / 2) {
+        read_tok(tl, 2 * j + 2, x[2 * j + 2]);
+        read_tok(tl, 2 * j + 3, x[2 * j + 3]);
+      } else {
+        read_rev(tl, LEN - 1, rx[LEN - 1]);
+        read_rev(tl, LEN - 2, rx[LEN - 2]);
+      }
+      replay(b, x[2 * j], h[2 * j]);
+      replay(b, x[2 * j + 1], h[2 * j + 1]);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+#pragma unroll
+    for (int j = 0; j < LEN / 2; ++j) {
+      const int hi = LEN - 1 - 2 * j, lo = hi - 1;
+      if (j + 1 < LEN / 2) {
+        read_rev(tl, lo - 1, rx[lo - 1]);
+        read_rev(tl, lo - 2, rx[lo - 2]);
+      }
+      reverse(tl, hi, rx[hi], h[hi]);
+      reverse(tl, lo, rx[lo], h[lo]);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  };
+
+  auto store_grads = [&](const float* tl, int64_t c, int len) __attribute__((always_inline)) {
+    const int64_t t0 = c * SUB;
+    const uint32_t s4 = static_cast<uint32_t>(t0) * 16u, s8 = static_cast<uint32_t>(t0) * 32u,
+                   s1 = static_cast<uint32_t>(t0) * 4u;
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int tok = 4 * j + (lane >> 4);
+      const uint32_t off = tok < len ? dk : kOob;
+      const int e = (64 * j + lane) * 4;
+      st128(rgk, *reinterpret_cast<const v4f*>(&(tl + BwdTile::K)[e]), off, s4 + 64 * j);
+      st128(rgq, *reinterpret_cast<const v4f*>(&(tl + BwdTile::Q)[e]), off, s4 + 64 * j);
+      if (a.gd) st128(rgd, *reinterpret_cast<const v4f*>(&(tl + BwdTile::D)[e]), off, s4 + 64 * j);
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int tok = (4 * j + (lane >> 4)) >> 1;
+      st128(rgv, *reinterpret_cast<const v4f*>(&(tl + BwdTile::V)[(64 * j + lane) * 4]), tok < len ? dv : kOob, s8 + 64 * j);
+    }
+    // Per-token scalars: chunk lane of the tile holds tokens 4 (lane / 16) .. + 3.
+    const uint32_t off1 = (lane < 32 && 4 * (lane >> 4) < len) ? dp : kOob;
+    if (a.gp) st128(rgp, *reinterpret_cast<const v4f*>(&(tl + BwdTile::P)[lane * 4]), off1, s1);
+    if (a.gr) st128(rgr, *reinterpret_cast<const v4f*>(&(tl + BwdTile::R)[lane * 4]), off1, s1);
+  };
+
+  auto chunk_len = [&](int64_t c) __attribute__((always_inline)) {
+    return static_cast<int>((T - c * SUB) < SUB ? (T - c * SUB) : SUB);
+  };
+  // Chunk c = nb - 1 - i is processed in slot i % 2.  At its start every
+  // outstanding memory operation was issued a whole chunk earlier, so the
+  // full wait is short: then the gradients of chunk c + 1 leave the other
+  // slot, which receives chunk c - 1 while chunk c is replayed and reversed.
+  auto run_chunk = [&](float* cur, float* other, int64_t c) __attribute__((always_inline)) {
+    vm_wait<0>();
+    Bel b;
+    bel_from_lds(b, cur + BwdTile::CK, s, g);
+    if (c + 1 < nb) store_grads(other, c + 1, chunk_len(c + 1));
+    if (c > 0) issue(other, c - 1);
+    if (chunk_len(c) == SUB) process(cur, b, std::integral_constant<int, SUB>{});
+    else process(cur, b, std::integral_constant<int, 4>{});
+  };
+
+  if (nb > 0) issue(ta, nb - 1);
+  for (int64_t i = 0; i < nb; i += 2) {
+    run_chunk(ta, tb, nb - 1 - i);
+    if (i + 1 < nb) run_chunk(tb, ta, nb - 2 - i);
+  }
+  if (nb > 0) store_grads((nb - 1) % 2 == 0 ? ta : tb, 0, chunk_len(0));
+
+  if (a.gm0) {
+    const Rsrc rgm0 = make_rsrc(a.gm0 + n0 * 32, valid * 128u);
+#pragma unroll
+    for (int m = 0; m < 4; ++m) {
+      v2f x;
+      x[0] = gM[m][0];
+      x[1] = gM[m][1];
+      st64(rgm0, x, unit.m[m], 0);
+    }
+  }
+  if (a.gc0) {
+    const Rsrc rgc0 = make_rsrc(a.gc0 + n0 * 16, valid * 64u);
+#pragma unroll
+    for (int m = 0; m < 4; ++m) st32(rgc0, gc0[m], unit.c[m], 0);
+  }
+}
+
+}  // namespace r4
+
+// Launch helpers used by the dispatch in bssm_recurrence.hip.
+hipError_t launch_forward_r4(bool fixed, const FwdArgs& a, hipStream_t stream) {
+  const int64_t blocks = (a.n + r4::SPW - 1) / r4::SPW;
+  if (blocks == 0) return hipSuccess;
+  if (fixed)
+    hipLaunchKernelGGL(r4::forward_kernel<true>, dim3(static_cast<unsigned>(blocks)), dim3(kWave), 0, stream, a);
+  else
+    hipLaunchKernelGGL(r4::forward_kernel<false>, dim3(static_cast<unsigned>(blocks)), dim3(kWave), 0, stream, a);
+  return hipGetLastError();
+}
+
+hipError_t launch_backward_r4(bool fixed, bool dyn, const BwdArgs& a, hipStream_t stream) {
+  const int64_t blocks = (a.n + r4::SPW - 1) / r4::SPW;
+  if (blocks == 0) return hipSuccess;
+  const dim3 grid(static_cast<unsigned>(blocks)), block(kWave);
+  if (fixed) hipLaunchKernelGGL((r4::backward_kernel<true, false>), grid, block, 0, stream, a);
+  else if (dyn) hipLaunchKernelGGL((r4::backward_kernel<false, true>), grid, block, 0, stream, a);
+  else hipLaunchKernelGGL((r4::backward_kernel<false, false>), grid, block, 0, stream, a);
+  return hipGetLastError();
+}
+
+}  // namespace bssm

@@ -68,12 +68,19 @@ def _fixed_dynamics(c):
     return out
 
 
+# T = 45 takes the generic kernels; T = 52 (a multiple of 4 that is not a
+# multiple of the 8-token tile) takes the D4 rotated-layout kernels with a
+# partial last tile.  N = 37 leaves idle sequence slots in the last wave.
+TIMES = [45, 52]
+
+
 @pytest.mark.parametrize("d", DIMS)
 @pytest.mark.parametrize("fixed", [False, True])
 @pytest.mark.parametrize("chunk", [1, 8, 13, 64])
-def test_forward_matches_oracle(ext_for, cuda_device, d, fixed, chunk):
-    print(f"forward d={d} fixed={fixed} chunk={chunk}", flush=True)
-    n, t = 37, 45
+@pytest.mark.parametrize("t", TIMES)
+def test_forward_matches_oracle(ext_for, cuda_device, d, fixed, chunk, t):
+    print(f"forward d={d} fixed={fixed} chunk={chunk} t={t}", flush=True)
+    n = 37
     cpu, dev = _case(n, t, d, seed=d * 10 + chunk, device=cuda_device)
     ext = ext_for(d)
     fn = ext.forward_chunked_fixed if fixed else ext.forward_chunked
@@ -131,12 +138,11 @@ ABIS = [
 @pytest.mark.parametrize("abi", ABIS, ids=[a[0] for a in ABIS])
 @pytest.mark.parametrize("final_grads", [False, True])
 @pytest.mark.parametrize("chunk", [8, 13])
-def test_backward_matches_oracle(ext_for, cuda_device, d, abi, final_grads, chunk):
+@pytest.mark.parametrize("t", TIMES)
+def test_backward_matches_oracle(ext_for, cuda_device, d, abi, final_grads, chunk, t):
     name, fixed, nout = abi
-    print(f"backward {name} d={d} final_grads={final_grads} chunk={chunk}", flush=True)
-    from bayes_ssm import _hip
-
-    n, t = 37, 45
+    print(f"backward {name} d={d} final_grads={final_grads} chunk={chunk} t={t}", flush=True)
+    n = 37
     cpu, dev = _case(n, t, d, seed=7 * d + chunk, device=cuda_device)
     ref = _fixed_dynamics(cpu) if fixed else cpu
     ext_name = name
@@ -168,12 +174,13 @@ def test_backward_matches_oracle(ext_for, cuda_device, d, abi, final_grads, chun
 
 
 @pytest.mark.parametrize("d", DIMS)
-def test_autograd_boundary(cuda_device, d):
+@pytest.mark.parametrize("t", [70, 64])
+def test_autograd_boundary(cuda_device, d, t):
     """fused_diagonal_bayesian under autograd: values and all input gradients."""
-    print(f"autograd d={d}", flush=True)
+    print(f"autograd d={d} t={t}", flush=True)
     from bayes_ssm.fused_cuda import fused_diagonal_bayesian
 
-    n, t = 20, 70
+    n = 20
     cpu, dev = _case(n, t, d, seed=11 + d, device=cuda_device)
     leaves = {k: dev[k].clone().requires_grad_(True) for k in ("k", "v", "q", "d", "p", "r")}
     y, mT, cT = fused_diagonal_bayesian(leaves["k"], leaves["v"], leaves["q"], leaves["d"], leaves["p"],
