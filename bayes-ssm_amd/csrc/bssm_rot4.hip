@@ -19,9 +19,9 @@
 // Memory: all streamed tensors move through LDS tiles written by LDS-DMA
 // (buffer_load ... lds), addressed by per-workgroup buffer descriptors whose
 // range ends at the last valid sequence, so rows past N read as zero and
-// their stores are dropped without branches.  Tiles are token-major inside
-// LDS (16-byte chunk (token, sequence) at chunk index token * 16 + sequence),
-// which makes the per-token reads of 16 sequences bank-conflict free.  A
+// their stores are dropped without branches.  Tiles move whole cache lines
+// of each sequence row and are laid out in LDS so that the per-token reads
+// of 16 sequences are bank-conflict free (see Map).  A
 // workgroup is a single wave, so LDS needs no barriers; the compiler tracks
 // the LDS-DMA of each tile slot (separate __shared__ objects) and waits only
 // for the slot it reads next.
@@ -365,6 +365,64 @@ __device__ __forceinline__ void reverse_step(const RevTok& in, const Hist& h, fl
 }
 
 // ------------------------------------------------------------------ forward
+// Tile layout.  A tile holds 8 tokens of the 16 sequences of a wave for
+// one stream with W floats per token, moved as 16-byte pieces; lane l of
+// DMA/store instruction j moves LDS piece 64 j + l.  Each instruction covers
+// whole row segments in memory -- 8 rows x 8 pieces (128 B) for W = 4,
+// 4 rows x 16 pieces (256 B) for W = 8, 16 rows x 2 pieces for W = 1 -- so
+// every sequence row is read and written back as whole cache lines.  The
+// order of the pieces inside an instruction's block puts the 16 rows' pieces
+// of one token in distinct LDS banks (two per bank for the 512-byte W = 8
+// reads) and keeps every lane's read address an affine function of the
+// token, so the unrolled token loop addresses LDS with immediate offsets:
+//   W = 4, piece t of row s = 8 j + a (j < 2):   slot 8 (t ^ j) + a
+//   W = 8, piece c of row s = 4 j + a (j < 4):   slot 4 (c ^ 2 j) + a
+//   W = 1, piece c of row s:                     piece 2 s + c
+// Map holds, per instruction, the lane's byte offset inside the stream's
+// 16-row block (relative to token 0 of the tile) and the first token its
+// piece carries (for the tail masks).
+struct Map {
+  uint32_t d4[2], d8[4], d1;
+  int t4[2], t8[4], t1;
+  __device__ __forceinline__ Map(int lane, uint32_t row4, uint32_t row8, uint32_t row1) {
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int t = (lane >> 3) ^ j, sr = 8 * j + (lane & 7);
+      d4[j] = static_cast<uint32_t>(sr) * row4 + t * 16;
+      t4[j] = t;
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int c = (lane >> 2) ^ (2 * j), sr = 4 * j + (lane & 3);
+      d8[j] = static_cast<uint32_t>(sr) * row8 + c * 16;
+      t8[j] = c >> 1;
+    }
+    d1 = lane < 32 ? static_cast<uint32_t>(lane >> 1) * row1 + (lane & 1) * 16 : kOob;
+    t1 = lane < 32 ? 4 * (lane & 1) : 1 << 20;
+  }
+};
+
+// LDS float indices of one lane's reads inside a tile.  For sequence s and
+// token tt (a compile-time constant in the unrolled loops):
+//   W = 4: word w of the token   = w4[tt & 1] + 32 tt + w
+//   W = 8: own columns 2g, 2g+1  = w8[tt & 3] + 128 (tt >> 2)
+//   W = 1: the token             = 8 s + tt
+struct Idx {
+  int w4[2], w8[4], w1;
+  __device__ __forceinline__ Idx(int s, int g) {
+    const int j4 = s >> 3, a4 = s & 7;
+#pragma unroll
+    for (int par = 0; par < 2; ++par) w4[par] = 4 * (64 * j4 + 8 * (par ^ j4) + a4) - 32 * par;
+    const int j8 = s >> 2, a8 = s & 3, h = g >> 1;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) w8[w] = 4 * (64 * j8 + 8 * (w ^ j8) + 4 * h + a8) + 2 * (g & 1);
+    w1 = 8 * s;
+  }
+  __device__ __forceinline__ int i4(int tt, int w) const { return w4[tt & 1] + 32 * tt + w; }
+  __device__ __forceinline__ int i8(int tt) const { return w8[tt & 3] + 128 * (tt >> 2); }
+  __device__ __forceinline__ int i1(int tt) const { return w1 + tt; }
+};
+
 // One forward tile slot (floats): k, d, q [8 tokens x 16 sequences x 4],
 // v [8 x 16 x 8] (values in, readouts out, in place), p and r [16 x 8 used;
 // the rest catches the idle half of their DMA].  Each slot is one __shared__
@@ -399,16 +457,8 @@ __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(1, 1))) v
   const Rsrc rmT = make_rsrc(a.mT + n0 * 32, valid * 128u);
   const Rsrc rcT = make_rsrc(a.cT + n0 * 16, valid * 64u);
 
-  // DMA lane offsets: chunk column lane >> 4 of sequence row lane & 15.
-  const uint32_t dk = (lane & 15) * row4 + (lane >> 4) * 16;
-  const uint32_t dv = (lane & 15) * row8 + (lane >> 4) * 16;
-  const uint32_t dp = lane < 32 ? (lane & 15) * row1 + (lane >> 4) * 16 : kOob;
-  // LDS read offsets (floats) of this lane inside a tile.
-  int ok4[4];
-#pragma unroll
-  for (int m = 0; m < 4; ++m) ok4[m] = s * 4 + ((g + m) & 3);
-  const int ov = (g >> 1) * 64 + s * 4 + (g & 1) * 2;
-  const int o1 = s * 4;
+  const Map mp(lane, row4, row8, row1);
+  const Idx ix(s, g);
 
   const BelOff unit(s, g, 128u, 64u);
   const RecOff ckoff(lane, nbp * 128u, nbp * 64u);
@@ -431,15 +481,15 @@ __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(1, 1))) v
                    s1 = static_cast<uint32_t>(t0) * 4u;
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
-      dma16(rk, (tl + FwdTile::K) + 256 * j, dk + s4 + 64 * j);
-      dma16(rq, (tl + FwdTile::Q) + 256 * j, dk + s4 + 64 * j);
-      if constexpr (!FIXED) dma16(rd, (tl + FwdTile::D) + 256 * j, dk + s4 + 64 * j);
+      dma16(rk, (tl + FwdTile::K) + 256 * j, mp.d4[j] + s4);
+      dma16(rq, (tl + FwdTile::Q) + 256 * j, mp.d4[j] + s4);
+      if constexpr (!FIXED) dma16(rd, (tl + FwdTile::D) + 256 * j, mp.d4[j] + s4);
     }
 #pragma unroll
-    for (int j = 0; j < 4; ++j) dma16(rv, (tl + FwdTile::V) + 256 * j, dv + s8 + 64 * j);
+    for (int j = 0; j < 4; ++j) dma16(rv, (tl + FwdTile::V) + 256 * j, mp.d8[j] + s8);
     if constexpr (!FIXED) {
-      dma16(rp, (tl + FwdTile::P), dp + s1);
-      dma16(rr, (tl + FwdTile::R), dp + s1);
+      dma16(rp, (tl + FwdTile::P), mp.d1 + s1);
+      dma16(rr, (tl + FwdTile::R), mp.d1 + s1);
     }
   };
 
@@ -454,15 +504,16 @@ __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(1, 1))) v
   auto read_in = [&](const float* tl, int tt, FwdIn& x) __attribute__((always_inline)) {
 #pragma unroll
     for (int m = 0; m < 4; ++m) {
-      x.t.kr[m] = (tl + FwdTile::K)[tt * 64 + ok4[m]];
-      x.t.dr[m] = FIXED ? kFixedDecay : (tl + FwdTile::D)[tt * 64 + ok4[m]];
-      x.qr[m] = (tl + FwdTile::Q)[tt * 64 + ok4[m]];
+      const int e = ix.i4(tt, (g + m) & 3);
+      x.t.kr[m] = (tl + FwdTile::K)[e];
+      x.t.dr[m] = FIXED ? kFixedDecay : (tl + FwdTile::D)[e];
+      x.qr[m] = (tl + FwdTile::Q)[e];
     }
-    const v2f vv = *reinterpret_cast<const v2f*>(&(tl + FwdTile::V)[tt * 128 + ov]);
+    const v2f vv = *reinterpret_cast<const v2f*>(&(tl + FwdTile::V)[ix.i8(tt)]);
     x.t.v[0] = vv[0];
     x.t.v[1] = vv[1];
-    x.t.p = FIXED ? kFixedProcess : (tl + FwdTile::P)[(tt >> 2) * 64 + o1 + (tt & 3)];
-    x.t.r = FIXED ? kFixedObservation : (tl + FwdTile::R)[(tt >> 2) * 64 + o1 + (tt & 3)];
+    x.t.p = FIXED ? kFixedProcess : (tl + FwdTile::P)[ix.i1(tt)];
+    x.t.r = FIXED ? kFixedObservation : (tl + FwdTile::R)[ix.i1(tt)];
   };
   auto step = [&](const FwdIn& x, v2f& y) __attribute__((always_inline)) {
     StepOut o;
@@ -476,7 +527,7 @@ __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(1, 1))) v
     }
   };
   auto put_y = [&](float* tl, int tt, v2f y) __attribute__((always_inline)) {
-    *reinterpret_cast<v2f*>(&(tl + FwdTile::V)[tt * 128 + ov]) = y;
+    *reinterpret_cast<v2f*>(&(tl + FwdTile::V)[ix.i8(tt)]) = y;
   };
   // A full tile: the LDS reads of tokens 2j+2 and 2j+3 are issued before
   // tokens 2j and 2j+1 are computed (the scheduling barrier keeps them
@@ -506,15 +557,14 @@ __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(1, 1))) v
   auto tile_len = [&](int64_t i) __attribute__((always_inline)) {
     return static_cast<int>((T - i * TT) < TT ? (T - i * TT) : TT);
   };
-  // Readouts of tile i (slot `tl`): chunk 64 j + lane holds token (4 j + lane / 16) / 2.
+  // Readouts of tile i (slot `tl`), written back piece by piece.
   auto store_y = [&](const float* tl, int64_t i) __attribute__((always_inline)) {
     const int len = tile_len(i);
     const uint32_t s8 = static_cast<uint32_t>(i * TT) * 32u;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      const int tok = (4 * j + (lane >> 4)) >> 1;
       const v4f x = *reinterpret_cast<const v4f*>(&(tl + FwdTile::V)[(64 * j + lane) * 4]);
-      st128(ry, x, tok < len ? dv : kOob, s8 + 64 * j);
+      st128(ry, x, mp.t8[j] < len ? mp.d8[j] : kOob, s8);
     }
   };
   // Tile i lives in slot i % 3.  At its start: wait for its DMA (issued two
@@ -605,15 +655,8 @@ __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(1, 1))) v
   const Rsrc rbm = make_rsrc(a.bm + n0 * nbp * 32, valid * nbp * 128u);
   const Rsrc rbc = make_rsrc(a.bc + n0 * nbp * 16, valid * nbp * 64u);
 
-  const uint32_t dk = (lane & 15) * row4 + (lane >> 4) * 16;
-  const uint32_t dv = (lane & 15) * row8 + (lane >> 4) * 16;
-  const uint32_t dp = lane < 32 ? (lane & 15) * row1 + (lane >> 4) * 16 : kOob;
-  int ok4[4];
-#pragma unroll
-  for (int m = 0; m < 4; ++m) ok4[m] = s * 4 + ((g + m) & 3);
-  const int ov = (g >> 1) * 64 + s * 4 + (g & 1) * 2;
-  const int o1 = s * 4;
-  const int ow = s * 4 + g;  // own-row word of a W=4 token chunk
+  const Map mp(lane, row4, row8, row1);
+  const Idx ix(s, g);
 
   // Carried adjoints from the final-state gradients (null = zero).
   const BelOff unit(s, g, 128u, 64u);
@@ -644,18 +687,18 @@ __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(1, 1))) v
                    s1 = static_cast<uint32_t>(t0) * 4u;
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
-      dma16(rk, (tl + BwdTile::K) + 256 * j, dk + s4 + 64 * j);
-      dma16(rq, (tl + BwdTile::Q) + 256 * j, dk + s4 + 64 * j);
-      if constexpr (!FIXED) dma16(rd, (tl + BwdTile::D) + 256 * j, dk + s4 + 64 * j);
+      dma16(rk, (tl + BwdTile::K) + 256 * j, mp.d4[j] + s4);
+      dma16(rq, (tl + BwdTile::Q) + 256 * j, mp.d4[j] + s4);
+      if constexpr (!FIXED) dma16(rd, (tl + BwdTile::D) + 256 * j, mp.d4[j] + s4);
     }
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      dma16(rv, (tl + BwdTile::V) + 256 * j, dv + s8 + 64 * j);
-      dma16(rgy, (tl + BwdTile::GY) + 256 * j, dv + s8 + 64 * j);
+      dma16(rv, (tl + BwdTile::V) + 256 * j, mp.d8[j] + s8);
+      dma16(rgy, (tl + BwdTile::GY) + 256 * j, mp.d8[j] + s8);
     }
     if constexpr (!FIXED) {
-      dma16(rp, (tl + BwdTile::P), dp + s1);
-      dma16(rr, (tl + BwdTile::R), dp + s1);
+      dma16(rp, (tl + BwdTile::P), mp.d1 + s1);
+      dma16(rr, (tl + BwdTile::R), mp.d1 + s1);
     }
     const uint32_t cm = static_cast<uint32_t>(c) * 128u, cc = static_cast<uint32_t>(c) * 64u;
     dma16(rbm, (tl + BwdTile::CK), ckoff.m0 + cm);
@@ -666,27 +709,29 @@ __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(1, 1))) v
   auto read_tok = [&](const float* tl, int tt, Tok& in) __attribute__((always_inline)) {
 #pragma unroll
     for (int m = 0; m < 4; ++m) {
-      in.kr[m] = (tl + BwdTile::K)[tt * 64 + ok4[m]];
-      in.dr[m] = FIXED ? kFixedDecay : (tl + BwdTile::D)[tt * 64 + ok4[m]];
+      const int e = ix.i4(tt, (g + m) & 3);
+      in.kr[m] = (tl + BwdTile::K)[e];
+      in.dr[m] = FIXED ? kFixedDecay : (tl + BwdTile::D)[e];
     }
-    const v2f vv = *reinterpret_cast<const v2f*>(&(tl + BwdTile::V)[tt * 128 + ov]);
+    const v2f vv = *reinterpret_cast<const v2f*>(&(tl + BwdTile::V)[ix.i8(tt)]);
     in.v[0] = vv[0];
     in.v[1] = vv[1];
-    in.p = FIXED ? kFixedProcess : (tl + BwdTile::P)[(tt >> 2) * 64 + o1 + (tt & 3)];
-    in.r = FIXED ? kFixedObservation : (tl + BwdTile::R)[(tt >> 2) * 64 + o1 + (tt & 3)];
+    in.p = FIXED ? kFixedProcess : (tl + BwdTile::P)[ix.i1(tt)];
+    in.r = FIXED ? kFixedObservation : (tl + BwdTile::R)[ix.i1(tt)];
   };
 
   auto read_rev = [&](const float* tl, int tt, RevTok& in) __attribute__((always_inline)) {
 #pragma unroll
     for (int m = 0; m < 4; ++m) {
-      in.kr[m] = (tl + BwdTile::K)[tt * 64 + ok4[m]];
-      in.dr[m] = FIXED ? kFixedDecay : (tl + BwdTile::D)[tt * 64 + ok4[m]];
-      in.qr[m] = (tl + BwdTile::Q)[tt * 64 + ok4[m]];
+      const int e = ix.i4(tt, (g + m) & 3);
+      in.kr[m] = (tl + BwdTile::K)[e];
+      in.dr[m] = FIXED ? kFixedDecay : (tl + BwdTile::D)[e];
+      in.qr[m] = (tl + BwdTile::Q)[e];
     }
-    const v2f gyv = *reinterpret_cast<const v2f*>(&(tl + BwdTile::GY)[tt * 128 + ov]);
+    const v2f gyv = *reinterpret_cast<const v2f*>(&(tl + BwdTile::GY)[ix.i8(tt)]);
     in.gy[0] = gyv[0];
     in.gy[1] = gyv[1];
-    in.p = FIXED ? kFixedProcess : (tl + BwdTile::P)[(tt >> 2) * 64 + o1 + (tt & 3)];
+    in.p = FIXED ? kFixedProcess : (tl + BwdTile::P)[ix.i1(tt)];
   };
   auto replay = [&](Bel& b, const Tok& in, Hist& h) __attribute__((always_inline)) {
 #pragma unroll
@@ -705,52 +750,40 @@ __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(1, 1))) v
   auto reverse = [&](float* tl, int tt, const RevTok& in, const Hist& h) __attribute__((always_inline)) {
     RevOut o;
     reverse_step<DYN>(in, h, gM, S, a.floor, gc0, o);
-    (tl + BwdTile::K)[tt * 64 + ow] = o.gk;
-    (tl + BwdTile::Q)[tt * 64 + ow] = o.gq;
-    (tl + BwdTile::D)[tt * 64 + ow] = o.gd;
+    const int ow = ix.i4(tt, g);  // own-row word of the token's piece
+    (tl + BwdTile::K)[ow] = o.gk;
+    (tl + BwdTile::Q)[ow] = o.gq;
+    (tl + BwdTile::D)[ow] = o.gd;
     v2f gv;
     gv[0] = o.gv[0];
     gv[1] = o.gv[1];
-    *reinterpret_cast<v2f*>(&(tl + BwdTile::V)[tt * 128 + ov]) = gv;
-    (tl + BwdTile::P)[(tt >> 2) * 64 + o1 + (tt & 3)] = o.gp;
-    (tl + BwdTile::R)[(tt >> 2) * 64 + o1 + (tt & 3)] = o.gr;
+    *reinterpret_cast<v2f*>(&(tl + BwdTile::V)[ix.i8(tt)]) = gv;
+    (tl + BwdTile::P)[ix.i1(tt)] = o.gp;
+    (tl + BwdTile::R)[ix.i1(tt)] = o.gr;
   };
 
   // Replay the chunk from its checkpoint, then reverse it; gradients
-  // overwrite the chunk's input tiles.  Token pairs are separated by
-  // scheduling barriers, and each pair's LDS reads are issued one pair ahead
-  // (the reads of the first reverse pair during the last replay pair), in
+  // overwrite the chunk's input tiles.  Tokens are separated by scheduling
+  // barriers, and each token's LDS reads are issued one token ahead (the
+  // reads of the first reverse token during the last replay token), in
   // program order before the gradient writes that follow them.
   auto process = [&](float* tl, Bel& b, auto len_tag) __attribute__((always_inline)) {
     constexpr int LEN = decltype(len_tag)::value;
-    static_assert(LEN % 2 == 0, "token pairs");
     Hist h[LEN];
     Tok x[LEN];
     RevTok rx[LEN];
     read_tok(tl, 0, x[0]);
-    read_tok(tl, 1, x[1]);
 #pragma unroll
-    for (int j = 0; j < LEN / 2; ++j) {
-      if (j + 1 < LEN / 2) {
-        read_tok(tl, 2 * j + 2, x[2 * j + 2]);
-        read_tok(tl, 2 * j + 3, x[2 * j + 3]);
-      } else {
-        read_rev(tl, LEN - 1, rx[LEN - 1]);
-        read_rev(tl, LEN - 2, rx[LEN - 2]);
-      }
-      replay(b, x[2 * j], h[2 * j]);
-      replay(b, x[2 * j + 1], h[2 * j + 1]);
+    for (int tt = 0; tt < LEN; ++tt) {
+      if (tt + 1 < LEN) read_tok(tl, tt + 1, x[tt + 1]);
+      else read_rev(tl, LEN - 1, rx[LEN - 1]);
+      replay(b, x[tt], h[tt]);
       __builtin_amdgcn_sched_barrier(0);
     }
 #pragma unroll
-    for (int j = 0; j < LEN / 2; ++j) {
-      const int hi = LEN - 1 - 2 * j, lo = hi - 1;
-      if (j + 1 < LEN / 2) {
-        read_rev(tl, lo - 1, rx[lo - 1]);
-        read_rev(tl, lo - 2, rx[lo - 2]);
-      }
-      reverse(tl, hi, rx[hi], h[hi]);
-      reverse(tl, lo, rx[lo], h[lo]);
+    for (int tt = LEN - 1; tt >= 0; --tt) {
+      if (tt > 0) read_rev(tl, tt - 1, rx[tt - 1]);
+      reverse(tl, tt, rx[tt], h[tt]);
       __builtin_amdgcn_sched_barrier(0);
     }
   };
@@ -761,20 +794,17 @@ __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(1, 1))) v
                    s1 = static_cast<uint32_t>(t0) * 4u;
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
-      const int tok = 4 * j + (lane >> 4);
-      const uint32_t off = tok < len ? dk : kOob;
+      const uint32_t off = mp.t4[j] < len ? mp.d4[j] : kOob;
       const int e = (64 * j + lane) * 4;
-      st128(rgk, *reinterpret_cast<const v4f*>(&(tl + BwdTile::K)[e]), off, s4 + 64 * j);
-      st128(rgq, *reinterpret_cast<const v4f*>(&(tl + BwdTile::Q)[e]), off, s4 + 64 * j);
-      if (a.gd) st128(rgd, *reinterpret_cast<const v4f*>(&(tl + BwdTile::D)[e]), off, s4 + 64 * j);
+      st128(rgk, *reinterpret_cast<const v4f*>(&(tl + BwdTile::K)[e]), off, s4);
+      st128(rgq, *reinterpret_cast<const v4f*>(&(tl + BwdTile::Q)[e]), off, s4);
+      if (a.gd) st128(rgd, *reinterpret_cast<const v4f*>(&(tl + BwdTile::D)[e]), off, s4);
     }
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int tok = (4 * j + (lane >> 4)) >> 1;
-      st128(rgv, *reinterpret_cast<const v4f*>(&(tl + BwdTile::V)[(64 * j + lane) * 4]), tok < len ? dv : kOob, s8 + 64 * j);
-    }
-    // Per-token scalars: chunk lane of the tile holds tokens 4 (lane / 16) .. + 3.
-    const uint32_t off1 = (lane < 32 && 4 * (lane >> 4) < len) ? dp : kOob;
+    for (int j = 0; j < 4; ++j)
+      st128(rgv, *reinterpret_cast<const v4f*>(&(tl + BwdTile::V)[(64 * j + lane) * 4]),
+            mp.t8[j] < len ? mp.d8[j] : kOob, s8);
+    const uint32_t off1 = mp.t1 < len ? mp.d1 : kOob;
     if (a.gp) st128(rgp, *reinterpret_cast<const v4f*>(&(tl + BwdTile::P)[lane * 4]), off1, s1);
     if (a.gr) st128(rgr, *reinterpret_cast<const v4f*>(&(tl + BwdTile::R)[lane * 4]), off1, s1);
   };
