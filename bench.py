@@ -120,12 +120,22 @@ def main() -> int:
     b, t, h, d, m = args.batch, args.seq, args.heads, args.key_dim, 8
     n = b * h
     leaves, m0, c0, gy = make_workload(b, t, h, d, m, device)
+    copy_gbs = None
     if args.copy_calibration:
-        # 64 Mi floats read + 64 Mi floats written (256 MiB each way).
+        # A plain 256 MiB device copy (64 Mi floats read + 64 Mi written): the
+        # reference kernel for scaling the PMC byte counters, and the measured
+        # streaming bandwidth of this device next to the 8 TB/s spec peak.
         src = torch.randn(64 << 20, device=device)
         dst = torch.empty_like(src)
         dst.copy_(src)
         torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(10):
+            dst.copy_(src)
+        e1.record()
+        torch.cuda.synchronize()
+        copy_gbs = 2 * src.numel() * 4 / (e0.elapsed_time(e1) / 10 * 1e-3) / 1e9
         del src, dst
 
     def step():
@@ -170,10 +180,14 @@ def main() -> int:
     fwd_gbs = fwd_b * units / (fwd_ms * 1e-3) / 1e9
     step_frac = (fwd_b + bwd_b) * units / (ms_per_step * 1e-3) / HBM_PEAK
 
+    # HBM bytes per backward launch from the committed PMC summary (FETCH_SIZE
+    # and WRITE_SIZE, each scaled by the counter's reading on a 256 MiB copy).
     traffic = None
-    traffic_file = ROOT / "profiles" / f"traffic_d{d}m{m}_b{b}t{t}h{h}.json"
+    traffic_file = ROOT / "profiles" / f"traffic_d{d}m{m}_b{b}t{t}h{h}.txt"
     if traffic_file.exists():
-        traffic = json.loads(traffic_file.read_text()).get("backward_bytes_per_launch")
+        for line in traffic_file.read_text().splitlines():
+            if line.startswith("backward_bytes_per_launch ="):
+                traffic = int(line.split("=")[1])
 
     result = {
         "metric": METRIC,
@@ -197,7 +211,7 @@ def main() -> int:
         },
         "roofline": {
             "bound": "hbm",
-            "kernel": "backward_kernel<4,8,4,8,false,true> (chunk replay + reverse)",
+            "kernel": "bssm::r4::backward_kernel<false, true> (checkpoint replay + reverse, D4M8)",
             "achieved": bwd_gbs,
             "peak": HBM_PEAK / 1e9,
             "unit": "GB/s",
@@ -209,6 +223,7 @@ def main() -> int:
         "roofline_forward": {"achieved": fwd_gbs, "frac": fwd_gbs * 1e9 / HBM_PEAK, "avg_launch_ms": fwd_ms,
                              "bytes_per_launch": fwd_b * units},
         "roofline_step_frac": step_frac,
+        "measured_copy_gbs": copy_gbs,
         "device": torch.cuda.get_device_name(device),
         "hip_library": str(_hip.LIB_PATH.relative_to(ROOT)),
     }
