@@ -44,6 +44,15 @@ constexpr int TT = 8;     // forward tile, tokens
 constexpr int SUB = 8;    // backward checkpoint chunk, tokens
 constexpr int kDword3 = 0x00020000;  // raw fp32 buffer, gfx9 family
 constexpr uint32_t kOob = 0x80000000u;  // offset past every descriptor range: load 0, drop store
+#ifndef BSSM_R4_NT
+#define BSSM_R4_NT 7
+#endif
+// Nontemporal hints: bit 0 token-stream loads, bit 1 token-stream stores,
+// bit 2 checkpoint stores and loads.
+constexpr bool kNtLoad = (BSSM_R4_NT & 1) != 0;
+constexpr int kStoreNt = 2;  // gfx9 cache policy: nt
+constexpr int kNtStore = (BSSM_R4_NT & 2) ? kStoreNt : 0;
+constexpr bool kNtCkpt = (BSSM_R4_NT & 4) != 0;
 
 typedef float v2f __attribute__((ext_vector_type(2)));
 using Rsrc = __amdgpu_buffer_rsrc_t;
@@ -59,12 +68,21 @@ __device__ __forceinline__ Rsrc make_rsrc(const float* base, uint32_t bytes) {
 // compiler; their completion is awaited explicitly with vm_wait().
 // The whole offset goes in the VGPR operand so that the descriptor's range
 // check covers it (the scalar offset is outside the check on gfx9).
+// NT = nontemporal (streamed once): used for streams whose DMA rows are
+// whole 128-byte lines.
+template <bool NT = false>
 __device__ __forceinline__ void dma16(Rsrc r, const float* lds, uint32_t voff) {
   const uint32_t base = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(lds));
-  asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
-               :
-               : "s"(base), "v"(voff), "s"(r)
-               : "memory");
+  if constexpr (NT)
+    asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen nt lds"
+                 :
+                 : "s"(base), "v"(voff), "s"(r)
+                 : "memory");
+  else
+    asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
+                 :
+                 : "s"(base), "v"(voff), "s"(r)
+                 : "memory");
 }
 
 // Wait until at most N vector-memory operations are outstanding.  Loads
@@ -85,9 +103,11 @@ __device__ __forceinline__ void vm_wait() {
 // The raw buffer builtins move untyped 32-bit words; floats are bit-cast.
 typedef uint32_t v2u __attribute__((ext_vector_type(2)));
 typedef uint32_t v4u __attribute__((ext_vector_type(4)));
+// AUX = cache-policy bits of the store (kStoreNt: nontemporal).
+template <int AUX = 0>
 __device__ __forceinline__ void st128(Rsrc r, v4f x, uint32_t voff, uint32_t soff) {
   __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(v4u, x), r, static_cast<int>(voff),
-                                         static_cast<int>(soff), 0);
+                                         static_cast<int>(soff), AUX);
 }
 __device__ __forceinline__ void st64(Rsrc r, v2f x, uint32_t voff, uint32_t soff) {
   __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(v2u, x), r, static_cast<int>(voff),
@@ -470,8 +490,8 @@ __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(1, 1))) v
     const v4f x0 = *reinterpret_cast<const v4f*>(&ckst[lane * 4]);
     const v4f x1 = *reinterpret_cast<const v4f*>(&ckst[256 + lane * 4]);
     const v4f x2 = *reinterpret_cast<const v4f*>(&ckst[512 + lane * 4]);
-    st128(rbm, x0, ckoff.m0, c * 128u);
-    st128(rbm, x1, ckoff.m1, c * 128u);
+    st128<kNtCkpt ? kStoreNt : 0>(rbm, x0, ckoff.m0, c * 128u);
+    st128<kNtCkpt ? kStoreNt : 0>(rbm, x1, ckoff.m1, c * 128u);
     st128(rbc, x2, ckoff.c, c * 64u);
   };
   store_ckpt(0);
@@ -481,12 +501,12 @@ __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(1, 1))) v
                    s1 = static_cast<uint32_t>(t0) * 4u;
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
-      dma16(rk, (tl + FwdTile::K) + 256 * j, mp.d4[j] + s4);
-      dma16(rq, (tl + FwdTile::Q) + 256 * j, mp.d4[j] + s4);
-      if constexpr (!FIXED) dma16(rd, (tl + FwdTile::D) + 256 * j, mp.d4[j] + s4);
+      dma16<kNtLoad>(rk, (tl + FwdTile::K) + 256 * j, mp.d4[j] + s4);
+      dma16<kNtLoad>(rq, (tl + FwdTile::Q) + 256 * j, mp.d4[j] + s4);
+      if constexpr (!FIXED) dma16<kNtLoad>(rd, (tl + FwdTile::D) + 256 * j, mp.d4[j] + s4);
     }
 #pragma unroll
-    for (int j = 0; j < 4; ++j) dma16(rv, (tl + FwdTile::V) + 256 * j, mp.d8[j] + s8);
+    for (int j = 0; j < 4; ++j) dma16<kNtLoad>(rv, (tl + FwdTile::V) + 256 * j, mp.d8[j] + s8);
     if constexpr (!FIXED) {
       dma16(rp, (tl + FwdTile::P), mp.d1 + s1);
       dma16(rr, (tl + FwdTile::R), mp.d1 + s1);
@@ -564,7 +584,7 @@ __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(1, 1))) v
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const v4f x = *reinterpret_cast<const v4f*>(&(tl + FwdTile::V)[(64 * j + lane) * 4]);
-      st128(ry, x, mp.t8[j] < len ? mp.d8[j] : kOob, s8);
+      st128<kNtStore>(ry, x, mp.t8[j] < len ? mp.d8[j] : kOob, s8);
     }
   };
   // Tile i lives in slot i % 3.  At its start: wait for its DMA (issued two
@@ -687,22 +707,22 @@ __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(1, 1))) v
                    s1 = static_cast<uint32_t>(t0) * 4u;
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
-      dma16(rk, (tl + BwdTile::K) + 256 * j, mp.d4[j] + s4);
-      dma16(rq, (tl + BwdTile::Q) + 256 * j, mp.d4[j] + s4);
-      if constexpr (!FIXED) dma16(rd, (tl + BwdTile::D) + 256 * j, mp.d4[j] + s4);
+      dma16<kNtLoad>(rk, (tl + BwdTile::K) + 256 * j, mp.d4[j] + s4);
+      dma16<kNtLoad>(rq, (tl + BwdTile::Q) + 256 * j, mp.d4[j] + s4);
+      if constexpr (!FIXED) dma16<kNtLoad>(rd, (tl + BwdTile::D) + 256 * j, mp.d4[j] + s4);
     }
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      dma16(rv, (tl + BwdTile::V) + 256 * j, mp.d8[j] + s8);
-      dma16(rgy, (tl + BwdTile::GY) + 256 * j, mp.d8[j] + s8);
+      dma16<kNtLoad>(rv, (tl + BwdTile::V) + 256 * j, mp.d8[j] + s8);
+      dma16<kNtLoad>(rgy, (tl + BwdTile::GY) + 256 * j, mp.d8[j] + s8);
     }
     if constexpr (!FIXED) {
       dma16(rp, (tl + BwdTile::P), mp.d1 + s1);
       dma16(rr, (tl + BwdTile::R), mp.d1 + s1);
     }
     const uint32_t cm = static_cast<uint32_t>(c) * 128u, cc = static_cast<uint32_t>(c) * 64u;
-    dma16(rbm, (tl + BwdTile::CK), ckoff.m0 + cm);
-    dma16(rbm, (tl + BwdTile::CK) + 256, ckoff.m1 + cm);
+    dma16<kNtCkpt>(rbm, (tl + BwdTile::CK), ckoff.m0 + cm);
+    dma16<kNtCkpt>(rbm, (tl + BwdTile::CK) + 256, ckoff.m1 + cm);
     dma16(rbc, (tl + BwdTile::CK) + 512, ckoff.c + cc);
   };
 
@@ -796,13 +816,13 @@ __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(1, 1))) v
     for (int j = 0; j < 2; ++j) {
       const uint32_t off = mp.t4[j] < len ? mp.d4[j] : kOob;
       const int e = (64 * j + lane) * 4;
-      st128(rgk, *reinterpret_cast<const v4f*>(&(tl + BwdTile::K)[e]), off, s4);
-      st128(rgq, *reinterpret_cast<const v4f*>(&(tl + BwdTile::Q)[e]), off, s4);
-      if (a.gd) st128(rgd, *reinterpret_cast<const v4f*>(&(tl + BwdTile::D)[e]), off, s4);
+      st128<kNtStore>(rgk, *reinterpret_cast<const v4f*>(&(tl + BwdTile::K)[e]), off, s4);
+      st128<kNtStore>(rgq, *reinterpret_cast<const v4f*>(&(tl + BwdTile::Q)[e]), off, s4);
+      if (a.gd) st128<kNtStore>(rgd, *reinterpret_cast<const v4f*>(&(tl + BwdTile::D)[e]), off, s4);
     }
 #pragma unroll
     for (int j = 0; j < 4; ++j)
-      st128(rgv, *reinterpret_cast<const v4f*>(&(tl + BwdTile::V)[(64 * j + lane) * 4]),
+      st128<kNtStore>(rgv, *reinterpret_cast<const v4f*>(&(tl + BwdTile::V)[(64 * j + lane) * 4]),
             mp.t8[j] < len ? mp.d8[j] : kOob, s8);
     const uint32_t off1 = mp.t1 < len ? mp.d1 : kOob;
     if (a.gp) st128(rgp, *reinterpret_cast<const v4f*>(&(tl + BwdTile::P)[lane * 4]), off1, s1);
