@@ -16,20 +16,20 @@
 // and the covariance stays bitwise symmetric, because entry (g, h) and its
 // mirror (h, g) are computed by two lanes from commutative products only.
 //
-// Memory: all streamed tensors move through LDS tiles written by LDS-DMA
-// (buffer_load ... lds), addressed by per-workgroup buffer descriptors whose
-// range ends at the last valid sequence, so rows past N read as zero and
-// their stores are dropped without branches.  Tiles move whole cache lines
-// of each sequence row and are laid out in LDS so that the per-token reads
-// of 16 sequences are bank-conflict free (see Map).  A
-// workgroup is a single wave, so LDS needs no barriers; the compiler tracks
-// the LDS-DMA of each tile slot (separate __shared__ objects) and waits only
-// for the slot it reads next.
+// Memory: all streamed tensors move through LDS tiles, addressed by
+// per-workgroup buffer descriptors whose range ends at the last valid
+// sequence, so rows past N read as zero and their stores are dropped without
+// branches.  Tiles move whole cache lines of each sequence row (with
+// nontemporal hints) and are laid out in LDS so that the per-token reads of
+// 16 sequences are bank-conflict free (see Map).  A workgroup is a single
+// wave, so LDS needs no barriers.
 //
-// Forward: ring of 3 tiles of 8 tokens (two in flight).  Backward: the
-// belief is checkpointed every 8 tokens; each chunk is replayed on chip
-// (history in registers) and reversed, with the next chunk's inputs and
-// checkpoint loading meanwhile (ring of 2).  Checkpoints move as whole
+// Forward: 16-token tiles staged in registers (the next tile's loads are in
+// flight while the current one is computed from LDS), so each sequence row
+// is requested 256 bytes at a time.  Backward: the belief is checkpointed
+// every 8 tokens; each chunk is replayed on chip (history in registers) and
+// reversed, with the next chunk's inputs and checkpoint arriving by LDS-DMA
+// (buffer_load ... lds) meanwhile (ring of 2).  Checkpoints move as whole
 // 16-byte pieces of each belief record (staged through LDS).
 
 #include <type_traits>
@@ -443,17 +443,33 @@ struct Idx {
   __device__ __forceinline__ int i1(int tt) const { return w1 + tt; }
 };
 
-// One forward tile slot (floats): k, d, q [8 tokens x 16 sequences x 4],
-// v [8 x 16 x 8] (values in, readouts out, in place), p and r [16 x 8 used;
-// the rest catches the idle half of their DMA].  Each slot is one __shared__
-// object so the compiler can wait for the LDS-DMA of one slot at a time.
+// One forward tile holds 16 tokens of the 16 sequences as two 8-token
+// sub-tiles in the layout above (floats per sub-tile): k, d, q [8 x 16 x 4],
+// v [8 x 16 x 8] (values in, readouts out, in place), p and r [16 x 8].
 struct FwdTile {
-  static constexpr int K = 0, D = 512, Q = 1024, V = 1536, P = 2560, R = 2816, SIZE = 3072;
+  static constexpr int K = 0, D = 512, Q = 1024, V = 1536, P = 2560, R = 2688, SIZE = 2816;
+};
+constexpr int LT = 2 * TT;  // tokens per register-staged load tile
+
+// 16-byte load of one lane's piece (voff carries the whole offset so that
+// the descriptor's range check covers it).
+template <bool NT>
+__device__ __forceinline__ v4f ld128(Rsrc r, uint32_t voff) {
+  return __builtin_bit_cast(v4f, __builtin_amdgcn_raw_buffer_load_b128(r, static_cast<int>(voff), 0, NT ? 2 : 0));
+}
+
+// Register staging of one 16-token forward tile: for each sub-tile h and
+// DMA-shaped instruction j, the lane's piece (the same pieces the Map
+// describes, so every instruction still moves whole row segments and the two
+// halves of a row are requested back to back).  p and r take one
+// instruction each: lane l -> row l >> 2, piece l & 3 (16 rows x 64 B).
+struct FwdStage {
+  v4f k[4], q[4], d[4], v[8], p, r;
 };
 
 template <bool FIXED>
 __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(1, 1))) void forward_kernel(FwdArgs a) {
-  __shared__ float ta[FwdTile::SIZE], tb[FwdTile::SIZE], tc[FwdTile::SIZE];
+  __shared__ float tile[2 * FwdTile::SIZE];
   __shared__ float ckst[kRecFloats];  // checkpoint staging
   const int lane = threadIdx.x;
   const int g = lane & 3, s = lane >> 2;
@@ -479,6 +495,8 @@ __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(1, 1))) v
 
   const Map mp(lane, row4, row8, row1);
   const Idx ix(s, g);
+  const uint32_t off1 = static_cast<uint32_t>(lane >> 2) * row1 + static_cast<uint32_t>(lane & 3) * 16u;
+  const int dst1 = ((lane & 3) >> 1) * FwdTile::SIZE + 4 * (2 * (lane >> 2) + (lane & 1));
 
   const BelOff unit(s, g, 128u, 64u);
   const RecOff ckoff(lane, nbp * 128u, nbp * 64u);
@@ -496,20 +514,41 @@ __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(1, 1))) v
   };
   store_ckpt(0);
 
-  auto issue = [&](float* tl, int64_t t0) __attribute__((always_inline)) {
-    const uint32_t s4 = static_cast<uint32_t>(t0) * 16u, s8 = static_cast<uint32_t>(t0) * 32u,
-                   s1 = static_cast<uint32_t>(t0) * 4u;
+  auto load = [&](FwdStage& x, int64_t t0) __attribute__((always_inline)) {
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      dma16<kNtLoad>(rk, (tl + FwdTile::K) + 256 * j, mp.d4[j] + s4);
-      dma16<kNtLoad>(rq, (tl + FwdTile::Q) + 256 * j, mp.d4[j] + s4);
-      if constexpr (!FIXED) dma16<kNtLoad>(rd, (tl + FwdTile::D) + 256 * j, mp.d4[j] + s4);
+    for (int h = 0; h < 2; ++h) {
+      const uint32_t s4 = static_cast<uint32_t>(t0 + TT * h) * 16u, s8 = static_cast<uint32_t>(t0 + TT * h) * 32u;
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        x.k[2 * h + j] = ld128<kNtLoad>(rk, mp.d4[j] + s4);
+        x.q[2 * h + j] = ld128<kNtLoad>(rq, mp.d4[j] + s4);
+        if constexpr (!FIXED) x.d[2 * h + j] = ld128<kNtLoad>(rd, mp.d4[j] + s4);
+      }
+#pragma unroll
+      for (int j = 0; j < 4; ++j) x.v[4 * h + j] = ld128<kNtLoad>(rv, mp.d8[j] + s8);
     }
-#pragma unroll
-    for (int j = 0; j < 4; ++j) dma16<kNtLoad>(rv, (tl + FwdTile::V) + 256 * j, mp.d8[j] + s8);
     if constexpr (!FIXED) {
-      dma16(rp, (tl + FwdTile::P), mp.d1 + s1);
-      dma16(rr, (tl + FwdTile::R), mp.d1 + s1);
+      const uint32_t s1 = static_cast<uint32_t>(t0) * 4u;
+      x.p = ld128<false>(rp, off1 + s1);
+      x.r = ld128<false>(rr, off1 + s1);
+    }
+  };
+  auto put = [&](const FwdStage& x) __attribute__((always_inline)) {
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      float* tl = tile + h * FwdTile::SIZE;
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        *reinterpret_cast<v4f*>(&(tl + FwdTile::K)[256 * j + 4 * lane]) = x.k[2 * h + j];
+        *reinterpret_cast<v4f*>(&(tl + FwdTile::Q)[256 * j + 4 * lane]) = x.q[2 * h + j];
+        if constexpr (!FIXED) *reinterpret_cast<v4f*>(&(tl + FwdTile::D)[256 * j + 4 * lane]) = x.d[2 * h + j];
+      }
+#pragma unroll
+      for (int j = 0; j < 4; ++j) *reinterpret_cast<v4f*>(&(tl + FwdTile::V)[256 * j + 4 * lane]) = x.v[4 * h + j];
+    }
+    if constexpr (!FIXED) {
+      *reinterpret_cast<v4f*>(&(tile + FwdTile::P)[dst1]) = x.p;
+      *reinterpret_cast<v4f*>(&(tile + FwdTile::R)[dst1]) = x.r;
     }
   };
 
@@ -549,7 +588,7 @@ __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(1, 1))) v
   auto put_y = [&](float* tl, int tt, v2f y) __attribute__((always_inline)) {
     *reinterpret_cast<v2f*>(&(tl + FwdTile::V)[ix.i8(tt)]) = y;
   };
-  // A full tile: the LDS reads of tokens 2j+2 and 2j+3 are issued before
+  // A full sub-tile: the LDS reads of tokens 2j+2 and 2j+3 are issued before
   // tokens 2j and 2j+1 are computed (the scheduling barrier keeps them
   // there), and the readouts stay in registers until the last token, so no
   // LDS write sits between reads.
@@ -571,40 +610,16 @@ __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(1, 1))) v
 #pragma unroll
     for (int tt = 0; tt < TT; ++tt) put_y(tl, tt, y[tt]);
   };
-
-  const int64_t ntiles = (T + TT - 1) / TT;
-  constexpr int kTileLoads = FIXED ? 8 : 12;  // DMA instructions per tile (see issue)
-  auto tile_len = [&](int64_t i) __attribute__((always_inline)) {
-    return static_cast<int>((T - i * TT) < TT ? (T - i * TT) : TT);
-  };
-  // Readouts of tile i (slot `tl`), written back piece by piece.
-  auto store_y = [&](const float* tl, int64_t i) __attribute__((always_inline)) {
-    const int len = tile_len(i);
-    const uint32_t s8 = static_cast<uint32_t>(i * TT) * 32u;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const v4f x = *reinterpret_cast<const v4f*>(&(tl + FwdTile::V)[(64 * j + lane) * 4]);
-      st128<kNtStore>(ry, x, mp.t8[j] < len ? mp.d8[j] : kOob, s8);
-    }
-  };
-  // Tile i lives in slot i % 3.  At its start: wait for its DMA (issued two
-  // tiles earlier; only the kTileLoads DMA loads of tile i + 1 may still be
-  // in flight), store the readouts of tile i - 1 from the slot that tile i + 2
-  // then loads into, and compute.
-  auto run_tile = [&](float* cur, float* prev, int64_t i) __attribute__((always_inline)) {
-    if (i + 1 < ntiles) vm_wait<kTileLoads>();
-    else vm_wait<0>();
-    if (i > 0) store_y(prev, i - 1);
-    if (i + 2 < ntiles) issue(prev, (i + 2) * TT);
-    const int64_t t0 = i * TT;
-    const int len = tile_len(i);
-    if (t0 == next_ckpt && t0 > 0) {
+  // Sub-tile starting at token t0 (fewer than TT tokens at the end).
+  auto run_sub = [&](float* tl, int64_t t0) __attribute__((always_inline)) {
+    const int len = static_cast<int>((T - t0) < TT ? (T - t0) : TT);
+    if (t0 == next_ckpt) {
       store_ckpt(ckpt);
       ++ckpt;
       next_ckpt += a.chunk;
     }
     if (len == TT && next_ckpt >= t0 + TT) {
-      full_tile(cur);
+      full_tile(tl);
     } else {
 #pragma unroll 1
       for (int tt = 0; tt < len; ++tt) {
@@ -615,23 +630,60 @@ __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(1, 1))) v
         }
         FwdIn x;
         v2f y;
-        read_in(cur, tt, x);
+        read_in(tl, tt, x);
         step(x, y);
-        put_y(cur, tt, y);
+        put_y(tl, tt, y);
       }
     }
   };
 
-  if (ntiles > 0) issue(ta, 0);
-  if (ntiles > 1) issue(tb, TT);
-  for (int64_t i = 0; i < ntiles; i += 3) {
-    run_tile(ta, tc, i);
-    if (i + 1 < ntiles) run_tile(tb, ta, i + 1);
-    if (i + 2 < ntiles) run_tile(tc, tb, i + 2);
+  // Readouts of a tile: read out of LDS before the next tile is written
+  // there, stored after that tile's loads have been awaited.
+  struct FwdOut {
+    v4f y[8];
+  };
+  auto take_y = [&](FwdOut& o) __attribute__((always_inline)) {
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        o.y[4 * h + j] = *reinterpret_cast<const v4f*>(&(tile + h * FwdTile::SIZE + FwdTile::V)[256 * j + 4 * lane]);
+  };
+  auto store_y = [&](const FwdOut& o, int64_t t0) __attribute__((always_inline)) {
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int64_t th = t0 + TT * h;
+      const int len = static_cast<int>((T - th) < TT ? (T - th) : TT);
+      const uint32_t s8 = static_cast<uint32_t>(th) * 32u;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) st128<kNtStore>(ry, o.y[4 * h + j], mp.t8[j] < len ? mp.d8[j] : kOob, s8);
+    }
+  };
+
+  // Tile i: its loads were issued at the start of tile i - 1 (the compiler
+  // waits for them before they are written to LDS); the readouts of tile
+  // i - 1 leave LDS first and are stored after that wait, then the loads of
+  // tile i + 1 are issued and the two sub-tiles computed.
+  const int64_t ntiles = (T + LT - 1) / LT;
+  FwdStage st;
+  load(st, 0);
+  for (int64_t i = 0; i < ntiles; ++i) {
+    FwdOut yo;
+    if (i > 0) take_y(yo);
+    __builtin_amdgcn_sched_barrier(0);
+    put(st);
+    __builtin_amdgcn_sched_barrier(0);
+    if (i > 0) store_y(yo, (i - 1) * LT);
+    if (i + 1 < ntiles) load(st, (i + 1) * LT);
+    __builtin_amdgcn_sched_barrier(0);
+    const int64_t t0 = i * LT;
+    run_sub(tile, t0);
+    if (t0 + TT < T) run_sub(tile + FwdTile::SIZE, t0 + TT);
   }
-  if (ntiles > 0) {
-    const int64_t last = ntiles - 1;
-    store_y(last % 3 == 0 ? ta : (last % 3 == 1 ? tb : tc), last);
+  {
+    FwdOut yo;
+    take_y(yo);
+    store_y(yo, (ntiles - 1) * LT);
   }
   store_bel(b, rmT, rcT, unit, 0, 0);
   const uint32_t nbc = static_cast<uint32_t>(a.nb);
