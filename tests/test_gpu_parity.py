@@ -69,8 +69,9 @@ def _fixed_dynamics(c):
 
 
 # T = 45 takes the generic kernels; T = 52 (a multiple of 4 that is not a
-# multiple of the 8-token tile) takes the D4 rotated-layout kernels with a
-# partial last tile.  N = 37 leaves idle sequence slots in the last wave.
+# multiple of the 16-token forward tile) takes the D4 rotated-layout kernels
+# with a partial last tile (their backward needs the library's preferred
+# checkpoint chunk, 8).  N = 37 leaves idle sequence slots in the last wave.
 TIMES = [45, 52]
 
 
@@ -137,7 +138,7 @@ ABIS = [
 @pytest.mark.parametrize("d", DIMS)
 @pytest.mark.parametrize("abi", ABIS, ids=[a[0] for a in ABIS])
 @pytest.mark.parametrize("final_grads", [False, True])
-@pytest.mark.parametrize("chunk", [8, 13])
+@pytest.mark.parametrize("chunk", [8, 13, 16])
 @pytest.mark.parametrize("t", TIMES)
 def test_backward_matches_oracle(ext_for, cuda_device, d, abi, final_grads, chunk, t):
     name, fixed, nout = abi
@@ -171,6 +172,35 @@ def test_backward_matches_oracle(ext_for, cuda_device, d, abi, final_grads, chun
             assert torch.count_nonzero(grads[i]) == 0, f"{names[i]} must be zero for fixed dynamics"
             continue
         close(grads[i], eg[i], names[i])
+
+
+@pytest.mark.parametrize("t", [4, 8, 12, 16, 20, 24, 56, 60])
+@pytest.mark.parametrize("fixed", [False, True])
+def test_rot4_backward_tails(ext_for, cuda_device, t, fixed):
+    """D4 rotated-layout kernels at the preferred checkpoint chunk: every shape of the last tiles."""
+    from bayes_ssm import _hip
+
+    print(f"rot4 backward tails t={t} fixed={fixed}", flush=True)
+    n, d = 21, 4
+    chunk = _hip.preferred_checkpoint(d)
+    cpu, dev = _case(n, t, d, seed=100 + t, device=cuda_device)
+    ref = _fixed_dynamics(cpu) if fixed else cpu
+    ext = ext_for(d)
+    fwd = ext.forward_chunked_fixed if fixed else ext.forward_chunked
+    bwd = ext.backward_chunked_fixed if fixed else ext.backward_chunked
+    _, _, _, bm, bc = fwd(dev["k"], dev["v"], dev["q"], dev["d"], dev["p"], dev["r"], dev["m0"], dev["c0"], chunk,
+                          1e-6)
+    grads = bwd(dev["k"], dev["v"], dev["q"], dev["d"], dev["p"], dev["r"], dev["m0"], dev["c0"], bm, bc, dev["gy"],
+                dev["gmf"], dev["gcf"], chunk, 1e-6)
+    torch.cuda.synchronize()
+    f64 = {k: x.double() for k, x in ref.items()}
+    _, _, _, eg = O.diagonal_grads(f64["k"], f64["v"], f64["q"], f64["d"], f64["p"], f64["r"], f64["m0"], f64["c0"],
+                                   f64["gy"], f64["gmf"], f64["gcf"])
+    for i, name in enumerate(["gk", "gv", "gq", "gd", "gp", "gr", "gm0", "gc0"]):
+        if fixed and name in ("gd", "gp", "gr"):
+            assert torch.count_nonzero(grads[i]) == 0, f"{name} must be zero for fixed dynamics"
+            continue
+        close(grads[i], eg[i], name)
 
 
 @pytest.mark.parametrize("d", DIMS)
