@@ -57,6 +57,80 @@ def make_workload(b, t, h, d, m, device, seed=0):
     return leaves, m0, c0, gy
 
 
+def cpu_model() -> str:
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown CPU"
+
+
+def time_layer(b, t, h, d, m, chunk, steps, warmup, device) -> dict:
+    """fwd+bwd of fused_diagonal_bayesian at one shape: ms/step, tokens/s, step roofline fraction."""
+    from bayes_ssm import fused_cuda
+
+    leaves, m0, c0, gy = make_workload(b, t, h, d, m, device, seed=1)
+
+    def step():
+        y, _, _ = fused_cuda.fused_diagonal_bayesian(*leaves, m0, c0, chunk_length=chunk, denominator_floor=1e-6)
+        return torch.autograd.grad(y, leaves, gy)
+
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(steps):
+        step()
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / steps
+    fwd_b, bwd_b = algorithmic_bytes(d, m)
+    return {"B": b, "T": t, "H": h, "D": d, "M": m, "ms_per_step": ms, "tokens_per_s": b * t / (ms * 1e-3),
+            "roofline_step_frac": (fwd_b + bwd_b) * b * h * t / (ms * 1e-3) / HBM_PEAK}
+
+
+def time_scan(b, t, d, m, iters, device) -> dict:
+    """Forward of associative_static_bayesian_cuda (one HIP kernel): mean microseconds per call."""
+    from bayes_ssm.replay_ssm import associative_static_bayesian_cuda
+
+    g = torch.Generator(device=device).manual_seed(0)
+    k = torch.randn(b, t, d, device=device, generator=g) / d ** 0.5
+    v = torch.randn(b, t, m, device=device, generator=g)
+    q = torch.randn(b, t, d, device=device, generator=g)
+    r = 1e-4 + torch.nn.functional.softplus(torch.randn(b, t, device=device, generator=g))
+    for _ in range(5):
+        associative_static_bayesian_cuda(k, v, q, observation_variances=r)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(iters):
+        associative_static_bayesian_cuda(k, v, q, observation_variances=r)
+    e1.record()
+    torch.cuda.synchronize()
+    api_us = e0.elapsed_time(e1) / iters * 1e3
+    # The kernel alone, through the C ABI (the API call above also validates
+    # its inputs on the host, which synchronizes, as the reference does).
+    from bayes_ssm import _hip
+
+    m0 = torch.zeros(b, d, m, device=device)
+    c0 = torch.eye(d, device=device).expand(b, d, d).contiguous()
+    out, mT, cT = torch.empty(b, t, m, device=device), torch.empty(b, d, m, device=device), torch.empty_like(c0)
+    P = _hip.ptr
+    args = (P(k), P(v), P(q), P(r), P(m0), P(c0), P(out), P(mT), P(cT), b, t, d, m, _hip.stream_of(device))
+    _hip.call("bssm_associative_static_scan", *args)
+    torch.cuda.synchronize()
+    e0.record()
+    for _ in range(iters):
+        _hip.call("bssm_associative_static_scan", *args)
+    e1.record()
+    torch.cuda.synchronize()
+    return {"B": b, "T": t, "D": d, "M": m, "api_us_per_call": api_us,
+            "kernel_us_per_call": e0.elapsed_time(e1) / iters * 1e3}
+
+
 def cpu_baseline(t: int, d: int, m: int, heads: int, budget_s: float) -> dict:
     """Time the CPU restatement of the reference CPU path on a bounded sample.
 
@@ -85,16 +159,17 @@ def cpu_baseline(t: int, d: int, m: int, heads: int, budget_s: float) -> dict:
         "cores": threads,
         "kind": "port",
         "sample": (f"{n} of 16384 head-sequences x T={t} (D{d}M{m}), fwd+bwd of the oracle's restatement of "
-                   f"bayesian_layer(optimized=False, chunk_length=64) with autograd, fp32, {threads} threads, "
-                   f"{elapsed:.1f} s; sequences are independent, so tokens/s scales linearly to the full batch"),
+                   f"bayesian_layer(optimized=False, chunk_length=64) with autograd, fp32, {threads} threads of "
+                   f"{cpu_model()}, torch {torch.__version__}, {elapsed:.1f} s; sequences are independent, so "
+                   f"tokens/s scales linearly to the full batch"),
     }
 
 
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--steps", type=int, default=30)
+    ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--batch", type=int, default=256)
     ap.add_argument("--seq", type=int, default=512)
     ap.add_argument("--heads", type=int, default=64)
@@ -102,6 +177,8 @@ def main() -> int:
     ap.add_argument("--chunk", type=int, default=64)
     ap.add_argument("--kernel-iters", type=int, default=20, help="iterations of the per-kernel event timing")
     ap.add_argument("--cpu-budget", type=float, default=20.0, help="seconds of CPU-baseline work (0 = skip)")
+    ap.add_argument("--no-extras", action="store_true",
+                    help="skip the secondary shapes (per-GPU DP shape, D1/D2/D8 variants, associative scan)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="also run one 256 MiB device copy (reference kernel for PMC byte counters)")
     args = ap.parse_args()
@@ -227,6 +304,16 @@ def main() -> int:
         "device": torch.cuda.get_device_name(device),
         "hip_library": str(_hip.LIB_PATH.relative_to(ROOT)),
     }
+    if not args.no_extras:
+        # Secondary shapes (not the metric): config 3 divided by 8 (one GPU's
+        # share under 8-way data parallelism), the D2M8 / D8M8 variants of
+        # config 3, config 2 (D1M8, B64), and the associative-scan configs.
+        extras = {"dp8_share_d4m8": time_layer(b // 8, t, h, d, m, args.chunk, 30, 10, device)}
+        for name, (eb, ed) in {"config3_d2m8": (b, 2), "config3_d8m8": (b, 8), "config2_d1m8": (64, 1)}.items():
+            extras[name] = time_layer(eb, t, h, ed, m, args.chunk, 10, 3, device)
+        extras["assoc_scan_config0"] = time_scan(1, 16, 4, 4, 50, device)
+        extras["assoc_scan_config1"] = time_scan(4, 64, 16, 16, 50, device)
+        result["extras"] = extras
     if args.cpu_budget > 0:
         result["cpu_baseline"] = cpu_baseline(t, d, m, h, args.cpu_budget)
     print(json.dumps(result), flush=True)

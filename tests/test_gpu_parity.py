@@ -316,6 +316,28 @@ def test_associative_scan_configs(cuda_device, cfg):
     close(y, dy, "y vs dense")
 
 
+@pytest.mark.parametrize("cfg", [(3, 5, 1, 8), (2, 9, 3, 5), (2, 12, 5, 7), (3, 20, 12, 33), (2, 10, 20, 9),
+                                 (1, 6, 32, 64)])
+def test_associative_scan_priors_and_sizes(cuda_device, cfg):
+    """Key dims padded to the register kernel's sizes and the LDS kernel (D > 16), with a random SPD prior."""
+    import bayes_ssm
+
+    b, t, d, m = cfg
+    print(f"associative scan b={b} t={t} d={d} m={m}", flush=True)
+    k, v, q, r = O.make_scan_inputs(b, t, d, m, seed=d + m)
+    gen = torch.Generator().manual_seed(7)
+    a = torch.randn(b, d, d, generator=gen) / d ** 0.5
+    c0 = a @ a.transpose(-1, -2) + 0.5 * torch.eye(d)
+    m0 = torch.randn(b, d, m, generator=gen)
+    y, mT, cT = bayes_ssm.associative_static_bayesian_cuda(
+        k.to(cuda_device), v.to(cuda_device), q.to(cuda_device), observation_variances=r.to(cuda_device),
+        initial_mean=m0.to(cuda_device), initial_covariance=c0.to(cuda_device))
+    ey, em, ec = O.associative_static(k.double(), v.double(), q.double(), r.double(), m0.double(), c0.double())
+    close(y, ey, "y")
+    close(mT, em, "mean")
+    close(cT, ec, "cov")
+
+
 def test_config3_full_size_subset(cuda_device):
     """Config 3 at full size (B256 x T512 x H64, D4M8): fwd+bwd on the GPU, a seeded subset of sequences against the oracle."""
     from bayes_ssm.fused_cuda import fused_diagonal_bayesian
