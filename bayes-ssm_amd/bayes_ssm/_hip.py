@@ -45,12 +45,14 @@ _SIGNATURES = {
     "bssm_backward_chunked_noinitial_fixed": _BWD_SIX,
     "bssm_backward_chunked_saved": _BWD_SAVED_HEAD + [_P] * 8 + [_L, _L, _L, _F, _P],
     "bssm_backward_chunked_saved_lean": _BWD_SAVED_HEAD + [_P] * 3 + [_L, _L, _L, _F, _P],
+    "bssm_forward_chunked_bf16": [_I, _I, _I] + [_P] * 8 + [_P] * 5 + [_L, _L, _L, _F, _P],
+    "bssm_backward_chunked_bf16": [_I, _I, _I] + [_P] * 10 + [_P] * 3 + [_P] * 8 + [_L, _L, _L, _F, _P],
     "bssm_associative_static_scan": [_P] * 9 + [_L, _L, _I, _I, _P],
     "bssm_supported": [_I, _I],
     "bssm_preferred_checkpoint": [_I],
     "bssm_abi_version": [],
 }
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 _lock = threading.Lock()
 _lib: Optional[ctypes.CDLL] = None

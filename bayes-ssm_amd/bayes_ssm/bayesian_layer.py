@@ -335,6 +335,10 @@ def bayesian_layer(
     batch_shape = keys.shape[:-2]
     device = keys.device
     dtype = torch.float32 if keys.dtype in _LOW_PRECISION else keys.dtype
+    # bfloat16 keys/values/queries go to the fused kernels as bfloat16 (they
+    # widen on chip); every other path sees the promoted tensors.
+    bf16_kqv = ((keys, values, queries) if all(x.dtype == torch.bfloat16 for x in (keys, values, queries))
+                else None)
     keys, values, queries = keys.to(dtype), values.to(dtype), queries.to(dtype)
     for x, name in ((keys, "keys"), (values, "values"), (queries, "queries")):
         _check_finite(x, name)
@@ -500,7 +504,8 @@ def bayesian_layer(
             and process_covariances is None and not (mean.requires_grad or cov.requires_grad)):
         from .fused_cuda import fused_diagonal_bayesian
 
-        fused = fused_diagonal_bayesian(keys, values, queries, diagonal, process_variances, observation_variances,
+        fk, fv, fq = bf16_kqv if bf16_kqv is not None else (keys, values, queries)
+        fused = fused_diagonal_bayesian(fk, fv, fq, diagonal, process_variances, observation_variances,
                                         mean, cov, chunk_length=chunk_length, denominator_floor=floor,
                                         fixed_dynamics=fixed_dynamics)
         if fused is not None:

@@ -28,6 +28,13 @@ Deliberate differences from the reference, all result-preserving:
 * D1 keeps its boundaries through the replay kernel by default; the reference
   saved-history ABI (forward_chunked_saved / backward_chunked_saved*) is still
   exported and is used when ``BAYES_SSM_D1_SAVED_HISTORY=1``.
+
+Extension beyond the reference contract: ``fused_diagonal_bayesian`` also
+accepts bfloat16 keys, values and queries (everything else float32).  For
+D = 4, M = 8 they are read as bfloat16 by the kernels (no float32 copies in
+HBM) and their gradients are written as bfloat16; results equal those of the
+float32 path on the widened values, whose gradients autograd would round to
+bfloat16 the same way.  Other shapes widen first and take the float32 path.
 """
 from __future__ import annotations
 
@@ -368,6 +375,77 @@ class _ChunkedBayesianFunction(torch.autograd.Function):
         return (*gradients, None, None, None)
 
 
+class _ChunkedBayesianBF16Function(torch.autograd.Function):
+    """bfloat16 keys/values/queries read as such by the D4M8 kernels (C ABI ``bssm_*_chunked_bf16``).
+
+    Outputs are float32; the gradients of keys, values and queries are
+    bfloat16 (the float32 gradient rounded to nearest even), the others
+    float32.  Gradients are computed only for inputs that require them.
+    """
+
+    @staticmethod
+    def forward(ctx, keys, values, queries, decay, process, observation, initial_mean, initial_covariance,
+                denominator_floor, fixed_dynamics):
+        n, t, d = keys.shape
+        m = values.shape[-1]
+        interval = _hip.preferred_checkpoint(d)
+        nb = -(-t // interval)
+        dev = keys.device
+        out = torch.empty(n, t, m, device=dev, dtype=torch.float32)
+        mean_t = torch.empty(n, d, m, device=dev, dtype=torch.float32)
+        cov_t = torch.empty(n, d, d, device=dev, dtype=torch.float32)
+        bmean = torch.empty(n, nb + 1, d, m, device=dev, dtype=torch.float32)
+        bcov = torch.empty(n, nb + 1, d, d, device=dev, dtype=torch.float32)
+        P = _hip.ptr
+        with torch.cuda.device(dev):
+            _hip.call("bssm_forward_chunked_bf16", d, m, int(bool(fixed_dynamics)), P(keys), P(values), P(queries),
+                      P(decay), P(process), P(observation), P(initial_mean), P(initial_covariance), P(out),
+                      P(mean_t), P(cov_t), P(bmean), P(bcov), n, t, interval, float(denominator_floor),
+                      _hip.stream_of(dev))
+        ctx.save_for_backward(keys, values, queries, decay, process, observation, initial_mean, initial_covariance,
+                              bmean, bcov)
+        ctx.interval = interval
+        ctx.denominator_floor = float(denominator_floor)
+        ctx.fixed_dynamics = bool(fixed_dynamics)
+        ctx.set_materialize_grads(False)
+        return out, mean_t, cov_t
+
+    @staticmethod
+    def backward(ctx, grad_output, grad_mean, grad_covariance):
+        keys, values, queries, decay, process, observation, mean0, cov0, bmean, bcov = ctx.saved_tensors
+        n, t, d = keys.shape
+        m = values.shape[-1]
+        need = ctx.needs_input_grad
+        if grad_output is None:
+            grad_output = torch.zeros(n, t, m, device=keys.device, dtype=torch.float32)
+        else:
+            grad_output = grad_output.contiguous()
+        gm = None if grad_mean is None else grad_mean.contiguous()
+        gc = None if grad_covariance is None else grad_covariance.contiguous()
+        gk, gv, gq = torch.empty_like(keys), torch.empty_like(values), torch.empty_like(queries)
+        dyn = any(need[3:6])
+        gd = torch.empty_like(decay) if dyn else None
+        gp = torch.empty_like(process) if dyn else None
+        gr = torch.empty_like(observation) if dyn else None
+        gm0 = torch.empty_like(mean0) if need[6] else None
+        gc0 = torch.empty_like(cov0) if need[7] else None
+        P = _hip.ptr
+        with torch.cuda.device(keys.device):
+            _hip.call("bssm_backward_chunked_bf16", d, m, int(ctx.fixed_dynamics), P(keys), P(values), P(queries),
+                      P(decay), P(process), P(observation), P(mean0), P(cov0), P(bmean), P(bcov), P(grad_output),
+                      P(gm), P(gc), P(gk), P(gv), P(gq), P(gd), P(gp), P(gr), P(gm0), P(gc0), n, t, ctx.interval,
+                      ctx.denominator_floor, _hip.stream_of(keys.device))
+        return (gk if need[0] else None, gv if need[1] else None, gq if need[2] else None,
+                gd if need[3] else None, gp if need[4] else None, gr if need[5] else None, gm0, gc0, None, None)
+
+
+def _bf16_kernels_apply(keys: Tensor, values: Tensor, queries: Tensor) -> bool:
+    """The D4M8 kernels read these bfloat16 streams directly (else: widen, float32 path)."""
+    n, t, d = keys.shape
+    return ((d, values.shape[-1]) == (4, 8) and t > 0 and t % 4 == 0 and _hip.preferred_checkpoint(d) > 0
+            and all(x.data_ptr() % 16 == 0 for x in (keys, values, queries)))
+
+
 def fused_diagonal_bayesian(
     keys: Tensor,
     values: Tensor,
@@ -387,7 +465,10 @@ def fused_diagonal_bayesian(
     Contract (fused_cuda.py:346-371): CUDA device, 3-D fp32 tensors,
     (D, M) in {(1,8), (2,8), (4,8), (8,8)}, decay [N,T,D], process and
     observation [N,T], initial mean [N,D,M] and covariance [N,D,D].
+    Keys, values and queries may instead all be bfloat16 (see the module
+    docstring).
     """
+    bf16 = all(x.dtype == torch.bfloat16 for x in (keys, values, queries))
     if (
         keys.device.type != "cuda"
         or keys.ndim != 3
@@ -397,8 +478,9 @@ def fused_diagonal_bayesian(
         or queries.shape[-1] != keys.shape[-1]
         or keys.shape != queries.shape
         or values.shape[:2] != keys.shape[:2]
-        or not all(x.dtype == torch.float32 for x in (keys, values, queries, decay, process, observation,
-                                                      initial_mean, initial_covariance))
+        or not all(x.dtype == torch.float32 for x in (decay, process, observation, initial_mean,
+                                                      initial_covariance))
+        or not (bf16 or all(x.dtype == torch.float32 for x in (keys, values, queries)))
     ):
         return None
     key_dim = keys.shape[-1]
@@ -419,6 +501,12 @@ def fused_diagonal_bayesian(
     observation = observation.contiguous()
     initial_mean = initial_mean.contiguous()
     initial_covariance = initial_covariance.contiguous()
+    if bf16:
+        if _bf16_kernels_apply(keys, values, queries):
+            return _ChunkedBayesianBF16Function.apply(
+                keys, values, queries, decay, process, observation, initial_mean, initial_covariance,
+                float(denominator_floor), bool(fixed_dynamics))
+        keys, values, queries = keys.float(), values.float(), queries.float()
     return _ChunkedBayesianFunction.apply(
         keys, values, queries, decay, process, observation, initial_mean, initial_covariance,
         int(chunk_length), float(denominator_floor), bool(fixed_dynamics),

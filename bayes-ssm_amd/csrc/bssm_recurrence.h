@@ -27,6 +27,7 @@ struct FwdArgs {
   float floor;
   int vec_kqd, vec_v, vec_pr;  // 16-byte staging allowed per stream class
   int rot4;                    // D = 4 rotated-layout kernels allowed (see bssm_rot4.hip)
+  int bf16;                    // k, q, v hold bfloat16 (rotated-layout kernels only)
 };
 
 struct BwdArgs {
@@ -58,6 +59,7 @@ struct BwdArgs {
   float floor;
   int vec_kqd, vec_v, vec_pr;
   int rot4;  // D = 4 rotated-layout kernels allowed (see bssm_rot4.hip)
+  int bf16;  // k, q, v and gk, gq, gv hold bfloat16 (rotated-layout kernels only)
 };
 
 // Replay-history tensors of the saved-history ABI.

@@ -100,6 +100,13 @@ __device__ __forceinline__ void vm_wait() {
   asm volatile("" : : : "memory");
 }
 
+// Wait until every LDS operation of the wave has completed.
+__device__ __forceinline__ void lds_wait() {
+  asm volatile("" : : : "memory");
+  __builtin_amdgcn_s_waitcnt((15) | (3 << 14) | (7 << 4) | (0 << 8));
+  asm volatile("" : : : "memory");
+}
+
 // The raw buffer builtins move untyped 32-bit words; floats are bit-cast.
 typedef uint32_t v2u __attribute__((ext_vector_type(2)));
 typedef uint32_t v4u __attribute__((ext_vector_type(4)));
@@ -294,6 +301,7 @@ struct RevTok {
 struct RevOut {
   float gk, gq, gd, gp, gr;
   float gv[2];
+  float gu;  // dL/du_g of the token
 };
 
 // Reverse of one token.  Carried adjoints (rotated like the belief):
@@ -305,12 +313,9 @@ struct RevOut {
 //   dL/dk = -d*(M_prev ge) + gs u + P' gu,   dL/dq = d*(M_prev gy) + beta u (e.gy)
 //   H = S + sym(gu k^T),  dL/dd_i = 2 sum_j H_ij d_j P_ij + sum_c (gM - k ge^T)_ic M_prev_ic
 //   dL/dp = trace(H),  S_prev = H * d d^T,  gM_prev = (gM - k ge^T) * d
-// gc0 receives (S + gu k^T) * d d^T (the full asymmetric adjoint of the
-// covariance entering the token, persistent_bayes_chunked_d4m8.cu:320-326);
-// the caller keeps the value of the sequence's first token.
 template <bool DYN>
 __device__ __forceinline__ void reverse_step(const RevTok& in, const Hist& h, float (&gM)[4][2], float (&S)[4],
-                                             float floor, float (&gc0)[4], RevOut& o) {
+                                             float floor, RevOut& o) {
   const float beta = fast_rcp(fmaxf(h.s, floor));
   float ur[4];
   ur[0] = h.ug;
@@ -377,11 +382,30 @@ __device__ __forceinline__ void reverse_step(const RevTok& in, const Hist& h, fl
     const float hs = fmaf(hg, in.kr[m], fmaf(gur[m], hk, S[m]));
     if (DYN) gd = fmaf(hs * in.dr[m], h.Pp[m], gd);
     if (m == 0) o.gp = DYN ? quad_sum(hs) : 0.f;
-    gc0[m] = fmaf(gu, in.kr[m], S[m]) * dd[m];
     S[m] = hs * dd[m];
   }
   o.gd = DYN ? fmaf(2.f, gd, reduce_scatter(Bv)) : 0.f;
   o.gr = DYN ? gs : 0.f;
+  o.gu = gu;
+}
+
+// Adjoint of the initial covariance: the full (asymmetric) derivative with
+// respect to the covariance entering the first token,
+// (S_in + gu k^T) * d d^T (persistent_bayes_chunked_d4m8.cu:320-326),
+// recovered from the carried S_out = (S_in + sym(gu k^T)) * d d^T that the
+// reverse of that token leaves:  S_out + (gu k^T - sym(gu k^T)) * d d^T.
+__device__ __forceinline__ void initial_cov_adjoint(const float (&S)[4], float gu, const float (&kr)[4],
+                                                    const float (&dr)[4], float (&gc0)[4]) {
+  float gur[4];
+  gur[0] = gu;
+  gur[1] = rot<1>(gu);
+  gur[2] = rot<2>(gu);
+  gur[3] = rot<3>(gu);
+#pragma unroll
+  for (int m = 0; m < 4; ++m) {
+    const float asym = 0.5f * fmaf(gu, kr[m], -gur[m] * kr[0]);
+    gc0[m] = fmaf(asym, dr[0] * dr[m], S[m]);
+  }
 }
 
 // ------------------------------------------------------------------ forward
@@ -466,8 +490,88 @@ __device__ __forceinline__ v4f ld128(Rsrc r, uint32_t voff) {
 struct FwdStage {
   v4f k[4], q[4], d[4], v[8], p, r;
 };
+// With bf16 keys, queries and values (H): the bf16 pieces of the maps in
+// HalfMap, widened into the same float32 slots when written to LDS.
+struct FwdStageH {
+  v4f k[2], q[2], d[4], v[4], p, r;
+};
 
-template <bool FIXED>
+__device__ __forceinline__ const float* byte_offset(const float* p, int64_t bytes) {
+  return reinterpret_cast<const float*>(reinterpret_cast<const char*>(p) + bytes);
+}
+
+// bf16 pairs (low half first) to float32, and back with round to nearest even.
+__device__ __forceinline__ v4f widen_lo(v4f piece) {
+  const v4u w = __builtin_bit_cast(v4u, piece);
+  v4f out;
+  out[0] = __builtin_bit_cast(float, w[0] << 16);
+  out[1] = __builtin_bit_cast(float, w[0] & 0xffff0000u);
+  out[2] = __builtin_bit_cast(float, w[1] << 16);
+  out[3] = __builtin_bit_cast(float, w[1] & 0xffff0000u);
+  return out;
+}
+__device__ __forceinline__ v4f widen_hi(v4f piece) {
+  const v4u w = __builtin_bit_cast(v4u, piece);
+  v4f out;
+  out[0] = __builtin_bit_cast(float, w[2] << 16);
+  out[1] = __builtin_bit_cast(float, w[2] & 0xffff0000u);
+  out[2] = __builtin_bit_cast(float, w[3] << 16);
+  out[3] = __builtin_bit_cast(float, w[3] & 0xffff0000u);
+  return out;
+}
+typedef __bf16 bf2 __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ uint32_t narrow2(float x, float y) {
+  bf2 v;
+  v[0] = static_cast<__bf16>(x);
+  v[1] = static_cast<__bf16>(y);
+  return __builtin_bit_cast(uint32_t, v);
+}
+__device__ __forceinline__ v4f narrow(v4f lo, v4f hi) {
+  v4u w;
+  w[0] = narrow2(lo[0], lo[1]);
+  w[1] = narrow2(lo[2], lo[3]);
+  w[2] = narrow2(hi[0], hi[1]);
+  w[3] = narrow2(hi[2], hi[3]);
+  return __builtin_bit_cast(v4f, w);
+}
+
+// Per-lane maps of the bf16 streams of a 16-token tile (16-byte pieces):
+//   k, q: row 8I + (l & 7), tokens t0 + 2 (l >> 3) and + 1 (I < 2)
+//   v:    row 4I + (l & 3), token t0 + (l >> 2) (I < 4)
+// with their global byte offsets and the LDS float offsets (relative to the
+// K or Q region, and to the V region, of an 8-token slot of slot_floats) of
+// the two widened float32 pieces each becomes, in the float32 slot layout.
+struct HalfMap {
+  int k_lds[2][2], v_lds[4][2];
+  uint32_t k_off[2], v_off[4];
+  int k_tok, v_tok;  // first token of the lane's piece within the tile
+  __device__ __forceinline__ HalfMap(int lane, int slot_floats, uint32_t row4h, uint32_t row8h) {
+    const int pc = lane >> 3, a8 = lane & 7;
+    k_tok = 2 * pc;
+#pragma unroll
+    for (int I = 0; I < 2; ++I) {
+      k_off[I] = static_cast<uint32_t>(8 * I + a8) * row4h + static_cast<uint32_t>(pc) * 16u;
+#pragma unroll
+      for (int e = 0; e < 2; ++e) {
+        const int tok = k_tok + e, tt = tok & 7;
+        k_lds[I][e] = (tok >> 3) * slot_floats + 4 * (64 * I + 8 * (tt ^ I) + a8);
+      }
+    }
+    const int tv = lane >> 2, a4 = lane & 3;
+    v_tok = tv;
+#pragma unroll
+    for (int I = 0; I < 4; ++I) {
+      v_off[I] = static_cast<uint32_t>(4 * I + a4) * row8h + static_cast<uint32_t>(tv) * 16u;
+#pragma unroll
+      for (int e = 0; e < 2; ++e) {
+        const int c = 2 * (tv & 7) + e;
+        v_lds[I][e] = (tv >> 3) * slot_floats + 4 * (64 * I + 4 * (c ^ (2 * I)) + a4);
+      }
+    }
+  }
+};
+
+template <bool FIXED, bool H>
 __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(1, 1))) void forward_kernel(FwdArgs a) {
   __shared__ float tile[2 * FwdTile::SIZE];
   __shared__ float ckst[kRecFloats];  // checkpoint staging
@@ -478,13 +582,15 @@ __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(1, 1))) v
   const uint32_t valid = static_cast<uint32_t>((a.n - n0) < SPW ? (a.n - n0) : SPW);
   const uint32_t row4 = static_cast<uint32_t>(T) * 16u, row8 = static_cast<uint32_t>(T) * 32u,
                  row1 = static_cast<uint32_t>(T) * 4u;
-  const Rsrc rk = make_rsrc(a.k + n0 * T * 4, valid * row4);
-  const Rsrc rq = make_rsrc(a.q + n0 * T * 4, valid * row4);
-  const Rsrc rv = make_rsrc(a.v + n0 * T * 8, valid * row8);
+  // Keys, queries and values are bf16 (half the row bytes) when H.
+  const uint32_t kb = H ? 2u : 1u;
+  const Rsrc rk = make_rsrc(byte_offset(a.k, n0 * T * 16 / kb), valid * row4 / kb);
+  const Rsrc rq = make_rsrc(byte_offset(a.q, n0 * T * 16 / kb), valid * row4 / kb);
+  const Rsrc rv = make_rsrc(byte_offset(a.v, n0 * T * 32 / kb), valid * row8 / kb);
   const Rsrc ry = make_rsrc(a.y + n0 * T * 8, valid * row8);
-  const Rsrc rd = make_rsrc(FIXED ? a.k : a.d + n0 * T * 4, valid * row4);
-  const Rsrc rp = make_rsrc(FIXED ? a.k : a.p + n0 * T, valid * row1);
-  const Rsrc rr = make_rsrc(FIXED ? a.k : a.r + n0 * T, valid * row1);
+  const Rsrc rd = make_rsrc(FIXED ? a.y : a.d + n0 * T * 4, valid * row4);
+  const Rsrc rp = make_rsrc(FIXED ? a.y : a.p + n0 * T, valid * row1);
+  const Rsrc rr = make_rsrc(FIXED ? a.y : a.r + n0 * T, valid * row1);
   const uint32_t nbp = static_cast<uint32_t>(a.nb + 1);
   const Rsrc rbm = make_rsrc(a.bm + n0 * nbp * 32, valid * nbp * 128u);
   const Rsrc rbc = make_rsrc(a.bc + n0 * nbp * 16, valid * nbp * 64u);
@@ -494,6 +600,7 @@ __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(1, 1))) v
   const Rsrc rcT = make_rsrc(a.cT + n0 * 16, valid * 64u);
 
   const Map mp(lane, row4, row8, row1);
+  const HalfMap hm(lane, FwdTile::SIZE, row4 / 2, row8 / 2);
   const Idx ix(s, g);
   const uint32_t off1 = static_cast<uint32_t>(lane >> 2) * row1 + static_cast<uint32_t>(lane & 3) * 16u;
   const int dst1 = ((lane & 3) >> 1) * FwdTile::SIZE + 4 * (2 * (lane >> 2) + (lane & 1));
@@ -514,18 +621,33 @@ __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(1, 1))) v
   };
   store_ckpt(0);
 
-  auto load = [&](FwdStage& x, int64_t t0) __attribute__((always_inline)) {
+  using Stage = std::conditional_t<H, FwdStageH, FwdStage>;
+  auto load = [&](Stage& x, int64_t t0) __attribute__((always_inline)) {
+    if constexpr (H) {
+      const uint32_t sk = static_cast<uint32_t>(t0) * 8u, sv = static_cast<uint32_t>(t0) * 16u;
+#pragma unroll
+      for (int I = 0; I < 2; ++I) {
+        x.k[I] = ld128<kNtLoad>(rk, hm.k_off[I] + sk);
+        x.q[I] = ld128<kNtLoad>(rq, hm.k_off[I] + sk);
+      }
+#pragma unroll
+      for (int I = 0; I < 4; ++I) x.v[I] = ld128<kNtLoad>(rv, hm.v_off[I] + sv);
+    }
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
       const uint32_t s4 = static_cast<uint32_t>(t0 + TT * h) * 16u, s8 = static_cast<uint32_t>(t0 + TT * h) * 32u;
 #pragma unroll
       for (int j = 0; j < 2; ++j) {
-        x.k[2 * h + j] = ld128<kNtLoad>(rk, mp.d4[j] + s4);
-        x.q[2 * h + j] = ld128<kNtLoad>(rq, mp.d4[j] + s4);
+        if constexpr (!H) {
+          x.k[2 * h + j] = ld128<kNtLoad>(rk, mp.d4[j] + s4);
+          x.q[2 * h + j] = ld128<kNtLoad>(rq, mp.d4[j] + s4);
+        }
         if constexpr (!FIXED) x.d[2 * h + j] = ld128<kNtLoad>(rd, mp.d4[j] + s4);
       }
+      if constexpr (!H) {
 #pragma unroll
-      for (int j = 0; j < 4; ++j) x.v[4 * h + j] = ld128<kNtLoad>(rv, mp.d8[j] + s8);
+        for (int j = 0; j < 4; ++j) x.v[4 * h + j] = ld128<kNtLoad>(rv, mp.d8[j] + s8);
+      }
     }
     if constexpr (!FIXED) {
       const uint32_t s1 = static_cast<uint32_t>(t0) * 4u;
@@ -533,18 +655,36 @@ __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(1, 1))) v
       x.r = ld128<false>(rr, off1 + s1);
     }
   };
-  auto put = [&](const FwdStage& x) __attribute__((always_inline)) {
+  auto put = [&](const Stage& x) __attribute__((always_inline)) {
+    if constexpr (H) {
+#pragma unroll
+      for (int I = 0; I < 2; ++I) {
+        *reinterpret_cast<v4f*>(&tile[FwdTile::K + hm.k_lds[I][0]]) = widen_lo(x.k[I]);
+        *reinterpret_cast<v4f*>(&tile[FwdTile::K + hm.k_lds[I][1]]) = widen_hi(x.k[I]);
+        *reinterpret_cast<v4f*>(&tile[FwdTile::Q + hm.k_lds[I][0]]) = widen_lo(x.q[I]);
+        *reinterpret_cast<v4f*>(&tile[FwdTile::Q + hm.k_lds[I][1]]) = widen_hi(x.q[I]);
+      }
+#pragma unroll
+      for (int I = 0; I < 4; ++I) {
+        *reinterpret_cast<v4f*>(&tile[FwdTile::V + hm.v_lds[I][0]]) = widen_lo(x.v[I]);
+        *reinterpret_cast<v4f*>(&tile[FwdTile::V + hm.v_lds[I][1]]) = widen_hi(x.v[I]);
+      }
+    }
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
       float* tl = tile + h * FwdTile::SIZE;
 #pragma unroll
       for (int j = 0; j < 2; ++j) {
-        *reinterpret_cast<v4f*>(&(tl + FwdTile::K)[256 * j + 4 * lane]) = x.k[2 * h + j];
-        *reinterpret_cast<v4f*>(&(tl + FwdTile::Q)[256 * j + 4 * lane]) = x.q[2 * h + j];
+        if constexpr (!H) {
+          *reinterpret_cast<v4f*>(&(tl + FwdTile::K)[256 * j + 4 * lane]) = x.k[2 * h + j];
+          *reinterpret_cast<v4f*>(&(tl + FwdTile::Q)[256 * j + 4 * lane]) = x.q[2 * h + j];
+        }
         if constexpr (!FIXED) *reinterpret_cast<v4f*>(&(tl + FwdTile::D)[256 * j + 4 * lane]) = x.d[2 * h + j];
       }
+      if constexpr (!H) {
 #pragma unroll
-      for (int j = 0; j < 4; ++j) *reinterpret_cast<v4f*>(&(tl + FwdTile::V)[256 * j + 4 * lane]) = x.v[4 * h + j];
+        for (int j = 0; j < 4; ++j) *reinterpret_cast<v4f*>(&(tl + FwdTile::V)[256 * j + 4 * lane]) = x.v[4 * h + j];
+      }
     }
     if constexpr (!FIXED) {
       *reinterpret_cast<v4f*>(&(tile + FwdTile::P)[dst1]) = x.p;
@@ -665,7 +805,7 @@ __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(1, 1))) v
   // i - 1 leave LDS first and are stored after that wait, then the loads of
   // tile i + 1 are issued and the two sub-tiles computed.
   const int64_t ntiles = (T + LT - 1) / LT;
-  FwdStage st;
+  Stage st;
   load(st, 0);
   for (int64_t i = 0; i < ntiles; ++i) {
     FwdOut yo;
@@ -700,6 +840,152 @@ struct BwdTile {
                        SIZE = 4096 + kRecFloats;
 };
 
+// Replay and reverse of one checkpoint chunk held in a BwdTile slot, and the
+// adjoints carried across chunks (shared by the backward kernels).
+template <bool FIXED, bool DYN>
+struct BwdCore {
+  Idx ix;
+  int g;
+  float floor;
+  float gM[4][2], S[4];
+  // Token 0 of the chunk reversed last: the sequence's first token once the
+  // whole sequence has been reversed (for the initial-covariance adjoint).
+  float first_gu, first_kr[4], first_dr[4];
+
+  __device__ __forceinline__ BwdCore(int s, int g_, float floor_) : ix(s, g_), g(g_), floor(floor_) {}
+
+  // Carried adjoints from the final-state gradients (null = zero).
+  __device__ __forceinline__ void init(const BwdArgs& a, int64_t n0, uint32_t valid, const BelOff& unit, int s) {
+    const bool has_m = a.gmf != nullptr, has_c = a.gcf != nullptr;
+    const Rsrc rgm = make_rsrc(has_m ? a.gmf + n0 * 32 : a.m0, has_m ? valid * 128u : 0u);
+    const Rsrc rgc = make_rsrc(has_c ? a.gcf + n0 * 16 : a.m0, has_c ? valid * 64u : 0u);
+#pragma unroll
+    for (int m = 0; m < 4; ++m) {
+      const v2f x = ld64(rgm, unit.m[m], 0);
+      gM[m][0] = x[0];
+      gM[m][1] = x[1];
+      // Mirror entry (row (g+m)%4, column g) sits at the transposed offset.
+      const int h = (g + m) & 3;
+      const uint32_t tr = static_cast<uint32_t>(s) * 64u + h * 16 + g * 4;
+      S[m] = 0.5f * (ld32(rgc, unit.c[m], 0) + ld32(rgc, tr, 0));
+    }
+  }
+  // Adjoints of the initial mean and covariance.
+  __device__ __forceinline__ void store_initial(const BwdArgs& a, int64_t n0, uint32_t valid,
+                                                const BelOff& unit) const {
+    if (a.gm0) {
+      const Rsrc rgm0 = make_rsrc(a.gm0 + n0 * 32, valid * 128u);
+#pragma unroll
+      for (int m = 0; m < 4; ++m) {
+        v2f x;
+        x[0] = gM[m][0];
+        x[1] = gM[m][1];
+        st64(rgm0, x, unit.m[m], 0);
+      }
+    }
+    if (a.gc0) {
+      float gc0[4];
+      initial_cov_adjoint(S, first_gu, first_kr, first_dr, gc0);
+      const Rsrc rgc0 = make_rsrc(a.gc0 + n0 * 16, valid * 64u);
+#pragma unroll
+      for (int m = 0; m < 4; ++m) st32(rgc0, gc0[m], unit.c[m], 0);
+    }
+  }
+
+  __device__ __forceinline__ void read_tok(const float* tl, int tt, Tok& in) const {
+#pragma unroll
+    for (int m = 0; m < 4; ++m) {
+      const int e = ix.i4(tt, (g + m) & 3);
+      in.kr[m] = (tl + BwdTile::K)[e];
+      in.dr[m] = FIXED ? kFixedDecay : (tl + BwdTile::D)[e];
+    }
+    const v2f vv = *reinterpret_cast<const v2f*>(&(tl + BwdTile::V)[ix.i8(tt)]);
+    in.v[0] = vv[0];
+    in.v[1] = vv[1];
+    in.p = FIXED ? kFixedProcess : (tl + BwdTile::P)[ix.i1(tt)];
+    in.r = FIXED ? kFixedObservation : (tl + BwdTile::R)[ix.i1(tt)];
+  }
+  __device__ __forceinline__ void read_rev(const float* tl, int tt, RevTok& in) const {
+#pragma unroll
+    for (int m = 0; m < 4; ++m) {
+      const int e = ix.i4(tt, (g + m) & 3);
+      in.kr[m] = (tl + BwdTile::K)[e];
+      in.dr[m] = FIXED ? kFixedDecay : (tl + BwdTile::D)[e];
+      in.qr[m] = (tl + BwdTile::Q)[e];
+    }
+    const v2f gyv = *reinterpret_cast<const v2f*>(&(tl + BwdTile::GY)[ix.i8(tt)]);
+    in.gy[0] = gyv[0];
+    in.gy[1] = gyv[1];
+    in.p = FIXED ? kFixedProcess : (tl + BwdTile::P)[ix.i1(tt)];
+  }
+  __device__ __forceinline__ void replay(Bel& b, const Tok& in, Hist& h) const {
+#pragma unroll
+    for (int m = 0; m < 4; ++m) {
+      h.Pp[m] = b.P[m];
+      h.Mp[m][0] = b.Mv[m][0];
+      h.Mp[m][1] = b.Mv[m][1];
+    }
+    StepOut o;
+    forward_step(b, in, floor, o);
+    h.ug = o.ug;
+    h.s = o.s;
+    h.e[0] = o.e[0];
+    h.e[1] = o.e[1];
+  }
+  __device__ __forceinline__ void reverse(float* tl, int tt, const RevTok& in, const Hist& h) {
+    RevOut o;
+    reverse_step<DYN>(in, h, gM, S, floor, o);
+    if (tt == 0) {
+      first_gu = o.gu;
+#pragma unroll
+      for (int m = 0; m < 4; ++m) {
+        first_kr[m] = in.kr[m];
+        first_dr[m] = in.dr[m];
+      }
+    }
+    const int ow = ix.i4(tt, g);  // own-row word of the token's piece
+    (tl + BwdTile::K)[ow] = o.gk;
+    (tl + BwdTile::Q)[ow] = o.gq;
+    (tl + BwdTile::D)[ow] = o.gd;
+    v2f gv;
+    gv[0] = o.gv[0];
+    gv[1] = o.gv[1];
+    *reinterpret_cast<v2f*>(&(tl + BwdTile::V)[ix.i8(tt)]) = gv;
+    (tl + BwdTile::P)[ix.i1(tt)] = o.gp;
+    (tl + BwdTile::R)[ix.i1(tt)] = o.gr;
+  }
+  // Replay the chunk from its checkpoint, then reverse it; gradients
+  // overwrite the chunk's input tiles.  Tokens are separated by scheduling
+  // barriers, and each token's LDS reads are issued one token ahead (the
+  // reads of the first reverse token during the last replay token), in
+  // program order before the gradient writes that follow them.
+  template <int LEN>
+  __device__ __forceinline__ void process(float* tl, Bel& b) {
+    Hist h[LEN];
+    Tok x[LEN];
+    RevTok rx[LEN];
+    read_tok(tl, 0, x[0]);
+#pragma unroll
+    for (int tt = 0; tt < LEN; ++tt) {
+      if (tt + 1 < LEN) read_tok(tl, tt + 1, x[tt + 1]);
+      else read_rev(tl, LEN - 1, rx[LEN - 1]);
+      replay(b, x[tt], h[tt]);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+#pragma unroll
+    for (int tt = LEN - 1; tt >= 0; --tt) {
+      if (tt > 0) read_rev(tl, tt - 1, rx[tt - 1]);
+      reverse(tl, tt, rx[tt], h[tt]);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  }
+  // A chunk of `len` tokens (SUB, or 4 for the last one of T = 8n + 4).
+  __device__ __forceinline__ void run(float* tl, Bel& b, int len) {
+    if (len == SUB) process<SUB>(tl, b);
+    else process<4>(tl, b);
+  }
+};
+
 template <bool FIXED, bool DYN>
 __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(1, 1))) void backward_kernel(BwdArgs a) {
   __shared__ float ta[BwdTile::SIZE], tb[BwdTile::SIZE];
@@ -728,27 +1014,9 @@ __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(1, 1))) v
   const Rsrc rbc = make_rsrc(a.bc + n0 * nbp * 16, valid * nbp * 64u);
 
   const Map mp(lane, row4, row8, row1);
-  const Idx ix(s, g);
-
-  // Carried adjoints from the final-state gradients (null = zero).
   const BelOff unit(s, g, 128u, 64u);
-  float gM[4][2], S[4], gc0[4];
-  {
-    const bool has_m = a.gmf != nullptr, has_c = a.gcf != nullptr;
-    const Rsrc rgm = make_rsrc(has_m ? a.gmf + n0 * 32 : a.gk, has_m ? valid * 128u : 0u);
-    const Rsrc rgc = make_rsrc(has_c ? a.gcf + n0 * 16 : a.gk, has_c ? valid * 64u : 0u);
-#pragma unroll
-    for (int m = 0; m < 4; ++m) {
-      const v2f x = ld64(rgm, unit.m[m], 0);
-      gM[m][0] = x[0];
-      gM[m][1] = x[1];
-      // Mirror entry (row (g+m)%4, column g) sits at the transposed offset.
-      const int h = (g + m) & 3;
-      const uint32_t tr = static_cast<uint32_t>(s) * 64u + h * 16 + g * 4;
-      S[m] = 0.5f * (ld32(rgc, unit.c[m], 0) + ld32(rgc, tr, 0));
-      gc0[m] = 0.f;
-    }
-  }
+  BwdCore<FIXED, DYN> core(s, g, a.floor);
+  core.init(a, n0, valid, unit, s);
 
   const RecOff ckoff(lane, nbp * 128u, nbp * 64u);
   const int64_t nb = a.nb;
@@ -776,88 +1044,6 @@ __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(1, 1))) v
     dma16<kNtCkpt>(rbm, (tl + BwdTile::CK), ckoff.m0 + cm);
     dma16<kNtCkpt>(rbm, (tl + BwdTile::CK) + 256, ckoff.m1 + cm);
     dma16(rbc, (tl + BwdTile::CK) + 512, ckoff.c + cc);
-  };
-
-  auto read_tok = [&](const float* tl, int tt, Tok& in) __attribute__((always_inline)) {
-#pragma unroll
-    for (int m = 0; m < 4; ++m) {
-      const int e = ix.i4(tt, (g + m) & 3);
-      in.kr[m] = (tl + BwdTile::K)[e];
-      in.dr[m] = FIXED ? kFixedDecay : (tl + BwdTile::D)[e];
-    }
-    const v2f vv = *reinterpret_cast<const v2f*>(&(tl + BwdTile::V)[ix.i8(tt)]);
-    in.v[0] = vv[0];
-    in.v[1] = vv[1];
-    in.p = FIXED ? kFixedProcess : (tl + BwdTile::P)[ix.i1(tt)];
-    in.r = FIXED ? kFixedObservation : (tl + BwdTile::R)[ix.i1(tt)];
-  };
-
-  auto read_rev = [&](const float* tl, int tt, RevTok& in) __attribute__((always_inline)) {
-#pragma unroll
-    for (int m = 0; m < 4; ++m) {
-      const int e = ix.i4(tt, (g + m) & 3);
-      in.kr[m] = (tl + BwdTile::K)[e];
-      in.dr[m] = FIXED ? kFixedDecay : (tl + BwdTile::D)[e];
-      in.qr[m] = (tl + BwdTile::Q)[e];
-    }
-    const v2f gyv = *reinterpret_cast<const v2f*>(&(tl + BwdTile::GY)[ix.i8(tt)]);
-    in.gy[0] = gyv[0];
-    in.gy[1] = gyv[1];
-    in.p = FIXED ? kFixedProcess : (tl + BwdTile::P)[ix.i1(tt)];
-  };
-  auto replay = [&](Bel& b, const Tok& in, Hist& h) __attribute__((always_inline)) {
-#pragma unroll
-    for (int m = 0; m < 4; ++m) {
-      h.Pp[m] = b.P[m];
-      h.Mp[m][0] = b.Mv[m][0];
-      h.Mp[m][1] = b.Mv[m][1];
-    }
-    StepOut o;
-    forward_step(b, in, a.floor, o);
-    h.ug = o.ug;
-    h.s = o.s;
-    h.e[0] = o.e[0];
-    h.e[1] = o.e[1];
-  };
-  auto reverse = [&](float* tl, int tt, const RevTok& in, const Hist& h) __attribute__((always_inline)) {
-    RevOut o;
-    reverse_step<DYN>(in, h, gM, S, a.floor, gc0, o);
-    const int ow = ix.i4(tt, g);  // own-row word of the token's piece
-    (tl + BwdTile::K)[ow] = o.gk;
-    (tl + BwdTile::Q)[ow] = o.gq;
-    (tl + BwdTile::D)[ow] = o.gd;
-    v2f gv;
-    gv[0] = o.gv[0];
-    gv[1] = o.gv[1];
-    *reinterpret_cast<v2f*>(&(tl + BwdTile::V)[ix.i8(tt)]) = gv;
-    (tl + BwdTile::P)[ix.i1(tt)] = o.gp;
-    (tl + BwdTile::R)[ix.i1(tt)] = o.gr;
-  };
-
-  // Replay the chunk from its checkpoint, then reverse it; gradients
-  // overwrite the chunk's input tiles.  Tokens are separated by scheduling
-  // barriers, and each token's LDS reads are issued one token ahead (the
-  // reads of the first reverse token during the last replay token), in
-  // program order before the gradient writes that follow them.
-  auto process = [&](float* tl, Bel& b, auto len_tag) __attribute__((always_inline)) {
-    constexpr int LEN = decltype(len_tag)::value;
-    Hist h[LEN];
-    Tok x[LEN];
-    RevTok rx[LEN];
-    read_tok(tl, 0, x[0]);
-#pragma unroll
-    for (int tt = 0; tt < LEN; ++tt) {
-      if (tt + 1 < LEN) read_tok(tl, tt + 1, x[tt + 1]);
-      else read_rev(tl, LEN - 1, rx[LEN - 1]);
-      replay(b, x[tt], h[tt]);
-      __builtin_amdgcn_sched_barrier(0);
-    }
-#pragma unroll
-    for (int tt = LEN - 1; tt >= 0; --tt) {
-      if (tt > 0) read_rev(tl, tt - 1, rx[tt - 1]);
-      reverse(tl, tt, rx[tt], h[tt]);
-      __builtin_amdgcn_sched_barrier(0);
-    }
   };
 
   auto store_grads = [&](const float* tl, int64_t c, int len) __attribute__((always_inline)) {
@@ -894,8 +1080,7 @@ __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(1, 1))) v
     bel_from_lds(b, cur + BwdTile::CK, s, g);
     if (c + 1 < nb) store_grads(other, c + 1, chunk_len(c + 1));
     if (c > 0) issue(other, c - 1);
-    if (chunk_len(c) == SUB) process(cur, b, std::integral_constant<int, SUB>{});
-    else process(cur, b, std::integral_constant<int, 4>{});
+    core.run(cur, b, chunk_len(c));
   };
 
   if (nb > 0) issue(ta, nb - 1);
@@ -904,22 +1089,221 @@ __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(1, 1))) v
     if (i + 1 < nb) run_chunk(tb, ta, nb - 2 - i);
   }
   if (nb > 0) store_grads((nb - 1) % 2 == 0 ? ta : tb, 0, chunk_len(0));
+  core.store_initial(a, n0, valid, unit);
+}
 
-  if (a.gm0) {
-    const Rsrc rgm0 = make_rsrc(a.gm0 + n0 * 32, valid * 128u);
+// ------------------------------------------------------ bf16-input backward
+// Keys, values and queries arrive as bfloat16 and their gradients leave as
+// bfloat16 (round to nearest even); everything else is float32.  A 16-token
+// tile (chunks 2J, 2J + 1) is staged in registers while the previous tile is
+// replayed and reversed from LDS, as in the forward: the bf16 pieces are
+// widened into the same float32 slot layout the float32 backward uses, and
+// the gradient pieces are narrowed on the way out.  Checkpoint records
+// arrive by LDS-DMA into their chunk's slot once its chunk has read its own.
+//
+// bf16 piece maps (16-byte pieces, 16-token tile starting at t0):
+//   k, q: row 8I + (l & 7), tokens t0 + 2 (l >> 3) and + 1 (I < 2)
+//   v:    row 4I + (l & 3), token t0 + (l >> 2) (I < 4)
+struct BwdStageH {
+  v4f k[2], q[2], v[4], d[4], gy[8], p, r;
+};
+struct BwdOutH {
+  v4f k[2], q[2], v[4], d[4], p, r;
+};
+
+template <bool FIXED, bool DYN>
+__global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(1, 1))) void backward_bf16_kernel(
+    BwdArgs a) {
+  __shared__ float tile[2 * BwdTile::SIZE];
+  const int lane = threadIdx.x;
+  const int g = lane & 3, s = lane >> 2;
+  const int64_t n0 = static_cast<int64_t>(blockIdx.x) * SPW;
+  const int64_t T = a.t;
+  const uint32_t valid = static_cast<uint32_t>((a.n - n0) < SPW ? (a.n - n0) : SPW);
+  const uint32_t row4 = static_cast<uint32_t>(T) * 16u, row8 = static_cast<uint32_t>(T) * 32u,
+                 row1 = static_cast<uint32_t>(T) * 4u;
+  const uint32_t row4h = row4 / 2, row8h = row8 / 2;
+  const Rsrc rk = make_rsrc(byte_offset(a.k, n0 * T * 8), valid * row4h);
+  const Rsrc rq = make_rsrc(byte_offset(a.q, n0 * T * 8), valid * row4h);
+  const Rsrc rv = make_rsrc(byte_offset(a.v, n0 * T * 16), valid * row8h);
+  const Rsrc rgk = make_rsrc(byte_offset(a.gk, n0 * T * 8), valid * row4h);
+  const Rsrc rgq = make_rsrc(byte_offset(a.gq, n0 * T * 8), valid * row4h);
+  const Rsrc rgv = make_rsrc(byte_offset(a.gv, n0 * T * 16), valid * row8h);
+  const Rsrc rgy = make_rsrc(a.gy + n0 * T * 8, valid * row8);
+  const Rsrc rd = make_rsrc(FIXED ? a.gy : a.d + n0 * T * 4, valid * row4);
+  const Rsrc rp = make_rsrc(FIXED ? a.gy : a.p + n0 * T, valid * row1);
+  const Rsrc rr = make_rsrc(FIXED ? a.gy : a.r + n0 * T, valid * row1);
+  const Rsrc rgd = make_rsrc(a.gd ? a.gd + n0 * T * 4 : a.gy, a.gd ? valid * row4 : 0u);
+  const Rsrc rgp = make_rsrc(a.gp ? a.gp + n0 * T : a.gy, a.gp ? valid * row1 : 0u);
+  const Rsrc rgr = make_rsrc(a.gr ? a.gr + n0 * T : a.gy, a.gr ? valid * row1 : 0u);
+  const uint32_t nbp = static_cast<uint32_t>(a.nb + 1);
+  const Rsrc rbm = make_rsrc(a.bm + n0 * nbp * 32, valid * nbp * 128u);
+  const Rsrc rbc = make_rsrc(a.bc + n0 * nbp * 16, valid * nbp * 64u);
+
+  const Map mp(lane, row4, row8, row1);
+  const HalfMap hm(lane, BwdTile::SIZE, row4h, row8h);
+  // p and r: one instruction per 16-token tile, lane -> row lane >> 2, piece
+  // lane & 3 (tokens 4 (lane & 3) .. + 3), into the chunk slot of its tokens.
+  const uint32_t off1 = static_cast<uint32_t>(lane >> 2) * row1 + static_cast<uint32_t>(lane & 3) * 16u;
+  const int dst1 = ((lane & 3) >> 1) * BwdTile::SIZE + 4 * (2 * (lane >> 2) + (lane & 1));
+
+  const BelOff unit(s, g, 128u, 64u);
+  BwdCore<FIXED, DYN> core(s, g, a.floor);
+  core.init(a, n0, valid, unit, s);
+  const RecOff ckoff(lane, nbp * 128u, nbp * 64u);
+  const int64_t nb = a.nb;
+  const int64_t ntiles = (nb + 1) / 2;
+
+  auto load = [&](BwdStageH& x, int64_t J) __attribute__((always_inline)) {
+    const int64_t t0 = J * 2 * SUB;
+    const uint32_t sk = static_cast<uint32_t>(t0) * 8u, sv = static_cast<uint32_t>(t0) * 16u;
 #pragma unroll
-    for (int m = 0; m < 4; ++m) {
-      v2f x;
-      x[0] = gM[m][0];
-      x[1] = gM[m][1];
-      st64(rgm0, x, unit.m[m], 0);
+    for (int I = 0; I < 2; ++I) {
+      x.k[I] = ld128<kNtLoad>(rk, hm.k_off[I] + sk);
+      x.q[I] = ld128<kNtLoad>(rq, hm.k_off[I] + sk);
     }
-  }
-  if (a.gc0) {
-    const Rsrc rgc0 = make_rsrc(a.gc0 + n0 * 16, valid * 64u);
 #pragma unroll
-    for (int m = 0; m < 4; ++m) st32(rgc0, gc0[m], unit.c[m], 0);
+    for (int I = 0; I < 4; ++I) x.v[I] = ld128<kNtLoad>(rv, hm.v_off[I] + sv);
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const uint32_t s4 = static_cast<uint32_t>(t0 + SUB * h) * 16u, s8 = static_cast<uint32_t>(t0 + SUB * h) * 32u;
+      if constexpr (!FIXED) {
+#pragma unroll
+        for (int j = 0; j < 2; ++j) x.d[2 * h + j] = ld128<kNtLoad>(rd, mp.d4[j] + s4);
+      }
+#pragma unroll
+      for (int j = 0; j < 4; ++j) x.gy[4 * h + j] = ld128<kNtLoad>(rgy, mp.d8[j] + s8);
+    }
+    if constexpr (!FIXED) {
+      const uint32_t s1 = static_cast<uint32_t>(t0) * 4u;
+      x.p = ld128<false>(rp, off1 + s1);
+      x.r = ld128<false>(rr, off1 + s1);
+    }
+  };
+  auto put = [&](const BwdStageH& x) __attribute__((always_inline)) {
+#pragma unroll
+    for (int I = 0; I < 2; ++I) {
+      *reinterpret_cast<v4f*>(&tile[BwdTile::K + hm.k_lds[I][0]]) = widen_lo(x.k[I]);
+      *reinterpret_cast<v4f*>(&tile[BwdTile::K + hm.k_lds[I][1]]) = widen_hi(x.k[I]);
+      *reinterpret_cast<v4f*>(&tile[BwdTile::Q + hm.k_lds[I][0]]) = widen_lo(x.q[I]);
+      *reinterpret_cast<v4f*>(&tile[BwdTile::Q + hm.k_lds[I][1]]) = widen_hi(x.q[I]);
+    }
+#pragma unroll
+    for (int I = 0; I < 4; ++I) {
+      *reinterpret_cast<v4f*>(&tile[BwdTile::V + hm.v_lds[I][0]]) = widen_lo(x.v[I]);
+      *reinterpret_cast<v4f*>(&tile[BwdTile::V + hm.v_lds[I][1]]) = widen_hi(x.v[I]);
+    }
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      float* tl = tile + h * BwdTile::SIZE;
+      if constexpr (!FIXED) {
+#pragma unroll
+        for (int j = 0; j < 2; ++j) *reinterpret_cast<v4f*>(&(tl + BwdTile::D)[256 * j + 4 * lane]) = x.d[2 * h + j];
+      }
+#pragma unroll
+      for (int j = 0; j < 4; ++j) *reinterpret_cast<v4f*>(&(tl + BwdTile::GY)[256 * j + 4 * lane]) = x.gy[4 * h + j];
+    }
+    if constexpr (!FIXED) {
+      *reinterpret_cast<v4f*>(&tile[BwdTile::P + dst1]) = x.p;
+      *reinterpret_cast<v4f*>(&tile[BwdTile::R + dst1]) = x.r;
+    }
+  };
+  // Checkpoint record c into the CK region of slot tl, once the LDS reads of
+  // the record that was there have completed.
+  auto issue_ck = [&](float* tl, int64_t c) __attribute__((always_inline)) {
+    lds_wait();
+    const uint32_t cm = static_cast<uint32_t>(c) * 128u, cc = static_cast<uint32_t>(c) * 64u;
+    dma16<kNtCkpt>(rbm, (tl + BwdTile::CK), ckoff.m0 + cm);
+    dma16<kNtCkpt>(rbm, (tl + BwdTile::CK) + 256, ckoff.m1 + cm);
+    dma16(rbc, (tl + BwdTile::CK) + 512, ckoff.c + cc);
+  };
+  auto take = [&](BwdOutH& o) __attribute__((always_inline)) {
+#pragma unroll
+    for (int I = 0; I < 2; ++I) {
+      o.k[I] = narrow(*reinterpret_cast<const v4f*>(&tile[BwdTile::K + hm.k_lds[I][0]]),
+                      *reinterpret_cast<const v4f*>(&tile[BwdTile::K + hm.k_lds[I][1]]));
+      o.q[I] = narrow(*reinterpret_cast<const v4f*>(&tile[BwdTile::Q + hm.k_lds[I][0]]),
+                      *reinterpret_cast<const v4f*>(&tile[BwdTile::Q + hm.k_lds[I][1]]));
+    }
+#pragma unroll
+    for (int I = 0; I < 4; ++I)
+      o.v[I] = narrow(*reinterpret_cast<const v4f*>(&tile[BwdTile::V + hm.v_lds[I][0]]),
+                      *reinterpret_cast<const v4f*>(&tile[BwdTile::V + hm.v_lds[I][1]]));
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+        o.d[2 * h + j] = *reinterpret_cast<const v4f*>(&(tile + h * BwdTile::SIZE + BwdTile::D)[256 * j + 4 * lane]);
+    o.p = *reinterpret_cast<const v4f*>(&tile[BwdTile::P + dst1]);
+    o.r = *reinterpret_cast<const v4f*>(&tile[BwdTile::R + dst1]);
+  };
+  // Gradients of tile J; pieces of tokens at or past T are dropped.
+  auto store_grads = [&](const BwdOutH& o, int64_t J) __attribute__((always_inline)) {
+    const int64_t t0 = J * 2 * SUB;
+    const uint32_t sk = static_cast<uint32_t>(t0) * 8u, sv = static_cast<uint32_t>(t0) * 16u;
+    const bool kin = t0 + hm.k_tok < T, vin = t0 + hm.v_tok < T;
+#pragma unroll
+    for (int I = 0; I < 2; ++I) {
+      st128<kNtStore>(rgk, o.k[I], kin ? hm.k_off[I] : kOob, sk);
+      st128<kNtStore>(rgq, o.q[I], kin ? hm.k_off[I] : kOob, sk);
+    }
+#pragma unroll
+    for (int I = 0; I < 4; ++I) st128<kNtStore>(rgv, o.v[I], vin ? hm.v_off[I] : kOob, sv);
+    if (a.gd) {
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const int64_t th = t0 + SUB * h;
+        const int len = static_cast<int>((T - th) < SUB ? (T - th) : SUB);
+        const uint32_t s4 = static_cast<uint32_t>(th) * 16u;
+#pragma unroll
+        for (int j = 0; j < 2; ++j) st128<kNtStore>(rgd, o.d[2 * h + j], mp.t4[j] < len ? mp.d4[j] : kOob, s4);
+      }
+    }
+    const uint32_t offp = t0 + 4 * (lane & 3) < T ? off1 : kOob, s1 = static_cast<uint32_t>(t0) * 4u;
+    if (a.gp) st128(rgp, o.p, offp, s1);
+    if (a.gr) st128(rgr, o.r, offp, s1);
+  };
+  auto chunk_len = [&](int64_t c) __attribute__((always_inline)) {
+    return static_cast<int>((T - c * SUB) < SUB ? (T - c * SUB) : SUB);
+  };
+  // Chunk c from slot tl; the slot's checkpoint region then receives the
+  // record of chunk c - 2 (the same slot's chunk in the next tile).
+  auto run_chunk = [&](float* tl, int64_t c) __attribute__((always_inline)) {
+    Bel b;
+    bel_from_lds(b, tl + BwdTile::CK, s, g);
+    if (c >= 2) issue_ck(tl, c - 2);
+    core.run(tl, b, chunk_len(c));
+  };
+
+  // Tiles run from the last to the first.  At the start of tile J every
+  // outstanding load was issued during tile J + 1 and is awaited; the
+  // gradients of tile J + 1 are read out of LDS, the tile's staged inputs
+  // written there, those gradients stored, the loads of tile J - 1 issued,
+  // and chunks 2J + 1 and 2J replayed and reversed.
+  BwdStageH st;
+  load(st, ntiles - 1);
+  issue_ck(tile, 2 * (ntiles - 1));
+  if (2 * ntiles - 1 < nb) issue_ck(tile + BwdTile::SIZE, 2 * ntiles - 1);
+  else if (ntiles > 1) issue_ck(tile + BwdTile::SIZE, 2 * ntiles - 3);
+  for (int64_t J = ntiles - 1; J >= 0; --J) {
+    BwdOutH go;
+    vm_wait<0>();
+    if (J + 1 < ntiles) take(go);
+    __builtin_amdgcn_sched_barrier(0);
+    put(st);
+    __builtin_amdgcn_sched_barrier(0);
+    if (J + 1 < ntiles) store_grads(go, J + 1);
+    if (J > 0) load(st, J - 1);
+    __builtin_amdgcn_sched_barrier(0);
+    if (2 * J + 1 < nb) run_chunk(tile + BwdTile::SIZE, 2 * J + 1);
+    run_chunk(tile, 2 * J);
   }
+  {
+    BwdOutH go;
+    take(go);
+    store_grads(go, 0);
+  }
+  core.store_initial(a, n0, valid, unit);
 }
 
 }  // namespace r4
@@ -928,10 +1312,14 @@ __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(1, 1))) v
 hipError_t launch_forward_r4(bool fixed, const FwdArgs& a, hipStream_t stream) {
   const int64_t blocks = (a.n + r4::SPW - 1) / r4::SPW;
   if (blocks == 0) return hipSuccess;
-  if (fixed)
-    hipLaunchKernelGGL(r4::forward_kernel<true>, dim3(static_cast<unsigned>(blocks)), dim3(kWave), 0, stream, a);
-  else
-    hipLaunchKernelGGL(r4::forward_kernel<false>, dim3(static_cast<unsigned>(blocks)), dim3(kWave), 0, stream, a);
+  const dim3 grid(static_cast<unsigned>(blocks)), block(kWave);
+  if (a.bf16) {
+    if (fixed) hipLaunchKernelGGL((r4::forward_kernel<true, true>), grid, block, 0, stream, a);
+    else hipLaunchKernelGGL((r4::forward_kernel<false, true>), grid, block, 0, stream, a);
+  } else {
+    if (fixed) hipLaunchKernelGGL((r4::forward_kernel<true, false>), grid, block, 0, stream, a);
+    else hipLaunchKernelGGL((r4::forward_kernel<false, false>), grid, block, 0, stream, a);
+  }
   return hipGetLastError();
 }
 
@@ -939,9 +1327,15 @@ hipError_t launch_backward_r4(bool fixed, bool dyn, const BwdArgs& a, hipStream_
   const int64_t blocks = (a.n + r4::SPW - 1) / r4::SPW;
   if (blocks == 0) return hipSuccess;
   const dim3 grid(static_cast<unsigned>(blocks)), block(kWave);
-  if (fixed) hipLaunchKernelGGL((r4::backward_kernel<true, false>), grid, block, 0, stream, a);
-  else if (dyn) hipLaunchKernelGGL((r4::backward_kernel<false, true>), grid, block, 0, stream, a);
-  else hipLaunchKernelGGL((r4::backward_kernel<false, false>), grid, block, 0, stream, a);
+  if (a.bf16) {
+    if (fixed) hipLaunchKernelGGL((r4::backward_bf16_kernel<true, false>), grid, block, 0, stream, a);
+    else if (dyn) hipLaunchKernelGGL((r4::backward_bf16_kernel<false, true>), grid, block, 0, stream, a);
+    else hipLaunchKernelGGL((r4::backward_bf16_kernel<false, false>), grid, block, 0, stream, a);
+  } else {
+    if (fixed) hipLaunchKernelGGL((r4::backward_kernel<true, false>), grid, block, 0, stream, a);
+    else if (dyn) hipLaunchKernelGGL((r4::backward_kernel<false, true>), grid, block, 0, stream, a);
+    else hipLaunchKernelGGL((r4::backward_kernel<false, false>), grid, block, 0, stream, a);
+  }
   return hipGetLastError();
 }
 

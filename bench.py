@@ -41,12 +41,14 @@ def algorithmic_bytes(d: int, m: int) -> tuple[int, int]:
     return (inputs + m) * 4, (2 * inputs + m) * 4
 
 
-def make_workload(b, t, h, d, m, device, seed=0):
+def make_workload(b, t, h, d, m, device, seed=0, bf16_kqv=False):
+    """Synthetic config-3 inputs; k, v, q are bf16 values (kept as bfloat16 tensors when bf16_kqv)."""
     n = b * h
     g = torch.Generator(device=device).manual_seed(seed)
-    k = torch.randn(n, t, d, device=device, generator=g).bfloat16().float()
-    v = torch.randn(n, t, m, device=device, generator=g).bfloat16().float()
-    q = torch.randn(n, t, d, device=device, generator=g).bfloat16().float()
+    cast = (lambda x: x.bfloat16()) if bf16_kqv else (lambda x: x.bfloat16().float())
+    k = cast(torch.randn(n, t, d, device=device, generator=g))
+    v = cast(torch.randn(n, t, m, device=device, generator=g))
+    q = cast(torch.randn(n, t, d, device=device, generator=g))
     dec = torch.sigmoid(torch.randn(n, t, d, device=device, generator=g) + 2.0)
     p = torch.nn.functional.softplus(torch.randn(n, t, device=device, generator=g) - 3.0)
     r = 1e-4 + torch.nn.functional.softplus(torch.randn(n, t, device=device, generator=g))
@@ -67,11 +69,16 @@ def cpu_model() -> str:
     return "unknown CPU"
 
 
-def time_layer(b, t, h, d, m, chunk, steps, warmup, device) -> dict:
-    """fwd+bwd of fused_diagonal_bayesian at one shape: ms/step, tokens/s, step roofline fraction."""
+def time_layer(b, t, h, d, m, chunk, steps, warmup, device, bf16_kqv=False) -> dict:
+    """fwd+bwd of fused_diagonal_bayesian at one shape: ms/step, tokens/s, step roofline fraction.
+
+    With bf16_kqv the keys, values and queries are bfloat16 tensors (read as
+    such by the kernels; their gradients are bfloat16) and the roofline bytes
+    count the dtypes actually streamed.
+    """
     from bayes_ssm import fused_cuda
 
-    leaves, m0, c0, gy = make_workload(b, t, h, d, m, device, seed=1)
+    leaves, m0, c0, gy = make_workload(b, t, h, d, m, device, seed=1, bf16_kqv=bf16_kqv)
 
     def step():
         y, _, _ = fused_cuda.fused_diagonal_bayesian(*leaves, m0, c0, chunk_length=chunk, denominator_floor=1e-6)
@@ -88,8 +95,16 @@ def time_layer(b, t, h, d, m, chunk, steps, warmup, device) -> dict:
     torch.cuda.synchronize()
     ms = e0.elapsed_time(e1) / steps
     fwd_b, bwd_b = algorithmic_bytes(d, m)
-    return {"B": b, "T": t, "H": h, "D": d, "M": m, "ms_per_step": ms, "tokens_per_s": b * t / (ms * 1e-3),
-            "roofline_step_frac": (fwd_b + bwd_b) * b * h * t / (ms * 1e-3) / HBM_PEAK}
+    if bf16_kqv:
+        # k, q, v (2D + M values) read at 2 bytes in both passes and their
+        # gradients written at 2 bytes: 3 (2D + M) x 2 bytes fewer.
+        fwd_b -= (2 * d + m) * 2
+        bwd_b -= (2 * d + m) * 4
+    out = {"B": b, "T": t, "H": h, "D": d, "M": m, "ms_per_step": ms, "tokens_per_s": b * t / (ms * 1e-3),
+           "roofline_step_frac": (fwd_b + bwd_b) * b * h * t / (ms * 1e-3) / HBM_PEAK}
+    if bf16_kqv:
+        out["bytes_per_token_head"] = fwd_b + bwd_b
+    return out
 
 
 def time_scan(b, t, d, m, iters, device) -> dict:
@@ -308,7 +323,8 @@ def main() -> int:
         # Secondary shapes (not the metric): config 3 divided by 8 (one GPU's
         # share under 8-way data parallelism), the D2M8 / D8M8 variants of
         # config 3, config 2 (D1M8, B64), and the associative-scan configs.
-        extras = {"dp8_share_d4m8": time_layer(b // 8, t, h, d, m, args.chunk, 30, 10, device)}
+        extras = {"config3_bf16_kqv": time_layer(b, t, h, d, m, args.chunk, 30, 10, device, bf16_kqv=True),
+                  "dp8_share_d4m8": time_layer(b // 8, t, h, d, m, args.chunk, 30, 10, device)}
         for name, (eb, ed) in {"config3_d2m8": (b, 2), "config3_d8m8": (b, 8), "config2_d1m8": (64, 1)}.items():
             extras[name] = time_layer(eb, t, h, ed, m, args.chunk, 10, 3, device)
         extras["assoc_scan_config0"] = time_scan(1, 16, 4, 4, 50, device)

@@ -213,6 +213,44 @@ int bssm_backward_chunked_saved_lean(int key_dim, int value_dim,
                                      void* stream);
 
 /* ------------------------------------------------------------------------
+ * bfloat16 keys, values and queries.
+ * No reference counterpart: the reference promotes bfloat16 projections to
+ * float32 before its extension (bayes_ssm/bayesian_layer.py:823-827); these
+ * entry points read them as bfloat16 and widen them on chip, with results
+ * identical to the float32 entry points on the widened values.  D = 4, M = 8
+ * only, T a positive multiple of 4, 16-byte aligned streams; anything else
+ * returns BSSM_ERR_UNSUPPORTED (the caller widens and uses the float32 ABI).
+ */
+
+/* Forward: as bssm_forward_chunked (fixed == 0) or
+ * bssm_forward_chunked_fixed (fixed != 0); keys, values, queries are
+ * bfloat16 [N,T,D] / [N,T,M] / [N,T,D]; out and all other tensors float32. */
+int bssm_forward_chunked_bf16(int key_dim, int value_dim, int fixed,
+                              const void* keys, const void* values, const void* queries,
+                              const float* decay, const float* process, const float* observation,
+                              const float* mean0, const float* cov0,
+                              float* out, float* mean_final, float* cov_final,
+                              float* bmean, float* bcov,
+                              int64_t n, int64_t t, int64_t chunk, float denominator_floor,
+                              void* stream);
+
+/* Reverse: gk, gv, gq are bfloat16, each the float32 gradient rounded to
+ * nearest even (the gradient of a bfloat16 -> float32 widening).  gd, gp,
+ * gr (float32) are given together or all NULL (then not computed; with
+ * fixed != 0 they are written as zeros when given); gm0, gc0 may be NULL.
+ * chunk must equal bssm_preferred_checkpoint(4). */
+int bssm_backward_chunked_bf16(int key_dim, int value_dim, int fixed,
+                               const void* keys, const void* values, const void* queries,
+                               const float* decay, const float* process, const float* observation,
+                               const float* mean0, const float* cov0,
+                               const float* bmean, const float* bcov,
+                               const float* gy, const float* gmf, const float* gcf,
+                               void* gk, void* gv, void* gq, float* gd, float* gp, float* gr,
+                               float* gm0, float* gc0,
+                               int64_t n, int64_t t, int64_t chunk, float denominator_floor,
+                               void* stream);
+
+/* ------------------------------------------------------------------------
  * Static (A = I, Q = 0) associative scan in information form.
  * Replaces the torch-op chain of `associative_static_bayesian`
  * (bayes_ssm/replay_ssm.py:251-270):

@@ -400,3 +400,106 @@ def test_edge_sizes(ext_for, cuda_device):
         if n and t:
             ey, em, ec = _oracle_forward(cpu, False)
             close(y, ey, "y")
+
+
+def _bf16_case(n, t, seed, device):
+    cpu, dev = _case(n, t, 4, seed=seed, device=device)
+    for name in ("k", "v", "q"):
+        dev[name + "h"] = dev[name].bfloat16().contiguous()
+        dev[name] = dev[name + "h"].float().contiguous()
+    return cpu, dev
+
+
+@pytest.mark.parametrize("t", [4, 8, 12, 16, 20, 52, 64])
+@pytest.mark.parametrize("fixed", [False, True])
+def test_bf16_abi_matches_float32_kernels(cuda_device, t, fixed):
+    """bf16 k/v/q C ABI: outputs bit-identical to the float32 kernels on the widened values;
+    gk/gv/gq are the float32 gradients rounded to bfloat16, the other gradients bit-identical."""
+    from bayes_ssm import _hip, fused_cuda
+
+    print(f"bf16 abi t={t} fixed={fixed}", flush=True)
+    n = 37
+    _, dev = _bf16_case(n, t, seed=500 + t, device=cuda_device)
+    ext = fused_cuda._load_extension(4)
+    chunk = _hip.preferred_checkpoint(4)
+    nb = -(-t // chunk)
+    P = _hip.ptr
+    fwd = ext.forward_chunked_fixed if fixed else ext.forward_chunked
+    bwd = ext.backward_chunked_fixed if fixed else ext.backward_chunked
+    args = [dev[x] for x in ("k", "v", "q", "d", "p", "r", "m0", "c0")]
+    y, mT, cT, bm, bc = fwd(*args, chunk, 1e-6)
+    ref = bwd(*args, bm, bc, dev["gy"], dev["gmf"], dev["gcf"], chunk, 1e-6)
+
+    yh, mh, ch = torch.empty_like(y), torch.empty_like(mT), torch.empty_like(cT)
+    bmh, bch = torch.empty_like(bm), torch.empty_like(bc)
+    assert bmh.shape[1] == nb + 1
+    stream = _hip.stream_of(cuda_device)
+    _hip.call("bssm_forward_chunked_bf16", 4, 8, int(fixed), P(dev["kh"]), P(dev["vh"]), P(dev["qh"]),
+              P(dev["d"]), P(dev["p"]), P(dev["r"]), P(dev["m0"]), P(dev["c0"]), P(yh), P(mh), P(ch), P(bmh),
+              P(bch), n, t, chunk, 1e-6, stream)
+    gk, gv, gq = (torch.empty_like(dev[x]) for x in ("kh", "vh", "qh"))
+    gd, gp, gr = torch.empty_like(dev["d"]), torch.empty_like(dev["p"]), torch.empty_like(dev["r"])
+    gm0, gc0 = torch.empty_like(dev["m0"]), torch.empty_like(dev["c0"])
+    _hip.call("bssm_backward_chunked_bf16", 4, 8, int(fixed), P(dev["kh"]), P(dev["vh"]), P(dev["qh"]),
+              P(dev["d"]), P(dev["p"]), P(dev["r"]), P(dev["m0"]), P(dev["c0"]), P(bmh), P(bch), P(dev["gy"]),
+              P(dev["gmf"]), P(dev["gcf"]), P(gk), P(gv), P(gq), P(gd), P(gp), P(gr), P(gm0), P(gc0), n, t, chunk,
+              1e-6, stream)
+    torch.cuda.synchronize()
+    for name, a, b in (("y", yh, y), ("mean_T", mh, mT), ("cov_T", ch, cT), ("bmean", bmh, bm), ("bcov", bch, bc)):
+        assert torch.equal(a, b), f"{name} differs from the float32 kernels"
+    for name, a, b in (("gk", gk, ref[0]), ("gv", gv, ref[1]), ("gq", gq, ref[2])):
+        assert a.dtype == torch.bfloat16
+        assert torch.equal(a, b.bfloat16()), f"{name} is not the float32 gradient rounded to bfloat16"
+    for name, a, b in (("gd", gd, ref[3]), ("gp", gp, ref[4]), ("gr", gr, ref[5]), ("gm0", gm0, ref[6]),
+                       ("gc0", gc0, ref[7])):
+        assert torch.equal(a, b), f"{name} differs from the float32 kernels"
+
+
+@pytest.mark.parametrize("t", [64, 45])
+@pytest.mark.parametrize("leaves", ["all", "kqv"])
+def test_bf16_autograd_boundary(cuda_device, t, leaves):
+    """fused_diagonal_bayesian with bf16 k/v/q leaves equals the float32 path on the widened values
+    (T = 45 is not a multiple of 4: the bf16 inputs are widened and take the float32 kernels)."""
+    from bayes_ssm.fused_cuda import fused_diagonal_bayesian
+
+    print(f"bf16 autograd t={t} leaves={leaves}", flush=True)
+    n = 24
+    _, dev = _bf16_case(n, t, seed=700 + t, device=cuda_device)
+    names = ("k", "v", "q", "d", "p", "r") if leaves == "all" else ("k", "v", "q")
+    lh = {x: (dev[x + "h"] if x in "kvq" else dev[x]).clone().requires_grad_(x in names) for x in "kvqdpr"}
+    lf = {x: dev[x].clone().requires_grad_(x in names) for x in "kvqdpr"}
+    outs = []
+    for lv in (lh, lf):
+        y, mT, cT = fused_diagonal_bayesian(lv["k"], lv["v"], lv["q"], lv["d"], lv["p"], lv["r"], dev["m0"],
+                                            dev["c0"], chunk_length=64, denominator_floor=1e-6)
+        torch.autograd.backward([y, mT], [dev["gy"], dev["gmf"]])
+        outs.append((y, mT, cT))
+    for a, b in zip(outs[0], outs[1]):
+        assert torch.equal(a, b)
+    for x in names:
+        expected = lf[x].grad.bfloat16() if x in "kvq" else lf[x].grad
+        assert lh[x].grad.dtype == expected.dtype
+        assert torch.equal(lh[x].grad, expected), f"grad {x}"
+
+
+def test_bf16_bayesian_layer_routes_to_bf16_kernels(cuda_device, monkeypatch):
+    """bayesian_layer passes bf16 keys/values/queries to the bf16 kernels (no float32 copies on that path)."""
+    import bayes_ssm
+    from bayes_ssm import fused_cuda
+
+    calls = []
+    orig = fused_cuda._ChunkedBayesianBF16Function.apply
+    monkeypatch.setattr(fused_cuda._ChunkedBayesianBF16Function, "apply",
+                        staticmethod(lambda *a: calls.append(1) or orig(*a)))
+    n, t = 16, 32
+    cpu, dev = _bf16_case(n, t, seed=9, device=cuda_device)
+    y, mT, cT = bayes_ssm.bayesian_layer(dev["kh"], dev["vh"], dev["qh"], transition_diagonals=dev["d"],
+                                         process_variances=dev["p"], observation_variances=dev["r"],
+                                         chunk_length=16, optimized=True)
+    assert calls, "bf16 kernels were not used"
+    ry, rm, rc = bayes_ssm.bayesian_layer(dev["k"].cpu(), dev["v"].cpu(), dev["q"].cpu(),
+                                          transition_diagonals=cpu["d"], process_variances=cpu["p"],
+                                          observation_variances=cpu["r"], chunk_length=16, optimized=False)
+    close(y, ry, "y vs reference fp32 path")
+    close(mT, rm, "mean")
+    close(cT, rc, "cov")
