@@ -1,0 +1,231 @@
+"""Producer-fused layer core of the Bayes mixer (key dim 4, value dim 8, learned dynamics).
+
+The reference mixer (example/train_6layer.py:613-709) turns its bfloat16
+projections into the inputs of the exact layer with a chain of torch ops::
+
+    q = normalize(silu(q_proj.float()).view(b, t, H, 4))        # :627-639
+    k = normalize(silu(k_proj.float()).view(b, t, H, 4))
+    v = silu(v_proj.float()).view(b, t, H, 8)
+    process, observation = softplus(noise.view(b, t, H, 2)) + 1e-4   # :664-668
+    decay = exp(-softplus(decay_logits))                             # :690
+    (each permuted to [b * H, t, .])                                 # :648-658, :669-670, :691-693
+    read, _, _ = bayesian_layer(k, v, q, ...)                        # :709
+    read = read.view(b, H, t, 8).permute(0, 2, 1, 3)                 # :710
+
+which materialises every transformed and permuted tensor in float32 before
+the recurrence reads them once.  ``bayes_mixer_core`` returns the same
+``read`` ([b, t, H, 8], float32) from one forward and one backward kernel that
+read the bfloat16 projections in place (each may be a column view of one
+fused projection output) and apply the transforms, and their chain rule, on
+chip (C ABI ``bssm_mixer_forward`` / ``bssm_mixer_backward``).  Projection
+gradients come back as bfloat16, the float32 gradient rounded to nearest even,
+which is what autograd through the reference's ``.float()`` widening yields.
+
+Shapes the kernels do not take (heads not a multiple of 16, T not a multiple
+of 4, other dtypes or devices, strided rows the kernels cannot address) run the
+reference's op chain through ``bayesian_layer`` instead.
+"""
+from __future__ import annotations
+
+from typing import Optional
+
+import torch
+import torch.nn.functional as F
+from torch import Tensor
+
+from . import _hip
+from .bayesian_layer import bayesian_layer
+
+KEY_DIM = 4
+VALUE_DIM = 8
+NOISE_FLOOR = 1e-4  # softplus(noise) + 1e-4 (train_6layer.py:667-668)
+
+# Per-head widths of the five projections: q, k, v, decay logits, noise.
+_WIDTHS = (KEY_DIM, KEY_DIM, VALUE_DIM, KEY_DIM, 2)
+
+
+def _row_stride(x: Tensor, t: int) -> Optional[int]:
+    """Row stride (elements) of a [B, T, W] view the kernels can address, else None."""
+    if x.ndim != 3 or x.stride(2) != 1:
+        return None
+    ld = x.stride(1)
+    if ld % 8 != 0 or x.data_ptr() % 16 != 0:
+        return None
+    if x.shape[0] > 1 and x.stride(0) != t * ld:
+        return None
+    return ld
+
+
+def _fused_eligible(projections: tuple[Tensor, ...], heads: int) -> Optional[tuple[int, ...]]:
+    q = projections[0]
+    if q.device.type != "cuda" or q.ndim != 3:
+        return None
+    b, t, _ = q.shape
+    if heads % 16 != 0 or t <= 0 or t % 4 != 0:
+        return None
+    lds = []
+    for x, w in zip(projections, _WIDTHS):
+        if x.dtype != torch.bfloat16 or x.device != q.device or tuple(x.shape) != (b, t, w * heads):
+            return None
+        ld = _row_stride(x, t)
+        if ld is None:
+            return None
+        lds.append(ld)
+    return tuple(lds)
+
+
+class _MixerCoreFunction(torch.autograd.Function):
+    """Autograd boundary of the producer-fused kernels (C ABI ``bssm_mixer_*``)."""
+
+    @staticmethod
+    def forward(ctx, q_proj, k_proj, v_proj, decay_logits, noise, initial_mean, initial_covariance, heads,
+                denominator_floor, lds):
+        b, t, _ = q_proj.shape
+        n = b * heads
+        interval = _hip.preferred_checkpoint(KEY_DIM)
+        nb = -(-t // interval)
+        dev = q_proj.device
+        read = torch.empty(b, t, heads, VALUE_DIM, device=dev, dtype=torch.float32)
+        mean_t = torch.empty(n, KEY_DIM, VALUE_DIM, device=dev, dtype=torch.float32)
+        cov_t = torch.empty(n, KEY_DIM, KEY_DIM, device=dev, dtype=torch.float32)
+        bmean = torch.empty(n, nb + 1, KEY_DIM, VALUE_DIM, device=dev, dtype=torch.float32)
+        bcov = torch.empty(n, nb + 1, KEY_DIM, KEY_DIM, device=dev, dtype=torch.float32)
+        P = _hip.ptr
+        with torch.cuda.device(dev):
+            _hip.call("bssm_mixer_forward", P(q_proj), lds[0], P(k_proj), lds[1], P(v_proj), lds[2],
+                      P(decay_logits), lds[3], P(noise), lds[4], P(initial_mean), P(initial_covariance), P(read),
+                      P(mean_t), P(cov_t), P(bmean), P(bcov), b, t, heads, interval, float(denominator_floor),
+                      _hip.stream_of(dev))
+        ctx.save_for_backward(q_proj, k_proj, v_proj, decay_logits, noise, initial_mean, initial_covariance,
+                              bmean, bcov)
+        ctx.heads = heads
+        ctx.interval = interval
+        ctx.lds = lds
+        ctx.denominator_floor = float(denominator_floor)
+        ctx.set_materialize_grads(False)
+        return read, mean_t, cov_t
+
+    @staticmethod
+    def backward(ctx, grad_read, grad_mean, grad_covariance):
+        q_proj, k_proj, v_proj, decay_logits, noise, mean0, cov0, bmean, bcov = ctx.saved_tensors
+        b, t, _ = q_proj.shape
+        heads, lds = ctx.heads, ctx.lds
+        need = ctx.needs_input_grad
+        dev = q_proj.device
+        if grad_read is None:
+            grad_read = torch.zeros(b, t, heads, VALUE_DIM, device=dev, dtype=torch.float32)
+        else:
+            grad_read = grad_read.float().contiguous()
+        gm = None if grad_mean is None else grad_mean.float().contiguous()
+        gc = None if grad_covariance is None else grad_covariance.float().contiguous()
+
+        def empty(x: Tensor) -> Tensor:
+            return torch.empty(x.shape, device=dev, dtype=torch.bfloat16)
+
+        gq, gk, gv = empty(q_proj), empty(k_proj), empty(v_proj)
+        dyn = need[3] or need[4]
+        gdl = empty(decay_logits) if dyn else None
+        gnz = empty(noise) if dyn else None
+        gm0 = torch.empty_like(mean0) if need[5] else None
+        gc0 = torch.empty_like(cov0) if need[6] else None
+        P = _hip.ptr
+        with torch.cuda.device(dev):
+            _hip.call("bssm_mixer_backward", P(q_proj), lds[0], P(k_proj), lds[1], P(v_proj), lds[2],
+                      P(decay_logits), lds[3], P(noise), lds[4], P(mean0), P(cov0), P(bmean), P(bcov),
+                      P(grad_read), P(gm), P(gc), P(gq), P(gk), P(gv), P(gdl), P(gnz), P(gm0), P(gc0), b, t, heads,
+                      ctx.interval, ctx.denominator_floor, 0, _hip.stream_of(dev))
+        return (gq if need[0] else None, gk if need[1] else None, gv if need[2] else None,
+                gdl if need[3] else None, gnz if need[4] else None, gm0, gc0, None, None, None)
+
+
+def _initial_state(initial_mean: Optional[Tensor], initial_covariance: Optional[Tensor], n: int,
+                   device: torch.device) -> tuple[Tensor, Tensor]:
+    if initial_mean is None:
+        mean0 = torch.zeros(n, KEY_DIM, VALUE_DIM, device=device, dtype=torch.float32)
+    else:
+        mean0 = initial_mean.to(device=device, dtype=torch.float32).expand(n, KEY_DIM, VALUE_DIM)
+    if initial_covariance is None:
+        cov0 = torch.eye(KEY_DIM, device=device, dtype=torch.float32).expand(n, KEY_DIM, KEY_DIM)
+    else:
+        cov0 = initial_covariance.to(device=device, dtype=torch.float32).expand(n, KEY_DIM, KEY_DIM)
+    return mean0.contiguous(), cov0.contiguous()
+
+
+def mixer_layer_inputs(q_proj: Tensor, k_proj: Tensor, v_proj: Tensor, decay_logits: Tensor, noise: Tensor,
+                       heads: int) -> tuple[Tensor, ...]:
+    """The reference's op chain from projections to layer inputs (train_6layer.py:627-693).
+
+    Returns (keys, values, queries, decay, process, observation) in the
+    layer's [B * H, T, .] sequence layout, float32.
+    """
+    b, t, _ = q_proj.shape
+
+    def heads_first(x: Tensor, w: int) -> Tensor:
+        return x.view(b, t, heads, w).permute(0, 2, 1, 3).reshape(b * heads, t, w)
+
+    q = F.normalize(F.silu(q_proj.float()).view(b, t, heads, KEY_DIM), dim=-1)
+    k = F.normalize(F.silu(k_proj.float()).view(b, t, heads, KEY_DIM), dim=-1)
+    v = F.silu(v_proj.float())
+    nz = noise.float().view(b, t, heads, 2)
+    process = (F.softplus(nz[..., 0]) + NOISE_FLOOR).permute(0, 2, 1).reshape(b * heads, t)
+    observation = (F.softplus(nz[..., 1]) + NOISE_FLOOR).permute(0, 2, 1).reshape(b * heads, t)
+    decay = torch.exp(-F.softplus(decay_logits.float()))
+    return (heads_first(k.reshape(b, t, -1), KEY_DIM), heads_first(v, VALUE_DIM),
+            heads_first(q.reshape(b, t, -1), KEY_DIM), heads_first(decay, KEY_DIM), process, observation)
+
+
+def bayes_mixer_core(
+    q_proj: Tensor,
+    k_proj: Tensor,
+    v_proj: Tensor,
+    decay_logits: Tensor,
+    noise: Tensor,
+    *,
+    heads: int,
+    initial_mean: Optional[Tensor] = None,
+    initial_covariance: Optional[Tensor] = None,
+    chunk_length: Optional[int] = None,
+    denominator_floor: float = 1e-6,
+) -> tuple[Tensor, Tensor, Tensor]:
+    """Readout of the mixer's exact Bayes layer from its raw projections.
+
+    q_proj, k_proj, decay_logits: [B, T, H*4]; v_proj: [B, T, H*8]; noise:
+    [B, T, H*2] ((process, observation) logits per head).  The initial state
+    defaults to the layer's (zero mean, identity covariance) and may be given
+    broadcastable to [B*H, 4, 8] / [B*H, 4, 4].  Returns ``read`` [B, T, H, 8]
+    (float32; the reference's permuted view, made contiguous) and the final
+    mean [B*H, 4, 8] and covariance [B*H, 4, 4].
+
+    Eligible inputs (CUDA, bfloat16, H % 16 == 0, T % 4 == 0, rows
+    addressable as described in the module docstring) run the fused kernels;
+    others run the reference op chain and ``bayesian_layer`` with
+    ``chunk_length`` (which the fused kernels do not need: the recurrence is
+    exact for every chunk length).
+    """
+    if q_proj.ndim != 3:
+        raise ValueError("q_proj must have shape [B, T, H*4]")
+    if heads <= 0:
+        raise ValueError("heads must be positive")
+    if not (denominator_floor > 0):
+        raise ValueError("denominator_floor must be positive")
+    b, t, _ = q_proj.shape
+    projections = (q_proj, k_proj, v_proj, decay_logits, noise)
+    for x, w, name in zip(projections, _WIDTHS, ("q_proj", "k_proj", "v_proj", "decay_logits", "noise")):
+        if tuple(x.shape) != (b, t, w * heads):
+            raise ValueError(f"{name} must have shape [B, T, H*{w}] = {(b, t, w * heads)}, got {tuple(x.shape)}")
+    lds = _fused_eligible(projections, heads)
+    if lds is not None:
+        _hip.load()  # on a GPU the fused path never degrades silently
+        mean0, cov0 = _initial_state(initial_mean, initial_covariance, b * heads, q_proj.device)
+        return _MixerCoreFunction.apply(q_proj, k_proj, v_proj, decay_logits, noise, mean0, cov0, int(heads),
+                                        float(denominator_floor), lds)
+    k, v, q, decay, process, observation = mixer_layer_inputs(*projections, heads)
+    read, mean_t, cov_t = bayesian_layer(
+        k, v, q, transition_diagonals=decay, process_variances=process, observation_variances=observation,
+        initial_mean=initial_mean, initial_covariance=initial_covariance, chunk_length=chunk_length,
+        denominator_floor=denominator_floor)
+    read = read.view(b, heads, t, VALUE_DIM).permute(0, 2, 1, 3).contiguous()
+    return read, mean_t, cov_t
+
+
+__all__ = ["bayes_mixer_core", "mixer_layer_inputs"]

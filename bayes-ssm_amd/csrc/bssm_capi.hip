@@ -183,13 +183,42 @@ int backward_impl(const char* fn, bool fixed, bool dyn, int d, int m, const floa
   return launched(fn, bssm::launch_backward(d, fixed, dyn, a, static_cast<hipStream_t>(stream)));
 }
 
+// Shape and layout checks of the producer-fused mixer entry points.  The
+// kernels take 16 heads of one batch row per wave and address each batch
+// row of a stream through a 32-bit buffer range of T rows.
+int mixer_check(const char* fn, const void* const (&in)[5], const int64_t (&ld)[5], int64_t b, int64_t t, int64_t h,
+                int64_t chunk, float floor) {
+  static const int64_t kWidth[5] = {4, 4, 8, 4, 2};  // q, k, v, decay logits, noise (per head)
+  static const char* kName[5] = {"q_proj", "k_proj", "v_proj", "decay_logits", "noise"};
+  if (b < 0 || t < 0 || h < 0)
+    return fail(BSSM_ERR_ARGUMENT, "%s: negative size b=%lld t=%lld h=%lld", fn, (long long)b, (long long)t,
+                (long long)h);
+  if (!(floor > 0.f)) return fail(BSSM_ERR_ARGUMENT, "%s: denominator_floor must be positive", fn);
+  if (h % 16 != 0 || t <= 0 || t % 4 != 0 || chunk != bssm::kRot4Chunk)
+    return fail(BSSM_ERR_UNSUPPORTED, "%s: needs heads %% 16 == 0, T a positive multiple of 4 and chunk == %d (got h=%lld t=%lld "
+                "chunk=%lld)", fn, bssm::kRot4Chunk, (long long)h, (long long)t, (long long)chunk);
+  if (b * h / 16 > 0x7fffffff) return fail(BSSM_ERR_ARGUMENT, "%s: batch * heads too large", fn);
+  const int64_t nb = (t + chunk - 1) / chunk;
+  if ((nb + 1) * 128 * 16 >= ((int64_t)1 << 31) || t * h * 32 >= ((int64_t)1 << 31))
+    return fail(BSSM_ERR_ARGUMENT, "%s: T * heads too large for 32-bit stream offsets", fn);
+  for (int i = 0; i < 5; ++i) {
+    if (b * h * t > 0 && in[i] == nullptr) return fail(BSSM_ERR_ARGUMENT, "%s: %s is null", fn, kName[i]);
+    if (ld[i] < kWidth[i] * h || ld[i] % 8 != 0 || !aligned16(in[i]))
+      return fail(BSSM_ERR_UNSUPPORTED, "%s: %s needs a row stride >= %lld elements, a multiple of 8, and a "
+                  "16-byte aligned base (got ld=%lld)", fn, kName[i], (long long)(kWidth[i] * h), (long long)ld[i]);
+    if ((t + 16) * ld[i] * 2 >= ((int64_t)1 << 31))
+      return fail(BSSM_ERR_ARGUMENT, "%s: T * ld of %s too large for 32-bit stream offsets", fn, kName[i]);
+  }
+  return BSSM_OK;
+}
+
 }  // namespace
 
 extern "C" {
 
 const char* bssm_last_error(void) { return g_error; }
 
-int bssm_abi_version(void) { return 2; }
+int bssm_abi_version(void) { return 3; }
 
 int bssm_supported(int key_dim, int value_dim) { return supported(key_dim, value_dim) ? 1 : 0; }
 
@@ -422,6 +451,77 @@ int bssm_backward_chunked_bf16(int key_dim, int value_dim, int fixed, const void
                        BwdOut{static_cast<float*>(gk), static_cast<float*>(gv), static_cast<float*>(gq), gd, gp, gr,
                               gm0, gc0},
                        n, t, chunk, denominator_floor, stream, true);
+}
+
+int bssm_mixer_forward(const void* q_proj, int64_t ldq, const void* k_proj, int64_t ldk, const void* v_proj,
+                       int64_t ldv, const void* decay_logits, int64_t ldd, const void* noise, int64_t ldn,
+                       const float* mean0, const float* cov0, float* read, float* mean_final, float* cov_final,
+                       float* bmean, float* bcov, int64_t batch, int64_t t, int64_t heads, int64_t chunk,
+                       float denominator_floor, void* stream) {
+  const char* fn = "bssm_mixer_forward";
+  if (int rc = mixer_check(fn, {q_proj, k_proj, v_proj, decay_logits, noise}, {ldq, ldk, ldv, ldd, ldn}, batch, t,
+                           heads, chunk, denominator_floor))
+    return rc;
+  const int64_t n = batch * heads;
+  BSSM_REQUIRE(mean0);
+  BSSM_REQUIRE(cov0);
+  BSSM_REQUIRE(mean_final);
+  BSSM_REQUIRE(cov_final);
+  BSSM_REQUIRE(bmean);
+  BSSM_REQUIRE(bcov);
+  BSSM_REQUIRE_T(read);
+  for (const void* p : {(const void*)mean0, (const void*)cov0, (const void*)mean_final, (const void*)cov_final,
+                        (const void*)bmean, (const void*)bcov})
+    if (p != nullptr && !aligned8(p)) return fail(BSSM_ERR_ARGUMENT, "%s: belief tensors must be 8-byte aligned", fn);
+  if (read != nullptr && !aligned16(read)) return fail(BSSM_ERR_ARGUMENT, "%s: read must be 16-byte aligned", fn);
+  bssm::MixArgs a{};
+  a.q = q_proj; a.k = k_proj; a.v = v_proj; a.dl = decay_logits; a.nz = noise;
+  a.ldq = ldq; a.ldk = ldk; a.ldv = ldv; a.ldd = ldd; a.ldn = ldn;
+  a.m0 = mean0; a.c0 = cov0; a.y = read; a.mT = mean_final; a.cT = cov_final; a.bm = bmean; a.bc = bcov;
+  a.b = batch; a.t = t; a.h = heads; a.chunk = chunk; a.nb = (t + chunk - 1) / chunk; a.floor = denominator_floor;
+  if (n == 0) return ok();
+  return launched(fn, bssm::launch_mixer_forward(a, static_cast<hipStream_t>(stream)));
+}
+
+int bssm_mixer_backward(const void* q_proj, int64_t ldq, const void* k_proj, int64_t ldk, const void* v_proj,
+                        int64_t ldv, const void* decay_logits, int64_t ldd, const void* noise, int64_t ldn,
+                        const float* mean0, const float* cov0, const float* bmean, const float* bcov,
+                        const float* grad_read, const float* gmf, const float* gcf, void* grad_q, void* grad_k,
+                        void* grad_v, void* grad_decay_logits, void* grad_noise, float* gm0, float* gc0,
+                        int64_t batch, int64_t t, int64_t heads, int64_t chunk, float denominator_floor,
+                        int grad_f32, void* stream) {
+  const char* fn = "bssm_mixer_backward";
+  if (int rc = mixer_check(fn, {q_proj, k_proj, v_proj, decay_logits, noise}, {ldq, ldk, ldv, ldd, ldn}, batch, t,
+                           heads, chunk, denominator_floor))
+    return rc;
+  const int64_t n = batch * heads;
+  if ((grad_decay_logits == nullptr) != (grad_noise == nullptr))
+    return fail(BSSM_ERR_ARGUMENT, "%s: grad_decay_logits and grad_noise must be given together or both be null", fn);
+  BSSM_REQUIRE(mean0);
+  BSSM_REQUIRE(cov0);
+  BSSM_REQUIRE(bmean);
+  BSSM_REQUIRE(bcov);
+  BSSM_REQUIRE_T(grad_read);
+  BSSM_REQUIRE_T(grad_q);
+  BSSM_REQUIRE_T(grad_k);
+  BSSM_REQUIRE_T(grad_v);
+  for (const void* p : {(const void*)bmean, (const void*)bcov, (const void*)gmf, (const void*)gcf, (const void*)gm0,
+                        (const void*)gc0})
+    if (p != nullptr && !aligned8(p)) return fail(BSSM_ERR_ARGUMENT, "%s: belief tensors must be 8-byte aligned", fn);
+  for (const void* p : {(const void*)grad_read, (const void*)grad_q, (const void*)grad_k, (const void*)grad_v,
+                        (const void*)grad_decay_logits, (const void*)grad_noise})
+    if (p != nullptr && !aligned16(p))
+      return fail(BSSM_ERR_ARGUMENT, "%s: grad_read and the projection gradients must be 16-byte aligned", fn);
+  bssm::MixArgs a{};
+  a.q = q_proj; a.k = k_proj; a.v = v_proj; a.dl = decay_logits; a.nz = noise;
+  a.ldq = ldq; a.ldk = ldk; a.ldv = ldv; a.ldd = ldd; a.ldn = ldn;
+  a.m0 = mean0; a.c0 = cov0; a.bmr = bmean; a.bcr = bcov; a.gy = grad_read; a.gmf = gmf; a.gcf = gcf;
+  a.gq = grad_q; a.gk = grad_k; a.gv = grad_v; a.gdl = grad_decay_logits; a.gnz = grad_noise;
+  a.gm0 = gm0; a.gc0 = gc0;
+  a.b = batch; a.t = t; a.h = heads; a.chunk = chunk; a.nb = (t + chunk - 1) / chunk; a.floor = denominator_floor;
+  a.grad_f32 = grad_f32 != 0;
+  if (n == 0) return ok();
+  return launched(fn, bssm::launch_mixer_backward(a, static_cast<hipStream_t>(stream)));
 }
 
 int bssm_associative_static_scan(const float* keys, const float* values, const float* queries,

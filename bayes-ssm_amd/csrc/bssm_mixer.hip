@@ -1,0 +1,505 @@
+// Producer-fused D = 4, M = 8 layer core of the Bayes mixer, gfx950.
+//
+// The mixer (example/train_6layer.py:613-729, learned dynamics) turns its
+// bfloat16 projections into the layer inputs per (batch b, token t, head h):
+//   q, k = normalize(silu(q_proj), silu(k_proj))    (per-head L2, eps 1e-12)
+//   v = silu(v_proj),  d = exp(-softplus(decay_logits)),
+//   p = softplus(noise[.., 0]) + 1e-4,  r = softplus(noise[.., 1]) + 1e-4
+// then permutes [B, T, H, .] to the layer's [B * H, T, .] rows, runs the
+// recurrence, and permutes the readout back to [B, T, H, 8].  Here all of it
+// happens in the recurrence kernels: a wave takes 16 consecutive heads of one
+// batch row, whose per-token slices are contiguous in the [B, T, H, .]
+// tensors (128 bytes of keys, 256 of values), so every projection is read
+// once, in place, and widened, transformed and written into the float32 LDS
+// slot layout of bssm_rot4.h at the tile's staging; the readout leaves the
+// same way.  The transforms run in float32 on the widened bf16 values (the
+// reference computes them in float32 after .to(float32) unless its
+// bf16_state_projection option is set).
+//
+// The backward stages the same raw pieces, keeps them in registers for the
+// tile, and at the tile's write-out applies the chain rule of the
+// transforms to the gradients the reverse leaves in LDS, so the projection
+// gradients are written directly (bfloat16, or float32 for testing).
+//
+// Piece maps of a 16-token tile starting at t0 (lane l, instruction I):
+//   q, k, decay logits (8 per token):  token 8I + (l >> 3), heads 2 (l & 7), +1
+//   v (16 per token):                  token 4I + (l >> 4), head l & 15
+//   noise (4 per token):               token l >> 2, heads 4 (l & 3) .. + 3
+//   readout, gy (32 per token):        token 2I + (l >> 5), head (l >> 1) & 15, half l & 1
+// Each map's rows are addressed through a per-batch-row buffer descriptor
+// whose range ends at token T, so a partial last tile reads zeros and drops
+// its stores without per-lane masks.
+
+#include "bssm_rot4.h"
+
+namespace bssm {
+namespace r4 {
+namespace {
+
+constexpr float kNormEps = 1e-12f;   // F.normalize default eps
+constexpr float kNoiseFloor = 1e-4f;  // softplus(noise) + 1e-4 (train_6layer.py:667-668)
+
+__device__ __forceinline__ float sigmoidf_(float x) { return 1.f / (1.f + __expf(-x)); }
+// torch.nn.functional.softplus (beta 1, threshold 20).
+__device__ __forceinline__ float softplusf_(float x) { return x > 20.f ? x : log1pf(__expf(x)); }
+__device__ __forceinline__ float dsoftplusf_(float x) { return x > 20.f ? 1.f : sigmoidf_(x); }
+__device__ __forceinline__ float siluf_(float x) { return x * sigmoidf_(x); }
+__device__ __forceinline__ float dsiluf_(float x) {
+  const float sg = sigmoidf_(x);
+  return sg * fmaf(x, 1.f - sg, 1.f);
+}
+
+// normalize(silu(x)) of one head's key or query vector.
+__device__ __forceinline__ v4f unit_silu(v4f x) {
+  v4f a;
+  float ss = 0.f;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    a[i] = siluf_(x[i]);
+    ss = fmaf(a[i], a[i], ss);
+  }
+  const float rn = 1.f / fmaxf(sqrtf(ss), kNormEps);
+  return a * rn;
+}
+// Gradient through normalize(silu(x)): g is dL/d(output).
+__device__ __forceinline__ v4f unit_silu_grad(v4f x, v4f g) {
+  v4f a;
+  float ss = 0.f;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    a[i] = siluf_(x[i]);
+    ss = fmaf(a[i], a[i], ss);
+  }
+  const float n = sqrtf(ss);
+  const float rn = 1.f / fmaxf(n, kNormEps);
+  v4f out;
+  if (n > kNormEps) {
+    // (g - u (u . g)) / n with u = a / n.
+    float ug = 0.f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) ug = fmaf(a[i] * rn, g[i], ug);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) out[i] = fmaf(-a[i] * rn, ug, g[i]) * rn * dsiluf_(x[i]);
+  } else {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) out[i] = g[i] * rn * dsiluf_(x[i]);
+  }
+  return out;
+}
+
+__device__ __forceinline__ const float* as_f(const void* p, int64_t bytes) {
+  return reinterpret_cast<const float*>(reinterpret_cast<const char*>(p) + bytes);
+}
+
+// Per-lane piece offsets (bytes within a token row of the wave's heads, and
+// the row index) and LDS float offsets of the maps above, for an 8-token slot
+// layout of slot_floats floats.
+struct MixMap {
+  int kq_tok[2];        // token of the q/k/decay piece (within the tile)
+  uint32_t kq_col;      // byte offset of the piece within the wave's q/k/decay slice
+  int kq_lds[2][2];     // LDS offsets (relative to the region) of its two heads
+  int v_tok[4];
+  uint32_t v_col;
+  int v_lds[4][2];      // the two halves (value columns 0-3, 4-7)
+  int nz_tok;
+  uint32_t nz_col;
+  int nz_lds[4];        // P-region offsets of the piece's four heads (R: same + R - P)
+  int y_tok[8];
+  uint32_t y_col;
+  int y_lds[8];
+
+  __device__ __forceinline__ MixMap(int lane, int slot_floats) {
+    const int pc = lane & 7;
+#pragma unroll
+    for (int I = 0; I < 2; ++I) {
+      kq_tok[I] = 8 * I + (lane >> 3);
+      const int tt = kq_tok[I] & 7, sub = kq_tok[I] >> 3;
+#pragma unroll
+      for (int e = 0; e < 2; ++e) {
+        const int sq = 2 * pc + e, j = sq >> 3, a8 = sq & 7;
+        kq_lds[I][e] = sub * slot_floats + 4 * (64 * j + 8 * (tt ^ j) + a8);
+      }
+    }
+    kq_col = static_cast<uint32_t>(pc) * 16u;
+    const int hh = lane & 15;
+#pragma unroll
+    for (int I = 0; I < 4; ++I) {
+      v_tok[I] = 4 * I + (lane >> 4);
+      const int tt = v_tok[I] & 7, sub = v_tok[I] >> 3, j = hh >> 2, a4 = hh & 3;
+#pragma unroll
+      for (int e = 0; e < 2; ++e) {
+        const int c = 2 * tt + e;
+        v_lds[I][e] = sub * slot_floats + 4 * (64 * j + 4 * (c ^ (2 * j)) + a4);
+      }
+    }
+    v_col = static_cast<uint32_t>(hh) * 16u;
+    nz_tok = lane >> 2;
+    nz_col = static_cast<uint32_t>(lane & 3) * 16u;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int sq = 4 * (lane & 3) + e;
+      nz_lds[e] = (nz_tok >> 3) * slot_floats + 8 * sq + (nz_tok & 7);
+    }
+    const int yh = (lane >> 1) & 15, half = lane & 1;
+#pragma unroll
+    for (int I = 0; I < 8; ++I) {
+      y_tok[I] = 2 * I + (lane >> 5);
+      const int tt = y_tok[I] & 7, sub = y_tok[I] >> 3, j = yh >> 2, a4 = yh & 3, c = 2 * tt + half;
+      y_lds[I] = sub * slot_floats + 4 * (64 * j + 4 * (c ^ (2 * j)) + a4);
+    }
+    y_col = static_cast<uint32_t>(yh) * 32u + static_cast<uint32_t>(half) * 16u;
+  }
+};
+
+// Raw projection pieces of one 16-token tile.
+struct MixRaw {
+  v4f q[2], k[2], dl[2], v[4], nz;
+};
+
+// Buffer descriptors of one batch row (range ends at token T) and row bytes.
+struct MixRows {
+  Rsrc q, k, v, dl, nz;
+  uint32_t rq, rk, rv, rd, rn;       // row bytes
+  uint32_t cq, ck, cv, cd, cn;       // byte offset of the wave's first head within a row
+  __device__ __forceinline__ MixRows(const MixArgs& a, int64_t bb, int64_t h0) {
+    const int64_t T = a.t;
+    rq = static_cast<uint32_t>(a.ldq * 2);
+    rk = static_cast<uint32_t>(a.ldk * 2);
+    rv = static_cast<uint32_t>(a.ldv * 2);
+    rd = static_cast<uint32_t>(a.ldd * 2);
+    rn = static_cast<uint32_t>(a.ldn * 2);
+    q = make_rsrc(as_f(a.q, bb * T * rq), static_cast<uint32_t>(T) * rq);
+    k = make_rsrc(as_f(a.k, bb * T * rk), static_cast<uint32_t>(T) * rk);
+    v = make_rsrc(as_f(a.v, bb * T * rv), static_cast<uint32_t>(T) * rv);
+    dl = make_rsrc(as_f(a.dl, bb * T * rd), static_cast<uint32_t>(T) * rd);
+    nz = make_rsrc(as_f(a.nz, bb * T * rn), static_cast<uint32_t>(T) * rn);
+    cq = cd = ck = static_cast<uint32_t>(h0) * 8u;  // 4 bf16 per head
+    cv = static_cast<uint32_t>(h0) * 16u;           // 8 bf16 per head
+    cn = static_cast<uint32_t>(h0) * 4u;            // 2 bf16 per head
+  }
+  __device__ __forceinline__ void load(MixRaw& x, const MixMap& mm, int64_t t0) const {
+#pragma unroll
+    for (int I = 0; I < 2; ++I) {
+      const uint32_t t = static_cast<uint32_t>(t0 + mm.kq_tok[I]);
+      x.q[I] = ld128<kNtLoad>(q, t * rq + cq + mm.kq_col);
+      x.k[I] = ld128<kNtLoad>(k, t * rk + ck + mm.kq_col);
+      x.dl[I] = ld128<kNtLoad>(dl, t * rd + cd + mm.kq_col);
+    }
+#pragma unroll
+    for (int I = 0; I < 4; ++I) {
+      const uint32_t t = static_cast<uint32_t>(t0 + mm.v_tok[I]);
+      x.v[I] = ld128<kNtLoad>(v, t * rv + cv + mm.v_col);
+    }
+    const uint32_t t = static_cast<uint32_t>(t0 + mm.nz_tok);
+    x.nz = ld128<false>(nz, t * rn + cn + mm.nz_col);
+  }
+};
+
+// Transformed inputs of a tile into the LDS slot regions (K, Q, D, V, P, R of
+// an FwdTile or BwdTile layout).
+template <int K, int Q, int D, int V, int P, int R>
+__device__ __forceinline__ void mix_put(const MixRaw& x, const MixMap& mm, float* tile) {
+#pragma unroll
+  for (int I = 0; I < 2; ++I) {
+    *reinterpret_cast<v4f*>(&tile[K + mm.kq_lds[I][0]]) = unit_silu(widen_lo(x.k[I]));
+    *reinterpret_cast<v4f*>(&tile[K + mm.kq_lds[I][1]]) = unit_silu(widen_hi(x.k[I]));
+    *reinterpret_cast<v4f*>(&tile[Q + mm.kq_lds[I][0]]) = unit_silu(widen_lo(x.q[I]));
+    *reinterpret_cast<v4f*>(&tile[Q + mm.kq_lds[I][1]]) = unit_silu(widen_hi(x.q[I]));
+#pragma unroll
+    for (int e = 0; e < 2; ++e) {
+      const v4f z = e ? widen_hi(x.dl[I]) : widen_lo(x.dl[I]);
+      v4f d;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) d[i] = __expf(-softplusf_(z[i]));
+      *reinterpret_cast<v4f*>(&tile[D + mm.kq_lds[I][e]]) = d;
+    }
+  }
+#pragma unroll
+  for (int I = 0; I < 4; ++I) {
+#pragma unroll
+    for (int e = 0; e < 2; ++e) {
+      const v4f z = e ? widen_hi(x.v[I]) : widen_lo(x.v[I]);
+      v4f o;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) o[i] = siluf_(z[i]);
+      *reinterpret_cast<v4f*>(&tile[V + mm.v_lds[I][e]]) = o;
+    }
+  }
+  const v4f lo = widen_lo(x.nz), hi = widen_hi(x.nz);  // (p, r) of heads 0, 1 | 2, 3
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const float zp = e < 2 ? lo[2 * e] : hi[2 * e - 4];
+    const float zr = e < 2 ? lo[2 * e + 1] : hi[2 * e - 3];
+    tile[P + mm.nz_lds[e]] = softplusf_(zp) + kNoiseFloor;
+    tile[R + mm.nz_lds[e]] = softplusf_(zr) + kNoiseFloor;
+  }
+}
+
+__global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(1, 1))) void mixer_forward_kernel(MixArgs a) {
+  __shared__ float tile[2 * FwdTile::SIZE];
+  __shared__ float ckst[kRecFloats];
+  const int lane = threadIdx.x;
+  const int g = lane & 3, s = lane >> 2;
+  const int64_t n0 = static_cast<int64_t>(blockIdx.x) * SPW;
+  const int64_t bb = n0 / a.h, h0 = n0 - bb * a.h;
+  const int64_t T = a.t;
+  const uint32_t nbp = static_cast<uint32_t>(a.nb + 1);
+  const uint32_t yrow = static_cast<uint32_t>(a.h) * 32u;
+  const MixRows rows(a, bb, h0);
+  const MixMap mm(lane, FwdTile::SIZE);
+  const Rsrc ry = make_rsrc(a.y + bb * T * a.h * 8, static_cast<uint32_t>(T) * yrow);
+  const uint32_t ycol = static_cast<uint32_t>(h0) * 32u + mm.y_col;
+  const Rsrc rbm = make_rsrc(a.bm + n0 * nbp * 32, SPW * nbp * 128u);
+  const Rsrc rbc = make_rsrc(a.bc + n0 * nbp * 16, SPW * nbp * 64u);
+  const Rsrc rm0 = make_rsrc(a.m0 + n0 * 32, SPW * 128u);
+  const Rsrc rc0 = make_rsrc(a.c0 + n0 * 16, SPW * 64u);
+  const Rsrc rmT = make_rsrc(a.mT + n0 * 32, SPW * 128u);
+  const Rsrc rcT = make_rsrc(a.cT + n0 * 16, SPW * 64u);
+
+  const BelOff unit(s, g, 128u, 64u);
+  FwdCore<false> core(lane, a.floor, a.chunk, rbm, rbc, nbp, ckst);
+  load_bel(core.b, rm0, rc0, unit, 0, 0);
+  core.store_ckpt(0);
+
+  struct Out {
+    v4f y[8];
+  };
+  auto take_y = [&](Out& o) __attribute__((always_inline)) {
+#pragma unroll
+    for (int I = 0; I < 8; ++I) o.y[I] = *reinterpret_cast<const v4f*>(&tile[FwdTile::V + mm.y_lds[I]]);
+  };
+  auto store_y = [&](const Out& o, int64_t t0) __attribute__((always_inline)) {
+#pragma unroll
+    for (int I = 0; I < 8; ++I)
+      st128<kNtStore>(ry, o.y[I], static_cast<uint32_t>(t0 + mm.y_tok[I]) * yrow + ycol, 0);
+  };
+
+  // As the float32 forward: tile i + 1 loads while tile i computes.
+  const int64_t ntiles = (T + LT - 1) / LT;
+  MixRaw st;
+  rows.load(st, mm, 0);
+  for (int64_t i = 0; i < ntiles; ++i) {
+    Out yo;
+    if (i > 0) take_y(yo);
+    __builtin_amdgcn_sched_barrier(0);
+    mix_put<FwdTile::K, FwdTile::Q, FwdTile::D, FwdTile::V, FwdTile::P, FwdTile::R>(st, mm, tile);
+    __builtin_amdgcn_sched_barrier(0);
+    if (i > 0) store_y(yo, (i - 1) * LT);
+    if (i + 1 < ntiles) rows.load(st, mm, (i + 1) * LT);
+    __builtin_amdgcn_sched_barrier(0);
+    const int64_t t0 = i * LT;
+    core.run_sub(tile, t0, T);
+    if (t0 + TT < T) core.run_sub(tile + FwdTile::SIZE, t0 + TT, T);
+  }
+  {
+    Out yo;
+    take_y(yo);
+    store_y(yo, (ntiles - 1) * LT);
+  }
+  store_bel(core.b, rmT, rcT, unit, 0, 0);
+  core.store_ckpt(static_cast<uint32_t>(a.nb));
+}
+
+// Gradient outputs: contiguous [B, T, H * w] rows, bfloat16 or float32.
+struct MixGrads {
+  Rsrc q, k, v, dl, nz;
+  uint32_t rkq, rv, rn;  // row bytes of the bf16 layout
+  uint32_t ckq, cv, cn;  // byte offset of the wave's first head, bf16 layout
+  bool f32;
+  __device__ __forceinline__ MixGrads(const MixArgs& a, int64_t bb, int64_t h0) {
+    const int64_t T = a.t, H = a.h;
+    f32 = a.grad_f32 != 0;
+    rkq = static_cast<uint32_t>(H) * 8u;
+    rv = static_cast<uint32_t>(H) * 16u;
+    rn = static_cast<uint32_t>(H) * 4u;
+    ckq = static_cast<uint32_t>(h0) * 8u;
+    cv = static_cast<uint32_t>(h0) * 16u;
+    cn = static_cast<uint32_t>(h0) * 4u;
+    // Offsets are computed in the bf16 layout; float32 rows are twice as long.
+    const int64_t e = f32 ? 2 : 1;
+    const uint32_t tkq = static_cast<uint32_t>(T * e) * rkq, tv = static_cast<uint32_t>(T * e) * rv,
+                   tn = static_cast<uint32_t>(T * e) * rn;
+    q = make_rsrc(as_f(a.gq, bb * tkq), tkq);
+    k = make_rsrc(as_f(a.gk, bb * tkq), tkq);
+    v = make_rsrc(as_f(a.gv, bb * tv), tv);
+    const bool dyn = a.gdl != nullptr;
+    dl = make_rsrc(as_f(dyn ? a.gdl : a.gq, dyn ? bb * tkq : 0), dyn ? tkq : 0u);
+    nz = make_rsrc(as_f(dyn ? a.gnz : a.gq, dyn ? bb * tn : 0), dyn ? tn : 0u);
+  }
+  // One piece of 8 values (lo = first four, hi = last four) at the bf16
+  // byte offset `off`: bf16 as one 16-byte piece, float32 as two.
+  __device__ __forceinline__ void put8(Rsrc r, uint32_t off, v4f lo, v4f hi) const {
+    if (f32) {
+      st128<kNtStore>(r, lo, 2u * off, 0);
+      st128<kNtStore>(r, hi, 2u * off + 16u, 0);
+    } else {
+      st128<kNtStore>(r, narrow(lo, hi), off, 0);
+    }
+  }
+};
+
+template <bool DYN>
+__global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(1, 1))) void mixer_backward_kernel(
+    MixArgs a) {
+  __shared__ float tile[2 * BwdTile::SIZE];
+  const int lane = threadIdx.x;
+  const int g = lane & 3, s = lane >> 2;
+  const int64_t n0 = static_cast<int64_t>(blockIdx.x) * SPW;
+  const int64_t bb = n0 / a.h, h0 = n0 - bb * a.h;
+  const int64_t T = a.t;
+  const uint32_t nbp = static_cast<uint32_t>(a.nb + 1);
+  const uint32_t yrow = static_cast<uint32_t>(a.h) * 32u;
+  const MixRows rows(a, bb, h0);
+  const MixGrads gr(a, bb, h0);
+  const MixMap mm(lane, BwdTile::SIZE);
+  const Rsrc rgy = make_rsrc(a.gy + bb * T * a.h * 8, static_cast<uint32_t>(T) * yrow);
+  const uint32_t ycol = static_cast<uint32_t>(h0) * 32u + mm.y_col;
+  const Rsrc rbm = make_rsrc(a.bmr + n0 * nbp * 32, SPW * nbp * 128u);
+  const Rsrc rbc = make_rsrc(a.bcr + n0 * nbp * 16, SPW * nbp * 64u);
+  const RecOff ckoff(lane, nbp * 128u, nbp * 64u);
+
+  const BelOff unit(s, g, 128u, 64u);
+  BwdCore<false, DYN> core(s, g, a.floor);
+  core.init(a.gmf, a.gcf, a.m0, n0, SPW, unit, s);
+  const int64_t nb = a.nb;
+  const int64_t ntiles = (nb + 1) / 2;
+
+  struct Stage {
+    MixRaw raw;
+    v4f gy[8];
+  };
+  auto load = [&](Stage& x, int64_t J) __attribute__((always_inline)) {
+    const int64_t t0 = J * 2 * SUB;
+    rows.load(x.raw, mm, t0);
+#pragma unroll
+    for (int I = 0; I < 8; ++I)
+      x.gy[I] = ld128<kNtLoad>(rgy, static_cast<uint32_t>(t0 + mm.y_tok[I]) * yrow + ycol);
+  };
+  auto put = [&](const Stage& x) __attribute__((always_inline)) {
+    mix_put<BwdTile::K, BwdTile::Q, BwdTile::D, BwdTile::V, BwdTile::P, BwdTile::R>(x.raw, mm, tile);
+#pragma unroll
+    for (int I = 0; I < 8; ++I) *reinterpret_cast<v4f*>(&tile[BwdTile::GY + mm.y_lds[I]]) = x.gy[I];
+  };
+  auto issue_ck = [&](float* tl, int64_t c) __attribute__((always_inline)) {
+    lds_wait();
+    const uint32_t cm = static_cast<uint32_t>(c) * 128u, cc = static_cast<uint32_t>(c) * 64u;
+    dma16<kNtCkpt>(rbm, (tl + BwdTile::CK), ckoff.m0 + cm);
+    dma16<kNtCkpt>(rbm, (tl + BwdTile::CK) + 256, ckoff.m1 + cm);
+    dma16(rbc, (tl + BwdTile::CK) + 512, ckoff.c + cc);
+  };
+  // Projection gradients of tile J: the reverse left dL/d(transformed input)
+  // in the LDS regions; the raw pieces of the tile give the chain rule.
+  auto write_grads = [&](const MixRaw& x, int64_t J) __attribute__((always_inline)) {
+    const int64_t t0 = J * 2 * SUB;
+#pragma unroll
+    for (int I = 0; I < 2; ++I) {
+      const uint32_t t = static_cast<uint32_t>(t0 + mm.kq_tok[I]);
+      const int o0 = mm.kq_lds[I][0], o1 = mm.kq_lds[I][1];
+      const v4f gk0 = *reinterpret_cast<const v4f*>(&tile[BwdTile::K + o0]);
+      const v4f gk1 = *reinterpret_cast<const v4f*>(&tile[BwdTile::K + o1]);
+      gr.put8(gr.k, t * gr.rkq + gr.ckq + mm.kq_col, unit_silu_grad(widen_lo(x.k[I]), gk0),
+              unit_silu_grad(widen_hi(x.k[I]), gk1));
+      const v4f gq0 = *reinterpret_cast<const v4f*>(&tile[BwdTile::Q + o0]);
+      const v4f gq1 = *reinterpret_cast<const v4f*>(&tile[BwdTile::Q + o1]);
+      gr.put8(gr.q, t * gr.rkq + gr.ckq + mm.kq_col, unit_silu_grad(widen_lo(x.q[I]), gq0),
+              unit_silu_grad(widen_hi(x.q[I]), gq1));
+      if constexpr (DYN) {
+        v4f out[2];
+#pragma unroll
+        for (int e = 0; e < 2; ++e) {
+          const v4f z = e ? widen_hi(x.dl[I]) : widen_lo(x.dl[I]);
+          const v4f gd = *reinterpret_cast<const v4f*>(&tile[BwdTile::D + (e ? o1 : o0)]);
+#pragma unroll
+          for (int i = 0; i < 4; ++i) out[e][i] = -gd[i] * __expf(-softplusf_(z[i])) * dsoftplusf_(z[i]);
+        }
+        gr.put8(gr.dl, t * gr.rkq + gr.ckq + mm.kq_col, out[0], out[1]);
+      }
+    }
+#pragma unroll
+    for (int I = 0; I < 4; ++I) {
+      const uint32_t t = static_cast<uint32_t>(t0 + mm.v_tok[I]);
+      v4f out[2];
+#pragma unroll
+      for (int e = 0; e < 2; ++e) {
+        const v4f z = e ? widen_hi(x.v[I]) : widen_lo(x.v[I]);
+        const v4f gv = *reinterpret_cast<const v4f*>(&tile[BwdTile::V + mm.v_lds[I][e]]);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) out[e][i] = gv[i] * dsiluf_(z[i]);
+      }
+      gr.put8(gr.v, t * gr.rv + gr.cv + mm.v_col, out[0], out[1]);
+    }
+    if constexpr (DYN) {
+      const uint32_t t = static_cast<uint32_t>(t0 + mm.nz_tok);
+      const v4f lo = widen_lo(x.nz), hi = widen_hi(x.nz);
+      v4f out[2];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float zp = e < 2 ? lo[2 * e] : hi[2 * e - 4];
+        const float zr = e < 2 ? lo[2 * e + 1] : hi[2 * e - 3];
+        const float gp = tile[BwdTile::P + mm.nz_lds[e]] * dsoftplusf_(zp);
+        const float grr = tile[BwdTile::R + mm.nz_lds[e]] * dsoftplusf_(zr);
+        out[e >> 1][2 * (e & 1)] = gp;
+        out[e >> 1][2 * (e & 1) + 1] = grr;
+      }
+      gr.put8(gr.nz, t * gr.rn + gr.cn + mm.nz_col, out[0], out[1]);
+    }
+  };
+  auto chunk_len = [&](int64_t c) __attribute__((always_inline)) {
+    return static_cast<int>((T - c * SUB) < SUB ? (T - c * SUB) : SUB);
+  };
+  auto run_chunk = [&](float* tl, int64_t c) __attribute__((always_inline)) {
+    Bel b;
+    bel_from_lds(b, tl + BwdTile::CK, s, g);
+    if (c >= 2) issue_ck(tl, c - 2);
+    core.run(tl, b, chunk_len(c));
+  };
+
+  // As the bf16-input backward: tile J's loads were issued during tile J + 1;
+  // the raw pieces of the tile being written out are kept until its
+  // gradients have left.
+  Stage st;
+  MixRaw kept;
+  load(st, ntiles - 1);
+  issue_ck(tile, 2 * (ntiles - 1));
+  if (2 * ntiles - 1 < nb) issue_ck(tile + BwdTile::SIZE, 2 * ntiles - 1);
+  else if (ntiles > 1) issue_ck(tile + BwdTile::SIZE, 2 * ntiles - 3);
+  for (int64_t J = ntiles - 1; J >= 0; --J) {
+    vm_wait<0>();
+    if (J + 1 < ntiles) write_grads(kept, J + 1);
+    __builtin_amdgcn_sched_barrier(0);
+    lds_wait();
+    put(st);
+    kept = st.raw;
+    __builtin_amdgcn_sched_barrier(0);
+    if (J > 0) load(st, J - 1);
+    __builtin_amdgcn_sched_barrier(0);
+    if (2 * J + 1 < nb) run_chunk(tile + BwdTile::SIZE, 2 * J + 1);
+    run_chunk(tile, 2 * J);
+  }
+  write_grads(kept, 0);
+  core.store_initial(a.gm0, a.gc0, n0, SPW, unit);
+}
+
+}  // namespace
+}  // namespace r4
+
+hipError_t launch_mixer_forward(const MixArgs& a, hipStream_t stream) {
+  const int64_t blocks = a.b * a.h / r4::SPW;
+  if (blocks == 0) return hipSuccess;
+  hipLaunchKernelGGL(r4::mixer_forward_kernel, dim3(static_cast<unsigned>(blocks)), dim3(kWave), 0, stream, a);
+  return hipGetLastError();
+}
+
+hipError_t launch_mixer_backward(const MixArgs& a, hipStream_t stream) {
+  const int64_t blocks = a.b * a.h / r4::SPW;
+  if (blocks == 0) return hipSuccess;
+  if (a.gdl != nullptr)
+    hipLaunchKernelGGL(r4::mixer_backward_kernel<true>, dim3(static_cast<unsigned>(blocks)), dim3(kWave), 0, stream,
+                       a);
+  else
+    hipLaunchKernelGGL(r4::mixer_backward_kernel<false>, dim3(static_cast<unsigned>(blocks)), dim3(kWave), 0,
+                       stream, a);
+  return hipGetLastError();
+}
+
+}  // namespace bssm

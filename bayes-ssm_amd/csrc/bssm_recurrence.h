@@ -84,6 +84,38 @@ constexpr int kRot4Chunk = 8;
 hipError_t launch_forward_r4(bool fixed, const FwdArgs& a, hipStream_t stream);
 hipError_t launch_backward_r4(bool fixed, bool dyn, const BwdArgs& a, hipStream_t stream);
 
+// Producer-fused D = 4, M = 8 layer core of the Bayes mixer (bssm_mixer.hip).
+// Inputs are the bfloat16 projections in [B, T, *] layout, each with its own
+// row stride (elements): queries, keys and decay logits [.., H * 4], values
+// [.., H * 8], noise [.., H * 2] (process, observation per head).  The
+// output and its gradient are float32 [B, T, H * 8]; the input gradients are
+// contiguous, bfloat16 (float32 when grad_f32).  Belief tensors are the
+// [B * H, ...] ones of the float32 ABI (sequence n = b * H + h).
+struct MixArgs {
+  const void *q, *k, *v, *dl, *nz;
+  int64_t ldq, ldk, ldv, ldd, ldn;
+  const float* m0;
+  const float* c0;
+  float* y;
+  float* mT;
+  float* cT;
+  float* bm;
+  float* bc;
+  const float* bmr;  // backward: the forward's checkpoints
+  const float* bcr;
+  const float* gy;
+  const float* gmf;  // may be null (zero)
+  const float* gcf;  // may be null (zero)
+  void *gq, *gk, *gv, *gdl, *gnz;  // gdl, gnz null: dynamics gradients not requested
+  float* gm0;  // may be null
+  float* gc0;  // may be null
+  int64_t b, t, h, chunk, nb;
+  float floor;
+  int grad_f32;
+};
+hipError_t launch_mixer_forward(const MixArgs& a, hipStream_t stream);
+hipError_t launch_mixer_backward(const MixArgs& a, hipStream_t stream);
+
 hipError_t launch_associative_scan(const float* k, const float* v, const float* q, const float* r,
                                    const float* m0, const float* c0, float* y, float* mT, float* cT,
                                    int64_t b, int64_t t, int d, int m, hipStream_t stream);

@@ -265,6 +265,55 @@ int bssm_associative_static_scan(const float* keys, const float* values, const f
                                  int64_t b, int64_t t, int key_dim, int value_dim,
                                  void* stream);
 
+/* ------------------------------------------------------------------------
+ * Producer-fused layer core of the Bayes mixer (D = 4, M = 8, learned
+ * dynamics).  Replaces the torch-op chain between the projections and the
+ * readout of example/train_6layer.py:627-693 and :702-709:
+ *   q, k = normalize(silu(q_proj)), normalize(silu(k_proj))  (per head, eps 1e-12)
+ *   v = silu(v_proj), decay = exp(-softplus(decay_logits)),
+ *   process, observation = softplus(noise[.., 0]), softplus(noise[.., 1]) + 1e-4,
+ *   the [B,T,H,.] -> [B*H,T,.] permutes, bayesian_layer, and the readout
+ *   permute back to [B,T,H,8].
+ * Inputs are bfloat16 [B, T, *] views with a row stride in elements (ld*):
+ * q_proj, k_proj, decay_logits [.., H*4], v_proj [.., H*8], noise [.., H*2]
+ * ((process, observation) per head); the innermost dimension is contiguous,
+ * each ld* is a multiple of 8 and each base 16-byte aligned, so that one
+ * fused projection output can be passed as five column views.  mean0 [B*H,4,8],
+ * cov0 [B*H,4,4] float32 (sequence b*H + h).  Outputs: read [B,T,H*8] float32
+ * (contiguous), mean_final, cov_final, and the checkpoints bmean
+ * [B*H, nb+1, 4, 8], bcov [B*H, nb+1, 4, 4] with nb = ceil(T / chunk).
+ * Needs H % 16 == 0, T a positive multiple of 4, chunk ==
+ * bssm_preferred_checkpoint(4);
+ * otherwise BSSM_ERR_UNSUPPORTED.  No counterpart in the reference library:
+ * its mixer materialises every transformed and permuted tensor in float32. */
+int bssm_mixer_forward(const void* q_proj, int64_t ldq, const void* k_proj, int64_t ldk,
+                       const void* v_proj, int64_t ldv, const void* decay_logits, int64_t ldd,
+                       const void* noise, int64_t ldn,
+                       const float* mean0, const float* cov0,
+                       float* read, float* mean_final, float* cov_final,
+                       float* bmean, float* bcov,
+                       int64_t batch, int64_t t, int64_t heads, int64_t chunk,
+                       float denominator_floor, void* stream);
+
+/* Reverse of bssm_mixer_forward: gradients of the five projections, written
+ * contiguous ([B,T,H*4] for q, k, decay logits; [B,T,H*8] for v; [B,T,H*2]
+ * for noise) as bfloat16, the float32 gradient rounded to nearest even (what
+ * autograd through the reference's .float() widening yields); with
+ * grad_f32 != 0 they are written as float32 instead (same shapes).
+ * grad_decay_logits and grad_noise are given together or both NULL (then
+ * not computed); grad_read [B,T,H*8] float32 contiguous; gmf, gcf, gm0, gc0
+ * may be NULL. */
+int bssm_mixer_backward(const void* q_proj, int64_t ldq, const void* k_proj, int64_t ldk,
+                        const void* v_proj, int64_t ldv, const void* decay_logits, int64_t ldd,
+                        const void* noise, int64_t ldn,
+                        const float* mean0, const float* cov0,
+                        const float* bmean, const float* bcov,
+                        const float* grad_read, const float* gmf, const float* gcf,
+                        void* grad_q, void* grad_k, void* grad_v, void* grad_decay_logits,
+                        void* grad_noise, float* gm0, float* gc0,
+                        int64_t batch, int64_t t, int64_t heads, int64_t chunk,
+                        float denominator_floor, int grad_f32, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -18,6 +18,8 @@ float32, autograd-friendly), written from the equations:
 * ``checkpoints``                    — boundary layout of persistent_bayes_chunked_d4m8.cu:208-211, :244
 * ``associative_static``             — bayes_ssm/replay_ssm.py:155-270 (information-form scan)
 * ``closed_form_static``             — Bayesian linear regression, the A=I, Q=0 closed form
+* ``mixer_inputs`` / ``mixer_core``  — the Bayes mixer's producer chain and readout permute
+                                       (example/train_6layer.py:627-693, :709-710)
 
 Pinning (tests/test_oracle.py): closed forms (scalar Kalman filter, one-step
 u = (d^2+p)k, no-update limits, Bayesian linear regression), invariants
@@ -25,6 +27,10 @@ u = (d^2+p)k, no-update limits, Bayesian linear regression), invariants
 cross-formulation agreement (dense == diagonal == transported-history ==
 information-form, as the reference's own tests assert at 1e-12/1e-10), and
 fp64 gradcheck of the gradients that the reference obtains by autograd.
+The mixer producer chain is pinned by identities the reference's formulas
+must satisfy (exp(-softplus(x)) = sigmoid(-x), softplus(x) - softplus(-x) = x,
+unit-norm heads, the [B, T, H] -> [B*H, T] sequence map checked with
+head-tagged inputs) and by its reduction to ``run_diagonal``.
 No function here is left "parity unpinned".
 """
 from __future__ import annotations
@@ -220,6 +226,104 @@ def closed_form_static(k, v, r, mean0, cov0):
     nat = lam0 @ mean0 + torch.einsum("...ti,...tc->...ic", k / r[..., :, None], v)
     mean = torch.linalg.solve(lam, nat)
     return mean, torch.linalg.inv(lam)
+
+
+# ----------------------------------------------------------- Bayes mixer
+MIXER_NOISE_FLOOR = 1e-4
+
+
+def _softplus(x: Tensor) -> Tensor:
+    """torch.nn.functional.softplus with beta 1 and threshold 20: x above 20, else log(1 + e^x)."""
+    return torch.where(x > 20, x, torch.log1p(torch.exp(x.clamp(max=20))))
+
+
+def _silu(x: Tensor) -> Tensor:
+    return x * torch.sigmoid(x)
+
+
+def mixer_inputs(q_proj, k_proj, v_proj, decay_logits, noise, heads: int, dtype=torch.float64):
+    """Layer inputs of the Bayes mixer from its projections (train_6layer.py:627-693).
+
+    q_proj, k_proj, decay_logits [B, T, H*4], v_proj [B, T, H*8], noise
+    [B, T, H*2] ((process, observation) logits per head), any float dtype
+    (computed in ``dtype``).  Per head: q, k = silu(x) / max(|silu(x)|, 1e-12),
+    v = silu(x), d = exp(-softplus(x)), p, r = softplus(x) + 1e-4.  Sequence
+    b*H + h of the layer is head h of batch row b.  Returns (k, v, q, d, p, r)
+    in the layer's [B*H, T, .] layout.
+    """
+    b, t, _ = q_proj.shape
+
+    def split(x: Tensor, w: int) -> Tensor:
+        return x.to(dtype).reshape(b, t, heads, w)
+
+    def unit(x: Tensor) -> Tensor:
+        a = _silu(x)
+        return a / a.square().sum(-1, keepdim=True).sqrt().clamp_min(1e-12)
+
+    def seq(x: Tensor) -> Tensor:  # [B, T, H, ...] -> [B*H, T, ...]
+        return x.transpose(1, 2).reshape(b * heads, t, *x.shape[3:])
+
+    q = unit(split(q_proj, 4))
+    k = unit(split(k_proj, 4))
+    v = _silu(split(v_proj, 8))
+    d = torch.exp(-_softplus(split(decay_logits, 4)))
+    nz = split(noise, 2)
+    p = _softplus(nz[..., 0]) + MIXER_NOISE_FLOOR
+    r = _softplus(nz[..., 1]) + MIXER_NOISE_FLOOR
+    return seq(k), seq(v), seq(q), seq(d), seq(p), seq(r)
+
+
+def mixer_core(q_proj, k_proj, v_proj, decay_logits, noise, heads: int, mean0=None, cov0=None, floor=1e-6,
+               dtype=torch.float64):
+    """Readout [B, T, H, 8] of the mixer's layer (train_6layer.py:709-710) and the final belief [B*H, ...]."""
+    b, t, _ = q_proj.shape
+    k, v, q, d, p, r = mixer_inputs(q_proj, k_proj, v_proj, decay_logits, noise, heads, dtype)
+    n = b * heads
+    if mean0 is None:
+        mean0 = torch.zeros(n, 4, 8, dtype=dtype)
+    if cov0 is None:
+        cov0 = torch.eye(4, dtype=dtype).expand(n, 4, 4)
+    y, mT, cT = run_diagonal(k, v, q, d, p, r, mean0.to(dtype), cov0.to(dtype), floor)
+    return y.reshape(b, heads, t, 8).transpose(1, 2), mT, cT
+
+
+def mixer_grads(q_proj, k_proj, v_proj, decay_logits, noise, heads: int, mean0, cov0, g_read, gmf=None, gcf=None,
+                floor=1e-6, dtype=torch.float64):
+    """Readout, final belief and the gradients of the five projections and the initial belief.
+
+    Autograd through ``mixer_core`` with loss <read, g_read> + <mT, gmf> + <cT, gcf>.
+    Returns (read, mT, cT, [g_q, g_k, g_v, g_decay_logits, g_noise, g_mean0, g_cov0]).
+    """
+    leaves = [x.detach().to(dtype).clone().requires_grad_(True)
+              for x in (q_proj, k_proj, v_proj, decay_logits, noise, mean0, cov0)]
+    read, mT, cT = mixer_core(*leaves[:5], heads, leaves[5], leaves[6], floor, dtype)
+    loss = (read * g_read.to(dtype)).sum()
+    if gmf is not None:
+        loss = loss + (mT * gmf.to(dtype)).sum()
+    if gcf is not None:
+        loss = loss + (cT * gcf.to(dtype)).sum()
+    grads = torch.autograd.grad(loss, leaves)
+    return read.detach(), mT.detach(), cT.detach(), list(grads)
+
+
+def make_mixer_inputs(b: int, t: int, heads: int, *, seed: int = 0, ld_pad: int = 0):
+    """Seeded bf16 projections of the mixer (CPU tensors), drawn as one fused projection.
+
+    Draw order: one [B, T, H*22 + ld_pad] N(0,1) block whose columns are
+    q (H*4), k (H*4), v (H*8), decay logits (H*4, shifted by +2) and noise
+    (H*2, process logits shifted by -3); the five are returned as column
+    views (row stride H*22 + ld_pad), then the readout gradient [B, T, H, 8].
+    """
+    gen = torch.Generator().manual_seed(seed)
+    width = heads * 22 + ld_pad
+    fused = torch.randn(b, t, width, generator=gen)
+    fused[..., heads * 16:heads * 20] += 2.0
+    fused[..., heads * 20:heads * 22:2] -= 3.0
+    fused = fused.to(torch.bfloat16)
+    cuts = [0, heads * 4, heads * 8, heads * 16, heads * 20, heads * 22]
+    views = [fused[..., cuts[i]:cuts[i + 1]] for i in range(5)]
+    g_read = torch.randn(b, t, heads, 8, generator=gen)
+    return views, g_read
 
 
 # --------------------------------------------------------------- inputs

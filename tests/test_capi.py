@@ -121,3 +121,27 @@ def test_contract_gate_returns_none_on_cpu():
                                   torch.ones(2, 3), torch.zeros(2, 4, 8), torch.eye(4).expand(2, 4, 4),
                                   chunk_length=2, denominator_floor=1e-6)
     assert out is None
+
+
+def _mixer_fwd(lib, b=1, t=8, h=16, chunk=8, lds=(64, 64, 128, 64, 32), null=True, floor=1e-6):
+    args = []
+    for ld in lds:
+        args += [None, ld]
+    return lib.bssm_mixer_forward(*args, *([None] * 7), b, t, h, chunk, ctypes.c_float(floor), None)
+
+
+def test_mixer_argument_errors_are_reported(lib):
+    assert _mixer_fwd(lib, h=8) == 2 and b"heads" in lib.bssm_last_error()
+    assert _mixer_fwd(lib, t=6) == 2
+    assert _mixer_fwd(lib, t=0) == 2
+    assert _mixer_fwd(lib, chunk=16) == 2
+    assert _mixer_fwd(lib, floor=0.0) == 1
+    assert _mixer_fwd(lib, b=-1) == 1
+    assert _mixer_fwd(lib) == 1 and b"null" in lib.bssm_last_error()
+    args = []
+    for ld in (64, 64, 128, 64, 32):
+        args += [None, ld]
+    rc = lib.bssm_mixer_backward(*args, *([None] * 14), 1, 8, 16, 8, ctypes.c_float(1e-6), 0, None)
+    assert rc == 1 and b"null" in lib.bssm_last_error()
+    # Nothing to do: success without touching a device.
+    assert _mixer_fwd(lib, b=0) == 0

@@ -1,0 +1,202 @@
+"""GPU parity of the producer-fused mixer kernels (C ABI bssm_mixer_*) against the CPU oracle.
+
+The oracle composes the mixer's producer chain and readout permute
+(example/train_6layer.py:627-710) with the float64 diagonal recurrence.
+Tolerance: 1e-5 relative, 1e-4 absolute for outputs and float32 gradients;
+the bfloat16 gradients are the float32 ones rounded to nearest even, bit for
+bit; checkpoints are the oracle's boundary beliefs.
+"""
+from __future__ import annotations
+
+import pytest
+import torch
+
+from oracle import bssm_oracle as O
+
+pytestmark = pytest.mark.gpu
+
+RTOL, ATOL = 1e-5, 1e-4
+CHUNK = 8
+
+
+def close(actual, expected, name="", rtol=RTOL, atol=ATOL):
+    actual = actual.detach().double().cpu()
+    expected = expected.detach().double().cpu()
+    torch.testing.assert_close(actual, expected, rtol=rtol, atol=atol, msg=lambda m: f"{name}: {m}")
+
+
+def _device_views(views, device):
+    """The five column views re-created over one device copy of their fused projection."""
+    base = views[0]._base
+    assert base is not None and all(x._base is base for x in views)
+    dev = base.to(device)
+    return [torch.as_strided(dev, x.shape, x.stride(), x.storage_offset()) for x in views]
+
+
+def _state(n, seed):
+    g = torch.Generator().manual_seed(seed)
+    m0 = 0.2 * torch.randn(n, 4, 8, generator=g)
+    a = torch.randn(n, 4, 4, generator=g)
+    c0 = a @ a.transpose(-1, -2) / 4 + 0.5 * torch.eye(4)
+    c0 = 0.5 * (c0 + c0.transpose(-1, -2))
+    gmf = torch.randn(n, 4, 8, generator=g)
+    gcf = torch.randn(n, 4, 4, generator=g)
+    return m0, c0, gmf, gcf
+
+
+def _lds(views):
+    return [x.stride(1) for x in views]
+
+
+def _forward(dv, lds, m0, c0, b, t, h):
+    from bayes_ssm import _hip
+
+    n = b * h
+    nb = -(-t // CHUNK)
+    dev = dv[0].device
+    read = torch.empty(b, t, h * 8, device=dev)
+    mT, cT = torch.empty(n, 4, 8, device=dev), torch.empty(n, 4, 4, device=dev)
+    bm, bc = torch.empty(n, nb + 1, 4, 8, device=dev), torch.empty(n, nb + 1, 4, 4, device=dev)
+    P = _hip.ptr
+    args = []
+    for x, ld in zip(dv, lds):
+        args += [P(x), ld]
+    _hip.call("bssm_mixer_forward", *args, P(m0), P(c0), P(read), P(mT), P(cT), P(bm), P(bc), b, t, h, CHUNK,
+              1e-6, _hip.stream_of(dev))
+    return read, mT, cT, bm, bc
+
+
+def _backward(dv, lds, m0, c0, bm, bc, gy, gmf, gcf, b, t, h, *, f32, dyn=True, initial=True):
+    from bayes_ssm import _hip
+
+    dev = dv[0].device
+    dtype = torch.float32 if f32 else torch.bfloat16
+    grads = [torch.empty(x.shape, device=dev, dtype=dtype) if (i < 3 or dyn) else None for i, x in enumerate(dv)]
+    gm0 = torch.empty_like(m0) if initial else None
+    gc0 = torch.empty_like(c0) if initial else None
+    P = _hip.ptr
+    args = []
+    for x, ld in zip(dv, lds):
+        args += [P(x), ld]
+    _hip.call("bssm_mixer_backward", *args, P(m0), P(c0), P(bm), P(bc), P(gy), P(gmf), P(gcf),
+              *[P(g) for g in grads], P(gm0), P(gc0), b, t, h, CHUNK, 1e-6, int(f32), _hip.stream_of(dev))
+    return grads + [gm0, gc0]
+
+
+CASES = [  # batch, tokens, heads, extra row padding of the fused projection (elements)
+    (2, 36, 16, 0),
+    (1, 64, 32, 8),
+    (3, 20, 16, 24),
+    (1, 4, 16, 0),
+    (2, 100, 48, 16),
+]
+
+
+@pytest.mark.parametrize("b,t,h,pad", CASES)
+def test_mixer_abi_matches_oracle(cuda_device, b, t, h, pad):
+    print(f"mixer abi b={b} t={t} h={h} pad={pad}", flush=True)
+    views, g_read = O.make_mixer_inputs(b, t, h, seed=900 + t, ld_pad=pad)
+    n = b * h
+    m0, c0, gmf, gcf = _state(n, seed=t)
+    dv = _device_views(views, cuda_device)
+    lds = _lds(views)
+    assert lds[0] == 22 * h + pad
+    d = {name: x.to(cuda_device) for name, x in dict(m0=m0, c0=c0, gmf=gmf, gcf=gcf, gy=g_read).items()}
+
+    read, mT, cT, bm, bc = _forward(dv, lds, d["m0"], d["c0"], b, t, h)
+    g32 = _backward(dv, lds, d["m0"], d["c0"], bm, bc, d["gy"], d["gmf"], d["gcf"], b, t, h, f32=True)
+    g16 = _backward(dv, lds, d["m0"], d["c0"], bm, bc, d["gy"], d["gmf"], d["gcf"], b, t, h, f32=False)
+    lean = _backward(dv, lds, d["m0"], d["c0"], bm, bc, d["gy"], None, None, b, t, h, f32=True, dyn=False,
+                     initial=False)
+    torch.cuda.synchronize()
+
+    e_read, e_mT, e_cT, e_grads = O.mixer_grads(*views, h, m0, c0, g_read, gmf, gcf)
+    close(read.view(b, t, h, 8), e_read, "read")
+    close(mT, e_mT, "mean_T")
+    close(cT, e_cT, "cov_T")
+    inputs = O.mixer_inputs(*views, h)
+    e_bm, e_bc = O.checkpoints(*inputs, m0.double(), c0.double(), CHUNK, 1e-6)
+    close(bm, e_bm, "bmean")
+    close(bc, e_bc, "bcov")
+    names = ["g_q", "g_k", "g_v", "g_decay_logits", "g_noise", "g_mean0", "g_cov0"]
+    for name, a, e in zip(names, g32, e_grads):
+        close(a, e, name)
+    for name, a, e in zip(names[:5], g16[:5], g32[:5]):
+        assert a.dtype == torch.bfloat16
+        assert torch.equal(a, e.bfloat16()), f"{name} (bf16) is not the float32 gradient rounded"
+    for name, a, e in zip(names[5:], g16[5:], g32[5:]):
+        assert torch.equal(a, e), name
+    # Without final-state gradients and dynamics gradients: the readout-only
+    # loss's q/k/v gradients.
+    _, _, _, e_lean = O.mixer_grads(*views, h, m0, c0, g_read)
+    for name, a, e in zip(names[:3], lean[:3], e_lean[:3]):
+        close(a, e, f"lean {name}")
+
+
+def test_mixer_matches_reference_float32_chain(cuda_device):
+    """Same readout as the reference's own op chain run in float32 on the CPU (bayesian_layer, optimized=False)."""
+    import bayes_ssm
+
+    from bayes_ssm.mixer import bayes_mixer_core, mixer_layer_inputs
+
+    b, t, h = 2, 48, 16
+    views, _ = O.make_mixer_inputs(b, t, h, seed=31)
+    dv = _device_views(views, cuda_device)
+    read, mT, cT = bayes_mixer_core(*dv, heads=h)
+    k, v, q, dec, p, r = mixer_layer_inputs(*views, h)
+    ry, rm, rc = bayes_ssm.bayesian_layer(k, v, q, transition_diagonals=dec, process_variances=p,
+                                          observation_variances=r, chunk_length=16, optimized=False)
+    close(read, ry.view(b, h, t, 8).permute(0, 2, 1, 3), "read vs reference float32 path")
+    close(mT, rm, "mean_T")
+    close(cT, rc, "cov_T")
+
+
+@pytest.mark.parametrize("leaves", ["all", "qkv"])
+def test_mixer_autograd_boundary(cuda_device, monkeypatch, leaves):
+    """bayes_mixer_core on bf16 column views runs the fused kernels; its gradients are the C ABI's."""
+    from bayes_ssm import mixer
+
+    calls = []
+    orig = mixer._MixerCoreFunction.apply
+    monkeypatch.setattr(mixer._MixerCoreFunction, "apply", staticmethod(lambda *a: calls.append(1) or orig(*a)))
+    b, t, h = 2, 40, 32
+    views, g_read = O.make_mixer_inputs(b, t, h, seed=77, ld_pad=8)
+    base = views[0]._base.to(cuda_device)
+    dv = [torch.as_strided(base, x.shape, x.stride(), x.storage_offset()) for x in views]
+    # Leaves: the column views of one fused projection (gradients accumulate into it).
+    leaf_views = [x.detach().requires_grad_(leaves == "all" or i < 3) for i, x in enumerate(dv)]
+    m0 = torch.zeros(b * h, 4, 8, device=cuda_device, requires_grad=True)
+    read, mT, cT = mixer.bayes_mixer_core(*leaf_views, heads=h, initial_mean=m0)
+    assert calls, "fused mixer kernels were not used"
+    gy = g_read.to(cuda_device)
+    torch.autograd.backward([read], [gy])
+
+    lds = _lds(views)
+    c0 = torch.eye(4, device=cuda_device).expand(b * h, 4, 4).contiguous()
+    r2, m2, c2, bm, bc = _forward(dv, lds, m0.detach(), c0, b, t, h)
+    g32 = _backward([x.detach() for x in dv], lds, m0.detach(), c0, bm, bc, gy, None, None, b, t, h, f32=True)
+    torch.cuda.synchronize()
+    assert torch.equal(read.view(b, t, h * 8), r2)
+    assert torch.equal(mT, m2) and torch.equal(cT, c2)
+    for i, x in enumerate(leaf_views):
+        if x.requires_grad:
+            assert x.grad.dtype == torch.bfloat16
+            assert torch.equal(x.grad, g32[i].bfloat16()), f"grad of projection {i}"
+        else:
+            assert x.grad is None
+    assert torch.equal(m0.grad, g32[5])
+
+
+def test_mixer_unsupported_shapes_take_the_op_chain(cuda_device):
+    """Heads not a multiple of 16 or T not a multiple of 4: the reference op chain + bayesian_layer."""
+    from bayes_ssm import mixer
+
+    for b, t, h in ((1, 24, 8), (2, 30, 16)):
+        views, _ = O.make_mixer_inputs(b, t, h, seed=5)
+        dv = _device_views(views, cuda_device)
+        assert mixer._fused_eligible(tuple(dv), h) is None
+        read, mT, cT = mixer.bayes_mixer_core(*dv, heads=h)
+        e_read, e_mT, e_cT = O.mixer_core(*views, h)
+        close(read, e_read, f"read b={b} t={t} h={h}")
+        close(mT, e_mT, "mean_T")
+        close(cT, e_cT, "cov_T")

@@ -227,3 +227,91 @@ def test_mutation_is_detected():
     _, good, _ = O.run_diagonal(k, v, q, dec, p, r, m0, c0, 1e-6)
     _, bad, _ = O.run_diagonal(k, v, q, dec, torch.zeros_like(p), r, m0, c0, 1e-6)
     assert (good - bad).abs().max() > 1e-3
+
+
+# ------------------------------------------------------------- Bayes mixer
+def test_mixer_transforms_satisfy_identities():
+    """exp(-softplus(x)) = sigmoid(-x); softplus(x) - softplus(-x) = x; unit heads along silu(x)."""
+    b, t, h = 1, 7, 2
+    x = torch.linspace(-30.0, 30.0, b * t * h * 4).reshape(b, t, h * 4)
+    nz = torch.linspace(-25.0, 25.0, b * t * h * 2).reshape(b, t, h * 2)
+    v = torch.linspace(-6.0, 6.0, b * t * h * 8).reshape(b, t, h * 8)
+    k, vv, q, d, p, r = O.mixer_inputs(x, x, v, x, nz, h)
+    _, _, _, _, p_neg, r_neg = O.mixer_inputs(x, x, v, x, -nz, h)
+    xs = x.reshape(b, t, h, 4).transpose(1, 2).reshape(b * h, t, 4)
+    torch.testing.assert_close(d, torch.sigmoid(-xs), rtol=1e-8, atol=0)
+    nzs = nz.reshape(b, t, h, 2).transpose(1, 2).reshape(b * h, t, 2)
+    # Exact below the threshold (20); above it softplus(x) = x drops log1p(e^-x) < 2.1e-9.
+    torch.testing.assert_close(p - p_neg, nzs[..., 0], rtol=0, atol=1e-8)
+    torch.testing.assert_close(r - r_neg, nzs[..., 1], rtol=0, atol=1e-8)
+    inside = nzs.abs() < 20
+    torch.testing.assert_close((p - p_neg)[inside[..., 0]], nzs[..., 0][inside[..., 0]], rtol=0, atol=1e-12)
+    assert float((p - O.MIXER_NOISE_FLOOR).min()) > 0 and float(r.min()) > O.MIXER_NOISE_FLOOR
+    torch.testing.assert_close(k.norm(dim=-1), torch.ones(b * h, t), rtol=0, atol=1e-12)
+    a = xs / (1 + torch.exp(-xs))  # silu
+    cos = (k * a).sum(-1) / a.norm(dim=-1)
+    torch.testing.assert_close(cos, torch.ones_like(cos), rtol=0, atol=1e-12)
+    vs = v.reshape(b, t, h, 8).transpose(1, 2).reshape(b * h, t, 8)
+    torch.testing.assert_close(vv, vs / (1 + torch.exp(-vs)), rtol=1e-14, atol=1e-14)
+    # All-zero head: normalize's eps keeps it at zero instead of NaN.
+    k0, _, _, _, _, _ = O.mixer_inputs(torch.zeros(1, 1, 4), torch.zeros(1, 1, 4), torch.zeros(1, 1, 8),
+                                       torch.zeros(1, 1, 4), torch.zeros(1, 1, 2), 1)
+    assert torch.equal(k0, torch.zeros_like(k0))
+
+
+def test_mixer_sequence_map_with_tagged_heads():
+    """Sequence b*H + h, token t of every layer input is head h of batch row b at token t."""
+    b, t, h = 3, 5, 4
+    tag = torch.arange(b).view(b, 1, 1) * 1000.0 + torch.arange(t).view(1, t, 1) * 10.0 \
+        + torch.arange(h).view(1, 1, h)
+    x4 = 1e-3 * tag.repeat_interleave(4, dim=-1)
+    x8 = 1e-3 * tag.repeat_interleave(8, dim=-1)
+    x2 = 1e-3 * tag.repeat_interleave(2, dim=-1)
+    _, v, _, d, p, _ = O.mixer_inputs(x4, x4, x8, x4, x2, h)
+    for bb in range(b):
+        for hh in range(h):
+            for tt in range(t):
+                want = 1e-3 * (bb * 1000.0 + tt * 10.0 + hh)
+                n = bb * h + hh
+                assert math.isclose(float(v[n, tt, 3]), want / (1 + math.exp(-want)), rel_tol=1e-12)
+                assert math.isclose(float(d[n, tt, 0]), 1 / (1 + math.exp(want)), rel_tol=1e-12)
+                assert math.isclose(float(p[n, tt]), math.log1p(math.exp(want)) + 1e-4, rel_tol=1e-12)
+    # The readout goes back the same way: read[b, t, h] is sequence b*H + h.
+    qk = torch.randn(b, t, h * 4)
+    read, _, _ = O.mixer_core(qk, qk, x8, x4, x2, h)
+    k, vv, q, dd, pp, rr = O.mixer_inputs(qk, qk, x8, x4, x2, h)
+    y, _, _ = O.run_diagonal(k[h + 2:h + 3], vv[h + 2:h + 3], q[h + 2:h + 3], dd[h + 2:h + 3], pp[h + 2:h + 3],
+                             rr[h + 2:h + 3], torch.zeros(1, 4, 8), torch.eye(4).expand(1, 4, 4), 1e-6)
+    torch.testing.assert_close(read[1, :, 2], y[0], rtol=0, atol=0)
+
+
+def test_mixer_gradcheck():
+    views, _ = O.make_mixer_inputs(1, 3, 2, seed=5)
+    leaves = [x.double().requires_grad_(True) for x in views]
+    m0 = (0.3 * torch.randn(2, 4, 8)).requires_grad_(True)
+    c0 = (torch.eye(4) * 0.8).expand(2, 4, 4).clone().requires_grad_(True)
+
+    def fn(*xs):
+        read, mT, cT = O.mixer_core(*xs[:5], 2, xs[5], xs[6])
+        return read, mT, cT
+
+    assert torch.autograd.gradcheck(fn, (*leaves, m0, c0), eps=1e-6, atol=1e-6)
+
+
+def test_product_mixer_chain_matches_oracle():
+    """The package's unfused op chain (float32) equals the oracle's (float64) transforms."""
+    from bayes_ssm.mixer import mixer_layer_inputs
+
+    views, _ = O.make_mixer_inputs(2, 9, 3, seed=6)
+    ours = mixer_layer_inputs(*views, 3)
+    want = O.mixer_inputs(*views, 3)
+    for a, w in zip(ours, want):
+        assert a.dtype == torch.float32
+        torch.testing.assert_close(a.double(), w, rtol=1e-6, atol=1e-7)
+
+
+def test_mixer_mutation_is_detected():
+    """A planted sign error in the decay (exp(+softplus)) fails the sigmoid identity."""
+    x = torch.linspace(-4.0, 4.0, 8).reshape(1, 1, 8)
+    bad = torch.exp(O._softplus(x))
+    assert not torch.allclose(bad, torch.sigmoid(-x), rtol=1e-8, atol=0)
