@@ -186,6 +186,7 @@ def bayes_mixer_core(
     initial_covariance: Optional[Tensor] = None,
     chunk_length: Optional[int] = None,
     denominator_floor: float = 1e-6,
+    optimized: bool = True,
 ) -> tuple[Tensor, Tensor, Tensor]:
     """Readout of the mixer's exact Bayes layer from its raw projections.
 
@@ -200,7 +201,8 @@ def bayes_mixer_core(
     addressable as described in the module docstring) run the fused kernels;
     others run the reference op chain and ``bayesian_layer`` with
     ``chunk_length`` (which the fused kernels do not need: the recurrence is
-    exact for every chunk length).
+    exact for every chunk length) and ``optimized``, the mixer's own switch
+    (train_6layer.py:711, true for CUDA runs with --optimize-bayes, :987).
     """
     if q_proj.ndim != 3:
         raise ValueError("q_proj must have shape [B, T, H*4]")
@@ -223,7 +225,7 @@ def bayes_mixer_core(
     read, mean_t, cov_t = bayesian_layer(
         k, v, q, transition_diagonals=decay, process_variances=process, observation_variances=observation,
         initial_mean=initial_mean, initial_covariance=initial_covariance, chunk_length=chunk_length,
-        denominator_floor=denominator_floor)
+        denominator_floor=denominator_floor, optimized=optimized)
     read = read.view(b, heads, t, VALUE_DIM).permute(0, 2, 1, 3).contiguous()
     return read, mean_t, cov_t
 

@@ -36,18 +36,40 @@ namespace bssm {
 namespace r4 {
 namespace {
 
-constexpr float kNormEps = 1e-12f;   // F.normalize default eps
 constexpr float kNoiseFloor = 1e-4f;  // softplus(noise) + 1e-4 (train_6layer.py:667-668)
+// F.normalize divides by max(|a|, 1e-12): 1 / max(|a|, eps) = min(rsq(|a|^2), 1e12).
+constexpr float kInvNormEps = 1e12f;
+constexpr float kNormEps2 = 1e-24f;
 
-__device__ __forceinline__ float sigmoidf_(float x) { return 1.f / (1.f + __expf(-x)); }
-// torch.nn.functional.softplus (beta 1, threshold 20).
-__device__ __forceinline__ float softplusf_(float x) { return x > 20.f ? x : log1pf(__expf(x)); }
-__device__ __forceinline__ float dsoftplusf_(float x) { return x > 20.f ? 1.f : sigmoidf_(x); }
-__device__ __forceinline__ float siluf_(float x) { return x * sigmoidf_(x); }
-__device__ __forceinline__ float dsiluf_(float x) {
-  const float sg = sigmoidf_(x);
-  return sg * fmaf(x, 1.f - sg, 1.f);
+// The transforms run on the hardware exponential, reciprocal and reciprocal
+// square root (v_exp_f32, v_rcp_f32, v_rsq_f32, each within 1 ulp, the
+// exponential's argument scaled by log2 e first); the library logf/log1pf
+// and the IEEE divide cost 13 to 117 instructions each.
+__device__ __forceinline__ float exp_(float x) { return __builtin_amdgcn_exp2f(x * 1.44269504088896341f); }
+__device__ __forceinline__ float rcp_(float x) { return __builtin_amdgcn_rcpf(x); }
+__device__ __forceinline__ float sigmoid_(float x) { return rcp_(1.f + exp_(-x)); }
+
+// log(1 + u) for u in [0, 1]: 2 atanh(s) with s = u / (2 + u) <= 1/3, the
+// odd series through s^15 (next term below 2e-9 relative).
+__device__ __forceinline__ float log1p01(float u) {
+  const float s = u * rcp_(2.f + u), z = s * s;
+  float p = 1.f / 15.f;
+  p = fmaf(p, z, 1.f / 13.f);
+  p = fmaf(p, z, 1.f / 11.f);
+  p = fmaf(p, z, 1.f / 9.f);
+  p = fmaf(p, z, 1.f / 7.f);
+  p = fmaf(p, z, 1.f / 5.f);
+  p = fmaf(p, z, 1.f / 3.f);
+  p = fmaf(p, z, 1.f);
+  return 2.f * s * p;
 }
+// softplus(x) = max(x, 0) + log(1 + e^-|x|) and its derivative sigmoid(x).
+// torch's softplus returns x itself above 20, where log(1 + e^-x) < 2.1e-9
+// is below half an ulp of x, so the two agree.
+__device__ __forceinline__ float softplus_(float x) { return fmaxf(x, 0.f) + log1p01(exp_(-fabsf(x))); }
+
+// silu(x) = x sigmoid(x); silu'(x) = sigmoid(x) (1 + x (1 - sigmoid(x))).
+__device__ __forceinline__ float silu_(float x) { return x * sigmoid_(x); }
 
 // normalize(silu(x)) of one head's key or query vector.
 __device__ __forceinline__ v4f unit_silu(v4f x) {
@@ -55,35 +77,33 @@ __device__ __forceinline__ v4f unit_silu(v4f x) {
   float ss = 0.f;
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    a[i] = siluf_(x[i]);
+    a[i] = silu_(x[i]);
     ss = fmaf(a[i], a[i], ss);
   }
-  const float rn = 1.f / fmaxf(sqrtf(ss), kNormEps);
-  return a * rn;
+  return a * fminf(__builtin_amdgcn_rsqf(ss), kInvNormEps);
 }
-// Gradient through normalize(silu(x)): g is dL/d(output).
+// Gradient through normalize(silu(x)): g is dL/d(output).  Above the eps
+// clamp, d(a/|a|) = (g - w (w . g)) / |a| with w = a / |a|; below it the map
+// is a / eps.
 __device__ __forceinline__ v4f unit_silu_grad(v4f x, v4f g) {
-  v4f a;
+  v4f a, ds;
   float ss = 0.f;
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    a[i] = siluf_(x[i]);
+    const float sg = sigmoid_(x[i]);
+    a[i] = x[i] * sg;
+    ds[i] = sg * fmaf(x[i], 1.f - sg, 1.f);
     ss = fmaf(a[i], a[i], ss);
   }
-  const float n = sqrtf(ss);
-  const float rn = 1.f / fmaxf(n, kNormEps);
-  v4f out;
-  if (n > kNormEps) {
-    // (g - u (u . g)) / n with u = a / n.
-    float ug = 0.f;
+  const float rn = fminf(__builtin_amdgcn_rsqf(ss), kInvNormEps);
+  float wg = 0.f;
+  if (ss > kNormEps2) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) ug = fmaf(a[i] * rn, g[i], ug);
-#pragma unroll
-    for (int i = 0; i < 4; ++i) out[i] = fmaf(-a[i] * rn, ug, g[i]) * rn * dsiluf_(x[i]);
-  } else {
-#pragma unroll
-    for (int i = 0; i < 4; ++i) out[i] = g[i] * rn * dsiluf_(x[i]);
+    for (int i = 0; i < 4; ++i) wg = fmaf(a[i] * rn, g[i], wg);
   }
+  v4f out;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) out[i] = fmaf(-a[i] * rn, wg, g[i]) * rn * ds[i];
   return out;
 }
 
@@ -210,7 +230,7 @@ __device__ __forceinline__ void mix_put(const MixRaw& x, const MixMap& mm, float
       const v4f z = e ? widen_hi(x.dl[I]) : widen_lo(x.dl[I]);
       v4f d;
 #pragma unroll
-      for (int i = 0; i < 4; ++i) d[i] = __expf(-softplusf_(z[i]));
+      for (int i = 0; i < 4; ++i) d[i] = sigmoid_(-z[i]);  // exp(-softplus(z))
       *reinterpret_cast<v4f*>(&tile[D + mm.kq_lds[I][e]]) = d;
     }
   }
@@ -221,7 +241,7 @@ __device__ __forceinline__ void mix_put(const MixRaw& x, const MixMap& mm, float
       const v4f z = e ? widen_hi(x.v[I]) : widen_lo(x.v[I]);
       v4f o;
 #pragma unroll
-      for (int i = 0; i < 4; ++i) o[i] = siluf_(z[i]);
+      for (int i = 0; i < 4; ++i) o[i] = silu_(z[i]);
       *reinterpret_cast<v4f*>(&tile[V + mm.v_lds[I][e]]) = o;
     }
   }
@@ -230,8 +250,8 @@ __device__ __forceinline__ void mix_put(const MixRaw& x, const MixMap& mm, float
   for (int e = 0; e < 4; ++e) {
     const float zp = e < 2 ? lo[2 * e] : hi[2 * e - 4];
     const float zr = e < 2 ? lo[2 * e + 1] : hi[2 * e - 3];
-    tile[P + mm.nz_lds[e]] = softplusf_(zp) + kNoiseFloor;
-    tile[R + mm.nz_lds[e]] = softplusf_(zr) + kNoiseFloor;
+    tile[P + mm.nz_lds[e]] = softplus_(zp) + kNoiseFloor;
+    tile[R + mm.nz_lds[e]] = softplus_(zr) + kNoiseFloor;
   }
 }
 
@@ -410,7 +430,12 @@ __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(1, 1))) v
           const v4f z = e ? widen_hi(x.dl[I]) : widen_lo(x.dl[I]);
           const v4f gd = *reinterpret_cast<const v4f*>(&tile[BwdTile::D + (e ? o1 : o0)]);
 #pragma unroll
-          for (int i = 0; i < 4; ++i) out[e][i] = -gd[i] * __expf(-softplusf_(z[i])) * dsoftplusf_(z[i]);
+          for (int i = 0; i < 4; ++i) {
+            // d/dz exp(-softplus(z)) = -d sigmoid(z), d = 1 / (1 + e^z), and
+            // sigmoid(z) = e^z d below 0, 1 - d above (no cancellation either way).
+            const float u = exp_(z[i]), d = rcp_(1.f + u);
+            out[e][i] = -gd[i] * d * (z[i] > 0.f ? 1.f - d : u * d);
+          }
         }
         gr.put8(gr.dl, t * gr.rkq + gr.ckq + mm.kq_col, out[0], out[1]);
       }
@@ -424,7 +449,10 @@ __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(1, 1))) v
         const v4f z = e ? widen_hi(x.v[I]) : widen_lo(x.v[I]);
         const v4f gv = *reinterpret_cast<const v4f*>(&tile[BwdTile::V + mm.v_lds[I][e]]);
 #pragma unroll
-        for (int i = 0; i < 4; ++i) out[e][i] = gv[i] * dsiluf_(z[i]);
+        for (int i = 0; i < 4; ++i) {
+          const float sg = sigmoid_(z[i]);
+          out[e][i] = gv[i] * sg * fmaf(z[i], 1.f - sg, 1.f);
+        }
       }
       gr.put8(gr.v, t * gr.rv + gr.cv + mm.v_col, out[0], out[1]);
     }
@@ -436,8 +464,8 @@ __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(1, 1))) v
       for (int e = 0; e < 4; ++e) {
         const float zp = e < 2 ? lo[2 * e] : hi[2 * e - 4];
         const float zr = e < 2 ? lo[2 * e + 1] : hi[2 * e - 3];
-        const float gp = tile[BwdTile::P + mm.nz_lds[e]] * dsoftplusf_(zp);
-        const float grr = tile[BwdTile::R + mm.nz_lds[e]] * dsoftplusf_(zr);
+        const float gp = tile[BwdTile::P + mm.nz_lds[e]] * sigmoid_(zp);
+        const float grr = tile[BwdTile::R + mm.nz_lds[e]] * sigmoid_(zr);
         out[e >> 1][2 * (e & 1)] = gp;
         out[e >> 1][2 * (e & 1) + 1] = grr;
       }

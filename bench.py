@@ -107,6 +107,60 @@ def time_layer(b, t, h, d, m, chunk, steps, warmup, device, bf16_kqv=False) -> d
     return out
 
 
+MIXER_FWD_BYTES = 2 * 22 + 4 * 8   # bf16 q, k, decay (4 each), v (8), noise (2) in; float32 read out
+MIXER_BWD_BYTES = 2 * 22 + 4 * 8 + 2 * 22  # projections and read gradient in; bf16 projection gradients out
+
+
+def time_mixer(b, t, h, steps, warmup, device, fused=True) -> dict:
+    """fwd+bwd of the Bayes mixer's layer core from its bf16 projections (train_6layer.py:627-710).
+
+    fused: ``bayes_mixer_core`` (the producer-fused kernels).  Otherwise the
+    reference's op chain on the same GPU: the float32 transforms and permutes
+    (``mixer_layer_inputs``), ``bayesian_layer`` on the float32 layer kernels,
+    and the readout permute.  The five projections are separate bf16 leaves.
+    """
+    import bayes_ssm
+    from bayes_ssm.mixer import bayes_mixer_core, mixer_layer_inputs
+
+    gen = torch.Generator(device=device).manual_seed(3)
+    shift = {3: 2.0, 4: 0.0}
+    leaves = []
+    for i, w in enumerate((4, 4, 8, 4, 2)):
+        x = torch.randn(b, t, h * w, device=device, generator=gen) + shift.get(i, 0.0)
+        if i == 4:
+            x[..., 0::2] -= 3.0
+        leaves.append(x.to(torch.bfloat16).requires_grad_(True))
+    gy = torch.randn(b, t, h, 8, device=device, generator=gen)
+
+    def step():
+        if fused:
+            read, _, _ = bayes_mixer_core(*leaves, heads=h)
+        else:
+            k, v, q, dec, p, r = mixer_layer_inputs(*leaves, h)
+            y, _, _ = bayes_ssm.bayesian_layer(k, v, q, transition_diagonals=dec, process_variances=p,
+                                               observation_variances=r, chunk_length=64, optimized=True)
+            read = y.view(b, h, t, 8).permute(0, 2, 1, 3)
+        return torch.autograd.grad(read, leaves, gy)
+
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(steps):
+        step()
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / steps
+    out = {"B": b, "T": t, "H": h, "D": 4, "M": 8, "ms_per_step": ms, "tokens_per_s": b * t / (ms * 1e-3),
+           "path": "producer-fused kernels" if fused else "reference op chain + float32 layer kernels"}
+    if fused:
+        per = MIXER_FWD_BYTES + MIXER_BWD_BYTES
+        out["bytes_per_token_head"] = per
+        out["roofline_step_frac"] = per * b * h * t / (ms * 1e-3) / HBM_PEAK
+    return out
+
+
 def time_scan(b, t, d, m, iters, device) -> dict:
     """Forward of associative_static_bayesian_cuda (one HIP kernel): mean microseconds per call."""
     from bayes_ssm.replay_ssm import associative_static_bayesian_cuda
@@ -322,11 +376,15 @@ def main() -> int:
     if not args.no_extras:
         # Secondary shapes (not the metric): config 3 divided by 8 (one GPU's
         # share under 8-way data parallelism), the D2M8 / D8M8 variants of
-        # config 3, config 2 (D1M8, B64), and the associative-scan configs.
+        # config 3, config 2 (D1M8, B64), the mixer's layer core at config 3
+        # (fused producer kernels, and the reference op chain beside it), and
+        # the associative-scan configs.
         extras = {"config3_bf16_kqv": time_layer(b, t, h, d, m, args.chunk, 30, 10, device, bf16_kqv=True),
                   "dp8_share_d4m8": time_layer(b // 8, t, h, d, m, args.chunk, 30, 10, device)}
         for name, (eb, ed) in {"config3_d2m8": (b, 2), "config3_d8m8": (b, 8), "config2_d1m8": (64, 1)}.items():
             extras[name] = time_layer(eb, t, h, ed, m, args.chunk, 10, 3, device)
+        extras["mixer_core_config3_fused"] = time_mixer(b, t, h, 30, 10, device, fused=True)
+        extras["mixer_core_config3_op_chain"] = time_mixer(b, t, h, 10, 3, device, fused=False)
         extras["assoc_scan_config0"] = time_scan(1, 16, 4, 4, 50, device)
         extras["assoc_scan_config1"] = time_scan(4, 64, 16, 16, 50, device)
         result["extras"] = extras

@@ -306,17 +306,19 @@ def mixer_grads(q_proj, k_proj, v_proj, decay_logits, noise, heads: int, mean0, 
     return read.detach(), mT.detach(), cT.detach(), list(grads)
 
 
-def make_mixer_inputs(b: int, t: int, heads: int, *, seed: int = 0, ld_pad: int = 0):
+def make_mixer_inputs(b: int, t: int, heads: int, *, seed: int = 0, ld_pad: int = 0, scale: float = 1.0):
     """Seeded bf16 projections of the mixer (CPU tensors), drawn as one fused projection.
 
     Draw order: one [B, T, H*22 + ld_pad] N(0,1) block whose columns are
     q (H*4), k (H*4), v (H*8), decay logits (H*4, shifted by +2) and noise
     (H*2, process logits shifted by -3); the five are returned as column
     views (row stride H*22 + ld_pad), then the readout gradient [B, T, H, 8].
+    ``scale`` multiplies the N(0,1) draw (before the shifts): large values
+    reach the saturated ends of silu, sigmoid and softplus.
     """
     gen = torch.Generator().manual_seed(seed)
     width = heads * 22 + ld_pad
-    fused = torch.randn(b, t, width, generator=gen)
+    fused = scale * torch.randn(b, t, width, generator=gen)
     fused[..., heads * 16:heads * 20] += 2.0
     fused[..., heads * 20:heads * 22:2] -= 3.0
     fused = fused.to(torch.bfloat16)

@@ -83,19 +83,20 @@ def _backward(dv, lds, m0, c0, bm, bc, gy, gmf, gcf, b, t, h, *, f32, dyn=True, 
     return grads + [gm0, gc0]
 
 
-CASES = [  # batch, tokens, heads, extra row padding of the fused projection (elements)
-    (2, 36, 16, 0),
-    (1, 64, 32, 8),
-    (3, 20, 16, 24),
-    (1, 4, 16, 0),
-    (2, 100, 48, 16),
+CASES = [  # batch, tokens, heads, extra row padding of the fused projection (elements), input scale
+    (2, 36, 16, 0, 1.0),
+    (1, 64, 32, 8, 1.0),
+    (3, 20, 16, 24, 1.0),
+    (1, 4, 16, 0, 1.0),
+    (2, 100, 48, 16, 1.0),
+    (2, 24, 16, 8, 6.0),  # logits beyond +-20: saturated sigmoid/silu, softplus threshold
 ]
 
 
-@pytest.mark.parametrize("b,t,h,pad", CASES)
-def test_mixer_abi_matches_oracle(cuda_device, b, t, h, pad):
-    print(f"mixer abi b={b} t={t} h={h} pad={pad}", flush=True)
-    views, g_read = O.make_mixer_inputs(b, t, h, seed=900 + t, ld_pad=pad)
+@pytest.mark.parametrize("b,t,h,pad,scale", CASES)
+def test_mixer_abi_matches_oracle(cuda_device, b, t, h, pad, scale):
+    print(f"mixer abi b={b} t={t} h={h} pad={pad} scale={scale}", flush=True)
+    views, g_read = O.make_mixer_inputs(b, t, h, seed=900 + t, ld_pad=pad, scale=scale)
     n = b * h
     m0, c0, gmf, gcf = _state(n, seed=t)
     dv = _device_views(views, cuda_device)
