@@ -230,4 +230,132 @@ def bayes_mixer_core(
     return read, mean_t, cov_t
 
 
-__all__ = ["bayes_mixer_core", "mixer_layer_inputs"]
+class _MixerReadoutFunction(torch.autograd.Function):
+    """Autograd boundary of the gated kernels (C ABI ``bssm_mixer_gated_*``)."""
+
+    @staticmethod
+    def forward(ctx, q_proj, k_proj, v_proj, decay_logits, noise, gate, norm_weight, initial_mean,
+                initial_covariance, heads, norm_eps, denominator_floor, lds):
+        b, t, _ = q_proj.shape
+        n = b * heads
+        interval = _hip.preferred_checkpoint(KEY_DIM)
+        nb = -(-t // interval)
+        dev = q_proj.device
+        out = torch.empty(b, t, heads * VALUE_DIM, device=dev, dtype=torch.bfloat16)
+        read_bf16 = torch.empty_like(out)
+        mean_t = torch.empty(n, KEY_DIM, VALUE_DIM, device=dev, dtype=torch.float32)
+        cov_t = torch.empty(n, KEY_DIM, KEY_DIM, device=dev, dtype=torch.float32)
+        bmean = torch.empty(n, nb + 1, KEY_DIM, VALUE_DIM, device=dev, dtype=torch.float32)
+        bcov = torch.empty(n, nb + 1, KEY_DIM, KEY_DIM, device=dev, dtype=torch.float32)
+        w32 = norm_weight.detach().float().contiguous()
+        P = _hip.ptr
+        with torch.cuda.device(dev):
+            _hip.call("bssm_mixer_gated_forward", P(q_proj), lds[0], P(k_proj), lds[1], P(v_proj), lds[2],
+                      P(decay_logits), lds[3], P(noise), lds[4], P(gate), lds[5], P(w32), float(norm_eps),
+                      P(initial_mean), P(initial_covariance), P(out), P(read_bf16), P(mean_t), P(cov_t), P(bmean),
+                      P(bcov), b, t, heads, interval, float(denominator_floor), 0, _hip.stream_of(dev))
+        ctx.save_for_backward(q_proj, k_proj, v_proj, decay_logits, noise, gate, w32, initial_mean,
+                              initial_covariance, bmean, bcov, read_bf16)
+        ctx.heads = heads
+        ctx.interval = interval
+        ctx.lds = lds
+        ctx.norm_eps = float(norm_eps)
+        ctx.weight_dtype = norm_weight.dtype
+        ctx.denominator_floor = float(denominator_floor)
+        ctx.set_materialize_grads(False)
+        return out, mean_t, cov_t
+
+    @staticmethod
+    def backward(ctx, grad_out, grad_mean, grad_covariance):
+        (q_proj, k_proj, v_proj, decay_logits, noise, gate, w32, mean0, cov0, bmean, bcov,
+         read_bf16) = ctx.saved_tensors
+        b, t, _ = q_proj.shape
+        heads, lds = ctx.heads, ctx.lds
+        need = ctx.needs_input_grad
+        dev = q_proj.device
+        if grad_out is None:
+            grad_out = torch.zeros(b, t, heads * VALUE_DIM, device=dev, dtype=torch.bfloat16)
+        else:
+            grad_out = grad_out.to(torch.bfloat16).contiguous()
+        gm = None if grad_mean is None else grad_mean.float().contiguous()
+        gc = None if grad_covariance is None else grad_covariance.float().contiguous()
+
+        def empty(x: Tensor) -> Tensor:
+            return torch.empty(x.shape, device=dev, dtype=torch.bfloat16)
+
+        gq, gk, gv = empty(q_proj), empty(k_proj), empty(v_proj)
+        dyn = need[3] or need[4]
+        gdl = empty(decay_logits) if dyn else None
+        gnz = empty(noise) if dyn else None
+        ggate = empty(gate)
+        partials = torch.empty(b * heads // 16, VALUE_DIM, device=dev, dtype=torch.float32)
+        gm0 = torch.empty_like(mean0) if need[7] else None
+        gc0 = torch.empty_like(cov0) if need[8] else None
+        P = _hip.ptr
+        with torch.cuda.device(dev):
+            _hip.call("bssm_mixer_gated_backward", P(q_proj), lds[0], P(k_proj), lds[1], P(v_proj), lds[2],
+                      P(decay_logits), lds[3], P(noise), lds[4], P(gate), lds[5], P(w32), ctx.norm_eps, P(mean0),
+                      P(cov0), P(bmean), P(bcov), P(read_bf16), P(grad_out), P(gm), P(gc), P(gq), P(gk), P(gv),
+                      P(gdl), P(gnz), P(ggate), P(partials), P(gm0), P(gc0), b, t, heads, ctx.interval,
+                      ctx.denominator_floor, 0, _hip.stream_of(dev))
+        gw = partials.sum(0).to(ctx.weight_dtype) if need[6] else None
+        return (gq if need[0] else None, gk if need[1] else None, gv if need[2] else None,
+                gdl if need[3] else None, gnz if need[4] else None, ggate if need[5] else None, gw, gm0, gc0,
+                None, None, None, None)
+
+
+def bayes_mixer_readout(
+    q_proj: Tensor,
+    k_proj: Tensor,
+    v_proj: Tensor,
+    decay_logits: Tensor,
+    noise: Tensor,
+    gate: Tensor,
+    norm_weight: Tensor,
+    *,
+    heads: int,
+    norm_eps: Optional[float] = None,
+    initial_mean: Optional[Tensor] = None,
+    initial_covariance: Optional[Tensor] = None,
+    chunk_length: Optional[int] = None,
+    denominator_floor: float = 1e-6,
+    optimized: bool = True,
+) -> tuple[Tensor, Tensor, Tensor]:
+    """The mixer's gated readout from its raw projections (train_6layer.py:627-729, up to ``out_proj``).
+
+    Computes ``bayes_mixer_core`` and then, per head of 8 values,
+    ``read_norm(read.to(bf16)) * silu(gate)``: read_norm is an RMSNorm with
+    weight ``norm_weight`` [8] and ``norm_eps`` (None: the float32 epsilon,
+    as torch's rms_norm with eps None).  gate: [B, T, H*8].  Returns the
+    product as [B, T, H*8] (what the reference reshapes and feeds to
+    out_proj; bf16) and the final mean and covariance.
+
+    On the fused path (the conditions of ``bayes_mixer_core``, plus a bf16
+    gate with rows the kernels can address) the product is formed in float32
+    and rounded once, the readout never reaches HBM in float32, and the
+    backward forms the readout gradient on chip.  Otherwise the op chain runs
+    in torch.
+    """
+    b, t = q_proj.shape[:2]
+    if tuple(gate.shape) != (b, t, VALUE_DIM * heads):
+        raise ValueError(f"gate must have shape [B, T, H*8] = {(b, t, VALUE_DIM * heads)}, got {tuple(gate.shape)}")
+    if tuple(norm_weight.shape) != (VALUE_DIM,):
+        raise ValueError("norm_weight must have shape [8]")
+    eps = torch.finfo(torch.float32).eps if norm_eps is None else float(norm_eps)
+    projections = (q_proj, k_proj, v_proj, decay_logits, noise)
+    lds = _fused_eligible(projections, heads)
+    ldg = _row_stride(gate, t) if gate.dtype == torch.bfloat16 and gate.device == q_proj.device else None
+    if lds is not None and ldg is not None:
+        _hip.load()
+        mean0, cov0 = _initial_state(initial_mean, initial_covariance, b * heads, q_proj.device)
+        return _MixerReadoutFunction.apply(q_proj, k_proj, v_proj, decay_logits, noise, gate, norm_weight, mean0,
+                                           cov0, int(heads), eps, float(denominator_floor), (*lds, ldg))
+    read, mean_t, cov_t = bayes_mixer_core(*projections, heads=heads, initial_mean=initial_mean,
+                                           initial_covariance=initial_covariance, chunk_length=chunk_length,
+                                           denominator_floor=denominator_floor, optimized=optimized)
+    normed = F.rms_norm(read.to(gate.dtype), (VALUE_DIM,), norm_weight, eps)
+    out = (normed * F.silu(gate.view(b, t, heads, VALUE_DIM))).reshape(b, t, heads * VALUE_DIM)
+    return out, mean_t, cov_t
+
+
+__all__ = ["bayes_mixer_core", "bayes_mixer_readout", "mixer_layer_inputs"]

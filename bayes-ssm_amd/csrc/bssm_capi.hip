@@ -212,13 +212,30 @@ int mixer_check(const char* fn, const void* const (&in)[5], const int64_t (&ld)[
   return BSSM_OK;
 }
 
+// Checks of the readout-epilogue streams (gate view; contiguous [B, T, H * 8] tensors).
+int epilogue_check(const char* fn, const void* gate, int64_t ldg, const float* norm_weight, float norm_eps,
+                   std::initializer_list<const void*> contiguous, int64_t b, int64_t t, int64_t h) {
+  if (b * h * t > 0 && (gate == nullptr || norm_weight == nullptr))
+    return fail(BSSM_ERR_ARGUMENT, "%s: gate and norm_weight are required", fn);
+  if (ldg < 8 * h || ldg % 8 != 0 || !aligned16(gate))
+    return fail(BSSM_ERR_UNSUPPORTED, "%s: gate needs a row stride >= %lld elements, a multiple of 8, and a 16-byte "
+                "aligned base (got ld=%lld)", fn, (long long)(8 * h), (long long)ldg);
+  if ((t + 16) * ldg * 2 >= ((int64_t)1 << 31))
+    return fail(BSSM_ERR_ARGUMENT, "%s: T * ld of gate too large for 32-bit stream offsets", fn);
+  if (!(norm_eps >= 0.f)) return fail(BSSM_ERR_ARGUMENT, "%s: norm_eps must be non-negative", fn);
+  for (const void* p : contiguous)
+    if (b * h * t > 0 && (p == nullptr || !aligned16(p)))
+      return fail(BSSM_ERR_ARGUMENT, "%s: epilogue tensors must be non-null and 16-byte aligned", fn);
+  return BSSM_OK;
+}
+
 }  // namespace
 
 extern "C" {
 
 const char* bssm_last_error(void) { return g_error; }
 
-int bssm_abi_version(void) { return 3; }
+int bssm_abi_version(void) { return 4; }
 
 int bssm_supported(int key_dim, int value_dim) { return supported(key_dim, value_dim) ? 1 : 0; }
 
@@ -520,6 +537,86 @@ int bssm_mixer_backward(const void* q_proj, int64_t ldq, const void* k_proj, int
   a.gm0 = gm0; a.gc0 = gc0;
   a.b = batch; a.t = t; a.h = heads; a.chunk = chunk; a.nb = (t + chunk - 1) / chunk; a.floor = denominator_floor;
   a.grad_f32 = grad_f32 != 0;
+  if (n == 0) return ok();
+  return launched(fn, bssm::launch_mixer_backward(a, static_cast<hipStream_t>(stream)));
+}
+
+int bssm_mixer_gated_forward(const void* q_proj, int64_t ldq, const void* k_proj, int64_t ldk, const void* v_proj,
+                             int64_t ldv, const void* decay_logits, int64_t ldd, const void* noise, int64_t ldn,
+                             const void* gate, int64_t ldg, const float* norm_weight, float norm_eps,
+                             const float* mean0, const float* cov0, void* out, void* read_bf16, float* mean_final,
+                             float* cov_final, float* bmean, float* bcov, int64_t batch, int64_t t, int64_t heads,
+                             int64_t chunk, float denominator_floor, int precise, void* stream) {
+  const char* fn = "bssm_mixer_gated_forward";
+  if (int rc = mixer_check(fn, {q_proj, k_proj, v_proj, decay_logits, noise}, {ldq, ldk, ldv, ldd, ldn}, batch, t,
+                           heads, chunk, denominator_floor))
+    return rc;
+  if (int rc = epilogue_check(fn, gate, ldg, norm_weight, norm_eps, {out, read_bf16}, batch, t, heads)) return rc;
+  const int64_t n = batch * heads;
+  BSSM_REQUIRE(mean0);
+  BSSM_REQUIRE(cov0);
+  BSSM_REQUIRE(mean_final);
+  BSSM_REQUIRE(cov_final);
+  BSSM_REQUIRE(bmean);
+  BSSM_REQUIRE(bcov);
+  for (const void* p : {(const void*)mean0, (const void*)cov0, (const void*)mean_final, (const void*)cov_final,
+                        (const void*)bmean, (const void*)bcov})
+    if (p != nullptr && !aligned8(p)) return fail(BSSM_ERR_ARGUMENT, "%s: belief tensors must be 8-byte aligned", fn);
+  bssm::MixArgs a{};
+  a.q = q_proj; a.k = k_proj; a.v = v_proj; a.dl = decay_logits; a.nz = noise;
+  a.ldq = ldq; a.ldk = ldk; a.ldv = ldv; a.ldd = ldd; a.ldn = ldn;
+  a.m0 = mean0; a.c0 = cov0; a.mT = mean_final; a.cT = cov_final; a.bm = bmean; a.bc = bcov;
+  a.gate = gate; a.ldg = ldg; a.norm_w = norm_weight; a.norm_eps = norm_eps; a.out = out; a.yb = read_bf16;
+  a.precise = precise != 0;
+  a.b = batch; a.t = t; a.h = heads; a.chunk = chunk; a.nb = (t + chunk - 1) / chunk; a.floor = denominator_floor;
+  if (n == 0) return ok();
+  return launched(fn, bssm::launch_mixer_forward(a, static_cast<hipStream_t>(stream)));
+}
+
+int bssm_mixer_gated_backward(const void* q_proj, int64_t ldq, const void* k_proj, int64_t ldk, const void* v_proj,
+                              int64_t ldv, const void* decay_logits, int64_t ldd, const void* noise, int64_t ldn,
+                              const void* gate, int64_t ldg, const float* norm_weight, float norm_eps,
+                              const float* mean0, const float* cov0, const float* bmean, const float* bcov,
+                              const void* read_bf16, const void* grad_out, const float* gmf, const float* gcf,
+                              void* grad_q, void* grad_k, void* grad_v, void* grad_decay_logits, void* grad_noise,
+                              void* grad_gate, float* grad_norm_weight_partials, float* gm0, float* gc0,
+                              int64_t batch, int64_t t, int64_t heads, int64_t chunk, float denominator_floor,
+                              int precise, void* stream) {
+  const char* fn = "bssm_mixer_gated_backward";
+  if (int rc = mixer_check(fn, {q_proj, k_proj, v_proj, decay_logits, noise}, {ldq, ldk, ldv, ldd, ldn}, batch, t,
+                           heads, chunk, denominator_floor))
+    return rc;
+  if (int rc = epilogue_check(fn, gate, ldg, norm_weight, norm_eps,
+                              {read_bf16, grad_out, grad_gate, grad_norm_weight_partials}, batch, t, heads))
+    return rc;
+  const int64_t n = batch * heads;
+  if ((grad_decay_logits == nullptr) != (grad_noise == nullptr))
+    return fail(BSSM_ERR_ARGUMENT, "%s: grad_decay_logits and grad_noise must be given together or both be null", fn);
+  BSSM_REQUIRE(mean0);
+  BSSM_REQUIRE(cov0);
+  BSSM_REQUIRE(bmean);
+  BSSM_REQUIRE(bcov);
+  BSSM_REQUIRE_T(grad_q);
+  BSSM_REQUIRE_T(grad_k);
+  BSSM_REQUIRE_T(grad_v);
+  for (const void* p : {(const void*)bmean, (const void*)bcov, (const void*)gmf, (const void*)gcf, (const void*)gm0,
+                        (const void*)gc0})
+    if (p != nullptr && !aligned8(p)) return fail(BSSM_ERR_ARGUMENT, "%s: belief tensors must be 8-byte aligned", fn);
+  for (const void* p : {(const void*)grad_q, (const void*)grad_k, (const void*)grad_v,
+                        (const void*)grad_decay_logits, (const void*)grad_noise})
+    if (p != nullptr && !aligned16(p))
+      return fail(BSSM_ERR_ARGUMENT, "%s: the projection gradients must be 16-byte aligned", fn);
+  bssm::MixArgs a{};
+  a.q = q_proj; a.k = k_proj; a.v = v_proj; a.dl = decay_logits; a.nz = noise;
+  a.ldq = ldq; a.ldk = ldk; a.ldv = ldv; a.ldd = ldd; a.ldn = ldn;
+  a.m0 = mean0; a.c0 = cov0; a.bmr = bmean; a.bcr = bcov; a.gmf = gmf; a.gcf = gcf;
+  a.gq = grad_q; a.gk = grad_k; a.gv = grad_v; a.gdl = grad_decay_logits; a.gnz = grad_noise;
+  a.gm0 = gm0; a.gc0 = gc0;
+  a.gate = gate; a.ldg = ldg; a.norm_w = norm_weight; a.norm_eps = norm_eps; a.yb = const_cast<void*>(read_bf16);
+  a.gout = grad_out; a.ggate = grad_gate; a.gw_part = grad_norm_weight_partials;
+  a.precise = precise != 0;
+  a.grad_f32 = precise != 0;
+  a.b = batch; a.t = t; a.h = heads; a.chunk = chunk; a.nb = (t + chunk - 1) / chunk; a.floor = denominator_floor;
   if (n == 0) return ok();
   return launched(fn, bssm::launch_mixer_backward(a, static_cast<hipStream_t>(stream)));
 }

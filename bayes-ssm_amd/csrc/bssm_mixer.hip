@@ -255,6 +255,80 @@ __device__ __forceinline__ void mix_put(const MixRaw& x, const MixMap& mm, float
   }
 }
 
+// ------------------------------------------------------------ readout epilogue
+// The mixer's readout (train_6layer.py:719-729) per head of 8 values:
+//   out = RMSNorm(bf16(read)) * w * silu(gate),
+// where RMSNorm computes in float32, eps defaulting to the float32 epsilon
+// (torch's rms_norm with eps None).  Here the whole product is formed in
+// float32 and rounded to bf16 once.  A head's 8 values sit in a lane pair
+// (half = lane & 1 holds values 4 half .. + 3), so the squared norm and the
+// backward's dot product are completed with one DPP exchange.
+
+// Four bf16 values (a 64-bit piece) to float32, and float32 to a bf16 piece.
+__device__ __forceinline__ v4f widen4(v2f piece) {
+  const v2u w = __builtin_bit_cast(v2u, piece);
+  v4f out;
+  out[0] = __builtin_bit_cast(float, w[0] << 16);
+  out[1] = __builtin_bit_cast(float, w[0] & 0xffff0000u);
+  out[2] = __builtin_bit_cast(float, w[1] << 16);
+  out[3] = __builtin_bit_cast(float, w[1] & 0xffff0000u);
+  return out;
+}
+__device__ __forceinline__ v2f narrow4(v4f x) {
+  v2u w;
+  w[0] = narrow2(x[0], x[1]);
+  w[1] = narrow2(x[2], x[3]);
+  return __builtin_bit_cast(v2f, w);
+}
+
+// Buffer descriptors and lane offsets of the epilogue's [B, T, H * 8] streams
+// (bf16 unless noted) for one batch row.
+struct MixEpi {
+  Rsrc gate, out, yb, gout, ggate;
+  uint32_t rg, cg;    // gate row bytes; lane byte offset in a row
+  uint32_t ro, co;    // contiguous bf16 rows (H * 16 bytes); lane byte offset
+  float w[4], eps;
+  bool precise;
+  __device__ __forceinline__ MixEpi(const MixArgs& a, int64_t bb, int64_t h0, int lane, bool backward) {
+    const int64_t T = a.t;
+    const uint32_t yh = static_cast<uint32_t>((lane >> 1) & 15), half = static_cast<uint32_t>(lane & 1);
+    precise = a.precise != 0;
+    rg = static_cast<uint32_t>(a.ldg * 2);
+    cg = (static_cast<uint32_t>(h0) + yh) * 16u + half * 8u;
+    ro = static_cast<uint32_t>(a.h) * 16u;
+    co = cg;
+    const uint32_t tro = static_cast<uint32_t>(T) * ro, trw = precise ? 2u * tro : tro;
+    gate = make_rsrc(as_f(a.gate, bb * T * rg), static_cast<uint32_t>(T) * rg);
+    yb = make_rsrc(as_f(a.yb, bb * tro), tro);
+    if (backward) {
+      gout = make_rsrc(as_f(a.gout, bb * tro), tro);
+      ggate = make_rsrc(as_f(a.ggate, bb * trw), trw);
+      out = gout;
+    } else {
+      out = make_rsrc(as_f(a.out, bb * trw), trw);
+      gout = ggate = out;
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) w[i] = a.norm_w[4 * half + i];
+    eps = a.norm_eps;
+  }
+  // 1 / sqrt(mean of the head's 8 squares + eps), from this lane's four values.
+  __device__ __forceinline__ float inv_rms(v4f x) const {
+    float ss = x[0] * x[0];
+#pragma unroll
+    for (int i = 1; i < 4; ++i) ss = fmaf(x[i], x[i], ss);
+    ss += dpp<kXor1>(ss);
+    return __builtin_amdgcn_rsqf(fmaf(ss, 0.125f, eps));
+  }
+  // Store a float32 result as bf16 (or float32 when precise) at byte offset
+  // off of the bf16 layout.
+  __device__ __forceinline__ void put4(Rsrc r, uint32_t off, v4f x) const {
+    if (precise) st128<kNtStore>(r, x, 2u * off, 0);
+    else st64(r, narrow4(x), off, 0);
+  }
+};
+
+template <bool EPI>
 __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(1, 1))) void mixer_forward_kernel(MixArgs a) {
   __shared__ float tile[2 * FwdTile::SIZE];
   __shared__ float ckst[kRecFloats];
@@ -267,8 +341,9 @@ __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(1, 1))) v
   const uint32_t yrow = static_cast<uint32_t>(a.h) * 32u;
   const MixRows rows(a, bb, h0);
   const MixMap mm(lane, FwdTile::SIZE);
-  const Rsrc ry = make_rsrc(a.y + bb * T * a.h * 8, static_cast<uint32_t>(T) * yrow);
+  const Rsrc ry = make_rsrc(EPI ? a.m0 : a.y + bb * T * a.h * 8, EPI ? 0u : static_cast<uint32_t>(T) * yrow);
   const uint32_t ycol = static_cast<uint32_t>(h0) * 32u + mm.y_col;
+  const MixEpi ep(a, bb, h0, lane, false);
   const Rsrc rbm = make_rsrc(a.bm + n0 * nbp * 32, SPW * nbp * 128u);
   const Rsrc rbc = make_rsrc(a.bc + n0 * nbp * 16, SPW * nbp * 64u);
   const Rsrc rm0 = make_rsrc(a.m0 + n0 * 32, SPW * 128u);
@@ -288,13 +363,36 @@ __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(1, 1))) v
 #pragma unroll
     for (int I = 0; I < 8; ++I) o.y[I] = *reinterpret_cast<const v4f*>(&tile[FwdTile::V + mm.y_lds[I]]);
   };
-  auto store_y = [&](const Out& o, int64_t t0) __attribute__((always_inline)) {
+  // Gate pieces of the tile whose readouts are stored next.
+  v2f gt[8];
+  auto load_gate = [&](int64_t t0) __attribute__((always_inline)) {
 #pragma unroll
     for (int I = 0; I < 8; ++I)
-      st128<kNtStore>(ry, o.y[I], static_cast<uint32_t>(t0 + mm.y_tok[I]) * yrow + ycol, 0);
+      gt[I] = __builtin_bit_cast(v2f, __builtin_amdgcn_raw_buffer_load_b64(
+                                           ep.gate, static_cast<int>((t0 + mm.y_tok[I]) * ep.rg + ep.cg), 0, 0));
+  };
+  auto store_y = [&](const Out& o, int64_t t0) __attribute__((always_inline)) {
+#pragma unroll
+    for (int I = 0; I < 8; ++I) {
+      const uint32_t t = static_cast<uint32_t>(t0 + mm.y_tok[I]);
+      if constexpr (EPI) {
+        const v2f yb = narrow4(o.y[I]);  // read.to(bf16)
+        const v4f y = widen4(yb), z = widen4(gt[I]);
+        const float r = ep.inv_rms(y);
+        v4f x;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) x[i] = y[i] * r * ep.w[i] * silu_(z[i]);
+        ep.put4(ep.out, t * ep.ro + ep.co, x);
+        st64(ep.yb, yb, t * ep.ro + ep.co, 0);
+      } else {
+        st128<kNtStore>(ry, o.y[I], t * yrow + ycol, 0);
+      }
+    }
   };
 
-  // As the float32 forward: tile i + 1 loads while tile i computes.
+  // As the float32 forward: tile i + 1 loads while tile i computes; with the
+  // epilogue, the gate of tile i loads then too (it is used when tile i's
+  // readouts leave, during tile i + 1).
   const int64_t ntiles = (T + LT - 1) / LT;
   MixRaw st;
   rows.load(st, mm, 0);
@@ -306,6 +404,7 @@ __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(1, 1))) v
     __builtin_amdgcn_sched_barrier(0);
     if (i > 0) store_y(yo, (i - 1) * LT);
     if (i + 1 < ntiles) rows.load(st, mm, (i + 1) * LT);
+    if constexpr (EPI) load_gate(i * LT);
     __builtin_amdgcn_sched_barrier(0);
     const int64_t t0 = i * LT;
     core.run_sub(tile, t0, T);
@@ -358,7 +457,7 @@ struct MixGrads {
   }
 };
 
-template <bool DYN>
+template <bool DYN, bool EPI>
 __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(1, 1))) void mixer_backward_kernel(
     MixArgs a) {
   __shared__ float tile[2 * BwdTile::SIZE];
@@ -372,8 +471,13 @@ __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(1, 1))) v
   const MixRows rows(a, bb, h0);
   const MixGrads gr(a, bb, h0);
   const MixMap mm(lane, BwdTile::SIZE);
-  const Rsrc rgy = make_rsrc(a.gy + bb * T * a.h * 8, static_cast<uint32_t>(T) * yrow);
+  const Rsrc rgy = make_rsrc(EPI ? a.m0 : a.gy + bb * T * a.h * 8, EPI ? 0u : static_cast<uint32_t>(T) * yrow);
   const uint32_t ycol = static_cast<uint32_t>(h0) * 32u + mm.y_col;
+  const MixEpi ep(a, bb, h0, lane, true);
+  // This lane's share of the norm-weight gradient, summed in LDS (a
+  // loop-carried register set would push the kernel past the register file).
+  __shared__ v4f dwl[EPI ? kWave : 1];
+  if constexpr (EPI) dwl[lane] = v4f{0.f, 0.f, 0.f, 0.f};
   const Rsrc rbm = make_rsrc(a.bmr + n0 * nbp * 32, SPW * nbp * 128u);
   const Rsrc rbc = make_rsrc(a.bcr + n0 * nbp * 16, SPW * nbp * 64u);
   const RecOff ckoff(lane, nbp * 128u, nbp * 64u);
@@ -386,19 +490,69 @@ __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(1, 1))) v
 
   struct Stage {
     MixRaw raw;
-    v4f gy[8];
+    v4f gy[8];  // without the epilogue
   };
-  auto load = [&](Stage& x, int64_t J) __attribute__((always_inline)) {
+  // Epilogue pieces of one sub-tile h (readout map instructions 4h .. 4h + 3).
+  struct EpiHalf {
+    v2f go[4], yb[4], gt[4];
+  };
+  auto load_raw = [&](Stage& x, int64_t J) __attribute__((always_inline)) { rows.load(x.raw, mm, J * 2 * SUB); };
+  auto load_y = [&](Stage& x, int64_t J) __attribute__((always_inline)) {
     const int64_t t0 = J * 2 * SUB;
-    rows.load(x.raw, mm, t0);
 #pragma unroll
     for (int I = 0; I < 8; ++I)
       x.gy[I] = ld128<kNtLoad>(rgy, static_cast<uint32_t>(t0 + mm.y_tok[I]) * yrow + ycol);
   };
-  auto put = [&](const Stage& x) __attribute__((always_inline)) {
-    mix_put<BwdTile::K, BwdTile::Q, BwdTile::D, BwdTile::V, BwdTile::P, BwdTile::R>(x.raw, mm, tile);
+  auto load_epi = [&](EpiHalf& x, int64_t J, int h) __attribute__((always_inline)) {
+    const int64_t t0 = J * 2 * SUB;
 #pragma unroll
-    for (int I = 0; I < 8; ++I) *reinterpret_cast<v4f*>(&tile[BwdTile::GY + mm.y_lds[I]]) = x.gy[I];
+    for (int i = 0; i < 4; ++i) {
+      const uint32_t t = static_cast<uint32_t>(t0 + mm.y_tok[4 * h + i]);
+      x.go[i] = ld64(ep.gout, t * ep.ro + ep.co, 0);
+      x.yb[i] = ld64(ep.yb, t * ep.ro + ep.co, 0);
+      x.gt[i] = ld64(ep.gate, t * ep.rg + ep.cg, 0);
+    }
+  };
+  auto put = [&](const Stage& x, int64_t J) __attribute__((always_inline)) {
+    mix_put<BwdTile::K, BwdTile::Q, BwdTile::D, BwdTile::V, BwdTile::P, BwdTile::R>(x.raw, mm, tile);
+    if constexpr (!EPI) {
+#pragma unroll
+      for (int I = 0; I < 8; ++I) *reinterpret_cast<v4f*>(&tile[BwdTile::GY + mm.y_lds[I]]) = x.gy[I];
+    }
+  };
+  // The readout gradient gy of sub-tile h of tile J into LDS, per head
+  // (n = y r, h = n w, out = h silu(z)):
+  //   dL/dh = gout silu(z),  dL/dz = gout h silu'(z),  dL/dw += dL/dh n,
+  //   gy = r (dL/dn - n mean(dL/dn n)) with dL/dn = dL/dh w.
+  auto put_epi = [&](const EpiHalf& x, int64_t J, int h) __attribute__((always_inline)) {
+    v4f dw = dwl[lane];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int I = 4 * h + i;
+      const v4f y = widen4(x.yb[i]), z = widen4(x.gt[i]), go = widen4(x.go[i]);
+      const float r = ep.inv_rms(y);
+      v4f gz, gn, n;
+      float dot = 0.f;
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        const float sg = sigmoid_(z[c]), sz = z[c] * sg;  // silu(z)
+        const float dsz = fmaf(sz, -sg, sg + sz);         // silu'(z) = sg + silu(z) (1 - sg)
+        n[c] = y[c] * r;
+        const float gh = go[c] * sz;
+        gz[c] = go[c] * (n[c] * ep.w[c]) * dsz;
+        gn[c] = gh * ep.w[c];
+        dw[c] = fmaf(gh, n[c], dw[c]);
+        dot = fmaf(gn[c], n[c], dot);
+      }
+      dot += dpp<kXor1>(dot);
+      v4f gy;
+#pragma unroll
+      for (int c = 0; c < 4; ++c) gy[c] = r * fmaf(-n[c], dot * 0.125f, gn[c]);
+      *reinterpret_cast<v4f*>(&tile[BwdTile::GY + mm.y_lds[I]]) = gy;
+      const uint32_t t = static_cast<uint32_t>(J * 2 * SUB + mm.y_tok[I]);
+      ep.put4(ep.ggate, t * ep.ro + ep.co, gz);
+    }
+    dwl[lane] = dw;
   };
   auto issue_ck = [&](float* tl, int64_t c) __attribute__((always_inline)) {
     lds_wait();
@@ -408,11 +562,14 @@ __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(1, 1))) v
     dma16(rbc, (tl + BwdTile::CK) + 512, ckoff.c + cc);
   };
   // Projection gradients of tile J: the reverse left dL/d(transformed input)
-  // in the LDS regions; the raw pieces of the tile give the chain rule.
-  auto write_grads = [&](const MixRaw& x, int64_t J) __attribute__((always_inline)) {
+  // in the LDS regions; the raw pieces of the tile give the chain rule.  The
+  // pieces of tokens 8..15 (q, k, decay I = 1; v I = 2, 3) are written once
+  // chunk 2J + 1 is reversed (HI), the rest and the noise once chunk 2J is
+  // (LO), so half of the kept pieces are free during chunk 2J.
+  auto write_grads = [&](const MixRaw& x, int64_t J, bool hi) __attribute__((always_inline)) {
     const int64_t t0 = J * 2 * SUB;
 #pragma unroll
-    for (int I = 0; I < 2; ++I) {
+    for (int I = hi ? 1 : 0; I < (hi ? 2 : 1); ++I) {
       const uint32_t t = static_cast<uint32_t>(t0 + mm.kq_tok[I]);
       const int o0 = mm.kq_lds[I][0], o1 = mm.kq_lds[I][1];
       const v4f gk0 = *reinterpret_cast<const v4f*>(&tile[BwdTile::K + o0]);
@@ -441,7 +598,7 @@ __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(1, 1))) v
       }
     }
 #pragma unroll
-    for (int I = 0; I < 4; ++I) {
+    for (int I = hi ? 2 : 0; I < (hi ? 4 : 2); ++I) {
       const uint32_t t = static_cast<uint32_t>(t0 + mm.v_tok[I]);
       v4f out[2];
 #pragma unroll
@@ -456,7 +613,7 @@ __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(1, 1))) v
       }
       gr.put8(gr.v, t * gr.rv + gr.cv + mm.v_col, out[0], out[1]);
     }
-    if constexpr (DYN) {
+    if (DYN && !hi) {
       const uint32_t t = static_cast<uint32_t>(t0 + mm.nz_tok);
       const v4f lo = widen_lo(x.nz), hi = widen_hi(x.nz);
       v4f out[2];
@@ -485,27 +642,62 @@ __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(1, 1))) v
   // As the bf16-input backward: tile J's loads were issued during tile J + 1;
   // the raw pieces of the tile being written out are kept until its
   // gradients have left.
+  // Tiles run from the last to the first; tile J's projection pieces were
+  // loaded during tile J + 1 and are kept until its gradients have left.
+  // Without the epilogue, tile J's gy is staged with them.  With it, the
+  // epilogue pieces of one sub-tile at a time are staged: those of sub-tile
+  // 1 (tokens 8..15, chunk 2J + 1) load during chunk 2J + 2 and form gy at the
+  // tile's put; those of sub-tile 0 load at the put and form gy between the
+  // two chunks.
   Stage st;
   MixRaw kept;
-  load(st, ntiles - 1);
+  EpiHalf eh;
+  load_raw(st, ntiles - 1);
+  if constexpr (EPI) load_epi(eh, ntiles - 1, 1);
+  else load_y(st, ntiles - 1);
   issue_ck(tile, 2 * (ntiles - 1));
   if (2 * ntiles - 1 < nb) issue_ck(tile + BwdTile::SIZE, 2 * ntiles - 1);
   else if (ntiles > 1) issue_ck(tile + BwdTile::SIZE, 2 * ntiles - 3);
   for (int64_t J = ntiles - 1; J >= 0; --J) {
     vm_wait<0>();
-    if (J + 1 < ntiles) write_grads(kept, J + 1);
+    if (J + 1 < ntiles) {
+      write_grads(kept, J + 1, false);
+      write_grads(kept, J + 1, true);
+    }
     __builtin_amdgcn_sched_barrier(0);
     lds_wait();
-    put(st);
+    put(st, J);
+    if constexpr (EPI) put_epi(eh, J, 1);
     kept = st.raw;
     __builtin_amdgcn_sched_barrier(0);
-    if (J > 0) load(st, J - 1);
+    if (J > 0) {
+      load_raw(st, J - 1);
+      if constexpr (!EPI) load_y(st, J - 1);
+    }
+    if constexpr (EPI) load_epi(eh, J, 0);
     __builtin_amdgcn_sched_barrier(0);
     if (2 * J + 1 < nb) run_chunk(tile + BwdTile::SIZE, 2 * J + 1);
+    if constexpr (EPI) {
+      __builtin_amdgcn_sched_barrier(0);
+      put_epi(eh, J, 0);
+      if (J > 0) load_epi(eh, J - 1, 1);
+      __builtin_amdgcn_sched_barrier(0);
+    }
     run_chunk(tile, 2 * J);
   }
-  write_grads(kept, 0);
+  write_grads(kept, 0, false);
+  write_grads(kept, 0, true);
   core.store_initial(a.gm0, a.gc0, n0, SPW, unit);
+  if constexpr (EPI) {
+    // Sum the weight-gradient shares of the 32 lanes of each half; lanes 0
+    // and 1 write the wave's 8 partials.
+    v4f dw = dwl[lane];
+#pragma unroll
+    for (int m = 2; m < kWave; m *= 2)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) dw[i] += __shfl_xor(dw[i], m);
+    if (lane < 2) *reinterpret_cast<v4f*>(a.gw_part + static_cast<int64_t>(blockIdx.x) * 8 + lane * 4) = dw;
+  }
 }
 
 }  // namespace
@@ -514,19 +706,21 @@ __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(1, 1))) v
 hipError_t launch_mixer_forward(const MixArgs& a, hipStream_t stream) {
   const int64_t blocks = a.b * a.h / r4::SPW;
   if (blocks == 0) return hipSuccess;
-  hipLaunchKernelGGL(r4::mixer_forward_kernel, dim3(static_cast<unsigned>(blocks)), dim3(kWave), 0, stream, a);
+  const dim3 grid(static_cast<unsigned>(blocks)), block(kWave);
+  if (a.gate != nullptr) hipLaunchKernelGGL(r4::mixer_forward_kernel<true>, grid, block, 0, stream, a);
+  else hipLaunchKernelGGL(r4::mixer_forward_kernel<false>, grid, block, 0, stream, a);
   return hipGetLastError();
 }
 
 hipError_t launch_mixer_backward(const MixArgs& a, hipStream_t stream) {
   const int64_t blocks = a.b * a.h / r4::SPW;
   if (blocks == 0) return hipSuccess;
-  if (a.gdl != nullptr)
-    hipLaunchKernelGGL(r4::mixer_backward_kernel<true>, dim3(static_cast<unsigned>(blocks)), dim3(kWave), 0, stream,
-                       a);
-  else
-    hipLaunchKernelGGL(r4::mixer_backward_kernel<false>, dim3(static_cast<unsigned>(blocks)), dim3(kWave), 0,
-                       stream, a);
+  const dim3 grid(static_cast<unsigned>(blocks)), block(kWave);
+  const bool dyn = a.gdl != nullptr, epi = a.gate != nullptr;
+  if (dyn && epi) hipLaunchKernelGGL((r4::mixer_backward_kernel<true, true>), grid, block, 0, stream, a);
+  else if (dyn) hipLaunchKernelGGL((r4::mixer_backward_kernel<true, false>), grid, block, 0, stream, a);
+  else if (epi) hipLaunchKernelGGL((r4::mixer_backward_kernel<false, true>), grid, block, 0, stream, a);
+  else hipLaunchKernelGGL((r4::mixer_backward_kernel<false, false>), grid, block, 0, stream, a);
   return hipGetLastError();
 }
 

@@ -112,6 +112,23 @@ struct MixArgs {
   int64_t b, t, h, chunk, nb;
   float floor;
   int grad_f32;
+  // Readout epilogue (gated entry points; gate == nullptr: none).  Forward:
+  // out = RMSNorm(bf16(read)) * norm_w * silu(gate), written bf16 (float32
+  // when precise) [B, T, H * 8], and yb = bf16(read) [B, T, H * 8] saved for
+  // the backward (y is not written).  Backward: gy is formed on chip from
+  // gout (bf16 [B, T, H * 8]), yb and gate; ggate [B, T, H * 8] is written
+  // bf16 (float32 when precise) and the weight gradient as per-wave partials
+  // gw_part [B * H / 16, 8].
+  const void* gate;
+  int64_t ldg;
+  const float* norm_w;
+  float norm_eps;
+  void* out;
+  void* yb;
+  const void* gout;
+  void* ggate;
+  float* gw_part;
+  int precise;
 };
 hipError_t launch_mixer_forward(const MixArgs& a, hipStream_t stream);
 hipError_t launch_mixer_backward(const MixArgs& a, hipStream_t stream);

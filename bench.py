@@ -111,16 +111,20 @@ MIXER_FWD_BYTES = 2 * 22 + 4 * 8   # bf16 q, k, decay (4 each), v (8), noise (2)
 MIXER_BWD_BYTES = 2 * 22 + 4 * 8 + 2 * 22  # projections and read gradient in; bf16 projection gradients out
 
 
-def time_mixer(b, t, h, steps, warmup, device, fused=True) -> dict:
+def time_mixer(b, t, h, steps, warmup, device, fused=True, gated=False) -> dict:
     """fwd+bwd of the Bayes mixer's layer core from its bf16 projections (train_6layer.py:627-710).
 
     fused: ``bayes_mixer_core`` (the producer-fused kernels).  Otherwise the
     reference's op chain on the same GPU: the float32 transforms and permutes
     (``mixer_layer_inputs``), ``bayesian_layer`` on the float32 layer kernels,
     and the readout permute.  The five projections are separate bf16 leaves.
+    gated: up to the input of out_proj (:719-729): the readout's RMSNorm and
+    SiLU gate as well (``bayes_mixer_readout``, or torch's rms_norm and silu
+    on bf16 after the op chain); the gate and the norm weight are leaves too.
     """
     import bayes_ssm
-    from bayes_ssm.mixer import bayes_mixer_core, mixer_layer_inputs
+    import torch.nn.functional as F
+    from bayes_ssm.mixer import bayes_mixer_core, bayes_mixer_readout, mixer_layer_inputs
 
     gen = torch.Generator(device=device).manual_seed(3)
     shift = {3: 2.0, 4: 0.0}
@@ -131,16 +135,26 @@ def time_mixer(b, t, h, steps, warmup, device, fused=True) -> dict:
             x[..., 0::2] -= 3.0
         leaves.append(x.to(torch.bfloat16).requires_grad_(True))
     gy = torch.randn(b, t, h, 8, device=device, generator=gen)
+    if gated:
+        gate = torch.randn(b, t, h * 8, device=device, generator=gen).to(torch.bfloat16).requires_grad_(True)
+        norm_w = torch.ones(8, device=device, dtype=torch.bfloat16, requires_grad=True)
+        gy = gy.view(b, t, h * 8).to(torch.bfloat16)
+        leaves = leaves + [gate, norm_w]
 
     def step():
-        if fused:
-            read, _, _ = bayes_mixer_core(*leaves, heads=h)
+        if fused and gated:
+            out, _, _ = bayes_mixer_readout(*leaves[:5], gate, norm_w, heads=h)
+        elif fused:
+            out, _, _ = bayes_mixer_core(*leaves, heads=h)
         else:
-            k, v, q, dec, p, r = mixer_layer_inputs(*leaves, h)
+            k, v, q, dec, p, r = mixer_layer_inputs(*leaves[:5], h)
             y, _, _ = bayes_ssm.bayesian_layer(k, v, q, transition_diagonals=dec, process_variances=p,
                                                observation_variances=r, chunk_length=64, optimized=True)
-            read = y.view(b, h, t, 8).permute(0, 2, 1, 3)
-        return torch.autograd.grad(read, leaves, gy)
+            out = y.view(b, h, t, 8).permute(0, 2, 1, 3)
+            if gated:
+                out = F.rms_norm(out.to(torch.bfloat16), (8,), norm_w, None)
+                out = (out * F.silu(gate.view(b, t, h, 8))).reshape(b, t, h * 8)
+        return torch.autograd.grad(out, leaves, gy)
 
     for _ in range(warmup):
         step()
@@ -153,8 +167,9 @@ def time_mixer(b, t, h, steps, warmup, device, fused=True) -> dict:
     torch.cuda.synchronize()
     ms = e0.elapsed_time(e1) / steps
     out = {"B": b, "T": t, "H": h, "D": 4, "M": 8, "ms_per_step": ms, "tokens_per_s": b * t / (ms * 1e-3),
-           "path": "producer-fused kernels" if fused else "reference op chain + float32 layer kernels"}
-    if fused:
+           "path": ("producer-fused kernels" if fused else "reference op chain + float32 layer kernels")
+           + (", gated readout epilogue" if gated else "")}
+    if fused and not gated:
         per = MIXER_FWD_BYTES + MIXER_BWD_BYTES
         out["bytes_per_token_head"] = per
         out["roofline_step_frac"] = per * b * h * t / (ms * 1e-3) / HBM_PEAK
@@ -392,6 +407,8 @@ def main() -> int:
             extras[name] = time_layer(eb, t, h, ed, m, args.chunk, 10, 3, device)
         extras["mixer_core_config3_fused"] = time_mixer(b, t, h, 30, 10, device, fused=True)
         extras["mixer_core_config3_op_chain"] = time_mixer(b, t, h, 10, 3, device, fused=False)
+        extras["mixer_readout_config3_fused"] = time_mixer(b, t, h, 30, 10, device, fused=True, gated=True)
+        extras["mixer_readout_config3_op_chain"] = time_mixer(b, t, h, 10, 3, device, fused=False, gated=True)
         extras["assoc_scan_config0"] = time_scan(1, 16, 4, 4, 50, device)
         extras["assoc_scan_config1"] = time_scan(4, 64, 16, 16, 50, device)
         result["extras"] = extras

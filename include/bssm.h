@@ -314,6 +314,48 @@ int bssm_mixer_backward(const void* q_proj, int64_t ldq, const void* k_proj, int
                         int64_t batch, int64_t t, int64_t heads, int64_t chunk,
                         float denominator_floor, int grad_f32, void* stream);
 
+/* ------------------------------------------------------------------------
+ * The mixer core with its readout epilogue.  Replaces, after the op chain
+ * of bssm_mixer_forward, the readout of example/train_6layer.py:719-729:
+ *   out = read_norm(read.to(bf16)) * silu(gate)     (per head of 8 values)
+ * with read_norm an RMSNorm over the head: x / sqrt(mean(x^2) + norm_eps) * w
+ * (torch's rms_norm with eps None uses the float32 epsilon, 1.1920929e-7).
+ * The product is formed in float32 from bf16(read) and rounded to bf16 once.
+ * gate: bf16 [B, T, H*8] view with row stride ldg (a multiple of 8, 16-byte
+ * aligned base); norm_weight: float32 [8].  Outputs: out [B, T, H*8] bf16
+ * (float32 when precise != 0), read_bf16 = bf16(read) [B, T, H*8] (kept for
+ * the backward), and the belief outputs of bssm_mixer_forward; read itself is
+ * not written.  No counterpart in the reference library. */
+int bssm_mixer_gated_forward(const void* q_proj, int64_t ldq, const void* k_proj, int64_t ldk,
+                             const void* v_proj, int64_t ldv, const void* decay_logits, int64_t ldd,
+                             const void* noise, int64_t ldn, const void* gate, int64_t ldg,
+                             const float* norm_weight, float norm_eps,
+                             const float* mean0, const float* cov0,
+                             void* out, void* read_bf16, float* mean_final, float* cov_final,
+                             float* bmean, float* bcov,
+                             int64_t batch, int64_t t, int64_t heads, int64_t chunk,
+                             float denominator_floor, int precise, void* stream);
+
+/* Reverse of bssm_mixer_gated_forward from grad_out (bf16 [B, T, H*8]):
+ * the readout gradient is formed on chip and never stored.  Writes the
+ * projection gradients as bssm_mixer_backward does, grad_gate [B, T, H*8]
+ * (bf16, contiguous) and the norm-weight gradient as per-wave partial sums
+ * grad_norm_weight_partials [B*H/16, 8] (float32; their column sums are the
+ * gradient).  precise != 0 writes every bf16 gradient as float32 instead. */
+int bssm_mixer_gated_backward(const void* q_proj, int64_t ldq, const void* k_proj, int64_t ldk,
+                              const void* v_proj, int64_t ldv, const void* decay_logits, int64_t ldd,
+                              const void* noise, int64_t ldn, const void* gate, int64_t ldg,
+                              const float* norm_weight, float norm_eps,
+                              const float* mean0, const float* cov0,
+                              const float* bmean, const float* bcov,
+                              const void* read_bf16, const void* grad_out,
+                              const float* gmf, const float* gcf,
+                              void* grad_q, void* grad_k, void* grad_v, void* grad_decay_logits,
+                              void* grad_noise, void* grad_gate, float* grad_norm_weight_partials,
+                              float* gm0, float* gc0,
+                              int64_t batch, int64_t t, int64_t heads, int64_t chunk,
+                              float denominator_floor, int precise, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

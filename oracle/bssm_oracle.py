@@ -20,6 +20,7 @@ float32, autograd-friendly), written from the equations:
 * ``closed_form_static``             — Bayesian linear regression, the A=I, Q=0 closed form
 * ``mixer_inputs`` / ``mixer_core``  — the Bayes mixer's producer chain and readout permute
                                        (example/train_6layer.py:627-693, :709-710)
+* ``mixer_readout``                  — its gated readout: RMSNorm(bf16(read)) * silu(gate) (:719-729)
 
 Pinning (tests/test_oracle.py): closed forms (scalar Kalman filter, one-step
 u = (d^2+p)k, no-update limits, Bayesian linear regression), invariants
@@ -30,7 +31,9 @@ fp64 gradcheck of the gradients that the reference obtains by autograd.
 The mixer producer chain is pinned by identities the reference's formulas
 must satisfy (exp(-softplus(x)) = sigmoid(-x), softplus(x) - softplus(-x) = x,
 unit-norm heads, the [B, T, H] -> [B*H, T] sequence map checked with
-head-tagged inputs) and by its reduction to ``run_diagonal``.
+head-tagged inputs) and by its reduction to ``run_diagonal``.  The readout
+epilogue is pinned against torch's own rms_norm / silu on bf16 tensors (the
+reference's ops), by unit RMS of the normalized head, and by gradcheck.
 No function here is left "parity unpinned".
 """
 from __future__ import annotations
@@ -304,6 +307,25 @@ def mixer_grads(q_proj, k_proj, v_proj, decay_logits, noise, heads: int, mean0, 
         loss = loss + (cT * gcf.to(dtype)).sum()
     grads = torch.autograd.grad(loss, leaves)
     return read.detach(), mT.detach(), cT.detach(), list(grads)
+
+
+def mixer_readout(read, gate, weight, eps: float = 1.1920928955078125e-07, read_bf16=None):
+    """The mixer's gated readout (train_6layer.py:719-729) per head of 8 values, in float64.
+
+    out = rms(r) * w * silu(gate) with r = read.to(bf16) and rms(x) =
+    x / sqrt(mean(x^2) + eps) (torch's rms_norm; eps None is the float32
+    epsilon).  The bf16 rounding of read is value-only: the gradient passes
+    through it to read, as autograd's through ``.to()``.  ``read_bf16``
+    (the rounded values, e.g. a kernel's) replaces the rounding done here.
+    read, gate: [B, T, H, 8] (or [B, T, H*8] for gate); returns [B, T, H*8].
+    """
+    b, t, h = read.shape[:3]
+    r64 = read.to(torch.float64)
+    rb = (read.to(torch.bfloat16) if read_bf16 is None else read_bf16.reshape(b, t, h, 8)).to(torch.float64)
+    y = r64 + (rb - r64).detach()
+    n = y / (y.square().mean(-1, keepdim=True) + eps).sqrt()
+    g = gate.reshape(b, t, h, 8).to(torch.float64)
+    return (n * weight.to(torch.float64) * _silu(g)).reshape(b, t, h * 8)
 
 
 def make_mixer_inputs(b: int, t: int, heads: int, *, seed: int = 0, ld_pad: int = 0, scale: float = 1.0):

@@ -201,3 +201,154 @@ def test_mixer_unsupported_shapes_take_the_op_chain(cuda_device):
         close(read, e_read, f"read b={b} t={t} h={h}")
         close(mT, e_mT, "mean_T")
         close(cT, e_cT, "cov_T")
+
+
+# ------------------------------------------------------- gated readout epilogue
+EPS32 = torch.finfo(torch.float32).eps
+
+
+def _gate_inputs(b, t, h, seed, gate_pad):
+    g = torch.Generator().manual_seed(seed)
+    gate_full = torch.randn(b, t, h * 8 + gate_pad, generator=g).to(torch.bfloat16)
+    w = (1 + 0.2 * torch.randn(8, generator=g)).to(torch.bfloat16).float()
+    gout = torch.randn(b, t, h * 8, generator=g).to(torch.bfloat16)
+    return gate_full[..., : h * 8], w, gout
+
+
+def _gated_forward(dv, lds, gate, w, m0, c0, b, t, h, precise):
+    from bayes_ssm import _hip
+
+    n, nb, dev = b * h, -(-t // CHUNK), dv[0].device
+    out = torch.empty(b, t, h * 8, device=dev, dtype=torch.float32 if precise else torch.bfloat16)
+    yb = torch.empty(b, t, h * 8, device=dev, dtype=torch.bfloat16)
+    mT, cT = torch.empty(n, 4, 8, device=dev), torch.empty(n, 4, 4, device=dev)
+    bm, bc = torch.empty(n, nb + 1, 4, 8, device=dev), torch.empty(n, nb + 1, 4, 4, device=dev)
+    P = _hip.ptr
+    args = []
+    for x, ld in zip(dv, lds):
+        args += [P(x), ld]
+    _hip.call("bssm_mixer_gated_forward", *args, P(gate), gate.stride(1), P(w), EPS32, P(m0), P(c0), P(out), P(yb),
+              P(mT), P(cT), P(bm), P(bc), b, t, h, CHUNK, 1e-6, int(precise), _hip.stream_of(dev))
+    return out, yb, mT, cT, bm, bc
+
+
+def _gated_backward(dv, lds, gate, w, m0, c0, bm, bc, yb, gout, gmf, gcf, b, t, h, precise):
+    from bayes_ssm import _hip
+
+    dev = dv[0].device
+    dtype = torch.float32 if precise else torch.bfloat16
+    grads = [torch.empty(x.shape, device=dev, dtype=dtype) for x in dv]
+    ggate = torch.empty(b, t, h * 8, device=dev, dtype=dtype)
+    part = torch.empty(b * h // 16, 8, device=dev)
+    gm0, gc0 = torch.empty_like(m0), torch.empty_like(c0)
+    P = _hip.ptr
+    args = []
+    for x, ld in zip(dv, lds):
+        args += [P(x), ld]
+    _hip.call("bssm_mixer_gated_backward", *args, P(gate), gate.stride(1), P(w), EPS32, P(m0), P(c0), P(bm), P(bc),
+              P(yb), P(gout), P(gmf), P(gcf), *[P(g) for g in grads], P(ggate), P(part), P(gm0), P(gc0), b, t, h,
+              CHUNK, 1e-6, int(precise), _hip.stream_of(dev))
+    return grads + [ggate, part, gm0, gc0]
+
+
+GATED_CASES = [  # batch, tokens, heads, projection row padding, gate row padding
+    (2, 36, 16, 0, 0),
+    (1, 4, 16, 8, 8),
+    (2, 100, 32, 16, 24),
+]
+
+
+@pytest.mark.parametrize("b,t,h,pad,gpad", GATED_CASES)
+def test_mixer_gated_abi_matches_oracle(cuda_device, b, t, h, pad, gpad):
+    print(f"mixer gated b={b} t={t} h={h} pad={pad} gpad={gpad}", flush=True)
+    views, _ = O.make_mixer_inputs(b, t, h, seed=1300 + t, ld_pad=pad)
+    gate, w, gout = _gate_inputs(b, t, h, seed=t, gate_pad=gpad)
+    n = b * h
+    m0, c0, gmf, gcf = _state(n, seed=t + 1)
+    dv = _device_views(views, cuda_device)
+    lds = _lds(views)
+    gate_d = _device_views([gate], cuda_device)[0] if gpad else gate.to(cuda_device)
+    d = {k: x.to(cuda_device) for k, x in dict(m0=m0, c0=c0, gmf=gmf, gcf=gcf, w=w, gout=gout).items()}
+
+    o32, yb, mT, cT, bm, bc = _gated_forward(dv, lds, gate_d, d["w"], d["m0"], d["c0"], b, t, h, True)
+    o16, yb2, *_ = _gated_forward(dv, lds, gate_d, d["w"], d["m0"], d["c0"], b, t, h, False)
+    g32 = _gated_backward(dv, lds, gate_d, d["w"], d["m0"], d["c0"], bm, bc, yb, d["gout"], d["gmf"], d["gcf"],
+                          b, t, h, True)
+    g16 = _gated_backward(dv, lds, gate_d, d["w"], d["m0"], d["c0"], bm, bc, yb, d["gout"], d["gmf"], d["gcf"],
+                          b, t, h, False)
+    torch.cuda.synchronize()
+
+    # Forward: bf16(read) within rounding of the oracle's read; the epilogue on those values.
+    leaves = [x.detach().double().requires_grad_(True) for x in (*views, gate, w, m0, c0)]
+    read, e_mT, e_cT = O.mixer_core(*leaves[:5], h, leaves[7], leaves[8])
+    e_out = O.mixer_readout(read, leaves[5], leaves[6], EPS32, read_bf16=yb.cpu())
+    close(yb.view(b, t, h, 8), read, "read_bf16", rtol=2 ** -8, atol=1e-6)
+    close(o32, e_out, "out")
+    close(mT, e_mT, "mean_T")
+    close(cT, e_cT, "cov_T")
+    assert torch.equal(yb, yb2)
+    assert torch.equal(o16, o32.bfloat16()), "bf16 out is not the float32 product rounded"
+
+    # Backward: every gradient against autograd through the oracle.
+    loss = (e_out * gout.double()).sum() + (e_mT * gmf.double()).sum() + (e_cT * gcf.double()).sum()
+    e_grads = torch.autograd.grad(loss, leaves)
+    names = ["g_q", "g_k", "g_v", "g_decay_logits", "g_noise", "g_gate"]
+    for name, a, e in zip(names, g32[:6], e_grads[:6]):
+        close(a, e, name)
+    close(g32[6].sum(0), e_grads[6], "g_norm_weight")
+    close(g32[7], e_grads[7], "g_mean0")
+    close(g32[8], e_grads[8], "g_cov0")
+    for name, a, e in zip(names, g16[:6], g32[:6]):
+        assert a.dtype == torch.bfloat16
+        assert torch.equal(a, e.bfloat16()), f"{name} (bf16) is not the float32 gradient rounded"
+    for a, e in zip(g16[6:], g32[6:]):
+        assert torch.equal(a, e)
+
+
+def test_mixer_readout_autograd_boundary(cuda_device, monkeypatch):
+    """bayes_mixer_readout on bf16 inputs runs the gated kernels; results and gradients are the C ABI's."""
+    from bayes_ssm import mixer
+
+    calls = []
+    orig = mixer._MixerReadoutFunction.apply
+    monkeypatch.setattr(mixer._MixerReadoutFunction, "apply", staticmethod(lambda *a: calls.append(1) or orig(*a)))
+    b, t, h = 2, 40, 16
+    views, _ = O.make_mixer_inputs(b, t, h, seed=41, ld_pad=8)
+    gate, w, gout = _gate_inputs(b, t, h, seed=42, gate_pad=0)
+    dv = _device_views(views, cuda_device)
+    leaves = [x.detach().requires_grad_(True) for x in dv]
+    gate_l = gate.to(cuda_device).requires_grad_(True)
+    w_l = w.to(cuda_device).to(torch.bfloat16).requires_grad_(True)
+    out, mT, cT = mixer.bayes_mixer_readout(*leaves, gate_l, w_l, heads=h)
+    assert calls, "gated kernels were not used"
+    gout_d = gout.to(cuda_device)
+    torch.autograd.backward([out], [gout_d])
+
+    lds = _lds(views)
+    m0 = torch.zeros(b * h, 4, 8, device=cuda_device)
+    c0 = torch.eye(4, device=cuda_device).expand(b * h, 4, 4).contiguous()
+    w32 = w_l.detach().float()
+    o16, yb, m2, c2, bm, bc = _gated_forward(dv, lds, gate_l.detach(), w32, m0, c0, b, t, h, False)
+    g16 = _gated_backward([x.detach() for x in dv], lds, gate_l.detach(), w32, m0, c0, bm, bc, yb, gout_d, None,
+                          None, b, t, h, False)
+    torch.cuda.synchronize()
+    assert out.dtype == torch.bfloat16 and torch.equal(out, o16)
+    assert torch.equal(mT, m2) and torch.equal(cT, c2)
+    for i, x in enumerate(leaves):
+        assert torch.equal(x.grad, g16[i]), f"grad of projection {i}"
+    assert torch.equal(gate_l.grad, g16[5])
+    assert w_l.grad.dtype == torch.bfloat16
+    assert torch.equal(w_l.grad, g16[6].sum(0).bfloat16())
+
+
+def test_mixer_readout_fallback_matches_oracle(cuda_device):
+    """Heads not a multiple of 16: the op chain (torch rms_norm and silu in bf16) within bf16 rounding."""
+    from bayes_ssm import mixer
+
+    b, t, h = 2, 20, 8
+    views, _ = O.make_mixer_inputs(b, t, h, seed=12)
+    gate, w, _ = _gate_inputs(b, t, h, seed=13, gate_pad=0)
+    dv = _device_views(views, cuda_device)
+    out, _, _ = mixer.bayes_mixer_readout(*dv, gate.to(cuda_device), w.to(cuda_device).bfloat16(), heads=h)
+    read, _, _ = O.mixer_core(*views, h)
+    close(out, O.mixer_readout(read, gate, w), "out", rtol=3 * 2 ** -8, atol=1e-3)

@@ -315,3 +315,39 @@ def test_mixer_mutation_is_detected():
     x = torch.linspace(-4.0, 4.0, 8).reshape(1, 1, 8)
     bad = torch.exp(O._softplus(x))
     assert not torch.allclose(bad, torch.sigmoid(-x), rtol=1e-8, atol=0)
+
+
+def test_mixer_readout_matches_torch_ops_and_invariants():
+    """mixer_readout equals torch's bf16 rms_norm * silu chain (the reference's ops) to bf16 rounding;
+    the normalized head has unit RMS; the float32-epsilon default matters for tiny heads."""
+    g = torch.Generator().manual_seed(8)
+    b, t, h = 2, 5, 3
+    read = torch.randn(b, t, h, 8, generator=g)
+    gate = torch.randn(b, t, h * 8, generator=g).to(torch.bfloat16)
+    w = (1 + 0.2 * torch.randn(8, generator=g)).to(torch.bfloat16)
+    ours = O.mixer_readout(read, gate, w)
+    rn = torch.nn.functional.rms_norm(read.to(torch.bfloat16), (8,), w, None)
+    ref = (rn * torch.nn.functional.silu(gate.view(b, t, h, 8))).reshape(b, t, h * 8)
+    # The torch chain rounds to bf16 three times (norm, silu, product), each within 2^-8 relative.
+    torch.testing.assert_close(ours, ref.double(), rtol=3 * 2 ** -8, atol=0)
+    unit = O.mixer_readout(read, torch.full((b, t, h * 8), 30.0), torch.ones(8), eps=0.0)  # silu(30) = 30
+    rms = (unit / 30.0).reshape(b, t, h, 8).square().mean(-1).sqrt()
+    torch.testing.assert_close(rms, torch.ones_like(rms), rtol=1e-12, atol=0)
+    tiny = 1e-4 * read
+    a = O.mixer_readout(tiny, gate, w)
+    rn_t = torch.nn.functional.rms_norm(tiny.to(torch.bfloat16), (8,), w, None)
+    ref_t = (rn_t * torch.nn.functional.silu(gate.view(b, t, h, 8))).reshape(b, t, h * 8)
+    torch.testing.assert_close(a, ref_t.double(), rtol=3 * 2 ** -8, atol=1e-6)
+    bad = O.mixer_readout(tiny, gate, w, eps=torch.finfo(torch.bfloat16).eps)
+    assert not torch.allclose(bad, ref_t.double(), rtol=3 * 2 ** -8, atol=1e-6)
+
+
+def test_mixer_readout_gradcheck():
+    g = torch.Generator().manual_seed(9)
+    read = torch.randn(1, 2, 2, 8, generator=g, dtype=torch.float64).requires_grad_(True)
+    gate = torch.randn(1, 2, 16, generator=g, dtype=torch.float64).requires_grad_(True)
+    w = (1 + 0.2 * torch.randn(8, generator=g, dtype=torch.float64)).requires_grad_(True)
+    # The bf16 rounding of read is value-only; with the rounded values taken as read itself the
+    # map is smooth and its autograd gradient is the one the rounding passes through.
+    assert torch.autograd.gradcheck(lambda r, z, ww: O.mixer_readout(r, z, ww, read_bf16=r), (read, gate, w),
+                                     eps=1e-6, atol=1e-6)
