@@ -51,12 +51,14 @@ _SIGNATURES = {
     "bssm_mixer_forward": [_P, _L] * 5 + [_P] * 7 + [_L, _L, _L, _L, _F, _P],
     "bssm_mixer_backward": [_P, _L] * 5 + [_P] * 7 + [_P] * 7 + [_L, _L, _L, _L, _F, _I, _P],
     "bssm_mixer_gated_forward": [_P, _L] * 6 + [_P, _F] + [_P] * 8 + [_L, _L, _L, _L, _F, _I, _P],
+    "bssm_causal_conv4_forward": [_I, _P, _L, _P, _P, _L, _L, _L, _P],
+    "bssm_causal_conv4_backward": [_I, _P, _L, _P, _P, _P, _P, _L, _L, _L, _P],
     "bssm_mixer_gated_backward": [_P, _L] * 6 + [_P, _F] + [_P] * 8 + [_P] * 9 + [_L, _L, _L, _L, _F, _I, _P],
     "bssm_supported": [_I, _I],
     "bssm_preferred_checkpoint": [_I],
     "bssm_abi_version": [],
 }
-ABI_VERSION = 4
+ABI_VERSION = 5
 
 _lock = threading.Lock()
 _lib: Optional[ctypes.CDLL] = None

@@ -229,13 +229,31 @@ int epilogue_check(const char* fn, const void* gate, int64_t ldg, const float* n
   return BSSM_OK;
 }
 
+int conv_check(const char* fn, int bf16, const void* x, int64_t ldx, const float* weight,
+               std::initializer_list<const void*> contiguous, int64_t b, int64_t t, int64_t c) {
+  const int64_t n = bf16 ? 8 : 4, elem = bf16 ? 2 : 4;
+  if (b < 0 || t < 0 || c < 0) return fail(BSSM_ERR_ARGUMENT, "%s: negative size", fn);
+  if (c % n != 0 || ldx < c || ldx % n != 0)
+    return fail(BSSM_ERR_UNSUPPORTED, "%s: channels and the row stride must be multiples of %lld (16 bytes), "
+                "row stride >= channels (got c=%lld ldx=%lld)", fn, (long long)n, (long long)c, (long long)ldx);
+  if ((t + 16) * ldx * elem >= ((int64_t)1 << 31) || (t + 16) * c * elem >= ((int64_t)1 << 31))
+    return fail(BSSM_ERR_ARGUMENT, "%s: T * row bytes too large for 32-bit stream offsets", fn);
+  if (b * ((c / n + 63) / 64) > 0x7fffffff) return fail(BSSM_ERR_ARGUMENT, "%s: batch * channels too large", fn);
+  if (b * t * c == 0) return BSSM_OK;
+  if (x == nullptr || weight == nullptr) return fail(BSSM_ERR_ARGUMENT, "%s: x and weight are required", fn);
+  if (!aligned16(x) || !aligned16(weight)) return fail(BSSM_ERR_ARGUMENT, "%s: x and weight must be 16-byte aligned", fn);
+  for (const void* p : contiguous)
+    if (p == nullptr || !aligned16(p)) return fail(BSSM_ERR_ARGUMENT, "%s: outputs must be non-null, 16-byte aligned", fn);
+  return BSSM_OK;
+}
+
 }  // namespace
 
 extern "C" {
 
 const char* bssm_last_error(void) { return g_error; }
 
-int bssm_abi_version(void) { return 4; }
+int bssm_abi_version(void) { return 5; }
 
 int bssm_supported(int key_dim, int value_dim) { return supported(key_dim, value_dim) ? 1 : 0; }
 
@@ -619,6 +637,29 @@ int bssm_mixer_gated_backward(const void* q_proj, int64_t ldq, const void* k_pro
   a.b = batch; a.t = t; a.h = heads; a.chunk = chunk; a.nb = (t + chunk - 1) / chunk; a.floor = denominator_floor;
   if (n == 0) return ok();
   return launched(fn, bssm::launch_mixer_backward(a, static_cast<hipStream_t>(stream)));
+}
+
+int bssm_causal_conv4_forward(int bf16, const void* x, int64_t ldx, const float* weight, void* y, int64_t batch,
+                              int64_t t, int64_t channels, void* stream) {
+  const char* fn = "bssm_causal_conv4_forward";
+  if (int rc = conv_check(fn, bf16, x, ldx, weight, {y}, batch, t, channels)) return rc;
+  bssm::ConvArgs a{};
+  a.x = x; a.ldx = ldx; a.w = weight; a.y = y; a.b = batch; a.t = t; a.c = channels; a.bf16 = bf16 != 0;
+  if (batch * t * channels == 0) return ok();
+  return launched(fn, bssm::launch_conv4_forward(a, static_cast<hipStream_t>(stream)));
+}
+
+int bssm_causal_conv4_backward(int bf16, const void* x, int64_t ldx, const float* weight, const void* grad_y,
+                               void* grad_x, float* grad_weight_partials, int64_t batch, int64_t t,
+                               int64_t channels, void* stream) {
+  const char* fn = "bssm_causal_conv4_backward";
+  if (int rc = conv_check(fn, bf16, x, ldx, weight, {grad_y, grad_x, grad_weight_partials}, batch, t, channels))
+    return rc;
+  bssm::ConvArgs a{};
+  a.x = x; a.ldx = ldx; a.w = weight; a.gy = grad_y; a.gx = grad_x; a.gw_part = grad_weight_partials;
+  a.b = batch; a.t = t; a.c = channels; a.bf16 = bf16 != 0;
+  if (batch * channels == 0) return ok();
+  return launched(fn, bssm::launch_conv4_backward(a, static_cast<hipStream_t>(stream)));
 }
 
 int bssm_associative_static_scan(const float* keys, const float* values, const float* queries,

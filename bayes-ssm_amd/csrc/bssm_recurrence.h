@@ -133,6 +133,24 @@ struct MixArgs {
 hipError_t launch_mixer_forward(const MixArgs& a, hipStream_t stream);
 hipError_t launch_mixer_backward(const MixArgs& a, hipStream_t stream);
 
+// Length-four causal depthwise filter on channels-last rows (bssm_conv4.hip):
+// x [B, T, C] with row stride ldx (elements), y / gy / gx contiguous
+// [B, T, C], weight float32 [C, 4], gw_part float32 [B, C, 4]; bfloat16 or
+// float32 streams.
+struct ConvArgs {
+  const void* x;
+  int64_t ldx;
+  const float* w;
+  void* y;
+  const void* gy;
+  void* gx;
+  float* gw_part;
+  int64_t b, t, c;
+  int bf16;
+};
+hipError_t launch_conv4_forward(const ConvArgs& a, hipStream_t stream);
+hipError_t launch_conv4_backward(const ConvArgs& a, hipStream_t stream);
+
 hipError_t launch_associative_scan(const float* k, const float* v, const float* q, const float* r,
                                    const float* m0, const float* c0, float* y, float* mT, float* cT,
                                    int64_t b, int64_t t, int d, int m, hipStream_t stream);

@@ -176,6 +176,44 @@ def time_mixer(b, t, h, steps, warmup, device, fused=True, gated=False) -> dict:
     return out
 
 
+def time_conv(b, t, c, steps, warmup, device, fused=True) -> dict:
+    """fwd+bwd of CausalDepthwise4 on a bf16 [B, T, C] stream, as the mixer applies it (train_6layer.py:474-480).
+
+    fused: the HIP kernels (``bayes_ssm.conv``); otherwise the reference's
+    four shifted products in torch on the same GPU.  Algorithmic bytes per
+    element: forward 2 in + 2 out, backward 2 + 2 in (x, grad) + 2 out.
+    """
+    from bayes_ssm.conv import CausalDepthwise4, _taps_formula
+
+    gen = torch.Generator(device=device).manual_seed(5)
+    value = torch.randn(b, t, c, device=device, generator=gen).to(torch.bfloat16).requires_grad_(True)
+    m = CausalDepthwise4(c, dtype=torch.bfloat16, device=device)
+    with torch.no_grad():
+        m.weight.copy_(0.5 * torch.randn(c, 1, 4, device=device, generator=gen))
+    gy = torch.randn(b, t, c, device=device, generator=gen).to(torch.bfloat16)
+
+    def step():
+        xv = value.transpose(1, 2)
+        out = (m(xv) if fused else _taps_formula(xv, m.weight)).transpose(1, 2)
+        return torch.autograd.grad(out, (value, m.weight), gy)
+
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(steps):
+        step()
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / steps
+    out = {"B": b, "T": t, "C": c, "ms_per_step": ms,
+           "path": "HIP kernels" if fused else "reference shifted products in torch"}
+    if fused:
+        out["roofline_step_frac"] = 10 * b * t * c / (ms * 1e-3) / HBM_PEAK
+    return out
+
+
 def time_scan(b, t, d, m, iters, device) -> dict:
     """Forward of associative_static_bayesian_cuda (one HIP kernel): mean microseconds per call."""
     from bayes_ssm.replay_ssm import associative_static_bayesian_cuda
@@ -409,6 +447,9 @@ def main() -> int:
         extras["mixer_core_config3_op_chain"] = time_mixer(b, t, h, 10, 3, device, fused=False)
         extras["mixer_readout_config3_fused"] = time_mixer(b, t, h, 30, 10, device, fused=True, gated=True)
         extras["mixer_readout_config3_op_chain"] = time_mixer(b, t, h, 10, 3, device, fused=False, gated=True)
+        qkv = h * (2 * d + m)  # channels of the mixer's fused q/k/v stream at this shape
+        extras["conv4_config3_qkv"] = time_conv(b, t, qkv, 30, 10, device, fused=True)
+        extras["conv4_config3_qkv_torch"] = time_conv(b, t, qkv, 10, 3, device, fused=False)
         extras["assoc_scan_config0"] = time_scan(1, 16, 4, 4, 50, device)
         extras["assoc_scan_config1"] = time_scan(4, 64, 16, 16, 50, device)
         result["extras"] = extras

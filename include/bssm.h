@@ -315,6 +315,28 @@ int bssm_mixer_backward(const void* q_proj, int64_t ldq, const void* k_proj, int
                         float denominator_floor, int grad_f32, void* stream);
 
 /* ------------------------------------------------------------------------
+ * Length-four causal depthwise filter.  Replaces CausalDepthwise4.forward
+ * (example/train_6layer.py:160-191) as the mixer applies it to each
+ * projected stream (:474-480): per channel c and token t,
+ *   y[t] = w[c,0] x[t-3] + w[c,1] x[t-2] + w[c,2] x[t-1] + w[c,3] x[t],
+ * x = 0 before token 0.  Channels-last rows: x [B, T, C] with row stride ldx
+ * (elements; a column view of a wider projection is fine), y [B, T, C]
+ * contiguous.  bf16 != 0: bfloat16 streams (else float32), computed in
+ * float32 and rounded once.  weight: float32 [C, 4] (the module's [C, 1, 4]).
+ * C and ldx must be multiples of 16 bytes' worth of elements (8 bf16,
+ * 4 float32) and the pointers 16-byte aligned. */
+int bssm_causal_conv4_forward(int bf16, const void* x, int64_t ldx, const float* weight, void* y,
+                              int64_t batch, int64_t t, int64_t channels, void* stream);
+
+/* Reverse: grad_x[s] = sum_j w[c,j] grad_y[s+3-j] (contiguous [B, T, C],
+ * same dtype) and the weight gradient as per-batch-entry partial sums
+ * grad_weight_partials [B, C, 4] (float32; their sum over B is the
+ * gradient of the [C, 1, 4] weight). */
+int bssm_causal_conv4_backward(int bf16, const void* x, int64_t ldx, const float* weight,
+                               const void* grad_y, void* grad_x, float* grad_weight_partials,
+                               int64_t batch, int64_t t, int64_t channels, void* stream);
+
+/* ------------------------------------------------------------------------
  * The mixer core with its readout epilogue.  Replaces, after the op chain
  * of bssm_mixer_forward, the readout of example/train_6layer.py:719-729:
  *   out = read_norm(read.to(bf16)) * silu(gate)     (per head of 8 values)

@@ -21,6 +21,7 @@ float32, autograd-friendly), written from the equations:
 * ``mixer_inputs`` / ``mixer_core``  — the Bayes mixer's producer chain and readout permute
                                        (example/train_6layer.py:627-693, :709-710)
 * ``mixer_readout``                  — its gated readout: RMSNorm(bf16(read)) * silu(gate) (:719-729)
+* ``causal_depthwise4``              — the length-four causal depthwise filter (:160-191)
 
 Pinning (tests/test_oracle.py): closed forms (scalar Kalman filter, one-step
 u = (d^2+p)k, no-update limits, Bayesian linear regression), invariants
@@ -33,7 +34,10 @@ must satisfy (exp(-softplus(x)) = sigmoid(-x), softplus(x) - softplus(-x) = x,
 unit-norm heads, the [B, T, H] -> [B*H, T] sequence map checked with
 head-tagged inputs) and by its reduction to ``run_diagonal``.  The readout
 epilogue is pinned against torch's own rms_norm / silu on bf16 tensors (the
-reference's ops), by unit RMS of the normalized head, and by gradcheck.
+reference's ops), by unit RMS of the normalized head, and by gradcheck.  The
+causal filter is pinned against torch's conv1d on the left-padded input (the
+reference's nn.Conv1d path, :478-480), by its impulse response and causality,
+and by gradcheck.
 No function here is left "parity unpinned".
 """
 from __future__ import annotations
@@ -326,6 +330,25 @@ def mixer_readout(read, gate, weight, eps: float = 1.1920928955078125e-07, read_
     n = y / (y.square().mean(-1, keepdim=True) + eps).sqrt()
     g = gate.reshape(b, t, h, 8).to(torch.float64)
     return (n * weight.to(torch.float64) * _silu(g)).reshape(b, t, h * 8)
+
+
+def causal_depthwise4(x, weight):
+    """CausalDepthwise4 (train_6layer.py:160-191): x [B, C, T], weight [C, 1, 4].
+
+    y[c, t] = sum_j weight[c, 0, j] x[c, t - 3 + j], with x = 0 before t = 0,
+    written as an explicit sum over the taps.
+    """
+    b, c, t = x.shape
+    w = weight.reshape(c, 4).to(x.dtype)
+    y = torch.zeros_like(x)
+    for j in range(4):
+        shift = 3 - j
+        if shift == 0:
+            y = y + w[:, j].view(1, c, 1) * x
+        elif shift < t:
+            y = y + torch.cat([torch.zeros(b, c, shift, dtype=x.dtype), w[:, j].view(1, c, 1) * x[..., : t - shift]],
+                              dim=-1)
+    return y
 
 
 def make_mixer_inputs(b: int, t: int, heads: int, *, seed: int = 0, ld_pad: int = 0, scale: float = 1.0):

@@ -351,3 +351,48 @@ def test_mixer_readout_gradcheck():
     # map is smooth and its autograd gradient is the one the rounding passes through.
     assert torch.autograd.gradcheck(lambda r, z, ww: O.mixer_readout(r, z, ww, read_bf16=r), (read, gate, w),
                                      eps=1e-6, atol=1e-6)
+
+
+# ------------------------------------------------------ causal depthwise filter
+def test_causal_depthwise4_matches_conv1d_and_impulse_response():
+    g = torch.Generator().manual_seed(10)
+    b, c, t = 2, 5, 9
+    x = torch.randn(b, c, t, generator=g)
+    w = torch.randn(c, 1, 4, generator=g)
+    ref = torch.nn.functional.conv1d(torch.nn.functional.pad(x, (3, 0)), w, groups=c)
+    torch.testing.assert_close(O.causal_depthwise4(x, w), ref, rtol=1e-12, atol=1e-12)
+    # Impulse at tau: y[t] = w[c, 0, 3 - (t - tau)] for 0 <= t - tau <= 3, else 0.
+    tau = 4
+    imp = torch.zeros(1, c, t)
+    imp[..., tau] = 1.0
+    y = O.causal_depthwise4(imp, w)
+    for tt in range(t):
+        want = w[:, 0, 3 - (tt - tau)] if 0 <= tt - tau <= 3 else torch.zeros(c)
+        torch.testing.assert_close(y[0, :, tt], want, rtol=0, atol=0)
+    # Causality: changing the future leaves the past alone.
+    x2 = x.clone()
+    x2[..., 6:] += 1.0
+    torch.testing.assert_close(O.causal_depthwise4(x2, w)[..., :6], O.causal_depthwise4(x, w)[..., :6], rtol=0, atol=0)
+    # Short sequences (T < 4) keep only the taps that fit.
+    torch.testing.assert_close(O.causal_depthwise4(x[..., :2], w), ref[..., :2], rtol=1e-12, atol=1e-12)
+
+
+def test_causal_depthwise4_gradcheck():
+    g = torch.Generator().manual_seed(11)
+    x = torch.randn(2, 3, 6, generator=g, dtype=torch.float64).requires_grad_(True)
+    w = torch.randn(3, 1, 4, generator=g, dtype=torch.float64).requires_grad_(True)
+    assert torch.autograd.gradcheck(O.causal_depthwise4, (x, w), eps=1e-6, atol=1e-7)
+
+
+def test_product_conv_formula_matches_oracle():
+    """The package's torch fallback (the reference's shifted products) equals the oracle."""
+    from bayes_ssm.conv import CausalDepthwise4
+
+    g = torch.Generator().manual_seed(12)
+    m = CausalDepthwise4(6, dtype=torch.float64)
+    with torch.no_grad():
+        m.weight.copy_(torch.randn(6, 1, 4, generator=g, dtype=torch.float64))
+    x = torch.randn(3, 6, 10, generator=g, dtype=torch.float64)
+    torch.testing.assert_close(m(x), O.causal_depthwise4(x, m.weight.detach()), rtol=1e-12, atol=1e-12)
+    with pytest.raises(ValueError):
+        CausalDepthwise4(6, 5)
