@@ -301,9 +301,10 @@ def main() -> int:
     ap.add_argument("--cpu-budget", type=float, default=20.0, help="seconds of CPU-baseline work (0 = skip)")
     ap.add_argument("--no-extras", action="store_true",
                     help="skip the secondary shapes (per-GPU DP shape, D1/D2/D8 variants, associative scan)")
-    ap.add_argument("--mixer", action="store_true",
-                    help="time only the mixer's producer-fused layer core at the configured shape (secondary "
-                         "workload, for profiling its kernels); prints its own JSON line")
+    ap.add_argument("--secondary", choices=("mixer", "mixer-readout", "conv4"),
+                    help="time only one secondary workload at the configured shape (the mixer's fused layer core, "
+                         "with its readout epilogue, or the causal depthwise-4 filter on the q/k/v stream), for "
+                         "profiling its kernels; prints its own JSON line")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="also run one 256 MiB device copy (reference kernel for PMC byte counters)")
     args = ap.parse_args()
@@ -320,9 +321,13 @@ def main() -> int:
     device = torch.device("cuda:0")
     torch.cuda.set_device(device)
     b, t, h, d, m = args.batch, args.seq, args.heads, args.key_dim, 8
-    if args.mixer:
-        row = time_mixer(b, t, h, args.steps, args.warmup, device, fused=True)
-        print(json.dumps({"workload": "mixer_core_fused", **row}), flush=True)
+    if args.secondary:
+        if args.secondary == "conv4":
+            row = time_conv(b, t, h * (2 * d + m), args.steps, args.warmup, device, fused=True)
+        else:
+            row = time_mixer(b, t, h, args.steps, args.warmup, device, fused=True,
+                             gated=args.secondary == "mixer-readout")
+        print(json.dumps({"workload": args.secondary, **row}), flush=True)
         return 0
     n = b * h
     leaves, m0, c0, gy = make_workload(b, t, h, d, m, device)
