@@ -51,6 +51,9 @@ _SIGNATURES = {
     "bssm_mixer_forward": [_P, _L] * 5 + [_P] * 7 + [_L, _L, _L, _L, _F, _P],
     "bssm_mixer_backward": [_P, _L] * 5 + [_P] * 7 + [_P] * 7 + [_L, _L, _L, _L, _F, _I, _P],
     "bssm_mixer_gated_forward": [_P, _L] * 6 + [_P, _F] + [_P] * 8 + [_L, _L, _L, _L, _F, _I, _P],
+    "bssm_rotation_checkpoint": [_I],
+    "bssm_forward_chunked_rotation": [_I, _I] + [_P] * 9 + [_P] * 5 + [_L, _L, _L, _F, _P],
+    "bssm_backward_chunked_rotation": [_I, _I] + [_P] * 9 + [_P] * 5 + [_P] * 9 + [_L, _L, _L, _F, _P],
     "bssm_causal_conv4_forward": [_I, _P, _L, _P, _P, _L, _L, _L, _P],
     "bssm_causal_conv4_backward": [_I, _P, _L, _P, _P, _P, _P, _L, _L, _L, _P],
     "bssm_mixer_gated_backward": [_P, _L] * 6 + [_P, _F] + [_P] * 8 + [_P] * 9 + [_L, _L, _L, _L, _F, _I, _P],
@@ -58,7 +61,7 @@ _SIGNATURES = {
     "bssm_preferred_checkpoint": [_I],
     "bssm_abi_version": [],
 }
-ABI_VERSION = 5
+ABI_VERSION = 6
 
 _lock = threading.Lock()
 _lib: Optional[ctypes.CDLL] = None

@@ -491,6 +491,14 @@ def bayesian_layer(
         return _chunked_transport(keys, values, queries, transitions, process_covariances, observation_variances,
                                   mean, cov, chunk_length=chunk_length, denominator_floor=floor)
     if rotation:
+        if device.type == "cuda" and len(batch_shape) == 1 and t > 0:
+            from .fused_cuda import fused_rotation_bayesian
+
+            fused = fused_rotation_bayesian(keys, values, queries, rotation_radii.expand(*batch_shape, t, d // 2),
+                                            rotation_angles.expand(*batch_shape, t, d // 2), process_variances,
+                                            observation_variances, mean, cov, denominator_floor=floor)
+            if fused is not None:
+                return fused
         outs = []
         for start in range(0, t, chunk_length):
             stop = min(t, start + chunk_length)

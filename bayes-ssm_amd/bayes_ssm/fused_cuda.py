@@ -513,4 +513,96 @@ def fused_diagonal_bayesian(
     )
 
 
-__all__ = ["fused_diagonal_bayesian"]
+class _ChunkedRotationFunction(torch.autograd.Function):
+    """Rotation dynamics on the HIP kernels (C ABI ``bssm_*_chunked_rotation``).
+
+    The reference runs its rotation core (bayesian_layer.py:254-323) through
+    torch.compile; here one forward and one checkpoint-replay backward kernel
+    replace it, with the same autograd results.
+    """
+
+    @staticmethod
+    def forward(ctx, keys, values, queries, radii, angles, process, observation, initial_mean, initial_covariance,
+                denominator_floor):
+        n, t, d = keys.shape
+        m = values.shape[-1]
+        interval = int(_hip.load().bssm_rotation_checkpoint(d))
+        nb = -(-t // interval)
+        dev = keys.device
+        out = torch.empty(n, t, m, device=dev, dtype=torch.float32)
+        mean_t = torch.empty(n, d, m, device=dev, dtype=torch.float32)
+        cov_t = torch.empty(n, d, d, device=dev, dtype=torch.float32)
+        bmean = torch.empty(n, nb + 1, d, m, device=dev, dtype=torch.float32)
+        bcov = torch.empty(n, nb + 1, d, d, device=dev, dtype=torch.float32)
+        P = _hip.ptr
+        with torch.cuda.device(dev):
+            _hip.call("bssm_forward_chunked_rotation", d, m, P(keys), P(values), P(queries), P(radii), P(angles),
+                      P(process), P(observation), P(initial_mean), P(initial_covariance), P(out), P(mean_t),
+                      P(cov_t), P(bmean), P(bcov), n, t, interval, float(denominator_floor), _hip.stream_of(dev))
+        ctx.save_for_backward(keys, values, queries, radii, angles, process, observation, initial_mean,
+                              initial_covariance, bmean, bcov)
+        ctx.interval = interval
+        ctx.denominator_floor = float(denominator_floor)
+        ctx.set_materialize_grads(False)
+        return out, mean_t, cov_t
+
+    @staticmethod
+    def backward(ctx, grad_output, grad_mean, grad_covariance):
+        keys, values, queries, radii, angles, process, observation, mean0, cov0, bmean, bcov = ctx.saved_tensors
+        n, t, d = keys.shape
+        m = values.shape[-1]
+        need = ctx.needs_input_grad
+        grad_output = (torch.zeros(n, t, m, device=keys.device, dtype=torch.float32) if grad_output is None
+                       else grad_output.contiguous())
+        gm = None if grad_mean is None else grad_mean.contiguous()
+        gc = None if grad_covariance is None else grad_covariance.contiguous()
+        grads = [torch.empty_like(x) for x in (keys, values, queries, radii, angles, process, observation)]
+        gm0 = torch.empty_like(mean0) if need[7] else None
+        gc0 = torch.empty_like(cov0) if need[8] else None
+        P = _hip.ptr
+        with torch.cuda.device(keys.device):
+            _hip.call("bssm_backward_chunked_rotation", d, m, P(keys), P(values), P(queries), P(radii), P(angles),
+                      P(process), P(observation), P(mean0), P(cov0), P(bmean), P(bcov), P(grad_output), P(gm),
+                      P(gc), *map(P, grads), P(gm0), P(gc0), n, t, ctx.interval, ctx.denominator_floor,
+                      _hip.stream_of(keys.device))
+        return (*(g if need[i] else None for i, g in enumerate(grads)), gm0, gc0, None)
+
+
+_ROTATION_SHAPES = ((2, 8), (4, 8), (8, 8))
+
+
+def fused_rotation_bayesian(
+    keys: Tensor,
+    values: Tensor,
+    queries: Tensor,
+    radii: Tensor,
+    angles: Tensor,
+    process: Tensor,
+    observation: Tensor,
+    initial_mean: Tensor,
+    initial_covariance: Tensor,
+    *,
+    denominator_floor: float,
+) -> tuple[Tensor, Tensor, Tensor] | None:
+    """Rotation-dynamics core on the HIP kernels; ``None`` means "use the torch path".
+
+    Contract: CUDA float32 tensors, keys/queries [N,T,D] with (D, M) in
+    {(2,8), (4,8), (8,8)}, values [N,T,M], radii/angles/process (per pair)
+    [N,T,D/2], observation [N,T], initial mean [N,D,M] and covariance [N,D,D].
+    """
+    tensors = (keys, values, queries, radii, angles, process, observation, initial_mean, initial_covariance)
+    if keys.device.type != "cuda" or keys.ndim != 3 or not all(x.dtype == torch.float32 for x in tensors):
+        return None
+    n, t, d = keys.shape
+    m = values.shape[-1]
+    if (d, m) not in _ROTATION_SHAPES or os.environ.get("BAYES_SSM_DISABLE_FUSED_CUDA", "0") == "1":
+        return None
+    expect = ((n, t, d), (n, t, m), (n, t, d), (n, t, d // 2), (n, t, d // 2), (n, t, d // 2), (n, t), (n, d, m),
+              (n, d, d))
+    if any(tuple(x.shape) != e for x, e in zip(tensors, expect)):
+        return None
+    _hip.load()
+    return _ChunkedRotationFunction.apply(*(x.contiguous() for x in tensors), float(denominator_floor))
+
+
+__all__ = ["fused_diagonal_bayesian", "fused_rotation_bayesian"]

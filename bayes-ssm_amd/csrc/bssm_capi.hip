@@ -253,7 +253,7 @@ extern "C" {
 
 const char* bssm_last_error(void) { return g_error; }
 
-int bssm_abi_version(void) { return 5; }
+int bssm_abi_version(void) { return 6; }
 
 int bssm_supported(int key_dim, int value_dim) { return supported(key_dim, value_dim) ? 1 : 0; }
 
@@ -637,6 +637,98 @@ int bssm_mixer_gated_backward(const void* q_proj, int64_t ldq, const void* k_pro
   a.b = batch; a.t = t; a.h = heads; a.chunk = chunk; a.nb = (t + chunk - 1) / chunk; a.floor = denominator_floor;
   if (n == 0) return ok();
   return launched(fn, bssm::launch_mixer_backward(a, static_cast<hipStream_t>(stream)));
+}
+
+int bssm_rotation_checkpoint(int key_dim) { return bssm::rotation_checkpoint(key_dim); }
+
+namespace {
+int rotation_common(const char* fn, int d, int m, int64_t n, int64_t t, int64_t chunk, float floor) {
+  if (m != 8 || (d != 2 && d != 4 && d != 8))
+    return fail(BSSM_ERR_UNSUPPORTED, "%s: rotation kernels support key_dim 2, 4, 8 with value_dim 8, got (%d, %d)",
+                fn, d, m);
+  if (n < 0 || t < 0) return fail(BSSM_ERR_ARGUMENT, "%s: negative size", fn);
+  if (chunk <= 0) return fail(BSSM_ERR_ARGUMENT, "%s: chunk must be positive, got %lld", fn, (long long)chunk);
+  if (!(floor > 0.f)) return fail(BSSM_ERR_ARGUMENT, "%s: denominator_floor must be positive", fn);
+  if (n > (int64_t)0x7fffffff * 4 || t * 8 > ((int64_t)1 << 25))
+    return fail(BSSM_ERR_ARGUMENT, "%s: n or t too large", fn);
+  return BSSM_OK;
+}
+int rotation_vec(std::initializer_list<const void*> streams, int64_t t, int d) {
+  for (const void* p : streams)
+    if (p != nullptr && !aligned16(p)) return 0;
+  return (t * (d / 2)) % 4 == 0 && t % 4 == 0;
+}
+}  // namespace
+
+int bssm_forward_chunked_rotation(int key_dim, int value_dim, const float* keys, const float* values,
+                                  const float* queries, const float* radii, const float* angles,
+                                  const float* process, const float* observation, const float* mean0,
+                                  const float* cov0, float* out, float* mean_final, float* cov_final, float* bmean,
+                                  float* bcov, int64_t n, int64_t t, int64_t chunk, float denominator_floor,
+                                  void* stream) {
+  const char* fn = "bssm_forward_chunked_rotation";
+  if (int rc = rotation_common(fn, key_dim, value_dim, n, t, chunk, denominator_floor)) return rc;
+  BSSM_REQUIRE_T(keys);
+  BSSM_REQUIRE_T(values);
+  BSSM_REQUIRE_T(queries);
+  BSSM_REQUIRE_T(radii);
+  BSSM_REQUIRE_T(angles);
+  BSSM_REQUIRE_T(process);
+  BSSM_REQUIRE_T(observation);
+  BSSM_REQUIRE_T(out);
+  BSSM_REQUIRE(mean0);
+  BSSM_REQUIRE(cov0);
+  BSSM_REQUIRE(mean_final);
+  BSSM_REQUIRE(cov_final);
+  BSSM_REQUIRE(bmean);
+  BSSM_REQUIRE(bcov);
+  bssm::RotArgs a{};
+  a.k = keys; a.v = values; a.q = queries; a.rad = radii; a.ang = angles; a.p = process; a.r = observation;
+  a.m0 = mean0; a.c0 = cov0; a.y = out; a.mT = mean_final; a.cT = cov_final; a.bm = bmean; a.bc = bcov;
+  a.n = n; a.t = t; a.chunk = chunk; a.nb = (t + chunk - 1) / chunk; a.floor = denominator_floor;
+  a.vec = rotation_vec({keys, values, queries, radii, angles, process, observation, out}, t, key_dim);
+  if (n == 0) return ok();
+  return launched(fn, bssm::launch_rotation_forward(key_dim, a, static_cast<hipStream_t>(stream)));
+}
+
+int bssm_backward_chunked_rotation(int key_dim, int value_dim, const float* keys, const float* values,
+                                   const float* queries, const float* radii, const float* angles,
+                                   const float* process, const float* observation, const float* mean0,
+                                   const float* cov0, const float* bmean, const float* bcov, const float* gy,
+                                   const float* gmf, const float* gcf, float* gk, float* gv, float* gq,
+                                   float* g_radii, float* g_angles, float* g_process, float* g_observation,
+                                   float* gm0, float* gc0, int64_t n, int64_t t, int64_t chunk,
+                                   float denominator_floor, void* stream) {
+  const char* fn = "bssm_backward_chunked_rotation";
+  if (int rc = rotation_common(fn, key_dim, value_dim, n, t, chunk, denominator_floor)) return rc;
+  BSSM_REQUIRE_T(keys);
+  BSSM_REQUIRE_T(values);
+  BSSM_REQUIRE_T(queries);
+  BSSM_REQUIRE_T(radii);
+  BSSM_REQUIRE_T(angles);
+  BSSM_REQUIRE_T(process);
+  BSSM_REQUIRE_T(observation);
+  BSSM_REQUIRE_T(gy);
+  BSSM_REQUIRE(bmean);
+  BSSM_REQUIRE(bcov);
+  BSSM_REQUIRE_T(gk);
+  BSSM_REQUIRE_T(gv);
+  BSSM_REQUIRE_T(gq);
+  BSSM_REQUIRE_T(g_radii);
+  BSSM_REQUIRE_T(g_angles);
+  BSSM_REQUIRE_T(g_process);
+  BSSM_REQUIRE_T(g_observation);
+  bssm::RotArgs a{};
+  a.k = keys; a.v = values; a.q = queries; a.rad = radii; a.ang = angles; a.p = process; a.r = observation;
+  a.m0 = mean0; a.c0 = cov0; a.bm = const_cast<float*>(bmean); a.bc = const_cast<float*>(bcov);
+  a.gy = gy; a.gmf = gmf; a.gcf = gcf;
+  a.gk = gk; a.gv = gv; a.gq = gq; a.grad = g_radii; a.gang = g_angles; a.gp = g_process; a.gr = g_observation;
+  a.gm0 = gm0; a.gc0 = gc0;
+  a.n = n; a.t = t; a.chunk = chunk; a.nb = (t + chunk - 1) / chunk; a.floor = denominator_floor;
+  a.vec = rotation_vec({keys, values, queries, radii, angles, process, observation, gy, gk, gv, gq, g_radii,
+                        g_angles, g_process, g_observation}, t, key_dim);
+  if (n == 0) return ok();
+  return launched(fn, bssm::launch_rotation_backward(key_dim, a, static_cast<hipStream_t>(stream)));
 }
 
 int bssm_causal_conv4_forward(int bf16, const void* x, int64_t ldx, const float* weight, void* y, int64_t batch,

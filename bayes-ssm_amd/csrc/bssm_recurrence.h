@@ -133,6 +133,24 @@ struct MixArgs {
 hipError_t launch_mixer_forward(const MixArgs& a, hipStream_t stream);
 hipError_t launch_mixer_backward(const MixArgs& a, hipStream_t stream);
 
+// Rotation dynamics (bssm_rotation.hip): keys/queries [N, T, D], values,
+// out, gy [N, T, 8], radii/angles/process (per pair) [N, T, D/2],
+// observation [N, T]; belief tensors as the diagonal ABI.  vec: every stream
+// 16-byte aligned with T a multiple of 4.
+struct RotArgs {
+  const float *k, *v, *q, *rad, *ang, *p, *r;
+  const float *m0, *c0;
+  float *y, *mT, *cT, *bm, *bc;
+  const float *gy, *gmf, *gcf;
+  float *gk, *gv, *gq, *grad, *gang, *gp, *gr, *gm0, *gc0;
+  int64_t n, t, chunk, nb;
+  float floor;
+  int vec;
+};
+int rotation_checkpoint(int key_dim);
+hipError_t launch_rotation_forward(int key_dim, const RotArgs& a, hipStream_t stream);
+hipError_t launch_rotation_backward(int key_dim, const RotArgs& a, hipStream_t stream);
+
 // Length-four causal depthwise filter on channels-last rows (bssm_conv4.hip):
 // x [B, T, C] with row stride ldx (elements), y / gy / gx contiguous
 // [B, T, C], weight float32 [C, 4], gw_part float32 [B, C, 4]; bfloat16 or

@@ -1,0 +1,776 @@
+// gfx950 kernels for the exact dense-covariance recurrence with
+// block-diagonal damped 2-D rotations (bayes_ssm/bayesian_layer.py:254-323).
+//
+// Pair k = state rows (2k, 2k+1) turns by R_k = [[c, -s], [s, c]] with
+// c = rho cos(theta), s = rho sin(theta), rho = min(max(radius, tiny), 1),
+// and its process variance is added to entry (2k, 2k) only:
+//   P' = R P R^T + Q     M' = R M     u = P' k     s = r + k.u
+//   beta = 1 / max(s, floor)          e = v - M'^T k
+//   M <- M' + beta u e^T              P <- P' - beta u u^T      y = M^T q
+// (the reference symmetrises P after every token; here P' is formed in a
+// symmetric summation order, so P stays bitwise symmetric as in the
+// diagonal kernels).
+//
+// Work decomposition as the diagonal kernels (bssm_common.h): a group of G
+// lanes per sequence, covariance rows round-robin over the group, value
+// columns split.  The two rows of a pair always sit in lanes g and g ^ 1 at
+// the same slot, so the row mixing of R is one DPP exchange; the column
+// mixing is local.  P'_ij sums its four terms t_ab = (R_ia R_jb) P_ab as
+// (t00 + t11) + (t01 + t10), which the owners of rows i and j evaluate to the
+// same bits.
+//
+// The backward replays each checkpoint chunk on chip and reverses it.  Per
+// token, with H = S + sym(gu k^T) (S = sym(dL/dP_new)) the adjoint of P':
+//   S_prev = R^T H R,   gM_prev = R^T (gM - k ge^T),
+//   dL/dR = 2 H R P_prev + (gM - k ge^T) M_prev^T  (pair blocks only),
+//   dL/dc_k = dR_{2k,2k} + dR_{2k+1,2k+1},  dL/ds_k = dR_{2k+1,2k} - dR_{2k,2k+1},
+//   dL/dtheta = rho (dL/ds cos - dL/dc sin),  dL/drho = dL/dc cos + dL/ds sin
+//   (zero where the radius clamp is active), dL/dq_k = H_{2k,2k}.
+// The initial-covariance adjoint keeps the asymmetric convention of the
+// diagonal kernels: R^T (S + gu k^T) R at the first token.
+
+#include <cfloat>
+
+#include "bssm_step.h"
+
+namespace bssm {
+namespace rot {
+namespace {
+
+constexpr float kTiny = FLT_MIN;  // torch.finfo(float32).tiny
+
+// sin and cos of x without a library call (an outlined call makes the
+// caller save its live registers to scratch).  Cody-Waite reduction by pi/2
+// in double precision (pi/2 as a two-double sum; n x pi/2 is exact in the
+// fma for any |x| below 2^40), then the Taylor series on |r| <= pi/4:
+// sin to r^9 (next term below 7e-10 relative) and cos to r^10 (below 1.2e-10).
+__device__ __forceinline__ void sincos_rad(float x, float& s, float& c) {
+  const double xd = x;
+  const double n = rint(xd * 0.6366197723675814);
+  const double rd = fma(-n, 6.123233995736766e-17, fma(-n, 1.5707963267948966, xd));
+  const float r = static_cast<float>(rd), r2 = r * r;
+  float ps = 1.f / 362880.f;
+  ps = fmaf(ps, r2, -1.f / 5040.f);
+  ps = fmaf(ps, r2, 1.f / 120.f);
+  ps = fmaf(ps, r2, -1.f / 6.f);
+  const float sr = fmaf(r * r2, ps, r);
+  float pc = -1.f / 3628800.f;
+  pc = fmaf(pc, r2, 1.f / 40320.f);
+  pc = fmaf(pc, r2, -1.f / 720.f);
+  pc = fmaf(pc, r2, 1.f / 24.f);
+  pc = fmaf(pc, r2, -0.5f);
+  const float cr = fmaf(r2, pc, 1.f);
+  const int q = static_cast<int>(static_cast<int64_t>(n) & 3);
+  s = (q == 0) ? sr : (q == 1) ? cr : (q == 2) ? -sr : -cr;
+  c = (q == 0) ? cr : (q == 1) ? -sr : (q == 2) ? -cr : sr;
+}
+
+template <int D, int M, int G>
+struct TokRot {
+  using L = Layout<D, M, G>;
+  static constexpr int J = D / 2;
+  float k[D], k_own[L::RPL];
+  float v[L::CPL];
+  float c[J], sn[J];    // rotation coefficients of every pair
+  float cs[J], si[J];   // cos, sin of the angles (backward)
+  float rho[J];         // clamped radii
+  bool live[J];         // the radius clamp passes gradients
+  float p[J], r;
+};
+
+// Rotation-dynamics tile pointers of one sequence.
+struct RotTile {
+  const float* k;
+  const float* v;
+  const float* rad;
+  const float* ang;
+  const float* p;
+  const float* r;
+};
+
+template <int D, int M, int G>
+__device__ __forceinline__ void read_rot(TokRot<D, M, G>& in, const RotTile& st, int tt, int g, bool need_v) {
+  using L = Layout<D, M, G>;
+  constexpr int J = D / 2;
+#pragma unroll
+  for (int j = 0; j < D; ++j) in.k[j] = st.k[tt * D + j];
+#pragma unroll
+  for (int jj = 0; jj < L::RPL; ++jj) in.k_own[jj] = st.k[tt * D + L::row(g, jj)];
+#pragma unroll
+  for (int m = 0; m < J; ++m) {
+    const float rc = fmaxf(st.rad[tt * J + m], kTiny);
+    in.live[m] = st.rad[tt * J + m] >= kTiny && rc <= 1.f;
+    in.rho[m] = rc <= 1.f ? rc : 1.f;
+    float sa, ca;
+    sincos_rad(st.ang[tt * J + m], sa, ca);
+    in.cs[m] = ca;
+    in.si[m] = sa;
+    in.c[m] = in.rho[m] * ca;
+    in.sn[m] = in.rho[m] * sa;
+    in.p[m] = st.p[tt * J + m];
+  }
+  in.r = st.r[tt];
+  if (need_v) {
+#pragma unroll
+    for (int c = 0; c < L::CPL; ++c) in.v[c] = st.v[tt * M + g * L::CPL + c];
+  }
+}
+
+// Element k of a small register array for a lane-dependent k, by selects
+// (indexing with it would move the array to scratch memory).  The empty asm
+// makes each element an opaque register value, so the selects are not
+// folded back into one indexed load.
+template <int J>
+__device__ __forceinline__ float pick(const float (&x)[J], int k) {
+  float v = x[0];
+#pragma unroll
+  for (int m = 1; m < J; ++m) {
+    float xm = x[m];
+    __asm__("" : "+v"(xm));
+    v = (k == m) ? xm : v;
+  }
+  return v;
+}
+
+// R_{i, a} for a = 2 (i >> 1) + t (t = 0, 1), and the transposed R_{a, i}.
+template <int J>
+__device__ __forceinline__ float r_row(const float (&c)[J], const float (&s)[J], int i, int t) {
+  const int k = i >> 1;
+  const float ck = pick<J>(c, k), sk = pick<J>(s, k);
+  if (i & 1) return t ? ck : sk;
+  return t ? -sk : ck;
+}
+template <int J>
+__device__ __forceinline__ float r_col(const float (&c)[J], const float (&s)[J], int i, int t) {
+  const int k = i >> 1;
+  const float ck = pick<J>(c, k), sk = pick<J>(s, k);
+  if (i & 1) return t ? ck : -sk;
+  return t ? sk : ck;
+}
+
+// X_ij = sum_{a in pair(i), b in pair(j)} A_ia X0_ab A_jb for the lane's own
+// rows, A = R (TRANS false) or R^T (TRANS true), in the symmetric order.
+// own[jj] is row(g, jj) of X0, part[jj] the partner row (row ^ 1).
+template <int D, int M, int G, bool TRANS>
+__device__ __forceinline__ void sandwich(const float (&c)[D / 2], const float (&s)[D / 2], const RowsArr<D, M, G>& own,
+                                         const RowsArr<D, M, G>& part, int g, RowsArr<D, M, G>& out) {
+  using L = Layout<D, M, G>;
+  constexpr int J = D / 2;
+#pragma unroll
+  for (int jj = 0; jj < L::RPL; ++jj) {
+    const int i = L::row(g, jj);
+    const bool odd = i & 1;
+    const float ri0 = TRANS ? r_col<J>(c, s, i, 0) : r_row<J>(c, s, i, 0);
+    const float ri1 = TRANS ? r_col<J>(c, s, i, 1) : r_row<J>(c, s, i, 1);
+#pragma unroll
+    for (int j = 0; j < D; ++j) {
+      const float rj0 = TRANS ? r_col<J>(c, s, j, 0) : r_row<J>(c, s, j, 0);
+      const float rj1 = TRANS ? r_col<J>(c, s, j, 1) : r_row<J>(c, s, j, 1);
+      const int b0 = j & ~1, b1 = j | 1;
+      const float a0b0 = odd ? part[jj][b0] : own[jj][b0], a0b1 = odd ? part[jj][b1] : own[jj][b1];
+      const float a1b0 = odd ? own[jj][b0] : part[jj][b0], a1b1 = odd ? own[jj][b1] : part[jj][b1];
+      const float t00 = (ri0 * rj0) * a0b0, t11 = (ri1 * rj1) * a1b1;
+      const float t01 = (ri0 * rj1) * a0b1, t10 = (ri1 * rj0) * a1b0;
+      out[jj][j] = (t00 + t11) + (t01 + t10);
+    }
+  }
+}
+
+template <int D, int M, int G>
+__device__ __forceinline__ void partner_rows(const RowsArr<D, M, G>& x, RowsArr<D, M, G>& y) {
+  using L = Layout<D, M, G>;
+#pragma unroll
+  for (int jj = 0; jj < L::RPL; ++jj)
+#pragma unroll
+    for (int j = 0; j < D; ++j) y[jj][j] = xor_lane<0>(x[jj][j]);
+}
+
+// One forward token.  Pb receives P' (own rows).
+template <int D, int M, int G>
+__device__ __forceinline__ void step_rot(Belief<D, M, G>& b, const TokRot<D, M, G>& in, float floor, int g, int lane,
+                                         StepOut<D, M, G>& o, RowsArr<D, M, G>& Pb) {
+  using L = Layout<D, M, G>;
+  constexpr int J = D / 2;
+  float Pn[L::RPL][D];
+  partner_rows<D, M, G>(b.P, Pn);
+  sandwich<D, M, G, false>(in.c, in.sn, b.P, Pn, g, Pb);
+#pragma unroll
+  for (int jj = 0; jj < L::RPL; ++jj) {
+    const int i = L::row(g, jj);
+    if (!(i & 1)) {
+#pragma unroll
+      for (int j = 0; j < D; j += 2)
+        if (j == i) Pb[jj][j] += in.p[j >> 1];
+    }
+    float acc = 0.f;
+#pragma unroll
+    for (int j = 0; j < D; ++j) acc = fmaf(Pb[jj][j], in.k[j], acc);
+    o.u_own[jj] = acc;
+  }
+  gather_rows<D, M, G>(o.u_own, o.u, lane);
+  float s = in.r;
+#pragma unroll
+  for (int j = 0; j < D; ++j) s = fmaf(in.k[j], o.u[j], s);
+  o.s = s;
+  const float beta = fast_rcp(fmaxf(s, floor));
+#pragma unroll
+  for (int cc = 0; cc < L::CPL; ++cc) {
+    float mr[D];
+#pragma unroll
+    for (int i = 0; i < D; ++i) {
+      const int a0 = i & ~1;
+      mr[i] = fmaf(r_row<J>(in.c, in.sn, i, 1), b.Mv[a0 + 1][cc], r_row<J>(in.c, in.sn, i, 0) * b.Mv[a0][cc]);
+    }
+    float e = in.v[cc];
+#pragma unroll
+    for (int i = 0; i < D; ++i) e = fmaf(-mr[i], in.k[i], e);
+    o.e[cc] = e;
+#pragma unroll
+    for (int i = 0; i < D; ++i) b.Mv[i][cc] = fmaf(beta * o.u[i], e, mr[i]);
+  }
+#pragma unroll
+  for (int jj = 0; jj < L::RPL; ++jj)
+#pragma unroll
+    for (int j = 0; j < D; ++j) b.P[jj][j] = fmaf(-beta, o.u_own[jj] * o.u[j], Pb[jj][j]);
+}
+
+template <int D, int M, int G>
+struct RotHist {
+  using L = Layout<D, M, G>;
+  float Pp[L::RPL][D];  // covariance rows before the token
+  float Mp[D][L::CPL];  // mean block before the token
+  float u[D];
+  float u_own[L::RPL];
+  float s;
+  float e[L::CPL];
+};
+
+template <int D, int M, int G>
+struct RotOut {
+  using L = Layout<D, M, G>;
+  float gk_own[L::RPL], gq_own[L::RPL];
+  float gv[L::CPL];
+  float grad_rad[D / 2], grad_ang[D / 2], gp[D / 2];
+  float gr;
+};
+
+// Reverse of one token (see the header comment).  gM, Gs: carried adjoints,
+// updated in place.
+template <int D, int M, int G>
+__device__ __forceinline__ void reverse_rot(const TokRot<D, M, G>& in, const RotHist<D, M, G>& h,
+                                            const float (&q)[D], const float (&gy)[Layout<D, M, G>::CPL],
+                                            ColsArr<D, M, G>& gM, RowsArr<D, M, G>& Gs, float floor, int g,
+                                            int lane, bool first_token, RowsArr<D, M, G>& gc0r,
+                                            RotOut<D, M, G>& o) {
+  using L = Layout<D, M, G>;
+  constexpr int RPL = L::RPL, CPL = L::CPL, J = D / 2;
+  const bool writer = L::row_writer(g);
+  const float beta = fast_rcp(fmaxf(h.s, floor));
+
+  // P' (own rows) and M' = R M_prev (own columns), recomputed from the history.
+  float Pb[RPL][D];
+  {
+    float Pn[RPL][D];
+    partner_rows<D, M, G>(h.Pp, Pn);
+    sandwich<D, M, G, false>(in.c, in.sn, h.Pp, Pn, g, Pb);
+#pragma unroll
+    for (int jj = 0; jj < RPL; ++jj) {
+      const int i = L::row(g, jj);
+#pragma unroll
+      for (int j = 0; j < D; j += 2)
+        if (j == i) Pb[jj][j] += in.p[j >> 1];
+    }
+  }
+  float mp[D][CPL];
+#pragma unroll
+  for (int cc = 0; cc < CPL; ++cc)
+#pragma unroll
+    for (int i = 0; i < D; ++i) {
+      const int a0 = i & ~1;
+      mp[i][cc] = fmaf(r_row<J>(in.c, in.sn, i, 1), h.Mp[a0 + 1][cc], r_row<J>(in.c, in.sn, i, 0) * h.Mp[a0][cc]);
+    }
+
+  // Value-column part.
+  float gqp[D], ap[D], gkp[D];
+#pragma unroll
+  for (int i = 0; i < D; ++i) gqp[i] = ap[i] = gkp[i] = 0.f;
+#pragma unroll
+  for (int i = 0; i < D; ++i) {
+    const float bu = beta * h.u[i];
+#pragma unroll
+    for (int cc = 0; cc < CPL; ++cc) {
+      gqp[i] = fmaf(fmaf(bu, h.e[cc], mp[i][cc]), gy[cc], gqp[i]);
+      gM[i][cc] = fmaf(q[i], gy[cc], gM[i][cc]);
+    }
+  }
+  float ge[CPL];
+#pragma unroll
+  for (int cc = 0; cc < CPL; ++cc) {
+    float z = 0.f;
+#pragma unroll
+    for (int i = 0; i < D; ++i) z = fmaf(gM[i][cc], h.u[i], z);
+    ge[cc] = beta * z;
+    o.gv[cc] = ge[cc];
+  }
+  float gcm[J], gsm[J];
+#pragma unroll
+  for (int m = 0; m < J; ++m) gcm[m] = gsm[m] = 0.f;
+#pragma unroll
+  for (int cc = 0; cc < CPL; ++cc) {
+    float gmb[D];
+#pragma unroll
+    for (int i = 0; i < D; ++i) {
+      ap[i] = fmaf(gM[i][cc], h.e[cc], ap[i]);
+      gkp[i] = fmaf(-mp[i][cc], ge[cc], gkp[i]);
+      gmb[i] = fmaf(-in.k[i], ge[cc], gM[i][cc]);
+    }
+#pragma unroll
+    for (int m = 0; m < J; ++m) {
+      const float g0 = gmb[2 * m], g1 = gmb[2 * m + 1];
+      const float m0 = h.Mp[2 * m][cc], m1 = h.Mp[2 * m + 1][cc];
+      gcm[m] = fmaf(g0, m0, fmaf(g1, m1, gcm[m]));
+      gsm[m] = fmaf(g1, m0, fmaf(-g0, m1, gsm[m]));
+      gM[2 * m][cc] = fmaf(in.sn[m], g1, in.c[m] * g0);
+      gM[2 * m + 1][cc] = fmaf(-in.sn[m], g0, in.c[m] * g1);
+    }
+  }
+#pragma unroll
+  for (int m = 0; m < J; ++m) {
+    gcm[m] = group_sum<G>(gcm[m]);
+    gsm[m] = group_sum<G>(gsm[m]);
+  }
+  float a_own[RPL], gkc[RPL];
+  group_reduce_rows<D, G>(ap, a_own, g);
+  group_reduce_rows<D, G>(gkp, gkc, g);
+  group_reduce_rows<D, G>(gqp, o.gq_own, g);
+
+  // Covariance-row part.
+  float w_own[RPL];
+  float zp = 0.f;
+#pragma unroll
+  for (int jj = 0; jj < RPL; ++jj) {
+    float w = 0.f;
+#pragma unroll
+    for (int j = 0; j < D; ++j) w = fmaf(Gs[jj][j], h.u[j], w);
+    w_own[jj] = w;
+    zp = fmaf(h.u_own[jj], a_own[jj] - w, zp);
+  }
+  const float z = group_sum<G>(writer ? zp : 0.f);
+  const float gs = (h.s > floor) ? -z * beta * beta : 0.f;
+  float gu_own[RPL], gu[D];
+#pragma unroll
+  for (int jj = 0; jj < RPL; ++jj) gu_own[jj] = fmaf(beta, a_own[jj] - 2.f * w_own[jj], gs * in.k_own[jj]);
+  gather_rows<D, M, G>(gu_own, gu, lane);
+
+  float H[RPL][D];
+#pragma unroll
+  for (int jj = 0; jj < RPL; ++jj) {
+    float gk = fmaf(gs, h.u_own[jj], gkc[jj]);
+#pragma unroll
+    for (int j = 0; j < D; ++j) {
+      gk = fmaf(Pb[jj][j], gu[j], gk);
+      H[jj][j] = fmaf(0.5f, gu_own[jj] * in.k[j] + gu[j] * in.k_own[jj], Gs[jj][j]);
+    }
+    o.gk_own[jj] = gk;
+  }
+
+  // dL/dR from the covariance: 2 H R P_prev on the pair blocks.  Y = P_prev R^T
+  // (row a of it is row a of P_prev with its columns mixed by R).
+  float Y[RPL][D], Yn[RPL][D];
+#pragma unroll
+  for (int jj = 0; jj < RPL; ++jj)
+#pragma unroll
+    for (int j = 0; j < D; ++j) {
+      const int b0 = j & ~1;
+      Y[jj][j] = fmaf(r_row<J>(in.c, in.sn, j, 1), h.Pp[jj][b0 + 1], r_row<J>(in.c, in.sn, j, 0) * h.Pp[jj][b0]);
+    }
+  partner_rows<D, M, G>(Y, Yn);
+  float gcp[J], gsp[J], gpp[J];
+#pragma unroll
+  for (int m = 0; m < J; ++m) gcp[m] = gsp[m] = gpp[m] = 0.f;
+#pragma unroll
+  for (int jj = 0; jj < RPL; ++jj) {
+    const int i = L::row(g, jj);
+    float self = 0.f, cross = 0.f;
+#pragma unroll
+    for (int j = 0; j < D; ++j) {
+      self = fmaf(H[jj][j], Y[jj][j], self);
+      cross = fmaf(H[jj][j], Yn[jj][j], cross);
+    }
+    // Row i even: dR_{i,i} = 2 self, dR_{i,i+1} = 2 cross; odd: dR_{i,i} = 2 self, dR_{i,i-1} = 2 cross.
+    const int m = i >> 1;
+    float hii = 0.f;
+#pragma unroll
+    for (int j = 0; j < D; ++j) hii = (j == i) ? H[jj][j] : hii;
+#pragma unroll
+    for (int mm = 0; mm < J; ++mm) {
+      if (mm == m) {
+        gcp[mm] += 2.f * self;
+        gsp[mm] += (i & 1) ? 2.f * cross : -2.f * cross;
+        if (!(i & 1)) gpp[mm] += hii;
+      }
+    }
+  }
+  // The two rows of a pair are in lanes g and g ^ 1; with replicated rows
+  // (D < G) each lane pair holds a full copy.
+#pragma unroll
+  for (int m = 0; m < J; ++m) {
+    float cp = gcp[m], sp = gsp[m], pq = gpp[m];
+    if constexpr (D >= G) {
+      // Rows of pair m: lanes owner(2m), owner(2m) + 1; other lanes hold 0.
+      cp = group_sum<G>(cp);
+      sp = group_sum<G>(sp);
+      pq = group_sum<G>(pq);
+    } else {
+      cp += xor_lane<0>(cp);
+      sp += xor_lane<0>(sp);
+      pq += xor_lane<0>(pq);
+    }
+    const float gc = gcm[m] + cp, gsn = gsm[m] + sp;
+    o.grad_rad[m] = in.live[m] ? fmaf(gc, in.cs[m], gsn * in.si[m]) : 0.f;
+    o.grad_ang[m] = in.rho[m] * fmaf(gsn, in.cs[m], -gc * in.si[m]);
+    o.gp[m] = pq;
+  }
+  o.gr = gs;
+
+  // Carried covariance adjoint S_prev = R^T H R (and the asymmetric initial
+  // adjoint R^T (S + gu k^T) R at the first token).
+  {
+    float Hn[RPL][D];
+    partner_rows<D, M, G>(H, Hn);
+    if (first_token) {
+      float A[RPL][D], An[RPL][D];
+#pragma unroll
+      for (int jj = 0; jj < RPL; ++jj)
+#pragma unroll
+        for (int j = 0; j < D; ++j) A[jj][j] = fmaf(gu_own[jj], in.k[j], Gs[jj][j]);
+      partner_rows<D, M, G>(A, An);
+      sandwich<D, M, G, true>(in.c, in.sn, A, An, g, gc0r);
+    }
+    sandwich<D, M, G, true>(in.c, in.sn, H, Hn, g, Gs);
+  }
+}
+
+// ------------------------------------------------------------------ kernels
+template <int D, int M, int G, int TT>
+__global__ __launch_bounds__(kWave) void forward_kernel(RotArgs a) {
+  using L = Layout<D, M, G>;
+  constexpr int SPW = L::SPW, J = D / 2;
+  constexpr int SD = Tile<D, TT>::STRIDE, SM = Tile<M, TT>::STRIDE, SJ = Tile<J, TT>::STRIDE,
+                S1 = Tile<1, TT>::STRIDE;
+  __shared__ float sk[SPW * SD];
+  __shared__ float sq[SPW * SD];
+  __shared__ float sv[SPW * SM];  // values in, readouts out
+  __shared__ float srad[SPW * SJ];
+  __shared__ float sang[SPW * SJ];
+  __shared__ float sp[SPW * SJ];
+  __shared__ float sr[SPW * S1];
+
+  const int lane = threadIdx.x;
+  const int g = lane % G;
+  const int s = lane / G;
+  const int64_t n0 = static_cast<int64_t>(blockIdx.x) * SPW;
+  const int64_t n = n0 + s;
+  const bool active = n < a.n;
+  const int64_t na = active ? n : 0;
+  const int64_t T = a.t;
+
+  Belief<D, M, G> b;
+  load_belief<D, M, G>(b, a.m0 + na * D * M, a.c0 + na * D * D, g, active);
+  const int64_t bm_seq = (a.nb + 1) * D * M, bc_seq = (a.nb + 1) * D * D;
+  if (active) store_belief<D, M, G>(b, a.bm + na * bm_seq, a.bc + na * bc_seq, g);
+
+  RotTile st{sk + s * SD, sv + s * SM, srad + s * SJ, sang + s * SJ, sp + s * SJ, sr + s * S1};
+  const float* qs = sq + s * SD;
+  float* ys = sv + s * SM;
+  int64_t next_ckpt = a.chunk, ckpt = 1;
+  for (int64_t t0 = 0; t0 < T; t0 += TT) {
+    const int len = tile_len(T, t0, TT);
+    const bool vec = a.vec && (t0 % 4 == 0);
+    stage_in<D, TT, SPW>(sk, a.k, n0, a.n, T, t0, len, vec, lane);
+    stage_in<D, TT, SPW>(sq, a.q, n0, a.n, T, t0, len, vec, lane);
+    stage_in<M, TT, SPW>(sv, a.v, n0, a.n, T, t0, len, vec, lane);
+    stage_in<J, TT, SPW>(srad, a.rad, n0, a.n, T, t0, len, vec, lane);
+    stage_in<J, TT, SPW>(sang, a.ang, n0, a.n, T, t0, len, vec, lane);
+    stage_in<J, TT, SPW>(sp, a.p, n0, a.n, T, t0, len, vec, lane);
+    stage_in<1, TT, SPW>(sr, a.r, n0, a.n, T, t0, len, vec, lane);
+    __syncthreads();
+    for (int tt = 0; tt < len; ++tt) {
+      if (t0 + tt == next_ckpt) {
+        if (active)
+          store_belief<D, M, G>(b, a.bm + na * bm_seq + ckpt * D * M, a.bc + na * bc_seq + ckpt * D * D, g);
+        ++ckpt;
+        next_ckpt += a.chunk;
+      }
+      TokRot<D, M, G> in;
+      read_rot<D, M, G>(in, st, tt, g, true);
+      StepOut<D, M, G> o;
+      float Pb[L::RPL][D];
+      step_rot<D, M, G>(b, in, a.floor, g, lane, o, Pb);
+#pragma unroll
+      for (int c = 0; c < L::CPL; ++c) {
+        float y = 0.f;
+#pragma unroll
+        for (int i = 0; i < D; ++i) y = fmaf(b.Mv[i][c], qs[tt * D + i], y);
+        ys[tt * M + g * L::CPL + c] = y;
+      }
+    }
+    __syncthreads();
+    stage_out<M, TT, SPW>(sv, a.y, n0, a.n, T, t0, len, vec, lane);
+    __syncthreads();
+  }
+  if (active) {
+    store_belief<D, M, G>(b, a.mT + na * D * M, a.cT + na * D * D, g);
+    if (T > 0) store_belief<D, M, G>(b, a.bm + na * bm_seq + a.nb * D * M, a.bc + na * bc_seq + a.nb * D * D, g);
+  }
+}
+
+template <int D, int M, int G, int SUB>
+__global__ __launch_bounds__(kWave) void backward_kernel(RotArgs a) {
+  using L = Layout<D, M, G>;
+  constexpr int SPW = L::SPW, RPL = L::RPL, CPL = L::CPL, J = D / 2;
+  constexpr int SD = Tile<D, SUB>::STRIDE, SM = Tile<M, SUB>::STRIDE, SJ = Tile<J, SUB>::STRIDE,
+                S1 = Tile<1, SUB>::STRIDE;
+  // Input tiles are overwritten in place by their gradients; sg holds gy.
+  __shared__ float sk[SPW * SD];
+  __shared__ float sq[SPW * SD];
+  __shared__ float sv[SPW * SM];
+  __shared__ float sg[SPW * SM];
+  __shared__ float srad[SPW * SJ];
+  __shared__ float sang[SPW * SJ];
+  __shared__ float sp[SPW * SJ];
+  __shared__ float sr[SPW * S1];
+
+  const int lane = threadIdx.x;
+  const int g = lane % G;
+  const int s = lane / G;
+  const int64_t n0 = static_cast<int64_t>(blockIdx.x) * SPW;
+  const int64_t n = n0 + s;
+  const bool active = n < a.n;
+  const int64_t na = active ? n : 0;
+  const int64_t T = a.t;
+  const bool writer = L::row_writer(g);
+
+  float gM[D][CPL];
+  float Gs[RPL][D];
+#pragma unroll
+  for (int i = 0; i < D; ++i)
+#pragma unroll
+    for (int c = 0; c < CPL; ++c) gM[i][c] = (active && a.gmf) ? a.gmf[na * D * M + i * M + g * CPL + c] : 0.f;
+#pragma unroll
+  for (int jj = 0; jj < RPL; ++jj) {
+    const int rr = L::row(g, jj);
+#pragma unroll
+    for (int j = 0; j < D; ++j)
+      Gs[jj][j] = (active && a.gcf) ? 0.5f * (a.gcf[na * D * D + rr * D + j] + a.gcf[na * D * D + j * D + rr]) : 0.f;
+  }
+  float gc0r[RPL][D];
+#pragma unroll
+  for (int jj = 0; jj < RPL; ++jj)
+#pragma unroll
+    for (int j = 0; j < D; ++j) gc0r[jj][j] = 0.f;
+
+  RotTile st{sk + s * SD, sv + s * SM, srad + s * SJ, sang + s * SJ, sp + s * SJ, sr + s * S1};
+  float* gks = sk + s * SD;
+  float* gqs = sq + s * SD;
+  float* gvs = sv + s * SM;
+  const float* gys = sg + s * SM;
+  float* grads = srad + s * SJ;
+  float* gangs = sang + s * SJ;
+  float* gps = sp + s * SJ;
+  float* grs = sr + s * S1;
+  const int64_t bm_seq = (a.nb + 1) * D * M, bc_seq = (a.nb + 1) * D * D;
+
+  auto stage_piece = [&](int64_t ts, int len, bool with_grad) {
+    const bool vec = a.vec && (ts % 4 == 0);
+    stage_in<D, SUB, SPW>(sk, a.k, n0, a.n, T, ts, len, vec, lane);
+    stage_in<M, SUB, SPW>(sv, a.v, n0, a.n, T, ts, len, vec, lane);
+    stage_in<J, SUB, SPW>(srad, a.rad, n0, a.n, T, ts, len, vec, lane);
+    stage_in<J, SUB, SPW>(sang, a.ang, n0, a.n, T, ts, len, vec, lane);
+    stage_in<J, SUB, SPW>(sp, a.p, n0, a.n, T, ts, len, vec, lane);
+    stage_in<1, SUB, SPW>(sr, a.r, n0, a.n, T, ts, len, vec, lane);
+    if (with_grad) {
+      stage_in<D, SUB, SPW>(sq, a.q, n0, a.n, T, ts, len, vec, lane);
+      stage_in<M, SUB, SPW>(sg, a.gy, n0, a.n, T, ts, len, vec, lane);
+    }
+  };
+
+  for (int64_t c = a.nb - 1; c >= 0; --c) {
+    const int64_t tc0 = c * a.chunk;
+    const int64_t lc = (T - tc0) < a.chunk ? (T - tc0) : a.chunk;
+    const int nsub = static_cast<int>((lc + SUB - 1) / SUB);
+    for (int sc = nsub - 1; sc >= 0; --sc) {
+      Belief<D, M, G> b;
+      load_belief<D, M, G>(b, a.bm + na * bm_seq + c * D * M, a.bc + na * bc_seq + c * D * D, g, active);
+      // Advance from the checkpoint to the piece.
+      for (int j = 0; j < sc; ++j) {
+        stage_piece(tc0 + static_cast<int64_t>(j) * SUB, SUB, false);
+        __syncthreads();
+#pragma unroll 1
+        for (int tt = 0; tt < SUB; ++tt) {
+          TokRot<D, M, G> in;
+          read_rot<D, M, G>(in, st, tt, g, true);
+          StepOut<D, M, G> o;
+          float Pb[RPL][D];
+          step_rot<D, M, G>(b, in, a.floor, g, lane, o, Pb);
+        }
+        __syncthreads();
+      }
+      const int64_t ts = tc0 + static_cast<int64_t>(sc) * SUB;
+      const int len = static_cast<int>((lc - sc * SUB) < SUB ? (lc - sc * SUB) : SUB);
+      stage_piece(ts, len, true);
+      __syncthreads();
+      RotHist<D, M, G> hist[SUB];
+#pragma unroll
+      for (int tt = 0; tt < SUB; ++tt) {
+        if (tt < len) {
+          TokRot<D, M, G> in;
+          read_rot<D, M, G>(in, st, tt, g, true);
+#pragma unroll
+          for (int jj = 0; jj < RPL; ++jj)
+#pragma unroll
+            for (int j = 0; j < D; ++j) hist[tt].Pp[jj][j] = b.P[jj][j];
+#pragma unroll
+          for (int i = 0; i < D; ++i)
+#pragma unroll
+            for (int cc = 0; cc < CPL; ++cc) hist[tt].Mp[i][cc] = b.Mv[i][cc];
+          StepOut<D, M, G> o;
+          float Pb[RPL][D];
+          step_rot<D, M, G>(b, in, a.floor, g, lane, o, Pb);
+#pragma unroll
+          for (int j = 0; j < D; ++j) hist[tt].u[j] = o.u[j];
+#pragma unroll
+          for (int jj = 0; jj < RPL; ++jj) hist[tt].u_own[jj] = o.u_own[jj];
+          hist[tt].s = o.s;
+#pragma unroll
+          for (int cc = 0; cc < CPL; ++cc) hist[tt].e[cc] = o.e[cc];
+        }
+      }
+#pragma unroll
+      for (int tt = SUB - 1; tt >= 0; --tt) {
+        if (tt < len) {
+          TokRot<D, M, G> in;
+          read_rot<D, M, G>(in, st, tt, g, false);
+          float q[D], gy[CPL];
+#pragma unroll
+          for (int j = 0; j < D; ++j) q[j] = gqs[tt * D + j];
+#pragma unroll
+          for (int cc = 0; cc < CPL; ++cc) gy[cc] = gys[tt * M + g * CPL + cc];
+          RotOut<D, M, G> o;
+          reverse_rot<D, M, G>(in, hist[tt], q, gy, gM, Gs, a.floor, g, lane, ts + tt == 0, gc0r, o);
+          // Every lane has read its token inputs (the reads above and the
+          // pair values inside) before any gradient overwrites them.
+          __builtin_amdgcn_wave_barrier();
+          if (writer) {
+#pragma unroll
+            for (int jj = 0; jj < RPL; ++jj) {
+              const int rr = L::row(g, jj);
+              gks[tt * D + rr] = o.gk_own[jj];
+              gqs[tt * D + rr] = o.gq_own[jj];
+            }
+          }
+#pragma unroll
+          for (int cc = 0; cc < CPL; ++cc) gvs[tt * M + g * CPL + cc] = o.gv[cc];
+          if (g == 0) {
+#pragma unroll
+            for (int m = 0; m < J; ++m) {
+              grads[tt * J + m] = o.grad_rad[m];
+              gangs[tt * J + m] = o.grad_ang[m];
+              gps[tt * J + m] = o.gp[m];
+            }
+            grs[tt] = o.gr;
+          }
+        }
+      }
+      __syncthreads();
+      const bool vec = a.vec && (ts % 4 == 0);
+      stage_out<D, SUB, SPW>(sk, a.gk, n0, a.n, T, ts, len, vec, lane);
+      stage_out<D, SUB, SPW>(sq, a.gq, n0, a.n, T, ts, len, vec, lane);
+      stage_out<M, SUB, SPW>(sv, a.gv, n0, a.n, T, ts, len, vec, lane);
+      stage_out<J, SUB, SPW>(srad, a.grad, n0, a.n, T, ts, len, vec, lane);
+      stage_out<J, SUB, SPW>(sang, a.gang, n0, a.n, T, ts, len, vec, lane);
+      stage_out<J, SUB, SPW>(sp, a.gp, n0, a.n, T, ts, len, vec, lane);
+      stage_out<1, SUB, SPW>(sr, a.gr, n0, a.n, T, ts, len, vec, lane);
+      __syncthreads();
+    }
+  }
+
+  if (active) {
+    if (a.gm0) {
+#pragma unroll
+      for (int i = 0; i < D; ++i)
+#pragma unroll
+        for (int cc = 0; cc < CPL; ++cc) a.gm0[na * D * M + i * M + g * CPL + cc] = gM[i][cc];
+    }
+    if (a.gc0 && writer) {
+#pragma unroll
+      for (int jj = 0; jj < RPL; ++jj) {
+        const int rr = L::row(g, jj);
+#pragma unroll
+        for (int j = 0; j < D; ++j) {
+          const float raw = a.gcf ? a.gcf[na * D * D + rr * D + j] : 0.f;
+          a.gc0[na * D * D + rr * D + j] = (T > 0) ? gc0r[jj][j] : raw;
+        }
+      }
+    }
+  }
+}
+
+template <int D>
+struct RotTuning;
+template <> struct RotTuning<2> { static constexpr int G = 4, TT = 16, SUB = 8; };
+template <> struct RotTuning<4> { static constexpr int G = 4, TT = 16, SUB = 8; };
+template <> struct RotTuning<8> { static constexpr int G = 8, TT = 16, SUB = 4; };
+
+template <int D>
+hipError_t fwd(const RotArgs& a, hipStream_t stream) {
+  using Tn = RotTuning<D>;
+  constexpr int SPW = kWave / Tn::G;
+  const int64_t blocks = (a.n + SPW - 1) / SPW;
+  hipLaunchKernelGGL((forward_kernel<D, 8, Tn::G, Tn::TT>), dim3(static_cast<unsigned>(blocks)), dim3(kWave), 0,
+                     stream, a);
+  return hipGetLastError();
+}
+template <int D>
+hipError_t bwd(const RotArgs& a, hipStream_t stream) {
+  using Tn = RotTuning<D>;
+  constexpr int SPW = kWave / Tn::G;
+  const int64_t blocks = (a.n + SPW - 1) / SPW;
+  hipLaunchKernelGGL((backward_kernel<D, 8, Tn::G, Tn::SUB>), dim3(static_cast<unsigned>(blocks)), dim3(kWave), 0,
+                     stream, a);
+  return hipGetLastError();
+}
+
+}  // namespace
+}  // namespace rot
+
+int rotation_checkpoint(int key_dim) {
+  switch (key_dim) {
+    case 2: return rot::RotTuning<2>::SUB;
+    case 4: return rot::RotTuning<4>::SUB;
+    case 8: return rot::RotTuning<8>::SUB;
+    default: return 0;
+  }
+}
+
+hipError_t launch_rotation_forward(int key_dim, const RotArgs& a, hipStream_t stream) {
+  if (a.n == 0) return hipSuccess;
+  switch (key_dim) {
+    case 2: return rot::fwd<2>(a, stream);
+    case 4: return rot::fwd<4>(a, stream);
+    case 8: return rot::fwd<8>(a, stream);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+hipError_t launch_rotation_backward(int key_dim, const RotArgs& a, hipStream_t stream) {
+  if (a.n == 0) return hipSuccess;
+  switch (key_dim) {
+    case 2: return rot::bwd<2>(a, stream);
+    case 4: return rot::bwd<4>(a, stream);
+    case 8: return rot::bwd<8>(a, stream);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+}  // namespace bssm

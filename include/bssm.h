@@ -315,6 +315,46 @@ int bssm_mixer_backward(const void* q_proj, int64_t ldq, const void* k_proj, int
                         float denominator_floor, int grad_f32, void* stream);
 
 /* ------------------------------------------------------------------------
+ * Rotation dynamics: block-diagonal damped 2-D rotations.  Replaces the
+ * reference's rotation core _core_loop_rotation (bayes_ssm/bayesian_layer.py
+ * :254-323, run there through torch.compile, :326-340).  Per token, pair
+ * j = state rows (2j, 2j+1) turns by [[c, -s], [s, c]], c = rho cos(angle),
+ * s = rho sin(angle), rho = min(max(radius, FLT_MIN), 1); the pair's process
+ * variance is added to covariance entry (2j, 2j); then the update of
+ * bssm_forward_chunked.  keys/queries [N,T,D], values/out [N,T,M],
+ * radii/angles/process [N,T,D/2], observation [N,T]; belief and checkpoint
+ * tensors as bssm_forward_chunked.  Supports (D, M) in {(2,8), (4,8), (8,8)}.
+ * No counterpart in the reference's CUDA extension. */
+int bssm_forward_chunked_rotation(int key_dim, int value_dim,
+                                  const float* keys, const float* values, const float* queries,
+                                  const float* radii, const float* angles, const float* process,
+                                  const float* observation, const float* mean0, const float* cov0,
+                                  float* out, float* mean_final, float* cov_final,
+                                  float* bmean, float* bcov,
+                                  int64_t n, int64_t t, int64_t chunk, float denominator_floor,
+                                  void* stream);
+
+/* Reverse: all seven input gradients (g_radii is zero where the radius clamp
+ * is active) and, when non-NULL, gm0 and the asymmetric gc0 (the convention
+ * of bssm_backward_chunked).  Replays each chunk of `chunk` tokens from its
+ * checkpoint; bssm_rotation_checkpoint(D) is the interval replayed in one
+ * piece. */
+int bssm_backward_chunked_rotation(int key_dim, int value_dim,
+                                   const float* keys, const float* values, const float* queries,
+                                   const float* radii, const float* angles, const float* process,
+                                   const float* observation, const float* mean0, const float* cov0,
+                                   const float* bmean, const float* bcov,
+                                   const float* gy, const float* gmf, const float* gcf,
+                                   float* gk, float* gv, float* gq, float* g_radii, float* g_angles,
+                                   float* g_process, float* g_observation, float* gm0, float* gc0,
+                                   int64_t n, int64_t t, int64_t chunk, float denominator_floor,
+                                   void* stream);
+
+/* Checkpoint interval of the rotation backward for key_dim (0 if unsupported).
+ * No reference counterpart. */
+int bssm_rotation_checkpoint(int key_dim);
+
+/* ------------------------------------------------------------------------
  * Length-four causal depthwise filter.  Replaces CausalDepthwise4.forward
  * (example/train_6layer.py:160-191) as the mixer applies it to each
  * projected stream (:474-480): per channel c and token t,

@@ -10,6 +10,7 @@ float32, autograd-friendly), written from the equations:
 * ``dense_step`` / ``run_dense``     — bayes_ssm/bayesian_layer.py:153-204 (_step, _core_loop)
 * ``run_diagonal``                   — bayesian_layer.py:207-251 (_core_loop_diagonal_transition)
 * ``run_fixed``                      — bayesian_layer.py:343-397 (_core_loop_fixed_diagonal)
+* ``run_rotation``                   — bayesian_layer.py:254-323 (_core_loop_rotation, damped 2-D rotations)
 * ``run_chunked``                    — bayesian_layer.py:670-732 (_run_chunked, paper §C.2
                                        transported-history chunk algorithm; the reference
                                        CPU path of ``bayesian_layer(optimized=False)``)
@@ -38,6 +39,10 @@ reference's ops), by unit RMS of the normalized head, and by gradcheck.  The
 causal filter is pinned against torch's conv1d on the left-padded input (the
 reference's nn.Conv1d path, :478-480), by its impulse response and causality,
 and by gradcheck.
+The rotation core is pinned against run_dense with an independently built
+block-rotation transition (the reference's own check,
+tests/test_bayesian_layer_diagonal.py:12-51), by the angle = 0 reduction to
+the diagonal core and by the radius clamp.
 No function here is left "parity unpinned".
 """
 from __future__ import annotations
@@ -127,6 +132,49 @@ def run_fixed(k, v, q, mean0, cov0, floor):
         bu = beta[..., None] * u
         mean = mean_pred + bu[..., :, None] * e[..., None, :]
         cov = _sym(rho2 * cov + FIXED_PROCESS * eye - bu[..., :, None] * u[..., None, :])
+        ys.append((mean * q[..., t, :, None]).sum(-2))
+    return torch.stack(ys, dim=-2), mean, cov
+
+
+def rotation_coefficients(radius, angle, tiny: float = 1.1754943508222875e-38):
+    """c, s of the damped rotations: rho = min(max(radius, tiny), 1) (bayesian_layer.py:279-281)."""
+    rho = radius.clamp_min(tiny)
+    rho = torch.where(rho <= 1.0, rho, torch.ones_like(rho))
+    return rho * torch.cos(angle), rho * torch.sin(angle)
+
+
+def run_rotation(k, v, q, radius, angle, p, r, mean0, cov0, floor):
+    """Block-diagonal damped 2-D rotations (bayesian_layer.py:254-323), pair by pair.
+
+    Pair j = rows (2j, 2j+1): mean and covariance rows, then covariance
+    columns, are turned by [[c, -s], [s, c]]; the pair's process variance p[.., j]
+    is added to entry (2j, 2j) only; then the Kalman update of run_dense with
+    the covariance symmetrised.  radius, angle, p: [..., T, D/2]; tiny is the
+    float32 one, as the reference's float32 covariance uses.
+    """
+    D = k.shape[-1]
+    J = D // 2
+    mean, cov = mean0, cov0
+
+    def turn(x, c, s):  # rows of x [..., D, W] by the pair rotations
+        pairs = x.reshape(*x.shape[:-2], J, 2, x.shape[-1])
+        a, b = pairs[..., 0, :], pairs[..., 1, :]
+        c, s = c[..., None], s[..., None]
+        return torch.stack((c * a - s * b, s * a + c * b), dim=-2).reshape(x.shape)
+
+    ys = []
+    for t in range(k.shape[-2]):
+        c, s = rotation_coefficients(radius[..., t, :], angle[..., t, :])
+        mean_pred = turn(mean, c, s)
+        cov_pred = turn(turn(cov, c, s).transpose(-1, -2), c, s).transpose(-1, -2)
+        noise = torch.stack((p[..., t, :], torch.zeros_like(p[..., t, :])), dim=-1).reshape(*p.shape[:-2], D)
+        cov_pred = cov_pred + torch.diag_embed(noise)
+        kt = k[..., t, :]
+        u = (cov_pred @ kt.unsqueeze(-1)).squeeze(-1)
+        beta = 1.0 / (r[..., t] + (kt * u).sum(-1)).clamp_min(floor)
+        e = v[..., t, :] - (mean_pred * kt[..., :, None]).sum(-2)
+        mean = mean_pred + beta[..., None, None] * u[..., :, None] * e[..., None, :]
+        cov = _sym(cov_pred - beta[..., None, None] * u[..., :, None] * u[..., None, :])
         ys.append((mean * q[..., t, :, None]).sum(-2))
     return torch.stack(ys, dim=-2), mean, cov
 

@@ -396,3 +396,67 @@ def test_product_conv_formula_matches_oracle():
     torch.testing.assert_close(m(x), O.causal_depthwise4(x, m.weight.detach()), rtol=1e-12, atol=1e-12)
     with pytest.raises(ValueError):
         CausalDepthwise4(6, 5)
+
+
+# ------------------------------------------------------------ rotation core
+def _rot_case(n, t, d, seed):
+    g = torch.Generator().manual_seed(seed)
+    k = torch.randn(n, t, d, generator=g)
+    v = torch.randn(n, t, 3, generator=g)
+    q = torch.randn(n, t, d, generator=g)
+    rad = 0.5 + 0.6 * torch.rand(n, t, d // 2, generator=g)  # some above 1: clamped
+    ang = 3.0 * torch.randn(n, t, d // 2, generator=g)
+    p = 0.05 + 0.2 * torch.rand(n, t, d // 2, generator=g)
+    r = 0.2 + torch.rand(n, t, generator=g)
+    m0 = 0.3 * torch.randn(n, d, 3, generator=g)
+    a = torch.randn(n, d, d, generator=g)
+    c0 = a @ a.transpose(-1, -2) / d + 0.5 * torch.eye(d)
+    return k, v, q, rad, ang, p, r, m0, c0
+
+
+def test_rotation_matches_dense_block_rotation():
+    """The pairwise rotation core equals run_dense with block-diagonal R_t and Q_t = diag(p on even entries)."""
+    k, v, q, rad, ang, p, r, m0, c0 = _rot_case(3, 7, 6, seed=20)
+    n, t, d = k.shape
+    rho = torch.clamp(rad, max=1.0)
+    A = torch.zeros(n, t, d, d)
+    Q = torch.zeros(n, t, d, d)
+    for j in range(d // 2):
+        cj, sj = rho[..., j] * torch.cos(ang[..., j]), rho[..., j] * torch.sin(ang[..., j])
+        A[..., 2 * j, 2 * j], A[..., 2 * j, 2 * j + 1] = cj, -sj
+        A[..., 2 * j + 1, 2 * j], A[..., 2 * j + 1, 2 * j + 1] = sj, cj
+        Q[..., 2 * j, 2 * j] = p[..., j]
+    yd, md, cd = O.run_dense(k, v, q, A, Q, r, m0, c0, 1e-6)
+    yr, mr, cr = O.run_rotation(k, v, q, rad, ang, p, r, m0, c0, 1e-6)
+    for a_, b_ in ((yr, yd), (mr, md), (cr, cd)):
+        torch.testing.assert_close(a_, b_, rtol=1e-12, atol=1e-12)
+
+
+def test_rotation_zero_angle_is_diagonal_with_even_noise():
+    """Angle 0: the transition is diag(rho per pair); noise only on even entries (checked via run_dense)."""
+    k, v, q, rad, _, p, r, m0, c0 = _rot_case(2, 5, 4, seed=21)
+    rad = rad.clamp(max=0.99)
+    ang = torch.zeros_like(rad)
+    d_full = rad.repeat_interleave(2, dim=-1)
+    yr, mr, cr = O.run_rotation(k, v, q, rad, ang, p, r, m0, c0, 1e-6)
+    Q = torch.diag_embed(torch.stack((p, torch.zeros_like(p)), dim=-1).reshape(*p.shape[:-1], 4))
+    yd, md, cd = O.run_dense(k, v, q, torch.diag_embed(d_full), Q, r, m0, c0, 1e-6)
+    torch.testing.assert_close(yr, yd, rtol=1e-12, atol=1e-12)
+    # With the same noise on every entry it would differ: the even-only placement matters.
+    yw, _, _ = O.run_dense(k, v, q, torch.diag_embed(d_full), torch.diag_embed(p.repeat_interleave(2, dim=-1)), r,
+                           m0, c0, 1e-6)
+    assert (yw - yr).abs().max() > 1e-6
+
+
+def test_rotation_gradcheck_and_clamp():
+    k, v, q, rad, ang, p, r, m0, c0 = _rot_case(1, 3, 4, seed=22)
+    rad = torch.tensor([[[0.7, 1.3], [0.9, 0.5], [1.2, 0.8]]], dtype=torch.float64)  # two clamped entries
+    leaves = [x.clone().requires_grad_(True) for x in (k, v, q, rad, ang, p, r)]
+
+    def fn(*xs):
+        return O.run_rotation(*xs, m0, c0, 1e-6)
+
+    assert torch.autograd.gradcheck(fn, tuple(leaves), eps=1e-6, atol=1e-6)
+    y, mT, cT = fn(*leaves)
+    g = torch.autograd.grad(y.sum() + mT.sum(), leaves[3])[0]
+    assert g[0, 0, 1] == 0 and g[0, 2, 0] == 0  # radius > 1: clamped, no gradient
