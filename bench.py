@@ -214,6 +214,63 @@ def time_conv(b, t, c, steps, warmup, device, fused=True) -> dict:
     return out
 
 
+def time_rotation(b, t, h, d, steps, warmup, device, fused=True) -> dict:
+    """fwd+bwd of bayesian_layer with rotation dynamics (bayesian_layer.py:254-323) at one shape.
+
+    fused: the HIP rotation kernels.  Otherwise the reference's rotation core
+    run eagerly on the same GPU (the reference compiles it with Inductor,
+    which this build does not use).  Algorithmic bytes per (sequence, token):
+    forward k, q (D), v (8), radius, angle, process (D/2), observation in and
+    y out; backward the inputs and gy in, their gradients out.
+    """
+    import bayes_ssm
+
+    n, m = b * h, 8
+    g = torch.Generator(device=device).manual_seed(4)
+    k = (torch.randn(n, t, d, device=device, generator=g) / d ** 0.5).requires_grad_(True)
+    v = torch.randn(n, t, m, device=device, generator=g).requires_grad_(True)
+    q = torch.randn(n, t, d, device=device, generator=g).requires_grad_(True)
+    rad = torch.exp(-torch.nn.functional.softplus(torch.randn(n, t, d // 2, device=device, generator=g) - 2.0))
+    rad = rad.requires_grad_(True)
+    ang = torch.randn(n, t, d // 2, device=device, generator=g).requires_grad_(True)
+    p = (1e-4 + torch.nn.functional.softplus(torch.randn(n, t, d // 2, device=device, generator=g) - 3.0))
+    r = (1e-4 + torch.nn.functional.softplus(torch.randn(n, t, device=device, generator=g))).requires_grad_(True)
+    p = p.requires_grad_(True)
+    gy = torch.randn(n, t, m, device=device, generator=g)
+    leaves = (k, v, q, rad, ang, p, r)
+    previous = os.environ.get("BAYES_SSM_DISABLE_FUSED_CUDA")
+    if not fused:
+        os.environ["BAYES_SSM_DISABLE_FUSED_CUDA"] = "1"
+    try:
+        def step():
+            y, _, _ = bayes_ssm.bayesian_layer(k, v, q, rotation_radii=rad, rotation_angles=ang, process_variances=p,
+                                               observation_variances=r, chunk_length=64, optimized=True)
+            return torch.autograd.grad(y, leaves, gy)
+
+        for _ in range(warmup):
+            step()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(steps):
+            step()
+        e1.record()
+        torch.cuda.synchronize()
+    finally:
+        if previous is None:
+            os.environ.pop("BAYES_SSM_DISABLE_FUSED_CUDA", None)
+        else:
+            os.environ["BAYES_SSM_DISABLE_FUSED_CUDA"] = previous
+    ms = e0.elapsed_time(e1) / steps
+    per = (2 * d + m + 3 * (d // 2) + 1) * 4
+    fwd_b, bwd_b = per + m * 4, 2 * per + m * 4
+    out = {"B": b, "T": t, "H": h, "D": d, "M": m, "ms_per_step": ms, "tokens_per_s": b * t / (ms * 1e-3),
+           "path": "HIP rotation kernels" if fused else "reference rotation core, eager torch"}
+    if fused:
+        out["roofline_step_frac"] = (fwd_b + bwd_b) * n * t / (ms * 1e-3) / HBM_PEAK
+    return out
+
+
 def time_scan(b, t, d, m, iters, device) -> dict:
     """Forward of associative_static_bayesian_cuda (one HIP kernel): mean microseconds per call."""
     from bayes_ssm.replay_ssm import associative_static_bayesian_cuda
@@ -301,7 +358,7 @@ def main() -> int:
     ap.add_argument("--cpu-budget", type=float, default=20.0, help="seconds of CPU-baseline work (0 = skip)")
     ap.add_argument("--no-extras", action="store_true",
                     help="skip the secondary shapes (per-GPU DP shape, D1/D2/D8 variants, associative scan)")
-    ap.add_argument("--secondary", choices=("mixer", "mixer-readout", "conv4"),
+    ap.add_argument("--secondary", choices=("mixer", "mixer-readout", "conv4", "rotation"),
                     help="time only one secondary workload at the configured shape (the mixer's fused layer core, "
                          "with its readout epilogue, or the causal depthwise-4 filter on the q/k/v stream), for "
                          "profiling its kernels; prints its own JSON line")
@@ -324,6 +381,8 @@ def main() -> int:
     if args.secondary:
         if args.secondary == "conv4":
             row = time_conv(b, t, h * (2 * d + m), args.steps, args.warmup, device, fused=True)
+        elif args.secondary == "rotation":
+            row = time_rotation(b, t, h, d, args.steps, args.warmup, device, fused=True)
         else:
             row = time_mixer(b, t, h, args.steps, args.warmup, device, fused=True,
                              gated=args.secondary == "mixer-readout")
@@ -455,6 +514,8 @@ def main() -> int:
         qkv = h * (2 * d + m)  # channels of the mixer's fused q/k/v stream at this shape
         extras["conv4_config3_qkv"] = time_conv(b, t, qkv, 30, 10, device, fused=True)
         extras["conv4_config3_qkv_torch"] = time_conv(b, t, qkv, 10, 3, device, fused=False)
+        extras["rotation_config3_d4m8"] = time_rotation(b, t, h, 4, 10, 3, device, fused=True)
+        extras["rotation_config3_d4m8_eager"] = time_rotation(b // 32, t, h, 4, 2, 1, device, fused=False)
         extras["assoc_scan_config0"] = time_scan(1, 16, 4, 4, 50, device)
         extras["assoc_scan_config1"] = time_scan(4, 64, 16, 16, 50, device)
         result["extras"] = extras
