@@ -352,9 +352,9 @@ __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(1, 1))) v
   const Rsrc rcT = make_rsrc(a.cT + n0 * 16, SPW * 64u);
 
   const BelOff unit(s, g, 128u, 64u);
-  FwdCore<false> core(lane, a.floor, a.chunk, rbm, rbc, nbp, ckst);
+  FwdCore<false> core(lane, a.floor, a.chunk, nbp, ckst);
   load_bel(core.b, rm0, rc0, unit, 0, 0);
-  core.store_ckpt(0);
+  core.store_ckpt(0, rbm, rbc);
 
   struct Out {
     v4f y[8];
@@ -407,8 +407,8 @@ __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(1, 1))) v
     if constexpr (EPI) load_gate(i * LT);
     __builtin_amdgcn_sched_barrier(0);
     const int64_t t0 = i * LT;
-    core.run_sub(tile, t0, T);
-    if (t0 + TT < T) core.run_sub(tile + FwdTile::SIZE, t0 + TT, T);
+    core.run_sub(tile, t0, T, rbm, rbc);
+    if (t0 + TT < T) core.run_sub(tile + FwdTile::SIZE, t0 + TT, T, rbm, rbc);
   }
   {
     Out yo;
@@ -416,7 +416,7 @@ __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(1, 1))) v
     store_y(yo, (ntiles - 1) * LT);
   }
   store_bel(core.b, rmT, rcT, unit, 0, 0);
-  core.store_ckpt(static_cast<uint32_t>(a.nb));
+  core.store_ckpt(static_cast<uint32_t>(a.nb), rbm, rbc);
 }
 
 // Gradient outputs: contiguous [B, T, H * w] rows, bfloat16 or float32.

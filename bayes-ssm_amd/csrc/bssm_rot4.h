@@ -55,6 +55,14 @@ constexpr bool kNtLoad = (BSSM_R4_NT & 1) != 0;
 constexpr int kStoreNt = 2;  // gfx9 cache policy: nt
 constexpr int kNtStore = (BSSM_R4_NT & 2) ? kStoreNt : 0;
 constexpr bool kNtCkpt = (BSSM_R4_NT & 4) != 0;
+#ifndef BSSM_R4_SCHED
+#define BSSM_R4_SCHED 7
+#endif
+// Scheduling barriers between tokens: bit 0 forward tiles (every two
+// tokens), bit 1 backward replay, bit 2 backward reverse.
+constexpr bool kSchedFwd = (BSSM_R4_SCHED & 1) != 0;
+constexpr bool kSchedReplay = (BSSM_R4_SCHED & 2) != 0;
+constexpr bool kSchedReverse = (BSSM_R4_SCHED & 4) != 0;
 
 typedef float v2f __attribute__((ext_vector_type(2)));
 using Rsrc = __amdgpu_buffer_rsrc_t;
@@ -450,22 +458,27 @@ struct Map {
 
 // LDS float indices of one lane's reads inside a tile.  For sequence s and
 // token tt (a compile-time constant in the unrolled loops):
-//   W = 4: word w of the token   = w4[tt & 1] + 32 tt + w
-//   W = 8: own columns 2g, 2g+1  = w8[tt & 3] + 128 (tt >> 2)
+//   W = 4: word w of the token   = 4 (64 j + 8 (p ^ j) + a) - 32 p + 32 tt + w,
+//          j = s >> 3, a = s & 7, p = tt & 1
+//   W = 8: own columns 2g, 2g+1  = 4 (64 j + 8 (c ^ j) + 4 (g >> 1) + a) + 2 (g & 1) + 128 (tt >> 2),
+//          j = s >> 2, a = s & 3, c = tt & 3
 //   W = 1: the token             = 8 s + tt
 struct Idx {
-  int w4[2], w8[4], w1;
+  // Plain arithmetic on scalars: the token index is a run-time value in the
+  // partial-tile loops, and any member chosen by it (an array element, or a
+  // select between members, which the compiler turns into a computed address)
+  // would force the whole per-lane core object out of registers.
+  int w4a, d4, w8, j8, w1;
   __device__ __forceinline__ Idx(int s, int g) {
     const int j4 = s >> 3, a4 = s & 7;
-#pragma unroll
-    for (int par = 0; par < 2; ++par) w4[par] = 4 * (64 * j4 + 8 * (par ^ j4) + a4) - 32 * par;
-    const int j8 = s >> 2, a8 = s & 3, h = g >> 1;
-#pragma unroll
-    for (int w = 0; w < 4; ++w) w8[w] = 4 * (64 * j8 + 8 * (w ^ j8) + 4 * h + a8) + 2 * (g & 1);
+    w4a = 4 * (64 * j4 + 8 * j4 + a4);  // parity 0; parity 1 is 64 j4 words lower
+    d4 = -64 * j4;
+    j8 = s >> 2;
+    w8 = 4 * (64 * j8 + 4 * (g >> 1) + (s & 3)) + 2 * (g & 1);
     w1 = 8 * s;
   }
-  __device__ __forceinline__ int i4(int tt, int w) const { return w4[tt & 1] + 32 * tt + w; }
-  __device__ __forceinline__ int i8(int tt) const { return w8[tt & 3] + 128 * (tt >> 2); }
+  __device__ __forceinline__ int i4(int tt, int w) const { return w4a + (tt & 1) * d4 + 32 * tt + w; }
+  __device__ __forceinline__ int i8(int tt) const { return w8 + 32 * ((tt & 3) ^ j8) + 128 * (tt >> 2); }
   __device__ __forceinline__ int i1(int tt) const { return w1 + tt; }
 };
 
@@ -489,17 +502,16 @@ struct FwdCore {
   float floor;
   int64_t chunk, next_ckpt;
   uint32_t ckpt;
-  Rsrc rbm, rbc;
   RecOff ckoff;
   float* ckst;  // LDS staging of one checkpoint record (kRecFloats)
 
-  __device__ __forceinline__ FwdCore(int lane_, float floor_, int64_t chunk_, Rsrc rbm_, Rsrc rbc_, uint32_t nbp,
+  __device__ __forceinline__ FwdCore(int lane_, float floor_, int64_t chunk_, uint32_t nbp,
                                      float* ckst_)
       : ix(lane_ >> 2, lane_ & 3), lane(lane_), g(lane_ & 3), s(lane_ >> 2), floor(floor_), chunk(chunk_),
-        next_ckpt(chunk_), ckpt(1), rbm(rbm_), rbc(rbc_), ckoff(lane_, nbp * 128u, nbp * 64u), ckst(ckst_) {}
+        next_ckpt(chunk_), ckpt(1), ckoff(lane_, nbp * 128u, nbp * 64u), ckst(ckst_) {}
 
   // Checkpoint record c of the 16 sequences.
-  __device__ __forceinline__ void store_ckpt(uint32_t c) {
+  __device__ __forceinline__ void store_ckpt(uint32_t c, Rsrc rbm, Rsrc rbc) {
     bel_to_lds(b, ckst, s, g);
     const v4f x0 = *reinterpret_cast<const v4f*>(&ckst[lane * 4]);
     const v4f x1 = *reinterpret_cast<const v4f*>(&ckst[256 + lane * 4]);
@@ -560,16 +572,16 @@ struct FwdCore {
       }
       step(x[2 * j], y[2 * j]);
       step(x[2 * j + 1], y[2 * j + 1]);
-      __builtin_amdgcn_sched_barrier(0);
+      if constexpr (kSchedFwd) __builtin_amdgcn_sched_barrier(0);
     }
 #pragma unroll
     for (int tt = 0; tt < TT; ++tt) put_y(tl, tt, y[tt]);
   }
   // Sub-tile starting at token t0 (fewer than TT tokens at the end of T).
-  __device__ __forceinline__ void run_sub(float* tl, int64_t t0, int64_t T) {
+  __device__ __forceinline__ void run_sub(float* tl, int64_t t0, int64_t T, Rsrc rbm, Rsrc rbc) {
     const int len = static_cast<int>((T - t0) < TT ? (T - t0) : TT);
     if (t0 == next_ckpt) {
-      store_ckpt(ckpt);
+      store_ckpt(ckpt, rbm, rbc);
       ++ckpt;
       next_ckpt += chunk;
     }
@@ -579,7 +591,7 @@ struct FwdCore {
 #pragma unroll 1
       for (int tt = 0; tt < len; ++tt) {
         if (t0 + tt == next_ckpt) {
-          store_ckpt(ckpt);
+          store_ckpt(ckpt, rbm, rbc);
           ++ckpt;
           next_ckpt += chunk;
         }
@@ -831,13 +843,13 @@ struct BwdCore {
       if (tt + 1 < LEN) read_tok(tl, tt + 1, x[tt + 1]);
       else read_rev(tl, LEN - 1, rx[LEN - 1]);
       replay(b, x[tt], h[tt]);
-      __builtin_amdgcn_sched_barrier(0);
+      if constexpr (kSchedReplay) __builtin_amdgcn_sched_barrier(0);
     }
 #pragma unroll
     for (int tt = LEN - 1; tt >= 0; --tt) {
       if (tt > 0) read_rev(tl, tt - 1, rx[tt - 1]);
       reverse(tl, tt, rx[tt], h[tt]);
-      __builtin_amdgcn_sched_barrier(0);
+      if constexpr (kSchedReverse) __builtin_amdgcn_sched_barrier(0);
     }
   }
   // A chunk of `len` tokens (SUB, or 4 for the last one of T = 8n + 4).

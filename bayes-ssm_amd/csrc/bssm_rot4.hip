@@ -42,9 +42,9 @@ __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(1, 1))) v
   const int dst1 = ((lane & 3) >> 1) * FwdTile::SIZE + 4 * (2 * (lane >> 2) + (lane & 1));
 
   const BelOff unit(s, g, 128u, 64u);
-  FwdCore<FIXED> core(lane, a.floor, a.chunk, rbm, rbc, nbp, ckst);
+  FwdCore<FIXED> core(lane, a.floor, a.chunk, nbp, ckst);
   load_bel(core.b, rm0, rc0, unit, 0, 0);
-  core.store_ckpt(0);
+  core.store_ckpt(0, rbm, rbc);
 
   using Stage = std::conditional_t<H, FwdStageH, FwdStage>;
   auto load = [&](Stage& x, int64_t t0) __attribute__((always_inline)) {
@@ -157,8 +157,8 @@ __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(1, 1))) v
     if (i + 1 < ntiles) load(st, (i + 1) * LT);
     __builtin_amdgcn_sched_barrier(0);
     const int64_t t0 = i * LT;
-    core.run_sub(tile, t0, T);
-    if (t0 + TT < T) core.run_sub(tile + FwdTile::SIZE, t0 + TT, T);
+    core.run_sub(tile, t0, T, rbm, rbc);
+    if (t0 + TT < T) core.run_sub(tile + FwdTile::SIZE, t0 + TT, T, rbm, rbc);
   }
   {
     FwdOut yo;
@@ -166,7 +166,7 @@ __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(1, 1))) v
     store_y(yo, (ntiles - 1) * LT);
   }
   store_bel(core.b, rmT, rcT, unit, 0, 0);
-  core.store_ckpt(static_cast<uint32_t>(a.nb));
+  core.store_ckpt(static_cast<uint32_t>(a.nb), rbm, rbc);
 }
 
 template <bool FIXED, bool DYN>
