@@ -61,7 +61,7 @@ _SIGNATURES = {
     "bssm_preferred_checkpoint": [_I],
     "bssm_abi_version": [],
 }
-ABI_VERSION = 6
+ABI_VERSION = 7
 
 _lock = threading.Lock()
 _lib: Optional[ctypes.CDLL] = None

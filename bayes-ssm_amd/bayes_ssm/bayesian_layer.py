@@ -36,7 +36,7 @@ _FLOAT8_DTYPES = tuple(
     if getattr(torch, name, None) is not None
 )
 _LOW_PRECISION = (torch.float16, torch.bfloat16, *_FLOAT8_DTYPES)
-_FUSED_SHAPES = ((1, 8), (2, 8), (4, 8), (8, 8))
+_FUSED_SHAPES = ((1, 8), (2, 8), (4, 8), (8, 8), (64, 64))  # bayesian_layer.py:1047-1051
 
 
 # ------------------------------------------------------------------ helpers

@@ -46,7 +46,7 @@ from torch import Tensor
 
 from . import _hip
 
-_SUPPORTED = ((1, 8), (2, 8), (4, 8), (8, 8))
+_SUPPORTED = ((1, 8), (2, 8), (4, 8), (8, 8), (64, 64))
 _EXTENSIONS: dict[int, "_Extension"] = {}
 
 # Method names of the reference extension module for each key_dim.
@@ -61,7 +61,13 @@ _EXPORTS = {
         "backward_chunked_lean_fixed", "backward_chunked_fixed"),
     8: ("forward_chunked", "backward_chunked", "backward_chunked_lean", "forward_chunked_fixed",
         "backward_chunked_lean_fixed", "backward_chunked_fixed"),
+    # persistent_bayes_chunked.cu:436
+    64: ("forward_chunked", "backward_chunked", "backward_chunked_lean", "forward_chunked_fixed",
+         "backward_chunked_lean_fixed", "backward_chunked_fixed"),
 }
+
+# Value dimension of each key dimension's kernels.
+_VALUE_DIM = {1: 8, 2: 8, 4: 8, 8: 8, 64: 64}
 
 
 _ALL_METHODS = frozenset(name for names in _EXPORTS.values() for name in names)
@@ -79,8 +85,9 @@ def _check_inputs(key_dim: int, tensors: tuple[Tensor, ...], names: tuple[str, .
         _check(x.dtype == torch.float32, "fused Bayesian inputs must be float32")
         _check(x.is_contiguous(), "fused Bayesian inputs must be contiguous")
     k, v, q = tensors[:3]
+    m = _VALUE_DIM[key_dim]
     _check(k.dim() == 3 and v.dim() == 3 and q.dim() == 3 and k.size(2) == key_dim and q.size(2) == key_dim
-           and v.size(2) == 8, f"fused Bayesian kernel expects [N,T,{key_dim}] keys/queries and [N,T,8] values")
+           and v.size(2) == m, f"fused Bayesian kernel expects [N,T,{key_dim}] keys/queries and [N,T,{m}] values")
     n, t = k.shape[:2]
     _check(tuple(v.shape[:2]) == (n, t) and tuple(q.shape[:2]) == (n, t), "keys/values/queries batch-time mismatch")
     _check(all(x.device == k.device for x in tensors), "fused Bayesian inputs must share one device")
@@ -91,7 +98,7 @@ class _Extension:
 
     def __init__(self, key_dim: int) -> None:
         self.key_dim = key_dim
-        self.value_dim = 8
+        self.value_dim = _VALUE_DIM[key_dim]
         self._exports = frozenset(_EXPORTS[key_dim])
 
     def __getattribute__(self, name: str):
@@ -463,7 +470,7 @@ def fused_diagonal_bayesian(
     """Run the exact HIP core when its contract holds; ``None`` means "use the torch path".
 
     Contract (fused_cuda.py:346-371): CUDA device, 3-D fp32 tensors,
-    (D, M) in {(1,8), (2,8), (4,8), (8,8)}, decay [N,T,D], process and
+    (D, M) in {(1,8), (2,8), (4,8), (8,8), (64,64)}, decay [N,T,D], process and
     observation [N,T], initial mean [N,D,M] and covariance [N,D,D].
     Keys, values and queries may instead all be bfloat16 (see the module
     docstring).

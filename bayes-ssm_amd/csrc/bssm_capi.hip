@@ -33,7 +33,7 @@ int ok() {
   return BSSM_OK;
 }
 
-bool supported(int d, int m) { return m == 8 && (d == 1 || d == 2 || d == 4 || d == 8); }
+bool supported(int d, int m) { return (m == 8 && (d == 1 || d == 2 || d == 4 || d == 8)) || (d == 64 && m == 64); }
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 bool aligned8(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 7u) == 0; }
@@ -253,7 +253,7 @@ extern "C" {
 
 const char* bssm_last_error(void) { return g_error; }
 
-int bssm_abi_version(void) { return 6; }
+int bssm_abi_version(void) { return 7; }
 
 int bssm_supported(int key_dim, int value_dim) { return supported(key_dim, value_dim) ? 1 : 0; }
 

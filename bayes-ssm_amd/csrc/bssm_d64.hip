@@ -1,0 +1,618 @@
+// gfx950 kernels for D = M = 64 (bayes_ssm/persistent_bayes_chunked.cu is
+// the reference extension for this shape: chunk_forward_kernel :175-261,
+// recompute_chunk_kernel :263-301, backward_chunk_kernel :303-343).
+//
+// Work decomposition: one wave64 per sequence and lane l owns dimension l --
+// row l of the covariance P (P[j] = P_lj) and column l of the mean M
+// (M[i] = M_il).  Every per-token matrix-vector product is then a local
+// 64-term dot product against a vector that all lanes read from LDS, the
+// scalar s = r + k.u is a wave all-reduce, and nothing is synchronized across
+// waves.  The covariance is carried as P~ + diag(pd): P~ collects the
+// rank-one downdates and pd the process noise on the diagonal, so no lane
+// has to address its own diagonal register (a run-time index) every token.
+// Products that must commute (d_l d_j, u_l u_j, gu_l k_j + gu_j k_l) are
+// formed without contraction, which keeps P and the covariance adjoint
+// bitwise symmetric, as the reference's mirrored upper-triangle update does
+// (persistent_bayes_chunked.cu:221-241).
+//
+// Backward: the reverse of token t needs the belief before t.  Instead of the
+// reference's per-token history in HBM (mp/pp/uh/bh/eh, 32 KB per token and
+// sequence at D = 64), the kernel replays from the chunk's checkpoint up to
+// t on chip before reversing t (quadratic in the chunk length; the autograd
+// path checkpoints every kD64Checkpoint tokens, bssm_recurrence.h).  Row sums of mean-shaped
+// products (sum over value columns = over lanes) go through a swizzled
+// 64 x 64 LDS transpose.
+
+#include "bssm_recurrence.h"
+#include "bssm_step.h"
+
+// No implicit contraction in this file: every fused multiply-add is an
+// explicit fmaf, and every other product or sum is rounded on its own.  The
+// all-reduce of s = r + k.u must not fuse its first sum with the product
+// (each lane would round differently), and the commuted products that keep
+// the covariance symmetric must round identically in both lanes.
+#pragma clang fp contract(off)
+
+namespace bssm {
+namespace d64 {
+
+constexpr int D = 64;
+
+// Separately rounded products and sums (the file compiles without contraction).
+__device__ __forceinline__ float mul_rn(float a, float b) { return a * b; }
+__device__ __forceinline__ float add_rn(float a, float b) { return a + b; }
+
+// Wave all-reduce with the bitwise-identical total in every lane: each step
+// adds two commuted operands (quad xor 1, 2; half-row mirror; row mirror;
+// xor 16; xor 32).
+__device__ __forceinline__ float wave_sum(float x) {
+  x = add_rn(x, dpp<kXor1>(x));
+  x = add_rn(x, dpp<kXor2>(x));
+  x = add_rn(x, dpp<kHalfMirror>(x));
+  x = add_rn(x, dpp<0x140>(x));  // row_mirror: lane l <- 15 - l
+  x = add_rn(x, __shfl_xor(x, 16, kWave));
+  x = add_rn(x, __shfl_xor(x, 32, kWave));
+  return x;
+}
+
+// Hand-off of LDS data between the lanes of the wave (a workgroup is one
+// wave): the writes complete before any lane reads.
+__device__ __forceinline__ void lds_handoff() { __syncthreads(); }
+
+// Scheduling fence every 16 elements of a 64-long unrolled loop: bounds how
+// many broadcast LDS reads the scheduler hoists ahead (register pressure).
+__device__ __forceinline__ void quarter_fence(int j) {
+  if (j != 0 && (j & 15) == 0) __builtin_amdgcn_sched_barrier(0);
+}
+
+// Dot product of the lane's 64 registers with a vector in LDS (all lanes read
+// the same address: broadcast), four partial sums for instruction-level
+// parallelism.
+__device__ __forceinline__ float dot64(const float (&x)[D], const float* vec) {
+  float acc[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int j = 0; j < D; j += 4) {
+    quarter_fence(j);
+    const v4f w = *reinterpret_cast<const v4f*>(&vec[j]);
+#pragma unroll
+    for (int c = 0; c < 4; ++c) acc[c] = fmaf(x[j + c], w[c], acc[c]);
+  }
+  return (acc[0] + acc[1]) + (acc[2] + acc[3]);
+}
+
+// LDS rows of 64 floats padded to kRow: lane l's row starts at l * kRow, so
+// the 16 lanes of one 16-byte access pass hit 16 distinct bank groups, and
+// every chunk is an immediate offset from one base address per lane.
+constexpr int kRow = D + 4;
+
+// Column sum over lanes: lane l receives sum_r x^(r)[l] where x^(r) is lane
+// r's register vector.  Lane r writes its vector as row r of a padded tile;
+// lane l then reads element l of every row (64 consecutive words per row).
+struct Transpose {
+  // f(c) yields the lane's x[4c .. 4c+3].
+  template <class F>
+  __device__ __forceinline__ float sum(float* tile, int l, F&& f) const {
+    float* row = tile + l * kRow;
+#pragma unroll
+    for (int c = 0; c < 16; ++c) {
+      quarter_fence(4 * c);
+      *reinterpret_cast<v4f*>(&row[4 * c]) = f(c);
+    }
+    lds_handoff();
+    const float* col = tile + l;
+    float acc[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int r = 0; r < D; ++r) {
+      quarter_fence(r);
+      acc[r & 3] += col[r * kRow];
+    }
+    lds_handoff();  // every lane has read the tile before it is rewritten
+    return (acc[0] + acc[1]) + (acc[2] + acc[3]);
+  }
+};
+
+// Per-lane token inputs.
+struct Tok {
+  float k, d, v, q, gy, p, r;
+};
+
+// The stream pointers are the sequence's rows (wave-uniform); t * D + l fits
+// 32 bits (the C ABI bounds t * D by 2^25).
+template <bool FIXED>
+__device__ __forceinline__ Tok load_tok(const float* k, const float* v, const float* q, const float* d,
+                                        const float* p, const float* r, const float* gy, int t, int l) {
+  Tok x;
+  const int e = t * D + l;
+  x.k = k[e];
+  x.v = v[e];
+  x.q = q[e];
+  x.gy = gy ? gy[e] : 0.f;
+  if constexpr (FIXED) {
+    x.d = kFixedDecay;
+    x.p = kFixedProcess;
+    x.r = kFixedObservation;
+  } else {
+    x.d = d[e];
+    x.p = p[t];
+    x.r = r[t];
+  }
+  return x;
+}
+
+// Broadcast vectors of the current token.
+struct Bcast {
+  float* k;
+  float* d;
+  float* q;
+  float* wk;
+  float* u;
+  float* gu;
+};
+
+// Intermediates of one token: u_l = (P' k)_l, the unclamped innovation
+// variance s, beta = 1 / max(s, floor) and the lane's innovation e_l.
+struct Pred {
+  float u, s, beta, e;
+};
+
+// Predict step of token x on the belief (P~ + diag(pd), M).  On the
+// sequence's first token P holds the initial covariance row as given
+// (possibly asymmetric), which u uses, as the reference does.
+__device__ __forceinline__ Pred predict(const float (&P)[D], float pd, const float (&M)[D], const Tok& x, float floor,
+                                        const Bcast& b, int l) {
+  const float wk = x.d * x.k;
+  b.k[l] = x.k;
+  b.d[l] = x.d;
+  b.q[l] = x.q;
+  b.wk[l] = wk;
+  lds_handoff();
+  Pred o;
+  float az[4] = {0.f, 0.f, 0.f, 0.f}, ae[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int j = 0; j < D; j += 4) {
+    quarter_fence(j);
+    const v4f w = *reinterpret_cast<const v4f*>(&b.wk[j]);
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      az[c] = fmaf(P[j + c], w[c], az[c]);
+      ae[c] = fmaf(M[j + c], w[c], ae[c]);
+    }
+  }
+  const float z = fmaf(pd, wk, (az[0] + az[1]) + (az[2] + az[3]));
+  o.u = fmaf(x.d, z, x.p * x.k);
+  o.s = wave_sum(x.k * o.u) + x.r;
+  o.beta = 1.0f / fmaxf(o.s, floor);
+  o.e = x.v - ((ae[0] + ae[1]) + (ae[2] + ae[3]));
+  b.u[l] = o.u;
+  lds_handoff();
+  return o;
+}
+
+// Update step: M_il <- d_i M_il + u_i beta e_l,  P~_lj <- P~_lj d_l d_j -
+// beta u_l u_j,  pd <- pd d_l^2 + p.  On the sequence's first token the
+// covariance entries left of the diagonal are replaced by their mirrors
+// (the initial covariance's upper triangle, read from `c0col`), as the
+// reference writes the upper triangle and mirrors it.
+__device__ __forceinline__ void update(float (&P)[D], float& pd, float (&M)[D], const Tok& x, const Pred& o,
+                                       const Bcast& b, int l, const float* c0col) {
+  const float be = o.beta * o.e;
+  if (c0col) {
+#pragma unroll
+    for (int j = 0; j < D; ++j)
+      if (j < l) P[j] = c0col[j * D];
+    // The lane's diagonal entry is the as-given P0_ll either way.
+  }
+#pragma unroll
+  for (int j = 0; j < D; j += 4) {
+    quarter_fence(j);
+    const v4f dv = *reinterpret_cast<const v4f*>(&b.d[j]);
+    const v4f uv = *reinterpret_cast<const v4f*>(&b.u[j]);
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      M[j + c] = fmaf(uv[c], be, dv[c] * M[j + c]);
+      P[j + c] = fmaf(-o.beta, mul_rn(o.u, uv[c]), P[j + c] * mul_rn(x.d, dv[c]));
+    }
+  }
+  pd = fmaf(pd, mul_rn(x.d, x.d), x.p);
+}
+
+// P~ + diag(pd) as a plain row (diagonal folded in), for storing.
+__device__ __forceinline__ float with_diag(const float (&P)[D], float pd, int j, int l) {
+  return j == l ? P[j] + pd : P[j];
+}
+
+// ------------------------------------------------------------------ forward
+template <bool FIXED>
+__global__ __launch_bounds__(kWave) void forward_kernel(FwdArgs a) {
+  __shared__ float sk[D], sd[D], sq[D], swk[D], su[D];
+  const Bcast b{sk, sd, sq, swk, su, nullptr};
+  const int l = threadIdx.x;
+  const int64_t n = blockIdx.x;
+  const int64_t T = a.t, nbp = a.nb + 1;
+  const float* c0 = a.c0 + n * D * D;
+  const float* m0 = a.m0 + n * D * D;
+  float* bm = a.bm + n * nbp * D * D;
+  float* bc = a.bc + n * nbp * D * D;
+
+  float P[D], M[D];
+  float pd = 0.f;
+#pragma unroll
+  for (int j = 0; j < D; ++j) P[j] = c0[l * D + j];  // row l, as given
+#pragma unroll
+  for (int i = 0; i < D; ++i) M[i] = m0[i * D + l];
+  // Checkpoint 0 is the initial belief as given.
+#pragma unroll
+  for (int i = 0; i < D; ++i) bm[i * D + l] = M[i];
+#pragma unroll
+  for (int j = 0; j < D; ++j) bc[l * D + j] = P[j];
+
+  // Symmetric after the first update: store column-wise (coalesced).
+  auto store_belief = [&](float* mdst, float* cdst) __attribute__((always_inline)) {
+#pragma unroll
+    for (int i = 0; i < D; ++i) mdst[i * D + l] = M[i];
+#pragma unroll
+    for (int j = 0; j < D; ++j) cdst[j * D + l] = with_diag(P, pd, j, l);
+  };
+
+  const float* kp = a.k + n * T * D;
+  const float* vp = a.v + n * T * D;
+  const float* qp = a.q + n * T * D;
+  const float* dp = FIXED ? nullptr : a.d + n * T * D;
+  const float* pp = FIXED ? nullptr : a.p + n * T;
+  const float* rp = FIXED ? nullptr : a.r + n * T;
+  float* yp = a.y + n * T * D;
+
+  Tok nxt = T > 0 ? load_tok<FIXED>(kp, vp, qp, dp, pp, rp, nullptr, 0, l) : Tok{};
+  if (T > 0) {  // the first token mirrors the initial covariance's upper triangle
+    const Tok x = nxt;
+    if (T > 1) nxt = load_tok<FIXED>(kp, vp, qp, dp, pp, rp, nullptr, 1, l);
+    const Pred o = predict(P, pd, M, x, a.floor, b, l);
+    update(P, pd, M, x, o, b, l, c0 + l);
+    yp[l] = dot64(M, sq);
+  }
+  int64_t c = 1;
+  for (int64_t t = 1; t < T; ++t) {
+    if (t % a.chunk == 0) {
+      store_belief(bm + c * D * D, bc + c * D * D);
+      ++c;
+    }
+    const Tok x = nxt;
+    if (t + 1 < T) nxt = load_tok<FIXED>(kp, vp, qp, dp, pp, rp, nullptr, static_cast<int>(t + 1), l);
+    const Pred o = predict(P, pd, M, x, a.floor, b, l);
+    update(P, pd, M, x, o, b, l, nullptr);
+    yp[static_cast<int>(t) * D + l] = dot64(M, sq);
+  }
+  if (T > 0) {
+    store_belief(a.mT + n * D * D, a.cT + n * D * D);
+    store_belief(bm + a.nb * D * D, bc + a.nb * D * D);
+  } else {
+#pragma unroll
+    for (int i = 0; i < D; ++i) a.mT[n * D * D + i * D + l] = M[i];
+#pragma unroll
+    for (int j = 0; j < D; ++j) a.cT[n * D * D + l * D + j] = P[j];
+  }
+}
+
+// ----------------------------------------------------------------- backward
+// Reverse of one token (persistent_bayes_chunked.cu:303-343), lane l holding
+// the belief before the token (P~, pd, M), its intermediates o, the carried
+// adjoints S (row l of the symmetrized covariance adjoint, in LDS; Sd its
+// diagonal entry) and gM (column l of the mean adjoint, in LDS like S).  `c0col` (first token only)
+// points at column l of the initial covariance, whose upper triangle the
+// predicted covariance of the first token mirrors.
+struct RevOut {
+  float gk, gq, gv, gd, gp, gr;
+};
+
+// Row l of the covariance adjoint and column l of the mean adjoint live in
+// LDS (padded rows, see kRow): the replayed belief fills the register file.
+__device__ __forceinline__ v4f& s_chunk(float* row, int c) { return *reinterpret_cast<v4f*>(&row[4 * c]); }
+
+template <bool FIXED, bool DYN>
+__device__ __forceinline__ RevOut reverse(const float (&P)[D], float pd, const float (&M)[D], const Tok& x,
+                                          const Pred& o, float* srow, float& Sd, float* grow, float floor,
+                                          const Bcast& b, float* tile, const Transpose& tr, int l,
+                                          const float* c0col) {
+  RevOut out;
+  // dL/dM after the token includes q gy^T; ge = beta gM^T u.
+  float gmu = 0.f;
+  {
+    float acc[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int c = 0; c < 16; ++c) {
+      quarter_fence(4 * c);
+      const v4f qv = *reinterpret_cast<const v4f*>(&b.q[4 * c]);
+      const v4f uv = *reinterpret_cast<const v4f*>(&b.u[4 * c]);
+      v4f& gref = s_chunk(grow, c);
+      v4f g4 = gref;
+#pragma unroll
+      for (int h = 0; h < 4; ++h) {
+        g4[h] = fmaf(qv[h], x.gy, g4[h]);
+        acc[h] = fmaf(g4[h], uv[h], acc[h]);
+      }
+      gref = g4;
+    }
+    gmu = (acc[0] + acc[1]) + (acc[2] + acc[3]);
+  }
+  const float ge = o.beta * gmu;
+  out.gv = ge;
+  // dL/dq_i = sum_c M_new_ic gy_c with M_new = d M + beta u e^T.
+  const float be = o.beta * o.e;
+  out.gq = tr.sum(tile, l, [&](int c) __attribute__((always_inline)) {
+    const v4f dv = *reinterpret_cast<const v4f*>(&b.d[4 * c]);
+    const v4f uv = *reinterpret_cast<const v4f*>(&b.u[4 * c]);
+    v4f r;
+#pragma unroll
+    for (int h = 0; h < 4; ++h) r[h] = fmaf(uv[h], be, dv[h] * M[4 * c + h]) * x.gy;
+    return r;
+  });
+  // -sum_c (d M)_ic ge_c enters dL/dk_i.
+  const float gk_mean = tr.sum(tile, l, [&](int c) __attribute__((always_inline)) {
+    const v4f dv = *reinterpret_cast<const v4f*>(&b.d[4 * c]);
+    v4f r;
+#pragma unroll
+    for (int h = 0; h < 4; ++h) r[h] = (dv[h] * M[4 * c + h]) * ge;
+    return r;
+  });
+  // a_i = sum_c gM_ic e_c.
+  const float a_l = tr.sum(tile, l, [&](int c) __attribute__((always_inline)) {
+    return s_chunk(grow, c) * o.e;
+  });
+  // gM_prev = gM - k ge^T (its product with M_prev enters dL/dd); the
+  // adjoint carried to the previous token is gM_prev * d.
+  float gd_mean = 0.f;
+  if constexpr (DYN) {
+    gd_mean = tr.sum(tile, l, [&](int c) __attribute__((always_inline)) {
+      const v4f kv = *reinterpret_cast<const v4f*>(&b.k[4 * c]);
+      const v4f dv = *reinterpret_cast<const v4f*>(&b.d[4 * c]);
+      v4f& gref = s_chunk(grow, c);
+      v4f g4 = gref, r;
+#pragma unroll
+      for (int h = 0; h < 4; ++h) {
+        g4[h] = fmaf(-kv[h], ge, g4[h]);
+        r[h] = g4[h] * M[4 * c + h];
+        g4[h] *= dv[h];
+      }
+      gref = g4;
+      return r;
+    });
+  } else {
+#pragma unroll
+    for (int c = 0; c < 16; ++c) {
+      quarter_fence(4 * c);
+      const v4f kv = *reinterpret_cast<const v4f*>(&b.k[4 * c]);
+      const v4f dv = *reinterpret_cast<const v4f*>(&b.d[4 * c]);
+      v4f& gref = s_chunk(grow, c);
+      v4f g4 = gref;
+#pragma unroll
+      for (int h = 0; h < 4; ++h) g4[h] = fmaf(-kv[h], ge, g4[h]) * dv[h];
+      gref = g4;
+    }
+  }
+  // w = S u, z = u.(a - w) summed over the wave.
+  float w;
+  {
+    float acc[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int c = 0; c < 16; ++c) {
+      quarter_fence(4 * c);
+      const v4f sv = s_chunk(srow, c);
+      const v4f uv = *reinterpret_cast<const v4f*>(&b.u[4 * c]);
+#pragma unroll
+      for (int h = 0; h < 4; ++h) acc[h] = fmaf(sv[h], uv[h], acc[h]);
+    }
+    w = (acc[0] + acc[1]) + (acc[2] + acc[3]);
+  }
+  const float z = wave_sum(fmaf(o.e, gmu, -(o.u * w)));
+  const float gs = (o.s > floor) ? -z * o.beta * o.beta : 0.f;
+  const float gu = fmaf(o.beta, fmaf(-2.f, w, a_l), gs * x.k);
+  b.gu[l] = gu;
+  lds_handoff();
+  // dL/dk = -(dM) ge + gs u + P' gu, P' = (P~ + diag(pd)) d d^T + p I.
+  float pgu;
+  {
+    float acc[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int j = 0; j < D; j += 4) {
+      quarter_fence(j);
+      const v4f dv = *reinterpret_cast<const v4f*>(&b.d[j]);
+      const v4f gv = *reinterpret_cast<const v4f*>(&b.gu[j]);
+#pragma unroll
+      for (int c = 0; c < 4; ++c) acc[c] = fmaf(P[j + c] * mul_rn(x.d, dv[c]), gv[c], acc[c]);
+    }
+    pgu = (acc[0] + acc[1]) + (acc[2] + acc[3]);
+  }
+  if (c0col != nullptr) {
+    // First token: its predicted covariance mirrors P0's upper triangle, so
+    // the entries left of the diagonal are P0_jl rather than the row's P0_lj.
+    float corr = 0.f;
+#pragma unroll
+    for (int j = 0; j < D; ++j) {
+      const float dj = (j < l) ? (c0col[j * D] - P[j]) : 0.f;
+      corr = fmaf(dj * mul_rn(x.d, b.d[j]), b.gu[j], corr);
+    }
+    pgu += corr;
+  }
+  out.gk = -gk_mean + fmaf(gs, o.u, fmaf(fmaf(pd, mul_rn(x.d, x.d), x.p), gu, pgu));
+  // H = S + sym(gu k^T); dL/dd_l = 2 sum_j H_lj P_lj d_j + sum_c gM_prev_lc M_lc;
+  // dL/dp = trace H; the adjoint before the token is H d d^T.
+  float gd_cov = 0.f;
+  const float hd = add_rn(Sd, 0.5f * add_rn(mul_rn(gu, x.k), mul_rn(gu, x.k)));
+#pragma unroll
+  for (int j = 0; j < D; j += 4) {
+    quarter_fence(j);
+    const v4f dv = *reinterpret_cast<const v4f*>(&b.d[j]);
+    const v4f kv = *reinterpret_cast<const v4f*>(&b.k[j]);
+    const v4f gv = *reinterpret_cast<const v4f*>(&b.gu[j]);
+    v4f& sref = s_chunk(srow, j >> 2);
+    const v4f sv = sref;
+    v4f sn;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const float h = add_rn(sv[c], 0.5f * add_rn(mul_rn(gu, kv[c]), mul_rn(gv[c], x.k)));
+      if constexpr (DYN) gd_cov = fmaf(h * P[j + c], dv[c], gd_cov);
+      sn[c] = h * mul_rn(x.d, dv[c]);
+    }
+    sref = sn;
+  }
+  Sd = hd * mul_rn(x.d, x.d);
+  if constexpr (DYN) {
+    gd_cov = fmaf(hd * pd, x.d, gd_cov);
+    out.gd = fmaf(2.f, gd_cov, gd_mean);
+    out.gp = wave_sum(hd);
+    out.gr = gs;
+  } else {
+    out.gd = out.gp = out.gr = 0.f;
+  }
+  return out;
+}
+
+template <bool FIXED, bool DYN>
+__global__ __launch_bounds__(kWave) void backward_kernel(BwdArgs a) {
+  __shared__ float sk[D], sd[D], sq[D], swk[D], su[D], sgu[D];
+  __shared__ float tile[D * kRow];
+  __shared__ float sadj[D * kRow];  // covariance adjoint, row l at sadj + l * kRow
+  __shared__ float gadj[D * kRow];  // mean adjoint, column l at gadj + l * kRow
+  const Bcast b{sk, sd, sq, swk, su, sgu};
+  const int l = threadIdx.x;
+  const int64_t n = blockIdx.x;
+  const int64_t T = a.t, nbp = a.nb + 1, chunk = a.chunk;
+  const Transpose tr;
+  const float* bm = a.bm + n * nbp * D * D;
+  const float* bc = a.bc + n * nbp * D * D;
+  const float* kp = a.k + n * T * D;
+  const float* vp = a.v + n * T * D;
+  const float* qp = a.q + n * T * D;
+  const float* gyp = a.gy + n * T * D;
+  const float* dp = FIXED ? nullptr : a.d + n * T * D;
+  const float* pp = FIXED ? nullptr : a.p + n * T;
+  const float* rp = FIXED ? nullptr : a.r + n * T;
+  float* gkp = a.gk + n * T * D;
+  float* gqp = a.gq + n * T * D;
+  float* gvp = a.gv + n * T * D;
+  float* gdp = a.gd ? a.gd + n * T * D : nullptr;
+  float* gpp = a.gp ? a.gp + n * T : nullptr;
+  float* grp = a.gr ? a.gr + n * T : nullptr;
+
+  // Carried adjoints from the final-state gradients (null: zero).
+  float* srow = sadj + l * kRow;
+  float* grow = gadj + l * kRow;
+  float Sd = 0.f;
+  if (a.gmf) {
+    const float* gmf = a.gmf + n * D * D;
+#pragma unroll
+    for (int c = 0; c < 16; ++c) {
+      v4f gv;
+#pragma unroll
+      for (int h = 0; h < 4; ++h) gv[h] = gmf[(4 * c + h) * D + l];
+      s_chunk(grow, c) = gv;
+    }
+  } else {
+#pragma unroll
+    for (int c = 0; c < 16; ++c) s_chunk(grow, c) = v4f{0.f, 0.f, 0.f, 0.f};
+  }
+  if (a.gcf) {
+    const float* gcf = a.gcf + n * D * D;
+#pragma unroll
+    for (int c = 0; c < 16; ++c) {
+      v4f sv;
+#pragma unroll
+      for (int h = 0; h < 4; ++h) {
+        const int j = 4 * c + h;
+        sv[h] = 0.5f * (gcf[l * D + j] + gcf[j * D + l]);
+      }
+      s_chunk(srow, c) = sv;
+    }
+    Sd = 0.5f * (gcf[l * D + l] + gcf[l * D + l]);
+  } else {
+#pragma unroll
+    for (int c = 0; c < 16; ++c) s_chunk(srow, c) = v4f{0.f, 0.f, 0.f, 0.f};
+  }
+
+  for (int64_t c = a.nb - 1; c >= 0; --c) {
+    const int64_t t0 = c * chunk;
+    const int64_t len = (T - t0) < chunk ? (T - t0) : chunk;
+    for (int64_t tt = len - 1; tt >= 0; --tt) {
+      // Belief before token t0 + tt: the checkpoint advanced tt tokens.
+      float P[D], M[D];
+      float pd = 0.f;
+      const float* cm = bm + c * D * D;
+      const float* cc = bc + c * D * D;
+      // Row l (checkpoint 0 is the initial covariance as given, possibly
+      // asymmetric; later checkpoints are symmetric).
+#pragma unroll
+      for (int j = 0; j < D; j += 4) {
+        const v4f r4 = *reinterpret_cast<const v4f*>(&cc[l * D + j]);
+#pragma unroll
+        for (int h = 0; h < 4; ++h) P[j + h] = r4[h];
+      }
+#pragma unroll
+      for (int i = 0; i < D; ++i) M[i] = cm[i * D + l];
+      Tok nxt = load_tok<FIXED>(kp, vp, qp, dp, pp, rp, gyp, static_cast<int>(t0), l);
+      int64_t j = 0;
+      if (c == 0 && tt > 0) {  // the sequence's first token mirrors P0's upper triangle
+        const Tok x = nxt;
+        nxt = load_tok<FIXED>(kp, vp, qp, dp, pp, rp, gyp, 1, l);
+        const Pred o = predict(P, pd, M, x, a.floor, b, l);
+        update(P, pd, M, x, o, b, l, cc + l);
+        j = 1;
+      }
+      for (; j < tt; ++j) {
+        const Tok x = nxt;
+        nxt = load_tok<FIXED>(kp, vp, qp, dp, pp, rp, gyp, static_cast<int>(t0 + j + 1), l);
+        const Pred o = predict(P, pd, M, x, a.floor, b, l);
+        update(P, pd, M, x, o, b, l, nullptr);
+      }
+      const int64_t t = t0 + tt;
+      const Pred o = predict(P, pd, M, nxt, a.floor, b, l);
+      const RevOut g = reverse<FIXED, DYN>(P, pd, M, nxt, o, srow, Sd, grow, a.floor, b, tile, tr, l,
+                                           t == 0 ? a.c0 + n * D * D + l : nullptr);
+      const int e = static_cast<int>(t) * D + l;
+      gkp[e] = g.gk;
+      gqp[e] = g.gq;
+      gvp[e] = g.gv;
+      if (gdp) gdp[e] = g.gd;
+      if (l == 0) {
+        if (gpp) gpp[t] = g.gp;
+        if (grp) grp[t] = g.gr;
+      }
+    }
+  }
+  if (a.gm0) {
+#pragma unroll
+    for (int c = 0; c < 16; ++c) {
+      const v4f gv = s_chunk(grow, c);
+#pragma unroll
+      for (int h = 0; h < 4; ++h) a.gm0[n * D * D + (4 * c + h) * D + l] = gv[h];
+    }
+  }
+  if (a.gc0) {
+#pragma unroll
+    for (int c = 0; c < 16; ++c) {
+      const v4f sv = s_chunk(srow, c);
+#pragma unroll
+      for (int h = 0; h < 4; ++h) a.gc0[n * D * D + (4 * c + h) * D + l] = sv[h];
+    }
+  }
+}
+
+}  // namespace d64
+
+hipError_t launch_forward_d64(bool fixed, const FwdArgs& a, hipStream_t stream) {
+  if (a.n == 0) return hipSuccess;
+  const dim3 grid(static_cast<unsigned>(a.n)), block(kWave);
+  if (fixed) hipLaunchKernelGGL((d64::forward_kernel<true>), grid, block, 0, stream, a);
+  else hipLaunchKernelGGL((d64::forward_kernel<false>), grid, block, 0, stream, a);
+  return hipGetLastError();
+}
+
+hipError_t launch_backward_d64(bool fixed, bool dyn, const BwdArgs& a, hipStream_t stream) {
+  if (a.n == 0) return hipSuccess;
+  const dim3 grid(static_cast<unsigned>(a.n)), block(kWave);
+  if (fixed) hipLaunchKernelGGL((d64::backward_kernel<true, false>), grid, block, 0, stream, a);
+  else if (dyn) hipLaunchKernelGGL((d64::backward_kernel<false, true>), grid, block, 0, stream, a);
+  else hipLaunchKernelGGL((d64::backward_kernel<false, false>), grid, block, 0, stream, a);
+  return hipGetLastError();
+}
+
+}  // namespace bssm

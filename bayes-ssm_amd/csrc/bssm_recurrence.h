@@ -84,6 +84,14 @@ constexpr int kRot4Chunk = 8;
 hipError_t launch_forward_r4(bool fixed, const FwdArgs& a, hipStream_t stream);
 hipError_t launch_backward_r4(bool fixed, bool dyn, const BwdArgs& a, hipStream_t stream);
 
+// D = M = 64 kernels (bssm_d64.hip): one wave per sequence, lane = dimension.
+// The backward replays each checkpoint chunk on chip before reversing a token,
+// so its cost grows with the square of the chunk length; the autograd path
+// checkpoints every kD64Checkpoint tokens.
+constexpr int kD64Checkpoint = 8;
+hipError_t launch_forward_d64(bool fixed, const FwdArgs& a, hipStream_t stream);
+hipError_t launch_backward_d64(bool fixed, bool dyn, const BwdArgs& a, hipStream_t stream);
+
 // Producer-fused D = 4, M = 8 layer core of the Bayes mixer (bssm_mixer.hip).
 // Inputs are the bfloat16 projections in [B, T, *] layout, each with its own
 // row stride (elements): queries, keys and decay logits [.., H * 4], values

@@ -482,6 +482,7 @@ int preferred_checkpoint(int key_dim) {
     case 2: return Tuning<2>::SUB;
     case 4: return Tuning<4>::SUB;
     case 8: return Tuning<8>::SUB;
+    case 64: return kD64Checkpoint;
     default: return 0;
   }
 }
@@ -493,6 +494,7 @@ hipError_t launch_forward(int key_dim, bool fixed, const FwdArgs& a, hipStream_t
     case 2: return fixed ? launch_forward_d<2, true>(a, stream) : launch_forward_d<2, false>(a, stream);
     case 4: return fixed ? launch_forward_d<4, true>(a, stream) : launch_forward_d<4, false>(a, stream);
     case 8: return fixed ? launch_forward_d<8, true>(a, stream) : launch_forward_d<8, false>(a, stream);
+    case 64: return launch_forward_d64(fixed, a, stream);
     default: return hipErrorInvalidValue;
   }
 }
@@ -510,6 +512,7 @@ hipError_t launch_backward(int key_dim, bool fixed, bool dyn, const BwdArgs& a, 
     case 2: return launch_backward_dd<2>(fixed, dyn, a, stream);
     case 4: return launch_backward_dd<4>(fixed, dyn, a, stream);
     case 8: return launch_backward_dd<8>(fixed, dyn, a, stream);
+    case 64: return launch_backward_d64(fixed, dyn, a, stream);
     default: return hipErrorInvalidValue;
   }
 }

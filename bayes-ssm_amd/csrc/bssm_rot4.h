@@ -56,13 +56,17 @@ constexpr int kStoreNt = 2;  // gfx9 cache policy: nt
 constexpr int kNtStore = (BSSM_R4_NT & 2) ? kStoreNt : 0;
 constexpr bool kNtCkpt = (BSSM_R4_NT & 4) != 0;
 #ifndef BSSM_R4_SCHED
-#define BSSM_R4_SCHED 7
+#define BSSM_R4_SCHED 15
 #endif
 // Scheduling barriers between tokens: bit 0 forward tiles (every two
-// tokens), bit 1 backward replay, bit 2 backward reverse.
+// tokens), bit 1 backward replay, bit 2 backward reverse.  Bit 3 adds a
+// barrier right after each token's look-ahead LDS reads: without it the
+// scheduler sinks those reads to the end of the previous token's region, and
+// the token that consumes them waits out the whole LDS latency.
 constexpr bool kSchedFwd = (BSSM_R4_SCHED & 1) != 0;
 constexpr bool kSchedReplay = (BSSM_R4_SCHED & 2) != 0;
 constexpr bool kSchedReverse = (BSSM_R4_SCHED & 4) != 0;
+constexpr bool kFenceReads = (BSSM_R4_SCHED & 8) != 0;
 
 typedef float v2f __attribute__((ext_vector_type(2)));
 using Rsrc = __amdgpu_buffer_rsrc_t;
@@ -569,6 +573,7 @@ struct FwdCore {
       if (j + 1 < TT / 2) {
         read_in(tl, 2 * j + 2, x[2 * j + 2]);
         read_in(tl, 2 * j + 3, x[2 * j + 3]);
+        if constexpr (kFenceReads) __builtin_amdgcn_sched_barrier(0);
       }
       step(x[2 * j], y[2 * j]);
       step(x[2 * j + 1], y[2 * j + 1]);
@@ -842,12 +847,14 @@ struct BwdCore {
     for (int tt = 0; tt < LEN; ++tt) {
       if (tt + 1 < LEN) read_tok(tl, tt + 1, x[tt + 1]);
       else read_rev(tl, LEN - 1, rx[LEN - 1]);
+      if constexpr (kFenceReads) __builtin_amdgcn_sched_barrier(0);
       replay(b, x[tt], h[tt]);
       if constexpr (kSchedReplay) __builtin_amdgcn_sched_barrier(0);
     }
 #pragma unroll
     for (int tt = LEN - 1; tt >= 0; --tt) {
       if (tt > 0) read_rev(tl, tt - 1, rx[tt - 1]);
+      if constexpr (kFenceReads) __builtin_amdgcn_sched_barrier(0);
       reverse(tl, tt, rx[tt], h[tt]);
       if constexpr (kSchedReverse) __builtin_amdgcn_sched_barrier(0);
     }

@@ -19,7 +19,14 @@
  * bmean[:, c] / bcov[:, c] hold the belief before token c*chunk; index nb
  * holds the final belief.
  *
- * Supported (D, M): (1, 8), (2, 8), (4, 8), (8, 8).
+ * Supported (D, M): (1, 8), (2, 8), (4, 8), (8, 8), (64, 64).  D = M = 64
+ * replaces the pybind module of bayes_ssm/persistent_bayes_chunked.cu
+ * (exports at :436: forward_chunked, forward_chunked_fixed, backward_chunked,
+ * backward_chunked_lean, backward_chunked_fixed, backward_chunked_lean_fixed;
+ * kernels at :175-343).  Its covariance adjoint follows that file's
+ * convention: the u = P'k adjoint gu k^T enters symmetrized
+ * (persistent_bayes_chunked.cu:329-333), so the initial-covariance gradient
+ * is symmetric, where D <= 8 return the full asymmetric one.
  */
 #ifndef BSSM_H_
 #define BSSM_H_
@@ -40,7 +47,8 @@ enum {
 /* Message of the last failure on this host thread ("" if none). */
 const char* bssm_last_error(void);
 
-/* ABI revision of this library (bumped on any signature change). */
+/* ABI revision of this library (bumped on any signature change or change of
+ * the supported (D, M) set). */
 int bssm_abi_version(void);
 
 /* 1 if (key_dim, value_dim) has a kernel, else 0. */

@@ -42,10 +42,10 @@ def test_abi_version_and_support(lib):
     from bayes_ssm import _hip
 
     assert lib.bssm_abi_version() == _hip.ABI_VERSION
-    for d in (1, 2, 4, 8):
-        assert lib.bssm_supported(d, 8) == 1
+    for d, m in ((1, 8), (2, 8), (4, 8), (8, 8), (64, 64)):
+        assert lib.bssm_supported(d, m) == 1
         assert lib.bssm_preferred_checkpoint(d) > 0
-    for d, m in ((3, 8), (4, 4), (64, 64), (16, 8)):
+    for d, m in ((3, 8), (4, 4), (64, 8), (8, 64), (16, 8)):
         assert lib.bssm_supported(d, m) == 0
     assert lib.bssm_preferred_checkpoint(3) == 0
 
@@ -96,12 +96,17 @@ def test_extension_method_sets_match_reference():
         assert hasattr(ext1, name) and not hasattr(ext4, name)
     for name in ("backward_chunked_noinitial", "backward_chunked_noinitial_fixed"):
         assert hasattr(ext2, name) and not hasattr(ext4, name) and not hasattr(ext1, name)
-    for ext in (ext1, ext2, ext4, fused_cuda._load_extension(8)):
+    ext64 = fused_cuda._load_extension(64)
+    for ext in (ext1, ext2, ext4, fused_cuda._load_extension(8), ext64):
         for name in ("forward_chunked", "forward_chunked_fixed", "backward_chunked", "backward_chunked_lean",
                      "backward_chunked_fixed", "backward_chunked_lean_fixed"):
             assert hasattr(ext, name)
+    # persistent_bayes_chunked.cu:436 exports no saved-history or no-initial variants.
+    for name in ("forward_chunked_saved", "backward_chunked_saved", "backward_chunked_noinitial"):
+        assert not hasattr(ext64, name)
+    assert ext64.value_dim == 64
     assert fused_cuda._load_extension(3) is None
-    assert fused_cuda._load_extension(64) is None
+    assert fused_cuda._load_extension(16) is None
 
 
 def test_disable_env(monkeypatch):
