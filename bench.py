@@ -271,6 +271,56 @@ def time_rotation(b, t, h, d, steps, warmup, device, fused=True) -> dict:
     return out
 
 
+def time_d64(b, t, h, steps, warmup, device, fused=True) -> dict:
+    """fwd+bwd of bayesian_layer with D = M = 64 diagonal dynamics (persistent_bayes_chunked.cu's shape).
+
+    fused: the HIP kernels (bssm_d64.hip) through the autograd boundary.
+    Otherwise the reference's diagonal core run eagerly on the same GPU (the
+    reference's non-fused path).  Keys and queries ~ N(0, 1/64); all six
+    inputs require gradients.  The D = 64 step is bound by the VALU
+    (about 20 thousand multiply-adds per token and sequence), not by HBM.
+    """
+    import bayes_ssm
+
+    n, d = b * h, 64
+    g = torch.Generator(device=device).manual_seed(5)
+    k = (torch.randn(n, t, d, device=device, generator=g) / 8).requires_grad_(True)
+    v = torch.randn(n, t, d, device=device, generator=g).requires_grad_(True)
+    q = (torch.randn(n, t, d, device=device, generator=g) / 8).requires_grad_(True)
+    dec = torch.sigmoid(torch.randn(n, t, d, device=device, generator=g) + 2.0).requires_grad_(True)
+    p = torch.nn.functional.softplus(torch.randn(n, t, device=device, generator=g) - 3.0).requires_grad_(True)
+    r = (1e-4 + torch.nn.functional.softplus(torch.randn(n, t, device=device, generator=g))).requires_grad_(True)
+    gy = torch.randn(n, t, d, device=device, generator=g)
+    leaves = (k, v, q, dec, p, r)
+    previous = os.environ.get("BAYES_SSM_DISABLE_FUSED_CUDA")
+    if not fused:
+        os.environ["BAYES_SSM_DISABLE_FUSED_CUDA"] = "1"
+    try:
+        def step():
+            y, _, _ = bayes_ssm.bayesian_layer(k, v, q, transition_diagonals=dec, process_variances=p,
+                                               observation_variances=r, chunk_length=64, optimized=True)
+            return torch.autograd.grad(y, leaves, gy)
+
+        for _ in range(warmup):
+            step()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(steps):
+            step()
+        e1.record()
+        torch.cuda.synchronize()
+    finally:
+        if previous is None:
+            os.environ.pop("BAYES_SSM_DISABLE_FUSED_CUDA", None)
+        else:
+            os.environ["BAYES_SSM_DISABLE_FUSED_CUDA"] = previous
+    ms = e0.elapsed_time(e1) / steps
+    return {"B": b, "T": t, "H": h, "D": d, "M": d, "sequences": n, "ms_per_step": ms,
+            "tokens_per_s": b * t / (ms * 1e-3),
+            "path": "HIP D64 kernels" if fused else "reference diagonal core, eager torch"}
+
+
 def time_scan(b, t, d, m, iters, device) -> dict:
     """Forward of associative_static_bayesian_cuda (one HIP kernel): mean microseconds per call."""
     from bayes_ssm.replay_ssm import associative_static_bayesian_cuda
@@ -358,7 +408,7 @@ def main() -> int:
     ap.add_argument("--cpu-budget", type=float, default=20.0, help="seconds of CPU-baseline work (0 = skip)")
     ap.add_argument("--no-extras", action="store_true",
                     help="skip the secondary shapes (per-GPU DP shape, D1/D2/D8 variants, associative scan)")
-    ap.add_argument("--secondary", choices=("mixer", "mixer-readout", "conv4", "rotation"),
+    ap.add_argument("--secondary", choices=("mixer", "mixer-readout", "conv4", "rotation", "d64"),
                     help="time only one secondary workload at the configured shape (the mixer's fused layer core, "
                          "with its readout epilogue, or the causal depthwise-4 filter on the q/k/v stream), for "
                          "profiling its kernels; prints its own JSON line")
@@ -383,6 +433,8 @@ def main() -> int:
             row = time_conv(b, t, h * (2 * d + m), args.steps, args.warmup, device, fused=True)
         elif args.secondary == "rotation":
             row = time_rotation(b, t, h, d, args.steps, args.warmup, device, fused=True)
+        elif args.secondary == "d64":
+            row = time_d64(b, t, h, args.steps, args.warmup, device, fused=True)
         else:
             row = time_mixer(b, t, h, args.steps, args.warmup, device, fused=True,
                              gated=args.secondary == "mixer-readout")
@@ -516,6 +568,10 @@ def main() -> int:
         extras["conv4_config3_qkv_torch"] = time_conv(b, t, qkv, 10, 3, device, fused=False)
         extras["rotation_config3_d4m8"] = time_rotation(b, t, h, 4, 10, 3, device, fused=True)
         extras["rotation_config3_d4m8_eager"] = time_rotation(b // 32, t, h, 4, 2, 1, device, fused=False)
+        # D = M = 64 at 8 heads (width 512): B = 32 (256 sequences) on the HIP
+        # kernels, and the eager torch core at B = 4 beside it.
+        extras["d64_b32t512h8"] = time_d64(32, t, 8, 3, 1, device, fused=True)
+        extras["d64_b4t512h8_eager"] = time_d64(4, t, 8, 1, 1, device, fused=False)
         extras["assoc_scan_config0"] = time_scan(1, 16, 4, 4, 50, device)
         extras["assoc_scan_config1"] = time_scan(4, 64, 16, 16, 50, device)
         result["extras"] = extras
