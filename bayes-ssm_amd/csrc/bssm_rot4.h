@@ -67,6 +67,12 @@ constexpr bool kSchedFwd = (BSSM_R4_SCHED & 1) != 0;
 constexpr bool kSchedReplay = (BSSM_R4_SCHED & 2) != 0;
 constexpr bool kSchedReverse = (BSSM_R4_SCHED & 4) != 0;
 constexpr bool kFenceReads = (BSSM_R4_SCHED & 8) != 0;
+#ifndef BSSM_R4_GQ_AFTER
+#define BSSM_R4_GQ_AFTER 1
+#endif
+// dL/dq from the mean after the token (one row sum) instead of
+// d * (M_prev gy) + beta u (e.gy) (a row sum and a quad all-reduce).
+constexpr bool kGqAfter = BSSM_R4_GQ_AFTER != 0;
 
 typedef float v2f __attribute__((ext_vector_type(2)));
 using Rsrc = __amdgpu_buffer_rsrc_t;
@@ -324,12 +330,13 @@ struct RevOut {
 //   ge = beta gM^T u (= dL/dv),  a = gM e,  w = S u,  z = u.(a - w)
 //   gs = (s > floor) ? -z beta^2 : 0 (= dL/dr)
 //   gu = beta (a - 2 w) + gs k
-//   dL/dk = -d*(M_prev ge) + gs u + P' gu,   dL/dq = d*(M_prev gy) + beta u (e.gy)
+//   dL/dk = -d*(M_prev ge) + gs u + P' gu,   dL/dq = M_new gy = d*(M_prev gy) + beta u (e.gy)
+// (M_new: the mean after the token, own columns, rotated like the belief).
 //   H = S + sym(gu k^T),  dL/dd_i = 2 sum_j H_ij d_j P_ij + sum_c (gM - k ge^T)_ic M_prev_ic
 //   dL/dp = trace(H),  S_prev = H * d d^T,  gM_prev = (gM - k ge^T) * d
 template <bool DYN>
-__device__ __forceinline__ void reverse_step(const RevTok& in, const Hist& h, float (&gM)[4][2], float (&S)[4],
-                                             float floor, RevOut& o) {
+__device__ __forceinline__ void reverse_step(const RevTok& in, const Hist& h, const float (&Mn)[4][2],
+                                             float (&gM)[4][2], float (&S)[4], float floor, RevOut& o) {
   const float beta = fast_rcp(fmaxf(h.s, floor));
   float ur[4];
   ur[0] = h.ug;
@@ -354,7 +361,8 @@ __device__ __forceinline__ void reverse_step(const RevTok& in, const Hist& h, fl
   for (int m = 0; m < 4; ++m) {
     av[m] = fmaf(gM[m][1], h.e[1], gM[m][0] * h.e[0]);
     Av[m] = fmaf(h.Mp[m][1], ge[1], h.Mp[m][0] * ge[0]);
-    Cv[m] = fmaf(h.Mp[m][1], in.gy[1], h.Mp[m][0] * in.gy[0]);
+    if constexpr (kGqAfter) Cv[m] = fmaf(Mn[m][1], in.gy[1], Mn[m][0] * in.gy[0]);
+    else Cv[m] = fmaf(h.Mp[m][1], in.gy[1], h.Mp[m][0] * in.gy[0]);
     float gb[2];
 #pragma unroll
     for (int c = 0; c < 2; ++c) {
@@ -363,11 +371,15 @@ __device__ __forceinline__ void reverse_step(const RevTok& in, const Hist& h, fl
     }
     Bv[m] = DYN ? fmaf(gb[1], h.Mp[m][1], gb[0] * h.Mp[m][0]) : 0.f;
   }
-  const float eg = quad_sum(fmaf(h.e[1], in.gy[1], h.e[0] * in.gy[0]));
   const float a_g = reduce_scatter(av);
   const float A_g = reduce_scatter(Av);
   const float C_g = reduce_scatter(Cv);
-  o.gq = fmaf(in.dr[0], C_g, (beta * h.ug) * eg);
+  if constexpr (kGqAfter) {
+    o.gq = C_g;
+  } else {
+    const float eg = quad_sum(fmaf(h.e[1], in.gy[1], h.e[0] * in.gy[0]));
+    o.gq = fmaf(in.dr[0], C_g, (beta * h.ug) * eg);
+  }
 
   float w = S[0] * ur[0];
 #pragma unroll
@@ -810,9 +822,10 @@ struct BwdCore {
     h.e[0] = o.e[0];
     h.e[1] = o.e[1];
   }
-  __device__ __forceinline__ void reverse(float* tl, int tt, const RevTok& in, const Hist& h) {
+  __device__ __forceinline__ void reverse(float* tl, int tt, const RevTok& in, const Hist& h,
+                                         const float (&Mn)[4][2]) {
     RevOut o;
-    reverse_step<DYN>(in, h, gM, S, floor, o);
+    reverse_step<DYN>(in, h, Mn, gM, S, floor, o);
     if (tt == 0) {
       first_gu = o.gu;
 #pragma unroll
@@ -855,7 +868,9 @@ struct BwdCore {
     for (int tt = LEN - 1; tt >= 0; --tt) {
       if (tt > 0) read_rev(tl, tt - 1, rx[tt - 1]);
       if constexpr (kFenceReads) __builtin_amdgcn_sched_barrier(0);
-      reverse(tl, tt, rx[tt], h[tt]);
+      // The mean after token tt: the next token's history, or the replayed
+      // belief after the chunk's last token.
+      reverse(tl, tt, rx[tt], h[tt], tt + 1 < LEN ? h[tt + 1 < LEN ? tt + 1 : tt].Mp : b.Mv);
       if constexpr (kSchedReverse) __builtin_amdgcn_sched_barrier(0);
     }
   }
