@@ -84,6 +84,16 @@ constexpr int kRot4Chunk = 8;
 hipError_t launch_forward_r4(bool fixed, const FwdArgs& a, hipStream_t stream);
 hipError_t launch_backward_r4(bool fixed, bool dyn, const BwdArgs& a, hipStream_t stream);
 
+// D = 1, M = 8 kernels with one lane per value column (bssm_d1.hip).  The
+// forward needs 16-byte aligned streams, T and the checkpoint chunk
+// multiples of 4; the backward also needs the checkpoint chunk to be 16 (the
+// library's preferred one for D = 1) and T a positive multiple of 16.
+// Other shapes take the generic kernels.
+bool d1_forward_ok(const FwdArgs& a);
+bool d1_backward_ok(const BwdArgs& a);
+hipError_t launch_forward_d1(bool fixed, const FwdArgs& a, hipStream_t stream);
+hipError_t launch_backward_d1(bool fixed, bool dyn, const BwdArgs& a, hipStream_t stream);
+
 // D = M = 64 kernels (bssm_d64.hip): one wave per sequence, lane = dimension.
 // The backward replays each checkpoint chunk on chip before reversing a token,
 // so its cost grows with the square of the chunk length; the autograd path

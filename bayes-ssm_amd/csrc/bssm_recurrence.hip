@@ -489,6 +489,7 @@ int preferred_checkpoint(int key_dim) {
 
 hipError_t launch_forward(int key_dim, bool fixed, const FwdArgs& a, hipStream_t stream) {
   if (key_dim == 4 && a.rot4) return launch_forward_r4(fixed, a, stream);
+  if (key_dim == 1 && d1_forward_ok(a)) return launch_forward_d1(fixed, a, stream);
   switch (key_dim) {
     case 1: return fixed ? launch_forward_d<1, true>(a, stream) : launch_forward_d<1, false>(a, stream);
     case 2: return fixed ? launch_forward_d<2, true>(a, stream) : launch_forward_d<2, false>(a, stream);
@@ -507,6 +508,7 @@ hipError_t launch_backward_dd(bool fixed, bool dyn, const BwdArgs& a, hipStream_
 
 hipError_t launch_backward(int key_dim, bool fixed, bool dyn, const BwdArgs& a, hipStream_t stream) {
   if (key_dim == 4 && a.rot4) return launch_backward_r4(fixed, dyn, a, stream);
+  if (key_dim == 1 && d1_backward_ok(a)) return launch_backward_d1(fixed, dyn, a, stream);
   switch (key_dim) {
     case 1: return launch_backward_dd<1>(fixed, dyn, a, stream);
     case 2: return launch_backward_dd<2>(fixed, dyn, a, stream);
