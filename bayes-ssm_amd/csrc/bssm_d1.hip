@@ -53,6 +53,10 @@ struct Slot {
   static constexpr int K = 0, D = SC, Q = 2 * SC, P = 3 * SC, R = 4 * SC, V = 5 * SC, GY = V + 64 * B;
 };
 constexpr int kFwdSlot = Slot<FB>::V + 64 * FB;        // 6656 floats
+// Forward ring of block slots: DMA up to kFwdSlots - 1 blocks ahead (a
+// three-slot ring measured no faster at config 2).
+constexpr int kFwdSlots = 2;
+static_assert(kFwdSlots == 2 || kFwdSlots == 3, "forward ring size");
 constexpr int kBwdSlot = Slot<BB>::GY + 64 * BB;       // 5376 floats
 
 // Per-lane DMA / store offsets of one block (bytes, relative to the wave's
@@ -135,7 +139,7 @@ __device__ __forceinline__ void step(float& P, float& M, float k, float d, float
 
 template <bool FIXED>
 __global__ __launch_bounds__(kWave) void forward_kernel(FwdArgs a) {
-  __shared__ float tile[2 * kFwdSlot];
+  __shared__ float tile[kFwdSlots * kFwdSlot];
   using S = Slot<FB>;
   const int lane = threadIdx.x;
   const int seq = lane >> 3, col = lane & 7;
@@ -182,23 +186,21 @@ __global__ __launch_bounds__(kWave) void forward_kernel(FwdArgs a) {
   constexpr int kLoads = FIXED ? 2 * 2 + 16 : 2 * 5 + 16;  // DMA instructions per block
 
   const uint32_t nblk = (T + FB - 1) / FB;
-  if (nblk > 0) issue(tile, 0);
-  if (nblk > 1) issue(tile + kFwdSlot, FB);
+#pragma unroll
+  for (int i = 0; i < kFwdSlots; ++i)
+    if (static_cast<uint32_t>(i) < nblk) issue(tile + i * kFwdSlot, i * FB);
   const uint32_t chunk = static_cast<uint32_t>(a.chunk);
   uint32_t next_ckpt = chunk, ckpt = 1;
   for (uint32_t b = 0; b < nblk; ++b) {
-    float* sl = tile + (b & 1) * kFwdSlot;
-    // Loads finish in issue order, so once at most the next block's DMA is
-    // outstanding this block's has landed.
-    if (b + 1 < nblk) vm_wait<kLoads>();
+    float* sl = tile + (b % kFwdSlots) * kFwdSlot;
+    // Loads finish in issue order, so once at most the DMA of the blocks
+    // after this one is outstanding this block's has landed.
+    if (kFwdSlots > 2 && b + 2 < nblk) vm_wait<(kFwdSlots > 2 ? 2 : 1) * kLoads>();
+    else if (b + 1 < nblk) vm_wait<kLoads>();
     else vm_wait<0>();
     const uint32_t t0 = b * FB;
     const int npc = static_cast<int>(((T - t0) < FB ? (T - t0) : FB) / 4);
-    Piece cur;
-    read_piece<FB, FIXED>(sl, 0, seq, lane, true, true, cur);
-    for (int pc = 0; pc < npc; ++pc) {
-      Piece nxt;
-      read_piece<FB, FIXED>(sl, pc + 1 < npc ? pc + 1 : pc, seq, lane, true, true, nxt);
+    auto run_piece = [&](int pc, const Piece& x) __attribute__((always_inline)) {
       if (t0 + 4u * pc == next_ckpt) {
         st32(rbm, M, bm_off, ckpt * 32u);
         st32(rbc, P, bc_off, ckpt * 4u);
@@ -208,15 +210,36 @@ __global__ __launch_bounds__(kWave) void forward_kernel(FwdArgs a) {
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         Hist h;
-        step(P, M, cur.k[j], cur.d[j], cur.p[j], cur.r[j], cur.v[j], a.floor, h);
-        sl[S::V + 64 * (4 * pc + j) + lane] = fmaf(M, cur.q[j], 0.f);
+        step(P, M, x.k[j], x.d[j], x.p[j], x.r[j], x.v[j], a.floor, h);
+        sl[S::V + 64 * (4 * pc + j) + lane] = fmaf(M, x.q[j], 0.f);
       }
-      cur = nxt;
+    };
+    if (npc == FB / 4) {
+      // Whole block: unrolled, each piece's LDS reads issued two pieces
+      // ahead into a ring of registers.
+      constexpr int A = 2;  // pieces read ahead
+      Piece x[A + 1];
+#pragma unroll
+      for (int pc = 0; pc < A; ++pc) read_piece<FB, FIXED>(sl, pc, seq, lane, true, true, x[pc]);
+#pragma unroll
+      for (int pc = 0; pc < FB / 4; ++pc) {
+        if (pc + A < FB / 4) read_piece<FB, FIXED>(sl, pc + A, seq, lane, true, true, x[(pc + A) % (A + 1)]);
+        run_piece(pc, x[pc % (A + 1)]);
+      }
+    } else {
+      Piece cur;
+      read_piece<FB, FIXED>(sl, 0, seq, lane, true, true, cur);
+      for (int pc = 0; pc < npc; ++pc) {
+        Piece nxt;
+        read_piece<FB, FIXED>(sl, pc + 1 < npc ? pc + 1 : pc, seq, lane, true, true, nxt);
+        run_piece(pc, cur);
+        cur = nxt;
+      }
     }
     __syncthreads();
 #pragma unroll
     for (int i = 0; i < 16; ++i) st128<kNtSt>(ry, lds4(sl + S::V + 256 * i + 4 * lane), mp.v(i, t0, T), 0);
-    if (b + 2 < nblk) issue(sl, t0 + 2 * FB);
+    if (b + kFwdSlots < nblk) issue(sl, t0 + kFwdSlots * FB);
   }
   st32(make_rsrc(a.mT + n0 * 8, valid * 32u), M, 4u * lane, 0);
   st32(make_rsrc(a.cT + n0, valid * 4u), P, col == 0 ? 4u * seq : kOob, 0);
@@ -350,27 +373,29 @@ __global__ __launch_bounds__(kWave) void backward_kernel(BwdArgs a) {
   // Replay one 16-token chunk (pieces pc0 .. pc0 + 3 of the slot) from its
   // checkpoint, then reverse it; the gradients overwrite the chunk's inputs.
   auto run_chunk = [&](float* sl, int pc0, float P, float M, bool first_chunk) __attribute__((always_inline)) {
-    Hist h[kChunk];
+    // The whole chunk's inputs are read up front: one LDS latency per chunk.
+    Piece x[4];
+    float gy[4][4];
 #pragma unroll
     for (int g4 = 0; g4 < 4; ++g4) {
-      Piece x;
-      read_piece<BB, FIXED>(sl, pc0 + g4, seq, lane, true, false, x);
+      read_piece<BB, FIXED>(sl, pc0 + g4, seq, lane, true, true, x[g4]);
 #pragma unroll
-      for (int j = 0; j < 4; ++j) step(P, M, x.k[j], x.d[j], x.p[j], x.r[j], x.v[j], a.floor, h[4 * g4 + j]);
+      for (int j = 0; j < 4; ++j) gy[g4][j] = sl[S::GY + 64 * (4 * (pc0 + g4) + j) + lane];
     }
+    Hist h[kChunk];
+#pragma unroll
+    for (int g4 = 0; g4 < 4; ++g4)
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        step(P, M, x[g4].k[j], x[g4].d[j], x[g4].p[j], x[g4].r[j], x[g4].v[j], a.floor, h[4 * g4 + j]);
 #pragma unroll
     for (int g4 = 3; g4 >= 0; --g4) {
       const int pc = pc0 + g4;
-      Piece x;
-      read_piece<BB, FIXED>(sl, pc, seq, lane, false, true, x);
-      float gy[4];
-#pragma unroll
-      for (int j = 0; j < 4; ++j) gy[j] = sl[S::GY + 64 * (4 * pc + j) + lane];
       v4f gk, gq, gd, gp, gr;
 #pragma unroll
       for (int j = 3; j >= 0; --j) {
         RevOut1 o;
-        reverse<DYN>(h[4 * g4 + j], x.k[j], x.d[j], x.p[j], x.q[j], gy[j], a.floor, gM, Gs,
+        reverse<DYN>(h[4 * g4 + j], x[g4].k[j], x[g4].d[j], x[g4].p[j], x[g4].q[j], gy[g4][j], a.floor, gM, Gs,
                      first_chunk && g4 == 0 && j == 0, gc0, o);
         gk[j] = o.gk;
         gq[j] = o.gq;
