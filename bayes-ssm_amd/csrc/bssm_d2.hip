@@ -1,0 +1,489 @@
+// gfx950 checkpoint-replay backward for D = 2, M = 8
+// (bayes_ssm/persistent_bayes_chunked_d2m8.cu is the reference extension for
+// this shape; the per-token equations are those of bssm_step.h with two key
+// dimensions), with two value columns per lane.  The forward of this shape
+// is the generic kernel of bssm_recurrence.hip (a column-per-lane forward
+// fed by 8-token LDS-DMA blocks measured slower than its register-staged
+// 16-token tiles: this forward does little arithmetic per byte and needs
+// more bytes in flight than such blocks leave).
+//
+// A wave holds 16 sequences; lane l = 4 s + g owns value columns 2g, 2g + 1
+// of sequence s.  Every lane carries the whole 2 x 2 covariance of its
+// sequence (the four lanes apply the same operations to the same inputs, so
+// they hold identical values; the two off-diagonal entries are carried
+// separately, as the row owners of the generic kernels carry them), so the
+// replay needs no cross-lane traffic and the reverse's sums over value
+// columns are 4-lane DPP all-reduces.
+//
+// Inputs arrive by LDS-DMA in blocks of 8 tokens (one checkpoint chunk), one
+// block ahead.  LDS layouts of a block (floats):
+//   k, d, q (two per token): piece-major [4 pieces][16 seq][2 tokens x 2];
+//   p, r: piece-major [2 pieces][16 seq][4 tokens] (the DMA instruction's
+//     upper 32 lanes are idle and fill the padding after it with zeros);
+//   v, gy: token-major [8][16 seq][8 col], so lane l reads floats
+//     128 t + 2 l, 2 l + 1 of token t;
+//   checkpoint records: mean [16 seq][2][8], covariance [16 seq][2][2]
+//     (+ padding).
+// Gradients overwrite their inputs in place and leave as 16-byte pieces
+// through the same maps.
+
+#include "bssm_rot4.h"
+#include "bssm_step.h"
+
+namespace bssm {
+namespace d2 {
+
+using r4::dma16;
+using r4::kOob;
+using r4::make_rsrc;
+using r4::Rsrc;
+using r4::st128;
+using r4::st64;
+using r4::vm_wait;
+
+typedef float v2f __attribute__((ext_vector_type(2)));
+
+constexpr int SPW = 16;     // sequences per wave
+constexpr int BT = 8;       // block, tokens
+constexpr int kChunk = 8;   // backward checkpoint chunk, tokens
+constexpr bool kNt = r4::kNtLoad;
+constexpr int kNtSt = r4::kNtStore;
+
+
+// Float offsets inside one block slot.
+struct Slot {
+  static constexpr int K = 0, D = 256, Q = 512, P = 768, R = 1024, V = 1280, GY = 2304, CKM = 3328, CKC = 3584;
+  static constexpr int BWD = 3840;
+};
+
+__device__ __forceinline__ v4f lds4(const float* p) { return *reinterpret_cast<const v4f*>(p); }
+__device__ __forceinline__ v2f lds2(const float* p) { return *reinterpret_cast<const v2f*>(p); }
+__device__ __forceinline__ void lds4_store(float* p, v4f x) { *reinterpret_cast<v4f*>(p) = x; }
+__device__ __forceinline__ void lds2_store(float* p, v2f x) { *reinterpret_cast<v2f*>(p) = x; }
+
+// Per-lane DMA / store offsets (bytes, relative to the wave's stream base)
+// of a block starting at token t0.
+struct Map {
+  uint32_t k_base, k_piece;  // k/d/q: sequence j & 15, piece j >> 4 (2 tokens)
+  uint32_t s_base, s_piece;  // p/r: sequence j & 15, piece j >> 4 (4 tokens), lanes < 32
+  uint32_t v_base, v_tok;    // v/gy: token 2 i + (j >> 5), sequence (j >> 1) & 15, half j & 1
+  __device__ __forceinline__ Map(int lane, uint32_t row1, uint32_t row2, uint32_t row8)
+      : k_base(static_cast<uint32_t>(lane & 15) * row2),
+        k_piece(static_cast<uint32_t>(lane >> 4)),
+        s_base(static_cast<uint32_t>(lane & 15) * row1),
+        s_piece(static_cast<uint32_t>(lane >> 4)),
+        v_base(static_cast<uint32_t>((lane >> 1) & 15) * row8 + static_cast<uint32_t>(lane & 1) * 16u),
+        v_tok(static_cast<uint32_t>(lane >> 5)) {}
+  __device__ __forceinline__ uint32_t k(uint32_t t0, uint32_t T) const {
+    const uint32_t t = t0 + 2u * k_piece;
+    return t < T ? k_base + 8u * t : kOob;
+  }
+  __device__ __forceinline__ uint32_t s(uint32_t t0, uint32_t T) const {
+    const uint32_t t = t0 + 4u * s_piece;
+    return (s_piece < 2u && t < T) ? s_base + 4u * t : kOob;
+  }
+  __device__ __forceinline__ uint32_t v(int i, uint32_t t0, uint32_t T) const {
+    const uint32_t t = t0 + 2u * i + v_tok;
+    return t < T ? v_base + 32u * t : kOob;
+  }
+};
+
+// Inputs of one token as lane (s, g) sees them.
+struct Tok {
+  float k[2], d[2], q[2], p, r;
+  float v[2];
+};
+
+// Inputs of a 4-token piece: two k/d/q pieces, one p/r piece, four v pairs.
+struct Piece {
+  v4f k[2], d[2], q[2], p, r;
+  v2f v[4];
+  __device__ __forceinline__ Tok tok(int j) const {
+    Tok t;
+    const int h = j >> 1, o = 2 * (j & 1);
+    t.k[0] = k[h][o];
+    t.k[1] = k[h][o + 1];
+    t.d[0] = d[h][o];
+    t.d[1] = d[h][o + 1];
+    t.q[0] = q[h][o];
+    t.q[1] = q[h][o + 1];
+    t.p = p[j];
+    t.r = r[j];
+    t.v[0] = v[j][0];
+    t.v[1] = v[j][1];
+    return t;
+  }
+};
+
+// Piece pc (tokens 4 pc .. 4 pc + 3 of the block) of slot sl.
+template <bool FIXED>
+__device__ __forceinline__ void read_piece(const float* sl, int pc, int seq, int lane, bool need_v, bool need_q,
+                                           Piece& x) {
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const int o = 64 * (2 * pc + h) + 4 * seq;
+    x.k[h] = lds4(sl + Slot::K + o);
+    if constexpr (FIXED) x.d[h] = v4f{kFixedDecay, kFixedDecay, kFixedDecay, kFixedDecay};
+    else x.d[h] = lds4(sl + Slot::D + o);
+    if (need_q) x.q[h] = lds4(sl + Slot::Q + o);
+  }
+  if constexpr (FIXED) {
+    x.p = v4f{kFixedProcess, kFixedProcess, kFixedProcess, kFixedProcess};
+    x.r = v4f{kFixedObservation, kFixedObservation, kFixedObservation, kFixedObservation};
+  } else {
+    x.p = lds4(sl + Slot::P + 64 * pc + 4 * seq);
+    x.r = lds4(sl + Slot::R + 64 * pc + 4 * seq);
+  }
+  if (need_v) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) x.v[j] = lds2(sl + Slot::V + 128 * (4 * pc + j) + 2 * lane);
+  }
+}
+
+// Belief of one lane: the covariance (row-major, both off-diagonal entries)
+// and the lane's two columns of both mean rows.
+struct Bel {
+  float P[4];
+  float M[2][2];  // [row][own column]
+};
+
+// What the reverse of one token needs from its replay.
+struct Hist {
+  float P[4], M[2][2];  // belief before the token
+  float u[2], s, e[2];  // u = P' k, s = r + k.u, own innovations
+};
+
+// One replayed token (the D = 2 case of forward_step in bssm_step.h: row i
+// of the covariance update uses row i's entries only).
+__device__ __forceinline__ void step(Bel& b, const Tok& x, float floor, Hist& h) {
+  float dp[4], Pb[4], u[2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    float acc = x.p * x.k[i];
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      dp[2 * i + j] = (x.d[i] * x.d[j]) * b.P[2 * i + j];
+      Pb[2 * i + j] = fmaf(x.p, i == j ? 1.f : 0.f, dp[2 * i + j]);
+      acc = fmaf(dp[2 * i + j], x.k[j], acc);
+    }
+    u[i] = acc;
+  }
+  const float s = fmaf(x.k[1], u[1], fmaf(x.k[0], u[0], x.r));
+  const float beta = fast_rcp(fmaxf(s, floor));
+  const float wk0 = x.d[0] * x.k[0], wk1 = x.d[1] * x.k[1];
+  const float bu0 = beta * u[0], bu1 = beta * u[1];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) h.P[i] = b.P[i];
+#pragma unroll
+  for (int c = 0; c < 2; ++c) {
+    h.M[0][c] = b.M[0][c];
+    h.M[1][c] = b.M[1][c];
+    const float e = fmaf(-b.M[1][c], wk1, fmaf(-b.M[0][c], wk0, x.v[c]));
+    h.e[c] = e;
+    b.M[0][c] = fmaf(bu0, e, x.d[0] * b.M[0][c]);
+    b.M[1][c] = fmaf(bu1, e, x.d[1] * b.M[1][c]);
+  }
+  h.u[0] = u[0];
+  h.u[1] = u[1];
+  h.s = s;
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j) b.P[2 * i + j] = fmaf(-beta, u[i] * u[j], Pb[2 * i + j]);
+}
+
+// Sum over the 4 lanes (column pairs) of the caller's sequence.
+__device__ __forceinline__ float colsum(float x) { return group_sum<4>(x); }
+
+// Token outputs of the reverse (per-sequence values identical on the 4 lanes).
+struct RevOut2 {
+  float gk[2], gq[2], gd[2], gp, gr;
+  float gv[2];
+};
+
+// Reverse of one token (the D = 2, two-columns-per-lane case of
+// reverse_step in bssm_step.h).  gM: own columns of dL/dM; Gs: sym(dL/dP)
+// (G00, G01, G11).  At the first token the full (asymmetric) adjoint of the
+// initial covariance is left in gc0.
+template <bool DYN>
+__device__ __forceinline__ void reverse(const Hist& h, const Tok& x, float floor, float (&gM)[2][2],
+                                        float (&Gs)[3], bool first, float (&gc0)[4], RevOut2& o) {
+  const float beta = fast_rcp(fmaxf(h.s, floor));
+  float mp[2][2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int c = 0; c < 2; ++c) mp[i][c] = x.d[i] * h.M[i][c];
+  float Pb[4];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j) Pb[2 * i + j] = fmaf(x.p, i == j ? 1.f : 0.f, (x.d[i] * x.d[j]) * h.P[2 * i + j]);
+
+  float gqp[2] = {0.f, 0.f}, ap[2] = {0.f, 0.f}, gkp[2] = {0.f, 0.f}, gdp[2] = {0.f, 0.f};
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const float bu = beta * h.u[i];
+#pragma unroll
+    for (int c = 0; c < 2; ++c) {
+      gqp[i] = fmaf(fmaf(bu, h.e[c], mp[i][c]), x.v[c], gqp[i]);  // x.v holds gy here
+      gM[i][c] = fmaf(x.q[i], x.v[c], gM[i][c]);
+    }
+  }
+  float ge[2];
+#pragma unroll
+  for (int c = 0; c < 2; ++c) {
+    ge[c] = beta * fmaf(gM[1][c], h.u[1], fmaf(gM[0][c], h.u[0], 0.f));
+    o.gv[c] = ge[c];
+  }
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int c = 0; c < 2; ++c) {
+      ap[i] = fmaf(gM[i][c], h.e[c], ap[i]);
+      gkp[i] = fmaf(-mp[i][c], ge[c], gkp[i]);
+      const float gmb = fmaf(-x.k[i], ge[c], gM[i][c]);
+      if constexpr (DYN) gdp[i] = fmaf(gmb, h.M[i][c], gdp[i]);
+      gM[i][c] = gmb * x.d[i];
+    }
+  float av[2], gkc[2], gdc[2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    av[i] = colsum(ap[i]);
+    gkc[i] = colsum(gkp[i]);
+    o.gq[i] = colsum(gqp[i]);
+    gdc[i] = DYN ? colsum(gdp[i]) : 0.f;
+  }
+  const float G[2][2] = {{Gs[0], Gs[1]}, {Gs[1], Gs[2]}};
+  float w[2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i) w[i] = fmaf(G[i][1], h.u[1], fmaf(G[i][0], h.u[0], 0.f));
+  const float z = fmaf(h.u[0], av[0] - w[0], 0.f) + fmaf(h.u[1], av[1] - w[1], 0.f);
+  const float gs = (h.s > floor) ? -z * beta * beta : 0.f;
+  float gu[2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i) gu[i] = fmaf(beta, av[i] - 2.f * w[i], gs * x.k[i]);
+  float hs[2][2], gd[2] = {0.f, 0.f};
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    float gk = fmaf(gs, h.u[i], gkc[i]);
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      gk = fmaf(Pb[2 * i + j], gu[j], gk);
+      hs[i][j] = fmaf(0.5f, gu[i] * x.k[j] + gu[j] * x.k[i], G[i][j]);
+      if constexpr (DYN) gd[i] = fmaf(hs[i][j] * x.d[j], h.P[2 * i + j], gd[i]);
+      if (first) gc0[2 * i + j] = fmaf(gu[i], x.k[j], G[i][j]) * (x.d[i] * x.d[j]);
+    }
+    o.gk[i] = gk;
+    o.gd[i] = DYN ? fmaf(2.f, gd[i], gdc[i]) : 0.f;
+  }
+  Gs[0] = hs[0][0] * (x.d[0] * x.d[0]);
+  Gs[1] = hs[0][1] * (x.d[0] * x.d[1]);
+  Gs[2] = hs[1][1] * (x.d[1] * x.d[1]);
+  o.gp = DYN ? hs[0][0] + hs[1][1] : 0.f;
+  o.gr = DYN ? gs : 0.f;
+}
+
+template <bool FIXED, bool DYN>
+__global__ __launch_bounds__(kWave) void backward_kernel(BwdArgs a) {
+  __shared__ float tile[2 * Slot::BWD];
+  const int lane = threadIdx.x;
+  const int seq = lane >> 2, g = lane & 3;
+  const int64_t n0 = static_cast<int64_t>(blockIdx.x) * SPW;
+  const uint32_t T = static_cast<uint32_t>(a.t);
+  const uint32_t valid = static_cast<uint32_t>((a.n - n0) < SPW ? (a.n - n0) : SPW);
+  const uint32_t row1 = T * 4u, row2 = T * 8u, row8 = T * 32u;
+  const Rsrc rk = make_rsrc(a.k + n0 * T * 2, valid * row2);
+  const Rsrc rq = make_rsrc(a.q + n0 * T * 2, valid * row2);
+  const Rsrc rv = make_rsrc(a.v + n0 * T * 8, valid * row8);
+  const Rsrc rgy = make_rsrc(a.gy + n0 * T * 8, valid * row8);
+  const Rsrc rd = make_rsrc(FIXED ? a.k : a.d + n0 * T * 2, FIXED ? 0u : valid * row2);
+  const Rsrc rp = make_rsrc(FIXED ? a.k : a.p + n0 * T, FIXED ? 0u : valid * row1);
+  const Rsrc rr = make_rsrc(FIXED ? a.k : a.r + n0 * T, FIXED ? 0u : valid * row1);
+  const Rsrc rgk = make_rsrc(a.gk + n0 * T * 2, valid * row2);
+  const Rsrc rgq = make_rsrc(a.gq + n0 * T * 2, valid * row2);
+  const Rsrc rgv = make_rsrc(a.gv + n0 * T * 8, valid * row8);
+  const Rsrc rgd = make_rsrc(a.gd ? a.gd + n0 * T * 2 : a.gk, a.gd ? valid * row2 : 0u);
+  const Rsrc rgp = make_rsrc(a.gp ? a.gp + n0 * T : a.gk, a.gp ? valid * row1 : 0u);
+  const Rsrc rgr = make_rsrc(a.gr ? a.gr + n0 * T : a.gk, a.gr ? valid * row1 : 0u);
+  const uint32_t nbp = static_cast<uint32_t>(a.nb + 1);
+  const Rsrc rbm = make_rsrc(a.bm + n0 * nbp * 16, valid * nbp * 64u);
+  const Rsrc rbc = make_rsrc(a.bc + n0 * nbp * 4, valid * nbp * 16u);
+  const Map mp(lane, row1, row2, row8);
+  // Checkpoint record DMA: mean records by (sequence j >> 2, piece j & 3),
+  // covariance records by lanes j < 16.
+  const uint32_t ckm_off = static_cast<uint32_t>(lane >> 2) * nbp * 64u + 16u * (lane & 3);
+  const uint32_t ckc_off = lane < 16 ? static_cast<uint32_t>(lane) * nbp * 16u : kOob;
+
+  // Carried adjoints: gM = dL/dM (own columns), Gs = sym(dL/dP).
+  float gM[2][2] = {{0.f, 0.f}, {0.f, 0.f}};
+  float Gs[3] = {0.f, 0.f, 0.f};
+  if (a.gmf) {
+    const Rsrc r = make_rsrc(a.gmf + n0 * 16, valid * 64u);
+    const uint32_t mo = static_cast<uint32_t>(seq) * 64u + 8u * g;
+    const v2f m0 = r4::ld64(r, mo, 0), m1 = r4::ld64(r, mo + 32u, 0);
+    gM[0][0] = m0[0];
+    gM[0][1] = m0[1];
+    gM[1][0] = m1[0];
+    gM[1][1] = m1[1];
+  }
+  v4f gcf = v4f{0.f, 0.f, 0.f, 0.f};
+  if (a.gcf) {
+    gcf = r4::ld128<false>(make_rsrc(a.gcf + n0 * 4, valid * 16u), static_cast<uint32_t>(seq) * 16u);
+    Gs[0] = 0.5f * (gcf[0] + gcf[0]);
+    Gs[1] = 0.5f * (gcf[1] + gcf[2]);
+    Gs[2] = 0.5f * (gcf[3] + gcf[3]);
+  }
+  float gc0[4] = {0.f, 0.f, 0.f, 0.f};
+
+  const uint32_t nblk = (T + BT - 1) / BT;
+  auto issue = [&](float* sl, uint32_t blk) __attribute__((always_inline)) {
+    const uint32_t t0 = blk * BT;
+    const uint32_t ok = mp.k(t0, T);
+    dma16<kNt>(rk, sl + Slot::K, ok);
+    dma16<kNt>(rq, sl + Slot::Q, ok);
+    if constexpr (!FIXED) {
+      dma16<kNt>(rd, sl + Slot::D, ok);
+      const uint32_t os = mp.s(t0, T);
+      dma16(rp, sl + Slot::P, os);
+      dma16(rr, sl + Slot::R, os);
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const uint32_t ov = mp.v(i, t0, T);
+      dma16<kNt>(rv, sl + Slot::V + 256 * i, ov);
+      dma16<kNt>(rgy, sl + Slot::GY + 256 * i, ov);
+    }
+    dma16(rbm, sl + Slot::CKM, ckm_off + 64u * blk);
+    dma16(rbc, sl + Slot::CKC, ckc_off == kOob ? kOob : ckc_off + 16u * blk);
+  };
+
+  auto store_grads = [&](const float* sl, uint32_t blk) __attribute__((always_inline)) {
+    const uint32_t t0 = blk * BT;
+    const int e = 4 * lane;
+    const uint32_t ok = mp.k(t0, T);
+    const v4f zero = v4f{0.f, 0.f, 0.f, 0.f};
+    st128<kNtSt>(rgk, lds4(sl + Slot::K + e), ok, 0);
+    st128<kNtSt>(rgq, lds4(sl + Slot::Q + e), ok, 0);
+    st128<kNtSt>(rgd, DYN ? lds4(sl + Slot::D + e) : zero, ok, 0);
+    const uint32_t os = mp.s(t0, T);
+    st128(rgp, DYN ? lds4(sl + Slot::P + e) : zero, os, 0);
+    st128(rgr, DYN ? lds4(sl + Slot::R + e) : zero, os, 0);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) st128<kNtSt>(rgv, lds4(sl + Slot::V + 256 * i + e), mp.v(i, t0, T), 0);
+  };
+
+  // Replay the block's chunk from its checkpoint record, then reverse it;
+  // the gradients overwrite the block's inputs.
+  auto run_chunk = [&](float* sl, int npc, bool first_chunk) __attribute__((always_inline)) {
+    Bel b;
+    {
+      const v2f m0 = lds2(sl + Slot::CKM + 16 * seq + 2 * g), m1 = lds2(sl + Slot::CKM + 16 * seq + 8 + 2 * g);
+      b.M[0][0] = m0[0];
+      b.M[0][1] = m0[1];
+      b.M[1][0] = m1[0];
+      b.M[1][1] = m1[1];
+      const v4f c = lds4(sl + Slot::CKC + 4 * seq);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) b.P[i] = c[i];
+    }
+    Piece x[2];
+    v2f gy[2][4];
+#pragma unroll
+    for (int pc = 0; pc < 2; ++pc) {
+      read_piece<FIXED>(sl, pc, seq, lane, true, true, x[pc]);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) gy[pc][j] = lds2(sl + Slot::GY + 128 * (4 * pc + j) + 2 * lane);
+    }
+    Hist h[kChunk];
+#pragma unroll
+    for (int pc = 0; pc < 2; ++pc)
+      if (pc < npc)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) step(b, x[pc].tok(j), a.floor, h[4 * pc + j]);
+#pragma unroll
+    for (int pc = 1; pc >= 0; --pc) {
+      if (pc < npc) {
+        v4f gk[2], gq[2], gd[2], gp, gr;
+#pragma unroll
+        for (int j = 3; j >= 0; --j) {
+          Tok t = x[pc].tok(j);
+          t.v[0] = gy[pc][j][0];
+          t.v[1] = gy[pc][j][1];
+          RevOut2 o;
+          reverse<DYN>(h[4 * pc + j], t, a.floor, gM, Gs, first_chunk && pc == 0 && j == 0, gc0, o);
+          const int hh = j >> 1, oo = 2 * (j & 1);
+          gk[hh][oo] = o.gk[0];
+          gk[hh][oo + 1] = o.gk[1];
+          gq[hh][oo] = o.gq[0];
+          gq[hh][oo + 1] = o.gq[1];
+          gd[hh][oo] = o.gd[0];
+          gd[hh][oo + 1] = o.gd[1];
+          gp[j] = o.gp;
+          gr[j] = o.gr;
+          lds2_store(sl + Slot::V + 128 * (4 * pc + j) + 2 * lane, v2f{o.gv[0], o.gv[1]});
+        }
+        if (g == 0) {
+#pragma unroll
+          for (int hh = 0; hh < 2; ++hh) {
+            const int o = 64 * (2 * pc + hh) + 4 * seq;
+            lds4_store(sl + Slot::K + o, gk[hh]);
+            lds4_store(sl + Slot::Q + o, gq[hh]);
+            if constexpr (DYN) lds4_store(sl + Slot::D + o, gd[hh]);
+          }
+          if constexpr (DYN) {
+            lds4_store(sl + Slot::P + 64 * pc + 4 * seq, gp);
+            lds4_store(sl + Slot::R + 64 * pc + 4 * seq, gr);
+          }
+        }
+      }
+    }
+  };
+
+  // Block b is processed in slot b % 2.  At its start every outstanding
+  // memory operation was issued a whole block earlier; then the gradients of
+  // block b + 1 leave the other slot, which receives block b - 1.
+  if (nblk > 0) issue(tile + ((nblk - 1) & 1) * Slot::BWD, nblk - 1);
+  for (uint32_t i = 0; i < nblk; ++i) {
+    const uint32_t blk = nblk - 1 - i;
+    float* cur = tile + (blk & 1) * Slot::BWD;
+    float* other = tile + ((blk + 1) & 1) * Slot::BWD;
+    vm_wait<0>();
+    __syncthreads();
+    if (blk + 1 < nblk) store_grads(other, blk + 1);
+    if (blk > 0) issue(other, blk - 1);
+    run_chunk(cur, (T - blk * BT) < BT ? 1 : 2, blk == 0);
+  }
+  if (nblk > 0) {
+    __syncthreads();
+    store_grads(tile, 0);
+  }
+  if (a.gm0) {
+    const Rsrc r = make_rsrc(a.gm0 + n0 * 16, valid * 64u);
+    const uint32_t mo = static_cast<uint32_t>(seq) * 64u + 8u * g;
+    st64(r, v2f{gM[0][0], gM[0][1]}, mo, 0);
+    st64(r, v2f{gM[1][0], gM[1][1]}, mo + 32u, 0);
+  }
+  if (a.gc0)
+    st128(make_rsrc(a.gc0 + n0 * 4, valid * 16u), T > 0 ? v4f{gc0[0], gc0[1], gc0[2], gc0[3]} : gcf,
+          g == 0 ? static_cast<uint32_t>(seq) * 16u : kOob, 0);
+}
+
+}  // namespace d2
+
+bool d2_backward_ok(const BwdArgs& a) {
+  return a.vec_kqd && a.vec_v && a.vec_pr && a.t > 0 && a.t % 4 == 0 && a.chunk == d2::kChunk &&
+         a.t * 512 < (int64_t(1) << 31) && (a.nb + 1) * 1024 < (int64_t(1) << 31);
+}
+
+hipError_t launch_backward_d2(bool fixed, bool dyn, const BwdArgs& a, hipStream_t stream) {
+  const int64_t blocks = (a.n + d2::SPW - 1) / d2::SPW;
+  if (blocks == 0) return hipSuccess;
+  const dim3 grid(static_cast<unsigned>(blocks)), block(kWave);
+  if (fixed) hipLaunchKernelGGL((d2::backward_kernel<true, false>), grid, block, 0, stream, a);
+  else if (dyn) hipLaunchKernelGGL((d2::backward_kernel<false, true>), grid, block, 0, stream, a);
+  else hipLaunchKernelGGL((d2::backward_kernel<false, false>), grid, block, 0, stream, a);
+  return hipGetLastError();
+}
+
+}  // namespace bssm

@@ -1,12 +1,14 @@
-"""GPU parity of the D = 1, M = 8 column-per-lane kernels (bssm_d1.hip) against the CPU oracle.
+"""GPU parity of the D = 1 and D = 2 (M = 8) column-per-lane kernels (bssm_d1.hip, bssm_d2.hip).
 
-These kernels take D1 calls whose streams are 16-byte aligned with T and the
-checkpoint chunk multiples of 4 (forward), and chunk 16 with T a positive
-multiple of 16 (backward); the shapes below are chosen to reach them, with
-N = 37 leaving idle sequence slots in the last wave and T values that end
-on partial 64-token forward blocks and on half-filled 32-token backward
-blocks.  Other D1 shapes take the generic kernels, which serve as a second
-reference here.  Tolerance (north star): 1e-5 relative, 1e-4 absolute.
+The D = 1 forward takes calls whose streams are 16-byte aligned with T and
+the checkpoint chunk multiples of 4 (the D = 2 forward is the generic
+kernel); the backwards take the library's preferred checkpoint chunk (16 for
+D = 1, 8 for D = 2), and for D = 1 also T a multiple of 16.  The shapes
+below are chosen to reach them, with N = 37 leaving idle sequence slots in
+the last wave and T values that end on partial forward blocks and on partly
+filled backward blocks.  Other shapes take the generic kernels, which serve
+as a second reference here.  Tolerance (north star): 1e-5 relative, 1e-4
+absolute.
 """
 from __future__ import annotations
 
@@ -18,14 +20,15 @@ from tests.test_gpu_parity import ABIS, _case, _fixed_dynamics, _oracle_forward,
 
 pytestmark = pytest.mark.gpu
 
-D = 1
+DIMS = [1, 2]
+CHUNK = {1: 16, 2: 8}  # the backward's checkpoint chunk
+BWD_TIMES = {1: [16, 48, 64, 80], 2: [4, 12, 16, 60]}
 
 
-@pytest.fixture(scope="module")
-def ext(cuda_device):
+def _ext(d):
     from bayes_ssm import fused_cuda
 
-    e = fused_cuda._load_extension(D)
+    e = fused_cuda._load_extension(d)
     assert e is not None
     return e
 
@@ -35,13 +38,15 @@ def _forward(ext, dev, fixed, chunk):
     return fn(dev["k"], dev["v"], dev["q"], dev["d"], dev["p"], dev["r"], dev["m0"], dev["c0"], chunk, 1e-6)
 
 
+@pytest.mark.parametrize("D", DIMS)
 @pytest.mark.parametrize("fixed", [False, True])
 @pytest.mark.parametrize("chunk", [4, 12, 16, 64])
 @pytest.mark.parametrize("t", [4, 60, 64, 68, 200])
-def test_d1_forward_matches_oracle(ext, cuda_device, fixed, chunk, t):
-    print(f"d1 forward fixed={fixed} chunk={chunk} t={t}", flush=True)
+def test_small_d_forward_matches_oracle(cuda_device, D, fixed, chunk, t):
+    print(f"small-D forward D={D} fixed={fixed} chunk={chunk} t={t}", flush=True)
+    ext = _ext(D)
     n = 37
-    cpu, dev = _case(n, t, D, seed=500 + t + chunk, device=cuda_device)
+    cpu, dev = _case(n, t, D, seed=500 + 7 * D + t + chunk, device=cuda_device)
     y, mT, cT, bm, bc = _forward(ext, dev, fixed, chunk)
     torch.cuda.synchronize()
     ref = _fixed_dynamics(cpu) if fixed else cpu
@@ -60,8 +65,10 @@ def test_d1_forward_matches_oracle(ext, cuda_device, fixed, chunk, t):
     assert torch.equal(bm[:, 0].cpu(), dev["m0"].cpu()) and torch.equal(bc[:, 0].cpu(), dev["c0"].cpu())
 
 
-def test_d1_forward_matches_generic_kernel(ext, cuda_device):
+@pytest.mark.parametrize("D", DIMS)
+def test_small_d_forward_matches_generic_kernel(cuda_device, D):
     """Chunk 13 (not a multiple of 4) takes the generic kernel: same recurrence, same checkpoint indexing."""
+    ext = _ext(D)
     n, t = 45, 104
     _, dev = _case(n, t, D, seed=77, device=cuda_device)
     fast = _forward(ext, dev, False, 52)
@@ -73,14 +80,17 @@ def test_d1_forward_matches_generic_kernel(ext, cuda_device):
     close(fast[4], generic[4][:, ::4], "bcov")
 
 
+@pytest.mark.parametrize("D", DIMS)
 @pytest.mark.parametrize("abi", ABIS, ids=[a[0] for a in ABIS])
 @pytest.mark.parametrize("final_grads", [False, True])
-@pytest.mark.parametrize("t", [16, 48, 64, 80])
-def test_d1_backward_matches_oracle(ext, cuda_device, abi, final_grads, t):
+@pytest.mark.parametrize("ti", range(4))
+def test_small_d_backward_matches_oracle(cuda_device, D, abi, final_grads, ti):
     name, fixed, nout = abi
-    print(f"d1 backward {name} final_grads={final_grads} t={t}", flush=True)
-    n, chunk = 37, 16
-    cpu, dev = _case(n, t, D, seed=600 + t, device=cuda_device)
+    t = BWD_TIMES[D][ti]
+    print(f"small-D backward D={D} {name} final_grads={final_grads} t={t}", flush=True)
+    ext = _ext(D)
+    n, chunk = 37, CHUNK[D]
+    cpu, dev = _case(n, t, D, seed=600 + 11 * D + t, device=cuda_device)
     ref = _fixed_dynamics(cpu) if fixed else cpu
     _, _, _, bm, bc = _forward(ext, dev, fixed, chunk)
     gmf = dev["gmf"] if final_grads else None
@@ -105,22 +115,25 @@ def test_d1_backward_matches_oracle(ext, cuda_device, abi, final_grads, t):
         close(grads[i], eg[i], names[i])
 
 
-def test_d1_backward_matches_generic_kernel(ext, cuda_device):
-    """Chunk 16 (column-per-lane kernel) against chunk 8 (generic kernel) at T = 112."""
+@pytest.mark.parametrize("D", DIMS)
+def test_small_d_backward_matches_generic_kernel(cuda_device, D):
+    """The preferred chunk (column-per-lane kernel) against chunk 4 (generic kernel) at T = 112."""
+    ext = _ext(D)
     n, t = 29, 112
     _, dev = _case(n, t, D, seed=91, device=cuda_device)
     out = {}
-    for chunk in (16, 8):
+    for chunk in (CHUNK[D], 4):
         _, _, _, bm, bc = _forward(ext, dev, False, chunk)
         out[chunk] = ext.backward_chunked(dev["k"], dev["v"], dev["q"], dev["d"], dev["p"], dev["r"], dev["m0"],
                                           dev["c0"], bm, bc, dev["gy"], dev["gmf"], dev["gcf"], chunk, 1e-6)
     torch.cuda.synchronize()
-    for name, a, b in zip(["gk", "gv", "gq", "gd", "gp", "gr", "gm0", "gc0"], out[16], out[8]):
+    for name, a, b in zip(["gk", "gv", "gq", "gd", "gp", "gr", "gm0", "gc0"], out[CHUNK[D]], out[4]):
         close(a, b, name)
 
 
-def test_d1_autograd_config2_shape(cuda_device):
-    """The autograd boundary at T = 512 (preferred checkpoint 16 for D = 1) against the oracle on a subset."""
+@pytest.mark.parametrize("D", DIMS)
+def test_small_d_autograd_config_shape(cuda_device, D):
+    """The autograd boundary at T = 512 (the preferred checkpoint chunk) against the oracle on a subset."""
     from bayes_ssm.fused_cuda import fused_diagonal_bayesian
 
     n, t = 300, 512
