@@ -151,3 +151,54 @@ def test_small_d_autograd_config_shape(cuda_device, D):
     close(y[idx.to(cuda_device)], ey, "y")
     for i, name in enumerate(("k", "v", "q", "d", "p", "r")):
         close(leaves[i].grad[idx.to(cuda_device)], eg[i], "grad " + name)
+
+
+@pytest.mark.parametrize("D", DIMS)
+def test_small_d_unaligned_streams_take_generic_kernels(cuda_device, D):
+    """Streams that start off a 16-byte boundary fail the column-per-lane kernels' preconditions: same results."""
+    ext = _ext(D)
+    n, t, chunk = 9, 64, CHUNK[D]
+    cpu, dev = _case(n, t, D, seed=300 + D, device=cuda_device)
+    shifted = {}
+    for name, x in dev.items():
+        flat = torch.empty(x.numel() + 1, device=cuda_device)
+        view = flat[1:].view(x.shape)  # contiguous, 4 bytes past an aligned start
+        view.copy_(x)
+        shifted[name] = view
+    assert shifted["k"].data_ptr() % 16 != 0
+    outs = {}
+    for label, src in (("aligned", dev), ("shifted", shifted)):
+        y, mT, cT, bm, bc = _forward(ext, src, False, chunk)
+        grads = ext.backward_chunked(src["k"], src["v"], src["q"], src["d"], src["p"], src["r"], src["m0"],
+                                     src["c0"], bm, bc, src["gy"], src["gmf"], src["gcf"], chunk, 1e-6)
+        outs[label] = [y, mT, cT, bm, bc, *grads]
+    torch.cuda.synchronize()
+    names = ["y", "mean_T", "cov_T", "bmean", "bcov", "gk", "gv", "gq", "gd", "gp", "gr", "gm0", "gc0"]
+    for name, a, b in zip(names, outs["aligned"], outs["shifted"]):
+        close(a, b, name)
+
+
+@pytest.mark.parametrize("D", DIMS)
+def test_small_d_single_sequence_and_long_chunk(cuda_device, D):
+    """N = 1 (one sequence in the wave) and a forward chunk longer than T."""
+    ext = _ext(D)
+    n, t = 1, 32
+    cpu, dev = _case(n, t, D, seed=410 + D, device=cuda_device)
+    y, mT, cT, bm, bc = _forward(ext, dev, False, 64)
+    torch.cuda.synchronize()
+    ey, em, ec = _oracle_forward(cpu, False)
+    close(y, ey, "y")
+    close(mT, em, "mean_T")
+    close(cT, ec, "cov_T")
+    assert bm.shape == (1, 2, D, 8)
+    assert torch.equal(bm[:, 1].cpu(), mT.cpu()) and torch.equal(bm[:, 0].cpu(), dev["m0"].cpu())
+    chunk = CHUNK[D]
+    _, _, _, bm, bc = _forward(ext, dev, False, chunk)
+    grads = ext.backward_chunked(dev["k"], dev["v"], dev["q"], dev["d"], dev["p"], dev["r"], dev["m0"], dev["c0"],
+                                 bm, bc, dev["gy"], dev["gmf"], dev["gcf"], chunk, 1e-6)
+    torch.cuda.synchronize()
+    f64 = {k: x.double() for k, x in cpu.items()}
+    _, _, _, eg = O.diagonal_grads(f64["k"], f64["v"], f64["q"], f64["d"], f64["p"], f64["r"], f64["m0"], f64["c0"],
+                                   f64["gy"], f64["gmf"], f64["gcf"])
+    for name, a, e in zip(["gk", "gv", "gq", "gd", "gp", "gr", "gm0", "gc0"], grads, eg):
+        close(a, e, name)
