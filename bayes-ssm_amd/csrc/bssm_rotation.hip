@@ -31,6 +31,7 @@
 
 #include <cfloat>
 
+#include "bssm_rot4.h"
 #include "bssm_step.h"
 
 namespace bssm {
@@ -553,6 +554,43 @@ __global__ __launch_bounds__(kWave) void forward_kernel(RotArgs a) {
   }
 }
 
+// LDS-DMA staging of one checkpoint chunk for the backward: each
+// stream's rows of the wave's SPW sequences land unpadded, [seq][R floats],
+// in a region rounded up to whole 1 KB instructions (lanes past the last
+// sequence load nothing and fill the region's tail with zeros).
+constexpr int stage_region(int spw, int r) { return (spw * r + 255) / 256 * 256; }
+
+// Rows of R floats per sequence from global rows `row` bytes apart, starting
+// `base` bytes into each row; W > 0: a token stream of W floats per token
+// (pieces whose first token is at or past T are skipped), W = 0: records.
+template <int SPW, int R, int W>
+__device__ __forceinline__ void dma_rows(r4::Rsrc rs, float* dst, uint32_t row, uint32_t base, uint32_t ts,
+                                         uint32_t T, int lane) {
+  constexpr int NI = (SPW * R + 255) / 256;
+  constexpr bool kNt = R * 4 >= 128;  // nontemporal where a row piece covers whole 128-byte lines
+#pragma unroll
+  for (int i = 0; i < NI; ++i) {
+    const uint32_t f = 256u * i + 4u * lane;
+    const uint32_t sq = f / R, o = f % R;
+    const bool ok = sq < static_cast<uint32_t>(SPW) && (W == 0 || ts + o / (W > 0 ? W : 1) < T);
+    r4::dma16<kNt>(rs, dst + 256 * i, ok ? sq * row + base + 4u * o : r4::kOob);
+  }
+}
+
+// Unpadded staged rows into the padded tile layout the kernels read.
+template <int SPW, int W, int SUB>
+__device__ __forceinline__ void copy_rows(const float* src, float* dst, int lane) {
+  constexpr int R = SUB * W, TOTAL = SPW * R;
+#pragma unroll
+  for (int it = 0; it < (TOTAL + 255) / 256; ++it) {
+    const int f = 256 * it + 4 * lane;
+    if (f < TOTAL) {
+      const int sq = f / R, o = f % R;
+      *reinterpret_cast<v4f*>(dst + sq * Tile<W, SUB>::STRIDE + o) = *reinterpret_cast<const v4f*>(src + f);
+    }
+  }
+}
+
 template <int D, int M, int G, int SUB>
 __global__ __launch_bounds__(kWave) void backward_kernel(RotArgs a) {
   using L = Layout<D, M, G>;
@@ -568,6 +606,12 @@ __global__ __launch_bounds__(kWave) void backward_kernel(RotArgs a) {
   __shared__ float sang[SPW * SJ];
   __shared__ float sp[SPW * SJ];
   __shared__ float sr[SPW * S1];
+  // LDS-DMA staging of the next chunk (see dma_rows).
+  constexpr int RK = stage_region(SPW, SUB * D), RV = stage_region(SPW, SUB * M), RJ = stage_region(SPW, SUB * J),
+                R1 = stage_region(SPW, SUB), RBM = stage_region(SPW, D * M), RBC = stage_region(SPW, D * D);
+  constexpr int OK = 0, OQ = RK, OV = 2 * RK, OG = OV + RV, ORAD = OG + RV, OANG = ORAD + RJ, OP = OANG + RJ,
+                OR = OP + RJ, OBM = OR + R1, OBC = OBM + RBM, STG = OBC + RBC;
+  __shared__ float stg[STG];
 
   const int lane = threadIdx.x;
   const int g = lane % G;
@@ -623,41 +667,164 @@ __global__ __launch_bounds__(kWave) void backward_kernel(RotArgs a) {
     }
   };
 
-  // Hot path (aligned streams, one replay piece per checkpoint chunk): the
-  // inputs and checkpoint belief of chunk c - 1 are loaded into registers
-  // while chunk c is replayed and reversed.  Used for D = 8 only: at D = 2
-  // and 4 the staging registers push the kernel into register spills, and
-  // it measured slower than staging each chunk synchronously (D = 4 at
-  // config 3's shape: 1.35 ms -> 1.75 ms; D = 8: 4.4 ms -> 3.8 ms).
-  const bool hot = D == 8 && a.vec && a.chunk == SUB;
-  TileRegs<D, SUB, SPW> rk, rq;
-  TileRegs<M, SUB, SPW> rv, rg;
-  TileRegs<J, SUB, SPW> rrad, rang, rp;
-  TileRegs<1, SUB, SPW> rr;
-  Belief<D, M, G> next_bel;
-  auto issue = [&](int64_t c) {
-    const int64_t ts = c * SUB;
-    const int len = tile_len(T, ts, SUB);
-    rk.load(a.k, n0, a.n, T, ts, len, lane);
-    rq.load(a.q, n0, a.n, T, ts, len, lane);
-    rv.load(a.v, n0, a.n, T, ts, len, lane);
-    rg.load(a.gy, n0, a.n, T, ts, len, lane);
-    rrad.load(a.rad, n0, a.n, T, ts, len, lane);
-    rang.load(a.ang, n0, a.n, T, ts, len, lane);
-    rp.load(a.p, n0, a.n, T, ts, len, lane);
-    rr.load(a.r, n0, a.n, T, ts, len, lane);
-    load_belief<D, M, G>(next_bel, a.bm + na * bm_seq + c * D * M, a.bc + na * bc_seq + c * D * D, g, active);
+  // Replay one piece (tokens [ts, ts + len) staged in the tiles) from belief
+  // b with the history in registers, then reverse it; the gradients
+  // overwrite the input tiles.
+  auto run_piece = [&](Belief<D, M, G>& b, int64_t ts, int len) __attribute__((always_inline)) {
+    RotHist<D, M, G> hist[SUB];
+#pragma unroll
+    for (int tt = 0; tt < SUB; ++tt) {
+      if (tt < len) {
+        TokRot<D, M, G> in;
+        read_rot<D, M, G>(in, st, tt, g, true);
+#pragma unroll
+        for (int jj = 0; jj < RPL; ++jj)
+#pragma unroll
+          for (int j = 0; j < D; ++j) hist[tt].Pp[jj][j] = b.P[jj][j];
+#pragma unroll
+        for (int i = 0; i < D; ++i)
+#pragma unroll
+          for (int cc = 0; cc < CPL; ++cc) hist[tt].Mp[i][cc] = b.Mv[i][cc];
+        StepOut<D, M, G> o;
+        float Pb[RPL][D];
+        step_rot<D, M, G>(b, in, a.floor, g, lane, o, Pb);
+#pragma unroll
+        for (int j = 0; j < D; ++j) hist[tt].u[j] = o.u[j];
+#pragma unroll
+        for (int jj = 0; jj < RPL; ++jj) hist[tt].u_own[jj] = o.u_own[jj];
+        hist[tt].s = o.s;
+#pragma unroll
+        for (int cc = 0; cc < CPL; ++cc) hist[tt].e[cc] = o.e[cc];
+      }
+    }
+#pragma unroll
+    for (int tt = SUB - 1; tt >= 0; --tt) {
+      if (tt < len) {
+        TokRot<D, M, G> in;
+        read_rot<D, M, G>(in, st, tt, g, false);
+        float q[D], gy[CPL];
+#pragma unroll
+        for (int j = 0; j < D; ++j) q[j] = gqs[tt * D + j];
+#pragma unroll
+        for (int cc = 0; cc < CPL; ++cc) gy[cc] = gys[tt * M + g * CPL + cc];
+        RotOut<D, M, G> o;
+        reverse_rot<D, M, G>(in, hist[tt], q, gy, gM, Gs, a.floor, g, lane, ts + tt == 0, gc0r, o);
+        // Every lane has read its token inputs (the reads above and the
+        // pair values inside) before any gradient overwrites them.
+        __builtin_amdgcn_wave_barrier();
+        if (writer) {
+#pragma unroll
+          for (int jj = 0; jj < RPL; ++jj) {
+            const int rr = L::row(g, jj);
+            gks[tt * D + rr] = o.gk_own[jj];
+            gqs[tt * D + rr] = o.gq_own[jj];
+          }
+        }
+#pragma unroll
+        for (int cc = 0; cc < CPL; ++cc) gvs[tt * M + g * CPL + cc] = o.gv[cc];
+        if (g == 0) {
+#pragma unroll
+          for (int m = 0; m < J; ++m) {
+            grads[tt * J + m] = o.grad_rad[m];
+            gangs[tt * J + m] = o.grad_ang[m];
+            gps[tt * J + m] = o.gp[m];
+          }
+          grs[tt] = o.gr;
+        }
+      }
+    }
   };
-  if (hot && a.nb > 0) issue(a.nb - 1);
+  auto store_piece = [&](int64_t ts, int len) __attribute__((always_inline)) {
+    const bool vec = a.vec && (ts % 4 == 0);
+    stage_out<D, SUB, SPW>(sk, a.gk, n0, a.n, T, ts, len, vec, lane);
+    stage_out<D, SUB, SPW>(sq, a.gq, n0, a.n, T, ts, len, vec, lane);
+    stage_out<M, SUB, SPW>(sv, a.gv, n0, a.n, T, ts, len, vec, lane);
+    stage_out<J, SUB, SPW>(srad, a.grad, n0, a.n, T, ts, len, vec, lane);
+    stage_out<J, SUB, SPW>(sang, a.gang, n0, a.n, T, ts, len, vec, lane);
+    stage_out<J, SUB, SPW>(sp, a.gp, n0, a.n, T, ts, len, vec, lane);
+    stage_out<1, SUB, SPW>(sr, a.gr, n0, a.n, T, ts, len, vec, lane);
+  };
 
-  for (int64_t c = a.nb - 1; c >= 0; --c) {
+  // Hot path (aligned streams, one replay piece per checkpoint chunk): the
+  // next chunk (inputs and checkpoint records) lands in the staging area by
+  // LDS-DMA while this one is computed; at a chunk's start the previous
+  // chunk's gradients leave the tiles, then the staged rows are copied into
+  // them.  Staging each chunk synchronously instead left the backward
+  // waiting on memory for about a third of its time.
+  const bool dma = a.vec && a.chunk == SUB && a.nb > 0 && T * 4 * M * SPW < (int64_t(1) << 31) &&
+                   (a.nb + 1) * 4 * D * M * SPW < (int64_t(1) << 31);
+  if (dma) {
+    const uint32_t Tu = static_cast<uint32_t>(T);
+    const uint32_t valid = static_cast<uint32_t>((a.n - n0) < SPW ? (a.n - n0) : SPW);
+    const uint32_t nbp = static_cast<uint32_t>(a.nb + 1);
+    const r4::Rsrc xk = r4::make_rsrc(a.k + n0 * T * D, valid * Tu * D * 4u);
+    const r4::Rsrc xq = r4::make_rsrc(a.q + n0 * T * D, valid * Tu * D * 4u);
+    const r4::Rsrc xv = r4::make_rsrc(a.v + n0 * T * M, valid * Tu * M * 4u);
+    const r4::Rsrc xg = r4::make_rsrc(a.gy + n0 * T * M, valid * Tu * M * 4u);
+    const r4::Rsrc xrad = r4::make_rsrc(a.rad + n0 * T * J, valid * Tu * J * 4u);
+    const r4::Rsrc xang = r4::make_rsrc(a.ang + n0 * T * J, valid * Tu * J * 4u);
+    const r4::Rsrc xp = r4::make_rsrc(a.p + n0 * T * J, valid * Tu * J * 4u);
+    const r4::Rsrc xr = r4::make_rsrc(a.r + n0 * T, valid * Tu * 4u);
+    const r4::Rsrc xbm = r4::make_rsrc(a.bm + n0 * nbp * D * M, valid * nbp * D * M * 4u);
+    const r4::Rsrc xbc = r4::make_rsrc(a.bc + n0 * nbp * D * D, valid * nbp * D * D * 4u);
+    auto issue_dma = [&](int64_t c) {
+      const uint32_t ts = static_cast<uint32_t>(c) * SUB, cu = static_cast<uint32_t>(c);
+      dma_rows<SPW, SUB * D, D>(xk, stg + OK, Tu * D * 4u, ts * D * 4u, ts, Tu, lane);
+      dma_rows<SPW, SUB * D, D>(xq, stg + OQ, Tu * D * 4u, ts * D * 4u, ts, Tu, lane);
+      dma_rows<SPW, SUB * M, M>(xv, stg + OV, Tu * M * 4u, ts * M * 4u, ts, Tu, lane);
+      dma_rows<SPW, SUB * M, M>(xg, stg + OG, Tu * M * 4u, ts * M * 4u, ts, Tu, lane);
+      dma_rows<SPW, SUB * J, J>(xrad, stg + ORAD, Tu * J * 4u, ts * J * 4u, ts, Tu, lane);
+      dma_rows<SPW, SUB * J, J>(xang, stg + OANG, Tu * J * 4u, ts * J * 4u, ts, Tu, lane);
+      dma_rows<SPW, SUB * J, J>(xp, stg + OP, Tu * J * 4u, ts * J * 4u, ts, Tu, lane);
+      dma_rows<SPW, SUB, 1>(xr, stg + OR, Tu * 4u, ts * 4u, ts, Tu, lane);
+      dma_rows<SPW, D * M, 0>(xbm, stg + OBM, nbp * D * M * 4u, cu * D * M * 4u, 0, Tu, lane);
+      dma_rows<SPW, D * D, 0>(xbc, stg + OBC, nbp * D * D * 4u, cu * D * D * 4u, 0, Tu, lane);
+    };
+    issue_dma(a.nb - 1);
+    for (int64_t c = a.nb - 1; c >= 0; --c) {
+      const int64_t ts = c * SUB;
+      const int len = tile_len(T, ts, SUB);
+      // Every outstanding memory operation was issued a whole chunk earlier.
+      r4::vm_wait<0>();
+      __syncthreads();
+      if (c + 1 < a.nb) store_piece(ts + SUB, tile_len(T, ts + SUB, SUB));
+      __syncthreads();
+      copy_rows<SPW, D, SUB>(stg + OK, sk, lane);
+      copy_rows<SPW, D, SUB>(stg + OQ, sq, lane);
+      copy_rows<SPW, M, SUB>(stg + OV, sv, lane);
+      copy_rows<SPW, M, SUB>(stg + OG, sg, lane);
+      copy_rows<SPW, J, SUB>(stg + ORAD, srad, lane);
+      copy_rows<SPW, J, SUB>(stg + OANG, sang, lane);
+      copy_rows<SPW, J, SUB>(stg + OP, sp, lane);
+      copy_rows<SPW, 1, SUB>(stg + OR, sr, lane);
+      Belief<D, M, G> b;
+#pragma unroll
+      for (int i = 0; i < D; ++i)
+#pragma unroll
+        for (int cc = 0; cc < CPL; ++cc) b.Mv[i][cc] = active ? stg[OBM + s * D * M + i * M + g * CPL + cc] : 0.f;
+#pragma unroll
+      for (int jj = 0; jj < RPL; ++jj)
+#pragma unroll
+        for (int j = 0; j < D; ++j)
+          b.P[jj][j] = active ? stg[OBC + s * D * D + L::row(g, jj) * D + j] : (L::row(g, jj) == j ? 1.f : 0.f);
+      __syncthreads();
+      // The staging reads are complete before the next chunk's DMA lands.
+      r4::lds_wait();
+      if (c > 0) issue_dma(c - 1);
+      run_piece(b, ts, len);
+    }
+    __syncthreads();
+    store_piece(0, tile_len(T, 0, SUB));
+  }
+
+
+  for (int64_t c = dma ? -1 : a.nb - 1; c >= 0; --c) {
     const int64_t tc0 = c * a.chunk;
     const int64_t lc = (T - tc0) < a.chunk ? (T - tc0) : a.chunk;
     const int nsub = static_cast<int>((lc + SUB - 1) / SUB);
     for (int sc = nsub - 1; sc >= 0; --sc) {
       Belief<D, M, G> b;
-      if (hot) b = next_bel;
-      else load_belief<D, M, G>(b, a.bm + na * bm_seq + c * D * M, a.bc + na * bc_seq + c * D * D, g, active);
+      load_belief<D, M, G>(b, a.bm + na * bm_seq + c * D * M, a.bc + na * bc_seq + c * D * D, g, active);
       // Advance from the checkpoint to the piece.
       for (int j = 0; j < sc; ++j) {
         stage_piece(tc0 + static_cast<int64_t>(j) * SUB, SUB, false);
@@ -674,91 +841,11 @@ __global__ __launch_bounds__(kWave) void backward_kernel(RotArgs a) {
       }
       const int64_t ts = tc0 + static_cast<int64_t>(sc) * SUB;
       const int len = static_cast<int>((lc - sc * SUB) < SUB ? (lc - sc * SUB) : SUB);
-      if (hot) {
-        rk.commit(sk, lane);
-        rq.commit(sq, lane);
-        rv.commit(sv, lane);
-        rg.commit(sg, lane);
-        rrad.commit(srad, lane);
-        rang.commit(sang, lane);
-        rp.commit(sp, lane);
-        rr.commit(sr, lane);
-      } else {
-        stage_piece(ts, len, true);
-      }
+      stage_piece(ts, len, true);
       __syncthreads();
-      if (hot && c > 0) issue(c - 1);
-      RotHist<D, M, G> hist[SUB];
-#pragma unroll
-      for (int tt = 0; tt < SUB; ++tt) {
-        if (tt < len) {
-          TokRot<D, M, G> in;
-          read_rot<D, M, G>(in, st, tt, g, true);
-#pragma unroll
-          for (int jj = 0; jj < RPL; ++jj)
-#pragma unroll
-            for (int j = 0; j < D; ++j) hist[tt].Pp[jj][j] = b.P[jj][j];
-#pragma unroll
-          for (int i = 0; i < D; ++i)
-#pragma unroll
-            for (int cc = 0; cc < CPL; ++cc) hist[tt].Mp[i][cc] = b.Mv[i][cc];
-          StepOut<D, M, G> o;
-          float Pb[RPL][D];
-          step_rot<D, M, G>(b, in, a.floor, g, lane, o, Pb);
-#pragma unroll
-          for (int j = 0; j < D; ++j) hist[tt].u[j] = o.u[j];
-#pragma unroll
-          for (int jj = 0; jj < RPL; ++jj) hist[tt].u_own[jj] = o.u_own[jj];
-          hist[tt].s = o.s;
-#pragma unroll
-          for (int cc = 0; cc < CPL; ++cc) hist[tt].e[cc] = o.e[cc];
-        }
-      }
-#pragma unroll
-      for (int tt = SUB - 1; tt >= 0; --tt) {
-        if (tt < len) {
-          TokRot<D, M, G> in;
-          read_rot<D, M, G>(in, st, tt, g, false);
-          float q[D], gy[CPL];
-#pragma unroll
-          for (int j = 0; j < D; ++j) q[j] = gqs[tt * D + j];
-#pragma unroll
-          for (int cc = 0; cc < CPL; ++cc) gy[cc] = gys[tt * M + g * CPL + cc];
-          RotOut<D, M, G> o;
-          reverse_rot<D, M, G>(in, hist[tt], q, gy, gM, Gs, a.floor, g, lane, ts + tt == 0, gc0r, o);
-          // Every lane has read its token inputs (the reads above and the
-          // pair values inside) before any gradient overwrites them.
-          __builtin_amdgcn_wave_barrier();
-          if (writer) {
-#pragma unroll
-            for (int jj = 0; jj < RPL; ++jj) {
-              const int rr = L::row(g, jj);
-              gks[tt * D + rr] = o.gk_own[jj];
-              gqs[tt * D + rr] = o.gq_own[jj];
-            }
-          }
-#pragma unroll
-          for (int cc = 0; cc < CPL; ++cc) gvs[tt * M + g * CPL + cc] = o.gv[cc];
-          if (g == 0) {
-#pragma unroll
-            for (int m = 0; m < J; ++m) {
-              grads[tt * J + m] = o.grad_rad[m];
-              gangs[tt * J + m] = o.grad_ang[m];
-              gps[tt * J + m] = o.gp[m];
-            }
-            grs[tt] = o.gr;
-          }
-        }
-      }
+      run_piece(b, ts, len);
       __syncthreads();
-      const bool vec = a.vec && (ts % 4 == 0);
-      stage_out<D, SUB, SPW>(sk, a.gk, n0, a.n, T, ts, len, vec, lane);
-      stage_out<D, SUB, SPW>(sq, a.gq, n0, a.n, T, ts, len, vec, lane);
-      stage_out<M, SUB, SPW>(sv, a.gv, n0, a.n, T, ts, len, vec, lane);
-      stage_out<J, SUB, SPW>(srad, a.grad, n0, a.n, T, ts, len, vec, lane);
-      stage_out<J, SUB, SPW>(sang, a.gang, n0, a.n, T, ts, len, vec, lane);
-      stage_out<J, SUB, SPW>(sp, a.gp, n0, a.n, T, ts, len, vec, lane);
-      stage_out<1, SUB, SPW>(sr, a.gr, n0, a.n, T, ts, len, vec, lane);
+      store_piece(ts, len);
       __syncthreads();
     }
   }
