@@ -1,9 +1,9 @@
 """GPU parity of the D = 1 and D = 2 (M = 8) column-per-lane kernels (bssm_d1.hip, bssm_d2.hip).
 
-The D = 1 forward takes calls whose streams are 16-byte aligned with T and
-the checkpoint chunk multiples of 4 (the D = 2 forward is the generic
-kernel); the backwards take the library's preferred checkpoint chunk (16 for
-D = 1, 8 for D = 2), and for D = 1 also T a multiple of 16.  The shapes
+The forwards take calls whose streams are 16-byte aligned with T a multiple
+of 4 (and, for D = 1, the checkpoint chunk too); the backwards take the
+library's preferred checkpoint chunk (16 for D = 1, 8 for D = 2), and for
+D = 1 also T a multiple of 16.  The shapes
 below are chosen to reach them, with N = 37 leaving idle sequence slots in
 the last wave and T values that end on partial forward blocks and on partly
 filled backward blocks.  Other shapes take the generic kernels, which serve
