@@ -15,9 +15,12 @@
 // replay needs no cross-lane traffic and the reverse's sums over value
 // columns are 4-lane DPP all-reduces.
 //
-// Inputs arrive by LDS-DMA in blocks of 8 tokens (one checkpoint chunk), one
-// block ahead.  LDS layouts of a block (floats):
-//   k, d, q (two per token): piece-major [4 pieces][16 seq][2 tokens x 2];
+// The backward's inputs arrive by LDS-DMA one block ahead, in blocks of 8
+// tokens (one checkpoint chunk); k, d and q come per pair of blocks (16
+// tokens, whole 128-byte rows per sequence: 8-token pieces are half lines,
+// and their lines were fetched once per half).  LDS layouts (floats):
+//   k, d, q (two per token): piece-major [8 pieces][16 seq][2 tokens x 2]
+//     per pair, in two pair buffers;
 //   p, r: piece-major [2 pieces][16 seq][4 tokens] (the DMA instruction's
 //     upper 32 lanes are idle and fill the padding after it with zeros);
 //   v, gy: token-major [8][16 seq][8 col], so lane l reads floats
@@ -52,8 +55,14 @@ constexpr int kNtSt = r4::kNtStore;
 
 // Float offsets inside one block slot.
 struct Slot {
-  static constexpr int K = 0, D = 256, Q = 512, P = 768, R = 1024, V = 1280, GY = 2304, CKM = 3328, CKC = 3584;
-  static constexpr int BWD = 3840;
+  static constexpr int P = 0, R = 256, V = 512, GY = 1536, CKM = 2560, CKC = 2816;
+  static constexpr int BWD = 3072;
+};
+// k, d, q of a pair of blocks (16 tokens: whole 128-byte rows per sequence),
+// piece-major [8 pieces][16 seq][2 tokens x 2] per stream; block 2m + h of
+// pair m reads pieces 4h .. 4h + 3.
+struct KQ {
+  static constexpr int K = 0, D = 512, Q = 1024, SIZE = 1536;
 };
 
 __device__ __forceinline__ v4f lds4(const float* p) { return *reinterpret_cast<const v4f*>(p); }
@@ -64,20 +73,13 @@ __device__ __forceinline__ void lds2_store(float* p, v2f x) { *reinterpret_cast<
 // Per-lane DMA / store offsets (bytes, relative to the wave's stream base)
 // of a block starting at token t0.
 struct Map {
-  uint32_t k_base, k_piece;  // k/d/q: sequence j & 15, piece j >> 4 (2 tokens)
   uint32_t s_base, s_piece;  // p/r: sequence j & 15, piece j >> 4 (4 tokens), lanes < 32
   uint32_t v_base, v_tok;    // v/gy: token 2 i + (j >> 5), sequence (j >> 1) & 15, half j & 1
   __device__ __forceinline__ Map(int lane, uint32_t row1, uint32_t row2, uint32_t row8)
-      : k_base(static_cast<uint32_t>(lane & 15) * row2),
-        k_piece(static_cast<uint32_t>(lane >> 4)),
-        s_base(static_cast<uint32_t>(lane & 15) * row1),
+      : s_base(static_cast<uint32_t>(lane & 15) * row1),
         s_piece(static_cast<uint32_t>(lane >> 4)),
         v_base(static_cast<uint32_t>((lane >> 1) & 15) * row8 + static_cast<uint32_t>(lane & 1) * 16u),
         v_tok(static_cast<uint32_t>(lane >> 5)) {}
-  __device__ __forceinline__ uint32_t k(uint32_t t0, uint32_t T) const {
-    const uint32_t t = t0 + 2u * k_piece;
-    return t < T ? k_base + 8u * t : kOob;
-  }
   __device__ __forceinline__ uint32_t s(uint32_t t0, uint32_t T) const {
     const uint32_t t = t0 + 4u * s_piece;
     return (s_piece < 2u && t < T) ? s_base + 4u * t : kOob;
@@ -115,17 +117,18 @@ struct Piece {
   }
 };
 
-// Piece pc (tokens 4 pc .. 4 pc + 3 of the block) of slot sl.
+// Piece pc (tokens 4 pc .. 4 pc + 3 of the block) of slot sl, with the
+// block's k, d, q at kq (its half of the pair area).
 template <bool FIXED>
-__device__ __forceinline__ void read_piece(const float* sl, int pc, int seq, int lane, bool need_v, bool need_q,
-                                           Piece& x) {
+__device__ __forceinline__ void read_piece(const float* sl, const float* kq, int pc, int seq, int lane,
+                                           bool need_v, bool need_q, Piece& x) {
 #pragma unroll
   for (int h = 0; h < 2; ++h) {
     const int o = 64 * (2 * pc + h) + 4 * seq;
-    x.k[h] = lds4(sl + Slot::K + o);
+    x.k[h] = lds4(kq + KQ::K + o);
     if constexpr (FIXED) x.d[h] = v4f{kFixedDecay, kFixedDecay, kFixedDecay, kFixedDecay};
-    else x.d[h] = lds4(sl + Slot::D + o);
-    if (need_q) x.q[h] = lds4(sl + Slot::Q + o);
+    else x.d[h] = lds4(kq + KQ::D + o);
+    if (need_q) x.q[h] = lds4(kq + KQ::Q + o);
   }
   if constexpr (FIXED) {
     x.p = v4f{kFixedProcess, kFixedProcess, kFixedProcess, kFixedProcess};
@@ -436,6 +439,7 @@ __device__ __forceinline__ void reverse(const Hist& h, const Tok& x, float floor
 template <bool FIXED, bool DYN>
 __global__ __launch_bounds__(kWave) void backward_kernel(BwdArgs a) {
   __shared__ float tile[2 * Slot::BWD];
+  __shared__ float kdq[2 * KQ::SIZE];
   const int lane = threadIdx.x;
   const int seq = lane >> 2, g = lane & 3;
   const int64_t n0 = static_cast<int64_t>(blockIdx.x) * SPW;
@@ -486,13 +490,36 @@ __global__ __launch_bounds__(kWave) void backward_kernel(BwdArgs a) {
   float gc0[4] = {0.f, 0.f, 0.f, 0.f};
 
   const uint32_t nblk = (T + BT - 1) / BT;
+  // k, d, q of pair m: instruction i, lane j covers piece 4 i + (j >> 4)
+  // (2 tokens) of sequence j & 15, so each sequence's 128-byte row is
+  // requested by the two instructions back to back.
+  auto kq_off = [&](int i, uint32_t m) __attribute__((always_inline)) {
+    const uint32_t t = 16u * m + 2u * (4u * i + static_cast<uint32_t>(lane >> 4));
+    return t < T ? static_cast<uint32_t>(lane & 15) * row2 + 8u * t : kOob;
+  };
+  auto issue_kq = [&](float* kb, uint32_t m) __attribute__((always_inline)) {
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const uint32_t off = kq_off(i, m);
+      dma16<kNt>(rk, kb + KQ::K + 256 * i, off);
+      dma16<kNt>(rq, kb + KQ::Q + 256 * i, off);
+      if constexpr (!FIXED) dma16<kNt>(rd, kb + KQ::D + 256 * i, off);
+    }
+  };
+  auto store_kq = [&](const float* kb, uint32_t m) __attribute__((always_inline)) {
+    const v4f zero = v4f{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const uint32_t off = kq_off(i, m);
+      const int e = 256 * i + 4 * lane;
+      st128<kNtSt>(rgk, lds4(kb + KQ::K + e), off, 0);
+      st128<kNtSt>(rgq, lds4(kb + KQ::Q + e), off, 0);
+      st128<kNtSt>(rgd, DYN ? lds4(kb + KQ::D + e) : zero, off, 0);
+    }
+  };
   auto issue = [&](float* sl, uint32_t blk) __attribute__((always_inline)) {
     const uint32_t t0 = blk * BT;
-    const uint32_t ok = mp.k(t0, T);
-    dma16<kNt>(rk, sl + Slot::K, ok);
-    dma16<kNt>(rq, sl + Slot::Q, ok);
     if constexpr (!FIXED) {
-      dma16<kNt>(rd, sl + Slot::D, ok);
       const uint32_t os = mp.s(t0, T);
       dma16(rp, sl + Slot::P, os);
       dma16(rr, sl + Slot::R, os);
@@ -510,11 +537,7 @@ __global__ __launch_bounds__(kWave) void backward_kernel(BwdArgs a) {
   auto store_grads = [&](const float* sl, uint32_t blk) __attribute__((always_inline)) {
     const uint32_t t0 = blk * BT;
     const int e = 4 * lane;
-    const uint32_t ok = mp.k(t0, T);
     const v4f zero = v4f{0.f, 0.f, 0.f, 0.f};
-    st128<kNtSt>(rgk, lds4(sl + Slot::K + e), ok, 0);
-    st128<kNtSt>(rgq, lds4(sl + Slot::Q + e), ok, 0);
-    st128<kNtSt>(rgd, DYN ? lds4(sl + Slot::D + e) : zero, ok, 0);
     const uint32_t os = mp.s(t0, T);
     st128(rgp, DYN ? lds4(sl + Slot::P + e) : zero, os, 0);
     st128(rgr, DYN ? lds4(sl + Slot::R + e) : zero, os, 0);
@@ -524,7 +547,7 @@ __global__ __launch_bounds__(kWave) void backward_kernel(BwdArgs a) {
 
   // Replay the block's chunk from its checkpoint record, then reverse it;
   // the gradients overwrite the block's inputs.
-  auto run_chunk = [&](float* sl, int npc, bool first_chunk) __attribute__((always_inline)) {
+  auto run_chunk = [&](float* sl, float* kq, int npc, bool first_chunk) __attribute__((always_inline)) {
     Bel b;
     {
       const v2f m0 = lds2(sl + Slot::CKM + 16 * seq + 2 * g), m1 = lds2(sl + Slot::CKM + 16 * seq + 8 + 2 * g);
@@ -540,7 +563,7 @@ __global__ __launch_bounds__(kWave) void backward_kernel(BwdArgs a) {
     v2f gy[2][4];
 #pragma unroll
     for (int pc = 0; pc < 2; ++pc) {
-      read_piece<FIXED>(sl, pc, seq, lane, true, true, x[pc]);
+      read_piece<FIXED>(sl, kq, pc, seq, lane, true, true, x[pc]);
 #pragma unroll
       for (int j = 0; j < 4; ++j) gy[pc][j] = lds2(sl + Slot::GY + 128 * (4 * pc + j) + 2 * lane);
     }
@@ -576,9 +599,9 @@ __global__ __launch_bounds__(kWave) void backward_kernel(BwdArgs a) {
 #pragma unroll
           for (int hh = 0; hh < 2; ++hh) {
             const int o = 64 * (2 * pc + hh) + 4 * seq;
-            lds4_store(sl + Slot::K + o, gk[hh]);
-            lds4_store(sl + Slot::Q + o, gq[hh]);
-            if constexpr (DYN) lds4_store(sl + Slot::D + o, gd[hh]);
+            lds4_store(kq + KQ::K + o, gk[hh]);
+            lds4_store(kq + KQ::Q + o, gq[hh]);
+            if constexpr (DYN) lds4_store(kq + KQ::D + o, gd[hh]);
           }
           if constexpr (DYN) {
             lds4_store(sl + Slot::P + 64 * pc + 4 * seq, gp);
@@ -590,22 +613,35 @@ __global__ __launch_bounds__(kWave) void backward_kernel(BwdArgs a) {
   };
 
   // Block b is processed in slot b % 2.  At its start every outstanding
-  // memory operation was issued a whole block earlier; then the gradients of
-  // block b + 1 leave the other slot, which receives block b - 1.
-  if (nblk > 0) issue(tile + ((nblk - 1) & 1) * Slot::BWD, nblk - 1);
+  // memory operation was issued at least a whole block earlier; then the
+  // gradients of block b + 1 leave the other slot, which receives block
+  // b - 1.  The k, d, q of pair m (blocks 2m, 2m + 1) live in pair buffer
+  // m % 2: at the first block of pair m processed, the gradients of pair
+  // m + 1 leave the other buffer, which receives pair m - 1.
+  const uint32_t npair = (nblk + 1) / 2;
+  auto kbuf = [&](uint32_t m) __attribute__((always_inline)) { return kdq + (m & 1) * KQ::SIZE; };
+  if (nblk > 0) {
+    issue(tile + ((nblk - 1) & 1) * Slot::BWD, nblk - 1);
+    issue_kq(kbuf(npair - 1), npair - 1);
+  }
   for (uint32_t i = 0; i < nblk; ++i) {
-    const uint32_t blk = nblk - 1 - i;
+    const uint32_t blk = nblk - 1 - i, m = blk >> 1;
     float* cur = tile + (blk & 1) * Slot::BWD;
     float* other = tile + ((blk + 1) & 1) * Slot::BWD;
     vm_wait<0>();
     __syncthreads();
     if (blk + 1 < nblk) store_grads(other, blk + 1);
+    if (blk == nblk - 1 || (blk & 1) == 1) {  // first block of pair m
+      if (m + 1 < npair) store_kq(kbuf(m + 1), m + 1);
+      if (m > 0) issue_kq(kbuf(m + 1), m - 1);
+    }
     if (blk > 0) issue(other, blk - 1);
-    run_chunk(cur, (T - blk * BT) < BT ? 1 : 2, blk == 0);
+    run_chunk(cur, kbuf(m) + 256 * (blk & 1), (T - blk * BT) < BT ? 1 : 2, blk == 0);
   }
   if (nblk > 0) {
     __syncthreads();
     store_grads(tile, 0);
+    store_kq(kbuf(0), 0);
   }
   if (a.gm0) {
     const Rsrc r = make_rsrc(a.gm0 + n0 * 16, valid * 64u);
