@@ -1,8 +1,7 @@
 // gfx950 forward and checkpoint-replay backward for D = 2, M = 8
 // (bayes_ssm/persistent_bayes_chunked_d2m8.cu is the reference extension for
 // this shape; the per-token equations are those of bssm_step.h with two key
-// dimensions), with two value columns per lane, and the matching forward.
-// The forward streams its inputs as the generic kernels do (register-staged
+// dimensions), with two value columns per lane.  The forward streams its inputs as the generic kernels do (register-staged
 // 16-token tiles, one tile ahead): a version fed by 8-token LDS-DMA blocks
 // measured slower, since this forward does little arithmetic per byte and
 // needs more bytes in flight than such blocks leave.
@@ -52,7 +51,6 @@ constexpr int kChunk = 8;   // backward checkpoint chunk, tokens
 constexpr bool kNt = r4::kNtLoad;
 constexpr int kNtSt = r4::kNtStore;
 
-
 // Float offsets inside one block slot.
 struct Slot {
   static constexpr int P = 0, R = 256, V = 512, GY = 1536, CKM = 2560, CKC = 2816;
@@ -75,7 +73,7 @@ __device__ __forceinline__ void lds2_store(float* p, v2f x) { *reinterpret_cast<
 struct Map {
   uint32_t s_base, s_piece;  // p/r: sequence j & 15, piece j >> 4 (4 tokens), lanes < 32
   uint32_t v_base, v_tok;    // v/gy: token 2 i + (j >> 5), sequence (j >> 1) & 15, half j & 1
-  __device__ __forceinline__ Map(int lane, uint32_t row1, uint32_t row2, uint32_t row8)
+  __device__ __forceinline__ Map(int lane, uint32_t row1, uint32_t row8)
       : s_base(static_cast<uint32_t>(lane & 15) * row1),
         s_piece(static_cast<uint32_t>(lane >> 4)),
         v_base(static_cast<uint32_t>((lane >> 1) & 15) * row8 + static_cast<uint32_t>(lane & 1) * 16u),
@@ -462,7 +460,7 @@ __global__ __launch_bounds__(kWave) void backward_kernel(BwdArgs a) {
   const uint32_t nbp = static_cast<uint32_t>(a.nb + 1);
   const Rsrc rbm = make_rsrc(a.bm + n0 * nbp * 16, valid * nbp * 64u);
   const Rsrc rbc = make_rsrc(a.bc + n0 * nbp * 4, valid * nbp * 16u);
-  const Map mp(lane, row1, row2, row8);
+  const Map mp(lane, row1, row8);
   // Checkpoint record DMA: mean records by (sequence j >> 2, piece j & 3),
   // covariance records by lanes j < 16.
   const uint32_t ckm_off = static_cast<uint32_t>(lane >> 2) * nbp * 64u + 16u * (lane & 3);
