@@ -358,4 +358,62 @@ def bayes_mixer_readout(
     return out, mean_t, cov_t
 
 
-__all__ = ["bayes_mixer_core", "bayes_mixer_readout", "mixer_layer_inputs"]
+def bayes_mixer_block(
+    projected: Tensor,
+    conv_weight: Tensor,
+    norm_weight: Tensor,
+    *,
+    heads: int,
+    aux_bias: Optional[Tensor] = None,
+    norm_eps: Optional[float] = None,
+    initial_mean: Optional[Tensor] = None,
+    initial_covariance: Optional[Tensor] = None,
+    chunk_length: Optional[int] = None,
+    denominator_floor: float = 1e-6,
+    optimized: bool = True,
+) -> tuple[Tensor, Tensor, Tensor]:
+    """The Bayes mixer from its fused projection to ``out_proj``'s input (train_6layer.py:583-729).
+
+    This is the paper configuration of config 4's Bayes blocks (key dim 4,
+    learned dynamics, fused Q/K/V/decay/noise/gate projection,
+    :585-600): ``projected`` [B, T, H*4 + H*4 + H*8 + H*4 + H*2 + H*8] holds,
+    per token, the Q, K and V core (``qkv_core_width``), the decay logits and
+    the interleaved (process, observation) noise logits (``aux_width``, plus
+    ``aux_bias`` when given, :589-593) and the gate (:594-597).  The core goes
+    through the causal depthwise-4 filter with ``conv_weight`` [2*H*4 + H*8,
+    1, 4] (:598, ``_causal_depthwise`` :474-480) and is split into q, k, v
+    (:599-601); the rest is ``bayes_mixer_readout``.  Returns the gated
+    readout [B, T, H*8] and the final mean and covariance.
+
+    On the GPU every stage runs on the HIP kernels: the filter reads the core
+    columns in place and writes one contiguous [B, T, 2*H*4 + H*8] tensor,
+    whose column views, with the aux and gate columns of ``projected``, feed
+    the producer-fused readout kernels.
+    """
+    if projected.ndim != 3:
+        raise ValueError("projected must have shape [B, T, width]")
+    state = heads * KEY_DIM
+    width = heads * VALUE_DIM
+    core = 2 * state + width
+    aux = state + 2 * heads
+    if projected.shape[-1] != core + aux + width:
+        raise ValueError(f"projected must have {core + aux + width} columns for {heads} heads, "
+                         f"got {projected.shape[-1]}")
+    if tuple(conv_weight.shape) != (core, 1, 4):
+        raise ValueError(f"conv_weight must have shape [{core}, 1, 4]")
+    from .conv import causal_depthwise4
+
+    qkv = projected[..., :core]
+    convolved = causal_depthwise4(qkv.transpose(1, 2), conv_weight).transpose(1, 2)
+    q_in, k_in, v_in = convolved.split((state, state, width), dim=-1)
+    aux_in = projected[..., core:core + aux]
+    if aux_bias is not None:
+        aux_in = aux_in + aux_bias
+    gate = projected[..., core + aux:]
+    return bayes_mixer_readout(q_in, k_in, v_in, aux_in[..., :state], aux_in[..., state:], gate, norm_weight,
+                               heads=heads, norm_eps=norm_eps, initial_mean=initial_mean,
+                               initial_covariance=initial_covariance, chunk_length=chunk_length,
+                               denominator_floor=denominator_floor, optimized=optimized)
+
+
+__all__ = ["bayes_mixer_block", "bayes_mixer_core", "bayes_mixer_readout", "mixer_layer_inputs"]

@@ -230,7 +230,9 @@ __device__ __forceinline__ void mix_put(const MixRaw& x, const MixMap& mm, float
       const v4f z = e ? widen_hi(x.dl[I]) : widen_lo(x.dl[I]);
       v4f d;
 #pragma unroll
-      for (int i = 0; i < 4; ++i) d[i] = sigmoid_(-z[i]);  // exp(-softplus(z))
+      // The reference's exp(-softplus(z)) as written (train_6layer.py:690-698),
+      // not the algebraically equal sigmoid(-z), which rounds differently.
+      for (int i = 0; i < 4; ++i) d[i] = exp_(-softplus_(z[i]));
       *reinterpret_cast<v4f*>(&tile[D + mm.kq_lds[I][e]]) = d;
     }
   }
@@ -588,10 +590,10 @@ __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(1, 1))) v
           const v4f gd = *reinterpret_cast<const v4f*>(&tile[BwdTile::D + (e ? o1 : o0)]);
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
-            // d/dz exp(-softplus(z)) = -d sigmoid(z), d = 1 / (1 + e^z), and
-            // sigmoid(z) = e^z d below 0, 1 - d above (no cancellation either way).
-            const float u = exp_(z[i]), d = rcp_(1.f + u);
-            out[e][i] = -gd[i] * d * (z[i] > 0.f ? 1.f - d : u * d);
+            // d/dz exp(-softplus(z)) = -exp(-softplus(z)) sigmoid(z), with the
+            // decay formed as in the forward.
+            const float d = exp_(-softplus_(z[i]));
+            out[e][i] = -gd[i] * d * sigmoid_(z[i]);
           }
         }
         gr.put8(gr.dl, t * gr.rkq + gr.ckq + mm.kq_col, out[0], out[1]);

@@ -357,7 +357,9 @@ __device__ __forceinline__ void reverse_rot(const TokRot<D, M, G>& in, const Rot
     zp = fmaf(h.u_own[jj], a_own[jj] - w, zp);
   }
   const float z = group_sum<G>(writer ? zp : 0.f);
-  const float gs = (h.s > floor) ? -z * beta * beta : 0.f;
+  // The reference runs this core in torch, where clamp_min passes the
+  // gradient at s == floor too (the diagonal kernels' gate is strict).
+  const float gs = (h.s >= floor) ? -z * beta * beta : 0.f;
   float gu_own[RPL], gu[D];
 #pragma unroll
   for (int jj = 0; jj < RPL; ++jj) gu_own[jj] = fmaf(beta, a_own[jj] - 2.f * w_own[jj], gs * in.k_own[jj]);

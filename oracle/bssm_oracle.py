@@ -22,7 +22,13 @@ float32, autograd-friendly), written from the equations:
 * ``mixer_inputs`` / ``mixer_core``  — the Bayes mixer's producer chain and readout permute
                                        (example/train_6layer.py:627-693, :709-710)
 * ``mixer_readout``                  — its gated readout: RMSNorm(bf16(read)) * silu(gate) (:719-729)
+* ``mixer_block``                    — the mixer from its fused projection to out_proj's input
+                                       (:583-729): filter, producer chain, layer, gated readout
 * ``causal_depthwise4``              — the length-four causal depthwise filter (:160-191)
+* ``floor_clamp``                    — the innovation floor: the CUDA reverse kernels' strict
+                                       ``s > floor`` gate (persistent_bayes_chunked_d4m8.cu:315),
+                                       used by run_diagonal / run_fixed / mixer_core, or
+                                       torch's clamp_min (the eager and chunked CPU paths)
 
 Pinning (tests/test_oracle.py): closed forms (scalar Kalman filter, one-step
 u = (d^2+p)k, no-update limits, Bayesian linear regression), invariants
@@ -36,9 +42,15 @@ unit-norm heads, the [B, T, H] -> [B*H, T] sequence map checked with
 head-tagged inputs) and by its reduction to ``run_diagonal``.  The readout
 epilogue is pinned against torch's own rms_norm / silu on bf16 tensors (the
 reference's ops), by unit RMS of the normalized head, and by gradcheck.  The
+mixer block is pinned against the reference's op sequence written out with
+torch's own ops (pad + shifted products, split, normalize, softplus, rms_norm,
+silu) on the same fused projection, and by gradcheck of its float64 chain.  The
 causal filter is pinned against torch's conv1d on the left-padded input (the
 reference's nn.Conv1d path, :478-480), by its impulse response and causality,
 and by gradcheck.
+The strict floor gate is pinned at a token built to have r + k.u == floor
+exactly: its dL/dr is the one-sided (left) finite difference, zero, while
+clamp_min's is the right one.
 The rotation core is pinned against run_dense with an independently built
 block-rotation transition (the reference's own check,
 tests/test_bayesian_layer_diagonal.py:12-51), by the angle = 0 reduction to
@@ -59,6 +71,33 @@ FIXED_OBSERVATION = 1.0
 
 def _sym(x: Tensor) -> Tensor:
     return 0.5 * (x + x.transpose(-1, -2))
+
+
+class _StrictFloor(torch.autograd.Function):
+    """max(s, floor) whose derivative is 1 only where s > floor (strictly).
+
+    The reference's CUDA reverse kernels gate the innovation-variance
+    adjoint with a strict comparison, ``(s > floor) ? -z beta^2 : 0``
+    (persistent_bayes_chunked_d4m8.cu:315, _d2m8.cu:318, _d1m8.cu:339, _d8.cu:381,
+    persistent_bayes_chunked.cu:324), while torch's ``clamp_min`` passes the
+    gradient at s == floor as well.  The two differ only at equality.
+    """
+
+    @staticmethod
+    def forward(ctx, s, floor):
+        ctx.save_for_backward(s)
+        ctx.floor = floor
+        return s.clamp_min(floor)
+
+    @staticmethod
+    def backward(ctx, grad):
+        (s,) = ctx.saved_tensors
+        return grad * (s > ctx.floor).to(grad.dtype), None
+
+
+def floor_clamp(s: Tensor, floor: float, strict: bool = True) -> Tensor:
+    """The innovation floor: the fused kernels' strict gate, or torch's clamp_min (strict=False)."""
+    return _StrictFloor.apply(s, floor) if strict else s.clamp_min(floor)
 
 
 def dense_step(mean, cov, k, v, q, A, Q, r, floor):
@@ -90,12 +129,15 @@ def run_dense(k, v, q, A, Q, r, mean0, cov0, floor):
     return torch.stack(ys, dim=-2), mean, cov
 
 
-def run_diagonal(k, v, q, d, p, r, mean0, cov0, floor):
+def run_diagonal(k, v, q, d, p, r, mean0, cov0, floor, strict=True, innovations=None):
     """Diagonal-transition token loop (bayesian_layer.py:207-251).
 
     The predicted covariance is d_i P_ij d_j + p delta_ij; the initial
     covariance is used as given (not symmetrised), so autograd yields the
     full asymmetric initial-covariance gradient the fused kernels return.
+    ``strict`` selects the fused kernels' floor gate (the default; see
+    ``_StrictFloor``); ``strict=False`` is the eager loop's clamp_min (:243).
+    ``innovations``, a list, receives each token's unclamped r + k.u.
     """
     mean, cov = mean0, cov0
     eye = torch.eye(k.shape[-1], dtype=k.dtype, device=k.device)
@@ -106,7 +148,10 @@ def run_diagonal(k, v, q, d, p, r, mean0, cov0, floor):
         cov_pred = dt[..., :, None] * cov * dt[..., None, :] + p[..., t, None, None] * eye
         kt = k[..., t, :]
         u = (cov_pred @ kt.unsqueeze(-1)).squeeze(-1)
-        s = (r[..., t] + (kt * u).sum(-1)).clamp_min(floor)
+        s_raw = r[..., t] + (kt * u).sum(-1)
+        if innovations is not None:
+            innovations.append(s_raw.detach())
+        s = floor_clamp(s_raw, floor, strict)
         beta = 1.0 / s
         e = v[..., t, :] - (mean_pred * kt[..., :, None]).sum(-2)
         bu = beta[..., None] * u
@@ -116,8 +161,8 @@ def run_diagonal(k, v, q, d, p, r, mean0, cov0, floor):
     return torch.stack(ys, dim=-2), mean, cov
 
 
-def run_fixed(k, v, q, mean0, cov0, floor):
-    """Constant dynamics A = 0.97 I, Q = 0.1 I, R = 1 (bayesian_layer.py:343-397)."""
+def run_fixed(k, v, q, mean0, cov0, floor, strict=True):
+    """Constant dynamics A = 0.97 I, Q = 0.1 I, R = 1 (bayesian_layer.py:343-397; floor gate as run_diagonal)."""
     mean, cov = mean0, cov0
     eye = torch.eye(k.shape[-1], dtype=k.dtype, device=k.device)
     rho, rho2 = FIXED_DECAY, FIXED_DECAY * FIXED_DECAY
@@ -126,7 +171,7 @@ def run_fixed(k, v, q, mean0, cov0, floor):
         kt = k[..., t, :]
         mean_pred = rho * mean
         u = rho2 * (cov * kt[..., None, :]).sum(-1) + FIXED_PROCESS * kt
-        s = (FIXED_OBSERVATION + (kt * u).sum(-1)).clamp_min(floor)
+        s = floor_clamp(FIXED_OBSERVATION + (kt * u).sum(-1), floor, strict)
         beta = 1.0 / s
         e = v[..., t, :] - (mean_pred * kt[..., :, None]).sum(-2)
         bu = beta[..., None] * u
@@ -143,14 +188,16 @@ def rotation_coefficients(radius, angle, tiny: float = 1.1754943508222875e-38):
     return rho * torch.cos(angle), rho * torch.sin(angle)
 
 
-def run_rotation(k, v, q, radius, angle, p, r, mean0, cov0, floor):
+def run_rotation(k, v, q, radius, angle, p, r, mean0, cov0, floor, innovations=None):
     """Block-diagonal damped 2-D rotations (bayesian_layer.py:254-323), pair by pair.
 
     Pair j = rows (2j, 2j+1): mean and covariance rows, then covariance
     columns, are turned by [[c, -s], [s, c]]; the pair's process variance p[.., j]
     is added to entry (2j, 2j) only; then the Kalman update of run_dense with
     the covariance symmetrised.  radius, angle, p: [..., T, D/2]; tiny is the
-    float32 one, as the reference's float32 covariance uses.
+    float32 one, as the reference's float32 covariance uses.  The reference
+    runs this core in torch, so the floor is clamp_min's (gradient passes at
+    s == floor), not the fused kernels' strict gate.
     """
     D = k.shape[-1]
     J = D // 2
@@ -171,7 +218,10 @@ def run_rotation(k, v, q, radius, angle, p, r, mean0, cov0, floor):
         cov_pred = cov_pred + torch.diag_embed(noise)
         kt = k[..., t, :]
         u = (cov_pred @ kt.unsqueeze(-1)).squeeze(-1)
-        beta = 1.0 / (r[..., t] + (kt * u).sum(-1)).clamp_min(floor)
+        s_raw = r[..., t] + (kt * u).sum(-1)
+        if innovations is not None:
+            innovations.append(s_raw.detach())
+        beta = 1.0 / floor_clamp(s_raw, floor, strict=False)
         e = v[..., t, :] - (mean_pred * kt[..., :, None]).sum(-2)
         mean = mean_pred + beta[..., None, None] * u[..., :, None] * e[..., None, :]
         cov = _sym(cov_pred - beta[..., None, None] * u[..., :, None] * u[..., None, :])
@@ -329,8 +379,12 @@ def mixer_inputs(q_proj, k_proj, v_proj, decay_logits, noise, heads: int, dtype=
 
 
 def mixer_core(q_proj, k_proj, v_proj, decay_logits, noise, heads: int, mean0=None, cov0=None, floor=1e-6,
-               dtype=torch.float64):
-    """Readout [B, T, H, 8] of the mixer's layer (train_6layer.py:709-710) and the final belief [B*H, ...]."""
+               dtype=torch.float64, innovations=None):
+    """Readout [B, T, H, 8] of the mixer's layer (train_6layer.py:709-710) and the final belief [B*H, ...].
+
+    The layer runs on the fused kernels in the reference (strict floor gate);
+    ``innovations`` as in ``run_diagonal``.
+    """
     b, t, _ = q_proj.shape
     k, v, q, d, p, r = mixer_inputs(q_proj, k_proj, v_proj, decay_logits, noise, heads, dtype)
     n = b * heads
@@ -338,7 +392,7 @@ def mixer_core(q_proj, k_proj, v_proj, decay_logits, noise, heads: int, mean0=No
         mean0 = torch.zeros(n, 4, 8, dtype=dtype)
     if cov0 is None:
         cov0 = torch.eye(4, dtype=dtype).expand(n, 4, 4)
-    y, mT, cT = run_diagonal(k, v, q, d, p, r, mean0.to(dtype), cov0.to(dtype), floor)
+    y, mT, cT = run_diagonal(k, v, q, d, p, r, mean0.to(dtype), cov0.to(dtype), floor, innovations=innovations)
     return y.reshape(b, heads, t, 8).transpose(1, 2), mT, cT
 
 
@@ -399,6 +453,42 @@ def causal_depthwise4(x, weight):
     return y
 
 
+def _round_bf16(x: Tensor) -> Tensor:
+    """x rounded to bfloat16 in value only (the gradient passes, as autograd's through ``.to()``)."""
+    return x + (x.to(torch.bfloat16).to(x.dtype) - x).detach()
+
+
+def mixer_block(projected, conv_weight, norm_weight, heads: int, aux_bias=None, conv_out=None, floor=1e-6,
+                eps: float = 1.1920928955078125e-07, round_bf16: bool = True):
+    """The Bayes mixer from its fused projection to out_proj's input (train_6layer.py:583-729), float64.
+
+    projected [B, T, H*4 + H*4 + H*8 | H*4 + H*2 | H*8]: the Q/K/V core, the
+    aux columns (decay logits, interleaved noise; plus ``aux_bias``, :589-593,
+    rounded to bf16 as the reference's bf16 add) and the gate.  The core goes
+    through ``causal_depthwise4`` (weight [C, 1, 4]) and is rounded to bf16,
+    the reference's tensor dtype there (``conv_out``, a kernel's bf16 filter
+    output, replaces the values of that rounding); then ``mixer_core`` and
+    ``mixer_readout``.  Returns (out [B, T, H*8], mean_T, cov_T), out unrounded.
+    ``round_bf16=False`` drops the bf16 roundings (a smooth chain, for gradcheck).
+    """
+    rnd = _round_bf16 if round_bf16 else (lambda v: v)
+    state, width = heads * 4, heads * 8
+    core, aux = 2 * state + width, state + 2 * heads
+    x = projected.to(torch.float64)
+    filtered = causal_depthwise4(x[..., :core].transpose(1, 2), conv_weight.to(torch.float64)).transpose(1, 2)
+    if conv_out is None:
+        filtered = rnd(filtered)
+    else:
+        filtered = filtered + (conv_out.to(torch.float64) - filtered).detach()
+    q_in, k_in, v_in = filtered.split((state, state, width), dim=-1)
+    aux_in = x[..., core:core + aux]
+    if aux_bias is not None:
+        aux_in = rnd(aux_in + aux_bias.to(torch.float64))
+    read, mean_t, cov_t = mixer_core(q_in, k_in, v_in, aux_in[..., :state], aux_in[..., state:], heads, floor=floor)
+    read_b = None if round_bf16 else read
+    return mixer_readout(read, x[..., core + aux:], norm_weight, eps, read_bf16=read_b), mean_t, cov_t
+
+
 def make_mixer_inputs(b: int, t: int, heads: int, *, seed: int = 0, ld_pad: int = 0, scale: float = 1.0):
     """Seeded bf16 projections of the mixer (CPU tensors), drawn as one fused projection.
 
@@ -457,17 +547,18 @@ def make_scan_inputs(b: int, t: int, d: int, m: int, *, seed: int = 0, dtype=tor
     return [x.to(dtype) for x in (k, v, q, r)]
 
 
-def diagonal_grads(k, v, q, d, p, r, mean0, cov0, gy, gmf=None, gcf=None, floor=1e-6, chunk=None):
+def diagonal_grads(k, v, q, d, p, r, mean0, cov0, gy, gmf=None, gcf=None, floor=1e-6, chunk=None, strict=True):
     """Outputs and all eight gradients by autograd through the oracle.
 
-    ``chunk=None`` differentiates ``run_diagonal``; an integer differentiates
-    the transported-history ``run_chunked`` (the reference CPU path).
+    ``chunk=None`` differentiates ``run_diagonal`` (floor gate per ``strict``);
+    an integer differentiates the transported-history ``run_chunked`` (the
+    reference CPU path, torch's clamp_min).
     Returns (y, mean_T, cov_T, [gk, gv, gq, gd, gp, gr, gm0, gc0]).
     """
     leaves = [x.detach().clone().requires_grad_(True) for x in (k, v, q, d, p, r, mean0, cov0)]
     k_, v_, q_, d_, p_, r_, m0_, c0_ = leaves
     if chunk is None:
-        y, mT, cT = run_diagonal(k_, v_, q_, d_, p_, r_, m0_, c0_, floor)
+        y, mT, cT = run_diagonal(k_, v_, q_, d_, p_, r_, m0_, c0_, floor, strict)
     else:
         A, Q = diagonal_as_dense(d_, p_)
         y, mT, cT = run_chunked(k_, v_, q_, A, Q, r_, m0_, c0_, chunk, floor)

@@ -1,0 +1,157 @@
+"""The public API on the GPU: which kernels each entry point reaches, checked against the float64 oracle.
+
+ReplaySSM (bayes_ssm/replay_ssm.py:34-145) and BayesianLayer
+(bayes_ssm/bayesian_layer.py:1185-1274) never reach the fused kernels in the
+reference (a replayed or learned-initial-state call keeps the dense path,
+:987-993, :1047-1061); their scan and the scalar-noise / low-precision /
+fixed-dynamics calls of ``bayesian_layer`` do.  Tolerance (north star): 1e-5
+relative, 1e-4 absolute.
+"""
+from __future__ import annotations
+
+import importlib
+
+import pytest
+import torch
+
+import bayes_ssm
+from oracle import bssm_oracle as O
+
+pytestmark = pytest.mark.gpu
+
+RTOL, ATOL = 1e-5, 1e-4
+F64 = torch.float64
+
+
+def close(actual, expected, name="", rtol=RTOL, atol=ATOL):
+    torch.testing.assert_close(actual.detach().double().cpu(), expected.detach().double().cpu(), rtol=rtol,
+                               atol=atol, msg=lambda m: f"{name}: {m}")
+
+
+def _count(monkeypatch, owner, attr="apply"):
+    calls = []
+    orig = getattr(owner, attr)
+    monkeypatch.setattr(owner, attr, staticmethod(lambda *a, **k: calls.append(1) or orig(*a, **k)))
+    return calls
+
+
+def test_replay_ssm_associative_scan_reaches_hip(cuda_device, monkeypatch):
+    rs = importlib.import_module("bayes_ssm.replay_ssm")
+    calls = _count(monkeypatch, rs._StaticScanFunction)
+    layer = bayes_ssm.ReplaySSM(16, 16, process_variance=0.0, observation_variance=0.4).to(cuda_device)
+    k, v, q, _ = O.make_scan_inputs(4, 64, 16, 16, seed=3)
+    y, mT, cT = layer.associative_scan(k.to(cuda_device), v.to(cuda_device), q.to(cuda_device))
+    assert calls, "the HIP scan was not used"
+    r = torch.full((4, 64), 0.4, dtype=F64)
+    ey, em, ec = O.associative_static(k.double(), v.double(), q.double(), r)
+    close(y, ey, "y")
+    close(mT, em, "mean_T")
+    close(cT, ec, "cov_T")
+
+
+def test_associative_scan_cuda_gradients(cuda_device):
+    """associative_static_bayesian_cuda is differentiable (replay_ssm.py:276-339): all six gradients."""
+    b, t, d, m = 3, 24, 4, 5
+    k, v, q, r = O.make_scan_inputs(b, t, d, m, seed=8)
+    g = torch.Generator().manual_seed(9)
+    a = torch.randn(b, d, d, generator=g) / d ** 0.5
+    c0 = a @ a.transpose(-1, -2) + 0.5 * torch.eye(d)
+    m0 = torch.randn(b, d, m, generator=g)
+    gy = torch.randn(b, t, m, generator=g)
+    gm = torch.randn(b, d, m, generator=g)
+    gc = torch.randn(b, d, d, generator=g)
+    leaves = [x.to(cuda_device).requires_grad_(True) for x in (k, v, q, r, m0, c0)]
+    y, mT, cT = bayes_ssm.associative_static_bayesian_cuda(
+        leaves[0], leaves[1], leaves[2], observation_variances=leaves[3], initial_mean=leaves[4],
+        initial_covariance=leaves[5])
+    torch.autograd.backward([y, mT, cT], [gy.to(cuda_device), gm.to(cuda_device), gc.to(cuda_device)])
+    el = [x.double().requires_grad_(True) for x in (k, v, q, r, m0, c0)]
+    ey, em, ec = O.associative_static(*el[:4], el[4], el[5])
+    torch.autograd.backward([ey, em, ec], [gy.double(), gm.double(), gc.double()])
+    close(y, ey, "y")
+    for name, x, e in zip(("k", "v", "q", "r", "mean0", "cov0"), leaves, el):
+        close(x.grad, e.grad, "grad " + name)
+
+
+def test_scalar_noise_reaches_the_fused_kernels(cuda_device, monkeypatch):
+    """Scalar process/observation noise expand to stride-0 [N, T] views that the gate makes contiguous."""
+    from bayes_ssm import fused_cuda
+
+    calls = _count(monkeypatch, fused_cuda._ChunkedBayesianFunction)
+    n, t, d = 32, 48, 4
+    k, v, q, dec, _, _, gy = O.make_inputs(n, t, d, seed=31)
+    leaves = [x.to(cuda_device).requires_grad_(True) for x in (k, v, q, dec)]
+    y, mT, cT = bayes_ssm.bayesian_layer(*leaves[:3], transition_diagonals=leaves[3], process_variances=0.03,
+                                         observation_variances=0.6, chunk_length=16, optimized=True)
+    assert calls, "fused HIP path was not taken"
+    y.backward(gy.to(cuda_device))
+    el = [x.double().requires_grad_(True) for x in (k, v, q, dec)]
+    ey, em, ec = O.run_diagonal(*el, torch.full((n, t), 0.03, dtype=F64), torch.full((n, t), 0.6, dtype=F64),
+                                torch.zeros(n, d, 8, dtype=F64), torch.eye(d, dtype=F64).expand(n, d, d), 1e-6)
+    ey.backward(gy.double())
+    close(y, ey, "y")
+    close(mT, em, "mean_T")
+    close(cT, ec, "cov_T")
+    for name, x, e in zip(("k", "v", "q", "decay"), leaves, el):
+        close(x.grad, e.grad, "grad " + name)
+
+
+def test_fp16_inputs_and_fixed_dynamics_reach_the_fused_kernels(cuda_device, monkeypatch):
+    """fp16 keys/values/queries are promoted (bayesian_layer.py:823-827); fixed_dynamics selects the
+    constant-dynamics kernels (A = 0.97 I, Q = 0.1 I, R = 1; :366-369)."""
+    from bayes_ssm import fused_cuda
+
+    calls = _count(monkeypatch, fused_cuda._ChunkedBayesianFunction)
+    n, t, d = 24, 40, 2
+    k, v, q, _, _, _, gy = O.make_inputs(n, t, d, seed=32)
+    kh, vh, qh = (x.half().to(cuda_device).requires_grad_(True) for x in (k, v, q))
+    dec = torch.full((n, t, d), O.FIXED_DECAY, device=cuda_device)
+    y, mT, cT = bayes_ssm.bayesian_layer(kh, vh, qh, transition_diagonals=dec, process_variances=O.FIXED_PROCESS,
+                                         observation_variances=O.FIXED_OBSERVATION, chunk_length=8,
+                                         optimized=True, fixed_dynamics=True)
+    assert calls, "fused HIP path was not taken"
+    assert y.dtype == torch.float32
+    y.backward(gy.to(cuda_device))
+    el = [x.half().double().requires_grad_(True) for x in (k, v, q)]
+    ey, em, ec = O.run_fixed(*el, torch.zeros(n, d, 8, dtype=F64), torch.eye(d, dtype=F64).expand(n, d, d), 1e-6)
+    ey.backward(gy.double())
+    close(y, ey, "y")
+    close(mT, em, "mean_T")
+    close(cT, ec, "cov_T")
+    for name, x, e in zip(("k", "v", "q"), (kh, vh, qh), el):
+        assert x.grad.dtype == torch.float16
+        close(x.grad, e.grad, "grad " + name, rtol=2 ** -10, atol=1e-3)
+
+
+def test_replay_ssm_and_bayesian_layer_modules_on_gpu(cuda_device):
+    """The modules on the GPU take the dense replay / chunk paths and match the oracle, gradients included."""
+    n, t, d, m = 6, 30, 4, 8
+    k, v, q, dec, _, _, gy = O.make_inputs(n, t, d, m, seed=33)
+    layer = bayes_ssm.ReplaySSM(d, m, chunk_length=8).to(cuda_device)
+    leaves = [x.to(cuda_device).requires_grad_(True) for x in (k, v, q, dec)]
+    y, _, _ = layer(*leaves[:3], transition_diagonals=leaves[3])
+    y.backward(gy.to(cuda_device))
+    el = [x.double().requires_grad_(True) for x in (k, v, q, dec)]
+    ey, _, _ = O.run_diagonal(*el, torch.full((n, t), 0.05, dtype=F64), torch.full((n, t), 0.2, dtype=F64),
+                              torch.zeros(n, d, m, dtype=F64), torch.eye(d, dtype=F64).expand(n, d, d), 1e-6,
+                              strict=False)
+    ey.backward(gy.double())
+    close(y, ey, "ReplaySSM y")
+    for name, x, e in zip(("k", "v", "q", "decay"), leaves, el):
+        close(x.grad, e.grad, "ReplaySSM grad " + name)
+
+    bl = bayes_ssm.BayesianLayer(d, m, learn_noise=True).to(cuda_device)
+    g = torch.Generator().manual_seed(34)
+    A = 0.9 * torch.eye(d) + 0.05 * torch.randn(n, t, d, d, generator=g)
+    y2, _, _ = bl(k.to(cuda_device), v.to(cuda_device), q.to(cuda_device), transitions=A.to(cuda_device),
+                  optimized=True)
+    y2.backward(gy.to(cuda_device))
+    raw = torch.tensor(bl._process_raw.item(), dtype=F64, requires_grad=True)
+    qv = torch.nn.functional.softplus(raw)
+    rv = torch.nn.functional.softplus(torch.tensor(bl._observation_raw.item(), dtype=F64))
+    ey2, _, _ = O.run_dense(k.double(), v.double(), q.double(), A.double(),
+                            qv * torch.eye(d, dtype=F64).expand(n, t, d, d), rv.expand(n, t),
+                            torch.zeros(n, d, m, dtype=F64), 3.0 * torch.eye(d, dtype=F64).expand(n, d, d), 1e-6)
+    ey2.backward(gy.double())
+    close(y2, ey2, "BayesianLayer y")
+    close(bl._process_raw.grad, raw.grad, "BayesianLayer grad process raw")

@@ -48,7 +48,7 @@ def _lds(views):
     return [x.stride(1) for x in views]
 
 
-def _forward(dv, lds, m0, c0, b, t, h):
+def _forward(dv, lds, m0, c0, b, t, h, floor=1e-6):
     from bayes_ssm import _hip
 
     n = b * h
@@ -62,11 +62,11 @@ def _forward(dv, lds, m0, c0, b, t, h):
     for x, ld in zip(dv, lds):
         args += [P(x), ld]
     _hip.call("bssm_mixer_forward", *args, P(m0), P(c0), P(read), P(mT), P(cT), P(bm), P(bc), b, t, h, CHUNK,
-              1e-6, _hip.stream_of(dev))
+              floor, _hip.stream_of(dev))
     return read, mT, cT, bm, bc
 
 
-def _backward(dv, lds, m0, c0, bm, bc, gy, gmf, gcf, b, t, h, *, f32, dyn=True, initial=True):
+def _backward(dv, lds, m0, c0, bm, bc, gy, gmf, gcf, b, t, h, *, f32, dyn=True, initial=True, floor=1e-6):
     from bayes_ssm import _hip
 
     dev = dv[0].device
@@ -79,7 +79,7 @@ def _backward(dv, lds, m0, c0, bm, bc, gy, gmf, gcf, b, t, h, *, f32, dyn=True, 
     for x, ld in zip(dv, lds):
         args += [P(x), ld]
     _hip.call("bssm_mixer_backward", *args, P(m0), P(c0), P(bm), P(bc), P(gy), P(gmf), P(gcf),
-              *[P(g) for g in grads], P(gm0), P(gc0), b, t, h, CHUNK, 1e-6, int(f32), _hip.stream_of(dev))
+              *[P(g) for g in grads], P(gm0), P(gc0), b, t, h, CHUNK, floor, int(f32), _hip.stream_of(dev))
     return grads + [gm0, gc0]
 
 
@@ -215,7 +215,7 @@ def _gate_inputs(b, t, h, seed, gate_pad):
     return gate_full[..., : h * 8], w, gout
 
 
-def _gated_forward(dv, lds, gate, w, m0, c0, b, t, h, precise):
+def _gated_forward(dv, lds, gate, w, m0, c0, b, t, h, precise, floor=1e-6):
     from bayes_ssm import _hip
 
     n, nb, dev = b * h, -(-t // CHUNK), dv[0].device
@@ -228,11 +228,11 @@ def _gated_forward(dv, lds, gate, w, m0, c0, b, t, h, precise):
     for x, ld in zip(dv, lds):
         args += [P(x), ld]
     _hip.call("bssm_mixer_gated_forward", *args, P(gate), gate.stride(1), P(w), EPS32, P(m0), P(c0), P(out), P(yb),
-              P(mT), P(cT), P(bm), P(bc), b, t, h, CHUNK, 1e-6, int(precise), _hip.stream_of(dev))
+              P(mT), P(cT), P(bm), P(bc), b, t, h, CHUNK, floor, int(precise), _hip.stream_of(dev))
     return out, yb, mT, cT, bm, bc
 
 
-def _gated_backward(dv, lds, gate, w, m0, c0, bm, bc, yb, gout, gmf, gcf, b, t, h, precise):
+def _gated_backward(dv, lds, gate, w, m0, c0, bm, bc, yb, gout, gmf, gcf, b, t, h, precise, floor=1e-6):
     from bayes_ssm import _hip
 
     dev = dv[0].device
@@ -247,7 +247,7 @@ def _gated_backward(dv, lds, gate, w, m0, c0, bm, bc, yb, gout, gmf, gcf, b, t, 
         args += [P(x), ld]
     _hip.call("bssm_mixer_gated_backward", *args, P(gate), gate.stride(1), P(w), EPS32, P(m0), P(c0), P(bm), P(bc),
               P(yb), P(gout), P(gmf), P(gcf), *[P(g) for g in grads], P(ggate), P(part), P(gm0), P(gc0), b, t, h,
-              CHUNK, 1e-6, int(precise), _hip.stream_of(dev))
+              CHUNK, floor, int(precise), _hip.stream_of(dev))
     return grads + [ggate, part, gm0, gc0]
 
 
@@ -352,3 +352,75 @@ def test_mixer_readout_fallback_matches_oracle(cuda_device):
     out, _, _ = mixer.bayes_mixer_readout(*dv, gate.to(cuda_device), w.to(cuda_device).bfloat16(), heads=h)
     read, _, _ = O.mixer_core(*views, h)
     close(out, O.mixer_readout(read, gate, w), "out", rtol=3 * 2 ** -8, atol=1e-3)
+
+
+# ------------------------------------------------- the benchmarked shape (H64 x T512)
+def _rows_views(views, rows):
+    """The five column views over a copy of just `rows` of their fused projection."""
+    base = views[0]._base[rows].contiguous()
+    return [torch.as_strided(base, (len(rows), *x.shape[1:]), x.stride(), x.storage_offset()) for x in views]
+
+
+def test_mixer_config3_shape_rows_match_subset_and_oracle(cuda_device):
+    """The core and the gated readout at B256 x T512 x H64: batch rows are independent, so the full-shape
+    rows equal a run on just those rows bit for bit, and that run matches the float64 oracle (1e-5 / 1e-4)."""
+    b, t, h = 256, 512, 64
+    rows = [0, 129, 255]
+    print("mixer config3 shape", flush=True)
+    views, g_read = O.make_mixer_inputs(b, t, h, seed=4242)
+    gate, w, gout = _gate_inputs(b, t, h, seed=4243, gate_pad=0)
+    n = b * h
+    m0 = torch.zeros(n, 4, 8)
+    c0 = torch.eye(4).expand(n, 4, 4).contiguous()
+    dv = _device_views(views, cuda_device)
+    lds = _lds(views)
+    d = {k: x.to(cuda_device) for k, x in dict(m0=m0, c0=c0, gy=g_read, gate=gate, w=w, gout=gout).items()}
+    read, mT, cT, bm, bc = _forward(dv, lds, d["m0"], d["c0"], b, t, h)
+    g32 = _backward(dv, lds, d["m0"], d["c0"], bm, bc, d["gy"], None, None, b, t, h, f32=True)
+    o32, yb, _, _, gbm, gbc = _gated_forward(dv, lds, d["gate"], d["w"], d["m0"], d["c0"], b, t, h, True)
+    gg = _gated_backward(dv, lds, d["gate"], d["w"], d["m0"], d["c0"], gbm, gbc, yb, d["gout"], None, None, b, t, h,
+                         True)
+    torch.cuda.synchronize()
+    assert torch.isfinite(read).all() and torch.isfinite(g32[0]).all()
+
+    print("mixer config3 shape: subset rows", flush=True)
+    ri = torch.tensor(rows)
+    seqs = (ri[:, None] * h + torch.arange(h)).flatten()
+    sv = _rows_views(views, ri)
+    sdv = _device_views(sv, cuda_device)
+    bs = len(rows)
+    sd = {k: x.to(cuda_device) for k, x in dict(m0=m0[seqs], c0=c0[seqs], gy=g_read[ri], gate=gate[ri],
+                                                gout=gout[ri]).items()}
+    s_read, s_mT, s_cT, s_bm, s_bc = _forward(sdv, lds, sd["m0"], sd["c0"], bs, t, h)
+    s_g32 = _backward(sdv, lds, sd["m0"], sd["c0"], s_bm, s_bc, sd["gy"], None, None, bs, t, h, f32=True)
+    s_o32, s_yb, _, _, s_gbm, s_gbc = _gated_forward(sdv, lds, sd["gate"], d["w"], sd["m0"], sd["c0"], bs, t, h,
+                                                     True)
+    s_gg = _gated_backward(sdv, lds, sd["gate"], d["w"], sd["m0"], sd["c0"], s_gbm, s_gbc, s_yb, sd["gout"], None,
+                           None, bs, t, h, True)
+    torch.cuda.synchronize()
+    rd = ri.to(cuda_device)
+    sq = seqs.to(cuda_device)
+    assert torch.equal(s_read, read[rd]) and torch.equal(s_mT, mT[sq]) and torch.equal(s_cT, cT[sq])
+    for i in range(5):
+        assert torch.equal(s_g32[i], g32[i][rd]), f"core gradient {i}"
+    assert torch.equal(s_o32, o32[rd]) and torch.equal(s_yb, yb[rd])
+    for i in range(6):
+        assert torch.equal(s_gg[i], gg[i][rd]), f"gated gradient {i}"
+
+    # The subset run against the oracle.
+    e_read, e_mT, e_cT, e_grads = O.mixer_grads(*sv, h, m0[seqs], c0[seqs], g_read[ri])
+    close(s_read.view(bs, t, h, 8), e_read, "read")
+    close(s_mT, e_mT, "mean_T")
+    close(s_cT, e_cT, "cov_T")
+    names = ["g_q", "g_k", "g_v", "g_decay_logits", "g_noise"]
+    for name, a, e in zip(names, s_g32, e_grads):
+        close(a, e, name)
+    leaves = [x.detach().double().requires_grad_(True) for x in (*sv, gate[ri], w)]
+    e_r2, _, _ = O.mixer_core(*leaves[:5], h, m0[seqs].double(), c0[seqs].double())
+    e_out = O.mixer_readout(e_r2, leaves[5], leaves[6], EPS32, read_bf16=s_yb.cpu())
+    close(s_yb.view(bs, t, h, 8), e_r2, "read_bf16", rtol=2 ** -8, atol=1e-6)
+    close(s_o32, e_out, "out")
+    eg = torch.autograd.grad((e_out * gout[ri].double()).sum(), leaves)
+    for name, a, e in zip(names + ["g_gate"], s_gg[:6], eg[:6]):
+        close(a, e, "gated " + name)
+    close(s_gg[6].sum(0), eg[6], "gated g_norm_weight")

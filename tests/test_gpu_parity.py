@@ -292,6 +292,14 @@ def test_bayesian_layer_routes_to_hip(cuda_device, monkeypatch):
     close(y, ry, "y vs reference fp32 path")
     close(mT, rm, "mean")
     close(cT, rc, "cov")
+    # Both against the float64 oracle (the CPU path above is this package's own code).
+    f64 = {k: x.double() for k, x in cpu.items()}
+    ey, em, ec = O.run_diagonal(f64["k"], f64["v"], f64["q"], f64["d"], f64["p"], f64["r"],
+                                torch.zeros(n, d, 8, dtype=torch.float64),
+                                torch.eye(d, dtype=torch.float64).expand(n, d, d), 1e-6)
+    for name, a, b, e in (("y", y, ry, ey), ("mean", mT, rm, em), ("cov", cT, rc, ec)):
+        close(a, e, name + " vs oracle")
+        close(b, e, name + " (CPU path) vs oracle")
 
 
 @pytest.mark.parametrize("cfg", [(1, 16, 4, 4), (4, 64, 16, 16)])
@@ -338,12 +346,14 @@ def test_associative_scan_priors_and_sizes(cuda_device, cfg):
     close(cT, ec, "cov")
 
 
-def test_config3_full_size_subset(cuda_device):
-    """Config 3 at full size (B256 x T512 x H64, D4M8): fwd+bwd on the GPU, a seeded subset of sequences against the oracle."""
+@pytest.mark.parametrize("d", [4, 2, 8])
+def test_config3_full_size_subset(cuda_device, d):
+    """Config 3 at full size (B256 x T512 x H64; D4M8 and the D2M8 / D8M8 variants): fwd+bwd on the GPU,
+    a seeded subset of sequences against the oracle."""
     from bayes_ssm.fused_cuda import fused_diagonal_bayesian
 
-    n, t, d = 256 * 64, 512, 4
-    print("config3 full size", flush=True)
+    n, t = 256 * 64, 512
+    print(f"config3 full size d={d}", flush=True)
     k, v, q, dec, p, r, gy = O.make_inputs(n, t, d, seed=0)
     leaves = [x.to(cuda_device).requires_grad_(True) for x in (k, v, q, dec, p, r)]
     m0 = torch.zeros(n, d, 8, device=cuda_device)

@@ -39,7 +39,7 @@ def _case(n, t, d, seed, angle_scale=2.0):
     return [k, v, q, rad, ang, p, r, m0, c0], gy, gmf, gcf
 
 
-def _run(ins, gy, gmf, gcf, chunk, device):
+def _run(ins, gy, gmf, gcf, chunk, device, floor=1e-6):
     from bayes_ssm import _hip
 
     k, v, q, rad, ang, p, r, m0, c0 = [x.to(device).contiguous() for x in ins]
@@ -51,11 +51,11 @@ def _run(ins, gy, gmf, gcf, chunk, device):
     P = _hip.ptr
     s = _hip.stream_of(device)
     _hip.call("bssm_forward_chunked_rotation", d, 8, P(k), P(v), P(q), P(rad), P(ang), P(p), P(r), P(m0), P(c0),
-              P(y), P(mT), P(cT), P(bm), P(bc), n, t, chunk, 1e-6, s)
+              P(y), P(mT), P(cT), P(bm), P(bc), n, t, chunk, floor, s)
     grads = [torch.empty_like(x) for x in (k, v, q, rad, ang, p, r, m0, c0)]
     gy_d, gmf_d, gcf_d = gy.to(device), gmf.to(device), gcf.to(device)
     _hip.call("bssm_backward_chunked_rotation", d, 8, P(k), P(v), P(q), P(rad), P(ang), P(p), P(r), P(m0), P(c0),
-              P(bm), P(bc), P(gy_d), P(gmf_d), P(gcf_d), *map(P, grads), n, t, chunk, 1e-6, s)
+              P(bm), P(bc), P(gy_d), P(gmf_d), P(gcf_d), *map(P, grads), n, t, chunk, floor, s)
     torch.cuda.synchronize()
     return y, mT, cT, bm, bc, grads
 

@@ -160,6 +160,71 @@ def test_floor_clamps_innovation():
     assert math.isclose(float(cT), 1.0 - u * u / floor, rel_tol=1e-12)
 
 
+def _equality_token(r_value):
+    """One D = 1 token with exact dyadic arithmetic: u = (d^2 P0 + p) k = 0.5, k.u = 0.25, s = r + 0.25."""
+    k = torch.full((1, 1, 1), 0.5)
+    v = torch.full((1, 1, 1), 1.5)
+    q = torch.full((1, 1, 1), 2.0)
+    dec = torch.ones(1, 1, 1)
+    p = torch.zeros(1, 1)
+    r = torch.full((1, 1), r_value)
+    m0 = torch.full((1, 1, 1), 0.25)
+    c0 = torch.ones(1, 1, 1)
+    return k, v, q, dec, p, r, m0, c0
+
+
+def test_strict_floor_gate_is_the_left_derivative():
+    """At r + k.u == floor exactly, the kernels' gate (s > floor) gives dL/dr = 0: the left-sided
+    finite difference.  torch's clamp_min passes the gradient (the right-sided one).  Away from the
+    floor both equal the central difference; below it both are zero."""
+    floor = 1.0
+    gy = torch.full((1, 1, 1), 0.75)
+
+    def loss(r_value):
+        k, v, q, dec, p, r, m0, c0 = _equality_token(r_value)
+        y, _, _ = O.run_diagonal(k, v, q, dec, p, r, m0, c0, floor)
+        return float((y * gy).sum())
+
+    def grad_r(r_value, strict):
+        k, v, q, dec, p, r, m0, c0 = _equality_token(r_value)
+        _, _, _, g = O.diagonal_grads(k, v, q, dec, p, r, m0, c0, gy, floor=floor, strict=strict)
+        return float(g[5])
+
+    eq = 0.75  # s = 0.75 + 0.25 == floor, every operation exact in binary
+    seen = []
+    k, v, q, dec, p, r, m0, c0 = _equality_token(eq)
+    O.run_diagonal(k, v, q, dec, p, r, m0, c0, floor, innovations=seen)
+    assert float(seen[0]) == floor
+    h = 1e-7
+    left = (loss(eq) - loss(eq - h)) / h
+    right = (loss(eq + h) - loss(eq)) / h
+    assert abs(left) < 1e-9 and abs(right) > 1e-2
+    assert grad_r(eq, strict=True) == 0.0
+    assert math.isclose(grad_r(eq, strict=False), right, rel_tol=1e-5)
+    for r_value in (0.9, 1.4):  # above the floor: both conventions are the derivative
+        central = (loss(r_value + h) - loss(r_value - h)) / (2 * h)
+        for strict in (True, False):
+            assert math.isclose(grad_r(r_value, strict), central, rel_tol=1e-6)
+    for strict in (True, False):  # below: clamped, no dependence on r
+        assert grad_r(0.5, strict) == 0.0
+    # A planted mistake (the gate written as s >= floor) is what clamp_min computes: caught above.
+    assert grad_r(eq, strict=False) != grad_r(eq, strict=True)
+
+
+def test_strict_floor_gate_gradcheck_away_from_floor():
+    """With the floor active on some tokens (none at equality), the gated oracle passes gradcheck."""
+    k, v, q, dec, p, r, m0, c0 = _rand(1, 5, 2, 2, seed=14)
+    floor = 1.3
+    seen = []
+    O.run_diagonal(k, v, q, dec, p, r, m0, c0, floor, innovations=seen)
+    s = torch.stack(seen)
+    assert (s < floor).any() and (s > floor).any()
+    assert ((s - floor).abs() > 1e-3).all()
+    leaves = [x.clone().requires_grad_(True) for x in (k, v, q, dec, p, r, m0, c0)]
+    assert torch.autograd.gradcheck(lambda *xs: O.run_diagonal(*xs, floor), leaves, eps=1e-7, atol=1e-7,
+                                    rtol=1e-5)
+
+
 def test_checkpoint_layout():
     """bm[:, c] is the belief before token c*chunk, bm[:, nb] the final belief."""
     k, v, q, dec, p, r, m0, c0 = _rand(2, 10, 2, 3, seed=10)
@@ -315,6 +380,81 @@ def test_mixer_mutation_is_detected():
     x = torch.linspace(-4.0, 4.0, 8).reshape(1, 1, 8)
     bad = torch.exp(O._softplus(x))
     assert not torch.allclose(bad, torch.sigmoid(-x), rtol=1e-8, atol=0)
+
+
+def _block_inputs(b, t, h, seed):
+    g = torch.Generator().manual_seed(seed)
+    state, width = 4 * h, 8 * h
+    core, aux = 2 * state + width, state + 2 * h
+    projected = torch.randn(b, t, core + aux + width, generator=g)
+    projected[..., core:core + state] -= 4.0          # decay logits: slow decay, as the learned init
+    projected[..., core + state:core + aux:2] -= 2.0  # process logits
+    projected = projected.to(torch.bfloat16).double()
+    weight = (0.5 * torch.randn(core, 1, 4, generator=g)).to(torch.bfloat16).double()
+    norm_w = (1 + 0.2 * torch.randn(8, generator=g)).to(torch.bfloat16).double()
+    aux_bias = (0.3 * torch.randn(aux, generator=g)).to(torch.bfloat16).double()
+    return projected, weight, norm_w, aux_bias
+
+
+def _reference_block_ops(projected, weight, norm_w, aux_bias, h, eps):
+    """train_6layer.py:583-729 written with torch's own ops (the bf16 tensors' values kept at each boundary)."""
+    F = torch.nn.functional
+    b, t, _ = projected.shape
+    state, width = 4 * h, 8 * h
+    core, aux = 2 * state + width, state + 2 * h
+
+    def bf16(x):
+        return x.to(torch.bfloat16).double()
+
+    x = projected[..., :core].transpose(1, 2)
+    w = weight[:, 0]
+    padded = F.pad(x, (3, 0))
+    y = padded[..., :t] * w[:, 0].view(1, -1, 1)
+    for j in range(1, 4):
+        y = y + padded[..., j:t + j] * w[:, j].view(1, -1, 1)
+    conv = bf16(y.transpose(1, 2))
+    q_in, k_in, v_in = conv.split((state, state, width), dim=-1)
+    auxv = bf16(projected[..., core:core + aux] + aux_bias)
+    gate = projected[..., core + aux:]
+    q = F.normalize(F.silu(q_in).view(b, t, h, 4), dim=-1).permute(0, 2, 1, 3).reshape(b * h, t, 4)
+    k = F.normalize(F.silu(k_in).view(b, t, h, 4), dim=-1).permute(0, 2, 1, 3).reshape(b * h, t, 4)
+    v = F.silu(v_in).view(b, t, h, 8).permute(0, 2, 1, 3).reshape(b * h, t, 8)
+    noise = auxv[..., state:].view(b, t, h, 2)
+    process = (F.softplus(noise[..., 0]) + 1e-4).permute(0, 2, 1).reshape(b * h, t)
+    observation = (F.softplus(noise[..., 1]) + 1e-4).permute(0, 2, 1).reshape(b * h, t)
+    decay = torch.exp(-F.softplus(auxv[..., :state])).view(b, t, h, 4).permute(0, 2, 1, 3).reshape(b * h, t, 4)
+    read, _, _ = O.reference_layer(k, v, q, decay, process, observation, chunk=64, floor=1e-6)
+    read = read.view(b, h, t, 8).permute(0, 2, 1, 3)
+    normed = F.rms_norm(bf16(read), (8,), norm_w, eps)
+    return (normed * F.silu(gate.view(b, t, h, 8))).reshape(b, t, width)
+
+
+def test_mixer_block_matches_reference_op_sequence():
+    """mixer_block equals the reference's mixer ops written with torch's own functions (filter as shifted
+    products, F.normalize, softplus, the transported-history layer, rms_norm, silu) at float64."""
+    h = 2
+    projected, weight, norm_w, aux_bias = _block_inputs(2, 11, h, seed=21)
+    eps = torch.finfo(torch.float32).eps
+    ours, _, _ = O.mixer_block(projected, weight, norm_w, h, aux_bias=aux_bias, eps=eps)
+    ref = _reference_block_ops(projected, weight, norm_w, aux_bias, h, eps)
+    torch.testing.assert_close(ours, ref, rtol=1e-10, atol=1e-12)
+    # A planted mistake (gate and v columns swapped) is detected.
+    core = 16 * h
+    swapped = projected.clone()
+    swapped[..., 8 * h:core], swapped[..., -8 * h:] = projected[..., -8 * h:], projected[..., 8 * h:core]
+    bad, _, _ = O.mixer_block(swapped, weight, norm_w, h, aux_bias=aux_bias, eps=eps)
+    assert (bad - ref).abs().max() > 1e-2
+
+
+def test_mixer_block_gradcheck():
+    projected, weight, norm_w, aux_bias = _block_inputs(1, 4, 1, seed=22)
+    leaves = [x.clone().requires_grad_(True) for x in (projected, weight, norm_w, aux_bias)]
+
+    def fn(p, w, n, a):
+        out, mT, cT = O.mixer_block(p, w, n, 1, aux_bias=a, round_bf16=False)
+        return out, mT, cT
+
+    assert torch.autograd.gradcheck(fn, leaves, eps=1e-6, atol=1e-6)
 
 
 def test_mixer_readout_matches_torch_ops_and_invariants():
