@@ -747,6 +747,10 @@ int bssm_causal_conv4_backward(int bf16, const void* x, int64_t ldx, const float
   const char* fn = "bssm_causal_conv4_backward";
   if (int rc = conv_check(fn, bf16, x, ldx, weight, {grad_y, grad_x, grad_weight_partials}, batch, t, channels))
     return rc;
+  // With T = 0 the kernel still reads the weight and writes zero partials.
+  if (batch * channels > 0 && (weight == nullptr || grad_weight_partials == nullptr || !aligned16(weight) ||
+                               !aligned16(grad_weight_partials)))
+    return fail(BSSM_ERR_ARGUMENT, "%s: weight and grad_weight_partials must be non-null and 16-byte aligned", fn);
   bssm::ConvArgs a{};
   a.x = x; a.ldx = ldx; a.w = weight; a.gy = grad_y; a.gx = grad_x; a.gw_part = grad_weight_partials;
   a.b = batch; a.t = t; a.c = channels; a.bf16 = bf16 != 0;

@@ -150,3 +150,11 @@ def test_mixer_argument_errors_are_reported(lib):
     assert rc == 1 and b"null" in lib.bssm_last_error()
     # Nothing to do: success without touching a device.
     assert _mixer_fwd(lib, b=0) == 0
+
+
+def test_conv_backward_checks_weight_and_partials_at_t0(lib):
+    """With T = 0 the backward still reads the weight and writes the partials: both are required."""
+    rc = lib.bssm_causal_conv4_backward(1, None, 8, None, None, None, None, 2, 0, 8, None)
+    assert rc == 1 and b"grad_weight_partials" in lib.bssm_last_error()
+    # No batch entries or channels: nothing to do, nothing required.
+    assert lib.bssm_causal_conv4_backward(1, None, 8, None, None, None, None, 0, 0, 8, None) == 0
