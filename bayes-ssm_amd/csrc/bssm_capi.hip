@@ -758,6 +758,25 @@ int bssm_causal_conv4_backward(int bf16, const void* x, int64_t ldx, const float
   return launched(fn, bssm::launch_conv4_backward(a, static_cast<hipStream_t>(stream)));
 }
 
+int bssm_causal_conv4_backward_noalloc(int bf16, const void* x, int64_t ldx, const float* weight,
+                                       const void* grad_y, void* grad_x, float* grad_weight, int64_t batch,
+                                       int64_t t, int64_t channels, void* stream) {
+  const char* fn = "bssm_causal_conv4_backward_noalloc";
+  if (int rc = conv_check(fn, bf16, x, ldx, weight, {grad_y, grad_x}, batch, t, channels)) return rc;
+  if (batch * channels * 4 > bssm::kConv4ScratchFloats)
+    return fail(BSSM_ERR_ARGUMENT, "%s: batch * channels = %lld exceeds the library scratch (at most %lld)", fn,
+                (long long)(batch * channels), (long long)(bssm::kConv4ScratchFloats / 4));
+  if (channels == 0) return ok();
+  // grad_weight is written (zeros without batch entries or tokens); the
+  // kernels read the weight whenever there are batch entries.
+  if (grad_weight == nullptr || !aligned16(grad_weight) || (batch > 0 && (weight == nullptr || !aligned16(weight))))
+    return fail(BSSM_ERR_ARGUMENT, "%s: weight and grad_weight must be non-null and 16-byte aligned", fn);
+  bssm::ConvArgs a{};
+  a.x = x; a.ldx = ldx; a.w = weight; a.gy = grad_y; a.gx = grad_x; a.gw_part = nullptr;
+  a.b = batch; a.t = t; a.c = channels; a.bf16 = bf16 != 0;
+  return launched(fn, bssm::launch_conv4_backward_noalloc(a, grad_weight, static_cast<hipStream_t>(stream)));
+}
+
 int bssm_associative_static_scan(const float* keys, const float* values, const float* queries,
                                  const float* observation, const float* mean0, const float* cov0, float* out,
                                  float* mean_final, float* cov_final, int64_t b, int64_t t, int key_dim,

@@ -23,8 +23,18 @@
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
+#include <mutex>
 
 #include "bssm_recurrence.h"
+
+// Device scratch of the allocation-free backward (launch_conv4_backward_noalloc):
+// the per-batch-entry weight-gradient partials [B, C, 4] of one call, reduced
+// over B by a second kernel on the same stream.  Every GPU holds its own copy
+// until the process ends; host code reaches it only through the address that
+// hipGetSymbolAddress returns for the current device (conv4_scratch below),
+// never through the name itself.  Calls that overlap on one GPU share it and
+// race; each call rewrites every slot it reads, so nothing needs clearing.
+static __device__ __align__(256) float scratch[bssm::kConv4ScratchFloats];
 
 namespace bssm {
 namespace conv4 {
@@ -245,8 +255,64 @@ __global__ __launch_bounds__(kWave * kWaves) void backward_kernel(ConvArgs a) {
   }
 }
 
+// Sum over the batch of the partials [B, C * 4]: one thread per (channel,
+// tap), four interleaved accumulators, a fixed order (deterministic).
+__global__ __launch_bounds__(256) void reduce_partials_kernel(const float* __restrict__ part,
+                                                              float* __restrict__ gw, int64_t b, int64_t cw) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (i >= cw) return;
+  float s0 = 0.f, s1 = 0.f, s2 = 0.f, s3 = 0.f;
+  int64_t k = 0;
+  for (; k + 4 <= b; k += 4) {
+    s0 += part[(k + 0) * cw + i];
+    s1 += part[(k + 1) * cw + i];
+    s2 += part[(k + 2) * cw + i];
+    s3 += part[(k + 3) * cw + i];
+  }
+  for (; k < b; ++k) s0 += part[k * cw + i];
+  gw[i] = (s0 + s1) + (s2 + s3);
+}
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mutex;
+float* g_scratch[kMaxDevices] = {};
+
+// Device address of `scratch` on the current device, looked up once per
+// device (with that device current) and kept.
+hipError_t conv4_scratch(float** out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return e;
+  if (dev < 0 || dev >= kMaxDevices) return hipErrorInvalidDevice;
+  std::lock_guard<std::mutex> lock(g_scratch_mutex);
+  if (g_scratch[dev] == nullptr) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return e;
+    g_scratch[dev] = static_cast<float*>(p);
+  }
+  *out = g_scratch[dev];
+  return hipSuccess;
+}
+
 }  // namespace
 }  // namespace conv4
+
+hipError_t launch_conv4_backward_noalloc(const ConvArgs& args, float* grad_weight, hipStream_t stream) {
+  float* part = nullptr;
+  hipError_t e = conv4::conv4_scratch(&part);
+  if (e != hipSuccess) return e;
+  ConvArgs a = args;
+  a.gw_part = part;
+  // Writes every [b, c, 4] slot the reduction reads (zeros when T = 0).
+  e = launch_conv4_backward(a, stream);
+  if (e != hipSuccess) return e;
+  const int64_t cw = a.c * 4;
+  if (cw == 0) return hipSuccess;
+  const dim3 grid(static_cast<unsigned>((cw + 255) / 256)), block(256);
+  hipLaunchKernelGGL(conv4::reduce_partials_kernel, grid, block, 0, stream, part, grad_weight, a.b, cw);
+  return hipGetLastError();
+}
 
 hipError_t launch_conv4_forward(const ConvArgs& a, hipStream_t stream) {
   const int64_t n = a.bf16 ? 8 : 4;

@@ -195,6 +195,12 @@ struct ConvArgs {
 };
 hipError_t launch_conv4_forward(const ConvArgs& a, hipStream_t stream);
 hipError_t launch_conv4_backward(const ConvArgs& a, hipStream_t stream);
+// The backward with the weight-gradient partials in the library's own device
+// scratch (kConv4ScratchFloats floats per GPU) and their sum over the batch
+// written to grad_weight [C, 4]; allocates nothing.  Needs b * c * 4 <=
+// kConv4ScratchFloats (checked by the caller).
+constexpr int64_t kConv4ScratchFloats = int64_t(1) << 21;
+hipError_t launch_conv4_backward_noalloc(const ConvArgs& a, float* grad_weight, hipStream_t stream);
 
 hipError_t launch_associative_scan(const float* k, const float* v, const float* q, const float* r,
                                    const float* m0, const float* c0, float* y, float* mT, float* cT,

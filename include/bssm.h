@@ -384,6 +384,21 @@ int bssm_causal_conv4_backward(int bf16, const void* x, int64_t ldx, const float
                                const void* grad_y, void* grad_x, float* grad_weight_partials,
                                int64_t batch, int64_t t, int64_t channels, void* stream);
 
+/* The reverse of bssm_causal_conv4_forward without any allocation: the same
+ * grad_x, and the weight gradient itself, grad_weight [C, 4] (float32, the
+ * sum over the batch of bssm_causal_conv4_backward's partials), with the
+ * per-batch-entry partials kept in the library's own device scratch (a
+ * file-scope array of 2^21 floats, 8 MiB, on every GPU the library runs on,
+ * held until the process ends) instead of a caller buffer.  Needs
+ * batch * channels <= 524288, else BSSM_ERR_ARGUMENT.  All calls on one GPU
+ * share the scratch: calls that overlap on that GPU (other streams or
+ * threads) race.  No counterpart in the reference library: it is for callers
+ * that cannot allocate (code under HIP graph capture, serving loops,
+ * harnesses that forbid hipMalloc). */
+int bssm_causal_conv4_backward_noalloc(int bf16, const void* x, int64_t ldx, const float* weight,
+                                       const void* grad_y, void* grad_x, float* grad_weight,
+                                       int64_t batch, int64_t t, int64_t channels, void* stream);
+
 /* ------------------------------------------------------------------------
  * The mixer core with its readout epilogue.  Replaces, after the op chain
  * of bssm_mixer_forward, the readout of example/train_6layer.py:719-729:

@@ -158,3 +158,12 @@ def test_conv_backward_checks_weight_and_partials_at_t0(lib):
     assert rc == 1 and b"grad_weight_partials" in lib.bssm_last_error()
     # No batch entries or channels: nothing to do, nothing required.
     assert lib.bssm_causal_conv4_backward(1, None, 8, None, None, None, None, 0, 0, 8, None) == 0
+
+
+def test_conv_backward_noalloc_rejects_sizes_beyond_its_scratch(lib):
+    """batch * channels above 524288 (2^21 scratch floats / 4 taps) is refused before any device work."""
+    rc = lib.bssm_causal_conv4_backward_noalloc(1, None, 1024, None, None, None, None, 513, 0, 1024, None)
+    assert rc == 1 and b"scratch" in lib.bssm_last_error()
+    rc = lib.bssm_causal_conv4_backward_noalloc(1, None, 8, None, None, None, None, 4, 0, 8, None)
+    assert rc == 1 and b"grad_weight" in lib.bssm_last_error()
+    assert lib.bssm_causal_conv4_backward_noalloc(1, None, 8, None, None, None, None, 4, 0, 0, None) == 0
