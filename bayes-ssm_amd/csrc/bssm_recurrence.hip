@@ -450,7 +450,7 @@ struct Tuning;
 template <> struct Tuning<1> { static constexpr int G = 8, TT = 32, SUB = 16; };
 template <> struct Tuning<2> { static constexpr int G = 4, TT = 16, SUB = 8; };
 template <> struct Tuning<4> { static constexpr int G = 4, TT = 16, SUB = 8; };
-template <> struct Tuning<8> { static constexpr int G = 8, TT = 16, SUB = 4; };
+template <> struct Tuning<8> { static constexpr int G = 8, TT = 16, SUB = 8; };
 
 template <int D, bool FIXED>
 hipError_t launch_forward_d(const FwdArgs& a, hipStream_t stream) {
