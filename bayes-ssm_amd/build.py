@@ -18,7 +18,7 @@ ROOT = Path(__file__).resolve().parent
 CSRC = ROOT / "csrc"
 OUT = Path(os.environ.get("BSSM_BUILD_OUT", ROOT / "bayes_ssm" / "libbssm_hip.so"))
 BUILD = Path(os.environ.get("BSSM_BUILD_DIR", ROOT / "_build"))
-# Extra compiler flags (e.g. -D tuning macros) for experiments.
+# Extra compiler flags (BSSM_EXTRA_FLAGS, space separated).
 EXTRA = os.environ.get("BSSM_EXTRA_FLAGS", "").split()
 ARCH = os.environ.get("BSSM_OFFLOAD_ARCH", "gfx950")
 

@@ -94,10 +94,10 @@ bool d1_backward_ok(const BwdArgs& a);
 hipError_t launch_forward_d1(bool fixed, const FwdArgs& a, hipStream_t stream);
 hipError_t launch_backward_d1(bool fixed, bool dyn, const BwdArgs& a, hipStream_t stream);
 
-// D = 2, M = 8 kernels with two value columns per lane (bssm_d2.hip).  Same
-// stream preconditions as the D = 1 kernels; the backward needs the
-// checkpoint chunk 8 (the library's preferred one for D = 2) and T a
-// positive multiple of 4.
+// D = 2, M = 8 kernels with two value columns per lane (bssm_d2.hip).  Both
+// need 16-byte aligned streams and T a multiple of 4 (the forward takes any
+// checkpoint chunk); the backward needs T > 0 and the checkpoint chunk 8
+// (the library's preferred one for D = 2).
 bool d2_forward_ok(const FwdArgs& a);
 bool d2_backward_ok(const BwdArgs& a);
 hipError_t launch_forward_d2(bool fixed, const FwdArgs& a, hipStream_t stream);

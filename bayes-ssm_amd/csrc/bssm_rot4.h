@@ -46,33 +46,19 @@ constexpr int TT = 8;     // forward tile, tokens
 constexpr int SUB = 8;    // backward checkpoint chunk, tokens
 constexpr int kDword3 = 0x00020000;  // raw fp32 buffer, gfx9 family
 constexpr uint32_t kOob = 0x80000000u;  // offset past every descriptor range: load 0, drop store
-#ifndef BSSM_R4_NT
-#define BSSM_R4_NT 7
-#endif
-// Nontemporal hints: bit 0 token-stream loads, bit 1 token-stream stores,
-// bit 2 checkpoint stores and loads.
-constexpr bool kNtLoad = (BSSM_R4_NT & 1) != 0;
+// Cache policies: token streams and checkpoints are loaded and stored with
+// the nontemporal hint (each byte moves once), except the 32- and 64-byte
+// row pieces (p, r and their gradients, covariance records), which stay
+// cached so that partial lines are merged before they reach HBM.
+constexpr bool kNtLoad = true;
 constexpr int kStoreNt = 2;  // gfx9 cache policy: nt
-constexpr int kNtStore = (BSSM_R4_NT & 2) ? kStoreNt : 0;
-constexpr bool kNtCkpt = (BSSM_R4_NT & 4) != 0;
-#ifndef BSSM_R4_SCHED
-#define BSSM_R4_SCHED 15
-#endif
-// Scheduling barriers between tokens: bit 0 forward tiles (every two
-// tokens), bit 1 backward replay, bit 2 backward reverse.  Bit 3 adds a
-// barrier right after each token's look-ahead LDS reads: without it the
-// scheduler sinks those reads to the end of the previous token's region, and
-// the token that consumes them waits out the whole LDS latency.
-constexpr bool kSchedFwd = (BSSM_R4_SCHED & 1) != 0;
-constexpr bool kSchedReplay = (BSSM_R4_SCHED & 2) != 0;
-constexpr bool kSchedReverse = (BSSM_R4_SCHED & 4) != 0;
-constexpr bool kFenceReads = (BSSM_R4_SCHED & 8) != 0;
-#ifndef BSSM_R4_GQ_AFTER
-#define BSSM_R4_GQ_AFTER 1
-#endif
-// dL/dq from the mean after the token (one row sum) instead of
-// d * (M_prev gy) + beta u (e.gy) (a row sum and a quad all-reduce).
-constexpr bool kGqAfter = BSSM_R4_GQ_AFTER != 0;
+constexpr int kNtStore = kStoreNt;
+constexpr bool kNtCkpt = true;
+// Tokens are separated by scheduling barriers (forward: every two tokens;
+// backward: every replayed and every reversed token), and each token's
+// look-ahead LDS reads are fenced right after their issue: without that
+// fence the scheduler sinks those reads to the end of the previous token's
+// region, and the token that consumes them waits out the whole LDS latency.
 
 typedef float v2f __attribute__((ext_vector_type(2)));
 using Rsrc = __amdgpu_buffer_rsrc_t;
@@ -361,8 +347,7 @@ __device__ __forceinline__ void reverse_step(const RevTok& in, const Hist& h, co
   for (int m = 0; m < 4; ++m) {
     av[m] = fmaf(gM[m][1], h.e[1], gM[m][0] * h.e[0]);
     Av[m] = fmaf(h.Mp[m][1], ge[1], h.Mp[m][0] * ge[0]);
-    if constexpr (kGqAfter) Cv[m] = fmaf(Mn[m][1], in.gy[1], Mn[m][0] * in.gy[0]);
-    else Cv[m] = fmaf(h.Mp[m][1], in.gy[1], h.Mp[m][0] * in.gy[0]);
+    Cv[m] = fmaf(Mn[m][1], in.gy[1], Mn[m][0] * in.gy[0]);
     float gb[2];
 #pragma unroll
     for (int c = 0; c < 2; ++c) {
@@ -374,12 +359,7 @@ __device__ __forceinline__ void reverse_step(const RevTok& in, const Hist& h, co
   const float a_g = reduce_scatter(av);
   const float A_g = reduce_scatter(Av);
   const float C_g = reduce_scatter(Cv);
-  if constexpr (kGqAfter) {
-    o.gq = C_g;
-  } else {
-    const float eg = quad_sum(fmaf(h.e[1], in.gy[1], h.e[0] * in.gy[0]));
-    o.gq = fmaf(in.dr[0], C_g, (beta * h.ug) * eg);
-  }
+  o.gq = C_g;
 
   float w = S[0] * ur[0];
 #pragma unroll
@@ -585,11 +565,11 @@ struct FwdCore {
       if (j + 1 < TT / 2) {
         read_in(tl, 2 * j + 2, x[2 * j + 2]);
         read_in(tl, 2 * j + 3, x[2 * j + 3]);
-        if constexpr (kFenceReads) __builtin_amdgcn_sched_barrier(0);
+        __builtin_amdgcn_sched_barrier(0);
       }
       step(x[2 * j], y[2 * j]);
       step(x[2 * j + 1], y[2 * j + 1]);
-      if constexpr (kSchedFwd) __builtin_amdgcn_sched_barrier(0);
+      __builtin_amdgcn_sched_barrier(0);
     }
 #pragma unroll
     for (int tt = 0; tt < TT; ++tt) put_y(tl, tt, y[tt]);
@@ -860,18 +840,18 @@ struct BwdCore {
     for (int tt = 0; tt < LEN; ++tt) {
       if (tt + 1 < LEN) read_tok(tl, tt + 1, x[tt + 1]);
       else read_rev(tl, LEN - 1, rx[LEN - 1]);
-      if constexpr (kFenceReads) __builtin_amdgcn_sched_barrier(0);
+      __builtin_amdgcn_sched_barrier(0);
       replay(b, x[tt], h[tt]);
-      if constexpr (kSchedReplay) __builtin_amdgcn_sched_barrier(0);
+      __builtin_amdgcn_sched_barrier(0);
     }
 #pragma unroll
     for (int tt = LEN - 1; tt >= 0; --tt) {
       if (tt > 0) read_rev(tl, tt - 1, rx[tt - 1]);
-      if constexpr (kFenceReads) __builtin_amdgcn_sched_barrier(0);
+      __builtin_amdgcn_sched_barrier(0);
       // The mean after token tt: the next token's history, or the replayed
       // belief after the chunk's last token.
       reverse(tl, tt, rx[tt], h[tt], tt + 1 < LEN ? h[tt + 1 < LEN ? tt + 1 : tt].Mp : b.Mv);
-      if constexpr (kSchedReverse) __builtin_amdgcn_sched_barrier(0);
+      __builtin_amdgcn_sched_barrier(0);
     }
   }
   // A chunk of `len` tokens (SUB, or 4 for the last one of T = 8n + 4).
