@@ -48,6 +48,7 @@ _SIGNATURES = {
     "bssm_forward_chunked_bf16": [_I, _I, _I] + [_P] * 8 + [_P] * 5 + [_L, _L, _L, _F, _P],
     "bssm_backward_chunked_bf16": [_I, _I, _I] + [_P] * 10 + [_P] * 3 + [_P] * 8 + [_L, _L, _L, _F, _P],
     "bssm_associative_static_scan": [_P] * 9 + [_L, _L, _I, _I, _P],
+    "bssm_associative_static_scan_backward": [_P] * 16 + [_L, _L, _I, _I, _P],
     "bssm_mixer_forward": [_P, _L] * 5 + [_P] * 7 + [_L, _L, _L, _L, _F, _P],
     "bssm_mixer_backward": [_P, _L] * 5 + [_P] * 7 + [_P] * 7 + [_L, _L, _L, _L, _F, _I, _P],
     "bssm_mixer_gated_forward": [_P, _L] * 6 + [_P, _F] + [_P] * 8 + [_L, _L, _L, _L, _F, _I, _P],

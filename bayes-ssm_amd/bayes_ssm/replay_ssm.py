@@ -166,7 +166,8 @@ def associative_static_bayesian(keys: Tensor, values: Tensor, queries: Tensor, *
 
 
 class _StaticScanFunction(torch.autograd.Function):
-    """HIP forward; the backward differentiates the torch-op scan (same math)."""
+    """HIP forward and, for key dims up to 16, HIP backward; larger key dims
+    differentiate the torch-op scan (same math)."""
 
     @staticmethod
     def forward(ctx, keys, values, queries, r2, mean0, cov0):
@@ -186,6 +187,12 @@ class _StaticScanFunction(torch.autograd.Function):
 
     @staticmethod
     def backward(ctx, g_out, g_mean, g_cov):
+        keys, values, queries, r2, mean0, cov0 = ctx.saved_tensors
+        b, t, d = keys.shape
+        m = values.shape[-1]
+        if d <= 16 and b <= 65535:
+            return _StaticScanFunction._hip_backward(ctx, keys, values, queries, r2, mean0, cov0, g_out, g_mean,
+                                                     g_cov)
         saved = [x.detach().requires_grad_(need) for x, need in zip(ctx.saved_tensors, ctx.needs_input_grad)]
         with torch.enable_grad():
             outs = associative_static_bayesian(saved[0], saved[1], saved[2], observation_variances=saved[3],
@@ -198,6 +205,31 @@ class _StaticScanFunction(torch.autograd.Function):
                 allow_unused=True)
         it = iter(grads)
         return tuple(next(it) if x.requires_grad else None for x in saved)
+
+    @staticmethod
+    def _hip_backward(ctx, keys, values, queries, r2, mean0, cov0, g_out, g_mean, g_cov):
+        from . import _hip
+
+        b, t, d = keys.shape
+        m = values.shape[-1]
+        dev = keys.device
+        f32 = lambda x: None if x is None else x.to(torch.float32).contiguous()  # noqa: E731
+        g_mean, g_cov = f32(g_mean), f32(g_cov)
+        if t == 0:
+            grads = (keys.new_zeros(keys.shape), values.new_zeros(values.shape), queries.new_zeros(queries.shape),
+                     r2.new_zeros(r2.shape), torch.zeros_like(mean0) if g_mean is None else g_mean,
+                     torch.zeros_like(cov0) if g_cov is None else g_cov)
+        else:
+            g_out = torch.zeros(b, t, m, device=dev) if g_out is None else f32(g_out)
+            grads = (torch.empty_like(keys), torch.empty_like(values), torch.empty_like(queries),
+                     torch.empty_like(r2), torch.empty_like(mean0), torch.empty_like(cov0))
+            ws = torch.empty(b * t * (d * d + d * m), device=dev, dtype=torch.float32)
+            P = _hip.ptr
+            with torch.cuda.device(dev):
+                _hip.call("bssm_associative_static_scan_backward", P(keys), P(values), P(queries), P(r2), P(mean0),
+                          P(cov0), P(g_out), P(g_mean), P(g_cov), P(ws), *map(P, grads), b, t, d, m,
+                          _hip.stream_of(dev))
+        return tuple(g if need else None for g, need in zip(grads, ctx.needs_input_grad))
 
 
 def associative_static_bayesian_cuda(keys: Tensor, values: Tensor, queries: Tensor, *,
@@ -225,7 +257,8 @@ def associative_static_bayesian_cuda(keys: Tensor, values: Tensor, queries: Tens
                                            initial_mean=initial_mean, initial_covariance=initial_covariance,
                                            denominator_floor=denominator_floor)
     batch = keys_p.shape[:-2]
-    flat = lambda x, tail: x.reshape(-1, *tail).contiguous()  # noqa: E731
+    rows = math.prod(batch)
+    flat = lambda x, tail: x.reshape(rows, *tail).contiguous()  # noqa: E731
     out, mT, cT = _StaticScanFunction.apply(flat(keys_p, (t, d)), flat(values_p, (t, m)), flat(queries_p, (t, d)),
                                             flat(r2, (t,)), flat(mean0, (d, m)), flat(cov0, (d, d)))
     return out.reshape(*batch, t, m), mT.reshape(*batch, d, m), cT.reshape(*batch, d, d)

@@ -802,4 +802,38 @@ int bssm_associative_static_scan(const float* keys, const float* values, const f
                                                     static_cast<hipStream_t>(stream)));
 }
 
+int bssm_associative_static_scan_backward(const float* keys, const float* values, const float* queries,
+                                          const float* observation, const float* mean0, const float* cov0,
+                                          const float* grad_out, const float* grad_mean_final,
+                                          const float* grad_cov_final, float* workspace, float* grad_keys,
+                                          float* grad_values, float* grad_queries, float* grad_observation,
+                                          float* grad_mean0, float* grad_cov0, int64_t b, int64_t t, int key_dim,
+                                          int value_dim, void* stream) {
+  const char* fn = "bssm_associative_static_scan_backward";
+  if (key_dim <= 0 || key_dim > bssm::kMaxBackwardD || value_dim <= 0 || value_dim > 64)
+    return fail(BSSM_ERR_UNSUPPORTED, "%s: needs 0 < key_dim <= %d and 0 < value_dim <= 64, got (%d, %d)", fn,
+                bssm::kMaxBackwardD, key_dim, value_dim);
+  if (b < 0 || t <= 0) return fail(BSSM_ERR_ARGUMENT, "%s: needs b >= 0 and t >= 1", fn);
+  if (b > 65535 || t > 0x7fffffff) return fail(BSSM_ERR_ARGUMENT, "%s: b or t too large", fn);
+  const int64_t n = b;
+  BSSM_REQUIRE(keys);
+  BSSM_REQUIRE(values);
+  BSSM_REQUIRE(queries);
+  BSSM_REQUIRE(observation);
+  BSSM_REQUIRE(mean0);
+  BSSM_REQUIRE(cov0);
+  BSSM_REQUIRE(grad_out);
+  BSSM_REQUIRE(workspace);
+  BSSM_REQUIRE(grad_keys);
+  BSSM_REQUIRE(grad_values);
+  BSSM_REQUIRE(grad_queries);
+  BSSM_REQUIRE(grad_observation);
+  BSSM_REQUIRE(grad_mean0);
+  BSSM_REQUIRE(grad_cov0);
+  return launched(fn, bssm::launch_associative_scan_backward(
+                          keys, values, queries, observation, mean0, cov0, grad_out, grad_mean_final, grad_cov_final,
+                          workspace, grad_keys, grad_values, grad_queries, grad_observation, grad_mean0, grad_cov0, b,
+                          t, key_dim, value_dim, static_cast<hipStream_t>(stream)));
+}
+
 }  // extern "C"

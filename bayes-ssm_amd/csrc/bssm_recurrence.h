@@ -205,6 +205,14 @@ hipError_t launch_conv4_backward_noalloc(const ConvArgs& a, float* grad_weight, 
 hipError_t launch_associative_scan(const float* k, const float* v, const float* q, const float* r,
                                    const float* m0, const float* c0, float* y, float* mT, float* cT,
                                    int64_t b, int64_t t, int d, int m, hipStream_t stream);
+// Reverse of the scan for key dims up to kMaxBackwardD (value dims up to 64),
+// T >= 1; ws holds b * t * (d * d + d * m) floats; gmT, gcT may be null.
+constexpr int kMaxBackwardD = 16;
+hipError_t launch_associative_scan_backward(const float* k, const float* v, const float* q, const float* r,
+                                            const float* m0, const float* c0, const float* gy, const float* gmT,
+                                            const float* gcT, float* ws, float* gk, float* gv, float* gq, float* gr,
+                                            float* gm0, float* gc0, int64_t b, int64_t t, int d, int m,
+                                            hipStream_t stream);
 
 // Checkpoint interval at which the replay backward needs no in-chunk replay
 // restarts (the register-history length for this key dimension).

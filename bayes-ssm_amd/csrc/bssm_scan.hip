@@ -126,23 +126,16 @@ __device__ __forceinline__ float ld_or_zero(const float* p, int i, int n) {
   return i < n ? x : 0.f;
 }
 
+// The state of token t of batch row b, shared by the forward and the
+// backward: on return the row owners hold row i of inv(P0) (lam0), LDS
+// `mat` / `idg` hold the Cholesky factor of L_t and 1 / its diagonal, and the
+// column owners hold column c of M_t = L_t^{-1} N_t in x.
 template <int D, bool EXACT>
-__global__ __launch_bounds__(kWave) void associative_scan_kernel(const float* __restrict__ keys,
-                                                                 const float* __restrict__ values,
-                                                                 const float* __restrict__ queries,
-                                                                 const float* __restrict__ obs,
-                                                                 const float* __restrict__ mean0,
-                                                                 const float* __restrict__ cov0,
-                                                                 float* __restrict__ out, float* __restrict__ mT,
-                                                                 float* __restrict__ cT, int64_t T, int Dr_, int M) {
-  // EXACT: the runtime key dimension equals D (no padding masks at all).
-  const int Dr = EXACT ? D : Dr_;
-  __shared__ float mat[D * D];   // a factor or inv(P0), row-major
-  __shared__ float tr[D * D];    // transpose staging for the symmetrization
-  __shared__ float idg[D];       // 1 / diag of the factor in mat
-  const int lane = threadIdx.x;
-  const int64_t b = blockIdx.y;
-  const int64_t t = blockIdx.x;
+__device__ __forceinline__ void token_state(const float* __restrict__ keys, const float* __restrict__ values,
+                                            const float* __restrict__ obs, const float* __restrict__ mean0,
+                                            const float* __restrict__ cov0, int64_t T, int Dr, int M, int64_t b,
+                                            int64_t t, int lane, float* mat, float* tr, float* idg,
+                                            float (&lam0)[D], float (&x)[D]) {
   const bool row_lane = lane < Dr, col_lane = lane < M;
   const int rl = row_lane ? lane : 0, cl = col_lane ? lane : 0;
 
@@ -157,7 +150,6 @@ __global__ __launch_bounds__(kWave) void associative_scan_kernel(const float* __
   }
   chol_rows<D>(l, inv_diag, lane, mat, idg);
   __syncthreads();
-  float lam0[D];
 #pragma unroll
   for (int j = 0; j < D; ++j) lam0[j] = lane == j ? 1.f : 0.f;
   chol_solve<D>(mat, idg, lam0);
@@ -166,7 +158,7 @@ __global__ __launch_bounds__(kWave) void associative_scan_kernel(const float* __
   __syncthreads();
 
   // N_t column c starts at inv(P0) M0[:, c].
-  float x[D], m0c[D];
+  float m0c[D];
   const float* M0 = mean0 + b * Dr * M + cl;
 #pragma unroll
   for (int k = 0; k < D; ++k) {
@@ -227,6 +219,28 @@ __global__ __launch_bounds__(kWave) void associative_scan_kernel(const float* __
   chol_rows<D>(lam, inv_lam, lane, mat, idg);  // mat = factor of L_t
   __syncthreads();
   chol_solve<D>(mat, idg, x);
+}
+
+template <int D, bool EXACT>
+__global__ __launch_bounds__(kWave) void associative_scan_kernel(const float* __restrict__ keys,
+                                                                 const float* __restrict__ values,
+                                                                 const float* __restrict__ queries,
+                                                                 const float* __restrict__ obs,
+                                                                 const float* __restrict__ mean0,
+                                                                 const float* __restrict__ cov0,
+                                                                 float* __restrict__ out, float* __restrict__ mT,
+                                                                 float* __restrict__ cT, int64_t T, int Dr_, int M) {
+  // EXACT: the runtime key dimension equals D (no padding masks at all).
+  const int Dr = EXACT ? D : Dr_;
+  __shared__ float mat[D * D];   // a factor or inv(P0), row-major
+  __shared__ float tr[D * D];    // transpose staging for the symmetrization
+  __shared__ float idg[D];       // 1 / diag of the factor in mat
+  const int lane = threadIdx.x;
+  const int64_t b = blockIdx.y;
+  const int64_t t = blockIdx.x;
+  const bool row_lane = lane < Dr, col_lane = lane < M;
+  float lam0[D], x[D];
+  token_state<D, EXACT>(keys, values, obs, mean0, cov0, T, Dr, M, b, t, lane, mat, tr, idg, lam0, x);
 
   const bool last = (t == T - 1);
   if (col_lane) {
@@ -251,6 +265,254 @@ __global__ __launch_bounds__(kWave) void associative_scan_kernel(const float* __
 #pragma unroll
       for (int i = 0; i < D; ++i)
         if (i < Dr) cT[(b * Dr + i) * Dr + lane] = e[i];
+    }
+  }
+}
+
+// ------------------------------------------------------------------ backward
+// Reverse of the scan (the chain rule of replay_ssm.py:251-270).  With
+// G_t = q_t gy_t^T (+ gM_T at the last token) the adjoint of M_t:
+//   gq_t = M_t gy_t,   gN_t = L_t^{-1} G_t,
+//   gL_t = sym(-gN_t M_t^T)  (+ sym(-P_T gP_T P_T) at the last token),
+// where sym is the symmetrization the forward applies to L_t.  With the
+// suffix sums SL_s = sum_{t>=s} gL_t and SN_s = sum_{t>=s} gN_t of the
+// prefix terms k_s k_s^T / r_s and k_s v_s^T / r_s:
+//   gk_s = (2 SL_s k_s + SN_s v_s) / r_s,   gv_s = SN_s^T k_s / r_s,
+//   gr_s = -(k_s^T SL_s k_s + k_s^T SN_s v_s) / r_s^2,
+// and for the prior (L_0 = inv(P0), N_0 = inv(P0) M0):
+//   gM0 = inv(P0) SN_0,   gP0 = -inv(P0)^T (SL_0 + SN_0 M0^T) inv(P0)^T.
+// Pass 1 (one wave per (b, t)) writes gq, gN_t and gL_t (workspace); pass 2
+// (one wave per (b, s)) forms the suffix sums and the per-token gradients,
+// and the s = 0 wave the prior's.
+template <int D, bool EXACT>
+__global__ __launch_bounds__(kWave) void scan_backward_token_kernel(
+    const float* __restrict__ keys, const float* __restrict__ values, const float* __restrict__ queries,
+    const float* __restrict__ obs, const float* __restrict__ mean0, const float* __restrict__ cov0,
+    const float* __restrict__ gy, const float* __restrict__ gmT, const float* __restrict__ gcT,
+    float* __restrict__ ws_gl, float* __restrict__ ws_gn, float* __restrict__ gq, int64_t T, int Dr_, int M) {
+  const int Dr = EXACT ? D : Dr_;
+  __shared__ float mat[D * D];
+  __shared__ float tr[D * D];
+  __shared__ float idg[D];
+  __shared__ float mt[D * kMaxM];   // M_t, row-major
+  __shared__ float gn[D * kMaxM];   // gN_t, row-major
+  __shared__ float pt[D * D];       // P_T (last token), then P_T gP_T
+  __shared__ float gys[kMaxM];
+  const int lane = threadIdx.x;
+  const int64_t b = blockIdx.y;
+  const int64_t t = blockIdx.x;
+  const bool row_lane = lane < Dr, col_lane = lane < M;
+  float lam0[D], x[D];
+  token_state<D, EXACT>(keys, values, obs, mean0, cov0, T, Dr, M, b, t, lane, mat, tr, idg, lam0, x);
+  const bool last = (t == T - 1);
+  const float* qt = queries + (b * T + t) * Dr;
+
+  // Column owners: G[:, c] = q_t gy_t[c] (+ gM_T[:, c]), then gN[:, c] = L_t^{-1} G[:, c].
+  float g[D];
+  const float gyc = col_lane ? gy[(b * T + t) * M + lane] : 0.f;
+#pragma unroll
+  for (int i = 0; i < D; ++i) {
+    float v = ld_or_zero(qt, i, Dr) * gyc;
+    if (last && gmT != nullptr && col_lane && i < Dr) v += gmT[(b * Dr + i) * M + lane];
+    g[i] = col_lane ? v : 0.f;
+  }
+  chol_solve<D>(mat, idg, g);
+  if (col_lane) {
+    gys[lane] = gyc;
+#pragma unroll
+    for (int i = 0; i < D; ++i) {
+      mt[i * kMaxM + lane] = x[i];
+      gn[i * kMaxM + lane] = g[i];
+      if (i < Dr) ws_gn[((b * T + t) * Dr + i) * M + lane] = g[i];
+    }
+  }
+  // P_T for the last token's covariance adjoint.
+  if (last && gcT != nullptr) {
+    float e[D];
+#pragma unroll
+    for (int i = 0; i < D; ++i) e[i] = lane == i ? 1.f : 0.f;
+    chol_solve<D>(mat, idg, e);  // lane c < D: column c of P_T (= row c)
+    if (lane < D) {
+#pragma unroll
+      for (int i = 0; i < D; ++i) pt[lane * D + i] = e[i];
+    }
+  }
+  __syncthreads();
+  // Row owners: gq_t[i] = sum_c M_t[i, c] gy_t[c] and row i of -gN_t M_t^T.
+  float gl[D];
+  if (lane < D) {
+    float acc = 0.f;
+    for (int c = 0; c < M; ++c) acc = fmaf(mt[lane * kMaxM + c], gys[c], acc);
+    if (row_lane) gq[(b * T + t) * Dr + lane] = acc;
+#pragma unroll
+    for (int j = 0; j < D; ++j) {
+      float a = 0.f;
+      for (int c = 0; c < M; ++c) a = fmaf(gn[lane * kMaxM + c], mt[j * kMaxM + c], a);
+      gl[j] = -a;
+    }
+  }
+  if (last && gcT != nullptr && lane < D) {
+    // -(P_T gP_T P_T)[i][:]: row i of A = P_T gP_T in registers, then A P_T
+    // (gP_T and the padded block of P_T: zero and the identity).
+    float a[D];
+#pragma unroll
+    for (int j = 0; j < D; ++j) {
+      float acc = 0.f;
+#pragma unroll
+      for (int k = 0; k < D; ++k) {
+        const float gkj = (k < Dr && j < Dr) ? gcT[(b * Dr + k) * Dr + j] : 0.f;
+        acc = fmaf(pt[lane * D + k], gkj, acc);
+      }
+      a[j] = acc;
+    }
+#pragma unroll
+    for (int j = 0; j < D; ++j) {
+      float acc = 0.f;
+#pragma unroll
+      for (int k = 0; k < D; ++k) acc = fmaf(a[k], pt[k * D + j], acc);
+      gl[j] -= acc;
+    }
+  }
+  // Symmetrize through LDS and store row i of gL_t.
+  __syncthreads();
+  if (lane < D) {
+#pragma unroll
+    for (int j = 0; j < D; ++j) tr[j * D + lane] = gl[j];
+  }
+  __syncthreads();
+  if (row_lane) {
+#pragma unroll
+    for (int j = 0; j < D; ++j)
+      if (j < Dr) ws_gl[((b * T + t) * Dr + lane) * Dr + j] = (gl[j] + tr[lane * D + j]) * 0.5f;
+  }
+}
+
+template <int D, bool EXACT>
+__global__ __launch_bounds__(kWave) void scan_backward_prefix_kernel(
+    const float* __restrict__ keys, const float* __restrict__ values, const float* __restrict__ obs,
+    const float* __restrict__ mean0, const float* __restrict__ cov0, const float* __restrict__ ws_gl,
+    const float* __restrict__ ws_gn, float* __restrict__ gk, float* __restrict__ gv, float* __restrict__ gr,
+    float* __restrict__ gm0, float* __restrict__ gc0, int64_t T, int Dr_, int M) {
+  const int Dr = EXACT ? D : Dr_;
+  __shared__ float mat[D * D];
+  __shared__ float idg[D];
+  __shared__ float sn[D * kMaxM];  // SN_s, row-major
+  __shared__ float part[kWave];
+  const int lane = threadIdx.x;
+  const int64_t b = blockIdx.y;
+  const int64_t s = blockIdx.x;
+  const bool row_lane = lane < Dr, col_lane = lane < M;
+  const int rl = row_lane ? lane : 0;
+  // Suffix sums over t >= s: row owners row i of SL, column owners column c of SN.
+  float sl[D], snc[D];
+#pragma unroll
+  for (int j = 0; j < D; ++j) {
+    sl[j] = 0.f;
+    snc[j] = 0.f;
+  }
+  for (int64_t t = T - 1; t >= s; --t) {
+    const float* glt = ws_gl + ((b * T + t) * Dr + rl) * Dr;
+    const float* gnt = ws_gn + (b * T + t) * Dr * M + (col_lane ? lane : 0);
+#pragma unroll
+    for (int j = 0; j < D; ++j) {
+      if (row_lane && j < Dr) sl[j] += glt[j];
+      if (col_lane && j < Dr) snc[j] += gnt[j * M];
+    }
+  }
+  if (col_lane) {
+#pragma unroll
+    for (int i = 0; i < D; ++i) sn[i * kMaxM + lane] = snc[i];
+  }
+  __syncthreads();
+  const float* ks = keys + (b * T + s) * Dr;
+  const float* vs = values + (b * T + s) * M;
+  const float rinv = 1.0f / obs[b * T + s];
+  // gk_s[i] = (2 (SL k)_i + (SN v)_i) / r;  k^T SL k and k^T SN v for gr.
+  float contrib = 0.f;
+  if (row_lane) {
+    float a = 0.f, n = 0.f;
+#pragma unroll
+    for (int j = 0; j < D; ++j) a = fmaf(sl[j], ld_or_zero(ks, j, Dr), a);
+    for (int c = 0; c < M; ++c) n = fmaf(sn[lane * kMaxM + c], vs[c], n);
+    gk[(b * T + s) * Dr + lane] = (2.f * a + n) * rinv;
+    contrib = ks[lane] * (a + n);
+  }
+  part[lane] = contrib;
+  if (col_lane) {
+    float a = 0.f;
+#pragma unroll
+    for (int i = 0; i < D; ++i) a = fmaf(snc[i], ld_or_zero(ks, i, Dr), a);
+    gv[(b * T + s) * M + lane] = a * rinv;
+  }
+  __syncthreads();
+  if (lane == 0) {
+    float z = 0.f;
+    for (int i = 0; i < Dr; ++i) z += part[i];
+    gr[b * T + s] = -z * rinv * rinv;
+  }
+  if (s != 0) return;
+  // The prior: inv(P0) again (as in the forward), then
+  // gM0 = inv(P0) SN_0 and gP0 = -inv(P0)^T (SL_0 + SN_0 M0^T) inv(P0)^T.
+  float l[D], inv_diag = 1.f;
+  const float* P0 = cov0 + (b * Dr + rl) * Dr;
+#pragma unroll
+  for (int j = 0; j < D; ++j) {
+    const float v = ld_or_zero(P0, j, Dr);
+    l[j] = row_lane ? v : (lane == j ? 1.f : 0.f);
+  }
+  __syncthreads();
+  chol_rows<D>(l, inv_diag, lane, mat, idg);
+  __syncthreads();
+  float lam0[D];
+#pragma unroll
+  for (int j = 0; j < D; ++j) lam0[j] = lane == j ? 1.f : 0.f;
+  chol_solve<D>(mat, idg, lam0);  // lane i < D: column i of inv(P0)
+  __syncthreads();
+  rows_to_lds<D>(lam0, mat, lane);  // mat = inv(P0)^T, row i = column i of inv(P0)
+  __syncthreads();
+  if (col_lane) {
+    // gM0[i][c] = sum_k inv(P0)[i][k] SN[k][c]
+#pragma unroll
+    for (int i = 0; i < D; ++i) {
+      float a = 0.f;
+#pragma unroll
+      for (int k = 0; k < D; ++k) a = fmaf(mat[k * D + i], snc[k], a);
+      if (i < Dr) gm0[(b * Dr + i) * M + lane] = a;
+    }
+  }
+  // gA = SL_0 + SN_0 M0^T (row owners, row i), then gP0 = -inv(P0)^T gA inv(P0)^T.
+  float ga[D];
+  if (lane < D) {
+    const float* M0 = mean0 + b * Dr * M;
+#pragma unroll
+    for (int j = 0; j < D; ++j) {
+      float a = sl[j];
+      if (row_lane && j < Dr)
+        for (int c = 0; c < M; ++c) a = fmaf(sn[lane * kMaxM + c], M0[j * M + c], a);
+      ga[j] = a;
+    }
+  }
+  __syncthreads();
+  float* tmp = sn;  // reuse: [D][D] rows of gA inv(P0)^T
+  if (lane < D) {
+#pragma unroll
+    for (int j = 0; j < D; ++j) {
+      // (gA inv(P0)^T)[i][j] = sum_k gA[i][k] inv(P0)[j][k]
+      float a = 0.f;
+#pragma unroll
+      for (int k = 0; k < D; ++k) a = fmaf(ga[k], mat[k * D + j], a);
+      tmp[lane * D + j] = a;
+    }
+  }
+  __syncthreads();
+  if (row_lane) {
+#pragma unroll
+    for (int j = 0; j < D; ++j) {
+      // gP0[i][j] = -sum_k inv(P0)[k][i] (gA inv(P0)^T)[k][j]
+      float a = 0.f;
+#pragma unroll
+      for (int k = 0; k < D; ++k) a = fmaf(mat[lane * D + k], tmp[k * D + j], a);
+      if (j < Dr) gc0[(b * Dr + lane) * Dr + j] = -a;
     }
   }
 }
@@ -397,7 +659,44 @@ hipError_t launch_scan(const float* k, const float* v, const float* q, const flo
   return hipGetLastError();
 }
 
+template <int D>
+hipError_t launch_scan_backward(const float* k, const float* v, const float* q, const float* r, const float* m0,
+                                const float* c0, const float* gy, const float* gmT, const float* gcT, float* ws,
+                                float* gk, float* gv, float* gq, float* gr, float* gm0, float* gc0, int64_t b,
+                                int64_t t, int d, int m, hipStream_t stream) {
+  const dim3 grid(static_cast<unsigned>(t), static_cast<unsigned>(b));
+  float* ws_gl = ws;
+  float* ws_gn = ws + b * t * d * d;
+  if (d == D) {
+    hipLaunchKernelGGL((scan_backward_token_kernel<D, true>), grid, dim3(kWave), 0, stream, k, v, q, r, m0, c0, gy,
+                       gmT, gcT, ws_gl, ws_gn, gq, t, d, m);
+    hipLaunchKernelGGL((scan_backward_prefix_kernel<D, true>), grid, dim3(kWave), 0, stream, k, v, r, m0, c0, ws_gl,
+                       ws_gn, gk, gv, gr, gm0, gc0, t, d, m);
+  } else {
+    hipLaunchKernelGGL((scan_backward_token_kernel<D, false>), grid, dim3(kWave), 0, stream, k, v, q, r, m0, c0, gy,
+                       gmT, gcT, ws_gl, ws_gn, gq, t, d, m);
+    hipLaunchKernelGGL((scan_backward_prefix_kernel<D, false>), grid, dim3(kWave), 0, stream, k, v, r, m0, c0, ws_gl,
+                       ws_gn, gk, gv, gr, gm0, gc0, t, d, m);
+  }
+  return hipGetLastError();
+}
+
 }  // namespace
+
+hipError_t launch_associative_scan_backward(const float* k, const float* v, const float* q, const float* r,
+                                            const float* m0, const float* c0, const float* gy, const float* gmT,
+                                            const float* gcT, float* ws, float* gk, float* gv, float* gq, float* gr,
+                                            float* gm0, float* gc0, int64_t b, int64_t t, int d, int m,
+                                            hipStream_t stream) {
+  if (d > kMaxBackwardD || m > kMaxM || d <= 0 || m <= 0 || t <= 0 || t > 0x7fffffff || b > 65535)
+    return hipErrorInvalidValue;
+  if (b == 0) return hipSuccess;
+  if (d <= 1) return launch_scan_backward<1>(k, v, q, r, m0, c0, gy, gmT, gcT, ws, gk, gv, gq, gr, gm0, gc0, b, t, d, m, stream);
+  if (d <= 2) return launch_scan_backward<2>(k, v, q, r, m0, c0, gy, gmT, gcT, ws, gk, gv, gq, gr, gm0, gc0, b, t, d, m, stream);
+  if (d <= 4) return launch_scan_backward<4>(k, v, q, r, m0, c0, gy, gmT, gcT, ws, gk, gv, gq, gr, gm0, gc0, b, t, d, m, stream);
+  if (d <= 8) return launch_scan_backward<8>(k, v, q, r, m0, c0, gy, gmT, gcT, ws, gk, gv, gq, gr, gm0, gc0, b, t, d, m, stream);
+  return launch_scan_backward<16>(k, v, q, r, m0, c0, gy, gmT, gcT, ws, gk, gv, gq, gr, gm0, gc0, b, t, d, m, stream);
+}
 
 hipError_t launch_associative_scan(const float* k, const float* v, const float* q, const float* r,
                                    const float* m0, const float* c0, float* y, float* mT, float* cT,

@@ -273,6 +273,29 @@ int bssm_associative_static_scan(const float* keys, const float* values, const f
                                  int64_t b, int64_t t, int key_dim, int value_dim,
                                  void* stream);
 
+/* Reverse of bssm_associative_static_scan.  Replaces the autograd of the
+ * differentiable torch-op chain behind associative_static_bayesian_cuda
+ * (bayes_ssm/replay_ssm.py:251-270, :276-339): given grad_out [B,T,M] and
+ * the (optional, NULL = zero) grad_mean_final [B,D,M] / grad_cov_final
+ * [B,D,D], writes the gradients of keys, values, queries [B,T,*],
+ * observation [B,T], mean0 [B,D,M] and cov0 [B,D,D].  With
+ * G_t = q_t gy_t^T (+ grad_mean_final at the last token):
+ *   gq_t = M_t gy_t,  gN_t = L_t^{-1} G_t,
+ *   gL_t = sym(-gN_t M_t^T) (+ sym(-P_T grad_cov_final P_T) at the last token),
+ * suffix sums SL_s, SN_s of gL_t, gN_t over t >= s, and
+ *   gk_s = (2 SL_s k_s + SN_s v_s) / r_s,  gv_s = SN_s^T k_s / r_s,
+ *   gr_s = -(k_s^T SL_s k_s + k_s^T SN_s v_s) / r_s^2,
+ *   gM0 = inv(P0)^T SN_0,  gP0 = -inv(P0)^T (SL_0 + SN_0 M0^T) inv(P0)^T.
+ * workspace: B * T * (D * D + D * M) floats (the caller's).  Supports
+ * key_dim <= 16, value_dim <= 64 and T >= 1. */
+int bssm_associative_static_scan_backward(const float* keys, const float* values, const float* queries,
+                                          const float* observation, const float* mean0, const float* cov0,
+                                          const float* grad_out, const float* grad_mean_final,
+                                          const float* grad_cov_final, float* workspace,
+                                          float* grad_keys, float* grad_values, float* grad_queries,
+                                          float* grad_observation, float* grad_mean0, float* grad_cov0,
+                                          int64_t b, int64_t t, int key_dim, int value_dim, void* stream);
+
 /* ------------------------------------------------------------------------
  * Producer-fused layer core of the Bayes mixer (D = 4, M = 8, learned
  * dynamics).  Replaces the torch-op chain between the projections and the

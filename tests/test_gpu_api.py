@@ -73,6 +73,67 @@ def test_associative_scan_cuda_gradients(cuda_device):
         close(x.grad, e.grad, "grad " + name)
 
 
+@pytest.mark.parametrize("b,t,d,m,with_final", [
+    (2, 1, 4, 8, True), (2, 33, 1, 1, True), (3, 17, 3, 7, True), (2, 9, 2, 64, True), (2, 40, 8, 8, False),
+    (1, 20, 16, 33, True), (2, 12, 13, 20, False), (2, 65, 5, 64, True), (4, 64, 16, 16, True),
+    (2, 300, 4, 8, True)])
+def test_associative_scan_hip_backward_shapes(cuda_device, monkeypatch, b, t, d, m, with_final):
+    """The HIP scan backward (key dims <= 16, exact and padded) against the oracle's autograd; without
+    final-state gradients the kernel takes null pointers for them."""
+    rs = importlib.import_module("bayes_ssm.replay_ssm")
+    calls = _count(monkeypatch, rs._StaticScanFunction, "_hip_backward")
+    print(f"scan backward b={b} t={t} d={d} m={m} final={with_final}", flush=True)
+    k, v, q, r = O.make_scan_inputs(b, t, d, m, seed=40 + d + t)
+    g = torch.Generator().manual_seed(41 + m)
+    a = torch.randn(b, d, d, generator=g) / d ** 0.5
+    c0 = a @ a.transpose(-1, -2) + 0.5 * torch.eye(d)
+    m0 = torch.randn(b, d, m, generator=g)
+    gy = torch.randn(b, t, m, generator=g)
+    gm = torch.randn(b, d, m, generator=g)
+    gc = torch.randn(b, d, d, generator=g)
+    leaves = [x.to(cuda_device).requires_grad_(True) for x in (k, v, q, r, m0, c0)]
+    y, mT, cT = bayes_ssm.associative_static_bayesian_cuda(
+        leaves[0], leaves[1], leaves[2], observation_variances=leaves[3], initial_mean=leaves[4],
+        initial_covariance=leaves[5])
+    el = [x.double().requires_grad_(True) for x in (k, v, q, r, m0, c0)]
+    ey, em, ec = O.associative_static(*el[:4], el[4], el[5])
+    if with_final:
+        torch.autograd.backward([y, mT, cT], [gy.to(cuda_device), gm.to(cuda_device), gc.to(cuda_device)])
+        torch.autograd.backward([ey, em, ec], [gy.double(), gm.double(), gc.double()])
+    else:
+        y.backward(gy.to(cuda_device))
+        ey.backward(gy.double())
+    assert calls, "the HIP scan backward was not used"
+    for name, x, e in zip(("k", "v", "q", "r", "mean0", "cov0"), leaves, el):
+        close(x.grad, e.grad, "grad " + name)
+
+
+def test_associative_scan_hip_backward_partial_inputs(cuda_device):
+    """Only some inputs need gradients; an empty sequence passes the final-state gradients to the prior."""
+    k, v, q, r = O.make_scan_inputs(2, 10, 4, 6, seed=50)
+    gy = torch.randn(2, 10, 6, generator=torch.Generator().manual_seed(51))
+    kk = k.to(cuda_device).requires_grad_(True)
+    y, _, _ = bayes_ssm.associative_static_bayesian_cuda(kk, v.to(cuda_device), q.to(cuda_device),
+                                                         observation_variances=r.to(cuda_device))
+    y.backward(gy.to(cuda_device))
+    ek = k.double().requires_grad_(True)
+    ey, _, _ = O.associative_static(ek, v.double(), q.double(), r.double())
+    ey.backward(gy.double())
+    close(kk.grad, ek.grad, "grad k")
+
+    m0 = torch.randn(2, 4, 6, device=cuda_device, requires_grad=True)
+    c0 = (2.0 * torch.eye(4, device=cuda_device)).expand(2, 4, 4).contiguous().requires_grad_(True)
+    empty_k = torch.zeros(2, 0, 4, device=cuda_device, requires_grad=True)
+    y0, mT, cT = bayes_ssm.associative_static_bayesian_cuda(empty_k, torch.zeros(2, 0, 6, device=cuda_device),
+                                                            torch.zeros(2, 0, 4, device=cuda_device),
+                                                            initial_mean=m0, initial_covariance=c0)
+    assert y0.shape == (2, 0, 6)
+    gm, gc = torch.randn_like(mT), torch.randn_like(cT)
+    torch.autograd.backward([mT, cT], [gm, gc])
+    close(m0.grad, gm, "grad mean0 (T = 0)")
+    close(c0.grad, gc, "grad cov0 (T = 0)")
+
+
 def test_scalar_noise_reaches_the_fused_kernels(cuda_device, monkeypatch):
     """Scalar process/observation noise expand to stride-0 [N, T] views that the gate makes contiguous."""
     from bayes_ssm import fused_cuda
