@@ -358,6 +358,78 @@ def bayes_mixer_readout(
     return out, mean_t, cov_t
 
 
+class _MixerBlockFunction(torch.autograd.Function):
+    """Autograd boundary of config 4's block kernels (C ABI ``bssm_mixer_block_*``): the filter and the
+    gated readout in one call per direction, the projection gradient written in place column by column."""
+
+    @staticmethod
+    def forward(ctx, projected, conv_weight, norm_weight, aux_bias, mean0, cov0, heads, norm_eps, denominator_floor,
+                ld):
+        b, t, _ = projected.shape
+        core, aux_w = 16 * heads, 6 * heads
+        interval = _hip.preferred_checkpoint(KEY_DIM)
+        nb = -(-t // interval)
+        dev = projected.device
+        # The aux bias is added in bf16 as the reference does (one rounding).
+        aux = None if aux_bias is None else (projected[..., core:core + aux_w] + aux_bias).contiguous()
+        convolved = torch.empty(b, t, core, device=dev, dtype=torch.bfloat16)
+        out = torch.empty(b, t, heads * VALUE_DIM, device=dev, dtype=torch.bfloat16)
+        read_bf16 = torch.empty_like(out)
+        n = b * heads
+        mean_t = torch.empty(n, KEY_DIM, VALUE_DIM, device=dev, dtype=torch.float32)
+        cov_t = torch.empty(n, KEY_DIM, KEY_DIM, device=dev, dtype=torch.float32)
+        bmean = torch.empty(n, nb + 1, KEY_DIM, VALUE_DIM, device=dev, dtype=torch.float32)
+        bcov = torch.empty(n, nb + 1, KEY_DIM, KEY_DIM, device=dev, dtype=torch.float32)
+        cw32 = conv_weight.detach().reshape(core, 4).float().contiguous()
+        nw32 = norm_weight.detach().float().contiguous()
+        P = _hip.ptr
+        with torch.cuda.device(dev):
+            _hip.call("bssm_mixer_block_forward", P(projected), ld, P(cw32), P(aux), aux_w, P(nw32), float(norm_eps),
+                      P(mean0), P(cov0), P(convolved), P(out), P(read_bf16), P(mean_t), P(cov_t), P(bmean),
+                      P(bcov), b, t, heads, interval, float(denominator_floor), _hip.stream_of(dev))
+        ctx.save_for_backward(projected, cw32, aux, convolved, nw32, mean0, cov0, bmean, bcov, read_bf16)
+        ctx.heads, ctx.interval, ctx.ld = heads, interval, ld
+        ctx.norm_eps, ctx.denominator_floor = float(norm_eps), float(denominator_floor)
+        ctx.conv_shape, ctx.conv_dtype = tuple(conv_weight.shape), conv_weight.dtype
+        ctx.norm_dtype = norm_weight.dtype
+        ctx.bias_dtype = None if aux_bias is None else aux_bias.dtype
+        ctx.set_materialize_grads(False)
+        return out, mean_t, cov_t
+
+    @staticmethod
+    def backward(ctx, grad_out, grad_mean, grad_covariance):
+        projected, cw32, aux, convolved, nw32, mean0, cov0, bmean, bcov, read_bf16 = ctx.saved_tensors
+        b, t, _ = projected.shape
+        heads = ctx.heads
+        core, aux_w = 16 * heads, 6 * heads
+        need = ctx.needs_input_grad
+        dev = projected.device
+        if grad_out is None:
+            grad_out = torch.zeros(b, t, heads * VALUE_DIM, device=dev, dtype=torch.bfloat16)
+        else:
+            grad_out = grad_out.to(torch.bfloat16).contiguous()
+        gm = None if grad_mean is None else grad_mean.float().contiguous()
+        gc = None if grad_covariance is None else grad_covariance.float().contiguous()
+        gproj = torch.empty(b, t, core + aux_w + heads * VALUE_DIM, device=dev, dtype=torch.bfloat16)
+        gconv = torch.empty(b, t, core, device=dev, dtype=torch.bfloat16)
+        cpart = torch.empty(b, core, 4, device=dev, dtype=torch.float32)
+        npart = torch.empty(b * heads // 16, VALUE_DIM, device=dev, dtype=torch.float32)
+        gm0 = torch.empty_like(mean0) if need[4] else None
+        gc0 = torch.empty_like(cov0) if need[5] else None
+        P = _hip.ptr
+        with torch.cuda.device(dev):
+            _hip.call("bssm_mixer_block_backward", P(projected), ctx.ld, P(cw32), P(aux), aux_w, P(convolved),
+                      P(nw32), ctx.norm_eps, P(mean0), P(cov0), P(bmean), P(bcov), P(read_bf16), P(grad_out), P(gm),
+                      P(gc), P(gconv), P(gproj), gproj.shape[-1], P(cpart), P(npart), P(gm0), P(gc0), b, t, heads,
+                      ctx.interval, ctx.denominator_floor, _hip.stream_of(dev))
+        g_conv = cpart.sum(0).reshape(ctx.conv_shape).to(ctx.conv_dtype) if need[1] else None
+        g_norm = npart.sum(0).to(ctx.norm_dtype) if need[2] else None
+        g_bias = None
+        if need[3]:
+            g_bias = torch.sum(gproj[..., core:core + aux_w], dim=(0, 1), dtype=torch.float32).to(ctx.bias_dtype)
+        return gproj if need[0] else None, g_conv, g_norm, g_bias, gm0, gc0, None, None, None, None
+
+
 def bayes_mixer_block(
     projected: Tensor,
     conv_weight: Tensor,
@@ -385,10 +457,14 @@ def bayes_mixer_block(
     (:599-601); the rest is ``bayes_mixer_readout``.  Returns the gated
     readout [B, T, H*8] and the final mean and covariance.
 
-    On the GPU every stage runs on the HIP kernels: the filter reads the core
-    columns in place and writes one contiguous [B, T, 2*H*4 + H*8] tensor,
-    whose column views, with the aux and gate columns of ``projected``, feed
-    the producer-fused readout kernels.
+    On the GPU (bf16 ``projected`` whose rows the kernels can address, heads a
+    multiple of 16, T a positive multiple of 4, a bf16 or absent aux bias) the
+    block is one C call per direction: the filter reads the core columns in
+    place and writes one contiguous [B, T, 2*H*4 + H*8] tensor, whose column
+    views, with the aux and gate columns of ``projected``, feed the
+    producer-fused readout kernels; the backward writes the projection
+    gradient column by column into one [B, T, 30 H] tensor.  Other inputs run
+    the same stages through ``causal_depthwise4`` and ``bayes_mixer_readout``.
     """
     if projected.ndim != 3:
         raise ValueError("projected must have shape [B, T, width]")
@@ -401,6 +477,19 @@ def bayes_mixer_block(
                          f"got {projected.shape[-1]}")
     if tuple(conv_weight.shape) != (core, 1, 4):
         raise ValueError(f"conv_weight must have shape [{core}, 1, 4]")
+    b, t = projected.shape[:2]
+    ld = _row_stride(projected, t) if projected.is_cuda and projected.dtype == torch.bfloat16 else None
+    fused = (ld is not None and heads % 16 == 0 and t > 0 and t % 4 == 0
+             and conv_weight.device == projected.device and norm_weight.device == projected.device
+             and tuple(norm_weight.shape) == (VALUE_DIM,)
+             and (aux_bias is None or (aux_bias.device == projected.device
+                                       and torch.result_type(projected, aux_bias) == torch.bfloat16)))
+    if fused:
+        _hip.load()
+        eps = torch.finfo(torch.float32).eps if norm_eps is None else float(norm_eps)
+        mean0, cov0 = _initial_state(initial_mean, initial_covariance, b * heads, projected.device)
+        return _MixerBlockFunction.apply(projected, conv_weight, norm_weight, aux_bias, mean0, cov0, int(heads), eps,
+                                         float(denominator_floor), ld)
     from .conv import causal_depthwise4
 
     qkv = projected[..., :core]

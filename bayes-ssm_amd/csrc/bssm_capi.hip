@@ -639,6 +639,141 @@ int bssm_mixer_gated_backward(const void* q_proj, int64_t ldq, const void* k_pro
   return launched(fn, bssm::launch_mixer_backward(a, static_cast<hipStream_t>(stream)));
 }
 
+namespace {
+// The streams of config 4's Bayes block inside the fused projection
+// [B, T, 30 H] (q, k, v core 16 H, decay logits 4 H, noise 2 H, gate 8 H per
+// token) and the filtered core [B, T, 16 H]; aux (null: the projection's own
+// aux columns) holds the decay logits and noise with the aux bias added.
+struct BlockStreams {
+  const char *q, *k, *v, *dl, *nz, *gate;
+  int64_t ldc, lda;
+  BlockStreams(const void* projected, const void* aux, int64_t ld_aux, const void* convolved, int64_t h) {
+    const char* p = static_cast<const char*>(projected);
+    const char* c = static_cast<const char*>(convolved);
+    const char* x = aux ? static_cast<const char*>(aux) : p + 2 * 16 * h;
+    q = c;
+    k = c + 2 * 4 * h;
+    v = c + 2 * 8 * h;
+    dl = x;
+    nz = x + 2 * 4 * h;
+    gate = p + 2 * 22 * h;
+    ldc = 16 * h;
+    lda = ld_aux;
+  }
+};
+
+int block_check(const char* fn, const void* projected, int64_t ld_projected, const float* conv_weight,
+                const void* aux, int64_t ld_aux, const void* convolved, int64_t b, int64_t t, int64_t h,
+                int64_t chunk, float floor, const BlockStreams& s) {
+  if (h <= 0 || b < 0) return fail(BSSM_ERR_ARGUMENT, "%s: needs heads > 0 and batch >= 0", fn);
+  if (ld_projected < 30 * h)
+    return fail(BSSM_ERR_ARGUMENT, "%s: the projection row stride must be >= 30 * heads = %lld (got %lld)", fn,
+                (long long)(30 * h), (long long)ld_projected);
+  if (b * t * h > 0 && (projected == nullptr || conv_weight == nullptr || convolved == nullptr))
+    return fail(BSSM_ERR_ARGUMENT, "%s: projected, conv_weight and convolved are required (null given)", fn);
+  const int64_t lda = aux ? ld_aux : ld_projected;
+  if (int rc = mixer_check(fn, {s.q, s.k, s.v, s.dl, s.nz}, {s.ldc, s.ldc, s.ldc, lda, lda}, b, t, h, chunk, floor))
+    return rc;
+  if (int rc = conv_check(fn, 1, projected, ld_projected, conv_weight, {convolved}, b, t, 16 * h)) return rc;
+  return BSSM_OK;
+}
+}  // namespace
+
+int bssm_mixer_block_forward(const void* projected, int64_t ld_projected, const float* conv_weight,
+                             const void* aux, int64_t ld_aux, const float* norm_weight, float norm_eps,
+                             const float* mean0, const float* cov0, void* convolved, void* out, void* read_bf16,
+                             float* mean_final, float* cov_final, float* bmean, float* bcov, int64_t batch,
+                             int64_t t, int64_t heads, int64_t chunk, float denominator_floor, void* stream) {
+  const char* fn = "bssm_mixer_block_forward";
+  const BlockStreams s(projected, aux, ld_aux, convolved, heads);
+  if (int rc = block_check(fn, projected, ld_projected, conv_weight, aux, ld_aux, convolved, batch, t, heads, chunk,
+                           denominator_floor, s))
+    return rc;
+  if (int rc = epilogue_check(fn, s.gate, ld_projected, norm_weight, norm_eps, {out, read_bf16}, batch, t, heads))
+    return rc;
+  const int64_t n = batch * heads;
+  BSSM_REQUIRE(mean0);
+  BSSM_REQUIRE(cov0);
+  BSSM_REQUIRE(mean_final);
+  BSSM_REQUIRE(cov_final);
+  BSSM_REQUIRE(bmean);
+  BSSM_REQUIRE(bcov);
+  for (const void* p : {(const void*)mean0, (const void*)cov0, (const void*)mean_final, (const void*)cov_final,
+                        (const void*)bmean, (const void*)bcov})
+    if (p != nullptr && !aligned8(p)) return fail(BSSM_ERR_ARGUMENT, "%s: belief tensors must be 8-byte aligned", fn);
+  if (batch == 0) return ok();
+  const hipStream_t st = static_cast<hipStream_t>(stream);
+  bssm::ConvArgs c{};
+  c.x = projected; c.ldx = ld_projected; c.w = conv_weight; c.y = convolved; c.b = batch; c.t = t; c.c = 16 * heads;
+  c.bf16 = 1;
+  if (hipError_t e = bssm::launch_conv4_forward(c, st); e != hipSuccess) return launched(fn, e);
+  bssm::MixArgs a{};
+  a.q = s.q; a.k = s.k; a.v = s.v; a.dl = s.dl; a.nz = s.nz;
+  a.ldq = a.ldk = a.ldv = s.ldc; a.ldd = a.ldn = aux ? ld_aux : ld_projected;
+  a.m0 = mean0; a.c0 = cov0; a.mT = mean_final; a.cT = cov_final; a.bm = bmean; a.bc = bcov;
+  a.gate = s.gate; a.ldg = ld_projected; a.norm_w = norm_weight; a.norm_eps = norm_eps; a.out = out;
+  a.yb = read_bf16;
+  a.b = batch; a.t = t; a.h = heads; a.chunk = chunk; a.nb = (t + chunk - 1) / chunk; a.floor = denominator_floor;
+  return launched(fn, bssm::launch_mixer_forward(a, st));
+}
+
+int bssm_mixer_block_backward(const void* projected, int64_t ld_projected, const float* conv_weight,
+                              const void* aux, int64_t ld_aux, const void* convolved, const float* norm_weight,
+                              float norm_eps, const float* mean0, const float* cov0, const float* bmean,
+                              const float* bcov, const void* read_bf16, const void* grad_out, const float* gmf,
+                              const float* gcf, void* grad_convolved, void* grad_projected,
+                              int64_t ld_grad_projected, float* grad_conv_weight_partials,
+                              float* grad_norm_weight_partials, float* gm0, float* gc0, int64_t batch, int64_t t,
+                              int64_t heads, int64_t chunk, float denominator_floor, void* stream) {
+  const char* fn = "bssm_mixer_block_backward";
+  const BlockStreams s(projected, aux, ld_aux, convolved, heads);
+  if (int rc = block_check(fn, projected, ld_projected, conv_weight, aux, ld_aux, convolved, batch, t, heads, chunk,
+                           denominator_floor, s))
+    return rc;
+  if (int rc = epilogue_check(fn, s.gate, ld_projected, norm_weight, norm_eps,
+                              {read_bf16, grad_out, grad_convolved, grad_norm_weight_partials,
+                               grad_conv_weight_partials},
+                              batch, t, heads))
+    return rc;
+  if (ld_grad_projected < 30 * heads || ld_grad_projected % 8 != 0 || !aligned16(grad_projected) ||
+      (batch > 0 && grad_projected == nullptr))
+    return fail(BSSM_ERR_ARGUMENT, "%s: grad_projected needs a 16-byte aligned base and a row stride >= 30 * heads, "
+                "a multiple of 8 (got %lld)", fn, (long long)ld_grad_projected);
+  if ((t + 16) * ld_grad_projected * 2 >= ((int64_t)1 << 31))
+    return fail(BSSM_ERR_ARGUMENT, "%s: T * ld of grad_projected too large for 32-bit stream offsets", fn);
+  const int64_t n = batch * heads;
+  BSSM_REQUIRE(mean0);
+  BSSM_REQUIRE(cov0);
+  BSSM_REQUIRE(bmean);
+  BSSM_REQUIRE(bcov);
+  for (const void* p : {(const void*)mean0, (const void*)cov0, (const void*)bmean, (const void*)bcov,
+                        (const void*)gmf, (const void*)gcf, (const void*)gm0, (const void*)gc0})
+    if (p != nullptr && !aligned8(p)) return fail(BSSM_ERR_ARGUMENT, "%s: belief tensors must be 8-byte aligned", fn);
+  if (batch == 0) return ok();
+  const hipStream_t st = static_cast<hipStream_t>(stream);
+  char* gp = static_cast<char*>(grad_projected);
+  char* gc = static_cast<char*>(grad_convolved);
+  bssm::MixArgs a{};
+  a.q = s.q; a.k = s.k; a.v = s.v; a.dl = s.dl; a.nz = s.nz;
+  a.ldq = a.ldk = a.ldv = s.ldc; a.ldd = a.ldn = aux ? ld_aux : ld_projected;
+  a.m0 = mean0; a.c0 = cov0; a.bmr = bmean; a.bcr = bcov; a.gmf = gmf; a.gcf = gcf;
+  a.gq = gc; a.gk = gc + 2 * 4 * heads; a.gv = gc + 2 * 8 * heads;
+  a.gdl = gp + 2 * 16 * heads; a.gnz = gp + 2 * 20 * heads;
+  a.ldgq = a.ldgk = a.ldgv = 16 * heads;
+  a.ldgd = a.ldgn = a.ldgg = ld_grad_projected;
+  a.gm0 = gm0; a.gc0 = gc0;
+  a.gate = s.gate; a.ldg = ld_projected; a.norm_w = norm_weight; a.norm_eps = norm_eps;
+  a.yb = const_cast<void*>(read_bf16); a.gout = grad_out; a.ggate = gp + 2 * 22 * heads;
+  a.gw_part = grad_norm_weight_partials;
+  a.b = batch; a.t = t; a.h = heads; a.chunk = chunk; a.nb = (t + chunk - 1) / chunk; a.floor = denominator_floor;
+  if (hipError_t e = bssm::launch_mixer_backward(a, st); e != hipSuccess) return launched(fn, e);
+  bssm::ConvArgs c{};
+  c.x = projected; c.ldx = ld_projected; c.w = conv_weight; c.gy = grad_convolved; c.gx = grad_projected;
+  c.ldgx = ld_grad_projected; c.gw_part = grad_conv_weight_partials; c.b = batch; c.t = t; c.c = 16 * heads;
+  c.bf16 = 1;
+  return launched(fn, bssm::launch_conv4_backward(c, st));
+}
+
 int bssm_rotation_checkpoint(int key_dim) { return bssm::rotation_checkpoint(key_dim); }
 
 namespace {

@@ -176,7 +176,8 @@ __global__ __launch_bounds__(kWave * kWaves) void backward_kernel(ConvArgs a) {
   const uint32_t rx = static_cast<uint32_t>(a.ldx * sizeof(T)), rc = static_cast<uint32_t>(a.c * sizeof(T));
   const Rsrc X = make_rsrc(reinterpret_cast<const char*>(a.x) + L.b * T_ * rx, static_cast<uint32_t>(T_) * rx);
   const Rsrc GY = make_rsrc(reinterpret_cast<const char*>(a.gy) + L.b * T_ * rc, static_cast<uint32_t>(T_) * rc);
-  const Rsrc GX = make_rsrc(reinterpret_cast<const char*>(a.gx) + L.b * T_ * rc, static_cast<uint32_t>(T_) * rc);
+  const uint32_t rgx = static_cast<uint32_t>((a.ldgx ? a.ldgx : a.c) * sizeof(T));
+  const Rsrc GX = make_rsrc(reinterpret_cast<char*>(a.gx) + L.b * T_ * rgx, static_cast<uint32_t>(T_) * rgx);
   float gw[N][4];
 #pragma unroll
   for (int i = 0; i < N; ++i)
@@ -224,7 +225,7 @@ __global__ __launch_bounds__(kWave * kWaves) void backward_kernel(ConvArgs a) {
             gq[1][i] = gq[2][i];
             gq[2][i] = g4[i];
           }
-          st16(GX, Group<T>::narrow(gx), static_cast<uint32_t>(t0 + s + k) * rc + L.col);
+          st16(GX, Group<T>::narrow(gx), static_cast<uint32_t>(t0 + s + k) * rgx + L.col);
         }
       }
     }

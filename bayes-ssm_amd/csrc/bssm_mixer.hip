@@ -289,6 +289,7 @@ struct MixEpi {
   Rsrc gate, out, yb, gout, ggate;
   uint32_t rg, cg;    // gate row bytes; lane byte offset in a row
   uint32_t ro, co;    // contiguous bf16 rows (H * 16 bytes); lane byte offset
+  uint32_t rgg;       // ggate row bytes (bf16 layout)
   float w[4], eps;
   bool precise;
   __device__ __forceinline__ MixEpi(const MixArgs& a, int64_t bb, int64_t h0, int lane, bool backward) {
@@ -299,12 +300,14 @@ struct MixEpi {
     cg = (static_cast<uint32_t>(h0) + yh) * 16u + half * 8u;
     ro = static_cast<uint32_t>(a.h) * 16u;
     co = cg;
+    rgg = static_cast<uint32_t>(a.ldgg ? a.ldgg : 8 * a.h) * 2u;
     const uint32_t tro = static_cast<uint32_t>(T) * ro, trw = precise ? 2u * tro : tro;
+    const uint32_t trg = (precise ? 2u : 1u) * static_cast<uint32_t>(T) * rgg;
     gate = make_rsrc(as_f(a.gate, bb * T * rg), static_cast<uint32_t>(T) * rg);
     yb = make_rsrc(as_f(a.yb, bb * tro), tro);
     if (backward) {
       gout = make_rsrc(as_f(a.gout, bb * tro), tro);
-      ggate = make_rsrc(as_f(a.ggate, bb * trw), trw);
+      ggate = make_rsrc(as_f(a.ggate, bb * trg), trg);
       out = gout;
     } else {
       out = make_rsrc(as_f(a.out, bb * trw), trw);
@@ -424,27 +427,31 @@ __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(1, 1))) v
 // Gradient outputs: contiguous [B, T, H * w] rows, bfloat16 or float32.
 struct MixGrads {
   Rsrc q, k, v, dl, nz;
-  uint32_t rkq, rv, rn;  // row bytes of the bf16 layout
-  uint32_t ckq, cv, cn;  // byte offset of the wave's first head, bf16 layout
+  uint32_t rq, rk, rv, rd, rn;  // row bytes of the bf16 layout
+  uint32_t ckq, cv, cn;         // byte offset of the wave's first head, bf16 layout
   bool f32;
   __device__ __forceinline__ MixGrads(const MixArgs& a, int64_t bb, int64_t h0) {
     const int64_t T = a.t, H = a.h;
     f32 = a.grad_f32 != 0;
-    rkq = static_cast<uint32_t>(H) * 8u;
-    rv = static_cast<uint32_t>(H) * 16u;
-    rn = static_cast<uint32_t>(H) * 4u;
+    // Row strides: the caller's, or contiguous rows of 4 / 8 / 2 values per head.
+    rq = static_cast<uint32_t>(a.ldgq ? a.ldgq : 4 * H) * 2u;
+    rk = static_cast<uint32_t>(a.ldgk ? a.ldgk : 4 * H) * 2u;
+    rv = static_cast<uint32_t>(a.ldgv ? a.ldgv : 8 * H) * 2u;
+    rd = static_cast<uint32_t>(a.ldgd ? a.ldgd : 4 * H) * 2u;
+    rn = static_cast<uint32_t>(a.ldgn ? a.ldgn : 2 * H) * 2u;
     ckq = static_cast<uint32_t>(h0) * 8u;
     cv = static_cast<uint32_t>(h0) * 16u;
     cn = static_cast<uint32_t>(h0) * 4u;
     // Offsets are computed in the bf16 layout; float32 rows are twice as long.
     const int64_t e = f32 ? 2 : 1;
-    const uint32_t tkq = static_cast<uint32_t>(T * e) * rkq, tv = static_cast<uint32_t>(T * e) * rv,
+    const uint32_t tq = static_cast<uint32_t>(T * e) * rq, tk = static_cast<uint32_t>(T * e) * rk,
+                   tv = static_cast<uint32_t>(T * e) * rv, td = static_cast<uint32_t>(T * e) * rd,
                    tn = static_cast<uint32_t>(T * e) * rn;
-    q = make_rsrc(as_f(a.gq, bb * tkq), tkq);
-    k = make_rsrc(as_f(a.gk, bb * tkq), tkq);
+    q = make_rsrc(as_f(a.gq, bb * tq), tq);
+    k = make_rsrc(as_f(a.gk, bb * tk), tk);
     v = make_rsrc(as_f(a.gv, bb * tv), tv);
     const bool dyn = a.gdl != nullptr;
-    dl = make_rsrc(as_f(dyn ? a.gdl : a.gq, dyn ? bb * tkq : 0), dyn ? tkq : 0u);
+    dl = make_rsrc(as_f(dyn ? a.gdl : a.gq, dyn ? bb * td : 0), dyn ? td : 0u);
     nz = make_rsrc(as_f(dyn ? a.gnz : a.gq, dyn ? bb * tn : 0), dyn ? tn : 0u);
   }
   // One piece of 8 values (lo = first four, hi = last four) at the bf16
@@ -552,7 +559,7 @@ __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(1, 1))) v
       for (int c = 0; c < 4; ++c) gy[c] = r * fmaf(-n[c], dot * 0.125f, gn[c]);
       *reinterpret_cast<v4f*>(&tile[BwdTile::GY + mm.y_lds[I]]) = gy;
       const uint32_t t = static_cast<uint32_t>(J * 2 * SUB + mm.y_tok[I]);
-      ep.put4(ep.ggate, t * ep.ro + ep.co, gz);
+      ep.put4(ep.ggate, t * ep.rgg + ep.co, gz);
     }
     dwl[lane] = dw;
   };
@@ -576,11 +583,11 @@ __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(1, 1))) v
       const int o0 = mm.kq_lds[I][0], o1 = mm.kq_lds[I][1];
       const v4f gk0 = *reinterpret_cast<const v4f*>(&tile[BwdTile::K + o0]);
       const v4f gk1 = *reinterpret_cast<const v4f*>(&tile[BwdTile::K + o1]);
-      gr.put8(gr.k, t * gr.rkq + gr.ckq + mm.kq_col, unit_silu_grad(widen_lo(x.k[I]), gk0),
+      gr.put8(gr.k, t * gr.rk + gr.ckq + mm.kq_col, unit_silu_grad(widen_lo(x.k[I]), gk0),
               unit_silu_grad(widen_hi(x.k[I]), gk1));
       const v4f gq0 = *reinterpret_cast<const v4f*>(&tile[BwdTile::Q + o0]);
       const v4f gq1 = *reinterpret_cast<const v4f*>(&tile[BwdTile::Q + o1]);
-      gr.put8(gr.q, t * gr.rkq + gr.ckq + mm.kq_col, unit_silu_grad(widen_lo(x.q[I]), gq0),
+      gr.put8(gr.q, t * gr.rq + gr.ckq + mm.kq_col, unit_silu_grad(widen_lo(x.q[I]), gq0),
               unit_silu_grad(widen_hi(x.q[I]), gq1));
       if constexpr (DYN) {
         v4f out[2];
@@ -596,7 +603,7 @@ __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(1, 1))) v
             out[e][i] = -gd[i] * d * sigmoid_(z[i]);
           }
         }
-        gr.put8(gr.dl, t * gr.rkq + gr.ckq + mm.kq_col, out[0], out[1]);
+        gr.put8(gr.dl, t * gr.rd + gr.ckq + mm.kq_col, out[0], out[1]);
       }
     }
 #pragma unroll

@@ -134,6 +134,9 @@ struct MixArgs {
   const float* gmf;  // may be null (zero)
   const float* gcf;  // may be null (zero)
   void *gq, *gk, *gv, *gdl, *gnz;  // gdl, gnz null: dynamics gradients not requested
+  // Row strides (elements) of the gradient streams gq, gk, gv, gdl, gnz and
+  // ggate; 0: contiguous rows of the stream's own width.
+  int64_t ldgq, ldgk, ldgv, ldgd, ldgn, ldgg;
   float* gm0;  // may be null
   float* gc0;  // may be null
   int64_t b, t, h, chunk, nb;
@@ -189,6 +192,7 @@ struct ConvArgs {
   void* y;
   const void* gy;
   void* gx;
+  int64_t ldgx;  // row stride of gx (elements); 0: c
   float* gw_part;
   int64_t b, t, c;
   int bf16;

@@ -282,8 +282,9 @@ __global__ __launch_bounds__(kWave) void associative_scan_kernel(const float* __
 // and for the prior (L_0 = inv(P0), N_0 = inv(P0) M0):
 //   gM0 = inv(P0) SN_0,   gP0 = -inv(P0)^T (SL_0 + SN_0 M0^T) inv(P0)^T.
 // Pass 1 (one wave per (b, t)) writes gq, gN_t and gL_t (workspace); pass 2
-// (one wave per (b, s)) forms the suffix sums and the per-token gradients,
-// and the s = 0 wave the prior's.
+// turns the workspace into its suffix sums in place (one thread per entry of
+// a batch row, tokens in reverse); pass 3 (one wave per (b, s)) forms the
+// per-token gradients, and the s = 0 wave the prior's.
 template <int D, bool EXACT>
 __global__ __launch_bounds__(kWave) void scan_backward_token_kernel(
     const float* __restrict__ keys, const float* __restrict__ values, const float* __restrict__ queries,
@@ -387,6 +388,37 @@ __global__ __launch_bounds__(kWave) void scan_backward_token_kernel(
   }
 }
 
+// Pass 2: ws rows [B, T, E] (E = D*D entries of gL_t, then D*M of gN_t, in
+// their two arrays) to suffix sums over t >= s.  Loads run kSuffixBatch
+// tokens ahead of the dependent sum.
+constexpr int kSuffixBatch = 8;
+__global__ __launch_bounds__(256) void scan_backward_suffix_kernel(float* __restrict__ ws_gl,
+                                                                   float* __restrict__ ws_gn, int64_t T, int e_gl,
+                                                                   int e_gn) {
+  const int e = blockIdx.x * 256 + threadIdx.x;
+  if (e >= e_gl + e_gn) return;
+  const int64_t b = blockIdx.y;
+  const bool gl = e < e_gl;
+  const int w = gl ? e_gl : e_gn;
+  float* p = (gl ? ws_gl + b * T * e_gl + e : ws_gn + b * T * e_gn + (e - e_gl));
+  float acc = 0.f;
+  int64_t t = T;
+  while (t > 0) {
+    const int n = t >= kSuffixBatch ? kSuffixBatch : static_cast<int>(t);
+    float x[kSuffixBatch];
+#pragma unroll
+    for (int i = 0; i < kSuffixBatch; ++i) x[i] = i < n ? p[(t - 1 - i) * w] : 0.f;
+#pragma unroll
+    for (int i = 0; i < kSuffixBatch; ++i) {
+      if (i < n) {
+        acc += x[i];
+        p[(t - 1 - i) * w] = acc;
+      }
+    }
+    t -= n;
+  }
+}
+
 template <int D, bool EXACT>
 __global__ __launch_bounds__(kWave) void scan_backward_prefix_kernel(
     const float* __restrict__ keys, const float* __restrict__ values, const float* __restrict__ obs,
@@ -403,20 +435,15 @@ __global__ __launch_bounds__(kWave) void scan_backward_prefix_kernel(
   const int64_t s = blockIdx.x;
   const bool row_lane = lane < Dr, col_lane = lane < M;
   const int rl = row_lane ? lane : 0;
-  // Suffix sums over t >= s: row owners row i of SL, column owners column c of SN.
+  // Suffix sums over t >= s (pass 2): row owners row i of SL, column owners column c of SN.
   float sl[D], snc[D];
-#pragma unroll
-  for (int j = 0; j < D; ++j) {
-    sl[j] = 0.f;
-    snc[j] = 0.f;
-  }
-  for (int64_t t = T - 1; t >= s; --t) {
-    const float* glt = ws_gl + ((b * T + t) * Dr + rl) * Dr;
-    const float* gnt = ws_gn + (b * T + t) * Dr * M + (col_lane ? lane : 0);
+  {
+    const float* glt = ws_gl + ((b * T + s) * Dr + rl) * Dr;
+    const float* gnt = ws_gn + (b * T + s) * Dr * M + (col_lane ? lane : 0);
 #pragma unroll
     for (int j = 0; j < D; ++j) {
-      if (row_lane && j < Dr) sl[j] += glt[j];
-      if (col_lane && j < Dr) snc[j] += gnt[j * M];
+      sl[j] = (row_lane && j < Dr) ? glt[j < Dr ? j : 0] : 0.f;
+      snc[j] = (col_lane && j < Dr) ? gnt[(j < Dr ? j : 0) * M] : 0.f;
     }
   }
   if (col_lane) {
@@ -670,11 +697,17 @@ hipError_t launch_scan_backward(const float* k, const float* v, const float* q, 
   if (d == D) {
     hipLaunchKernelGGL((scan_backward_token_kernel<D, true>), grid, dim3(kWave), 0, stream, k, v, q, r, m0, c0, gy,
                        gmT, gcT, ws_gl, ws_gn, gq, t, d, m);
-    hipLaunchKernelGGL((scan_backward_prefix_kernel<D, true>), grid, dim3(kWave), 0, stream, k, v, r, m0, c0, ws_gl,
-                       ws_gn, gk, gv, gr, gm0, gc0, t, d, m);
   } else {
     hipLaunchKernelGGL((scan_backward_token_kernel<D, false>), grid, dim3(kWave), 0, stream, k, v, q, r, m0, c0, gy,
                        gmT, gcT, ws_gl, ws_gn, gq, t, d, m);
+  }
+  const int e_gl = d * d, e_gn = d * m;
+  const dim3 sgrid(static_cast<unsigned>((e_gl + e_gn + 255) / 256), static_cast<unsigned>(b));
+  hipLaunchKernelGGL(scan_backward_suffix_kernel, sgrid, dim3(256), 0, stream, ws_gl, ws_gn, t, e_gl, e_gn);
+  if (d == D) {
+    hipLaunchKernelGGL((scan_backward_prefix_kernel<D, true>), grid, dim3(kWave), 0, stream, k, v, r, m0, c0, ws_gl,
+                       ws_gn, gk, gv, gr, gm0, gc0, t, d, m);
+  } else {
     hipLaunchKernelGGL((scan_backward_prefix_kernel<D, false>), grid, dim3(kWave), 0, stream, k, v, r, m0, c0, ws_gl,
                        ws_gn, gk, gv, gr, gm0, gc0, t, d, m);
   }

@@ -176,6 +176,49 @@ def time_mixer(b, t, h, steps, warmup, device, fused=True, gated=False) -> dict:
     return out
 
 
+BLOCK_FWD_BYTES = 2 * 30 + 2 * 8           # bf16 fused projection in (30 per head), bf16 gated readout out
+BLOCK_BWD_BYTES = 2 * 30 + 2 * 8 + 2 * 30  # projection and readout gradient in; projection gradient out
+
+
+def time_block(b, t, h, steps, warmup, device) -> dict:
+    """fwd+bwd of config 4's Bayes block (``bayes_mixer_block``, train_6layer.py:583-729): the causal depthwise-4
+    filter, the producer-fused layer core and the gated readout, from the fused bf16 projection to out_proj's
+    input, with the gradients of the projection, the filter and norm weights and the aux bias."""
+    from bayes_ssm.mixer import bayes_mixer_block
+
+    gen = torch.Generator(device=device).manual_seed(4)
+    state, width = 4 * h, 8 * h
+    core, aux = 2 * state + width, state + 2 * h
+    projected = torch.randn(b, t, core + aux + width, device=device, generator=gen)
+    projected[..., core:core + state] -= 4.0
+    projected[..., core + state:core + aux:2] -= 2.0
+    leaves = [projected.to(torch.bfloat16).requires_grad_(True),
+              (0.5 * torch.randn(core, 1, 4, device=device, generator=gen)).to(torch.bfloat16).requires_grad_(True),
+              torch.ones(8, device=device, dtype=torch.bfloat16, requires_grad=True),
+              torch.zeros(aux, device=device, dtype=torch.bfloat16, requires_grad=True)]
+    gy = torch.randn(b, t, width, device=device, generator=gen).to(torch.bfloat16)
+
+    def step():
+        out, _, _ = bayes_mixer_block(leaves[0], leaves[1], leaves[2], heads=h, aux_bias=leaves[3])
+        return torch.autograd.grad(out, leaves, gy)
+
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(steps):
+        step()
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / steps
+    per = BLOCK_FWD_BYTES + BLOCK_BWD_BYTES
+    return {"B": b, "T": t, "H": h, "W": width, "D": 4, "M": 8, "ms_per_step": ms,
+            "tokens_per_s": b * t / (ms * 1e-3), "bytes_per_token_head": per,
+            "roofline_step_frac": per * b * h * t / (ms * 1e-3) / HBM_PEAK,
+            "path": "causal depthwise-4 + producer-fused layer core + gated readout (HIP kernels)"}
+
+
 def time_conv(b, t, c, steps, warmup, device, fused=True) -> dict:
     """fwd+bwd of CausalDepthwise4 on a bf16 [B, T, C] stream, as the mixer applies it (train_6layer.py:474-480).
 
@@ -356,8 +399,40 @@ def time_scan(b, t, d, m, iters, device) -> dict:
         _hip.call("bssm_associative_static_scan", *args)
     e1.record()
     torch.cuda.synchronize()
-    return {"B": b, "T": t, "D": d, "M": m, "api_us_per_call": api_us,
-            "kernel_us_per_call": e0.elapsed_time(e1) / iters * 1e3}
+    kernel_us = e0.elapsed_time(e1) / iters * 1e3
+    # fwd+bwd through the API (HIP forward and HIP backward), all six inputs as leaves.
+    leaves = [x.clone().requires_grad_(True) for x in (k, v, q, r, m0, c0)]
+    gy = torch.randn(b, t, m, device=device, generator=g)
+
+    def step():
+        y, _, _ = associative_static_bayesian_cuda(leaves[0], leaves[1], leaves[2], observation_variances=leaves[3],
+                                                   initial_mean=leaves[4], initial_covariance=leaves[5])
+        return torch.autograd.grad(y, leaves, gy)
+
+    for _ in range(5):
+        step()
+    torch.cuda.synchronize()
+    e0.record()
+    for _ in range(iters):
+        step()
+    e1.record()
+    torch.cuda.synchronize()
+    step_us = e0.elapsed_time(e1) / iters * 1e3
+    # The backward kernels alone through the C ABI.
+    grads = [torch.empty_like(x) for x in (k, v, q, r, m0, c0)]
+    ws = torch.empty(b * t * (d * d + d * m), device=device)
+    bargs = (P(k), P(v), P(q), P(r), P(m0), P(c0), P(gy), None, None, P(ws), *map(P, grads), b, t, d, m,
+             _hip.stream_of(device))
+    _hip.call("bssm_associative_static_scan_backward", *bargs)
+    torch.cuda.synchronize()
+    e0.record()
+    for _ in range(iters):
+        _hip.call("bssm_associative_static_scan_backward", *bargs)
+    e1.record()
+    torch.cuda.synchronize()
+    return {"B": b, "T": t, "D": d, "M": m, "api_us_per_call": api_us, "kernel_us_per_call": kernel_us,
+            "api_fwd_bwd_us_per_step": step_us,
+            "backward_kernels_us_per_call": e0.elapsed_time(e1) / iters * 1e3}
 
 
 def cpu_baseline(t: int, d: int, m: int, heads: int, budget_s: float) -> dict:
@@ -408,9 +483,10 @@ def main() -> int:
     ap.add_argument("--cpu-budget", type=float, default=20.0, help="seconds of CPU-baseline work (0 = skip)")
     ap.add_argument("--no-extras", action="store_true",
                     help="skip the secondary shapes (per-GPU DP shape, D1/D2/D8 variants, associative scan)")
-    ap.add_argument("--secondary", choices=("mixer", "mixer-readout", "conv4", "rotation", "d64"),
+    ap.add_argument("--secondary", choices=("mixer", "mixer-readout", "block", "conv4", "rotation", "d64"),
                     help="time only one secondary workload at the configured shape (the mixer's fused layer core, "
-                         "with its readout epilogue, or the causal depthwise-4 filter on the q/k/v stream), for "
+                         "with its readout epilogue, config 4's whole Bayes block, or the causal depthwise-4 filter "
+                         "on the q/k/v stream, the rotation core or D = M = 64), for "
                          "profiling its kernels; prints its own JSON line")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="also run one 256 MiB device copy (reference kernel for PMC byte counters)")
@@ -435,6 +511,8 @@ def main() -> int:
             row = time_rotation(b, t, h, d, args.steps, args.warmup, device, fused=True)
         elif args.secondary == "d64":
             row = time_d64(b, t, h, args.steps, args.warmup, device, fused=True)
+        elif args.secondary == "block":
+            row = time_block(b, t, h, args.steps, args.warmup, device)
         else:
             row = time_mixer(b, t, h, args.steps, args.warmup, device, fused=True,
                              gated=args.secondary == "mixer-readout")
@@ -553,8 +631,9 @@ def main() -> int:
         # Secondary shapes (not the metric): config 3 divided by 8 (one GPU's
         # share under 8-way data parallelism), the D2M8 / D8M8 variants of
         # config 3, config 2 (D1M8, B64), the mixer's layer core at config 3
-        # (fused producer kernels, and the reference op chain beside it), and
-        # the associative-scan configs.
+        # (fused producer kernels, and the reference op chain beside it),
+        # config 4's Bayes block (filter + layer core + gated readout), and
+        # the associative-scan configs (forward, and fwd+bwd).
         extras = {"config3_bf16_kqv": time_layer(b, t, h, d, m, args.chunk, 30, 10, device, bf16_kqv=True),
                   "dp8_share_d4m8": time_layer(b // 8, t, h, d, m, args.chunk, 30, 10, device)}
         for name, (eb, ed) in {"config3_d2m8": (b, 2), "config3_d8m8": (b, 8), "config2_d1m8": (64, 1)}.items():
@@ -563,6 +642,7 @@ def main() -> int:
         extras["mixer_core_config3_op_chain"] = time_mixer(b, t, h, 10, 3, device, fused=False)
         extras["mixer_readout_config3_fused"] = time_mixer(b, t, h, 30, 10, device, fused=True, gated=True)
         extras["mixer_readout_config3_op_chain"] = time_mixer(b, t, h, 10, 3, device, fused=False, gated=True)
+        extras["block_config4_fused"] = time_block(b, t, h, 20, 5, device)
         qkv = h * (2 * d + m)  # channels of the mixer's fused q/k/v stream at this shape
         extras["conv4_config3_qkv"] = time_conv(b, t, qkv, 30, 10, device, fused=True)
         extras["conv4_config3_qkv_torch"] = time_conv(b, t, qkv, 10, 3, device, fused=False)

@@ -464,6 +464,48 @@ int bssm_mixer_gated_backward(const void* q_proj, int64_t ldq, const void* k_pro
                               int64_t batch, int64_t t, int64_t heads, int64_t chunk,
                               float denominator_floor, int precise, void* stream);
 
+/* ------------------------------------------------------------------------
+ * Config 4's Bayes block in one call per direction.  Replaces the torch chain
+ * of BayesianMixer.forward (example/train_6layer.py:583-729) from the fused
+ * projection to out_proj's input, paper features with the fused Q/K/V/aux/gate
+ * projection (:585-600), key dim 4, value dim 8:
+ *   convolved = CausalDepthwise4(projected[..., :16H])      (:598, :474-480)
+ *   q, k, v   = convolved split (4H, 4H, 8H)                (:599-601)
+ *   aux       = projected[..., 16H:22H] + aux_bias          (:589-593)
+ *   out       = bssm_mixer_gated_forward(q, k, v, aux[..., :4H], aux[..., 4H:],
+ *                                        gate = projected[..., 22H:])
+ * projected: bf16 [B, T, 30H] rows with stride ld_projected (>= 30H, a
+ * multiple of 8, 16-byte aligned).  aux: NULL (no bias: the projection's own
+ * columns) or the biased aux bf16 [B, T, 6H] with row stride ld_aux.
+ * conv_weight: float32 [16H, 4].  convolved: bf16 [B, T, 16H] (written by the
+ * forward, kept for the backward).  Other arguments as in the gated mixer
+ * (heads a multiple of 16, T a positive multiple of 4). */
+int bssm_mixer_block_forward(const void* projected, int64_t ld_projected, const float* conv_weight,
+                             const void* aux, int64_t ld_aux, const float* norm_weight, float norm_eps,
+                             const float* mean0, const float* cov0, void* convolved, void* out,
+                             void* read_bf16, float* mean_final, float* cov_final, float* bmean, float* bcov,
+                             int64_t batch, int64_t t, int64_t heads, int64_t chunk,
+                             float denominator_floor, void* stream);
+
+/* Reverse of bssm_mixer_block_forward.  Writes every column of
+ * grad_projected (bf16 [B, T, 30H], row stride ld_grad_projected): the
+ * filter's input gradient into the core columns, the aux and gate gradients
+ * into theirs (the aux gradient is also aux_bias's per token).  Workspace
+ * grad_convolved: bf16 [B, T, 16H].  The weight gradients come as partial
+ * sums: grad_conv_weight_partials [B, 16H, 4] (sum over the first axis) and
+ * grad_norm_weight_partials [B*H/16, 8] (column sums), float32. */
+int bssm_mixer_block_backward(const void* projected, int64_t ld_projected, const float* conv_weight,
+                              const void* aux, int64_t ld_aux, const void* convolved,
+                              const float* norm_weight, float norm_eps,
+                              const float* mean0, const float* cov0, const float* bmean, const float* bcov,
+                              const void* read_bf16, const void* grad_out,
+                              const float* gmf, const float* gcf,
+                              void* grad_convolved, void* grad_projected, int64_t ld_grad_projected,
+                              float* grad_conv_weight_partials, float* grad_norm_weight_partials,
+                              float* gm0, float* gc0,
+                              int64_t batch, int64_t t, int64_t heads, int64_t chunk,
+                              float denominator_floor, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

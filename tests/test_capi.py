@@ -152,6 +152,26 @@ def test_mixer_argument_errors_are_reported(lib):
     assert _mixer_fwd(lib, b=0) == 0
 
 
+def _block_fwd(lib, b=1, t=8, h=16, ld=480, chunk=8):
+    return lib.bssm_mixer_block_forward(None, ld, None, None, 0, None, ctypes.c_float(1e-6), *([None] * 9), b, t, h,
+                                        chunk, ctypes.c_float(1e-6), None)
+
+
+def test_block_argument_errors_are_reported(lib):
+    assert _block_fwd(lib, h=0) == 1
+    assert _block_fwd(lib, ld=472) == 1 and b"30 * heads" in lib.bssm_last_error()
+    assert _block_fwd(lib, b=0, h=8, ld=240) == 2 and b"heads" in lib.bssm_last_error()
+    assert _block_fwd(lib, b=0, t=6) == 2
+    assert _block_fwd(lib) == 1 and b"required" in lib.bssm_last_error()
+    assert _block_fwd(lib, b=0) == 0
+    rc = lib.bssm_mixer_block_backward(None, 480, None, None, 0, None, None, ctypes.c_float(1e-6), *([None] * 10),
+                                       480, *([None] * 4), 1, 8, 16, 8, ctypes.c_float(1e-6), None)
+    assert rc == 1 and b"required" in lib.bssm_last_error()
+    rc = lib.bssm_mixer_block_backward(None, 480, None, None, 0, None, None, ctypes.c_float(1e-6), *([None] * 10),
+                                       472, *([None] * 4), 0, 8, 16, 8, ctypes.c_float(1e-6), None)
+    assert rc == 1 and b"grad_projected" in lib.bssm_last_error()
+
+
 def test_conv_backward_checks_weight_and_partials_at_t0(lib):
     """With T = 0 the backward still reads the weight and writes the partials: both are required."""
     rc = lib.bssm_causal_conv4_backward(1, None, 8, None, None, None, None, 2, 0, 8, None)

@@ -61,19 +61,86 @@ def _bf16_close(actual, expected, name):
                                msg=lambda m: f"{name}: {m}")
 
 
-def test_config4_block_full_shape(cuda_device, monkeypatch):
-    from bayes_ssm import conv, mixer
+def _leaves(projected, weight, norm_w, aux_bias, wide):
+    """Fresh leaves; with ``wide`` the projection leaf is a wider tensor and the block sees a column view."""
+    w = projected.shape[-1]
+    if wide:
+        base = torch.zeros(*projected.shape[:2], w + 24, device=projected.device, dtype=projected.dtype)
+        base[..., 8:8 + w] = projected
+        base.requires_grad_(True)
+        view = base[..., 8:8 + w]
+    else:
+        base = projected.detach().clone().requires_grad_(True)
+        view = base
+    leaves = [base] + [x.detach().clone().requires_grad_(True) for x in (weight, norm_w)]
+    bias = None if aux_bias is None else aux_bias.detach().clone().requires_grad_(True)
+    return leaves, view, bias
 
-    calls = {"conv": 0, "readout": 0}
-    c_orig, r_orig = conv._CausalConv4Function.apply, mixer._MixerReadoutFunction.apply
-    monkeypatch.setattr(conv._CausalConv4Function, "apply",
-                        staticmethod(lambda *a: calls.__setitem__("conv", calls["conv"] + 1) or c_orig(*a)))
-    monkeypatch.setattr(mixer._MixerReadoutFunction, "apply",
-                        staticmethod(lambda *a: calls.__setitem__("readout", calls["readout"] + 1) or r_orig(*a)))
+
+def _staged(projected, weight, norm_w, aux_bias, gout, h, gm=None, gc=None, wide=False):
+    """The same block through its separate stages (filter, then the gated readout on column views)."""
+    from bayes_ssm.conv import causal_depthwise4
+    from bayes_ssm.mixer import bayes_mixer_readout
+
+    leaves, p, bias = _leaves(projected, weight, norm_w, aux_bias, wide)
+    state, width = 4 * h, 8 * h
+    core, aux = 2 * state + width, state + 2 * h
+    conv = causal_depthwise4(p[..., :core].transpose(1, 2), leaves[1]).transpose(1, 2)
+    q, k, v = conv.split((state, state, width), dim=-1)
+    a = p[..., core:core + aux] if bias is None else p[..., core:core + aux] + bias
+    out, mT, cT = bayes_mixer_readout(q, k, v, a[..., :state], a[..., state:], p[..., core + aux:], leaves[2],
+                                      heads=h)
+    outs, grads_in = [out], [gout]
+    if gm is not None:
+        outs += [mT, cT]
+        grads_in += [gm, gc]
+    torch.autograd.backward(outs, grads_in)
+    torch.cuda.synchronize()
+    return out.detach(), mT.detach(), cT.detach(), [x.grad for x in leaves], None if bias is None else bias.grad
+
+
+@pytest.mark.parametrize("b,t,h,wide,with_bias", [(3, 36, 16, False, True), (2, 64, 32, True, False),
+                                                   (1, 8, 16, True, True)])
+def test_block_call_matches_its_stages(cuda_device, monkeypatch, b, t, h, wide, with_bias):
+    """The one-call block kernels against the same kernels stage by stage: bitwise, gradients of the final
+    state included; ``projected`` as a column view of a wider tensor when ``wide``."""
+    from bayes_ssm import mixer
+    from bayes_ssm.mixer import bayes_mixer_block
+
+    calls = []
+    orig = mixer._MixerBlockFunction.apply
+    monkeypatch.setattr(mixer._MixerBlockFunction, "apply", staticmethod(lambda *a: calls.append(1) or orig(*a)))
+    print(f"block vs stages b={b} t={t} h={h} wide={wide} bias={with_bias}", flush=True)
+    projected, weight, norm_w, aux_bias, gout = _inputs(b, t, h, seed=5 + h, device=cuda_device)
+    aux_bias = aux_bias if with_bias else None
+    g = torch.Generator().manual_seed(6)
+    gm = torch.randn(b * h, 4, 8, generator=g).to(cuda_device)
+    gc = torch.randn(b * h, 4, 4, generator=g).to(cuda_device)
+    leaves, view, bias = _leaves(projected, weight, norm_w, aux_bias, wide)
+    assert view.is_contiguous() != wide
+    out, mT, cT = bayes_mixer_block(view, leaves[1], leaves[2], heads=h, aux_bias=bias)
+    assert calls, "the block kernels were not used"
+    torch.autograd.backward([out, mT, cT], [gout, gm, gc])
+    torch.cuda.synchronize()
+    s_out, s_mT, s_cT, s_grads, s_bias = _staged(projected, weight, norm_w, aux_bias, gout, h, gm, gc, wide)
+    assert torch.equal(out, s_out) and torch.equal(mT, s_mT) and torch.equal(cT, s_cT)
+    for name, a, e in zip(("projected", "conv weight", "norm weight"), [x.grad for x in leaves], s_grads):
+        assert a.dtype == e.dtype and torch.equal(a, e), f"grad {name} differs from the staged run"
+    if with_bias:
+        # Summation order over (B, T) differs from autograd's: one bf16 rounding.
+        torch.testing.assert_close(bias.grad.float(), s_bias.float(), rtol=2 ** -7, atol=1e-6)
+
+
+def test_config4_block_full_shape(cuda_device, monkeypatch):
+    from bayes_ssm import mixer
+
+    calls = []
+    orig = mixer._MixerBlockFunction.apply
+    monkeypatch.setattr(mixer._MixerBlockFunction, "apply", staticmethod(lambda *a: calls.append(1) or orig(*a)))
     print("config4 block full shape", flush=True)
     projected, weight, norm_w, aux_bias, gout = _inputs(B, T, H, seed=4, device=cuda_device)
     out, mT, cT, grads = _run(projected, weight, norm_w, aux_bias, gout, H)
-    assert calls == {"conv": 1, "readout": 1}, f"HIP kernels not used on every stage: {calls}"
+    assert calls, "the block kernels were not used"
     assert out.shape == (B, T, 8 * H) and out.dtype == torch.bfloat16
     assert torch.isfinite(out.float()).all() and torch.isfinite(grads[0].float()).all()
 
@@ -99,6 +166,7 @@ def test_config4_block_full_shape(cuda_device, monkeypatch):
     torch.testing.assert_close(conv_out.double(), e_filter, rtol=2 ** -8, atol=1e-6)
     e_out, e_mT, e_cT = O.mixer_block(leaves[0], leaves[1], leaves[2], H, aux_bias=leaves[3], conv_out=conv_out)
     e_grads = torch.autograd.grad((e_out * gout[rows].cpu().double()).sum(), leaves)
+    assert len(s_grads) == 4 and s_grads[3] is not None
     _bf16_close(s_out, e_out, "out")
     torch.testing.assert_close(s_mT.double().cpu(), e_mT, rtol=1e-5, atol=1e-4)
     torch.testing.assert_close(s_cT.double().cpu(), e_cT, rtol=1e-5, atol=1e-4)
