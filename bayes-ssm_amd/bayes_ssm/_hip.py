@@ -47,6 +47,9 @@ _SIGNATURES = {
     "bssm_backward_chunked_saved_lean": _BWD_SAVED_HEAD + [_P] * 3 + [_L, _L, _L, _F, _P],
     "bssm_forward_chunked_bf16": [_I, _I, _I] + [_P] * 8 + [_P] * 5 + [_L, _L, _L, _F, _P],
     "bssm_backward_chunked_bf16": [_I, _I, _I] + [_P] * 10 + [_P] * 3 + [_P] * 8 + [_L, _L, _L, _F, _P],
+    "bssm_forward_chunked_fp8": [_I, _I, _I, _I] + [_P] * 8 + [_P] * 5 + [_L, _L, _L, _F, _P],
+    "bssm_backward_chunked_fp8": [_I, _I, _I, _I] + [_P] * 10 + [_P] * 3 + [_P] * 8 + [_L, _L, _L, _F, _P],
+    "bssm_round_float8": [_I, _P, _P, _L],
     "bssm_associative_static_scan": [_P] * 9 + [_L, _L, _I, _I, _P],
     "bssm_associative_static_scan_backward": [_P] * 16 + [_L, _L, _I, _I, _P],
     "bssm_mixer_forward": [_P, _L] * 5 + [_P] * 7 + [_L, _L, _L, _L, _F, _P],

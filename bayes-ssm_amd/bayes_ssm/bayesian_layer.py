@@ -335,10 +335,11 @@ def bayesian_layer(
     batch_shape = keys.shape[:-2]
     device = keys.device
     dtype = torch.float32 if keys.dtype in _LOW_PRECISION else keys.dtype
-    # bfloat16 keys/values/queries go to the fused kernels as bfloat16 (they
-    # widen on chip); every other path sees the promoted tensors.
-    bf16_kqv = ((keys, values, queries) if all(x.dtype == torch.bfloat16 for x in (keys, values, queries))
-                else None)
+    # bfloat16 and OCP float8 keys/values/queries go to the fused kernels in
+    # their dtype (they widen on chip); every other path sees the promoted tensors.
+    narrow = (torch.bfloat16, torch.float8_e4m3fn, torch.float8_e5m2)
+    bf16_kqv = ((keys, values, queries)
+                if keys.dtype in narrow and all(x.dtype == keys.dtype for x in (values, queries)) else None)
     keys, values, queries = keys.to(dtype), values.to(dtype), queries.to(dtype)
     for x, name in ((keys, "keys"), (values, "values"), (queries, "queries")):
         _check_finite(x, name)

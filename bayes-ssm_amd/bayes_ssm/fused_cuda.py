@@ -30,11 +30,12 @@ Deliberate differences from the reference, all result-preserving:
   exported and is used when ``BAYES_SSM_D1_SAVED_HISTORY=1``.
 
 Extension beyond the reference contract: ``fused_diagonal_bayesian`` also
-accepts bfloat16 keys, values and queries (everything else float32).  For
-D = 4, M = 8 they are read as bfloat16 by the kernels (no float32 copies in
-HBM) and their gradients are written as bfloat16; results equal those of the
-float32 path on the widened values, whose gradients autograd would round to
-bfloat16 the same way.  Other shapes widen first and take the float32 path.
+accepts bfloat16 keys, values and queries, or float8 ones (float8_e4m3fn or
+float8_e5m2; everything else float32).  For D = 4, M = 8 they are read as
+such by the kernels (no float32 copies in HBM) and their gradients are
+written in their dtype; results equal those of the float32 path on the
+widened values, whose gradients autograd would round to that dtype the same
+way.  Other shapes widen first and take the float32 path.
 """
 from __future__ import annotations
 
@@ -382,12 +383,25 @@ class _ChunkedBayesianFunction(torch.autograd.Function):
         return (*gradients, None, None, None)
 
 
-class _ChunkedBayesianBF16Function(torch.autograd.Function):
-    """bfloat16 keys/values/queries read as such by the D4M8 kernels (C ABI ``bssm_*_chunked_bf16``).
+# float8 encodings the D4M8 kernels read (C ABI format argument).
+_FP8_FORMATS = {torch.float8_e4m3fn: 0, torch.float8_e5m2: 1}
 
-    Outputs are float32; the gradients of keys, values and queries are
-    bfloat16 (the float32 gradient rounded to nearest even), the others
-    float32.  Gradients are computed only for inputs that require them.
+
+def _narrow_call(keys: Tensor, direction: str) -> tuple[str, tuple[int, ...]]:
+    """C ABI entry point and leading format argument for narrow keys/values/queries."""
+    if keys.dtype == torch.bfloat16:
+        return f"bssm_{direction}_chunked_bf16", ()
+    return f"bssm_{direction}_chunked_fp8", (_FP8_FORMATS[keys.dtype],)
+
+
+class _ChunkedBayesianBF16Function(torch.autograd.Function):
+    """bfloat16 or float8 keys/values/queries read as such by the D4M8 kernels
+    (C ABI ``bssm_*_chunked_bf16`` / ``bssm_*_chunked_fp8``).
+
+    Outputs are float32; the gradients of keys, values and queries have
+    their dtype (the float32 gradient rounded to nearest even, as autograd
+    through a widening cast gives), the others float32.  Gradients are
+    computed only for inputs that require them.
     """
 
     @staticmethod
@@ -405,7 +419,8 @@ class _ChunkedBayesianBF16Function(torch.autograd.Function):
         bcov = torch.empty(n, nb + 1, d, d, device=dev, dtype=torch.float32)
         P = _hip.ptr
         with torch.cuda.device(dev):
-            _hip.call("bssm_forward_chunked_bf16", d, m, int(bool(fixed_dynamics)), P(keys), P(values), P(queries),
+            name, fmt = _narrow_call(keys, "forward")
+            _hip.call(name, d, m, int(bool(fixed_dynamics)), *fmt, P(keys), P(values), P(queries),
                       P(decay), P(process), P(observation), P(initial_mean), P(initial_covariance), P(out),
                       P(mean_t), P(cov_t), P(bmean), P(bcov), n, t, interval, float(denominator_floor),
                       _hip.stream_of(dev))
@@ -438,7 +453,8 @@ class _ChunkedBayesianBF16Function(torch.autograd.Function):
         gc0 = torch.empty_like(cov0) if need[7] else None
         P = _hip.ptr
         with torch.cuda.device(keys.device):
-            _hip.call("bssm_backward_chunked_bf16", d, m, int(ctx.fixed_dynamics), P(keys), P(values), P(queries),
+            name, fmt = _narrow_call(keys, "backward")
+            _hip.call(name, d, m, int(ctx.fixed_dynamics), *fmt, P(keys), P(values), P(queries),
                       P(decay), P(process), P(observation), P(mean0), P(cov0), P(bmean), P(bcov), P(grad_output),
                       P(gm), P(gc), P(gk), P(gv), P(gq), P(gd), P(gp), P(gr), P(gm0), P(gc0), n, t, ctx.interval,
                       ctx.denominator_floor, _hip.stream_of(keys.device))
@@ -447,7 +463,7 @@ class _ChunkedBayesianBF16Function(torch.autograd.Function):
 
 
 def _bf16_kernels_apply(keys: Tensor, values: Tensor, queries: Tensor) -> bool:
-    """The D4M8 kernels read these bfloat16 streams directly (else: widen, float32 path)."""
+    """The D4M8 kernels read these bfloat16 / float8 streams directly (else: widen, float32 path)."""
     n, t, d = keys.shape
     return ((d, values.shape[-1]) == (4, 8) and t > 0 and t % 4 == 0 and _hip.preferred_checkpoint(d) > 0
             and all(x.data_ptr() % 16 == 0 for x in (keys, values, queries)))
@@ -472,10 +488,11 @@ def fused_diagonal_bayesian(
     Contract (fused_cuda.py:346-371): CUDA device, 3-D fp32 tensors,
     (D, M) in {(1,8), (2,8), (4,8), (8,8), (64,64)}, decay [N,T,D], process and
     observation [N,T], initial mean [N,D,M] and covariance [N,D,D].
-    Keys, values and queries may instead all be bfloat16 (see the module
-    docstring).
+    Keys, values and queries may instead all be bfloat16, or all one float8
+    encoding (see the module docstring).
     """
-    bf16 = all(x.dtype == torch.bfloat16 for x in (keys, values, queries))
+    narrow_dtypes = (torch.bfloat16, *_FP8_FORMATS)
+    bf16 = keys.dtype in narrow_dtypes and all(x.dtype == keys.dtype for x in (values, queries))
     if (
         keys.device.type != "cuda"
         or keys.ndim != 3

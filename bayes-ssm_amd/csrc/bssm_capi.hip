@@ -54,9 +54,13 @@ bool rot4_ok(int d, int m, int64_t t, int64_t nb, bool streams16, std::initializ
 int vec_flag(const float* p, int64_t t, int64_t width) {
   return (p == nullptr || aligned16(p)) && ((t * width) % 4 == 0);
 }
-// The same for a bfloat16 stream (8 elements per 16 bytes).
-int vec_flag16(const void* p, int64_t t, int64_t width) {
-  return (p == nullptr || aligned16(p)) && ((t * width) % 8 == 0);
+// The same for a stream of the input format fmt (InFmt: 4, 8 or 16 elements per 16 bytes).
+int vec_flag_fmt(const void* p, int64_t t, int64_t width, int fmt) {
+  const int64_t per16 = fmt == bssm::kInF32 ? 4 : fmt == bssm::kInBf16 ? 8 : 16;
+  return (p == nullptr || aligned16(p)) && ((t * width) % per16 == 0);
+}
+const char* fmt_name(int fmt) {
+  return fmt == bssm::kInBf16 ? "bfloat16" : fmt == bssm::kInE4M3 ? "float8_e4m3fn" : "float8_e5m2";
 }
 
 int check_common(const char* fn, int d, int m, int64_t n, int64_t t, int64_t chunk, float floor) {
@@ -87,13 +91,14 @@ int launched(const char* fn, hipError_t err) {
   return ok();
 }
 
-// bf16: keys, values and queries point to bfloat16 data (rotated-layout
-// kernels only; anything else is reported as unsupported).
+// fmt (InFmt): keys, values and queries hold float32, bfloat16 or float8
+// data (all but float32: rotated-layout kernels only; anything else is
+// reported as unsupported).
 int forward_impl(const char* fn, bool fixed, int d, int m, const float* keys, const float* values,
                  const float* queries, const float* decay, const float* process, const float* observation,
                  const float* mean0, const float* cov0, float* out, float* mean_final, float* cov_final,
                  float* bmean, float* bcov, int64_t n, int64_t t, int64_t chunk, float floor, void* stream,
-                 bool bf16 = false) {
+                 int fmt = bssm::kInF32) {
   if (int rc = check_common(fn, d, m, n, t, chunk, floor)) return rc;
   BSSM_REQUIRE_T(keys);
   BSSM_REQUIRE_T(values);
@@ -114,19 +119,14 @@ int forward_impl(const char* fn, bool fixed, int d, int m, const float* keys, co
   a.k = keys; a.v = values; a.q = queries; a.d = decay; a.p = process; a.r = observation;
   a.m0 = mean0; a.c0 = cov0; a.y = out; a.mT = mean_final; a.cT = cov_final; a.bm = bmean; a.bc = bcov;
   a.n = n; a.t = t; a.chunk = chunk; a.nb = (t + chunk - 1) / chunk; a.floor = floor;
-  a.bf16 = bf16;
-  if (bf16) {
-    a.vec_kqd = vec_flag16(keys, t, d) && vec_flag16(queries, t, d) && (fixed || vec_flag(decay, t, d));
-    a.vec_v = vec_flag16(values, t, m) && vec_flag(out, t, m);
-  } else {
-    a.vec_kqd = vec_flag(keys, t, d) && vec_flag(queries, t, d) && (fixed || vec_flag(decay, t, d));
-    a.vec_v = vec_flag(values, t, m) && vec_flag(out, t, m);
-  }
+  a.in_fmt = fmt;
+  a.vec_kqd = vec_flag_fmt(keys, t, d, fmt) && vec_flag_fmt(queries, t, d, fmt) && (fixed || vec_flag(decay, t, d));
+  a.vec_v = vec_flag_fmt(values, t, m, fmt) && vec_flag(out, t, m);
   a.vec_pr = fixed || (vec_flag(process, t, 1) && vec_flag(observation, t, 1));
   a.rot4 = rot4_ok(d, m, t, a.nb, a.vec_kqd && a.vec_v && a.vec_pr, {mean0, cov0, mean_final, cov_final, bmean, bcov});
-  if (bf16 && !a.rot4 && n > 0)
-    return fail(BSSM_ERR_UNSUPPORTED, "%s: bfloat16 inputs need D = 4, M = 8, T a positive multiple of 4 and "
-                "16-byte aligned streams", fn);
+  if (fmt != bssm::kInF32 && !a.rot4 && n > 0)
+    return fail(BSSM_ERR_UNSUPPORTED, "%s: %s inputs need D = 4, M = 8, T a positive multiple of 4 and "
+                "16-byte aligned streams", fn, fmt_name(fmt));
   if (n == 0) return ok();
   return launched(fn, bssm::launch_forward(d, fixed, a, static_cast<hipStream_t>(stream)));
 }
@@ -135,13 +135,14 @@ struct BwdOut {
   float *gk, *gv, *gq, *gd, *gp, *gr, *gm0, *gc0;
 };
 
-// bf16: keys, values, queries and their gradients gk, gv, gq point to
-// bfloat16 data (rotated-layout kernels only).
+// fmt (InFmt): keys, values, queries and their gradients gk, gv, gq hold
+// float32, bfloat16 or float8 data (all but float32: rotated-layout kernels
+// only).
 int backward_impl(const char* fn, bool fixed, bool dyn, int d, int m, const float* keys, const float* values,
                   const float* queries, const float* decay, const float* process, const float* observation,
                   const float* mean0, const float* cov0, const float* bmean, const float* bcov, const float* gy,
                   const float* gmf, const float* gcf, BwdOut o, int64_t n, int64_t t, int64_t chunk, float floor,
-                  void* stream, bool bf16 = false) {
+                  void* stream, int fmt = bssm::kInF32) {
   if (int rc = check_common(fn, d, m, n, t, chunk, floor)) return rc;
   BSSM_REQUIRE_T(keys);
   BSSM_REQUIRE_T(values);
@@ -162,23 +163,17 @@ int backward_impl(const char* fn, bool fixed, bool dyn, int d, int m, const floa
   a.m0 = mean0; a.c0 = cov0; a.bm = bmean; a.bc = bcov; a.gy = gy; a.gmf = gmf; a.gcf = gcf;
   a.gk = o.gk; a.gv = o.gv; a.gq = o.gq; a.gd = o.gd; a.gp = o.gp; a.gr = o.gr; a.gm0 = o.gm0; a.gc0 = o.gc0;
   a.n = n; a.t = t; a.chunk = chunk; a.nb = (t + chunk - 1) / chunk; a.floor = floor;
-  a.bf16 = bf16;
-  if (bf16) {
-    a.vec_kqd = vec_flag16(keys, t, d) && vec_flag16(queries, t, d) && (fixed || vec_flag(decay, t, d)) &&
-                vec_flag16(o.gk, t, d) && vec_flag16(o.gq, t, d) && vec_flag(o.gd, t, d);
-    a.vec_v = vec_flag16(values, t, m) && vec_flag(gy, t, m) && vec_flag16(o.gv, t, m);
-  } else {
-    a.vec_kqd = vec_flag(keys, t, d) && vec_flag(queries, t, d) && (fixed || vec_flag(decay, t, d)) &&
-                vec_flag(o.gk, t, d) && vec_flag(o.gq, t, d) && vec_flag(o.gd, t, d);
-    a.vec_v = vec_flag(values, t, m) && vec_flag(gy, t, m) && vec_flag(o.gv, t, m);
-  }
+  a.in_fmt = fmt;
+  a.vec_kqd = vec_flag_fmt(keys, t, d, fmt) && vec_flag_fmt(queries, t, d, fmt) && (fixed || vec_flag(decay, t, d)) &&
+              vec_flag_fmt(o.gk, t, d, fmt) && vec_flag_fmt(o.gq, t, d, fmt) && vec_flag(o.gd, t, d);
+  a.vec_v = vec_flag_fmt(values, t, m, fmt) && vec_flag(gy, t, m) && vec_flag_fmt(o.gv, t, m, fmt);
   a.vec_pr = (fixed || (vec_flag(process, t, 1) && vec_flag(observation, t, 1))) && vec_flag(o.gp, t, 1) &&
              vec_flag(o.gr, t, 1);
   a.rot4 = chunk == bssm::kRot4Chunk &&
            rot4_ok(d, m, t, a.nb, a.vec_kqd && a.vec_v && a.vec_pr, {bmean, bcov, gmf, gcf, o.gm0, o.gc0});
-  if (bf16 && !a.rot4 && n > 0)
-    return fail(BSSM_ERR_UNSUPPORTED, "%s: bfloat16 inputs need D = 4, M = 8, T a positive multiple of 4, "
-                "checkpoint chunk %d and 16-byte aligned streams", fn, bssm::kRot4Chunk);
+  if (fmt != bssm::kInF32 && !a.rot4 && n > 0)
+    return fail(BSSM_ERR_UNSUPPORTED, "%s: %s inputs need D = 4, M = 8, T a positive multiple of 4, "
+                "checkpoint chunk %d and 16-byte aligned streams", fn, fmt_name(fmt), bssm::kRot4Chunk);
   if (n == 0) return ok();
   return launched(fn, bssm::launch_backward(d, fixed, dyn, a, static_cast<hipStream_t>(stream)));
 }
@@ -467,7 +462,7 @@ int bssm_forward_chunked_bf16(int key_dim, int value_dim, int fixed, const void*
   return forward_impl("bssm_forward_chunked_bf16", fixed != 0, key_dim, value_dim, static_cast<const float*>(keys),
                       static_cast<const float*>(values), static_cast<const float*>(queries), decay, process,
                       observation, mean0, cov0, out, mean_final, cov_final, bmean, bcov, n, t, chunk,
-                      denominator_floor, stream, true);
+                      denominator_floor, stream, bssm::kInBf16);
 }
 
 int bssm_backward_chunked_bf16(int key_dim, int value_dim, int fixed, const void* keys, const void* values,
@@ -485,7 +480,53 @@ int bssm_backward_chunked_bf16(int key_dim, int value_dim, int fixed, const void
                        observation, mean0, cov0, bmean, bcov, gy, gmf, gcf,
                        BwdOut{static_cast<float*>(gk), static_cast<float*>(gv), static_cast<float*>(gq), gd, gp, gr,
                               gm0, gc0},
-                       n, t, chunk, denominator_floor, stream, true);
+                       n, t, chunk, denominator_floor, stream, bssm::kInBf16);
+}
+
+int bssm_forward_chunked_fp8(int key_dim, int value_dim, int fixed, int format, const void* keys,
+                             const void* values, const void* queries, const float* decay, const float* process,
+                             const float* observation, const float* mean0, const float* cov0, float* out,
+                             float* mean_final, float* cov_final, float* bmean, float* bcov, int64_t n, int64_t t,
+                             int64_t chunk, float denominator_floor, void* stream) {
+  const char* fn = "bssm_forward_chunked_fp8";
+  if (format != 0 && format != 1)
+    return fail(BSSM_ERR_ARGUMENT, "%s: format must be 0 (float8_e4m3fn) or 1 (float8_e5m2), got %d", fn, format);
+  return forward_impl(fn, fixed != 0, key_dim, value_dim, static_cast<const float*>(keys),
+                      static_cast<const float*>(values), static_cast<const float*>(queries), decay, process,
+                      observation, mean0, cov0, out, mean_final, cov_final, bmean, bcov, n, t, chunk,
+                      denominator_floor, stream, format == 0 ? bssm::kInE4M3 : bssm::kInE5M2);
+}
+
+int bssm_backward_chunked_fp8(int key_dim, int value_dim, int fixed, int format, const void* keys,
+                              const void* values, const void* queries, const float* decay, const float* process,
+                              const float* observation, const float* mean0, const float* cov0, const float* bmean,
+                              const float* bcov, const float* gy, const float* gmf, const float* gcf, void* gk,
+                              void* gv, void* gq, float* gd, float* gp, float* gr, float* gm0, float* gc0,
+                              int64_t n, int64_t t, int64_t chunk, float denominator_floor, void* stream) {
+  const char* fn = "bssm_backward_chunked_fp8";
+  if (format != 0 && format != 1)
+    return fail(BSSM_ERR_ARGUMENT, "%s: format must be 0 (float8_e4m3fn) or 1 (float8_e5m2), got %d", fn, format);
+  const bool dyn = gd != nullptr;
+  if ((gd == nullptr) != (gp == nullptr) || (gd == nullptr) != (gr == nullptr))
+    return fail(BSSM_ERR_ARGUMENT, "%s: gd, gp and gr must be given together or all be null", fn);
+  return backward_impl(fn, fixed != 0, dyn && !fixed, key_dim, value_dim, static_cast<const float*>(keys),
+                       static_cast<const float*>(values), static_cast<const float*>(queries), decay, process,
+                       observation, mean0, cov0, bmean, bcov, gy, gmf, gcf,
+                       BwdOut{static_cast<float*>(gk), static_cast<float*>(gv), static_cast<float*>(gq), gd, gp, gr,
+                              gm0, gc0},
+                       n, t, chunk, denominator_floor, stream, format == 0 ? bssm::kInE4M3 : bssm::kInE5M2);
+}
+
+int bssm_round_float8(int format, const float* x, uint8_t* out, int64_t count) {
+  const char* fn = "bssm_round_float8";
+  if (format != 0 && format != 1)
+    return fail(BSSM_ERR_ARGUMENT, "%s: format must be 0 (float8_e4m3fn) or 1 (float8_e5m2), got %d", fn, format);
+  if (count < 0 || (count > 0 && (x == nullptr || out == nullptr)))
+    return fail(BSSM_ERR_ARGUMENT, "%s: needs count >= 0 and non-null arrays", fn);
+  for (int64_t i = 0; i < count; ++i)
+    out[i] = static_cast<uint8_t>(format == 0 ? bssm::float_to_f8<bssm::kInE4M3>(x[i])
+                                              : bssm::float_to_f8<bssm::kInE5M2>(x[i]));
+  return ok();
 }
 
 int bssm_mixer_forward(const void* q_proj, int64_t ldq, const void* k_proj, int64_t ldk, const void* v_proj,

@@ -2,6 +2,8 @@
 // recurrence kernels (bssm_recurrence.hip).
 #pragma once
 
+#include "bssm_fp8.h"
+
 #include "bssm_common.h"
 
 namespace bssm {
@@ -27,7 +29,7 @@ struct FwdArgs {
   float floor;
   int vec_kqd, vec_v, vec_pr;  // 16-byte staging allowed per stream class
   int rot4;                    // D = 4 rotated-layout kernels allowed (see bssm_rot4.hip)
-  int bf16;                    // k, q, v hold bfloat16 (rotated-layout kernels only)
+  int in_fmt;                  // InFmt of k, q, v (not float32: rotated-layout kernels only)
 };
 
 struct BwdArgs {
@@ -59,7 +61,7 @@ struct BwdArgs {
   float floor;
   int vec_kqd, vec_v, vec_pr;
   int rot4;  // D = 4 rotated-layout kernels allowed (see bssm_rot4.hip)
-  int bf16;  // k, q, v and gk, gq, gv hold bfloat16 (rotated-layout kernels only)
+  int in_fmt;  // InFmt of k, q, v and gk, gq, gv (not float32: rotated-layout kernels only)
 };
 
 // Replay-history tensors of the saved-history ABI.

@@ -36,6 +36,7 @@
 
 #include <type_traits>
 
+#include "bssm_fp8.h"
 #include "bssm_step.h"
 
 namespace bssm {
@@ -696,6 +697,47 @@ struct HalfMap {
       }
     }
   }
+};
+
+// Per-lane maps of the float8 streams of a 16-token tile (16-byte pieces):
+//   k, q: row l >> 2, tokens t0 + 4 (l & 3) .. + 3
+//   v:    row 8I + (l >> 3), tokens t0 + 2 (l & 7) and + 1 (I < 2)
+// Each 32-bit word of a piece is one token's 4 key values (k, q; word u is
+// token k_tok + u) or half of a token's 8 values (v; word w is token
+// v_tok + (w >> 1), values 4 (w & 1) .. + 3).  k_lds / v_lds are the LDS
+// float offsets of the float32 piece each word becomes, in HalfMap's slot
+// layout; a row's 64 (k, q) or 128 (v) bytes of the tile are read by 4 or 8
+// consecutive lanes.
+struct QuarterMap {
+  int k_lds[4], v_lds[2][4];
+  uint32_t k_off, v_off[2];
+  int k_tok, v_tok;  // first token of the lane's pieces within the tile
+  __device__ __forceinline__ QuarterMap(int lane, int slot_floats, uint32_t row4q, uint32_t row8q) {
+    const int kr = lane >> 2, pc = lane & 3, ki = kr >> 3, k8 = kr & 7;
+    k_tok = 4 * pc;
+    k_off = static_cast<uint32_t>(kr) * row4q + static_cast<uint32_t>(pc) * 16u;
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int tok = k_tok + u, tt = tok & 7;
+      k_lds[u] = (tok >> 3) * slot_floats + 4 * (64 * ki + 8 * (tt ^ ki) + k8);
+    }
+    const int tp = lane & 7;
+    v_tok = 2 * tp;
+#pragma unroll
+    for (int I = 0; I < 2; ++I) {
+      const int vr = 8 * I + (lane >> 3), vi = vr >> 2, a4 = vr & 3;
+      v_off[I] = static_cast<uint32_t>(vr) * row8q + static_cast<uint32_t>(tp) * 16u;
+#pragma unroll
+      for (int w = 0; w < 4; ++w) {
+        const int tok = v_tok + (w >> 1), c = 2 * (tok & 7) + (w & 1);
+        v_lds[I][w] = (tok >> 3) * slot_floats + 4 * (64 * vi + 4 * (c ^ (2 * vi)) + a4);
+      }
+    }
+  }
+};
+// Register staging of a forward tile with float8 keys, queries and values.
+struct FwdStageQ {
+  v4f k, q, d[4], v[2], p, r;
 };
 
 // ----------------------------------------------------------------- backward

@@ -8,8 +8,10 @@
 namespace bssm {
 namespace r4 {
 
-template <bool FIXED, bool H>
+// F: format of keys, queries and values (InFmt): float32, bfloat16 or float8.
+template <bool FIXED, int F>
 __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(1, 1))) void forward_kernel(FwdArgs a) {
+  constexpr bool H = F == kInBf16, Q8 = F >= kInE4M3, W = F == kInF32;
   __shared__ float tile[2 * FwdTile::SIZE];
   __shared__ float ckst[kRecFloats];  // checkpoint staging
   const int lane = threadIdx.x;
@@ -19,8 +21,8 @@ __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(1, 1))) v
   const uint32_t valid = static_cast<uint32_t>((a.n - n0) < SPW ? (a.n - n0) : SPW);
   const uint32_t row4 = static_cast<uint32_t>(T) * 16u, row8 = static_cast<uint32_t>(T) * 32u,
                  row1 = static_cast<uint32_t>(T) * 4u;
-  // Keys, queries and values are bf16 (half the row bytes) when H.
-  const uint32_t kb = H ? 2u : 1u;
+  // Keys, queries and values take half (bf16) or a quarter (float8) of the float32 row bytes.
+  const uint32_t kb = H ? 2u : Q8 ? 4u : 1u;
   const Rsrc rk = make_rsrc(byte_offset(a.k, n0 * T * 16 / kb), valid * row4 / kb);
   const Rsrc rq = make_rsrc(byte_offset(a.q, n0 * T * 16 / kb), valid * row4 / kb);
   const Rsrc rv = make_rsrc(byte_offset(a.v, n0 * T * 32 / kb), valid * row8 / kb);
@@ -38,6 +40,7 @@ __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(1, 1))) v
 
   const Map mp(lane, row4, row8, row1);
   const HalfMap hm(lane, FwdTile::SIZE, row4 / 2, row8 / 2);
+  const QuarterMap qm(lane, FwdTile::SIZE, row4 / 4, row8 / 4);
   const uint32_t off1 = static_cast<uint32_t>(lane >> 2) * row1 + static_cast<uint32_t>(lane & 3) * 16u;
   const int dst1 = ((lane & 3) >> 1) * FwdTile::SIZE + 4 * (2 * (lane >> 2) + (lane & 1));
 
@@ -46,8 +49,15 @@ __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(1, 1))) v
   load_bel(core.b, rm0, rc0, unit, 0, 0);
   core.store_ckpt(0, rbm, rbc);
 
-  using Stage = std::conditional_t<H, FwdStageH, FwdStage>;
+  using Stage = std::conditional_t<H, FwdStageH, std::conditional_t<Q8, FwdStageQ, FwdStage>>;
   auto load = [&](Stage& x, int64_t t0) __attribute__((always_inline)) {
+    if constexpr (Q8) {
+      const uint32_t sk = static_cast<uint32_t>(t0) * 4u, sv = static_cast<uint32_t>(t0) * 8u;
+      x.k = ld128<kNtLoad>(rk, qm.k_off + sk);
+      x.q = ld128<kNtLoad>(rq, qm.k_off + sk);
+#pragma unroll
+      for (int I = 0; I < 2; ++I) x.v[I] = ld128<kNtLoad>(rv, qm.v_off[I] + sv);
+    }
     if constexpr (H) {
       const uint32_t sk = static_cast<uint32_t>(t0) * 8u, sv = static_cast<uint32_t>(t0) * 16u;
 #pragma unroll
@@ -63,13 +73,13 @@ __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(1, 1))) v
       const uint32_t s4 = static_cast<uint32_t>(t0 + TT * h) * 16u, s8 = static_cast<uint32_t>(t0 + TT * h) * 32u;
 #pragma unroll
       for (int j = 0; j < 2; ++j) {
-        if constexpr (!H) {
+        if constexpr (W) {
           x.k[2 * h + j] = ld128<kNtLoad>(rk, mp.d4[j] + s4);
           x.q[2 * h + j] = ld128<kNtLoad>(rq, mp.d4[j] + s4);
         }
         if constexpr (!FIXED) x.d[2 * h + j] = ld128<kNtLoad>(rd, mp.d4[j] + s4);
       }
-      if constexpr (!H) {
+      if constexpr (W) {
 #pragma unroll
         for (int j = 0; j < 4; ++j) x.v[4 * h + j] = ld128<kNtLoad>(rv, mp.d8[j] + s8);
       }
@@ -81,6 +91,20 @@ __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(1, 1))) v
     }
   };
   auto put = [&](const Stage& x) __attribute__((always_inline)) {
+    if constexpr (Q8) {
+      const v4u wk = __builtin_bit_cast(v4u, x.k), wq = __builtin_bit_cast(v4u, x.q);
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        *reinterpret_cast<v4f*>(&tile[FwdTile::K + qm.k_lds[u]]) = widen_f8<F>(wk[u]);
+        *reinterpret_cast<v4f*>(&tile[FwdTile::Q + qm.k_lds[u]]) = widen_f8<F>(wq[u]);
+      }
+#pragma unroll
+      for (int I = 0; I < 2; ++I) {
+        const v4u wv = __builtin_bit_cast(v4u, x.v[I]);
+#pragma unroll
+        for (int w = 0; w < 4; ++w) *reinterpret_cast<v4f*>(&tile[FwdTile::V + qm.v_lds[I][w]]) = widen_f8<F>(wv[w]);
+      }
+    }
     if constexpr (H) {
 #pragma unroll
       for (int I = 0; I < 2; ++I) {
@@ -100,13 +124,13 @@ __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(1, 1))) v
       float* tl = tile + h * FwdTile::SIZE;
 #pragma unroll
       for (int j = 0; j < 2; ++j) {
-        if constexpr (!H) {
+        if constexpr (W) {
           *reinterpret_cast<v4f*>(&(tl + FwdTile::K)[256 * j + 4 * lane]) = x.k[2 * h + j];
           *reinterpret_cast<v4f*>(&(tl + FwdTile::Q)[256 * j + 4 * lane]) = x.q[2 * h + j];
         }
         if constexpr (!FIXED) *reinterpret_cast<v4f*>(&(tl + FwdTile::D)[256 * j + 4 * lane]) = x.d[2 * h + j];
       }
-      if constexpr (!H) {
+      if constexpr (W) {
 #pragma unroll
         for (int j = 0; j < 4; ++j) *reinterpret_cast<v4f*>(&(tl + FwdTile::V)[256 * j + 4 * lane]) = x.v[4 * h + j];
       }
@@ -293,10 +317,20 @@ struct BwdStageH {
 struct BwdOutH {
   v4f k[2], q[2], v[4], d[4], p, r;
 };
+// The same with float8 keys, queries and values (QuarterMap pieces).
+struct BwdStageQ {
+  v4f k, q, v[2], d[4], gy[8], p, r;
+};
+struct BwdOutQ {
+  v4f k, q, v[2], d[4], p, r;
+};
 
-template <bool FIXED, bool DYN>
+// F: kInBf16, kInE4M3 or kInE5M2 (keys, queries, values and their gradients).
+template <bool FIXED, bool DYN, int F>
 __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(1, 1))) void backward_bf16_kernel(
     BwdArgs a) {
+  constexpr bool Q8 = F >= kInE4M3;
+  constexpr uint32_t kb = Q8 ? 4u : 2u;  // float32 row bytes per stream row byte
   __shared__ float tile[2 * BwdTile::SIZE];
   const int lane = threadIdx.x;
   const int g = lane & 3, s = lane >> 2;
@@ -305,13 +339,14 @@ __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(1, 1))) v
   const uint32_t valid = static_cast<uint32_t>((a.n - n0) < SPW ? (a.n - n0) : SPW);
   const uint32_t row4 = static_cast<uint32_t>(T) * 16u, row8 = static_cast<uint32_t>(T) * 32u,
                  row1 = static_cast<uint32_t>(T) * 4u;
-  const uint32_t row4h = row4 / 2, row8h = row8 / 2;
-  const Rsrc rk = make_rsrc(byte_offset(a.k, n0 * T * 8), valid * row4h);
-  const Rsrc rq = make_rsrc(byte_offset(a.q, n0 * T * 8), valid * row4h);
-  const Rsrc rv = make_rsrc(byte_offset(a.v, n0 * T * 16), valid * row8h);
-  const Rsrc rgk = make_rsrc(byte_offset(a.gk, n0 * T * 8), valid * row4h);
-  const Rsrc rgq = make_rsrc(byte_offset(a.gq, n0 * T * 8), valid * row4h);
-  const Rsrc rgv = make_rsrc(byte_offset(a.gv, n0 * T * 16), valid * row8h);
+  const uint32_t row4h = row4 / kb, row8h = row8 / kb;
+  const int64_t e4 = 16 / kb, e8 = 32 / kb;  // stream bytes per token of k / v
+  const Rsrc rk = make_rsrc(byte_offset(a.k, n0 * T * e4), valid * row4h);
+  const Rsrc rq = make_rsrc(byte_offset(a.q, n0 * T * e4), valid * row4h);
+  const Rsrc rv = make_rsrc(byte_offset(a.v, n0 * T * e8), valid * row8h);
+  const Rsrc rgk = make_rsrc(byte_offset(a.gk, n0 * T * e4), valid * row4h);
+  const Rsrc rgq = make_rsrc(byte_offset(a.gq, n0 * T * e4), valid * row4h);
+  const Rsrc rgv = make_rsrc(byte_offset(a.gv, n0 * T * e8), valid * row8h);
   const Rsrc rgy = make_rsrc(a.gy + n0 * T * 8, valid * row8);
   const Rsrc rd = make_rsrc(FIXED ? a.gy : a.d + n0 * T * 4, valid * row4);
   const Rsrc rp = make_rsrc(FIXED ? a.gy : a.p + n0 * T, valid * row1);
@@ -325,6 +360,7 @@ __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(1, 1))) v
 
   const Map mp(lane, row4, row8, row1);
   const HalfMap hm(lane, BwdTile::SIZE, row4h, row8h);
+  const QuarterMap qm(lane, BwdTile::SIZE, row4h, row8h);
   // p and r: one instruction per 16-token tile, lane -> row lane >> 2, piece
   // lane & 3 (tokens 4 (lane & 3) .. + 3), into the chunk slot of its tokens.
   const uint32_t off1 = static_cast<uint32_t>(lane >> 2) * row1 + static_cast<uint32_t>(lane & 3) * 16u;
@@ -337,16 +373,25 @@ __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(1, 1))) v
   const int64_t nb = a.nb;
   const int64_t ntiles = (nb + 1) / 2;
 
-  auto load = [&](BwdStageH& x, int64_t J) __attribute__((always_inline)) {
+  using Stage = std::conditional_t<Q8, BwdStageQ, BwdStageH>;
+  using Out = std::conditional_t<Q8, BwdOutQ, BwdOutH>;
+  auto load = [&](Stage& x, int64_t J) __attribute__((always_inline)) {
     const int64_t t0 = J * 2 * SUB;
-    const uint32_t sk = static_cast<uint32_t>(t0) * 8u, sv = static_cast<uint32_t>(t0) * 16u;
+    const uint32_t sk = static_cast<uint32_t>(t0 * e4), sv = static_cast<uint32_t>(t0 * e8);
+    if constexpr (Q8) {
+      x.k = ld128<kNtLoad>(rk, qm.k_off + sk);
+      x.q = ld128<kNtLoad>(rq, qm.k_off + sk);
 #pragma unroll
-    for (int I = 0; I < 2; ++I) {
-      x.k[I] = ld128<kNtLoad>(rk, hm.k_off[I] + sk);
-      x.q[I] = ld128<kNtLoad>(rq, hm.k_off[I] + sk);
+      for (int I = 0; I < 2; ++I) x.v[I] = ld128<kNtLoad>(rv, qm.v_off[I] + sv);
+    } else {
+#pragma unroll
+      for (int I = 0; I < 2; ++I) {
+        x.k[I] = ld128<kNtLoad>(rk, hm.k_off[I] + sk);
+        x.q[I] = ld128<kNtLoad>(rq, hm.k_off[I] + sk);
+      }
+#pragma unroll
+      for (int I = 0; I < 4; ++I) x.v[I] = ld128<kNtLoad>(rv, hm.v_off[I] + sv);
     }
-#pragma unroll
-    for (int I = 0; I < 4; ++I) x.v[I] = ld128<kNtLoad>(rv, hm.v_off[I] + sv);
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
       const uint32_t s4 = static_cast<uint32_t>(t0 + SUB * h) * 16u, s8 = static_cast<uint32_t>(t0 + SUB * h) * 32u;
@@ -363,18 +408,33 @@ __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(1, 1))) v
       x.r = ld128<false>(rr, off1 + s1);
     }
   };
-  auto put = [&](const BwdStageH& x) __attribute__((always_inline)) {
+  auto put = [&](const Stage& x) __attribute__((always_inline)) {
+    if constexpr (Q8) {
+      const v4u wk = __builtin_bit_cast(v4u, x.k), wq = __builtin_bit_cast(v4u, x.q);
 #pragma unroll
-    for (int I = 0; I < 2; ++I) {
-      *reinterpret_cast<v4f*>(&tile[BwdTile::K + hm.k_lds[I][0]]) = widen_lo(x.k[I]);
-      *reinterpret_cast<v4f*>(&tile[BwdTile::K + hm.k_lds[I][1]]) = widen_hi(x.k[I]);
-      *reinterpret_cast<v4f*>(&tile[BwdTile::Q + hm.k_lds[I][0]]) = widen_lo(x.q[I]);
-      *reinterpret_cast<v4f*>(&tile[BwdTile::Q + hm.k_lds[I][1]]) = widen_hi(x.q[I]);
-    }
+      for (int u = 0; u < 4; ++u) {
+        *reinterpret_cast<v4f*>(&tile[BwdTile::K + qm.k_lds[u]]) = widen_f8<F>(wk[u]);
+        *reinterpret_cast<v4f*>(&tile[BwdTile::Q + qm.k_lds[u]]) = widen_f8<F>(wq[u]);
+      }
 #pragma unroll
-    for (int I = 0; I < 4; ++I) {
-      *reinterpret_cast<v4f*>(&tile[BwdTile::V + hm.v_lds[I][0]]) = widen_lo(x.v[I]);
-      *reinterpret_cast<v4f*>(&tile[BwdTile::V + hm.v_lds[I][1]]) = widen_hi(x.v[I]);
+      for (int I = 0; I < 2; ++I) {
+        const v4u wv = __builtin_bit_cast(v4u, x.v[I]);
+#pragma unroll
+        for (int w = 0; w < 4; ++w) *reinterpret_cast<v4f*>(&tile[BwdTile::V + qm.v_lds[I][w]]) = widen_f8<F>(wv[w]);
+      }
+    } else {
+#pragma unroll
+      for (int I = 0; I < 2; ++I) {
+        *reinterpret_cast<v4f*>(&tile[BwdTile::K + hm.k_lds[I][0]]) = widen_lo(x.k[I]);
+        *reinterpret_cast<v4f*>(&tile[BwdTile::K + hm.k_lds[I][1]]) = widen_hi(x.k[I]);
+        *reinterpret_cast<v4f*>(&tile[BwdTile::Q + hm.k_lds[I][0]]) = widen_lo(x.q[I]);
+        *reinterpret_cast<v4f*>(&tile[BwdTile::Q + hm.k_lds[I][1]]) = widen_hi(x.q[I]);
+      }
+#pragma unroll
+      for (int I = 0; I < 4; ++I) {
+        *reinterpret_cast<v4f*>(&tile[BwdTile::V + hm.v_lds[I][0]]) = widen_lo(x.v[I]);
+        *reinterpret_cast<v4f*>(&tile[BwdTile::V + hm.v_lds[I][1]]) = widen_hi(x.v[I]);
+      }
     }
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
@@ -400,18 +460,36 @@ __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(1, 1))) v
     dma16<kNtCkpt>(rbm, (tl + BwdTile::CK) + 256, ckoff.m1 + cm);
     dma16(rbc, (tl + BwdTile::CK) + 512, ckoff.c + cc);
   };
-  auto take = [&](BwdOutH& o) __attribute__((always_inline)) {
+  auto take = [&](Out& o) __attribute__((always_inline)) {
+    if constexpr (Q8) {
+      v4u wk, wq;
 #pragma unroll
-    for (int I = 0; I < 2; ++I) {
-      o.k[I] = narrow(*reinterpret_cast<const v4f*>(&tile[BwdTile::K + hm.k_lds[I][0]]),
-                      *reinterpret_cast<const v4f*>(&tile[BwdTile::K + hm.k_lds[I][1]]));
-      o.q[I] = narrow(*reinterpret_cast<const v4f*>(&tile[BwdTile::Q + hm.k_lds[I][0]]),
-                      *reinterpret_cast<const v4f*>(&tile[BwdTile::Q + hm.k_lds[I][1]]));
+      for (int u = 0; u < 4; ++u) {
+        wk[u] = narrow_f8<F>(*reinterpret_cast<const v4f*>(&tile[BwdTile::K + qm.k_lds[u]]));
+        wq[u] = narrow_f8<F>(*reinterpret_cast<const v4f*>(&tile[BwdTile::Q + qm.k_lds[u]]));
+      }
+      o.k = __builtin_bit_cast(v4f, wk);
+      o.q = __builtin_bit_cast(v4f, wq);
+#pragma unroll
+      for (int I = 0; I < 2; ++I) {
+        v4u wv;
+#pragma unroll
+        for (int w = 0; w < 4; ++w) wv[w] = narrow_f8<F>(*reinterpret_cast<const v4f*>(&tile[BwdTile::V + qm.v_lds[I][w]]));
+        o.v[I] = __builtin_bit_cast(v4f, wv);
+      }
+    } else {
+#pragma unroll
+      for (int I = 0; I < 2; ++I) {
+        o.k[I] = narrow(*reinterpret_cast<const v4f*>(&tile[BwdTile::K + hm.k_lds[I][0]]),
+                        *reinterpret_cast<const v4f*>(&tile[BwdTile::K + hm.k_lds[I][1]]));
+        o.q[I] = narrow(*reinterpret_cast<const v4f*>(&tile[BwdTile::Q + hm.k_lds[I][0]]),
+                        *reinterpret_cast<const v4f*>(&tile[BwdTile::Q + hm.k_lds[I][1]]));
+      }
+#pragma unroll
+      for (int I = 0; I < 4; ++I)
+        o.v[I] = narrow(*reinterpret_cast<const v4f*>(&tile[BwdTile::V + hm.v_lds[I][0]]),
+                        *reinterpret_cast<const v4f*>(&tile[BwdTile::V + hm.v_lds[I][1]]));
     }
-#pragma unroll
-    for (int I = 0; I < 4; ++I)
-      o.v[I] = narrow(*reinterpret_cast<const v4f*>(&tile[BwdTile::V + hm.v_lds[I][0]]),
-                      *reinterpret_cast<const v4f*>(&tile[BwdTile::V + hm.v_lds[I][1]]));
 #pragma unroll
     for (int h = 0; h < 2; ++h)
 #pragma unroll
@@ -421,17 +499,25 @@ __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(1, 1))) v
     o.r = *reinterpret_cast<const v4f*>(&tile[BwdTile::R + dst1]);
   };
   // Gradients of tile J; pieces of tokens at or past T are dropped.
-  auto store_grads = [&](const BwdOutH& o, int64_t J) __attribute__((always_inline)) {
+  auto store_grads = [&](const Out& o, int64_t J) __attribute__((always_inline)) {
     const int64_t t0 = J * 2 * SUB;
-    const uint32_t sk = static_cast<uint32_t>(t0) * 8u, sv = static_cast<uint32_t>(t0) * 16u;
-    const bool kin = t0 + hm.k_tok < T, vin = t0 + hm.v_tok < T;
+    const uint32_t sk = static_cast<uint32_t>(t0 * e4), sv = static_cast<uint32_t>(t0 * e8);
+    if constexpr (Q8) {
+      const bool kin = t0 + qm.k_tok < T, vin = t0 + qm.v_tok < T;
+      st128<kNtStore>(rgk, o.k, kin ? qm.k_off : kOob, sk);
+      st128<kNtStore>(rgq, o.q, kin ? qm.k_off : kOob, sk);
 #pragma unroll
-    for (int I = 0; I < 2; ++I) {
-      st128<kNtStore>(rgk, o.k[I], kin ? hm.k_off[I] : kOob, sk);
-      st128<kNtStore>(rgq, o.q[I], kin ? hm.k_off[I] : kOob, sk);
+      for (int I = 0; I < 2; ++I) st128<kNtStore>(rgv, o.v[I], vin ? qm.v_off[I] : kOob, sv);
+    } else {
+      const bool kin = t0 + hm.k_tok < T, vin = t0 + hm.v_tok < T;
+#pragma unroll
+      for (int I = 0; I < 2; ++I) {
+        st128<kNtStore>(rgk, o.k[I], kin ? hm.k_off[I] : kOob, sk);
+        st128<kNtStore>(rgq, o.q[I], kin ? hm.k_off[I] : kOob, sk);
+      }
+#pragma unroll
+      for (int I = 0; I < 4; ++I) st128<kNtStore>(rgv, o.v[I], vin ? hm.v_off[I] : kOob, sv);
     }
-#pragma unroll
-    for (int I = 0; I < 4; ++I) st128<kNtStore>(rgv, o.v[I], vin ? hm.v_off[I] : kOob, sv);
     if (a.gd) {
 #pragma unroll
       for (int h = 0; h < 2; ++h) {
@@ -463,13 +549,13 @@ __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(1, 1))) v
   // gradients of tile J + 1 are read out of LDS, the tile's staged inputs
   // written there, those gradients stored, the loads of tile J - 1 issued,
   // and chunks 2J + 1 and 2J replayed and reversed.
-  BwdStageH st;
+  Stage st;
   load(st, ntiles - 1);
   issue_ck(tile, 2 * (ntiles - 1));
   if (2 * ntiles - 1 < nb) issue_ck(tile + BwdTile::SIZE, 2 * ntiles - 1);
   else if (ntiles > 1) issue_ck(tile + BwdTile::SIZE, 2 * ntiles - 3);
   for (int64_t J = ntiles - 1; J >= 0; --J) {
-    BwdOutH go;
+    Out go;
     vm_wait<0>();
     if (J + 1 < ntiles) take(go);
     __builtin_amdgcn_sched_barrier(0);
@@ -482,7 +568,7 @@ __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(1, 1))) v
     run_chunk(tile, 2 * J);
   }
   {
-    BwdOutH go;
+    Out go;
     take(go);
     store_grads(go, 0);
   }
@@ -496,12 +582,22 @@ hipError_t launch_forward_r4(bool fixed, const FwdArgs& a, hipStream_t stream) {
   const int64_t blocks = (a.n + r4::SPW - 1) / r4::SPW;
   if (blocks == 0) return hipSuccess;
   const dim3 grid(static_cast<unsigned>(blocks)), block(kWave);
-  if (a.bf16) {
-    if (fixed) hipLaunchKernelGGL((r4::forward_kernel<true, true>), grid, block, 0, stream, a);
-    else hipLaunchKernelGGL((r4::forward_kernel<false, true>), grid, block, 0, stream, a);
-  } else {
-    if (fixed) hipLaunchKernelGGL((r4::forward_kernel<true, false>), grid, block, 0, stream, a);
-    else hipLaunchKernelGGL((r4::forward_kernel<false, false>), grid, block, 0, stream, a);
+  switch (a.in_fmt) {
+    case kInBf16:
+      if (fixed) hipLaunchKernelGGL((r4::forward_kernel<true, kInBf16>), grid, block, 0, stream, a);
+      else hipLaunchKernelGGL((r4::forward_kernel<false, kInBf16>), grid, block, 0, stream, a);
+      break;
+    case kInE4M3:
+      if (fixed) hipLaunchKernelGGL((r4::forward_kernel<true, kInE4M3>), grid, block, 0, stream, a);
+      else hipLaunchKernelGGL((r4::forward_kernel<false, kInE4M3>), grid, block, 0, stream, a);
+      break;
+    case kInE5M2:
+      if (fixed) hipLaunchKernelGGL((r4::forward_kernel<true, kInE5M2>), grid, block, 0, stream, a);
+      else hipLaunchKernelGGL((r4::forward_kernel<false, kInE5M2>), grid, block, 0, stream, a);
+      break;
+    default:
+      if (fixed) hipLaunchKernelGGL((r4::forward_kernel<true, kInF32>), grid, block, 0, stream, a);
+      else hipLaunchKernelGGL((r4::forward_kernel<false, kInF32>), grid, block, 0, stream, a);
   }
   return hipGetLastError();
 }
@@ -510,10 +606,18 @@ hipError_t launch_backward_r4(bool fixed, bool dyn, const BwdArgs& a, hipStream_
   const int64_t blocks = (a.n + r4::SPW - 1) / r4::SPW;
   if (blocks == 0) return hipSuccess;
   const dim3 grid(static_cast<unsigned>(blocks)), block(kWave);
-  if (a.bf16) {
-    if (fixed) hipLaunchKernelGGL((r4::backward_bf16_kernel<true, false>), grid, block, 0, stream, a);
-    else if (dyn) hipLaunchKernelGGL((r4::backward_bf16_kernel<false, true>), grid, block, 0, stream, a);
-    else hipLaunchKernelGGL((r4::backward_bf16_kernel<false, false>), grid, block, 0, stream, a);
+  if (a.in_fmt == kInBf16) {
+    if (fixed) hipLaunchKernelGGL((r4::backward_bf16_kernel<true, false, kInBf16>), grid, block, 0, stream, a);
+    else if (dyn) hipLaunchKernelGGL((r4::backward_bf16_kernel<false, true, kInBf16>), grid, block, 0, stream, a);
+    else hipLaunchKernelGGL((r4::backward_bf16_kernel<false, false, kInBf16>), grid, block, 0, stream, a);
+  } else if (a.in_fmt == kInE4M3) {
+    if (fixed) hipLaunchKernelGGL((r4::backward_bf16_kernel<true, false, kInE4M3>), grid, block, 0, stream, a);
+    else if (dyn) hipLaunchKernelGGL((r4::backward_bf16_kernel<false, true, kInE4M3>), grid, block, 0, stream, a);
+    else hipLaunchKernelGGL((r4::backward_bf16_kernel<false, false, kInE4M3>), grid, block, 0, stream, a);
+  } else if (a.in_fmt == kInE5M2) {
+    if (fixed) hipLaunchKernelGGL((r4::backward_bf16_kernel<true, false, kInE5M2>), grid, block, 0, stream, a);
+    else if (dyn) hipLaunchKernelGGL((r4::backward_bf16_kernel<false, true, kInE5M2>), grid, block, 0, stream, a);
+    else hipLaunchKernelGGL((r4::backward_bf16_kernel<false, false, kInE5M2>), grid, block, 0, stream, a);
   } else {
     if (fixed) hipLaunchKernelGGL((r4::backward_kernel<true, false>), grid, block, 0, stream, a);
     else if (dyn) hipLaunchKernelGGL((r4::backward_kernel<false, true>), grid, block, 0, stream, a);

@@ -41,11 +41,12 @@ def algorithmic_bytes(d: int, m: int) -> tuple[int, int]:
     return (inputs + m) * 4, (2 * inputs + m) * 4
 
 
-def make_workload(b, t, h, d, m, device, seed=0, bf16_kqv=False):
-    """Synthetic config-3 inputs; k, v, q are bf16 values (kept as bfloat16 tensors when bf16_kqv)."""
+def make_workload(b, t, h, d, m, device, seed=0, kqv_dtype=None):
+    """Synthetic config-3 inputs; k, v, q are bf16 values (kept as tensors of kqv_dtype when given:
+    bfloat16, or a float8 dtype, rounded from the bf16 values)."""
     n = b * h
     g = torch.Generator(device=device).manual_seed(seed)
-    cast = (lambda x: x.bfloat16()) if bf16_kqv else (lambda x: x.bfloat16().float())
+    cast = (lambda x: x.bfloat16().to(kqv_dtype)) if kqv_dtype is not None else (lambda x: x.bfloat16().float())
     k = cast(torch.randn(n, t, d, device=device, generator=g))
     v = cast(torch.randn(n, t, m, device=device, generator=g))
     q = cast(torch.randn(n, t, d, device=device, generator=g))
@@ -69,16 +70,16 @@ def cpu_model() -> str:
     return "unknown CPU"
 
 
-def time_layer(b, t, h, d, m, chunk, steps, warmup, device, bf16_kqv=False) -> dict:
+def time_layer(b, t, h, d, m, chunk, steps, warmup, device, kqv_dtype=None) -> dict:
     """fwd+bwd of fused_diagonal_bayesian at one shape: ms/step, tokens/s, step roofline fraction.
 
-    With bf16_kqv the keys, values and queries are bfloat16 tensors (read as
-    such by the kernels; their gradients are bfloat16) and the roofline bytes
-    count the dtypes actually streamed.
+    With kqv_dtype (bfloat16 or a float8 dtype) the keys, values and queries
+    are tensors of that dtype (read as such by the kernels; their gradients
+    have it too) and the roofline bytes count the dtypes actually streamed.
     """
     from bayes_ssm import fused_cuda
 
-    leaves, m0, c0, gy = make_workload(b, t, h, d, m, device, seed=1, bf16_kqv=bf16_kqv)
+    leaves, m0, c0, gy = make_workload(b, t, h, d, m, device, seed=1, kqv_dtype=kqv_dtype)
 
     def step():
         y, _, _ = fused_cuda.fused_diagonal_bayesian(*leaves, m0, c0, chunk_length=chunk, denominator_floor=1e-6)
@@ -95,14 +96,16 @@ def time_layer(b, t, h, d, m, chunk, steps, warmup, device, bf16_kqv=False) -> d
     torch.cuda.synchronize()
     ms = e0.elapsed_time(e1) / steps
     fwd_b, bwd_b = algorithmic_bytes(d, m)
-    if bf16_kqv:
-        # k, q, v (2D + M values) read at 2 bytes in both passes and their
-        # gradients written at 2 bytes: 3 (2D + M) x 2 bytes fewer.
-        fwd_b -= (2 * d + m) * 2
-        bwd_b -= (2 * d + m) * 4
+    if kqv_dtype is not None:
+        # k, q, v (2D + M values) read at the narrow width in both passes and
+        # their gradients written at it: 3 (2D + M) x (4 - width) bytes fewer.
+        saved = 4 - torch.empty(0, dtype=kqv_dtype).element_size()
+        fwd_b -= (2 * d + m) * saved
+        bwd_b -= (2 * d + m) * 2 * saved
     out = {"B": b, "T": t, "H": h, "D": d, "M": m, "ms_per_step": ms, "tokens_per_s": b * t / (ms * 1e-3),
            "roofline_step_frac": (fwd_b + bwd_b) * b * h * t / (ms * 1e-3) / HBM_PEAK}
-    if bf16_kqv:
+    if kqv_dtype is not None:
+        out["kqv_dtype"] = str(kqv_dtype).replace("torch.", "")
         out["bytes_per_token_head"] = fwd_b + bwd_b
     return out
 
@@ -483,10 +486,12 @@ def main() -> int:
     ap.add_argument("--cpu-budget", type=float, default=20.0, help="seconds of CPU-baseline work (0 = skip)")
     ap.add_argument("--no-extras", action="store_true",
                     help="skip the secondary shapes (per-GPU DP shape, D1/D2/D8 variants, associative scan)")
-    ap.add_argument("--secondary", choices=("mixer", "mixer-readout", "block", "conv4", "rotation", "d64"),
+    ap.add_argument("--secondary", choices=("mixer", "mixer-readout", "block", "conv4", "rotation", "d64",
+                                            "kqv-bf16", "kqv-fp8"),
                     help="time only one secondary workload at the configured shape (the mixer's fused layer core, "
                          "with its readout epilogue, config 4's whole Bayes block, or the causal depthwise-4 filter "
-                         "on the q/k/v stream, the rotation core or D = M = 64), for "
+                         "on the q/k/v stream, the rotation core, D = M = 64, or the layer with bf16 / float8 "
+                         "k/v/q tensors), for "
                          "profiling its kernels; prints its own JSON line")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="also run one 256 MiB device copy (reference kernel for PMC byte counters)")
@@ -513,6 +518,9 @@ def main() -> int:
             row = time_d64(b, t, h, args.steps, args.warmup, device, fused=True)
         elif args.secondary == "block":
             row = time_block(b, t, h, args.steps, args.warmup, device)
+        elif args.secondary.startswith("kqv-"):
+            dt = torch.bfloat16 if args.secondary == "kqv-bf16" else torch.float8_e4m3fn
+            row = time_layer(b, t, h, d, m, args.chunk, args.steps, args.warmup, device, kqv_dtype=dt)
         else:
             row = time_mixer(b, t, h, args.steps, args.warmup, device, fused=True,
                              gated=args.secondary == "mixer-readout")
@@ -634,7 +642,10 @@ def main() -> int:
         # (fused producer kernels, and the reference op chain beside it),
         # config 4's Bayes block (filter + layer core + gated readout), and
         # the associative-scan configs (forward, and fwd+bwd).
-        extras = {"config3_bf16_kqv": time_layer(b, t, h, d, m, args.chunk, 30, 10, device, bf16_kqv=True),
+        extras = {"config3_bf16_kqv": time_layer(b, t, h, d, m, args.chunk, 30, 10, device,
+                                                 kqv_dtype=torch.bfloat16),
+                  "config3_fp8_kqv": time_layer(b, t, h, d, m, args.chunk, 30, 10, device,
+                                                kqv_dtype=torch.float8_e4m3fn),
                   "dp8_share_d4m8": time_layer(b // 8, t, h, d, m, args.chunk, 30, 10, device)}
         for name, (eb, ed) in {"config3_d2m8": (b, 2), "config3_d8m8": (b, 8), "config2_d1m8": (64, 1)}.items():
             extras[name] = time_layer(eb, t, h, ed, m, args.chunk, 10, 3, device)

@@ -258,6 +258,37 @@ int bssm_backward_chunked_bf16(int key_dim, int value_dim, int fixed,
                                int64_t n, int64_t t, int64_t chunk, float denominator_floor,
                                void* stream);
 
+/* float8 keys, values and queries (format 0: torch.float8_e4m3fn, 1:
+ * torch.float8_e5m2, the OCP encodings), for D = 4, M = 8 under the same
+ * conditions as the bfloat16 entry points.  The kernels widen each value to
+ * float32 on chip (exactly), so outputs equal those of the float32 entry
+ * points on the widened inputs, bit for bit; the gradients of keys, values
+ * and queries leave as float8, the float32 gradient rounded to nearest even
+ * with torch's overflow rules (bssm_round_float8).  Replaces the float32
+ * promotion of float8 inputs (bayes_ssm/bayesian_layer.py:823-827) feeding
+ * the float32 entry points; no counterpart in the reference library. */
+int bssm_forward_chunked_fp8(int key_dim, int value_dim, int fixed, int format,
+                             const void* keys, const void* values, const void* queries,
+                             const float* decay, const float* process, const float* observation,
+                             const float* mean0, const float* cov0,
+                             float* out, float* mean_final, float* cov_final, float* bmean, float* bcov,
+                             int64_t n, int64_t t, int64_t chunk, float denominator_floor, void* stream);
+int bssm_backward_chunked_fp8(int key_dim, int value_dim, int fixed, int format,
+                              const void* keys, const void* values, const void* queries,
+                              const float* decay, const float* process, const float* observation,
+                              const float* mean0, const float* cov0, const float* bmean, const float* bcov,
+                              const float* gy, const float* gmf, const float* gcf,
+                              void* gk, void* gv, void* gq, float* gd, float* gp, float* gr,
+                              float* gm0, float* gc0,
+                              int64_t n, int64_t t, int64_t chunk, float denominator_floor, void* stream);
+
+/* Host-side float32 -> float8 rounding of the float8 gradients (format as
+ * above): round to nearest even; e4m3fn gives the NaN code 0x7f (with the
+ * sign) for magnitudes that round past 448, for infinities and NaN; e5m2
+ * overflows to infinity and gives 0x7f for NaN.  This is torch's
+ * float32 -> float8 conversion; no counterpart in the reference library. */
+int bssm_round_float8(int format, const float* x, uint8_t* out, int64_t count);
+
 /* ------------------------------------------------------------------------
  * Static (A = I, Q = 0) associative scan in information form.
  * Replaces the torch-op chain of `associative_static_bayesian`
