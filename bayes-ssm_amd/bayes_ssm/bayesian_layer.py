@@ -98,15 +98,52 @@ def _check_finite(x: Tensor, name: str) -> None:
         raise ValueError(f"{name} must contain only finite values")
 
 
-def _validate_variance(x: Tensor, name: str, *, strictly_positive: bool) -> None:
-    _check_finite(x, name)
-    if _skip_host_checks(x) or x.numel() == 0:
-        return
-    lowest = float(x.detach().min())
-    if strictly_positive and lowest <= 0:
-        raise ValueError(f"{name} must be strictly positive")
-    if not strictly_positive and lowest < 0:
-        raise ValueError(f"{name} must be nonnegative")
+class _DeferredChecks:
+    """bayesian_layer's value checks (finite entries; variance signs) as device reductions read back with one
+    device->host copy.
+
+    The reference checks each tensor in turn, each check with its own
+    synchronization (bayesian_layer.py:105-129).  Here every check is one
+    ``aminmax`` reduction (NaN propagates to both ends, infinities show at
+    one), and ``flush`` reads them all at once and raises the first failing
+    check in registration order, with the reference's messages.  Callers
+    flush before a check that synchronizes on its own and when a shape or type
+    error interrupts the sequence, so errors come in the reference's order.
+    """
+
+    def __init__(self) -> None:
+        self._pending: list[tuple[str, Optional[bool], Tensor]] = []
+
+    def _add(self, x: Tensor, name: str, kind: Optional[bool]) -> None:
+        if x.numel() == 0 or _skip_host_checks(x):
+            return
+        lo, hi = torch.aminmax(x.detach())
+        self._pending.append((name, kind, torch.stack((lo, hi)).double()))
+
+    def finite(self, x: Tensor, name: str) -> None:
+        self._add(x, name, None)
+
+    def variance(self, x: Tensor, name: str, *, strictly_positive: bool) -> None:
+        self._add(x, name, strictly_positive)
+
+    def flush(self) -> None:
+        pending, self._pending = self._pending, []
+        if not pending:
+            return
+        by_device: dict[torch.device, list[int]] = {}
+        for i, (_, _, stats) in enumerate(pending):
+            by_device.setdefault(stats.device, []).append(i)
+        values: list = [None] * len(pending)
+        for idx in by_device.values():
+            for i, pair in zip(idx, torch.stack([pending[i][2] for i in idx]).tolist()):
+                values[i] = pair
+        for (name, kind, _), (lo, hi) in zip(pending, values):
+            if not (math.isfinite(lo) and math.isfinite(hi)):
+                raise ValueError(f"{name} must contain only finite values")
+            if kind is True and lo <= 0:
+                raise ValueError(f"{name} must be strictly positive")
+            if kind is False and lo < 0:
+                raise ValueError(f"{name} must be nonnegative")
 
 
 def _validate_covariance(x: Tensor, name: str, d: int) -> None:
@@ -341,124 +378,132 @@ def bayesian_layer(
     bf16_kqv = ((keys, values, queries)
                 if keys.dtype in narrow and all(x.dtype == keys.dtype for x in (values, queries)) else None)
     keys, values, queries = keys.to(dtype), values.to(dtype), queries.to(dtype)
-    for x, name in ((keys, "keys"), (values, "values"), (queries, "queries")):
-        _check_finite(x, name)
-    if (rotation_radii is None) != (rotation_angles is None):
-        raise ValueError("rotation_radii and rotation_angles must be supplied together")
-    if transitions is not None and transition_diagonals is not None:
-        raise ValueError("pass transitions or transition_diagonals, not both")
-    if rotation_radii is not None and (transitions is not None or transition_diagonals is not None):
-        raise ValueError("rotation dynamics are mutually exclusive with transitions and transition_diagonals")
-    if not isinstance(replay_ssm, bool):
-        raise TypeError("replay_ssm must be a bool")
-    if not isinstance(fixed_dynamics, bool):
-        raise TypeError("fixed_dynamics must be a bool")
+    checks = _DeferredChecks()
+    try:
+        for x, name in ((keys, "keys"), (values, "values"), (queries, "queries")):
+            checks.finite(x, name)
+        if (rotation_radii is None) != (rotation_angles is None):
+            raise ValueError("rotation_radii and rotation_angles must be supplied together")
+        if transitions is not None and transition_diagonals is not None:
+            raise ValueError("pass transitions or transition_diagonals, not both")
+        if rotation_radii is not None and (transitions is not None or transition_diagonals is not None):
+            raise ValueError("rotation dynamics are mutually exclusive with transitions and transition_diagonals")
+        if not isinstance(replay_ssm, bool):
+            raise TypeError("replay_ssm must be a bool")
+        if not isinstance(fixed_dynamics, bool):
+            raise TypeError("fixed_dynamics must be a bool")
 
-    diagonal: Optional[Tensor] = None
-    rotation = False
-    if rotation_radii is not None:
-        if d % 2:
-            raise ValueError("rotational dynamics require an even key dimension")
-        checked = []
-        for name, x in (("rotation_radii", rotation_radii), ("rotation_angles", rotation_angles)):
-            if not isinstance(x, Tensor) or x.ndim < 2:
-                raise ValueError(f"{name} must have shape [..., T={t}, D/2={d // 2}]")
-            if not x.is_floating_point():
-                raise TypeError(f"{name} must have a floating-point dtype")
-            if x.shape[-2:] != (t, d // 2):
-                raise ValueError(f"{name} must end in {(t, d // 2)}, got {tuple(x.shape)}")
-            if not _broadcastable(x.shape[:-2], batch_shape):
-                raise ValueError(f"{name} batch dimensions are not broadcastable to input batch")
-            x = x.to(device=device, dtype=dtype)
-            _check_finite(x, name)
-            checked.append(x)
-        rotation_radii, rotation_angles = checked
-        rotation = True
-    elif transition_diagonals is not None:
-        if not isinstance(transition_diagonals, Tensor) or transition_diagonals.ndim < 2:
-            raise ValueError(f"transition_diagonals must have shape [..., T={t}, D={d}]")
-        if not transition_diagonals.is_floating_point():
-            raise TypeError("transition_diagonals must have a floating-point dtype")
-        diagonal = transition_diagonals.to(device=device, dtype=dtype)
-        if diagonal.shape[-2:] != (t, d):
-            raise ValueError(f"transition_diagonals must end in {(t, d)}, got {tuple(diagonal.shape)}")
-        if not _broadcastable(diagonal.shape[:-2], batch_shape):
-            raise ValueError("transition_diagonals batch dimensions are not broadcastable to the input batch")
-        _check_finite(diagonal, "transition_diagonals")
-    elif transitions is None:
-        transitions = torch.eye(d, device=device, dtype=dtype).expand(*batch_shape, t, d, d)
-    else:
-        if not isinstance(transitions, Tensor) or transitions.ndim < 3:
-            raise ValueError(f"transitions must have shape [..., T={t}, D={d}, D={d}]")
-        if not transitions.is_floating_point():
-            raise TypeError("transitions must have a floating-point dtype")
-        transitions = transitions.to(device=device, dtype=dtype)
-        if transitions.shape[-3:] != (t, d, d):
-            raise ValueError(f"transitions must end in {(t, d, d)}, got {tuple(transitions.shape)}")
-        if not _broadcastable(transitions.shape[:-3], batch_shape):
-            raise ValueError("transitions batch dimensions are not broadcastable to the input batch")
-        _check_finite(transitions, "transitions")
-
-    if rotation:
-        if process_covariances is not None:
-            raise ValueError("rotational dynamics require per-pair process_variances, not process_covariances")
-        if process_variances is None:
-            process_variances = torch.zeros(*batch_shape, t, d // 2, device=device, dtype=dtype)
+        diagonal: Optional[Tensor] = None
+        rotation = False
+        if rotation_radii is not None:
+            if d % 2:
+                raise ValueError("rotational dynamics require an even key dimension")
+            checked = []
+            for name, x in (("rotation_radii", rotation_radii), ("rotation_angles", rotation_angles)):
+                if not isinstance(x, Tensor) or x.ndim < 2:
+                    raise ValueError(f"{name} must have shape [..., T={t}, D/2={d // 2}]")
+                if not x.is_floating_point():
+                    raise TypeError(f"{name} must have a floating-point dtype")
+                if x.shape[-2:] != (t, d // 2):
+                    raise ValueError(f"{name} must end in {(t, d // 2)}, got {tuple(x.shape)}")
+                if not _broadcastable(x.shape[:-2], batch_shape):
+                    raise ValueError(f"{name} batch dimensions are not broadcastable to input batch")
+                x = x.to(device=device, dtype=dtype)
+                checks.finite(x, name)
+                checked.append(x)
+            rotation_radii, rotation_angles = checked
+            rotation = True
+        elif transition_diagonals is not None:
+            if not isinstance(transition_diagonals, Tensor) or transition_diagonals.ndim < 2:
+                raise ValueError(f"transition_diagonals must have shape [..., T={t}, D={d}]")
+            if not transition_diagonals.is_floating_point():
+                raise TypeError("transition_diagonals must have a floating-point dtype")
+            diagonal = transition_diagonals.to(device=device, dtype=dtype)
+            if diagonal.shape[-2:] != (t, d):
+                raise ValueError(f"transition_diagonals must end in {(t, d)}, got {tuple(diagonal.shape)}")
+            if not _broadcastable(diagonal.shape[:-2], batch_shape):
+                raise ValueError("transition_diagonals batch dimensions are not broadcastable to the input batch")
+            checks.finite(diagonal, "transition_diagonals")
+        elif transitions is None:
+            transitions = torch.eye(d, device=device, dtype=dtype).expand(*batch_shape, t, d, d)
         else:
-            process_variances = _as_tensor(process_variances, device=device, dtype=dtype, name="process_variances")
-            if process_variances.ndim == 0 or (process_variances.shape[-2:] == (t, d // 2)
-                                               and _broadcastable(process_variances.shape[:-2], batch_shape)):
-                process_variances = process_variances.expand(*batch_shape, t, d // 2)
-            else:
-                raise ValueError(f"rotational process_variances must be scalar or end in {(t, d // 2)}")
-            _validate_variance(process_variances, "process_variances", strictly_positive=False)
-    elif process_covariances is not None and process_variances is not None:
-        raise ValueError("pass process_covariances or process_variances, not both")
-    elif process_covariances is not None:
-        if not isinstance(process_covariances, Tensor) or process_covariances.ndim < 3:
-            raise ValueError(f"process_covariances must have shape [..., T={t}, D={d}, D={d}]")
-        if not process_covariances.is_floating_point():
-            raise TypeError("process_covariances must have a floating-point dtype")
-        process_covariances = process_covariances.to(device=device, dtype=dtype)
-        if process_covariances.shape[-3:] != (t, d, d):
-            raise ValueError(f"process_covariances must end in {(t, d, d)}, got {tuple(process_covariances.shape)}")
-        if not _broadcastable(process_covariances.shape[:-3], batch_shape):
-            raise ValueError("process_covariances batch dimensions are not broadcastable to the input batch")
-        _validate_covariance(process_covariances, "process_covariances", d)
-    else:
-        process_variances = _as_time_tensor(0.0 if process_variances is None else process_variances, t,
-                                            batch_shape, "process_variances", device=device, dtype=dtype)
-        _validate_variance(process_variances, "process_variances", strictly_positive=False)
-        if not (optimized and diagonal is not None):
-            process_covariances = process_variances[..., None, None] * torch.eye(d, device=device, dtype=dtype)
-    observation_variances = _as_time_tensor(1.0 if observation_variances is None else observation_variances, t,
-                                            batch_shape, "observation_variances", device=device, dtype=dtype)
-    _validate_variance(observation_variances, "observation_variances", strictly_positive=True)
+            if not isinstance(transitions, Tensor) or transitions.ndim < 3:
+                raise ValueError(f"transitions must have shape [..., T={t}, D={d}, D={d}]")
+            if not transitions.is_floating_point():
+                raise TypeError("transitions must have a floating-point dtype")
+            transitions = transitions.to(device=device, dtype=dtype)
+            if transitions.shape[-3:] != (t, d, d):
+                raise ValueError(f"transitions must end in {(t, d, d)}, got {tuple(transitions.shape)}")
+            if not _broadcastable(transitions.shape[:-3], batch_shape):
+                raise ValueError("transitions batch dimensions are not broadcastable to the input batch")
+            checks.finite(transitions, "transitions")
 
-    if initial_mean is None:
-        mean = torch.zeros(*batch_shape, d, m, device=device, dtype=dtype)
-    else:
-        if not isinstance(initial_mean, Tensor) or initial_mean.ndim < 2:
-            raise ValueError(f"initial_mean must have shape [..., D={d}, m={m}]")
-        if not initial_mean.is_floating_point():
-            raise TypeError("initial_mean must have a floating-point dtype")
-        mean = initial_mean.to(device=device, dtype=dtype)
-        if mean.shape[-2:] != (d, m) or not _broadcastable(mean.shape[:-2], batch_shape):
-            raise ValueError("initial_mean has incompatible dimensions or batch shape")
-        _check_finite(mean, "initial_mean")
-        mean = mean.expand(*batch_shape, d, m)
-    if initial_covariance is None:
-        cov = torch.eye(d, device=device, dtype=dtype).expand(*batch_shape, d, d).clone()
-    else:
-        if not isinstance(initial_covariance, Tensor) or initial_covariance.ndim < 2:
-            raise ValueError(f"initial_covariance must have shape [..., D={d}, D={d}]")
-        if not initial_covariance.is_floating_point():
-            raise TypeError("initial_covariance must have a floating-point dtype")
-        cov = initial_covariance.to(device=device, dtype=dtype)
-        if not _broadcastable(cov.shape[:-2], batch_shape):
-            raise ValueError("initial_covariance batch dimensions are not broadcastable to the input batch")
-        _validate_covariance(cov, "initial_covariance", d)
-        cov = cov.expand(*batch_shape, d, d)
+        if rotation:
+            if process_covariances is not None:
+                raise ValueError("rotational dynamics require per-pair process_variances, not process_covariances")
+            if process_variances is None:
+                process_variances = torch.zeros(*batch_shape, t, d // 2, device=device, dtype=dtype)
+            else:
+                process_variances = _as_tensor(process_variances, device=device, dtype=dtype, name="process_variances")
+                if process_variances.ndim == 0 or (process_variances.shape[-2:] == (t, d // 2)
+                                                   and _broadcastable(process_variances.shape[:-2], batch_shape)):
+                    process_variances = process_variances.expand(*batch_shape, t, d // 2)
+                else:
+                    raise ValueError(f"rotational process_variances must be scalar or end in {(t, d // 2)}")
+                checks.variance(process_variances, "process_variances", strictly_positive=False)
+        elif process_covariances is not None and process_variances is not None:
+            raise ValueError("pass process_covariances or process_variances, not both")
+        elif process_covariances is not None:
+            if not isinstance(process_covariances, Tensor) or process_covariances.ndim < 3:
+                raise ValueError(f"process_covariances must have shape [..., T={t}, D={d}, D={d}]")
+            if not process_covariances.is_floating_point():
+                raise TypeError("process_covariances must have a floating-point dtype")
+            process_covariances = process_covariances.to(device=device, dtype=dtype)
+            if process_covariances.shape[-3:] != (t, d, d):
+                raise ValueError(f"process_covariances must end in {(t, d, d)}, got {tuple(process_covariances.shape)}")
+            if not _broadcastable(process_covariances.shape[:-3], batch_shape):
+                raise ValueError("process_covariances batch dimensions are not broadcastable to the input batch")
+            checks.flush()
+            _validate_covariance(process_covariances, "process_covariances", d)
+        else:
+            process_variances = _as_time_tensor(0.0 if process_variances is None else process_variances, t,
+                                                batch_shape, "process_variances", device=device, dtype=dtype)
+            checks.variance(process_variances, "process_variances", strictly_positive=False)
+            if not (optimized and diagonal is not None):
+                process_covariances = process_variances[..., None, None] * torch.eye(d, device=device, dtype=dtype)
+        observation_variances = _as_time_tensor(1.0 if observation_variances is None else observation_variances, t,
+                                                batch_shape, "observation_variances", device=device, dtype=dtype)
+        checks.variance(observation_variances, "observation_variances", strictly_positive=True)
+
+        if initial_mean is None:
+            mean = torch.zeros(*batch_shape, d, m, device=device, dtype=dtype)
+        else:
+            if not isinstance(initial_mean, Tensor) or initial_mean.ndim < 2:
+                raise ValueError(f"initial_mean must have shape [..., D={d}, m={m}]")
+            if not initial_mean.is_floating_point():
+                raise TypeError("initial_mean must have a floating-point dtype")
+            mean = initial_mean.to(device=device, dtype=dtype)
+            if mean.shape[-2:] != (d, m) or not _broadcastable(mean.shape[:-2], batch_shape):
+                raise ValueError("initial_mean has incompatible dimensions or batch shape")
+            checks.finite(mean, "initial_mean")
+            mean = mean.expand(*batch_shape, d, m)
+        if initial_covariance is None:
+            cov = torch.eye(d, device=device, dtype=dtype).expand(*batch_shape, d, d).clone()
+        else:
+            if not isinstance(initial_covariance, Tensor) or initial_covariance.ndim < 2:
+                raise ValueError(f"initial_covariance must have shape [..., D={d}, D={d}]")
+            if not initial_covariance.is_floating_point():
+                raise TypeError("initial_covariance must have a floating-point dtype")
+            cov = initial_covariance.to(device=device, dtype=dtype)
+            if not _broadcastable(cov.shape[:-2], batch_shape):
+                raise ValueError("initial_covariance batch dimensions are not broadcastable to the input batch")
+            checks.flush()
+            _validate_covariance(cov, "initial_covariance", d)
+            cov = cov.expand(*batch_shape, d, d)
+    except (ValueError, TypeError):
+        checks.flush()  # a value error the reference would have raised first
+        raise
+    checks.flush()
 
     if not isinstance(denominator_floor, Real) or not math.isfinite(float(denominator_floor)):
         raise ValueError("denominator_floor must be finite")

@@ -414,19 +414,18 @@ class _MixerBlockFunction(torch.autograd.Function):
         gconv = torch.empty(b, t, core, device=dev, dtype=torch.bfloat16)
         cpart = torch.empty(b, core, 4, device=dev, dtype=torch.float32)
         npart = torch.empty(b * heads // 16, VALUE_DIM, device=dev, dtype=torch.float32)
+        apart = torch.empty(b, aux_w, device=dev, dtype=torch.float32) if need[3] else None
         gm0 = torch.empty_like(mean0) if need[4] else None
         gc0 = torch.empty_like(cov0) if need[5] else None
         P = _hip.ptr
         with torch.cuda.device(dev):
             _hip.call("bssm_mixer_block_backward", P(projected), ctx.ld, P(cw32), P(aux), aux_w, P(convolved),
                       P(nw32), ctx.norm_eps, P(mean0), P(cov0), P(bmean), P(bcov), P(read_bf16), P(grad_out), P(gm),
-                      P(gc), P(gconv), P(gproj), gproj.shape[-1], P(cpart), P(npart), P(gm0), P(gc0), b, t, heads,
-                      ctx.interval, ctx.denominator_floor, _hip.stream_of(dev))
+                      P(gc), P(gconv), P(gproj), gproj.shape[-1], P(cpart), P(npart), P(apart), P(gm0), P(gc0), b, t,
+                      heads, ctx.interval, ctx.denominator_floor, _hip.stream_of(dev))
         g_conv = cpart.sum(0).reshape(ctx.conv_shape).to(ctx.conv_dtype) if need[1] else None
         g_norm = npart.sum(0).to(ctx.norm_dtype) if need[2] else None
-        g_bias = None
-        if need[3]:
-            g_bias = torch.sum(gproj[..., core:core + aux_w], dim=(0, 1), dtype=torch.float32).to(ctx.bias_dtype)
+        g_bias = apart.sum(0).to(ctx.bias_dtype) if need[3] else None
         return gproj if need[0] else None, g_conv, g_norm, g_bias, gm0, gc0, None, None, None, None
 
 

@@ -764,8 +764,9 @@ int bssm_mixer_block_backward(const void* projected, int64_t ld_projected, const
                               const float* bcov, const void* read_bf16, const void* grad_out, const float* gmf,
                               const float* gcf, void* grad_convolved, void* grad_projected,
                               int64_t ld_grad_projected, float* grad_conv_weight_partials,
-                              float* grad_norm_weight_partials, float* gm0, float* gc0, int64_t batch, int64_t t,
-                              int64_t heads, int64_t chunk, float denominator_floor, void* stream) {
+                              float* grad_norm_weight_partials, float* grad_aux_partials, float* gm0, float* gc0,
+                              int64_t batch, int64_t t, int64_t heads, int64_t chunk, float denominator_floor,
+                              void* stream) {
   const char* fn = "bssm_mixer_block_backward";
   const BlockStreams s(projected, aux, ld_aux, convolved, heads);
   if (int rc = block_check(fn, projected, ld_projected, conv_weight, aux, ld_aux, convolved, batch, t, heads, chunk,
@@ -812,7 +813,10 @@ int bssm_mixer_block_backward(const void* projected, int64_t ld_projected, const
   c.x = projected; c.ldx = ld_projected; c.w = conv_weight; c.gy = grad_convolved; c.gx = grad_projected;
   c.ldgx = ld_grad_projected; c.gw_part = grad_conv_weight_partials; c.b = batch; c.t = t; c.c = 16 * heads;
   c.bf16 = 1;
-  return launched(fn, bssm::launch_conv4_backward(c, st));
+  if (hipError_t e = bssm::launch_conv4_backward(c, st); e != hipSuccess) return launched(fn, e);
+  if (grad_aux_partials == nullptr) return ok();
+  return launched(fn, bssm::launch_column_sums_bf16(gp + 2 * 16 * heads, ld_grad_projected, batch, t, 6 * heads,
+                                                    grad_aux_partials, st));
 }
 
 int bssm_rotation_checkpoint(int key_dim) { return bssm::rotation_checkpoint(key_dim); }

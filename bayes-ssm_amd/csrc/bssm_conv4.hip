@@ -274,6 +274,42 @@ __global__ __launch_bounds__(256) void reduce_partials_kernel(const float* __res
   gw[i] = (s0 + s1) + (s2 + s3);
 }
 
+// Column sums over the T rows of each batch entry of a bf16 [B, T, cols]
+// view with row stride ld: out [B, cols] (float32).  A lane owns a column
+// pair (one 4-byte load per row, a wave reading 256 contiguous bytes of a
+// row); the block's 4 waves take every 4th row and meet in LDS.
+__global__ __launch_bounds__(256) void column_sums_kernel(const uint32_t* __restrict__ x, int64_t ld2, int64_t t,
+                                                          int64_t pairs, float* __restrict__ out) {
+  __shared__ float red[kWaves - 1][kWave][2];
+  const int wave = threadIdx.x / kWave, lane = threadIdx.x & (kWave - 1);
+  const int64_t b = blockIdx.y;
+  const int64_t cp = static_cast<int64_t>(blockIdx.x) * kWave + lane;
+  const bool active = cp < pairs;
+  const uint32_t* row = x + b * t * ld2 + (active ? cp : 0);
+  float s0 = 0.f, s1 = 0.f;
+  if (active) {
+    for (int64_t r = wave; r < t; r += kWaves) {
+      const uint32_t w = row[r * ld2];
+      s0 += __builtin_bit_cast(float, w << 16);
+      s1 += __builtin_bit_cast(float, w & 0xffff0000u);
+    }
+  }
+  if (wave > 0) {
+    red[wave - 1][lane][0] = s0;
+    red[wave - 1][lane][1] = s1;
+  }
+  __syncthreads();
+  if (wave == 0 && active) {
+#pragma unroll
+    for (int k = 0; k < kWaves - 1; ++k) {
+      s0 += red[k][lane][0];
+      s1 += red[k][lane][1];
+    }
+    out[b * 2 * pairs + 2 * cp] = s0;
+    out[b * 2 * pairs + 2 * cp + 1] = s1;
+  }
+}
+
 constexpr int kMaxDevices = 64;
 std::mutex g_scratch_mutex;
 float* g_scratch[kMaxDevices] = {};
@@ -312,6 +348,16 @@ hipError_t launch_conv4_backward_noalloc(const ConvArgs& args, float* grad_weigh
   if (cw == 0) return hipSuccess;
   const dim3 grid(static_cast<unsigned>((cw + 255) / 256)), block(256);
   hipLaunchKernelGGL(conv4::reduce_partials_kernel, grid, block, 0, stream, part, grad_weight, a.b, cw);
+  return hipGetLastError();
+}
+
+hipError_t launch_column_sums_bf16(const void* x, int64_t ld, int64_t b, int64_t t, int64_t cols, float* out,
+                                  hipStream_t stream) {
+  const int64_t pairs = cols / 2;
+  if (b == 0 || pairs == 0) return hipSuccess;
+  const dim3 grid(static_cast<unsigned>((pairs + conv4::kWave - 1) / conv4::kWave), static_cast<unsigned>(b));
+  hipLaunchKernelGGL(conv4::column_sums_kernel, grid, dim3(conv4::kWave * conv4::kWaves), 0, stream,
+                     static_cast<const uint32_t*>(x), ld / 2, t, pairs, out);
   return hipGetLastError();
 }
 

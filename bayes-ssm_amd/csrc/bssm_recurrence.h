@@ -207,6 +207,10 @@ hipError_t launch_conv4_backward(const ConvArgs& a, hipStream_t stream);
 // kConv4ScratchFloats (checked by the caller).
 constexpr int64_t kConv4ScratchFloats = int64_t(1) << 21;
 hipError_t launch_conv4_backward_noalloc(const ConvArgs& a, float* grad_weight, hipStream_t stream);
+// Column sums over T of a bf16 [B, T, cols] view (row stride ld elements,
+// cols and ld even, 4-byte aligned): out [B, cols] float32.
+hipError_t launch_column_sums_bf16(const void* x, int64_t ld, int64_t b, int64_t t, int64_t cols, float* out,
+                                  hipStream_t stream);
 
 hipError_t launch_associative_scan(const float* k, const float* v, const float* q, const float* r,
                                    const float* m0, const float* c0, float* y, float* mT, float* cT,

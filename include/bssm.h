@@ -523,8 +523,10 @@ int bssm_mixer_block_forward(const void* projected, int64_t ld_projected, const 
  * filter's input gradient into the core columns, the aux and gate gradients
  * into theirs (the aux gradient is also aux_bias's per token).  Workspace
  * grad_convolved: bf16 [B, T, 16H].  The weight gradients come as partial
- * sums: grad_conv_weight_partials [B, 16H, 4] (sum over the first axis) and
- * grad_norm_weight_partials [B*H/16, 8] (column sums), float32. */
+ * sums: grad_conv_weight_partials [B, 16H, 4] (sum over the first axis),
+ * grad_norm_weight_partials [B*H/16, 8] (column sums) and, when not NULL,
+ * grad_aux_partials [B, 6H] (the aux gradient summed over T; its column
+ * sums are aux_bias's gradient), float32. */
 int bssm_mixer_block_backward(const void* projected, int64_t ld_projected, const float* conv_weight,
                               const void* aux, int64_t ld_aux, const void* convolved,
                               const float* norm_weight, float norm_eps,
@@ -533,7 +535,7 @@ int bssm_mixer_block_backward(const void* projected, int64_t ld_projected, const
                               const float* gmf, const float* gcf,
                               void* grad_convolved, void* grad_projected, int64_t ld_grad_projected,
                               float* grad_conv_weight_partials, float* grad_norm_weight_partials,
-                              float* gm0, float* gc0,
+                              float* grad_aux_partials, float* gm0, float* gc0,
                               int64_t batch, int64_t t, int64_t heads, int64_t chunk,
                               float denominator_floor, void* stream);
 

@@ -295,6 +295,36 @@ def test_validation_errors(mutate, exc, message):
         bayesian_layer(keys, values, queries, **args)
 
 
+def _nan_at(x, i=2):
+    return x.clone().index_fill_(1, torch.tensor([i]), float("nan"))
+
+
+@pytest.mark.parametrize("mutate, message", [
+    # A value error registered before a shape/type error is raised first, as the reference checks in turn.
+    (lambda a: a.update(keys=_nan_at(a["keys"]), rotation_radii=torch.ones(2, 5, 1)), "keys must contain only"),
+    (lambda a: a.update(queries=_nan_at(a["queries"]), replay_ssm=1), "queries must contain only"),
+    # Shape errors before any failing value check keep their place.
+    (lambda a: a.update(observation_variances=0.0, chunk_length=0), "strictly positive"),
+    (lambda a: a.update(rotation_radii=torch.ones(2, 5, 1), observation_variances=0.0), "together"),
+    # Among value checks the first registered wins.
+    (lambda a: a.update(values=_nan_at(a["values"]), observation_variances=0.0), "values must contain only"),
+    (lambda a: a.update(process_variances=-0.1, observation_variances=0.0), "nonnegative"),
+    (lambda a: a.update(observation_variances=float("inf")), "observation_variances must contain only"),
+    (lambda a: a.update(transition_diagonals=_nan_at(torch.ones(2, 5, 2))), "transition_diagonals must contain"),
+    (lambda a: a.update(initial_mean=torch.full((2, 3), float("nan")), observation_variances=0.0),
+     "strictly positive"),
+    (lambda a: a.update(process_variances=-0.1, initial_covariance=-torch.eye(2)), "nonnegative"),
+])
+def test_deferred_value_checks_keep_the_reference_order(mutate, message):
+    """Finite/sign checks are read back together; errors still come in the reference's order."""
+    k, v, q = _valid()
+    args = dict(keys=k, values=v, queries=q)
+    mutate(args)
+    keys, values, queries = args.pop("keys"), args.pop("values"), args.pop("queries")
+    with pytest.raises((ValueError, TypeError), match=message):
+        bayesian_layer(keys, values, queries, **args)
+
+
 def test_empty_time_axis_returns_the_prior():
     k, v, q = (x[:, :0] for x in _valid())
     y, mT, cT = bayesian_layer(k, v, q)

@@ -165,10 +165,10 @@ def test_block_argument_errors_are_reported(lib):
     assert _block_fwd(lib) == 1 and b"required" in lib.bssm_last_error()
     assert _block_fwd(lib, b=0) == 0
     rc = lib.bssm_mixer_block_backward(None, 480, None, None, 0, None, None, ctypes.c_float(1e-6), *([None] * 10),
-                                       480, *([None] * 4), 1, 8, 16, 8, ctypes.c_float(1e-6), None)
+                                       480, *([None] * 5), 1, 8, 16, 8, ctypes.c_float(1e-6), None)
     assert rc == 1 and b"required" in lib.bssm_last_error()
     rc = lib.bssm_mixer_block_backward(None, 480, None, None, 0, None, None, ctypes.c_float(1e-6), *([None] * 10),
-                                       472, *([None] * 4), 0, 8, 16, 8, ctypes.c_float(1e-6), None)
+                                       472, *([None] * 5), 0, 8, 16, 8, ctypes.c_float(1e-6), None)
     assert rc == 1 and b"grad_projected" in lib.bssm_last_error()
 
 
