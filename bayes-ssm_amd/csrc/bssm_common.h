@@ -131,6 +131,39 @@ using OwnRowVec = float[Layout<D, M, G>::RPL];
 template <int D, int G>
 __device__ __forceinline__ void group_reduce_rows(const float (&x)[D], float (&own)[(D >= G) ? D / G : 1],
                                                   int g) {
+  if constexpr (D == 8 && G == 8) {
+    // Eight lanes, one row each (row g): halve on the top lane bit first, so
+    // that its partner can be the half-row mirror (lane 7 - g, which also
+    // differs in bit 2) and every exchange stays a DPP move.  Stage k splits
+    // the rows still held on bit (2 - k) of the row index; the partner holds
+    // the same rows and keeps the other half.
+    float cur[8];
+#pragma unroll
+    for (int r = 0; r < 8; ++r) cur[r] = x[r];
+#pragma unroll
+    for (int k = 0; k < 3; ++k) {
+      const int half = 4 >> k;
+      const bool hi = (g >> (2 - k)) & 1;
+#pragma unroll
+      for (int m = 0; m < half; ++m) {
+        // Both halves summed with the partner's copy (two DPP adds), one select.
+        float lo, up;
+        if (k == 0) {
+          lo = cur[m] + dpp<kHalfMirror>(cur[m]);
+          up = cur[half + m] + dpp<kHalfMirror>(cur[half + m]);
+        } else if (k == 1) {
+          lo = cur[m] + xor_lane<1>(cur[m]);
+          up = cur[half + m] + xor_lane<1>(cur[half + m]);
+        } else {
+          lo = cur[m] + xor_lane<0>(cur[m]);
+          up = cur[half + m] + xor_lane<0>(cur[half + m]);
+        }
+        cur[m] = hi ? up : lo;
+      }
+    }
+    own[0] = cur[0];
+    return;
+  }
   constexpr int RS = (D >= G) ? G : D;  // lanes taking part in the scatter
   float cur[D];
 #pragma unroll
