@@ -288,7 +288,20 @@ __global__ __launch_bounds__(256) void column_sums_kernel(const uint32_t* __rest
   const uint32_t* row = x + b * t * ld2 + (active ? cp : 0);
   float s0 = 0.f, s1 = 0.f;
   if (active) {
-    for (int64_t r = wave; r < t; r += kWaves) {
+    // Eight rows' loads in flight before their sums.
+    constexpr int kAhead = 8;
+    int64_t r = wave;
+    for (; r + (kAhead - 1) * kWaves < t; r += kAhead * kWaves) {
+      uint32_t w[kAhead];
+#pragma unroll
+      for (int i = 0; i < kAhead; ++i) w[i] = row[(r + i * kWaves) * ld2];
+#pragma unroll
+      for (int i = 0; i < kAhead; ++i) {
+        s0 += __builtin_bit_cast(float, w[i] << 16);
+        s1 += __builtin_bit_cast(float, w[i] & 0xffff0000u);
+      }
+    }
+    for (; r < t; r += kWaves) {
       const uint32_t w = row[r * ld2];
       s0 += __builtin_bit_cast(float, w << 16);
       s1 += __builtin_bit_cast(float, w & 0xffff0000u);
