@@ -194,6 +194,27 @@ def test_backward_matches_oracle(ext, cuda_device, abi, final_grads, chunk, t):
         assert torch.equal(grads[7], grads[7].transpose(-1, -2)), "gc0 must be bitwise symmetric"
 
 
+def test_long_sequence_matches_oracle(ext, cuda_device):
+    """T = 160 (20 checkpoint chunks): forward and full backward against the float64 oracle."""
+    n, t, chunk = 2, 160, 8
+    print(f"d64 long t={t}", flush=True)
+    cpu, dev = _case(n, t, seed=99, device=cuda_device)
+    ref = _f64(cpu)
+    y, mT, cT, bm, bc = ext.forward_chunked(dev["k"], dev["v"], dev["q"], dev["d"], dev["p"], dev["r"], dev["m0"],
+                                            dev["c0"], chunk, 1e-6)
+    grads = ext.backward_chunked(dev["k"], dev["v"], dev["q"], dev["d"], dev["p"], dev["r"], dev["m0"], dev["c0"],
+                                 bm, bc, dev["gy"], dev["gmf"], dev["gcf"], chunk, 1e-6)
+    torch.cuda.synchronize()
+    ey, em, ec, eg = O.diagonal_grads(ref["k"], ref["v"], ref["q"], ref["d"], ref["p"], ref["r"], ref["m0"],
+                                      ref["c0"], ref["gy"], ref["gmf"], ref["gcf"])
+    eg[7] = _sym(eg[7])
+    close(y, ey, "y")
+    close(mT, em, "mean_T")
+    close(cT, ec, "cov_T")
+    for i, name in enumerate(["gk", "gv", "gq", "gd", "gp", "gr", "gm0", "gc0"]):
+        close(grads[i], eg[i], name)
+
+
 @pytest.mark.parametrize("t", [20, 16])
 def test_autograd_boundary(cuda_device, t):
     """fused_diagonal_bayesian at D = M = 64 under autograd (checkpoint interval of the library)."""

@@ -134,3 +134,56 @@ def test_bayesian_layer_routes_rotation_to_kernels(cuda_device, monkeypatch):
     close(y, ey, "y")
     for name, a, e in zip(["gk", "gv", "gq", "g_radii", "g_angles"], leaves, cl):
         close(a.grad, e.grad, name)
+
+
+@pytest.mark.parametrize("d", [2, 4, 8])
+def test_rotation_long_sequences(cuda_device, d):
+    """T = 512 (the config-3 length): 64 checkpoint chunks of float32 drift against the float64 oracle."""
+    from bayes_ssm import _hip
+
+    chunk = _hip.load().bssm_rotation_checkpoint(d)
+    n, t = 20, 512
+    print(f"rotation long d={d} n={n} t={t}", flush=True)
+    ins, gy, gmf, gcf = _case(n, t, d, seed=700 + d, angle_scale=1.0)
+    y, mT, cT, _, _, grads = _run(ins, gy, gmf, gcf, chunk, cuda_device)
+    leaves = [x.double().requires_grad_(True) for x in ins]
+    ey, em, ec = O.run_rotation(*leaves, 1e-6)
+    loss = (ey * gy.double()).sum() + (em * gmf.double()).sum() + (ec * gcf.double()).sum()
+    eg = torch.autograd.grad(loss, leaves)
+    close(y, ey, "y")
+    close(mT, em, "mean_T")
+    close(cT, ec, "cov_T")
+    names = ["gk", "gv", "gq", "g_radii", "g_angles", "g_process", "g_observation", "gm0", "gc0"]
+    for name, a, e in zip(names, grads, eg):
+        close(a, e, name)
+
+
+def test_rotation_config3_full_size_rows(cuda_device):
+    """Config 3's shape (16384 sequences x T512, D4M8) on the rotation kernels: rows run alone match the full
+    run's rows bit for bit (sequences are independent), and those rows match the oracle."""
+    from bayes_ssm import _hip
+
+    d, n, t = 4, 256 * 64, 512
+    chunk = _hip.load().bssm_rotation_checkpoint(d)
+    print("rotation config3 full size", flush=True)
+    ins, gy, gmf, gcf = _case(n, t, d, seed=733, angle_scale=1.0)
+    full = _run(ins, gy, gmf, gcf, chunk, cuda_device)
+    rows = torch.tensor([0, 4097, 9999, n - 1])
+    sub_ins = [x[rows].contiguous() for x in ins]
+    sub = _run(sub_ins, gy[rows], gmf[rows], gcf[rows], chunk, cuda_device)
+    rows_d = rows.to(cuda_device)
+    for name, a, b in zip(("y", "mean_T", "cov_T", "bmean", "bcov"), sub[:5], full[:5]):
+        assert torch.equal(a, b[rows_d]), f"{name}: subset rows differ from the full run"
+    for i, (a, b) in enumerate(zip(sub[5], full[5])):
+        assert torch.equal(a, b[rows_d]), f"gradient {i}: subset rows differ from the full run"
+    del full
+    leaves = [x.double().requires_grad_(True) for x in sub_ins]
+    ey, em, ec = O.run_rotation(*leaves, 1e-6)
+    loss = (ey * gy[rows].double()).sum() + (em * gmf[rows].double()).sum() + (ec * gcf[rows].double()).sum()
+    eg = torch.autograd.grad(loss, leaves)
+    close(sub[0], ey, "y")
+    close(sub[1], em, "mean_T")
+    close(sub[2], ec, "cov_T")
+    names = ["gk", "gv", "gq", "g_radii", "g_angles", "g_process", "g_observation", "gm0", "gc0"]
+    for name, a, e in zip(names, sub[5], eg):
+        close(a, e, name)
