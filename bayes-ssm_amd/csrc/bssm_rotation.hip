@@ -79,7 +79,8 @@ struct TokRot {
   float p[J], r;
 };
 
-// Rotation-dynamics tile pointers of one sequence.
+// Rotation-dynamics tile pointers of one sequence (cs, si: cos and sin of
+// the staged angles, filled by fill_trig; cs is the angle tile itself).
 struct RotTile {
   const float* k;
   const float* v;
@@ -87,7 +88,30 @@ struct RotTile {
   const float* ang;
   const float* p;
   const float* r;
+  const float* cs;
+  const float* si;
 };
+
+// cos and sin of every angle of a staged tile (SPW sequence rows of TTT
+// tokens x J pairs in the padded Tile<J, TTT> layout), each computed once per
+// wave: every lane of a sequence's group reads them instead of evaluating
+// sincos_rad for every pair itself.  cos replaces the angle in place (the
+// kernels need only the two values), sin goes to si.
+template <int SPW, int J, int TTT>
+__device__ __forceinline__ void fill_trig(float* ang, float* si, int lane) {
+  constexpr int PER = TTT * J, STRIDE = Tile<J, TTT>::STRIDE, TOTAL = SPW * PER;
+#pragma unroll
+  for (int it = 0; it < (TOTAL + kWave - 1) / kWave; ++it) {
+    const int f = it * kWave + lane;
+    if (f < TOTAL) {
+      const int idx = (f / PER) * STRIDE + f % PER;
+      float sa, ca;
+      sincos_rad(ang[idx], sa, ca);
+      ang[idx] = ca;
+      si[idx] = sa;
+    }
+  }
+}
 
 template <int D, int M, int G>
 __device__ __forceinline__ void read_rot(TokRot<D, M, G>& in, const RotTile& st, int tt, int g, bool need_v) {
@@ -102,8 +126,7 @@ __device__ __forceinline__ void read_rot(TokRot<D, M, G>& in, const RotTile& st,
     const float rc = fmaxf(st.rad[tt * J + m], kTiny);
     in.live[m] = st.rad[tt * J + m] >= kTiny && rc <= 1.f;
     in.rho[m] = rc <= 1.f ? rc : 1.f;
-    float sa, ca;
-    sincos_rad(st.ang[tt * J + m], sa, ca);
+    const float ca = st.cs[tt * J + m], sa = st.si[tt * J + m];
     in.cs[m] = ca;
     in.si[m] = sa;
     in.c[m] = in.rho[m] * ca;
@@ -468,6 +491,7 @@ __global__ __launch_bounds__(kWave) void forward_kernel(RotArgs a) {
   __shared__ float sang[SPW * SJ];
   __shared__ float sp[SPW * SJ];
   __shared__ float sr[SPW * S1];
+  __shared__ float ssi[SPW * SJ];
 
   const int lane = threadIdx.x;
   const int g = lane % G;
@@ -483,7 +507,8 @@ __global__ __launch_bounds__(kWave) void forward_kernel(RotArgs a) {
   const int64_t bm_seq = (a.nb + 1) * D * M, bc_seq = (a.nb + 1) * D * D;
   if (active) store_belief<D, M, G>(b, a.bm + na * bm_seq, a.bc + na * bc_seq, g);
 
-  RotTile st{sk + s * SD, sv + s * SM, srad + s * SJ, sang + s * SJ, sp + s * SJ, sr + s * S1};
+  RotTile st{sk + s * SD, sv + s * SM, srad + s * SJ, sang + s * SJ, sp + s * SJ, sr + s * S1, sang + s * SJ,
+             ssi + s * SJ};
   const float* qs = sq + s * SD;
   float* ys = sv + s * SM;
   // With every stream 16-byte aligned the next tile is loaded into
@@ -524,6 +549,8 @@ __global__ __launch_bounds__(kWave) void forward_kernel(RotArgs a) {
       stage_in<J, TT, SPW>(sp, a.p, n0, a.n, T, t0, len, false, lane);
       stage_in<1, TT, SPW>(sr, a.r, n0, a.n, T, t0, len, false, lane);
     }
+    __syncthreads();
+    fill_trig<SPW, J, TT>(sang, ssi, lane);
     __syncthreads();
     if (a.vec && t0 + TT < T) issue(t0 + TT);
     for (int tt = 0; tt < len; ++tt) {
@@ -608,6 +635,7 @@ __global__ __launch_bounds__(kWave) void backward_kernel(RotArgs a) {
   __shared__ float sang[SPW * SJ];
   __shared__ float sp[SPW * SJ];
   __shared__ float sr[SPW * S1];
+  __shared__ float ssi[SPW * SJ];
   // LDS-DMA staging of the next chunk (see dma_rows).
   constexpr int RK = stage_region(SPW, SUB * D), RV = stage_region(SPW, SUB * M), RJ = stage_region(SPW, SUB * J),
                 R1 = stage_region(SPW, SUB), RBM = stage_region(SPW, D * M), RBC = stage_region(SPW, D * D);
@@ -644,7 +672,8 @@ __global__ __launch_bounds__(kWave) void backward_kernel(RotArgs a) {
 #pragma unroll
     for (int j = 0; j < D; ++j) gc0r[jj][j] = 0.f;
 
-  RotTile st{sk + s * SD, sv + s * SM, srad + s * SJ, sang + s * SJ, sp + s * SJ, sr + s * S1};
+  RotTile st{sk + s * SD, sv + s * SM, srad + s * SJ, sang + s * SJ, sp + s * SJ, sr + s * S1, sang + s * SJ,
+             ssi + s * SJ};
   float* gks = sk + s * SD;
   float* gqs = sq + s * SD;
   float* gvs = sv + s * SM;
@@ -799,6 +828,8 @@ __global__ __launch_bounds__(kWave) void backward_kernel(RotArgs a) {
       copy_rows<SPW, J, SUB>(stg + OANG, sang, lane);
       copy_rows<SPW, J, SUB>(stg + OP, sp, lane);
       copy_rows<SPW, 1, SUB>(stg + OR, sr, lane);
+      __syncthreads();
+      fill_trig<SPW, J, SUB>(sang, ssi, lane);
       Belief<D, M, G> b;
 #pragma unroll
       for (int i = 0; i < D; ++i)
@@ -831,6 +862,8 @@ __global__ __launch_bounds__(kWave) void backward_kernel(RotArgs a) {
       for (int j = 0; j < sc; ++j) {
         stage_piece(tc0 + static_cast<int64_t>(j) * SUB, SUB, false);
         __syncthreads();
+        fill_trig<SPW, J, SUB>(sang, ssi, lane);
+        __syncthreads();
 #pragma unroll 1
         for (int tt = 0; tt < SUB; ++tt) {
           TokRot<D, M, G> in;
@@ -844,6 +877,8 @@ __global__ __launch_bounds__(kWave) void backward_kernel(RotArgs a) {
       const int64_t ts = tc0 + static_cast<int64_t>(sc) * SUB;
       const int len = static_cast<int>((lc - sc * SUB) < SUB ? (lc - sc * SUB) : SUB);
       stage_piece(ts, len, true);
+      __syncthreads();
+      fill_trig<SPW, J, SUB>(sang, ssi, lane);
       __syncthreads();
       run_piece(b, ts, len);
       __syncthreads();
