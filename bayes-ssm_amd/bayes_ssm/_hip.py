@@ -50,6 +50,8 @@ _SIGNATURES = {
     "bssm_forward_chunked_fp8": [_I, _I, _I, _I] + [_P] * 8 + [_P] * 5 + [_L, _L, _L, _F, _P],
     "bssm_backward_chunked_fp8": [_I, _I, _I, _I] + [_P] * 10 + [_P] * 3 + [_P] * 8 + [_L, _L, _L, _F, _P],
     "bssm_round_float8": [_I, _P, _P, _L],
+    "bssm_value_stats_workspace": [_I, _P],
+    "bssm_value_stats": [_I, _P, _P, _P, _P, _L, _P, _P],
     "bssm_associative_static_scan": [_P] * 9 + [_L, _L, _I, _I, _P],
     "bssm_associative_static_scan_backward": [_P] * 16 + [_L, _L, _I, _I, _P],
     "bssm_mixer_forward": [_P, _L] * 5 + [_P] * 7 + [_L, _L, _L, _L, _F, _P],
@@ -69,7 +71,7 @@ _SIGNATURES = {
     "bssm_preferred_checkpoint": [_I],
     "bssm_abi_version": [],
 }
-ABI_VERSION = 7
+ABI_VERSION = 8
 
 _lock = threading.Lock()
 _lib: Optional[ctypes.CDLL] = None
@@ -100,6 +102,7 @@ def load() -> ctypes.CDLL:
                 fn = getattr(lib, name)
                 fn.argtypes = argtypes
                 fn.restype = ctypes.c_int
+            lib.bssm_value_stats_workspace.restype = ctypes.c_int64
             lib.bssm_last_error.argtypes = []
             lib.bssm_last_error.restype = ctypes.c_char_p
             version = lib.bssm_abi_version()

@@ -98,17 +98,46 @@ def _check_finite(x: Tensor, name: str) -> None:
         raise ValueError(f"{name} must contain only finite values")
 
 
+def _stats_kernel_takes(x: Tensor) -> bool:
+    return x.is_cuda and x.dtype in (torch.float32, torch.float64) and x.is_contiguous()
+
+
+def _device_value_stats(xs: list[Tensor]) -> Tensor:
+    """(min, max, any non-finite) of up to 16 contiguous float32/float64 tensors of one GPU, one kernel pass
+    (C ABI ``bssm_value_stats``); returns a [len(xs), 3] float32 tensor on that GPU."""
+    import ctypes
+
+    from . import _hip
+
+    lib = _hip.load()
+    n = len(xs)
+    ptrs = (ctypes.c_void_p * n)(*[x.data_ptr() for x in xs])
+    numels = (ctypes.c_int64 * n)(*[x.numel() for x in xs])
+    dbl = (ctypes.c_int * n)(*[int(x.dtype == torch.float64) for x in xs])
+    as_ptr = lambda arr: ctypes.cast(arr, ctypes.c_void_p)  # noqa: E731
+    ws_n = int(lib.bssm_value_stats_workspace(n, as_ptr(numels)))
+    dev = xs[0].device
+    ws = torch.empty(max(ws_n, 1), device=dev, dtype=torch.float32)
+    out = torch.empty(n, 3, device=dev, dtype=torch.float32)
+    with torch.cuda.device(dev):
+        _hip.call("bssm_value_stats", n, as_ptr(ptrs), as_ptr(numels), as_ptr(dbl), ws.data_ptr(), ws_n,
+                  out.data_ptr(), _hip.stream_of(dev))
+    return out
+
+
 class _DeferredChecks:
-    """bayesian_layer's value checks (finite entries; variance signs) as device reductions read back with one
-    device->host copy.
+    """bayesian_layer's value checks (finite entries; variance signs) read back with one device->host copy.
 
     The reference checks each tensor in turn, each check with its own
-    synchronization (bayesian_layer.py:105-129).  Here every check is one
-    ``aminmax`` reduction (NaN propagates to both ends, infinities show at
-    one), and ``flush`` reads them all at once and raises the first failing
-    check in registration order, with the reference's messages.  Callers
-    flush before a check that synchronizes on its own and when a shape or type
-    error interrupts the sequence, so errors come in the reference's order.
+    reduction and synchronization (bayesian_layer.py:105-129).  Here the
+    tensors are collected and ``flush`` reduces them together: contiguous
+    float32/float64 GPU tensors in one pass of the ``bssm_value_stats``
+    kernel (up to 16 per launch), any other tensor with ``aminmax`` (NaN
+    propagates to both ends, infinities show at one).  It then raises the
+    first failing check in registration order, with the reference's
+    messages.  Callers flush before a check that synchronizes on its own and
+    when a shape or type error interrupts the sequence, so errors come in the
+    reference's order.
     """
 
     def __init__(self) -> None:
@@ -117,8 +146,7 @@ class _DeferredChecks:
     def _add(self, x: Tensor, name: str, kind: Optional[bool]) -> None:
         if x.numel() == 0 or _skip_host_checks(x):
             return
-        lo, hi = torch.aminmax(x.detach())
-        self._pending.append((name, kind, torch.stack((lo, hi)).double()))
+        self._pending.append((name, kind, x.detach()))
 
     def finite(self, x: Tensor, name: str) -> None:
         self._add(x, name, None)
@@ -130,15 +158,26 @@ class _DeferredChecks:
         pending, self._pending = self._pending, []
         if not pending:
             return
-        by_device: dict[torch.device, list[int]] = {}
-        for i, (_, _, stats) in enumerate(pending):
-            by_device.setdefault(stats.device, []).append(i)
+        rows: dict[torch.device, list[tuple[int, Tensor]]] = {}
+        fused: dict[torch.device, list[int]] = {}
+        for i, (_, _, x) in enumerate(pending):
+            if _stats_kernel_takes(x):
+                fused.setdefault(x.device, []).append(i)
+            else:
+                lo, hi = torch.aminmax(x)
+                bad = ~(torch.isfinite(lo) & torch.isfinite(hi))
+                rows.setdefault(x.device, []).append((i, torch.stack((lo.double(), hi.double(), bad.double()))))
+        for dev, idx in fused.items():
+            for c in range(0, len(idx), 16):
+                part = idx[c:c + 16]
+                out = _device_value_stats([pending[i][2] for i in part]).double()
+                rows.setdefault(dev, []).extend((i, out[j]) for j, i in enumerate(part))
         values: list = [None] * len(pending)
-        for idx in by_device.values():
-            for i, pair in zip(idx, torch.stack([pending[i][2] for i in idx]).tolist()):
-                values[i] = pair
-        for (name, kind, _), (lo, hi) in zip(pending, values):
-            if not (math.isfinite(lo) and math.isfinite(hi)):
+        for entries in rows.values():
+            for (i, _), triple in zip(entries, torch.stack([t for _, t in entries]).tolist()):
+                values[i] = triple
+        for (name, kind, _), (lo, hi, bad) in zip(pending, values):
+            if bad or not (math.isfinite(lo) and math.isfinite(hi)):
                 raise ValueError(f"{name} must contain only finite values")
             if kind is True and lo <= 0:
                 raise ValueError(f"{name} must be strictly positive")

@@ -248,7 +248,7 @@ extern "C" {
 
 const char* bssm_last_error(void) { return g_error; }
 
-int bssm_abi_version(void) { return 7; }
+int bssm_abi_version(void) { return 8; }
 
 int bssm_supported(int key_dim, int value_dim) { return supported(key_dim, value_dim) ? 1 : 0; }
 
@@ -515,6 +515,43 @@ int bssm_backward_chunked_fp8(int key_dim, int value_dim, int fixed, int format,
                        BwdOut{static_cast<float*>(gk), static_cast<float*>(gv), static_cast<float*>(gq), gd, gp, gr,
                               gm0, gc0},
                        n, t, chunk, denominator_floor, stream, format == 0 ? bssm::kInE4M3 : bssm::kInE5M2);
+}
+
+int64_t bssm_value_stats_workspace(int count, const int64_t* numels) {
+  if (count < 0 || count > bssm::kMaxStatTensors || (count > 0 && numels == nullptr)) return -1;
+  int64_t blocks = 0;
+  for (int i = 0; i < count; ++i) {
+    if (numels[i] < 0) return -1;
+    blocks += bssm::stat_blocks(numels[i]);
+  }
+  return 3 * blocks;
+}
+
+int bssm_value_stats(int count, const void* const* tensors, const int64_t* numels, const int* is_double,
+                     float* workspace, int64_t workspace_floats, float* out, void* stream) {
+  const char* fn = "bssm_value_stats";
+  if (count < 0 || count > bssm::kMaxStatTensors)
+    return fail(BSSM_ERR_ARGUMENT, "%s: count must be in [0, %d], got %d", fn, bssm::kMaxStatTensors, count);
+  if (count == 0) return ok();
+  if (tensors == nullptr || numels == nullptr || is_double == nullptr || out == nullptr)
+    return fail(BSSM_ERR_ARGUMENT, "%s: tensors, numels, is_double and out are required", fn);
+  bssm::StatArgs a{};
+  a.count = count;
+  int64_t blocks = 0;
+  for (int i = 0; i < count; ++i) {
+    if (numels[i] < 0) return fail(BSSM_ERR_ARGUMENT, "%s: negative numel", fn);
+    if (numels[i] > 0 && tensors[i] == nullptr) return fail(BSSM_ERR_ARGUMENT, "%s: tensor %d is null", fn, i);
+    a.ptr[i] = tensors[i];
+    a.numel[i] = numels[i];
+    a.is_double[i] = is_double[i] != 0;
+    a.first_block[i] = blocks;
+    blocks += bssm::stat_blocks(numels[i]);
+  }
+  a.total_blocks = blocks;
+  if (blocks > 0x7fffffff) return fail(BSSM_ERR_ARGUMENT, "%s: tensors too large", fn);
+  if (workspace_floats < 3 * blocks || (blocks > 0 && workspace == nullptr))
+    return fail(BSSM_ERR_ARGUMENT, "%s: workspace needs %lld floats", fn, (long long)(3 * blocks));
+  return launched(fn, bssm::launch_value_stats(a, workspace, out, static_cast<hipStream_t>(stream)));
 }
 
 int bssm_round_float8(int format, const float* x, uint8_t* out, int64_t count) {

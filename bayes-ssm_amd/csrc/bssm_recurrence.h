@@ -212,6 +212,22 @@ hipError_t launch_conv4_backward_noalloc(const ConvArgs& a, float* grad_weight, 
 hipError_t launch_column_sums_bf16(const void* x, int64_t ld, int64_t b, int64_t t, int64_t cols, float* out,
                                   hipStream_t stream);
 
+// One-pass (min, max, any non-finite) of up to kMaxStatTensors contiguous
+// float32 / float64 tensors (bssm_checks.hip).  first_block[i] is the pass-1
+// block where tensor i starts (prefix sums of stat_blocks(numel)); partials
+// holds 3 * total_blocks floats, out 3 * count.
+constexpr int kMaxStatTensors = 16;
+struct StatArgs {
+  const void* ptr[kMaxStatTensors];
+  int64_t numel[kMaxStatTensors];
+  int64_t first_block[kMaxStatTensors];
+  int is_double[kMaxStatTensors];
+  int count;
+  int64_t total_blocks;
+};
+int64_t stat_blocks(int64_t numel);
+hipError_t launch_value_stats(const StatArgs& a, float* partials, float* out, hipStream_t stream);
+
 hipError_t launch_associative_scan(const float* k, const float* v, const float* q, const float* r,
                                    const float* m0, const float* c0, float* y, float* mT, float* cT,
                                    int64_t b, int64_t t, int d, int m, hipStream_t stream);

@@ -289,6 +289,19 @@ int bssm_backward_chunked_fp8(int key_dim, int value_dim, int fixed, int format,
  * float32 -> float8 conversion; no counterpart in the reference library. */
 int bssm_round_float8(int format, const float* x, uint8_t* out, int64_t count);
 
+/* Value statistics behind bayesian_layer's argument checks (finite entries,
+ * variance signs; bayes_ssm/bayesian_layer.py:105-129, :798-985, where each
+ * tensor is checked with its own reduction and synchronization).  For each of
+ * `count` (at most 16) contiguous device tensors (float32, or float64 where
+ * is_double[i] != 0) writes out[3i .. 3i+2] = (min, max, any non-finite) on
+ * `stream`: min and max over the finite entries (float64 entries mapped to
+ * float32 with their sign kept), the third 1 if any entry is NaN or
+ * infinite.  workspace: bssm_value_stats_workspace(count, numels) floats
+ * (-1: invalid arguments).  No counterpart in the reference library. */
+int64_t bssm_value_stats_workspace(int count, const int64_t* numels);
+int bssm_value_stats(int count, const void* const* tensors, const int64_t* numels, const int* is_double,
+                     float* workspace, int64_t workspace_floats, float* out, void* stream);
+
 /* ------------------------------------------------------------------------
  * Static (A = I, Q = 0) associative scan in information form.
  * Replaces the torch-op chain of `associative_static_bayesian`

@@ -216,3 +216,68 @@ def test_replay_ssm_and_bayesian_layer_modules_on_gpu(cuda_device):
     ey2.backward(gy.double())
     close(y2, ey2, "BayesianLayer y")
     close(bl._process_raw.grad, raw.grad, "BayesianLayer grad process raw")
+
+
+def test_value_stats_kernel_matches_torch(cuda_device):
+    """bssm_value_stats (the batched argument checks): min / max over the finite entries and the non-finite flag,
+    float32 and float64, lengths that are not multiples of 4 or of the block chunk, unaligned views, more than
+    16 tensors (two launches)."""
+    from bayes_ssm.bayesian_layer import _device_value_stats
+
+    g = torch.Generator(device=cuda_device).manual_seed(5)
+    base = torch.randn(3 * 16384 + 7, device=cuda_device, generator=g)
+    xs = [base, base[1:], base[:5], base[3:40001], torch.full((1,), -2.5, device=cuda_device)]
+    bad = base.clone()
+    bad[12345] = float("nan")
+    xs.append(bad)
+    inf = base[:1000].clone()
+    inf[999] = float("-inf")
+    xs.append(inf)
+    d = torch.randn(20001, device=cuda_device, dtype=torch.float64, generator=g)
+    d[7] = 1e300
+    d[8] = -1e-320
+    xs.append(d)
+    pos = torch.full((33,), 1e-320, device=cuda_device, dtype=torch.float64)
+    xs.append(pos)
+    for j in range(10):
+        xs.append(torch.rand(1000 + j, device=cuda_device, generator=g) + j)
+    out = torch.cat([_device_value_stats(xs[c:c + 16]) for c in range(0, len(xs), 16)]).cpu()
+    assert out.shape == (len(xs), 3)
+    for i, x in enumerate(xs):
+        finite = x[torch.isfinite(x)]
+        flag = float(not bool(torch.isfinite(x).all()))
+        assert out[i, 2].item() == flag, f"tensor {i}: non-finite flag"
+        lo, hi = finite.min().item(), finite.max().item()
+        if x.dtype == torch.float32:
+            assert out[i, 0].item() == lo and out[i, 1].item() == hi, f"tensor {i}: min / max"
+        else:
+            # float64: the sign and (within float32) the value are kept.
+            assert (out[i, 0].item() > 0) == (lo > 0) and (out[i, 0].item() < 0) == (lo < 0), f"tensor {i}: min sign"
+            assert (out[i, 1].item() > 0) == (hi > 0), f"tensor {i}: max sign"
+    assert out[-11, 0].item() > 0, "a positive float64 below the float32 range must stay positive"
+
+
+def test_gpu_argument_checks_use_the_stats_kernel(cuda_device):
+    """bayesian_layer on CUDA inputs: the value checks raise the reference's errors, in its order."""
+    n, t, d = 4, 12, 4
+    k, v, q, dec, p, r, _ = O.make_inputs(n, t, d, seed=61)
+    dev = [x.to(cuda_device) for x in (k, v, q, dec, p, r)]
+    kk = dev[0].clone()
+    kk[1, 2, 3] = float("nan")
+    with pytest.raises(ValueError, match="keys must contain only finite"):
+        bayes_ssm.bayesian_layer(kk, dev[1], dev[2], transition_diagonals=dev[3], process_variances=dev[4],
+                                 observation_variances=dev[5])
+    with pytest.raises(ValueError, match="strictly positive"):
+        bayes_ssm.bayesian_layer(*dev[:3], transition_diagonals=dev[3], process_variances=dev[4],
+                                 observation_variances=torch.zeros_like(dev[5]))
+    with pytest.raises(ValueError, match="nonnegative"):
+        bayes_ssm.bayesian_layer(*dev[:3], transition_diagonals=dev[3], process_variances=-dev[4],
+                                 observation_variances=torch.zeros_like(dev[5]))
+    with pytest.raises(ValueError, match="transition_diagonals must contain only finite"):
+        bad = dev[3].clone()
+        bad[0, 0, 0] = float("inf")
+        bayes_ssm.bayesian_layer(*dev[:3], transition_diagonals=bad, process_variances=dev[4],
+                                 observation_variances=torch.zeros_like(dev[5]))
+    y, _, _ = bayes_ssm.bayesian_layer(*dev[:3], transition_diagonals=dev[3], process_variances=dev[4],
+                                       observation_variances=dev[5])
+    assert torch.isfinite(y).all()
