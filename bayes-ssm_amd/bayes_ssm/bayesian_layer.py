@@ -141,7 +141,9 @@ class _DeferredChecks:
     """
 
     def __init__(self) -> None:
-        self._pending: list[tuple[str, Optional[bool], Tensor]] = []
+        # (name or message, kind, tensor): kind None = finite, True / False =
+        # strictly positive / nonnegative variance, a float = lower bound.
+        self._pending: list[tuple[str, object, Tensor]] = []
 
     def _add(self, x: Tensor, name: str, kind: Optional[bool]) -> None:
         if x.numel() == 0 or _skip_host_checks(x):
@@ -154,14 +156,23 @@ class _DeferredChecks:
     def variance(self, x: Tensor, name: str, *, strictly_positive: bool) -> None:
         self._add(x, name, strictly_positive)
 
+    def at_least(self, x: Tensor, bound: float, message: str) -> None:
+        """Finite entries no smaller than ``bound`` (compared in x's dtype, as torch compares a tensor with a
+        Python float); else ``ValueError(message)``."""
+        if x.numel() == 0 or _skip_host_checks(x):
+            return
+        self._pending.append((message, torch.tensor(float(bound), dtype=x.dtype).item(), x.detach()))
+
     def flush(self) -> None:
         pending, self._pending = self._pending, []
         if not pending:
             return
         rows: dict[torch.device, list[tuple[int, Tensor]]] = {}
         fused: dict[torch.device, list[int]] = {}
-        for i, (_, _, x) in enumerate(pending):
-            if _stats_kernel_takes(x):
+        for i, (_, kind, x) in enumerate(pending):
+            # The kernel keeps float64 values only to float32 precision (signs exact): a float64 lower bound
+            # other than zero is tested on torch's exact minimum.
+            if _stats_kernel_takes(x) and not (isinstance(kind, float) and x.dtype == torch.float64):
                 fused.setdefault(x.device, []).append(i)
             else:
                 lo, hi = torch.aminmax(x)
@@ -177,7 +188,12 @@ class _DeferredChecks:
             for (i, _), triple in zip(entries, torch.stack([t for _, t in entries]).tolist()):
                 values[i] = triple
         for (name, kind, _), (lo, hi, bad) in zip(pending, values):
-            if bad or not (math.isfinite(lo) and math.isfinite(hi)):
+            finite = not bad and math.isfinite(lo) and math.isfinite(hi)
+            if isinstance(kind, float):
+                if not finite or lo < kind:
+                    raise ValueError(name)
+                continue
+            if not finite:
                 raise ValueError(f"{name} must contain only finite values")
             if kind is True and lo <= 0:
                 raise ValueError(f"{name} must be strictly positive")

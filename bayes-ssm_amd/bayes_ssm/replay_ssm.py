@@ -16,7 +16,7 @@ from typing import Optional
 import torch
 from torch import Tensor, nn
 
-from .bayesian_layer import _broadcastable, _check_finite, _validate_covariance, bayesian_layer
+from .bayesian_layer import _broadcastable, _DeferredChecks, _validate_covariance, bayesian_layer
 
 
 class ReplaySSM(nn.Module):
@@ -117,24 +117,34 @@ def _scan_prepare(keys, values, queries, observation_variances, initial_mean, in
     if not _broadcastable(cov0.shape[:-2], batch):
         raise ValueError("initial_covariance batch dimensions are not broadcastable to keys")
     cov0 = cov0.expand(*batch, d, d)
-    _validate_covariance(cov0, "initial_covariance", d)
-    mean0 = (torch.zeros(*batch, d, m, device=device, dtype=dtype) if initial_mean is None
-             else initial_mean.to(device=device, dtype=dtype))
-    if mean0.shape[-2:] != (d, m):
-        raise ValueError("initial_mean must end in [key_dim, value_dim]")
-    if not _broadcastable(mean0.shape[:-2], batch):
-        raise ValueError("initial_mean batch dimensions are not broadcastable to keys")
-    mean0 = mean0.expand(*batch, d, m)
-    _check_finite(mean0, "initial_mean")
-    if not isinstance(denominator_floor, Real) or not math.isfinite(float(denominator_floor)) \
-            or denominator_floor <= 0:
-        raise ValueError("denominator_floor must be finite and positive")
-    r2 = torch.broadcast_to(torch.as_tensor(observation_variances, device=device, dtype=dtype), (*batch, t))
-    # The information form divides by r itself, so r must not need the
-    # innovation floor (replay_ssm.py:239-248).
-    if r2.numel() and (not bool(torch.isfinite(r2).all()) or bool((r2 < float(denominator_floor)).any())):
-        raise ValueError("associative_static_bayesian requires finite observation_variances "
-                         "greater than or equal to denominator_floor")
+    # The default identity prior is finite, symmetric and positive definite:
+    # only a caller's covariance needs the checks (and their synchronizations).
+    if initial_covariance is not None:
+        _validate_covariance(cov0, "initial_covariance", d)
+    # The remaining value checks are read back together, in the reference's order.
+    checks = _DeferredChecks()
+    try:
+        mean0 = (torch.zeros(*batch, d, m, device=device, dtype=dtype) if initial_mean is None
+                 else initial_mean.to(device=device, dtype=dtype))
+        if mean0.shape[-2:] != (d, m):
+            raise ValueError("initial_mean must end in [key_dim, value_dim]")
+        if not _broadcastable(mean0.shape[:-2], batch):
+            raise ValueError("initial_mean batch dimensions are not broadcastable to keys")
+        mean0 = mean0.expand(*batch, d, m)
+        if initial_mean is not None:
+            checks.finite(mean0, "initial_mean")
+        if not isinstance(denominator_floor, Real) or not math.isfinite(float(denominator_floor)) \
+                or denominator_floor <= 0:
+            raise ValueError("denominator_floor must be finite and positive")
+        r2 = torch.broadcast_to(torch.as_tensor(observation_variances, device=device, dtype=dtype), (*batch, t))
+        # The information form divides by r itself, so r must not need the
+        # innovation floor (replay_ssm.py:239-248).
+        checks.at_least(r2, float(denominator_floor), "associative_static_bayesian requires finite "
+                        "observation_variances greater than or equal to denominator_floor")
+    except (ValueError, TypeError):
+        checks.flush()
+        raise
+    checks.flush()
     return keys, values, queries, r2, mean0, cov0
 
 

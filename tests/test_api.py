@@ -340,3 +340,23 @@ def test_public_names():
         "associative_static_bayesian_cuda"])
     with pytest.raises(ValueError, match="CUDA"):
         bayes_ssm.associative_static_bayesian_cuda(*_valid())
+
+
+def test_scan_checks_compare_the_floor_in_the_tensor_dtype():
+    """associative_static_bayesian: r equal to the floor passes in float32 and float64 (the reference's
+    ``r2 < floor`` compares in the tensor's dtype); below it, or non-finite, fails; a NaN initial mean fails
+    before a bad floor."""
+    from bayes_ssm import associative_static_bayesian
+
+    k, v, q = _valid()
+    for dtype in (torch.float32, torch.float64):
+        kk, vv, qq = (x.to(dtype) for x in (k, v, q))
+        associative_static_bayesian(kk, vv, qq, observation_variances=torch.full((2, 5), 1e-6, dtype=dtype),
+                                    denominator_floor=1e-6)
+        with pytest.raises(ValueError, match="greater than or equal"):
+            associative_static_bayesian(kk, vv, qq, observation_variances=torch.full((2, 5), 9e-7, dtype=dtype),
+                                        denominator_floor=1e-6)
+        with pytest.raises(ValueError, match="greater than or equal"):
+            associative_static_bayesian(kk, vv, qq, observation_variances=float("nan"))
+    with pytest.raises(ValueError, match="initial_mean must contain only finite"):
+        associative_static_bayesian(k, v, q, initial_mean=torch.full((2, 3), float("nan")), denominator_floor=0.0)
