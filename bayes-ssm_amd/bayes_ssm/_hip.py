@@ -9,6 +9,7 @@ receives raw device pointers and the ``hipStream_t`` of
 """
 from __future__ import annotations
 
+import contextlib
 import ctypes
 import os
 import threading
@@ -128,7 +129,16 @@ def ptr(x: Optional[Tensor]) -> Optional[int]:
 
 
 def stream_of(device: torch.device) -> int:
-    return torch.cuda.current_stream(device).cuda_stream
+    """The ``hipStream_t`` of torch's current stream on ``device``."""
+    index = device.index if device.index is not None else torch.cuda.current_device()
+    return torch._C._cuda_getCurrentRawStream(index)
+
+
+def on_device(device: torch.device):
+    """Context that makes ``device`` current for a launch (a no-op when it already is)."""
+    if device.index is None or device.index == torch._C._cuda_getDevice():
+        return contextlib.nullcontext()
+    return torch.cuda.device(device)
 
 
 def call(name: str, *args) -> None:
@@ -144,5 +154,13 @@ def supported(key_dim: int, value_dim: int) -> bool:
     return bool(load().bssm_supported(int(key_dim), int(value_dim)))
 
 
+_preferred: dict[int, int] = {}
+
+
 def preferred_checkpoint(key_dim: int) -> int:
-    return int(load().bssm_preferred_checkpoint(int(key_dim)))
+    # A property of the built kernels: asked once per key dimension.
+    key_dim = int(key_dim)
+    value = _preferred.get(key_dim)
+    if value is None:
+        value = _preferred.setdefault(key_dim, int(load().bssm_preferred_checkpoint(key_dim)))
+    return value

@@ -119,7 +119,7 @@ def _device_value_stats(xs: list[Tensor]) -> Tensor:
     dev = xs[0].device
     ws = torch.empty(max(ws_n, 1), device=dev, dtype=torch.float32)
     out = torch.empty(n, 3, device=dev, dtype=torch.float32)
-    with torch.cuda.device(dev):
+    with _hip.on_device(dev):
         _hip.call("bssm_value_stats", n, as_ptr(ptrs), as_ptr(numels), as_ptr(dbl), ws.data_ptr(), ws_n,
                   out.data_ptr(), _hip.stream_of(dev))
     return out

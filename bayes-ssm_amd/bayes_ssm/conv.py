@@ -63,7 +63,7 @@ class _CausalConv4Function(torch.autograd.Function):
         bf16 = int(x.dtype == torch.bfloat16)
         w32 = weight.detach().reshape(c, 4).float().contiguous()
         y = torch.empty(b, t, c, device=x.device, dtype=x.dtype)
-        with torch.cuda.device(x.device):
+        with _hip.on_device(x.device):
             _hip.call("bssm_causal_conv4_forward", bf16, x.data_ptr(), ld, w32.data_ptr(), y.data_ptr(), b, t, c,
                       _hip.stream_of(x.device))
         ctx.save_for_backward(x, w32)
@@ -80,7 +80,7 @@ class _CausalConv4Function(torch.autograd.Function):
         gy = grad_y.to(x.dtype).transpose(1, 2).contiguous()  # [B, T, C] rows
         gx = torch.empty(b, t, c, device=x.device, dtype=x.dtype)
         part = torch.empty(b, c, 4, device=x.device, dtype=torch.float32)
-        with torch.cuda.device(x.device):
+        with _hip.on_device(x.device):
             _hip.call("bssm_causal_conv4_backward", bf16, x.data_ptr(), ctx.ld, w32.data_ptr(), gy.data_ptr(),
                       gx.data_ptr(), part.data_ptr(), b, t, c, _hip.stream_of(x.device))
         gw = part.sum(0).reshape(ctx.weight_shape).to(ctx.weight_dtype) if ctx.needs_input_grad[1] else None

@@ -117,11 +117,14 @@ class _Extension:
         return int(keys.size(0)), int(keys.size(1))
 
     def _forward(self, name: str, fixed: bool, keys, values, queries, decay, process, observation, mean0, cov0,
-                 chunks: int, floor: float, saved: bool = False):
-        tensors = (keys, values, queries) + (() if fixed else (decay, process, observation)) + (mean0, cov0)
-        names = ("keys", "values", "queries") + (() if fixed else ("decay", "process", "observation")) + (
-            "mean0", "cov0")
-        _check_inputs(self.key_dim, tensors, names)
+                 chunks: int, floor: float, saved: bool = False, validate: bool = True):
+        # validate=False: the caller (the autograd boundary behind
+        # fused_diagonal_bayesian's contract check) has established the checks.
+        if validate:
+            tensors = (keys, values, queries) + (() if fixed else (decay, process, observation)) + (mean0, cov0)
+            names = ("keys", "values", "queries") + (() if fixed else ("decay", "process", "observation")) + (
+                "mean0", "cov0")
+            _check_inputs(self.key_dim, tensors, names)
         _check(int(chunks) > 0, "fused Bayesian chunk length must be positive")
         n, t = self._sizes(keys)
         d, m = self.key_dim, self.value_dim
@@ -137,7 +140,7 @@ class _Extension:
             hist = (torch.empty((n, t, d, m), **opt), torch.empty((n, t, d, d), **opt),
                     torch.empty((n, t, d), **opt), torch.empty((n, t), **opt), torch.empty((n, t, m), **opt))
         P = _hip.ptr
-        with torch.cuda.device(keys.device):
+        with _hip.on_device(keys.device):
             _hip.call(name, d, m, P(keys), P(values), P(queries),
                       None if fixed else P(decay), None if fixed else P(process), None if fixed else P(observation),
                       P(mean0), P(cov0), P(out), P(mf), P(cf), P(bm), P(bc), *[P(h) for h in hist],
@@ -145,22 +148,23 @@ class _Extension:
         return [out, mf, cf, bm, bc, *hist]
 
     def _backward(self, name: str, fixed: bool, outputs: int, keys, values, queries, decay, process, observation,
-                  mean0, cov0, bm, bc, history, gy, gmf, gcf, chunks: int, floor: float):
-        tensors = (keys, values, queries) + (() if fixed else (decay, process, observation)) + (bm, bc, gy)
-        names = ("keys", "values", "queries") + (() if fixed else ("decay", "process", "observation")) + (
-            "boundary_mean", "boundary_covariance", "grad_output")
-        _check_inputs(self.key_dim, tensors, names)
-        for extra in (gmf, gcf, *history):
-            if extra is not None:
-                _check(extra.is_cuda and extra.dtype == torch.float32 and extra.is_contiguous(),
-                       "fused Bayesian backward inputs must be contiguous CUDA float32 tensors")
-        _check(int(chunks) > 0, "fused Bayesian chunk length must be positive")
+                  mean0, cov0, bm, bc, history, gy, gmf, gcf, chunks: int, floor: float, validate: bool = True):
         n, t = self._sizes(keys)
-        nb = -(-t // int(chunks))
         d, m = self.key_dim, self.value_dim
-        _check(tuple(bm.shape) == (n, nb + 1, d, m) and tuple(bc.shape) == (n, nb + 1, d, d),
-               "boundary tensors do not match the chunk length")
-        _check(tuple(gy.shape) == (n, t, m), "grad_output must be [N,T,M]")
+        if validate:
+            tensors = (keys, values, queries) + (() if fixed else (decay, process, observation)) + (bm, bc, gy)
+            names = ("keys", "values", "queries") + (() if fixed else ("decay", "process", "observation")) + (
+                "boundary_mean", "boundary_covariance", "grad_output")
+            _check_inputs(self.key_dim, tensors, names)
+            for extra in (gmf, gcf, *history):
+                if extra is not None:
+                    _check(extra.is_cuda and extra.dtype == torch.float32 and extra.is_contiguous(),
+                           "fused Bayesian backward inputs must be contiguous CUDA float32 tensors")
+            _check(int(chunks) > 0, "fused Bayesian chunk length must be positive")
+            nb = -(-t // int(chunks))
+            _check(tuple(bm.shape) == (n, nb + 1, d, m) and tuple(bc.shape) == (n, nb + 1, d, d),
+                   "boundary tensors do not match the chunk length")
+            _check(tuple(gy.shape) == (n, t, m), "grad_output must be [N,T,M]")
         opt = dict(device=keys.device, dtype=torch.float32)
         gk = torch.empty((n, t, d), **opt)
         gv = torch.empty((n, t, m), **opt)
@@ -171,7 +175,7 @@ class _Extension:
         if outputs == 8:
             grads += [torch.empty((n, d, m), **opt), torch.empty((n, d, d), **opt)]
         P = _hip.ptr
-        with torch.cuda.device(keys.device):
+        with _hip.on_device(keys.device):
             _hip.call(name, d, m, P(keys), P(values), P(queries),
                       None if fixed else P(decay), None if fixed else P(process), None if fixed else P(observation),
                       P(mean0), P(cov0), P(bm), P(bc), *[P(h) for h in history], P(gy), P(gmf), P(gcf),
@@ -310,10 +314,10 @@ class _ChunkedBayesianFunction(torch.autograd.Function):
                                   u_history, beta_history, e_history)
         else:
             interval = _checkpoint_interval(d, t, chunk_length)
-            forward_impl = extension.forward_chunked_fixed if fixed_dynamics else extension.forward_chunked
-            output, final_mean, final_covariance, boundary_mean, boundary_covariance = forward_impl(
-                keys, values, queries, decay, process, observation, initial_mean, initial_covariance, interval,
-                float(denominator_floor))
+            name = "bssm_forward_chunked_fixed" if fixed_dynamics else "bssm_forward_chunked"
+            output, final_mean, final_covariance, boundary_mean, boundary_covariance = extension._forward(
+                name, bool(fixed_dynamics), keys, values, queries, decay, process, observation, initial_mean,
+                initial_covariance, interval, float(denominator_floor), validate=False)
             ctx.save_for_backward(keys, values, queries, decay, process, observation, initial_mean,
                                   initial_covariance, boundary_mean, boundary_covariance)
         ctx.use_saved_history = use_saved_history
@@ -360,19 +364,20 @@ class _ChunkedBayesianFunction(torch.autograd.Function):
                 backward = extension.backward_chunked_saved
             gradients = backward(*args_head, *history, grad_output, gm, gc, ctx.chunk_length, ctx.denominator_floor)
         else:
-            if ctx.fixed_dynamics:
-                if not lean and not ctx.need_initial_grad and _has(extension, "backward_chunked_noinitial_fixed"):
-                    backward = extension.backward_chunked_noinitial_fixed
-                    ctx.noinitial_backward = True
-                else:
-                    backward = extension.backward_chunked_lean_fixed if lean else extension.backward_chunked_fixed
+            # The reference's method choice (lean / noinitial / full), called
+            # through the C names; the tensors are the forward's own, so the
+            # argument checks of the public methods are not repeated.
+            fixed = ctx.fixed_dynamics
+            suffix = "_fixed" if fixed else ""
+            if not lean and not ctx.need_initial_grad and _has(extension, "backward_chunked_noinitial" + suffix):
+                name, outputs = "bssm_backward_chunked_noinitial" + suffix, 6
+                ctx.noinitial_backward = True
+            elif lean:
+                name, outputs = "bssm_backward_chunked_lean" + suffix, 3
             else:
-                if not lean and not ctx.need_initial_grad and _has(extension, "backward_chunked_noinitial"):
-                    backward = extension.backward_chunked_noinitial
-                    ctx.noinitial_backward = True
-                else:
-                    backward = extension.backward_chunked_lean if lean else extension.backward_chunked
-            gradients = backward(*args_head, grad_output, gm, gc, ctx.chunk_length, ctx.denominator_floor)
+                name, outputs = "bssm_backward_chunked" + suffix, 8
+            gradients = extension._backward(name, fixed, outputs, *args_head, (), grad_output, gm, gc,
+                                            ctx.chunk_length, ctx.denominator_floor, validate=False)
         if lean:
             # 3 tensor gradients + 5 tensor and 3 scalar non-differentiable slots.
             return (*gradients, None, None, None, None, None, None, None, None)
@@ -418,7 +423,7 @@ class _ChunkedBayesianBF16Function(torch.autograd.Function):
         bmean = torch.empty(n, nb + 1, d, m, device=dev, dtype=torch.float32)
         bcov = torch.empty(n, nb + 1, d, d, device=dev, dtype=torch.float32)
         P = _hip.ptr
-        with torch.cuda.device(dev):
+        with _hip.on_device(dev):
             name, fmt = _narrow_call(keys, "forward")
             _hip.call(name, d, m, int(bool(fixed_dynamics)), *fmt, P(keys), P(values), P(queries),
                       P(decay), P(process), P(observation), P(initial_mean), P(initial_covariance), P(out),
@@ -452,7 +457,7 @@ class _ChunkedBayesianBF16Function(torch.autograd.Function):
         gm0 = torch.empty_like(mean0) if need[6] else None
         gc0 = torch.empty_like(cov0) if need[7] else None
         P = _hip.ptr
-        with torch.cuda.device(keys.device):
+        with _hip.on_device(keys.device):
             name, fmt = _narrow_call(keys, "backward")
             _hip.call(name, d, m, int(ctx.fixed_dynamics), *fmt, P(keys), P(values), P(queries),
                       P(decay), P(process), P(observation), P(mean0), P(cov0), P(bmean), P(bcov), P(grad_output),
@@ -517,6 +522,10 @@ def fused_diagonal_bayesian(
     value_dim = values.shape[-1]
     if initial_mean.shape != (n, key_dim, value_dim) or initial_covariance.shape != (n, key_dim, key_dim):
         return None
+    dev = keys.device
+    _check(values.device == dev and queries.device == dev and decay.device == dev and process.device == dev
+           and observation.device == dev and initial_mean.device == dev and initial_covariance.device == dev,
+           "fused Bayesian inputs must share one device")
     keys = keys.contiguous()
     values = values.contiguous()
     queries = queries.contiguous()
@@ -559,7 +568,7 @@ class _ChunkedRotationFunction(torch.autograd.Function):
         bmean = torch.empty(n, nb + 1, d, m, device=dev, dtype=torch.float32)
         bcov = torch.empty(n, nb + 1, d, d, device=dev, dtype=torch.float32)
         P = _hip.ptr
-        with torch.cuda.device(dev):
+        with _hip.on_device(dev):
             _hip.call("bssm_forward_chunked_rotation", d, m, P(keys), P(values), P(queries), P(radii), P(angles),
                       P(process), P(observation), P(initial_mean), P(initial_covariance), P(out), P(mean_t),
                       P(cov_t), P(bmean), P(bcov), n, t, interval, float(denominator_floor), _hip.stream_of(dev))
@@ -584,7 +593,7 @@ class _ChunkedRotationFunction(torch.autograd.Function):
         gm0 = torch.empty_like(mean0) if need[7] else None
         gc0 = torch.empty_like(cov0) if need[8] else None
         P = _hip.ptr
-        with torch.cuda.device(keys.device):
+        with _hip.on_device(keys.device):
             _hip.call("bssm_backward_chunked_rotation", d, m, P(keys), P(values), P(queries), P(radii), P(angles),
                       P(process), P(observation), P(mean0), P(cov0), P(bmean), P(bcov), P(grad_output), P(gm),
                       P(gc), *map(P, grads), P(gm0), P(gc0), n, t, ctx.interval, ctx.denominator_floor,

@@ -91,7 +91,7 @@ class _MixerCoreFunction(torch.autograd.Function):
         bmean = torch.empty(n, nb + 1, KEY_DIM, VALUE_DIM, device=dev, dtype=torch.float32)
         bcov = torch.empty(n, nb + 1, KEY_DIM, KEY_DIM, device=dev, dtype=torch.float32)
         P = _hip.ptr
-        with torch.cuda.device(dev):
+        with _hip.on_device(dev):
             _hip.call("bssm_mixer_forward", P(q_proj), lds[0], P(k_proj), lds[1], P(v_proj), lds[2],
                       P(decay_logits), lds[3], P(noise), lds[4], P(initial_mean), P(initial_covariance), P(read),
                       P(mean_t), P(cov_t), P(bmean), P(bcov), b, t, heads, interval, float(denominator_floor),
@@ -129,7 +129,7 @@ class _MixerCoreFunction(torch.autograd.Function):
         gm0 = torch.empty_like(mean0) if need[5] else None
         gc0 = torch.empty_like(cov0) if need[6] else None
         P = _hip.ptr
-        with torch.cuda.device(dev):
+        with _hip.on_device(dev):
             _hip.call("bssm_mixer_backward", P(q_proj), lds[0], P(k_proj), lds[1], P(v_proj), lds[2],
                       P(decay_logits), lds[3], P(noise), lds[4], P(mean0), P(cov0), P(bmean), P(bcov),
                       P(grad_read), P(gm), P(gc), P(gq), P(gk), P(gv), P(gdl), P(gnz), P(gm0), P(gc0), b, t, heads,
@@ -249,7 +249,7 @@ class _MixerReadoutFunction(torch.autograd.Function):
         bcov = torch.empty(n, nb + 1, KEY_DIM, KEY_DIM, device=dev, dtype=torch.float32)
         w32 = norm_weight.detach().float().contiguous()
         P = _hip.ptr
-        with torch.cuda.device(dev):
+        with _hip.on_device(dev):
             _hip.call("bssm_mixer_gated_forward", P(q_proj), lds[0], P(k_proj), lds[1], P(v_proj), lds[2],
                       P(decay_logits), lds[3], P(noise), lds[4], P(gate), lds[5], P(w32), float(norm_eps),
                       P(initial_mean), P(initial_covariance), P(out), P(read_bf16), P(mean_t), P(cov_t), P(bmean),
@@ -292,7 +292,7 @@ class _MixerReadoutFunction(torch.autograd.Function):
         gm0 = torch.empty_like(mean0) if need[7] else None
         gc0 = torch.empty_like(cov0) if need[8] else None
         P = _hip.ptr
-        with torch.cuda.device(dev):
+        with _hip.on_device(dev):
             _hip.call("bssm_mixer_gated_backward", P(q_proj), lds[0], P(k_proj), lds[1], P(v_proj), lds[2],
                       P(decay_logits), lds[3], P(noise), lds[4], P(gate), lds[5], P(w32), ctx.norm_eps, P(mean0),
                       P(cov0), P(bmean), P(bcov), P(read_bf16), P(grad_out), P(gm), P(gc), P(gq), P(gk), P(gv),
@@ -383,7 +383,7 @@ class _MixerBlockFunction(torch.autograd.Function):
         cw32 = conv_weight.detach().reshape(core, 4).float().contiguous()
         nw32 = norm_weight.detach().float().contiguous()
         P = _hip.ptr
-        with torch.cuda.device(dev):
+        with _hip.on_device(dev):
             _hip.call("bssm_mixer_block_forward", P(projected), ld, P(cw32), P(aux), aux_w, P(nw32), float(norm_eps),
                       P(mean0), P(cov0), P(convolved), P(out), P(read_bf16), P(mean_t), P(cov_t), P(bmean),
                       P(bcov), b, t, heads, interval, float(denominator_floor), _hip.stream_of(dev))
@@ -418,7 +418,7 @@ class _MixerBlockFunction(torch.autograd.Function):
         gm0 = torch.empty_like(mean0) if need[4] else None
         gc0 = torch.empty_like(cov0) if need[5] else None
         P = _hip.ptr
-        with torch.cuda.device(dev):
+        with _hip.on_device(dev):
             _hip.call("bssm_mixer_block_backward", P(projected), ctx.ld, P(cw32), P(aux), aux_w, P(convolved),
                       P(nw32), ctx.norm_eps, P(mean0), P(cov0), P(bmean), P(bcov), P(read_bf16), P(grad_out), P(gm),
                       P(gc), P(gconv), P(gproj), gproj.shape[-1], P(cpart), P(npart), P(apart), P(gm0), P(gc0), b, t,

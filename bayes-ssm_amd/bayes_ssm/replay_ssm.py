@@ -189,7 +189,7 @@ class _StaticScanFunction(torch.autograd.Function):
         mT = torch.empty(b, d, m, device=keys.device, dtype=torch.float32)
         cT = torch.empty(b, d, d, device=keys.device, dtype=torch.float32)
         P = _hip.ptr
-        with torch.cuda.device(keys.device):
+        with _hip.on_device(keys.device):
             _hip.call("bssm_associative_static_scan", P(keys), P(values), P(queries), P(r2), P(mean0), P(cov0),
                       P(out), P(mT), P(cT), b, t, d, m, _hip.stream_of(keys.device))
         ctx.save_for_backward(keys, values, queries, r2, mean0, cov0)
@@ -235,7 +235,7 @@ class _StaticScanFunction(torch.autograd.Function):
                      torch.empty_like(r2), torch.empty_like(mean0), torch.empty_like(cov0))
             ws = torch.empty(b * t * (d * d + d * m), device=dev, dtype=torch.float32)
             P = _hip.ptr
-            with torch.cuda.device(dev):
+            with _hip.on_device(dev):
                 _hip.call("bssm_associative_static_scan_backward", P(keys), P(values), P(queries), P(r2), P(mean0),
                           P(cov0), P(g_out), P(g_mean), P(g_cov), P(ws), *map(P, grads), b, t, d, m,
                           _hip.stream_of(dev))
