@@ -558,92 +558,109 @@ def bayesian_layer(
     except (ValueError, TypeError):
         checks.flush()  # a value error the reference would have raised first
         raise
-    checks.flush()
+    # The value checks are read back once the fused HIP kernels are queued:
+    # those kernels index by shape only, so invalid values cannot make them
+    # fault, and the device->host wait then overlaps the layer's own work.
+    # Every other path (the torch formulations may raise on bad values)
+    # reads them back first, and any error is preceded by them, so the
+    # errors keep the reference's order.
+    try:
+        if not isinstance(denominator_floor, Real) or not math.isfinite(float(denominator_floor)):
+            raise ValueError("denominator_floor must be finite")
+        if denominator_floor <= 0:
+            raise ValueError("denominator_floor must be positive")
+        if chunk_length is not None and (not isinstance(chunk_length, int) or isinstance(chunk_length, bool)
+                                         or chunk_length <= 0):
+            raise ValueError("chunk_length must be a positive integer or None")
+        if t == 0:
+            checks.flush()
+            return torch.empty(*batch_shape, 0, m, device=device, dtype=dtype), mean, cov
+        # A learned initial state keeps the exact dense path (bayesian_layer.py:987-993).
+        if optimized and (mean.requires_grad or cov.requires_grad):
+            optimized = False
+        replayed = bool(torch.is_grad_enabled() and (replay_ssm or _replay_enabled()))
+        if diagonal is not None and (not optimized or replayed):
+            transitions = torch.diag_embed(diagonal)
+            if process_covariances is None:
+                eye = torch.eye(d, device=device, dtype=dtype)
+                process_covariances = process_variances[..., None, None] * eye
+            diagonal = None
+        if rotation and not optimized:
+            rad = rotation_radii.clamp_min(torch.finfo(dtype).tiny)
+            rad = torch.where(rad <= 1.0, rad, torch.ones_like(rad))
+            transitions = make_rotation_dynamics(torch.log(rad), rotation_angles)
+            process_covariances = make_rotation_process_covariances(process_variances)
+            rotation = False
+        if chunk_length is None:
+            chunk_length = t
+        floor = float(denominator_floor)
 
-    if not isinstance(denominator_floor, Real) or not math.isfinite(float(denominator_floor)):
-        raise ValueError("denominator_floor must be finite")
-    if denominator_floor <= 0:
-        raise ValueError("denominator_floor must be positive")
-    if chunk_length is not None and (not isinstance(chunk_length, int) or isinstance(chunk_length, bool)
-                                     or chunk_length <= 0):
-        raise ValueError("chunk_length must be a positive integer or None")
-    if t == 0:
-        return torch.empty(*batch_shape, 0, m, device=device, dtype=dtype), mean, cov
-    # A learned initial state keeps the exact dense path (bayesian_layer.py:987-993).
-    if optimized and (mean.requires_grad or cov.requires_grad):
-        optimized = False
-    replayed = bool(torch.is_grad_enabled() and (replay_ssm or _replay_enabled()))
-    if diagonal is not None and (not optimized or replayed):
-        transitions = torch.diag_embed(diagonal)
-        if process_covariances is None:
-            process_covariances = process_variances[..., None, None] * torch.eye(d, device=device, dtype=dtype)
-        diagonal = None
-    if rotation and not optimized:
-        rad = rotation_radii.clamp_min(torch.finfo(dtype).tiny)
-        rad = torch.where(rad <= 1.0, rad, torch.ones_like(rad))
-        transitions = make_rotation_dynamics(torch.log(rad), rotation_angles)
-        process_covariances = make_rotation_process_covariances(process_variances)
-        rotation = False
-    if chunk_length is None:
-        chunk_length = t
-    floor = float(denominator_floor)
+        if not optimized:
+            checks.flush()
+            return _chunked_transport(keys, values, queries, transitions, process_covariances,
+                                      observation_variances, mean, cov, chunk_length=chunk_length,
+                                      denominator_floor=floor)
+        if rotation:
+            if device.type == "cuda" and len(batch_shape) == 1 and t > 0:
+                from .fused_cuda import fused_rotation_bayesian
 
-    if not optimized:
-        return _chunked_transport(keys, values, queries, transitions, process_covariances, observation_variances,
-                                  mean, cov, chunk_length=chunk_length, denominator_floor=floor)
-    if rotation:
-        if device.type == "cuda" and len(batch_shape) == 1 and t > 0:
-            from .fused_cuda import fused_rotation_bayesian
+                fused = fused_rotation_bayesian(keys, values, queries,
+                                                rotation_radii.expand(*batch_shape, t, d // 2),
+                                                rotation_angles.expand(*batch_shape, t, d // 2), process_variances,
+                                                observation_variances, mean, cov, denominator_floor=floor)
+                if fused is not None:
+                    checks.flush()
+                    return fused
+            checks.flush()
+            outs = []
+            for start in range(0, t, chunk_length):
+                sl = slice(start, min(t, start + chunk_length))
+                y, mean, cov = _loop_rotation(keys[..., sl, :], values[..., sl, :], queries[..., sl, :],
+                                              rotation_radii[..., sl, :], rotation_angles[..., sl, :],
+                                              process_variances[..., sl, :], observation_variances[..., sl], mean,
+                                              cov, floor)
+                outs.append(y)
+            return torch.cat(outs, dim=-2), mean, cov
+        if (device.type == "cuda" and len(batch_shape) == 1 and (d, m) in _FUSED_SHAPES and diagonal is not None
+                and process_covariances is None and not (mean.requires_grad or cov.requires_grad)):
+            from .fused_cuda import fused_diagonal_bayesian
 
-            fused = fused_rotation_bayesian(keys, values, queries, rotation_radii.expand(*batch_shape, t, d // 2),
-                                            rotation_angles.expand(*batch_shape, t, d // 2), process_variances,
-                                            observation_variances, mean, cov, denominator_floor=floor)
+            fk, fv, fq = bf16_kqv if bf16_kqv is not None else (keys, values, queries)
+            fused = fused_diagonal_bayesian(fk, fv, fq, diagonal, process_variances, observation_variances,
+                                            mean, cov, chunk_length=chunk_length, denominator_floor=floor,
+                                            fixed_dynamics=fixed_dynamics)
             if fused is not None:
+                checks.flush()
                 return fused
+        checks.flush()
         outs = []
         for start in range(0, t, chunk_length):
-            stop = min(t, start + chunk_length)
-            y, mean, cov = _loop_rotation(keys[..., start:stop, :], values[..., start:stop, :],
-                                          queries[..., start:stop, :], rotation_radii[..., start:stop, :],
-                                          rotation_angles[..., start:stop, :], process_variances[..., start:stop, :],
-                                          observation_variances[..., start:stop], mean, cov, floor)
+            sl = slice(start, min(t, start + chunk_length))
+            if diagonal is not None and process_covariances is None and not replayed:
+                use_fixed = fixed_dynamics and not diagonal.requires_grad and (
+                    not (process_variances.requires_grad or observation_variances.requires_grad)
+                    or os.environ.get("BAYES_SSM_ALLOW_DYNAMIC_FUSED", "0") == "1")
+                core = _loop_fixed if use_fixed else _loop_diagonal
+                y, mean, cov = core(keys[..., sl, :], values[..., sl, :], queries[..., sl, :],
+                                    diagonal[..., sl, :], process_variances[..., sl], observation_variances[..., sl],
+                                    mean, cov, floor)
+            else:
+                if diagonal is not None:
+                    A = torch.diag_embed(diagonal[..., sl, :])
+                    Q = process_variances[..., sl, None, None] * torch.eye(d, device=device, dtype=dtype)
+                else:
+                    A, Q = transitions[..., sl, :, :], process_covariances[..., sl, :, :]
+                args = (keys[..., sl, :], values[..., sl, :], queries[..., sl, :], A, Q,
+                        observation_variances[..., sl], mean, cov)
+                if replayed:
+                    y, mean, cov = _ReplayChunk.apply(*args, floor)
+                else:
+                    y, mean, cov = _loop_dense(*args, floor)
             outs.append(y)
         return torch.cat(outs, dim=-2), mean, cov
-    if (device.type == "cuda" and len(batch_shape) == 1 and (d, m) in _FUSED_SHAPES and diagonal is not None
-            and process_covariances is None and not (mean.requires_grad or cov.requires_grad)):
-        from .fused_cuda import fused_diagonal_bayesian
-
-        fk, fv, fq = bf16_kqv if bf16_kqv is not None else (keys, values, queries)
-        fused = fused_diagonal_bayesian(fk, fv, fq, diagonal, process_variances, observation_variances,
-                                        mean, cov, chunk_length=chunk_length, denominator_floor=floor,
-                                        fixed_dynamics=fixed_dynamics)
-        if fused is not None:
-            return fused
-    outs = []
-    for start in range(0, t, chunk_length):
-        stop = min(t, start + chunk_length)
-        sl = slice(start, stop)
-        if diagonal is not None and process_covariances is None and not replayed:
-            use_fixed = fixed_dynamics and not diagonal.requires_grad and (
-                not (process_variances.requires_grad or observation_variances.requires_grad)
-                or os.environ.get("BAYES_SSM_ALLOW_DYNAMIC_FUSED", "0") == "1")
-            core = _loop_fixed if use_fixed else _loop_diagonal
-            y, mean, cov = core(keys[..., sl, :], values[..., sl, :], queries[..., sl, :], diagonal[..., sl, :],
-                                process_variances[..., sl], observation_variances[..., sl], mean, cov, floor)
-        else:
-            if diagonal is not None:
-                A = torch.diag_embed(diagonal[..., sl, :])
-                Q = process_variances[..., sl, None, None] * torch.eye(d, device=device, dtype=dtype)
-            else:
-                A, Q = transitions[..., sl, :, :], process_covariances[..., sl, :, :]
-            args = (keys[..., sl, :], values[..., sl, :], queries[..., sl, :], A, Q, observation_variances[..., sl],
-                    mean, cov)
-            if replayed:
-                y, mean, cov = _ReplayChunk.apply(*args, floor)
-            else:
-                y, mean, cov = _loop_dense(*args, floor)
-        outs.append(y)
-    return torch.cat(outs, dim=-2), mean, cov
+    except BaseException:
+        checks.flush()
+        raise
 
 
 class BayesianLayer(nn.Module):

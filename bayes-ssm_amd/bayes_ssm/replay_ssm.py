@@ -88,8 +88,12 @@ __all__ = ["ReplaySSM", "associative_static_bayesian", "associative_static_bayes
 
 
 def _scan_prepare(keys, values, queries, observation_variances, initial_mean, initial_covariance,
-                  denominator_floor):
-    """Validation and promotion shared by both scans (replay_ssm.py:183-250)."""
+                  denominator_floor, checks: Optional[_DeferredChecks] = None):
+    """Validation and promotion shared by both scans (replay_ssm.py:183-250).
+
+    With ``checks`` given, the value checks still pending at the end are left
+    in it for the caller to read back (after queueing its kernel).
+    """
     if keys.ndim < 2 or values.ndim < 2 or queries.ndim < 2:
         raise ValueError("keys, values and queries must have time and feature dimensions")
     if not all(x.is_floating_point() for x in (keys, values, queries)):
@@ -122,7 +126,8 @@ def _scan_prepare(keys, values, queries, observation_variances, initial_mean, in
     if initial_covariance is not None:
         _validate_covariance(cov0, "initial_covariance", d)
     # The remaining value checks are read back together, in the reference's order.
-    checks = _DeferredChecks()
+    defer = checks is not None
+    checks = checks if defer else _DeferredChecks()
     try:
         mean0 = (torch.zeros(*batch, d, m, device=device, dtype=dtype) if initial_mean is None
                  else initial_mean.to(device=device, dtype=dtype))
@@ -144,7 +149,8 @@ def _scan_prepare(keys, values, queries, observation_variances, initial_mean, in
     except (ValueError, TypeError):
         checks.flush()
         raise
-    checks.flush()
+    if not defer:
+        checks.flush()
     return keys, values, queries, r2, mean0, cov0
 
 
@@ -259,16 +265,26 @@ def associative_static_bayesian_cuda(keys: Tensor, values: Tensor, queries: Tens
         raise ValueError("keys, values, and queries must share a CUDA device")
     if keys.device != values.device or keys.device != queries.device:
         raise ValueError("keys, values, and queries must share a CUDA device")
+    # The value checks are read back after the scan kernel is queued (it
+    # indexes by shape only), so the device->host wait overlaps it.
+    checks = _DeferredChecks()
     keys_p, values_p, queries_p, r2, mean0, cov0 = _scan_prepare(
-        keys, values, queries, observation_variances, initial_mean, initial_covariance, denominator_floor)
-    d, m, t = keys_p.shape[-1], values_p.shape[-1], keys_p.shape[-2]
-    if keys_p.dtype != torch.float32 or d > 32 or m > 64:
-        return associative_static_bayesian(keys, values, queries, observation_variances=observation_variances,
-                                           initial_mean=initial_mean, initial_covariance=initial_covariance,
-                                           denominator_floor=denominator_floor)
-    batch = keys_p.shape[:-2]
-    rows = math.prod(batch)
-    flat = lambda x, tail: x.reshape(rows, *tail).contiguous()  # noqa: E731
-    out, mT, cT = _StaticScanFunction.apply(flat(keys_p, (t, d)), flat(values_p, (t, m)), flat(queries_p, (t, d)),
-                                            flat(r2, (t,)), flat(mean0, (d, m)), flat(cov0, (d, d)))
+        keys, values, queries, observation_variances, initial_mean, initial_covariance, denominator_floor, checks)
+    try:
+        d, m, t = keys_p.shape[-1], values_p.shape[-1], keys_p.shape[-2]
+        if keys_p.dtype != torch.float32 or d > 32 or m > 64:
+            checks.flush()
+            return associative_static_bayesian(keys, values, queries, observation_variances=observation_variances,
+                                               initial_mean=initial_mean, initial_covariance=initial_covariance,
+                                               denominator_floor=denominator_floor)
+        batch = keys_p.shape[:-2]
+        rows = math.prod(batch)
+        flat = lambda x, tail: x.reshape(rows, *tail).contiguous()  # noqa: E731
+        out, mT, cT = _StaticScanFunction.apply(flat(keys_p, (t, d)), flat(values_p, (t, m)),
+                                                flat(queries_p, (t, d)), flat(r2, (t,)), flat(mean0, (d, m)),
+                                                flat(cov0, (d, d)))
+        checks.flush()
+    except BaseException:
+        checks.flush()
+        raise
     return out.reshape(*batch, t, m), mT.reshape(*batch, d, m), cT.reshape(*batch, d, d)

@@ -281,3 +281,43 @@ def test_gpu_argument_checks_use_the_stats_kernel(cuda_device):
     y, _, _ = bayes_ssm.bayesian_layer(*dev[:3], transition_diagonals=dev[3], process_variances=dev[4],
                                        observation_variances=dev[5])
     assert torch.isfinite(y).all()
+
+
+def test_gpu_checks_read_back_after_the_fused_launch(cuda_device):
+    """The value checks are read back once the fused kernels are queued: the errors, and their order
+    (a tensor's value error before a bad denominator_floor), stay the reference's, on every fused path."""
+    n, t, d = 4, 12, 4
+    k, v, q, dec, p, r, _ = O.make_inputs(n, t, d, seed=62)
+    dev = [x.to(cuda_device) for x in (k, v, q, dec, p, r)]
+    kk = dev[0].clone()
+    kk[0, 5, 1] = float("inf")
+    with pytest.raises(ValueError, match="keys must contain only finite"):
+        bayes_ssm.bayesian_layer(kk, *dev[1:3], transition_diagonals=dev[3], process_variances=dev[4],
+                                 observation_variances=dev[5], denominator_floor=-1.0)
+    with pytest.raises(ValueError, match="denominator_floor must be positive"):
+        bayes_ssm.bayesian_layer(*dev[:3], transition_diagonals=dev[3], process_variances=dev[4],
+                                 observation_variances=dev[5], denominator_floor=-1.0)
+    # Rotation dynamics (fused rotation kernels).
+    rad = torch.full((n, t, d // 2), 0.9, device=cuda_device)
+    ang = torch.full((n, t, d // 2), 0.3, device=cuda_device)
+    with pytest.raises(ValueError, match="keys must contain only finite"):
+        bayes_ssm.bayesian_layer(kk, *dev[1:3], rotation_radii=rad, rotation_angles=ang,
+                                 process_variances=dev[4].unsqueeze(-1).expand(n, t, d // 2).contiguous(),
+                                 observation_variances=dev[5])
+    # The associative scan's kernel is queued before its checks are read back.
+    rr = torch.full((1, 16), 1e-9, device=cuda_device)
+    kk0, vv0, qq0 = (torch.randn(1, 16, w, device=cuda_device) for w in (4, 4, 4))
+    with pytest.raises(ValueError, match="greater than or equal to denominator_floor"):
+        bayes_ssm.associative_static_bayesian_cuda(kk0, vv0, qq0, observation_variances=rr)
+    with pytest.raises(ValueError, match="initial_mean must contain only finite"):
+        bayes_ssm.associative_static_bayesian_cuda(kk0, vv0, qq0,
+                                                   initial_mean=torch.full((1, 4, 4), float("nan"),
+                                                                           device=cuda_device))
+    # Valid calls after the failures still run and agree with the oracle.
+    y, _, _ = bayes_ssm.bayesian_layer(*dev[:3], transition_diagonals=dev[3], process_variances=dev[4],
+                                       observation_variances=dev[5])
+    ref = O.run_diagonal(*(x.double() for x in (k, v, q, dec, p, r)), torch.zeros(n, d, 8, dtype=torch.float64),
+                         torch.eye(d, dtype=torch.float64).expand(n, d, d), 1e-6)[0]
+    assert torch.allclose(y.double().cpu(), ref, rtol=1e-5, atol=1e-4)
+    y0, _, _ = bayes_ssm.associative_static_bayesian_cuda(kk0, vv0, qq0)
+    assert torch.isfinite(y0).all()
