@@ -65,14 +65,14 @@ _SIGNATURES = {
     "bssm_causal_conv4_backward": [_I, _P, _L, _P, _P, _P, _P, _L, _L, _L, _P],
     "bssm_causal_conv4_backward_noalloc": [_I, _P, _L, _P, _P, _P, _P, _L, _L, _L, _P],
     "bssm_mixer_gated_backward": [_P, _L] * 6 + [_P, _F] + [_P] * 8 + [_P] * 9 + [_L, _L, _L, _L, _F, _I, _P],
-    "bssm_mixer_block_forward": [_P, _L, _P, _P, _L, _P, _F] + [_P] * 9 + [_L, _L, _L, _L, _F, _P],
-    "bssm_mixer_block_backward": [_P, _L, _P, _P, _L, _P, _P, _F] + [_P] * 10 + [_L] + [_P] * 5
-                                 + [_L, _L, _L, _L, _F, _P],
+    "bssm_mixer_block_forward": [_P, _L, _P, _P, _P, _F] + [_P] * 9 + [_L, _L, _L, _L, _F, _P],
+    "bssm_mixer_block_backward": [_P, _L, _P, _P, _P, _P, _F] + [_P] * 10 + [_L] + [_P] * 6 + [_I]
+                                 + [_P] * 2 + [_L, _L, _L, _L, _F, _P],
     "bssm_supported": [_I, _I],
     "bssm_preferred_checkpoint": [_I],
     "bssm_abi_version": [],
 }
-ABI_VERSION = 8
+ABI_VERSION = 9
 
 _lock = threading.Lock()
 _lib: Optional[ctypes.CDLL] = None

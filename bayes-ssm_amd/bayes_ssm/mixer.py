@@ -370,8 +370,9 @@ class _MixerBlockFunction(torch.autograd.Function):
         interval = _hip.preferred_checkpoint(KEY_DIM)
         nb = -(-t // interval)
         dev = projected.device
-        # The aux bias is added in bf16 as the reference does (one rounding).
-        aux = None if aux_bias is None else (projected[..., core:core + aux_w] + aux_bias).contiguous()
+        # The kernels add the aux bias as they read the aux columns, in bf16
+        # as the reference does (one rounding).
+        bias = None if aux_bias is None else aux_bias.detach().contiguous()
         convolved = torch.empty(b, t, core, device=dev, dtype=torch.bfloat16)
         out = torch.empty(b, t, heads * VALUE_DIM, device=dev, dtype=torch.bfloat16)
         read_bf16 = torch.empty_like(out)
@@ -384,10 +385,10 @@ class _MixerBlockFunction(torch.autograd.Function):
         nw32 = norm_weight.detach().float().contiguous()
         P = _hip.ptr
         with _hip.on_device(dev):
-            _hip.call("bssm_mixer_block_forward", P(projected), ld, P(cw32), P(aux), aux_w, P(nw32), float(norm_eps),
+            _hip.call("bssm_mixer_block_forward", P(projected), ld, P(cw32), P(bias), P(nw32), float(norm_eps),
                       P(mean0), P(cov0), P(convolved), P(out), P(read_bf16), P(mean_t), P(cov_t), P(bmean),
                       P(bcov), b, t, heads, interval, float(denominator_floor), _hip.stream_of(dev))
-        ctx.save_for_backward(projected, cw32, aux, convolved, nw32, mean0, cov0, bmean, bcov, read_bf16)
+        ctx.save_for_backward(projected, cw32, bias, convolved, nw32, mean0, cov0, bmean, bcov, read_bf16)
         ctx.heads, ctx.interval, ctx.ld = heads, interval, ld
         ctx.norm_eps, ctx.denominator_floor = float(norm_eps), float(denominator_floor)
         ctx.conv_shape, ctx.conv_dtype = tuple(conv_weight.shape), conv_weight.dtype
@@ -398,7 +399,7 @@ class _MixerBlockFunction(torch.autograd.Function):
 
     @staticmethod
     def backward(ctx, grad_out, grad_mean, grad_covariance):
-        projected, cw32, aux, convolved, nw32, mean0, cov0, bmean, bcov, read_bf16 = ctx.saved_tensors
+        projected, cw32, bias, convolved, nw32, mean0, cov0, bmean, bcov, read_bf16 = ctx.saved_tensors
         b, t, _ = projected.shape
         heads = ctx.heads
         core, aux_w = 16 * heads, 6 * heads
@@ -415,17 +416,28 @@ class _MixerBlockFunction(torch.autograd.Function):
         cpart = torch.empty(b, core, 4, device=dev, dtype=torch.float32)
         npart = torch.empty(b * heads // 16, VALUE_DIM, device=dev, dtype=torch.float32)
         apart = torch.empty(b, aux_w, device=dev, dtype=torch.float32) if need[3] else None
+        # The weight gradients are summed from their partials in the same call,
+        # in the parameters' dtype when all of them are bf16 (else float32).
+        dtypes = [dt for dt, n in zip((ctx.conv_dtype, ctx.norm_dtype, ctx.bias_dtype), need[1:4]) if n]
+        wdt = torch.bfloat16 if dtypes and all(dt == torch.bfloat16 for dt in dtypes) else torch.float32
+        g_conv = torch.empty(ctx.conv_shape, device=dev, dtype=wdt) if need[1] else None
+        g_norm = torch.empty(VALUE_DIM, device=dev, dtype=wdt) if need[2] else None
+        g_bias = torch.empty(aux_w, device=dev, dtype=wdt) if need[3] else None
         gm0 = torch.empty_like(mean0) if need[4] else None
         gc0 = torch.empty_like(cov0) if need[5] else None
         P = _hip.ptr
         with _hip.on_device(dev):
-            _hip.call("bssm_mixer_block_backward", P(projected), ctx.ld, P(cw32), P(aux), aux_w, P(convolved),
+            _hip.call("bssm_mixer_block_backward", P(projected), ctx.ld, P(cw32), P(bias), P(convolved),
                       P(nw32), ctx.norm_eps, P(mean0), P(cov0), P(bmean), P(bcov), P(read_bf16), P(grad_out), P(gm),
-                      P(gc), P(gconv), P(gproj), gproj.shape[-1], P(cpart), P(npart), P(apart), P(gm0), P(gc0), b, t,
-                      heads, ctx.interval, ctx.denominator_floor, _hip.stream_of(dev))
-        g_conv = cpart.sum(0).reshape(ctx.conv_shape).to(ctx.conv_dtype) if need[1] else None
-        g_norm = npart.sum(0).to(ctx.norm_dtype) if need[2] else None
-        g_bias = apart.sum(0).to(ctx.bias_dtype) if need[3] else None
+                      P(gc), P(gconv), P(gproj), gproj.shape[-1], P(cpart), P(npart), P(apart), P(g_conv),
+                      P(g_norm), P(g_bias), int(wdt == torch.bfloat16), P(gm0), P(gc0), b, t, heads, ctx.interval,
+                      ctx.denominator_floor, _hip.stream_of(dev))
+        if g_conv is not None and g_conv.dtype != ctx.conv_dtype:
+            g_conv = g_conv.to(ctx.conv_dtype)
+        if g_norm is not None and g_norm.dtype != ctx.norm_dtype:
+            g_norm = g_norm.to(ctx.norm_dtype)
+        if g_bias is not None and g_bias.dtype != ctx.bias_dtype:
+            g_bias = g_bias.to(ctx.bias_dtype)
         return gproj if need[0] else None, g_conv, g_norm, g_bias, gm0, gc0, None, None, None, None
 
 
@@ -457,13 +469,15 @@ def bayes_mixer_block(
     readout [B, T, H*8] and the final mean and covariance.
 
     On the GPU (bf16 ``projected`` whose rows the kernels can address, heads a
-    multiple of 16, T a positive multiple of 4, a bf16 or absent aux bias) the
-    block is one C call per direction: the filter reads the core columns in
-    place and writes one contiguous [B, T, 2*H*4 + H*8] tensor, whose column
-    views, with the aux and gate columns of ``projected``, feed the
-    producer-fused readout kernels; the backward writes the projection
-    gradient column by column into one [B, T, 30 H] tensor.  Other inputs run
-    the same stages through ``causal_depthwise4`` and ``bayes_mixer_readout``.
+    multiple of 16, T a positive multiple of 4, an absent or bf16 [H*4 + H*2]
+    aux bias) the block is one C call per direction: the filter reads the
+    core columns in place and writes one contiguous [B, T, 2*H*4 + H*8]
+    tensor, whose column views, with the aux and gate columns of
+    ``projected``, feed the producer-fused readout kernels (which add the aux
+    bias as they read the aux columns); the backward writes the projection
+    gradient column by column into one [B, T, 30 H] tensor and sums the
+    weight and bias gradients from their partials.  Other inputs run the same
+    stages through ``causal_depthwise4`` and ``bayes_mixer_readout``.
     """
     if projected.ndim != 3:
         raise ValueError("projected must have shape [B, T, width]")
@@ -481,8 +495,8 @@ def bayes_mixer_block(
     fused = (ld is not None and heads % 16 == 0 and t > 0 and t % 4 == 0
              and conv_weight.device == projected.device and norm_weight.device == projected.device
              and tuple(norm_weight.shape) == (VALUE_DIM,)
-             and (aux_bias is None or (aux_bias.device == projected.device
-                                       and torch.result_type(projected, aux_bias) == torch.bfloat16)))
+             and (aux_bias is None or (aux_bias.device == projected.device and aux_bias.dtype == torch.bfloat16
+                                       and tuple(aux_bias.shape) == (aux,))))
     if fused:
         _hip.load()
         eps = torch.finfo(torch.float32).eps if norm_eps is None else float(norm_eps)

@@ -248,7 +248,7 @@ extern "C" {
 
 const char* bssm_last_error(void) { return g_error; }
 
-int bssm_abi_version(void) { return 8; }
+int bssm_abi_version(void) { return 9; }
 
 int bssm_supported(int key_dim, int value_dim) { return supported(key_dim, value_dim) ? 1 : 0; }
 
@@ -720,37 +720,38 @@ int bssm_mixer_gated_backward(const void* q_proj, int64_t ldq, const void* k_pro
 namespace {
 // The streams of config 4's Bayes block inside the fused projection
 // [B, T, 30 H] (q, k, v core 16 H, decay logits 4 H, noise 2 H, gate 8 H per
-// token) and the filtered core [B, T, 16 H]; aux (null: the projection's own
-// aux columns) holds the decay logits and noise with the aux bias added.
+// token) and the filtered core [B, T, 16 H]; the decay logits and noise are
+// the projection's aux columns (the aux bias, if any, is added as they are
+// read).
 struct BlockStreams {
   const char *q, *k, *v, *dl, *nz, *gate;
-  int64_t ldc, lda;
-  BlockStreams(const void* projected, const void* aux, int64_t ld_aux, const void* convolved, int64_t h) {
+  int64_t ldc;
+  BlockStreams(const void* projected, const void* convolved, int64_t h) {
     const char* p = static_cast<const char*>(projected);
     const char* c = static_cast<const char*>(convolved);
-    const char* x = aux ? static_cast<const char*>(aux) : p + 2 * 16 * h;
     q = c;
     k = c + 2 * 4 * h;
     v = c + 2 * 8 * h;
-    dl = x;
-    nz = x + 2 * 4 * h;
+    dl = p + 2 * 16 * h;
+    nz = p + 2 * 20 * h;
     gate = p + 2 * 22 * h;
     ldc = 16 * h;
-    lda = ld_aux;
   }
 };
 
 int block_check(const char* fn, const void* projected, int64_t ld_projected, const float* conv_weight,
-                const void* aux, int64_t ld_aux, const void* convolved, int64_t b, int64_t t, int64_t h,
-                int64_t chunk, float floor, const BlockStreams& s) {
+                const void* aux_bias, const void* convolved, int64_t b, int64_t t, int64_t h, int64_t chunk,
+                float floor, const BlockStreams& s) {
   if (h <= 0 || b < 0) return fail(BSSM_ERR_ARGUMENT, "%s: needs heads > 0 and batch >= 0", fn);
   if (ld_projected < 30 * h)
     return fail(BSSM_ERR_ARGUMENT, "%s: the projection row stride must be >= 30 * heads = %lld (got %lld)", fn,
                 (long long)(30 * h), (long long)ld_projected);
   if (b * t * h > 0 && (projected == nullptr || conv_weight == nullptr || convolved == nullptr))
     return fail(BSSM_ERR_ARGUMENT, "%s: projected, conv_weight and convolved are required (null given)", fn);
-  const int64_t lda = aux ? ld_aux : ld_projected;
-  if (int rc = mixer_check(fn, {s.q, s.k, s.v, s.dl, s.nz}, {s.ldc, s.ldc, s.ldc, lda, lda}, b, t, h, chunk, floor))
+  if (aux_bias != nullptr && !aligned16(aux_bias))
+    return fail(BSSM_ERR_ARGUMENT, "%s: aux_bias must be 16-byte aligned", fn);
+  const int64_t ldp = ld_projected;
+  if (int rc = mixer_check(fn, {s.q, s.k, s.v, s.dl, s.nz}, {s.ldc, s.ldc, s.ldc, ldp, ldp}, b, t, h, chunk, floor))
     return rc;
   if (int rc = conv_check(fn, 1, projected, ld_projected, conv_weight, {convolved}, b, t, 16 * h)) return rc;
   return BSSM_OK;
@@ -758,13 +759,13 @@ int block_check(const char* fn, const void* projected, int64_t ld_projected, con
 }  // namespace
 
 int bssm_mixer_block_forward(const void* projected, int64_t ld_projected, const float* conv_weight,
-                             const void* aux, int64_t ld_aux, const float* norm_weight, float norm_eps,
-                             const float* mean0, const float* cov0, void* convolved, void* out, void* read_bf16,
-                             float* mean_final, float* cov_final, float* bmean, float* bcov, int64_t batch,
-                             int64_t t, int64_t heads, int64_t chunk, float denominator_floor, void* stream) {
+                             const void* aux_bias, const float* norm_weight, float norm_eps, const float* mean0,
+                             const float* cov0, void* convolved, void* out, void* read_bf16, float* mean_final,
+                             float* cov_final, float* bmean, float* bcov, int64_t batch, int64_t t, int64_t heads,
+                             int64_t chunk, float denominator_floor, void* stream) {
   const char* fn = "bssm_mixer_block_forward";
-  const BlockStreams s(projected, aux, ld_aux, convolved, heads);
-  if (int rc = block_check(fn, projected, ld_projected, conv_weight, aux, ld_aux, convolved, batch, t, heads, chunk,
+  const BlockStreams s(projected, convolved, heads);
+  if (int rc = block_check(fn, projected, ld_projected, conv_weight, aux_bias, convolved, batch, t, heads, chunk,
                            denominator_floor, s))
     return rc;
   if (int rc = epilogue_check(fn, s.gate, ld_projected, norm_weight, norm_eps, {out, read_bf16}, batch, t, heads))
@@ -787,7 +788,7 @@ int bssm_mixer_block_forward(const void* projected, int64_t ld_projected, const 
   if (hipError_t e = bssm::launch_conv4_forward(c, st); e != hipSuccess) return launched(fn, e);
   bssm::MixArgs a{};
   a.q = s.q; a.k = s.k; a.v = s.v; a.dl = s.dl; a.nz = s.nz;
-  a.ldq = a.ldk = a.ldv = s.ldc; a.ldd = a.ldn = aux ? ld_aux : ld_projected;
+  a.ldq = a.ldk = a.ldv = s.ldc; a.ldd = a.ldn = ld_projected; a.abias = aux_bias;
   a.m0 = mean0; a.c0 = cov0; a.mT = mean_final; a.cT = cov_final; a.bm = bmean; a.bc = bcov;
   a.gate = s.gate; a.ldg = ld_projected; a.norm_w = norm_weight; a.norm_eps = norm_eps; a.out = out;
   a.yb = read_bf16;
@@ -796,19 +797,22 @@ int bssm_mixer_block_forward(const void* projected, int64_t ld_projected, const 
 }
 
 int bssm_mixer_block_backward(const void* projected, int64_t ld_projected, const float* conv_weight,
-                              const void* aux, int64_t ld_aux, const void* convolved, const float* norm_weight,
+                              const void* aux_bias, const void* convolved, const float* norm_weight,
                               float norm_eps, const float* mean0, const float* cov0, const float* bmean,
                               const float* bcov, const void* read_bf16, const void* grad_out, const float* gmf,
                               const float* gcf, void* grad_convolved, void* grad_projected,
                               int64_t ld_grad_projected, float* grad_conv_weight_partials,
-                              float* grad_norm_weight_partials, float* grad_aux_partials, float* gm0, float* gc0,
+                              float* grad_norm_weight_partials, float* grad_aux_partials, void* grad_conv_weight,
+                              void* grad_norm_weight, void* grad_aux_bias, int grad_bf16, float* gm0, float* gc0,
                               int64_t batch, int64_t t, int64_t heads, int64_t chunk, float denominator_floor,
                               void* stream) {
   const char* fn = "bssm_mixer_block_backward";
-  const BlockStreams s(projected, aux, ld_aux, convolved, heads);
-  if (int rc = block_check(fn, projected, ld_projected, conv_weight, aux, ld_aux, convolved, batch, t, heads, chunk,
+  const BlockStreams s(projected, convolved, heads);
+  if (int rc = block_check(fn, projected, ld_projected, conv_weight, aux_bias, convolved, batch, t, heads, chunk,
                            denominator_floor, s))
     return rc;
+  if (grad_aux_bias != nullptr && grad_aux_partials == nullptr)
+    return fail(BSSM_ERR_ARGUMENT, "%s: grad_aux_bias needs the grad_aux_partials workspace", fn);
   if (int rc = epilogue_check(fn, s.gate, ld_projected, norm_weight, norm_eps,
                               {read_bf16, grad_out, grad_convolved, grad_norm_weight_partials,
                                grad_conv_weight_partials},
@@ -834,7 +838,7 @@ int bssm_mixer_block_backward(const void* projected, int64_t ld_projected, const
   char* gc = static_cast<char*>(grad_convolved);
   bssm::MixArgs a{};
   a.q = s.q; a.k = s.k; a.v = s.v; a.dl = s.dl; a.nz = s.nz;
-  a.ldq = a.ldk = a.ldv = s.ldc; a.ldd = a.ldn = aux ? ld_aux : ld_projected;
+  a.ldq = a.ldk = a.ldv = s.ldc; a.ldd = a.ldn = ld_projected; a.abias = aux_bias;
   a.m0 = mean0; a.c0 = cov0; a.bmr = bmean; a.bcr = bcov; a.gmf = gmf; a.gcf = gcf;
   a.gq = gc; a.gk = gc + 2 * 4 * heads; a.gv = gc + 2 * 8 * heads;
   a.gdl = gp + 2 * 16 * heads; a.gnz = gp + 2 * 20 * heads;
@@ -851,9 +855,27 @@ int bssm_mixer_block_backward(const void* projected, int64_t ld_projected, const
   c.ldgx = ld_grad_projected; c.gw_part = grad_conv_weight_partials; c.b = batch; c.t = t; c.c = 16 * heads;
   c.bf16 = 1;
   if (hipError_t e = bssm::launch_conv4_backward(c, st); e != hipSuccess) return launched(fn, e);
-  if (grad_aux_partials == nullptr) return ok();
-  return launched(fn, bssm::launch_column_sums_bf16(gp + 2 * 16 * heads, ld_grad_projected, batch, t, 6 * heads,
-                                                    grad_aux_partials, st));
+  if (grad_aux_partials != nullptr) {
+    if (hipError_t e = bssm::launch_column_sums_bf16(gp + 2 * 16 * heads, ld_grad_projected, batch, t, 6 * heads,
+                                                     grad_aux_partials, st);
+        e != hipSuccess)
+      return launched(fn, e);
+  }
+  // The requested weight gradients: column sums of their partials.
+  bssm::FoldArgs f{};
+  const float* parts[3] = {grad_conv_weight_partials, grad_norm_weight_partials, grad_aux_partials};
+  void* outs[3] = {grad_conv_weight, grad_norm_weight, grad_aux_bias};
+  const int64_t rows[3] = {batch, batch * heads / 16, batch}, cols[3] = {16 * heads * 4, 8, 6 * heads};
+  for (int i = 0; i < 3; ++i) {
+    if (outs[i] == nullptr) continue;
+    f.part[f.count] = parts[i];
+    f.out[f.count] = outs[i];
+    f.rows[f.count] = rows[i];
+    f.cols[f.count] = cols[i];
+    ++f.count;
+  }
+  f.bf16 = grad_bf16 != 0;
+  return launched(fn, bssm::launch_fold(f, st));
 }
 
 int bssm_rotation_checkpoint(int key_dim) { return bssm::rotation_checkpoint(key_dim); }

@@ -323,6 +323,41 @@ __global__ __launch_bounds__(256) void column_sums_kernel(const uint32_t* __rest
   }
 }
 
+// Column sums of up to three row-major float32 matrices in one launch (the
+// block's weight-gradient partials), written float32 or bf16 (round to
+// nearest even).  A block takes w = 32 columns (8 for narrower matrices) of
+// one matrix; its 256 / w row groups sum every (256 / w)-th row, four loads in
+// flight, and meet in LDS in a fixed order.
+__global__ __launch_bounds__(256) void fold_kernel(FoldArgs a) {
+  __shared__ float red[256];
+  int m = 0;
+  while (m + 1 < a.count && static_cast<int64_t>(blockIdx.x) >= a.first[m + 1]) ++m;
+  const int64_t cols = a.cols[m], rows = a.rows[m];
+  const int w = cols >= 32 ? 32 : 8, groups = 256 / w;
+  const int cl = threadIdx.x % w, g = threadIdx.x / w;
+  const int64_t c = (static_cast<int64_t>(blockIdx.x) - a.first[m]) * w + cl;
+  const float* p = a.part[m];
+  float s0 = 0.f, s1 = 0.f, s2 = 0.f, s3 = 0.f;
+  if (c < cols) {
+    int64_t r = g;
+    for (; r + 3 * groups < rows; r += 4 * groups) {
+      s0 += p[r * cols + c];
+      s1 += p[(r + groups) * cols + c];
+      s2 += p[(r + 2 * groups) * cols + c];
+      s3 += p[(r + 3 * groups) * cols + c];
+    }
+    for (; r < rows; r += groups) s0 += p[r * cols + c];
+  }
+  red[threadIdx.x] = (s0 + s1) + (s2 + s3);
+  __syncthreads();
+  if (g == 0 && c < cols) {
+    float s = red[cl];
+    for (int k = 1; k < groups; ++k) s += red[k * w + cl];
+    if (a.bf16) static_cast<__bf16*>(a.out[m])[c] = static_cast<__bf16>(s);
+    else static_cast<float*>(a.out[m])[c] = s;
+  }
+}
+
 constexpr int kMaxDevices = 64;
 std::mutex g_scratch_mutex;
 float* g_scratch[kMaxDevices] = {};
@@ -371,6 +406,18 @@ hipError_t launch_column_sums_bf16(const void* x, int64_t ld, int64_t b, int64_t
   const dim3 grid(static_cast<unsigned>((pairs + conv4::kWave - 1) / conv4::kWave), static_cast<unsigned>(b));
   hipLaunchKernelGGL(conv4::column_sums_kernel, grid, dim3(conv4::kWave * conv4::kWaves), 0, stream,
                      static_cast<const uint32_t*>(x), ld / 2, t, pairs, out);
+  return hipGetLastError();
+}
+
+hipError_t launch_fold(FoldArgs a, hipStream_t stream) {
+  int64_t blocks = 0;
+  for (int i = 0; i < a.count; ++i) {
+    a.first[i] = blocks;
+    const int64_t w = a.cols[i] >= 32 ? 32 : 8;
+    blocks += (a.cols[i] + w - 1) / w;
+  }
+  if (blocks == 0) return hipSuccess;
+  hipLaunchKernelGGL(conv4::fold_kernel, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, stream, a);
   return hipGetLastError();
 }
 

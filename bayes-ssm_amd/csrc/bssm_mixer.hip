@@ -176,6 +176,32 @@ struct MixRaw {
   v4f q[2], k[2], dl[2], v[4], nz;
 };
 
+// The aux bias of the wave's 16 heads, staged in LDS at the kernel's start
+// (slot pc < 8: the decay-logit piece of lane pc's columns, slot 8 + j: the
+// noise piece of lane j's columns, 8 bf16 each), added to a tile's raw
+// decay-logit and noise pieces before they are used: bf16(x + b), rounded
+// to nearest even once, as torch adds two bf16 tensors.
+template <bool ON>
+struct MixBias {
+  v4f* lds;
+  __device__ __forceinline__ MixBias(const MixArgs& a, int64_t h0, int lane, v4f* lds_) : lds(lds_) {
+    if (ON && lane < 12) {
+      const int64_t col = lane < 8 ? h0 * 4 + 8 * lane : 4 * a.h + h0 * 2 + 8 * (lane - 8);
+      lds[lane] = *reinterpret_cast<const v4f*>(static_cast<const uint16_t*>(a.abias) + col);
+    }
+  }
+  __device__ __forceinline__ static v4f add8(v4f piece, v4f bias) {
+    return narrow(widen_lo(piece) + widen_lo(bias), widen_hi(piece) + widen_hi(bias));
+  }
+  __device__ __forceinline__ void apply(MixRaw& x, int lane) const {
+    if constexpr (!ON) return;
+    const v4f bd = lds[lane & 7], bn = lds[8 + (lane & 3)];
+    x.dl[0] = add8(x.dl[0], bd);
+    x.dl[1] = add8(x.dl[1], bd);
+    x.nz = add8(x.nz, bn);
+  }
+};
+
 // Buffer descriptors of one batch row (range ends at token T) and row bytes.
 struct MixRows {
   Rsrc q, k, v, dl, nz;
@@ -333,7 +359,7 @@ struct MixEpi {
   }
 };
 
-template <bool EPI>
+template <bool EPI, bool BIAS>
 __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(1, 1))) void mixer_forward_kernel(MixArgs a) {
   __shared__ float tile[2 * FwdTile::SIZE];
   __shared__ float ckst[kRecFloats];
@@ -346,6 +372,8 @@ __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(1, 1))) v
   const uint32_t yrow = static_cast<uint32_t>(a.h) * 32u;
   const MixRows rows(a, bb, h0);
   const MixMap mm(lane, FwdTile::SIZE);
+  __shared__ v4f bias_lds[BIAS ? 12 : 1];
+  const MixBias<BIAS> bias(a, h0, lane, bias_lds);
   const Rsrc ry = make_rsrc(EPI ? a.m0 : a.y + bb * T * a.h * 8, EPI ? 0u : static_cast<uint32_t>(T) * yrow);
   const uint32_t ycol = static_cast<uint32_t>(h0) * 32u + mm.y_col;
   const MixEpi ep(a, bb, h0, lane, false);
@@ -405,6 +433,7 @@ __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(1, 1))) v
     Out yo;
     if (i > 0) take_y(yo);
     __builtin_amdgcn_sched_barrier(0);
+    bias.apply(st, lane);
     mix_put<FwdTile::K, FwdTile::Q, FwdTile::D, FwdTile::V, FwdTile::P, FwdTile::R>(st, mm, tile);
     __builtin_amdgcn_sched_barrier(0);
     if (i > 0) store_y(yo, (i - 1) * LT);
@@ -466,7 +495,7 @@ struct MixGrads {
   }
 };
 
-template <bool DYN, bool EPI>
+template <bool DYN, bool EPI, bool BIAS>
 __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(1, 1))) void mixer_backward_kernel(
     MixArgs a) {
   __shared__ float tile[2 * BwdTile::SIZE];
@@ -480,6 +509,8 @@ __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(1, 1))) v
   const MixRows rows(a, bb, h0);
   const MixGrads gr(a, bb, h0);
   const MixMap mm(lane, BwdTile::SIZE);
+  __shared__ v4f bias_lds[BIAS ? 12 : 1];
+  const MixBias<BIAS> bias(a, h0, lane, bias_lds);
   const Rsrc rgy = make_rsrc(EPI ? a.m0 : a.gy + bb * T * a.h * 8, EPI ? 0u : static_cast<uint32_t>(T) * yrow);
   const uint32_t ycol = static_cast<uint32_t>(h0) * 32u + mm.y_col;
   const MixEpi ep(a, bb, h0, lane, true);
@@ -522,7 +553,10 @@ __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(1, 1))) v
       x.gt[i] = ld64(ep.gate, t * ep.rg + ep.cg, 0);
     }
   };
-  auto put = [&](const Stage& x, int64_t J) __attribute__((always_inline)) {
+  // The aux bias goes into the raw pieces here, so the pieces kept for the
+  // chain rule hold the biased logits too.
+  auto put = [&](Stage& x, int64_t J) __attribute__((always_inline)) {
+    bias.apply(x.raw, lane);
     mix_put<BwdTile::K, BwdTile::Q, BwdTile::D, BwdTile::V, BwdTile::P, BwdTile::R>(x.raw, mm, tile);
     if constexpr (!EPI) {
 #pragma unroll
@@ -597,10 +631,12 @@ __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(1, 1))) v
           const v4f gd = *reinterpret_cast<const v4f*>(&tile[BwdTile::D + (e ? o1 : o0)]);
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
-            // d/dz exp(-softplus(z)) = -exp(-softplus(z)) sigmoid(z), with the
-            // decay formed as in the forward.
-            const float d = exp_(-softplus_(z[i]));
-            out[e][i] = -gd[i] * d * sigmoid_(z[i]);
+            // d/dz exp(-softplus(z)) = -exp(-softplus(z)) sigmoid(z)
+            // = -sigmoid(-z) sigmoid(z) = -sigmoid(|z|)^2 e^-|z| (the same
+            // product whatever the sign of z), from one exponential and one
+            // reciprocal.
+            const float ea = exp_(-fabsf(z[i])), sa = rcp_(1.f + ea);
+            out[e][i] = -gd[i] * (ea * sa) * sa;
           }
         }
         gr.put8(gr.dl, t * gr.rd + gr.ckq + mm.kq_col, out[0], out[1]);
@@ -716,8 +752,11 @@ hipError_t launch_mixer_forward(const MixArgs& a, hipStream_t stream) {
   const int64_t blocks = a.b * a.h / r4::SPW;
   if (blocks == 0) return hipSuccess;
   const dim3 grid(static_cast<unsigned>(blocks)), block(kWave);
-  if (a.gate != nullptr) hipLaunchKernelGGL(r4::mixer_forward_kernel<true>, grid, block, 0, stream, a);
-  else hipLaunchKernelGGL(r4::mixer_forward_kernel<false>, grid, block, 0, stream, a);
+  // The aux bias only comes with the readout epilogue (the block entry points).
+  if (a.gate != nullptr && a.abias != nullptr)
+    hipLaunchKernelGGL((r4::mixer_forward_kernel<true, true>), grid, block, 0, stream, a);
+  else if (a.gate != nullptr) hipLaunchKernelGGL((r4::mixer_forward_kernel<true, false>), grid, block, 0, stream, a);
+  else hipLaunchKernelGGL((r4::mixer_forward_kernel<false, false>), grid, block, 0, stream, a);
   return hipGetLastError();
 }
 
@@ -726,10 +765,12 @@ hipError_t launch_mixer_backward(const MixArgs& a, hipStream_t stream) {
   if (blocks == 0) return hipSuccess;
   const dim3 grid(static_cast<unsigned>(blocks)), block(kWave);
   const bool dyn = a.gdl != nullptr, epi = a.gate != nullptr;
-  if (dyn && epi) hipLaunchKernelGGL((r4::mixer_backward_kernel<true, true>), grid, block, 0, stream, a);
-  else if (dyn) hipLaunchKernelGGL((r4::mixer_backward_kernel<true, false>), grid, block, 0, stream, a);
-  else if (epi) hipLaunchKernelGGL((r4::mixer_backward_kernel<false, true>), grid, block, 0, stream, a);
-  else hipLaunchKernelGGL((r4::mixer_backward_kernel<false, false>), grid, block, 0, stream, a);
+  if (dyn && epi && a.abias != nullptr)
+    hipLaunchKernelGGL((r4::mixer_backward_kernel<true, true, true>), grid, block, 0, stream, a);
+  else if (dyn && epi) hipLaunchKernelGGL((r4::mixer_backward_kernel<true, true, false>), grid, block, 0, stream, a);
+  else if (dyn) hipLaunchKernelGGL((r4::mixer_backward_kernel<true, false, false>), grid, block, 0, stream, a);
+  else if (epi) hipLaunchKernelGGL((r4::mixer_backward_kernel<false, true, false>), grid, block, 0, stream, a);
+  else hipLaunchKernelGGL((r4::mixer_backward_kernel<false, false, false>), grid, block, 0, stream, a);
   return hipGetLastError();
 }
 

@@ -161,6 +161,10 @@ struct MixArgs {
   void* ggate;
   float* gw_part;
   int precise;
+  // Aux bias (bf16 [6 H]: decay logits 4 H, then noise 2 H; null: none),
+  // added to the decay-logit and noise pieces in bf16 (one rounding) as
+  // they are read.
+  const void* abias;
 };
 hipError_t launch_mixer_forward(const MixArgs& a, hipStream_t stream);
 hipError_t launch_mixer_backward(const MixArgs& a, hipStream_t stream);
@@ -211,6 +215,17 @@ hipError_t launch_conv4_backward_noalloc(const ConvArgs& a, float* grad_weight, 
 // cols and ld even, 4-byte aligned): out [B, cols] float32.
 hipError_t launch_column_sums_bf16(const void* x, int64_t ld, int64_t b, int64_t t, int64_t cols, float* out,
                                   hipStream_t stream);
+// Column sums of up to three row-major float32 matrices part[i] [rows[i],
+// cols[i]] into out[i] [cols[i]], float32 or (bf16 != 0) bfloat16, in one
+// launch (bssm_conv4.hip; `first` is filled by the launcher).
+struct FoldArgs {
+  const float* part[3];
+  void* out[3];
+  int64_t rows[3], cols[3], first[3];
+  int count;
+  int bf16;
+};
+hipError_t launch_fold(FoldArgs a, hipStream_t stream);
 
 // One-pass (min, max, any non-finite) of up to kMaxStatTensors contiguous
 // float32 / float64 tensors (bssm_checks.hip).  first_block[i] is the pass-1

@@ -519,13 +519,14 @@ int bssm_mixer_gated_backward(const void* q_proj, int64_t ldq, const void* k_pro
  *   out       = bssm_mixer_gated_forward(q, k, v, aux[..., :4H], aux[..., 4H:],
  *                                        gate = projected[..., 22H:])
  * projected: bf16 [B, T, 30H] rows with stride ld_projected (>= 30H, a
- * multiple of 8, 16-byte aligned).  aux: NULL (no bias: the projection's own
- * columns) or the biased aux bf16 [B, T, 6H] with row stride ld_aux.
+ * multiple of 8, 16-byte aligned).  aux_bias: NULL (no bias) or bf16 [6H],
+ * 16-byte aligned; the kernels add it to the aux columns as they read them,
+ * in bf16 (one rounding to nearest even, as torch adds two bf16 tensors).
  * conv_weight: float32 [16H, 4].  convolved: bf16 [B, T, 16H] (written by the
  * forward, kept for the backward).  Other arguments as in the gated mixer
  * (heads a multiple of 16, T a positive multiple of 4). */
 int bssm_mixer_block_forward(const void* projected, int64_t ld_projected, const float* conv_weight,
-                             const void* aux, int64_t ld_aux, const float* norm_weight, float norm_eps,
+                             const void* aux_bias, const float* norm_weight, float norm_eps,
                              const float* mean0, const float* cov0, void* convolved, void* out,
                              void* read_bf16, float* mean_final, float* cov_final, float* bmean, float* bcov,
                              int64_t batch, int64_t t, int64_t heads, int64_t chunk,
@@ -535,20 +536,23 @@ int bssm_mixer_block_forward(const void* projected, int64_t ld_projected, const 
  * grad_projected (bf16 [B, T, 30H], row stride ld_grad_projected): the
  * filter's input gradient into the core columns, the aux and gate gradients
  * into theirs (the aux gradient is also aux_bias's per token).  Workspace
- * grad_convolved: bf16 [B, T, 16H].  The weight gradients come as partial
- * sums: grad_conv_weight_partials [B, 16H, 4] (sum over the first axis),
- * grad_norm_weight_partials [B*H/16, 8] (column sums) and, when not NULL,
- * grad_aux_partials [B, 6H] (the aux gradient summed over T; its column
- * sums are aux_bias's gradient), float32. */
+ * grad_convolved: bf16 [B, T, 16H], and the float32 partial sums of the
+ * weight gradients: grad_conv_weight_partials [B, 16H, 4] (over the first
+ * axis), grad_norm_weight_partials [B*H/16, 8] and, when not NULL,
+ * grad_aux_partials [B, 6H] (the aux gradient summed over T).  Each of
+ * grad_conv_weight [16H, 4], grad_norm_weight [8] and grad_aux_bias [6H]
+ * that is not NULL receives the column sums of its partials (grad_aux_bias
+ * needs grad_aux_partials), bf16 when grad_bf16 != 0, else float32. */
 int bssm_mixer_block_backward(const void* projected, int64_t ld_projected, const float* conv_weight,
-                              const void* aux, int64_t ld_aux, const void* convolved,
+                              const void* aux_bias, const void* convolved,
                               const float* norm_weight, float norm_eps,
                               const float* mean0, const float* cov0, const float* bmean, const float* bcov,
                               const void* read_bf16, const void* grad_out,
                               const float* gmf, const float* gcf,
                               void* grad_convolved, void* grad_projected, int64_t ld_grad_projected,
                               float* grad_conv_weight_partials, float* grad_norm_weight_partials,
-                              float* grad_aux_partials, float* gm0, float* gc0,
+                              float* grad_aux_partials, void* grad_conv_weight, void* grad_norm_weight,
+                              void* grad_aux_bias, int grad_bf16, float* gm0, float* gc0,
                               int64_t batch, int64_t t, int64_t heads, int64_t chunk,
                               float denominator_floor, void* stream);
 

@@ -153,7 +153,7 @@ def test_mixer_argument_errors_are_reported(lib):
 
 
 def _block_fwd(lib, b=1, t=8, h=16, ld=480, chunk=8):
-    return lib.bssm_mixer_block_forward(None, ld, None, None, 0, None, ctypes.c_float(1e-6), *([None] * 9), b, t, h,
+    return lib.bssm_mixer_block_forward(None, ld, None, None, None, ctypes.c_float(1e-6), *([None] * 9), b, t, h,
                                         chunk, ctypes.c_float(1e-6), None)
 
 
@@ -164,12 +164,20 @@ def test_block_argument_errors_are_reported(lib):
     assert _block_fwd(lib, b=0, t=6) == 2
     assert _block_fwd(lib) == 1 and b"required" in lib.bssm_last_error()
     assert _block_fwd(lib, b=0) == 0
-    rc = lib.bssm_mixer_block_backward(None, 480, None, None, 0, None, None, ctypes.c_float(1e-6), *([None] * 10),
-                                       480, *([None] * 5), 1, 8, 16, 8, ctypes.c_float(1e-6), None)
-    assert rc == 1 and b"required" in lib.bssm_last_error()
-    rc = lib.bssm_mixer_block_backward(None, 480, None, None, 0, None, None, ctypes.c_float(1e-6), *([None] * 10),
-                                       472, *([None] * 5), 0, 8, 16, 8, ctypes.c_float(1e-6), None)
-    assert rc == 1 and b"grad_projected" in lib.bssm_last_error()
+    def block_bwd(ld_grad, b, aux_bias=None, grad_aux=None, apart=None):
+        return lib.bssm_mixer_block_backward(None, 480, None, aux_bias, None, None, ctypes.c_float(1e-6),
+                                             *([None] * 10), ld_grad, None, None, apart, None, None, grad_aux, 1,
+                                             None, None, b, 8, 16, 8, ctypes.c_float(1e-6), None)
+
+    assert block_bwd(480, 1) == 1 and b"required" in lib.bssm_last_error()
+    assert block_bwd(472, 0) == 1 and b"grad_projected" in lib.bssm_last_error()
+    # A misaligned bias, and a bias gradient without its partials workspace.
+    assert block_bwd(480, 0, aux_bias=8) == 1 and b"aux_bias" in lib.bssm_last_error()
+    assert _block_fwd(lib, b=0) == 0
+    rc = lib.bssm_mixer_block_forward(None, 480, None, 8, None, ctypes.c_float(1e-6), *([None] * 9), 0, 8, 16, 8,
+                                      ctypes.c_float(1e-6), None)
+    assert rc == 1 and b"aux_bias" in lib.bssm_last_error()
+    assert block_bwd(480, 0, grad_aux=16) == 1 and b"grad_aux_partials" in lib.bssm_last_error()
 
 
 def test_conv_backward_checks_weight_and_partials_at_t0(lib):

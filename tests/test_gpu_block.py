@@ -124,8 +124,14 @@ def test_block_call_matches_its_stages(cuda_device, monkeypatch, b, t, h, wide, 
     torch.cuda.synchronize()
     s_out, s_mT, s_cT, s_grads, s_bias = _staged(projected, weight, norm_w, aux_bias, gout, h, gm, gc, wide)
     assert torch.equal(out, s_out) and torch.equal(mT, s_mT) and torch.equal(cT, s_cT)
-    for name, a, e in zip(("projected", "conv weight", "norm weight"), [x.grad for x in leaves], s_grads):
-        assert a.dtype == e.dtype and torch.equal(a, e), f"grad {name} differs from the staged run"
+    grads = [x.grad for x in leaves]
+    assert grads[0].dtype == s_grads[0].dtype and torch.equal(grads[0], s_grads[0]), \
+        "grad projected differs from the staged run"
+    # The weight and bias gradients: the same partials, summed over the batch in the block's own fold kernel
+    # (fixed order) rather than by torch's reduction: at most one bf16 rounding apart.
+    for name, a, e in zip(("conv weight", "norm weight"), grads[1:], s_grads[1:]):
+        assert a.dtype == e.dtype, name
+        torch.testing.assert_close(a.float(), e.float(), rtol=2 ** -7, atol=1e-6, msg=lambda m: f"{name}: {m}")
     if with_bias:
         # Summation order over (B, T) differs from autograd's: one bf16 rounding.
         torch.testing.assert_close(bias.grad.float(), s_bias.float(), rtol=2 ** -7, atol=1e-6)
