@@ -138,8 +138,28 @@ class _MixerCoreFunction(torch.autograd.Function):
                 gdl if need[3] else None, gnz if need[4] else None, gm0, gc0, None, None, None)
 
 
+# The default prior (zero mean, identity covariance) per (sequence count,
+# device): read-only inputs of the kernels, built once instead of by three
+# small kernels every step.  A few recent shapes are kept.
+_DEFAULT_PRIORS: dict[tuple[int, torch.device], tuple[Tensor, Tensor]] = {}
+
+
+def _default_prior(n: int, device: torch.device) -> tuple[Tensor, Tensor]:
+    key = (n, device)
+    prior = _DEFAULT_PRIORS.get(key)
+    if prior is None:
+        if len(_DEFAULT_PRIORS) >= 4:
+            _DEFAULT_PRIORS.pop(next(iter(_DEFAULT_PRIORS)))
+        mean0 = torch.zeros(n, KEY_DIM, VALUE_DIM, device=device, dtype=torch.float32)
+        cov0 = torch.eye(KEY_DIM, device=device, dtype=torch.float32).expand(n, KEY_DIM, KEY_DIM).contiguous()
+        prior = _DEFAULT_PRIORS.setdefault(key, (mean0, cov0))
+    return prior
+
+
 def _initial_state(initial_mean: Optional[Tensor], initial_covariance: Optional[Tensor], n: int,
                    device: torch.device) -> tuple[Tensor, Tensor]:
+    if initial_mean is None and initial_covariance is None:
+        return _default_prior(n, device)
     if initial_mean is None:
         mean0 = torch.zeros(n, KEY_DIM, VALUE_DIM, device=device, dtype=torch.float32)
     else:

@@ -68,6 +68,16 @@ __device__ __forceinline__ float log1p01(float u) {
 // is below half an ulp of x, so the two agree.
 __device__ __forceinline__ float softplus_(float x) { return fmaxf(x, 0.f) + log1p01(exp_(-fabsf(x))); }
 
+// The decay exp(-softplus(z)) = 2^-(max(z, 0) log2 e + log2(1 + e^-|z|)),
+// with the hardware log2: its absolute error (about 1e-7 in the exponent,
+// from rounding 1 + e^-|z|) is one ulp of the decay, so the series of
+// log1p01 (which the noise needs for its relative accuracy where softplus is
+// tiny) is not needed here.
+__device__ __forceinline__ float decay_(float z) {
+  const float l = __builtin_amdgcn_logf(1.f + exp_(-fabsf(z)));
+  return __builtin_amdgcn_exp2f(-fmaf(fmaxf(z, 0.f), 1.44269504088896341f, l));
+}
+
 // silu(x) = x sigmoid(x); silu'(x) = sigmoid(x) (1 + x (1 - sigmoid(x))).
 __device__ __forceinline__ float silu_(float x) { return x * sigmoid_(x); }
 
@@ -258,7 +268,7 @@ __device__ __forceinline__ void mix_put(const MixRaw& x, const MixMap& mm, float
 #pragma unroll
       // The reference's exp(-softplus(z)) as written (train_6layer.py:690-698),
       // not the algebraically equal sigmoid(-z), which rounds differently.
-      for (int i = 0; i < 4; ++i) d[i] = exp_(-softplus_(z[i]));
+      for (int i = 0; i < 4; ++i) d[i] = decay_(z[i]);
       *reinterpret_cast<v4f*>(&tile[D + mm.kq_lds[I][e]]) = d;
     }
   }
