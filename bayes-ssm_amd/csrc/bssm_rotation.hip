@@ -173,29 +173,35 @@ __device__ __forceinline__ float r_col(const float (&c)[J], const float (&s)[J],
 }
 
 // X_ij = sum_{a in pair(i), b in pair(j)} A_ia X0_ab A_jb for the lane's own
-// rows, A = R (TRANS false) or R^T (TRANS true), in the symmetric order.
-// own[jj] is row(g, jj) of X0, part[jj] the partner row (row ^ 1).
+// rows, A = R (TRANS false) or R^T (TRANS true).  own[jj] is row(g, jj) of
+// X0, part[jj] the partner row (row ^ 1).  Each term is (A_ia A_jb) X0_ab,
+// summed as ((own, b0) + (part, b1)) + ((own, b1) + (part, b0)): for an even
+// row that is (t00 + t11) + (t01 + t10) in pair positions, for an odd row
+// (t10 + t01) + (t11 + t00), so the owners of rows i and j evaluate X_ij and
+// X_ji to the same bits, and no lane-dependent operand selection is needed.
+// Coefficients: A_{i,own} = c, A_{i,part} = -s (R, even i), s (R, odd i),
+// s (R^T, even i), -s (R^T, odd i); for the columns of pair m,
+//   R:   A_{2m,b} = (c, -s), A_{2m+1,b} = (s, c);
+//   R^T: A_{2m,b} = (c, s),  A_{2m+1,b} = (-s, c);
+// the four coefficient products of a column pair are formed once.
 template <int D, int M, int G, bool TRANS>
 __device__ __forceinline__ void sandwich(const float (&c)[D / 2], const float (&s)[D / 2], const RowsArr<D, M, G>& own,
                                          const RowsArr<D, M, G>& part, int g, RowsArr<D, M, G>& out) {
   using L = Layout<D, M, G>;
   constexpr int J = D / 2;
+  constexpr float sg = TRANS ? 1.f : -1.f;
 #pragma unroll
   for (int jj = 0; jj < L::RPL; ++jj) {
     const int i = L::row(g, jj);
-    const bool odd = i & 1;
-    const float ri0 = TRANS ? r_col<J>(c, s, i, 0) : r_row<J>(c, s, i, 0);
-    const float ri1 = TRANS ? r_col<J>(c, s, i, 1) : r_row<J>(c, s, i, 1);
+    const float ao = pick<J>(c, i >> 1), sk = pick<J>(s, i >> 1);
+    const float ap = ((i & 1) != 0) != TRANS ? sk : -sk;
 #pragma unroll
-    for (int j = 0; j < D; ++j) {
-      const float rj0 = TRANS ? r_col<J>(c, s, j, 0) : r_row<J>(c, s, j, 0);
-      const float rj1 = TRANS ? r_col<J>(c, s, j, 1) : r_row<J>(c, s, j, 1);
-      const int b0 = j & ~1, b1 = j | 1;
-      const float a0b0 = odd ? part[jj][b0] : own[jj][b0], a0b1 = odd ? part[jj][b1] : own[jj][b1];
-      const float a1b0 = odd ? own[jj][b0] : part[jj][b0], a1b1 = odd ? own[jj][b1] : part[jj][b1];
-      const float t00 = (ri0 * rj0) * a0b0, t11 = (ri1 * rj1) * a1b1;
-      const float t01 = (ri0 * rj1) * a0b1, t10 = (ri1 * rj0) * a1b0;
-      out[jj][j] = (t00 + t11) + (t01 + t10);
+    for (int m = 0; m < J; ++m) {
+      const float oc = ao * c[m], os = ao * s[m], pc = ap * c[m], ps = ap * s[m];
+      const float xo0 = own[jj][2 * m], xo1 = own[jj][2 * m + 1];
+      const float xp0 = part[jj][2 * m], xp1 = part[jj][2 * m + 1];
+      out[jj][2 * m] = (oc * xo0 + (sg * ps) * xp1) + ((sg * os) * xo1 + pc * xp0);
+      out[jj][2 * m + 1] = ((-sg * os) * xo0 + pc * xp1) + (oc * xo1 + (-sg * ps) * xp0);
     }
   }
 }
