@@ -536,6 +536,41 @@ __global__ __launch_bounds__(kWave) void forward_kernel(RotArgs a) {
   };
   if (a.vec && T > 0) issue(0);
   int64_t next_ckpt = a.chunk, ckpt = 1;
+  // Eight tokens of a staged tile, unrolled: each token's LDS reads are
+  // issued before the previous token is computed (the scheduling barriers
+  // keep them there), so a token does not wait out the LDS latency.
+  struct FwdIn {
+    TokRot<D, M, G> t;
+    float q[D];
+  };
+  auto read_in = [&](FwdIn& x, int tt) __attribute__((always_inline)) {
+    read_rot<D, M, G>(x.t, st, tt, g, true);
+#pragma unroll
+    for (int i = 0; i < D; ++i) x.q[i] = qs[tt * D + i];
+  };
+  auto step_y = [&](const FwdIn& x, int tt) __attribute__((always_inline)) {
+    StepOut<D, M, G> o;
+    float Pb[L::RPL][D];
+    step_rot<D, M, G>(b, x.t, a.floor, g, lane, o, Pb);
+#pragma unroll
+    for (int c = 0; c < L::CPL; ++c) {
+      float y = 0.f;
+#pragma unroll
+      for (int i = 0; i < D; ++i) y = fmaf(b.Mv[i][c], x.q[i], y);
+      ys[tt * M + g * L::CPL + c] = y;
+    }
+  };
+  auto run8 = [&](int base) __attribute__((always_inline)) {
+    FwdIn x[8];
+    read_in(x[0], base);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      if (i + 1 < 8) read_in(x[i + 1], base + i + 1);
+      __builtin_amdgcn_sched_barrier(0);
+      step_y(x[i], base + i);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  };
   for (int64_t t0 = 0; t0 < T; t0 += TT) {
     const int len = tile_len(T, t0, TT);
     if (a.vec) {
@@ -559,24 +594,29 @@ __global__ __launch_bounds__(kWave) void forward_kernel(RotArgs a) {
     fill_trig<SPW, J, TT>(sang, ssi, lane);
     __syncthreads();
     if (a.vec && t0 + TT < T) issue(t0 + TT);
-    for (int tt = 0; tt < len; ++tt) {
-      if (t0 + tt == next_ckpt) {
-        if (active)
-          store_belief<D, M, G>(b, a.bm + na * bm_seq + ckpt * D * M, a.bc + na * bc_seq + ckpt * D * D, g);
-        ++ckpt;
-        next_ckpt += a.chunk;
+    if (len == TT && TT % 8 == 0 && a.chunk % 8 == 0) {
+      // Whole tile, checkpoints on 8-token boundaries only.
+#pragma unroll
+      for (int h = 0; h < TT / 8; ++h) {
+        if (t0 + 8 * h == next_ckpt) {
+          if (active)
+            store_belief<D, M, G>(b, a.bm + na * bm_seq + ckpt * D * M, a.bc + na * bc_seq + ckpt * D * D, g);
+          ++ckpt;
+          next_ckpt += a.chunk;
+        }
+        run8(8 * h);
       }
-      TokRot<D, M, G> in;
-      read_rot<D, M, G>(in, st, tt, g, true);
-      StepOut<D, M, G> o;
-      float Pb[L::RPL][D];
-      step_rot<D, M, G>(b, in, a.floor, g, lane, o, Pb);
-#pragma unroll
-      for (int c = 0; c < L::CPL; ++c) {
-        float y = 0.f;
-#pragma unroll
-        for (int i = 0; i < D; ++i) y = fmaf(b.Mv[i][c], qs[tt * D + i], y);
-        ys[tt * M + g * L::CPL + c] = y;
+    } else {
+      for (int tt = 0; tt < len; ++tt) {
+        if (t0 + tt == next_ckpt) {
+          if (active)
+            store_belief<D, M, G>(b, a.bm + na * bm_seq + ckpt * D * M, a.bc + na * bc_seq + ckpt * D * D, g);
+          ++ckpt;
+          next_ckpt += a.chunk;
+        }
+        FwdIn x;
+        read_in(x, tt);
+        step_y(x, tt);
       }
     }
     __syncthreads();
