@@ -747,67 +747,104 @@ __global__ __launch_bounds__(kWave) void backward_kernel(RotArgs a) {
   // Replay one piece (tokens [ts, ts + len) staged in the tiles) from belief
   // b with the history in registers, then reverse it; the gradients
   // overwrite the input tiles.
+  auto replay_tok = [&](Belief<D, M, G>& b, const TokRot<D, M, G>& in, RotHist<D, M, G>& h)
+      __attribute__((always_inline)) {
+#pragma unroll
+    for (int jj = 0; jj < RPL; ++jj)
+#pragma unroll
+      for (int j = 0; j < D; ++j) h.Pp[jj][j] = b.P[jj][j];
+#pragma unroll
+    for (int i = 0; i < D; ++i)
+#pragma unroll
+      for (int cc = 0; cc < CPL; ++cc) h.Mp[i][cc] = b.Mv[i][cc];
+    StepOut<D, M, G> o;
+    float Pb[RPL][D];
+    step_rot<D, M, G>(b, in, a.floor, g, lane, o, Pb);
+#pragma unroll
+    for (int j = 0; j < D; ++j) h.u[j] = o.u[j];
+#pragma unroll
+    for (int jj = 0; jj < RPL; ++jj) h.u_own[jj] = o.u_own[jj];
+    h.s = o.s;
+#pragma unroll
+    for (int cc = 0; cc < CPL; ++cc) h.e[cc] = o.e[cc];
+  };
+  struct RevIn {
+    TokRot<D, M, G> t;
+    float q[D], gy[CPL];
+  };
+  auto read_rev = [&](RevIn& x, int tt) __attribute__((always_inline)) {
+    read_rot<D, M, G>(x.t, st, tt, g, false);
+#pragma unroll
+    for (int j = 0; j < D; ++j) x.q[j] = gqs[tt * D + j];
+#pragma unroll
+    for (int cc = 0; cc < CPL; ++cc) x.gy[cc] = gys[tt * M + g * CPL + cc];
+  };
+  auto reverse_tok = [&](const RevIn& x, const RotHist<D, M, G>& h, int tt, int64_t ts)
+      __attribute__((always_inline)) {
+    RotOut<D, M, G> o;
+    reverse_rot<D, M, G>(x.t, h, x.q, x.gy, gM, Gs, a.floor, g, lane, ts + tt == 0, gc0r, o);
+    // Every lane has read its token inputs (the reads above and the
+    // pair values inside) before any gradient overwrites them.
+    __builtin_amdgcn_wave_barrier();
+    if (writer) {
+#pragma unroll
+      for (int jj = 0; jj < RPL; ++jj) {
+        const int rr = L::row(g, jj);
+        gks[tt * D + rr] = o.gk_own[jj];
+        gqs[tt * D + rr] = o.gq_own[jj];
+      }
+    }
+#pragma unroll
+    for (int cc = 0; cc < CPL; ++cc) gvs[tt * M + g * CPL + cc] = o.gv[cc];
+    if (g == 0) {
+#pragma unroll
+      for (int m = 0; m < J; ++m) {
+        grads[tt * J + m] = o.grad_rad[m];
+        gangs[tt * J + m] = o.grad_ang[m];
+        gps[tt * J + m] = o.gp[m];
+      }
+      grs[tt] = o.gr;
+    }
+  };
   auto run_piece = [&](Belief<D, M, G>& b, int64_t ts, int len) __attribute__((always_inline)) {
     RotHist<D, M, G> hist[SUB];
+    if (len == SUB) {
+      // A whole piece: each token's LDS reads are issued a token ahead (the
+      // scheduling barriers keep them there), in both directions.
+      TokRot<D, M, G> x[SUB];
+      read_rot<D, M, G>(x[0], st, 0, g, true);
+#pragma unroll
+      for (int tt = 0; tt < SUB; ++tt) {
+        if (tt + 1 < SUB) read_rot<D, M, G>(x[tt + 1], st, tt + 1, g, true);
+        __builtin_amdgcn_sched_barrier(0);
+        replay_tok(b, x[tt], hist[tt]);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+      RevIn r[SUB];
+      read_rev(r[SUB - 1], SUB - 1);
+#pragma unroll
+      for (int tt = SUB - 1; tt >= 0; --tt) {
+        if (tt > 0) read_rev(r[tt - 1], tt - 1);
+        __builtin_amdgcn_sched_barrier(0);
+        reverse_tok(r[tt], hist[tt], tt, ts);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+      return;
+    }
 #pragma unroll
     for (int tt = 0; tt < SUB; ++tt) {
       if (tt < len) {
         TokRot<D, M, G> in;
         read_rot<D, M, G>(in, st, tt, g, true);
-#pragma unroll
-        for (int jj = 0; jj < RPL; ++jj)
-#pragma unroll
-          for (int j = 0; j < D; ++j) hist[tt].Pp[jj][j] = b.P[jj][j];
-#pragma unroll
-        for (int i = 0; i < D; ++i)
-#pragma unroll
-          for (int cc = 0; cc < CPL; ++cc) hist[tt].Mp[i][cc] = b.Mv[i][cc];
-        StepOut<D, M, G> o;
-        float Pb[RPL][D];
-        step_rot<D, M, G>(b, in, a.floor, g, lane, o, Pb);
-#pragma unroll
-        for (int j = 0; j < D; ++j) hist[tt].u[j] = o.u[j];
-#pragma unroll
-        for (int jj = 0; jj < RPL; ++jj) hist[tt].u_own[jj] = o.u_own[jj];
-        hist[tt].s = o.s;
-#pragma unroll
-        for (int cc = 0; cc < CPL; ++cc) hist[tt].e[cc] = o.e[cc];
+        replay_tok(b, in, hist[tt]);
       }
     }
 #pragma unroll
     for (int tt = SUB - 1; tt >= 0; --tt) {
       if (tt < len) {
-        TokRot<D, M, G> in;
-        read_rot<D, M, G>(in, st, tt, g, false);
-        float q[D], gy[CPL];
-#pragma unroll
-        for (int j = 0; j < D; ++j) q[j] = gqs[tt * D + j];
-#pragma unroll
-        for (int cc = 0; cc < CPL; ++cc) gy[cc] = gys[tt * M + g * CPL + cc];
-        RotOut<D, M, G> o;
-        reverse_rot<D, M, G>(in, hist[tt], q, gy, gM, Gs, a.floor, g, lane, ts + tt == 0, gc0r, o);
-        // Every lane has read its token inputs (the reads above and the
-        // pair values inside) before any gradient overwrites them.
-        __builtin_amdgcn_wave_barrier();
-        if (writer) {
-#pragma unroll
-          for (int jj = 0; jj < RPL; ++jj) {
-            const int rr = L::row(g, jj);
-            gks[tt * D + rr] = o.gk_own[jj];
-            gqs[tt * D + rr] = o.gq_own[jj];
-          }
-        }
-#pragma unroll
-        for (int cc = 0; cc < CPL; ++cc) gvs[tt * M + g * CPL + cc] = o.gv[cc];
-        if (g == 0) {
-#pragma unroll
-          for (int m = 0; m < J; ++m) {
-            grads[tt * J + m] = o.grad_rad[m];
-            gangs[tt * J + m] = o.grad_ang[m];
-            gps[tt * J + m] = o.gp[m];
-          }
-          grs[tt] = o.gr;
-        }
+        RevIn x;
+        read_rev(x, tt);
+        reverse_tok(x, hist[tt], tt, ts);
       }
     }
   };
