@@ -146,14 +146,13 @@ __device__ __forceinline__ void read_rot(TokRot<D, M, G>& in, const RotTile& st,
 // folded back into one indexed load.
 template <int J>
 __device__ __forceinline__ float pick(const float (&x)[J], int k) {
-  float v = x[0];
+  uint32_t v = __builtin_bit_cast(uint32_t, x[0]);
 #pragma unroll
   for (int m = 1; m < J; ++m) {
-    float xm = x[m];
-    __asm__("" : "+v"(xm));
-    v = (k == m) ? xm : v;
+    const uint32_t mask = 0u - static_cast<uint32_t>(k == m);
+    v = (__builtin_bit_cast(uint32_t, x[m]) & mask) | (v & ~mask);
   }
-  return v;
+  return __builtin_bit_cast(float, v);
 }
 
 // R_{i, a} for a = 2 (i >> 1) + t (t = 0, 1), and the transposed R_{a, i}.
@@ -510,6 +509,11 @@ __global__ __launch_bounds__(kWave) void forward_kernel(RotArgs a) {
 
   Belief<D, M, G> b;
   load_belief<D, M, G>(b, a.m0 + na * D * M, a.c0 + na * D * D, g, active);
+  // The initial belief has landed before the token loop: otherwise the
+  // compiler's wait bookkeeping keeps its loads pending at the loop header
+  // and waits for every outstanding load (the next tile's prefetch too) at
+  // the belief's first use in each iteration.
+  r4::vm_wait<0>();
   const int64_t bm_seq = (a.nb + 1) * D * M, bc_seq = (a.nb + 1) * D * D;
   if (active) store_belief<D, M, G>(b, a.bm + na * bm_seq, a.bc + na * bc_seq, g);
 
