@@ -880,6 +880,10 @@ int bssm_mixer_block_backward(const void* projected, int64_t ld_projected, const
 
 int bssm_rotation_checkpoint(int key_dim) { return bssm::rotation_checkpoint(key_dim); }
 
+int64_t bssm_small_batch_limit(int64_t limit) {
+  return limit >= 0 ? bssm::set_small_batch_limit(limit) : bssm::small_batch_limit();
+}
+
 namespace {
 int rotation_common(const char* fn, int d, int m, int64_t n, int64_t t, int64_t chunk, float floor) {
   if (m != 8 || (d != 2 && d != 4 && d != 8))

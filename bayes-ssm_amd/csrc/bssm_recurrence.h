@@ -85,6 +85,12 @@ hipError_t launch_backward_saved(int key_dim, bool dynamics_grads, const BwdArgs
 constexpr int kRot4Chunk = 8;
 hipError_t launch_forward_r4(bool fixed, const FwdArgs& a, hipStream_t stream);
 hipError_t launch_backward_r4(bool fixed, bool dyn, const BwdArgs& a, hipStream_t stream);
+// Row-per-sequence D = 4 kernels for small sequence counts (bssm_small.hip):
+// used for float32 streams when the rotated-layout kernels apply and n is at
+// most small_batch_limit().
+hipError_t launch_forward_small(bool fixed, const FwdArgs& a, hipStream_t stream);
+int64_t small_batch_limit();
+int64_t set_small_batch_limit(int64_t limit);
 
 // D = 1, M = 8 kernels with one lane per value column (bssm_d1.hip).  The
 // forward needs 16-byte aligned streams, T and the checkpoint chunk

@@ -488,6 +488,8 @@ int preferred_checkpoint(int key_dim) {
 }
 
 hipError_t launch_forward(int key_dim, bool fixed, const FwdArgs& a, hipStream_t stream) {
+  if (key_dim == 4 && a.rot4 && a.in_fmt == kInF32 && a.n <= small_batch_limit())
+    return launch_forward_small(fixed, a, stream);
   if (key_dim == 4 && a.rot4) return launch_forward_r4(fixed, a, stream);
   if (key_dim == 1 && d1_forward_ok(a)) return launch_forward_d1(fixed, a, stream);
   if (key_dim == 2 && d2_forward_ok(a)) return launch_forward_d2(fixed, a, stream);

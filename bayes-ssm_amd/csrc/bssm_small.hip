@@ -1,0 +1,333 @@
+// Row-per-sequence kernels for D = 4, M = 8 at small sequence counts, gfx950.
+//
+// The rotated-layout kernels (bssm_rot4.h) give a quad of 4 lanes to each
+// sequence, 16 sequences per wave.  Below about 1024 x 16 sequences their
+// waves do not fill the SIMDs, and each wave's time is its own instruction
+// stream: a wave issues the same instructions whatever number of its lanes
+// hold live sequences.  Here a 16-lane DPP row holds one sequence (4 per
+// wave) and every lane one entry of the covariance, so the per-token stream
+// is about 40 % shorter (four times as many waves, each doing a quarter of
+// the state).
+//
+// Lane (i, j) of a sequence's row (i = row bits 3:2, j = bits 1:0) holds
+//   P[i][j]                    (the covariance, bitwise symmetric)
+//   M[j][2i], M[j][2i + 1]     (the mean, transposed: row j of M)
+// Sums over j are quad all-reduces (xor 1, xor 2); sums over i are
+// "column" all-reduces over the row: the pair (i, i ^ 1) through the half-row
+// mirror and a quad reversal, then the pairs through a row rotation by 8.
+// Both pair their four terms as ((a0 + a1) + (a2 + a3)), so a row sum and the
+// matching column sum of the symmetric covariance give the same bits, and
+// every quantity a lane needs in both orientations (u_i and u_j) is formed
+// from them identically: the covariance update stays bitwise symmetric.
+//
+// The equations are those of bssm_rot4.h (forward_step): u = d * (P (d * k))
+// + p k, s = r + k.u, beta = 1 / max(s, floor), e = v - (d * M)^T k,
+// M <- d * M + beta u e^T, P <- d d^T * P + p I - beta u u^T, y = M^T q.
+
+#include <atomic>
+
+#include "bssm_rot4.h"
+
+// No contraction: a sum like x + dpp(x) with x = a * b would otherwise be
+// fused into fma(a, b, dpp(x)), which rounds the two lanes of a pair
+// differently and breaks the bitwise agreement of row and column sums.
+// Every intended fused multiply-add is an explicit fmaf.
+#pragma clang fp contract(off)
+
+namespace bssm {
+namespace sn {
+namespace {
+
+constexpr int SPW = 4;   // sequences per wave
+constexpr int TT = 16;   // tokens per staged tile
+constexpr int kRowRor8 = 0x128;
+constexpr int kQuadRev = quad_perm(3, 2, 1, 0);
+
+using r4::Rsrc;
+using r4::make_rsrc;
+using r4::kOob;
+typedef float v2f __attribute__((ext_vector_type(2)));
+
+// Sum over the 4 lanes j of the quad; identical bits in the quad.
+__device__ __forceinline__ float quad_sum(float x) {
+  x += dpp<kXor1>(x);
+  return x + dpp<kXor2>(x);
+}
+// Sum over the 4 rows i of the 16-lane row at fixed j; identical bits in the
+// column, and equal to quad_sum of the transposed terms.
+__device__ __forceinline__ float col_sum(float x) {
+  const float m = dpp<kHalfMirror>(x);  // lane (i ^ 1, 3 - j)
+  x += dpp<kQuadRev>(m);                // + lane (i ^ 1, j)
+  return x + dpp<kRowRor8>(x);          // + rows i ^ 2, i ^ 3
+}
+
+// LDS tile of one wave: per sequence (padded stride so the 4 sequences'
+// reads of one token fall in different banks) k, d, q [TT][4], v / y [TT][8],
+// p, r [TT].
+struct Tile {
+  static constexpr int K = 0, D = 64, Q = 128, V = 192, P = 320, R = 336, SEQ = 356, SIZE = SPW * SEQ;
+};
+
+// Register staging of one tile: lane (s, c) (s = lane >> 4, c = lane & 15)
+// loads token c's 16-byte k / d / q piece of sequence s, v pieces c and
+// c + 16 (token piece >> 1, half piece & 1), and for c < 4 the p / r piece c
+// (tokens 4c .. 4c + 3).
+struct Stage {
+  v4f k, d, q, v0, v1, p, r;
+};
+
+struct Streams {
+  Rsrc k, d, q, v, p, r, y;
+  uint32_t row4, row8, row1;  // bytes per sequence row
+};
+
+template <bool FIXED>
+__device__ __forceinline__ void load_tile(Stage& x, const Streams& st, int s, int c, uint32_t t0) {
+  const uint32_t o4 = static_cast<uint32_t>(s) * st.row4 + (t0 + c) * 16u;
+  x.k = r4::ld128<true>(st.k, o4);
+  x.q = r4::ld128<true>(st.q, o4);
+  if constexpr (!FIXED) x.d = r4::ld128<true>(st.d, o4);
+  const uint32_t o8 = static_cast<uint32_t>(s) * st.row8 + t0 * 32u + c * 16u;
+  x.v0 = r4::ld128<true>(st.v, o8);
+  x.v1 = r4::ld128<true>(st.v, o8 + 256u);
+  if constexpr (!FIXED) {
+    const uint32_t o1 = c < 4 ? static_cast<uint32_t>(s) * st.row1 + t0 * 4u + c * 16u : kOob;
+    x.p = r4::ld128<false>(st.p, o1);
+    x.r = r4::ld128<false>(st.r, o1);
+  }
+}
+
+template <bool FIXED>
+__device__ __forceinline__ void put_tile(const Stage& x, float* tl, int s, int c) {
+  float* b = tl + s * Tile::SEQ;
+  *reinterpret_cast<v4f*>(b + Tile::K + 4 * c) = x.k;
+  *reinterpret_cast<v4f*>(b + Tile::Q + 4 * c) = x.q;
+  *reinterpret_cast<v4f*>(b + Tile::V + 4 * c) = x.v0;
+  *reinterpret_cast<v4f*>(b + Tile::V + 64 + 4 * c) = x.v1;
+  if constexpr (!FIXED) {
+    *reinterpret_cast<v4f*>(b + Tile::D + 4 * c) = x.d;
+    if (c < 4) {
+      *reinterpret_cast<v4f*>(b + Tile::P + 4 * c) = x.p;
+      *reinterpret_cast<v4f*>(b + Tile::R + 4 * c) = x.r;
+    }
+  }
+}
+
+// Token inputs of lane (i, j).
+struct Tok {
+  float ki, kj, di, dj, qj, p, r;
+  v2f v;  // v[2i], v[2i + 1]
+};
+
+template <bool FIXED>
+__device__ __forceinline__ void read_tok(Tok& x, const float* b, int tt, int i, int j) {
+  x.ki = b[Tile::K + 4 * tt + i];
+  x.kj = b[Tile::K + 4 * tt + j];
+  x.qj = b[Tile::Q + 4 * tt + j];
+  x.v = *reinterpret_cast<const v2f*>(b + Tile::V + 8 * tt + 2 * i);
+  if constexpr (FIXED) {
+    x.di = x.dj = kFixedDecay;
+    x.p = kFixedProcess;
+    x.r = kFixedObservation;
+  } else {
+    x.di = b[Tile::D + 4 * tt + i];
+    x.dj = b[Tile::D + 4 * tt + j];
+    x.p = b[Tile::P + tt];
+    x.r = b[Tile::R + tt];
+  }
+}
+
+// Belief of lane (i, j) and its step.
+struct Bel {
+  float P, M0, M1;
+};
+
+struct StepOut {
+  float ui, uj, s;
+  v2f e;
+};
+
+__device__ __forceinline__ void forward_step(Bel& b, const Tok& x, float delta, float floor, StepOut& o) {
+  const float wki = x.di * x.ki, wkj = x.dj * x.kj;
+  const float zi = quad_sum(b.P * wkj);  // (P (d * k))_i
+  const float zj = col_sum(b.P * wki);   // (P (d * k))_j, the same bits for i == j
+  const float ui = fmaf(x.di, zi, x.p * x.ki), uj = fmaf(x.dj, zj, x.p * x.kj);
+  const float s = quad_sum(x.kj * uj) + x.r;
+  const float beta = fast_rcp(fmaxf(s, floor));
+  // Innovations of the lane's columns 2i, 2i + 1: e = v - sum_j M[j][c] d_j k_j.
+  const float e0 = x.v[0] - quad_sum(b.M0 * wkj);
+  const float e1 = x.v[1] - quad_sum(b.M1 * wkj);
+  const float bu = beta * uj;
+  b.M0 = fmaf(bu, e0, x.dj * b.M0);
+  b.M1 = fmaf(bu, e1, x.dj * b.M1);
+  const float dp = fmaf(x.p, delta, (x.di * x.dj) * b.P);
+  b.P = fmaf(-beta, ui * uj, dp);
+  o.ui = ui;
+  o.uj = uj;
+  o.s = s;
+  o.e[0] = e0;
+  o.e[1] = e1;
+}
+
+// Readouts of the lane's columns after the token: y_c = sum_j M[j][c] q_j.
+__device__ __forceinline__ v2f readout(const Bel& b, float qj) {
+  v2f y;
+  y[0] = quad_sum(b.M0 * qj);
+  y[1] = quad_sum(b.M1 * qj);
+  return y;
+}
+
+// Belief record offsets of lane (i, j) (bytes within one sequence's record).
+__device__ __forceinline__ uint32_t mean_off(int i, int j) { return static_cast<uint32_t>(j * 32 + i * 8); }
+__device__ __forceinline__ uint32_t cov_off(int i, int j) { return static_cast<uint32_t>(i * 16 + j * 4); }
+
+template <bool FIXED>
+__global__ __launch_bounds__(kWave) void forward_kernel(FwdArgs a) {
+  __shared__ float tile[Tile::SIZE];
+  const int lane = threadIdx.x;
+  const int s = lane >> 4, c = lane & 15, i = c >> 2, j = c & 3;
+  const float delta = i == j ? 1.f : 0.f;
+  const int64_t n0 = static_cast<int64_t>(blockIdx.x) * SPW;
+  const int64_t T = a.t;
+  const uint32_t valid = static_cast<uint32_t>((a.n - n0) < SPW ? (a.n - n0) : SPW);
+  Streams st;
+  st.row4 = static_cast<uint32_t>(T) * 16u;
+  st.row8 = static_cast<uint32_t>(T) * 32u;
+  st.row1 = static_cast<uint32_t>(T) * 4u;
+  st.k = make_rsrc(a.k + n0 * T * 4, valid * st.row4);
+  st.q = make_rsrc(a.q + n0 * T * 4, valid * st.row4);
+  st.v = make_rsrc(a.v + n0 * T * 8, valid * st.row8);
+  st.y = make_rsrc(a.y + n0 * T * 8, valid * st.row8);
+  st.d = make_rsrc(FIXED ? a.k : a.d + n0 * T * 4, FIXED ? 0u : valid * st.row4);
+  st.p = make_rsrc(FIXED ? a.k : a.p + n0 * T, FIXED ? 0u : valid * st.row1);
+  st.r = make_rsrc(FIXED ? a.k : a.r + n0 * T, FIXED ? 0u : valid * st.row1);
+  const uint32_t nbp = static_cast<uint32_t>(a.nb + 1);
+  const Rsrc rbm = make_rsrc(a.bm + n0 * nbp * 32, valid * nbp * 128u);
+  const Rsrc rbc = make_rsrc(a.bc + n0 * nbp * 16, valid * nbp * 64u);
+  const Rsrc rm0 = make_rsrc(a.m0 + n0 * 32, valid * 128u);
+  const Rsrc rc0 = make_rsrc(a.c0 + n0 * 16, valid * 64u);
+  const Rsrc rmT = make_rsrc(a.mT + n0 * 32, valid * 128u);
+  const Rsrc rcT = make_rsrc(a.cT + n0 * 16, valid * 64u);
+  // Lane offsets in the belief records: the state tensors hold one record per
+  // sequence, the checkpoints nb + 1.
+  const uint32_t mo = static_cast<uint32_t>(s) * 128u + mean_off(i, j), co = static_cast<uint32_t>(s) * 64u + cov_off(i, j);
+  const uint32_t cmo = static_cast<uint32_t>(s) * nbp * 128u + mean_off(i, j),
+                 cco = static_cast<uint32_t>(s) * nbp * 64u + cov_off(i, j);
+
+  Bel b;
+  {
+    const v2f m = r4::ld64(rm0, mo, 0);
+    b.M0 = m[0];
+    b.M1 = m[1];
+    b.P = r4::ld32(rc0, co, 0);
+  }
+  // The initial belief has landed before the loop (a load pending at the
+  // loop header would make every iteration wait for all outstanding loads).
+  r4::vm_wait<0>();
+  auto store_ckpt = [&](uint32_t rec) __attribute__((always_inline)) {
+    v2f m;
+    m[0] = b.M0;
+    m[1] = b.M1;
+    r4::st64(rbm, m, cmo, rec * 128u);
+    r4::st32(rbc, b.P, cco, rec * 64u);
+  };
+  store_ckpt(0);
+
+  float* mine = tile + s * Tile::SEQ;
+  const int64_t ntiles = (T + TT - 1) / TT;
+  Stage x;
+  if (ntiles > 0) load_tile<FIXED>(x, st, s, c, 0);
+  int64_t next_ckpt = a.chunk;
+  uint32_t ckpt = 1;
+  v4f ys0 = v4f{0.f, 0.f, 0.f, 0.f}, ys1 = ys0;
+  for (int64_t ti = 0; ti < ntiles; ++ti) {
+    const uint32_t t0 = static_cast<uint32_t>(ti * TT);
+    const int len = static_cast<int>((T - t0) < TT ? (T - t0) : TT);
+    // The previous tile's readouts leave LDS before this tile lands there.
+    if (ti > 0) {
+      ys0 = *reinterpret_cast<const v4f*>(mine + Tile::V + 4 * c);
+      ys1 = *reinterpret_cast<const v4f*>(mine + Tile::V + 64 + 4 * c);
+    }
+    r4::vm_wait<0>();
+    put_tile<FIXED>(x, tile, s, c);
+    if (ti > 0) {
+      // Pieces c (token c >> 1) and c + 16 of the previous tile, all of whose tokens were computed.
+      const uint32_t p0 = t0 - TT, o8 = static_cast<uint32_t>(s) * st.row8 + p0 * 32u + c * 16u;
+      r4::st128<r4::kNtStore>(st.y, ys0, o8, 0);
+      r4::st128<r4::kNtStore>(st.y, ys1, o8 + 256u, 0);
+    }
+    if (ti + 1 < ntiles) load_tile<FIXED>(x, st, s, c, t0 + TT);
+    r4::lds_wait();
+    if (len == TT && a.chunk % 8 == 0) {
+#pragma unroll
+      for (int h = 0; h < TT / 8; ++h) {
+        if (static_cast<int64_t>(t0) + 8 * h == next_ckpt) {
+          store_ckpt(ckpt++);
+          next_ckpt += a.chunk;
+        }
+        Tok cur, nxt;
+        read_tok<FIXED>(cur, mine, 8 * h, i, j);
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+          const int tt = 8 * h + u;
+          if (u + 1 < 8) read_tok<FIXED>(nxt, mine, tt + 1, i, j);
+          StepOut o;
+          forward_step(b, cur, delta, a.floor, o);
+          const v2f y = readout(b, cur.qj);
+          mine[Tile::V + 8 * tt + 2 * i + (j & 1)] = (j & 1) ? y[1] : y[0];
+          cur = nxt;
+        }
+      }
+    } else {
+      for (int tt = 0; tt < len; ++tt) {
+        if (static_cast<int64_t>(t0) + tt == next_ckpt) {
+          store_ckpt(ckpt++);
+          next_ckpt += a.chunk;
+        }
+        Tok cur;
+        read_tok<FIXED>(cur, mine, tt, i, j);
+        StepOut o;
+        forward_step(b, cur, delta, a.floor, o);
+        const v2f y = readout(b, cur.qj);
+        mine[Tile::V + 8 * tt + 2 * i + (j & 1)] = (j & 1) ? y[1] : y[0];
+      }
+    }
+  }
+  if (ntiles > 0) {
+    // The last tile's readouts: only the pieces of its valid tokens.
+    const uint32_t t0 = static_cast<uint32_t>((ntiles - 1) * TT);
+    const int len = static_cast<int>(T - t0);
+    r4::lds_wait();
+    ys0 = *reinterpret_cast<const v4f*>(mine + Tile::V + 4 * c);
+    ys1 = *reinterpret_cast<const v4f*>(mine + Tile::V + 64 + 4 * c);
+    const uint32_t o8 = static_cast<uint32_t>(s) * st.row8 + t0 * 32u + c * 16u;
+    r4::st128<r4::kNtStore>(st.y, ys0, (c >> 1) < len ? o8 : kOob, 0);
+    r4::st128<r4::kNtStore>(st.y, ys1, ((c + 16) >> 1) < len ? o8 + 256u : kOob, 0);
+  }
+  v2f m;
+  m[0] = b.M0;
+  m[1] = b.M1;
+  r4::st64(rmT, m, mo, 0);
+  r4::st32(rcT, b.P, co, 0);
+  store_ckpt(static_cast<uint32_t>(a.nb));
+}
+
+}  // namespace
+}  // namespace sn
+
+namespace {
+std::atomic<int64_t> g_small_limit{0};
+}  // namespace
+
+int64_t small_batch_limit() { return g_small_limit.load(std::memory_order_relaxed); }
+int64_t set_small_batch_limit(int64_t limit) { return g_small_limit.exchange(limit, std::memory_order_relaxed); }
+
+hipError_t launch_forward_small(bool fixed, const FwdArgs& a, hipStream_t stream) {
+  const int64_t blocks = (a.n + sn::SPW - 1) / sn::SPW;
+  if (blocks == 0) return hipSuccess;
+  if (fixed) hipLaunchKernelGGL(sn::forward_kernel<true>, dim3(static_cast<unsigned>(blocks)), dim3(kWave), 0, stream, a);
+  else hipLaunchKernelGGL(sn::forward_kernel<false>, dim3(static_cast<unsigned>(blocks)), dim3(kWave), 0, stream, a);
+  return hipGetLastError();
+}
+
+}  // namespace bssm

@@ -429,6 +429,16 @@ int bssm_backward_chunked_rotation(int key_dim, int value_dim,
  * No reference counterpart. */
 int bssm_rotation_checkpoint(int key_dim);
 
+/* Largest sequence count N for which the D = 4, M = 8 float32 entry points
+ * use the row-per-sequence kernels (a 16-lane row per sequence, 4 per wave)
+ * instead of the rotated-layout ones (a quad per sequence, 16 per wave): at
+ * small N the waves of the latter do not fill the GPU and each wave's time is
+ * its instruction stream, which the row layout shortens.  Sets the limit when
+ * limit >= 0 and returns the previous one; limit < 0 only reads it.  Results
+ * agree within float32 rounding, not bitwise.  No counterpart in the
+ * reference (a tuning switch of this library). */
+int64_t bssm_small_batch_limit(int64_t limit);
+
 /* ------------------------------------------------------------------------
  * Length-four causal depthwise filter.  Replaces CausalDepthwise4.forward
  * (example/train_6layer.py:160-191) as the mixer applies it to each
