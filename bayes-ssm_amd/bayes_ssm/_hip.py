@@ -59,7 +59,7 @@ _SIGNATURES = {
     "bssm_mixer_backward": [_P, _L] * 5 + [_P] * 7 + [_P] * 7 + [_L, _L, _L, _L, _F, _I, _P],
     "bssm_mixer_gated_forward": [_P, _L] * 6 + [_P, _F] + [_P] * 8 + [_L, _L, _L, _L, _F, _I, _P],
     "bssm_rotation_checkpoint": [_I],
-    "bssm_small_batch_limit": [_L],
+    "bssm_small_batch_limit": [_I, _L],
     "bssm_forward_chunked_rotation": [_I, _I] + [_P] * 9 + [_P] * 5 + [_L, _L, _L, _F, _P],
     "bssm_backward_chunked_rotation": [_I, _I] + [_P] * 9 + [_P] * 5 + [_P] * 9 + [_L, _L, _L, _F, _P],
     "bssm_causal_conv4_forward": [_I, _P, _L, _P, _P, _L, _L, _L, _P],

@@ -87,10 +87,12 @@ hipError_t launch_forward_r4(bool fixed, const FwdArgs& a, hipStream_t stream);
 hipError_t launch_backward_r4(bool fixed, bool dyn, const BwdArgs& a, hipStream_t stream);
 // Row-per-sequence D = 4 kernels for small sequence counts (bssm_small.hip):
 // used for float32 streams when the rotated-layout kernels apply and n is at
-// most small_batch_limit().
+// most small_batch_limit(0) (forward) or small_batch_limit(1) (backward).
 hipError_t launch_forward_small(bool fixed, const FwdArgs& a, hipStream_t stream);
-int64_t small_batch_limit();
-int64_t set_small_batch_limit(int64_t limit);
+// The backward needs T a multiple of 16 and the kRot4Chunk checkpoint chunk.
+hipError_t launch_backward_small(bool fixed, bool dyn, const BwdArgs& a, hipStream_t stream);
+int64_t small_batch_limit(int direction);
+int64_t set_small_batch_limit(int direction, int64_t limit);
 
 // D = 1, M = 8 kernels with one lane per value column (bssm_d1.hip).  The
 // forward needs 16-byte aligned streams, T and the checkpoint chunk

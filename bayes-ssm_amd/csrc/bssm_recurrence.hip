@@ -488,7 +488,7 @@ int preferred_checkpoint(int key_dim) {
 }
 
 hipError_t launch_forward(int key_dim, bool fixed, const FwdArgs& a, hipStream_t stream) {
-  if (key_dim == 4 && a.rot4 && a.in_fmt == kInF32 && a.n <= small_batch_limit())
+  if (key_dim == 4 && a.rot4 && a.in_fmt == kInF32 && a.n <= small_batch_limit(0))
     return launch_forward_small(fixed, a, stream);
   if (key_dim == 4 && a.rot4) return launch_forward_r4(fixed, a, stream);
   if (key_dim == 1 && d1_forward_ok(a)) return launch_forward_d1(fixed, a, stream);
@@ -510,6 +510,9 @@ hipError_t launch_backward_dd(bool fixed, bool dyn, const BwdArgs& a, hipStream_
 }
 
 hipError_t launch_backward(int key_dim, bool fixed, bool dyn, const BwdArgs& a, hipStream_t stream) {
+  if (key_dim == 4 && a.rot4 && a.in_fmt == kInF32 && a.n <= small_batch_limit(1) && a.t % 16 == 0 &&
+      a.chunk == kRot4Chunk)
+    return launch_backward_small(fixed, dyn, a, stream);
   if (key_dim == 4 && a.rot4) return launch_backward_r4(fixed, dyn, a, stream);
   if (key_dim == 1 && d1_backward_ok(a)) return launch_backward_d1(fixed, dyn, a, stream);
   if (key_dim == 2 && d2_backward_ok(a)) return launch_backward_d2(fixed, dyn, a, stream);

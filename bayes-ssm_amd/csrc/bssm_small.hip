@@ -7,7 +7,11 @@
 // hold live sequences.  Here a 16-lane DPP row holds one sequence (4 per
 // wave) and every lane one entry of the covariance, so the per-token stream
 // is about 40 % shorter (four times as many waves, each doing a quarter of
-// the state).
+// the state).  The row layout spends about 2.4 times the lane work per
+// sequence, so once every SIMD holds several waves the rotated layout wins:
+// for the backward above about 8192 sequences, for the forward (which at
+// 16384 sequences still gains from its 4 waves per SIMD against the rotated
+// layout's one) above about 24576.
 //
 // Lane (i, j) of a sequence's row (i = row bits 3:2, j = bits 1:0) holds
 //   P[i][j]                    (the covariance, bitwise symmetric)
@@ -312,21 +316,405 @@ __global__ __launch_bounds__(kWave) void forward_kernel(FwdArgs a) {
   store_ckpt(static_cast<uint32_t>(a.nb));
 }
 
+// ----------------------------------------------------------------- backward
+// A 16-token tile holds two checkpoint chunks of 8 tokens (T a multiple of
+// 16); tiles are visited last to first, and in each the chunk 2J + 1 before
+// the chunk 2J.  A chunk is replayed from its checkpoint, keeping each
+// token's belief and step intermediates in registers, and then reversed.
+// Gradients overwrite their inputs in the tile (gk over k, gq over q, gd over
+// d, gv over v, gp over p, gr over r) and leave with the next tile's loads.
+//
+// LDS per sequence: k, d, q [TT][4], v, gy [TT][8], p, r [TT]; the stride
+// (mod 32 banks = 8) puts the 4 sequences' reads of one token in different
+// banks.
+struct BTile {
+  static constexpr int K = 0, D = 64, Q = 128, V = 192, GY = 320, P = 448, R = 464, SEQ = 488, SIZE = SPW * SEQ;
+};
+
+struct BStage {
+  v4f k, d, q, v0, v1, g0, g1, p, r;
+};
+// Gradient pieces of one tile, in the loaders' geometry.
+struct GStage {
+  v4f k, d, q, v0, v1, p, r;
+};
+
+struct BStreams {
+  Rsrc k, d, q, v, gy, p, r;
+  Rsrc gk, gd, gq, gv, gp, gr;
+  uint32_t row4, row8, row1;
+};
+
+template <bool FIXED>
+__device__ __forceinline__ void load_btile(BStage& x, const BStreams& st, int s, int c, uint32_t t0) {
+  const uint32_t o4 = static_cast<uint32_t>(s) * st.row4 + (t0 + c) * 16u;
+  x.k = r4::ld128<true>(st.k, o4);
+  x.q = r4::ld128<true>(st.q, o4);
+  if constexpr (!FIXED) x.d = r4::ld128<true>(st.d, o4);
+  const uint32_t o8 = static_cast<uint32_t>(s) * st.row8 + t0 * 32u + c * 16u;
+  x.v0 = r4::ld128<true>(st.v, o8);
+  x.v1 = r4::ld128<true>(st.v, o8 + 256u);
+  x.g0 = r4::ld128<true>(st.gy, o8);
+  x.g1 = r4::ld128<true>(st.gy, o8 + 256u);
+  if constexpr (!FIXED) {
+    const uint32_t o1 = c < 4 ? static_cast<uint32_t>(s) * st.row1 + t0 * 4u + c * 16u : kOob;
+    x.p = r4::ld128<false>(st.p, o1);
+    x.r = r4::ld128<false>(st.r, o1);
+  }
+}
+
+template <bool FIXED>
+__device__ __forceinline__ void put_btile(const BStage& x, float* tl, int s, int c) {
+  float* b = tl + s * BTile::SEQ;
+  *reinterpret_cast<v4f*>(b + BTile::K + 4 * c) = x.k;
+  *reinterpret_cast<v4f*>(b + BTile::Q + 4 * c) = x.q;
+  *reinterpret_cast<v4f*>(b + BTile::V + 4 * c) = x.v0;
+  *reinterpret_cast<v4f*>(b + BTile::V + 64 + 4 * c) = x.v1;
+  *reinterpret_cast<v4f*>(b + BTile::GY + 4 * c) = x.g0;
+  *reinterpret_cast<v4f*>(b + BTile::GY + 64 + 4 * c) = x.g1;
+  if constexpr (!FIXED) {
+    *reinterpret_cast<v4f*>(b + BTile::D + 4 * c) = x.d;
+    if (c < 4) {
+      *reinterpret_cast<v4f*>(b + BTile::P + 4 * c) = x.p;
+      *reinterpret_cast<v4f*>(b + BTile::R + 4 * c) = x.r;
+    }
+  }
+}
+
+// The gradient pieces of a tile: read from LDS, then stored (requested
+// outputs only) at the loaders' offsets.
+template <bool DYN>
+__device__ __forceinline__ void get_grads(GStage& g, const float* tl, int s, int c) {
+  const float* b = tl + s * BTile::SEQ;
+  g.k = *reinterpret_cast<const v4f*>(b + BTile::K + 4 * c);
+  g.q = *reinterpret_cast<const v4f*>(b + BTile::Q + 4 * c);
+  g.v0 = *reinterpret_cast<const v4f*>(b + BTile::V + 4 * c);
+  g.v1 = *reinterpret_cast<const v4f*>(b + BTile::V + 64 + 4 * c);
+  if constexpr (DYN) {
+    g.d = *reinterpret_cast<const v4f*>(b + BTile::D + 4 * c);
+    g.p = *reinterpret_cast<const v4f*>(b + BTile::P + 4 * (c & 3));
+    g.r = *reinterpret_cast<const v4f*>(b + BTile::R + 4 * (c & 3));
+  }
+}
+
+template <bool DYN>
+__device__ __forceinline__ void store_grads(const GStage& g, const BStreams& st, const BwdArgs& a, int s, int c,
+                                            uint32_t t0) {
+  const uint32_t o4 = static_cast<uint32_t>(s) * st.row4 + (t0 + c) * 16u;
+  r4::st128<r4::kNtStore>(st.gk, g.k, o4, 0);
+  r4::st128<r4::kNtStore>(st.gq, g.q, o4, 0);
+  const uint32_t o8 = static_cast<uint32_t>(s) * st.row8 + t0 * 32u + c * 16u;
+  r4::st128<r4::kNtStore>(st.gv, g.v0, o8, 0);
+  r4::st128<r4::kNtStore>(st.gv, g.v1, o8 + 256u, 0);
+  // Without dynamics gradients, requested gd / gp / gr outputs are zero.
+  const v4f zero = v4f{0.f, 0.f, 0.f, 0.f};
+  if (a.gd) r4::st128<r4::kNtStore>(st.gd, DYN ? g.d : zero, o4, 0);
+  const uint32_t o1 = c < 4 ? static_cast<uint32_t>(s) * st.row1 + t0 * 4u + c * 16u : kOob;
+  if (a.gp) r4::st128(st.gp, DYN ? g.p : zero, o1, 0);
+  if (a.gr) r4::st128(st.gr, DYN ? g.r : zero, o1, 0);
+}
+
+// Replay record of one token: the belief before it and the step's
+// intermediates.
+struct Hist {
+  float P, M0, M1, ui, uj, s;
+  v2f e;
+};
+
+// Reverse-step inputs of lane (i, j).
+struct RTok {
+  float ki, kj, di, dj, qj, p;
+  v2f gy;  // gy[2i], gy[2i + 1]
+};
+
+template <bool FIXED>
+__device__ __forceinline__ void read_rtok(RTok& x, const float* b, int tt, int i, int j) {
+  x.ki = b[BTile::K + 4 * tt + i];
+  x.kj = b[BTile::K + 4 * tt + j];
+  x.qj = b[BTile::Q + 4 * tt + j];
+  x.gy = *reinterpret_cast<const v2f*>(b + BTile::GY + 8 * tt + 2 * i);
+  if constexpr (FIXED) {
+    x.di = x.dj = kFixedDecay;
+    x.p = kFixedProcess;
+  } else {
+    x.di = b[BTile::D + 4 * tt + i];
+    x.dj = b[BTile::D + 4 * tt + j];
+    x.p = b[BTile::P + tt];
+  }
+}
+
+// The replay reads the same token inputs as the forward (v, r from the
+// backward tile's regions).
+template <bool FIXED>
+__device__ __forceinline__ void read_ftok(Tok& x, const float* b, int tt, int i, int j) {
+  x.ki = b[BTile::K + 4 * tt + i];
+  x.kj = b[BTile::K + 4 * tt + j];
+  x.qj = 0.f;
+  x.v = *reinterpret_cast<const v2f*>(b + BTile::V + 8 * tt + 2 * i);
+  if constexpr (FIXED) {
+    x.di = x.dj = kFixedDecay;
+    x.p = kFixedProcess;
+    x.r = kFixedObservation;
+  } else {
+    x.di = b[BTile::D + 4 * tt + i];
+    x.dj = b[BTile::D + 4 * tt + j];
+    x.p = b[BTile::P + tt];
+    x.r = b[BTile::R + tt];
+  }
+}
+
+// x at lane (i, i) of the row, given at every lane of quad i: the transpose
+// of a quantity indexed by the column j (constant down each column).
+__device__ __forceinline__ float diag_pick(float x, bool i1, bool i2) {
+  const float x0 = dpp<quad_perm(0, 0, 0, 0)>(x), x1 = dpp<quad_perm(1, 1, 1, 1)>(x);
+  const float x2 = dpp<quad_perm(2, 2, 2, 2)>(x), x3 = dpp<quad_perm(3, 3, 3, 3)>(x);
+  const float lo = i1 ? x1 : x0, hi = i1 ? x3 : x2;
+  return i2 ? hi : lo;
+}
+
+// Adjoint of one token, lane (i, j).  Carried: gM0, gM1 = dL/dM[j][2i],
+// dL/dM[j][2i + 1] and S = sym(dL/dP)[i][j], updated in place to their values
+// before the token.  With dL/dM_new including q gy^T (the equations of
+// reverse_step in bssm_rot4.h, one covariance entry per lane):
+//   ge = beta gM^T u (= dL/dv),  a = gM e,  w = S u,  z = u.(a - w)
+//   gs = (s > floor) ? -z beta^2 : 0 (= dL/dr),  gu = beta (a - 2 w) + gs k
+//   dL/dk = -d*(M_prev ge) + gs u + P' gu  (P' = d d^T * P_prev + p I)
+//   dL/dq = M_new gy,  H = S + sym(gu k^T)
+//   dL/dd = 2 (H * P_prev) d + sum_c (gM - k ge^T) * M_prev,  dL/dp = trace H
+//   S_prev = H * d d^T,  gM_prev = (gM - k ge^T) * d
+struct ROut {
+  float gk, gq, gd, gp, gs, gui, guj;
+  v2f ge;
+};
+
+template <bool DYN>
+__device__ __forceinline__ void reverse_step(const RTok& x, const Hist& h, float Mn0, float Mn1, float& gM0,
+                                             float& gM1, float& S, float floor, float delta, bool i1, bool i2,
+                                             ROut& o) {
+  const float beta = fast_rcp(fmaxf(h.s, floor));
+  gM0 = fmaf(x.qj, x.gy[0], gM0);
+  gM1 = fmaf(x.qj, x.gy[1], gM1);
+  const float ge0 = beta * quad_sum(gM0 * h.uj), ge1 = beta * quad_sum(gM1 * h.uj);
+  const float a = col_sum(fmaf(gM1, h.e[1], gM0 * h.e[0]));
+  const float A = col_sum(fmaf(h.M1, ge1, h.M0 * ge0));
+  o.gq = col_sum(fmaf(Mn1, x.gy[1], Mn0 * x.gy[0]));
+  const float gb0 = fmaf(-x.kj, ge0, gM0), gb1 = fmaf(-x.kj, ge1, gM1);
+  gM0 = gb0 * x.dj;
+  gM1 = gb1 * x.dj;
+  const float w = col_sum(S * h.ui);  // (S u)_j
+  const float z = quad_sum(h.uj * (a - w));
+  const float gs = h.s > floor ? -z * beta * beta : 0.f;
+  const float guj = fmaf(beta, fmaf(-2.f, w, a), gs * x.kj);
+  const float gui = diag_pick(guj, i1, i2);
+  const float dd = x.di * x.dj;
+  const float pb = fmaf(x.p, delta, dd * h.P);
+  o.gk = fmaf(-x.dj, A, gs * h.uj) + col_sum(pb * gui);
+  const float H = fmaf(0.5f, gui * x.kj + guj * x.ki, S);  // bitwise symmetric with S
+  if constexpr (DYN) {
+    const float Bv = col_sum(fmaf(gb1, h.M1, gb0 * h.M0));
+    o.gd = fmaf(2.f, col_sum((H * x.di) * h.P), Bv);
+    o.gp = col_sum(quad_sum(delta * H));
+  } else {
+    o.gd = o.gp = 0.f;
+  }
+  S = H * dd;
+  o.gs = gs;
+  o.gui = gui;
+  o.guj = guj;
+  o.ge[0] = ge0;
+  o.ge[1] = ge1;
+}
+
+// What the initial-covariance adjoint needs of a sequence's first token.
+struct First {
+  float gui, guj, ki, kj, dd;
+};
+
+template <bool FIXED, bool DYN>
+__global__ __launch_bounds__(kWave) void backward_kernel(BwdArgs a) {
+  __shared__ float tile[BTile::SIZE];
+  const int lane = threadIdx.x;
+  const int s = lane >> 4, c = lane & 15, i = c >> 2, j = c & 3;
+  const float delta = i == j ? 1.f : 0.f;
+  const bool i1 = (i & 1) != 0, i2 = (i & 2) != 0;
+  const int64_t n0 = static_cast<int64_t>(blockIdx.x) * SPW;
+  const int64_t T = a.t;
+  const uint32_t valid = static_cast<uint32_t>((a.n - n0) < SPW ? (a.n - n0) : SPW);
+  BStreams st;
+  st.row4 = static_cast<uint32_t>(T) * 16u;
+  st.row8 = static_cast<uint32_t>(T) * 32u;
+  st.row1 = static_cast<uint32_t>(T) * 4u;
+  st.k = make_rsrc(a.k + n0 * T * 4, valid * st.row4);
+  st.q = make_rsrc(a.q + n0 * T * 4, valid * st.row4);
+  st.v = make_rsrc(a.v + n0 * T * 8, valid * st.row8);
+  st.gy = make_rsrc(a.gy + n0 * T * 8, valid * st.row8);
+  st.d = make_rsrc(FIXED ? a.k : a.d + n0 * T * 4, FIXED ? 0u : valid * st.row4);
+  st.p = make_rsrc(FIXED ? a.k : a.p + n0 * T, FIXED ? 0u : valid * st.row1);
+  st.r = make_rsrc(FIXED ? a.k : a.r + n0 * T, FIXED ? 0u : valid * st.row1);
+  st.gk = make_rsrc(a.gk + n0 * T * 4, valid * st.row4);
+  st.gq = make_rsrc(a.gq + n0 * T * 4, valid * st.row4);
+  st.gv = make_rsrc(a.gv + n0 * T * 8, valid * st.row8);
+  st.gd = make_rsrc(a.gd ? a.gd + n0 * T * 4 : a.gk, a.gd ? valid * st.row4 : 0u);
+  st.gp = make_rsrc(a.gp ? a.gp + n0 * T : a.gk, a.gp ? valid * st.row1 : 0u);
+  st.gr = make_rsrc(a.gr ? a.gr + n0 * T : a.gk, a.gr ? valid * st.row1 : 0u);
+  const uint32_t nbp = static_cast<uint32_t>(a.nb + 1);
+  const Rsrc rbm = make_rsrc(a.bm + n0 * nbp * 32, valid * nbp * 128u);
+  const Rsrc rbc = make_rsrc(a.bc + n0 * nbp * 16, valid * nbp * 64u);
+  const uint32_t mo = static_cast<uint32_t>(s) * 128u + mean_off(i, j), co = static_cast<uint32_t>(s) * 64u + cov_off(i, j);
+  const uint32_t cmo = static_cast<uint32_t>(s) * nbp * 128u + mean_off(i, j),
+                 cco = static_cast<uint32_t>(s) * nbp * 64u + cov_off(i, j);
+
+  // Carried adjoints from the final-state gradients (null: zero).
+  float gM0, gM1, S;
+  {
+    const bool has_m = a.gmf != nullptr, has_c = a.gcf != nullptr;
+    const Rsrc rgm = make_rsrc(has_m ? a.gmf + n0 * 32 : a.k, has_m ? valid * 128u : 0u);
+    const Rsrc rgc = make_rsrc(has_c ? a.gcf + n0 * 16 : a.k, has_c ? valid * 64u : 0u);
+    const v2f m = r4::ld64(rgm, mo, 0);
+    gM0 = m[0];
+    gM1 = m[1];
+    const uint32_t tr = static_cast<uint32_t>(s) * 64u + cov_off(j, i);
+    S = 0.5f * (r4::ld32(rgc, co, 0) + r4::ld32(rgc, tr, 0));
+  }
+  auto load_ckpt = [&](Bel& b, int64_t rec) __attribute__((always_inline)) {
+    const v2f m = r4::ld64(rbm, cmo + static_cast<uint32_t>(rec) * 128u, 0);
+    b.M0 = m[0];
+    b.M1 = m[1];
+    b.P = r4::ld32(rbc, cco + static_cast<uint32_t>(rec) * 64u, 0);
+  };
+
+  float* mine = tile + s * BTile::SEQ;
+  First first = {0.f, 0.f, 0.f, 0.f, 0.f};
+  // Replay and reverse of the chunk at tile token base (0 or 8).
+  auto run_chunk = [&](Bel b, int base) __attribute__((always_inline)) {
+    Hist h[8];
+    {
+      Tok cur, nxt;
+      read_ftok<FIXED>(cur, mine, base, i, j);
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        if (u + 1 < 8) read_ftok<FIXED>(nxt, mine, base + u + 1, i, j);
+        h[u].P = b.P;
+        h[u].M0 = b.M0;
+        h[u].M1 = b.M1;
+        StepOut o;
+        forward_step(b, cur, delta, a.floor, o);
+        h[u].ui = o.ui;
+        h[u].uj = o.uj;
+        h[u].s = o.s;
+        h[u].e = o.e;
+        cur = nxt;
+      }
+    }
+    RTok cur, nxt;
+    read_rtok<FIXED>(cur, mine, base + 7, i, j);
+#pragma unroll
+    for (int u = 7; u >= 0; --u) {
+      const int tt = base + u;
+      if (u > 0) read_rtok<FIXED>(nxt, mine, tt - 1, i, j);
+      // The mean after the token: the next token's record, or the replayed
+      // belief after the chunk's last token.
+      const float Mn0 = u < 7 ? h[u < 7 ? u + 1 : u].M0 : b.M0;
+      const float Mn1 = u < 7 ? h[u < 7 ? u + 1 : u].M1 : b.M1;
+      ROut o;
+      reverse_step<DYN>(cur, h[u], Mn0, Mn1, gM0, gM1, S, a.floor, delta, i1, i2, o);
+      mine[BTile::K + 4 * tt + j] = o.gk;
+      mine[BTile::Q + 4 * tt + j] = o.gq;
+      mine[BTile::V + 8 * tt + 2 * i + (j & 1)] = (j & 1) ? o.ge[1] : o.ge[0];
+      if constexpr (DYN) {
+        mine[BTile::D + 4 * tt + j] = o.gd;
+        mine[BTile::P + tt] = o.gp;
+        mine[BTile::R + tt] = o.gs;
+      }
+      if (u == 0) {
+        first.gui = o.gui;
+        first.guj = o.guj;
+        first.ki = cur.ki;
+        first.kj = cur.kj;
+        first.dd = cur.di * cur.dj;
+      }
+      cur = nxt;
+    }
+  };
+
+  const int64_t ntiles = T / TT;
+  BStage x;
+  Bel nk0, nk1;
+  if (ntiles > 0) {
+    load_btile<FIXED>(x, st, s, c, static_cast<uint32_t>((ntiles - 1) * TT));
+    load_ckpt(nk0, 2 * (ntiles - 1));
+    load_ckpt(nk1, 2 * (ntiles - 1) + 1);
+  }
+  GStage go;
+  for (int64_t ti = ntiles - 1; ti >= 0; --ti) {
+    const uint32_t t0 = static_cast<uint32_t>(ti * TT);
+    // The next tile's gradients leave LDS before this tile lands there.
+    if (ti + 1 < ntiles) get_grads<DYN>(go, tile, s, c);
+    r4::vm_wait<0>();
+    const Bel k0 = nk0, k1 = nk1;
+    put_btile<FIXED>(x, tile, s, c);
+    if (ti + 1 < ntiles) store_grads<DYN>(go, st, a, s, c, t0 + TT);
+    if (ti > 0) {
+      load_btile<FIXED>(x, st, s, c, t0 - TT);
+      load_ckpt(nk0, 2 * ti - 2);
+      load_ckpt(nk1, 2 * ti - 1);
+    }
+    r4::lds_wait();
+    run_chunk(k1, 8);
+    run_chunk(k0, 0);
+  }
+  if (ntiles > 0) {
+    r4::lds_wait();
+    get_grads<DYN>(go, tile, s, c);
+    store_grads<DYN>(go, st, a, s, c, 0);
+  }
+  if (a.gm0) {
+    const Rsrc rgm0 = make_rsrc(a.gm0 + n0 * 32, valid * 128u);
+    v2f m;
+    m[0] = gM0;
+    m[1] = gM1;
+    r4::st64(rgm0, m, mo, 0);
+  }
+  if (a.gc0) {
+    // The full (asymmetric) derivative for the covariance entering the first
+    // token: S + (gu k^T - sym(gu k^T)) * d d^T.
+    const Rsrc rgc0 = make_rsrc(a.gc0 + n0 * 16, valid * 64u);
+    const float asym = 0.5f * (first.gui * first.kj - first.guj * first.ki);
+    r4::st32(rgc0, fmaf(asym, first.dd, S), co, 0);
+  }
+}
+
 }  // namespace
 }  // namespace sn
 
 namespace {
-std::atomic<int64_t> g_small_limit{0};
+// Measured crossovers against the rotated-layout kernels (T = 512): the row
+// forward is faster up to about 24576 sequences and level beyond, the row
+// backward up to about 8192.
+std::atomic<int64_t> g_small_limit[2] = {{24576}, {8192}};
 }  // namespace
 
-int64_t small_batch_limit() { return g_small_limit.load(std::memory_order_relaxed); }
-int64_t set_small_batch_limit(int64_t limit) { return g_small_limit.exchange(limit, std::memory_order_relaxed); }
+int64_t small_batch_limit(int direction) { return g_small_limit[direction].load(std::memory_order_relaxed); }
+int64_t set_small_batch_limit(int direction, int64_t limit) {
+  return g_small_limit[direction].exchange(limit, std::memory_order_relaxed);
+}
 
 hipError_t launch_forward_small(bool fixed, const FwdArgs& a, hipStream_t stream) {
   const int64_t blocks = (a.n + sn::SPW - 1) / sn::SPW;
   if (blocks == 0) return hipSuccess;
   if (fixed) hipLaunchKernelGGL(sn::forward_kernel<true>, dim3(static_cast<unsigned>(blocks)), dim3(kWave), 0, stream, a);
   else hipLaunchKernelGGL(sn::forward_kernel<false>, dim3(static_cast<unsigned>(blocks)), dim3(kWave), 0, stream, a);
+  return hipGetLastError();
+}
+
+hipError_t launch_backward_small(bool fixed, bool dyn, const BwdArgs& a, hipStream_t stream) {
+  if (a.t % sn::TT != 0 || a.chunk != kRot4Chunk) return hipErrorInvalidValue;
+  const int64_t blocks = (a.n + sn::SPW - 1) / sn::SPW;
+  if (blocks == 0) return hipSuccess;
+  const dim3 grid(static_cast<unsigned>(blocks)), block(kWave);
+  if (fixed) hipLaunchKernelGGL((sn::backward_kernel<true, false>), grid, block, 0, stream, a);
+  else if (dyn) hipLaunchKernelGGL((sn::backward_kernel<false, true>), grid, block, 0, stream, a);
+  else hipLaunchKernelGGL((sn::backward_kernel<false, false>), grid, block, 0, stream, a);
   return hipGetLastError();
 }
 

@@ -429,15 +429,20 @@ int bssm_backward_chunked_rotation(int key_dim, int value_dim,
  * No reference counterpart. */
 int bssm_rotation_checkpoint(int key_dim);
 
-/* Largest sequence count N for which the D = 4, M = 8 float32 entry points
- * use the row-per-sequence kernels (a 16-lane row per sequence, 4 per wave)
- * instead of the rotated-layout ones (a quad per sequence, 16 per wave): at
- * small N the waves of the latter do not fill the GPU and each wave's time is
- * its instruction stream, which the row layout shortens.  Sets the limit when
- * limit >= 0 and returns the previous one; limit < 0 only reads it.  Results
- * agree within float32 rounding, not bitwise.  No counterpart in the
- * reference (a tuning switch of this library). */
-int64_t bssm_small_batch_limit(int64_t limit);
+/* Largest sequence count N for which the D = 4, M = 8 float32 forward
+ * (direction 0) or backward (direction 1) uses the row-per-sequence kernels
+ * (a 16-lane row per sequence, 4 per wave) instead of the rotated-layout ones
+ * (a quad per sequence, 16 per wave).  Below about 1024 x 16 sequences the
+ * waves of the latter do not fill the GPU and each wave's time is its own
+ * instruction stream, which the row layout shortens; at large N the row
+ * layout's extra lane work costs more than it saves (the backward first).
+ * The backward also needs T a multiple of 16 and the preferred checkpoint
+ * chunk.  Defaults: 24576 (forward), 8192 (backward), the measured
+ * crossovers.  Sets the limit when limit >= 0 and returns the previous one;
+ * limit < 0 only reads it; -1 for any other direction.  Results agree within
+ * float32 rounding, not bitwise.  No counterpart in the reference (a tuning
+ * switch of this library). */
+int64_t bssm_small_batch_limit(int direction, int64_t limit);
 
 /* ------------------------------------------------------------------------
  * Length-four causal depthwise filter.  Replaces CausalDepthwise4.forward

@@ -34,3 +34,12 @@ def cuda_device():
     if not torch.cuda.is_available():
         pytest.skip("no GPU")
     return torch.device("cuda:0")
+
+
+@pytest.fixture
+def rotated_layout(cuda_device):
+    """D4M8 float32 calls take the rotated-layout kernels (those the bf16 and float8 entry points share)."""
+    from tests._layouts import layout
+
+    with layout("quad"):
+        yield

@@ -195,3 +195,20 @@ def test_conv_backward_noalloc_rejects_sizes_beyond_its_scratch(lib):
     rc = lib.bssm_causal_conv4_backward_noalloc(1, None, 8, None, None, None, None, 4, 0, 8, None)
     assert rc == 1 and b"grad_weight" in lib.bssm_last_error()
     assert lib.bssm_causal_conv4_backward_noalloc(1, None, 8, None, None, None, None, 4, 0, 0, None) == 0
+
+
+def test_small_batch_limits_read_set_restore(lib):
+    """Forward and backward limits of the row-per-sequence D4 kernels: defaults, set, read, restore."""
+    fwd, bwd = lib.bssm_small_batch_limit(0, -1), lib.bssm_small_batch_limit(1, -1)
+    assert (fwd, bwd) == (24576, 8192)
+    try:
+        assert lib.bssm_small_batch_limit(0, 7) == fwd
+        assert lib.bssm_small_batch_limit(0, -1) == 7
+        assert lib.bssm_small_batch_limit(1, -1) == bwd, "directions are independent"
+        assert lib.bssm_small_batch_limit(1, 0) == bwd
+        assert lib.bssm_small_batch_limit(1, -1) == 0
+    finally:
+        lib.bssm_small_batch_limit(0, fwd)
+        lib.bssm_small_batch_limit(1, bwd)
+    assert lib.bssm_small_batch_limit(2, 5) == -1 and lib.bssm_small_batch_limit(-1, -1) == -1
+    assert (lib.bssm_small_batch_limit(0, -1), lib.bssm_small_batch_limit(1, -1)) == (fwd, bwd)

@@ -163,7 +163,7 @@ def test_floor_autograd_boundary_config_length(cuda_device, d):
 
 
 @pytest.mark.parametrize("t", [64, 52])
-def test_floor_bf16_kernels_equal_float32_kernels(cuda_device, t):
+def test_floor_bf16_kernels_equal_float32_kernels(cuda_device, rotated_layout, t):
     """The bf16 k/v/q D4M8 kernels with the floor active: bitwise the float32 kernels' results."""
     from bayes_ssm.fused_cuda import fused_diagonal_bayesian
 

@@ -18,7 +18,7 @@ import torch
 from oracle import bssm_oracle as O
 from tests.test_gpu_parity import _case, close
 
-pytestmark = pytest.mark.gpu
+pytestmark = [pytest.mark.gpu, pytest.mark.usefixtures("rotated_layout")]
 
 FMTS = {0: torch.float8_e4m3fn, 1: torch.float8_e5m2}
 

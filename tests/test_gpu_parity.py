@@ -422,7 +422,7 @@ def _bf16_case(n, t, seed, device):
 
 @pytest.mark.parametrize("t", [4, 8, 12, 16, 20, 52, 64])
 @pytest.mark.parametrize("fixed", [False, True])
-def test_bf16_abi_matches_float32_kernels(cuda_device, t, fixed):
+def test_bf16_abi_matches_float32_kernels(cuda_device, rotated_layout, t, fixed):
     """bf16 k/v/q C ABI: outputs bit-identical to the float32 kernels on the widened values;
     gk/gv/gq are the float32 gradients rounded to bfloat16, the other gradients bit-identical."""
     from bayes_ssm import _hip, fused_cuda
@@ -467,7 +467,7 @@ def test_bf16_abi_matches_float32_kernels(cuda_device, t, fixed):
 
 @pytest.mark.parametrize("t", [64, 45])
 @pytest.mark.parametrize("leaves", ["all", "kqv"])
-def test_bf16_autograd_boundary(cuda_device, t, leaves):
+def test_bf16_autograd_boundary(cuda_device, rotated_layout, t, leaves):
     """fused_diagonal_bayesian with bf16 k/v/q leaves equals the float32 path on the widened values
     (T = 45 is not a multiple of 4: the bf16 inputs are widened and take the float32 kernels)."""
     from bayes_ssm.fused_cuda import fused_diagonal_bayesian

@@ -1,0 +1,159 @@
+"""D4M8 float32 kernels in both wave layouts: the row-per-sequence kernels
+(a 16-lane row per sequence, used up to the small-batch limits) and the
+rotated-layout kernels (a quad per sequence), each forced through the C ABI's
+``bssm_small_batch_limit`` and checked against the float64 oracle.
+
+The library picks the layout from the sequence count, so at the parity
+tests' sizes the other files see the row kernels; here both layouts run the
+same cases.  Tolerance (north star): 1e-5 relative, 1e-4 absolute; checkpoint
+indexing and chunk invariance bit-exact.
+"""
+from __future__ import annotations
+
+import contextlib
+
+import pytest
+import torch
+
+from oracle import bssm_oracle as O
+from tests.test_gpu_floor import NAMES, _check, _floor_case, _run_abi
+from tests._layouts import LAYOUTS, layout
+from tests.test_gpu_parity import ABIS, _case, _fixed_dynamics, _oracle_forward, close
+
+pytestmark = pytest.mark.gpu
+
+def _ext():
+    from bayes_ssm import fused_cuda
+
+    e = fused_cuda._load_extension(4)
+    assert e is not None
+    return e
+
+
+def _forward(ext, dev, fixed, chunk, floor=1e-6):
+    fn = ext.forward_chunked_fixed if fixed else ext.forward_chunked
+    return fn(dev["k"], dev["v"], dev["q"], dev["d"], dev["p"], dev["r"], dev["m0"], dev["c0"], chunk, floor)
+
+
+def _backward(ext, name, fixed, nout, dev, bm, bc, chunk, final_grads, floor=1e-6):
+    gmf = dev["gmf"] if final_grads else None
+    gcf = dev["gcf"] if final_grads else None
+    args = (dev["k"], dev["v"], dev["q"], dev["d"], dev["p"], dev["r"], dev["m0"], dev["c0"], bm, bc, dev["gy"], gmf,
+            gcf, chunk, floor)
+    if hasattr(ext, name):
+        return getattr(ext, name)(*args)
+    return ext._backward("bssm_" + name, fixed, nout, *args[:8], bm, bc, (), dev["gy"], gmf, gcf, chunk, floor)
+
+
+# Both layouts need T a multiple of 4 (other T take the generic kernels).
+# T = 4, 20 and 52: partial last tiles (the row backward needs T a multiple of
+# 16, so there the backward keeps the rotated layout); N = 37, 6 and 1 leave
+# idle rows in the last wave.
+@pytest.mark.parametrize("name", list(LAYOUTS))
+@pytest.mark.parametrize("fixed", [False, True])
+@pytest.mark.parametrize("chunk", [1, 8, 13])
+@pytest.mark.parametrize("n,t", [(37, 16), (37, 20), (37, 52), (1, 64), (6, 4)])
+def test_layout_forward_matches_oracle(cuda_device, name, fixed, chunk, n, t):
+    print(f"layout {name} forward fixed={fixed} chunk={chunk} n={n} t={t}", flush=True)
+    cpu, dev = _case(n, t, 4, seed=11 * chunk + t, device=cuda_device)
+    with layout(name):
+        y, mT, cT, bm, bc = _forward(_ext(), dev, fixed, chunk)
+        torch.cuda.synchronize()
+    ref = _fixed_dynamics(cpu) if fixed else cpu
+    ey, em, ec = _oracle_forward(ref, False)
+    close(y, ey, "y")
+    close(mT, em, "mean_T")
+    close(cT, ec, "cov_T")
+    f64 = {k: x.double() for k, x in ref.items()}
+    ebm, ebc = O.checkpoints(f64["k"], f64["v"], f64["q"], f64["d"], f64["p"], f64["r"], f64["m0"], f64["c0"],
+                             chunk, 1e-6)
+    close(bm, ebm, "bmean")
+    close(bc, ebc, "bcov")
+    nb = -(-t // chunk)
+    assert torch.equal(bm[:, nb].cpu(), mT.cpu()) and torch.equal(bc[:, nb].cpu(), cT.cpu())
+    assert torch.equal(bm[:, 0].cpu(), dev["m0"].cpu())
+
+
+@pytest.mark.parametrize("name", list(LAYOUTS))
+@pytest.mark.parametrize("abi", ABIS, ids=[a[0] for a in ABIS])
+@pytest.mark.parametrize("final_grads", [False, True])
+@pytest.mark.parametrize("n,t", [(37, 16), (37, 48), (5, 64), (37, 52)])
+def test_layout_backward_matches_oracle(cuda_device, name, abi, final_grads, n, t):
+    abi_name, fixed, nout = abi
+    print(f"layout {name} backward {abi_name} final_grads={final_grads} n={n} t={t}", flush=True)
+    cpu, dev = _case(n, t, 4, seed=3 * t + n, device=cuda_device)
+    ext = _ext()
+    with layout(name):
+        _, _, _, bm, bc = _forward(ext, dev, fixed, 8)
+        grads = _backward(ext, abi_name, fixed, nout, dev, bm, bc, 8, final_grads)
+        torch.cuda.synchronize()
+    assert len(grads) == nout
+    ref = _fixed_dynamics(cpu) if fixed else cpu
+    f64 = {k: x.double() for k, x in ref.items()}
+    _, _, _, eg = O.diagonal_grads(f64["k"], f64["v"], f64["q"], f64["d"], f64["p"], f64["r"], f64["m0"], f64["c0"],
+                                   f64["gy"], f64["gmf"] if final_grads else None,
+                                   f64["gcf"] if final_grads else None)
+    for i in range(nout):
+        if fixed and NAMES[i] in ("gd", "gp", "gr"):
+            assert torch.count_nonzero(grads[i]) == 0, f"{NAMES[i]} must be zero for fixed dynamics"
+            continue
+        close(grads[i], eg[i], NAMES[i])
+
+
+@pytest.mark.parametrize("name", list(LAYOUTS))
+@pytest.mark.parametrize("abi", ABIS, ids=[a[0] for a in ABIS])
+def test_layout_floor_active(cuda_device, name, abi):
+    """The innovation floor on a share of the tokens, and the strict gate at tokens exactly at it."""
+    abi_name, fixed, nout = abi
+    print(f"layout {name} floor {abi_name}", flush=True)
+    cpu, dev, floor = _floor_case(29, 64, 4, seed=41, device=cuda_device, fixed=fixed)
+    with layout(name):
+        outs, grads = _run_abi(_ext(), abi_name, fixed, nout, dev, 8, floor)
+    _check(cpu, fixed, floor, outs, grads, nout)
+
+
+@pytest.mark.parametrize("fixed", [False, True])
+def test_row_layout_chunk_invariance_and_symmetry(cuda_device, fixed):
+    """Row forward: outputs bitwise identical for every chunk, checkpoint c = state before token c * chunk,
+    and the covariance bitwise symmetric."""
+    print(f"row chunk invariance fixed={fixed}", flush=True)
+    _, dev = _case(9, 80, 4, seed=5, device=cuda_device)
+    ext = _ext()
+    with layout("row"):
+        runs = {c: _forward(ext, dev, fixed, c) for c in (1, 4, 8, 16, 80, 200)}
+        torch.cuda.synchronize()
+    for c, out in runs.items():
+        for a, b in zip(out[:3], runs[8][:3]):
+            assert torch.equal(a, b), f"chunk {c} changes the recurrence"
+    for c in (4, 8, 16, 80):
+        assert torch.equal(runs[c][3], runs[1][3][:, ::c]), f"bmean layout chunk {c}"
+        assert torch.equal(runs[c][4], runs[1][4][:, ::c]), f"bcov layout chunk {c}"
+    cT, bc = runs[8][2], runs[1][4]
+    assert torch.equal(cT, cT.transpose(-1, -2))
+    assert torch.equal(bc, bc.transpose(-1, -2))
+
+
+def test_layouts_at_many_sequences(cuda_device):
+    """4099 sequences (a partial last wave): both layouts match the oracle on every output and gradient, and
+    the default limits route this size to the row kernels (whose results differ from the rotated ones in the
+    last bits)."""
+    print("layouts n=4099 t=64", flush=True)
+    cpu, dev = _case(4099, 64, 4, seed=9, device=cuda_device)
+    ext = _ext()
+    res = {}
+    for name in ("row", "quad", None):
+        with (layout(name) if name else contextlib.nullcontext()):
+            y, mT, cT, bm, bc = _forward(ext, dev, False, 8)
+            grads = _backward(ext, "backward_chunked", False, 8, dev, bm, bc, 8, True)
+            torch.cuda.synchronize()
+        res[name] = [y, mT, cT, *grads]
+    f64 = {k: x.double() for k, x in cpu.items()}
+    ey, em, ec, eg = O.diagonal_grads(f64["k"], f64["v"], f64["q"], f64["d"], f64["p"], f64["r"], f64["m0"],
+                                      f64["c0"], f64["gy"], f64["gmf"], f64["gcf"])
+    labels = ["y", "mean_T", "cov_T"] + NAMES
+    for name in ("row", "quad"):
+        for lab, a, e in zip(labels, res[name], [ey, em, ec, *eg]):
+            close(a, e, f"{name} {lab}")
+    for lab, a, b in zip(labels, res[None], res["row"]):
+        assert torch.equal(a, b), f"default dispatch at N = 4099 is not the row layout ({lab})"
+    assert not torch.equal(res["row"][0], res["quad"][0])
