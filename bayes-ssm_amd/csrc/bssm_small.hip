@@ -16,6 +16,14 @@
 // Lane (i, j) of a sequence's row (i = row bits 3:2, j = bits 1:0) holds
 //   P[i][j]                    (the covariance, bitwise symmetric)
 //   M[j][2i], M[j][2i + 1]     (the mean, transposed: row j of M)
+// The forward keeps the lane's mean pair in its own order instead,
+// (M[j][c], M[j][c ^ 1]) with c = 2i + (j & 1): the lanes j, j ^ 1 of a quad
+// then hold the same column pair in opposite order, so a sum over j of a
+// column is an exchange between them and one quad step that leaves each lane
+// its own column's sum (and its partner the other's): a reduce-scatter in
+// place of two all-reduces for the readout and the innovations.  In the
+// backward the extra exchange lengthens the chained reverse; it keeps the
+// record order.
 // Sums over j are quad all-reduces (xor 1, xor 2); sums over i are
 // "column" all-reduces over the row: the pair (i, i ^ 1) through the half-row
 // mirror and a quad reversal, then the pairs through a row rotation by 8.
@@ -120,7 +128,7 @@ __device__ __forceinline__ void put_tile(const Stage& x, float* tl, int s, int c
 // Token inputs of lane (i, j).
 struct Tok {
   float ki, kj, di, dj, qj, p, r;
-  v2f v;  // v[2i], v[2i + 1]
+  v2f v;  // v[2i], v[2i + 1]; in the forward's own order v[c], v[c ^ 1]
 };
 
 template <bool FIXED>
@@ -128,7 +136,9 @@ __device__ __forceinline__ void read_tok(Tok& x, const float* b, int tt, int i, 
   x.ki = b[Tile::K + 4 * tt + i];
   x.kj = b[Tile::K + 4 * tt + j];
   x.qj = b[Tile::Q + 4 * tt + j];
-  x.v = *reinterpret_cast<const v2f*>(b + Tile::V + 8 * tt + 2 * i);
+  const int co = 2 * i + (j & 1);
+  x.v[0] = b[Tile::V + 8 * tt + co];
+  x.v[1] = b[Tile::V + 8 * tt + (co ^ 1)];
   if constexpr (FIXED) {
     x.di = x.dj = kFixedDecay;
     x.p = kFixedProcess;
@@ -146,11 +156,29 @@ struct Bel {
   float P, M0, M1;
 };
 
+// The lane's mean pair between record order (columns 2i, 2i + 1) and its own
+// order (c, c ^ 1); the same swap both ways.
+__device__ __forceinline__ v2f own_order(v2f m, bool odd) {
+  v2f r;
+  r[0] = odd ? m[1] : m[0];
+  r[1] = odd ? m[0] : m[1];
+  return r;
+}
+
+// Sum over the quad of the lane's own column, given the lane's terms of its
+// own column (x0) and of the other (x1).
+__device__ __forceinline__ float own_sum(float x0, float x1) {
+  const float t = x0 + dpp<kXor1>(x1);
+  return t + dpp<kXor2>(t);
+}
+
 struct StepOut {
   float ui, uj, s;
   v2f e;
 };
 
+// OWN: mean pair, values and innovations in the lane's own order.
+template <bool OWN>
 __device__ __forceinline__ void forward_step(Bel& b, const Tok& x, float delta, float floor, StepOut& o) {
   const float wki = x.di * x.ki, wkj = x.dj * x.kj;
   const float zi = quad_sum(b.P * wkj);  // (P (d * k))_i
@@ -158,9 +186,17 @@ __device__ __forceinline__ void forward_step(Bel& b, const Tok& x, float delta, 
   const float ui = fmaf(x.di, zi, x.p * x.ki), uj = fmaf(x.dj, zj, x.p * x.kj);
   const float s = quad_sum(x.kj * uj) + x.r;
   const float beta = fast_rcp(fmaxf(s, floor));
-  // Innovations of the lane's columns 2i, 2i + 1: e = v - sum_j M[j][c] d_j k_j.
-  const float e0 = x.v[0] - quad_sum(b.M0 * wkj);
-  const float e1 = x.v[1] - quad_sum(b.M1 * wkj);
+  // Innovations of the lane's two columns: e = v - sum_j M[j][.] d_j k_j (in
+  // own order the other column's sum is the partner's own).
+  float e0, e1;
+  if constexpr (OWN) {
+    const float so = own_sum(b.M0 * wkj, b.M1 * wkj);
+    e0 = x.v[0] - so;
+    e1 = x.v[1] - dpp<kXor1>(so);
+  } else {
+    e0 = x.v[0] - quad_sum(b.M0 * wkj);
+    e1 = x.v[1] - quad_sum(b.M1 * wkj);
+  }
   const float bu = beta * uj;
   b.M0 = fmaf(bu, e0, x.dj * b.M0);
   b.M1 = fmaf(bu, e1, x.dj * b.M1);
@@ -173,13 +209,9 @@ __device__ __forceinline__ void forward_step(Bel& b, const Tok& x, float delta, 
   o.e[1] = e1;
 }
 
-// Readouts of the lane's columns after the token: y_c = sum_j M[j][c] q_j.
-__device__ __forceinline__ v2f readout(const Bel& b, float qj) {
-  v2f y;
-  y[0] = quad_sum(b.M0 * qj);
-  y[1] = quad_sum(b.M1 * qj);
-  return y;
-}
+// Readout of the lane's own column after the token (own order):
+// y_c = sum_j M[j][c] q_j.
+__device__ __forceinline__ float readout(const Bel& b, float qj) { return own_sum(b.M0 * qj, b.M1 * qj); }
 
 // Belief record offsets of lane (i, j) (bytes within one sequence's record).
 __device__ __forceinline__ uint32_t mean_off(int i, int j) { return static_cast<uint32_t>(j * 32 + i * 8); }
@@ -190,6 +222,8 @@ __global__ __launch_bounds__(kWave) void forward_kernel(FwdArgs a) {
   __shared__ float tile[Tile::SIZE];
   const int lane = threadIdx.x;
   const int s = lane >> 4, c = lane & 15, i = c >> 2, j = c & 3;
+  const int co = 2 * i + (j & 1);  // the lane's own value column
+  const bool odd = (j & 1) != 0;
   const float delta = i == j ? 1.f : 0.f;
   const int64_t n0 = static_cast<int64_t>(blockIdx.x) * SPW;
   const int64_t T = a.t;
@@ -214,16 +248,16 @@ __global__ __launch_bounds__(kWave) void forward_kernel(FwdArgs a) {
   const Rsrc rcT = make_rsrc(a.cT + n0 * 16, valid * 64u);
   // Lane offsets in the belief records: the state tensors hold one record per
   // sequence, the checkpoints nb + 1.
-  const uint32_t mo = static_cast<uint32_t>(s) * 128u + mean_off(i, j), co = static_cast<uint32_t>(s) * 64u + cov_off(i, j);
+  const uint32_t mo = static_cast<uint32_t>(s) * 128u + mean_off(i, j), cvo = static_cast<uint32_t>(s) * 64u + cov_off(i, j);
   const uint32_t cmo = static_cast<uint32_t>(s) * nbp * 128u + mean_off(i, j),
                  cco = static_cast<uint32_t>(s) * nbp * 64u + cov_off(i, j);
 
   Bel b;
   {
-    const v2f m = r4::ld64(rm0, mo, 0);
+    const v2f m = own_order(r4::ld64(rm0, mo, 0), odd);
     b.M0 = m[0];
     b.M1 = m[1];
-    b.P = r4::ld32(rc0, co, 0);
+    b.P = r4::ld32(rc0, cvo, 0);
   }
   // The initial belief has landed before the loop (a load pending at the
   // loop header would make every iteration wait for all outstanding loads).
@@ -232,7 +266,7 @@ __global__ __launch_bounds__(kWave) void forward_kernel(FwdArgs a) {
     v2f m;
     m[0] = b.M0;
     m[1] = b.M1;
-    r4::st64(rbm, m, cmo, rec * 128u);
+    r4::st64(rbm, own_order(m, odd), cmo, rec * 128u);
     r4::st32(rbc, b.P, cco, rec * 64u);
   };
   store_ckpt(0);
@@ -276,9 +310,8 @@ __global__ __launch_bounds__(kWave) void forward_kernel(FwdArgs a) {
           const int tt = 8 * h + u;
           if (u + 1 < 8) read_tok<FIXED>(nxt, mine, tt + 1, i, j);
           StepOut o;
-          forward_step(b, cur, delta, a.floor, o);
-          const v2f y = readout(b, cur.qj);
-          mine[Tile::V + 8 * tt + 2 * i + (j & 1)] = (j & 1) ? y[1] : y[0];
+          forward_step<true>(b, cur, delta, a.floor, o);
+          mine[Tile::V + 8 * tt + co] = readout(b, cur.qj);
           cur = nxt;
         }
       }
@@ -291,9 +324,8 @@ __global__ __launch_bounds__(kWave) void forward_kernel(FwdArgs a) {
         Tok cur;
         read_tok<FIXED>(cur, mine, tt, i, j);
         StepOut o;
-        forward_step(b, cur, delta, a.floor, o);
-        const v2f y = readout(b, cur.qj);
-        mine[Tile::V + 8 * tt + 2 * i + (j & 1)] = (j & 1) ? y[1] : y[0];
+        forward_step<true>(b, cur, delta, a.floor, o);
+        mine[Tile::V + 8 * tt + co] = readout(b, cur.qj);
       }
     }
   }
@@ -311,8 +343,8 @@ __global__ __launch_bounds__(kWave) void forward_kernel(FwdArgs a) {
   v2f m;
   m[0] = b.M0;
   m[1] = b.M1;
-  r4::st64(rmT, m, mo, 0);
-  r4::st32(rcT, b.P, co, 0);
+  r4::st64(rmT, own_order(m, odd), mo, 0);
+  r4::st32(rcT, b.P, cvo, 0);
   store_ckpt(static_cast<uint32_t>(a.nb));
 }
 
@@ -598,7 +630,7 @@ __global__ __launch_bounds__(kWave) void backward_kernel(BwdArgs a) {
         h[u].M0 = b.M0;
         h[u].M1 = b.M1;
         StepOut o;
-        forward_step(b, cur, delta, a.floor, o);
+        forward_step<false>(b, cur, delta, a.floor, o);
         h[u].ui = o.ui;
         h[u].uj = o.uj;
         h[u].s = o.s;
