@@ -348,6 +348,314 @@ __global__ __launch_bounds__(kWave) void forward_kernel(FwdArgs a) {
   store_ckpt(static_cast<uint32_t>(a.nb));
 }
 
+// ------------------------------------------------- two-wave forward (split)
+// At the smallest sequence counts the single-wave kernels leave SIMDs idle,
+// and each wave's time is its instruction stream.  The step splits into a
+// covariance half and a mean half that only talk one way: the mean update
+// needs the gain column bu_j = beta u_j, nothing else of the covariance
+// chain.  Here a workgroup of two waves holds the same 4 sequences: wave 0
+// runs the covariance chain (u, s, beta, P) one 16-token tile ahead and
+// leaves bu in LDS; wave 1 runs the innovations, the mean update and the
+// readouts of the tile before, from those bu.  One barrier per tile; each
+// wave stages and stores its own streams (wave 0: k, d, p, r, the covariance
+// checkpoints and final covariance; wave 1: v, q, the readouts, the mean
+// checkpoints and final mean).  The operations are those of forward_step, in
+// the same order, so the results are bitwise those of forward_kernel.
+struct STile {
+  // Input slot per sequence (3 slots: tile t + 1 lands while tiles t and
+  // t - 1 are read): k, d, q [TT][4], v [TT][8], p, r [TT].
+  static constexpr int K = 0, D = 64, Q = 128, V = 192, P = 320, R = 336, SEQ = 360, SLOT = SPW * SEQ;
+  // Readouts of a tile (2 slots) and the gain columns bu (2 slots).
+  static constexpr int YSEQ = 136, YSLOT = SPW * YSEQ, BSEQ = 72, BSLOT = SPW * BSEQ;
+  static constexpr int IN = 0, Y = 3 * SLOT, BU = Y + 2 * YSLOT, SIZE = BU + 2 * BSLOT;
+};
+
+// Covariance half of forward_step: P advanced, the gain column bu_j returned.
+__device__ __forceinline__ float cov_step(float& P, float ki, float kj, float di, float dj, float p, float r,
+                                          float delta, float floor) {
+  const float wki = di * ki, wkj = dj * kj;
+  const float zi = quad_sum(P * wkj);
+  const float zj = col_sum(P * wki);
+  const float ui = fmaf(di, zi, p * ki), uj = fmaf(dj, zj, p * kj);
+  const float s = quad_sum(kj * uj) + r;
+  const float beta = fast_rcp(fmaxf(s, floor));
+  const float bu = beta * uj;
+  const float dp = fmaf(p, delta, (di * dj) * P);
+  P = fmaf(-beta, ui * uj, dp);
+  return bu;
+}
+
+// Mean half (own order) and the readout of the lane's own column.
+__device__ __forceinline__ float mean_step(float& M0, float& M1, float kj, float dj, float qj, v2f v, float bu) {
+  const float wkj = dj * kj;
+  const float so = own_sum(M0 * wkj, M1 * wkj);
+  const float e0 = v[0] - so;
+  const float e1 = v[1] - dpp<kXor1>(so);
+  M0 = fmaf(bu, e0, dj * M0);
+  M1 = fmaf(bu, e1, dj * M1);
+  return own_sum(M0 * qj, M1 * qj);
+}
+
+template <bool FIXED>
+__global__ __launch_bounds__(2 * kWave) void forward_split_kernel(FwdArgs a) {
+  __shared__ float lds[STile::SIZE];
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int s = lane >> 4, c = lane & 15, i = c >> 2, j = c & 3;
+  const int co = 2 * i + (j & 1);
+  const bool odd = (j & 1) != 0;
+  const float delta = i == j ? 1.f : 0.f;
+  const int64_t n0 = static_cast<int64_t>(blockIdx.x) * SPW;
+  const int64_t T = a.t;
+  const uint32_t valid = static_cast<uint32_t>((a.n - n0) < SPW ? (a.n - n0) : SPW);
+  const uint32_t row4 = static_cast<uint32_t>(T) * 16u, row8 = static_cast<uint32_t>(T) * 32u,
+                 row1 = static_cast<uint32_t>(T) * 4u;
+  const uint32_t nbp = static_cast<uint32_t>(a.nb + 1);
+  const int64_t ntiles = (T + TT - 1) / TT;
+  auto in_slot = [&](int64_t t) __attribute__((always_inline)) {
+    return lds + STile::IN + static_cast<int>(t % 3) * STile::SLOT + s * STile::SEQ;
+  };
+  auto y_slot = [&](int64_t t) __attribute__((always_inline)) {
+    return lds + STile::Y + static_cast<int>(t & 1) * STile::YSLOT + s * STile::YSEQ;
+  };
+  auto bu_slot = [&](int64_t t) __attribute__((always_inline)) {
+    return lds + STile::BU + static_cast<int>(t & 1) * STile::BSLOT + s * STile::BSEQ;
+  };
+  auto tile_len = [&](int64_t t) __attribute__((always_inline)) {
+    return static_cast<int>((T - t * TT) < TT ? (T - t * TT) : TT);
+  };
+
+  if (wave == 0) {
+    // ---- covariance wave
+    const Rsrc rk = make_rsrc(a.k + n0 * T * 4, valid * row4);
+    const Rsrc rd = make_rsrc(FIXED ? a.k : a.d + n0 * T * 4, FIXED ? 0u : valid * row4);
+    const Rsrc rp = make_rsrc(FIXED ? a.k : a.p + n0 * T, FIXED ? 0u : valid * row1);
+    const Rsrc rr = make_rsrc(FIXED ? a.k : a.r + n0 * T, FIXED ? 0u : valid * row1);
+    const Rsrc rbc = make_rsrc(a.bc + n0 * nbp * 16, valid * nbp * 64u);
+    const Rsrc rc0 = make_rsrc(a.c0 + n0 * 16, valid * 64u);
+    const Rsrc rcT = make_rsrc(a.cT + n0 * 16, valid * 64u);
+    const uint32_t cvo = static_cast<uint32_t>(s) * 64u + cov_off(i, j);
+    const uint32_t cco = static_cast<uint32_t>(s) * nbp * 64u + cov_off(i, j);
+    v4f sk, sd, sp, sr;
+    auto load = [&](int64_t t) __attribute__((always_inline)) {
+      const uint32_t t0 = static_cast<uint32_t>(t * TT);
+      const uint32_t o4 = static_cast<uint32_t>(s) * row4 + (t0 + c) * 16u;
+      sk = r4::ld128<true>(rk, o4);
+      if constexpr (!FIXED) {
+        sd = r4::ld128<true>(rd, o4);
+        const uint32_t o1 = c < 4 ? static_cast<uint32_t>(s) * row1 + t0 * 4u + c * 16u : kOob;
+        sp = r4::ld128<false>(rp, o1);
+        sr = r4::ld128<false>(rr, o1);
+      }
+    };
+    auto put = [&](int64_t t) __attribute__((always_inline)) {
+      float* b = in_slot(t);
+      *reinterpret_cast<v4f*>(b + STile::K + 4 * c) = sk;
+      if constexpr (!FIXED) {
+        *reinterpret_cast<v4f*>(b + STile::D + 4 * c) = sd;
+        if (c < 4) {
+          *reinterpret_cast<v4f*>(b + STile::P + 4 * c) = sp;
+          *reinterpret_cast<v4f*>(b + STile::R + 4 * c) = sr;
+        }
+      }
+    };
+    float P = r4::ld32(rc0, cvo, 0);
+    r4::vm_wait<0>();
+    r4::st32(rbc, P, cco, 0);
+    if (ntiles > 0) {
+      load(0);
+      r4::vm_wait<0>();
+      put(0);
+      if (ntiles > 1) load(1);
+    }
+    __syncthreads();
+    int64_t next_ckpt = a.chunk;
+    uint32_t ckpt = 1;
+    for (int64_t it = 0; it <= ntiles; ++it) {
+      if (it + 1 < ntiles) {
+        r4::vm_wait<0>();
+        put(it + 1);
+        if (it + 2 < ntiles) load(it + 2);
+      }
+      if (it < ntiles) {
+        const float* b = in_slot(it);
+        float* bu = bu_slot(it);
+        const int64_t t0 = it * TT;
+        const int len = tile_len(it);
+        // Each token's inputs are read one token ahead, before the previous
+        // token's bu write (LDS reads may not pass that write).
+        struct In {
+          float ki, kj, di, dj, p, r;
+        };
+        auto read = [&](In& x, int tt) __attribute__((always_inline)) {
+          x.ki = b[STile::K + 4 * tt + i];
+          x.kj = b[STile::K + 4 * tt + j];
+          x.di = FIXED ? kFixedDecay : b[STile::D + 4 * tt + i];
+          x.dj = FIXED ? kFixedDecay : b[STile::D + 4 * tt + j];
+          x.p = FIXED ? kFixedProcess : b[STile::P + tt];
+          x.r = FIXED ? kFixedObservation : b[STile::R + tt];
+        };
+        auto ckpt_at = [&](int64_t t) __attribute__((always_inline)) {
+          if (t == next_ckpt) {
+            r4::st32(rbc, P, cco, ckpt * 64u);
+            ++ckpt;
+            next_ckpt += a.chunk;
+          }
+        };
+        In cur, nxt;
+        read(cur, 0);
+        if (len == TT && a.chunk % 8 == 0) {
+          // Checkpoints can only fall on tokens 0 and 8 of a full tile: two
+          // straight 8-token runs.
+#pragma unroll
+          for (int h = 0; h < TT / 8; ++h) {
+            ckpt_at(t0 + 8 * h);
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+              const int tt = 8 * h + u;
+              if (tt + 1 < TT) read(nxt, tt + 1);
+              bu[4 * tt + j] = cov_step(P, cur.ki, cur.kj, cur.di, cur.dj, cur.p, cur.r, delta, a.floor);
+              cur = nxt;
+            }
+          }
+        } else {
+          for (int tt = 0; tt < len; ++tt) {
+            if (tt + 1 < len) read(nxt, tt + 1);
+            ckpt_at(t0 + tt);
+            bu[4 * tt + j] = cov_step(P, cur.ki, cur.kj, cur.di, cur.dj, cur.p, cur.r, delta, a.floor);
+            cur = nxt;
+          }
+        }
+      }
+      __syncthreads();
+    }
+    r4::st32(rcT, P, cvo, 0);
+    r4::st32(rbc, P, cco, static_cast<uint32_t>(a.nb) * 64u);
+  } else {
+    // ---- mean wave
+    const Rsrc rq = make_rsrc(a.q + n0 * T * 4, valid * row4);
+    const Rsrc rv = make_rsrc(a.v + n0 * T * 8, valid * row8);
+    const Rsrc ry = make_rsrc(a.y + n0 * T * 8, valid * row8);
+    const Rsrc rbm = make_rsrc(a.bm + n0 * nbp * 32, valid * nbp * 128u);
+    const Rsrc rm0 = make_rsrc(a.m0 + n0 * 32, valid * 128u);
+    const Rsrc rmT = make_rsrc(a.mT + n0 * 32, valid * 128u);
+    const uint32_t mo = static_cast<uint32_t>(s) * 128u + mean_off(i, j);
+    const uint32_t cmo = static_cast<uint32_t>(s) * nbp * 128u + mean_off(i, j);
+    v4f sq, sv0, sv1;
+    auto load = [&](int64_t t) __attribute__((always_inline)) {
+      const uint32_t t0 = static_cast<uint32_t>(t * TT);
+      sq = r4::ld128<true>(rq, static_cast<uint32_t>(s) * row4 + (t0 + c) * 16u);
+      const uint32_t o8 = static_cast<uint32_t>(s) * row8 + t0 * 32u + c * 16u;
+      sv0 = r4::ld128<true>(rv, o8);
+      sv1 = r4::ld128<true>(rv, o8 + 256u);
+    };
+    auto put = [&](int64_t t) __attribute__((always_inline)) {
+      float* b = in_slot(t);
+      *reinterpret_cast<v4f*>(b + STile::Q + 4 * c) = sq;
+      *reinterpret_cast<v4f*>(b + STile::V + 4 * c) = sv0;
+      *reinterpret_cast<v4f*>(b + STile::V + 64 + 4 * c) = sv1;
+    };
+    // Readouts of tile t leave its y slot as whole pieces (valid tokens only).
+    auto store_y = [&](int64_t t) __attribute__((always_inline)) {
+      const float* yb = y_slot(t);
+      const v4f y0 = *reinterpret_cast<const v4f*>(yb + 4 * c);
+      const v4f y1 = *reinterpret_cast<const v4f*>(yb + 64 + 4 * c);
+      const int len = tile_len(t);
+      const uint32_t o8 = static_cast<uint32_t>(s) * row8 + static_cast<uint32_t>(t * TT) * 32u + c * 16u;
+      r4::st128<r4::kNtStore>(ry, y0, (c >> 1) < len ? o8 : kOob, 0);
+      r4::st128<r4::kNtStore>(ry, y1, ((c + 16) >> 1) < len ? o8 + 256u : kOob, 0);
+    };
+    float M0, M1;
+    {
+      const v2f m = own_order(r4::ld64(rm0, mo, 0), odd);
+      M0 = m[0];
+      M1 = m[1];
+    }
+    r4::vm_wait<0>();
+    auto store_ckpt = [&](uint32_t rec) __attribute__((always_inline)) {
+      v2f m;
+      m[0] = M0;
+      m[1] = M1;
+      r4::st64(rbm, own_order(m, odd), cmo, rec * 128u);
+    };
+    store_ckpt(0);
+    if (ntiles > 0) {
+      load(0);
+      r4::vm_wait<0>();
+      put(0);
+      if (ntiles > 1) load(1);
+    }
+    __syncthreads();
+    int64_t next_ckpt = a.chunk;
+    uint32_t ckpt = 1;
+    for (int64_t it = 0; it <= ntiles; ++it) {
+      if (it >= 2) store_y(it - 2);
+      if (it + 1 < ntiles) {
+        r4::vm_wait<0>();
+        put(it + 1);
+        if (it + 2 < ntiles) load(it + 2);
+      }
+      if (it >= 1) {
+        const int64_t tl = it - 1;
+        const float* b = in_slot(tl);
+        const float* bu = bu_slot(tl);
+        float* yb = y_slot(tl);
+        const int64_t t0 = tl * TT;
+        const int len = tile_len(tl);
+        struct In {
+          float kj, dj, qj, bu;
+          v2f v;
+        };
+        auto read = [&](In& x, int tt) __attribute__((always_inline)) {
+          x.kj = b[STile::K + 4 * tt + j];
+          x.dj = FIXED ? kFixedDecay : b[STile::D + 4 * tt + j];
+          x.qj = b[STile::Q + 4 * tt + j];
+          x.v[0] = b[STile::V + 8 * tt + co];
+          x.v[1] = b[STile::V + 8 * tt + (co ^ 1)];
+          x.bu = bu[4 * tt + j];
+        };
+        auto ckpt_at = [&](int64_t t) __attribute__((always_inline)) {
+          if (t == next_ckpt) {
+            store_ckpt(ckpt++);
+            next_ckpt += a.chunk;
+          }
+        };
+        In cur, nxt;
+        read(cur, 0);
+        if (len == TT && a.chunk % 8 == 0) {
+#pragma unroll
+          for (int h = 0; h < TT / 8; ++h) {
+            ckpt_at(t0 + 8 * h);
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+              const int tt = 8 * h + u;
+              if (tt + 1 < TT) read(nxt, tt + 1);
+              yb[8 * tt + co] = mean_step(M0, M1, cur.kj, cur.dj, cur.qj, cur.v, cur.bu);
+              cur = nxt;
+            }
+          }
+        } else {
+          for (int tt = 0; tt < len; ++tt) {
+            if (tt + 1 < len) read(nxt, tt + 1);
+            ckpt_at(t0 + tt);
+            yb[8 * tt + co] = mean_step(M0, M1, cur.kj, cur.dj, cur.qj, cur.v, cur.bu);
+            cur = nxt;
+          }
+        }
+      }
+      __syncthreads();
+    }
+    if (ntiles >= 1) {
+      r4::lds_wait();
+      store_y(ntiles - 1);
+    }
+    v2f m;
+    m[0] = M0;
+    m[1] = M1;
+    r4::st64(rmT, own_order(m, odd), mo, 0);
+    store_ckpt(static_cast<uint32_t>(a.nb));
+  }
+}
+
 // ----------------------------------------------------------------- backward
 // A 16-token tile holds two checkpoint chunks of 8 tokens (T a multiple of
 // 16); tiles are visited last to first, and in each the chunk 2J + 1 before
@@ -722,8 +1030,9 @@ __global__ __launch_bounds__(kWave) void backward_kernel(BwdArgs a) {
 namespace {
 // Measured crossovers against the rotated-layout kernels (T = 512): the row
 // forward is faster up to about 24576 sequences and level beyond, the row
-// backward up to about 8192.
-std::atomic<int64_t> g_small_limit[2] = {{24576}, {8192}};
+// backward up to about 8192; the two-wave forward beats the one-wave row
+// forward up to 2048 (by 15 % at 1024 and below, 4 % at 2048).
+std::atomic<int64_t> g_small_limit[3] = {{24576}, {8192}, {2048}};
 }  // namespace
 
 int64_t small_batch_limit(int direction) { return g_small_limit[direction].load(std::memory_order_relaxed); }
@@ -734,6 +1043,11 @@ int64_t set_small_batch_limit(int direction, int64_t limit) {
 hipError_t launch_forward_small(bool fixed, const FwdArgs& a, hipStream_t stream) {
   const int64_t blocks = (a.n + sn::SPW - 1) / sn::SPW;
   if (blocks == 0) return hipSuccess;
+  if (a.n <= small_batch_limit(2)) {
+    if (fixed) hipLaunchKernelGGL(sn::forward_split_kernel<true>, dim3(static_cast<unsigned>(blocks)), dim3(2 * kWave), 0, stream, a);
+    else hipLaunchKernelGGL(sn::forward_split_kernel<false>, dim3(static_cast<unsigned>(blocks)), dim3(2 * kWave), 0, stream, a);
+    return hipGetLastError();
+  }
   if (fixed) hipLaunchKernelGGL(sn::forward_kernel<true>, dim3(static_cast<unsigned>(blocks)), dim3(kWave), 0, stream, a);
   else hipLaunchKernelGGL(sn::forward_kernel<false>, dim3(static_cast<unsigned>(blocks)), dim3(kWave), 0, stream, a);
   return hipGetLastError();

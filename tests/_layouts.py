@@ -11,19 +11,19 @@ from __future__ import annotations
 import contextlib
 
 BIG = 1 << 40
-LAYOUTS = {"row": (BIG, BIG), "quad": (0, 0)}
+# Limits (forward row, backward row, forward two-wave) per layout.
+LAYOUTS = {"row": (BIG, BIG, 0), "split": (BIG, BIG, BIG), "quad": (0, 0, 0)}
 
 
 @contextlib.contextmanager
 def layout(name):
-    """Force the D4 kernels of one layout (forward and backward), restoring the limits after."""
+    """Force the D4 kernels of one layout, restoring the limits after."""
     from bayes_ssm import _hip
 
     lib = _hip.load()
-    fwd, bwd = LAYOUTS[name]
-    old = (lib.bssm_small_batch_limit(0, fwd), lib.bssm_small_batch_limit(1, bwd))
+    old = [lib.bssm_small_batch_limit(d, v) for d, v in enumerate(LAYOUTS[name])]
     try:
         yield
     finally:
-        lib.bssm_small_batch_limit(0, old[0])
-        lib.bssm_small_batch_limit(1, old[1])
+        for d, v in enumerate(old):
+            lib.bssm_small_batch_limit(d, v)

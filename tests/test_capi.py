@@ -199,16 +199,17 @@ def test_conv_backward_noalloc_rejects_sizes_beyond_its_scratch(lib):
 
 def test_small_batch_limits_read_set_restore(lib):
     """Forward and backward limits of the row-per-sequence D4 kernels: defaults, set, read, restore."""
-    fwd, bwd = lib.bssm_small_batch_limit(0, -1), lib.bssm_small_batch_limit(1, -1)
-    assert (fwd, bwd) == (24576, 8192)
+    old = [lib.bssm_small_batch_limit(d, -1) for d in range(3)]
+    assert old == [24576, 8192, 2048]
     try:
-        assert lib.bssm_small_batch_limit(0, 7) == fwd
+        assert lib.bssm_small_batch_limit(0, 7) == old[0]
         assert lib.bssm_small_batch_limit(0, -1) == 7
-        assert lib.bssm_small_batch_limit(1, -1) == bwd, "directions are independent"
-        assert lib.bssm_small_batch_limit(1, 0) == bwd
+        assert lib.bssm_small_batch_limit(1, -1) == old[1], "directions are independent"
+        assert lib.bssm_small_batch_limit(1, 0) == old[1]
         assert lib.bssm_small_batch_limit(1, -1) == 0
+        assert lib.bssm_small_batch_limit(2, 3) == old[2] and lib.bssm_small_batch_limit(2, -1) == 3
     finally:
-        lib.bssm_small_batch_limit(0, fwd)
-        lib.bssm_small_batch_limit(1, bwd)
-    assert lib.bssm_small_batch_limit(2, 5) == -1 and lib.bssm_small_batch_limit(-1, -1) == -1
-    assert (lib.bssm_small_batch_limit(0, -1), lib.bssm_small_batch_limit(1, -1)) == (fwd, bwd)
+        for d in range(3):
+            lib.bssm_small_batch_limit(d, old[d])
+    assert lib.bssm_small_batch_limit(3, 5) == -1 and lib.bssm_small_batch_limit(-1, -1) == -1
+    assert [lib.bssm_small_batch_limit(d, -1) for d in range(3)] == old

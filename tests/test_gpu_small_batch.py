@@ -112,14 +112,15 @@ def test_layout_floor_active(cuda_device, name, abi):
     _check(cpu, fixed, floor, outs, grads, nout)
 
 
+@pytest.mark.parametrize("name", ["row", "split"])
 @pytest.mark.parametrize("fixed", [False, True])
-def test_row_layout_chunk_invariance_and_symmetry(cuda_device, fixed):
-    """Row forward: outputs bitwise identical for every chunk, checkpoint c = state before token c * chunk,
-    and the covariance bitwise symmetric."""
-    print(f"row chunk invariance fixed={fixed}", flush=True)
+def test_row_layout_chunk_invariance_and_symmetry(cuda_device, name, fixed):
+    """Row forward (one or two waves): outputs bitwise identical for every chunk, checkpoint c = state before
+    token c * chunk, and the covariance bitwise symmetric."""
+    print(f"{name} chunk invariance fixed={fixed}", flush=True)
     _, dev = _case(9, 80, 4, seed=5, device=cuda_device)
     ext = _ext()
-    with layout("row"):
+    with layout(name):
         runs = {c: _forward(ext, dev, fixed, c) for c in (1, 4, 8, 16, 80, 200)}
         torch.cuda.synchronize()
     for c, out in runs.items():
@@ -131,6 +132,23 @@ def test_row_layout_chunk_invariance_and_symmetry(cuda_device, fixed):
     cT, bc = runs[8][2], runs[1][4]
     assert torch.equal(cT, cT.transpose(-1, -2))
     assert torch.equal(bc, bc.transpose(-1, -2))
+
+
+@pytest.mark.parametrize("fixed", [False, True])
+@pytest.mark.parametrize("chunk", [1, 8, 13])
+@pytest.mark.parametrize("n,t", [(1, 16), (7, 20), (37, 52), (9, 64), (6, 4), (33, 512)])
+def test_two_wave_forward_is_bitwise_the_one_wave_forward(cuda_device, fixed, chunk, n, t):
+    """The covariance / mean split over two waves performs the one-wave kernel's operations in its order."""
+    print(f"two-wave forward n={n} t={t} chunk={chunk} fixed={fixed}", flush=True)
+    _, dev = _case(n, t, 4, seed=n + t + chunk, device=cuda_device)
+    ext = _ext()
+    outs = {}
+    for name in ("row", "split"):
+        with layout(name):
+            outs[name] = [x.clone() for x in _forward(ext, dev, fixed, chunk)]
+            torch.cuda.synchronize()
+    for lab, a, b in zip(("y", "mean_T", "cov_T", "bmean", "bcov"), outs["row"], outs["split"]):
+        assert torch.equal(a, b), lab
 
 
 def test_layouts_at_many_sequences(cuda_device):
