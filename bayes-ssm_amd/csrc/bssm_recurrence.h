@@ -87,7 +87,8 @@ hipError_t launch_forward_r4(bool fixed, const FwdArgs& a, hipStream_t stream);
 hipError_t launch_backward_r4(bool fixed, bool dyn, const BwdArgs& a, hipStream_t stream);
 // Row-per-sequence D = 4 kernels for small sequence counts (bssm_small.hip):
 // used for float32 streams when the rotated-layout kernels apply and n is at
-// most small_batch_limit(0) (forward) or small_batch_limit(1) (backward).
+// most small_batch_limit(0) (forward) or small_batch_limit(1) (backward);
+// as two / three waves per 4 sequences up to small_batch_limit(2) / (3).
 hipError_t launch_forward_small(bool fixed, const FwdArgs& a, hipStream_t stream);
 // The backward needs T a multiple of 16 and the kRot4Chunk checkpoint chunk.
 hipError_t launch_backward_small(bool fixed, bool dyn, const BwdArgs& a, hipStream_t stream);

@@ -1024,6 +1024,442 @@ __global__ __launch_bounds__(kWave) void backward_kernel(BwdArgs a) {
   }
 }
 
+// ---------------------------------------------- three-wave backward (split)
+// A wave issues at most one instruction every ~6 cycles, so at the smallest
+// batches (one wave per SIMD or fewer) each wave's time is its instruction
+// count.  The backward splits three ways: the mean adjoint (gM, ge = dL/dv,
+// dL/dq) needs of the covariance side only u and beta; the covariance
+// adjoint (S, gu, dL/dk, dL/dd, dL/dp, dL/dr) needs of the mean side only
+// three column sums per token, a = gM e, A = M_prev ge and sum_c gb M_prev;
+// and the covariance replay feeds both.  A workgroup of three waves holds the
+// same 4 sequences and walks the checkpoint chunks (8 tokens) last to first
+// in steps, one barrier per step.  With x the chunk's position in that
+// order, at step x:
+//   wave 0 replays the covariance of chunk x (its records P, u, s go to
+//          LDS, and u_j and beta for the mean wave);
+//   wave 2 replays and reverses the mean of chunk x - 1 (from u and beta)
+//          and leaves the three sums;
+//   wave 1 reverses the covariance of chunk x - 2 (from the records and the
+//          sums).
+// Wave 0 stages k, d, p, r and the covariance checkpoints one step ahead,
+// wave 2 q, v, gy and the mean checkpoints; wave 1 stores gk, gd, gp, gr and
+// wave 2 gq, gv.  The operations are those of backward_kernel in its order:
+// the results are bitwise the same.
+struct SBTile {
+  static constexpr int CH = 8;
+  // Chunk slot per sequence (5 slots: a chunk is staged one step before its
+  // replay and its last gradients leave three steps after): k, d, q [CH][4],
+  // v, gy [CH][8], p, r [CH].
+  static constexpr int K = 0, D = 32, Q = 64, V = 96, GY = 160, P = 224, R = 232, SEQ = 264, SLOT = SPW * SEQ;
+  static constexpr int NSLOT = 5;
+  // Covariance to mean (2 slots): u_j [CH][4], beta [CH].
+  static constexpr int USEQ = 40, USLOT = SPW * USEQ;
+  // Mean to covariance (2 slots): a, A, sum_c gb M_prev [CH][4] each.
+  static constexpr int ASEQ = 104, ASLOT = SPW * ASEQ;
+  // Covariance records (3 slots: written at step x, read at step x + 2):
+  // [CH][64 lanes] of (P, u_i, u_j, s).
+  static constexpr int RSLOT = CH * kWave * 4;
+  static constexpr int IN = 0, U = NSLOT * SLOT, A = U + 2 * USLOT, REC = A + 2 * ASLOT, SIZE = REC + 3 * RSLOT;
+};
+
+// Covariance record of one replayed token (one 16-byte LDS word per lane).
+struct PRec {
+  float P, ui, uj, s;
+};
+__device__ __forceinline__ v4f pack(const PRec& r) { return v4f{r.P, r.ui, r.uj, r.s}; }
+__device__ __forceinline__ PRec unpack(v4f x) { return PRec{x[0], x[1], x[2], x[3]}; }
+// Mean record of one replayed token (record order, as backward_kernel).
+struct MRec {
+  float M0, M1;
+  v2f e;
+};
+
+// Mean half of the reverse (reverse_step's gM, ge, a, A, C, gb, Bv).
+template <bool DYN>
+__device__ __forceinline__ void mean_reverse(float kj, float dj, float qj, v2f gy, const MRec& h, float uj, float beta,
+                                             float Mn0, float Mn1, float& gM0, float& gM1, float& a_out,
+                                             float& A_out, float& Bv_out, float& gq, float& ge0, float& ge1) {
+  gM0 = fmaf(qj, gy[0], gM0);
+  gM1 = fmaf(qj, gy[1], gM1);
+  ge0 = beta * quad_sum(gM0 * uj);
+  ge1 = beta * quad_sum(gM1 * uj);
+  a_out = col_sum(fmaf(gM1, h.e[1], gM0 * h.e[0]));
+  A_out = col_sum(fmaf(h.M1, ge1, h.M0 * ge0));
+  gq = col_sum(fmaf(Mn1, gy[1], Mn0 * gy[0]));
+  const float gb0 = fmaf(-kj, ge0, gM0), gb1 = fmaf(-kj, ge1, gM1);
+  gM0 = gb0 * dj;
+  gM1 = gb1 * dj;
+  Bv_out = DYN ? col_sum(fmaf(gb1, h.M1, gb0 * h.M0)) : 0.f;
+}
+
+// Covariance half of the reverse (reverse_step's w, z, gs, gu, gk, H, gd,
+// gp, S).
+template <bool DYN>
+__device__ __forceinline__ void cov_reverse(float ki, float kj, float di, float dj, float p, const PRec& h, float a,
+                                            float A, float Bv, float& S, float floor, float delta, bool i1, bool i2,
+                                            ROut& o) {
+  const float beta = fast_rcp(fmaxf(h.s, floor));
+  const float w = col_sum(S * h.ui);
+  const float z = quad_sum(h.uj * (a - w));
+  const float gs = h.s > floor ? -z * beta * beta : 0.f;
+  const float guj = fmaf(beta, fmaf(-2.f, w, a), gs * kj);
+  const float gui = diag_pick(guj, i1, i2);
+  const float dd = di * dj;
+  const float pb = fmaf(p, delta, dd * h.P);
+  o.gk = fmaf(-dj, A, gs * h.uj) + col_sum(pb * gui);
+  const float H = fmaf(0.5f, gui * kj + guj * ki, S);
+  if constexpr (DYN) {
+    o.gd = fmaf(2.f, col_sum((H * di) * h.P), Bv);
+    o.gp = col_sum(quad_sum(delta * H));
+  } else {
+    o.gd = o.gp = 0.f;
+  }
+  S = H * dd;
+  o.gs = gs;
+  o.gui = gui;
+  o.guj = guj;
+}
+
+template <bool FIXED, bool DYN>
+__global__ __launch_bounds__(3 * kWave) void backward_split_kernel(BwdArgs a) {
+  __shared__ float lds[SBTile::SIZE];
+  constexpr int CH = SBTile::CH;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int s = lane >> 4, c = lane & 15, i = c >> 2, j = c & 3;
+  const float delta = i == j ? 1.f : 0.f;
+  const int64_t n0 = static_cast<int64_t>(blockIdx.x) * SPW;
+  const int64_t T = a.t;
+  const uint32_t valid = static_cast<uint32_t>((a.n - n0) < SPW ? (a.n - n0) : SPW);
+  const uint32_t row4 = static_cast<uint32_t>(T) * 16u, row8 = static_cast<uint32_t>(T) * 32u,
+                 row1 = static_cast<uint32_t>(T) * 4u;
+  const uint32_t nbp = static_cast<uint32_t>(a.nb + 1);
+  const int64_t nb = T / CH;  // chunks; position x is chunk nb - 1 - x
+  // Ring slots of step position x (T / 8 positions: 32-bit arithmetic).
+  auto slot = [&](int64_t x) __attribute__((always_inline)) {
+    return lds + SBTile::IN + static_cast<int>(static_cast<uint32_t>(x) % SBTile::NSLOT) * SBTile::SLOT +
+           s * SBTile::SEQ;
+  };
+  auto uslot = [&](int64_t x) __attribute__((always_inline)) {
+    return lds + SBTile::U + static_cast<int>(x & 1) * SBTile::USLOT + s * SBTile::USEQ;
+  };
+  auto aslot = [&](int64_t x) __attribute__((always_inline)) {
+    return lds + SBTile::A + static_cast<int>(x & 1) * SBTile::ASLOT + s * SBTile::ASEQ;
+  };
+  auto rslot = [&](int64_t x) __attribute__((always_inline)) {
+    return lds + SBTile::REC + static_cast<int>(static_cast<uint32_t>(x) % 3u) * SBTile::RSLOT + 4 * lane;
+  };
+  // First token of chunk position x.
+  auto tok0 = [&](int64_t x) __attribute__((always_inline)) { return static_cast<uint32_t>((nb - 1 - x) * CH); };
+  const uint32_t o4 = static_cast<uint32_t>(s) * row4 + static_cast<uint32_t>(c) * 16u;  // + t0 * 16
+  const uint32_t o8 = static_cast<uint32_t>(s) * row8 + static_cast<uint32_t>(c) * 16u;  // + t0 * 32
+  const uint32_t o1 = static_cast<uint32_t>(s) * row1 + static_cast<uint32_t>(c) * 16u;  // + t0 * 4
+
+  if (wave == 0) {
+    // ------------------------------------------------ covariance replay wave
+    const Rsrc rk = make_rsrc(a.k + n0 * T * 4, valid * row4);
+    const Rsrc rd = make_rsrc(FIXED ? a.k : a.d + n0 * T * 4, FIXED ? 0u : valid * row4);
+    const Rsrc rp = make_rsrc(FIXED ? a.k : a.p + n0 * T, FIXED ? 0u : valid * row1);
+    const Rsrc rr = make_rsrc(FIXED ? a.k : a.r + n0 * T, FIXED ? 0u : valid * row1);
+    const Rsrc rbc = make_rsrc(a.bc + n0 * nbp * 16, valid * nbp * 64u);
+    const uint32_t cco = static_cast<uint32_t>(s) * nbp * 64u + cov_off(i, j);
+    v4f sk, sd, sp, sr;
+    auto load = [&](int64_t x) __attribute__((always_inline)) {
+      const uint32_t t0 = tok0(x);
+      const uint32_t q4 = c < CH ? o4 + t0 * 16u : kOob;
+      sk = r4::ld128<true>(rk, q4);
+      if constexpr (!FIXED) {
+        sd = r4::ld128<true>(rd, q4);
+        const uint32_t q1 = c < CH / 4 ? o1 + t0 * 4u : kOob;
+        sp = r4::ld128<false>(rp, q1);
+        sr = r4::ld128<false>(rr, q1);
+      }
+    };
+    auto put = [&](int64_t x) __attribute__((always_inline)) {
+      float* b = slot(x);
+      if (c < CH) {
+        *reinterpret_cast<v4f*>(b + SBTile::K + 4 * c) = sk;
+        if constexpr (!FIXED) *reinterpret_cast<v4f*>(b + SBTile::D + 4 * c) = sd;
+      }
+      if constexpr (!FIXED) {
+        if (c < CH / 4) {
+          *reinterpret_cast<v4f*>(b + SBTile::P + 4 * c) = sp;
+          *reinterpret_cast<v4f*>(b + SBTile::R + 4 * c) = sr;
+        }
+      }
+    };
+    auto ckpt = [&](int64_t x) __attribute__((always_inline)) {
+      return r4::ld32(rbc, cco + static_cast<uint32_t>(nb - 1 - x) * 64u, 0);
+    };
+    float Pload = 0.f;
+    if (nb > 0) {
+      load(0);
+      Pload = ckpt(0);
+      r4::vm_wait<0>();
+      put(0);
+      if (nb > 1) load(1);
+    }
+    __syncthreads();
+    struct In {
+      float ki, kj, di, dj, p, r;
+    };
+    for (int64_t x = 0; x <= nb + 1; ++x) {
+      r4::vm_wait<0>();
+      float Pc = Pload;
+      if (x + 1 < nb) {
+        Pload = ckpt(x + 1);
+        put(x + 1);
+        if (x + 2 < nb) load(x + 2);
+      }
+      if (x < nb) {
+        const float* pb = slot(x);
+        float* ub = uslot(x);
+        float* rec = rslot(x);
+        auto read = [&](In& y, int k) __attribute__((always_inline)) {
+          y.ki = pb[SBTile::K + 4 * k + i];
+          y.kj = pb[SBTile::K + 4 * k + j];
+          y.di = FIXED ? kFixedDecay : pb[SBTile::D + 4 * k + i];
+          y.dj = FIXED ? kFixedDecay : pb[SBTile::D + 4 * k + j];
+          y.p = FIXED ? kFixedProcess : pb[SBTile::P + k];
+          y.r = FIXED ? kFixedObservation : pb[SBTile::R + k];
+        };
+        In cur, nxt;
+        read(cur, 0);
+#pragma unroll
+        for (int k = 0; k < CH; ++k) {
+          if (k + 1 < CH) read(nxt, k + 1);
+          // forward_step's covariance operations, in its order.
+          PRec h;
+          h.P = Pc;
+          const float wki = cur.di * cur.ki, wkj = cur.dj * cur.kj;
+          const float zi = quad_sum(Pc * wkj);
+          const float zj = col_sum(Pc * wki);
+          const float ui = fmaf(cur.di, zi, cur.p * cur.ki), uj = fmaf(cur.dj, zj, cur.p * cur.kj);
+          const float sv = quad_sum(cur.kj * uj) + cur.r;
+          const float beta = fast_rcp(fmaxf(sv, a.floor));
+          const float dp = fmaf(cur.p, delta, (cur.di * cur.dj) * Pc);
+          Pc = fmaf(-beta, ui * uj, dp);
+          h.ui = ui;
+          h.uj = uj;
+          h.s = sv;
+          *reinterpret_cast<v4f*>(rec + k * 4 * kWave) = pack(h);
+          ub[4 * k + j] = uj;
+          ub[4 * CH + k] = beta;
+          cur = nxt;
+        }
+      }
+      __syncthreads();
+    }
+  } else if (wave == 1) {
+    // ------------------------------------------------ covariance reverse wave
+    const bool i1 = (i & 1) != 0, i2 = (i & 2) != 0;
+    const Rsrc rgk = make_rsrc(a.gk + n0 * T * 4, valid * row4);
+    const Rsrc rgd = make_rsrc(a.gd ? a.gd + n0 * T * 4 : a.gk, a.gd ? valid * row4 : 0u);
+    const Rsrc rgp = make_rsrc(a.gp ? a.gp + n0 * T : a.gk, a.gp ? valid * row1 : 0u);
+    const Rsrc rgr = make_rsrc(a.gr ? a.gr + n0 * T : a.gk, a.gr ? valid * row1 : 0u);
+    const uint32_t cvo = static_cast<uint32_t>(s) * 64u + cov_off(i, j);
+    float S;
+    {
+      const bool has_c = a.gcf != nullptr;
+      const Rsrc rgc = make_rsrc(has_c ? a.gcf + n0 * 16 : a.k, has_c ? valid * 64u : 0u);
+      const uint32_t tr = static_cast<uint32_t>(s) * 64u + cov_off(j, i);
+      S = 0.5f * (r4::ld32(rgc, cvo, 0) + r4::ld32(rgc, tr, 0));
+    }
+    // Gradients of chunk position x leave its slot (requested outputs; zero
+    // gd / gp / gr without dynamics gradients).
+    auto store = [&](int64_t x) __attribute__((always_inline)) {
+      const float* b = slot(x);
+      const uint32_t t0 = tok0(x);
+      const uint32_t q4 = c < CH ? o4 + t0 * 16u : kOob, q1 = c < CH / 4 ? o1 + t0 * 4u : kOob;
+      const v4f zero = v4f{0.f, 0.f, 0.f, 0.f};
+      const int c8 = c & (CH - 1), c2 = c & (CH / 4 - 1);
+      r4::st128<r4::kNtStore>(rgk, *reinterpret_cast<const v4f*>(b + SBTile::K + 4 * c8), q4, 0);
+      if (a.gd) r4::st128<r4::kNtStore>(rgd, DYN ? *reinterpret_cast<const v4f*>(b + SBTile::D + 4 * c8) : zero, q4, 0);
+      if (a.gp) r4::st128(rgp, DYN ? *reinterpret_cast<const v4f*>(b + SBTile::P + 4 * c2) : zero, q1, 0);
+      if (a.gr) r4::st128(rgr, DYN ? *reinterpret_cast<const v4f*>(b + SBTile::R + 4 * c2) : zero, q1, 0);
+    };
+    First first = {0.f, 0.f, 0.f, 0.f, 0.f};
+    __syncthreads();
+    struct In {
+      float ki, kj, di, dj, p, a, A, Bv;
+      v4f rec;
+    };
+    for (int64_t x = 0; x <= nb + 1; ++x) {
+      r4::vm_wait<0>();
+      if (x >= 3) store(x - 3);
+      if (x >= 2) {
+        float* rb = slot(x - 2);
+        const float* ab = aslot(x - 2);
+        const float* rec = rslot(x - 2);
+        auto read = [&](In& y, int u) __attribute__((always_inline)) {
+          y.ki = rb[SBTile::K + 4 * u + i];
+          y.kj = rb[SBTile::K + 4 * u + j];
+          y.di = FIXED ? kFixedDecay : rb[SBTile::D + 4 * u + i];
+          y.dj = FIXED ? kFixedDecay : rb[SBTile::D + 4 * u + j];
+          y.p = FIXED ? kFixedProcess : rb[SBTile::P + u];
+          y.a = ab[4 * u + j];
+          y.A = ab[4 * CH + 4 * u + j];
+          y.Bv = DYN ? ab[8 * CH + 4 * u + j] : 0.f;
+          y.rec = *reinterpret_cast<const v4f*>(rec + u * 4 * kWave);
+        };
+        In cur, nxt;
+        read(cur, CH - 1);
+#pragma unroll
+        for (int u = CH - 1; u >= 0; --u) {
+          if (u > 0) read(nxt, u - 1);
+          ROut o;
+          cov_reverse<DYN>(cur.ki, cur.kj, cur.di, cur.dj, cur.p, unpack(cur.rec), cur.a, cur.A, cur.Bv, S, a.floor,
+                           delta, i1, i2, o);
+          rb[SBTile::K + 4 * u + j] = o.gk;
+          if constexpr (DYN) {
+            rb[SBTile::D + 4 * u + j] = o.gd;
+            rb[SBTile::P + u] = o.gp;
+            rb[SBTile::R + u] = o.gs;
+          }
+          if (u == 0) {
+            first.gui = o.gui;
+            first.guj = o.guj;
+            first.ki = cur.ki;
+            first.kj = cur.kj;
+            first.dd = cur.di * cur.dj;
+          }
+          cur = nxt;
+        }
+      }
+      __syncthreads();
+    }
+    if (nb > 0) {
+      r4::lds_wait();
+      store(nb - 1);
+    }
+    if (a.gc0) {
+      const Rsrc rgc0 = make_rsrc(a.gc0 + n0 * 16, valid * 64u);
+      const float asym = 0.5f * (first.gui * first.kj - first.guj * first.ki);
+      r4::st32(rgc0, fmaf(asym, first.dd, S), cvo, 0);
+    }
+  } else {
+    // ------------------------------------------------ mean wave
+    const Rsrc rq = make_rsrc(a.q + n0 * T * 4, valid * row4);
+    const Rsrc rv = make_rsrc(a.v + n0 * T * 8, valid * row8);
+    const Rsrc rgy = make_rsrc(a.gy + n0 * T * 8, valid * row8);
+    const Rsrc rgq = make_rsrc(a.gq + n0 * T * 4, valid * row4);
+    const Rsrc rgv = make_rsrc(a.gv + n0 * T * 8, valid * row8);
+    const Rsrc rbm = make_rsrc(a.bm + n0 * nbp * 32, valid * nbp * 128u);
+    const uint32_t mo = static_cast<uint32_t>(s) * 128u + mean_off(i, j);
+    const uint32_t cmo = static_cast<uint32_t>(s) * nbp * 128u + mean_off(i, j);
+    float gM0, gM1;
+    {
+      const bool has_m = a.gmf != nullptr;
+      const Rsrc rgm = make_rsrc(has_m ? a.gmf + n0 * 32 : a.k, has_m ? valid * 128u : 0u);
+      const v2f m = r4::ld64(rgm, mo, 0);
+      gM0 = m[0];
+      gM1 = m[1];
+    }
+    v4f sq, sv, sg;
+    auto load = [&](int64_t x) __attribute__((always_inline)) {
+      const uint32_t t0 = tok0(x);
+      sq = r4::ld128<true>(rq, c < CH ? o4 + t0 * 16u : kOob);
+      sv = r4::ld128<true>(rv, o8 + t0 * 32u);
+      sg = r4::ld128<true>(rgy, o8 + t0 * 32u);
+    };
+    auto put = [&](int64_t x) __attribute__((always_inline)) {
+      float* b = slot(x);
+      if (c < CH) *reinterpret_cast<v4f*>(b + SBTile::Q + 4 * c) = sq;
+      *reinterpret_cast<v4f*>(b + SBTile::V + 4 * c) = sv;
+      *reinterpret_cast<v4f*>(b + SBTile::GY + 4 * c) = sg;
+    };
+    auto store = [&](int64_t x) __attribute__((always_inline)) {
+      const float* b = slot(x);
+      const uint32_t t0 = tok0(x);
+      r4::st128<r4::kNtStore>(rgq, *reinterpret_cast<const v4f*>(b + SBTile::Q + 4 * (c & (CH - 1))),
+                              c < CH ? o4 + t0 * 16u : kOob, 0);
+      r4::st128<r4::kNtStore>(rgv, *reinterpret_cast<const v4f*>(b + SBTile::V + 4 * c), o8 + t0 * 32u, 0);
+    };
+    auto ckpt = [&](int64_t x) __attribute__((always_inline)) {
+      return r4::ld64(rbm, cmo + static_cast<uint32_t>(nb - 1 - x) * 128u, 0);
+    };
+    v2f Mload = v2f{0.f, 0.f};
+    if (nb > 0) {
+      load(0);
+      r4::vm_wait<0>();
+      put(0);
+      if (nb > 1) load(1);
+    }
+    __syncthreads();
+    for (int64_t x = 0; x <= nb + 1; ++x) {
+      r4::vm_wait<0>();
+      const v2f Mc = Mload;  // checkpoint of chunk x - 1
+      if (x < nb) Mload = ckpt(x);
+      if (x + 1 < nb) {
+        put(x + 1);
+        if (x + 2 < nb) load(x + 2);
+      }
+      if (x >= 2) store(x - 2);
+      if (x >= 1 && x <= nb) {
+        float* b = slot(x - 1);
+        const float* ub = uslot(x - 1);
+        float* ab = aslot(x - 1);
+        MRec h[CH];
+        float M0 = Mc[0], M1 = Mc[1];
+#pragma unroll
+        for (int k = 0; k < CH; ++k) {
+          const float kj = b[SBTile::K + 4 * k + j];
+          const float dj = FIXED ? kFixedDecay : b[SBTile::D + 4 * k + j];
+          const v2f v = *reinterpret_cast<const v2f*>(b + SBTile::V + 8 * k + 2 * i);
+          const float uj = ub[4 * k + j], beta = ub[4 * CH + k];
+          // forward_step's mean operations, in its order.
+          h[k].M0 = M0;
+          h[k].M1 = M1;
+          const float wkj = dj * kj;
+          const float e0 = v[0] - quad_sum(M0 * wkj);
+          const float e1 = v[1] - quad_sum(M1 * wkj);
+          const float bu = beta * uj;
+          M0 = fmaf(bu, e0, dj * M0);
+          M1 = fmaf(bu, e1, dj * M1);
+          h[k].e[0] = e0;
+          h[k].e[1] = e1;
+        }
+        struct In {
+          float kj, dj, qj, uj, beta;
+          v2f gy;
+        };
+        auto read = [&](In& y, int u) __attribute__((always_inline)) {
+          y.kj = b[SBTile::K + 4 * u + j];
+          y.dj = FIXED ? kFixedDecay : b[SBTile::D + 4 * u + j];
+          y.qj = b[SBTile::Q + 4 * u + j];
+          y.gy = *reinterpret_cast<const v2f*>(b + SBTile::GY + 8 * u + 2 * i);
+          y.uj = ub[4 * u + j];
+          y.beta = ub[4 * CH + u];
+        };
+        In cur, nxt;
+        read(cur, CH - 1);
+#pragma unroll
+        for (int u = CH - 1; u >= 0; --u) {
+          if (u > 0) read(nxt, u - 1);
+          const float Mn0 = u < CH - 1 ? h[u < CH - 1 ? u + 1 : u].M0 : M0;
+          const float Mn1 = u < CH - 1 ? h[u < CH - 1 ? u + 1 : u].M1 : M1;
+          float av, Av, Bv, gq, ge0, ge1;
+          mean_reverse<DYN>(cur.kj, cur.dj, cur.qj, cur.gy, h[u], cur.uj, cur.beta, Mn0, Mn1, gM0, gM1, av, Av, Bv,
+                            gq, ge0, ge1);
+          ab[4 * u + j] = av;
+          ab[4 * CH + 4 * u + j] = Av;
+          if constexpr (DYN) ab[8 * CH + 4 * u + j] = Bv;
+          b[SBTile::Q + 4 * u + j] = gq;
+          b[SBTile::V + 8 * u + 2 * i + (j & 1)] = (j & 1) ? ge1 : ge0;
+          cur = nxt;
+        }
+      }
+      __syncthreads();
+    }
+    if (a.gm0) {
+      const Rsrc rgm0 = make_rsrc(a.gm0 + n0 * 32, valid * 128u);
+      v2f m;
+      m[0] = gM0;
+      m[1] = gM1;
+      r4::st64(rgm0, m, mo, 0);
+    }
+  }
+}
+
 }  // namespace
 }  // namespace sn
 
@@ -1031,8 +1467,10 @@ namespace {
 // Measured crossovers against the rotated-layout kernels (T = 512): the row
 // forward is faster up to about 24576 sequences and level beyond, the row
 // backward up to about 8192; the two-wave forward beats the one-wave row
-// forward up to 2048 (by 15 % at 1024 and below, 4 % at 2048).
-std::atomic<int64_t> g_small_limit[3] = {{24576}, {8192}, {2048}};
+// forward up to 2048 (by 15 % at 1024 and below, 4 % at 2048), the
+// three-wave backward the one-wave one up to 2048 (30 %, 12 %; beyond that
+// its 50 KB of LDS per workgroup leave too few workgroups per CU).
+std::atomic<int64_t> g_small_limit[4] = {{24576}, {8192}, {2048}, {2048}};
 }  // namespace
 
 int64_t small_batch_limit(int direction) { return g_small_limit[direction].load(std::memory_order_relaxed); }
@@ -1057,6 +1495,13 @@ hipError_t launch_backward_small(bool fixed, bool dyn, const BwdArgs& a, hipStre
   if (a.t % sn::TT != 0 || a.chunk != kRot4Chunk) return hipErrorInvalidValue;
   const int64_t blocks = (a.n + sn::SPW - 1) / sn::SPW;
   if (blocks == 0) return hipSuccess;
+  if (a.n <= small_batch_limit(3)) {
+    const dim3 grid(static_cast<unsigned>(blocks)), block(3 * kWave);
+    if (fixed) hipLaunchKernelGGL((sn::backward_split_kernel<true, false>), grid, block, 0, stream, a);
+    else if (dyn) hipLaunchKernelGGL((sn::backward_split_kernel<false, true>), grid, block, 0, stream, a);
+    else hipLaunchKernelGGL((sn::backward_split_kernel<false, false>), grid, block, 0, stream, a);
+    return hipGetLastError();
+  }
   const dim3 grid(static_cast<unsigned>(blocks)), block(kWave);
   if (fixed) hipLaunchKernelGGL((sn::backward_kernel<true, false>), grid, block, 0, stream, a);
   else if (dyn) hipLaunchKernelGGL((sn::backward_kernel<false, true>), grid, block, 0, stream, a);

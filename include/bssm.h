@@ -437,12 +437,14 @@ int bssm_rotation_checkpoint(int key_dim);
  * instruction stream, which the row layout shortens; at large N the row
  * layout's extra lane work costs more than it saves (the backward first).
  * The backward also needs T a multiple of 16 and the preferred checkpoint
- * chunk.  Direction 2: the largest N (within direction 0's) for which the row
- * forward runs as two waves per 4 sequences, covariance and mean halves on
- * separate SIMDs (bitwise the one-wave results).  Defaults: 24576, 8192,
- * 2048, the measured crossovers.  Sets the limit when limit >= 0 and returns
- * the previous one; limit < 0 only reads it; -1 for any other direction.
- * Results of the two layouts agree within float32 rounding, not bitwise.  No
+ * chunk.  Direction 2 (3): the largest N, within direction 0's (1's), for
+ * which the row forward (backward) runs as two (three) waves per 4
+ * sequences, the covariance and mean halves (the covariance replay, the
+ * covariance reverse and the mean) on separate SIMDs, bitwise the one-wave
+ * results.  Defaults: 24576, 8192, 2048, 2048, the measured crossovers.
+ * Sets the limit when limit >= 0 and returns the previous one; limit < 0
+ * only reads it; -1 for any other direction.  Results of the row and
+ * rotated layouts agree within float32 rounding, not bitwise.  No
  * counterpart in the reference (a tuning switch of this library). */
 int64_t bssm_small_batch_limit(int direction, int64_t limit);
 

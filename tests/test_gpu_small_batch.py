@@ -151,6 +151,26 @@ def test_two_wave_forward_is_bitwise_the_one_wave_forward(cuda_device, fixed, ch
         assert torch.equal(a, b), lab
 
 
+@pytest.mark.parametrize("abi", ABIS, ids=[a[0] for a in ABIS])
+@pytest.mark.parametrize("final_grads", [False, True])
+@pytest.mark.parametrize("n,t", [(1, 16), (7, 32), (37, 48), (9, 64), (33, 512)])
+def test_three_wave_backward_is_bitwise_the_one_wave_backward(cuda_device, abi, final_grads, n, t):
+    """The covariance replay / covariance reverse / mean split over three waves performs the one-wave
+    kernel's operations in its order."""
+    abi_name, fixed, nout = abi
+    print(f"three-wave backward {abi_name} final_grads={final_grads} n={n} t={t}", flush=True)
+    _, dev = _case(n, t, 4, seed=5 * n + t, device=cuda_device)
+    ext = _ext()
+    outs = {}
+    for name in ("row", "split"):
+        with layout(name):
+            _, _, _, bm, bc = _forward(ext, dev, fixed, 8)
+            outs[name] = [g.clone() for g in _backward(ext, abi_name, fixed, nout, dev, bm, bc, 8, final_grads)]
+            torch.cuda.synchronize()
+    for lab, a, b in zip(NAMES, outs["row"], outs["split"]):
+        assert torch.equal(a, b), lab
+
+
 def test_layouts_at_many_sequences(cuda_device):
     """4099 sequences (a partial last wave): both layouts match the oracle on every output and gradient, and
     the default limits route this size to the row kernels (whose results differ from the rotated ones in the
