@@ -73,11 +73,11 @@ __device__ __forceinline__ float col_sum(float x) {
   return x + dpp<kRowRor8>(x);          // + rows i ^ 2, i ^ 3
 }
 
-// LDS tile of one wave: per sequence (padded stride so the 4 sequences'
-// reads of one token fall in different banks) k, d, q [TT][4], v / y [TT][8],
-// p, r [TT].
+// LDS tile of one wave: per sequence k, d, q [TT][4], v / y [TT][8], p, r
+// [TT], at a stride of 8 banks (mod 32), so that the 4 sequences' reads of
+// one token (4 key or 8 value words each) fall in different banks.
 struct Tile {
-  static constexpr int K = 0, D = 64, Q = 128, V = 192, P = 320, R = 336, SEQ = 356, SIZE = SPW * SEQ;
+  static constexpr int K = 0, D = 64, Q = 128, V = 192, P = 320, R = 336, SEQ = 360, SIZE = SPW * SEQ;
 };
 
 // Register staging of one tile: lane (s, c) (s = lane >> 4, c = lane & 15)
