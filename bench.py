@@ -41,6 +41,31 @@ def algorithmic_bytes(d: int, m: int) -> tuple[int, int]:
     return (inputs + m) * 4, (2 * inputs + m) * 4
 
 
+def dispatched_kernels(d: int, m: int, n: int, t: int, interval: int) -> tuple[str, str]:
+    """Names of the forward and backward kernels the C ABI launches for float32 streams of this shape
+    (D4M8: the row-per-sequence kernels up to the library's small-batch limits, else the rotated layout)."""
+    from bayes_ssm import _hip
+
+    if (d, m) != (4, 8) or t % 4:
+        return f"bssm forward kernel (D{d}M{m})", f"bssm backward kernel (D{d}M{m})"
+    lib = _hip.load()
+    lim = [lib.bssm_small_batch_limit(k, -1) for k in range(4)]
+    if n <= lim[2]:
+        fwd = "bssm::sn::forward_split_kernel<false> (row layout, two waves per 4 sequences)"
+    elif n <= lim[0]:
+        fwd = "bssm::sn::forward_kernel<false> (row layout, 16 lanes per sequence)"
+    else:
+        fwd = "bssm::r4::forward_kernel<false, 0> (rotated layout, 4 lanes per sequence)"
+    row_bwd = t % 16 == 0 and interval == _hip.preferred_checkpoint(4)
+    if row_bwd and n <= lim[3]:
+        bwd = "bssm::sn::backward_split_kernel<false, true> (row layout, three waves per 4 sequences)"
+    elif row_bwd and n <= lim[1]:
+        bwd = "bssm::sn::backward_kernel<false, true> (row layout, 16 lanes per sequence)"
+    else:
+        bwd = "bssm::r4::backward_kernel<false, true> (rotated layout, 4 lanes per sequence)"
+    return fwd, bwd
+
+
 def make_workload(b, t, h, d, m, device, seed=0, kqv_dtype=None):
     """Synthetic config-3 inputs; k, v, q are bf16 values (kept as tensors of kqv_dtype when given:
     bfloat16, or a float8 dtype, rounded from the bf16 values)."""
@@ -597,6 +622,7 @@ def main() -> int:
             if line.startswith("backward_bytes_per_launch ="):
                 traffic = int(line.split("=")[1])
 
+    fwd_kernel, bwd_kernel = dispatched_kernels(d, m, n, t, interval)
     result = {
         "metric": METRIC,
         "value": tokens_per_s,
@@ -619,7 +645,7 @@ def main() -> int:
         },
         "roofline": {
             "bound": "hbm",
-            "kernel": "bssm::r4::backward_kernel<false, true> (checkpoint replay + reverse, D4M8)",
+            "kernel": bwd_kernel + ", checkpoint replay + reverse",
             "achieved": bwd_gbs,
             "peak": HBM_PEAK / 1e9,
             "unit": "GB/s",
@@ -628,8 +654,8 @@ def main() -> int:
             "bytes_per_launch": bwd_b * units,
             "avg_launch_ms": bwd_ms,
         },
-        "roofline_forward": {"achieved": fwd_gbs, "frac": fwd_gbs * 1e9 / HBM_PEAK, "avg_launch_ms": fwd_ms,
-                             "bytes_per_launch": fwd_b * units},
+        "roofline_forward": {"kernel": fwd_kernel, "achieved": fwd_gbs, "frac": fwd_gbs * 1e9 / HBM_PEAK,
+                             "avg_launch_ms": fwd_ms, "bytes_per_launch": fwd_b * units},
         "roofline_step_frac": step_frac,
         "measured_copy_gbs": copy_gbs,
         "device": torch.cuda.get_device_name(device),
