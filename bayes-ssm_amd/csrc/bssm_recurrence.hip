@@ -25,6 +25,8 @@
 // only commutative products (d_i*d_j, u_i*u_j), so the owner of row i and the
 // owner of row j compute identical values.
 
+#include <algorithm>
+
 #include "bssm_step.h"
 
 namespace bssm {
@@ -488,8 +490,11 @@ int preferred_checkpoint(int key_dim) {
 }
 
 hipError_t launch_forward(int key_dim, bool fixed, const FwdArgs& a, hipStream_t stream) {
-  if (key_dim == 4 && a.rot4 && a.in_fmt == kInF32 && a.n <= small_batch_limit(0))
-    return launch_forward_small(fixed, a, stream);
+  // bf16 / float8 streams take the row kernels only within the two-wave
+  // limit: above it their rotated-layout forward is the faster one.
+  const int64_t row_limit = a.in_fmt == kInF32 ? small_batch_limit(0)
+                                               : std::min(small_batch_limit(0), small_batch_limit(2));
+  if (key_dim == 4 && a.rot4 && a.n <= row_limit) return launch_forward_small(fixed, a, stream);
   if (key_dim == 4 && a.rot4) return launch_forward_r4(fixed, a, stream);
   if (key_dim == 1 && d1_forward_ok(a)) return launch_forward_d1(fixed, a, stream);
   if (key_dim == 2 && d2_forward_ok(a)) return launch_forward_d2(fixed, a, stream);

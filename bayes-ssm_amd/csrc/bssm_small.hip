@@ -58,6 +58,7 @@ constexpr int kQuadRev = quad_perm(3, 2, 1, 0);
 using r4::Rsrc;
 using r4::make_rsrc;
 using r4::kOob;
+using r4::v4u;
 typedef float v2f __attribute__((ext_vector_type(2)));
 
 // Sum over the 4 lanes j of the quad; identical bits in the quad.
@@ -88,20 +89,84 @@ struct Stage {
   v4f k, d, q, v0, v1, p, r;
 };
 
+// Keys, queries and values may arrive as bfloat16 or float8 (F, an InFmt);
+// they are widened exactly to float32 as they are written to LDS, so the
+// kernels' arithmetic is the float32 one on the widened values.  Bytes per
+// token of a 4-value stream (k, q) in format F; a value row takes twice that.
+template <int F>
+constexpr uint32_t kq_bytes() {
+  return F == kInF32 ? 16u : F == kInBf16 ? 8u : 4u;
+}
+// Lanes (of a sequence's 16) that move a 16-token tile's 16-byte pieces of a
+// 4-value stream; a value stream takes twice as many pieces (float32: two per
+// lane, c and c + 16).
+template <int F>
+constexpr int kq_lanes() {
+  return static_cast<int>(TT * kq_bytes<F>() / 16u);
+}
+
+// Raw 16-byte pieces of the tile at token t0 of sequence s (lane c) of the
+// 4-value stream r, and of the value stream rv (two pieces for float32).
+template <int F>
+__device__ __forceinline__ v4f load_kq(Rsrc r, uint32_t row, int s, int c, uint32_t t0) {
+  const uint32_t off = static_cast<uint32_t>(s) * row + t0 * kq_bytes<F>() + static_cast<uint32_t>(c) * 16u;
+  return r4::ld128<true>(r, c < kq_lanes<F>() ? off : kOob);
+}
+template <int F>
+__device__ __forceinline__ void load_v(v4f& v0, v4f& v1, Rsrc rv, uint32_t row, int s, int c, uint32_t t0) {
+  const uint32_t off = static_cast<uint32_t>(s) * row + t0 * 2u * kq_bytes<F>() + static_cast<uint32_t>(c) * 16u;
+  v0 = r4::ld128<true>(rv, c < 2 * kq_lanes<F>() ? off : kOob);
+  if constexpr (F == kInF32) v1 = r4::ld128<true>(rv, off + 256u);
+}
+// Widen and write those pieces into a tile region of TT x 4 (k, q) or TT x 8
+// (v) floats.
+template <int F>
+__device__ __forceinline__ void put_kq(float* dst, v4f x, int c) {
+  if constexpr (F == kInF32) {
+    *reinterpret_cast<v4f*>(dst + 4 * c) = x;
+  } else if constexpr (F == kInBf16) {  // tokens 2c, 2c + 1
+    if (c < kq_lanes<F>()) {
+      *reinterpret_cast<v4f*>(dst + 8 * c) = r4::widen_lo(x);
+      *reinterpret_cast<v4f*>(dst + 8 * c + 4) = r4::widen_hi(x);
+    }
+  } else {  // tokens 4c .. 4c + 3, one 32-bit word each
+    if (c < kq_lanes<F>()) {
+      const v4u w = __builtin_bit_cast(v4u, x);
+#pragma unroll
+      for (int u = 0; u < 4; ++u) *reinterpret_cast<v4f*>(dst + 16 * c + 4 * u) = widen_f8<F>(w[u]);
+    }
+  }
+}
+template <int F>
+__device__ __forceinline__ void put_v(float* dst, v4f v0, v4f v1, int c) {
+  if constexpr (F == kInF32) {  // pieces c and c + 16 (token piece >> 1, half piece & 1)
+    *reinterpret_cast<v4f*>(dst + 4 * c) = v0;
+    *reinterpret_cast<v4f*>(dst + 64 + 4 * c) = v1;
+  } else if constexpr (F == kInBf16) {  // token c
+    *reinterpret_cast<v4f*>(dst + 8 * c) = r4::widen_lo(v0);
+    *reinterpret_cast<v4f*>(dst + 8 * c + 4) = r4::widen_hi(v0);
+  } else {  // tokens 2c, 2c + 1, half a token per word
+    if (c < 2 * kq_lanes<F>()) {
+      const v4u w = __builtin_bit_cast(v4u, v0);
+#pragma unroll
+      for (int u = 0; u < 4; ++u) *reinterpret_cast<v4f*>(dst + 16 * c + 4 * u) = widen_f8<F>(w[u]);
+    }
+  }
+}
+
 struct Streams {
   Rsrc k, d, q, v, p, r, y;
-  uint32_t row4, row8, row1;  // bytes per sequence row
+  uint32_t row4, row8, row1;    // float32 bytes per sequence row
+  uint32_t row4n, row8n;        // bytes per sequence row of k, q and of v in their format
 };
 
-template <bool FIXED>
+template <bool FIXED, int F>
 __device__ __forceinline__ void load_tile(Stage& x, const Streams& st, int s, int c, uint32_t t0) {
   const uint32_t o4 = static_cast<uint32_t>(s) * st.row4 + (t0 + c) * 16u;
-  x.k = r4::ld128<true>(st.k, o4);
-  x.q = r4::ld128<true>(st.q, o4);
+  x.k = load_kq<F>(st.k, st.row4n, s, c, t0);
+  x.q = load_kq<F>(st.q, st.row4n, s, c, t0);
   if constexpr (!FIXED) x.d = r4::ld128<true>(st.d, o4);
-  const uint32_t o8 = static_cast<uint32_t>(s) * st.row8 + t0 * 32u + c * 16u;
-  x.v0 = r4::ld128<true>(st.v, o8);
-  x.v1 = r4::ld128<true>(st.v, o8 + 256u);
+  load_v<F>(x.v0, x.v1, st.v, st.row8n, s, c, t0);
   if constexpr (!FIXED) {
     const uint32_t o1 = c < 4 ? static_cast<uint32_t>(s) * st.row1 + t0 * 4u + c * 16u : kOob;
     x.p = r4::ld128<false>(st.p, o1);
@@ -109,13 +174,12 @@ __device__ __forceinline__ void load_tile(Stage& x, const Streams& st, int s, in
   }
 }
 
-template <bool FIXED>
+template <bool FIXED, int F>
 __device__ __forceinline__ void put_tile(const Stage& x, float* tl, int s, int c) {
   float* b = tl + s * Tile::SEQ;
-  *reinterpret_cast<v4f*>(b + Tile::K + 4 * c) = x.k;
-  *reinterpret_cast<v4f*>(b + Tile::Q + 4 * c) = x.q;
-  *reinterpret_cast<v4f*>(b + Tile::V + 4 * c) = x.v0;
-  *reinterpret_cast<v4f*>(b + Tile::V + 64 + 4 * c) = x.v1;
+  put_kq<F>(b + Tile::K, x.k, c);
+  put_kq<F>(b + Tile::Q, x.q, c);
+  put_v<F>(b + Tile::V, x.v0, x.v1, c);
   if constexpr (!FIXED) {
     *reinterpret_cast<v4f*>(b + Tile::D + 4 * c) = x.d;
     if (c < 4) {
@@ -217,7 +281,7 @@ __device__ __forceinline__ float readout(const Bel& b, float qj) { return own_su
 __device__ __forceinline__ uint32_t mean_off(int i, int j) { return static_cast<uint32_t>(j * 32 + i * 8); }
 __device__ __forceinline__ uint32_t cov_off(int i, int j) { return static_cast<uint32_t>(i * 16 + j * 4); }
 
-template <bool FIXED>
+template <bool FIXED, int F>
 __global__ __launch_bounds__(kWave) void forward_kernel(FwdArgs a) {
   __shared__ float tile[Tile::SIZE];
   const int lane = threadIdx.x;
@@ -232,11 +296,13 @@ __global__ __launch_bounds__(kWave) void forward_kernel(FwdArgs a) {
   st.row4 = static_cast<uint32_t>(T) * 16u;
   st.row8 = static_cast<uint32_t>(T) * 32u;
   st.row1 = static_cast<uint32_t>(T) * 4u;
-  st.k = make_rsrc(a.k + n0 * T * 4, valid * st.row4);
-  st.q = make_rsrc(a.q + n0 * T * 4, valid * st.row4);
-  st.v = make_rsrc(a.v + n0 * T * 8, valid * st.row8);
+  st.row4n = static_cast<uint32_t>(T) * kq_bytes<F>();
+  st.row8n = 2u * st.row4n;
+  st.k = make_rsrc(r4::byte_offset(a.k, n0 * st.row4n), valid * st.row4n);
+  st.q = make_rsrc(r4::byte_offset(a.q, n0 * st.row4n), valid * st.row4n);
+  st.v = make_rsrc(r4::byte_offset(a.v, n0 * st.row8n), valid * st.row8n);
   st.y = make_rsrc(a.y + n0 * T * 8, valid * st.row8);
-  st.d = make_rsrc(FIXED ? a.k : a.d + n0 * T * 4, FIXED ? 0u : valid * st.row4);
+  st.d = make_rsrc(FIXED ? a.y : a.d + n0 * T * 4, FIXED ? 0u : valid * st.row4);
   st.p = make_rsrc(FIXED ? a.k : a.p + n0 * T, FIXED ? 0u : valid * st.row1);
   st.r = make_rsrc(FIXED ? a.k : a.r + n0 * T, FIXED ? 0u : valid * st.row1);
   const uint32_t nbp = static_cast<uint32_t>(a.nb + 1);
@@ -274,7 +340,7 @@ __global__ __launch_bounds__(kWave) void forward_kernel(FwdArgs a) {
   float* mine = tile + s * Tile::SEQ;
   const int64_t ntiles = (T + TT - 1) / TT;
   Stage x;
-  if (ntiles > 0) load_tile<FIXED>(x, st, s, c, 0);
+  if (ntiles > 0) load_tile<FIXED, F>(x, st, s, c, 0);
   int64_t next_ckpt = a.chunk;
   uint32_t ckpt = 1;
   v4f ys0 = v4f{0.f, 0.f, 0.f, 0.f}, ys1 = ys0;
@@ -287,14 +353,14 @@ __global__ __launch_bounds__(kWave) void forward_kernel(FwdArgs a) {
       ys1 = *reinterpret_cast<const v4f*>(mine + Tile::V + 64 + 4 * c);
     }
     r4::vm_wait<0>();
-    put_tile<FIXED>(x, tile, s, c);
+    put_tile<FIXED, F>(x, tile, s, c);
     if (ti > 0) {
       // Pieces c (token c >> 1) and c + 16 of the previous tile, all of whose tokens were computed.
       const uint32_t p0 = t0 - TT, o8 = static_cast<uint32_t>(s) * st.row8 + p0 * 32u + c * 16u;
       r4::st128<r4::kNtStore>(st.y, ys0, o8, 0);
       r4::st128<r4::kNtStore>(st.y, ys1, o8 + 256u, 0);
     }
-    if (ti + 1 < ntiles) load_tile<FIXED>(x, st, s, c, t0 + TT);
+    if (ti + 1 < ntiles) load_tile<FIXED, F>(x, st, s, c, t0 + TT);
     r4::lds_wait();
     if (len == TT && a.chunk % 8 == 0) {
 #pragma unroll
@@ -396,7 +462,7 @@ __device__ __forceinline__ float mean_step(float& M0, float& M1, float kj, float
   return own_sum(M0 * qj, M1 * qj);
 }
 
-template <bool FIXED>
+template <bool FIXED, int F>
 __global__ __launch_bounds__(2 * kWave) void forward_split_kernel(FwdArgs a) {
   __shared__ float lds[STile::SIZE];
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
@@ -426,7 +492,8 @@ __global__ __launch_bounds__(2 * kWave) void forward_split_kernel(FwdArgs a) {
 
   if (wave == 0) {
     // ---- covariance wave
-    const Rsrc rk = make_rsrc(a.k + n0 * T * 4, valid * row4);
+    const uint32_t row4n = static_cast<uint32_t>(T) * kq_bytes<F>();
+    const Rsrc rk = make_rsrc(r4::byte_offset(a.k, n0 * row4n), valid * row4n);
     const Rsrc rd = make_rsrc(FIXED ? a.k : a.d + n0 * T * 4, FIXED ? 0u : valid * row4);
     const Rsrc rp = make_rsrc(FIXED ? a.k : a.p + n0 * T, FIXED ? 0u : valid * row1);
     const Rsrc rr = make_rsrc(FIXED ? a.k : a.r + n0 * T, FIXED ? 0u : valid * row1);
@@ -439,7 +506,7 @@ __global__ __launch_bounds__(2 * kWave) void forward_split_kernel(FwdArgs a) {
     auto load = [&](int64_t t) __attribute__((always_inline)) {
       const uint32_t t0 = static_cast<uint32_t>(t * TT);
       const uint32_t o4 = static_cast<uint32_t>(s) * row4 + (t0 + c) * 16u;
-      sk = r4::ld128<true>(rk, o4);
+      sk = load_kq<F>(rk, row4n, s, c, t0);
       if constexpr (!FIXED) {
         sd = r4::ld128<true>(rd, o4);
         const uint32_t o1 = c < 4 ? static_cast<uint32_t>(s) * row1 + t0 * 4u + c * 16u : kOob;
@@ -449,7 +516,7 @@ __global__ __launch_bounds__(2 * kWave) void forward_split_kernel(FwdArgs a) {
     };
     auto put = [&](int64_t t) __attribute__((always_inline)) {
       float* b = in_slot(t);
-      *reinterpret_cast<v4f*>(b + STile::K + 4 * c) = sk;
+      put_kq<F>(b + STile::K, sk, c);
       if constexpr (!FIXED) {
         *reinterpret_cast<v4f*>(b + STile::D + 4 * c) = sd;
         if (c < 4) {
@@ -532,8 +599,9 @@ __global__ __launch_bounds__(2 * kWave) void forward_split_kernel(FwdArgs a) {
     r4::st32(rbc, P, cco, static_cast<uint32_t>(a.nb) * 64u);
   } else {
     // ---- mean wave
-    const Rsrc rq = make_rsrc(a.q + n0 * T * 4, valid * row4);
-    const Rsrc rv = make_rsrc(a.v + n0 * T * 8, valid * row8);
+    const uint32_t row4n = static_cast<uint32_t>(T) * kq_bytes<F>(), row8n = 2u * row4n;
+    const Rsrc rq = make_rsrc(r4::byte_offset(a.q, n0 * row4n), valid * row4n);
+    const Rsrc rv = make_rsrc(r4::byte_offset(a.v, n0 * row8n), valid * row8n);
     const Rsrc ry = make_rsrc(a.y + n0 * T * 8, valid * row8);
     const Rsrc rbm = make_rsrc(a.bm + n0 * nbp * 32, valid * nbp * 128u);
     const Rsrc rm0 = make_rsrc(a.m0 + n0 * 32, valid * 128u);
@@ -543,16 +611,13 @@ __global__ __launch_bounds__(2 * kWave) void forward_split_kernel(FwdArgs a) {
     v4f sq, sv0, sv1;
     auto load = [&](int64_t t) __attribute__((always_inline)) {
       const uint32_t t0 = static_cast<uint32_t>(t * TT);
-      sq = r4::ld128<true>(rq, static_cast<uint32_t>(s) * row4 + (t0 + c) * 16u);
-      const uint32_t o8 = static_cast<uint32_t>(s) * row8 + t0 * 32u + c * 16u;
-      sv0 = r4::ld128<true>(rv, o8);
-      sv1 = r4::ld128<true>(rv, o8 + 256u);
+      sq = load_kq<F>(rq, row4n, s, c, t0);
+      load_v<F>(sv0, sv1, rv, row8n, s, c, t0);
     };
     auto put = [&](int64_t t) __attribute__((always_inline)) {
       float* b = in_slot(t);
-      *reinterpret_cast<v4f*>(b + STile::Q + 4 * c) = sq;
-      *reinterpret_cast<v4f*>(b + STile::V + 4 * c) = sv0;
-      *reinterpret_cast<v4f*>(b + STile::V + 64 + 4 * c) = sv1;
+      put_kq<F>(b + STile::Q, sq, c);
+      put_v<F>(b + STile::V, sv0, sv1, c);
     };
     // Readouts of tile t leave its y slot as whole pieces (valid tokens only).
     auto store_y = [&](int64_t t) __attribute__((always_inline)) {
@@ -1478,17 +1543,32 @@ int64_t set_small_batch_limit(int direction, int64_t limit) {
   return g_small_limit[direction].exchange(limit, std::memory_order_relaxed);
 }
 
+namespace {
+// bf16 / float8 streams run the two-wave kernel only (the dispatch keeps them
+// within its limit).
+template <int F>
+hipError_t launch_forward_small_fmt(bool fixed, const FwdArgs& a, int64_t blocks, hipStream_t stream) {
+  const dim3 grid(static_cast<unsigned>(blocks));
+  if (F != kInF32 || a.n <= small_batch_limit(2)) {
+    if (fixed) hipLaunchKernelGGL((sn::forward_split_kernel<true, F>), grid, dim3(2 * kWave), 0, stream, a);
+    else hipLaunchKernelGGL((sn::forward_split_kernel<false, F>), grid, dim3(2 * kWave), 0, stream, a);
+  } else if constexpr (F == kInF32) {
+    if (fixed) hipLaunchKernelGGL((sn::forward_kernel<true, F>), grid, dim3(kWave), 0, stream, a);
+    else hipLaunchKernelGGL((sn::forward_kernel<false, F>), grid, dim3(kWave), 0, stream, a);
+  }
+  return hipGetLastError();
+}
+}  // namespace
+
 hipError_t launch_forward_small(bool fixed, const FwdArgs& a, hipStream_t stream) {
   const int64_t blocks = (a.n + sn::SPW - 1) / sn::SPW;
   if (blocks == 0) return hipSuccess;
-  if (a.n <= small_batch_limit(2)) {
-    if (fixed) hipLaunchKernelGGL(sn::forward_split_kernel<true>, dim3(static_cast<unsigned>(blocks)), dim3(2 * kWave), 0, stream, a);
-    else hipLaunchKernelGGL(sn::forward_split_kernel<false>, dim3(static_cast<unsigned>(blocks)), dim3(2 * kWave), 0, stream, a);
-    return hipGetLastError();
+  switch (a.in_fmt) {
+    case kInBf16: return launch_forward_small_fmt<kInBf16>(fixed, a, blocks, stream);
+    case kInE4M3: return launch_forward_small_fmt<kInE4M3>(fixed, a, blocks, stream);
+    case kInE5M2: return launch_forward_small_fmt<kInE5M2>(fixed, a, blocks, stream);
+    default: return launch_forward_small_fmt<kInF32>(fixed, a, blocks, stream);
   }
-  if (fixed) hipLaunchKernelGGL(sn::forward_kernel<true>, dim3(static_cast<unsigned>(blocks)), dim3(kWave), 0, stream, a);
-  else hipLaunchKernelGGL(sn::forward_kernel<false>, dim3(static_cast<unsigned>(blocks)), dim3(kWave), 0, stream, a);
-  return hipGetLastError();
 }
 
 hipError_t launch_backward_small(bool fixed, bool dyn, const BwdArgs& a, hipStream_t stream) {

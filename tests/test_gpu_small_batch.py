@@ -171,6 +171,38 @@ def test_three_wave_backward_is_bitwise_the_one_wave_backward(cuda_device, abi, 
         assert torch.equal(a, b), lab
 
 
+NARROW = {"bf16": (torch.bfloat16, None), "e4m3": (torch.float8_e4m3fn, 0), "e5m2": (torch.float8_e5m2, 1)}
+
+
+@pytest.mark.parametrize("fmt", list(NARROW))
+@pytest.mark.parametrize("fixed", [False, True])
+@pytest.mark.parametrize("n,t,chunk", [(37, 52, 8), (5, 64, 13), (9, 16, 1), (2, 4, 8)])
+def test_row_forward_narrow_inputs_equal_float32(cuda_device, fmt, fixed, n, t, chunk):
+    """The two-wave row forward with bf16 / float8 keys, values and queries (widened on chip, exactly) gives bit
+    for bit the row forward on the widened float32 values; bf16 / float8 streams take it at these sizes by
+    default."""
+    from bayes_ssm import _hip
+
+    name = "split"
+    print(f"narrow row forward {fmt} fixed={fixed} n={n} t={t} chunk={chunk}", flush=True)
+    dtype, code = NARROW[fmt]
+    _, dev = _case(n, t, 4, seed=7 * n + t, device=cuda_device)
+    for x in "kvq":
+        dev[x + "h"] = dev[x].to(dtype).contiguous()
+        dev[x] = dev[x + "h"].float().contiguous()
+    P = _hip.ptr
+    with layout(name):
+        ref = _forward(_ext(), dev, fixed, chunk)
+        out = [torch.empty_like(x) for x in ref]
+        head = ("bssm_forward_chunked_bf16", 4, 8, int(fixed)) if code is None else \
+            ("bssm_forward_chunked_fp8", 4, 8, int(fixed), code)
+        _hip.call(*head, P(dev["kh"]), P(dev["vh"]), P(dev["qh"]), P(dev["d"]), P(dev["p"]), P(dev["r"]),
+                  P(dev["m0"]), P(dev["c0"]), *[P(x) for x in out], n, t, chunk, 1e-6, _hip.stream_of(cuda_device))
+        torch.cuda.synchronize()
+    for lab, a, b in zip(("y", "mean_T", "cov_T", "bmean", "bcov"), out, ref):
+        assert torch.equal(a, b), lab
+
+
 def test_layouts_at_many_sequences(cuda_device):
     """4099 sequences (a partial last wave): both layouts match the oracle on every output and gradient, and
     the default limits route this size to the row kernels (whose results differ from the rotated ones in the
