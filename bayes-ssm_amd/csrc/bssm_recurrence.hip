@@ -515,8 +515,10 @@ hipError_t launch_backward_dd(bool fixed, bool dyn, const BwdArgs& a, hipStream_
 }
 
 hipError_t launch_backward(int key_dim, bool fixed, bool dyn, const BwdArgs& a, hipStream_t stream) {
-  if (key_dim == 4 && a.rot4 && a.in_fmt == kInF32 && a.n <= small_batch_limit(1) && a.t % 16 == 0 &&
-      a.chunk == kRot4Chunk)
+  // bf16 / float8 streams: only within the three-wave limit (as the forward).
+  const int64_t row_limit = a.in_fmt == kInF32 ? small_batch_limit(1)
+                                               : std::min(small_batch_limit(1), small_batch_limit(3));
+  if (key_dim == 4 && a.rot4 && a.n <= row_limit && a.t % 16 == 0 && a.chunk == kRot4Chunk)
     return launch_backward_small(fixed, dyn, a, stream);
   if (key_dim == 4 && a.rot4) return launch_backward_r4(fixed, dyn, a, stream);
   if (key_dim == 1 && d1_backward_ok(a)) return launch_backward_d1(fixed, dyn, a, stream);

@@ -97,61 +97,103 @@ template <int F>
 constexpr uint32_t kq_bytes() {
   return F == kInF32 ? 16u : F == kInBf16 ? 8u : 4u;
 }
-// Lanes (of a sequence's 16) that move a 16-token tile's 16-byte pieces of a
-// 4-value stream; a value stream takes twice as many pieces (float32: two per
-// lane, c and c + 16).
-template <int F>
+// Lanes (of a sequence's 16) that move the 16-byte pieces of a 4-value
+// stream over TOK tokens; a value stream takes twice as many pieces (float32
+// at 16 tokens: two per lane, c and c + 16).
+template <int F, int TOK = TT>
 constexpr int kq_lanes() {
-  return static_cast<int>(TT * kq_bytes<F>() / 16u);
+  return static_cast<int>(TOK * kq_bytes<F>() / 16u);
 }
 
-// Raw 16-byte pieces of the tile at token t0 of sequence s (lane c) of the
-// 4-value stream r, and of the value stream rv (two pieces for float32).
-template <int F>
+// Raw 16-byte pieces (lane c of sequence s) of the TOK tokens from t0 of the
+// 4-value stream r, and of the value stream rv (two pieces for float32 at 16
+// tokens).
+template <int F, int TOK = TT>
 __device__ __forceinline__ v4f load_kq(Rsrc r, uint32_t row, int s, int c, uint32_t t0) {
   const uint32_t off = static_cast<uint32_t>(s) * row + t0 * kq_bytes<F>() + static_cast<uint32_t>(c) * 16u;
-  return r4::ld128<true>(r, c < kq_lanes<F>() ? off : kOob);
+  return r4::ld128<true>(r, c < kq_lanes<F, TOK>() ? off : kOob);
 }
-template <int F>
+template <int F, int TOK = TT>
 __device__ __forceinline__ void load_v(v4f& v0, v4f& v1, Rsrc rv, uint32_t row, int s, int c, uint32_t t0) {
   const uint32_t off = static_cast<uint32_t>(s) * row + t0 * 2u * kq_bytes<F>() + static_cast<uint32_t>(c) * 16u;
-  v0 = r4::ld128<true>(rv, c < 2 * kq_lanes<F>() ? off : kOob);
-  if constexpr (F == kInF32) v1 = r4::ld128<true>(rv, off + 256u);
+  v0 = r4::ld128<true>(rv, c < 2 * kq_lanes<F, TOK>() ? off : kOob);
+  if constexpr (F == kInF32 && TOK == 16) v1 = r4::ld128<true>(rv, off + 256u);
 }
-// Widen and write those pieces into a tile region of TT x 4 (k, q) or TT x 8
+// Widen and write those pieces into a tile region of TOK x 4 (k, q) or TOK x 8
 // (v) floats.
-template <int F>
+template <int F, int TOK = TT>
 __device__ __forceinline__ void put_kq(float* dst, v4f x, int c) {
+  if (c >= kq_lanes<F, TOK>()) return;
   if constexpr (F == kInF32) {
     *reinterpret_cast<v4f*>(dst + 4 * c) = x;
   } else if constexpr (F == kInBf16) {  // tokens 2c, 2c + 1
-    if (c < kq_lanes<F>()) {
-      *reinterpret_cast<v4f*>(dst + 8 * c) = r4::widen_lo(x);
-      *reinterpret_cast<v4f*>(dst + 8 * c + 4) = r4::widen_hi(x);
-    }
+    *reinterpret_cast<v4f*>(dst + 8 * c) = r4::widen_lo(x);
+    *reinterpret_cast<v4f*>(dst + 8 * c + 4) = r4::widen_hi(x);
   } else {  // tokens 4c .. 4c + 3, one 32-bit word each
-    if (c < kq_lanes<F>()) {
-      const v4u w = __builtin_bit_cast(v4u, x);
+    const v4u w = __builtin_bit_cast(v4u, x);
 #pragma unroll
-      for (int u = 0; u < 4; ++u) *reinterpret_cast<v4f*>(dst + 16 * c + 4 * u) = widen_f8<F>(w[u]);
-    }
+    for (int u = 0; u < 4; ++u) *reinterpret_cast<v4f*>(dst + 16 * c + 4 * u) = widen_f8<F>(w[u]);
   }
 }
-template <int F>
+template <int F, int TOK = TT>
 __device__ __forceinline__ void put_v(float* dst, v4f v0, v4f v1, int c) {
-  if constexpr (F == kInF32) {  // pieces c and c + 16 (token piece >> 1, half piece & 1)
+  if constexpr (F == kInF32 && TOK == 16) {  // pieces c and c + 16 (token piece >> 1, half piece & 1)
     *reinterpret_cast<v4f*>(dst + 4 * c) = v0;
     *reinterpret_cast<v4f*>(dst + 64 + 4 * c) = v1;
-  } else if constexpr (F == kInBf16) {  // token c
-    *reinterpret_cast<v4f*>(dst + 8 * c) = r4::widen_lo(v0);
-    *reinterpret_cast<v4f*>(dst + 8 * c + 4) = r4::widen_hi(v0);
-  } else {  // tokens 2c, 2c + 1, half a token per word
-    if (c < 2 * kq_lanes<F>()) {
+  } else {
+    if (c >= 2 * kq_lanes<F, TOK>()) return;
+    if constexpr (F == kInF32) {  // piece c
+      *reinterpret_cast<v4f*>(dst + 4 * c) = v0;
+    } else if constexpr (F == kInBf16) {  // token c
+      *reinterpret_cast<v4f*>(dst + 8 * c) = r4::widen_lo(v0);
+      *reinterpret_cast<v4f*>(dst + 8 * c + 4) = r4::widen_hi(v0);
+    } else {  // tokens 2c, 2c + 1, half a token per word
       const v4u w = __builtin_bit_cast(v4u, v0);
 #pragma unroll
       for (int u = 0; u < 4; ++u) *reinterpret_cast<v4f*>(dst + 16 * c + 4 * u) = widen_f8<F>(w[u]);
     }
   }
+}
+// The reverse: gradients in a region of TOK x 4 / TOK x 8 floats leave as
+// 16-byte pieces of format F (bfloat16: round to nearest even; float8:
+// narrow_f8, torch's rounding), at the loaders' offsets.
+template <int F, int TOK>
+__device__ __forceinline__ void store_kq(Rsrc r, uint32_t row, int s, int c, uint32_t t0, const float* src) {
+  const uint32_t off = static_cast<uint32_t>(s) * row + t0 * kq_bytes<F>() + static_cast<uint32_t>(c) * 16u;
+  const uint32_t o = c < kq_lanes<F, TOK>() ? off : kOob;
+  const int cc = c & (kq_lanes<F, TOK>() - 1);
+  v4f x;
+  if constexpr (F == kInF32) {
+    x = *reinterpret_cast<const v4f*>(src + 4 * cc);
+  } else if constexpr (F == kInBf16) {
+    x = r4::narrow(*reinterpret_cast<const v4f*>(src + 8 * cc), *reinterpret_cast<const v4f*>(src + 8 * cc + 4));
+  } else {
+    v4u w;
+#pragma unroll
+    for (int u = 0; u < 4; ++u) w[u] = narrow_f8<F>(*reinterpret_cast<const v4f*>(src + 16 * cc + 4 * u));
+    x = __builtin_bit_cast(v4f, w);
+  }
+  r4::st128<r4::kNtStore>(r, x, o, 0);
+}
+template <int F, int TOK>
+__device__ __forceinline__ void store_v(Rsrc r, uint32_t row, int s, int c, uint32_t t0, const float* src) {
+  static_assert(TOK * 2 * kq_bytes<F>() <= 256u, "one piece per lane");
+  const uint32_t off = static_cast<uint32_t>(s) * row + t0 * 2u * kq_bytes<F>() + static_cast<uint32_t>(c) * 16u;
+  const int lanes = 2 * kq_lanes<F, TOK>();
+  const uint32_t o = c < lanes ? off : kOob;
+  const int cc = c & (lanes - 1);
+  v4f x;
+  if constexpr (F == kInF32) {
+    x = *reinterpret_cast<const v4f*>(src + 4 * cc);
+  } else if constexpr (F == kInBf16) {
+    x = r4::narrow(*reinterpret_cast<const v4f*>(src + 8 * cc), *reinterpret_cast<const v4f*>(src + 8 * cc + 4));
+  } else {
+    v4u w;
+#pragma unroll
+    for (int u = 0; u < 4; ++u) w[u] = narrow_f8<F>(*reinterpret_cast<const v4f*>(src + 16 * cc + 4 * u));
+    x = __builtin_bit_cast(v4f, w);
+  }
+  r4::st128<r4::kNtStore>(r, x, o, 0);
 }
 
 struct Streams {
@@ -1185,7 +1227,7 @@ __device__ __forceinline__ void cov_reverse(float ki, float kj, float di, float 
   o.guj = guj;
 }
 
-template <bool FIXED, bool DYN>
+template <bool FIXED, bool DYN, int F>
 __global__ __launch_bounds__(3 * kWave) void backward_split_kernel(BwdArgs a) {
   __shared__ float lds[SBTile::SIZE];
   constexpr int CH = SBTile::CH;
@@ -1218,10 +1260,12 @@ __global__ __launch_bounds__(3 * kWave) void backward_split_kernel(BwdArgs a) {
   const uint32_t o4 = static_cast<uint32_t>(s) * row4 + static_cast<uint32_t>(c) * 16u;  // + t0 * 16
   const uint32_t o8 = static_cast<uint32_t>(s) * row8 + static_cast<uint32_t>(c) * 16u;  // + t0 * 32
   const uint32_t o1 = static_cast<uint32_t>(s) * row1 + static_cast<uint32_t>(c) * 16u;  // + t0 * 4
+  // Bytes per sequence row of k, q (and gk, gq) and of v (and gv) in format F.
+  const uint32_t row4n = static_cast<uint32_t>(T) * kq_bytes<F>(), row8n = 2u * row4n;
 
   if (wave == 0) {
     // ------------------------------------------------ covariance replay wave
-    const Rsrc rk = make_rsrc(a.k + n0 * T * 4, valid * row4);
+    const Rsrc rk = make_rsrc(r4::byte_offset(a.k, n0 * row4n), valid * row4n);
     const Rsrc rd = make_rsrc(FIXED ? a.k : a.d + n0 * T * 4, FIXED ? 0u : valid * row4);
     const Rsrc rp = make_rsrc(FIXED ? a.k : a.p + n0 * T, FIXED ? 0u : valid * row1);
     const Rsrc rr = make_rsrc(FIXED ? a.k : a.r + n0 * T, FIXED ? 0u : valid * row1);
@@ -1231,7 +1275,7 @@ __global__ __launch_bounds__(3 * kWave) void backward_split_kernel(BwdArgs a) {
     auto load = [&](int64_t x) __attribute__((always_inline)) {
       const uint32_t t0 = tok0(x);
       const uint32_t q4 = c < CH ? o4 + t0 * 16u : kOob;
-      sk = r4::ld128<true>(rk, q4);
+      sk = load_kq<F, CH>(rk, row4n, s, c, t0);
       if constexpr (!FIXED) {
         sd = r4::ld128<true>(rd, q4);
         const uint32_t q1 = c < CH / 4 ? o1 + t0 * 4u : kOob;
@@ -1241,9 +1285,9 @@ __global__ __launch_bounds__(3 * kWave) void backward_split_kernel(BwdArgs a) {
     };
     auto put = [&](int64_t x) __attribute__((always_inline)) {
       float* b = slot(x);
-      if (c < CH) {
-        *reinterpret_cast<v4f*>(b + SBTile::K + 4 * c) = sk;
-        if constexpr (!FIXED) *reinterpret_cast<v4f*>(b + SBTile::D + 4 * c) = sd;
+      put_kq<F, CH>(b + SBTile::K, sk, c);
+      if constexpr (!FIXED) {
+        if (c < CH) *reinterpret_cast<v4f*>(b + SBTile::D + 4 * c) = sd;
       }
       if constexpr (!FIXED) {
         if (c < CH / 4) {
@@ -1317,7 +1361,7 @@ __global__ __launch_bounds__(3 * kWave) void backward_split_kernel(BwdArgs a) {
   } else if (wave == 1) {
     // ------------------------------------------------ covariance reverse wave
     const bool i1 = (i & 1) != 0, i2 = (i & 2) != 0;
-    const Rsrc rgk = make_rsrc(a.gk + n0 * T * 4, valid * row4);
+    const Rsrc rgk = make_rsrc(r4::byte_offset(a.gk, n0 * row4n), valid * row4n);
     const Rsrc rgd = make_rsrc(a.gd ? a.gd + n0 * T * 4 : a.gk, a.gd ? valid * row4 : 0u);
     const Rsrc rgp = make_rsrc(a.gp ? a.gp + n0 * T : a.gk, a.gp ? valid * row1 : 0u);
     const Rsrc rgr = make_rsrc(a.gr ? a.gr + n0 * T : a.gk, a.gr ? valid * row1 : 0u);
@@ -1337,7 +1381,7 @@ __global__ __launch_bounds__(3 * kWave) void backward_split_kernel(BwdArgs a) {
       const uint32_t q4 = c < CH ? o4 + t0 * 16u : kOob, q1 = c < CH / 4 ? o1 + t0 * 4u : kOob;
       const v4f zero = v4f{0.f, 0.f, 0.f, 0.f};
       const int c8 = c & (CH - 1), c2 = c & (CH / 4 - 1);
-      r4::st128<r4::kNtStore>(rgk, *reinterpret_cast<const v4f*>(b + SBTile::K + 4 * c8), q4, 0);
+      store_kq<F, CH>(rgk, row4n, s, c, t0, b + SBTile::K);
       if (a.gd) r4::st128<r4::kNtStore>(rgd, DYN ? *reinterpret_cast<const v4f*>(b + SBTile::D + 4 * c8) : zero, q4, 0);
       if (a.gp) r4::st128(rgp, DYN ? *reinterpret_cast<const v4f*>(b + SBTile::P + 4 * c2) : zero, q1, 0);
       if (a.gr) r4::st128(rgr, DYN ? *reinterpret_cast<const v4f*>(b + SBTile::R + 4 * c2) : zero, q1, 0);
@@ -1403,11 +1447,11 @@ __global__ __launch_bounds__(3 * kWave) void backward_split_kernel(BwdArgs a) {
     }
   } else {
     // ------------------------------------------------ mean wave
-    const Rsrc rq = make_rsrc(a.q + n0 * T * 4, valid * row4);
-    const Rsrc rv = make_rsrc(a.v + n0 * T * 8, valid * row8);
+    const Rsrc rq = make_rsrc(r4::byte_offset(a.q, n0 * row4n), valid * row4n);
+    const Rsrc rv = make_rsrc(r4::byte_offset(a.v, n0 * row8n), valid * row8n);
     const Rsrc rgy = make_rsrc(a.gy + n0 * T * 8, valid * row8);
-    const Rsrc rgq = make_rsrc(a.gq + n0 * T * 4, valid * row4);
-    const Rsrc rgv = make_rsrc(a.gv + n0 * T * 8, valid * row8);
+    const Rsrc rgq = make_rsrc(r4::byte_offset(a.gq, n0 * row4n), valid * row4n);
+    const Rsrc rgv = make_rsrc(r4::byte_offset(a.gv, n0 * row8n), valid * row8n);
     const Rsrc rbm = make_rsrc(a.bm + n0 * nbp * 32, valid * nbp * 128u);
     const uint32_t mo = static_cast<uint32_t>(s) * 128u + mean_off(i, j);
     const uint32_t cmo = static_cast<uint32_t>(s) * nbp * 128u + mean_off(i, j);
@@ -1419,25 +1463,24 @@ __global__ __launch_bounds__(3 * kWave) void backward_split_kernel(BwdArgs a) {
       gM0 = m[0];
       gM1 = m[1];
     }
-    v4f sq, sv, sg;
+    v4f sq, sv, sv1, sg;
     auto load = [&](int64_t x) __attribute__((always_inline)) {
       const uint32_t t0 = tok0(x);
-      sq = r4::ld128<true>(rq, c < CH ? o4 + t0 * 16u : kOob);
-      sv = r4::ld128<true>(rv, o8 + t0 * 32u);
+      sq = load_kq<F, CH>(rq, row4n, s, c, t0);
+      load_v<F, CH>(sv, sv1, rv, row8n, s, c, t0);
       sg = r4::ld128<true>(rgy, o8 + t0 * 32u);
     };
     auto put = [&](int64_t x) __attribute__((always_inline)) {
       float* b = slot(x);
-      if (c < CH) *reinterpret_cast<v4f*>(b + SBTile::Q + 4 * c) = sq;
-      *reinterpret_cast<v4f*>(b + SBTile::V + 4 * c) = sv;
+      put_kq<F, CH>(b + SBTile::Q, sq, c);
+      put_v<F, CH>(b + SBTile::V, sv, sv1, c);
       *reinterpret_cast<v4f*>(b + SBTile::GY + 4 * c) = sg;
     };
     auto store = [&](int64_t x) __attribute__((always_inline)) {
       const float* b = slot(x);
       const uint32_t t0 = tok0(x);
-      r4::st128<r4::kNtStore>(rgq, *reinterpret_cast<const v4f*>(b + SBTile::Q + 4 * (c & (CH - 1))),
-                              c < CH ? o4 + t0 * 16u : kOob, 0);
-      r4::st128<r4::kNtStore>(rgv, *reinterpret_cast<const v4f*>(b + SBTile::V + 4 * c), o8 + t0 * 32u, 0);
+      store_kq<F, CH>(rgq, row4n, s, c, t0, b + SBTile::Q);
+      store_v<F, CH>(rgv, row8n, s, c, t0, b + SBTile::V);
     };
     auto ckpt = [&](int64_t x) __attribute__((always_inline)) {
       return r4::ld64(rbm, cmo + static_cast<uint32_t>(nb - 1 - x) * 128u, 0);
@@ -1571,18 +1614,34 @@ hipError_t launch_forward_small(bool fixed, const FwdArgs& a, hipStream_t stream
   }
 }
 
+namespace {
+template <int F>
+void launch_backward_split(bool fixed, bool dyn, const BwdArgs& a, dim3 grid, hipStream_t stream) {
+  const dim3 block(3 * kWave);
+  if (fixed) hipLaunchKernelGGL((sn::backward_split_kernel<true, false, F>), grid, block, 0, stream, a);
+  else if (dyn) hipLaunchKernelGGL((sn::backward_split_kernel<false, true, F>), grid, block, 0, stream, a);
+  else hipLaunchKernelGGL((sn::backward_split_kernel<false, false, F>), grid, block, 0, stream, a);
+}
+}  // namespace
+
+// bf16 / float8 streams run the three-wave kernel only (the dispatch keeps
+// them within its limit).
 hipError_t launch_backward_small(bool fixed, bool dyn, const BwdArgs& a, hipStream_t stream) {
   if (a.t % sn::TT != 0 || a.chunk != kRot4Chunk) return hipErrorInvalidValue;
   const int64_t blocks = (a.n + sn::SPW - 1) / sn::SPW;
   if (blocks == 0) return hipSuccess;
+  const dim3 grid(static_cast<unsigned>(blocks));
+  switch (a.in_fmt) {
+    case kInBf16: launch_backward_split<kInBf16>(fixed, dyn, a, grid, stream); return hipGetLastError();
+    case kInE4M3: launch_backward_split<kInE4M3>(fixed, dyn, a, grid, stream); return hipGetLastError();
+    case kInE5M2: launch_backward_split<kInE5M2>(fixed, dyn, a, grid, stream); return hipGetLastError();
+    default: break;
+  }
   if (a.n <= small_batch_limit(3)) {
-    const dim3 grid(static_cast<unsigned>(blocks)), block(3 * kWave);
-    if (fixed) hipLaunchKernelGGL((sn::backward_split_kernel<true, false>), grid, block, 0, stream, a);
-    else if (dyn) hipLaunchKernelGGL((sn::backward_split_kernel<false, true>), grid, block, 0, stream, a);
-    else hipLaunchKernelGGL((sn::backward_split_kernel<false, false>), grid, block, 0, stream, a);
+    launch_backward_split<kInF32>(fixed, dyn, a, grid, stream);
     return hipGetLastError();
   }
-  const dim3 grid(static_cast<unsigned>(blocks)), block(kWave);
+  const dim3 block(kWave);
   if (fixed) hipLaunchKernelGGL((sn::backward_kernel<true, false>), grid, block, 0, stream, a);
   else if (dyn) hipLaunchKernelGGL((sn::backward_kernel<false, true>), grid, block, 0, stream, a);
   else hipLaunchKernelGGL((sn::backward_kernel<false, false>), grid, block, 0, stream, a);

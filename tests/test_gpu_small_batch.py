@@ -203,6 +203,47 @@ def test_row_forward_narrow_inputs_equal_float32(cuda_device, fmt, fixed, n, t, 
         assert torch.equal(a, b), lab
 
 
+@pytest.mark.parametrize("fmt", list(NARROW))
+@pytest.mark.parametrize("fixed,dyn", [(False, True), (False, False), (True, False)])
+@pytest.mark.parametrize("n,t", [(37, 48), (5, 16), (9, 64)])
+def test_row_backward_narrow_inputs_equal_float32(cuda_device, fmt, fixed, dyn, n, t):
+    """The three-wave row backward with bf16 / float8 keys, values and queries: gk, gv, gq are the float32 row
+    backward's gradients on the widened values rounded as torch rounds them (.to(dtype)); every other gradient
+    is bit for bit the float32 one."""
+    from bayes_ssm import _hip
+
+    print(f"narrow row backward {fmt} fixed={fixed} dyn={dyn} n={n} t={t}", flush=True)
+    dtype, code = NARROW[fmt]
+    _, dev = _case(n, t, 4, seed=3 * n + t, device=cuda_device)
+    for x in "kvq":
+        dev[x + "h"] = dev[x].to(dtype).contiguous()
+        dev[x] = dev[x + "h"].float().contiguous()
+    P = _hip.ptr
+    ext = _ext()
+    with layout("split"):
+        _, _, _, bm, bc = _forward(ext, dev, fixed, 8)
+        name = "backward_chunked" + ("" if dyn or fixed else "_lean") + ("_fixed" if fixed else "")
+        nout = 8 if (dyn or fixed) else 3
+        ref = _backward(ext, name, fixed, nout, dev, bm, bc, 8, True)
+        gk, gv, gq = (torch.empty_like(dev[x + "h"]) for x in "kvq")
+        gd, gp, gr = ((torch.empty_like(dev[x]) for x in "dpr") if nout == 8 else (None, None, None))
+        gm0, gc0 = torch.empty_like(dev["m0"]), torch.empty_like(dev["c0"])
+        head = ("bssm_backward_chunked_bf16", 4, 8, int(fixed)) if code is None else \
+            ("bssm_backward_chunked_fp8", 4, 8, int(fixed), code)
+        _hip.call(*head, P(dev["kh"]), P(dev["vh"]), P(dev["qh"]), P(dev["d"]), P(dev["p"]), P(dev["r"]),
+                  P(dev["m0"]), P(dev["c0"]), P(bm), P(bc), P(dev["gy"]), P(dev["gmf"]), P(dev["gcf"]),
+                  P(gk), P(gv), P(gq), P(gd), P(gp), P(gr), P(gm0), P(gc0), n, t, 8, 1e-6,
+                  _hip.stream_of(cuda_device))
+        torch.cuda.synchronize()
+    for lab, a, b in (("gk", gk, ref[0]), ("gv", gv, ref[1]), ("gq", gq, ref[2])):
+        assert a.dtype == dtype
+        assert torch.equal(a.view(torch.uint8) if a.element_size() == 1 else a, b.to(dtype).view(torch.uint8)
+                           if a.element_size() == 1 else b.to(dtype)), lab
+    if nout == 8:
+        for lab, a, b in zip(("gd", "gp", "gr", "gm0", "gc0"), (gd, gp, gr, gm0, gc0), ref[3:]):
+            assert torch.equal(a, b), lab
+
+
 def test_layouts_at_many_sequences(cuda_device):
     """4099 sequences (a partial last wave): both layouts match the oracle on every output and gradient, and
     the default limits route this size to the row kernels (whose results differ from the rotated ones in the
