@@ -881,7 +881,7 @@ int bssm_mixer_block_backward(const void* projected, int64_t ld_projected, const
 int bssm_rotation_checkpoint(int key_dim) { return bssm::rotation_checkpoint(key_dim); }
 
 int64_t bssm_small_batch_limit(int direction, int64_t limit) {
-  if (direction < 0 || direction > 3) return -1;
+  if (direction < 0 || direction > 4) return -1;
   return limit >= 0 ? bssm::set_small_batch_limit(direction, limit) : bssm::small_batch_limit(direction);
 }
 

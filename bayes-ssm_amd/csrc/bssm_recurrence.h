@@ -194,6 +194,10 @@ struct RotArgs {
 };
 int rotation_checkpoint(int key_dim);
 hipError_t launch_rotation_forward(int key_dim, const RotArgs& a, hipStream_t stream);
+// Row-per-sequence rotation forward for D = 4, M = 8 (bssm_small.hip): used
+// with 16-byte aligned streams (vec), T a multiple of 4 and 8-byte aligned
+// mean tensors, for n up to small_batch_limit(4).
+hipError_t launch_rotation_forward_small(const RotArgs& a, hipStream_t stream);
 hipError_t launch_rotation_backward(int key_dim, const RotArgs& a, hipStream_t stream);
 
 // Length-four causal depthwise filter on channels-last rows (bssm_conv4.hip):

@@ -34,37 +34,17 @@
 #include "bssm_rot4.h"
 #include "bssm_step.h"
 
+// No contraction: the four-term sums of P' would otherwise be fused as
+// fma(first product, second), which the owners of rows i and j evaluate with
+// the products in swapped roles, so P_ij and P_ji would differ in the last
+// bit.  Every intended fused multiply-add is an explicit fmaf.
+#pragma clang fp contract(off)
+
 namespace bssm {
 namespace rot {
 namespace {
 
 constexpr float kTiny = FLT_MIN;  // torch.finfo(float32).tiny
-
-// sin and cos of x without a library call (an outlined call makes the
-// caller save its live registers to scratch).  Cody-Waite reduction by pi/2
-// in double precision (pi/2 as a two-double sum; n x pi/2 is exact in the
-// fma for any |x| below 2^40), then the Taylor series on |r| <= pi/4:
-// sin to r^9 (next term below 7e-10 relative) and cos to r^10 (below 1.2e-10).
-__device__ __forceinline__ void sincos_rad(float x, float& s, float& c) {
-  const double xd = x;
-  const double n = rint(xd * 0.6366197723675814);
-  const double rd = fma(-n, 6.123233995736766e-17, fma(-n, 1.5707963267948966, xd));
-  const float r = static_cast<float>(rd), r2 = r * r;
-  float ps = 1.f / 362880.f;
-  ps = fmaf(ps, r2, -1.f / 5040.f);
-  ps = fmaf(ps, r2, 1.f / 120.f);
-  ps = fmaf(ps, r2, -1.f / 6.f);
-  const float sr = fmaf(r * r2, ps, r);
-  float pc = -1.f / 3628800.f;
-  pc = fmaf(pc, r2, 1.f / 40320.f);
-  pc = fmaf(pc, r2, -1.f / 720.f);
-  pc = fmaf(pc, r2, 1.f / 24.f);
-  pc = fmaf(pc, r2, -0.5f);
-  const float cr = fmaf(r2, pc, 1.f);
-  const int q = static_cast<int>(static_cast<int64_t>(n) & 3);
-  s = (q == 0) ? sr : (q == 1) ? cr : (q == 2) ? -sr : -cr;
-  c = (q == 0) ? cr : (q == 1) ? -sr : (q == 2) ? -cr : sr;
-}
 
 template <int D, int M, int G>
 struct TokRot {
@@ -1034,6 +1014,9 @@ int rotation_checkpoint(int key_dim) {
 
 hipError_t launch_rotation_forward(int key_dim, const RotArgs& a, hipStream_t stream) {
   if (a.n == 0) return hipSuccess;
+  auto al8 = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 7u) == 0; };
+  if (key_dim == 4 && a.vec && a.t % 4 == 0 && a.n <= small_batch_limit(4) && al8(a.m0) && al8(a.mT) && al8(a.bm))
+    return launch_rotation_forward_small(a, stream);
   switch (key_dim) {
     case 2: return rot::fwd<2>(a, stream);
     case 4: return rot::fwd<4>(a, stream);

@@ -37,6 +37,7 @@
 // M <- d * M + beta u e^T, P <- d d^T * P + p I - beta u u^T, y = M^T q.
 
 #include <atomic>
+#include <cfloat>
 
 #include "bssm_rot4.h"
 
@@ -761,6 +762,234 @@ __global__ __launch_bounds__(2 * kWave) void forward_split_kernel(FwdArgs a) {
     r4::st64(rmT, own_order(m, odd), mo, 0);
     store_ckpt(static_cast<uint32_t>(a.nb));
   }
+}
+
+// --------------------------------------------------- rotation dynamics forward
+// The row layout for block-diagonal damped rotations (the equations of
+// bssm_rotation.hip): P' = R P R^T + Q, M' = R M, u = P' k, s = r + k.u,
+// beta = 1 / max(s, floor), e = v - M'^T k, M <- M' + beta u e^T,
+// P <- P' - beta u u^T, y = M^T q, with R = diag of [[c, -s], [s, c]] per
+// pair (c = rho cos, s = rho sin, rho = min(max(radius, tiny), 1)) and the
+// pair's process variance on entry (2k, 2k).  Lane (i, j) forms
+//   P'_ij = (P_ij R_ii R_jj + P_{i^1,j^1} R_{i,i^1} R_{j,j^1})
+//         + (P_{i,j^1} R_ii R_{j,j^1} + P_{i^1,j} R_{i,i^1} R_jj)
+// from three neighbours (quad exchange, half-row mirror + quad reversal, and
+// the exchange of that); the mirror lane (j, i) forms the same products and
+// sums them in the same pairs, so P stays bitwise symmetric.  The rotation
+// coefficients are computed once per token and pair as the tile is staged
+// (sin and cos by sincos_rad) and read from LDS per token.  The mean pair is
+// kept in the lane's own column order as in forward_kernel; its row mixing
+// is one quad exchange.
+struct RTile {
+  // k, q [TT][4], v / y [TT][8], (c0, s0, c1, s1) [TT][4], p [TT][2], r [TT].
+  static constexpr int K = 0, Q = 64, V = 128, CS = 256, PP = 320, R = 352, SEQ = 392, SIZE = SPW * SEQ;
+};
+
+template <int F = kInF32>
+__global__ __launch_bounds__(kWave) void rotation_forward_kernel(RotArgs a) {
+  __shared__ float tile[RTile::SIZE];
+  const int lane = threadIdx.x;
+  const int s = lane >> 4, c = lane & 15, i = c >> 2, j = c & 3;
+  const int co = 2 * i + (j & 1);
+  const bool odd = (j & 1) != 0;
+  // R_{i,i^1} = -s_i for an even row, +s_i for an odd one.
+  const float sgi = (i & 1) ? 1.f : -1.f, sgj = (j & 1) ? 1.f : -1.f;
+  // Process variance on the even diagonal entries only.
+  const bool qdiag = i == j && !(i & 1);
+  const int64_t n0 = static_cast<int64_t>(blockIdx.x) * SPW;
+  const int64_t T = a.t;
+  const uint32_t valid = static_cast<uint32_t>((a.n - n0) < SPW ? (a.n - n0) : SPW);
+  const uint32_t row4 = static_cast<uint32_t>(T) * 16u, row8 = static_cast<uint32_t>(T) * 32u,
+                 row2 = static_cast<uint32_t>(T) * 8u, row1 = static_cast<uint32_t>(T) * 4u;
+  const Rsrc rk = make_rsrc(a.k + n0 * T * 4, valid * row4);
+  const Rsrc rq = make_rsrc(a.q + n0 * T * 4, valid * row4);
+  const Rsrc rv = make_rsrc(a.v + n0 * T * 8, valid * row8);
+  const Rsrc ry = make_rsrc(a.y + n0 * T * 8, valid * row8);
+  const Rsrc rrad = make_rsrc(a.rad + n0 * T * 2, valid * row2);
+  const Rsrc rang = make_rsrc(a.ang + n0 * T * 2, valid * row2);
+  const Rsrc rp = make_rsrc(a.p + n0 * T * 2, valid * row2);
+  const Rsrc rr = make_rsrc(a.r + n0 * T, valid * row1);
+  const uint32_t nbp = static_cast<uint32_t>(a.nb + 1);
+  const Rsrc rbm = make_rsrc(a.bm + n0 * nbp * 32, valid * nbp * 128u);
+  const Rsrc rbc = make_rsrc(a.bc + n0 * nbp * 16, valid * nbp * 64u);
+  const Rsrc rm0 = make_rsrc(a.m0 + n0 * 32, valid * 128u);
+  const Rsrc rc0 = make_rsrc(a.c0 + n0 * 16, valid * 64u);
+  const Rsrc rmT = make_rsrc(a.mT + n0 * 32, valid * 128u);
+  const Rsrc rcT = make_rsrc(a.cT + n0 * 16, valid * 64u);
+  const uint32_t mo = static_cast<uint32_t>(s) * 128u + mean_off(i, j), cvo = static_cast<uint32_t>(s) * 64u + cov_off(i, j);
+  const uint32_t cmo = static_cast<uint32_t>(s) * nbp * 128u + mean_off(i, j),
+                 cco = static_cast<uint32_t>(s) * nbp * 64u + cov_off(i, j);
+
+  float P, M0, M1;
+  {
+    const v2f m = own_order(r4::ld64(rm0, mo, 0), odd);
+    M0 = m[0];
+    M1 = m[1];
+    P = r4::ld32(rc0, cvo, 0);
+  }
+  r4::vm_wait<0>();
+  auto store_ckpt = [&](uint32_t rec) __attribute__((always_inline)) {
+    v2f m;
+    m[0] = M0;
+    m[1] = M1;
+    r4::st64(rbm, own_order(m, odd), cmo, rec * 128u);
+    r4::st32(rbc, P, cco, rec * 64u);
+  };
+  store_ckpt(0);
+
+  // Staging: lane (s, c) moves token c's k / q piece, v pieces c and c + 16,
+  // for c < 8 the radius / angle / process piece of tokens 2c, 2c + 1 (two
+  // pairs each), and for c < 4 the observation piece of tokens 4c .. 4c + 3.
+  struct RStage {
+    v4f k, q, v0, v1, rad, ang, p, r;
+  };
+  auto load = [&](RStage& x, uint32_t t0) __attribute__((always_inline)) {
+    const uint32_t o4 = static_cast<uint32_t>(s) * row4 + (t0 + c) * 16u;
+    x.k = r4::ld128<true>(rk, o4);
+    x.q = r4::ld128<true>(rq, o4);
+    const uint32_t o8 = static_cast<uint32_t>(s) * row8 + t0 * 32u + c * 16u;
+    x.v0 = r4::ld128<true>(rv, o8);
+    x.v1 = r4::ld128<true>(rv, o8 + 256u);
+    const uint32_t o2 = c < 8 ? static_cast<uint32_t>(s) * row2 + t0 * 8u + c * 16u : kOob;
+    x.rad = r4::ld128<false>(rrad, o2);
+    x.ang = r4::ld128<false>(rang, o2);
+    x.p = r4::ld128<false>(rp, o2);
+    const uint32_t o1 = c < 4 ? static_cast<uint32_t>(s) * row1 + t0 * 4u + c * 16u : kOob;
+    x.r = r4::ld128<false>(rr, o1);
+  };
+  auto put = [&](const RStage& x) __attribute__((always_inline)) {
+    float* b = tile + s * RTile::SEQ;
+    *reinterpret_cast<v4f*>(b + RTile::K + 4 * c) = x.k;
+    *reinterpret_cast<v4f*>(b + RTile::Q + 4 * c) = x.q;
+    *reinterpret_cast<v4f*>(b + RTile::V + 4 * c) = x.v0;
+    *reinterpret_cast<v4f*>(b + RTile::V + 64 + 4 * c) = x.v1;
+    if (c < 8) {
+      // Coefficients of tokens 2c (pairs 0, 1) and 2c + 1, as bssm_rotation.hip forms them.
+      v4f cs[2];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float rc = fmaxf(x.rad[e], FLT_MIN);
+        const float rho = rc <= 1.f ? rc : 1.f;
+        float sa, ca;
+        sincos_rad(x.ang[e], sa, ca);
+        cs[e >> 1][2 * (e & 1)] = rho * ca;
+        cs[e >> 1][2 * (e & 1) + 1] = rho * sa;
+      }
+      *reinterpret_cast<v4f*>(b + RTile::CS + 8 * c) = cs[0];
+      *reinterpret_cast<v4f*>(b + RTile::CS + 8 * c + 4) = cs[1];
+      *reinterpret_cast<v4f*>(b + RTile::PP + 4 * c) = x.p;
+    }
+    if (c < 4) *reinterpret_cast<v4f*>(b + RTile::R + 4 * c) = x.r;
+  };
+
+  struct In {
+    float ki, kj, qj, p, r;
+    v2f v, csi, csj;  // (c, s) of the pairs of rows i and j
+  };
+  const float* mine = tile + s * RTile::SEQ;
+  auto read = [&](In& x, int tt) __attribute__((always_inline)) {
+    x.ki = mine[RTile::K + 4 * tt + i];
+    x.kj = mine[RTile::K + 4 * tt + j];
+    x.qj = mine[RTile::Q + 4 * tt + j];
+    x.v[0] = mine[RTile::V + 8 * tt + co];
+    x.v[1] = mine[RTile::V + 8 * tt + (co ^ 1)];
+    x.csi = *reinterpret_cast<const v2f*>(mine + RTile::CS + 4 * tt + 2 * (i >> 1));
+    x.csj = *reinterpret_cast<const v2f*>(mine + RTile::CS + 4 * tt + 2 * (j >> 1));
+    x.p = mine[RTile::PP + 2 * tt + (i >> 1)];
+    x.r = mine[RTile::R + tt];
+  };
+  auto step = [&](const In& x) __attribute__((always_inline)) {
+    const float Rii = x.csi[0], Rio = sgi * x.csi[1], Rjj = x.csj[0], Rjo = sgj * x.csj[1];
+    const float x1 = dpp<kXor1>(P);                   // P[i][j ^ 1]
+    const float x2 = dpp<kQuadRev>(dpp<kHalfMirror>(P));  // P[i ^ 1][j]
+    const float x3 = dpp<kXor1>(x2);                  // P[i ^ 1][j ^ 1]
+    const float Ps = (P * (Rii * Rjj) + x3 * (Rio * Rjo)) + (x1 * (Rii * Rjo) + x2 * (Rio * Rjj));
+    const float Pp = qdiag ? Ps + x.p : Ps;
+    const float zi = quad_sum(Pp * x.kj);  // u_i
+    const float zj = col_sum(Pp * x.ki);   // u_j, the same bits for i == j
+    const float sv = quad_sum(x.kj * zj) + x.r;
+    const float beta = fast_rcp(fmaxf(sv, a.floor));
+    // M' = R M: row j mixes with row j ^ 1, held by lane (i, j ^ 1) in swapped order.
+    const float Mp0 = fmaf(Rjo, dpp<kXor1>(M1), Rjj * M0);
+    const float Mp1 = fmaf(Rjo, dpp<kXor1>(M0), Rjj * M1);
+    const float so = own_sum(Mp0 * x.kj, Mp1 * x.kj);
+    const float e0 = x.v[0] - so;
+    const float e1 = x.v[1] - dpp<kXor1>(so);
+    const float bu = beta * zj;
+    M0 = fmaf(bu, e0, Mp0);
+    M1 = fmaf(bu, e1, Mp1);
+    P = fmaf(-beta, zi * zj, Pp);
+    return own_sum(M0 * x.qj, M1 * x.qj);
+  };
+
+  const int64_t ntiles = (T + TT - 1) / TT;
+  RStage x;
+  if (ntiles > 0) load(x, 0);
+  int64_t next_ckpt = a.chunk;
+  uint32_t ckpt = 1;
+  float* mw = tile + s * RTile::SEQ;
+  v4f ys0 = v4f{0.f, 0.f, 0.f, 0.f}, ys1 = ys0;
+  for (int64_t ti = 0; ti < ntiles; ++ti) {
+    const uint32_t t0 = static_cast<uint32_t>(ti * TT);
+    const int len = static_cast<int>((T - t0) < TT ? (T - t0) : TT);
+    if (ti > 0) {
+      ys0 = *reinterpret_cast<const v4f*>(mw + RTile::V + 4 * c);
+      ys1 = *reinterpret_cast<const v4f*>(mw + RTile::V + 64 + 4 * c);
+    }
+    r4::vm_wait<0>();
+    put(x);
+    if (ti > 0) {
+      const uint32_t o8 = static_cast<uint32_t>(s) * row8 + (t0 - TT) * 32u + c * 16u;
+      r4::st128<r4::kNtStore>(ry, ys0, o8, 0);
+      r4::st128<r4::kNtStore>(ry, ys1, o8 + 256u, 0);
+    }
+    if (ti + 1 < ntiles) load(x, t0 + TT);
+    r4::lds_wait();
+    if (len == TT && a.chunk % 8 == 0) {
+#pragma unroll
+      for (int h = 0; h < TT / 8; ++h) {
+        if (static_cast<int64_t>(t0) + 8 * h == next_ckpt) {
+          store_ckpt(ckpt++);
+          next_ckpt += a.chunk;
+        }
+        In cur, nxt;
+        read(cur, 8 * h);
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+          const int tt = 8 * h + u;
+          if (u + 1 < 8) read(nxt, tt + 1);
+          mw[RTile::V + 8 * tt + co] = step(cur);
+          cur = nxt;
+        }
+      }
+    } else {
+      for (int tt = 0; tt < len; ++tt) {
+        if (static_cast<int64_t>(t0) + tt == next_ckpt) {
+          store_ckpt(ckpt++);
+          next_ckpt += a.chunk;
+        }
+        In cur;
+        read(cur, tt);
+        mw[RTile::V + 8 * tt + co] = step(cur);
+      }
+    }
+  }
+  if (ntiles > 0) {
+    const uint32_t t0 = static_cast<uint32_t>((ntiles - 1) * TT);
+    const int len = static_cast<int>(T - t0);
+    r4::lds_wait();
+    ys0 = *reinterpret_cast<const v4f*>(mw + RTile::V + 4 * c);
+    ys1 = *reinterpret_cast<const v4f*>(mw + RTile::V + 64 + 4 * c);
+    const uint32_t o8 = static_cast<uint32_t>(s) * row8 + t0 * 32u + c * 16u;
+    r4::st128<r4::kNtStore>(ry, ys0, (c >> 1) < len ? o8 : kOob, 0);
+    r4::st128<r4::kNtStore>(ry, ys1, ((c + 16) >> 1) < len ? o8 + 256u : kOob, 0);
+  }
+  v2f m;
+  m[0] = M0;
+  m[1] = M1;
+  r4::st64(rmT, own_order(m, odd), mo, 0);
+  r4::st32(rcT, P, cvo, 0);
+  store_ckpt(static_cast<uint32_t>(a.nb));
 }
 
 // ----------------------------------------------------------------- backward
@@ -1578,7 +1807,7 @@ namespace {
 // forward up to 2048 (by 15 % at 1024 and below, 4 % at 2048), the
 // three-wave backward the one-wave one up to 2048 (30 %, 12 %; beyond that
 // its 50 KB of LDS per workgroup leave too few workgroups per CU).
-std::atomic<int64_t> g_small_limit[4] = {{24576}, {8192}, {2048}, {2048}};
+std::atomic<int64_t> g_small_limit[5] = {{24576}, {8192}, {2048}, {2048}, {14336}};
 }  // namespace
 
 int64_t small_batch_limit(int direction) { return g_small_limit[direction].load(std::memory_order_relaxed); }
@@ -1645,6 +1874,13 @@ hipError_t launch_backward_small(bool fixed, bool dyn, const BwdArgs& a, hipStre
   if (fixed) hipLaunchKernelGGL((sn::backward_kernel<true, false>), grid, block, 0, stream, a);
   else if (dyn) hipLaunchKernelGGL((sn::backward_kernel<false, true>), grid, block, 0, stream, a);
   else hipLaunchKernelGGL((sn::backward_kernel<false, false>), grid, block, 0, stream, a);
+  return hipGetLastError();
+}
+
+hipError_t launch_rotation_forward_small(const RotArgs& a, hipStream_t stream) {
+  const int64_t blocks = (a.n + sn::SPW - 1) / sn::SPW;
+  if (blocks == 0) return hipSuccess;
+  hipLaunchKernelGGL((sn::rotation_forward_kernel<>), dim3(static_cast<unsigned>(blocks)), dim3(kWave), 0, stream, a);
   return hipGetLastError();
 }
 

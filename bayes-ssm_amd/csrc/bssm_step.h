@@ -305,4 +305,30 @@ __device__ __forceinline__ void reverse_step(const TokenIn<D, M, G>& in, const R
   o.gr = DYN ? gs : 0.f;
 }
 
+// sin and cos of x without a library call (an outlined call makes the
+// caller save its live registers to scratch).  Cody-Waite reduction by pi/2
+// in double precision (pi/2 as a two-double sum; n x pi/2 is exact in the
+// fma for any |x| below 2^40), then the Taylor series on |r| <= pi/4:
+// sin to r^9 (next term below 7e-10 relative) and cos to r^10 (below 1.2e-10).
+__device__ __forceinline__ void sincos_rad(float x, float& s, float& c) {
+  const double xd = x;
+  const double n = rint(xd * 0.6366197723675814);
+  const double rd = fma(-n, 6.123233995736766e-17, fma(-n, 1.5707963267948966, xd));
+  const float r = static_cast<float>(rd), r2 = r * r;
+  float ps = 1.f / 362880.f;
+  ps = fmaf(ps, r2, -1.f / 5040.f);
+  ps = fmaf(ps, r2, 1.f / 120.f);
+  ps = fmaf(ps, r2, -1.f / 6.f);
+  const float sr = fmaf(r * r2, ps, r);
+  float pc = -1.f / 3628800.f;
+  pc = fmaf(pc, r2, 1.f / 40320.f);
+  pc = fmaf(pc, r2, -1.f / 720.f);
+  pc = fmaf(pc, r2, 1.f / 24.f);
+  pc = fmaf(pc, r2, -0.5f);
+  const float cr = fmaf(r2, pc, 1.f);
+  const int q = static_cast<int>(static_cast<int64_t>(n) & 3);
+  s = (q == 0) ? sr : (q == 1) ? cr : (q == 2) ? -sr : -cr;
+  c = (q == 0) ? cr : (q == 1) ? -sr : (q == 2) ? -cr : sr;
+}
+
 }  // namespace bssm

@@ -442,10 +442,12 @@ int bssm_rotation_checkpoint(int key_dim);
  * sequences, the covariance and mean halves (the covariance replay, the
  * covariance reverse and the mean) on separate SIMDs, bitwise the one-wave
  * results.  bf16 and float8 keys, values and queries (the _bf16 / _fp8 entry
- * points) take the row forward only up to direction 2's limit (widened on
- * chip, bitwise the float32 row forward on the widened values) and the
- * rotated-layout backward at every N.  Defaults: 24576, 8192, 2048, 2048, the
- * measured crossovers.
+ * points) take the row kernels only within the two-wave (three-wave) limits
+ * (widened on chip, bitwise the float32 split kernels on the widened values).
+ * Direction 4: the largest N for which the D = 4 rotation forward
+ * (bssm_forward_chunked_rotation) uses its row-per-sequence kernel (16-byte
+ * aligned streams, T a multiple of 4).  Defaults: 24576, 8192, 2048, 2048,
+ * 14336, the measured crossovers.
  * Sets the limit when limit >= 0 and returns the previous one; limit < 0
  * only reads it; -1 for any other direction.  Results of the row and
  * rotated layouts agree within float32 rounding, not bitwise.  No

@@ -11,8 +11,9 @@ from __future__ import annotations
 import contextlib
 
 BIG = 1 << 40
-# Limits (forward row, backward row, forward two-wave, backward three-wave) per layout.
-LAYOUTS = {"row": (BIG, BIG, 0, 0), "split": (BIG, BIG, BIG, BIG), "quad": (0, 0, 0, 0)}
+# Limits (forward row, backward row, forward two-wave, backward three-wave,
+# rotation forward row) per layout.
+LAYOUTS = {"row": (BIG, BIG, 0, 0, BIG), "split": (BIG, BIG, BIG, BIG, BIG), "quad": (0, 0, 0, 0, 0)}
 
 
 @contextlib.contextmanager

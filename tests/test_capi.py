@@ -199,8 +199,8 @@ def test_conv_backward_noalloc_rejects_sizes_beyond_its_scratch(lib):
 
 def test_small_batch_limits_read_set_restore(lib):
     """Forward and backward limits of the row-per-sequence D4 kernels: defaults, set, read, restore."""
-    old = [lib.bssm_small_batch_limit(d, -1) for d in range(4)]
-    assert old == [24576, 8192, 2048, 2048]
+    old = [lib.bssm_small_batch_limit(d, -1) for d in range(5)]
+    assert old == [24576, 8192, 2048, 2048, 14336]
     try:
         assert lib.bssm_small_batch_limit(0, 7) == old[0]
         assert lib.bssm_small_batch_limit(0, -1) == 7
@@ -209,8 +209,9 @@ def test_small_batch_limits_read_set_restore(lib):
         assert lib.bssm_small_batch_limit(1, -1) == 0
         assert lib.bssm_small_batch_limit(2, 3) == old[2] and lib.bssm_small_batch_limit(2, -1) == 3
         assert lib.bssm_small_batch_limit(3, 9) == old[3] and lib.bssm_small_batch_limit(3, -1) == 9
+        assert lib.bssm_small_batch_limit(4, 11) == old[4] and lib.bssm_small_batch_limit(4, -1) == 11
     finally:
-        for d in range(4):
+        for d in range(5):
             lib.bssm_small_batch_limit(d, old[d])
-    assert lib.bssm_small_batch_limit(4, 5) == -1 and lib.bssm_small_batch_limit(-1, -1) == -1
-    assert [lib.bssm_small_batch_limit(d, -1) for d in range(4)] == old
+    assert lib.bssm_small_batch_limit(5, 5) == -1 and lib.bssm_small_batch_limit(-1, -1) == -1
+    assert [lib.bssm_small_batch_limit(d, -1) for d in range(5)] == old

@@ -372,6 +372,33 @@ def test_config3_full_size_subset(cuda_device, d):
         close(leaves[i].grad[idx.to(cuda_device)], eg[i], "grad " + name)
 
 
+@pytest.mark.parametrize("b", [32, 2])
+def test_config3_per_gpu_share_subset(cuda_device, b):
+    """Config 3's batch divided over GPUs (B32: one GPU's share under 8-way data parallelism; B2 x H64 = 128
+    sequences), D4M8 at T512, through the autograd boundary: the default dispatch takes the split row kernels
+    (two-wave forward, three-wave backward); a seeded subset of sequences against the oracle."""
+    from bayes_ssm.fused_cuda import fused_diagonal_bayesian
+
+    n, t, d = b * 64, 512, 4
+    print(f"config3 share b={b}", flush=True)
+    k, v, q, dec, p, r, gy = O.make_inputs(n, t, d, seed=1)
+    leaves = [x.to(cuda_device).requires_grad_(True) for x in (k, v, q, dec, p, r)]
+    m0 = torch.zeros(n, d, 8, device=cuda_device)
+    c0 = torch.eye(d, device=cuda_device).expand(n, d, d).contiguous()
+    y, _, _ = fused_diagonal_bayesian(*leaves, m0, c0, chunk_length=64, denominator_floor=1e-6)
+    y.backward(gy.to(cuda_device))
+    torch.cuda.synchronize()
+    assert torch.isfinite(y).all()
+    idx = torch.tensor(sorted({0, 1, 3, 4, 63, 64, n // 2 + 5, n - 5, n - 2, n - 1}))
+    sub = [x[idx].double() for x in (k, v, q, dec, p, r)]
+    ey, _, _, eg = O.diagonal_grads(*sub, torch.zeros(len(idx), d, 8, dtype=torch.float64),
+                                    torch.eye(d, dtype=torch.float64).expand(len(idx), d, d).clone(),
+                                    gy[idx].double())
+    close(y[idx.to(cuda_device)], ey, "y")
+    for i, name in enumerate(("k", "v", "q", "d", "p", "r")):
+        close(leaves[i].grad[idx.to(cuda_device)], eg[i], "grad " + name)
+
+
 def test_config2_d1_full_size_subset(cuda_device):
     """Config 2 (B64 x T512 x H64, D1M8)."""
     from bayes_ssm.fused_cuda import fused_diagonal_bayesian

@@ -92,6 +92,43 @@ def test_rotation_abi_matches_oracle(cuda_device, d, n, t, chunk):
             close(bc[:, c], cc, f"bcov[{c}]")
 
 
+@pytest.mark.parametrize("lay", ["row", "quad"])
+# T multiple of 4 with aligned streams: the row-per-sequence forward (row) or
+# the quad-per-sequence one (quad) for D = 4.  Chunk 4 and the partial tiles
+# (T = 52, 36, 4, 8) take the row kernel's token-by-token path; n = 65 leaves
+# one sequence in the last wave of four.
+@pytest.mark.parametrize("n,t,chunk", [(5, 16, 0), (7, 52, 0), (9, 20, 4), (65, 36, 0), (3, 4, 0), (2, 8, 8)])
+def test_rotation_d4_forward_layouts(cuda_device, lay, n, t, chunk):
+    from bayes_ssm import _hip
+    from tests._layouts import layout
+
+    chunk = chunk or _hip.load().bssm_rotation_checkpoint(4)
+    print(f"rotation d4 layout={lay} n={n} t={t} chunk={chunk}", flush=True)
+    ins, gy, gmf, gcf = _case(n, t, 4, seed=300 + t + n)
+    with layout(lay):
+        y, mT, cT, bm, bc, grads = _run(ins, gy, gmf, gcf, chunk, cuda_device)
+    leaves = [x.double().requires_grad_(True) for x in ins]
+    ey, em, ec = O.run_rotation(*leaves, 1e-6)
+    close(y, ey, "y")
+    close(mT, em, "mean_T")
+    close(cT, ec, "cov_T")
+    assert torch.equal(cT, cT.transpose(-1, -2)), "cov_T not bitwise symmetric"
+    if t:
+        loss = (ey * gy.double()).sum() + (em * gmf.double()).sum() + (ec * gcf.double()).sum()
+        eg = torch.autograd.grad(loss, leaves)
+        names = ["gk", "gv", "gq", "g_radii", "g_angles", "g_process", "g_observation", "gm0", "gc0"]
+        for name, a, e in zip(names, grads, eg):
+            close(a, e, name)
+    with torch.no_grad():
+        for c in range(bm.shape[1]):
+            stop = min(c * chunk, t)
+            _, mc, cc = O.run_rotation(*(x.double()[:, :stop] for x in ins[:7]), ins[7].double(), ins[8].double(),
+                                       1e-6) if stop else (None, ins[7].double(), ins[8].double())
+            close(bm[:, c], mc, f"bmean[{c}]")
+            close(bc[:, c], cc, f"bcov[{c}]")
+            assert torch.equal(bc[:, c], bc[:, c].transpose(-1, -2)), f"bcov[{c}] not bitwise symmetric"
+
+
 def test_rotation_large_angles(cuda_device):
     """Angles of tens of radians: the kernels' own sin/cos reduction stays within tolerance."""
     ins, gy, gmf, gcf = _case(8, 24, 4, seed=7, angle_scale=40.0)
