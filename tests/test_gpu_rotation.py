@@ -195,19 +195,23 @@ def test_rotation_long_sequences(cuda_device, d):
         close(a, e, name)
 
 
-def test_rotation_config3_full_size_rows(cuda_device):
-    """Config 3's shape (16384 sequences x T512, D4M8) on the rotation kernels: rows run alone match the full
-    run's rows bit for bit (sequences are independent), and those rows match the oracle."""
+@pytest.mark.parametrize("lay", ["row", "quad"])
+def test_rotation_config3_full_size_rows(cuda_device, lay):
+    """Config 3's shape (16384 sequences x T512, D4M8) on the rotation kernels, the forward in either layout
+    (the default picks by sequence count, so both runs are pinned to one): rows run alone match the full run's
+    rows bit for bit (sequences are independent), and those rows match the oracle."""
     from bayes_ssm import _hip
+    from tests._layouts import layout
 
     d, n, t = 4, 256 * 64, 512
     chunk = _hip.load().bssm_rotation_checkpoint(d)
-    print("rotation config3 full size", flush=True)
+    print(f"rotation config3 full size layout={lay}", flush=True)
     ins, gy, gmf, gcf = _case(n, t, d, seed=733, angle_scale=1.0)
-    full = _run(ins, gy, gmf, gcf, chunk, cuda_device)
     rows = torch.tensor([0, 4097, 9999, n - 1])
     sub_ins = [x[rows].contiguous() for x in ins]
-    sub = _run(sub_ins, gy[rows], gmf[rows], gcf[rows], chunk, cuda_device)
+    with layout(lay):
+        full = _run(ins, gy, gmf, gcf, chunk, cuda_device)
+        sub = _run(sub_ins, gy[rows], gmf[rows], gcf[rows], chunk, cuda_device)
     rows_d = rows.to(cuda_device)
     for name, a, b in zip(("y", "mean_T", "cov_T", "bmean", "bcov"), sub[:5], full[:5]):
         assert torch.equal(a, b[rows_d]), f"{name}: subset rows differ from the full run"
