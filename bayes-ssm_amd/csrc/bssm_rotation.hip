@@ -34,10 +34,11 @@
 #include "bssm_rot4.h"
 #include "bssm_step.h"
 
-// No contraction: the four-term sums of P' would otherwise be fused as
-// fma(first product, second), which the owners of rows i and j evaluate with
-// the products in swapped roles, so P_ij and P_ji would differ in the last
-// bit.  Every intended fused multiply-add is an explicit fmaf.
+// No contraction (except in the reverse arithmetic of the backward): the
+// four-term sums of P' would otherwise be fused as fma(first product,
+// second), which the owners of rows i and j evaluate with the products in
+// swapped roles, so P_ij and P_ji would differ in the last bit.  Every
+// intended fused multiply-add is an explicit fmaf.
 #pragma clang fp contract(off)
 
 namespace bssm {
@@ -271,6 +272,9 @@ __device__ __forceinline__ void reverse_rot(const TokRot<D, M, G>& in, const Rot
                                             ColsArr<D, M, G>& gM, RowsArr<D, M, G>& Gs, float floor, int g,
                                             int lane, bool first_token, RowsArr<D, M, G>& gc0r,
                                             RotOut<D, M, G>& o) {
+  // The adjoint arithmetic may contract (the replayed P' comes from
+  // sandwich / step_rot, which do not, so it is bitwise the forward's).
+#pragma clang fp contract(fast)
   using L = Layout<D, M, G>;
   constexpr int RPL = L::RPL, CPL = L::CPL, J = D / 2;
   const bool writer = L::row_writer(g);
@@ -652,6 +656,7 @@ __device__ __forceinline__ void copy_rows(const float* src, float* dst, int lane
 
 template <int D, int M, int G, int SUB>
 __global__ __launch_bounds__(kWave) void backward_kernel(RotArgs a) {
+#pragma clang fp contract(fast)
   using L = Layout<D, M, G>;
   constexpr int SPW = L::SPW, RPL = L::RPL, CPL = L::CPL, J = D / 2;
   constexpr int SD = Tile<D, SUB>::STRIDE, SM = Tile<M, SUB>::STRIDE, SJ = Tile<J, SUB>::STRIDE,

@@ -1807,7 +1807,7 @@ namespace {
 // forward up to 2048 (by 15 % at 1024 and below, 4 % at 2048), the
 // three-wave backward the one-wave one up to 2048 (30 %, 12 %; beyond that
 // its 50 KB of LDS per workgroup leave too few workgroups per CU).
-std::atomic<int64_t> g_small_limit[5] = {{24576}, {8192}, {2048}, {2048}, {14336}};
+std::atomic<int64_t> g_small_limit[5] = {{24576}, {8192}, {2048}, {2048}, {32768}};
 }  // namespace
 
 int64_t small_batch_limit(int direction) { return g_small_limit[direction].load(std::memory_order_relaxed); }

@@ -447,7 +447,7 @@ int bssm_rotation_checkpoint(int key_dim);
  * Direction 4: the largest N for which the D = 4 rotation forward
  * (bssm_forward_chunked_rotation) uses its row-per-sequence kernel (16-byte
  * aligned streams, T a multiple of 4).  Defaults: 24576, 8192, 2048, 2048,
- * 14336, the measured crossovers.
+ * 32768, the measured crossovers.
  * Sets the limit when limit >= 0 and returns the previous one; limit < 0
  * only reads it; -1 for any other direction.  Results of the row and
  * rotated layouts agree within float32 rounding, not bitwise.  No

@@ -200,7 +200,7 @@ def test_conv_backward_noalloc_rejects_sizes_beyond_its_scratch(lib):
 def test_small_batch_limits_read_set_restore(lib):
     """Forward and backward limits of the row-per-sequence D4 kernels: defaults, set, read, restore."""
     old = [lib.bssm_small_batch_limit(d, -1) for d in range(5)]
-    assert old == [24576, 8192, 2048, 2048, 14336]
+    assert old == [24576, 8192, 2048, 2048, 32768]
     try:
         assert lib.bssm_small_batch_limit(0, 7) == old[0]
         assert lib.bssm_small_batch_limit(0, -1) == 7
