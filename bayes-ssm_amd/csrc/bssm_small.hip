@@ -837,11 +837,13 @@ __global__ __launch_bounds__(kWave) void rotation_forward_kernel(RotArgs a) {
   };
   store_ckpt(0);
 
-  // Staging: lane (s, c) moves token c's k / q piece, v pieces c and c + 16,
-  // for c < 8 the radius / angle / process piece of tokens 2c, 2c + 1 (two
-  // pairs each), and for c < 4 the observation piece of tokens 4c .. 4c + 3.
+  // Staging: lane (s, c) moves token c's k / q piece, radii and angles (and
+  // turns them into the rotation coefficients), v pieces c and c + 16, for
+  // c < 8 the process piece of tokens 2c, 2c + 1, and for c < 4 the
+  // observation piece of tokens 4c .. 4c + 3.
   struct RStage {
-    v4f k, q, v0, v1, rad, ang, p, r;
+    v4f k, q, v0, v1, p, r;
+    v2f rad, ang;
   };
   auto load = [&](RStage& x, uint32_t t0) __attribute__((always_inline)) {
     const uint32_t o4 = static_cast<uint32_t>(s) * row4 + (t0 + c) * 16u;
@@ -850,10 +852,10 @@ __global__ __launch_bounds__(kWave) void rotation_forward_kernel(RotArgs a) {
     const uint32_t o8 = static_cast<uint32_t>(s) * row8 + t0 * 32u + c * 16u;
     x.v0 = r4::ld128<true>(rv, o8);
     x.v1 = r4::ld128<true>(rv, o8 + 256u);
-    const uint32_t o2 = c < 8 ? static_cast<uint32_t>(s) * row2 + t0 * 8u + c * 16u : kOob;
-    x.rad = r4::ld128<false>(rrad, o2);
-    x.ang = r4::ld128<false>(rang, o2);
-    x.p = r4::ld128<false>(rp, o2);
+    const uint32_t o2 = static_cast<uint32_t>(s) * row2 + (t0 + c) * 8u;
+    x.rad = r4::ld64(rrad, o2, 0);
+    x.ang = r4::ld64(rang, o2, 0);
+    x.p = r4::ld128<false>(rp, c < 8 ? static_cast<uint32_t>(s) * row2 + t0 * 8u + c * 16u : kOob);
     const uint32_t o1 = c < 4 ? static_cast<uint32_t>(s) * row1 + t0 * 4u + c * 16u : kOob;
     x.r = r4::ld128<false>(rr, o1);
   };
@@ -863,22 +865,21 @@ __global__ __launch_bounds__(kWave) void rotation_forward_kernel(RotArgs a) {
     *reinterpret_cast<v4f*>(b + RTile::Q + 4 * c) = x.q;
     *reinterpret_cast<v4f*>(b + RTile::V + 4 * c) = x.v0;
     *reinterpret_cast<v4f*>(b + RTile::V + 64 + 4 * c) = x.v1;
-    if (c < 8) {
-      // Coefficients of tokens 2c (pairs 0, 1) and 2c + 1, as bssm_rotation.hip forms them.
-      v4f cs[2];
+    {
+      // Coefficients of token c's two pairs, as bssm_rotation.hip forms them.
+      v4f cs;
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
+      for (int e = 0; e < 2; ++e) {
         const float rc = fmaxf(x.rad[e], FLT_MIN);
         const float rho = rc <= 1.f ? rc : 1.f;
         float sa, ca;
         sincos_rad(x.ang[e], sa, ca);
-        cs[e >> 1][2 * (e & 1)] = rho * ca;
-        cs[e >> 1][2 * (e & 1) + 1] = rho * sa;
+        cs[2 * e] = rho * ca;
+        cs[2 * e + 1] = rho * sa;
       }
-      *reinterpret_cast<v4f*>(b + RTile::CS + 8 * c) = cs[0];
-      *reinterpret_cast<v4f*>(b + RTile::CS + 8 * c + 4) = cs[1];
-      *reinterpret_cast<v4f*>(b + RTile::PP + 4 * c) = x.p;
+      *reinterpret_cast<v4f*>(b + RTile::CS + 4 * c) = cs;
     }
+    if (c < 8) *reinterpret_cast<v4f*>(b + RTile::PP + 4 * c) = x.p;
     if (c < 4) *reinterpret_cast<v4f*>(b + RTile::R + 4 * c) = x.r;
   };
 
