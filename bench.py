@@ -10,7 +10,8 @@ softplus(N(0,1)); all six require grad (full 8-gradient ABI), gy ~ N(0,1).
 One step = the fused forward plus the full backward of
 ``bayes_ssm.fused_cuda.fused_diagonal_bayesian`` (inputs resident in HBM).
 Prints one JSON line.  ``--gpus`` above 1 is rejected: this build measures
-one GPU (sequences shard with no exchange).
+one GPU (sequences are independent, so a multi-GPU run would shard them
+with no exchange between GPUs).
 """
 from __future__ import annotations
 
