@@ -284,13 +284,24 @@ struct StepOut {
   v2f e;
 };
 
-// OWN: mean pair, values and innovations in the lane's own order.
-template <bool OWN>
-__device__ __forceinline__ void forward_step(Bel& b, const Tok& x, float delta, float floor, StepOut& o) {
-  const float wki = x.di * x.ki, wkj = x.dj * x.kj;
+// OWN: mean pair, values and innovations in the lane's own order.  TR: u_j
+// is read from the transposed lane (j, i) of the sequence (byte address tr
+// for ds_bpermute), whose u_i has the same bits as the column sum gives (P
+// is bitwise symmetric and col_sum pairs its terms as quad_sum does): one LDS
+// crossbar instruction in place of six VALU instructions.
+template <bool OWN, bool TR = false>
+__device__ __forceinline__ void forward_step(Bel& b, const Tok& x, float delta, float floor, StepOut& o,
+                                             int tr = 0) {
+  const float wkj = x.dj * x.kj;
   const float zi = quad_sum(b.P * wkj);  // (P (d * k))_i
-  const float zj = col_sum(b.P * wki);   // (P (d * k))_j, the same bits for i == j
-  const float ui = fmaf(x.di, zi, x.p * x.ki), uj = fmaf(x.dj, zj, x.p * x.kj);
+  const float ui = fmaf(x.di, zi, x.p * x.ki);
+  float uj;
+  if constexpr (TR) {
+    uj = __builtin_bit_cast(float, __builtin_amdgcn_ds_bpermute(tr, __builtin_bit_cast(int, ui)));
+  } else {
+    const float zj = col_sum(b.P * (x.di * x.ki));  // (P (d * k))_j, the same bits for i == j
+    uj = fmaf(x.dj, zj, x.p * x.kj);
+  }
   const float s = quad_sum(x.kj * uj) + x.r;
   const float beta = fast_rcp(fmaxf(s, floor));
   // Innovations of the lane's two columns: e = v - sum_j M[j][.] d_j k_j (in
@@ -330,6 +341,7 @@ __global__ __launch_bounds__(kWave) void forward_kernel(FwdArgs a) {
   const int lane = threadIdx.x;
   const int s = lane >> 4, c = lane & 15, i = c >> 2, j = c & 3;
   const int co = 2 * i + (j & 1);  // the lane's own value column
+  const int tr = 4 * (16 * s + 4 * j + i);  // ds_bpermute address of lane (j, i)
   const bool odd = (j & 1) != 0;
   const float delta = i == j ? 1.f : 0.f;
   const int64_t n0 = static_cast<int64_t>(blockIdx.x) * SPW;
@@ -419,7 +431,7 @@ __global__ __launch_bounds__(kWave) void forward_kernel(FwdArgs a) {
           const int tt = 8 * h + u;
           if (u + 1 < 8) read_tok<FIXED>(nxt, mine, tt + 1, i, j);
           StepOut o;
-          forward_step<true>(b, cur, delta, a.floor, o);
+          forward_step<true, true>(b, cur, delta, a.floor, o, tr);
           mine[Tile::V + 8 * tt + co] = readout(b, cur.qj);
           cur = nxt;
         }
@@ -433,7 +445,7 @@ __global__ __launch_bounds__(kWave) void forward_kernel(FwdArgs a) {
         Tok cur;
         read_tok<FIXED>(cur, mine, tt, i, j);
         StepOut o;
-        forward_step<true>(b, cur, delta, a.floor, o);
+        forward_step<true, true>(b, cur, delta, a.floor, o, tr);
         mine[Tile::V + 8 * tt + co] = readout(b, cur.qj);
       }
     }
@@ -792,6 +804,7 @@ __global__ __launch_bounds__(kWave) void rotation_forward_kernel(RotArgs a) {
   const int s = lane >> 4, c = lane & 15, i = c >> 2, j = c & 3;
   const int co = 2 * i + (j & 1);
   const bool odd = (j & 1) != 0;
+  const int tr = 4 * (16 * s + 4 * j + i);  // ds_bpermute address of lane (j, i)
   // R_{i,i^1} = -s_i for an even row, +s_i for an odd one.
   const float sgi = (i & 1) ? 1.f : -1.f, sgj = (j & 1) ? 1.f : -1.f;
   // Process variance on the even diagonal entries only.
@@ -884,12 +897,11 @@ __global__ __launch_bounds__(kWave) void rotation_forward_kernel(RotArgs a) {
   };
 
   struct In {
-    float ki, kj, qj, p, r;
+    float kj, qj, p, r;
     v2f v, csi, csj;  // (c, s) of the pairs of rows i and j
   };
   const float* mine = tile + s * RTile::SEQ;
   auto read = [&](In& x, int tt) __attribute__((always_inline)) {
-    x.ki = mine[RTile::K + 4 * tt + i];
     x.kj = mine[RTile::K + 4 * tt + j];
     x.qj = mine[RTile::Q + 4 * tt + j];
     x.v[0] = mine[RTile::V + 8 * tt + co];
@@ -907,7 +919,8 @@ __global__ __launch_bounds__(kWave) void rotation_forward_kernel(RotArgs a) {
     const float Ps = (P * (Rii * Rjj) + x3 * (Rio * Rjo)) + (x1 * (Rii * Rjo) + x2 * (Rio * Rjj));
     const float Pp = qdiag ? Ps + x.p : Ps;
     const float zi = quad_sum(Pp * x.kj);  // u_i
-    const float zj = col_sum(Pp * x.ki);   // u_j, the same bits for i == j
+    // u_j: u_i of the transposed lane (j, i), the bits of the column sum.
+    const float zj = __builtin_bit_cast(float, __builtin_amdgcn_ds_bpermute(tr, __builtin_bit_cast(int, zi)));
     const float sv = quad_sum(x.kj * zj) + x.r;
     const float beta = fast_rcp(fmaxf(sv, a.floor));
     // M' = R M: row j mixes with row j ^ 1, held by lane (i, j ^ 1) in swapped order.
