@@ -789,12 +789,16 @@ __global__ __launch_bounds__(2 * kWave) void forward_split_kernel(FwdArgs a) {
 // the exchange of that); the mirror lane (j, i) forms the same products and
 // sums them in the same pairs, so P stays bitwise symmetric.  The rotation
 // coefficients are computed once per token and pair as the tile is staged
-// (sin and cos by sincos_rad) and read from LDS per token.  The mean pair is
+// (sin and cos by sincos_rad) and stored with both signs of s, so that a lane
+// reads its row's (R_ii, R_{i,i^1}) as one pair; the process variances are
+// stored beside zeros, which the lanes off the even diagonal read (adding a
+// zero instead of selecting).  The mean pair is
 // kept in the lane's own column order as in forward_kernel; its row mixing
 // is one quad exchange.
 struct RTile {
-  // k, q [TT][4], v / y [TT][8], (c0, s0, c1, s1) [TT][4], p [TT][2], r [TT].
-  static constexpr int K = 0, Q = 64, V = 128, CS = 256, PP = 320, R = 352, SEQ = 392, SIZE = SPW * SEQ;
+  // k, q [TT][4], v / y [TT][8], (c0, -s0, c0, s0, c1, -s1, c1, s1) [TT][8],
+  // (p0, 0, p1, 0) [TT][4], r [TT]; sequences 8 banks apart (488 mod 32).
+  static constexpr int K = 0, Q = 64, V = 128, CS = 256, PP = 384, R = 448, SEQ = 488, SIZE = SPW * SEQ;
 };
 
 template <int F = kInF32>
@@ -805,10 +809,10 @@ __global__ __launch_bounds__(kWave) void rotation_forward_kernel(RotArgs a) {
   const int co = 2 * i + (j & 1);
   const bool odd = (j & 1) != 0;
   const int tr = 4 * (16 * s + 4 * j + i);  // ds_bpermute address of lane (j, i)
-  // R_{i,i^1} = -s_i for an even row, +s_i for an odd one.
-  const float sgi = (i & 1) ? 1.f : -1.f, sgj = (j & 1) ? 1.f : -1.f;
-  // Process variance on the even diagonal entries only.
-  const bool qdiag = i == j && !(i & 1);
+  // (R_ii, R_{i,i^1}) of row i: R_{i,i^1} = -s_i for an even row, +s_i for an odd one.
+  const int csi_off = 4 * (i >> 1) + 2 * (i & 1), csj_off = 4 * (j >> 1) + 2 * (j & 1);
+  // Process variance on the even diagonal entries only (the others read a zero).
+  const int p_off = (i == j && !(i & 1)) ? 2 * (i >> 1) : 1;
   const int64_t n0 = static_cast<int64_t>(blockIdx.x) * SPW;
   const int64_t T = a.t;
   const uint32_t valid = static_cast<uint32_t>((a.n - n0) < SPW ? (a.n - n0) : SPW);
@@ -880,25 +884,26 @@ __global__ __launch_bounds__(kWave) void rotation_forward_kernel(RotArgs a) {
     *reinterpret_cast<v4f*>(b + RTile::V + 64 + 4 * c) = x.v1;
     {
       // Coefficients of token c's two pairs, as bssm_rotation.hip forms them.
-      v4f cs;
 #pragma unroll
       for (int e = 0; e < 2; ++e) {
         const float rc = fmaxf(x.rad[e], FLT_MIN);
         const float rho = rc <= 1.f ? rc : 1.f;
         float sa, ca;
         sincos_rad(x.ang[e], sa, ca);
-        cs[2 * e] = rho * ca;
-        cs[2 * e + 1] = rho * sa;
+        const float cc = rho * ca, ss = rho * sa;
+        *reinterpret_cast<v4f*>(b + RTile::CS + 8 * c + 4 * e) = v4f{cc, -ss, cc, ss};
       }
-      *reinterpret_cast<v4f*>(b + RTile::CS + 4 * c) = cs;
     }
-    if (c < 8) *reinterpret_cast<v4f*>(b + RTile::PP + 4 * c) = x.p;
+    if (c < 8) {
+      *reinterpret_cast<v4f*>(b + RTile::PP + 8 * c) = v4f{x.p[0], 0.f, x.p[1], 0.f};
+      *reinterpret_cast<v4f*>(b + RTile::PP + 8 * c + 4) = v4f{x.p[2], 0.f, x.p[3], 0.f};
+    }
     if (c < 4) *reinterpret_cast<v4f*>(b + RTile::R + 4 * c) = x.r;
   };
 
   struct In {
     float kj, qj, p, r;
-    v2f v, csi, csj;  // (c, s) of the pairs of rows i and j
+    v2f v, csi, csj;  // (R_ii, R_{i,i^1}) and (R_jj, R_{j,j^1})
   };
   const float* mine = tile + s * RTile::SEQ;
   auto read = [&](In& x, int tt) __attribute__((always_inline)) {
@@ -906,18 +911,18 @@ __global__ __launch_bounds__(kWave) void rotation_forward_kernel(RotArgs a) {
     x.qj = mine[RTile::Q + 4 * tt + j];
     x.v[0] = mine[RTile::V + 8 * tt + co];
     x.v[1] = mine[RTile::V + 8 * tt + (co ^ 1)];
-    x.csi = *reinterpret_cast<const v2f*>(mine + RTile::CS + 4 * tt + 2 * (i >> 1));
-    x.csj = *reinterpret_cast<const v2f*>(mine + RTile::CS + 4 * tt + 2 * (j >> 1));
-    x.p = mine[RTile::PP + 2 * tt + (i >> 1)];
+    x.csi = *reinterpret_cast<const v2f*>(mine + RTile::CS + 8 * tt + csi_off);
+    x.csj = *reinterpret_cast<const v2f*>(mine + RTile::CS + 8 * tt + csj_off);
+    x.p = mine[RTile::PP + 4 * tt + p_off];
     x.r = mine[RTile::R + tt];
   };
   auto step = [&](const In& x) __attribute__((always_inline)) {
-    const float Rii = x.csi[0], Rio = sgi * x.csi[1], Rjj = x.csj[0], Rjo = sgj * x.csj[1];
+    const float Rii = x.csi[0], Rio = x.csi[1], Rjj = x.csj[0], Rjo = x.csj[1];
     const float x1 = dpp<kXor1>(P);                   // P[i][j ^ 1]
     const float x2 = dpp<kQuadRev>(dpp<kHalfMirror>(P));  // P[i ^ 1][j]
     const float x3 = dpp<kXor1>(x2);                  // P[i ^ 1][j ^ 1]
     const float Ps = (P * (Rii * Rjj) + x3 * (Rio * Rjo)) + (x1 * (Rii * Rjo) + x2 * (Rio * Rjj));
-    const float Pp = qdiag ? Ps + x.p : Ps;
+    const float Pp = Ps + x.p;
     const float zi = quad_sum(Pp * x.kj);  // u_i
     // u_j: u_i of the transposed lane (j, i), the bits of the column sum.
     const float zj = __builtin_bit_cast(float, __builtin_amdgcn_ds_bpermute(tr, __builtin_bit_cast(int, zi)));
