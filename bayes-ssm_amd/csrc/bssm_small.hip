@@ -918,9 +918,10 @@ __global__ __launch_bounds__(kWave) void rotation_forward_kernel(RotArgs a) {
   };
   auto step = [&](const In& x) __attribute__((always_inline)) {
     const float Rii = x.csi[0], Rio = x.csi[1], Rjj = x.csj[0], Rjo = x.csj[1];
-    const float x1 = dpp<kXor1>(P);                   // P[i][j ^ 1]
-    const float x2 = dpp<kQuadRev>(dpp<kHalfMirror>(P));  // P[i ^ 1][j]
-    const float x3 = dpp<kXor1>(x2);                  // P[i ^ 1][j ^ 1]
+    const float x1 = dpp<kXor1>(P);         // P[i][j ^ 1]
+    const float hm = dpp<kHalfMirror>(P);   // P[i ^ 1][3 - j]
+    const float x2 = dpp<kQuadRev>(hm);     // P[i ^ 1][j]
+    const float x3 = dpp<kXor2>(hm);        // P[i ^ 1][j ^ 1] (quad reversal, then exchange)
     const float Ps = (P * (Rii * Rjj) + x3 * (Rio * Rjo)) + (x1 * (Rii * Rjo) + x2 * (Rio * Rjj));
     const float Pp = Ps + x.p;
     const float zi = quad_sum(Pp * x.kj);  // u_i
@@ -929,8 +930,8 @@ __global__ __launch_bounds__(kWave) void rotation_forward_kernel(RotArgs a) {
     const float sv = quad_sum(x.kj * zj) + x.r;
     const float beta = fast_rcp(fmaxf(sv, a.floor));
     // M' = R M: row j mixes with row j ^ 1, held by lane (i, j ^ 1) in swapped order.
-    const float Mp0 = fmaf(Rjo, dpp<kXor1>(M1), Rjj * M0);
-    const float Mp1 = fmaf(Rjo, dpp<kXor1>(M0), Rjj * M1);
+    const float Mp0 = fmaf(Rjj, M0, dpp<kXor1>(M1) * Rjo);
+    const float Mp1 = fmaf(Rjj, M1, dpp<kXor1>(M0) * Rjo);
     const float so = own_sum(Mp0 * x.kj, Mp1 * x.kj);
     const float e0 = x.v[0] - so;
     const float e1 = x.v[1] - dpp<kXor1>(so);
