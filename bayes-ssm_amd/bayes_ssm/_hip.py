@@ -77,7 +77,7 @@ ABI_VERSION = 9
 
 _lock = threading.Lock()
 _lib: Optional[ctypes.CDLL] = None
-_load_error: Optional[BaseException] = None
+_load_error: Optional[Exception] = None
 
 
 class HipLibraryError(RuntimeError):
@@ -111,7 +111,7 @@ def load() -> ctypes.CDLL:
             version = lib.bssm_abi_version()
             if version != ABI_VERSION:
                 raise HipLibraryError(f"{path} has ABI {version}, expected {ABI_VERSION}; rebuild it")
-        except BaseException as exc:  # cache the failure, re-raise loudly every time
+        except Exception as exc:  # cache the failure, re-raise loudly every time
             _load_error = exc
             raise HipLibraryError(str(exc)) from exc
         _lib = lib

@@ -658,7 +658,9 @@ def bayesian_layer(
                     y, mean, cov = _loop_dense(*args, floor)
             outs.append(y)
         return torch.cat(outs, dim=-2), mean, cov
-    except BaseException:
+    except Exception:
+        # A failure inside the call: the value checks deferred so far may name its cause (a
+        # non-finite input), so they run first. Interrupts and exits propagate untouched.
         checks.flush()
         raise
 

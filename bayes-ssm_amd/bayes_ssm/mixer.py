@@ -44,6 +44,13 @@ NOISE_FLOOR = 1e-4  # softplus(noise) + 1e-4 (train_6layer.py:667-668)
 _WIDTHS = (KEY_DIM, KEY_DIM, VALUE_DIM, KEY_DIM, 2)
 
 
+def _aligned(x: Tensor) -> Tensor:
+    """``x`` contiguous with a 16-byte aligned base (the C ABI's requirement for weights, biases and belief
+    tensors): a contiguous view at an unaligned offset, e.g. a slice of a flattened parameter buffer, is copied."""
+    x = x.contiguous()
+    return x if x.data_ptr() % 16 == 0 else x.clone()
+
+
 def _row_stride(x: Tensor, t: int) -> Optional[int]:
     """Row stride (elements) of a [B, T, W] view the kernels can address, else None."""
     if x.ndim != 3 or x.stride(2) != 1:
@@ -168,7 +175,7 @@ def _initial_state(initial_mean: Optional[Tensor], initial_covariance: Optional[
         cov0 = torch.eye(KEY_DIM, device=device, dtype=torch.float32).expand(n, KEY_DIM, KEY_DIM)
     else:
         cov0 = initial_covariance.to(device=device, dtype=torch.float32).expand(n, KEY_DIM, KEY_DIM)
-    return mean0.contiguous(), cov0.contiguous()
+    return _aligned(mean0), _aligned(cov0)
 
 
 def mixer_layer_inputs(q_proj: Tensor, k_proj: Tensor, v_proj: Tensor, decay_logits: Tensor, noise: Tensor,
@@ -267,7 +274,7 @@ class _MixerReadoutFunction(torch.autograd.Function):
         cov_t = torch.empty(n, KEY_DIM, KEY_DIM, device=dev, dtype=torch.float32)
         bmean = torch.empty(n, nb + 1, KEY_DIM, VALUE_DIM, device=dev, dtype=torch.float32)
         bcov = torch.empty(n, nb + 1, KEY_DIM, KEY_DIM, device=dev, dtype=torch.float32)
-        w32 = norm_weight.detach().float().contiguous()
+        w32 = _aligned(norm_weight.detach().float())
         P = _hip.ptr
         with _hip.on_device(dev):
             _hip.call("bssm_mixer_gated_forward", P(q_proj), lds[0], P(k_proj), lds[1], P(v_proj), lds[2],
@@ -392,7 +399,7 @@ class _MixerBlockFunction(torch.autograd.Function):
         dev = projected.device
         # The kernels add the aux bias as they read the aux columns, in bf16
         # as the reference does (one rounding).
-        bias = None if aux_bias is None else aux_bias.detach().contiguous()
+        bias = None if aux_bias is None else _aligned(aux_bias.detach())
         convolved = torch.empty(b, t, core, device=dev, dtype=torch.bfloat16)
         out = torch.empty(b, t, heads * VALUE_DIM, device=dev, dtype=torch.bfloat16)
         read_bf16 = torch.empty_like(out)
@@ -401,8 +408,8 @@ class _MixerBlockFunction(torch.autograd.Function):
         cov_t = torch.empty(n, KEY_DIM, KEY_DIM, device=dev, dtype=torch.float32)
         bmean = torch.empty(n, nb + 1, KEY_DIM, VALUE_DIM, device=dev, dtype=torch.float32)
         bcov = torch.empty(n, nb + 1, KEY_DIM, KEY_DIM, device=dev, dtype=torch.float32)
-        cw32 = conv_weight.detach().reshape(core, 4).float().contiguous()
-        nw32 = norm_weight.detach().float().contiguous()
+        cw32 = _aligned(conv_weight.detach().reshape(core, 4).float())
+        nw32 = _aligned(norm_weight.detach().float())
         P = _hip.ptr
         with _hip.on_device(dev):
             _hip.call("bssm_mixer_block_forward", P(projected), ld, P(cw32), P(bias), P(nw32), float(norm_eps),
@@ -501,6 +508,10 @@ def bayes_mixer_block(
     """
     if projected.ndim != 3:
         raise ValueError("projected must have shape [B, T, width]")
+    if heads <= 0:
+        raise ValueError("heads must be positive")
+    if not (denominator_floor > 0):
+        raise ValueError("denominator_floor must be positive")
     state = heads * KEY_DIM
     width = heads * VALUE_DIM
     core = 2 * state + width

@@ -284,7 +284,9 @@ def associative_static_bayesian_cuda(keys: Tensor, values: Tensor, queries: Tens
                                                 flat(queries_p, (t, d)), flat(r2, (t,)), flat(mean0, (d, m)),
                                                 flat(cov0, (d, d)))
         checks.flush()
-    except BaseException:
+    except Exception:
+        # A failure inside the call: the value checks deferred so far may name its cause (a
+        # non-finite input), so they run first. Interrupts and exits propagate untouched.
         checks.flush()
         raise
     return out.reshape(*batch, t, m), mT.reshape(*batch, d, m), cT.reshape(*batch, d, d)

@@ -4,9 +4,17 @@
  * Every entry point takes raw device pointers (row-major, contiguous fp32),
  * sizes, scalar options and a HIP stream handle passed as `void*`
  * (a `hipStream_t`; NULL = the legacy default stream).  Nothing here
- * allocates device memory, synchronises the stream or keeps state between
- * calls, so every entry point is safe to call under HIP graph capture and
- * from several host threads (each call only enqueues kernels).
+ * allocates device memory or synchronises the stream, and each call only
+ * enqueues kernels.  Two exceptions to "keeps no state between calls":
+ *   - bssm_small_batch_limit() sets process-wide tuning limits that pick the
+ *     D = 4, M = 8 kernel layout for a sequence count (row-per-sequence or
+ *     rotated).  The layouts round differently, so changing a limit changes
+ *     the low bits of those results; set it once, before the calls whose
+ *     bits must be reproducible, not concurrently with them.
+ *   - bssm_causal_conv4_backward_noalloc() keeps its partial sums in one
+ *     device scratch array per GPU: calls that overlap on one GPU race.
+ * Every other entry point is safe under HIP graph capture and from several
+ * host threads at once.
  *
  * Return value: BSSM_OK (0) or a BSSM_ERR_* code; bssm_last_error() returns
  * the message of the most recent failure on the calling host thread.

@@ -194,9 +194,11 @@ def test_backward_matches_oracle(ext, cuda_device, abi, final_grads, chunk, t):
         assert torch.equal(grads[7], grads[7].transpose(-1, -2)), "gc0 must be bitwise symmetric"
 
 
-def test_long_sequence_matches_oracle(ext, cuda_device):
-    """T = 160 (20 checkpoint chunks): forward and full backward against the float64 oracle."""
-    n, t, chunk = 2, 160, 8
+@pytest.mark.parametrize("t", [160, 512])
+def test_long_sequence_matches_oracle(ext, cuda_device, t):
+    """T = 160 and T = 512 (the length bench.py times; 64 checkpoint chunks): forward and full backward against
+    the float64 oracle, with the symmetric initial-covariance adjoint of the D = 64 reference."""
+    n, chunk = 2, 8
     print(f"d64 long t={t}", flush=True)
     cpu, dev = _case(n, t, seed=99, device=cuda_device)
     ref = _f64(cpu)
@@ -215,9 +217,10 @@ def test_long_sequence_matches_oracle(ext, cuda_device):
         close(grads[i], eg[i], name)
 
 
-@pytest.mark.parametrize("t", [20, 16])
+@pytest.mark.parametrize("t", [20, 16, 512])
 def test_autograd_boundary(cuda_device, t):
-    """fused_diagonal_bayesian at D = M = 64 under autograd (checkpoint interval of the library)."""
+    """fused_diagonal_bayesian at D = M = 64 under autograd (checkpoint interval of the library), up to the
+    T = 512 that bench.py times."""
     from bayes_ssm.fused_cuda import fused_diagonal_bayesian
 
     n = 3
