@@ -193,124 +193,28 @@ __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(1, 1))) v
   core.store_ckpt(static_cast<uint32_t>(a.nb), rbm, rbc);
 }
 
-template <bool FIXED, bool DYN>
-__global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(1, 1))) void backward_kernel(BwdArgs a) {
-  __shared__ float ta[BwdTile::SIZE], tb[BwdTile::SIZE];
-  const int lane = threadIdx.x;
-  const int g = lane & 3, s = lane >> 2;
-  const int64_t n0 = static_cast<int64_t>(blockIdx.x) * SPW;
-  const int64_t T = a.t;
-  const uint32_t valid = static_cast<uint32_t>((a.n - n0) < SPW ? (a.n - n0) : SPW);
-  const uint32_t row4 = static_cast<uint32_t>(T) * 16u, row8 = static_cast<uint32_t>(T) * 32u,
-                 row1 = static_cast<uint32_t>(T) * 4u;
-  const Rsrc rk = make_rsrc(a.k + n0 * T * 4, valid * row4);
-  const Rsrc rq = make_rsrc(a.q + n0 * T * 4, valid * row4);
-  const Rsrc rv = make_rsrc(a.v + n0 * T * 8, valid * row8);
-  const Rsrc rgy = make_rsrc(a.gy + n0 * T * 8, valid * row8);
-  const Rsrc rd = make_rsrc(FIXED ? a.k : a.d + n0 * T * 4, valid * row4);
-  const Rsrc rp = make_rsrc(FIXED ? a.k : a.p + n0 * T, valid * row1);
-  const Rsrc rr = make_rsrc(FIXED ? a.k : a.r + n0 * T, valid * row1);
-  const Rsrc rgk = make_rsrc(a.gk + n0 * T * 4, valid * row4);
-  const Rsrc rgq = make_rsrc(a.gq + n0 * T * 4, valid * row4);
-  const Rsrc rgv = make_rsrc(a.gv + n0 * T * 8, valid * row8);
-  const Rsrc rgd = make_rsrc(a.gd ? a.gd + n0 * T * 4 : a.gk, a.gd ? valid * row4 : 0u);
-  const Rsrc rgp = make_rsrc(a.gp ? a.gp + n0 * T : a.gk, a.gp ? valid * row1 : 0u);
-  const Rsrc rgr = make_rsrc(a.gr ? a.gr + n0 * T : a.gk, a.gr ? valid * row1 : 0u);
-  const uint32_t nbp = static_cast<uint32_t>(a.nb + 1);
-  const Rsrc rbm = make_rsrc(a.bm + n0 * nbp * 32, valid * nbp * 128u);
-  const Rsrc rbc = make_rsrc(a.bc + n0 * nbp * 16, valid * nbp * 64u);
-
-  const Map mp(lane, row4, row8, row1);
-  const BelOff unit(s, g, 128u, 64u);
-  BwdCore<FIXED, DYN> core(s, g, a.floor);
-  core.init(a.gmf, a.gcf, a.m0, n0, valid, unit, s);
-
-  const RecOff ckoff(lane, nbp * 128u, nbp * 64u);
-  const int64_t nb = a.nb;
-
-  auto issue = [&](float* tl, int64_t c) __attribute__((always_inline)) {
-    const int64_t t0 = c * SUB;
-    const uint32_t s4 = static_cast<uint32_t>(t0) * 16u, s8 = static_cast<uint32_t>(t0) * 32u,
-                   s1 = static_cast<uint32_t>(t0) * 4u;
-#pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      dma16<kNtLoad>(rk, (tl + BwdTile::K) + 256 * j, mp.d4[j] + s4);
-      dma16<kNtLoad>(rq, (tl + BwdTile::Q) + 256 * j, mp.d4[j] + s4);
-      if constexpr (!FIXED) dma16<kNtLoad>(rd, (tl + BwdTile::D) + 256 * j, mp.d4[j] + s4);
-    }
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      dma16<kNtLoad>(rv, (tl + BwdTile::V) + 256 * j, mp.d8[j] + s8);
-      dma16<kNtLoad>(rgy, (tl + BwdTile::GY) + 256 * j, mp.d8[j] + s8);
-    }
-    if constexpr (!FIXED) {
-      dma16(rp, (tl + BwdTile::P), mp.d1 + s1);
-      dma16(rr, (tl + BwdTile::R), mp.d1 + s1);
-    }
-    const uint32_t cm = static_cast<uint32_t>(c) * 128u, cc = static_cast<uint32_t>(c) * 64u;
-    dma16<kNtCkpt>(rbm, (tl + BwdTile::CK), ckoff.m0 + cm);
-    dma16<kNtCkpt>(rbm, (tl + BwdTile::CK) + 256, ckoff.m1 + cm);
-    dma16(rbc, (tl + BwdTile::CK) + 512, ckoff.c + cc);
-  };
-
-  auto store_grads = [&](const float* tl, int64_t c, int len) __attribute__((always_inline)) {
-    const int64_t t0 = c * SUB;
-    const uint32_t s4 = static_cast<uint32_t>(t0) * 16u, s8 = static_cast<uint32_t>(t0) * 32u,
-                   s1 = static_cast<uint32_t>(t0) * 4u;
-#pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      const uint32_t off = mp.t4[j] < len ? mp.d4[j] : kOob;
-      const int e = (64 * j + lane) * 4;
-      st128<kNtStore>(rgk, *reinterpret_cast<const v4f*>(&(tl + BwdTile::K)[e]), off, s4);
-      st128<kNtStore>(rgq, *reinterpret_cast<const v4f*>(&(tl + BwdTile::Q)[e]), off, s4);
-      if (a.gd) st128<kNtStore>(rgd, *reinterpret_cast<const v4f*>(&(tl + BwdTile::D)[e]), off, s4);
-    }
-#pragma unroll
-    for (int j = 0; j < 4; ++j)
-      st128<kNtStore>(rgv, *reinterpret_cast<const v4f*>(&(tl + BwdTile::V)[(64 * j + lane) * 4]),
-            mp.t8[j] < len ? mp.d8[j] : kOob, s8);
-    const uint32_t off1 = mp.t1 < len ? mp.d1 : kOob;
-    if (a.gp) st128(rgp, *reinterpret_cast<const v4f*>(&(tl + BwdTile::P)[lane * 4]), off1, s1);
-    if (a.gr) st128(rgr, *reinterpret_cast<const v4f*>(&(tl + BwdTile::R)[lane * 4]), off1, s1);
-  };
-
-  auto chunk_len = [&](int64_t c) __attribute__((always_inline)) {
-    return static_cast<int>((T - c * SUB) < SUB ? (T - c * SUB) : SUB);
-  };
-  // Chunk c = nb - 1 - i is processed in slot i % 2.  At its start every
-  // outstanding memory operation was issued a whole chunk earlier, so the
-  // full wait is short: then the gradients of chunk c + 1 leave the other
-  // slot, which receives chunk c - 1 while chunk c is replayed and reversed.
-  auto run_chunk = [&](float* cur, float* other, int64_t c) __attribute__((always_inline)) {
-    vm_wait<0>();
-    Bel b;
-    bel_from_lds(b, cur + BwdTile::CK, s, g);
-    if (c + 1 < nb) store_grads(other, c + 1, chunk_len(c + 1));
-    if (c > 0) issue(other, c - 1);
-    core.run(cur, b, chunk_len(c));
-  };
-
-  if (nb > 0) issue(ta, nb - 1);
-  for (int64_t i = 0; i < nb; i += 2) {
-    run_chunk(ta, tb, nb - 1 - i);
-    if (i + 1 < nb) run_chunk(tb, ta, nb - 2 - i);
-  }
-  if (nb > 0) store_grads((nb - 1) % 2 == 0 ? ta : tb, 0, chunk_len(0));
-  core.store_initial(a.gm0, a.gc0, n0, valid, unit);
-}
-
-// ------------------------------------------------------ bf16-input backward
-// Keys, values and queries arrive as bfloat16 and their gradients leave as
-// bfloat16 (round to nearest even); everything else is float32.  A 16-token
-// tile (chunks 2J, 2J + 1) is staged in registers while the previous tile is
-// replayed and reversed from LDS, as in the forward: the bf16 pieces are
-// widened into the same float32 slot layout the float32 backward uses, and
-// the gradient pieces are narrowed on the way out.  Checkpoint records
-// arrive by LDS-DMA into their chunk's slot once its chunk has read its own.
+// ------------------------------------------- register-staged tile backward
+// A 16-token tile (chunks 2J, 2J + 1) is staged in registers while the
+// previous tile is replayed and reversed from LDS; at the tile boundary the
+// gradients of the finished tile leave LDS for registers, the staged inputs
+// take their place, and the gradients are stored.  Float32 streams (all of
+// them for F = float32; d and gy otherwise) move as whole 16-token row
+// segments per instruction (TileMap).  With bfloat16 or float8 keys, values
+// and queries those three arrive in their format and are widened into the
+// same float32 slot layout, and their gradients are narrowed on the way out
+// (bf16: round to nearest even; float8: torch's rounding).  Checkpoint
+// records arrive by LDS-DMA into their chunk's slot once its chunk has read
+// its own.
 //
 // bf16 piece maps (16-byte pieces, 16-token tile starting at t0):
 //   k, q: row 8I + (l & 7), tokens t0 + 2 (l >> 3) and + 1 (I < 2)
 //   v:    row 4I + (l & 3), token t0 + (l >> 2) (I < 4)
+struct BwdStageF {
+  v4f k[4], q[4], v[8], d[4], gy[8], p, r;
+};
+struct BwdOutF {
+  v4f k[4], q[4], v[8], d[4], p, r;
+};
 struct BwdStageH {
   v4f k[2], q[2], v[4], d[4], gy[8], p, r;
 };
@@ -325,12 +229,12 @@ struct BwdOutQ {
   v4f k, q, v[2], d[4], p, r;
 };
 
-// F: kInBf16, kInE4M3 or kInE5M2 (keys, queries, values and their gradients).
+// F: format of keys, values, queries and their gradients (InFmt).
 template <bool FIXED, bool DYN, int F>
-__global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(1, 1))) void backward_bf16_kernel(
+__global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(1, 1))) void backward_tile_kernel(
     BwdArgs a) {
-  constexpr bool Q8 = F >= kInE4M3;
-  constexpr uint32_t kb = Q8 ? 4u : 2u;  // float32 row bytes per stream row byte
+  constexpr bool Q8 = F >= kInE4M3, W = F == kInF32;
+  constexpr uint32_t kb = Q8 ? 4u : W ? 1u : 2u;  // float32 row bytes per stream row byte
   __shared__ float tile[2 * BwdTile::SIZE];
   const int lane = threadIdx.x;
   const int g = lane & 3, s = lane >> 2;
@@ -358,13 +262,9 @@ __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(1, 1))) v
   const Rsrc rbm = make_rsrc(a.bm + n0 * nbp * 32, valid * nbp * 128u);
   const Rsrc rbc = make_rsrc(a.bc + n0 * nbp * 16, valid * nbp * 64u);
 
-  const Map mp(lane, row4, row8, row1);
+  const TileMap tm(lane, row4, row8, row1);
   const HalfMap hm(lane, BwdTile::SIZE, row4h, row8h);
   const QuarterMap qm(lane, BwdTile::SIZE, row4h, row8h);
-  // p and r: one instruction per 16-token tile, lane -> row lane >> 2, piece
-  // lane & 3 (tokens 4 (lane & 3) .. + 3), into the chunk slot of its tokens.
-  const uint32_t off1 = static_cast<uint32_t>(lane >> 2) * row1 + static_cast<uint32_t>(lane & 3) * 16u;
-  const int dst1 = ((lane & 3) >> 1) * BwdTile::SIZE + 4 * (2 * (lane >> 2) + (lane & 1));
 
   const BelOff unit(s, g, 128u, 64u);
   BwdCore<FIXED, DYN> core(s, g, a.floor);
@@ -373,12 +273,24 @@ __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(1, 1))) v
   const int64_t nb = a.nb;
   const int64_t ntiles = (nb + 1) / 2;
 
-  using Stage = std::conditional_t<Q8, BwdStageQ, BwdStageH>;
-  using Out = std::conditional_t<Q8, BwdOutQ, BwdOutH>;
+  using Stage = std::conditional_t<W, BwdStageF, std::conditional_t<Q8, BwdStageQ, BwdStageH>>;
+  using Out = std::conditional_t<W, BwdOutF, std::conditional_t<Q8, BwdOutQ, BwdOutH>>;
   auto load = [&](Stage& x, int64_t J) __attribute__((always_inline)) {
     const int64_t t0 = J * 2 * SUB;
     const uint32_t sk = static_cast<uint32_t>(t0 * e4), sv = static_cast<uint32_t>(t0 * e8);
-    if constexpr (Q8) {
+    const uint32_t s4 = static_cast<uint32_t>(t0) * 16u, s8 = static_cast<uint32_t>(t0) * 32u;
+    // Pieces of tokens at or past T (a partial last tile) are not requested.
+    const bool full = t0 + 2 * SUB <= T;
+    const bool in4 = full || t0 + tm.t4 < T, in8 = full || t0 + tm.t8 < T, in1 = full || t0 + tm.t1 < T;
+    if constexpr (W) {
+#pragma unroll
+      for (int I = 0; I < 4; ++I) {
+        x.k[I] = ld128<kNtLoad>(rk, in4 ? tm.o4[I] : kOob, s4);
+        x.q[I] = ld128<kNtLoad>(rq, in4 ? tm.o4[I] : kOob, s4);
+      }
+#pragma unroll
+      for (int I = 0; I < 8; ++I) x.v[I] = ld128<kNtLoad>(rv, in8 ? tm.o8[I] : kOob, s8);
+    } else if constexpr (Q8) {
       x.k = ld128<kNtLoad>(rk, qm.k_off + sk);
       x.q = ld128<kNtLoad>(rq, qm.k_off + sk);
 #pragma unroll
@@ -392,24 +304,28 @@ __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(1, 1))) v
 #pragma unroll
       for (int I = 0; I < 4; ++I) x.v[I] = ld128<kNtLoad>(rv, hm.v_off[I] + sv);
     }
+    if constexpr (!FIXED) {
 #pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      const uint32_t s4 = static_cast<uint32_t>(t0 + SUB * h) * 16u, s8 = static_cast<uint32_t>(t0 + SUB * h) * 32u;
-      if constexpr (!FIXED) {
-#pragma unroll
-        for (int j = 0; j < 2; ++j) x.d[2 * h + j] = ld128<kNtLoad>(rd, mp.d4[j] + s4);
-      }
-#pragma unroll
-      for (int j = 0; j < 4; ++j) x.gy[4 * h + j] = ld128<kNtLoad>(rgy, mp.d8[j] + s8);
+      for (int I = 0; I < 4; ++I) x.d[I] = ld128<kNtLoad>(rd, in4 ? tm.o4[I] : kOob, s4);
     }
+#pragma unroll
+    for (int I = 0; I < 8; ++I) x.gy[I] = ld128<kNtLoad>(rgy, in8 ? tm.o8[I] : kOob, s8);
     if constexpr (!FIXED) {
       const uint32_t s1 = static_cast<uint32_t>(t0) * 4u;
-      x.p = ld128<false>(rp, off1 + s1);
-      x.r = ld128<false>(rr, off1 + s1);
+      x.p = ld128<false>(rp, in1 ? tm.o1 : kOob, s1);
+      x.r = ld128<false>(rr, in1 ? tm.o1 : kOob, s1);
     }
   };
   auto put = [&](const Stage& x) __attribute__((always_inline)) {
-    if constexpr (Q8) {
+    if constexpr (W) {
+#pragma unroll
+      for (int I = 0; I < 4; ++I) {
+        *reinterpret_cast<v4f*>(&tile[BwdTile::K + tm.s4[I]]) = x.k[I];
+        *reinterpret_cast<v4f*>(&tile[BwdTile::Q + tm.s4[I]]) = x.q[I];
+      }
+#pragma unroll
+      for (int I = 0; I < 8; ++I) *reinterpret_cast<v4f*>(&tile[BwdTile::V + tm.s8[I]]) = x.v[I];
+    } else if constexpr (Q8) {
       const v4u wk = __builtin_bit_cast(v4u, x.k), wq = __builtin_bit_cast(v4u, x.q);
 #pragma unroll
       for (int u = 0; u < 4; ++u) {
@@ -436,19 +352,15 @@ __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(1, 1))) v
         *reinterpret_cast<v4f*>(&tile[BwdTile::V + hm.v_lds[I][1]]) = widen_hi(x.v[I]);
       }
     }
-#pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      float* tl = tile + h * BwdTile::SIZE;
-      if constexpr (!FIXED) {
-#pragma unroll
-        for (int j = 0; j < 2; ++j) *reinterpret_cast<v4f*>(&(tl + BwdTile::D)[256 * j + 4 * lane]) = x.d[2 * h + j];
-      }
-#pragma unroll
-      for (int j = 0; j < 4; ++j) *reinterpret_cast<v4f*>(&(tl + BwdTile::GY)[256 * j + 4 * lane]) = x.gy[4 * h + j];
-    }
     if constexpr (!FIXED) {
-      *reinterpret_cast<v4f*>(&tile[BwdTile::P + dst1]) = x.p;
-      *reinterpret_cast<v4f*>(&tile[BwdTile::R + dst1]) = x.r;
+#pragma unroll
+      for (int I = 0; I < 4; ++I) *reinterpret_cast<v4f*>(&tile[BwdTile::D + tm.s4[I]]) = x.d[I];
+    }
+#pragma unroll
+    for (int I = 0; I < 8; ++I) *reinterpret_cast<v4f*>(&tile[BwdTile::GY + tm.s8[I]]) = x.gy[I];
+    if constexpr (!FIXED) {
+      *reinterpret_cast<v4f*>(&tile[BwdTile::P + tm.s1]) = x.p;
+      *reinterpret_cast<v4f*>(&tile[BwdTile::R + tm.s1]) = x.r;
     }
   };
   // Checkpoint record c into the CK region of slot tl, once the LDS reads of
@@ -461,7 +373,15 @@ __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(1, 1))) v
     dma16(rbc, (tl + BwdTile::CK) + 512, ckoff.c + cc);
   };
   auto take = [&](Out& o) __attribute__((always_inline)) {
-    if constexpr (Q8) {
+    if constexpr (W) {
+#pragma unroll
+      for (int I = 0; I < 4; ++I) {
+        o.k[I] = *reinterpret_cast<const v4f*>(&tile[BwdTile::K + tm.s4[I]]);
+        o.q[I] = *reinterpret_cast<const v4f*>(&tile[BwdTile::Q + tm.s4[I]]);
+      }
+#pragma unroll
+      for (int I = 0; I < 8; ++I) o.v[I] = *reinterpret_cast<const v4f*>(&tile[BwdTile::V + tm.s8[I]]);
+    } else if constexpr (Q8) {
       v4u wk, wq;
 #pragma unroll
       for (int u = 0; u < 4; ++u) {
@@ -491,18 +411,25 @@ __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(1, 1))) v
                         *reinterpret_cast<const v4f*>(&tile[BwdTile::V + hm.v_lds[I][1]]));
     }
 #pragma unroll
-    for (int h = 0; h < 2; ++h)
-#pragma unroll
-      for (int j = 0; j < 2; ++j)
-        o.d[2 * h + j] = *reinterpret_cast<const v4f*>(&(tile + h * BwdTile::SIZE + BwdTile::D)[256 * j + 4 * lane]);
-    o.p = *reinterpret_cast<const v4f*>(&tile[BwdTile::P + dst1]);
-    o.r = *reinterpret_cast<const v4f*>(&tile[BwdTile::R + dst1]);
+    for (int I = 0; I < 4; ++I) o.d[I] = *reinterpret_cast<const v4f*>(&tile[BwdTile::D + tm.s4[I]]);
+    o.p = *reinterpret_cast<const v4f*>(&tile[BwdTile::P + tm.s1]);
+    o.r = *reinterpret_cast<const v4f*>(&tile[BwdTile::R + tm.s1]);
   };
   // Gradients of tile J; pieces of tokens at or past T are dropped.
   auto store_grads = [&](const Out& o, int64_t J) __attribute__((always_inline)) {
     const int64_t t0 = J * 2 * SUB;
     const uint32_t sk = static_cast<uint32_t>(t0 * e4), sv = static_cast<uint32_t>(t0 * e8);
-    if constexpr (Q8) {
+    const uint32_t s4 = static_cast<uint32_t>(t0) * 16u, s8 = static_cast<uint32_t>(t0) * 32u;
+    const bool in4 = t0 + tm.t4 < T, in8 = t0 + tm.t8 < T;
+    if constexpr (W) {
+#pragma unroll
+      for (int I = 0; I < 4; ++I) {
+        st128<kNtStore>(rgk, o.k[I], in4 ? tm.o4[I] : kOob, s4);
+        st128<kNtStore>(rgq, o.q[I], in4 ? tm.o4[I] : kOob, s4);
+      }
+#pragma unroll
+      for (int I = 0; I < 8; ++I) st128<kNtStore>(rgv, o.v[I], in8 ? tm.o8[I] : kOob, s8);
+    } else if constexpr (Q8) {
       const bool kin = t0 + qm.k_tok < T, vin = t0 + qm.v_tok < T;
       st128<kNtStore>(rgk, o.k, kin ? qm.k_off : kOob, sk);
       st128<kNtStore>(rgq, o.q, kin ? qm.k_off : kOob, sk);
@@ -520,15 +447,9 @@ __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(1, 1))) v
     }
     if (a.gd) {
 #pragma unroll
-      for (int h = 0; h < 2; ++h) {
-        const int64_t th = t0 + SUB * h;
-        const int len = static_cast<int>((T - th) < SUB ? (T - th) : SUB);
-        const uint32_t s4 = static_cast<uint32_t>(th) * 16u;
-#pragma unroll
-        for (int j = 0; j < 2; ++j) st128<kNtStore>(rgd, o.d[2 * h + j], mp.t4[j] < len ? mp.d4[j] : kOob, s4);
-      }
+      for (int I = 0; I < 4; ++I) st128<kNtStore>(rgd, o.d[I], in4 ? tm.o4[I] : kOob, s4);
     }
-    const uint32_t offp = t0 + 4 * (lane & 3) < T ? off1 : kOob, s1 = static_cast<uint32_t>(t0) * 4u;
+    const uint32_t offp = t0 + tm.t1 < T ? tm.o1 : kOob, s1 = static_cast<uint32_t>(t0) * 4u;
     if (a.gp) st128(rgp, o.p, offp, s1);
     if (a.gr) st128(rgr, o.r, offp, s1);
   };
@@ -607,21 +528,21 @@ hipError_t launch_backward_r4(bool fixed, bool dyn, const BwdArgs& a, hipStream_
   if (blocks == 0) return hipSuccess;
   const dim3 grid(static_cast<unsigned>(blocks)), block(kWave);
   if (a.in_fmt == kInBf16) {
-    if (fixed) hipLaunchKernelGGL((r4::backward_bf16_kernel<true, false, kInBf16>), grid, block, 0, stream, a);
-    else if (dyn) hipLaunchKernelGGL((r4::backward_bf16_kernel<false, true, kInBf16>), grid, block, 0, stream, a);
-    else hipLaunchKernelGGL((r4::backward_bf16_kernel<false, false, kInBf16>), grid, block, 0, stream, a);
+    if (fixed) hipLaunchKernelGGL((r4::backward_tile_kernel<true, false, kInBf16>), grid, block, 0, stream, a);
+    else if (dyn) hipLaunchKernelGGL((r4::backward_tile_kernel<false, true, kInBf16>), grid, block, 0, stream, a);
+    else hipLaunchKernelGGL((r4::backward_tile_kernel<false, false, kInBf16>), grid, block, 0, stream, a);
   } else if (a.in_fmt == kInE4M3) {
-    if (fixed) hipLaunchKernelGGL((r4::backward_bf16_kernel<true, false, kInE4M3>), grid, block, 0, stream, a);
-    else if (dyn) hipLaunchKernelGGL((r4::backward_bf16_kernel<false, true, kInE4M3>), grid, block, 0, stream, a);
-    else hipLaunchKernelGGL((r4::backward_bf16_kernel<false, false, kInE4M3>), grid, block, 0, stream, a);
+    if (fixed) hipLaunchKernelGGL((r4::backward_tile_kernel<true, false, kInE4M3>), grid, block, 0, stream, a);
+    else if (dyn) hipLaunchKernelGGL((r4::backward_tile_kernel<false, true, kInE4M3>), grid, block, 0, stream, a);
+    else hipLaunchKernelGGL((r4::backward_tile_kernel<false, false, kInE4M3>), grid, block, 0, stream, a);
   } else if (a.in_fmt == kInE5M2) {
-    if (fixed) hipLaunchKernelGGL((r4::backward_bf16_kernel<true, false, kInE5M2>), grid, block, 0, stream, a);
-    else if (dyn) hipLaunchKernelGGL((r4::backward_bf16_kernel<false, true, kInE5M2>), grid, block, 0, stream, a);
-    else hipLaunchKernelGGL((r4::backward_bf16_kernel<false, false, kInE5M2>), grid, block, 0, stream, a);
+    if (fixed) hipLaunchKernelGGL((r4::backward_tile_kernel<true, false, kInE5M2>), grid, block, 0, stream, a);
+    else if (dyn) hipLaunchKernelGGL((r4::backward_tile_kernel<false, true, kInE5M2>), grid, block, 0, stream, a);
+    else hipLaunchKernelGGL((r4::backward_tile_kernel<false, false, kInE5M2>), grid, block, 0, stream, a);
   } else {
-    if (fixed) hipLaunchKernelGGL((r4::backward_kernel<true, false>), grid, block, 0, stream, a);
-    else if (dyn) hipLaunchKernelGGL((r4::backward_kernel<false, true>), grid, block, 0, stream, a);
-    else hipLaunchKernelGGL((r4::backward_kernel<false, false>), grid, block, 0, stream, a);
+    if (fixed) hipLaunchKernelGGL((r4::backward_tile_kernel<true, false, kInF32>), grid, block, 0, stream, a);
+    else if (dyn) hipLaunchKernelGGL((r4::backward_tile_kernel<false, true, kInF32>), grid, block, 0, stream, a);
+    else hipLaunchKernelGGL((r4::backward_tile_kernel<false, false, kInF32>), grid, block, 0, stream, a);
   }
   return hipGetLastError();
 }

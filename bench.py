@@ -96,6 +96,22 @@ def cpu_model() -> str:
     return "unknown CPU"
 
 
+def _settle(step, warmup: int, min_ms: float = 40.0) -> None:
+    """Warm-up calls of a secondary workload's step: at least `warmup`, and after the first call (whose host
+    work, new shapes and new allocations can leave the device idle for over 10 ms) enough back-to-back calls to
+    keep the device busy for `min_ms`.  An idle of 10 ms or more sends the next ~20 steps through a
+    power-management dip of up to 25 %; the timed calls then start at the sustained rate."""
+    step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    step()
+    torch.cuda.synchronize()
+    per = time.perf_counter() - t0
+    for _ in range(max(warmup, int(min_ms * 1e-3 / max(per, 1e-5)) + 1)):
+        step()
+    torch.cuda.synchronize()
+
+
 def time_layer(b, t, h, d, m, chunk, steps, warmup, device, kqv_dtype=None) -> dict:
     """fwd+bwd of fused_diagonal_bayesian at one shape: ms/step, tokens/s, step roofline fraction.
 
@@ -111,9 +127,7 @@ def time_layer(b, t, h, d, m, chunk, steps, warmup, device, kqv_dtype=None) -> d
         y, _, _ = fused_cuda.fused_diagonal_bayesian(*leaves, m0, c0, chunk_length=chunk, denominator_floor=1e-6)
         return torch.autograd.grad(y, leaves, gy)
 
-    for _ in range(warmup):
-        step()
-    torch.cuda.synchronize()
+    _settle(step, warmup)
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     e0.record()
     for _ in range(steps):
@@ -185,9 +199,7 @@ def time_mixer(b, t, h, steps, warmup, device, fused=True, gated=False) -> dict:
                 out = (out * F.silu(gate.view(b, t, h, 8))).reshape(b, t, h * 8)
         return torch.autograd.grad(out, leaves, gy)
 
-    for _ in range(warmup):
-        step()
-    torch.cuda.synchronize()
+    _settle(step, warmup)
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     e0.record()
     for _ in range(steps):
@@ -231,9 +243,7 @@ def time_block(b, t, h, steps, warmup, device) -> dict:
         out, _, _ = bayes_mixer_block(leaves[0], leaves[1], leaves[2], heads=h, aux_bias=leaves[3])
         return torch.autograd.grad(out, leaves, gy)
 
-    for _ in range(warmup):
-        step()
-    torch.cuda.synchronize()
+    _settle(step, warmup)
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     e0.record()
     for _ in range(steps):
@@ -269,9 +279,7 @@ def time_conv(b, t, c, steps, warmup, device, fused=True) -> dict:
         out = (m(xv) if fused else _taps_formula(xv, m.weight)).transpose(1, 2)
         return torch.autograd.grad(out, (value, m.weight), gy)
 
-    for _ in range(warmup):
-        step()
-    torch.cuda.synchronize()
+    _settle(step, warmup)
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     e0.record()
     for _ in range(steps):
@@ -319,9 +327,7 @@ def time_rotation(b, t, h, d, steps, warmup, device, fused=True) -> dict:
                                                observation_variances=r, chunk_length=64, optimized=True)
             return torch.autograd.grad(y, leaves, gy)
 
-        for _ in range(warmup):
-            step()
-        torch.cuda.synchronize()
+        _settle(step, warmup)
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         e0.record()
         for _ in range(steps):
@@ -373,9 +379,7 @@ def time_d64(b, t, h, steps, warmup, device, fused=True) -> dict:
                                                observation_variances=r, chunk_length=64, optimized=True)
             return torch.autograd.grad(y, leaves, gy)
 
-        for _ in range(warmup):
-            step()
-        torch.cuda.synchronize()
+        _settle(step, warmup)
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         e0.record()
         for _ in range(steps):
@@ -391,6 +395,21 @@ def time_d64(b, t, h, steps, warmup, device, fused=True) -> dict:
     return {"B": b, "T": t, "H": h, "D": d, "M": d, "sequences": n, "ms_per_step": ms,
             "tokens_per_s": b * t / (ms * 1e-3),
             "path": "HIP D64 kernels" if fused else "reference diagonal core, eager torch"}
+
+
+def _single_launch_us(launch, iters: int) -> float:
+    """Median device time of one launch (microseconds): each launch and its two events are queued behind a
+    device-side delay, so the events bracket the kernel(s) alone, not the host's launch rate."""
+    times = []
+    for _ in range(iters):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda._sleep(200_000)
+        e0.record()
+        launch()
+        e1.record()
+        torch.cuda.synchronize()
+        times.append(e0.elapsed_time(e1) * 1e3)
+    return sorted(times)[len(times) // 2]
 
 
 def time_scan(b, t, d, m, iters, device) -> dict:
@@ -423,12 +442,7 @@ def time_scan(b, t, d, m, iters, device) -> dict:
     args = (P(k), P(v), P(q), P(r), P(m0), P(c0), P(out), P(mT), P(cT), b, t, d, m, _hip.stream_of(device))
     _hip.call("bssm_associative_static_scan", *args)
     torch.cuda.synchronize()
-    e0.record()
-    for _ in range(iters):
-        _hip.call("bssm_associative_static_scan", *args)
-    e1.record()
-    torch.cuda.synchronize()
-    kernel_us = e0.elapsed_time(e1) / iters * 1e3
+    kernel_us = _single_launch_us(lambda: _hip.call("bssm_associative_static_scan", *args), iters)
     # fwd+bwd through the API (HIP forward and HIP backward), all six inputs as leaves.
     leaves = [x.clone().requires_grad_(True) for x in (k, v, q, r, m0, c0)]
     gy = torch.randn(b, t, m, device=device, generator=g)
@@ -454,14 +468,10 @@ def time_scan(b, t, d, m, iters, device) -> dict:
              _hip.stream_of(device))
     _hip.call("bssm_associative_static_scan_backward", *bargs)
     torch.cuda.synchronize()
-    e0.record()
-    for _ in range(iters):
-        _hip.call("bssm_associative_static_scan_backward", *bargs)
-    e1.record()
-    torch.cuda.synchronize()
+    bwd_us = _single_launch_us(lambda: _hip.call("bssm_associative_static_scan_backward", *bargs), iters)
     return {"B": b, "T": t, "D": d, "M": m, "api_us_per_call": api_us, "kernel_us_per_call": kernel_us,
-            "api_fwd_bwd_us_per_step": step_us,
-            "backward_kernels_us_per_call": e0.elapsed_time(e1) / iters * 1e3}
+            "api_fwd_bwd_us_per_step": step_us, "backward_kernels_us_per_call": bwd_us,
+            "kernel_timing": "events around one launch queued behind a device-side delay (median of the calls)"}
 
 
 def cpu_baseline(t: int, d: int, m: int, heads: int, budget_s: float) -> dict:
@@ -508,7 +518,8 @@ def main() -> int:
     ap.add_argument("--heads", type=int, default=64)
     ap.add_argument("--key-dim", type=int, default=4)
     ap.add_argument("--chunk", type=int, default=64)
-    ap.add_argument("--kernel-iters", type=int, default=20, help="iterations of the per-kernel event timing")
+    ap.add_argument("--kernel-iters", type=int, default=50,
+                    help="launches of each kernel alone (event-timed, before the warmup steps)")
     ap.add_argument("--cpu-budget", type=float, default=20.0, help="seconds of CPU-baseline work (0 = skip)")
     ap.add_argument("--no-extras", action="store_true",
                     help="skip the secondary shapes (per-GPU DP shape, D1/D2/D8 variants, associative scan)")
@@ -519,8 +530,6 @@ def main() -> int:
                          "on the q/k/v stream, the rotation core, D = M = 64, or the layer with bf16 / float8 "
                          "k/v/q tensors), for "
                          "profiling its kernels; prints its own JSON line")
-    ap.add_argument("--copy-calibration", action="store_true",
-                    help="also run one 256 MiB device copy (reference kernel for PMC byte counters)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: the layer shards over sequences with no exchange, "
@@ -554,49 +563,48 @@ def main() -> int:
         return 0
     n = b * h
     leaves, m0, c0, gy = make_workload(b, t, h, d, m, device)
-    copy_gbs = None
-    if args.copy_calibration:
-        # A plain 256 MiB device copy (64 Mi floats read + 64 Mi written): the
-        # reference kernel for scaling the PMC byte counters, and the measured
-        # streaming bandwidth of this device next to the 8 TB/s spec peak.
-        src = torch.randn(64 << 20, device=device)
-        dst = torch.empty_like(src)
-        dst.copy_(src)
-        torch.cuda.synchronize()
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        e0.record()
-        for _ in range(10):
-            dst.copy_(src)
-        e1.record()
-        torch.cuda.synchronize()
-        copy_gbs = 2 * src.numel() * 4 / (e0.elapsed_time(e1) / 10 * 1e-3) / 1e9
-        del src, dst
 
     def step():
         y, _, _ = fused_cuda.fused_diagonal_bayesian(*leaves, m0, c0, chunk_length=args.chunk,
                                                      denominator_floor=1e-6)
         return torch.autograd.grad(y, leaves, gy)
 
-    for _ in range(args.warmup):
-        step()
+    # 0. One call of the step as setup: its first-call host work (autograd's
+    #    device threads, the ctypes bindings, the caching allocator's blocks)
+    #    takes longer than 10 ms, and an idle device for 10 ms or more sends
+    #    the next ~20 steps of this workload through a power-management dip
+    #    (up to 25 % slower per step; per-step times in profiles/).  Done here,
+    #    that idle precedes the ~30 ms of calibration work below instead of the
+    #    warmup and timed steps.
+    step()
     torch.cuda.synchronize()
-    start = torch.cuda.Event(enable_timing=True)
-    stop = torch.cuda.Event(enable_timing=True)
-    start.record()
-    for _ in range(args.steps):
-        step()
-    stop.record()
-    torch.cuda.synchronize()
-    ms_per_step = start.elapsed_time(stop) / args.steps
-    tokens_per_s = b * t / (ms_per_step * 1e-3)
 
-    # Per-kernel timing with events on the launch stream (torch's current stream).
+    # 1. Streaming ceiling of this device: a plain 256 MiB device copy (64 Mi
+    #    floats read + 64 Mi written), also the reference kernel for scaling
+    #    the PMC byte counters.
+    src = torch.randn(64 << 20, device=device)
+    dst = torch.empty_like(src)
+    dst.copy_(src)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(20):
+        dst.copy_(src)
+    e1.record()
+    torch.cuda.synchronize()
+    copy_gbs = 2 * src.numel() * 4 / (e0.elapsed_time(e1) / 20 * 1e-3) / 1e9
+    del src, dst
+
+    # 2. Each kernel alone: --kernel-iters back-to-back launches of the
+    #    forward, then of the backward, through the extension object, with
+    #    events on the launch stream (torch's current stream).  These loops
+    #    (about 30 ms of device work) run before the warmup steps.
     ext = fused_cuda._load_extension(d)
     interval = fused_cuda._checkpoint_interval(d, t, args.chunk)
     raw = [x.detach() for x in leaves]
     fwd_out = ext.forward_chunked(*raw, m0, c0, interval, 1e-6)
     bm, bc = fwd_out[3], fwd_out[4]
-    ev = [torch.cuda.Event(enable_timing=True) for _ in range(4)]
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(3)]
     torch.cuda.synchronize()
     ev[0].record()
     for _ in range(args.kernel_iters):
@@ -606,8 +614,35 @@ def main() -> int:
         ext.backward_chunked(*raw, m0, c0, bm, bc, gy, None, None, interval, 1e-6)
     ev[2].record()
     torch.cuda.synchronize()
-    fwd_ms = ev[0].elapsed_time(ev[1]) / args.kernel_iters
-    bwd_ms = ev[1].elapsed_time(ev[2]) / args.kernel_iters
+    iso_fwd_ms = ev[0].elapsed_time(ev[1]) / args.kernel_iters
+    iso_bwd_ms = ev[1].elapsed_time(ev[2]) / args.kernel_iters
+    del fwd_out, bm, bc
+
+    # 3. W warmup steps, then exactly K timed steps.  Inside the timed region
+    #    an event marks each step's start, the end of its forward (the
+    #    forward kernel's launch is the only device work between the two) and
+    #    its end (the backward kernel), all on the launch stream: the in-step
+    #    kernel times behind the roofline figures.
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    marks = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(args.steps)]
+    start = torch.cuda.Event(enable_timing=True)
+    stop = torch.cuda.Event(enable_timing=True)
+    start.record()
+    for i in range(args.steps):
+        marks[i][0].record()
+        y, _, _ = fused_cuda.fused_diagonal_bayesian(*leaves, m0, c0, chunk_length=args.chunk,
+                                                     denominator_floor=1e-6)
+        marks[i][1].record()
+        torch.autograd.grad(y, leaves, gy)
+        marks[i][2].record()
+    stop.record()
+    torch.cuda.synchronize()
+    ms_per_step = start.elapsed_time(stop) / args.steps
+    tokens_per_s = b * t / (ms_per_step * 1e-3)
+    fwd_ms = sum(mk[0].elapsed_time(mk[1]) for mk in marks) / args.steps
+    bwd_ms = sum(mk[1].elapsed_time(mk[2]) for mk in marks) / args.steps
     fwd_b, bwd_b = algorithmic_bytes(d, m)
     units = n * t
     bwd_gbs = bwd_b * units / (bwd_ms * 1e-3) / 1e9
@@ -654,11 +689,15 @@ def main() -> int:
             "traffic": traffic,
             "bytes_per_launch": bwd_b * units,
             "avg_launch_ms": bwd_ms,
+            "timing": "events around the backward of each timed step, on its launch stream",
+            "isolated_launch_ms": iso_bwd_ms,
         },
         "roofline_forward": {"kernel": fwd_kernel, "achieved": fwd_gbs, "frac": fwd_gbs * 1e9 / HBM_PEAK,
-                             "avg_launch_ms": fwd_ms, "bytes_per_launch": fwd_b * units},
+                             "avg_launch_ms": fwd_ms, "bytes_per_launch": fwd_b * units,
+                             "isolated_launch_ms": iso_fwd_ms},
         "roofline_step_frac": step_frac,
         "measured_copy_gbs": copy_gbs,
+        "step_frac_of_measured_copy": (fwd_b + bwd_b) * units / (ms_per_step * 1e-3) / (copy_gbs * 1e9),
         "device": torch.cuda.get_device_name(device),
         "hip_library": str(_hip.LIB_PATH.relative_to(ROOT)),
     }
