@@ -169,11 +169,12 @@ int backward_impl(const char* fn, bool fixed, bool dyn, int d, int m, const floa
   a.vec_v = vec_flag_fmt(values, t, m, fmt) && vec_flag(gy, t, m) && vec_flag_fmt(o.gv, t, m, fmt);
   a.vec_pr = (fixed || (vec_flag(process, t, 1) && vec_flag(observation, t, 1))) && vec_flag(o.gp, t, 1) &&
              vec_flag(o.gr, t, 1);
-  a.rot4 = chunk == bssm::kRot4Chunk &&
+  a.rot4 = (chunk == bssm::kRot4Chunk || chunk == 2 * bssm::kRot4Chunk) &&
            rot4_ok(d, m, t, a.nb, a.vec_kqd && a.vec_v && a.vec_pr, {bmean, bcov, gmf, gcf, o.gm0, o.gc0});
   if (fmt != bssm::kInF32 && !a.rot4 && n > 0)
     return fail(BSSM_ERR_UNSUPPORTED, "%s: %s inputs need D = 4, M = 8, T a positive multiple of 4, "
-                "checkpoint chunk %d and 16-byte aligned streams", fn, fmt_name(fmt), bssm::kRot4Chunk);
+                "checkpoint chunk %d or %d and 16-byte aligned streams", fn, fmt_name(fmt), bssm::kRot4Chunk,
+                2 * bssm::kRot4Chunk);
   if (n == 0) return ok();
   return launched(fn, bssm::launch_backward(d, fixed, dyn, a, static_cast<hipStream_t>(stream)));
 }

@@ -81,7 +81,9 @@ hipError_t launch_backward_saved(int key_dim, bool dynamics_grads, const BwdArgs
 // D = 4, M = 8 kernels with the rotated per-lane layout (bssm_rot4.hip).
 // Preconditions (checked by the C ABI, recorded in rot4): 16-byte aligned
 // streams, T a positive multiple of 4, 8-byte aligned belief tensors, and for
-// the backward a checkpoint chunk of exactly kRot4Chunk tokens.
+// the backward a checkpoint chunk of kRot4Chunk tokens (a record per chunk)
+// or 2 * kRot4Chunk (a record per 16-token tile; the tile's second chunk
+// starts from the belief advanced on chip over its first 8 tokens).
 constexpr int kRot4Chunk = 8;
 hipError_t launch_forward_r4(bool fixed, const FwdArgs& a, hipStream_t stream);
 hipError_t launch_backward_r4(bool fixed, bool dyn, const BwdArgs& a, hipStream_t stream);

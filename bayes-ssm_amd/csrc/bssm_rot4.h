@@ -946,6 +946,20 @@ struct BwdCore {
       __builtin_amdgcn_sched_barrier(0);
     }
   }
+  // Advance the belief over the 8 tokens of a slot without keeping history
+  // (the start of a tile's second chunk when one record covers 16 tokens).
+  __device__ __forceinline__ void advance(const float* tl, Bel& b) const {
+    Tok x[SUB];
+    read_tok(tl, 0, x[0]);
+#pragma unroll
+    for (int tt = 0; tt < SUB; ++tt) {
+      if (tt + 1 < SUB) read_tok(tl, tt + 1, x[tt + 1]);
+      __builtin_amdgcn_sched_barrier(0);
+      StepOut o;
+      forward_step(b, x[tt], floor, o);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  }
   // A chunk of `len` tokens (SUB, or 4 for the last one of T = 8n + 4).
   __device__ __forceinline__ void run(float* tl, Bel& b, int len) {
     if (len == SUB) process<SUB>(tl, b);

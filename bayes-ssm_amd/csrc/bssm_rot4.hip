@@ -229,10 +229,13 @@ struct BwdOutQ {
   v4f k, q, v[2], d[4], p, r;
 };
 
-// F: format of keys, values, queries and their gradients (InFmt).
-template <bool FIXED, bool DYN, int F>
+// F: format of keys, values, queries and their gradients (InFmt).  IV:
+// checkpoint interval, 8 (a record per chunk slot) or 16 (a record per tile:
+// the tile's second chunk starts from the belief advanced over its first).
+template <bool FIXED, bool DYN, int F, int IV>
 __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(1, 1))) void backward_tile_kernel(
     BwdArgs a) {
+  static_assert(IV == SUB || IV == 2 * SUB, "checkpoint interval of one or two chunk slots");
   constexpr bool Q8 = F >= kInE4M3, W = F == kInF32;
   constexpr uint32_t kb = Q8 ? 4u : W ? 1u : 2u;  // float32 row bytes per stream row byte
   __shared__ float tile[2 * BwdTile::SIZE];
@@ -270,8 +273,9 @@ __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(1, 1))) v
   BwdCore<FIXED, DYN> core(s, g, a.floor);
   core.init(a.gmf, a.gcf, a.m0, n0, valid, unit, s);
   const RecOff ckoff(lane, nbp * 128u, nbp * 64u);
-  const int64_t nb = a.nb;
-  const int64_t ntiles = (nb + 1) / 2;
+  const int64_t nb = a.nb;                    // checkpoint chunks of IV tokens
+  const int64_t nsub = (T + SUB - 1) / SUB;   // chunk slots of SUB tokens
+  const int64_t ntiles = (nsub + 1) / 2;
 
   using Stage = std::conditional_t<W, BwdStageF, std::conditional_t<Q8, BwdStageQ, BwdStageH>>;
   using Out = std::conditional_t<W, BwdOutF, std::conditional_t<Q8, BwdOutQ, BwdOutH>>;
@@ -464,6 +468,22 @@ __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(1, 1))) v
     if (c >= 2) issue_ck(tl, c - 2);
     core.run(tl, b, chunk_len(c));
   };
+  // Tile J with one record (interval 16, in slot 0's checkpoint region): the
+  // second chunk starts from the record advanced over the first chunk's 8
+  // tokens, the first from the record itself; the region then receives the
+  // record of tile J - 1.
+  auto run_tile16 = [&](int64_t J) __attribute__((always_inline)) {
+    if (2 * J + 1 < nsub) {
+      Bel b;
+      bel_from_lds(b, tile + BwdTile::CK, s, g);
+      core.advance(tile, b);
+      core.run(tile + BwdTile::SIZE, b, chunk_len(2 * J + 1));
+    }
+    Bel b0;
+    bel_from_lds(b0, tile + BwdTile::CK, s, g);
+    if (J > 0) issue_ck(tile, J - 1);
+    core.run(tile, b0, chunk_len(2 * J));
+  };
 
   // Tiles run from the last to the first.  At the start of tile J every
   // outstanding load was issued during tile J + 1 and is awaited; the
@@ -472,9 +492,13 @@ __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(1, 1))) v
   // and chunks 2J + 1 and 2J replayed and reversed.
   Stage st;
   load(st, ntiles - 1);
-  issue_ck(tile, 2 * (ntiles - 1));
-  if (2 * ntiles - 1 < nb) issue_ck(tile + BwdTile::SIZE, 2 * ntiles - 1);
-  else if (ntiles > 1) issue_ck(tile + BwdTile::SIZE, 2 * ntiles - 3);
+  if constexpr (IV == SUB) {
+    issue_ck(tile, 2 * (ntiles - 1));
+    if (2 * ntiles - 1 < nb) issue_ck(tile + BwdTile::SIZE, 2 * ntiles - 1);
+    else if (ntiles > 1) issue_ck(tile + BwdTile::SIZE, 2 * ntiles - 3);
+  } else {
+    issue_ck(tile, ntiles - 1);
+  }
   for (int64_t J = ntiles - 1; J >= 0; --J) {
     Out go;
     vm_wait<0>();
@@ -485,8 +509,12 @@ __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(1, 1))) v
     if (J + 1 < ntiles) store_grads(go, J + 1);
     if (J > 0) load(st, J - 1);
     __builtin_amdgcn_sched_barrier(0);
-    if (2 * J + 1 < nb) run_chunk(tile + BwdTile::SIZE, 2 * J + 1);
-    run_chunk(tile, 2 * J);
+    if constexpr (IV == SUB) {
+      if (2 * J + 1 < nb) run_chunk(tile + BwdTile::SIZE, 2 * J + 1);
+      run_chunk(tile, 2 * J);
+    } else {
+      run_tile16(J);
+    }
   }
   {
     Out go;
@@ -523,28 +551,41 @@ hipError_t launch_forward_r4(bool fixed, const FwdArgs& a, hipStream_t stream) {
   return hipGetLastError();
 }
 
+template <int IV>
+hipError_t launch_backward_r4_iv(bool fixed, bool dyn, const BwdArgs& a, hipStream_t stream) {
+  const int64_t blocks = (a.n + r4::SPW - 1) / r4::SPW;
+  const dim3 grid(static_cast<unsigned>(blocks)), block(kWave);
+  switch (a.in_fmt) {
+    case kInBf16:
+      if (fixed) hipLaunchKernelGGL((r4::backward_tile_kernel<true, false, kInBf16, IV>), grid, block, 0, stream, a);
+      else if (dyn) hipLaunchKernelGGL((r4::backward_tile_kernel<false, true, kInBf16, IV>), grid, block, 0, stream, a);
+      else hipLaunchKernelGGL((r4::backward_tile_kernel<false, false, kInBf16, IV>), grid, block, 0, stream, a);
+      break;
+    case kInE4M3:
+      if (fixed) hipLaunchKernelGGL((r4::backward_tile_kernel<true, false, kInE4M3, IV>), grid, block, 0, stream, a);
+      else if (dyn) hipLaunchKernelGGL((r4::backward_tile_kernel<false, true, kInE4M3, IV>), grid, block, 0, stream, a);
+      else hipLaunchKernelGGL((r4::backward_tile_kernel<false, false, kInE4M3, IV>), grid, block, 0, stream, a);
+      break;
+    case kInE5M2:
+      if (fixed) hipLaunchKernelGGL((r4::backward_tile_kernel<true, false, kInE5M2, IV>), grid, block, 0, stream, a);
+      else if (dyn) hipLaunchKernelGGL((r4::backward_tile_kernel<false, true, kInE5M2, IV>), grid, block, 0, stream, a);
+      else hipLaunchKernelGGL((r4::backward_tile_kernel<false, false, kInE5M2, IV>), grid, block, 0, stream, a);
+      break;
+    default:
+      if (fixed) hipLaunchKernelGGL((r4::backward_tile_kernel<true, false, kInF32, IV>), grid, block, 0, stream, a);
+      else if (dyn) hipLaunchKernelGGL((r4::backward_tile_kernel<false, true, kInF32, IV>), grid, block, 0, stream, a);
+      else hipLaunchKernelGGL((r4::backward_tile_kernel<false, false, kInF32, IV>), grid, block, 0, stream, a);
+  }
+  return hipGetLastError();
+}
+
+// Checkpoint chunk kRot4Chunk or twice that (checked by the C ABI).
 hipError_t launch_backward_r4(bool fixed, bool dyn, const BwdArgs& a, hipStream_t stream) {
   const int64_t blocks = (a.n + r4::SPW - 1) / r4::SPW;
   if (blocks == 0) return hipSuccess;
-  const dim3 grid(static_cast<unsigned>(blocks)), block(kWave);
-  if (a.in_fmt == kInBf16) {
-    if (fixed) hipLaunchKernelGGL((r4::backward_tile_kernel<true, false, kInBf16>), grid, block, 0, stream, a);
-    else if (dyn) hipLaunchKernelGGL((r4::backward_tile_kernel<false, true, kInBf16>), grid, block, 0, stream, a);
-    else hipLaunchKernelGGL((r4::backward_tile_kernel<false, false, kInBf16>), grid, block, 0, stream, a);
-  } else if (a.in_fmt == kInE4M3) {
-    if (fixed) hipLaunchKernelGGL((r4::backward_tile_kernel<true, false, kInE4M3>), grid, block, 0, stream, a);
-    else if (dyn) hipLaunchKernelGGL((r4::backward_tile_kernel<false, true, kInE4M3>), grid, block, 0, stream, a);
-    else hipLaunchKernelGGL((r4::backward_tile_kernel<false, false, kInE4M3>), grid, block, 0, stream, a);
-  } else if (a.in_fmt == kInE5M2) {
-    if (fixed) hipLaunchKernelGGL((r4::backward_tile_kernel<true, false, kInE5M2>), grid, block, 0, stream, a);
-    else if (dyn) hipLaunchKernelGGL((r4::backward_tile_kernel<false, true, kInE5M2>), grid, block, 0, stream, a);
-    else hipLaunchKernelGGL((r4::backward_tile_kernel<false, false, kInE5M2>), grid, block, 0, stream, a);
-  } else {
-    if (fixed) hipLaunchKernelGGL((r4::backward_tile_kernel<true, false, kInF32>), grid, block, 0, stream, a);
-    else if (dyn) hipLaunchKernelGGL((r4::backward_tile_kernel<false, true, kInF32>), grid, block, 0, stream, a);
-    else hipLaunchKernelGGL((r4::backward_tile_kernel<false, false, kInF32>), grid, block, 0, stream, a);
-  }
-  return hipGetLastError();
+  if (a.chunk == 2 * kRot4Chunk) return launch_backward_r4_iv<2 * kRot4Chunk>(fixed, dyn, a, stream);
+  if (a.chunk != kRot4Chunk) return hipErrorInvalidValue;
+  return launch_backward_r4_iv<kRot4Chunk>(fixed, dyn, a, stream);
 }
 
 }  // namespace bssm

@@ -117,7 +117,10 @@ int bssm_forward_chunked_saved(int key_dim, int value_dim,
 /* ------------------------------------------------------------------------
  * Chunk-replay reverse.  Each checkpoint chunk is replayed on chip from
  * bmean/bcov and then reversed; the adjoint of the belief is carried across
- * chunks inside the kernel (one launch per call).
+ * chunks inside the kernel (one launch per call).  For D = 4, M = 8 the
+ * tiled kernels take checkpoint chunks of 8 tokens (the preferred interval)
+ * or 16 (the start of each 16-token tile's second half re-advanced on chip);
+ * other chunks run the generic kernels.
  *
  * gmf / gcf are the gradients of mean_final / cov_final; NULL means zero.
  * Output gradients: gk, gq, gd [N,T,D]; gv [N,T,M]; gp, gr [N,T];

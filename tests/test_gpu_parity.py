@@ -174,15 +174,14 @@ def test_backward_matches_oracle(ext_for, cuda_device, d, abi, final_grads, chun
         close(grads[i], eg[i], names[i])
 
 
-@pytest.mark.parametrize("t", [4, 8, 12, 16, 20, 24, 56, 60])
+@pytest.mark.parametrize("t", [4, 8, 12, 16, 20, 24, 28, 56, 60])
 @pytest.mark.parametrize("fixed", [False, True])
-def test_rot4_backward_tails(ext_for, cuda_device, t, fixed):
-    """D4 rotated-layout kernels at the preferred checkpoint chunk: every shape of the last tiles."""
-    from bayes_ssm import _hip
-
-    print(f"rot4 backward tails t={t} fixed={fixed}", flush=True)
+@pytest.mark.parametrize("chunk", [8, 16])
+def test_rot4_backward_tails(ext_for, cuda_device, rotated_layout, t, fixed, chunk):
+    """D4 rotated-layout backward at checkpoint chunks 8 (a record per 8-token chunk) and 16 (a record per
+    16-token tile, the second chunk's start advanced on chip): every shape of the last tiles."""
+    print(f"rot4 backward tails t={t} fixed={fixed} chunk={chunk}", flush=True)
     n, d = 21, 4
-    chunk = _hip.preferred_checkpoint(d)
     cpu, dev = _case(n, t, d, seed=100 + t, device=cuda_device)
     ref = _fixed_dynamics(cpu) if fixed else cpu
     ext = ext_for(d)
