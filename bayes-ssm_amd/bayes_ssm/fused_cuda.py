@@ -526,14 +526,11 @@ def fused_diagonal_bayesian(
     _check(values.device == dev and queries.device == dev and decay.device == dev and process.device == dev
            and observation.device == dev and initial_mean.device == dev and initial_covariance.device == dev,
            "fused Bayesian inputs must share one device")
-    keys = keys.contiguous()
-    values = values.contiguous()
-    queries = queries.contiguous()
-    decay = decay.contiguous()
-    process = process.contiguous()
-    observation = observation.contiguous()
-    initial_mean = initial_mean.contiguous()
-    initial_covariance = initial_covariance.contiguous()
+    # .contiguous() as the reference (fused_cuda.py:376-383); the check first
+    # skips a dispatcher round trip per tensor on the common contiguous case.
+    keys, values, queries, decay, process, observation, initial_mean, initial_covariance = (
+        x if x.is_contiguous() else x.contiguous()
+        for x in (keys, values, queries, decay, process, observation, initial_mean, initial_covariance))
     if bf16:
         if _bf16_kernels_apply(keys, values, queries):
             return _ChunkedBayesianBF16Function.apply(

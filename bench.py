@@ -96,11 +96,12 @@ def cpu_model() -> str:
     return "unknown CPU"
 
 
-def _settle(step, warmup: int, min_ms: float = 40.0) -> None:
+def _settle(step, warmup: int, min_ms: float = 40.0) -> float:
     """Warm-up calls of a secondary workload's step: at least `warmup`, and after the first call (whose host
     work, new shapes and new allocations can leave the device idle for over 10 ms) enough back-to-back calls to
     keep the device busy for `min_ms`.  An idle of 10 ms or more sends the next ~20 steps through a
-    power-management dip of up to 25 %; the timed calls then start at the sustained rate."""
+    power-management dip of up to 25 %; the timed calls then start at the sustained rate.  Returns the wall
+    time of one synchronized call (seconds)."""
     step()
     torch.cuda.synchronize()
     t0 = time.perf_counter()
@@ -110,6 +111,7 @@ def _settle(step, warmup: int, min_ms: float = 40.0) -> None:
     for _ in range(max(warmup, int(min_ms * 1e-3 / max(per, 1e-5)) + 1)):
         step()
     torch.cuda.synchronize()
+    return per
 
 
 def time_layer(b, t, h, d, m, chunk, steps, warmup, device, kqv_dtype=None) -> dict:
@@ -127,14 +129,25 @@ def time_layer(b, t, h, d, m, chunk, steps, warmup, device, kqv_dtype=None) -> d
         y, _, _ = fused_cuda.fused_diagonal_bayesian(*leaves, m0, c0, chunk_length=chunk, denominator_floor=1e-6)
         return torch.autograd.grad(y, leaves, gy)
 
-    _settle(step, warmup)
+    per = _settle(step, warmup)
+    # At least ~20 ms of timed steps, so that short steps are not dominated by
+    # the host's latency to the first launch; events around each step's
+    # forward and backward give the in-step kernel times beside the step.
+    steps = max(steps, int(20e-3 / max(per, 1e-5)) + 1)
+    marks = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(steps)]
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     e0.record()
-    for _ in range(steps):
-        step()
+    for i in range(steps):
+        marks[i][0].record()
+        y, _, _ = fused_cuda.fused_diagonal_bayesian(*leaves, m0, c0, chunk_length=chunk, denominator_floor=1e-6)
+        marks[i][1].record()
+        torch.autograd.grad(y, leaves, gy)
+        marks[i][2].record()
     e1.record()
     torch.cuda.synchronize()
     ms = e0.elapsed_time(e1) / steps
+    fwd_ms = sum(mk[0].elapsed_time(mk[1]) for mk in marks) / steps
+    bwd_ms = sum(mk[1].elapsed_time(mk[2]) for mk in marks) / steps
     fwd_b, bwd_b = algorithmic_bytes(d, m)
     if kqv_dtype is not None:
         # k, q, v (2D + M values) read at the narrow width in both passes and
@@ -143,7 +156,10 @@ def time_layer(b, t, h, d, m, chunk, steps, warmup, device, kqv_dtype=None) -> d
         fwd_b -= (2 * d + m) * saved
         bwd_b -= (2 * d + m) * 2 * saved
     out = {"B": b, "T": t, "H": h, "D": d, "M": m, "ms_per_step": ms, "tokens_per_s": b * t / (ms * 1e-3),
-           "roofline_step_frac": (fwd_b + bwd_b) * b * h * t / (ms * 1e-3) / HBM_PEAK}
+           "roofline_step_frac": (fwd_b + bwd_b) * b * h * t / (ms * 1e-3) / HBM_PEAK, "steps": steps,
+           "forward_ms_in_step": fwd_ms, "backward_ms_in_step": bwd_ms,
+           "forward_roofline_frac": fwd_b * b * h * t / (fwd_ms * 1e-3) / HBM_PEAK,
+           "backward_roofline_frac": bwd_b * b * h * t / (bwd_ms * 1e-3) / HBM_PEAK}
     if kqv_dtype is not None:
         out["kqv_dtype"] = str(kqv_dtype).replace("torch.", "")
         out["bytes_per_token_head"] = fwd_b + bwd_b

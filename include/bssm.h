@@ -461,8 +461,16 @@ int bssm_rotation_checkpoint(int key_dim);
  * 32768, the measured crossovers.
  * Sets the limit when limit >= 0 and returns the previous one; limit < 0
  * only reads it; -1 for any other direction.  Results of the row and
- * rotated layouts agree within float32 rounding, not bitwise.  No
- * counterpart in the reference (a tuning switch of this library). */
+ * rotated layouts agree within float32 rounding, not bitwise.  With the
+ * default limits the forward results of a sequence are the same bits for
+ * every N up to 24576 (the row layout's one- and two-wave forwards are
+ * bitwise one another); its gradients change layout above 8192 sequences
+ * and then differ in the last bits: at config 3 (T = 512), the same
+ * sequences inside N = 16384 and inside N = 2048 or 32 differ by at most
+ * 1.2e-4 absolute (dL/dr) and 2e-5 for the other gradients, inside the
+ * 1e-5 relative + 1e-4 absolute tolerance both meet against the float64
+ * oracle (tests/test_gpu_batch_invariance.py).  No counterpart in the
+ * reference (a tuning switch of this library). */
 int64_t bssm_small_batch_limit(int direction, int64_t limit);
 
 /* ------------------------------------------------------------------------
