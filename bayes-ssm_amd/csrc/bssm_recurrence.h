@@ -116,6 +116,13 @@ bool d2_backward_ok(const BwdArgs& a);
 hipError_t launch_forward_d2(bool fixed, const FwdArgs& a, hipStream_t stream);
 hipError_t launch_backward_d2(bool fixed, bool dyn, const BwdArgs& a, hipStream_t stream);
 
+// D = 8, M = 8 checkpoint-replay backward with 8 lanes per sequence in XOR
+// order (bssm_d8.hip): T a positive multiple of 8, the checkpoint chunk 8
+// (the library's preferred one for D = 8), 16-byte aligned streams and
+// checkpoint tensors.  Other shapes take the generic kernels.
+bool d8_backward_ok(const BwdArgs& a);
+hipError_t launch_backward_d8(bool fixed, bool dyn, const BwdArgs& a, hipStream_t stream);
+
 // D = M = 64 kernels (bssm_d64.hip): one wave per sequence, lane = dimension.
 // The backward replays each checkpoint chunk on chip before reversing a token,
 // so its cost grows with the square of the chunk length; the autograd path

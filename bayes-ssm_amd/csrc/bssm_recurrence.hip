@@ -523,6 +523,7 @@ hipError_t launch_backward(int key_dim, bool fixed, bool dyn, const BwdArgs& a, 
   if (key_dim == 4 && a.rot4) return launch_backward_r4(fixed, dyn, a, stream);
   if (key_dim == 1 && d1_backward_ok(a)) return launch_backward_d1(fixed, dyn, a, stream);
   if (key_dim == 2 && d2_backward_ok(a)) return launch_backward_d2(fixed, dyn, a, stream);
+  if (key_dim == 8 && d8_backward_ok(a)) return launch_backward_d8(fixed, dyn, a, stream);
   switch (key_dim) {
     case 1: return launch_backward_dd<1>(fixed, dyn, a, stream);
     case 2: return launch_backward_dd<2>(fixed, dyn, a, stream);
