@@ -131,23 +131,33 @@ def time_layer(b, t, h, d, m, chunk, steps, warmup, device, kqv_dtype=None) -> d
 
     per = _settle(step, warmup)
     # At least ~20 ms of timed steps, so that short steps are not dominated by
-    # the host's latency to the first launch; events around each step's
-    # forward and backward give the in-step kernel times beside the step.
+    # the host's latency to the first launch.
     steps = max(steps, int(20e-3 / max(per, 1e-5)) + 1)
-    marks = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(steps)]
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     e0.record()
-    for i in range(steps):
-        marks[i][0].record()
-        y, _, _ = fused_cuda.fused_diagonal_bayesian(*leaves, m0, c0, chunk_length=chunk, denominator_floor=1e-6)
-        marks[i][1].record()
-        torch.autograd.grad(y, leaves, gy)
-        marks[i][2].record()
+    for _ in range(steps):
+        step()
     e1.record()
     torch.cuda.synchronize()
     ms = e0.elapsed_time(e1) / steps
-    fwd_ms = sum(mk[0].elapsed_time(mk[1]) for mk in marks) / steps
-    bwd_ms = sum(mk[1].elapsed_time(mk[2]) for mk in marks) / steps
+    # Device time of each kernel: each step's forward and backward queued
+    # behind a device-side delay, so the events around them bracket the
+    # kernels, not the host's launch latency (a separate pass: events inside
+    # the timed loop would add host work to steps this short).
+    fwd_t, bwd_t = [], []
+    for _ in range(8):
+        mk = [torch.cuda.Event(enable_timing=True) for _ in range(3)]
+        torch.cuda._sleep(1_000_000)
+        mk[0].record()
+        y, _, _ = fused_cuda.fused_diagonal_bayesian(*leaves, m0, c0, chunk_length=chunk, denominator_floor=1e-6)
+        mk[1].record()
+        torch.autograd.grad(y, leaves, gy)
+        mk[2].record()
+        torch.cuda.synchronize()
+        fwd_t.append(mk[0].elapsed_time(mk[1]))
+        bwd_t.append(mk[1].elapsed_time(mk[2]))
+    fwd_ms = sorted(fwd_t)[4]
+    bwd_ms = sorted(bwd_t)[4]
     fwd_b, bwd_b = algorithmic_bytes(d, m)
     if kqv_dtype is not None:
         # k, q, v (2D + M values) read at the narrow width in both passes and
@@ -157,7 +167,7 @@ def time_layer(b, t, h, d, m, chunk, steps, warmup, device, kqv_dtype=None) -> d
         bwd_b -= (2 * d + m) * 2 * saved
     out = {"B": b, "T": t, "H": h, "D": d, "M": m, "ms_per_step": ms, "tokens_per_s": b * t / (ms * 1e-3),
            "roofline_step_frac": (fwd_b + bwd_b) * b * h * t / (ms * 1e-3) / HBM_PEAK, "steps": steps,
-           "forward_ms_in_step": fwd_ms, "backward_ms_in_step": bwd_ms,
+           "forward_kernel_ms": fwd_ms, "backward_kernel_ms": bwd_ms,
            "forward_roofline_frac": fwd_b * b * h * t / (fwd_ms * 1e-3) / HBM_PEAK,
            "backward_roofline_frac": bwd_b * b * h * t / (bwd_ms * 1e-3) / HBM_PEAK}
     if kqv_dtype is not None:
@@ -490,6 +500,40 @@ def time_scan(b, t, d, m, iters, device) -> dict:
             "kernel_timing": "events around one launch queued behind a device-side delay (median of the calls)"}
 
 
+def idle_probe(b, t, h, d, m, chunk, device) -> dict:
+    """Per-step device times of the config-3 step right after an idle gap of 0, 1, 10 and 100 ms (the gap
+    follows 60 back-to-back steps and a synchronize).  Shows the device's power-management transient: after
+    an idle of 10 ms or more the following ~20 steps run up to 25 % slower, after 1 ms or less they do not."""
+    from bayes_ssm import fused_cuda
+
+    leaves, m0, c0, gy = make_workload(b, t, h, d, m, device)
+
+    def step():
+        y, _, _ = fused_cuda.fused_diagonal_bayesian(*leaves, m0, c0, chunk_length=chunk, denominator_floor=1e-6)
+        return torch.autograd.grad(y, leaves, gy)
+
+    for _ in range(80):
+        step()
+    torch.cuda.synchronize()
+    rows = {}
+    for gap_ms in (0.0, 1.0, 10.0, 100.0):
+        for _ in range(60):
+            step()
+        torch.cuda.synchronize()
+        if gap_ms:
+            time.sleep(gap_ms * 1e-3)
+        ev = [torch.cuda.Event(enable_timing=True) for _ in range(41)]
+        ev[0].record()
+        for i in range(40):
+            step()
+            ev[i + 1].record()
+        torch.cuda.synchronize()
+        per = [ev[i].elapsed_time(ev[i + 1]) * 1e3 for i in range(40)]
+        rows[f"gap_{gap_ms:g}ms"] = {"first20_mean_us": sum(per[:20]) / 20, "last20_mean_us": sum(per[20:]) / 20,
+                                     "per_step_us": [round(x, 1) for x in per]}
+    return rows
+
+
 def cpu_baseline(t: int, d: int, m: int, heads: int, budget_s: float) -> dict:
     """Time the CPU restatement of the reference CPU path on a bounded sample.
 
@@ -537,6 +581,9 @@ def main() -> int:
     ap.add_argument("--kernel-iters", type=int, default=50,
                     help="launches of each kernel alone (event-timed, before the warmup steps)")
     ap.add_argument("--cpu-budget", type=float, default=20.0, help="seconds of CPU-baseline work (0 = skip)")
+    ap.add_argument("--idle-probe", action="store_true",
+                    help="print per-step times of the config-3 step after idle gaps of 0-100 ms (power transient) "
+                         "as its own JSON line, instead of the benchmark")
     ap.add_argument("--no-extras", action="store_true",
                     help="skip the secondary shapes (per-GPU DP shape, D1/D2/D8 variants, associative scan)")
     ap.add_argument("--secondary", choices=("mixer", "mixer-readout", "block", "conv4", "rotation", "d64",
@@ -560,6 +607,9 @@ def main() -> int:
     device = torch.device("cuda:0")
     torch.cuda.set_device(device)
     b, t, h, d, m = args.batch, args.seq, args.heads, args.key_dim, 8
+    if args.idle_probe:
+        print(json.dumps({"workload": "idle_probe", **idle_probe(b, t, h, d, m, args.chunk, device)}), flush=True)
+        return 0
     if args.secondary:
         if args.secondary == "conv4":
             row = time_conv(b, t, h * (2 * d + m), args.steps, args.warmup, device, fused=True)
