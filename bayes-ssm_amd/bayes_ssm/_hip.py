@@ -143,13 +143,39 @@ def on_device(device: torch.device):
     return torch.cuda.device(device)
 
 
+_functions: dict = {}
+
+
+def function(name: str):
+    """The ctypes function object of entry point ``name`` (looked up once per process)."""
+    fn = _functions.get(name)
+    if fn is None:
+        fn = _functions.setdefault(name, getattr(load(), name))
+    return fn
+
+
+def _raise(name: str, rc: int) -> None:
+    msg = load().bssm_last_error().decode(errors="replace")
+    raise RuntimeError(f"{name} failed (code {rc}): {msg}")
+
+
 def call(name: str, *args) -> None:
     """Invoke ``name`` and raise ``RuntimeError`` with the library message on failure."""
-    lib = load()
-    rc = getattr(lib, name)(*args)
+    rc = function(name)(*args)
     if rc != 0:
-        msg = lib.bssm_last_error().decode(errors="replace")
-        raise RuntimeError(f"{name} failed (code {rc}): {msg}")
+        _raise(name, rc)
+
+
+def launch(device: torch.device, name: str, *args) -> None:
+    """``call`` with ``device`` current; the common case (already current) enters no context."""
+    index = device.index
+    if index is None or index == torch._C._cuda_getDevice():
+        rc = function(name)(*args)
+    else:
+        with torch.cuda.device(index):
+            rc = function(name)(*args)
+    if rc != 0:
+        _raise(name, rc)
 
 
 def supported(key_dim: int, value_dim: int) -> bool:

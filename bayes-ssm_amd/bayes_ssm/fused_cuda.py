@@ -94,6 +94,53 @@ def _check_inputs(key_dim: int, tensors: tuple[Tensor, ...], names: tuple[str, .
     _check(all(x.device == k.device for x in tensors), "fused Bayesian inputs must share one device")
 
 
+def _launch_forward(d: int, m: int, name: str, fixed: bool, keys, values, queries, decay, process, observation,
+                    mean0, cov0, chunks: int, floor: float, saved: bool = False) -> list:
+    """Allocate the forward outputs and launch ``name`` on the current stream (arguments already checked)."""
+    n, t = keys.shape[0], keys.shape[1]
+    nb = -(-t // chunks)
+    dev = keys.device
+    f32 = torch.float32
+    out = torch.empty((n, t, m), device=dev, dtype=f32)
+    mf = torch.empty((n, d, m), device=dev, dtype=f32)
+    cf = torch.empty((n, d, d), device=dev, dtype=f32)
+    bm = torch.empty((n, nb + 1, d, m), device=dev, dtype=f32)
+    bc = torch.empty((n, nb + 1, d, d), device=dev, dtype=f32)
+    hist = ()
+    if saved:
+        hist = (torch.empty((n, t, d, m), device=dev, dtype=f32), torch.empty((n, t, d, d), device=dev, dtype=f32),
+                torch.empty((n, t, d), device=dev, dtype=f32), torch.empty((n, t), device=dev, dtype=f32),
+                torch.empty((n, t, m), device=dev, dtype=f32))
+    _hip.launch(dev, name, d, m, keys.data_ptr(), values.data_ptr(), queries.data_ptr(),
+                None if fixed else decay.data_ptr(), None if fixed else process.data_ptr(),
+                None if fixed else observation.data_ptr(), mean0.data_ptr(), cov0.data_ptr(), out.data_ptr(),
+                mf.data_ptr(), cf.data_ptr(), bm.data_ptr(), bc.data_ptr(), *[h.data_ptr() for h in hist],
+                n, t, chunks, floor, _hip.stream_of(dev))
+    return [out, mf, cf, bm, bc, *hist]
+
+
+def _launch_backward(d: int, m: int, name: str, fixed: bool, outputs: int, keys, values, queries, decay, process,
+                     observation, mean0, cov0, bm, bc, history, gy, gmf, gcf, chunks: int, floor: float) -> list:
+    """Allocate ``outputs`` gradients (3, 6 or 8) and launch ``name`` (arguments already checked)."""
+    n, t = keys.shape[0], keys.shape[1]
+    dev = keys.device
+    f32 = torch.float32
+    grads = [torch.empty((n, t, d), device=dev, dtype=f32), torch.empty((n, t, m), device=dev, dtype=f32),
+             torch.empty((n, t, d), device=dev, dtype=f32)]
+    if outputs >= 6:
+        grads += [torch.empty((n, t, d), device=dev, dtype=f32), torch.empty((n, t), device=dev, dtype=f32),
+                  torch.empty((n, t), device=dev, dtype=f32)]
+    if outputs == 8:
+        grads += [torch.empty((n, d, m), device=dev, dtype=f32), torch.empty((n, d, d), device=dev, dtype=f32)]
+    _hip.launch(dev, name, d, m, keys.data_ptr(), values.data_ptr(), queries.data_ptr(),
+                None if fixed else decay.data_ptr(), None if fixed else process.data_ptr(),
+                None if fixed else observation.data_ptr(), mean0.data_ptr(), cov0.data_ptr(), bm.data_ptr(),
+                bc.data_ptr(), *[h.data_ptr() for h in history], gy.data_ptr(),
+                None if gmf is None else gmf.data_ptr(), None if gcf is None else gcf.data_ptr(),
+                *[g.data_ptr() for g in grads], n, t, chunks, floor, _hip.stream_of(dev))
+    return grads
+
+
 class _Extension:
     """Per-key-dim method table over the C ABI (replaces the pybind module)."""
 
@@ -126,32 +173,14 @@ class _Extension:
                 "mean0", "cov0")
             _check_inputs(self.key_dim, tensors, names)
         _check(int(chunks) > 0, "fused Bayesian chunk length must be positive")
-        n, t = self._sizes(keys)
-        d, m = self.key_dim, self.value_dim
-        nb = -(-t // int(chunks))
-        opt = dict(device=keys.device, dtype=torch.float32)
-        out = torch.empty((n, t, m), **opt)
-        mf = torch.empty_like(mean0)
-        cf = torch.empty_like(cov0)
-        bm = torch.empty((n, nb + 1, d, m), **opt)
-        bc = torch.empty((n, nb + 1, d, d), **opt)
-        hist = ()
-        if saved:
-            hist = (torch.empty((n, t, d, m), **opt), torch.empty((n, t, d, d), **opt),
-                    torch.empty((n, t, d), **opt), torch.empty((n, t), **opt), torch.empty((n, t, m), **opt))
-        P = _hip.ptr
-        with _hip.on_device(keys.device):
-            _hip.call(name, d, m, P(keys), P(values), P(queries),
-                      None if fixed else P(decay), None if fixed else P(process), None if fixed else P(observation),
-                      P(mean0), P(cov0), P(out), P(mf), P(cf), P(bm), P(bc), *[P(h) for h in hist],
-                      n, t, int(chunks), float(floor), _hip.stream_of(keys.device))
-        return [out, mf, cf, bm, bc, *hist]
+        return _launch_forward(self.key_dim, self.value_dim, name, fixed, keys, values, queries, decay, process,
+                               observation, mean0, cov0, int(chunks), float(floor), saved)
 
     def _backward(self, name: str, fixed: bool, outputs: int, keys, values, queries, decay, process, observation,
                   mean0, cov0, bm, bc, history, gy, gmf, gcf, chunks: int, floor: float, validate: bool = True):
-        n, t = self._sizes(keys)
-        d, m = self.key_dim, self.value_dim
         if validate:
+            n, t = self._sizes(keys)
+            d, m = self.key_dim, self.value_dim
             tensors = (keys, values, queries) + (() if fixed else (decay, process, observation)) + (bm, bc, gy)
             names = ("keys", "values", "queries") + (() if fixed else ("decay", "process", "observation")) + (
                 "boundary_mean", "boundary_covariance", "grad_output")
@@ -165,22 +194,9 @@ class _Extension:
             _check(tuple(bm.shape) == (n, nb + 1, d, m) and tuple(bc.shape) == (n, nb + 1, d, d),
                    "boundary tensors do not match the chunk length")
             _check(tuple(gy.shape) == (n, t, m), "grad_output must be [N,T,M]")
-        opt = dict(device=keys.device, dtype=torch.float32)
-        gk = torch.empty((n, t, d), **opt)
-        gv = torch.empty((n, t, m), **opt)
-        gq = torch.empty((n, t, d), **opt)
-        grads = [gk, gv, gq]
-        if outputs >= 6:
-            grads += [torch.empty((n, t, d), **opt), torch.empty((n, t), **opt), torch.empty((n, t), **opt)]
-        if outputs == 8:
-            grads += [torch.empty((n, d, m), **opt), torch.empty((n, d, d), **opt)]
-        P = _hip.ptr
-        with _hip.on_device(keys.device):
-            _hip.call(name, d, m, P(keys), P(values), P(queries),
-                      None if fixed else P(decay), None if fixed else P(process), None if fixed else P(observation),
-                      P(mean0), P(cov0), P(bm), P(bc), *[P(h) for h in history], P(gy), P(gmf), P(gcf),
-                      *[P(g) for g in grads], n, t, int(chunks), float(floor), _hip.stream_of(keys.device))
-        return grads
+        return _launch_backward(self.key_dim, self.value_dim, name, fixed, outputs, keys, values, queries, decay,
+                                process, observation, mean0, cov0, bm, bc, history, gy, gmf, gcf, int(chunks),
+                                float(floor))
 
     # -- reference method names ------------------------------------------
     def forward_chunked(self, keys, values, queries, decay, process, observation, mean0, cov0, chunks, floor):
@@ -295,12 +311,14 @@ class _ChunkedBayesianFunction(torch.autograd.Function):
     @staticmethod
     def forward(ctx, keys, values, queries, decay, process, observation, initial_mean, initial_covariance,
                 chunk_length, denominator_floor, fixed_dynamics):
-        extension = _load_extension(keys.shape[-1])
+        n, t, d = keys.shape
+        extension = _load_extension(d)
         if extension is None:
             raise RuntimeError("the fused Bayesian HIP extension is unavailable")
-        n, t, d = keys.shape
+        floor = float(denominator_floor)
+        fixed = bool(fixed_dynamics)
         use_saved_history = (
-            d == 1 and not fixed_dynamics and os.environ.get("BAYES_SSM_D1_SAVED_HISTORY", "0") == "1"
+            d == 1 and not fixed and os.environ.get("BAYES_SSM_D1_SAVED_HISTORY", "0") == "1"
             and os.environ.get("BAYES_SSM_DISABLE_SAVED_HISTORY", "0") != "1"
         )
         if use_saved_history:
@@ -308,29 +326,26 @@ class _ChunkedBayesianFunction(torch.autograd.Function):
             (output, final_mean, final_covariance, boundary_mean, boundary_covariance, mp_history, pp_history,
              u_history, beta_history, e_history) = extension.forward_chunked_saved(
                 keys, values, queries, decay, process, observation, initial_mean, initial_covariance, interval,
-                float(denominator_floor))
+                floor)
             ctx.save_for_backward(keys, values, queries, decay, process, observation, initial_mean,
                                   initial_covariance, boundary_mean, boundary_covariance, mp_history, pp_history,
                                   u_history, beta_history, e_history)
         else:
             interval = _checkpoint_interval(d, t, chunk_length)
-            name = "bssm_forward_chunked_fixed" if fixed_dynamics else "bssm_forward_chunked"
-            output, final_mean, final_covariance, boundary_mean, boundary_covariance = extension._forward(
-                name, bool(fixed_dynamics), keys, values, queries, decay, process, observation, initial_mean,
-                initial_covariance, interval, float(denominator_floor), validate=False)
+            output, final_mean, final_covariance, boundary_mean, boundary_covariance = _launch_forward(
+                d, _VALUE_DIM[d], "bssm_forward_chunked_fixed" if fixed else "bssm_forward_chunked", fixed, keys,
+                values, queries, decay, process, observation, initial_mean, initial_covariance, interval, floor)
             ctx.save_for_backward(keys, values, queries, decay, process, observation, initial_mean,
                                   initial_covariance, boundary_mean, boundary_covariance)
+        need = ctx.needs_input_grad
+        ctx.extension = extension
         ctx.use_saved_history = use_saved_history
         ctx.chunk_length = interval
-        ctx.denominator_floor = float(denominator_floor)
-        ctx.fixed_dynamics = bool(fixed_dynamics)
-        ctx.need_dynamics_grad = any(
-            x.requires_grad for x in (decay, process, observation, initial_mean, initial_covariance))
-        ctx.need_initial_grad = initial_mean.requires_grad or initial_covariance.requires_grad
+        ctx.denominator_floor = floor
+        ctx.fixed_dynamics = fixed
+        ctx.need_dynamics_grad = need[3] or need[4] or need[5] or need[6] or need[7]
+        ctx.need_initial_grad = need[6] or need[7]
         ctx.noinitial_backward = False
-        ctx.mean_shape = tuple(final_mean.shape)
-        ctx.covariance_shape = tuple(final_covariance.shape)
-        ctx.output_shape = tuple(output.shape)
         ctx.set_materialize_grads(False)
         return output, final_mean, final_covariance
 
@@ -340,13 +355,13 @@ class _ChunkedBayesianFunction(torch.autograd.Function):
         (keys, values, queries, decay, process, observation, initial_mean, initial_covariance, boundary_mean,
          boundary_covariance) = saved[:10]
         history = saved[10:]
-        extension = _load_extension(keys.shape[-1])
-        if extension is None:  # pragma: no cover - loaded in forward
-            raise RuntimeError("the fused Bayesian HIP extension is unavailable")
+        extension = ctx.extension
         lean = not ctx.need_dynamics_grad and grad_mean is None and grad_covariance is None
+        d = keys.shape[2]
+        m = _VALUE_DIM[d]
         if grad_output is None:
-            grad_output = torch.zeros(ctx.output_shape, device=keys.device, dtype=keys.dtype)
-        else:
+            grad_output = torch.zeros((keys.shape[0], keys.shape[1], m), device=keys.device, dtype=keys.dtype)
+        elif not grad_output.is_contiguous():
             grad_output = grad_output.contiguous()
         # Null final-state gradients mean zero in the C ABI; no zero tensors needed.
         gm = None if grad_mean is None else grad_mean.contiguous()
@@ -376,8 +391,8 @@ class _ChunkedBayesianFunction(torch.autograd.Function):
                 name, outputs = "bssm_backward_chunked_lean" + suffix, 3
             else:
                 name, outputs = "bssm_backward_chunked" + suffix, 8
-            gradients = extension._backward(name, fixed, outputs, *args_head, (), grad_output, gm, gc,
-                                            ctx.chunk_length, ctx.denominator_floor, validate=False)
+            gradients = _launch_backward(d, m, name, fixed, outputs, *args_head, (), grad_output, gm, gc,
+                                         ctx.chunk_length, ctx.denominator_floor)
         if lean:
             # 3 tensor gradients + 5 tensor and 3 scalar non-differentiable slots.
             return (*gradients, None, None, None, None, None, None, None, None)
@@ -496,31 +511,33 @@ def fused_diagonal_bayesian(
     Keys, values and queries may instead all be bfloat16, or all one float8
     encoding (see the module docstring).
     """
-    narrow_dtypes = (torch.bfloat16, *_FP8_FORMATS)
-    bf16 = keys.dtype in narrow_dtypes and all(x.dtype == keys.dtype for x in (values, queries))
-    if (
-        keys.device.type != "cuda"
-        or keys.ndim != 3
-        or values.ndim != 3
-        or queries.ndim != 3
-        or (keys.shape[-1], values.shape[-1]) not in _SUPPORTED
-        or queries.shape[-1] != keys.shape[-1]
-        or keys.shape != queries.shape
-        or values.shape[:2] != keys.shape[:2]
-        or not all(x.dtype == torch.float32 for x in (decay, process, observation, initial_mean,
-                                                      initial_covariance))
-        or not (bf16 or all(x.dtype == torch.float32 for x in (keys, values, queries)))
-    ):
+    if keys.device.type != "cuda":
         return None
-    key_dim = keys.shape[-1]
+    ks = keys.shape
+    if len(ks) != 3 or values.ndim != 3 or queries.shape != ks:
+        return None
+    n, t, key_dim = ks
+    value_dim = values.shape[2]
+    f32 = torch.float32
+    kdt = keys.dtype
+    if kdt == f32:
+        bf16 = False
+        if values.dtype != f32 or queries.dtype != f32:
+            return None
+    else:
+        bf16 = (kdt == torch.bfloat16 or kdt in _FP8_FORMATS) and values.dtype == kdt and queries.dtype == kdt
+        if not bf16:
+            return None
+    if ((key_dim, value_dim) not in _SUPPORTED or values.shape[:2] != ks[:2]
+            or decay.dtype != f32 or process.dtype != f32 or observation.dtype != f32
+            or initial_mean.dtype != f32 or initial_covariance.dtype != f32):
+        return None
     extension = _load_extension(key_dim)
     if extension is None:
         return None
-    n, t, _ = keys.shape
-    if decay.shape != (n, t, key_dim) or process.shape != (n, t) or observation.shape != (n, t):
-        return None
-    value_dim = values.shape[-1]
-    if initial_mean.shape != (n, key_dim, value_dim) or initial_covariance.shape != (n, key_dim, key_dim):
+    if (decay.shape != (n, t, key_dim) or process.shape != (n, t) or observation.shape != (n, t)
+            or initial_mean.shape != (n, key_dim, value_dim)
+            or initial_covariance.shape != (n, key_dim, key_dim)):
         return None
     dev = keys.device
     _check(values.device == dev and queries.device == dev and decay.device == dev and process.device == dev

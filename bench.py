@@ -176,6 +176,96 @@ def time_layer(b, t, h, d, m, chunk, steps, warmup, device, kqv_dtype=None) -> d
     return out
 
 
+class _NoopCore(torch.autograd.Function):
+    """The fused function's autograd shape without its work: same inputs, outputs and saved tensors, no launch."""
+
+    @staticmethod
+    def forward(ctx, k, v, q, dec, p, r, m0, c0):
+        n, t, d = k.shape
+        m = v.shape[2]
+        out = torch.empty(n, t, m, device=k.device)
+        mf, cf = torch.empty_like(m0), torch.empty_like(c0)
+        ctx.save_for_backward(k, v, q, dec, p, r, m0, c0, out, out)
+        ctx.set_materialize_grads(False)
+        return out, mf, cf
+
+    @staticmethod
+    def backward(ctx, gy, gm, gc):
+        return tuple(torch.empty_like(x) for x in ctx.saved_tensors[:8])
+
+
+def host_costs(b, t, h, d, m, chunk, device) -> dict:
+    """Host wall time of one fwd+bwd call with the device kept busy (no waits inside): the fused function, and
+    ``_NoopCore`` (torch's autograd machinery alone for the same inputs and outputs)."""
+    from bayes_ssm import fused_cuda
+
+    leaves, m0, c0, gy = make_workload(b, t, h, d, m, device, seed=1)
+    leaves8 = [*leaves, m0.requires_grad_(True), c0.requires_grad_(True)]
+
+    def fused():
+        y, _, _ = fused_cuda.fused_diagonal_bayesian(*leaves8, chunk_length=chunk, denominator_floor=1e-6)
+        torch.autograd.grad(y, leaves8, gy)
+
+    def noop():
+        y, _, _ = _NoopCore.apply(*leaves8)
+        torch.autograd.grad(y, leaves8, gy)
+
+    res = {}
+    for name, fn in (("fused_host_ms", fused), ("autograd_noop_host_ms", noop)):
+        for _ in range(20):
+            fn()
+        torch.cuda.synchronize()
+        ts = []
+        for _ in range(41):
+            torch.cuda._sleep(2_000_000)
+            t0 = time.perf_counter()
+            fn()
+            ts.append(time.perf_counter() - t0)
+            torch.cuda.synchronize()
+        res[name] = sorted(ts)[20] * 1e3
+    return res
+
+
+def time_layer_graphed(b, t, h, d, m, chunk, steps, device) -> dict:
+    """fwd+bwd of fused_diagonal_bayesian captured once in a HIP graph (torch.cuda.graph) and replayed.
+
+    The same kernels on the same inputs as ``time_layer``, without the
+    per-call host work (Python, torch's autograd engine, the launch calls):
+    the rate at which the device runs the step.
+    """
+    from bayes_ssm import fused_cuda
+
+    leaves, m0, c0, gy = make_workload(b, t, h, d, m, device, seed=1)
+
+    def step():
+        y, _, _ = fused_cuda.fused_diagonal_bayesian(*leaves, m0, c0, chunk_length=chunk, denominator_floor=1e-6)
+        return torch.autograd.grad(y, leaves, gy)
+
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for _ in range(3):
+            step()
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        step()
+    per = _settle(graph.replay, 3)
+    steps = max(steps, int(20e-3 / max(per, 1e-5)) + 1)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(steps):
+        graph.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / steps
+    del graph
+    fwd_b, bwd_b = algorithmic_bytes(d, m)
+    return {"B": b, "T": t, "H": h, "D": d, "M": m, "ms_per_step": ms, "tokens_per_s": b * t / (ms * 1e-3),
+            "roofline_step_frac": (fwd_b + bwd_b) * b * h * t / (ms * 1e-3) / HBM_PEAK, "steps": steps,
+            "path": "forward + autograd.grad captured in one torch.cuda.graph, replayed"}
+
+
 MIXER_FWD_BYTES = 2 * 22 + 4 * 8   # bf16 q, k, decay (4 each), v (8), noise (2) in; float32 read out
 MIXER_BWD_BYTES = 2 * 22 + 4 * 8 + 2 * 22  # projections and read gradient in; bf16 projection gradients out
 
@@ -781,6 +871,11 @@ def main() -> int:
                   "dp8_share_d4m8": time_layer(b // 8, t, h, d, m, args.chunk, 30, 10, device)}
         for name, (eb, ed) in {"config3_d2m8": (b, 2), "config3_d8m8": (b, 8), "config2_d1m8": (64, 1)}.items():
             extras[name] = time_layer(eb, t, h, ed, m, args.chunk, 10, 3, device)
+        # Config 2's step is short enough for host work to bound it: its host
+        # costs, and the same step replayed from a HIP graph.
+        extras["config2_d1m8"].update(host_costs(64, t, h, 1, m, args.chunk, device))
+        extras["config2_d1m8_graphed"] = time_layer_graphed(64, t, h, 1, m, args.chunk, 10, device)
+        extras["dp8_share_d4m8_graphed"] = time_layer_graphed(b // 8, t, h, d, m, args.chunk, 10, device)
         extras["mixer_core_config3_fused"] = time_mixer(b, t, h, 30, 10, device, fused=True)
         extras["mixer_core_config3_op_chain"] = time_mixer(b, t, h, 10, 3, device, fused=False)
         extras["mixer_readout_config3_fused"] = time_mixer(b, t, h, 30, 10, device, fused=True, gated=True)
