@@ -136,7 +136,9 @@ def test_row_layout_chunk_invariance_and_symmetry(cuda_device, name, fixed):
 
 @pytest.mark.parametrize("fixed", [False, True])
 @pytest.mark.parametrize("chunk", [1, 8, 13])
-@pytest.mark.parametrize("n,t", [(1, 16), (7, 20), (37, 52), (9, 64), (6, 4), (33, 512)])
+# N = 1029 and 1028: above 1024 sequences two groups of 4 share a workgroup (the last workgroup's second group
+# holds one sequence, or none).
+@pytest.mark.parametrize("n,t", [(1, 16), (7, 20), (37, 52), (9, 64), (6, 4), (33, 512), (1029, 20), (1028, 16)])
 def test_two_wave_forward_is_bitwise_the_one_wave_forward(cuda_device, fixed, chunk, n, t):
     """The covariance / mean split over two waves performs the one-wave kernel's operations in its order."""
     print(f"two-wave forward n={n} t={t} chunk={chunk} fixed={fixed}", flush=True)
@@ -153,7 +155,7 @@ def test_two_wave_forward_is_bitwise_the_one_wave_forward(cuda_device, fixed, ch
 
 @pytest.mark.parametrize("abi", ABIS, ids=[a[0] for a in ABIS])
 @pytest.mark.parametrize("final_grads", [False, True])
-@pytest.mark.parametrize("n,t", [(1, 16), (7, 32), (37, 48), (9, 64), (33, 512)])
+@pytest.mark.parametrize("n,t", [(1, 16), (7, 32), (37, 48), (9, 64), (33, 512), (1029, 32), (1028, 16)])
 def test_three_wave_backward_is_bitwise_the_one_wave_backward(cuda_device, abi, final_grads, n, t):
     """The covariance replay / covariance reverse / mean split over three waves performs the one-wave
     kernel's operations in its order."""
@@ -176,7 +178,7 @@ NARROW = {"bf16": (torch.bfloat16, None), "e4m3": (torch.float8_e4m3fn, 0), "e5m
 
 @pytest.mark.parametrize("fmt", list(NARROW))
 @pytest.mark.parametrize("fixed", [False, True])
-@pytest.mark.parametrize("n,t,chunk", [(37, 52, 8), (5, 64, 13), (9, 16, 1), (2, 4, 8)])
+@pytest.mark.parametrize("n,t,chunk", [(37, 52, 8), (5, 64, 13), (9, 16, 1), (2, 4, 8), (1029, 16, 8)])
 def test_row_forward_narrow_inputs_equal_float32(cuda_device, fmt, fixed, n, t, chunk):
     """The two-wave row forward with bf16 / float8 keys, values and queries (widened on chip, exactly) gives bit
     for bit the row forward on the widened float32 values; bf16 / float8 streams take it at these sizes by
@@ -205,7 +207,7 @@ def test_row_forward_narrow_inputs_equal_float32(cuda_device, fmt, fixed, n, t, 
 
 @pytest.mark.parametrize("fmt", list(NARROW))
 @pytest.mark.parametrize("fixed,dyn", [(False, True), (False, False), (True, False)])
-@pytest.mark.parametrize("n,t", [(37, 48), (5, 16), (9, 64)])
+@pytest.mark.parametrize("n,t", [(37, 48), (5, 16), (9, 64), (1029, 16)])
 def test_row_backward_narrow_inputs_equal_float32(cuda_device, fmt, fixed, dyn, n, t):
     """The three-wave row backward with bf16 / float8 keys, values and queries: gk, gv, gq are the float32 row
     backward's gradients on the widened values rounded as torch rounds them (.to(dtype)); every other gradient
