@@ -52,9 +52,14 @@ constexpr uint32_t kOob = 0x80000000u;  // offset past every descriptor range: l
 // Cache policies: token streams and checkpoints are loaded and stored with
 // the nontemporal hint (each byte moves once), except the 32- and 64-byte
 // row pieces (p, r and their gradients, covariance records), which stay
-// cached so that partial lines are merged before they reach HBM.
+// cached so that partial lines are merged before they reach HBM.  Streamed
+// stores also carry the system-scope bit (sc1): at config 3 the step runs
+// 8-9 us faster with it (D2M8 12 us; D8M8 and small batches unchanged; the
+// same bit on loads changes nothing), consistent with the stores no longer
+// displacing, in the 256 MB Infinity Cache, the lines the next kernel reads
+// first.
 constexpr bool kNtLoad = true;
-constexpr int kStoreNt = 2;  // gfx9 cache policy: nt
+constexpr int kStoreNt = 18;  // gfx940+ cache policy bits: nt (2) | sc1 (16)
 constexpr int kNtStore = kStoreNt;
 constexpr bool kNtCkpt = true;
 // Tokens are separated by scheduling barriers (forward: every two tokens;
