@@ -542,18 +542,20 @@ __global__ __launch_bounds__(2 * G * kWave) void forward_split_kernel(FwdArgs a)
   const uint32_t row4 = static_cast<uint32_t>(T) * 16u, row8 = static_cast<uint32_t>(T) * 32u,
                  row1 = static_cast<uint32_t>(T) * 4u;
   const uint32_t nbp = static_cast<uint32_t>(a.nb + 1);
-  const int64_t ntiles = (T + TT - 1) / TT;
-  auto in_slot = [&](int64_t t) __attribute__((always_inline)) {
-    return lds + STile::IN + static_cast<int>(t % 3) * STile::SLOT + s * STile::SEQ;
+  // Tile indices in 32-bit arithmetic (T * 32 bytes fits a descriptor's range).
+  const uint32_t T32 = static_cast<uint32_t>(T);
+  const uint32_t ntiles = (T32 + TT - 1) / TT;
+  auto in_slot = [&](uint32_t t) __attribute__((always_inline)) {
+    return lds + STile::IN + static_cast<int>(t % 3u) * STile::SLOT + s * STile::SEQ;
   };
-  auto y_slot = [&](int64_t t) __attribute__((always_inline)) {
-    return lds + STile::Y + static_cast<int>(t & 1) * STile::YSLOT + s * STile::YSEQ;
+  auto y_slot = [&](uint32_t t) __attribute__((always_inline)) {
+    return lds + STile::Y + static_cast<int>(t & 1u) * STile::YSLOT + s * STile::YSEQ;
   };
-  auto bu_slot = [&](int64_t t) __attribute__((always_inline)) {
-    return lds + STile::BU + static_cast<int>(t & 1) * STile::BSLOT + s * STile::BSEQ;
+  auto bu_slot = [&](uint32_t t) __attribute__((always_inline)) {
+    return lds + STile::BU + static_cast<int>(t & 1u) * STile::BSLOT + s * STile::BSEQ;
   };
-  auto tile_len = [&](int64_t t) __attribute__((always_inline)) {
-    return static_cast<int>((T - t * TT) < TT ? (T - t * TT) : TT);
+  auto tile_len = [&](uint32_t t) __attribute__((always_inline)) {
+    return static_cast<int>((T32 - t * TT) < TT ? (T32 - t * TT) : TT);
   };
 
   if (cov_wave) {
@@ -569,8 +571,8 @@ __global__ __launch_bounds__(2 * G * kWave) void forward_split_kernel(FwdArgs a)
     const uint32_t cvo = static_cast<uint32_t>(s) * 64u + cov_off(i, j);
     const uint32_t cco = static_cast<uint32_t>(s) * nbp * 64u + cov_off(i, j);
     v4f sk, sd, sp, sr;
-    auto load = [&](int64_t t) __attribute__((always_inline)) {
-      const uint32_t t0 = static_cast<uint32_t>(t * TT);
+    auto load = [&](uint32_t t) __attribute__((always_inline)) {
+      const uint32_t t0 = t * TT;
       const uint32_t o4 = static_cast<uint32_t>(s) * row4 + (t0 + c) * 16u;
       sk = load_kq<F>(rk, row4n, s, c, t0);
       if constexpr (!FIXED) {
@@ -580,7 +582,7 @@ __global__ __launch_bounds__(2 * G * kWave) void forward_split_kernel(FwdArgs a)
         sr = r4::ld128<false>(rr, o1);
       }
     };
-    auto put = [&](int64_t t) __attribute__((always_inline)) {
+    auto put = [&](uint32_t t) __attribute__((always_inline)) {
       float* b = in_slot(t);
       put_kq<F>(b + STile::K, sk, c);
       if constexpr (!FIXED) {
@@ -603,7 +605,7 @@ __global__ __launch_bounds__(2 * G * kWave) void forward_split_kernel(FwdArgs a)
     __syncthreads();
     int64_t next_ckpt = a.chunk;
     uint32_t ckpt = 1;
-    for (int64_t it = 0; it <= ntiles; ++it) {
+    for (uint32_t it = 0; it <= ntiles; ++it) {
       if (it + 1 < ntiles) {
         r4::vm_wait<0>();
         put(it + 1);
@@ -675,18 +677,18 @@ __global__ __launch_bounds__(2 * G * kWave) void forward_split_kernel(FwdArgs a)
     const uint32_t mo = static_cast<uint32_t>(s) * 128u + mean_off(i, j);
     const uint32_t cmo = static_cast<uint32_t>(s) * nbp * 128u + mean_off(i, j);
     v4f sq, sv0, sv1;
-    auto load = [&](int64_t t) __attribute__((always_inline)) {
-      const uint32_t t0 = static_cast<uint32_t>(t * TT);
+    auto load = [&](uint32_t t) __attribute__((always_inline)) {
+      const uint32_t t0 = t * TT;
       sq = load_kq<F>(rq, row4n, s, c, t0);
       load_v<F>(sv0, sv1, rv, row8n, s, c, t0);
     };
-    auto put = [&](int64_t t) __attribute__((always_inline)) {
+    auto put = [&](uint32_t t) __attribute__((always_inline)) {
       float* b = in_slot(t);
       put_kq<F>(b + STile::Q, sq, c);
       put_v<F>(b + STile::V, sv0, sv1, c);
     };
     // Readouts of tile t leave its y slot as whole pieces (valid tokens only).
-    auto store_y = [&](int64_t t) __attribute__((always_inline)) {
+    auto store_y = [&](uint32_t t) __attribute__((always_inline)) {
       const float* yb = y_slot(t);
       const v4f y0 = *reinterpret_cast<const v4f*>(yb + 4 * c);
       const v4f y1 = *reinterpret_cast<const v4f*>(yb + 64 + 4 * c);
@@ -718,7 +720,7 @@ __global__ __launch_bounds__(2 * G * kWave) void forward_split_kernel(FwdArgs a)
     __syncthreads();
     int64_t next_ckpt = a.chunk;
     uint32_t ckpt = 1;
-    for (int64_t it = 0; it <= ntiles; ++it) {
+    for (uint32_t it = 0; it <= ntiles; ++it) {
       if (it >= 2) store_y(it - 2);
       if (it + 1 < ntiles) {
         r4::vm_wait<0>();
@@ -726,7 +728,7 @@ __global__ __launch_bounds__(2 * G * kWave) void forward_split_kernel(FwdArgs a)
         if (it + 2 < ntiles) load(it + 2);
       }
       if (it >= 1) {
-        const int64_t tl = it - 1;
+        const uint32_t tl = it - 1;
         const float* b = in_slot(tl);
         const float* bu = bu_slot(tl);
         float* yb = y_slot(tl);
