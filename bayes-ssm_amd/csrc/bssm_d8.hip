@@ -421,7 +421,274 @@ __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(1, 1))) v
   }
 }
 
+// ------------------------------------------------------------- forward
+// The backward's lane layout and step(), so the backward's replay rebuilds
+// the forward's beliefs bit for bit.  16-token tiles are staged in
+// registers (the next tile's loads are in flight while the current one is
+// computed from LDS); every load instruction covers whole 512-byte row
+// segments of two sequences, and the pieces are written to the token-major
+// LDS layout [t][s][8] whose XOR-ordered per-token reads hit 64 distinct
+// banks.  Readouts overwrite the consumed values in LDS and leave through
+// the loads' map.  Belief records are stored entry by entry from the
+// rotated registers (cached, so each record's lines are merged before they
+// reach HBM).
+struct FwdSlot {
+  static constexpr int K = 0, D = 1024, Q = 2048, V = 3072, P = 4096, R = 4224, SIZE = 4352;
+};
+constexpr int kFwdTile = 16;
+
+// Register staging of one tile: 8-value streams, instruction I < 4: lane l
+// -> sequence 2 I + (l >> 5), piece l & 31 (token (l & 31) >> 1, half l & 1);
+// p, r: lanes < 32 -> sequence l >> 2, tokens 4 (l & 3) .. + 3.
+struct FwdStage {
+  v4f k[4], d[4], q[4], v[4], p, r;
+};
+
+template <bool FIXED>
+__global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(2))) void forward_kernel(FwdArgs a) {
+  __shared__ float tile[FwdSlot::SIZE];
+  const int lane = threadIdx.x;
+  const int g = lane & 7, s = lane >> 3;
+  const int64_t n0 = static_cast<int64_t>(blockIdx.x) * SPW;
+  const int64_t T = a.t;
+  const uint32_t valid = static_cast<uint32_t>((a.n - n0) < SPW ? (a.n - n0) : SPW);
+  const uint32_t row8 = static_cast<uint32_t>(T) * 32u, row1 = static_cast<uint32_t>(T) * 4u;
+  const Rsrc rk = make_rsrc(a.k + n0 * T * 8, valid * row8);
+  const Rsrc rq = make_rsrc(a.q + n0 * T * 8, valid * row8);
+  const Rsrc rv = make_rsrc(a.v + n0 * T * 8, valid * row8);
+  const Rsrc ry = make_rsrc(a.y + n0 * T * 8, valid * row8);
+  const Rsrc rd = make_rsrc(FIXED ? a.k : a.d + n0 * T * 8, FIXED ? 0u : valid * row8);
+  const Rsrc rp = make_rsrc(FIXED ? a.k : a.p + n0 * T, FIXED ? 0u : valid * row1);
+  const Rsrc rr = make_rsrc(FIXED ? a.k : a.r + n0 * T, FIXED ? 0u : valid * row1);
+  const uint32_t nbp = static_cast<uint32_t>(a.nb + 1);
+  const Rsrc rbm = make_rsrc(a.bm + n0 * nbp * 64, valid * nbp * 256u);
+  const Rsrc rbc = make_rsrc(a.bc + n0 * nbp * 64, valid * nbp * 256u);
+
+  // Load / store map of the 8-value streams (byte offset inside the row
+  // block, relative to the tile's first token; LDS float offset).
+  const int c32 = lane & 31, tok8 = c32 >> 1;
+  uint32_t o8[4];
+  int l8[4];
+#pragma unroll
+  for (int I = 0; I < 4; ++I) {
+    const int sq = 2 * I + (lane >> 5);
+    o8[I] = static_cast<uint32_t>(sq) * row8 + static_cast<uint32_t>(c32) * 16u;
+    l8[I] = 64 * tok8 + 8 * sq + 4 * (lane & 1);
+  }
+  const int tok1 = 4 * (lane & 3);
+  const uint32_t o1 = lane < 32 ? static_cast<uint32_t>(lane >> 2) * row1 + static_cast<uint32_t>(lane & 3) * 16u
+                                : kOob;
+
+  // XOR-ordered LDS reads of a token row (token 0; token t adds 64 t).
+  int ix[8];
+#pragma unroll
+  for (int m = 0; m < 8; ++m) ix[m] = s * 8 + (g ^ m);
+
+  // Belief of the lane: covariance row g and mean column g, XOR order.
+  Bel b;
+  {
+    const Rsrc rm0 = make_rsrc(a.m0 + n0 * 64, valid * 256u);
+    const Rsrc rc0 = make_rsrc(a.c0 + n0 * 64, valid * 256u);
+#pragma unroll
+    for (int m = 0; m < 8; ++m) {
+      b.P[m] = r4::ld32(rc0, static_cast<uint32_t>(s * 256 + g * 32 + (g ^ m) * 4), 0);
+      b.Mv[m] = r4::ld32(rm0, static_cast<uint32_t>(s * 256 + (g ^ m) * 32 + g * 4), 0);
+    }
+  }
+  vm_wait<0>();
+  const uint32_t rec_seq = static_cast<uint32_t>(s) * nbp * 256u;
+  auto store_bel = [&](Rsrc rm, Rsrc rc, uint32_t base, uint32_t soff) __attribute__((always_inline)) {
+#pragma unroll
+    for (int m = 0; m < 8; ++m) {
+      r4::st32(rc, b.P[m], base + static_cast<uint32_t>(g * 32 + (g ^ m) * 4), soff);
+      r4::st32(rm, b.Mv[m], base + static_cast<uint32_t>((g ^ m) * 32 + g * 4), soff);
+    }
+  };
+  // Record c, entry by entry (records inside a tile's first half).
+  auto store_ckpt = [&](uint32_t c) __attribute__((always_inline)) { store_bel(rbm, rbc, rec_seq, c * 256u); };
+  // Record c through LDS: the belief is written over the spent first half
+  // of the tile's K (means) and D (covariances) regions, each sequence's
+  // 8 x 8 block with row r at position (r + s) % 8 (the XOR-ordered writes
+  // of 64 lanes then hit 64 distinct banks), read back as 16-byte pieces
+  // (instruction j < 2: lane l -> sequence 4 j + (l >> 4), piece l & 15)
+  // and stored as whole records.
+  const int rp_seq = lane >> 4, rp_row = (lane >> 1) & 7, rp_half = lane & 1;
+  uint32_t orec[2];
+  int lrec[2];
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const int sp = 4 * j + rp_seq;
+    orec[j] = static_cast<uint32_t>(sp) * nbp * 256u + static_cast<uint32_t>(lane & 15) * 16u;
+    lrec[j] = sp * 64 + ((rp_row + sp) & 7) * 8 + 4 * rp_half;
+  }
+  auto stage_ckpt = [&](uint32_t c) __attribute__((always_inline)) {
+#pragma unroll
+    for (int m = 0; m < 8; ++m) {
+      tile[FwdSlot::K + s * 64 + (((g ^ m) + s) & 7) * 8 + g] = b.Mv[m];
+      tile[FwdSlot::D + s * 64 + ((g + s) & 7) * 8 + (g ^ m)] = b.P[m];
+    }
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const v4f pm = *reinterpret_cast<const v4f*>(&tile[FwdSlot::K + lrec[j]]);
+      const v4f pc = *reinterpret_cast<const v4f*>(&tile[FwdSlot::D + lrec[j]]);
+      st128<2>(rbm, pm, orec[j], c * 256u);
+      st128<2>(rbc, pc, orec[j], c * 256u);
+    }
+  };
+  stage_ckpt(0);
+
+  auto load = [&](FwdStage& x, uint32_t t0) __attribute__((always_inline)) {
+    const bool full = static_cast<int64_t>(t0) + kFwdTile <= T;
+    const bool in8 = full || static_cast<int64_t>(t0) + tok8 < T, in1 = full || static_cast<int64_t>(t0) + tok1 < T;
+    const uint32_t s8 = t0 * 32u, s1 = t0 * 4u;
+#pragma unroll
+    for (int I = 0; I < 4; ++I) {
+      const uint32_t off = in8 ? o8[I] : kOob;
+      x.k[I] = r4::ld128<kNt>(rk, off, s8);
+      if constexpr (!FIXED) x.d[I] = r4::ld128<kNt>(rd, off, s8);
+      x.q[I] = r4::ld128<kNt>(rq, off, s8);
+      x.v[I] = r4::ld128<kNt>(rv, off, s8);
+    }
+    if constexpr (!FIXED) {
+      const uint32_t off = (in1 && o1 != kOob) ? o1 : kOob;
+      x.p = r4::ld128<false>(rp, off, s1);
+      x.r = r4::ld128<false>(rr, off, s1);
+    }
+  };
+  auto put = [&](const FwdStage& x) __attribute__((always_inline)) {
+#pragma unroll
+    for (int I = 0; I < 4; ++I) {
+      *reinterpret_cast<v4f*>(&tile[FwdSlot::K + l8[I]]) = x.k[I];
+      if constexpr (!FIXED) *reinterpret_cast<v4f*>(&tile[FwdSlot::D + l8[I]]) = x.d[I];
+      *reinterpret_cast<v4f*>(&tile[FwdSlot::Q + l8[I]]) = x.q[I];
+      *reinterpret_cast<v4f*>(&tile[FwdSlot::V + l8[I]]) = x.v[I];
+    }
+    if constexpr (!FIXED) {
+      if (lane < 32) {
+        *reinterpret_cast<v4f*>(&tile[FwdSlot::P + 4 * lane]) = x.p;
+        *reinterpret_cast<v4f*>(&tile[FwdSlot::R + 4 * lane]) = x.r;
+      }
+    }
+  };
+  auto read_tok = [&](int tt, Tok& x, float (&qx)[8]) __attribute__((always_inline)) {
+#pragma unroll
+    for (int m = 0; m < 8; ++m) {
+      x.kx[m] = tile[FwdSlot::K + 64 * tt + ix[m]];
+      x.dx[m] = FIXED ? kFixedDecay : tile[FwdSlot::D + 64 * tt + ix[m]];
+      qx[m] = tile[FwdSlot::Q + 64 * tt + ix[m]];
+    }
+    x.v = tile[FwdSlot::V + 64 * tt + ix[0]];
+    x.p = FIXED ? kFixedProcess : tile[FwdSlot::P + 16 * s + tt];
+    x.r = FIXED ? kFixedObservation : tile[FwdSlot::R + 16 * s + tt];
+  };
+  // One token: the step, then the readout y_g = sum_j M[j][g] q_j of the
+  // mean after it, into the token's value slot.
+  auto token = [&](int tt, const Tok& x, const float (&qx)[8]) __attribute__((always_inline)) {
+    Hist h;
+    step(b, x, a.floor, h);
+    float y = b.Mv[0] * qx[0];
+#pragma unroll
+    for (int m = 1; m < 8; ++m) y = fmaf(b.Mv[m], qx[m], y);
+    tile[FwdSlot::V + 64 * tt + ix[0]] = y;
+  };
+
+  const int64_t ntiles = (T + kFwdTile - 1) / kFwdTile;
+  const bool fast = a.chunk % 8 == 0;
+  int64_t next_ckpt = a.chunk;
+  uint32_t ckpt = 1;
+  FwdStage x;
+  if (ntiles > 0) load(x, 0);
+  v4f ys[4];
+  for (int64_t ti = 0; ti < ntiles; ++ti) {
+    const uint32_t t0 = static_cast<uint32_t>(ti) * kFwdTile;
+    const int len = static_cast<int>((T - t0) < kFwdTile ? (T - t0) : kFwdTile);
+    // The previous tile's readouts leave LDS before this tile lands there.
+    if (ti > 0) {
+#pragma unroll
+      for (int I = 0; I < 4; ++I) ys[I] = *reinterpret_cast<const v4f*>(&tile[FwdSlot::V + l8[I]]);
+    }
+    vm_wait<0>();
+    put(x);
+    if (ti > 0) {
+      const uint32_t s8 = (t0 - kFwdTile) * 32u;
+#pragma unroll
+      for (int I = 0; I < 4; ++I) st128<kNtSt>(ry, ys[I], o8[I], s8);
+    }
+    if (ti + 1 < ntiles) load(x, t0 + kFwdTile);
+    lds_wait();
+    if (fast) {
+      // Records fall on 8-token boundaries (T is a multiple of 8); each is
+      // staged after the token before it, over the spent first half.
+#pragma unroll
+      for (int hh = 0; hh < 2; ++hh) {
+        if (hh * 8 >= len) break;
+        Tok cur, nxt;
+        float qc[8], qn[8];
+        read_tok(8 * hh, cur, qc);
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+          const int tt = 8 * hh + u;
+          if (u + 1 < 8) read_tok(tt + 1, nxt, qn);
+          __builtin_amdgcn_sched_barrier(0);
+          token(tt, cur, qc);
+          __builtin_amdgcn_sched_barrier(0);
+          cur = nxt;
+#pragma unroll
+          for (int m = 0; m < 8; ++m) qc[m] = qn[m];
+        }
+        const int64_t te = static_cast<int64_t>(t0) + 8 * (hh + 1);
+        if (te == next_ckpt && te < T) {
+          stage_ckpt(ckpt++);
+          next_ckpt += a.chunk;
+        }
+      }
+    } else {
+      for (int tt = 0; tt < len; ++tt) {
+        if (static_cast<int64_t>(t0) + tt == next_ckpt) {
+          store_ckpt(ckpt++);
+          next_ckpt += a.chunk;
+        }
+        Tok cur;
+        float qc[8];
+        read_tok(tt, cur, qc);
+        token(tt, cur, qc);
+      }
+    }
+  }
+  if (ntiles > 0) {
+    // The last tile's readouts (pieces of tokens past T are dropped).
+    const uint32_t t0 = static_cast<uint32_t>(ntiles - 1) * kFwdTile;
+    lds_wait();
+    const bool in8 = static_cast<int64_t>(t0) + tok8 < T;
+#pragma unroll
+    for (int I = 0; I < 4; ++I) {
+      const v4f yv = *reinterpret_cast<const v4f*>(&tile[FwdSlot::V + l8[I]]);
+      st128<kNtSt>(ry, yv, in8 ? o8[I] : kOob, t0 * 32u);
+    }
+  }
+  const Rsrc rmT = make_rsrc(a.mT + n0 * 64, valid * 256u);
+  const Rsrc rcT = make_rsrc(a.cT + n0 * 64, valid * 256u);
+  store_bel(rmT, rcT, static_cast<uint32_t>(s) * 256u, 0);
+  stage_ckpt(static_cast<uint32_t>(a.nb));
+}
+
 }  // namespace d8
+
+// D = 8, M = 8 forward: T a positive multiple of 8, any checkpoint chunk,
+// 16-byte aligned streams (the records are stored entry by entry).
+bool d8_forward_ok(const FwdArgs& a) {
+  return a.vec_kqd && a.vec_v && a.vec_pr && a.in_fmt == kInF32 && a.t > 0 && a.t % 8 == 0 &&
+         a.t * 256 < (int64_t(1) << 31) && (a.nb + 1) * 2048 < (int64_t(1) << 31);
+}
+
+hipError_t launch_forward_d8(bool fixed, const FwdArgs& a, hipStream_t stream) {
+  const int64_t blocks = (a.n + d8::SPW - 1) / d8::SPW;
+  if (blocks == 0) return hipSuccess;
+  const dim3 grid(static_cast<unsigned>(blocks)), block(kWave);
+  if (fixed) hipLaunchKernelGGL((d8::forward_kernel<true>), grid, block, 0, stream, a);
+  else hipLaunchKernelGGL((d8::forward_kernel<false>), grid, block, 0, stream, a);
+  return hipGetLastError();
+}
 
 // D = 8, M = 8 with T a positive multiple of 8, the preferred checkpoint
 // chunk (8), 16-byte aligned streams and 16-byte aligned checkpoint tensors.

@@ -116,10 +116,13 @@ bool d2_backward_ok(const BwdArgs& a);
 hipError_t launch_forward_d2(bool fixed, const FwdArgs& a, hipStream_t stream);
 hipError_t launch_backward_d2(bool fixed, bool dyn, const BwdArgs& a, hipStream_t stream);
 
-// D = 8, M = 8 checkpoint-replay backward with 8 lanes per sequence in XOR
-// order (bssm_d8.hip): T a positive multiple of 8, the checkpoint chunk 8
-// (the library's preferred one for D = 8), 16-byte aligned streams and
-// checkpoint tensors.  Other shapes take the generic kernels.
+// D = 8, M = 8 kernels with 8 lanes per sequence in XOR order (bssm_d8.hip).
+// The forward needs 16-byte aligned float32 streams and T a positive
+// multiple of 8 (any checkpoint chunk); the checkpoint-replay backward also
+// needs the checkpoint chunk 8 (the library's preferred one for D = 8) and
+// 16-byte aligned checkpoint tensors.  Other shapes take the generic kernels.
+bool d8_forward_ok(const FwdArgs& a);
+hipError_t launch_forward_d8(bool fixed, const FwdArgs& a, hipStream_t stream);
 bool d8_backward_ok(const BwdArgs& a);
 hipError_t launch_backward_d8(bool fixed, bool dyn, const BwdArgs& a, hipStream_t stream);
 

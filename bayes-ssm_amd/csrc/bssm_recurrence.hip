@@ -498,6 +498,7 @@ hipError_t launch_forward(int key_dim, bool fixed, const FwdArgs& a, hipStream_t
   if (key_dim == 4 && a.rot4) return launch_forward_r4(fixed, a, stream);
   if (key_dim == 1 && d1_forward_ok(a)) return launch_forward_d1(fixed, a, stream);
   if (key_dim == 2 && d2_forward_ok(a)) return launch_forward_d2(fixed, a, stream);
+  if (key_dim == 8 && d8_forward_ok(a)) return launch_forward_d8(fixed, a, stream);
   switch (key_dim) {
     case 1: return fixed ? launch_forward_d<1, true>(a, stream) : launch_forward_d<1, false>(a, stream);
     case 2: return fixed ? launch_forward_d<2, true>(a, stream) : launch_forward_d<2, false>(a, stream);

@@ -1,9 +1,10 @@
 """GPU parity of the D = 8, M = 8 kernels against the float64 oracle.
 
-The forward is the generic kernel (bssm_recurrence.hip, any T and chunk); the backward is bssm_d8.hip, for T a
-positive multiple of 8 with the library's preferred checkpoint chunk (8).  Their reference is
-bayes_ssm/persistent_bayes_chunked_d8.cu:209-419.  Cases: the forward's outputs, final state and every
-checkpoint record at chunks that are and are not multiples of 8, their chunk invariance (bit for bit);
+Both kernels are bssm_d8.hip for T a positive multiple of 8 (the forward at any chunk, the backward at the
+library's preferred checkpoint chunk, 8); other T take the generic kernels (bssm_recurrence.hip; T = 44 below).
+Their reference is bayes_ssm/persistent_bayes_chunked_d8.cu:209-419.  Cases: the forward's outputs, final state
+and every checkpoint record at chunks that are and are not multiples of 8 (records between and inside 8-token
+blocks), with full and partial 16-token tiles, their chunk invariance (bit for bit);
 every backward ABI, with and without final-state gradients, T from one chunk to several; N = 13 (a partial
 last wave of 8 sequences).  Tolerance (north star): 1e-5 relative, 1e-4 absolute.
 """
@@ -32,7 +33,7 @@ def ext(cuda_device):
 
 @pytest.mark.parametrize("fixed", [False, True])
 @pytest.mark.parametrize("chunk", [1, 5, 8, 13, 16, 64])
-@pytest.mark.parametrize("t", [8, 16, 40, 64])
+@pytest.mark.parametrize("t", [8, 16, 40, 44, 64])
 def test_d8_forward_matches_oracle(ext, cuda_device, fixed, chunk, t):
     print(f"d8 forward fixed={fixed} chunk={chunk} t={t}", flush=True)
     n = 13
@@ -112,16 +113,17 @@ def test_d8_backward_matches_oracle(ext, cuda_device, abi, final_grads, t):
 
 
 def test_d8_backward_sequences_independent(ext, cuda_device):
-    """A sequence's gradients are the same bits whichever wave slot it lands in (8 sequences per wave)."""
+    """A sequence's outputs, records and gradients are the same bits whichever wave slot it lands in (8
+    sequences per wave, forward and backward)."""
     n, t, chunk = 16, 24, 8
     _, dev = _case(n, t, D, seed=321, device=cuda_device)
     perm = torch.roll(torch.arange(n), 3)
 
     def run(x):
-        _, _, _, bm, bc = ext.forward_chunked(x["k"], x["v"], x["q"], x["d"], x["p"], x["r"], x["m0"], x["c0"],
-                                              chunk, 1e-6)
-        return ext.backward_chunked(x["k"], x["v"], x["q"], x["d"], x["p"], x["r"], x["m0"], x["c0"], bm, bc,
-                                    x["gy"], x["gmf"], x["gcf"], chunk, 1e-6)
+        fwd = ext.forward_chunked(x["k"], x["v"], x["q"], x["d"], x["p"], x["r"], x["m0"], x["c0"], chunk, 1e-6)
+        bm, bc = fwd[3], fwd[4]
+        return (*fwd, *ext.backward_chunked(x["k"], x["v"], x["q"], x["d"], x["p"], x["r"], x["m0"], x["c0"], bm,
+                                            bc, x["gy"], x["gmf"], x["gcf"], chunk, 1e-6))
 
     base = run(dev)
     moved = run({k: v[perm.to(v.device)].contiguous() for k, v in dev.items()})
