@@ -429,9 +429,11 @@ __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(1, 1))) v
 // segments of two sequences, and the pieces are written to the token-major
 // LDS layout [t][s][8] whose XOR-ordered per-token reads hit 64 distinct
 // banks.  Readouts overwrite the consumed values in LDS and leave through
-// the loads' map.  Belief records are stored entry by entry from the
-// rotated registers (cached, so each record's lines are merged before they
-// reach HBM).
+// the loads' map.  Checkpoint records at 8-token boundaries are staged
+// through the spent half of the tile and leave as whole 16-byte pieces
+// (cached: 8 us faster than with the nontemporal hint, and 80 us faster
+// than 4-byte stores from the XOR-ordered registers); other records are
+// stored entry by entry.
 struct FwdSlot {
   static constexpr int K = 0, D = 1024, Q = 2048, V = 3072, P = 4096, R = 4224, SIZE = 4352;
 };
@@ -531,8 +533,8 @@ __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(2))) void
     for (int j = 0; j < 2; ++j) {
       const v4f pm = *reinterpret_cast<const v4f*>(&tile[FwdSlot::K + lrec[j]]);
       const v4f pc = *reinterpret_cast<const v4f*>(&tile[FwdSlot::D + lrec[j]]);
-      st128<2>(rbm, pm, orec[j], c * 256u);
-      st128<2>(rbc, pc, orec[j], c * 256u);
+      st128<0>(rbm, pm, orec[j], c * 256u);
+      st128<0>(rbc, pc, orec[j], c * 256u);
     }
   };
   stage_ckpt(0);
