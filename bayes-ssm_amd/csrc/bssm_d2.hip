@@ -14,20 +14,25 @@
 // replay needs no cross-lane traffic and the reverse's sums over value
 // columns are 4-lane DPP all-reduces.
 //
-// The backward's inputs arrive by LDS-DMA one block ahead, in blocks of 8
-// tokens (one checkpoint chunk); k, d and q come per pair of blocks (16
-// tokens, whole 128-byte rows per sequence: 8-token pieces are half lines,
-// and their lines were fetched once per half).  LDS layouts (floats):
+// The backward's inputs arrive one block ahead, in blocks of 8 tokens (one
+// checkpoint chunk): p, r and the checkpoint records by LDS-DMA; v and gy
+// through registers, each load instruction requesting whole 256-byte row
+// segments of four sequences (a DMA instruction could only fill the
+// token-major layout from 64-byte pieces of 16 rows); k, d and q by LDS-DMA
+// per pair of blocks (16 tokens, whole 128-byte rows per sequence: 8-token
+// pieces are half lines, and their lines were fetched once per half).
+// LDS layouts (floats):
 //   k, d, q (two per token): piece-major [8 pieces][16 seq][2 tokens x 2]
 //     per pair, in two pair buffers;
 //   p, r: piece-major [2 pieces][16 seq][4 tokens] (the DMA instruction's
 //     upper 32 lanes are idle and fill the padding after it with zeros);
-//   v, gy: token-major [8][16 seq][8 col], so lane l reads floats
-//     128 t + 2 l, 2 l + 1 of token t;
+//   v, gy: token-major [8][16 seq][8 col] with the sequences of token t in
+//     XOR order (sequence s at position s ^ t), so lane l = 4 s + g reads
+//     floats 128 t + 8 (s ^ t) + 2 g, + 1 of token t;
 //   checkpoint records: mean [16 seq][2][8], covariance [16 seq][2][2]
 //     (+ padding).
 // Gradients overwrite their inputs in place and leave as 16-byte pieces
-// through the same maps.
+// through the same maps (dL/dv through the row-segment map of v).
 
 #include "bssm_rot4.h"
 #include "bssm_step.h"
@@ -72,19 +77,11 @@ __device__ __forceinline__ void lds2_store(float* p, v2f x) { *reinterpret_cast<
 // of a block starting at token t0.
 struct Map {
   uint32_t s_base, s_piece;  // p/r: sequence j & 15, piece j >> 4 (4 tokens), lanes < 32
-  uint32_t v_base, v_tok;    // v/gy: token 2 i + (j >> 5), sequence (j >> 1) & 15, half j & 1
-  __device__ __forceinline__ Map(int lane, uint32_t row1, uint32_t row8)
-      : s_base(static_cast<uint32_t>(lane & 15) * row1),
-        s_piece(static_cast<uint32_t>(lane >> 4)),
-        v_base(static_cast<uint32_t>((lane >> 1) & 15) * row8 + static_cast<uint32_t>(lane & 1) * 16u),
-        v_tok(static_cast<uint32_t>(lane >> 5)) {}
+  __device__ __forceinline__ Map(int lane, uint32_t row1)
+      : s_base(static_cast<uint32_t>(lane & 15) * row1), s_piece(static_cast<uint32_t>(lane >> 4)) {}
   __device__ __forceinline__ uint32_t s(uint32_t t0, uint32_t T) const {
     const uint32_t t = t0 + 4u * s_piece;
     return (s_piece < 2u && t < T) ? s_base + 4u * t : kOob;
-  }
-  __device__ __forceinline__ uint32_t v(int i, uint32_t t0, uint32_t T) const {
-    const uint32_t t = t0 + 2u * i + v_tok;
-    return t < T ? v_base + 32u * t : kOob;
   }
 };
 
@@ -118,7 +115,7 @@ struct Piece {
 // Piece pc (tokens 4 pc .. 4 pc + 3 of the block) of slot sl, with the
 // block's k, d, q at kq (its half of the pair area).
 template <bool FIXED>
-__device__ __forceinline__ void read_piece(const float* sl, const float* kq, int pc, int seq, int lane,
+__device__ __forceinline__ void read_piece(const float* sl, const float* kq, int pc, int seq, const int (&vsw)[8],
                                            bool need_v, bool need_q, Piece& x) {
 #pragma unroll
   for (int h = 0; h < 2; ++h) {
@@ -137,7 +134,7 @@ __device__ __forceinline__ void read_piece(const float* sl, const float* kq, int
   }
   if (need_v) {
 #pragma unroll
-    for (int j = 0; j < 4; ++j) x.v[j] = lds2(sl + Slot::V + 128 * (4 * pc + j) + 2 * lane);
+    for (int j = 0; j < 4; ++j) x.v[j] = lds2(sl + Slot::V + 128 * (4 * pc + j) + vsw[4 * pc + j]);
   }
 }
 
@@ -460,7 +457,7 @@ __global__ __launch_bounds__(kWave) void backward_kernel(BwdArgs a) {
   const uint32_t nbp = static_cast<uint32_t>(a.nb + 1);
   const Rsrc rbm = make_rsrc(a.bm + n0 * nbp * 16, valid * nbp * 64u);
   const Rsrc rbc = make_rsrc(a.bc + n0 * nbp * 4, valid * nbp * 16u);
-  const Map mp(lane, row1, row8);
+  const Map mp(lane, row1);
   // Checkpoint record DMA: mean records by (sequence j >> 2, piece j & 3),
   // covariance records by lanes j < 16.
   const uint32_t ckm_off = static_cast<uint32_t>(lane >> 2) * nbp * 64u + 16u * (lane & 3);
@@ -486,6 +483,43 @@ __global__ __launch_bounds__(kWave) void backward_kernel(BwdArgs a) {
     Gs[2] = 0.5f * (gcf[3] + gcf[3]);
   }
   float gc0[4] = {0.f, 0.f, 0.f, 0.f};
+
+  // v, gy and dL/dv move as whole 256-byte row segments: load instruction
+  // I < 4, lane l -> sequence 4 I + (l >> 4), piece l & 15 (token
+  // (l & 15) >> 1, half l & 1) of the block, staged in registers one block
+  // ahead and written into the XOR-ordered token-major layout (4-way bank
+  // use per write, the minimum for 16-byte writes).
+  const int vt = (lane & 15) >> 1;
+  uint32_t vo[4];
+  int vl[4];
+#pragma unroll
+  for (int I = 0; I < 4; ++I) {
+    const int sq = 4 * I + (lane >> 4);
+    vo[I] = static_cast<uint32_t>(sq) * row8 + static_cast<uint32_t>(lane & 15) * 16u;
+    vl[I] = 128 * vt + 8 * (sq ^ vt) + 4 * (lane & 1);
+  }
+  // Per-token offsets of the lane's own pair (token t of a block).
+  int vsw[8];
+#pragma unroll
+  for (int t = 0; t < 8; ++t) vsw[t] = 8 * (seq ^ t) + 2 * g;
+  v4f sv[4], sgy[4];
+  auto load_v = [&](uint32_t blk) __attribute__((always_inline)) {
+    const uint32_t t0 = blk * BT;
+    const bool in = t0 + static_cast<uint32_t>(vt) < T;
+#pragma unroll
+    for (int I = 0; I < 4; ++I) {
+      const uint32_t off = in ? vo[I] : kOob;
+      sv[I] = r4::ld128<kNt>(rv, off, t0 * 32u);
+      sgy[I] = r4::ld128<kNt>(rgy, off, t0 * 32u);
+    }
+  };
+  auto put_v = [&](float* sl) __attribute__((always_inline)) {
+#pragma unroll
+    for (int I = 0; I < 4; ++I) {
+      lds4_store(sl + Slot::V + vl[I], sv[I]);
+      lds4_store(sl + Slot::GY + vl[I], sgy[I]);
+    }
+  };
 
   const uint32_t nblk = (T + BT - 1) / BT;
   // k, d, q of pair m: instruction i, lane j covers piece 4 i + (j >> 4)
@@ -522,12 +556,6 @@ __global__ __launch_bounds__(kWave) void backward_kernel(BwdArgs a) {
       dma16(rp, sl + Slot::P, os);
       dma16(rr, sl + Slot::R, os);
     }
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const uint32_t ov = mp.v(i, t0, T);
-      dma16<kNt>(rv, sl + Slot::V + 256 * i, ov);
-      dma16<kNt>(rgy, sl + Slot::GY + 256 * i, ov);
-    }
     dma16(rbm, sl + Slot::CKM, ckm_off + 64u * blk);
     dma16(rbc, sl + Slot::CKC, ckc_off == kOob ? kOob : ckc_off + 16u * blk);
   };
@@ -539,8 +567,9 @@ __global__ __launch_bounds__(kWave) void backward_kernel(BwdArgs a) {
     const uint32_t os = mp.s(t0, T);
     st128(rgp, DYN ? lds4(sl + Slot::P + e) : zero, os, 0);
     st128(rgr, DYN ? lds4(sl + Slot::R + e) : zero, os, 0);
+    const bool in = t0 + static_cast<uint32_t>(vt) < T;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) st128<kNtSt>(rgv, lds4(sl + Slot::V + 256 * i + e), mp.v(i, t0, T), 0);
+    for (int I = 0; I < 4; ++I) st128<kNtSt>(rgv, lds4(sl + Slot::V + vl[I]), in ? vo[I] : kOob, t0 * 32u);
   };
 
   // Replay the block's chunk from its checkpoint record, then reverse it;
@@ -561,9 +590,9 @@ __global__ __launch_bounds__(kWave) void backward_kernel(BwdArgs a) {
     v2f gy[2][4];
 #pragma unroll
     for (int pc = 0; pc < 2; ++pc) {
-      read_piece<FIXED>(sl, kq, pc, seq, lane, true, true, x[pc]);
+      read_piece<FIXED>(sl, kq, pc, seq, vsw, true, true, x[pc]);
 #pragma unroll
-      for (int j = 0; j < 4; ++j) gy[pc][j] = lds2(sl + Slot::GY + 128 * (4 * pc + j) + 2 * lane);
+      for (int j = 0; j < 4; ++j) gy[pc][j] = lds2(sl + Slot::GY + 128 * (4 * pc + j) + vsw[4 * pc + j]);
     }
     Hist h[kChunk];
 #pragma unroll
@@ -591,7 +620,7 @@ __global__ __launch_bounds__(kWave) void backward_kernel(BwdArgs a) {
           gd[hh][oo + 1] = o.gd[1];
           gp[j] = o.gp;
           gr[j] = o.gr;
-          lds2_store(sl + Slot::V + 128 * (4 * pc + j) + 2 * lane, v2f{o.gv[0], o.gv[1]});
+          lds2_store(sl + Slot::V + 128 * (4 * pc + j) + vsw[4 * pc + j], v2f{o.gv[0], o.gv[1]});
         }
         if (g == 0) {
 #pragma unroll
@@ -621,6 +650,7 @@ __global__ __launch_bounds__(kWave) void backward_kernel(BwdArgs a) {
   if (nblk > 0) {
     issue(tile + ((nblk - 1) & 1) * Slot::BWD, nblk - 1);
     issue_kq(kbuf(npair - 1), npair - 1);
+    load_v(nblk - 1);
   }
   for (uint32_t i = 0; i < nblk; ++i) {
     const uint32_t blk = nblk - 1 - i, m = blk >> 1;
@@ -628,6 +658,8 @@ __global__ __launch_bounds__(kWave) void backward_kernel(BwdArgs a) {
     float* other = tile + ((blk + 1) & 1) * Slot::BWD;
     vm_wait<0>();
     __syncthreads();
+    put_v(cur);
+    if (blk > 0) load_v(blk - 1);
     if (blk + 1 < nblk) store_grads(other, blk + 1);
     if (blk == nblk - 1 || (blk & 1) == 1) {  // first block of pair m
       if (m + 1 < npair) store_kq(kbuf(m + 1), m + 1);
