@@ -1,13 +1,14 @@
 // gfx950 forward and checkpoint-replay backward for D = 2, M = 8
 // (bayes_ssm/persistent_bayes_chunked_d2m8.cu is the reference extension for
 // this shape; the per-token equations are those of bssm_step.h with two key
-// dimensions), with two value columns per lane.  The forward streams its inputs as the generic kernels do (register-staged
-// 16-token tiles, one tile ahead): a version fed by 8-token LDS-DMA blocks
-// measured slower, since this forward does little arithmetic per byte and
-// needs more bytes in flight than such blocks leave.
+// dimensions).  The forward streams its inputs as the generic kernels do
+// (register-staged 16-token tiles, one tile ahead), one value column per
+// lane: a version fed by 8-token LDS-DMA blocks measured slower, since this
+// forward does little arithmetic per byte and needs more bytes in flight
+// than such blocks leave.
 //
-// A wave holds 16 sequences; lane l = 4 s + g owns value columns 2g, 2g + 1
-// of sequence s.  Every lane carries the whole 2 x 2 covariance of its
+// In the backward a wave holds 16 sequences; lane l = 4 s + g owns value
+// columns 2g, 2g + 1 of sequence s.  Every lane carries the whole 2 x 2 covariance of its
 // sequence (the four lanes apply the same operations to the same inputs, so
 // they hold identical values; the two off-diagonal entries are carried
 // separately, as the row owners of the generic kernels carry them), so the
@@ -192,8 +193,13 @@ __device__ __forceinline__ void step(Bel& b, const Tok& x, float floor, Hist& h)
 
 // Forward: the generic kernels' register-staged 16-token tiles (the next
 // tile is loaded into registers while this one is computed, then written
-// into padded LDS rows), with the two-columns-per-lane update above.  Each
-// token's LDS reads are issued one token ahead.
+// into padded LDS rows), with one value column per lane: 8 sequences per
+// wave, so config 3's 16384 sequences give two waves per SIMD (with two
+// columns per lane, one: 170 against 166 us).  The covariance chain is that
+// of step() (every lane of a sequence carries it), and each column's mean
+// update is that of step()'s column loop, so the backward's replay rebuilds
+// the forward's beliefs bit for bit.  Each token's LDS reads are issued one
+// token ahead.
 constexpr int kFwdTile = 16;
 
 struct FwdTok {
@@ -201,73 +207,85 @@ struct FwdTok {
   float p, r;
 };
 
-template <bool FIXED>
-__device__ __forceinline__ FwdTok read_fwd(const float* sk, const float* sq, const float* sv, const float* sd,
-                                           const float* sp, const float* sr, int tt, int lane) {
-  FwdTok x;
-  x.k = lds2(sk + 2 * tt);
-  x.q = lds2(sq + 2 * tt);
-  x.v = lds2(sv + 8 * tt + 2 * (lane & 3));
-  if constexpr (FIXED) {
-    x.d = v2f{kFixedDecay, kFixedDecay};
-    x.p = kFixedProcess;
-    x.r = kFixedObservation;
-  } else {
-    x.d = lds2(sd + 2 * tt);
-    x.p = sp[tt];
-    x.r = sr[tt];
+constexpr int SPW8 = 8;
+
+struct Bel1 {
+  float P[4];
+  float M[2];  // rows 0, 1 of the lane's column
+};
+
+__device__ __forceinline__ void step1(Bel1& b, const FwdTok& x, float floor) {
+  float dp[4], Pb[4], u[2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    float acc = x.p * x.k[i];
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      dp[2 * i + j] = (x.d[i] * x.d[j]) * b.P[2 * i + j];
+      Pb[2 * i + j] = fmaf(x.p, i == j ? 1.f : 0.f, dp[2 * i + j]);
+      acc = fmaf(dp[2 * i + j], x.k[j], acc);
+    }
+    u[i] = acc;
   }
-  return x;
+  const float s = fmaf(x.k[1], u[1], fmaf(x.k[0], u[0], x.r));
+  const float beta = fast_rcp(fmaxf(s, floor));
+  const float wk0 = x.d[0] * x.k[0], wk1 = x.d[1] * x.k[1];
+  const float bu0 = beta * u[0], bu1 = beta * u[1];
+  const float e = fmaf(-b.M[1], wk1, fmaf(-b.M[0], wk0, x.v[0]));
+  b.M[0] = fmaf(bu0, e, x.d[0] * b.M[0]);
+  b.M[1] = fmaf(bu1, e, x.d[1] * b.M[1]);
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j) b.P[2 * i + j] = fmaf(-beta, u[i] * u[j], Pb[2 * i + j]);
 }
 
 template <bool FIXED>
-__global__ __launch_bounds__(kWave) void forward_kernel(FwdArgs a) {
+__global__ __launch_bounds__(kWave) void forward8_kernel(FwdArgs a) {
   constexpr int TT = kFwdTile;
   constexpr int SD = Tile<2, TT>::STRIDE, SM = Tile<8, TT>::STRIDE, S1 = Tile<1, TT>::STRIDE;
-  __shared__ float tk[SPW * SD];
-  __shared__ float tq[SPW * SD];
-  __shared__ float tv[SPW * SM];  // values in, readouts out (in place)
-  __shared__ float td[FIXED ? 1 : SPW * SD];
-  __shared__ float tp[FIXED ? 1 : SPW * S1];
-  __shared__ float tr[FIXED ? 1 : SPW * S1];
+  __shared__ float tk[SPW8 * SD];
+  __shared__ float tq[SPW8 * SD];
+  __shared__ float tv[SPW8 * SM];  // values in, readouts out (in place)
+  __shared__ float td[FIXED ? 1 : SPW8 * SD];
+  __shared__ float tp[FIXED ? 1 : SPW8 * S1];
+  __shared__ float tr[FIXED ? 1 : SPW8 * S1];
   const int lane = threadIdx.x;
-  const int seq = lane >> 2, g = lane & 3;
-  const int64_t n0 = static_cast<int64_t>(blockIdx.x) * SPW;
+  const int seq = lane >> 3, g = lane & 7;
+  const int64_t n0 = static_cast<int64_t>(blockIdx.x) * SPW8;
   const int64_t T = a.t;
-  const uint32_t valid = static_cast<uint32_t>((a.n - n0) < SPW ? (a.n - n0) : SPW);
+  const uint32_t valid = static_cast<uint32_t>((a.n - n0) < SPW8 ? (a.n - n0) : SPW8);
   const uint32_t nbp = static_cast<uint32_t>(a.nb + 1);
   const Rsrc rbm = make_rsrc(a.bm + n0 * nbp * 16, valid * nbp * 64u);
   const Rsrc rbc = make_rsrc(a.bc + n0 * nbp * 4, valid * nbp * 16u);
-  // Belief record offsets of this lane: its column pair of both mean rows,
-  // and the covariance record (written by lane 0 of the sequence).
-  const uint32_t bm_off = static_cast<uint32_t>(seq) * nbp * 64u + 8u * g;
+  // Belief record offsets of this lane: its column of both mean rows (the 8
+  // lanes of a sequence write each 32-byte row together), and the
+  // covariance record (written by lane 0 of the sequence).
+  const uint32_t bm_off = static_cast<uint32_t>(seq) * nbp * 64u + 4u * g;
   const uint32_t bc_off = g == 0 ? static_cast<uint32_t>(seq) * nbp * 16u : kOob;
 
-  Bel b;
+  Bel1 b;
   {
     const Rsrc rm0 = make_rsrc(a.m0 + n0 * 16, valid * 64u);
     const Rsrc rc0 = make_rsrc(a.c0 + n0 * 4, valid * 16u);
-    const uint32_t mo = static_cast<uint32_t>(seq) * 64u + 8u * g;
-    const v2f m0 = r4::ld64(rm0, mo, 0), m1 = r4::ld64(rm0, mo + 32u, 0);
-    b.M[0][0] = m0[0];
-    b.M[0][1] = m0[1];
-    b.M[1][0] = m1[0];
-    b.M[1][1] = m1[1];
+    const uint32_t mo = static_cast<uint32_t>(seq) * 64u + 4u * g;
+    b.M[0] = r4::ld32(rm0, mo, 0);
+    b.M[1] = r4::ld32(rm0, mo + 32u, 0);
     const v4f c = r4::ld128<false>(rc0, static_cast<uint32_t>(seq) * 16u);
 #pragma unroll
     for (int i = 0; i < 4; ++i) b.P[i] = c[i];
   }
   auto store_bel = [&](Rsrc rm, Rsrc rc, uint32_t moff, uint32_t coff, uint32_t soff_m, uint32_t soff_c)
       __attribute__((always_inline)) {
-    st64(rm, v2f{b.M[0][0], b.M[0][1]}, moff, soff_m);
-    st64(rm, v2f{b.M[1][0], b.M[1][1]}, moff + 32u, soff_m);
+    r4::st32(rm, b.M[0], moff, soff_m);
+    r4::st32(rm, b.M[1], moff + 32u, soff_m);
     st128(rc, v4f{b.P[0], b.P[1], b.P[2], b.P[3]}, coff, soff_c);
   };
   store_bel(rbm, rbc, bm_off, bc_off, 0, 0);
 
-  TileRegs<2, TT, SPW> rk, rq, rd;
-  TileRegs<8, TT, SPW> rv;
-  TileRegs<1, TT, SPW> rp, rr;
+  TileRegs<2, TT, SPW8> rk, rq, rd;
+  TileRegs<8, TT, SPW8> rv;
+  TileRegs<1, TT, SPW8> rp, rr;
   auto issue = [&](int64_t t0) __attribute__((always_inline)) {
     const int len = tile_len(T, t0, TT);
     rk.load(a.k, n0, a.n, T, t0, len, lane);
@@ -286,6 +304,22 @@ __global__ __launch_bounds__(kWave) void forward_kernel(FwdArgs a) {
   const float* sd = FIXED ? tk : td + seq * SD;
   const float* sp = FIXED ? tk : tp + seq * S1;
   const float* sr = FIXED ? tk : tr + seq * S1;
+  auto read = [&](int tt) __attribute__((always_inline)) {
+    FwdTok x;
+    x.k = lds2(sk + 2 * tt);
+    x.q = lds2(sq + 2 * tt);
+    x.v[0] = sv[8 * tt + g];
+    if constexpr (FIXED) {
+      x.d = v2f{kFixedDecay, kFixedDecay};
+      x.p = kFixedProcess;
+      x.r = kFixedObservation;
+    } else {
+      x.d = lds2(sd + 2 * tt);
+      x.p = sp[tt];
+      x.r = sr[tt];
+    }
+    return x;
+  };
   const uint32_t chunk = static_cast<uint32_t>(a.chunk);
   uint32_t next_ckpt = chunk, ckpt = 1;
   for (int64_t t0 = 0; t0 < T; t0 += TT) {
@@ -300,39 +334,24 @@ __global__ __launch_bounds__(kWave) void forward_kernel(FwdArgs a) {
     }
     __syncthreads();
     if (t0 + TT < T) issue(t0 + TT);
-    FwdTok cur = read_fwd<FIXED>(sk, sq, sv, sd, sp, sr, 0, lane);
+    FwdTok cur = read(0);
     for (int tt = 0; tt < len; ++tt) {
-      const FwdTok nxt = read_fwd<FIXED>(sk, sq, sv, sd, sp, sr, tt + 1 < len ? tt + 1 : tt, lane);
+      const FwdTok nxt = read(tt + 1 < len ? tt + 1 : tt);
       if (static_cast<uint32_t>(t0) + tt == next_ckpt) {
         store_bel(rbm, rbc, bm_off, bc_off, ckpt * 64u, ckpt * 16u);
         ++ckpt;
         next_ckpt += chunk;
       }
-      Tok x;
-      x.k[0] = cur.k[0];
-      x.k[1] = cur.k[1];
-      x.d[0] = cur.d[0];
-      x.d[1] = cur.d[1];
-      x.q[0] = cur.q[0];
-      x.q[1] = cur.q[1];
-      x.p = cur.p;
-      x.r = cur.r;
-      x.v[0] = cur.v[0];
-      x.v[1] = cur.v[1];
-      Hist h;
-      step(b, x, a.floor, h);
-      v2f y;
-#pragma unroll
-      for (int c = 0; c < 2; ++c) y[c] = fmaf(b.M[1][c], x.q[1], fmaf(b.M[0][c], x.q[0], 0.f));
-      lds2_store(sv + 8 * tt + 2 * g, y);
+      step1(b, cur, a.floor);
+      sv[8 * tt + g] = fmaf(b.M[1], cur.q[1], fmaf(b.M[0], cur.q[0], 0.f));
       cur = nxt;
     }
     __syncthreads();
-    stage_out<8, TT, SPW>(tv, a.y, n0, a.n, T, t0, len, true, lane);
+    stage_out<8, TT, SPW8>(tv, a.y, n0, a.n, T, t0, len, true, lane);
     __syncthreads();
   }
   store_bel(make_rsrc(a.mT + n0 * 16, valid * 64u), make_rsrc(a.cT + n0 * 4, valid * 16u),
-            static_cast<uint32_t>(seq) * 64u + 8u * g, g == 0 ? static_cast<uint32_t>(seq) * 16u : kOob, 0, 0);
+            static_cast<uint32_t>(seq) * 64u + 4u * g, g == 0 ? static_cast<uint32_t>(seq) * 16u : kOob, 0, 0);
   if (T > 0) {
     const uint32_t nb = static_cast<uint32_t>(a.nb);
     store_bel(rbm, rbc, bm_off, bc_off, nb * 64u, nb * 16u);
@@ -697,11 +716,11 @@ bool d2_backward_ok(const BwdArgs& a) {
 }
 
 hipError_t launch_forward_d2(bool fixed, const FwdArgs& a, hipStream_t stream) {
-  const int64_t blocks = (a.n + d2::SPW - 1) / d2::SPW;
+  const int64_t blocks = (a.n + d2::SPW8 - 1) / d2::SPW8;
   if (blocks == 0) return hipSuccess;
   const dim3 grid(static_cast<unsigned>(blocks)), block(kWave);
-  if (fixed) hipLaunchKernelGGL((d2::forward_kernel<true>), grid, block, 0, stream, a);
-  else hipLaunchKernelGGL((d2::forward_kernel<false>), grid, block, 0, stream, a);
+  if (fixed) hipLaunchKernelGGL((d2::forward8_kernel<true>), grid, block, 0, stream, a);
+  else hipLaunchKernelGGL((d2::forward8_kernel<false>), grid, block, 0, stream, a);
   return hipGetLastError();
 }
 
