@@ -19,9 +19,10 @@
 // checkpoint chunk): p, r and the checkpoint records by LDS-DMA; v and gy
 // through registers, each load instruction requesting whole 256-byte row
 // segments of four sequences (a DMA instruction could only fill the
-// token-major layout from 64-byte pieces of 16 rows); k, d and q by LDS-DMA
-// per pair of blocks (16 tokens, whole 128-byte rows per sequence: 8-token
-// pieces are half lines, and their lines were fetched once per half).
+// token-major layout from 64-byte pieces of 16 rows); k, d and q through
+// registers per pair of blocks (16 tokens: whole 128-byte rows per sequence,
+// each requested by one instruction; 8-token pieces are half lines, and
+// their lines were fetched once per half).
 // LDS layouts (floats):
 //   k, d, q (two per token): piece-major [8 pieces][16 seq][2 tokens x 2]
 //     per pair, in two pair buffers;
@@ -541,31 +542,46 @@ __global__ __launch_bounds__(kWave) void backward_kernel(BwdArgs a) {
   };
 
   const uint32_t nblk = (T + BT - 1) / BT;
-  // k, d, q of pair m: instruction i, lane j covers piece 4 i + (j >> 4)
-  // (2 tokens) of sequence j & 15, so each sequence's 128-byte row is
-  // requested by the two instructions back to back.
-  auto kq_off = [&](int i, uint32_t m) __attribute__((always_inline)) {
-    const uint32_t t = 16u * m + 2u * (4u * i + static_cast<uint32_t>(lane >> 4));
-    return t < T ? static_cast<uint32_t>(lane & 15) * row2 + 8u * t : kOob;
-  };
-  auto issue_kq = [&](float* kb, uint32_t m) __attribute__((always_inline)) {
+  // k, d, q of pair m, staged in registers a pair ahead: instruction i,
+  // lane j covers piece j & 7 (2 tokens) of sequence 8 i + (j >> 3), so each
+  // sequence's 128-byte row is requested by 8 lanes of one instruction.
+  const int kq_piece = lane & 7;
+  uint32_t kq_row[2];
+  int kq_lds[2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const int sq = 8 * i + (lane >> 3);
+    kq_row[i] = static_cast<uint32_t>(sq) * row2 + 16u * static_cast<uint32_t>(kq_piece);
+    kq_lds[i] = 64 * kq_piece + 4 * sq;
+  }
+  v4f skk[2], sqq[2], sdd[2];
+  auto load_kq = [&](uint32_t m) __attribute__((always_inline)) {
+    const bool in = 16u * m + 2u * static_cast<uint32_t>(kq_piece) < T;
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
-      const uint32_t off = kq_off(i, m);
-      dma16<kNt>(rk, kb + KQ::K + 256 * i, off);
-      dma16<kNt>(rq, kb + KQ::Q + 256 * i, off);
-      if constexpr (!FIXED) dma16<kNt>(rd, kb + KQ::D + 256 * i, off);
+      const uint32_t off = in ? kq_row[i] : kOob;
+      skk[i] = r4::ld128<kNt>(rk, off, 128u * m);
+      sqq[i] = r4::ld128<kNt>(rq, off, 128u * m);
+      if constexpr (!FIXED) sdd[i] = r4::ld128<kNt>(rd, off, 128u * m);
+    }
+  };
+  auto put_kq = [&](float* kb) __attribute__((always_inline)) {
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      lds4_store(kb + KQ::K + kq_lds[i], skk[i]);
+      lds4_store(kb + KQ::Q + kq_lds[i], sqq[i]);
+      if constexpr (!FIXED) lds4_store(kb + KQ::D + kq_lds[i], sdd[i]);
     }
   };
   auto store_kq = [&](const float* kb, uint32_t m) __attribute__((always_inline)) {
     const v4f zero = v4f{0.f, 0.f, 0.f, 0.f};
+    const bool in = 16u * m + 2u * static_cast<uint32_t>(kq_piece) < T;
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
-      const uint32_t off = kq_off(i, m);
-      const int e = 256 * i + 4 * lane;
-      st128<kNtSt>(rgk, lds4(kb + KQ::K + e), off, 0);
-      st128<kNtSt>(rgq, lds4(kb + KQ::Q + e), off, 0);
-      st128<kNtSt>(rgd, DYN ? lds4(kb + KQ::D + e) : zero, off, 0);
+      const uint32_t off = in ? kq_row[i] : kOob;
+      st128<kNtSt>(rgk, lds4(kb + KQ::K + kq_lds[i]), off, 128u * m);
+      st128<kNtSt>(rgq, lds4(kb + KQ::Q + kq_lds[i]), off, 128u * m);
+      st128<kNtSt>(rgd, DYN ? lds4(kb + KQ::D + kq_lds[i]) : zero, off, 128u * m);
     }
   };
   auto issue = [&](float* sl, uint32_t blk) __attribute__((always_inline)) {
@@ -662,13 +678,14 @@ __global__ __launch_bounds__(kWave) void backward_kernel(BwdArgs a) {
   // memory operation was issued at least a whole block earlier; then the
   // gradients of block b + 1 leave the other slot, which receives block
   // b - 1.  The k, d, q of pair m (blocks 2m, 2m + 1) live in pair buffer
-  // m % 2: at the first block of pair m processed, the gradients of pair
-  // m + 1 leave the other buffer, which receives pair m - 1.
+  // m % 2: at the first block of pair m processed, pair m's k, d, q (staged
+  // in registers during pair m + 1) land there and the loads of pair m - 1
+  // are issued; the gradients of pair m + 1 leave the other buffer.
   const uint32_t npair = (nblk + 1) / 2;
   auto kbuf = [&](uint32_t m) __attribute__((always_inline)) { return kdq + (m & 1) * KQ::SIZE; };
   if (nblk > 0) {
     issue(tile + ((nblk - 1) & 1) * Slot::BWD, nblk - 1);
-    issue_kq(kbuf(npair - 1), npair - 1);
+    load_kq(npair - 1);
     load_v(nblk - 1);
   }
   for (uint32_t i = 0; i < nblk; ++i) {
@@ -681,8 +698,9 @@ __global__ __launch_bounds__(kWave) void backward_kernel(BwdArgs a) {
     if (blk > 0) load_v(blk - 1);
     if (blk + 1 < nblk) store_grads(other, blk + 1);
     if (blk == nblk - 1 || (blk & 1) == 1) {  // first block of pair m
+      put_kq(kbuf(m));
+      if (m > 0) load_kq(m - 1);
       if (m + 1 < npair) store_kq(kbuf(m + 1), m + 1);
-      if (m > 0) issue_kq(kbuf(m + 1), m - 1);
     }
     if (blk > 0) issue(other, blk - 1);
     run_chunk(cur, kbuf(m) + 256 * (blk & 1), (T - blk * BT) < BT ? 1 : 2, blk == 0);
