@@ -52,9 +52,12 @@ __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(1, 1))) v
   using Stage = std::conditional_t<H, FwdStageH, std::conditional_t<Q8, FwdStageQ, FwdStage>>;
   auto load = [&](Stage& x, int64_t t0) __attribute__((always_inline)) {
     if constexpr (Q8) {
+      // A float8 key or query row of 16 tokens is half a 128-byte line: the
+      // cached hint keeps the other half in L2 for the next tile (the
+      // nontemporal one refetched it, about 6 B per token more traffic).
       const uint32_t sk = static_cast<uint32_t>(t0) * 4u, sv = static_cast<uint32_t>(t0) * 8u;
-      x.k = ld128<kNtLoad>(rk, qm.k_off + sk);
-      x.q = ld128<kNtLoad>(rq, qm.k_off + sk);
+      x.k = ld128<false>(rk, qm.k_off + sk);
+      x.q = ld128<false>(rq, qm.k_off + sk);
 #pragma unroll
       for (int I = 0; I < 2; ++I) x.v[I] = ld128<kNtLoad>(rv, qm.v_off[I] + sv);
     }
@@ -295,8 +298,9 @@ __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(1, 1))) v
 #pragma unroll
       for (int I = 0; I < 8; ++I) x.v[I] = ld128<kNtLoad>(rv, in8 ? tm.o8[I] : kOob, s8);
     } else if constexpr (Q8) {
-      x.k = ld128<kNtLoad>(rk, qm.k_off + sk);
-      x.q = ld128<kNtLoad>(rq, qm.k_off + sk);
+      // Half-line float8 rows: cached, as in the forward.
+      x.k = ld128<false>(rk, qm.k_off + sk);
+      x.q = ld128<false>(rq, qm.k_off + sk);
 #pragma unroll
       for (int I = 0; I < 2; ++I) x.v[I] = ld128<kNtLoad>(rv, qm.v_off[I] + sv);
     } else {
