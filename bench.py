@@ -508,8 +508,11 @@ def time_d64(b, t, h, steps, warmup, device, fused=True) -> dict:
         else:
             os.environ["BAYES_SSM_DISABLE_FUSED_CUDA"] = previous
     ms = e0.elapsed_time(e1) / steps
+    fwd_b, bwd_b = algorithmic_bytes(d, d)
     return {"B": b, "T": t, "H": h, "D": d, "M": d, "sequences": n, "ms_per_step": ms,
             "tokens_per_s": b * t / (ms * 1e-3),
+            # The HBM roofline of this shape is far from its bound (the VALU; 256 waves on 1024 SIMDs).
+            "roofline_step_frac": n * t * (fwd_b + bwd_b) / (ms * 1e-3) / HBM_PEAK,
             "path": "HIP D64 kernels" if fused else "reference diagonal core, eager torch"}
 
 
