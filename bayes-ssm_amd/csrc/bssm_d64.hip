@@ -596,18 +596,451 @@ __global__ __launch_bounds__(kWave) void backward_kernel(BwdArgs a) {
   }
 }
 
+// ------------------------------------------- four waves per sequence
+// One workgroup of four waves per sequence: thread (w, l) owns the 16
+// columns J_w = [16 w, 16 w + 16) of covariance row l (P~_lj, j in J_w) and
+// the 16 rows J_w of mean column l (M_il, i in J_w); the diagonal part pd_l
+// and every per-lane scalar (u_l, s, e_l, ...) are carried by all four
+// waves with identical bits.  Sums over j of a row (u = P'k, e = M^T wk,
+// y = M^T q, ...) are four partial sums exchanged through LDS (one barrier),
+// added in the same order by every wave; sums over the lanes of a wave's 16
+// rows go through a wave-private LDS transpose.  The token's k, d, q entries
+// of J_w are wave-uniform (scalar loads); u_j and gu_j of J_w are read from
+// their lanes (v_readlane).  At B32 x H8 (256 sequences) every SIMD holds a
+// wave, and the backward keeps a whole 8-token chunk's history in registers
+// (36 floats per token and thread), so each token is replayed once.
+typedef float v2f __attribute__((ext_vector_type(2)));
+constexpr int kW = 4;           // waves per sequence
+constexpr int kB = D / kW;      // columns (rows) of a wave's block
+constexpr int kThreads = kW * kWave;
+constexpr int kHist = 8;        // backward chunk (tokens of history in registers)
+
+__device__ __forceinline__ int wave_index() { return __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6)); }
+__device__ __forceinline__ float lane_value(float x, int src) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, x), src));
+}
+// ((x0 + x1) + (x2 + x3)) of the four waves' partials: the same bits in every wave.
+__device__ __forceinline__ float sum4(float x0, float x1, float x2, float x3) { return (x0 + x1) + (x2 + x3); }
+
+// Sum over the wave's 64 lanes of each of the lane's 16 values x[ii]: the
+// total of row ii lands in lanes 4 ii .. 4 ii + 3.  `tile` is wave-private
+// (64 rows of 16 floats, the 16-byte pieces of row r rotated by (r >> 2) & 3
+// so that both the row writes and the column reads are free of bank
+// conflicts); a wave's LDS operations complete in issue order, so no barrier
+// separates the writes from the reads.
+__device__ __forceinline__ float wave_rowsum(float* tile, int l, const float (&x)[kB]) {
+  float* row = tile + l * kB;
+  const int rot = (l >> 2) & 3;
+#pragma unroll
+  for (int c = 0; c < kB / 4; ++c)
+    *reinterpret_cast<v4f*>(&row[4 * (c ^ rot)]) = v4f{x[4 * c], x[4 * c + 1], x[4 * c + 2], x[4 * c + 3]};
+  __builtin_amdgcn_wave_barrier();
+  const int ii = l >> 2, qd = l & 3;
+  float acc[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int m = 0; m < kWave / 4; ++m)
+    acc[m & 3] += tile[(4 * m + qd) * kB + 4 * ((ii >> 2) ^ (m & 3)) + (ii & 3)];
+  __builtin_amdgcn_wave_barrier();
+  float t = (acc[0] + acc[1]) + (acc[2] + acc[3]);
+  t = add_rn(t, dpp<kXor1>(t));
+  return add_rn(t, dpp<kXor2>(t));
+}
+
+// Token inputs of thread (w, l): the lane's own entries and the wave's block.
+struct Tok4 {
+  float k, d, v, q, gy, p, r;
+  float kJ[kB], dJ[kB], qJ[kB];
+};
+
+template <bool FIXED, bool GY>
+__device__ __forceinline__ void load_tok4(Tok4& x, const float* k, const float* v, const float* q, const float* d,
+                                          const float* p, const float* r, const float* gy, int t, int l, int j0) {
+  const int e = t * D + l, b = t * D + j0;
+  x.k = k[e];
+  x.v = v[e];
+  x.q = q[e];
+  x.gy = GY ? gy[e] : 0.f;
+#pragma unroll
+  for (int jj = 0; jj < kB; ++jj) {
+    x.kJ[jj] = k[b + jj];
+    x.qJ[jj] = q[b + jj];
+  }
+  if constexpr (FIXED) {
+    x.d = kFixedDecay;
+    x.p = kFixedProcess;
+    x.r = kFixedObservation;
+#pragma unroll
+    for (int jj = 0; jj < kB; ++jj) x.dJ[jj] = kFixedDecay;
+  } else {
+    x.d = d[e];
+    x.p = p[t];
+    x.r = r[t];
+#pragma unroll
+    for (int jj = 0; jj < kB; ++jj) x.dJ[jj] = d[b + jj];
+  }
+}
+
+// Belief block of thread (w, l) and one token's intermediates.
+struct Bel4 {
+  float P[kB];  // P~_lj, j in J_w
+  float M[kB];  // M_il, i in J_w
+  float pd;
+};
+struct Pred4 {
+  float u, s, beta, e;
+};
+
+// Partial sums of the predict step over the wave's block: (P~ wk)_l and (M^T wk)_l.
+__device__ __forceinline__ v2f predict_partials(const Bel4& b, const Tok4& x) {
+  float az[4] = {0.f, 0.f, 0.f, 0.f}, ae[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int jj = 0; jj < kB; ++jj) {
+    const float wk = x.dJ[jj] * x.kJ[jj];
+    az[jj & 3] = fmaf(b.P[jj], wk, az[jj & 3]);
+    ae[jj & 3] = fmaf(b.M[jj], wk, ae[jj & 3]);
+  }
+  return v2f{(az[0] + az[1]) + (az[2] + az[3]), (ae[0] + ae[1]) + (ae[2] + ae[3])};
+}
+
+// The token's u_l, s, beta, e_l from the four waves' partials (xch: [kW][64]).
+template <class V>
+__device__ __forceinline__ Pred4 predict_finish(const Bel4& b, const Tok4& x, const V* xch, int l, float floor) {
+  const V p0 = xch[l], p1 = xch[kWave + l], p2 = xch[2 * kWave + l], p3 = xch[3 * kWave + l];
+  const float wk = x.d * x.k;
+  const float z = fmaf(b.pd, wk, sum4(p0[0], p1[0], p2[0], p3[0]));
+  Pred4 o;
+  o.u = fmaf(x.d, z, x.p * x.k);
+  o.s = wave_sum(x.k * o.u) + x.r;
+  o.beta = 1.0f / fmaxf(o.s, floor);
+  o.e = x.v - sum4(p0[1], p1[1], p2[1], p3[1]);
+  return o;
+}
+
+// Update of the block: M_il <- d_i M_il + u_i beta e_l, P~_lj <- P~_lj d_l d_j
+// - beta u_l u_j, pd <- pd d_l^2 + p.  On the sequence's first token the
+// entries left of the diagonal are first replaced by their mirrors P0_jl
+// (c0col: column l of the initial covariance).
+__device__ __forceinline__ void update4(Bel4& b, const Tok4& x, const Pred4& o, int l, int j0,
+                                        const float* c0col) {
+  if (c0col) {
+#pragma unroll
+    for (int jj = 0; jj < kB; ++jj)
+      if (j0 + jj < l) b.P[jj] = c0col[(j0 + jj) * D];
+  }
+  const float be = o.beta * o.e;
+#pragma unroll
+  for (int jj = 0; jj < kB; ++jj) {
+    const float uj = lane_value(o.u, j0 + jj);
+    b.M[jj] = fmaf(uj, be, x.dJ[jj] * b.M[jj]);
+    b.P[jj] = fmaf(-o.beta, mul_rn(o.u, uj), b.P[jj] * mul_rn(x.d, x.dJ[jj]));
+  }
+  b.pd = fmaf(b.pd, mul_rn(x.d, x.d), x.p);
+}
+
+template <bool FIXED>
+__global__ __launch_bounds__(kThreads) void forward4_kernel(FwdArgs a) {
+  // Exchange of the token's partial sums {P~ wk, M^T wk, M_prev^T q_prev}:
+  // double-buffered, so one barrier per token suffices.
+  __shared__ v4f xz[2][kW * kWave];
+  const int w = wave_index(), l = static_cast<int>(threadIdx.x) & (kWave - 1), j0 = kB * w;
+  const int64_t n = blockIdx.x;
+  const int64_t T = a.t, nbp = a.nb + 1;
+  const float* c0 = a.c0 + n * D * D;
+  const float* m0 = a.m0 + n * D * D;
+  float* bm = a.bm + n * nbp * D * D;
+  float* bc = a.bc + n * nbp * D * D;
+  const float* kp = a.k + n * T * D;
+  const float* vp = a.v + n * T * D;
+  const float* qp = a.q + n * T * D;
+  const float* dp = FIXED ? nullptr : a.d + n * T * D;
+  const float* pp = FIXED ? nullptr : a.p + n * T;
+  const float* rp = FIXED ? nullptr : a.r + n * T;
+  float* yp = a.y + n * T * D;
+
+  Bel4 b;
+  b.pd = 0.f;
+#pragma unroll
+  for (int c = 0; c < kB / 4; ++c) {
+    const v4f r4 = *reinterpret_cast<const v4f*>(&c0[l * D + j0 + 4 * c]);  // row l as given
+#pragma unroll
+    for (int h = 0; h < 4; ++h) b.P[4 * c + h] = r4[h];
+  }
+#pragma unroll
+  for (int ii = 0; ii < kB; ++ii) b.M[ii] = m0[(j0 + ii) * D + l];
+  // A belief record: mean column l (rows J_w) and covariance row l (columns
+  // J_w, the diagonal folded in); record 0 is the initial belief as given.
+  auto store = [&](float* mdst, float* cdst) __attribute__((always_inline)) {
+#pragma unroll
+    for (int ii = 0; ii < kB; ++ii) mdst[(j0 + ii) * D + l] = b.M[ii];
+#pragma unroll
+    for (int c = 0; c < kB / 4; ++c) {
+      v4f r4;
+#pragma unroll
+      for (int h = 0; h < 4; ++h) r4[h] = (j0 + 4 * c + h == l) ? b.P[4 * c + h] + b.pd : b.P[4 * c + h];
+      *reinterpret_cast<v4f*>(&cdst[l * D + j0 + 4 * c]) = r4;
+    }
+  };
+  store(bm, bc);
+
+  Tok4 nxt;
+  if (T > 0) load_tok4<FIXED, false>(nxt, kp, vp, qp, dp, pp, rp, nullptr, 0, l, j0);
+  float ypart = 0.f;  // the wave's partial of y of the previous token
+  int64_t c = 1;
+  for (int64_t t = 0; t < T; ++t) {
+    if (t > 0 && t % a.chunk == 0) {
+      store(bm + c * D * D, bc + c * D * D);
+      ++c;
+    }
+    const Tok4 x = nxt;
+    if (t + 1 < T) load_tok4<FIXED, false>(nxt, kp, vp, qp, dp, pp, rp, nullptr, static_cast<int>(t + 1), l, j0);
+    v4f* xs = xz[t & 1];
+    const v2f pz = predict_partials(b, x);
+    xs[w * kWave + l] = v4f{pz[0], pz[1], ypart, 0.f};
+    __syncthreads();
+    if (w == 0 && t > 0)
+      yp[static_cast<int>(t - 1) * D + l] = sum4(xs[l][2], xs[kWave + l][2], xs[2 * kWave + l][2], xs[3 * kWave + l][2]);
+    const Pred4 o = predict_finish(b, x, xs, l, a.floor);
+    update4(b, x, o, l, j0, t == 0 ? c0 + l : nullptr);
+    float ay[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int ii = 0; ii < kB; ++ii) ay[ii & 3] = fmaf(b.M[ii], x.qJ[ii], ay[ii & 3]);
+    ypart = (ay[0] + ay[1]) + (ay[2] + ay[3]);
+  }
+  if (T > 0) {
+    v4f* xs = xz[T & 1];
+    xs[w * kWave + l] = v4f{0.f, 0.f, ypart, 0.f};
+    __syncthreads();
+    if (w == 0)
+      yp[static_cast<int>(T - 1) * D + l] = sum4(xs[l][2], xs[kWave + l][2], xs[2 * kWave + l][2], xs[3 * kWave + l][2]);
+  }
+  store(a.mT + n * D * D, a.cT + n * D * D);
+  if (T > 0) store(bm + a.nb * D * D, bc + a.nb * D * D);
+}
+
+// Backward at a checkpoint chunk of kHist tokens: each chunk is replayed
+// once from its record with the belief blocks and intermediates of every
+// token kept in registers, then reversed token by token (the reverse of
+// persistent_bayes_chunked.cu:303-343 with the conventions of the one-wave
+// kernel above: symmetrized gu k^T adjoint, first-token mirror correction).
+// Three barriers per token: the replay's partial sums, then the reverse's
+// two rounds of partial sums.
+template <bool FIXED, bool DYN>
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1))) void backward4_kernel(BwdArgs a) {
+  __shared__ v2f xz[2][kW * kWave];
+  __shared__ v2f xb[kW * kWave], xc[kW * kWave];
+  __shared__ float ra[D], rkm[D], rdm[D];
+  __shared__ float tiles[kW * kWave * kB];
+  const int w = wave_index(), l = static_cast<int>(threadIdx.x) & (kWave - 1), j0 = kB * w;
+  float* tile = tiles + w * kWave * kB;
+  const int64_t n = blockIdx.x;
+  const int64_t T = a.t, nbp = a.nb + 1;
+  const float* bm = a.bm + n * nbp * D * D;
+  const float* bc = a.bc + n * nbp * D * D;
+  const float* c0 = a.c0 + n * D * D;
+  const float* kp = a.k + n * T * D;
+  const float* vp = a.v + n * T * D;
+  const float* qp = a.q + n * T * D;
+  const float* gyp = a.gy + n * T * D;
+  const float* dp = FIXED ? nullptr : a.d + n * T * D;
+  const float* pp = FIXED ? nullptr : a.p + n * T;
+  const float* rp = FIXED ? nullptr : a.r + n * T;
+  float* gkp = a.gk + n * T * D;
+  float* gqp = a.gq + n * T * D;
+  float* gvp = a.gv + n * T * D;
+  float* gdp = a.gd ? a.gd + n * T * D : nullptr;
+  float* gpp = a.gp ? a.gp + n * T : nullptr;
+  float* grp = a.gr ? a.gr + n * T : nullptr;
+
+  // Carried adjoints: S = sym(dL/dP) (row l, columns J_w; Sd the diagonal
+  // part that pairs with pd), gM = dL/dM (column l, rows J_w).
+  float S[kB], gM[kB], Sd = 0.f;
+  if (a.gmf) {
+    const float* gmf = a.gmf + n * D * D;
+#pragma unroll
+    for (int ii = 0; ii < kB; ++ii) gM[ii] = gmf[(j0 + ii) * D + l];
+  } else {
+#pragma unroll
+    for (int ii = 0; ii < kB; ++ii) gM[ii] = 0.f;
+  }
+  if (a.gcf) {
+    const float* gcf = a.gcf + n * D * D;
+#pragma unroll
+    for (int jj = 0; jj < kB; ++jj) {
+      const int j = j0 + jj;
+      S[jj] = 0.5f * (gcf[l * D + j] + gcf[j * D + l]);
+    }
+    Sd = 0.5f * (gcf[l * D + l] + gcf[l * D + l]);
+  } else {
+#pragma unroll
+    for (int jj = 0; jj < kB; ++jj) S[jj] = 0.f;
+  }
+
+  int par = 0;
+  for (int64_t c = a.nb - 1; c >= 0; --c) {
+    const int64_t t0 = c * kHist;
+    const int len = static_cast<int>((T - t0) < kHist ? (T - t0) : kHist);
+    Bel4 hb[kHist];
+    Pred4 ho[kHist];
+    {
+      Bel4 b;
+      const float* cm = bm + c * D * D;
+      const float* cc = bc + c * D * D;
+#pragma unroll
+      for (int q4 = 0; q4 < kB / 4; ++q4) {
+        const v4f r4 = *reinterpret_cast<const v4f*>(&cc[l * D + j0 + 4 * q4]);
+#pragma unroll
+        for (int h = 0; h < 4; ++h) b.P[4 * q4 + h] = r4[h];
+      }
+#pragma unroll
+      for (int ii = 0; ii < kB; ++ii) b.M[ii] = cm[(j0 + ii) * D + l];
+      b.pd = 0.f;
+#pragma unroll
+      for (int tt = 0; tt < kHist; ++tt) {
+        if (tt < len) {
+          Tok4 x;
+          load_tok4<FIXED, false>(x, kp, vp, qp, dp, pp, rp, nullptr, static_cast<int>(t0 + tt), l, j0);
+          hb[tt] = b;
+          v2f* xs = xz[par];
+          par ^= 1;
+          xs[w * kWave + l] = predict_partials(b, x);
+          __syncthreads();
+          ho[tt] = predict_finish(b, x, xs, l, a.floor);
+          if (tt + 1 < len) update4(b, x, ho[tt], l, j0, (c == 0 && tt == 0) ? c0 + l : nullptr);
+        }
+      }
+    }
+#pragma unroll
+    for (int tt = kHist - 1; tt >= 0; --tt) {
+      if (tt < len) {
+        const Bel4& hbt = hb[tt];
+        const Pred4& o = ho[tt];
+        const int t = static_cast<int>(t0 + tt);
+        Tok4 x;
+        load_tok4<FIXED, true>(x, kp, vp, qp, dp, pp, rp, gyp, t, l, j0);
+        float uJ[kB];
+#pragma unroll
+        for (int jj = 0; jj < kB; ++jj) uJ[jj] = lane_value(o.u, j0 + jj);
+        // Phase 1: gM += q gy^T; partials of gM^T u and S u; row sums of
+        // M_new gy (dL/dq) and gM e.
+        float am[4] = {0.f, 0.f, 0.f, 0.f}, aw[4] = {0.f, 0.f, 0.f, 0.f};
+        float vq[kB], va[kB];
+        const float be = o.beta * o.e;
+#pragma unroll
+        for (int ii = 0; ii < kB; ++ii) {
+          gM[ii] = fmaf(x.qJ[ii], x.gy, gM[ii]);
+          am[ii & 3] = fmaf(gM[ii], uJ[ii], am[ii & 3]);
+          aw[ii & 3] = fmaf(S[ii], uJ[ii], aw[ii & 3]);
+          vq[ii] = fmaf(uJ[ii], be, x.dJ[ii] * hbt.M[ii]) * x.gy;
+          va[ii] = gM[ii] * o.e;
+        }
+        {
+          const float rq = wave_rowsum(tile, l, vq);
+          if ((l & 3) == 0) gqp[t * D + j0 + (l >> 2)] = rq;
+          const float r_a = wave_rowsum(tile, l, va);
+          if ((l & 3) == 0) ra[j0 + (l >> 2)] = r_a;
+        }
+        xb[w * kWave + l] = v2f{(am[0] + am[1]) + (am[2] + am[3]), (aw[0] + aw[1]) + (aw[2] + aw[3])};
+        __syncthreads();
+        // Phase 2: ge, gs, gu; row sums of (dM) ge and (gM - k ge^T) M;
+        // partials of P' gu and of the decay's covariance term.
+        const float gmu = sum4(xb[l][0], xb[kWave + l][0], xb[2 * kWave + l][0], xb[3 * kWave + l][0]);
+        const float wl = sum4(xb[l][1], xb[kWave + l][1], xb[2 * kWave + l][1], xb[3 * kWave + l][1]);
+        const float a_l = ra[l];
+        const float ge = o.beta * gmu;
+        const float z = wave_sum(fmaf(o.e, gmu, -(o.u * wl)));
+        const float gs = (o.s > a.floor) ? -z * o.beta * o.beta : 0.f;
+        const float gu = fmaf(o.beta, fmaf(-2.f, wl, a_l), gs * x.k);
+        float vk[kB], vd[kB];
+#pragma unroll
+        for (int ii = 0; ii < kB; ++ii) {
+          vk[ii] = (x.dJ[ii] * hbt.M[ii]) * ge;
+          const float g = fmaf(-x.kJ[ii], ge, gM[ii]);
+          vd[ii] = g * hbt.M[ii];
+          gM[ii] = g * x.dJ[ii];
+        }
+        {
+          const float r_k = wave_rowsum(tile, l, vk);
+          if ((l & 3) == 0) rkm[j0 + (l >> 2)] = r_k;
+          if constexpr (DYN) {
+            const float r_d = wave_rowsum(tile, l, vd);
+            if ((l & 3) == 0) rdm[j0 + (l >> 2)] = r_d;
+          }
+        }
+        float ap[4] = {0.f, 0.f, 0.f, 0.f}, gdc = 0.f;
+        const bool first = t == 0;
+#pragma unroll
+        for (int jj = 0; jj < kB; ++jj) {
+          const int j = j0 + jj;
+          const float guj = lane_value(gu, j);
+          const float dd = mul_rn(x.d, x.dJ[jj]);
+          ap[jj & 3] = fmaf(hbt.P[jj] * dd, guj, ap[jj & 3]);
+          if (first && j < l) ap[jj & 3] = fmaf((c0[j * D + l] - hbt.P[jj]) * dd, guj, ap[jj & 3]);
+          const float h = add_rn(S[jj], 0.5f * add_rn(mul_rn(gu, x.kJ[jj]), mul_rn(guj, x.k)));
+          if constexpr (DYN) gdc = fmaf(h * hbt.P[jj], x.dJ[jj], gdc);
+          S[jj] = h * dd;
+        }
+        const float hd = add_rn(Sd, 0.5f * add_rn(mul_rn(gu, x.k), mul_rn(gu, x.k)));
+        Sd = hd * mul_rn(x.d, x.d);
+        xc[w * kWave + l] = v2f{(ap[0] + ap[1]) + (ap[2] + ap[3]), gdc};
+        __syncthreads();
+        // Phase 3: dL/dk, dL/dd, dL/dp, dL/dr of the token.
+        const float pgu = sum4(xc[l][0], xc[kWave + l][0], xc[2 * kWave + l][0], xc[3 * kWave + l][0]);
+        const float gk = -rkm[l] + fmaf(gs, o.u, fmaf(fmaf(hbt.pd, mul_rn(x.d, x.d), x.p), gu, pgu));
+        if (w == 0) {
+          gkp[t * D + l] = gk;
+          gvp[t * D + l] = ge;
+        }
+        if constexpr (DYN) {
+          float gdl = sum4(xc[l][1], xc[kWave + l][1], xc[2 * kWave + l][1], xc[3 * kWave + l][1]);
+          gdl = fmaf(hd * hbt.pd, x.d, gdl);
+          const float gd = fmaf(2.f, gdl, rdm[l]);
+          const float gp = wave_sum(hd);
+          if (w == 0) {
+            if (gdp) gdp[t * D + l] = gd;
+            if (l == 0) {
+              if (gpp) gpp[t] = gp;
+              if (grp) grp[t] = gs;
+            }
+          }
+        } else if (w == 0) {
+          if (gdp) gdp[t * D + l] = 0.f;
+          if (l == 0) {
+            if (gpp) gpp[t] = 0.f;
+            if (grp) grp[t] = 0.f;
+          }
+        }
+      }
+    }
+  }
+  if (a.gm0) {
+#pragma unroll
+    for (int ii = 0; ii < kB; ++ii) a.gm0[n * D * D + (j0 + ii) * D + l] = gM[ii];
+  }
+  if (a.gc0) {
+#pragma unroll
+    for (int jj = 0; jj < kB; ++jj) a.gc0[n * D * D + (j0 + jj) * D + l] = S[jj];
+  }
+}
+
 }  // namespace d64
 
 hipError_t launch_forward_d64(bool fixed, const FwdArgs& a, hipStream_t stream) {
   if (a.n == 0) return hipSuccess;
-  const dim3 grid(static_cast<unsigned>(a.n)), block(kWave);
-  if (fixed) hipLaunchKernelGGL((d64::forward_kernel<true>), grid, block, 0, stream, a);
-  else hipLaunchKernelGGL((d64::forward_kernel<false>), grid, block, 0, stream, a);
+  const dim3 grid(static_cast<unsigned>(a.n)), block(d64::kThreads);
+  if (fixed) hipLaunchKernelGGL((d64::forward4_kernel<true>), grid, block, 0, stream, a);
+  else hipLaunchKernelGGL((d64::forward4_kernel<false>), grid, block, 0, stream, a);
   return hipGetLastError();
 }
 
 hipError_t launch_backward_d64(bool fixed, bool dyn, const BwdArgs& a, hipStream_t stream) {
   if (a.n == 0) return hipSuccess;
+  if (a.chunk == d64::kHist) {
+    const dim3 grid(static_cast<unsigned>(a.n)), block(d64::kThreads);
+    if (fixed) hipLaunchKernelGGL((d64::backward4_kernel<true, false>), grid, block, 0, stream, a);
+    else if (dyn) hipLaunchKernelGGL((d64::backward4_kernel<false, true>), grid, block, 0, stream, a);
+    else hipLaunchKernelGGL((d64::backward4_kernel<false, false>), grid, block, 0, stream, a);
+    return hipGetLastError();
+  }
   const dim3 grid(static_cast<unsigned>(a.n)), block(kWave);
   if (fixed) hipLaunchKernelGGL((d64::backward_kernel<true, false>), grid, block, 0, stream, a);
   else if (dyn) hipLaunchKernelGGL((d64::backward_kernel<false, true>), grid, block, 0, stream, a);
