@@ -596,105 +596,218 @@ __global__ __launch_bounds__(kWave) void backward_kernel(BwdArgs a) {
   }
 }
 
-// ------------------------------------------- four waves per sequence
-// One workgroup of four waves per sequence: thread (w, l) owns the 16
-// columns J_w = [16 w, 16 w + 16) of covariance row l (P~_lj, j in J_w) and
-// the 16 rows J_w of mean column l (M_il, i in J_w); the diagonal part pd_l
-// and every per-lane scalar (u_l, s, e_l, ...) are carried by all four
-// waves with identical bits.  Sums over j of a row (u = P'k, e = M^T wk,
-// y = M^T q, ...) are four partial sums exchanged through LDS (one barrier),
-// added in the same order by every wave; sums over the lanes of a wave's 16
-// rows go through a wave-private LDS transpose.  The token's k, d, q entries
-// of J_w are wave-uniform (scalar loads); u_j and gu_j of J_w are read from
-// their lanes (v_readlane).  At B32 x H8 (256 sequences) every SIMD holds a
-// wave, and the backward keeps a whole 8-token chunk's history in registers
-// (36 floats per token and thread), so each token is replayed once.
+// ------------------------------------------------ wave groups per sequence
+// One workgroup of W waves per sequence (W = kGroupWaves): thread (w, l)
+// owns the KB = 64 / W columns J_w = [KB w, KB w + KB) of covariance row l
+// (P~_lj, j in J_w) and the rows J_w of mean column l (M_il, i in J_w); the
+// diagonal part pd_l and every per-lane scalar (u_l, s, e_l, ...) are
+// carried by all W waves with identical bits.  Sums over j of a row
+// (P~ wk, M^T wk, M^T q, ...) are W partial sums exchanged through LDS (one
+// barrier) and added in the same order by every wave; sums over the lanes of
+// a wave's KB rows go through a wave-private LDS transpose.  u_j and gu_j of
+// J_w are read from their lanes (v_readlane).
+//
+// Inputs are staged per block of kBlk tokens: the workgroup loads the
+// block's k, v, q (gy, d) rows and p, r with 16-byte loads a block ahead
+// into registers and writes them to a double-buffered LDS stage, from which
+// each lane reads its own entries and the wave's KB-wide slices (broadcast
+// reads).  The backward checkpoints every kBlk tokens and keeps a whole
+// chunk's replayed beliefs and intermediates in registers, so each token is
+// replayed once.
+#ifndef BSSM_D64_WAVES
+#define BSSM_D64_WAVES 4
+#endif
+constexpr int kGroupWaves = BSSM_D64_WAVES;
+static_assert(kGroupWaves == 4 || kGroupWaves == 8, "wave groups of 4 or 8 waves");
+constexpr int kBlk = 8;  // tokens per staged block and per backward chunk
+
 typedef float v2f __attribute__((ext_vector_type(2)));
-constexpr int kW = 4;           // waves per sequence
-constexpr int kB = D / kW;      // columns (rows) of a wave's block
-constexpr int kThreads = kW * kWave;
-constexpr int kHist = 8;        // backward chunk (tokens of history in registers)
 
 __device__ __forceinline__ int wave_index() { return __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6)); }
 __device__ __forceinline__ float lane_value(float x, int src) {
   return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, x), src));
 }
-// ((x0 + x1) + (x2 + x3)) of the four waves' partials: the same bits in every wave.
-__device__ __forceinline__ float sum4(float x0, float x1, float x2, float x3) { return (x0 + x1) + (x2 + x3); }
 
-// Sum over the wave's 64 lanes of each of the lane's 16 values x[ii]: the
-// total of row ii lands in lanes 4 ii .. 4 ii + 3.  `tile` is wave-private
-// (64 rows of 16 floats, the 16-byte pieces of row r rotated by (r >> 2) & 3
-// so that both the row writes and the column reads are free of bank
-// conflicts); a wave's LDS operations complete in issue order, so no barrier
-// separates the writes from the reads.
-__device__ __forceinline__ float wave_rowsum(float* tile, int l, const float (&x)[kB]) {
-  float* row = tile + l * kB;
-  const int rot = (l >> 2) & 3;
+// x + (x of the lane 16 (32) apart), via the gfx950 row swaps: both
+// registers of the swap are added, the same pair in every lane.  Written as
+// inline assembly because this toolchain's optimizer folds the second result
+// of __builtin_amdgcn_permlane{16,32}_swap into the first; the s_nop gives
+// the swap the two wait states it needs after the VALU writes of its operands.
+__device__ __forceinline__ float swap_add16(float x) {
+  float a = x, b = x;
+  asm volatile("s_nop 1\n\tv_permlane16_swap_b32 %0, %1" : "+v"(a), "+v"(b));
+  return a + b;
+}
+__device__ __forceinline__ float swap_add32(float x) {
+  float a = x, b = x;
+  asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1" : "+v"(a), "+v"(b));
+  return a + b;
+}
+// Wave all-reduce with the same bits in every lane (no LDS traffic).
+__device__ __forceinline__ float wave_total(float x) {
+  x = add_rn(x, dpp<kXor1>(x));
+  x = add_rn(x, dpp<kXor2>(x));
+  x = add_rn(x, dpp<kHalfMirror>(x));
+  x = add_rn(x, dpp<0x140>(x));  // row_mirror
+  return swap_add32(swap_add16(x));
+}
+
+// Pairwise sum of the W waves' partials, the same order in every wave.
+template <int W>
+__device__ __forceinline__ float tree(const float (&x)[W]) {
+  if constexpr (W == 4) return (x[0] + x[1]) + (x[2] + x[3]);
+  else return ((x[0] + x[1]) + (x[2] + x[3])) + ((x[4] + x[5]) + (x[6] + x[7]));
+}
+
+// Sum over the wave's 64 lanes of each of the lane's KB values x[ii]: the
+// total of row ii lands in the G = 64 / KB lanes G ii .. G ii + G - 1.
+// `tile` is wave-private, 64 rows of KB floats with the 16-byte pieces of row
+// r rotated by (r / G) % (KB / 4), which keeps both the row writes and the
+// column reads free of bank conflicts; a wave's LDS operations complete in
+// issue order, so no barrier separates the writes from the reads.
+template <int KB>
+__device__ __forceinline__ float lane_rowsum(float* tile, int l, const float (&x)[KB]) {
+  constexpr int G = kWave / KB, NP = KB / 4;
+  float* row = tile + l * KB;
+  const int rot = (l / G) % NP;
 #pragma unroll
-  for (int c = 0; c < kB / 4; ++c)
+  for (int c = 0; c < NP; ++c)
     *reinterpret_cast<v4f*>(&row[4 * (c ^ rot)]) = v4f{x[4 * c], x[4 * c + 1], x[4 * c + 2], x[4 * c + 3]};
   __builtin_amdgcn_wave_barrier();
-  const int ii = l >> 2, qd = l & 3;
+  const int ii = l / G, g = l % G;
   float acc[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-  for (int m = 0; m < kWave / 4; ++m)
-    acc[m & 3] += tile[(4 * m + qd) * kB + 4 * ((ii >> 2) ^ (m & 3)) + (ii & 3)];
+  for (int m = 0; m < KB; ++m) acc[m & 3] += tile[(G * m + g) * KB + 4 * ((ii >> 2) ^ (m % NP)) + (ii & 3)];
   __builtin_amdgcn_wave_barrier();
   float t = (acc[0] + acc[1]) + (acc[2] + acc[3]);
   t = add_rn(t, dpp<kXor1>(t));
-  return add_rn(t, dpp<kXor2>(t));
+  t = add_rn(t, dpp<kXor2>(t));
+  if constexpr (G == 8) t = add_rn(t, dpp<kHalfMirror>(t));
+  return t;
 }
 
-// Token inputs of thread (w, l): the lane's own entries and the wave's block.
-struct Tok4 {
-  float k, d, v, q, gy, p, r;
-  float kJ[kB], dJ[kB], qJ[kB];
+// LDS stage of one block (floats): rows of k, v, q, gy, d (kBlk x 64 each),
+// then p and r of the block's tokens.
+constexpr int kSK = 0, kSV = kBlk * D, kSQ = 2 * kBlk * D, kSG = 3 * kBlk * D, kSD = 4 * kBlk * D;
+constexpr int kSP = 5 * kBlk * D, kSR = kSP + kBlk, kStage = kSR + kBlk;
+constexpr int kRowVecs = kBlk * D / 4;  // 16-byte pieces of one array's block
+
+// The sequence's input streams.
+struct Streams {
+  const float *k, *v, *q, *gy, *d, *p, *r;
 };
 
-template <bool FIXED, bool GY>
-__device__ __forceinline__ void load_tok4(Tok4& x, const float* k, const float* v, const float* q, const float* d,
-                                          const float* p, const float* r, const float* gy, int t, int l, int j0) {
-  const int e = t * D + l, b = t * D + j0;
-  x.k = k[e];
-  x.v = v[e];
-  x.q = q[e];
-  x.gy = GY ? gy[e] : 0.f;
+// A block of staged inputs held in registers between its load and its LDS
+// write (loaded a block ahead).  Arrays k, v, q, then gy (backward), then d
+// (dynamic decay); piece i of the block is array i / kRowVecs.
+template <int NT, bool FIXED, bool GY>
+struct Prefetch {
+  static constexpr int kArrays = 3 + (GY ? 1 : 0) + (FIXED ? 0 : 1);
+  static constexpr int kVecs = kArrays * kRowVecs;
+  static constexpr int kReps = (kVecs + NT - 1) / NT;
+  v4f x[kReps];
+  float s;
+
+  __device__ __forceinline__ static int array_offset(int arr) {
+    return arr == 0 ? kSK : arr == 1 ? kSV : arr == 2 ? kSQ : (arr == 3 && GY) ? kSG : kSD;
+  }
+  __device__ __forceinline__ static const float* array_src(const Streams& sp, int arr) {
+    return arr == 0 ? sp.k : arr == 1 ? sp.v : arr == 2 ? sp.q : (arr == 3 && GY) ? sp.gy : sp.d;
+  }
+  // Loads of the block starting at token t0 (zeros past the end T).
+  __device__ __forceinline__ void fetch(const Streams& sp, int t0, int T, int tid) {
 #pragma unroll
-  for (int jj = 0; jj < kB; ++jj) {
-    x.kJ[jj] = k[b + jj];
-    x.qJ[jj] = q[b + jj];
+    for (int rep = 0; rep < kReps; ++rep) {
+      const int i = tid + rep * NT;
+      if (kVecs % NT == 0 || i < kVecs) {
+        const int arr = i / kRowVecs, o = (i % kRowVecs) * 4;
+        const int t = t0 + o / D;
+        x[rep] = t < T ? *reinterpret_cast<const v4f*>(array_src(sp, arr) + t0 * D + o) : v4f{0.f, 0.f, 0.f, 0.f};
+      }
+    }
+    if (!FIXED && tid < 2 * kBlk) {
+      const int t = t0 + tid % kBlk;
+      s = t < T ? (tid < kBlk ? sp.p[t] : sp.r[t]) : 0.f;
+    }
+  }
+  __device__ __forceinline__ void put(float* stage, int tid) const {
+#pragma unroll
+    for (int rep = 0; rep < kReps; ++rep) {
+      const int i = tid + rep * NT;
+      if (kVecs % NT == 0 || i < kVecs) {
+        const int arr = i / kRowVecs, o = (i % kRowVecs) * 4;
+        *reinterpret_cast<v4f*>(&stage[array_offset(arr) + o]) = x[rep];
+      }
+    }
+    if (!FIXED && tid < 2 * kBlk) stage[kSP + tid] = s;
+  }
+};
+
+// One token's inputs for thread (w, l): the lane's entries and the wave's
+// KB-wide slices.
+template <int KB>
+struct TokG {
+  float k, d, v, q, gy, p, r;
+  float kJ[KB], dJ[KB], qJ[KB];
+};
+
+template <int KB, bool FIXED, bool GY>
+__device__ __forceinline__ void read_tok(TokG<KB>& x, const float* st, int tt, int l, int j0) {
+  const int e = tt * D + l, b = tt * D + j0;
+  x.k = st[kSK + e];
+  x.v = st[kSV + e];
+  x.q = st[kSQ + e];
+  x.gy = GY ? st[kSG + e] : 0.f;
+#pragma unroll
+  for (int c = 0; c < KB / 4; ++c) {
+    const v4f kv = *reinterpret_cast<const v4f*>(&st[kSK + b + 4 * c]);
+    const v4f qv = *reinterpret_cast<const v4f*>(&st[kSQ + b + 4 * c]);
+#pragma unroll
+    for (int h = 0; h < 4; ++h) {
+      x.kJ[4 * c + h] = kv[h];
+      x.qJ[4 * c + h] = qv[h];
+    }
   }
   if constexpr (FIXED) {
     x.d = kFixedDecay;
     x.p = kFixedProcess;
     x.r = kFixedObservation;
 #pragma unroll
-    for (int jj = 0; jj < kB; ++jj) x.dJ[jj] = kFixedDecay;
+    for (int jj = 0; jj < KB; ++jj) x.dJ[jj] = kFixedDecay;
   } else {
-    x.d = d[e];
-    x.p = p[t];
-    x.r = r[t];
+    x.d = st[kSD + e];
+    x.p = st[kSP + tt];
+    x.r = st[kSR + tt];
 #pragma unroll
-    for (int jj = 0; jj < kB; ++jj) x.dJ[jj] = d[b + jj];
+    for (int c = 0; c < KB / 4; ++c) {
+      const v4f dv = *reinterpret_cast<const v4f*>(&st[kSD + b + 4 * c]);
+#pragma unroll
+      for (int h = 0; h < 4; ++h) x.dJ[4 * c + h] = dv[h];
+    }
   }
 }
 
-// Belief block of thread (w, l) and one token's intermediates.
-struct Bel4 {
-  float P[kB];  // P~_lj, j in J_w
-  float M[kB];  // M_il, i in J_w
+// Belief block of thread (w, l).
+template <int KB>
+struct BelG {
+  float P[KB];  // P~_lj, j in J_w
+  float M[KB];  // M_il, i in J_w
   float pd;
 };
-struct Pred4 {
-  float u, s, beta, e;
+
+// A token's intermediates: u_l, beta = 1 / max(s, floor) and e_l; `clamped`
+// records s <= floor (no gradient through s).
+struct PredG {
+  float u, beta, e;
+  bool clamped;
 };
 
-// Partial sums of the predict step over the wave's block: (P~ wk)_l and (M^T wk)_l.
-__device__ __forceinline__ v2f predict_partials(const Bel4& b, const Tok4& x) {
+// Partial sums of the predict step over the wave's block: (P~ wk)_l, (M^T wk)_l.
+template <int KB>
+__device__ __forceinline__ v2f predict_part(const BelG<KB>& b, const TokG<KB>& x) {
   float az[4] = {0.f, 0.f, 0.f, 0.f}, ae[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-  for (int jj = 0; jj < kB; ++jj) {
+  for (int jj = 0; jj < KB; ++jj) {
     const float wk = x.dJ[jj] * x.kJ[jj];
     az[jj & 3] = fmaf(b.P[jj], wk, az[jj & 3]);
     ae[jj & 3] = fmaf(b.M[jj], wk, ae[jj & 3]);
@@ -702,78 +815,81 @@ __device__ __forceinline__ v2f predict_partials(const Bel4& b, const Tok4& x) {
   return v2f{(az[0] + az[1]) + (az[2] + az[3]), (ae[0] + ae[1]) + (ae[2] + ae[3])};
 }
 
-// The token's u_l, s, beta, e_l from the four waves' partials (xch: [kW][64]).
-template <class V>
-__device__ __forceinline__ Pred4 predict_finish(const Bel4& b, const Tok4& x, const V* xch, int l, float floor) {
-  const V p0 = xch[l], p1 = xch[kWave + l], p2 = xch[2 * kWave + l], p3 = xch[3 * kWave + l];
-  const float wk = x.d * x.k;
-  const float z = fmaf(b.pd, wk, sum4(p0[0], p1[0], p2[0], p3[0]));
-  Pred4 o;
+// u_l, beta, e_l from the W waves' partial sums zs (of P~ wk) and es (of M^T wk).
+template <int W, int KB>
+__device__ __forceinline__ PredG predict_done(const BelG<KB>& b, const TokG<KB>& x, const float (&zs)[W],
+                                              const float (&es)[W], float floor) {
+  const float z = fmaf(b.pd, x.d * x.k, tree<W>(zs));
+  PredG o;
   o.u = fmaf(x.d, z, x.p * x.k);
-  o.s = wave_sum(x.k * o.u) + x.r;
-  o.beta = 1.0f / fmaxf(o.s, floor);
-  o.e = x.v - sum4(p0[1], p1[1], p2[1], p3[1]);
+  const float s = wave_total(x.k * o.u) + x.r;
+  o.clamped = !(s > floor);
+  o.beta = 1.0f / fmaxf(s, floor);
+  o.e = x.v - tree<W>(es);
   return o;
 }
 
 // Update of the block: M_il <- d_i M_il + u_i beta e_l, P~_lj <- P~_lj d_l d_j
-// - beta u_l u_j, pd <- pd d_l^2 + p.  On the sequence's first token the
-// entries left of the diagonal are first replaced by their mirrors P0_jl
-// (c0col: column l of the initial covariance).
-__device__ __forceinline__ void update4(Bel4& b, const Tok4& x, const Pred4& o, int l, int j0,
-                                        const float* c0col) {
+// - beta u_l u_j, pd <- pd d_l^2 + p.  The rank-one terms are formed from
+// g = sqrt(beta) u as one fused multiply-add, fma(-g_l, g_j, P~_lj d_l d_j),
+// whose exact product commutes, so the covariance stays bitwise symmetric.
+// On the sequence's first token the entries left of the diagonal are first
+// replaced by their mirrors P0_jl (c0col: column l of the initial covariance).
+template <int KB>
+__device__ __forceinline__ void update_g(BelG<KB>& b, const TokG<KB>& x, const PredG& o, int l, int j0,
+                                         const float* c0col) {
   if (c0col) {
 #pragma unroll
-    for (int jj = 0; jj < kB; ++jj)
+    for (int jj = 0; jj < KB; ++jj)
       if (j0 + jj < l) b.P[jj] = c0col[(j0 + jj) * D];
   }
-  const float be = o.beta * o.e;
+  const float rb = __builtin_amdgcn_sqrtf(o.beta);
+  const float gl = rb * o.u, ge = rb * o.e;
 #pragma unroll
-  for (int jj = 0; jj < kB; ++jj) {
-    const float uj = lane_value(o.u, j0 + jj);
-    b.M[jj] = fmaf(uj, be, x.dJ[jj] * b.M[jj]);
-    b.P[jj] = fmaf(-o.beta, mul_rn(o.u, uj), b.P[jj] * mul_rn(x.d, x.dJ[jj]));
+  for (int jj = 0; jj < KB; ++jj) {
+    const float gj = lane_value(gl, j0 + jj);
+    b.M[jj] = fmaf(gj, ge, x.dJ[jj] * b.M[jj]);
+    b.P[jj] = fmaf(-gl, gj, b.P[jj] * mul_rn(x.d, x.dJ[jj]));
   }
   b.pd = fmaf(b.pd, mul_rn(x.d, x.d), x.p);
 }
 
-template <bool FIXED>
-__global__ __launch_bounds__(kThreads) void forward4_kernel(FwdArgs a) {
-  // Exchange of the token's partial sums {P~ wk, M^T wk, M_prev^T q_prev}:
-  // double-buffered, so one barrier per token suffices.
-  __shared__ v4f xz[2][kW * kWave];
-  const int w = wave_index(), l = static_cast<int>(threadIdx.x) & (kWave - 1), j0 = kB * w;
+template <int W, bool FIXED>
+__global__ __launch_bounds__(W * kWave) void forward_group_kernel(FwdArgs a) {
+  constexpr int KB = D / W, NT = W * kWave;
+  // Exchange of {P~ wk, M^T wk, M^T q of the previous token} partials,
+  // double-buffered: one barrier per token.
+  __shared__ v4f xz[2][W * kWave];
+  __shared__ __attribute__((aligned(16))) float stage[2][kStage];
+  const int tid = static_cast<int>(threadIdx.x), w = wave_index(), l = tid & (kWave - 1), j0 = KB * w;
   const int64_t n = blockIdx.x;
-  const int64_t T = a.t, nbp = a.nb + 1;
+  const int T = static_cast<int>(a.t);
+  const int64_t nbp = a.nb + 1;
   const float* c0 = a.c0 + n * D * D;
   const float* m0 = a.m0 + n * D * D;
   float* bm = a.bm + n * nbp * D * D;
   float* bc = a.bc + n * nbp * D * D;
-  const float* kp = a.k + n * T * D;
-  const float* vp = a.v + n * T * D;
-  const float* qp = a.q + n * T * D;
-  const float* dp = FIXED ? nullptr : a.d + n * T * D;
-  const float* pp = FIXED ? nullptr : a.p + n * T;
-  const float* rp = FIXED ? nullptr : a.r + n * T;
+  const Streams sp{a.k + n * T * D, a.v + n * T * D, a.q + n * T * D, nullptr,
+                   FIXED ? nullptr : a.d + n * T * D, FIXED ? nullptr : a.p + n * T, FIXED ? nullptr : a.r + n * T};
   float* yp = a.y + n * T * D;
 
-  Bel4 b;
+  BelG<KB> b;
   b.pd = 0.f;
 #pragma unroll
-  for (int c = 0; c < kB / 4; ++c) {
+  for (int c = 0; c < KB / 4; ++c) {
     const v4f r4 = *reinterpret_cast<const v4f*>(&c0[l * D + j0 + 4 * c]);  // row l as given
 #pragma unroll
     for (int h = 0; h < 4; ++h) b.P[4 * c + h] = r4[h];
   }
 #pragma unroll
-  for (int ii = 0; ii < kB; ++ii) b.M[ii] = m0[(j0 + ii) * D + l];
-  // A belief record: mean column l (rows J_w) and covariance row l (columns
-  // J_w, the diagonal folded in); record 0 is the initial belief as given.
+  for (int ii = 0; ii < KB; ++ii) b.M[ii] = m0[(j0 + ii) * D + l];
+  // A belief record: mean column l (rows J_w), covariance row l (columns J_w,
+  // the diagonal folded in); record 0 is the initial belief as given.
   auto store = [&](float* mdst, float* cdst) __attribute__((always_inline)) {
 #pragma unroll
-    for (int ii = 0; ii < kB; ++ii) mdst[(j0 + ii) * D + l] = b.M[ii];
+    for (int ii = 0; ii < KB; ++ii) mdst[(j0 + ii) * D + l] = b.M[ii];
 #pragma unroll
-    for (int c = 0; c < kB / 4; ++c) {
+    for (int c = 0; c < KB / 4; ++c) {
       v4f r4;
 #pragma unroll
       for (int h = 0; h < 4; ++h) r4[h] = (j0 + 4 * c + h == l) ? b.P[4 * c + h] + b.pd : b.P[4 * c + h];
@@ -782,68 +898,85 @@ __global__ __launch_bounds__(kThreads) void forward4_kernel(FwdArgs a) {
   };
   store(bm, bc);
 
-  Tok4 nxt;
-  if (T > 0) load_tok4<FIXED, false>(nxt, kp, vp, qp, dp, pp, rp, nullptr, 0, l, j0);
+  Prefetch<NT, FIXED, false> pf;
+  if (T > 0) {
+    pf.fetch(sp, 0, T, tid);
+    pf.put(stage[0], tid);
+  }
+  __syncthreads();
+  if (T > kBlk) pf.fetch(sp, kBlk, T, tid);
   float ypart = 0.f;  // the wave's partial of y of the previous token
-  int64_t c = 1;
-  for (int64_t t = 0; t < T; ++t) {
-    if (t > 0 && t % a.chunk == 0) {
-      store(bm + c * D * D, bc + c * D * D);
-      ++c;
+  int64_t rec = 1, next_rec = a.chunk;
+  for (int t = 0; t < T; ++t) {
+    if (t == next_rec) {
+      store(bm + rec * D * D, bc + rec * D * D);
+      ++rec;
+      next_rec += a.chunk;
     }
-    const Tok4 x = nxt;
-    if (t + 1 < T) load_tok4<FIXED, false>(nxt, kp, vp, qp, dp, pp, rp, nullptr, static_cast<int>(t + 1), l, j0);
+    const int tt = t % kBlk, blk = t / kBlk;
+    TokG<KB> x;
+    read_tok<KB, FIXED, false>(x, stage[blk & 1], tt, l, j0);
     v4f* xs = xz[t & 1];
-    const v2f pz = predict_partials(b, x);
+    const v2f pz = predict_part(b, x);
     xs[w * kWave + l] = v4f{pz[0], pz[1], ypart, 0.f};
+    const bool block_end = tt == kBlk - 1 && t + 1 < T;
+    if (block_end) pf.put(stage[(blk + 1) & 1], tid);
     __syncthreads();
-    if (w == 0 && t > 0)
-      yp[static_cast<int>(t - 1) * D + l] = sum4(xs[l][2], xs[kWave + l][2], xs[2 * kWave + l][2], xs[3 * kWave + l][2]);
-    const Pred4 o = predict_finish(b, x, xs, l, a.floor);
-    update4(b, x, o, l, j0, t == 0 ? c0 + l : nullptr);
+    float zs[W], es[W], ys[W];
+#pragma unroll
+    for (int i = 0; i < W; ++i) {
+      const v4f v = xs[i * kWave + l];
+      zs[i] = v[0];
+      es[i] = v[1];
+      ys[i] = v[2];
+    }
+    if (block_end && t + 1 + kBlk < T) pf.fetch(sp, t + 1 + kBlk, T, tid);
+    if (w == 0 && t > 0) yp[(t - 1) * D + l] = tree<W>(ys);
+    const PredG o = predict_done<W>(b, x, zs, es, a.floor);
+    update_g(b, x, o, l, j0, t == 0 ? c0 + l : nullptr);
     float ay[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int ii = 0; ii < kB; ++ii) ay[ii & 3] = fmaf(b.M[ii], x.qJ[ii], ay[ii & 3]);
+    for (int ii = 0; ii < KB; ++ii) ay[ii & 3] = fmaf(b.M[ii], x.qJ[ii], ay[ii & 3]);
     ypart = (ay[0] + ay[1]) + (ay[2] + ay[3]);
   }
   if (T > 0) {
     v4f* xs = xz[T & 1];
     xs[w * kWave + l] = v4f{0.f, 0.f, ypart, 0.f};
     __syncthreads();
-    if (w == 0)
-      yp[static_cast<int>(T - 1) * D + l] = sum4(xs[l][2], xs[kWave + l][2], xs[2 * kWave + l][2], xs[3 * kWave + l][2]);
+    float ys[W];
+#pragma unroll
+    for (int i = 0; i < W; ++i) ys[i] = xs[i * kWave + l][2];
+    if (w == 0) yp[(T - 1) * D + l] = tree<W>(ys);
   }
   store(a.mT + n * D * D, a.cT + n * D * D);
   if (T > 0) store(bm + a.nb * D * D, bc + a.nb * D * D);
 }
 
-// Backward at a checkpoint chunk of kHist tokens: each chunk is replayed
-// once from its record with the belief blocks and intermediates of every
-// token kept in registers, then reversed token by token (the reverse of
-// persistent_bayes_chunked.cu:303-343 with the conventions of the one-wave
+// Backward at checkpoint interval kBlk: each chunk is replayed once from its
+// record with the belief blocks and intermediates of every token kept in
+// registers, then reversed token by token (the reverse of
+// persistent_bayes_chunked.cu:303-343 in the conventions of the one-wave
 // kernel above: symmetrized gu k^T adjoint, first-token mirror correction).
-// Three barriers per token: the replay's partial sums, then the reverse's
-// two rounds of partial sums.
-template <bool FIXED, bool DYN>
-__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1))) void backward4_kernel(BwdArgs a) {
-  __shared__ v2f xz[2][kW * kWave];
-  __shared__ v2f xb[kW * kWave], xc[kW * kWave];
+// Barriers per token: one in the replay, two in the reverse.
+template <int W, bool FIXED, bool DYN>
+__global__ __launch_bounds__(W * kWave) __attribute__((amdgpu_waves_per_eu(W / 4, W / 4)))
+void backward_group_kernel(BwdArgs a) {
+  constexpr int KB = D / W, NT = W * kWave, G = kWave / KB;
+  __shared__ v2f xz[2][W * kWave];
+  __shared__ v2f xb[W * kWave], xc[W * kWave];
   __shared__ float ra[D], rkm[D], rdm[D];
-  __shared__ float tiles[kW * kWave * kB];
-  const int w = wave_index(), l = static_cast<int>(threadIdx.x) & (kWave - 1), j0 = kB * w;
-  float* tile = tiles + w * kWave * kB;
+  __shared__ __attribute__((aligned(16))) float tiles[W * kWave * KB];
+  __shared__ __attribute__((aligned(16))) float stage[2][kStage];
+  const int tid = static_cast<int>(threadIdx.x), w = wave_index(), l = tid & (kWave - 1), j0 = KB * w;
+  float* tile = tiles + w * kWave * KB;
   const int64_t n = blockIdx.x;
-  const int64_t T = a.t, nbp = a.nb + 1;
+  const int T = static_cast<int>(a.t);
+  const int64_t nbp = a.nb + 1;
   const float* bm = a.bm + n * nbp * D * D;
   const float* bc = a.bc + n * nbp * D * D;
   const float* c0 = a.c0 + n * D * D;
-  const float* kp = a.k + n * T * D;
-  const float* vp = a.v + n * T * D;
-  const float* qp = a.q + n * T * D;
-  const float* gyp = a.gy + n * T * D;
-  const float* dp = FIXED ? nullptr : a.d + n * T * D;
-  const float* pp = FIXED ? nullptr : a.p + n * T;
-  const float* rp = FIXED ? nullptr : a.r + n * T;
+  const Streams sp{a.k + n * T * D, a.v + n * T * D, a.q + n * T * D, a.gy + n * T * D,
+                   FIXED ? nullptr : a.d + n * T * D, FIXED ? nullptr : a.p + n * T, FIXED ? nullptr : a.r + n * T};
   float* gkp = a.gk + n * T * D;
   float* gqp = a.gq + n * T * D;
   float* gvp = a.gv + n * T * D;
@@ -853,148 +986,185 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1))
 
   // Carried adjoints: S = sym(dL/dP) (row l, columns J_w; Sd the diagonal
   // part that pairs with pd), gM = dL/dM (column l, rows J_w).
-  float S[kB], gM[kB], Sd = 0.f;
+  float S[KB], gM[KB], Sd = 0.f;
   if (a.gmf) {
     const float* gmf = a.gmf + n * D * D;
 #pragma unroll
-    for (int ii = 0; ii < kB; ++ii) gM[ii] = gmf[(j0 + ii) * D + l];
+    for (int ii = 0; ii < KB; ++ii) gM[ii] = gmf[(j0 + ii) * D + l];
   } else {
 #pragma unroll
-    for (int ii = 0; ii < kB; ++ii) gM[ii] = 0.f;
+    for (int ii = 0; ii < KB; ++ii) gM[ii] = 0.f;
   }
   if (a.gcf) {
     const float* gcf = a.gcf + n * D * D;
 #pragma unroll
-    for (int jj = 0; jj < kB; ++jj) {
+    for (int jj = 0; jj < KB; ++jj) {
       const int j = j0 + jj;
       S[jj] = 0.5f * (gcf[l * D + j] + gcf[j * D + l]);
     }
     Sd = 0.5f * (gcf[l * D + l] + gcf[l * D + l]);
   } else {
 #pragma unroll
-    for (int jj = 0; jj < kB; ++jj) S[jj] = 0.f;
+    for (int jj = 0; jj < KB; ++jj) S[jj] = 0.f;
   }
 
+  const int nb = static_cast<int>(a.nb);
+  Prefetch<NT, FIXED, true> pf;
+  if (nb > 0) {
+    pf.fetch(sp, (nb - 1) * kBlk, T, tid);
+    pf.put(stage[(nb - 1) & 1], tid);
+  }
+  __syncthreads();
+  if (nb > 1) pf.fetch(sp, (nb - 2) * kBlk, T, tid);
   int par = 0;
-  for (int64_t c = a.nb - 1; c >= 0; --c) {
-    const int64_t t0 = c * kHist;
-    const int len = static_cast<int>((T - t0) < kHist ? (T - t0) : kHist);
-    Bel4 hb[kHist];
-    Pred4 ho[kHist];
+  for (int c = nb - 1; c >= 0; --c) {
+    const int t0 = c * kBlk;
+    const int len = (T - t0) < kBlk ? (T - t0) : kBlk;
+    const float* st = stage[c & 1];
+    BelG<KB> hb[kBlk];
+    PredG ho[kBlk];
     {
-      Bel4 b;
-      const float* cm = bm + c * D * D;
-      const float* cc = bc + c * D * D;
+      BelG<KB> b;
+      const float* cm = bm + static_cast<int64_t>(c) * D * D;
+      const float* cc = bc + static_cast<int64_t>(c) * D * D;
 #pragma unroll
-      for (int q4 = 0; q4 < kB / 4; ++q4) {
+      for (int q4 = 0; q4 < KB / 4; ++q4) {
         const v4f r4 = *reinterpret_cast<const v4f*>(&cc[l * D + j0 + 4 * q4]);
 #pragma unroll
         for (int h = 0; h < 4; ++h) b.P[4 * q4 + h] = r4[h];
       }
 #pragma unroll
-      for (int ii = 0; ii < kB; ++ii) b.M[ii] = cm[(j0 + ii) * D + l];
+      for (int ii = 0; ii < KB; ++ii) b.M[ii] = cm[(j0 + ii) * D + l];
       b.pd = 0.f;
 #pragma unroll
-      for (int tt = 0; tt < kHist; ++tt) {
+      for (int tt = 0; tt < kBlk; ++tt) {
         if (tt < len) {
-          Tok4 x;
-          load_tok4<FIXED, false>(x, kp, vp, qp, dp, pp, rp, nullptr, static_cast<int>(t0 + tt), l, j0);
+          TokG<KB> x;
+          read_tok<KB, FIXED, false>(x, st, tt, l, j0);
           hb[tt] = b;
           v2f* xs = xz[par];
           par ^= 1;
-          xs[w * kWave + l] = predict_partials(b, x);
+          xs[w * kWave + l] = predict_part(b, x);
           __syncthreads();
-          ho[tt] = predict_finish(b, x, xs, l, a.floor);
-          if (tt + 1 < len) update4(b, x, ho[tt], l, j0, (c == 0 && tt == 0) ? c0 + l : nullptr);
+          float zs[W], es[W];
+#pragma unroll
+          for (int i = 0; i < W; ++i) {
+            const v2f v = xs[i * kWave + l];
+            zs[i] = v[0];
+            es[i] = v[1];
+          }
+          ho[tt] = predict_done<W>(b, x, zs, es, a.floor);
+          if (tt + 1 < len) update_g(b, x, ho[tt], l, j0, (c == 0 && tt == 0) ? c0 + l : nullptr);
         }
       }
     }
 #pragma unroll
-    for (int tt = kHist - 1; tt >= 0; --tt) {
+    for (int tt = kBlk - 1; tt >= 0; --tt) {
       if (tt < len) {
-        const Bel4& hbt = hb[tt];
-        const Pred4& o = ho[tt];
-        const int t = static_cast<int>(t0 + tt);
-        Tok4 x;
-        load_tok4<FIXED, true>(x, kp, vp, qp, dp, pp, rp, gyp, t, l, j0);
-        float uJ[kB];
+        const BelG<KB>& hbt = hb[tt];
+        const PredG& o = ho[tt];
+        const int t = t0 + tt;
+        TokG<KB> x;
+        read_tok<KB, FIXED, true>(x, st, tt, l, j0);
+        float uJ[KB], dM[KB];
 #pragma unroll
-        for (int jj = 0; jj < kB; ++jj) uJ[jj] = lane_value(o.u, j0 + jj);
+        for (int jj = 0; jj < KB; ++jj) {
+          uJ[jj] = lane_value(o.u, j0 + jj);
+          dM[jj] = x.dJ[jj] * hbt.M[jj];
+        }
         // Phase 1: gM += q gy^T; partials of gM^T u and S u; row sums of
         // M_new gy (dL/dq) and gM e.
         float am[4] = {0.f, 0.f, 0.f, 0.f}, aw[4] = {0.f, 0.f, 0.f, 0.f};
-        float vq[kB], va[kB];
+        float vq[KB], va[KB];
         const float be = o.beta * o.e;
 #pragma unroll
-        for (int ii = 0; ii < kB; ++ii) {
+        for (int ii = 0; ii < KB; ++ii) {
           gM[ii] = fmaf(x.qJ[ii], x.gy, gM[ii]);
           am[ii & 3] = fmaf(gM[ii], uJ[ii], am[ii & 3]);
           aw[ii & 3] = fmaf(S[ii], uJ[ii], aw[ii & 3]);
-          vq[ii] = fmaf(uJ[ii], be, x.dJ[ii] * hbt.M[ii]) * x.gy;
+          vq[ii] = fmaf(uJ[ii], be, dM[ii]) * x.gy;
           va[ii] = gM[ii] * o.e;
         }
         {
-          const float rq = wave_rowsum(tile, l, vq);
-          if ((l & 3) == 0) gqp[t * D + j0 + (l >> 2)] = rq;
-          const float r_a = wave_rowsum(tile, l, va);
-          if ((l & 3) == 0) ra[j0 + (l >> 2)] = r_a;
+          const float rq = lane_rowsum<KB>(tile, l, vq);
+          if (l % G == 0) gqp[t * D + j0 + l / G] = rq;
+          const float r_a = lane_rowsum<KB>(tile, l, va);
+          if (l % G == 0) ra[j0 + l / G] = r_a;
         }
         xb[w * kWave + l] = v2f{(am[0] + am[1]) + (am[2] + am[3]), (aw[0] + aw[1]) + (aw[2] + aw[3])};
         __syncthreads();
-        // Phase 2: ge, gs, gu; row sums of (dM) ge and (gM - k ge^T) M;
-        // partials of P' gu and of the decay's covariance term.
-        const float gmu = sum4(xb[l][0], xb[kWave + l][0], xb[2 * kWave + l][0], xb[3 * kWave + l][0]);
-        const float wl = sum4(xb[l][1], xb[kWave + l][1], xb[2 * kWave + l][1], xb[3 * kWave + l][1]);
+        // Phase 2: ge, gs, gu; row sums of (d M) ge and (gM - k ge^T) M;
+        // partials of P' gu and of the decay's covariance term.  gu enters
+        // halved (hg = gu / 2, exact), which gives the symmetrized outer
+        // product sym(gu k^T) without a further rounding.
+        float gms[W], ws[W];
+#pragma unroll
+        for (int i = 0; i < W; ++i) {
+          const v2f v = xb[i * kWave + l];
+          gms[i] = v[0];
+          ws[i] = v[1];
+        }
+        const float gmu = tree<W>(gms), wl = tree<W>(ws);
         const float a_l = ra[l];
         const float ge = o.beta * gmu;
-        const float z = wave_sum(fmaf(o.e, gmu, -(o.u * wl)));
-        const float gs = (o.s > a.floor) ? -z * o.beta * o.beta : 0.f;
+        const float z = wave_total(fmaf(o.e, gmu, -(o.u * wl)));
+        const float gs = o.clamped ? 0.f : -z * o.beta * o.beta;
         const float gu = fmaf(o.beta, fmaf(-2.f, wl, a_l), gs * x.k);
-        float vk[kB], vd[kB];
+        const float hg = 0.5f * gu;
+        float vk[KB], vd[KB];
 #pragma unroll
-        for (int ii = 0; ii < kB; ++ii) {
-          vk[ii] = (x.dJ[ii] * hbt.M[ii]) * ge;
+        for (int ii = 0; ii < KB; ++ii) {
+          vk[ii] = dM[ii] * ge;
           const float g = fmaf(-x.kJ[ii], ge, gM[ii]);
           vd[ii] = g * hbt.M[ii];
           gM[ii] = g * x.dJ[ii];
         }
         {
-          const float r_k = wave_rowsum(tile, l, vk);
-          if ((l & 3) == 0) rkm[j0 + (l >> 2)] = r_k;
+          const float r_k = lane_rowsum<KB>(tile, l, vk);
+          if (l % G == 0) rkm[j0 + l / G] = r_k;
           if constexpr (DYN) {
-            const float r_d = wave_rowsum(tile, l, vd);
-            if ((l & 3) == 0) rdm[j0 + (l >> 2)] = r_d;
+            const float r_d = lane_rowsum<KB>(tile, l, vd);
+            if (l % G == 0) rdm[j0 + l / G] = r_d;
           }
         }
         float ap[4] = {0.f, 0.f, 0.f, 0.f}, gdc = 0.f;
         const bool first = t == 0;
 #pragma unroll
-        for (int jj = 0; jj < kB; ++jj) {
+        for (int jj = 0; jj < KB; ++jj) {
           const int j = j0 + jj;
-          const float guj = lane_value(gu, j);
+          const float hj = lane_value(hg, j);
           const float dd = mul_rn(x.d, x.dJ[jj]);
-          ap[jj & 3] = fmaf(hbt.P[jj] * dd, guj, ap[jj & 3]);
-          if (first && j < l) ap[jj & 3] = fmaf((c0[j * D + l] - hbt.P[jj]) * dd, guj, ap[jj & 3]);
-          const float h = add_rn(S[jj], 0.5f * add_rn(mul_rn(gu, x.kJ[jj]), mul_rn(guj, x.k)));
+          ap[jj & 3] = fmaf(hbt.P[jj] * dd, hj, ap[jj & 3]);
+          if (first && j < l) ap[jj & 3] = fmaf((c0[j * D + l] - hbt.P[jj]) * dd, hj, ap[jj & 3]);
+          const float h = add_rn(S[jj], add_rn(mul_rn(hg, x.kJ[jj]), mul_rn(hj, x.k)));
           if constexpr (DYN) gdc = fmaf(h * hbt.P[jj], x.dJ[jj], gdc);
           S[jj] = h * dd;
         }
-        const float hd = add_rn(Sd, 0.5f * add_rn(mul_rn(gu, x.k), mul_rn(gu, x.k)));
+        const float hd = add_rn(Sd, add_rn(mul_rn(hg, x.k), mul_rn(hg, x.k)));
         Sd = hd * mul_rn(x.d, x.d);
         xc[w * kWave + l] = v2f{(ap[0] + ap[1]) + (ap[2] + ap[3]), gdc};
+        const bool chunk_end = tt == 0 && c > 0;
+        if (chunk_end) pf.put(stage[(c - 1) & 1], tid);
         __syncthreads();
-        // Phase 3: dL/dk, dL/dd, dL/dp, dL/dr of the token.
-        const float pgu = sum4(xc[l][0], xc[kWave + l][0], xc[2 * kWave + l][0], xc[3 * kWave + l][0]);
+        if (chunk_end && c > 1) pf.fetch(sp, (c - 2) * kBlk, T, tid);
+        // Phase 3: dL/dk, dL/dd, dL/dp, dL/dr of the token (P' gu = 2 P' hg).
+        float pgs[W], gds[W];
+#pragma unroll
+        for (int i = 0; i < W; ++i) {
+          const v2f v = xc[i * kWave + l];
+          pgs[i] = v[0];
+          gds[i] = v[1];
+        }
+        const float pgu = 2.f * tree<W>(pgs);
         const float gk = -rkm[l] + fmaf(gs, o.u, fmaf(fmaf(hbt.pd, mul_rn(x.d, x.d), x.p), gu, pgu));
         if (w == 0) {
           gkp[t * D + l] = gk;
           gvp[t * D + l] = ge;
         }
         if constexpr (DYN) {
-          float gdl = sum4(xc[l][1], xc[kWave + l][1], xc[2 * kWave + l][1], xc[3 * kWave + l][1]);
-          gdl = fmaf(hd * hbt.pd, x.d, gdl);
+          const float gdl = fmaf(hd * hbt.pd, x.d, tree<W>(gds));
           const float gd = fmaf(2.f, gdl, rdm[l]);
-          const float gp = wave_sum(hd);
+          const float gp = wave_total(hd);
           if (w == 0) {
             if (gdp) gdp[t * D + l] = gd;
             if (l == 0) {
@@ -1014,11 +1184,11 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1))
   }
   if (a.gm0) {
 #pragma unroll
-    for (int ii = 0; ii < kB; ++ii) a.gm0[n * D * D + (j0 + ii) * D + l] = gM[ii];
+    for (int ii = 0; ii < KB; ++ii) a.gm0[n * D * D + (j0 + ii) * D + l] = gM[ii];
   }
   if (a.gc0) {
 #pragma unroll
-    for (int jj = 0; jj < kB; ++jj) a.gc0[n * D * D + (j0 + jj) * D + l] = S[jj];
+    for (int jj = 0; jj < KB; ++jj) a.gc0[n * D * D + (j0 + jj) * D + l] = S[jj];
   }
 }
 
@@ -1026,19 +1196,21 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1))
 
 hipError_t launch_forward_d64(bool fixed, const FwdArgs& a, hipStream_t stream) {
   if (a.n == 0) return hipSuccess;
-  const dim3 grid(static_cast<unsigned>(a.n)), block(d64::kThreads);
-  if (fixed) hipLaunchKernelGGL((d64::forward4_kernel<true>), grid, block, 0, stream, a);
-  else hipLaunchKernelGGL((d64::forward4_kernel<false>), grid, block, 0, stream, a);
+  constexpr int W = d64::kGroupWaves;
+  const dim3 grid(static_cast<unsigned>(a.n)), block(W * kWave);
+  if (fixed) hipLaunchKernelGGL((d64::forward_group_kernel<W, true>), grid, block, 0, stream, a);
+  else hipLaunchKernelGGL((d64::forward_group_kernel<W, false>), grid, block, 0, stream, a);
   return hipGetLastError();
 }
 
 hipError_t launch_backward_d64(bool fixed, bool dyn, const BwdArgs& a, hipStream_t stream) {
   if (a.n == 0) return hipSuccess;
-  if (a.chunk == d64::kHist) {
-    const dim3 grid(static_cast<unsigned>(a.n)), block(d64::kThreads);
-    if (fixed) hipLaunchKernelGGL((d64::backward4_kernel<true, false>), grid, block, 0, stream, a);
-    else if (dyn) hipLaunchKernelGGL((d64::backward4_kernel<false, true>), grid, block, 0, stream, a);
-    else hipLaunchKernelGGL((d64::backward4_kernel<false, false>), grid, block, 0, stream, a);
+  if (a.chunk == d64::kBlk) {
+    constexpr int W = d64::kGroupWaves;
+    const dim3 grid(static_cast<unsigned>(a.n)), block(W * kWave);
+    if (fixed) hipLaunchKernelGGL((d64::backward_group_kernel<W, true, false>), grid, block, 0, stream, a);
+    else if (dyn) hipLaunchKernelGGL((d64::backward_group_kernel<W, false, true>), grid, block, 0, stream, a);
+    else hipLaunchKernelGGL((d64::backward_group_kernel<W, false, false>), grid, block, 0, stream, a);
     return hipGetLastError();
   }
   const dim3 grid(static_cast<unsigned>(a.n)), block(kWave);
