@@ -23,7 +23,10 @@
 // products (sum over value columns = over lanes) go through a swizzled
 // 64 x 64 LDS transpose.
 
+#include <type_traits>
+
 #include "bssm_recurrence.h"
+#include "bssm_rot4.h"
 #include "bssm_step.h"
 
 // No implicit contraction in this file: every fused multiply-add is an
@@ -597,7 +600,8 @@ __global__ __launch_bounds__(kWave) void backward_kernel(BwdArgs a) {
 }
 
 // ------------------------------------------------ wave groups per sequence
-// One workgroup of W waves per sequence (W = kGroupWaves): thread (w, l)
+// One workgroup of W waves per sequence (W = kForwardWaves in the forward,
+// kBackwardWaves in the backward): thread (w, l)
 // owns the KB = 64 / W columns J_w = [KB w, KB w + KB) of covariance row l
 // (P~_lj, j in J_w) and the rows J_w of mean column l (M_il, i in J_w); the
 // diagonal part pd_l and every per-lane scalar (u_l, s, e_l, ...) are
@@ -614,11 +618,19 @@ __global__ __launch_bounds__(kWave) void backward_kernel(BwdArgs a) {
 // reads).  The backward checkpoints every kBlk tokens and keeps a whole
 // chunk's replayed beliefs and intermediates in registers, so each token is
 // replayed once.
-#ifndef BSSM_D64_WAVES
-#define BSSM_D64_WAVES 4
+#ifndef BSSM_D64_FWD_WAVES
+#define BSSM_D64_FWD_WAVES 4
 #endif
-constexpr int kGroupWaves = BSSM_D64_WAVES;
-static_assert(kGroupWaves == 4 || kGroupWaves == 8, "wave groups of 4 or 8 waves");
+#ifndef BSSM_D64_BWD_WAVES
+#define BSSM_D64_BWD_WAVES 8
+#endif
+#ifndef BSSM_D64_SPLIT
+#define BSSM_D64_SPLIT 0
+#endif
+constexpr int kForwardWaves = BSSM_D64_FWD_WAVES;
+constexpr int kBackwardWaves = BSSM_D64_BWD_WAVES;
+static_assert((kForwardWaves == 4 || kForwardWaves == 8) && (kBackwardWaves == 4 || kBackwardWaves == 8),
+              "wave groups of 4 or 8 waves");
 constexpr int kBlk = 8;  // tokens per staged block and per backward chunk
 
 typedef float v2f __attribute__((ext_vector_type(2)));
@@ -662,14 +674,19 @@ __device__ __forceinline__ float tree(const float (&x)[W]) {
 // Sum over the wave's 64 lanes of each of the lane's KB values x[ii]: the
 // total of row ii lands in the G = 64 / KB lanes G ii .. G ii + G - 1.
 // `tile` is wave-private, 64 rows of KB floats with the 16-byte pieces of row
-// r rotated by (r / G) % (KB / 4), which keeps both the row writes and the
-// column reads free of bank conflicts; a wave's LDS operations complete in
+// r permuted by tile_rot(r): the 16-byte row writes of any 8 (or 16)
+// consecutive lanes then cover all 32 (64) banks, and the column reads of a
+// row sum touch 64 consecutive words.  A wave's LDS operations complete in
 // issue order, so no barrier separates the writes from the reads.
+template <int KB>
+__device__ __forceinline__ int tile_rot(int r) {
+  return ((r >> 1) ^ (r >> 3)) & (KB / 4 - 1);
+}
 template <int KB>
 __device__ __forceinline__ float lane_rowsum(float* tile, int l, const float (&x)[KB]) {
   constexpr int G = kWave / KB, NP = KB / 4;
   float* row = tile + l * KB;
-  const int rot = (l / G) % NP;
+  const int rot = tile_rot<KB>(l);
 #pragma unroll
   for (int c = 0; c < NP; ++c)
     *reinterpret_cast<v4f*>(&row[4 * (c ^ rot)]) = v4f{x[4 * c], x[4 * c + 1], x[4 * c + 2], x[4 * c + 3]};
@@ -677,7 +694,10 @@ __device__ __forceinline__ float lane_rowsum(float* tile, int l, const float (&x
   const int ii = l / G, g = l % G;
   float acc[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-  for (int m = 0; m < KB; ++m) acc[m & 3] += tile[(G * m + g) * KB + 4 * ((ii >> 2) ^ (m % NP)) + (ii & 3)];
+  for (int m = 0; m < KB; ++m) {
+    const int r = G * m + g;
+    acc[m & 3] += tile[r * KB + 4 * ((ii >> 2) ^ tile_rot<KB>(r)) + (ii & 3)];
+  }
   __builtin_amdgcn_wave_barrier();
   float t = (acc[0] + acc[1]) + (acc[2] + acc[3]);
   t = add_rn(t, dpp<kXor1>(t));
@@ -742,6 +762,35 @@ struct Prefetch {
     if (!FIXED && tid < 2 * kBlk) stage[kSP + tid] = s;
   }
 };
+
+// The backward's block loads go straight from global memory into the stage
+// (buffer_load ... lds): the rows of k, v, q, gy and d of the block starting
+// at token t0, 16 bytes per lane, past the end T read as zeros by the
+// descriptor's range check.  Nothing is held in registers while they are in
+// flight; the issuing wave awaits them with a vmcnt wait before the barrier
+// that publishes the stage.  p and r (8 floats each) go through the
+// registers of threads 0 .. 2 kBlk - 1 (dma_pr / put_pr).
+template <int NT, bool FIXED>
+__device__ __forceinline__ void stage_dma(const Streams& sp, float* stage, int t0, int T, int tid) {
+  constexpr int kArrays = 4 + (FIXED ? 0 : 1);
+  constexpr int kVecs = kArrays * kRowVecs;
+  const uint32_t bytes = static_cast<uint32_t>(T) * D * 4;
+#pragma unroll
+  for (int rep = 0; rep < (kVecs + NT - 1) / NT; ++rep) {
+    const int i0 = __builtin_amdgcn_readfirstlane((tid & ~(kWave - 1)) + rep * NT);  // the wave's first piece
+    if (kVecs % NT == 0 || i0 < kVecs) {
+      const int arr = i0 / kRowVecs, o = (i0 % kRowVecs) * 4;
+      const float* src = arr == 0 ? sp.k : arr == 1 ? sp.v : arr == 2 ? sp.q : arr == 3 ? sp.gy : sp.d;
+      const int off = arr == 0 ? kSK : arr == 1 ? kSV : arr == 2 ? kSQ : arr == 3 ? kSG : kSD;
+      r4::dma16<true>(r4::make_rsrc(src, bytes), stage + off + o,
+                      static_cast<uint32_t>(t0 * D + o + 4 * (tid & (kWave - 1))) * 4u);
+    }
+  }
+}
+__device__ __forceinline__ float dma_pr(const Streams& sp, int t0, int T, int tid) {
+  const int t = t0 + tid % kBlk;
+  return t < T ? (tid < kBlk ? sp.p[t] : sp.r[t]) : 0.f;
+}
 
 // One token's inputs for thread (w, l): the lane's entries and the wave's
 // KB-wide slices.
@@ -1009,178 +1058,203 @@ void backward_group_kernel(BwdArgs a) {
   }
 
   const int nb = static_cast<int>(a.nb);
-  Prefetch<NT, FIXED, true> pf;
+  // Stage of the last chunk; each chunk c > 0 issues the loads of chunk
+  // c - 1 after its first barrier (the other stage buffer is free then) and
+  // publishes them at its last.
+  float pr = 0.f;
   if (nb > 0) {
-    pf.fetch(sp, (nb - 1) * kBlk, T, tid);
-    pf.put(stage[(nb - 1) & 1], tid);
+    stage_dma<NT, FIXED>(sp, stage[(nb - 1) & 1], (nb - 1) * kBlk, T, tid);
+    if (!FIXED && tid < 2 * kBlk) stage[(nb - 1) & 1][kSP + tid] = dma_pr(sp, (nb - 1) * kBlk, T, tid);
+    r4::vm_wait<0>();
   }
   __syncthreads();
-  if (nb > 1) pf.fetch(sp, (nb - 2) * kBlk, T, tid);
   int par = 0;
   for (int c = nb - 1; c >= 0; --c) {
+    bool dma_pending = c > 0;
     const int t0 = c * kBlk;
     const int len = (T - t0) < kBlk ? (T - t0) : kBlk;
     const float* st = stage[c & 1];
-    BelG<KB> hb[kBlk];
-    PredG ho[kBlk];
-    {
-      BelG<KB> b;
-      const float* cm = bm + static_cast<int64_t>(c) * D * D;
-      const float* cc = bc + static_cast<int64_t>(c) * D * D;
+    // One pass: replay tokens [0, min(len, HI)) from the chunk's record,
+    // keeping the beliefs and intermediates of tokens [LO, HI), then reverse
+    // those tokens.
+    auto pass = [&](auto lo_c, auto hi_c) __attribute__((always_inline)) {
+      constexpr int LO = decltype(lo_c)::value, HI = decltype(hi_c)::value, NH = HI - LO;
+      BelG<KB> hb[NH];
+      PredG ho[NH];
+      {
+        BelG<KB> b;
+        const float* cm = bm + static_cast<int64_t>(c) * D * D;
+        const float* cc = bc + static_cast<int64_t>(c) * D * D;
 #pragma unroll
-      for (int q4 = 0; q4 < KB / 4; ++q4) {
-        const v4f r4 = *reinterpret_cast<const v4f*>(&cc[l * D + j0 + 4 * q4]);
+        for (int q4 = 0; q4 < KB / 4; ++q4) {
+          const v4f r4 = *reinterpret_cast<const v4f*>(&cc[l * D + j0 + 4 * q4]);
 #pragma unroll
-        for (int h = 0; h < 4; ++h) b.P[4 * q4 + h] = r4[h];
+          for (int h = 0; h < 4; ++h) b.P[4 * q4 + h] = r4[h];
+        }
+#pragma unroll
+        for (int ii = 0; ii < KB; ++ii) b.M[ii] = cm[(j0 + ii) * D + l];
+        b.pd = 0.f;
+#pragma unroll
+        for (int tt = 0; tt < HI; ++tt) {
+          if (tt < len) {
+            TokG<KB> x;
+            read_tok<KB, FIXED, false>(x, st, tt, l, j0);
+            if (tt >= LO) hb[tt >= LO ? tt - LO : 0] = b;
+            v2f* xs = xz[par];
+            par ^= 1;
+            xs[w * kWave + l] = predict_part(b, x);
+            __syncthreads();
+            if (tt == 0 && dma_pending) {
+              stage_dma<NT, FIXED>(sp, stage[(c - 1) & 1], (c - 1) * kBlk, T, tid);
+              if (!FIXED && tid < 2 * kBlk) pr = dma_pr(sp, (c - 1) * kBlk, T, tid);
+              dma_pending = false;
+            }
+            float zs[W], es[W];
+#pragma unroll
+            for (int i = 0; i < W; ++i) {
+              const v2f v = xs[i * kWave + l];
+              zs[i] = v[0];
+              es[i] = v[1];
+            }
+            const PredG o = predict_done<W>(b, x, zs, es, a.floor);
+            if (tt >= LO) ho[tt >= LO ? tt - LO : 0] = o;
+            if (tt + 1 < len && tt + 1 < HI) update_g(b, x, o, l, j0, (c == 0 && tt == 0) ? c0 + l : nullptr);
+          }
+        }
       }
 #pragma unroll
-      for (int ii = 0; ii < KB; ++ii) b.M[ii] = cm[(j0 + ii) * D + l];
-      b.pd = 0.f;
-#pragma unroll
-      for (int tt = 0; tt < kBlk; ++tt) {
+      for (int tt = HI - 1; tt >= LO; --tt) {
         if (tt < len) {
+          const BelG<KB>& hbt = hb[tt - LO];
+          const PredG& o = ho[tt - LO];
+          const int t = t0 + tt;
           TokG<KB> x;
-          read_tok<KB, FIXED, false>(x, st, tt, l, j0);
-          hb[tt] = b;
-          v2f* xs = xz[par];
-          par ^= 1;
-          xs[w * kWave + l] = predict_part(b, x);
+          read_tok<KB, FIXED, true>(x, st, tt, l, j0);
+          float uJ[KB], dM[KB];
+#pragma unroll
+          for (int jj = 0; jj < KB; ++jj) {
+            uJ[jj] = lane_value(o.u, j0 + jj);
+            dM[jj] = x.dJ[jj] * hbt.M[jj];
+          }
+          // Phase 1: gM += q gy^T; partials of gM^T u and S u; row sums of
+          // M_new gy (dL/dq) and gM e.
+          float am[4] = {0.f, 0.f, 0.f, 0.f}, aw[4] = {0.f, 0.f, 0.f, 0.f};
+          float vq[KB], va[KB];
+          const float be = o.beta * o.e;
+#pragma unroll
+          for (int ii = 0; ii < KB; ++ii) {
+            gM[ii] = fmaf(x.qJ[ii], x.gy, gM[ii]);
+            am[ii & 3] = fmaf(gM[ii], uJ[ii], am[ii & 3]);
+            aw[ii & 3] = fmaf(S[ii], uJ[ii], aw[ii & 3]);
+            vq[ii] = fmaf(uJ[ii], be, dM[ii]) * x.gy;
+            va[ii] = gM[ii] * o.e;
+          }
+          {
+            const float rq = lane_rowsum<KB>(tile, l, vq);
+            if (l % G == 0) gqp[t * D + j0 + l / G] = rq;
+            const float r_a = lane_rowsum<KB>(tile, l, va);
+            if (l % G == 0) ra[j0 + l / G] = r_a;
+          }
+          xb[w * kWave + l] = v2f{(am[0] + am[1]) + (am[2] + am[3]), (aw[0] + aw[1]) + (aw[2] + aw[3])};
           __syncthreads();
-          float zs[W], es[W];
+          // Phase 2: ge, gs, gu; row sums of (d M) ge and (gM - k ge^T) M;
+          // partials of P' gu and of the decay's covariance term.  gu enters
+          // halved (hg = gu / 2, exact), which gives the symmetrized outer
+          // product sym(gu k^T) without a further rounding.
+          float gms[W], ws[W];
 #pragma unroll
           for (int i = 0; i < W; ++i) {
-            const v2f v = xs[i * kWave + l];
-            zs[i] = v[0];
-            es[i] = v[1];
+            const v2f v = xb[i * kWave + l];
+            gms[i] = v[0];
+            ws[i] = v[1];
           }
-          ho[tt] = predict_done<W>(b, x, zs, es, a.floor);
-          if (tt + 1 < len) update_g(b, x, ho[tt], l, j0, (c == 0 && tt == 0) ? c0 + l : nullptr);
-        }
-      }
-    }
+          const float gmu = tree<W>(gms), wl = tree<W>(ws);
+          const float a_l = ra[l];
+          const float ge = o.beta * gmu;
+          const float z = wave_total(fmaf(o.e, gmu, -(o.u * wl)));
+          const float gs = o.clamped ? 0.f : -z * o.beta * o.beta;
+          const float gu = fmaf(o.beta, fmaf(-2.f, wl, a_l), gs * x.k);
+          const float hg = 0.5f * gu;
+          float vk[KB], vd[KB];
 #pragma unroll
-    for (int tt = kBlk - 1; tt >= 0; --tt) {
-      if (tt < len) {
-        const BelG<KB>& hbt = hb[tt];
-        const PredG& o = ho[tt];
-        const int t = t0 + tt;
-        TokG<KB> x;
-        read_tok<KB, FIXED, true>(x, st, tt, l, j0);
-        float uJ[KB], dM[KB];
-#pragma unroll
-        for (int jj = 0; jj < KB; ++jj) {
-          uJ[jj] = lane_value(o.u, j0 + jj);
-          dM[jj] = x.dJ[jj] * hbt.M[jj];
-        }
-        // Phase 1: gM += q gy^T; partials of gM^T u and S u; row sums of
-        // M_new gy (dL/dq) and gM e.
-        float am[4] = {0.f, 0.f, 0.f, 0.f}, aw[4] = {0.f, 0.f, 0.f, 0.f};
-        float vq[KB], va[KB];
-        const float be = o.beta * o.e;
-#pragma unroll
-        for (int ii = 0; ii < KB; ++ii) {
-          gM[ii] = fmaf(x.qJ[ii], x.gy, gM[ii]);
-          am[ii & 3] = fmaf(gM[ii], uJ[ii], am[ii & 3]);
-          aw[ii & 3] = fmaf(S[ii], uJ[ii], aw[ii & 3]);
-          vq[ii] = fmaf(uJ[ii], be, dM[ii]) * x.gy;
-          va[ii] = gM[ii] * o.e;
-        }
-        {
-          const float rq = lane_rowsum<KB>(tile, l, vq);
-          if (l % G == 0) gqp[t * D + j0 + l / G] = rq;
-          const float r_a = lane_rowsum<KB>(tile, l, va);
-          if (l % G == 0) ra[j0 + l / G] = r_a;
-        }
-        xb[w * kWave + l] = v2f{(am[0] + am[1]) + (am[2] + am[3]), (aw[0] + aw[1]) + (aw[2] + aw[3])};
-        __syncthreads();
-        // Phase 2: ge, gs, gu; row sums of (d M) ge and (gM - k ge^T) M;
-        // partials of P' gu and of the decay's covariance term.  gu enters
-        // halved (hg = gu / 2, exact), which gives the symmetrized outer
-        // product sym(gu k^T) without a further rounding.
-        float gms[W], ws[W];
-#pragma unroll
-        for (int i = 0; i < W; ++i) {
-          const v2f v = xb[i * kWave + l];
-          gms[i] = v[0];
-          ws[i] = v[1];
-        }
-        const float gmu = tree<W>(gms), wl = tree<W>(ws);
-        const float a_l = ra[l];
-        const float ge = o.beta * gmu;
-        const float z = wave_total(fmaf(o.e, gmu, -(o.u * wl)));
-        const float gs = o.clamped ? 0.f : -z * o.beta * o.beta;
-        const float gu = fmaf(o.beta, fmaf(-2.f, wl, a_l), gs * x.k);
-        const float hg = 0.5f * gu;
-        float vk[KB], vd[KB];
-#pragma unroll
-        for (int ii = 0; ii < KB; ++ii) {
-          vk[ii] = dM[ii] * ge;
-          const float g = fmaf(-x.kJ[ii], ge, gM[ii]);
-          vd[ii] = g * hbt.M[ii];
-          gM[ii] = g * x.dJ[ii];
-        }
-        {
-          const float r_k = lane_rowsum<KB>(tile, l, vk);
-          if (l % G == 0) rkm[j0 + l / G] = r_k;
-          if constexpr (DYN) {
-            const float r_d = lane_rowsum<KB>(tile, l, vd);
-            if (l % G == 0) rdm[j0 + l / G] = r_d;
+          for (int ii = 0; ii < KB; ++ii) {
+            vk[ii] = dM[ii] * ge;
+            const float g = fmaf(-x.kJ[ii], ge, gM[ii]);
+            vd[ii] = g * hbt.M[ii];
+            gM[ii] = g * x.dJ[ii];
           }
-        }
-        float ap[4] = {0.f, 0.f, 0.f, 0.f}, gdc = 0.f;
-        const bool first = t == 0;
-#pragma unroll
-        for (int jj = 0; jj < KB; ++jj) {
-          const int j = j0 + jj;
-          const float hj = lane_value(hg, j);
-          const float dd = mul_rn(x.d, x.dJ[jj]);
-          ap[jj & 3] = fmaf(hbt.P[jj] * dd, hj, ap[jj & 3]);
-          if (first && j < l) ap[jj & 3] = fmaf((c0[j * D + l] - hbt.P[jj]) * dd, hj, ap[jj & 3]);
-          const float h = add_rn(S[jj], add_rn(mul_rn(hg, x.kJ[jj]), mul_rn(hj, x.k)));
-          if constexpr (DYN) gdc = fmaf(h * hbt.P[jj], x.dJ[jj], gdc);
-          S[jj] = h * dd;
-        }
-        const float hd = add_rn(Sd, add_rn(mul_rn(hg, x.k), mul_rn(hg, x.k)));
-        Sd = hd * mul_rn(x.d, x.d);
-        xc[w * kWave + l] = v2f{(ap[0] + ap[1]) + (ap[2] + ap[3]), gdc};
-        const bool chunk_end = tt == 0 && c > 0;
-        if (chunk_end) pf.put(stage[(c - 1) & 1], tid);
-        __syncthreads();
-        if (chunk_end && c > 1) pf.fetch(sp, (c - 2) * kBlk, T, tid);
-        // Phase 3: dL/dk, dL/dd, dL/dp, dL/dr of the token (P' gu = 2 P' hg).
-        float pgs[W], gds[W];
-#pragma unroll
-        for (int i = 0; i < W; ++i) {
-          const v2f v = xc[i * kWave + l];
-          pgs[i] = v[0];
-          gds[i] = v[1];
-        }
-        const float pgu = 2.f * tree<W>(pgs);
-        const float gk = -rkm[l] + fmaf(gs, o.u, fmaf(fmaf(hbt.pd, mul_rn(x.d, x.d), x.p), gu, pgu));
-        if (w == 0) {
-          gkp[t * D + l] = gk;
-          gvp[t * D + l] = ge;
-        }
-        if constexpr (DYN) {
-          const float gdl = fmaf(hd * hbt.pd, x.d, tree<W>(gds));
-          const float gd = fmaf(2.f, gdl, rdm[l]);
-          const float gp = wave_total(hd);
-          if (w == 0) {
-            if (gdp) gdp[t * D + l] = gd;
-            if (l == 0) {
-              if (gpp) gpp[t] = gp;
-              if (grp) grp[t] = gs;
+          {
+            const float r_k = lane_rowsum<KB>(tile, l, vk);
+            if (l % G == 0) rkm[j0 + l / G] = r_k;
+            if constexpr (DYN) {
+              const float r_d = lane_rowsum<KB>(tile, l, vd);
+              if (l % G == 0) rdm[j0 + l / G] = r_d;
             }
           }
-        } else if (w == 0) {
-          if (gdp) gdp[t * D + l] = 0.f;
-          if (l == 0) {
-            if (gpp) gpp[t] = 0.f;
-            if (grp) grp[t] = 0.f;
+          float ap[4] = {0.f, 0.f, 0.f, 0.f}, gdc = 0.f;
+          const bool first = t == 0;
+#pragma unroll
+          for (int jj = 0; jj < KB; ++jj) {
+            const int j = j0 + jj;
+            const float hj = lane_value(hg, j);
+            const float dd = mul_rn(x.d, x.dJ[jj]);
+            ap[jj & 3] = fmaf(hbt.P[jj] * dd, hj, ap[jj & 3]);
+            if (first && j < l) ap[jj & 3] = fmaf((c0[j * D + l] - hbt.P[jj]) * dd, hj, ap[jj & 3]);
+            const float h = add_rn(S[jj], add_rn(mul_rn(hg, x.kJ[jj]), mul_rn(hj, x.k)));
+            if constexpr (DYN) gdc = fmaf(h * hbt.P[jj], x.dJ[jj], gdc);
+            S[jj] = h * dd;
+          }
+          const float hd = add_rn(Sd, add_rn(mul_rn(hg, x.k), mul_rn(hg, x.k)));
+          Sd = hd * mul_rn(x.d, x.d);
+          xc[w * kWave + l] = v2f{(ap[0] + ap[1]) + (ap[2] + ap[3]), gdc};
+          if (tt == 0 && c > 0) {  // publish the next chunk's stage
+            if (!FIXED && tid < 2 * kBlk) stage[(c - 1) & 1][kSP + tid] = pr;
+            r4::vm_wait<0>();
+          }
+          __syncthreads();
+          // Phase 3: dL/dk, dL/dd, dL/dp, dL/dr of the token (P' gu = 2 P' hg).
+          float pgs[W], gds[W];
+#pragma unroll
+          for (int i = 0; i < W; ++i) {
+            const v2f v = xc[i * kWave + l];
+            pgs[i] = v[0];
+            gds[i] = v[1];
+          }
+          const float pgu = 2.f * tree<W>(pgs);
+          const float gk = -rkm[l] + fmaf(gs, o.u, fmaf(fmaf(hbt.pd, mul_rn(x.d, x.d), x.p), gu, pgu));
+          if (w == 0) {
+            gkp[t * D + l] = gk;
+            gvp[t * D + l] = ge;
+          }
+          if constexpr (DYN) {
+            const float gdl = fmaf(hd * hbt.pd, x.d, tree<W>(gds));
+            const float gd = fmaf(2.f, gdl, rdm[l]);
+            const float gp = wave_total(hd);
+            if (w == 0) {
+              if (gdp) gdp[t * D + l] = gd;
+              if (l == 0) {
+                if (gpp) gpp[t] = gp;
+                if (grp) grp[t] = gs;
+              }
+            }
+          } else if (w == 0) {
+            if (gdp) gdp[t * D + l] = 0.f;
+            if (l == 0) {
+              if (gpp) gpp[t] = 0.f;
+              if (grp) grp[t] = 0.f;
+            }
           }
         }
       }
-    }
+    };
+#if BSSM_D64_SPLIT
+    // Two passes of half a chunk each (the first half replayed twice): half
+    // the history in registers.
+    if (len > kBlk / 2) pass(std::integral_constant<int, kBlk / 2>{}, std::integral_constant<int, kBlk>{});
+    pass(std::integral_constant<int, 0>{}, std::integral_constant<int, kBlk / 2>{});
+#else
+    pass(std::integral_constant<int, 0>{}, std::integral_constant<int, kBlk>{});
+#endif
   }
   if (a.gm0) {
 #pragma unroll
@@ -1196,7 +1270,7 @@ void backward_group_kernel(BwdArgs a) {
 
 hipError_t launch_forward_d64(bool fixed, const FwdArgs& a, hipStream_t stream) {
   if (a.n == 0) return hipSuccess;
-  constexpr int W = d64::kGroupWaves;
+  constexpr int W = d64::kForwardWaves;
   const dim3 grid(static_cast<unsigned>(a.n)), block(W * kWave);
   if (fixed) hipLaunchKernelGGL((d64::forward_group_kernel<W, true>), grid, block, 0, stream, a);
   else hipLaunchKernelGGL((d64::forward_group_kernel<W, false>), grid, block, 0, stream, a);
@@ -1206,7 +1280,7 @@ hipError_t launch_forward_d64(bool fixed, const FwdArgs& a, hipStream_t stream) 
 hipError_t launch_backward_d64(bool fixed, bool dyn, const BwdArgs& a, hipStream_t stream) {
   if (a.n == 0) return hipSuccess;
   if (a.chunk == d64::kBlk) {
-    constexpr int W = d64::kGroupWaves;
+    constexpr int W = d64::kBackwardWaves;
     const dim3 grid(static_cast<unsigned>(a.n)), block(W * kWave);
     if (fixed) hipLaunchKernelGGL((d64::backward_group_kernel<W, true, false>), grid, block, 0, stream, a);
     else if (dyn) hipLaunchKernelGGL((d64::backward_group_kernel<W, false, true>), grid, block, 0, stream, a);
