@@ -2,26 +2,33 @@
 // the reference extension for this shape: chunk_forward_kernel :175-261,
 // recompute_chunk_kernel :263-301, backward_chunk_kernel :303-343).
 //
-// Work decomposition: one wave64 per sequence and lane l owns dimension l --
-// row l of the covariance P (P[j] = P_lj) and column l of the mean M
-// (M[i] = M_il).  Every per-token matrix-vector product is then a local
-// 64-term dot product against a vector that all lanes read from LDS, the
-// scalar s = r + k.u is a wave all-reduce, and nothing is synchronized across
-// waves.  The covariance is carried as P~ + diag(pd): P~ collects the
+// Two work decompositions share the per-token conventions below.
+//
+// Wave groups (the forward for every chunk, the backward at the preferred
+// checkpoint interval kBlk = kD64Checkpoint = 8, bssm_recurrence.h): a
+// workgroup of W waves per sequence, thread (w, l) holding 64 / W columns of
+// covariance row l and the same rows of mean column l; row sums over j are W
+// partial sums exchanged through LDS, sums over lanes go through a
+// wave-private LDS transpose.  Inputs are staged per 8-token block through
+// LDS.  The backward replays each chunk once, its history in registers.
+//
+// One wave per sequence (the backward at other chunks): lane l owns row l of
+// the covariance P (P[j] = P_lj) and column l of the mean M (M[i] = M_il);
+// every per-token matrix-vector product is a local 64-term dot product
+// against a vector that all lanes read from LDS, and the reverse of token t
+// replays from the chunk's checkpoint up to t (quadratic in the chunk
+// length).  Row sums of mean-shaped products go through a padded 64 x 64 LDS
+// transpose.
+//
+// Conventions: the covariance is carried as P~ + diag(pd): P~ collects the
 // rank-one downdates and pd the process noise on the diagonal, so no lane
 // has to address its own diagonal register (a run-time index) every token.
 // Products that must commute (d_l d_j, u_l u_j, gu_l k_j + gu_j k_l) are
 // formed without contraction, which keeps P and the covariance adjoint
 // bitwise symmetric, as the reference's mirrored upper-triangle update does
-// (persistent_bayes_chunked.cu:221-241).
-//
-// Backward: the reverse of token t needs the belief before t.  Instead of the
-// reference's per-token history in HBM (mp/pp/uh/bh/eh, 32 KB per token and
-// sequence at D = 64), the kernel replays from the chunk's checkpoint up to
-// t on chip before reversing t (quadratic in the chunk length; the autograd
-// path checkpoints every kD64Checkpoint tokens, bssm_recurrence.h).  Row sums of mean-shaped
-// products (sum over value columns = over lanes) go through a swizzled
-// 64 x 64 LDS transpose.
+// (persistent_bayes_chunked.cu:221-241).  Instead of the reference's
+// per-token history in HBM (mp/pp/uh/bh/eh, 32 KB per token and sequence at
+// D = 64), both backwards replay from the checkpoints on chip.
 
 #include <type_traits>
 
@@ -222,78 +229,6 @@ __device__ __forceinline__ void update(float (&P)[D], float& pd, float (&M)[D], 
 // P~ + diag(pd) as a plain row (diagonal folded in), for storing.
 __device__ __forceinline__ float with_diag(const float (&P)[D], float pd, int j, int l) {
   return j == l ? P[j] + pd : P[j];
-}
-
-// ------------------------------------------------------------------ forward
-template <bool FIXED>
-__global__ __launch_bounds__(kWave) void forward_kernel(FwdArgs a) {
-  __shared__ float sk[D], sd[D], sq[D], swk[D], su[D];
-  const Bcast b{sk, sd, sq, swk, su, nullptr};
-  const int l = threadIdx.x;
-  const int64_t n = blockIdx.x;
-  const int64_t T = a.t, nbp = a.nb + 1;
-  const float* c0 = a.c0 + n * D * D;
-  const float* m0 = a.m0 + n * D * D;
-  float* bm = a.bm + n * nbp * D * D;
-  float* bc = a.bc + n * nbp * D * D;
-
-  float P[D], M[D];
-  float pd = 0.f;
-#pragma unroll
-  for (int j = 0; j < D; ++j) P[j] = c0[l * D + j];  // row l, as given
-#pragma unroll
-  for (int i = 0; i < D; ++i) M[i] = m0[i * D + l];
-  // Checkpoint 0 is the initial belief as given.
-#pragma unroll
-  for (int i = 0; i < D; ++i) bm[i * D + l] = M[i];
-#pragma unroll
-  for (int j = 0; j < D; ++j) bc[l * D + j] = P[j];
-
-  // Symmetric after the first update: store column-wise (coalesced).
-  auto store_belief = [&](float* mdst, float* cdst) __attribute__((always_inline)) {
-#pragma unroll
-    for (int i = 0; i < D; ++i) mdst[i * D + l] = M[i];
-#pragma unroll
-    for (int j = 0; j < D; ++j) cdst[j * D + l] = with_diag(P, pd, j, l);
-  };
-
-  const float* kp = a.k + n * T * D;
-  const float* vp = a.v + n * T * D;
-  const float* qp = a.q + n * T * D;
-  const float* dp = FIXED ? nullptr : a.d + n * T * D;
-  const float* pp = FIXED ? nullptr : a.p + n * T;
-  const float* rp = FIXED ? nullptr : a.r + n * T;
-  float* yp = a.y + n * T * D;
-
-  Tok nxt = T > 0 ? load_tok<FIXED>(kp, vp, qp, dp, pp, rp, nullptr, 0, l) : Tok{};
-  if (T > 0) {  // the first token mirrors the initial covariance's upper triangle
-    const Tok x = nxt;
-    if (T > 1) nxt = load_tok<FIXED>(kp, vp, qp, dp, pp, rp, nullptr, 1, l);
-    const Pred o = predict(P, pd, M, x, a.floor, b, l);
-    update(P, pd, M, x, o, b, l, c0 + l);
-    yp[l] = dot64(M, sq);
-  }
-  int64_t c = 1;
-  for (int64_t t = 1; t < T; ++t) {
-    if (t % a.chunk == 0) {
-      store_belief(bm + c * D * D, bc + c * D * D);
-      ++c;
-    }
-    const Tok x = nxt;
-    if (t + 1 < T) nxt = load_tok<FIXED>(kp, vp, qp, dp, pp, rp, nullptr, static_cast<int>(t + 1), l);
-    const Pred o = predict(P, pd, M, x, a.floor, b, l);
-    update(P, pd, M, x, o, b, l, nullptr);
-    yp[static_cast<int>(t) * D + l] = dot64(M, sq);
-  }
-  if (T > 0) {
-    store_belief(a.mT + n * D * D, a.cT + n * D * D);
-    store_belief(bm + a.nb * D * D, bc + a.nb * D * D);
-  } else {
-#pragma unroll
-    for (int i = 0; i < D; ++i) a.mT[n * D * D + i * D + l] = M[i];
-#pragma unroll
-    for (int j = 0; j < D; ++j) a.cT[n * D * D + l * D + j] = P[j];
-  }
 }
 
 // ----------------------------------------------------------------- backward
@@ -618,19 +553,11 @@ __global__ __launch_bounds__(kWave) void backward_kernel(BwdArgs a) {
 // reads).  The backward checkpoints every kBlk tokens and keeps a whole
 // chunk's replayed beliefs and intermediates in registers, so each token is
 // replayed once.
-#ifndef BSSM_D64_FWD_WAVES
-#define BSSM_D64_FWD_WAVES 4
-#endif
-#ifndef BSSM_D64_BWD_WAVES
-#define BSSM_D64_BWD_WAVES 8
-#endif
-#ifndef BSSM_D64_SPLIT
-#define BSSM_D64_SPLIT 0
-#endif
-constexpr int kForwardWaves = BSSM_D64_FWD_WAVES;
-constexpr int kBackwardWaves = BSSM_D64_BWD_WAVES;
-static_assert((kForwardWaves == 4 || kForwardWaves == 8) && (kBackwardWaves == 4 || kBackwardWaves == 8),
-              "wave groups of 4 or 8 waves");
+// Waves per sequence: four in the forward (one wave per SIMD at 256
+// sequences), eight in the backward (two per SIMD; its history of 8 tokens
+// fits in 256 registers per lane only with 8-column blocks).
+constexpr int kForwardWaves = 4;
+constexpr int kBackwardWaves = 8;
 constexpr int kBlk = 8;  // tokens per staged block and per backward chunk
 
 typedef float v2f __attribute__((ext_vector_type(2)));
@@ -1247,14 +1174,7 @@ void backward_group_kernel(BwdArgs a) {
         }
       }
     };
-#if BSSM_D64_SPLIT
-    // Two passes of half a chunk each (the first half replayed twice): half
-    // the history in registers.
-    if (len > kBlk / 2) pass(std::integral_constant<int, kBlk / 2>{}, std::integral_constant<int, kBlk>{});
-    pass(std::integral_constant<int, 0>{}, std::integral_constant<int, kBlk / 2>{});
-#else
     pass(std::integral_constant<int, 0>{}, std::integral_constant<int, kBlk>{});
-#endif
   }
   if (a.gm0) {
 #pragma unroll
