@@ -191,7 +191,7 @@ __device__ __forceinline__ Pred predict(const float (&P)[D], float pd, const flo
   const float z = fmaf(pd, wk, (az[0] + az[1]) + (az[2] + az[3]));
   o.u = fmaf(x.d, z, x.p * x.k);
   o.s = wave_sum(x.k * o.u) + x.r;
-  o.beta = 1.0f / fmaxf(o.s, floor);
+  o.beta = fast_rcp(fmaxf(o.s, floor));
   o.e = x.v - ((ae[0] + ae[1]) + (ae[2] + ae[3]));
   b.u[l] = o.u;
   lds_handoff();
@@ -634,9 +634,11 @@ __device__ __forceinline__ float lane_rowsum(float* tile, int l, const float (&x
 }
 
 // LDS stage of one block (floats): rows of k, v, q, gy, d (kBlk x 64 each),
-// then p and r of the block's tokens.
+// then p and r of the block's tokens; the forward's stage also holds the
+// rows of wk = d k (kSW).
 constexpr int kSK = 0, kSV = kBlk * D, kSQ = 2 * kBlk * D, kSG = 3 * kBlk * D, kSD = 4 * kBlk * D;
 constexpr int kSP = 5 * kBlk * D, kSR = kSP + kBlk, kStage = kSR + kBlk;
+constexpr int kSW = kStage, kStageFwd = kSW + kBlk * D;
 constexpr int kRowVecs = kBlk * D / 4;  // 16-byte pieces of one array's block
 
 // The sequence's input streams.
@@ -644,22 +646,25 @@ struct Streams {
   const float *k, *v, *q, *gy, *d, *p, *r;
 };
 
-// A block of staged inputs held in registers between its load and its LDS
-// write (loaded a block ahead).  Arrays k, v, q, then gy (backward), then d
-// (dynamic decay); piece i of the block is array i / kRowVecs.
-template <int NT, bool FIXED, bool GY>
+// The forward's block of staged inputs, held in registers between its load
+// and its LDS write (loaded a block ahead).  Piece i of the block is array
+// i / kRowVecs of k, v, d, q (k, v, q for fixed dynamics): with 256 threads
+// the thread that holds a piece of k also holds the same piece of d, and
+// writes their product to the wk rows.
+template <int NT, bool FIXED>
 struct Prefetch {
-  static constexpr int kArrays = 3 + (GY ? 1 : 0) + (FIXED ? 0 : 1);
+  static_assert(NT == 2 * kRowVecs, "k and d pieces in one thread");
+  static constexpr int kArrays = FIXED ? 3 : 4;
   static constexpr int kVecs = kArrays * kRowVecs;
   static constexpr int kReps = (kVecs + NT - 1) / NT;
   v4f x[kReps];
   float s;
 
   __device__ __forceinline__ static int array_offset(int arr) {
-    return arr == 0 ? kSK : arr == 1 ? kSV : arr == 2 ? kSQ : (arr == 3 && GY) ? kSG : kSD;
+    return arr == 0 ? kSK : arr == 1 ? kSV : (arr == 2 && !FIXED) ? kSD : kSQ;
   }
   __device__ __forceinline__ static const float* array_src(const Streams& sp, int arr) {
-    return arr == 0 ? sp.k : arr == 1 ? sp.v : arr == 2 ? sp.q : (arr == 3 && GY) ? sp.gy : sp.d;
+    return arr == 0 ? sp.k : arr == 1 ? sp.v : (arr == 2 && !FIXED) ? sp.d : sp.q;
   }
   // Loads of the block starting at token t0 (zeros past the end T).
   __device__ __forceinline__ void fetch(const Streams& sp, int t0, int T, int tid) {
@@ -685,6 +690,11 @@ struct Prefetch {
         const int arr = i / kRowVecs, o = (i % kRowVecs) * 4;
         *reinterpret_cast<v4f*>(&stage[array_offset(arr) + o]) = x[rep];
       }
+    }
+    if (tid < kRowVecs) {  // x[0] is a piece of k; x[1] the same piece of d
+      const v4f dv = FIXED ? v4f{kFixedDecay, kFixedDecay, kFixedDecay, kFixedDecay} : x[1];
+      *reinterpret_cast<v4f*>(&stage[kSW + 4 * tid]) = v4f{dv[0] * x[0][0], dv[1] * x[0][1], dv[2] * x[0][2],
+                                                           dv[3] * x[0][3]};
     }
     if (!FIXED && tid < 2 * kBlk) stage[kSP + tid] = s;
   }
@@ -724,10 +734,12 @@ __device__ __forceinline__ float dma_pr(const Streams& sp, int t0, int T, int ti
 template <int KB>
 struct TokG {
   float k, d, v, q, gy, p, r;
-  float kJ[KB], dJ[KB], qJ[KB];
+  float kJ[KB], dJ[KB], qJ[KB], wJ[KB];  // wJ = dJ kJ
 };
 
-template <int KB, bool FIXED, bool GY>
+// WK: the stage holds the wk rows (forward); otherwise wJ is formed here
+// (the same single rounding).
+template <int KB, bool FIXED, bool GY, bool WK = false>
 __device__ __forceinline__ void read_tok(TokG<KB>& x, const float* st, int tt, int l, int j0) {
   const int e = tt * D + l, b = tt * D + j0;
   x.k = st[kSK + e];
@@ -761,6 +773,17 @@ __device__ __forceinline__ void read_tok(TokG<KB>& x, const float* st, int tt, i
       for (int h = 0; h < 4; ++h) x.dJ[4 * c + h] = dv[h];
     }
   }
+  if constexpr (WK) {
+#pragma unroll
+    for (int c = 0; c < KB / 4; ++c) {
+      const v4f wv = *reinterpret_cast<const v4f*>(&st[kSW + b + 4 * c]);
+#pragma unroll
+      for (int h = 0; h < 4; ++h) x.wJ[4 * c + h] = wv[h];
+    }
+  } else {
+#pragma unroll
+    for (int jj = 0; jj < KB; ++jj) x.wJ[jj] = x.dJ[jj] * x.kJ[jj];
+  }
 }
 
 // Belief block of thread (w, l).
@@ -784,9 +807,8 @@ __device__ __forceinline__ v2f predict_part(const BelG<KB>& b, const TokG<KB>& x
   float az[4] = {0.f, 0.f, 0.f, 0.f}, ae[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
   for (int jj = 0; jj < KB; ++jj) {
-    const float wk = x.dJ[jj] * x.kJ[jj];
-    az[jj & 3] = fmaf(b.P[jj], wk, az[jj & 3]);
-    ae[jj & 3] = fmaf(b.M[jj], wk, ae[jj & 3]);
+    az[jj & 3] = fmaf(b.P[jj], x.wJ[jj], az[jj & 3]);
+    ae[jj & 3] = fmaf(b.M[jj], x.wJ[jj], ae[jj & 3]);
   }
   return v2f{(az[0] + az[1]) + (az[2] + az[3]), (ae[0] + ae[1]) + (ae[2] + ae[3])};
 }
@@ -800,7 +822,7 @@ __device__ __forceinline__ PredG predict_done(const BelG<KB>& b, const TokG<KB>&
   o.u = fmaf(x.d, z, x.p * x.k);
   const float s = wave_total(x.k * o.u) + x.r;
   o.clamped = !(s > floor);
-  o.beta = 1.0f / fmaxf(s, floor);
+  o.beta = fast_rcp(fmaxf(s, floor));
   o.e = x.v - tree<W>(es);
   return o;
 }
@@ -836,7 +858,7 @@ __global__ __launch_bounds__(W * kWave) void forward_group_kernel(FwdArgs a) {
   // Exchange of {P~ wk, M^T wk, M^T q of the previous token} partials,
   // double-buffered: one barrier per token.
   __shared__ v4f xz[2][W * kWave];
-  __shared__ __attribute__((aligned(16))) float stage[2][kStage];
+  __shared__ __attribute__((aligned(16))) float stage[2][kStageFwd];
   const int tid = static_cast<int>(threadIdx.x), w = wave_index(), l = tid & (kWave - 1), j0 = KB * w;
   const int64_t n = blockIdx.x;
   const int T = static_cast<int>(a.t);
@@ -874,7 +896,7 @@ __global__ __launch_bounds__(W * kWave) void forward_group_kernel(FwdArgs a) {
   };
   store(bm, bc);
 
-  Prefetch<NT, FIXED, false> pf;
+  Prefetch<NT, FIXED> pf;
   if (T > 0) {
     pf.fetch(sp, 0, T, tid);
     pf.put(stage[0], tid);
@@ -891,7 +913,7 @@ __global__ __launch_bounds__(W * kWave) void forward_group_kernel(FwdArgs a) {
     }
     const int tt = t % kBlk, blk = t / kBlk;
     TokG<KB> x;
-    read_tok<KB, FIXED, false>(x, stage[blk & 1], tt, l, j0);
+    read_tok<KB, FIXED, false, true>(x, stage[blk & 1], tt, l, j0);
     v4f* xs = xz[t & 1];
     const v2f pz = predict_part(b, x);
     xs[w * kWave + l] = v4f{pz[0], pz[1], ypart, 0.f};
