@@ -194,6 +194,28 @@ def test_backward_matches_oracle(ext, cuda_device, abi, final_grads, chunk, t):
         assert torch.equal(grads[7], grads[7].transpose(-1, -2)), "gc0 must be bitwise symmetric"
 
 
+def test_sequence_results_independent_of_batch(ext, cuda_device):
+    """A sequence's outputs, checkpoints and gradients are bitwise the same in a batch of 300 (more workgroups
+    than the device runs at once) as alone: each sequence is one workgroup with fixed arithmetic."""
+    print("d64 batch invariance n=300 t=20 chunk=8", flush=True)
+    n, t, chunk = 300, 20, 8
+    _, dev = _case(n, t, seed=41, device=cuda_device)
+    names = ("k", "v", "q", "d", "p", "r", "m0", "c0", "gy", "gmf", "gcf")
+
+    def run(c):
+        fwd = ext.forward_chunked(c["k"], c["v"], c["q"], c["d"], c["p"], c["r"], c["m0"], c["c0"], chunk, 1e-6)
+        bm, bc = fwd[3], fwd[4]
+        grads = ext.backward_chunked(c["k"], c["v"], c["q"], c["d"], c["p"], c["r"], c["m0"], c["c0"], bm, bc,
+                                     c["gy"], c["gmf"], c["gcf"], chunk, 1e-6)
+        return list(fwd) + list(grads)
+
+    whole = run(dev)
+    for i in (0, 137, n - 1):
+        alone = run({name: dev[name][i:i + 1].contiguous() for name in names})
+        for j, (a, b) in enumerate(zip(alone, whole)):
+            assert torch.equal(a, b[i:i + 1]), f"sequence {i}, result {j} differs between N = 1 and N = {n}"
+
+
 @pytest.mark.parametrize("t", [160, 512])
 def test_long_sequence_matches_oracle(ext, cuda_device, t):
     """T = 160 and T = 512 (the length bench.py times; 64 checkpoint chunks): forward and full backward against
