@@ -51,19 +51,21 @@ def dispatched_kernels(d: int, m: int, n: int, t: int, interval: int) -> tuple[s
         return f"bssm forward kernel (D{d}M{m})", f"bssm backward kernel (D{d}M{m})"
     lib = _hip.load()
     lim = [lib.bssm_small_batch_limit(k, -1) for k in range(4)]
+    groups = 2 if n > 4 * 256 else 1  # 4-sequence groups per workgroup of the split kernels
     if n <= lim[2]:
-        fwd = "bssm::sn::forward_split_kernel<false> (row layout, two waves per 4 sequences)"
+        fwd = f"bssm::sn::forward_split_kernel<false, 0, {groups}> (row layout, two waves per 4 sequences)"
     elif n <= lim[0]:
-        fwd = "bssm::sn::forward_kernel<false> (row layout, 16 lanes per sequence)"
+        fwd = "bssm::sn::forward_kernel<false, 0> (row layout, 16 lanes per sequence)"
     else:
         fwd = "bssm::r4::forward_kernel<false, 0> (rotated layout, 4 lanes per sequence)"
     row_bwd = t % 16 == 0 and interval == _hip.preferred_checkpoint(4)
     if row_bwd and n <= lim[3]:
-        bwd = "bssm::sn::backward_split_kernel<false, true> (row layout, three waves per 4 sequences)"
+        bwd = f"bssm::sn::backward_split_kernel<false, true, 0, {groups}> (row layout, three waves per 4 sequences)"
     elif row_bwd and n <= lim[1]:
         bwd = "bssm::sn::backward_kernel<false, true> (row layout, 16 lanes per sequence)"
     else:
-        bwd = "bssm::r4::backward_kernel<false, true> (rotated layout, 4 lanes per sequence)"
+        bwd = (f"bssm::r4::backward_tile_kernel<false, true, 0, {interval}> (rotated layout, 4 lanes per sequence, "
+               "16-token tiles)")
     return fwd, bwd
 
 
