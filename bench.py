@@ -30,6 +30,7 @@ import torch  # noqa: E402
 
 METRIC = "Bayes-layer fwd+bwd tokens/s at B256×T512×H64 D4M8; % HBM roofline"
 HBM_PEAK = 8.0e12  # MI355X spec peak, bytes/s
+FP32_PEAK = 157.3e12  # MI355X spec peak of fp32 vector arithmetic, flop/s
 
 
 def algorithmic_bytes(d: int, m: int) -> tuple[int, int]:
@@ -40,6 +41,19 @@ def algorithmic_bytes(d: int, m: int) -> tuple[int, int]:
     """
     inputs = 3 * d + m + 2
     return (inputs + m) * 4, (2 * inputs + m) * 4
+
+
+def dense_flops(d: int, m: int) -> tuple[int, int]:
+    """(forward, backward) arithmetic per (sequence, token) of the dense-covariance recurrence, counting a fused
+    multiply-add as two operations.
+
+    forward: wk = d k (D), z = P wk (2 D^2), u = d z + p k (3 D), s = k.u (2 D), e = v - M^T wk (2 D M),
+    M <- d M + u (beta e)^T (3 D M), P <- P d d^T - beta u u^T (4 D^2), y = M^T q (2 D M);
+    backward: the replay (the forward without y) plus the reverse: 16 D M for the mean adjoint, the row sums of
+    dL/dq, dL/dk, dL/dd and a = gM e, and 14 D^2 for S u, P' gu, sym(gu k^T), the decay term and S d d^T.
+    """
+    fwd = d + 2 * d * d + 3 * d + 2 * d + 2 * d * m + 3 * d * m + 4 * d * d + 2 * d * m
+    return fwd, (fwd - 2 * d * m) + 16 * d * m + 14 * d * d
 
 
 def dispatched_kernels(d: int, m: int, n: int, t: int, interval: int) -> tuple[str, str]:
@@ -511,10 +525,13 @@ def time_d64(b, t, h, steps, warmup, device, fused=True) -> dict:
             os.environ["BAYES_SSM_DISABLE_FUSED_CUDA"] = previous
     ms = e0.elapsed_time(e1) / steps
     fwd_b, bwd_b = algorithmic_bytes(d, d)
+    fwd_f, bwd_f = dense_flops(d, d)
+    flops = n * t * (fwd_f + bwd_f) / (ms * 1e-3)
     return {"B": b, "T": t, "H": h, "D": d, "M": d, "sequences": n, "ms_per_step": ms,
             "tokens_per_s": b * t / (ms * 1e-3),
-            # The HBM roofline of this shape is far from its bound (the VALU; 256 waves on 1024 SIMDs).
+            # The HBM roofline of this shape is far from its bound; the vector ALUs bound it.
             "roofline_step_frac": n * t * (fwd_b + bwd_b) / (ms * 1e-3) / HBM_PEAK,
+            "fp32_tflops": flops / 1e12, "fp32_roofline_frac": flops / FP32_PEAK,
             "path": "HIP D64 kernels" if fused else "reference diagonal core, eager torch"}
 
 
