@@ -546,13 +546,15 @@ __global__ __launch_bounds__(kWave) void backward_kernel(BwdArgs a) {
 // a wave's KB rows go through a wave-private LDS transpose.  u_j and gu_j of
 // J_w are read from their lanes (v_readlane).
 //
-// Inputs are staged per block of kBlk tokens: the workgroup loads the
-// block's k, v, q (gy, d) rows and p, r with 16-byte loads a block ahead
-// into registers and writes them to a double-buffered LDS stage, from which
-// each lane reads its own entries and the wave's KB-wide slices (broadcast
-// reads).  The backward checkpoints every kBlk tokens and keeps a whole
+// Inputs are staged per block of kBlk tokens in a double-buffered LDS stage,
+// a block ahead, from which each lane reads its own entries and the wave's
+// KB-wide slices (broadcast reads).  The forward loads the block's k, v, d, q
+// rows into registers and writes them, with the rows of wk = d k, to the
+// stage; the backward's k, v, q, gy, d rows go straight to the stage by
+// LDS-DMA.  The backward checkpoints every kBlk tokens and keeps a whole
 // chunk's replayed beliefs and intermediates in registers, so each token is
 // replayed once.
+//
 // Waves per sequence: four in the forward (one wave per SIMD at 256
 // sequences), eight in the backward (two per SIMD; its history of 8 tokens
 // fits in 256 registers per lane only with 8-column blocks).
